@@ -1,0 +1,312 @@
+/*
+ * cpuops.c -- TEST INFRASTRUCTURE ONLY. A plain-C restatement of Roost's CPU reference ops (CpuOps, C#) for the
+ * attention + Gated DeltaNet path, used as the parity oracle by tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg. Nothing in the product library links, calls or falls back to this code.
+ *
+ * Each function follows the reference source it cites, line for line in meaning: every element is widened to double,
+ * all arithmetic is double, and each output element is rounded once into its element type (round to nearest even;
+ * bf16 through round-to-odd to float first so the two roundings act as one). Where CpuOps throws an ArgumentException
+ * before writing, these functions return a non-zero code before writing and leave a message in oracle_last_error().
+ *
+ * Parity pinning (which check pins which function) is listed in tests/test_oracle.py.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+enum { DT_F32 = 1, DT_F16 = 2, DT_BF16 = 3, DT_F64 = 4, DT_I32 = 10, DT_I64 = 12 };
+
+static char g_err[512];
+const char* oracle_last_error(void) { return g_err; }
+static int fail(const char* msg) {
+  snprintf(g_err, sizeof g_err, "%s", msg);
+  return 1;
+}
+
+/* ---- Elements (reference: src/Starlings.Roost.Ops/CpuElements.cs:28-79, 128-160) ---- */
+
+static float f32_from_bits(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+static uint32_t bits_from_f32(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+
+/* double -> bf16: NaN -> 0x7FC0, +-inf kept; otherwise round to float with round-to-odd, then to bf16 with RNE. */
+uint16_t oracle_to_bf16(double v) {
+  if (isnan(v)) return 0x7FC0;
+  if (isinf(v)) return v > 0 ? 0x7F80 : 0xFF80;
+  float f = (float)v;
+  if (!isinf(f) && (double)f != v) {
+    uint32_t bits = bits_from_f32(f);
+    if ((bits & 1u) == 0) {
+      bits += fabs((double)f) < fabs(v) ? 1 : (uint32_t)-1;
+      f = f32_from_bits(bits);
+    }
+  }
+  uint32_t u = bits_from_f32(f);
+  if (isinf(f)) return (uint16_t)(u >> 16);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+double oracle_from_bf16(uint16_t b) { return (double)f32_from_bits((uint32_t)b << 16); }
+
+static double load(const void* p, int dt, int64_t i) {
+  switch (dt) {
+    case DT_F32: return ((const float*)p)[i];
+    case DT_F64: return ((const double*)p)[i];
+    case DT_BF16: return oracle_from_bf16(((const uint16_t*)p)[i]);
+    default: return NAN;
+  }
+}
+
+static void store(void* p, int dt, int64_t i, double v) {
+  switch (dt) {
+    case DT_F32: ((float*)p)[i] = (float)v; break;
+    case DT_F64: ((double*)p)[i] = v; break;
+    case DT_BF16: ((uint16_t*)p)[i] = oracle_to_bf16(v); break;
+    default: break;
+  }
+}
+
+static int elem_size(int dt) { return dt == DT_F64 || dt == DT_I64 ? 8 : (dt == DT_F32 || dt == DT_I32 ? 4 : 2); }
+
+/* ---- PagedAttention (reference: src/Starlings.Roost.Ops/CpuOps.cs:198-351) ---- */
+
+typedef struct {
+  int64_t q0, n, p0, kv_len;
+} Seq;
+
+static int attention_sequence(const int32_t* q_indptr, const int32_t* kv_indptr, const int32_t* last_len,
+                              int64_t kv_indices_len, int b, int tokens, int page_size, int causal, Seq* s) {
+  /* CpuOps.cs:300-335 AttentionSequence */
+  int64_t q0 = q_indptr[b], q1 = q_indptr[b + 1], p0 = kv_indptr[b], p1 = kv_indptr[b + 1];
+  int64_t pages = p1 - p0, n = q1 - q0;
+  if (n < 0 || pages < 0 || q0 < 0 || p0 < 0 || q1 > tokens) return fail("invalid QIndptr or KvIndptr range");
+  int64_t last = last_len[b];
+  if (pages > 0 && (last < 1 || last > page_size)) return fail("KvLastPageLength outside [1, BlockSize]");
+  int64_t kv_len = pages == 0 ? 0 : (pages - 1) * page_size + last;
+  if (kv_len < n && causal) return fail("fewer keys than query tokens");
+  if (p1 > kv_indices_len) return fail("KvIndices is shorter than KvIndptr needs");
+  s->q0 = q0; s->n = n; s->p0 = p0; s->kv_len = kv_len;
+  return 0;
+}
+
+int oracle_paged_attention(const void* q, void* out, const void* k_cache, const void* v_cache, int dtype,
+                           int kv_dtype, const int32_t* q_indptr, const int32_t* kv_indptr,
+                           const int32_t* kv_indices, const int32_t* last_len, int64_t kv_indices_len,
+                           int64_t cache_len, int batch, int tokens, int q_heads, int kv_heads, int head_dim,
+                           int page_size, int hnd, float scale_arg, float soft_cap, int window_left, int causal,
+                           int threads) {
+  const int hd = head_dim;
+  if (hd < 1 || hd > 1024) return fail("HeadDim must be in [1, 1024]");
+  if (kv_heads < 1 || q_heads % kv_heads != 0) return fail("QHeads must be a multiple of KvHeads");
+  if (page_size < 1) return fail("BlockSize must be positive");
+  if (window_left == 0) return fail("PagedAttention: WindowLeft is 0");
+  const double scale = scale_arg == 0.0f ? 1.0 / sqrt((double)hd) : (double)scale_arg;
+  const int group = q_heads / kv_heads;
+  Seq* seqs = (Seq*)malloc(sizeof(Seq) * (size_t)(batch > 0 ? batch : 1));
+  for (int b = 0; b < batch; ++b) {
+    /* CpuOps.cs:337-351 CheckAttentionSequence: validate every sequence before the first write. */
+    if (attention_sequence(q_indptr, kv_indptr, last_len, kv_indices_len, b, tokens, page_size, causal, &seqs[b])) {
+      free(seqs);
+      return 1;
+    }
+    const Seq* s = &seqs[b];
+    if (s->n == 0 || s->kv_len == 0) continue;
+    int64_t first_key = window_left >= 0 ? (s->kv_len - s->n - window_left > 0 ? s->kv_len - s->n - window_left : 0) : 0;
+    for (int64_t page = first_key / page_size; page <= (s->kv_len - 1) / page_size; ++page) {
+      if (kv_indices[s->p0 + page] < 0) {
+        free(seqs);
+        return fail("PagedAttention: a released block is inside a query's window");
+      }
+    }
+  }
+  /* Rows are range-checked (NeedRange) before use; a row outside the pool is an error. */
+  int err = 0;
+  const int64_t work = (int64_t)batch * q_heads;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads > 0 ? threads : 1) reduction(| : err)
+#endif
+  for (int64_t bh = 0; bh < work; ++bh) {
+    const int b = (int)(bh / q_heads);
+    const int h = (int)(bh % q_heads);
+    const Seq* s = &seqs[b];
+    const int kvh = h / group;
+    double* acc = (double*)malloc(sizeof(double) * (size_t)hd);
+    for (int64_t i = 0; i < s->n; ++i) {
+      const int64_t qpos = s->kv_len - s->n + i;
+      const int64_t hi = causal ? qpos : s->kv_len - 1;
+      const int64_t lo = window_left >= 0 ? (qpos - window_left > 0 ? qpos - window_left : 0) : 0;
+      const int64_t qo = ((s->q0 + i) * q_heads + h) * (int64_t)hd;
+      double m = -INFINITY, denom = 0.0;
+      for (int d = 0; d < hd; ++d) acc[d] = 0.0;
+      for (int64_t j = lo; j <= hi; ++j) {
+        const int64_t block = kv_indices[s->p0 + j / page_size];
+        const int64_t off = j % page_size;
+        const int64_t row = hnd ? ((block * kv_heads + kvh) * page_size + off) * hd
+                                : ((block * page_size + off) * kv_heads + kvh) * hd;
+        if (row < 0 || row + hd > cache_len) {
+          err |= 1;
+          break;
+        }
+        double sc = 0.0;
+        for (int d = 0; d < hd; ++d) sc += load(q, dtype, qo + d) * load(k_cache, kv_dtype, row + d);
+        sc *= scale;
+        if (soft_cap != 0.0f) sc = soft_cap * tanh(sc / soft_cap);
+        const double new_m = sc > m ? sc : m;
+        const double corr = isinf(m) && m < 0 ? 0.0 : exp(m - new_m);
+        const double w = exp(sc - new_m);
+        denom = denom * corr + w;
+        for (int d = 0; d < hd; ++d) acc[d] = acc[d] * corr + w * load(v_cache, kv_dtype, row + d);
+        m = new_m;
+      }
+      for (int d = 0; d < hd; ++d) store(out, dtype, qo + d, denom == 0.0 ? 0.0 : acc[d] / denom);
+    }
+    free(acc);
+  }
+  free(seqs);
+  if (err) return fail("a KV row is outside the cache span");
+  return 0;
+}
+
+/* ---- CacheWrite (reference: src/Starlings.Roost.Ops/CpuOps.cs:515-569; same-dtype byte copy) ---- */
+
+int oracle_cache_write(const void* k, const void* v, void* k_cache, void* v_cache, int dtype,
+                       const int64_t* slot_mapping, int64_t cache_len, int tokens, int kv_heads, int head_dim,
+                       int page_size, int hnd) {
+  const int64_t es = elem_size(dtype);
+  const int64_t per_token = (int64_t)kv_heads * head_dim;
+  for (int t = 0; t < tokens; ++t) {
+    const int64_t slot = slot_mapping[t];
+    if (slot < 0) continue;
+    const int64_t block = slot / page_size;
+    const int64_t off = slot % page_size;
+    for (int h = 0; h < kv_heads; ++h) {
+      const int64_t dst = hnd ? ((block * kv_heads + h) * page_size + off) * head_dim
+                              : ((block * page_size + off) * kv_heads + h) * head_dim;
+      if (dst < 0 || dst + head_dim > cache_len) return fail("CacheWrite: slot outside the cache span");
+      const int64_t src = t * per_token + (int64_t)h * head_dim;
+      memcpy((char*)k_cache + dst * es, (const char*)k + src * es, (size_t)(head_dim * es));
+      memcpy((char*)v_cache + dst * es, (const char*)v + src * es, (size_t)(head_dim * es));
+    }
+  }
+  return 0;
+}
+
+/* ---- GatedDeltaRule (reference: src/Starlings.Roost.Ops/CpuOps.Hybrid.cs:30-157, 233-241) ---- */
+
+int oracle_gated_delta_rule(const void* q, const void* k, const void* v, const void* g, int g_dtype,
+                            const void* beta, int beta_dtype, void* out, float* state, int64_t state_len,
+                            const int32_t* slots, const int32_t* cu, int dtype, int batch, int tokens, int k_heads,
+                            int v_heads, int k_dim, int v_dim, int64_t q_stride, int64_t k_stride, int64_t v_stride,
+                            int use_initial_state, int l2_norm_qk, float scale_arg, int threads) {
+  if (k_heads < 1 || v_heads % k_heads != 0) return fail("VHeads must be a multiple of KHeads");
+  const int kd = k_dim, vd = v_dim;
+  const int64_t qrow = (int64_t)k_heads * kd, vrow = (int64_t)v_heads * vd;
+  const int64_t qs = q_stride == 0 ? qrow : q_stride;
+  const int64_t ks = k_stride == 0 ? qrow : k_stride;
+  const int64_t vs = v_stride == 0 ? vrow : v_stride;
+  if (qs < qrow || ks < qrow || vs < vrow) return fail("a stride is smaller than the row width");
+  const double scale = scale_arg == 0.0f ? 1.0 / sqrt((double)kd) : (double)scale_arg;
+  const int group = v_heads / k_heads;
+  const int64_t state_elems = (int64_t)kd * vd;
+  for (int b = 0; b < batch; ++b) {
+    const int64_t t0 = cu[b], t1 = cu[b + 1];
+    if (t0 < 0 || t1 < t0 || t1 > tokens) return fail("invalid CuSeqlens range");
+    if (t1 > t0) {
+      const int64_t so = ((int64_t)slots[b] * v_heads) * state_elems;
+      if (so < 0 || so + (int64_t)v_heads * state_elems > state_len) return fail("state slot outside the pool");
+    }
+  }
+  const int64_t work = (int64_t)batch * v_heads;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads > 0 ? threads : 1)
+#endif
+  for (int64_t bh = 0; bh < work; ++bh) {
+    const int b = (int)(bh / v_heads);
+    const int h = (int)(bh % v_heads);
+    const int64_t t0 = cu[b], t1 = cu[b + 1];
+    if (t1 == t0) continue;
+    double* s = (double*)malloc(sizeof(double) * (size_t)(state_elems + 2 * kd + vd));
+    double* qv = s + state_elems;
+    double* kv = qv + kd;
+    double* dv = kv + kd;
+    float* st = state + ((int64_t)slots[b] * v_heads + h) * state_elems;
+    for (int64_t i = 0; i < state_elems; ++i) s[i] = use_initial_state ? (double)st[i] : 0.0;
+    const int kh = h / group;
+    for (int64_t t = t0; t < t1; ++t) {
+      const int64_t qo = t * qs + (int64_t)kh * kd;
+      const int64_t ko = t * ks + (int64_t)kh * kd;
+      double qq = 0.0, kk = 0.0;
+      for (int i = 0; i < kd; ++i) {
+        qv[i] = load(q, dtype, qo + i);
+        kv[i] = load(k, dtype, ko + i);
+        qq += qv[i] * qv[i];
+        kk += kv[i] * kv[i];
+      }
+      const double qn = l2_norm_qk ? 1.0 / sqrt(qq + 1e-6) : 1.0;
+      const double kn = l2_norm_qk ? 1.0 / sqrt(kk + 1e-6) : 1.0;
+      for (int i = 0; i < kd; ++i) {
+        qv[i] *= qn * scale;
+        kv[i] *= kn;
+      }
+      const double decay = exp(load(g, g_dtype, t * v_heads + h));
+      const double bt = load(beta, beta_dtype, t * v_heads + h);
+      const int64_t vo = t * vs + (int64_t)h * vd;
+      const int64_t oo = (t * v_heads + h) * (int64_t)vd;
+      for (int j = 0; j < vd; ++j) {
+        double kvs = 0.0;
+        for (int i = 0; i < kd; ++i) {
+          s[(int64_t)i * vd + j] *= decay;
+          kvs += s[(int64_t)i * vd + j] * kv[i];
+        }
+        dv[j] = bt * (load(v, dtype, vo + j) - kvs);
+      }
+      for (int j = 0; j < vd; ++j) {
+        double o = 0.0;
+        for (int i = 0; i < kd; ++i) {
+          s[(int64_t)i * vd + j] += kv[i] * dv[j];
+          o += s[(int64_t)i * vd + j] * qv[i];
+        }
+        store(out, dtype, oo + j, o);
+      }
+    }
+    for (int64_t i = 0; i < state_elems; ++i) st[i] = (float)s[i];
+    free(s);
+  }
+  return 0;
+}
+
+/* ---- Plan region: slot mapping and batch tables (reference: src/Starlings.Roost.Worker/Eager/PlanRegionWriter.cs:19-64) ---- */
+
+/* Sequences are given as (token_start, token_count, position_offset, kv_length, block list). Writes q_indptr and
+ * cu_seqlens [batch+1], kv_indptr [batch+1], kv_indices, kv_last_page_len [batch] and slot_mapping [tokens]. */
+int oracle_plan_region(int batch, const int32_t* token_start, const int32_t* token_count,
+                       const int32_t* position_offset, const int32_t* kv_length, const int32_t* block_indptr,
+                       const int32_t* blocks, int block_size, int32_t* q_indptr, int32_t* cu_seqlens,
+                       int32_t* kv_indptr, int32_t* kv_indices, int32_t* kv_last_page_len, int64_t* slot_mapping) {
+  int32_t block_at = 0, q_end = 0;
+  for (int b = 0; b < batch; ++b) {
+    q_indptr[b] = token_start[b];
+    cu_seqlens[b] = token_start[b];
+    kv_indptr[b] = block_at;
+    const int32_t nblocks = block_indptr[b + 1] - block_indptr[b];
+    for (int i = 0; i < nblocks; ++i) kv_indices[block_at + i] = blocks[block_indptr[b] + i];
+    block_at += nblocks;
+    kv_last_page_len[b] = kv_length[b] - (nblocks - 1) * block_size;
+    for (int t = 0; t < token_count[b]; ++t) {
+      const int32_t index = token_start[b] + t;
+      const int32_t position = position_offset[b] + t;
+      if (position / block_size >= nblocks) return fail("a position has no block");
+      slot_mapping[index] = (int64_t)blocks[block_indptr[b] + position / block_size] * block_size + position % block_size;
+    }
+    q_end = token_start[b] + token_count[b];
+  }
+  q_indptr[batch] = q_end;
+  cu_seqlens[batch] = q_end;
+  kv_indptr[batch] = block_at;
+  return 0;
+}

@@ -1,0 +1,332 @@
+"""roost_amd -- host side of the MI355X (gfx950) Roost attention + Gated DeltaNet kernel library.
+
+The product is ``libroost_kernels_gfx950.so`` (built from ``roost_amd/csrc`` by ``roost_amd/build.py``), exporting
+Roost's C ABI 1.3. This package is the Python mirror of the reference's host interface for that library:
+
+* ``KernelLibrary`` mirrors ``Starlings.Roost.Kernels.KernelLibrary`` (reference src/Starlings.Roost.Kernels/
+  KernelLibrary.cs:107-373): load by exports, check the ABI version, read the registration table with its
+  ``entry_size`` stride, refuse a NEEDS_PLAN/plan disagreement, create the context;
+* ``OpSession`` mirrors ``CudaOpsSession.Launch`` (src/Starlings.Roost.Worker/Eager/CudaOpsSession.cs:184-254): query
+  the workspace, (re)allocate it when it does not fit, ``plan()`` when the variant needs one, then ``run()`` on the
+  session's stream;
+* ``paged_attention``, ``cache_write`` and ``gated_delta_rule`` mirror ``CudaOps.PagedAttention / CacheWrite /
+  GatedDeltaRule`` (src/Starlings.Roost.Worker/Eager/CudaOps.cs:106-144, 251-272; CudaOps.Hybrid.cs:9-40): they fill
+  the params struct from tensors and pick the variant the worker would pick.
+
+PyTorch is used only for device memory and streams. There is no fallback: if the library is missing or fails to load,
+every call raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from pathlib import Path
+from typing import Optional
+
+from . import abi
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "libroost_kernels_gfx950.so"
+
+RECURRENT_VARIANT = "gated-delta-rule-recurrent-aot"
+CHUNK_VARIANT = "gated-delta-rule-chunk-gfx950"
+ATTENTION_VARIANT = "paged-attention-gfx950"
+CACHE_WRITE_VARIANT = "cache-write-gfx950"
+
+
+class KernelError(RuntimeError):
+    def __init__(self, op: str, status: int, message: str):
+        name = abi.STATUS_NAMES[status] if 0 <= status < len(abi.STATUS_NAMES) else str(status)
+        super().__init__(f"{op}: {name} ({status}): {message}")
+        self.status = status
+
+
+@dataclass
+class Entry:
+    op: int
+    flags: int
+    variant_id: str
+    params_struct_size: int
+    params_abi_minor: int
+    constraints: abi.Constraints
+    run: Optional[abi.RunFn]
+    plan: Optional[abi.PlanFn]
+    workspace: Optional[abi.WorkspaceFn]
+
+    @property
+    def needs_plan(self) -> bool:
+        return bool(self.flags & abi.FLAG_NEEDS_PLAN)
+
+
+class KernelLibrary:
+    """The loaded library: exports, registration table and last-error text."""
+
+    EXPORTS = ("roost_abi_version", "roost_last_error", "roost_register", "roost_context_create",
+               "roost_context_destroy")
+
+    def __init__(self, path: Path | str = LIB_PATH):
+        path = Path(path)
+        if not path.exists():
+            raise FileNotFoundError(f"{path} is missing: run `python -m roost_amd.build` (or __graft_entry__.build())")
+        self.path = path
+        # The library must share the process's HIP runtime (streams and device pointers pass between them). In a
+        # Python host that runtime is the one PyTorch loads: its libamdhip64 carries the soname libamdhip64.so.7, so
+        # loading torch first makes the library's DT_NEEDED entry bind to it instead of a second copy.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
+        self.dll = C.CDLL(str(path))
+        for name in self.EXPORTS:
+            if not hasattr(self.dll, name):
+                raise RuntimeError(f"{path}: export {name} is missing")
+        self.dll.roost_abi_version.restype = C.c_uint32
+        self.dll.roost_last_error.restype = C.c_char_p
+        self.dll.roost_register.argtypes = [C.POINTER(abi.OpTable)]
+        self.dll.roost_register.restype = C.c_int32
+        self.dll.roost_context_create.argtypes = [C.POINTER(abi.ContextCreateParams), C.POINTER(C.c_void_p)]
+        self.dll.roost_context_create.restype = C.c_int32
+        self.dll.roost_context_destroy.argtypes = [C.c_void_p]
+        self.dll.roost_context_destroy.restype = C.c_int32
+        version = self.dll.roost_abi_version()
+        if version >> 16 != abi.ABI_MAJOR or (version & 0xFFFF) < abi.ABI_MINOR:
+            raise RuntimeError(f"{path}: ABI {version >> 16}.{version & 0xFFFF} is not {abi.ABI_MAJOR}.{abi.ABI_MINOR}")
+        self.table = abi.new(abi.OpTable)
+        status = self.dll.roost_register(C.byref(self.table))
+        if status != abi.OK:
+            raise KernelError("roost_register", status, self.last_error())
+        self.library_name = self.table.library_name.decode()
+        self.entries: list[Entry] = []
+        base = self.table.entries
+        seen = set()
+        for i in range(self.table.entry_count):
+            raw = abi.OpEntry.from_address(base + i * self.table.entry_size)
+            vid = raw.variant_id.decode()
+            if (raw.op, vid) in seen:
+                raise RuntimeError(f"duplicate variant {vid}")
+            seen.add((raw.op, vid))
+            if bool(raw.flags & abi.FLAG_NEEDS_PLAN) != bool(raw.plan):
+                raise RuntimeError(f"variant {vid}: NEEDS_PLAN and the plan entry point disagree")
+            self.entries.append(Entry(
+                raw.op, raw.flags, vid, raw.params_struct_size, raw.params_abi_minor, raw.constraints,
+                abi.RunFn(raw.run) if raw.run else None, abi.PlanFn(raw.plan) if raw.plan else None,
+                abi.WorkspaceFn(raw.workspace) if raw.workspace else None))
+
+    def last_error(self) -> str:
+        return self.dll.roost_last_error().decode(errors="replace")
+
+    def entry(self, variant_id: str) -> Entry:
+        for e in self.entries:
+            if e.variant_id == variant_id:
+                return e
+        raise KeyError(f"variant {variant_id} is not registered by {self.library_name}")
+
+    def create_context(self, device: int = 0, flags: int = 0) -> C.c_void_p:
+        p = abi.new(abi.ContextCreateParams)
+        p.device = device
+        p.flags = flags
+        ctx = C.c_void_p()
+        status = self.dll.roost_context_create(C.byref(p), C.byref(ctx))
+        if status != abi.OK:
+            raise KernelError("roost_context_create", status, self.last_error())
+        return ctx
+
+    def destroy_context(self, ctx: C.c_void_p) -> None:
+        self.dll.roost_context_destroy(ctx)
+
+
+_LIBRARY: Optional[KernelLibrary] = None
+
+
+def library() -> KernelLibrary:
+    """The process-wide library (loaded on first use; raises if it is not built)."""
+    global _LIBRARY
+    if _LIBRARY is None:
+        _LIBRARY = KernelLibrary()
+    return _LIBRARY
+
+
+# ---- tensors -> spans -------------------------------------------------------------------------------------------------
+
+def _torch():
+    import torch  # noqa: WPS433 -- torch is plumbing for device memory and streams
+    return torch
+
+
+def dtype_of(t) -> int:
+    torch = _torch()
+    return {torch.float32: abi.DTYPE_F32, torch.float16: abi.DTYPE_F16, torch.bfloat16: abi.DTYPE_BF16,
+            torch.float64: abi.DTYPE_F64, torch.int32: abi.DTYPE_I32, torch.int64: abi.DTYPE_I64}[t.dtype]
+
+
+def span(t, *, length: Optional[int] = None, dtype: Optional[int] = None, offset_elems: int = 0) -> abi.DeviceSpan:
+    """A RoostDeviceSpan over tensor t (optionally a sub-range starting offset_elems in)."""
+    s = abi.DeviceSpan()
+    if t is None:
+        return s
+    s.address = t.data_ptr() + offset_elems * t.element_size()
+    s.length = t.numel() - offset_elems if length is None else length
+    s.dtype = dtype_of(t) if dtype is None else dtype
+    return s
+
+
+def host_ptr(a) -> Optional[int]:
+    """Address of a host (numpy or CPU tensor) int32 table, or None."""
+    if a is None:
+        return None
+    if hasattr(a, "data_ptr"):
+        assert not a.is_cuda
+        return a.data_ptr()
+    return a.ctypes.data
+
+
+class OpSession:
+    """One context + stream: workspace query, allocation, plan and run, as the worker's CudaOpsSession does."""
+
+    def __init__(self, lib: Optional[KernelLibrary] = None, device: int = 0, stream=None):
+        torch = _torch()
+        if not torch.cuda.is_available():
+            raise RuntimeError("OpSession needs a GPU (the gfx950 library has no CPU path)")
+        self.lib = lib or library()
+        self.device = torch.device("cuda", device)
+        self.stream = stream or torch.cuda.current_stream(self.device)
+        self.ctx = self.lib.create_context(device)
+        self._ws = {}  # (variant, key) -> [device tensor, pinned tensor, plan buffer, Workspace, event]
+
+    @property
+    def stream_handle(self) -> int:
+        return self.stream.cuda_stream
+
+    def workspace_sizes(self, entry: Entry, params) -> abi.WorkspaceSizes:
+        sizes = abi.new(abi.WorkspaceSizes)
+        if entry.workspace is not None:
+            status = entry.workspace(self.ctx, C.addressof(params), C.addressof(sizes))
+            if status != abi.OK:
+                raise KernelError(f"{entry.variant_id} workspace", status, self.lib.last_error())
+        return sizes
+
+    def _workspace(self, entry: Entry, params, key) -> abi.Workspace:
+        torch = _torch()
+        sizes = self.workspace_sizes(entry, params)
+        slot = self._ws.get((entry.variant_id, key))
+        fits = slot is not None and slot[3].device_bytes >= sizes.device_bytes and \
+            slot[3].pinned_host_bytes >= sizes.pinned_host_bytes and slot[3].plan_bytes >= sizes.plan_bytes
+        if not fits:
+            self.stream.synchronize()  # in-flight kernels may still read the old buffers
+            dev = torch.empty(max(int(sizes.device_bytes), 1) + 256, dtype=torch.uint8, device=self.device)
+            pinned = torch.empty(max(int(sizes.pinned_host_bytes), 1), dtype=torch.uint8, pin_memory=True)
+            plan = C.create_string_buffer(max(int(sizes.plan_bytes), 1))
+            ws = abi.new(abi.Workspace)
+            base = dev.data_ptr()
+            ws.device = (base + 255) // 256 * 256
+            ws.device_bytes = sizes.device_bytes
+            ws.pinned_host = pinned.data_ptr()
+            ws.pinned_host_bytes = sizes.pinned_host_bytes
+            ws.plan = C.addressof(plan)
+            ws.plan_bytes = sizes.plan_bytes
+            slot = [dev, pinned, plan, ws, None]
+            self._ws[(entry.variant_id, key)] = slot
+        return slot
+
+    def launch(self, entry: Entry, params, key=0, plan: bool = True) -> None:
+        """Workspace -> (plan) -> run on the session stream."""
+        if entry.workspace is None:
+            self.run(entry, params, None)
+            return
+        slot = self._workspace(entry, params, key)
+        ws = slot[3]
+        if entry.needs_plan and plan:
+            if slot[4] is not None:
+                slot[4].synchronize()  # the previous plan's host->device copy has left the pinned buffer
+            status = entry.plan(self.ctx, C.addressof(params), C.addressof(ws), C.c_void_p(self.stream_handle))
+            if status != abi.OK:
+                raise KernelError(f"{entry.variant_id} plan", status, self.lib.last_error())
+            ev = _torch().cuda.Event()
+            ev.record(self.stream)
+            slot[4] = ev
+        self.run(entry, params, ws)
+
+    def run(self, entry: Entry, params, ws: Optional[abi.Workspace]) -> None:
+        status = self.run_raw(entry, params, ws)
+        if status != abi.OK:
+            raise KernelError(f"{entry.variant_id} run", status, self.lib.last_error())
+
+    def run_raw(self, entry: Entry, params, ws: Optional[abi.Workspace]) -> int:
+        return entry.run(self.ctx, C.addressof(params), C.addressof(ws) if ws is not None else None,
+                         C.c_void_p(self.stream_handle))
+
+    def close(self) -> None:
+        if self.ctx:
+            self.stream.synchronize()
+            self.lib.destroy_context(self.ctx)
+            self.ctx = None
+            self._ws.clear()
+
+
+# ---- op mirrors (CudaOps) ---------------------------------------------------------------------------------------------
+
+def paged_attention_params(q, output, k_cache, v_cache, q_indptr, kv_indptr, kv_indices, kv_last_page_len, *,
+                           q_indptr_host, kv_indptr_host, kv_last_page_len_host, batch, q_heads, kv_heads, head_dim,
+                           page_size, kv_layout=abi.LAYOUT_PAGED_NHD, sm_scale=0.0, causal=True, lse=None,
+                           mode=None, window_left=-1, soft_cap=0.0):
+    """Fills RoostPagedAttentionParams as CudaOps.PagedAttention does: prefill whenever tokens > batch."""
+    tokens = q.shape[0]
+    p = abi.new(abi.PagedAttentionParams)
+    p.q, p.output, p.lse = span(q), span(output), span(lse)
+    p.k_cache, p.v_cache = span(k_cache), span(v_cache)
+    p.q_indptr, p.kv_indptr, p.kv_indices = span(q_indptr), span(kv_indptr), span(kv_indices)
+    p.kv_last_page_len = span(kv_last_page_len)
+    p.q_indptr_host = host_ptr(q_indptr_host)
+    p.kv_indptr_host = host_ptr(kv_indptr_host)
+    p.kv_last_page_len_host = host_ptr(kv_last_page_len_host)
+    p.mode = (abi.ATTENTION_PREFILL if tokens > batch else abi.ATTENTION_DECODE) if mode is None else mode
+    p.batch, p.tokens = batch, tokens
+    p.q_heads, p.kv_heads, p.head_dim = q_heads, kv_heads, head_dim
+    p.page_size, p.kv_layout = page_size, kv_layout
+    p.sm_scale, p.logits_soft_cap, p.window_left, p.causal = sm_scale, soft_cap, window_left, int(causal)
+    return p
+
+
+def paged_attention(session: OpSession, *args, **kwargs) -> None:
+    p = paged_attention_params(*args, **kwargs)
+    session.launch(session.lib.entry(ATTENTION_VARIANT), p, key=(p.mode, p.batch, p.tokens))
+
+
+def cache_write_params(k, v, k_cache, v_cache, slot_mapping, *, kv_heads, head_dim, page_size,
+                       kv_layout=abi.LAYOUT_PAGED_NHD):
+    p = abi.new(abi.CacheWriteParams)
+    p.k, p.v, p.k_cache, p.v_cache, p.slot_mapping = span(k), span(v), span(k_cache), span(v_cache), span(slot_mapping)
+    p.tokens = k.shape[0]
+    p.kv_heads, p.head_dim, p.page_size, p.kv_layout = kv_heads, head_dim, page_size, kv_layout
+    p.k_scale = p.v_scale = 1.0
+    return p
+
+
+def cache_write(session: OpSession, *args, **kwargs) -> None:
+    p = cache_write_params(*args, **kwargs)
+    session.launch(session.lib.entry(CACHE_WRITE_VARIANT), p)
+
+
+def gated_delta_rule_params(q, k, v, g, beta, output, state, state_slots, cu_seqlens, *, batch, tokens, k_heads=16,
+                            v_heads=16, k_dim=128, v_dim=128, q_stride=0, k_stride=0, v_stride=0,
+                            use_initial_state=True, l2_norm_qk=True, scale=0.0, cu_seqlens_host=None,
+                            q_len=None, k_len=None, v_len=None, q_offset=0, k_offset=0, v_offset=0):
+    """Fills RoostGatedDeltaRuleParams. q/k/v may be column views of one fused tensor (offset + stride)."""
+    p = abi.new(abi.GatedDeltaRuleParams)
+    p.q = span(q, length=q_len, offset_elems=q_offset)
+    p.k = span(k, length=k_len, offset_elems=k_offset)
+    p.v = span(v, length=v_len, offset_elems=v_offset)
+    p.g, p.beta, p.output = span(g), span(beta), span(output)
+    p.state, p.state_slots, p.cu_seqlens = span(state), span(state_slots), span(cu_seqlens)
+    p.cu_seqlens_host = host_ptr(cu_seqlens_host)
+    p.batch, p.tokens = batch, tokens
+    p.k_heads, p.v_heads, p.k_dim, p.v_dim = k_heads, v_heads, k_dim, v_dim
+    p.q_stride, p.k_stride, p.v_stride = q_stride, k_stride, v_stride
+    p.use_initial_state, p.l2_norm_qk, p.scale = int(use_initial_state), int(l2_norm_qk), scale
+    return p
+
+
+def gated_delta_rule(session: OpSession, *args, variant: str = RECURRENT_VARIANT, **kwargs) -> None:
+    """CudaOps.GatedDeltaRule runs the recurrent variant for every length; the chunk variant is selectable."""
+    p = gated_delta_rule_params(*args, **kwargs)
+    session.launch(session.lib.entry(variant), p, key=(p.batch, p.tokens))

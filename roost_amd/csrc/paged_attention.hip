@@ -1,0 +1,962 @@
+// PagedAttention (ROOST_OP_PAGED_ATTENTION) for gfx950: paged GQA decode and varlen causal chunked prefill over a
+// block-tabled KV cache, behind the C1 workspace / plan / run entry points.
+//
+// Semantics are CpuOps.PagedAttention (reference: src/Starlings.Roost.Ops/CpuOps.cs:198-298): sequence b has
+// n = q_indptr[b+1]-q_indptr[b] queries and kvLen = (pages-1)*page_size + kv_last_page_len[b] keys; query i sits at
+// key position kvLen-n+i and (causal) sees keys j <= that position; a decode query sees every key; query head h reads
+// KV head h / (q_heads / kv_heads); score = q.k * scale (scale 0 -> 1/sqrt(head_dim)); softmax; sum p*v; a query that
+// sees no key outputs zeros. The entry-point contract is the reference's (kernels/src/paged_attention.cu:78-349):
+// workspace() and plan() read the host batch tables, run() never does and refuses with NOT_PLANNED until plan() has
+// written a plan record for this batch shape. The optional lse output is the base-2 log-sum-exp of the scaled scores,
+// log2(sum_j 2^(s_j * log2 e)), which is the convention of the FlashInfer kernels the reference wraps.
+//
+// Decode (mode DECODE) -- bandwidth bound, no MFMA:
+//   * split-K over fixed 512-token chunks of each sequence; the chunk size depends only on the sequence's own length,
+//     so a row's result does not depend on the rest of the batch (BATCH_INVARIANT) and the fixed merge order makes it
+//     DETERMINISTIC;
+//   * one workgroup = one (chunk, KV head); its 4 wavefronts take 16-token groups in turn; every K/V byte is loaded once
+//     with 16-byte coalesced reads (a 512-byte bf16 row per 32 lanes) straight into registers and shared by the 4 query
+//     heads of the GQA group;
+//   * q.k uses v_dot2 bf16 dot products; the per-(token, head) partial sums are reduce-scattered across the lanes of a
+//     row so that each lane ends with exactly one score; the online-softmax max is a wavefront max-reduction; the
+//     weights are exchanged through a 256-byte LDS slot per wavefront; P.V accumulates in fp32 registers;
+//   * the 4 wavefronts merge through LDS; a sequence with several chunks writes fp32 partials (o, m, l) that a small
+//     merge kernel combines in chunk order.
+// Prefill (mode PREFILL) -- MFMA bound:
+//   * one workgroup = 32 query tokens x the 4 query heads of one KV head (one wavefront per head), all sharing each
+//     64-key K and V tile staged in LDS (K row-major, V transposed so both MFMA operands read contiguous LDS);
+//   * S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_32x32x16_bf16 with fp32 accumulation; with queries on the MFMA N axis
+//     the softmax statistics of a query live in one lane pair, so the online softmax needs one cross-lane exchange per
+//     tile; P is rounded to bf16 before the P.V product (as FlashAttention-2 does);
+//   * plan() orders the (tile, KV head) work items longest-first so the ragged causal tail does not set the makespan.
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <type_traits>
+#include <vector>
+
+#include "common.h"
+
+namespace {
+
+using namespace roost_dev;
+
+constexpr uint32_t kGroup = 4;                  // query heads per KV head (Qwen3.5: 8 over 2)
+constexpr uint32_t kDecodeChunkTokens = 512;    // split-K chunk
+constexpr uint32_t kPrefillTileQ = 32;          // query tokens per prefill workgroup
+constexpr uint32_t kPrefillTileK = 64;          // keys per LDS tile
+constexpr uint32_t kAlign = 256;
+constexpr uint32_t kPlanMagic = 0x41504752;     // "RGPA"
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct DecodeWork {
+  int32_t seq;
+  int32_t page_begin;  // first page entry of the chunk, relative to the sequence
+  int32_t token_begin; // first key of the chunk
+  int32_t split;       // partial slot, or -1 when the sequence has a single chunk
+};
+struct SeqSplits {
+  int32_t first;  // first partial slot
+  int32_t count;  // chunks of the sequence (0: no keys)
+};
+struct PrefillWork {
+  int32_t seq;
+  int32_t q0;  // first query of the tile, relative to the sequence
+  int32_t kv_head;
+  int32_t reserved;
+};
+
+// What plan() leaves for run(); trivially copyable, read back with memcpy.
+struct PlanRecord {
+  uint32_t magic;
+  uint32_t mode;
+  uint32_t batch;
+  uint32_t tokens;
+  uint32_t page_size;
+  uint32_t kv_layout;
+  uint32_t head_dim;
+  uint32_t kv_heads;
+  uint64_t pages;        // kv_indptr_host[batch]
+  uint64_t work_items;
+  uint64_t splits;       // decode partial slots
+  uint64_t int_bytes;    // [work items | seq splits]
+  uint64_t float_offset; // partials start here
+  uint64_t float_bytes;
+};
+
+struct Layout {
+  uint64_t work_items = 0;
+  uint64_t splits = 0;
+  uint64_t seq_offset = 0;  // byte offset of SeqSplits in the int region
+  uint64_t int_bytes = 0;
+  uint64_t float_offset = 0;
+  uint64_t float_bytes = 0;
+  uint64_t total = 0;
+};
+
+// ---- Validation (reference: kernels/src/paged_attention.cu:78-130) ------------------------------------------------
+
+RoostStatus Validate(const RoostPagedAttentionParams& p, bool for_run) {
+  using roost::Fail;
+  constexpr char kOp[] = "PagedAttention";
+  if (p.mode != ROOST_ATTENTION_DECODE && p.mode != ROOST_ATTENTION_PREFILL) {
+    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: mode must be DECODE or PREFILL");
+  }
+  if (p.head_dim != 64 && p.head_dim != 128 && p.head_dim != 256) {
+    return Fail(ROOST_STATUS_UNSUPPORTED, "PagedAttention: head_dim must be 64, 128 or 256");
+  }
+  if (p.mode == ROOST_ATTENTION_PREFILL && p.head_dim != 256) {
+    return Fail(ROOST_STATUS_UNSUPPORTED, "PagedAttention: prefill is built for head_dim 256");
+  }
+  if (p.kv_heads == 0 || p.q_heads != p.kv_heads * kGroup) {
+    return Fail(ROOST_STATUS_UNSUPPORTED, "PagedAttention: only 4 query heads per KV head are built");
+  }
+  if (p.window_left != -1) {
+    return Fail(ROOST_STATUS_UNSUPPORTED, "PagedAttention: sliding window is not built (window_left must be -1)");
+  }
+  if (p.logits_soft_cap != 0.0f) return Fail(ROOST_STATUS_UNSUPPORTED, "PagedAttention: logit soft capping is not built");
+  if (p.kv_layout != ROOST_LAYOUT_PAGED_NHD && p.kv_layout != ROOST_LAYOUT_PAGED_HND) {
+    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: kv_layout must be PAGED_NHD or PAGED_HND");
+  }
+  if (p.batch == 0 || p.page_size == 0) {
+    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: batch and page_size must be non-zero");
+  }
+  if (p.mode == ROOST_ATTENTION_DECODE && p.tokens != p.batch) {
+    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: decode takes exactly one query token per sequence");
+  }
+  if (!for_run) {
+    if (p.q_indptr_host == nullptr || p.kv_indptr_host == nullptr) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: q_indptr_host and kv_indptr_host are required");
+    }
+    if (p.q_indptr_host[0] != 0 || p.q_indptr_host[p.batch] != static_cast<int32_t>(p.tokens)) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: q_indptr_host must start at 0 and end at tokens");
+    }
+    if (p.kv_indptr_host[0] != 0) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: kv_indptr_host must start at 0 and not decrease");
+    }
+    for (uint32_t b = 0; b < p.batch; ++b) {
+      if (p.q_indptr_host[b + 1] < p.q_indptr_host[b] || p.kv_indptr_host[b + 1] < p.kv_indptr_host[b]) {
+        return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: q_indptr_host and kv_indptr_host must not decrease");
+      }
+      if (p.kv_last_page_len_host != nullptr && p.kv_indptr_host[b + 1] > p.kv_indptr_host[b]) {
+        const int32_t last = p.kv_last_page_len_host[b];
+        if (last < 1 || last > static_cast<int32_t>(p.page_size)) {
+          return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: kv_last_page_len_host outside [1, page_size]");
+        }
+      }
+      if (p.mode == ROOST_ATTENTION_PREFILL && p.causal && p.kv_last_page_len_host != nullptr) {
+        // CpuOps refuses a causal sequence with fewer keys than queries (reference CpuOps.cs:326-329).
+        const int64_t pages = p.kv_indptr_host[b + 1] - p.kv_indptr_host[b];
+        const int64_t kv = pages == 0 ? 0 : (pages - 1) * p.page_size + p.kv_last_page_len_host[b];
+        if (kv < p.q_indptr_host[b + 1] - p.q_indptr_host[b]) {
+          return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: a causal sequence has fewer keys than queries");
+        }
+      }
+    }
+    return ROOST_STATUS_OK;
+  }
+  const uint32_t dt = p.q.dtype;
+  if (dt != ROOST_DTYPE_BF16 && dt != ROOST_DTYPE_F32) {
+    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: q must be bf16 (or f32 for decode)");
+  }
+  if (dt == ROOST_DTYPE_F32 && p.mode == ROOST_ATTENTION_PREFILL) {
+    return Fail(ROOST_STATUS_UNSUPPORTED, "PagedAttention: f32 prefill is not built (bf16 MFMA only)");
+  }
+  const uint64_t q_elems = static_cast<uint64_t>(p.tokens) * p.q_heads * p.head_dim;
+  ROOST_TRY(roost::CheckSpan(p.q, dt, q_elems, kOp, "q"));
+  ROOST_TRY(roost::CheckSpan(p.output, dt, q_elems, kOp, "output"));
+  ROOST_TRY(roost::CheckSpan(p.lse, ROOST_DTYPE_F32, static_cast<uint64_t>(p.tokens) * p.q_heads, kOp, "lse", true));
+  const uint64_t page_elems = static_cast<uint64_t>(p.page_size) * p.kv_heads * p.head_dim;
+  ROOST_TRY(roost::CheckSpan(p.k_cache, dt, page_elems, kOp, "k_cache"));
+  ROOST_TRY(roost::CheckSpan(p.v_cache, dt, page_elems, kOp, "v_cache"));
+  ROOST_TRY(roost::CheckSpan(p.q_indptr, ROOST_DTYPE_I32, p.batch + 1ull, kOp, "q_indptr"));
+  ROOST_TRY(roost::CheckSpan(p.kv_indptr, ROOST_DTYPE_I32, p.batch + 1ull, kOp, "kv_indptr"));
+  ROOST_TRY(roost::CheckSpan(p.kv_last_page_len, ROOST_DTYPE_I32, p.batch, kOp, "kv_last_page_len"));
+  if (!roost::Aligned(p.q.address, 16) || !roost::Aligned(p.output.address, 16) ||
+      !roost::Aligned(p.k_cache.address, 16) || !roost::Aligned(p.v_cache.address, 16)) {
+    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: q, output and the KV pools must be 16-byte aligned");
+  }
+  return ROOST_STATUS_OK;
+}
+
+// ---- Host planning ---------------------------------------------------------------------------------------------------
+
+Layout MakeLayout(uint64_t work_items, uint64_t splits, uint64_t batch, uint32_t q_heads, uint32_t head_dim,
+                  uint32_t mode) {
+  Layout l;
+  l.work_items = work_items;
+  l.splits = splits;
+  const uint64_t item_bytes = mode == ROOST_ATTENTION_DECODE ? sizeof(DecodeWork) : sizeof(PrefillWork);
+  l.seq_offset = roost::AlignUp(work_items * item_bytes, 16);
+  l.int_bytes = l.seq_offset + (mode == ROOST_ATTENTION_DECODE ? batch * sizeof(SeqSplits) : 0);
+  l.float_offset = roost::AlignUp(l.int_bytes, kAlign);
+  l.float_bytes = splits * q_heads * (static_cast<uint64_t>(head_dim) + 2) * sizeof(float);
+  l.total = l.float_offset + l.float_bytes;
+  return l;
+}
+
+uint32_t KvLenHost(const RoostPagedAttentionParams& p, uint32_t b) {
+  const int64_t pages = p.kv_indptr_host[b + 1] - p.kv_indptr_host[b];
+  if (pages <= 0) return 0;
+  const int64_t last = p.kv_last_page_len_host != nullptr ? p.kv_last_page_len_host[b] : p.page_size;
+  return static_cast<uint32_t>((pages - 1) * p.page_size + last);
+}
+
+// Decode: one work item per 512-token chunk. Writes items and per-sequence split tables into `host` when non-NULL.
+Layout PlanDecode(const RoostPagedAttentionParams& p, unsigned char* host) {
+  uint64_t items = 0, splits = 0;
+  std::vector<SeqSplits> seqs(p.batch);
+  for (uint32_t b = 0; b < p.batch; ++b) {
+    const uint32_t kv = KvLenHost(p, b);
+    const uint32_t chunks = static_cast<uint32_t>(roost::CeilDiv(kv, kDecodeChunkTokens));
+    seqs[b].count = static_cast<int32_t>(chunks);
+    seqs[b].first = chunks > 1 ? static_cast<int32_t>(splits) : -1;
+    items += chunks;
+    if (chunks > 1) splits += chunks;
+  }
+  Layout l = MakeLayout(items, splits, p.batch, p.q_heads, p.head_dim, ROOST_ATTENTION_DECODE);
+  if (host != nullptr) {
+    auto* w = reinterpret_cast<DecodeWork*>(host);
+    uint64_t i = 0;
+    for (uint32_t b = 0; b < p.batch; ++b) {
+      for (int32_t c = 0; c < seqs[b].count; ++c) {
+        const int32_t tok = c * static_cast<int32_t>(kDecodeChunkTokens);
+        w[i++] = DecodeWork{static_cast<int32_t>(b), tok / static_cast<int32_t>(p.page_size), tok,
+                            seqs[b].count > 1 ? seqs[b].first + c : -1};
+      }
+    }
+    std::memcpy(host + l.seq_offset, seqs.data(), seqs.size() * sizeof(SeqSplits));
+  }
+  return l;
+}
+
+// Prefill: one work item per (32-query tile, KV head), longest first.
+Layout PlanPrefill(const RoostPagedAttentionParams& p, unsigned char* host) {
+  struct Item {
+    PrefillWork w;
+    uint64_t cost;
+  };
+  std::vector<Item> items;
+  for (uint32_t b = 0; b < p.batch; ++b) {
+    const int64_t n = p.q_indptr_host[b + 1] - p.q_indptr_host[b];
+    const int64_t kv = KvLenHost(p, b);
+    for (int64_t q0 = 0; q0 < n; q0 += kPrefillTileQ) {
+      const int64_t last = std::min<int64_t>(q0 + kPrefillTileQ, n) - 1;
+      int64_t keys = p.causal ? std::min<int64_t>(kv, kv - n + last + 1) : kv;
+      if (keys < 0) keys = 0;
+      for (uint32_t h = 0; h < p.kv_heads; ++h) {
+        items.push_back(Item{PrefillWork{static_cast<int32_t>(b), static_cast<int32_t>(q0), static_cast<int32_t>(h), 0},
+                             static_cast<uint64_t>(keys) + 64});
+      }
+    }
+  }
+  std::stable_sort(items.begin(), items.end(), [](const Item& a, const Item& b) { return a.cost > b.cost; });
+  Layout l = MakeLayout(items.size(), 0, p.batch, p.q_heads, p.head_dim, ROOST_ATTENTION_PREFILL);
+  if (host != nullptr) {
+    auto* w = reinterpret_cast<PrefillWork*>(host);
+    for (size_t i = 0; i < items.size(); ++i) w[i] = items[i].w;
+  }
+  return l;
+}
+
+Layout PlanLayout(const RoostPagedAttentionParams& p, unsigned char* host) {
+  return p.mode == ROOST_ATTENTION_DECODE ? PlanDecode(p, host) : PlanPrefill(p, host);
+}
+
+// ---- Device helpers --------------------------------------------------------------------------------------------------
+
+struct KvView {
+  const void* k;
+  const void* v;
+  const int32_t* kv_indptr;
+  const int32_t* kv_indices;
+  const int32_t* last_len;
+  uint64_t pool_pages;  // pages the pools hold; page ids outside [0, pool_pages) are skipped
+  uint32_t page_size;
+  uint32_t kv_heads;
+  uint32_t hnd;
+};
+
+__device__ __forceinline__ uint32_t SeqKvLen(const KvView& kv, int32_t b, int32_t* p0) {
+  const int32_t a = kv.kv_indptr[b];
+  const int32_t e = kv.kv_indptr[b + 1];
+  *p0 = a;
+  const int32_t pages = e - a;
+  if (pages <= 0) return 0;
+  int32_t last = kv.last_len[b];
+  last = last < 1 ? 1 : (last > static_cast<int32_t>(kv.page_size) ? static_cast<int32_t>(kv.page_size) : last);
+  return static_cast<uint32_t>((pages - 1) * static_cast<int32_t>(kv.page_size) + last);
+}
+
+// Element offset of key `j` of a sequence (page table starting at entry p0) for KV head h, or -1 when its page id is
+// outside the pool (a released or corrupt entry: the key is treated as absent instead of faulting).
+template <int D>
+__device__ __forceinline__ int64_t KeyRow(const KvView& kv, int32_t p0, uint32_t j, uint32_t h) {
+  const uint32_t pi = j / kv.page_size;
+  const uint32_t off = j - pi * kv.page_size;
+  const int32_t page = kv.kv_indices[p0 + pi];
+  if (page < 0 || static_cast<uint64_t>(page) >= kv.pool_pages) return -1;
+  const uint64_t pg = static_cast<uint64_t>(page);
+  const uint64_t row = kv.hnd ? (pg * kv.kv_heads + h) * kv.page_size + off : (pg * kv.page_size + off) * kv.kv_heads + h;
+  return static_cast<int64_t>(row * D);
+}
+
+// Branch-free form for the prefill tile loads: key j (clamped into [0, key_end)) always yields a loadable offset;
+// *ok says whether the key exists (j < key_end and its page id is inside the pool).
+template <int D>
+__device__ __forceinline__ uint64_t KeyRowSafe(const KvView& kv, int32_t p0, int32_t j, int32_t key_end, uint32_t h,
+                                               bool* ok) {
+  const uint32_t jc = static_cast<uint32_t>(min(j, key_end - 1));
+  const uint32_t pi = jc / kv.page_size;
+  const uint32_t off = jc - pi * kv.page_size;
+  const int32_t page = kv.kv_indices[p0 + pi];
+  const bool good = j < key_end && page >= 0 && static_cast<uint64_t>(page) < kv.pool_pages;
+  *ok = good;
+  const uint64_t pg = good ? static_cast<uint64_t>(page) : 0;
+  const uint64_t row = kv.hnd ? (pg * kv.kv_heads + h) * kv.page_size + off : (pg * kv.page_size + off) * kv.kv_heads + h;
+  return good ? row * D : 0;
+}
+
+template <typename T>
+struct Vec;  // 16-byte vector of T, widened to float
+template <>
+struct Vec<uint16_t> {  // bf16
+  static constexpr int N = 8;
+  __device__ static void Widen(const uint4& r, float* f) {
+    f[0] = Bf16LoToF32(r.x); f[1] = Bf16HiToF32(r.x);
+    f[2] = Bf16LoToF32(r.y); f[3] = Bf16HiToF32(r.y);
+    f[4] = Bf16LoToF32(r.z); f[5] = Bf16HiToF32(r.z);
+    f[6] = Bf16LoToF32(r.w); f[7] = Bf16HiToF32(r.w);
+  }
+  __device__ static uint16_t Narrow(float x) { return F32ToBf16(x); }
+};
+template <>
+struct Vec<float> {
+  static constexpr int N = 4;
+  __device__ static void Widen(const uint4& r, float* f) {
+    f[0] = __uint_as_float(r.x); f[1] = __uint_as_float(r.y);
+    f[2] = __uint_as_float(r.z); f[3] = __uint_as_float(r.w);
+  }
+  __device__ static float Narrow(float x) { return x; }
+};
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Partial dot product of a 16-byte K vector with the matching 16 bytes of q (both bf16; q kept as packed pairs).
+__device__ __forceinline__ float Dot16(const uint4& k, const uint32_t* q, float acc) {
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, k.x), __builtin_bit_cast(bf16x2_t, q[0]), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, k.y), __builtin_bit_cast(bf16x2_t, q[1]), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, k.z), __builtin_bit_cast(bf16x2_t, q[2]), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, k.w), __builtin_bit_cast(bf16x2_t, q[3]), acc, false);
+  return acc;
+}
+__device__ __forceinline__ float Dot16(const uint4& k, const float* q, float acc) {
+  acc = fmaf(__uint_as_float(k.x), q[0], acc);
+  acc = fmaf(__uint_as_float(k.y), q[1], acc);
+  acc = fmaf(__uint_as_float(k.z), q[2], acc);
+  acc = fmaf(__uint_as_float(k.w), q[3], acc);
+  return acc;
+}
+
+__device__ __forceinline__ float ShflXor(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+// x[i] for a runtime i in [0, 4) without indexing a register array (which would spill it to scratch).
+__device__ __forceinline__ float Pick4(const float* x, int i) {
+  return i == 0 ? x[0] : (i == 1 ? x[1] : (i == 2 ? x[2] : x[3]));
+}
+
+// ---- Decode kernel ---------------------------------------------------------------------------------------------------
+
+template <typename T, int D>
+struct DecodeCfg {
+  static constexpr int kVec = Vec<T>::N;            // elements per 16-byte vector
+  static constexpr int kLpr = D / kVec;              // lanes per K/V row
+  static constexpr int kTpi = 64 / kLpr;             // rows (tokens) per wave-wide load
+  static constexpr int kNi = 16 / kTpi;              // loads per 16-token group per lane
+  static constexpr int kQWords = sizeof(T) == 2 ? kVec / 2 : kVec;  // q registers per head
+  static_assert(kLpr <= 64 && 64 % kLpr == 0 && 16 % kTpi == 0, "shape");
+  static_assert(kNi * kGroup == kLpr, "each lane must end the reduce-scatter with one (token, head) score");
+};
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256) DecodeKernel(const T* __restrict__ q, T* __restrict__ out, float* __restrict__ lse,
+                                                    KvView kv, const DecodeWork* __restrict__ work,
+                                                    float* __restrict__ part_o, float* __restrict__ part_ml,
+                                                    uint32_t q_heads, float scale_log2) {
+  using C = DecodeCfg<T, D>;
+  constexpr int kVec = C::kVec, kLpr = C::kLpr, kTpi = C::kTpi, kNi = C::kNi;
+  __shared__ float p_lds[4][64];
+  __shared__ float m_lds[4][kGroup];
+  __shared__ float l_lds[4][kGroup];
+  __shared__ float o_lds[4][kGroup][D];
+
+  const DecodeWork wk = work[blockIdx.x];
+  const uint32_t kvh = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r = lane % kLpr;    // which 16-byte slice of a row
+  const int ri = lane / kLpr;   // which row of a wave-wide load
+  const T* kbase = static_cast<const T*>(kv.k);
+  const T* vbase = static_cast<const T*>(kv.v);
+
+  int32_t p0 = 0;
+  const uint32_t kv_len = SeqKvLen(kv, wk.seq, &p0);
+  const uint32_t t_begin = static_cast<uint32_t>(wk.token_begin);
+  const uint32_t t_end = min(kv_len, t_begin + kDecodeChunkTokens);
+
+  // q slice of the 4 heads: for bf16 kept as packed pairs for v_dot2, for f32 as floats.
+  using QW = typename std::conditional<sizeof(T) == 2, uint32_t, float>::type;
+  QW qr[kGroup][C::kQWords];
+  {
+    const T* qrow = q + (static_cast<uint64_t>(wk.seq) * q_heads + kvh * kGroup) * D + r * kVec;
+#pragma unroll
+    for (int h = 0; h < (int)kGroup; ++h) {
+      const uint4 v = *reinterpret_cast<const uint4*>(qrow + h * D);
+      const QW* w = reinterpret_cast<const QW*>(&v);
+#pragma unroll
+      for (int i = 0; i < C::kQWords; ++i) qr[h][i] = w[i];
+    }
+  }
+
+  float acc[kGroup][kVec];
+#pragma unroll
+  for (int h = 0; h < (int)kGroup; ++h)
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) acc[h][e] = 0.0f;
+  float m[kGroup];
+#pragma unroll
+  for (int h = 0; h < (int)kGroup; ++h) m[h] = -INFINITY;
+  float l_lane = 0.0f;
+  const int my_head = r % kGroup;
+
+  for (uint32_t g0 = t_begin + 16u * wave; g0 < t_end; g0 += 64u) {
+    uint4 kr[kNi], vr[kNi];
+    bool valid[kNi];
+#pragma unroll
+    for (int i = 0; i < kNi; ++i) {
+      const uint32_t j = g0 + i * kTpi + ri;
+      int64_t row = j < t_end ? KeyRow<D>(kv, p0, j, kvh) : -1;
+      valid[i] = row >= 0;
+      if (valid[i]) {
+        kr[i] = *reinterpret_cast<const uint4*>(kbase + row + r * kVec);
+        vr[i] = *reinterpret_cast<const uint4*>(vbase + row + r * kVec);
+      } else {
+        kr[i] = make_uint4(0, 0, 0, 0);
+        vr[i] = make_uint4(0, 0, 0, 0);
+      }
+    }
+    // Partial scores s[i*4 + h] over this lane's 16-byte slice.
+    float s[kLpr];
+#pragma unroll
+    for (int i = 0; i < kNi; ++i)
+#pragma unroll
+      for (int h = 0; h < (int)kGroup; ++h) s[i * kGroup + h] = Dot16(kr[i], qr[h], 0.0f);
+    // Reduce-scatter across the kLpr lanes of a row: afterwards lane r holds the full score of index r.
+#pragma unroll
+    for (int mk = kLpr / 2; mk >= 1; mk >>= 1) {
+      const bool upper = (r & mk) != 0;
+#pragma unroll
+      for (int j = 0; j < mk; ++j) {
+        const float send = upper ? s[j] : s[j + mk];
+        const float keep = upper ? s[j + mk] : s[j];
+        s[j] = keep + ShflXor(send, mk);
+      }
+    }
+    const int my_i = r / kGroup;  // load index of the token this lane's score belongs to
+    bool my_valid = false;
+#pragma unroll
+    for (int i = 0; i < kNi; ++i) my_valid = i == my_i ? valid[i] : my_valid;
+    const float sc = my_valid ? s[0] * scale_log2 : -INFINITY;
+    // Group max per head: lanes sharing r % 4.
+    float gm = sc;
+#pragma unroll
+    for (int mk = 4; mk < 64; mk <<= 1) gm = fmaxf(gm, ShflXor(gm, mk));
+    // Every lane learns the max of all 4 heads.
+    float hm[kGroup];
+    {
+      const float x1 = ShflXor(gm, 1), x2 = ShflXor(gm, 2), x3 = ShflXor(gm, 3);
+#pragma unroll
+      for (int h = 0; h < (int)kGroup; ++h) {
+        const int d = h ^ my_head;
+        hm[h] = d == 0 ? gm : (d == 1 ? x1 : (d == 2 ? x2 : x3));
+      }
+    }
+    float corr[kGroup];
+    bool rescale = false;
+#pragma unroll
+    for (int h = 0; h < (int)kGroup; ++h) {
+      const float mn = fmaxf(m[h], hm[h]);
+      corr[h] = mn == -INFINITY ? 1.0f : exp2f(m[h] - mn);
+      rescale |= mn != m[h];
+      m[h] = mn;
+    }
+    const float pw = sc == -INFINITY ? 0.0f : exp2f(sc - Pick4(m, my_head));
+    l_lane = l_lane * Pick4(corr, my_head) + pw;
+    if (rescale) {
+#pragma unroll
+      for (int h = 0; h < (int)kGroup; ++h)
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) acc[h][e] *= corr[h];
+    }
+    // Exchange the weights: lane (ri, r) needs p of index i*4+h for its own row group ri.
+    p_lds[wave][lane] = pw;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float pv[kLpr];
+#pragma unroll
+    for (int i = 0; i < kLpr; i += 4) {
+      const float4 t4 = *reinterpret_cast<const float4*>(&p_lds[wave][ri * kLpr + i]);
+      pv[i] = t4.x; pv[i + 1] = t4.y; pv[i + 2] = t4.z; pv[i + 3] = t4.w;
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 0; i < kNi; ++i) {
+      float vf[kVec];
+      Vec<T>::Widen(vr[i], vf);
+#pragma unroll
+      for (int h = 0; h < (int)kGroup; ++h) {
+        const float w = pv[i * kGroup + h];
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) acc[h][e] = fmaf(w, vf[e], acc[h][e]);
+      }
+    }
+  }
+
+  // Wave: fold the row groups (lanes sharing r) and total the per-lane denominators per head.
+#pragma unroll
+  for (int mk = kLpr; mk < 64; mk <<= 1)
+#pragma unroll
+    for (int h = 0; h < (int)kGroup; ++h)
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) acc[h][e] += ShflXor(acc[h][e], mk);
+  float lsum = l_lane;
+#pragma unroll
+  for (int mk = 4; mk < 64; mk <<= 1) lsum += ShflXor(lsum, mk);
+  if (lane < (int)kGroup) {
+    m_lds[wave][lane] = Pick4(m, lane);
+    l_lds[wave][lane] = lsum;  // lane h holds the total of head h (lanes with r % 4 == h)
+  }
+  if (ri == 0) {
+#pragma unroll
+    for (int h = 0; h < (int)kGroup; ++h)
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) o_lds[wave][h][r * kVec + e] = acc[h][e];
+  }
+  __syncthreads();
+
+  // Workgroup: merge the 4 wavefronts, then write the final row or this chunk's partial.
+  for (int idx = threadIdx.x; idx < (int)(kGroup * D); idx += 256) {
+    const int h = idx / D;
+    const int d = idx - h * D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, m_lds[w][h]);
+    float o = 0.0f, L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float f = m_lds[w][h] == -INFINITY ? 0.0f : exp2f(m_lds[w][h] - M);
+      o += o_lds[w][h][d] * f;
+      L += l_lds[w][h] * f;
+    }
+    const uint32_t qh = kvh * kGroup + h;
+    if (wk.split < 0) {
+      const uint64_t row = static_cast<uint64_t>(wk.seq) * q_heads + qh;
+      out[row * D + d] = Vec<T>::Narrow(L > 0.0f ? o / L : 0.0f);
+      if (lse != nullptr && d == 0) lse[row] = L > 0.0f ? M + log2f(L) : -INFINITY;
+    } else {
+      const uint64_t prow = static_cast<uint64_t>(wk.split) * q_heads + qh;
+      part_o[prow * D + d] = o;
+      if (d == 0) {
+        part_ml[prow * 2] = M;
+        part_ml[prow * 2 + 1] = L;
+      }
+    }
+  }
+}
+
+// Combines the chunks of multi-chunk sequences in chunk order and zero-fills sequences without keys.
+template <typename T, int D>
+__global__ void __launch_bounds__(256) DecodeMergeKernel(T* __restrict__ out, float* __restrict__ lse,
+                                                         const SeqSplits* __restrict__ seqs,
+                                                         const float* __restrict__ part_o,
+                                                         const float* __restrict__ part_ml, uint32_t q_heads) {
+  const uint32_t b = blockIdx.x;
+  const uint32_t qh = blockIdx.y;
+  const SeqSplits s = seqs[b];
+  if (s.count == 1) return;
+  const uint64_t row = static_cast<uint64_t>(b) * q_heads + qh;
+  if (s.count == 0) {
+    for (int d = threadIdx.x; d < D; d += blockDim.x) out[row * D + d] = Vec<T>::Narrow(0.0f);
+    if (lse != nullptr && threadIdx.x == 0) lse[row] = -INFINITY;
+    return;
+  }
+  float M = -INFINITY;
+  for (int c = 0; c < s.count; ++c) M = fmaxf(M, part_ml[(static_cast<uint64_t>(s.first + c) * q_heads + qh) * 2]);
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float o = 0.0f, L = 0.0f;
+    for (int c = 0; c < s.count; ++c) {
+      const uint64_t prow = static_cast<uint64_t>(s.first + c) * q_heads + qh;
+      const float mc = part_ml[prow * 2];
+      const float f = mc == -INFINITY ? 0.0f : exp2f(mc - M);
+      o += part_o[prow * D + d] * f;
+      L += part_ml[prow * 2 + 1] * f;
+    }
+    out[row * D + d] = Vec<T>::Narrow(L > 0.0f ? o / L : 0.0f);
+    if (lse != nullptr && d == 0) lse[row] = L > 0.0f ? M + log2f(L) : -INFINITY;
+  }
+}
+
+// ---- Prefill kernel (bf16, head_dim 256, MFMA) -----------------------------------------------------------------------
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kPD = 256;                 // head_dim
+constexpr int kKStride = kPD + 8;        // K tile row stride in LDS (elements): 528 bytes
+constexpr int kVtStride = kPrefillTileK + 8;  // V^T tile row stride (elements): 144 bytes
+
+__device__ __forceinline__ f32x16_t Mfma32(const u32x4_t& a, const u32x4_t& b, const f32x16_t& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c, 0,
+                                                 0, 0);
+}
+
+__global__ void __launch_bounds__(256, 1)
+    PrefillKernel(const uint16_t* __restrict__ q, uint16_t* __restrict__ out, float* __restrict__ lse, KvView kv,
+                  const int32_t* __restrict__ q_indptr, const PrefillWork* __restrict__ work, uint32_t q_heads,
+                  uint32_t causal, float scale_log2) {
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[kPrefillTileK * kKStride];
+  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kPD * kVtStride];
+
+  const PrefillWork wk = work[blockIdx.x];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int hl = lane >> 5;   // half of the wave
+  const int col = lane & 31;  // MFMA N index: this lane's query within the tile
+  const uint32_t kvh = static_cast<uint32_t>(wk.kv_head);
+  const uint32_t head = kvh * kGroup + wave;
+  const uint16_t* kbase = static_cast<const uint16_t*>(kv.k);
+  const uint16_t* vbase = static_cast<const uint16_t*>(kv.v);
+
+  int32_t p0 = 0;
+  const uint32_t kv_len = SeqKvLen(kv, wk.seq, &p0);
+  const int32_t qbeg = q_indptr[wk.seq];
+  const int32_t n = q_indptr[wk.seq + 1] - qbeg;
+  const int32_t q0 = wk.q0;
+  const int32_t rows = min(static_cast<int32_t>(kPrefillTileQ), n - q0);
+  // Key position of this lane's query, and of the tile's first / last query.
+  const int32_t base_pos = static_cast<int32_t>(kv_len) - n + q0;
+  const int32_t my_pos = base_pos + col;
+  int32_t key_end = static_cast<int32_t>(kv_len);
+  if (causal) key_end = min(key_end, base_pos + rows);  // last query sees keys <= base_pos + rows - 1
+  if (key_end < 0) key_end = 0;
+
+  // Q^T operand: lane holds q[query col][ks*16 + hl*8 .. +8] for ks = 0..15.
+  u32x4_t qreg[16];
+  {
+    const bool ok = col < rows;
+    const uint16_t* qrow = q + (static_cast<uint64_t>(qbeg + q0 + (ok ? col : 0)) * q_heads + head) * kPD + hl * 8;
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) {
+      qreg[ks] = ok ? *reinterpret_cast<const u32x4_t*>(qrow + ks * 16) : u32x4_t{0, 0, 0, 0};
+    }
+  }
+
+  f32x16_t o[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) o[dt][v] = 0.0f;
+  float m_run = -INFINITY;
+  float l_run = 0.0f;
+
+  // K/V of the next 64-key tile are fetched into registers while the current tile is computed (software pipeline).
+  u32x4_t kpre[8];
+  u32x4_t vpre[2][4];
+  auto fetch = [&](int32_t kb) {
+    const u32x4_t zero{0, 0, 0, 0};
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int vi = tid + 256 * it;
+      bool ok;
+      const uint64_t row = KeyRowSafe<kPD>(kv, p0, kb + (vi >> 5), key_end, kvh, &ok);
+      const u32x4_t x = *reinterpret_cast<const u32x4_t*>(kbase + row + (vi & 31) * 8);
+      kpre[it] = ok ? x : zero;
+    }
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int vi = tid + 256 * it;  // 16 groups of 4 keys x 32 slices of 8 dims
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        bool ok;
+        const uint64_t row = KeyRowSafe<kPD>(kv, p0, kb + (vi >> 5) * 4 + t, key_end, kvh, &ok);
+        const u32x4_t x = *reinterpret_cast<const u32x4_t*>(vbase + row + (vi & 31) * 8);
+        vpre[it][t] = ok ? x : zero;
+      }
+    }
+  };
+  if (key_end > 0) fetch(0);
+
+  for (int32_t kb = 0; kb < key_end; kb += kPrefillTileK) {
+    __syncthreads();  // every wavefront is done reading the previous tile
+    // K row-major; V transposed: 4 keys x 8 dims become 8 rows (dims) of 4 keys.
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int vi = tid + 256 * it;
+      *reinterpret_cast<u32x4_t*>(&k_lds[(vi >> 5) * kKStride + (vi & 31) * 8]) = kpre[it];
+    }
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int vi = tid + 256 * it;
+      const int kg = vi >> 5;
+      const int c = vi & 31;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int w = e >> 1;
+        uint32_t k01, k23;
+        if ((e & 1) == 0) {
+          k01 = (vpre[it][0][w] & 0xFFFFu) | (vpre[it][1][w] << 16);
+          k23 = (vpre[it][2][w] & 0xFFFFu) | (vpre[it][3][w] << 16);
+        } else {
+          k01 = (vpre[it][0][w] >> 16) | (vpre[it][1][w] & 0xFFFF0000u);
+          k23 = (vpre[it][2][w] >> 16) | (vpre[it][3][w] & 0xFFFF0000u);
+        }
+        *reinterpret_cast<u32x2_t*>(&vt_lds[(c * 8 + e) * kVtStride + kg * 4]) = u32x2_t{k01, k23};
+      }
+    }
+    __syncthreads();
+    if (kb + static_cast<int32_t>(kPrefillTileK) < key_end) fetch(kb + kPrefillTileK);
+
+    // S^T = K Q^T for two 32-key halves: lane holds keys 8i + 4hl + jj of half kt for query col.
+    f32x16_t s[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) s[kt][v] = 0.0f;
+#pragma unroll
+      for (int ks = 0; ks < 16; ++ks) {
+        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&k_lds[(kt * 32 + col) * kKStride + ks * 16 + hl * 8]);
+        s[kt] = Mfma32(a, qreg[ks], s[kt]);
+      }
+    }
+    // Scale, mask, online softmax for this lane's query.
+    const bool need_mask = (kb + static_cast<int32_t>(kPrefillTileK) > key_end) ||
+                           (causal && kb + static_cast<int32_t>(kPrefillTileK) - 1 > base_pos);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int32_t key = kb + kt * 32 + (v >> 2) * 8 + hl * 4 + (v & 3);
+        float x = s[kt][v] * scale_log2;
+        if (need_mask && (key >= key_end || (causal && key > my_pos))) x = -INFINITY;
+        s[kt][v] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = fmaxf(mx, ShflXor(mx, 32));
+    // Lazy rescaling: the running max only moves when a score exceeds it by more than 2^8, so P stays below 256 (safe
+    // in fp32 and bf16) and the O accumulators are rescaled on a handful of tiles instead of every tile.
+    const bool grow = mx > m_run + 8.0f;
+    if (__any(grow)) {
+      const float m_new = grow ? mx : m_run;
+      const float corr = m_run == -INFINITY ? 0.0f : exp2f(m_run - m_new);
+      l_run *= corr;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[dt][v] *= corr;
+      m_run = m_new;
+    }
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;  // a query with no visible key yet keeps p = 0
+    float psum = 0.0f;
+    u32x4_t pb[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int kt = c >> 1;
+      const int i0 = (c & 1) * 2;
+      float pf[8];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        pf[t] = exp2f(s[kt][i0 * 4 + t] - m_use);
+        pf[4 + t] = exp2f(s[kt][(i0 + 1) * 4 + t] - m_use);
+      }
+#pragma unroll
+      for (int t = 0; t < 8; ++t) psum += pf[t];
+      pb[c] = u32x4_t{PackBf16(pf[0], pf[1]), PackBf16(pf[2], pf[3]), PackBf16(pf[4], pf[5]), PackBf16(pf[6], pf[7])};
+    }
+    l_run += psum;
+    // O^T += V^T P^T: A = V^T rows (dims) with the keys in the order the P^T operand holds them.
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint16_t* vrow = &vt_lds[(dt * 32 + col) * kVtStride + c * 16 + hl * 4];
+        const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vrow);
+        const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vrow + 8);
+        o[dt] = Mfma32(u32x4_t{lo[0], lo[1], hi[0], hi[1]}, pb[c], o[dt]);
+      }
+    }
+  }
+
+  // Normalise and write: lane holds dims dt*32 + 8i + 4hl + jj of query col.
+  const float l_tot = l_run + ShflXor(l_run, 32);
+  if (col < rows) {
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    const uint64_t orow = (static_cast<uint64_t>(qbeg + q0 + col) * q_heads + head) * kPD;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d = dt * 32 + i * 8 + hl * 4;
+        const u32x2_t w{PackBf16(o[dt][i * 4] * inv, o[dt][i * 4 + 1] * inv),
+                        PackBf16(o[dt][i * 4 + 2] * inv, o[dt][i * 4 + 3] * inv)};
+        *reinterpret_cast<u32x2_t*>(out + orow + d) = w;
+      }
+    if (lse != nullptr && hl == 0) {
+      lse[static_cast<uint64_t>(qbeg + q0 + col) * q_heads + head] = l_tot > 0.0f ? m_run + log2f(l_tot) : -INFINITY;
+    }
+  }
+}
+
+template <typename T, int D>
+RoostStatus LaunchDecode(const RoostPagedAttentionParams& p, const PlanRecord& rec, unsigned char* dev, const KvView& kv,
+                         float scale_log2, hipStream_t stream) {
+  const auto* items = reinterpret_cast<const DecodeWork*>(dev);
+  const auto* seqs = reinterpret_cast<const SeqSplits*>(dev + roost::AlignUp(rec.work_items * sizeof(DecodeWork), 16));
+  auto* part_o = reinterpret_cast<float*>(dev + rec.float_offset);
+  auto* part_ml = part_o + rec.splits * p.q_heads * D;
+  auto* out = static_cast<T*>(p.output.address);
+  auto* lse = static_cast<float*>(p.lse.address);
+  if (rec.work_items > 0) {
+    hipLaunchKernelGGL((DecodeKernel<T, D>), dim3(static_cast<uint32_t>(rec.work_items), p.kv_heads), dim3(256), 0,
+                       stream, static_cast<const T*>(p.q.address), out, lse, kv, items, part_o, part_ml, p.q_heads,
+                       scale_log2);
+    ROOST_TRY(roost::FromHip(hipGetLastError(), "PagedAttention decode launch"));
+  }
+  hipLaunchKernelGGL((DecodeMergeKernel<T, D>), dim3(p.batch, p.q_heads), dim3(D < 256 ? D : 256), 0, stream, out, lse,
+                     seqs, part_o, part_ml, p.q_heads);
+  return roost::FromHip(hipGetLastError(), "PagedAttention merge launch");
+}
+
+}  // namespace
+
+extern "C" ROOST_API RoostStatus roost_paged_attention_workspace(RoostContext*, const void* params,
+                                                                 RoostWorkspaceSizes* sizes) {
+  using namespace roost;
+  ROOST_TRY(CheckHeader(params, sizeof(RoostPagedAttentionParams), "PagedAttention"));
+  if (sizes == nullptr) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: sizes is NULL");
+  const auto& p = *static_cast<const RoostPagedAttentionParams*>(params);
+  return Guarded("PagedAttention", [&]() -> RoostStatus {
+    ROOST_TRY(Validate(p, false));
+    const Layout l = PlanLayout(p, nullptr);
+    sizes->device_bytes = l.total;
+    sizes->pinned_host_bytes = l.int_bytes;
+    sizes->plan_bytes = sizeof(PlanRecord);
+    sizes->device_alignment = kAlign;
+    return ROOST_STATUS_OK;
+  });
+}
+
+extern "C" ROOST_API RoostStatus roost_paged_attention_plan(RoostContext*, const void* params, const RoostWorkspace* ws,
+                                                            void* stream) {
+  using namespace roost;
+  ROOST_TRY(CheckHeader(params, sizeof(RoostPagedAttentionParams), "PagedAttention"));
+  const auto& p = *static_cast<const RoostPagedAttentionParams*>(params);
+  return Guarded("PagedAttention", [&]() -> RoostStatus {
+    ROOST_TRY(Validate(p, false));
+    if (ws == nullptr || ws->plan == nullptr) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: plan needs a workspace with a plan record");
+    }
+    const Layout l = PlanLayout(p, nullptr);
+    if (ws->plan_bytes < sizeof(PlanRecord) || ws->device_bytes < l.total || ws->pinned_host_bytes < l.int_bytes ||
+        (l.int_bytes > 0 && ws->pinned_host == nullptr) || (l.total > 0 && ws->device == nullptr) ||
+        !Aligned(ws->device, kAlign)) {
+      return Fail(ROOST_STATUS_WORKSPACE_TOO_SMALL, "PagedAttention: workspace is smaller than the query reported");
+    }
+    auto* host = static_cast<unsigned char*>(ws->pinned_host);
+    if (l.int_bytes > 0) {
+      std::memset(host, 0, l.int_bytes);
+      PlanLayout(p, host);
+      ROOST_TRY(FromHip(hipMemcpyAsync(ws->device, host, l.int_bytes, hipMemcpyHostToDevice, Stream(stream)),
+                        "PagedAttention plan copy"));
+    }
+    PlanRecord rec{};
+    rec.magic = kPlanMagic;
+    rec.mode = p.mode;
+    rec.batch = p.batch;
+    rec.tokens = p.tokens;
+    rec.page_size = p.page_size;
+    rec.kv_layout = p.kv_layout;
+    rec.head_dim = p.head_dim;
+    rec.kv_heads = p.kv_heads;
+    rec.pages = static_cast<uint64_t>(p.kv_indptr_host[p.batch]);
+    rec.work_items = l.work_items;
+    rec.splits = l.splits;
+    rec.int_bytes = l.int_bytes;
+    rec.float_offset = l.float_offset;
+    rec.float_bytes = l.float_bytes;
+    std::memcpy(ws->plan, &rec, sizeof(rec));
+    return ROOST_STATUS_OK;
+  });
+}
+
+extern "C" ROOST_API RoostStatus roost_paged_attention_run(RoostContext*, const void* params, const RoostWorkspace* ws,
+                                                           void* stream) {
+  using namespace roost;
+  ROOST_TRY(CheckHeader(params, sizeof(RoostPagedAttentionParams), "PagedAttention"));
+  const auto& p = *static_cast<const RoostPagedAttentionParams*>(params);
+  return Guarded("PagedAttention", [&]() -> RoostStatus {
+    ROOST_TRY(Validate(p, true));
+    if (ws == nullptr || ws->plan == nullptr || ws->plan_bytes < sizeof(PlanRecord)) {
+      return Fail(ROOST_STATUS_NOT_PLANNED, "PagedAttention: no plan record in the workspace");
+    }
+    PlanRecord rec;
+    std::memcpy(&rec, ws->plan, sizeof(rec));
+    if (rec.magic != kPlanMagic) return Fail(ROOST_STATUS_NOT_PLANNED, "PagedAttention: no plan was made in this workspace");
+    if (rec.mode != p.mode || rec.batch != p.batch || rec.tokens != p.tokens || rec.page_size != p.page_size ||
+        rec.kv_layout != p.kv_layout || rec.head_dim != p.head_dim || rec.kv_heads != p.kv_heads) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: the plan was made for another batch shape");
+    }
+    ROOST_TRY(CheckSpan(p.kv_indices, ROOST_DTYPE_I32, rec.pages, "PagedAttention", "kv_indices"));
+    const uint64_t total = rec.float_offset + rec.float_bytes;
+    if (!DeviceWorkspaceOk(ws, total, kAlign)) {
+      return Fail(ROOST_STATUS_WORKSPACE_TOO_SMALL, "PagedAttention: device workspace is smaller than the plan");
+    }
+    const float scale = p.sm_scale != 0.0f ? p.sm_scale : 1.0f / std::sqrt(static_cast<float>(p.head_dim));
+    const float scale_log2 = scale * kLog2e;
+    KvView kv{};
+    kv.k = p.k_cache.address;
+    kv.v = p.v_cache.address;
+    kv.kv_indptr = static_cast<const int32_t*>(p.kv_indptr.address);
+    kv.kv_indices = static_cast<const int32_t*>(p.kv_indices.address);
+    kv.last_len = static_cast<const int32_t*>(p.kv_last_page_len.address);
+    const uint64_t page_elems = static_cast<uint64_t>(p.page_size) * p.kv_heads * p.head_dim;
+    kv.pool_pages = std::min(p.k_cache.length, p.v_cache.length) / page_elems;
+    kv.page_size = p.page_size;
+    kv.kv_heads = p.kv_heads;
+    kv.hnd = p.kv_layout == ROOST_LAYOUT_PAGED_HND ? 1u : 0u;
+    auto* dev = static_cast<unsigned char*>(ws->device);
+    hipStream_t s = Stream(stream);
+    if (p.mode == ROOST_ATTENTION_DECODE) {
+      const bool bf16 = p.q.dtype == ROOST_DTYPE_BF16;
+      switch (p.head_dim) {
+        case 64: return bf16 ? LaunchDecode<uint16_t, 64>(p, rec, dev, kv, scale_log2, s)
+                             : LaunchDecode<float, 64>(p, rec, dev, kv, scale_log2, s);
+        case 128: return bf16 ? LaunchDecode<uint16_t, 128>(p, rec, dev, kv, scale_log2, s)
+                              : LaunchDecode<float, 128>(p, rec, dev, kv, scale_log2, s);
+        default: return bf16 ? LaunchDecode<uint16_t, 256>(p, rec, dev, kv, scale_log2, s)
+                             : LaunchDecode<float, 256>(p, rec, dev, kv, scale_log2, s);
+      }
+    }
+    if (rec.work_items == 0) return ROOST_STATUS_OK;
+    hipLaunchKernelGGL(PrefillKernel, dim3(static_cast<uint32_t>(rec.work_items)), dim3(256), 0, s,
+                       static_cast<const uint16_t*>(p.q.address), static_cast<uint16_t*>(p.output.address),
+                       static_cast<float*>(p.lse.address), kv, static_cast<const int32_t*>(p.q_indptr.address),
+                       reinterpret_cast<const PrefillWork*>(dev), p.q_heads, p.causal, scale_log2);
+    return FromHip(hipGetLastError(), "PagedAttention prefill launch");
+  });
+}

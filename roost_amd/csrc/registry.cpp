@@ -1,0 +1,167 @@
+// The five C1 exports and the registration table of the gfx950 Roost kernel library.
+//
+// Behaviour follows the reference's registry (kernels/src/registry.cu:60-143): a thread-local last-error string that is
+// never NULL, roost_register() filling a caller-owned RoostOpTable with static entries that live until unload, and
+// roost_context_create()/destroy() managing a per-device context. Unlike the reference there is no cuBLASLt handle and
+// no module loading: every kernel is compiled into this library for gfx950, so a context only records its device.
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstring>
+#include <new>
+#include <string>
+
+#include "common.h"
+
+// The ABI layouts must match the reference header byte for byte (fixture: abi-layout.golden.txt of the reference's
+// Starlings.Roost.Abstractions.Tests). A mismatch fails the build here rather than corrupting a caller's struct.
+static_assert(sizeof(RoostDeviceSpan) == 24 && offsetof(RoostDeviceSpan, dtype) == 16, "RoostDeviceSpan layout");
+static_assert(sizeof(RoostWorkspaceSizes) == 40 && offsetof(RoostWorkspaceSizes, device_alignment) == 32, "sizes");
+static_assert(sizeof(RoostWorkspace) == 56 && offsetof(RoostWorkspace, plan_bytes) == 48, "RoostWorkspace layout");
+static_assert(sizeof(RoostConstraints) == 72 && offsetof(RoostConstraints, group_size_mask) == 64, "constraints");
+static_assert(sizeof(RoostContextCreateParams) == 32 && offsetof(RoostContextCreateParams, stream) == 16, "ctx");
+static_assert(sizeof(RoostOpEntry) == 128 && offsetof(RoostOpEntry, run) == 96 && offsetof(RoostOpEntry, workspace) == 112,
+              "RoostOpEntry layout");
+static_assert(sizeof(RoostOpTable) == 40 && offsetof(RoostOpTable, library_name) == 24, "RoostOpTable layout");
+static_assert(sizeof(RoostPagedAttentionParams) == 296 && offsetof(RoostPagedAttentionParams, q_indptr_host) == 224 &&
+                  offsetof(RoostPagedAttentionParams, mode) == 248 && offsetof(RoostPagedAttentionParams, causal) == 292,
+              "RoostPagedAttentionParams layout");
+static_assert(sizeof(RoostCacheWriteParams) == 160 && offsetof(RoostCacheWriteParams, slot_mapping) == 104 &&
+                  offsetof(RoostCacheWriteParams, v_scale) == 152,
+              "RoostCacheWriteParams layout");
+static_assert(sizeof(RoostGatedDeltaRuleParams) == 280 && offsetof(RoostGatedDeltaRuleParams, cu_seqlens_host) == 224 &&
+                  offsetof(RoostGatedDeltaRuleParams, use_initial_state) == 268 &&
+                  offsetof(RoostGatedDeltaRuleParams, scale) == 276,
+              "RoostGatedDeltaRuleParams layout");
+
+namespace {
+
+thread_local std::string g_last_error;
+
+using roost::DtypeBit;
+
+constexpr uint64_t HeadDimBit(uint32_t d) { return uint64_t{1} << (d / 16 - 1); }
+constexpr uint32_t kPaged = (1u << ROOST_LAYOUT_PAGED_NHD) | (1u << ROOST_LAYOUT_PAGED_HND);
+constexpr uint32_t kAnyPageSize = 0xFFu;  // bit i = page size 2^i: 1 .. 128 tokens
+constexpr uint32_t kGroup4 = 1u << 3;     // 4 query heads per KV head
+
+RoostConstraints BaseConstraints() {
+  RoostConstraints c{};
+  c.sm_min = ROOST_AMD_ARCH_ID;
+  return c;
+}
+
+RoostConstraints AttentionConstraints() {
+  RoostConstraints c = BaseConstraints();
+  c.act_dtype_mask = DtypeBit(ROOST_DTYPE_BF16) | DtypeBit(ROOST_DTYPE_F32);
+  c.kv_dtype_mask = DtypeBit(ROOST_DTYPE_BF16) | DtypeBit(ROOST_DTYPE_F32);
+  c.head_dim_mask = HeadDimBit(64) | HeadDimBit(128) | HeadDimBit(256);
+  c.layout_mask = kPaged;
+  c.page_size_mask = kAnyPageSize;
+  c.min_alignment = 16;
+  c.group_size_mask = kGroup4;
+  return c;
+}
+
+RoostConstraints CacheWriteConstraints() {
+  RoostConstraints c = BaseConstraints();
+  c.act_dtype_mask = DtypeBit(ROOST_DTYPE_BF16) | DtypeBit(ROOST_DTYPE_F16) | DtypeBit(ROOST_DTYPE_F32);
+  c.kv_dtype_mask = c.act_dtype_mask;
+  c.head_dim_mask = ~uint64_t{0};
+  c.layout_mask = kPaged;
+  c.page_size_mask = kAnyPageSize;
+  c.min_alignment = 2;
+  return c;
+}
+
+RoostConstraints GdnConstraints() {
+  RoostConstraints c = BaseConstraints();
+  c.act_dtype_mask = DtypeBit(ROOST_DTYPE_BF16);
+  c.head_dim_mask = HeadDimBit(128);
+  c.layout_mask = 1u << ROOST_LAYOUT_ROW_MAJOR;
+  c.min_alignment = 16;
+  c.group_size_mask = 1u;  // one value head per key head (16 over 16)
+  return c;
+}
+
+RoostOpEntry Entry(uint32_t op, uint32_t flags, const char* id, uint32_t params_size, const RoostConstraints& c,
+                   RoostRunFn run, RoostPlanFn plan, RoostWorkspaceFn workspace) {
+  RoostOpEntry e{};
+  e.op = op;
+  e.flags = flags;
+  e.variant_id = id;
+  e.params_struct_size = params_size;
+  e.params_abi_minor = ROOST_ABI_MINOR;
+  e.constraints = c;
+  e.run = run;
+  e.plan = plan;
+  e.workspace = workspace;
+  return e;
+}
+
+constexpr uint32_t kDet = ROOST_FLAG_DETERMINISTIC | ROOST_FLAG_BATCH_INVARIANT;
+
+const RoostOpEntry* Entries(uint32_t* count) {
+  static const RoostOpEntry entries[] = {
+      Entry(ROOST_OP_PAGED_ATTENTION, kDet | ROOST_FLAG_NEEDS_PLAN, "paged-attention-gfx950",
+            sizeof(RoostPagedAttentionParams), AttentionConstraints(), roost_paged_attention_run,
+            roost_paged_attention_plan, roost_paged_attention_workspace),
+      Entry(ROOST_OP_CACHE_WRITE, kDet | ROOST_FLAG_GRAPH_CAPTURABLE, "cache-write-gfx950", sizeof(RoostCacheWriteParams),
+            CacheWriteConstraints(), roost_cache_write_run, nullptr, nullptr),
+      Entry(ROOST_OP_GATED_DELTA_RULE, kDet | ROOST_FLAG_NEEDS_PLAN, "gated-delta-rule-chunk-gfx950",
+            sizeof(RoostGatedDeltaRuleParams), GdnConstraints(), roost_gdn_chunk_run, roost_gdn_chunk_plan,
+            roost_gdn_chunk_workspace),
+      Entry(ROOST_OP_GATED_DELTA_RULE, kDet | ROOST_FLAG_GRAPH_CAPTURABLE, "gated-delta-rule-recurrent-aot",
+            sizeof(RoostGatedDeltaRuleParams), GdnConstraints(), roost_gdn_recurrent_run, nullptr,
+            roost_gdn_recurrent_workspace),
+  };
+  *count = static_cast<uint32_t>(sizeof(entries) / sizeof(entries[0]));
+  return entries;
+}
+
+}  // namespace
+
+void roost_set_error(const char* message) { g_last_error = message != nullptr ? message : ""; }
+
+extern "C" {
+
+ROOST_API uint32_t roost_abi_version(void) { return ROOST_ABI_VERSION; }
+
+ROOST_API const char* roost_last_error(void) { return g_last_error.c_str(); }
+
+ROOST_API RoostStatus roost_register(RoostOpTable* table) {
+  if (table == nullptr) return roost::Fail(ROOST_STATUS_INVALID_ARGUMENT, "roost_register: table is NULL");
+  if (table->struct_size < sizeof(RoostOpTable) || table->abi_minor > ROOST_ABI_MINOR) {
+    return roost::Fail(ROOST_STATUS_ABI_MISMATCH, "roost_register: table struct_size or abi_minor is not supported");
+  }
+  uint32_t count = 0;
+  const RoostOpEntry* entries = Entries(&count);
+  table->entry_size = static_cast<uint32_t>(sizeof(RoostOpEntry));
+  table->entry_count = count;
+  table->entries = entries;
+  table->library_name = "roost-kernels-gfx950";
+  table->library_abi_major = ROOST_ABI_MAJOR;
+  table->library_abi_minor = ROOST_ABI_MINOR;
+  return ROOST_STATUS_OK;
+}
+
+ROOST_API RoostStatus roost_context_create(const RoostContextCreateParams* params, RoostContext** out) {
+  if (params == nullptr || out == nullptr) {
+    return roost::Fail(ROOST_STATUS_INVALID_ARGUMENT, "roost_context_create: params or out is NULL");
+  }
+  if (params->struct_size < sizeof(RoostContextCreateParams) || params->abi_minor > ROOST_ABI_MINOR) {
+    return roost::Fail(ROOST_STATUS_ABI_MISMATCH, "roost_context_create: params struct_size or abi_minor is not supported");
+  }
+  if (params->reserved0 != 0) return roost::Fail(ROOST_STATUS_INVALID_ARGUMENT, "roost_context_create: reserved0 must be zero");
+  *out = new (std::nothrow) RoostContext{params->device, params->flags};
+  if (*out == nullptr) return roost::Fail(ROOST_STATUS_OUT_OF_MEMORY, "roost_context_create: out of host memory");
+  return ROOST_STATUS_OK;
+}
+
+ROOST_API RoostStatus roost_context_destroy(RoostContext* ctx) {
+  delete ctx;
+  return ROOST_STATUS_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,327 @@
+"""PagedAttention on the GPU through the C ABI vs the CpuOps oracle (reference harness:
+kernels/tests/ops-cuda/AttentionCases.cs:29-288). Tolerances: BASELINE.json's max-abs 2e-2 and max-rel 1e-2 for bf16
+I/O, plus the reference harness's attention-bf16 class; 1e-5 for the fp32 decode of config 1."""
+import ctypes as C
+import zlib
+
+import numpy as np
+import pytest
+
+import cases
+import roost_amd
+from roost_amd import abi
+
+pytestmark = pytest.mark.gpu
+
+
+def torch():
+    import torch as t
+
+    return t
+
+
+def to_dev(a: np.ndarray, bf16=False):
+    t = torch()
+    x = t.from_numpy(np.ascontiguousarray(a))
+    if bf16:
+        x = x.view(t.bfloat16)
+    return x.cuda()
+
+
+def from_dev(x, bf16=False):
+    t = torch()
+    t.cuda.synchronize()
+    if bf16:
+        return x.view(t.int16).cpu().numpy().view(np.uint16)
+    return x.cpu().numpy()
+
+
+class Dev:
+    """A PagedBatch on the device plus its params."""
+
+    def __init__(self, b: cases.PagedBatch, causal=True, with_lse=False):
+        self.b = b
+        self.q = to_dev(b.q, b.bf16)
+        self.k = to_dev(b.k_cache, b.bf16)
+        self.v = to_dev(b.v_cache, b.bf16)
+        self.q_indptr = to_dev(b.q_indptr)
+        self.kv_indptr = to_dev(b.kv_indptr)
+        self.kv_indices = to_dev(b.kv_indices if b.kv_indices.size else np.zeros(1, np.int32))
+        self.last = to_dev(b.kv_last_page_len)
+        self.out = torch().full_like(self.q, float("nan"))
+        self.lse = torch().zeros((b.tokens, b.hq), dtype=torch().float32, device="cuda") if with_lse else None
+        self.causal = causal
+
+    def params(self, host=True, **over):
+        b = self.b
+        kw = dict(q_indptr_host=b.q_indptr if host else None, kv_indptr_host=b.kv_indptr if host else None,
+                  kv_last_page_len_host=b.kv_last_page_len if host else None, batch=b.batch, q_heads=b.hq,
+                  kv_heads=b.hkv, head_dim=b.d, page_size=b.page_size,
+                  kv_layout=abi.LAYOUT_PAGED_HND if b.hnd else abi.LAYOUT_PAGED_NHD, causal=self.causal, lse=self.lse)
+        kw.update(over)
+        return roost_amd.paged_attention_params(self.q, self.out, self.k, self.v, self.q_indptr, self.kv_indptr,
+                                                self.kv_indices, self.last, **kw)
+
+    def result(self):
+        return cases.values(from_dev(self.out, self.b.bf16), self.b.bf16)
+
+
+def run_case(session, b: cases.PagedBatch, causal=True, check_nohost=True, check_determinism=True):
+    d = Dev(b, causal)
+    entry = session.lib.entry(roost_amd.ATTENTION_VARIANT)
+    p = d.params()
+    # Run before plan: NOT_PLANNED (a fresh, zeroed plan record).
+    sizes = session.workspace_sizes(entry, p)
+    ws = abi.new(abi.Workspace)
+    plan_buf = C.create_string_buffer(max(int(sizes.plan_bytes), 1))
+    ws.plan, ws.plan_bytes = C.addressof(plan_buf), sizes.plan_bytes
+    assert session.run_raw(entry, p, ws) == abi.NOT_PLANNED
+    session.launch(entry, p, key=("case", b.batch, b.tokens))
+    got = from_dev(d.out, b.bf16)
+    if check_nohost:
+        # run() never reads the host tables: NULL host pointers give the same bits (AttentionCases.cs:216-224).
+        d.out.fill_(float("nan"))
+        session.run(entry, d.params(host=False), session._ws[(entry.variant_id, ("case", b.batch, b.tokens))][3])
+        assert np.array_equal(from_dev(d.out, b.bf16), got)
+    if check_determinism:
+        d.out.fill_(float("nan"))
+        session.launch(entry, p, key=("case", b.batch, b.tokens))
+        assert np.array_equal(from_dev(d.out, b.bf16), got), "second run is not bit-identical"
+    return cases.values(got, b.bf16)
+
+
+def check_against_oracle(got, b, causal=True):
+    ref = cases.values(cases.oracle_attention(b, causal), b.bf16)
+    a, r = cases.assert_close(got, ref, what="attention")
+    if b.bf16:
+        cases.assert_attention_class(got, ref, float(np.abs(cases.values(b.v_cache, True)).max()), what="attention")
+    return a, r
+
+
+DECODE_CASES = [
+    ("mixed4 NHD ps16", [5, 37, 130, 16], 16, False),
+    ("mixed4 HND ps16", [5, 37, 130, 16], 16, True),
+    ("mixed4 NHD ps32", [5, 37, 130, 16], 32, False),
+    ("mixed4 HND ps64", [5, 37, 130, 16], 64, True),
+    ("single-token-history", [1], 16, False),
+    ("page-multiples", [16, 32, 48, 64], 16, False),
+    ("single-6000 split", [6000], 16, False),
+    ("mixed8", [900, 17, 1, 2048, 333, 64, 1024, 777], 16, False),
+    ("mixed8 HND ps64", [900, 17, 1, 2048, 333, 64, 1024, 777], 64, True),
+    ("odd page size 7", [5, 37, 130, 1000], 7, False),
+]
+
+
+@pytest.mark.parametrize("name,kv_lens,ps,hnd", DECODE_CASES, ids=[c[0] for c in DECODE_CASES])
+def test_decode_bf16_matches_cpuops(session, name, kv_lens, ps, hnd):
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    b = cases.make_paged_batch(rng, kv_lens, [1] * len(kv_lens), page_size=ps, hnd=hnd)
+    got = run_case(session, b)
+    check_against_oracle(got, b)
+
+
+def test_decode_batch64_short(session):
+    rng = np.random.default_rng(64)
+    kv = rng.integers(1, 301, size=64)
+    b = cases.make_paged_batch(rng, kv, [1] * 64)
+    check_against_oracle(run_case(session, b), b)
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_decode_head_dims_bf16(session, d):
+    rng = np.random.default_rng(d)
+    b = cases.make_paged_batch(rng, [3, 700, 40], [1, 1, 1], d=d)
+    check_against_oracle(run_case(session, b), b)
+
+
+def test_config1_fp32_decode_with_kv_append(session):
+    """fp32, hd 64, 8q/2kv, B=4, ctx ~ U(17, 300), page 16, randomly permuted block table into a
+    64-page pool, Q/K/V ~ N(0, 1), scale 1/8; the new token's K/V is appended at its slot-mapped position first."""
+    import oracle
+
+    t = torch()
+    rng = np.random.default_rng(1)
+    kv_lens = rng.integers(17, 301, size=4)
+    b = cases.make_paged_batch(rng, kv_lens, [1] * 4, page_size=16, bf16=False, d=64, pool_factor=None,
+                               spare_pages=64 - sum((int(k) + 15) // 16 for k in kv_lens))
+    assert b.k_cache.shape[0] == 64
+    # Slot mapping of the new token (position kvLen - 1) through the plan-region rule.
+    seqs, start = [], 0
+    for i, kv in enumerate(b.kv_lens):
+        blocks = b.kv_indices[b.kv_indptr[i]:b.kv_indptr[i + 1]]
+        seqs.append(dict(token_start=i, token_count=1, position_offset=kv - 1, kv_length=kv, blocks=blocks))
+    _, _, _, _, _, slots = oracle.plan_region(seqs, 16)
+    new_k = rng.standard_normal((4, 2, 64), dtype=np.float32)
+    new_v = rng.standard_normal((4, 2, 64), dtype=np.float32)
+    k_ref, v_ref = b.k_cache.copy(), b.v_cache.copy()
+    oracle.cache_write(new_k, new_v, k_ref, v_ref, slots, tokens=4, kv_heads=2, head_dim=64, page_size=16)
+    d = Dev(b)
+    roost_amd.cache_write(session, to_dev(new_k), to_dev(new_v), d.k, d.v, to_dev(slots), kv_heads=2, head_dim=64,
+                          page_size=16)
+    assert np.array_equal(from_dev(d.k), k_ref) and np.array_equal(from_dev(d.v), v_ref), "KV append not bit-exact"
+    b.k_cache, b.v_cache = k_ref, v_ref
+    session.launch(session.lib.entry(roost_amd.ATTENTION_VARIANT), d.params(sm_scale=0.125), key="cfg1")
+    got = d.result()
+    out = np.zeros_like(b.q)
+    oracle.paged_attention(b.q, out, k_ref, v_ref, b.q_indptr, b.kv_indptr, b.kv_indices, b.kv_last_page_len, batch=4,
+                           tokens=4, q_heads=8, kv_heads=2, head_dim=64, page_size=16, scale=0.125)
+    cases.assert_close(got, out, max_abs=1e-5, max_rel=1e-5, what="config 1 fp32 decode")
+
+
+def test_config2_decode_full_size(session):
+    """BASELINE config 2 at full size: B=64, ctx ~ U(512, 8192), hd 256, bf16, 0.5*N(0,1), pool 1.25x tokens."""
+    rng = np.random.default_rng(2)
+    kv = rng.integers(512, 8193, size=64)
+    b = cases.make_paged_batch(rng, kv, [1] * 64, std=0.5, pool_factor=1.25)
+    got = run_case(session, b, check_nohost=False)
+    check_against_oracle(got, b)
+
+
+def test_decode_batch_invariance(session):
+    rng = np.random.default_rng(7)
+    b = cases.make_paged_batch(rng, [3000, 17, 900], [1, 1, 1])
+    many = run_case(session, b, check_nohost=False, check_determinism=False)
+    one = cases.PagedBatch(b.q[:1].copy(), b.k_cache, b.v_cache, np.array([0, 1], np.int32),
+                           b.kv_indptr[:2].copy(), b.kv_indices[:b.kv_indptr[1]].copy(), b.kv_last_page_len[:1].copy(),
+                           b.kv_lens[:1], [1], b.page_size, b.hnd, b.bf16)
+    alone = run_case(session, one, check_nohost=False, check_determinism=False)
+    assert np.array_equal(alone, many[:1])
+
+
+def test_decode_lse_is_base2_logsumexp(session):
+    rng = np.random.default_rng(11)
+    b = cases.make_paged_batch(rng, [700, 33], [1, 1])
+    d = Dev(b, with_lse=True)
+    session.launch(session.lib.entry(roost_amd.ATTENTION_VARIANT), d.params(), key="lse")
+    lse = from_dev(d.lse)
+    qv = cases.values(b.q, True)
+    kv = cases.values(b.k_cache, True)
+    for s in range(2):
+        pages = b.kv_indices[b.kv_indptr[s]:b.kv_indptr[s + 1]]
+        keys = kv[pages].reshape(-1, 2, 256)[: b.kv_lens[s]]
+        for h in range(8):
+            sc = keys[:, h // 4, :] @ qv[s, h] / 16.0
+            want = np.log2(np.exp(sc - sc.max()).sum()) + sc.max() / np.log(2)
+            assert abs(lse[s, h] - want) < 1e-3
+
+
+def test_decode_zero_length_sequence_outputs_zeros(session):
+    rng = np.random.default_rng(5)
+    b = cases.make_paged_batch(rng, [40, 0, 17], [1, 1, 1])
+    got = run_case(session, b, causal=False, check_nohost=False)
+    assert np.all(got[1] == 0)
+    check_against_oracle(got, b, causal=False)
+
+
+PREFILL_CASES = [
+    ("one-token", [(1, 1)], 16, False, True),
+    ("fresh-100", [(100, 100)], 16, False, True),
+    ("fresh-100 HND", [(100, 100)], 16, True, True),
+    ("fresh-700 ps64", [(700, 700)], 64, False, True),
+    ("fresh-1024", [(1024, 1024)], 16, False, True),
+    ("chunk-128-of-1000", [(128, 1000)], 16, False, True),
+    ("chunk-128-of-1000 HND ps32", [(128, 1000)], 32, True, True),
+    ("multi-seq", [(17, 17), (64, 300), (1, 50), (200, 200)], 16, False, True),
+    ("non-causal-32-of-200", [(32, 200)], 16, False, False),
+    ("partial-last-page", [(33, 33), (5, 21)], 16, False, True),
+]
+
+
+@pytest.mark.parametrize("name,seqs,ps,hnd,causal", PREFILL_CASES, ids=[c[0] for c in PREFILL_CASES])
+def test_prefill_matches_cpuops(session, name, seqs, ps, hnd, causal):
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    b = cases.make_paged_batch(rng, [s[1] for s in seqs], [s[0] for s in seqs], page_size=ps, hnd=hnd)
+    got = run_case(session, b, causal=causal)
+    check_against_oracle(got, b, causal=causal)
+
+
+def test_config3_prefill_full_size(session):
+    """BASELINE config 3 at full size (8 sequences, chunk U(256, 2048) onto prefix U(0, 6144), causal): the whole batch
+    against a float32 torch reference of the same math, and two sampled sequences against the CpuOps oracle."""
+    t = torch()
+    rng = np.random.default_rng(3)
+    n = rng.integers(256, 2049, size=8)
+    pre = rng.integers(0, 6145, size=8)
+    b = cases.make_paged_batch(rng, n + pre, n, std=0.5, pool_factor=1.25)
+    got = run_case(session, b, check_nohost=False, check_determinism=False)
+    qv = t.from_numpy(cases.values(b.q, True).astype(np.float32)).cuda()
+    kc = t.from_numpy(cases.values(b.k_cache, True).astype(np.float32)).cuda()
+    vc = t.from_numpy(cases.values(b.v_cache, True).astype(np.float32)).cuda()
+    ref = np.zeros_like(got)
+    for s in range(8):
+        pages = t.from_numpy(b.kv_indices[b.kv_indptr[s]:b.kv_indptr[s + 1]].astype(np.int64)).cuda()
+        kl = int(b.kv_lens[s])
+        k = kc[pages].reshape(-1, 2, 256)[:kl]
+        v = vc[pages].reshape(-1, 2, 256)[:kl]
+        q = qv[b.q_indptr[s]:b.q_indptr[s + 1]]
+        nq = q.shape[0]
+        qpos = t.arange(kl - nq, kl, device="cuda")
+        mask = t.arange(kl, device="cuda")[None, :] <= qpos[:, None]
+        for h in range(8):
+            sc = (q[:, h, :] @ k[:, h // 4, :].T) / 16.0
+            sc = sc.masked_fill(~mask, float("-inf"))
+            ref[b.q_indptr[s]:b.q_indptr[s + 1], h] = (t.softmax(sc, dim=-1) @ v[:, h // 4, :]).cpu().numpy()
+    cases.assert_close(got, ref, what="config 3 vs fp32 torch")
+    for s in (int(np.argmin(n + pre)), 3):
+        one = cases.PagedBatch(b.q[b.q_indptr[s]:b.q_indptr[s + 1]].copy(), b.k_cache, b.v_cache,
+                               np.array([0, n[s]], np.int32), np.array([0, b.kv_indptr[s + 1] - b.kv_indptr[s]], np.int32),
+                               b.kv_indices[b.kv_indptr[s]:b.kv_indptr[s + 1]].copy(), b.kv_last_page_len[s:s + 1].copy(),
+                               [int(b.kv_lens[s])], [int(n[s])], 16, False, True)
+        ref1 = cases.values(cases.oracle_attention(one), True)
+        cases.assert_close(got[b.q_indptr[s]:b.q_indptr[s + 1]], ref1, what=f"config 3 seq {s} vs CpuOps")
+
+
+def test_prefill_batch_invariance(session):
+    rng = np.random.default_rng(9)
+    b = cases.make_paged_batch(rng, [333, 500, 129], [333, 100, 129])
+    many = run_case(session, b, check_nohost=False, check_determinism=False)
+    one = cases.PagedBatch(b.q[:333].copy(), b.k_cache, b.v_cache, np.array([0, 333], np.int32),
+                           b.kv_indptr[:2].copy(), b.kv_indices[:b.kv_indptr[1]].copy(), b.kv_last_page_len[:1].copy(),
+                           b.kv_lens[:1], [333], 16, False, True)
+    alone = run_case(session, one, check_nohost=False, check_determinism=False)
+    assert np.array_equal(alone, many[:333])
+
+
+def test_rejections(session):
+    """Typed refusals before any launch (reference AttentionCases.cs:234-288)."""
+    rng = np.random.default_rng(4)
+    b = cases.make_paged_batch(rng, [40, 17], [1, 1])
+    d = Dev(b)
+    entry = session.lib.entry(roost_amd.ATTENTION_VARIANT)
+    good = d.params()
+    session.launch(entry, good, key="rej")
+    ws = session._ws[(entry.variant_id, "rej")][3]
+
+    def status(**over):
+        return session.run_raw(entry, d.params(**over), ws)
+
+    assert status(head_dim=96) == abi.UNSUPPORTED
+    assert status(q_heads=16) == abi.UNSUPPORTED
+    assert status(window_left=128) == abi.UNSUPPORTED
+    assert status(soft_cap=30.0) == abi.UNSUPPORTED
+    p = d.params()
+    p.tokens = 3
+    assert session.run_raw(entry, p, ws) == abi.INVALID_ARGUMENT
+    assert status(mode=abi.ATTENTION_PREFILL) == abi.INVALID_ARGUMENT  # the plan was made for decode
+    p = d.params()
+    p.kv_indices.length = 1
+    assert session.run_raw(entry, p, ws) == abi.INVALID_ARGUMENT
+    p = d.params()
+    p.q.dtype = abi.DTYPE_F16
+    assert session.run_raw(entry, p, ws) == abi.INVALID_ARGUMENT
+    assert status(kv_layout=abi.LAYOUT_ROW_MAJOR) == abi.INVALID_ARGUMENT
+    p = d.params()
+    p.struct_size = 64
+    assert session.run_raw(entry, p, ws) == abi.ABI_MISMATCH
+    # plan without host tables; plan into a too-small workspace.
+    p = d.params()
+    p.kv_indptr_host = None
+    assert entry.plan(session.ctx, C.addressof(p), C.addressof(ws), C.c_void_p(session.stream_handle)) == \
+        abi.INVALID_ARGUMENT
+    small = abi.new(abi.Workspace)
+    small.device, small.device_bytes = ws.device, 64
+    small.pinned_host, small.pinned_host_bytes = ws.pinned_host, 64
+    small.plan, small.plan_bytes = ws.plan, ws.plan_bytes
+    assert entry.plan(session.ctx, C.addressof(good), C.addressof(small), C.c_void_p(session.stream_handle)) == \
+        abi.WORKSPACE_TOO_SMALL
+    torch().cuda.synchronize()

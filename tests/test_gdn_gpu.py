@@ -1,0 +1,200 @@
+"""GatedDeltaRule (chunk and recurrent variants) on the GPU through the C ABI vs the CpuOps oracle (reference harness:
+kernels/tests/hybrid-conformance/GdnCases.cs:31-471). Tolerances: output max-abs 2e-2 and max-rel 1e-2; final state
+max-rel 1e-3 (relative to |ref_i| + max|ref|), per BASELINE.json."""
+import numpy as np
+import pytest
+
+import cases
+import roost_amd
+from cases import DIM, FUSED, HEADS, ROW
+from roost_amd import abi
+from test_attention_gpu import from_dev, to_dev
+
+pytestmark = pytest.mark.gpu
+
+VARIANTS = [roost_amd.RECURRENT_VARIANT, roost_amd.CHUNK_VARIANT]
+
+
+class DevGdn:
+    def __init__(self, d: cases.GdnData, strided=True):
+        import torch
+
+        self.d = d
+        self.strided = strided
+        self.fused = to_dev(d.fused, True)
+        if not strided:
+            self.q, self.k, self.v = (to_dev(d.view(i), True) for i in range(3))
+        self.g = to_dev(d.g)
+        self.beta = to_dev(d.beta, True)
+        self.pool = to_dev(d.pool)
+        self.slots = to_dev(d.slots)
+        self.cu = to_dev(d.cu)
+        self.out = torch.full((max(d.tokens, 1), HEADS, DIM), float("nan"), dtype=torch.bfloat16, device="cuda")
+
+    def params(self, init=True, **over):
+        d = self.d
+        reach = 0 if d.tokens == 0 else (d.tokens - 1) * FUSED + ROW
+        if self.strided:
+            kw = dict(q_stride=FUSED, k_stride=FUSED, v_stride=FUSED, q_len=reach, k_len=reach, v_len=reach,
+                      q_offset=0, k_offset=ROW, v_offset=2 * ROW)
+            q = k = v = self.fused
+        else:
+            kw = {}
+            q, k, v = self.q, self.k, self.v
+        kw.update(batch=d.batch, tokens=d.tokens, use_initial_state=init, cu_seqlens_host=d.cu)
+        kw.update(over)
+        return roost_amd.gated_delta_rule_params(q, k, v, self.g, self.beta, self.out, self.pool, self.slots, self.cu,
+                                                 **kw)
+
+
+def run(session, dev: DevGdn, variant, init=True):
+    p = dev.params(init)
+    session.launch(session.lib.entry(variant), p, key=(dev.d.batch, dev.d.tokens))
+    return from_dev(dev.out, True)[: dev.d.tokens], from_dev(dev.pool)
+
+
+CASES = [
+    ("packed [300,77,1500,64,1] init strided", [300, 77, 1500, 64, 1], True, True, 0.2, 11),
+    ("packed [300,77,1500] no init strided", [300, 77, 1500], True, False, 0.2, 12),
+    ("one 1000 contiguous init", [1000], False, True, 0.2, 13),
+    ("chunk boundaries [64,128,65,1,0,63]", [64, 128, 65, 1, 0, 63], True, True, 0.2, 14),
+    ("strong decay [200,40]", [200, 40], True, True, 2.5, 15),
+    ("decode 4x1 strided init", [1, 1, 1, 1], True, True, 0.2, 21),
+    ("packed [5,1,1] contiguous", [5, 1, 1], False, True, 0.2, 22),
+    ("one of 3 no init", [3], True, False, 0.2, 23),
+    ("decode with empty [1,0,1]", [1, 0, 1], True, True, 0.2, 24),
+    ("32 x 1 serving decode", [1] * 32, True, True, 0.2, 26),
+]
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
+@pytest.mark.parametrize("name,lens,strided,init,decay,seed", CASES, ids=[c[0] for c in CASES])
+def test_matches_cpuops(session, variant, name, lens, strided, init, decay, seed):
+    rng = np.random.default_rng(seed)
+    pool_slots = 41
+    d = cases.make_gdn(rng, lens, pool_slots, decay=decay)
+    want_o, want_pool = cases.oracle_gdn(d, use_initial_state=init)
+    dev = DevGdn(d, strided)
+    got_o, got_pool = run(session, dev, variant, init)
+    cases.assert_close(cases.bf16_values(got_o), cases.bf16_values(want_o), what="gdn output")
+    owned = {int(d.slots[b]) for b in range(d.batch) if d.lens[b] > 0}
+    for s in range(pool_slots):
+        if s in owned:
+            cases.assert_close(got_pool[s], want_pool[s], max_abs=1.0, max_rel=cases.STATE_REL, what=f"state slot {s}")
+        else:
+            assert got_pool[s].tobytes() == d.pool[s].tobytes(), f"slot {s} was touched"
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_negative_slot_runs_from_zero_and_is_not_written(session, variant):
+    lens = [100, 70] if variant == roost_amd.CHUNK_VARIANT else [1, 1]
+    rng = np.random.default_rng(51)
+    d = cases.make_gdn(rng, lens, 9, slots=[-1, 3])
+    a = DevGdn(d)
+    o_neg, pool_neg = run(session, a, variant, init=True)
+    b = DevGdn(d)
+    o_zero, _ = run(session, b, variant, init=False)
+    n0 = lens[0]
+    assert o_neg[:n0].tobytes() == o_zero[:n0].tobytes()
+    for s in range(9):
+        if s != 3:
+            assert pool_neg[s].tobytes() == d.pool[s].tobytes()
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_batch_invariance(session, variant):
+    lens = [333, 200, 129] if variant == roost_amd.CHUNK_VARIANT else [1, 1, 1]
+    rng = np.random.default_rng(31)
+    many = cases.make_gdn(rng, lens, 9, slots=[4, 7, 2])
+    n0 = lens[0]
+    one = cases.GdnData(many.fused[:n0].copy(), many.g[:n0].copy(), many.beta[:n0].copy(), many.pool.copy(),
+                        np.array([4], np.int32), np.array([0, n0], np.int32), [n0])
+    o_many, p_many = run(session, DevGdn(many), variant)
+    o_one, p_one = run(session, DevGdn(one), variant)
+    assert o_many[:n0].tobytes() == o_one.tobytes()
+    assert p_many[4].tobytes() == p_one[4].tobytes()
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_deterministic(session, variant):
+    rng = np.random.default_rng(77)
+    d = cases.make_gdn(rng, [130, 7], 5)
+    o1, p1 = run(session, DevGdn(d), variant)
+    o2, p2 = run(session, DevGdn(d), variant)
+    assert o1.tobytes() == o2.tobytes() and p1.tobytes() == p2.tobytes()
+
+
+def test_config4_chunked_prefill_then_recurrent_decode(session):
+    """4 x 4096 tokens, 16 heads x 128, beta = sigmoid(N(0,1)), g = -softplus(N(0,1)),
+    S0 ~ N(0, 0.01); chunked prefill vs CpuOps; then recurrent decode steps on 128 states vs CpuOps."""
+    rng = np.random.default_rng(4)
+    d = cases.make_gdn(rng, [4096] * 4, 4, slots=[0, 1, 2, 3], baseline_style=True)
+    want_o, want_pool = cases.oracle_gdn(d)
+    got_o, got_pool = run(session, DevGdn(d), roost_amd.CHUNK_VARIANT)
+    cases.assert_close(cases.bf16_values(got_o), cases.bf16_values(want_o), what="config 4 chunk output")
+    for s in range(4):
+        cases.assert_close(got_pool[s], want_pool[s], max_abs=1.0, max_rel=cases.STATE_REL, what=f"config 4 state {s}")
+    # Decode: 128 states, 4 steps of one token each through the recurrent variant, chained through the pool.
+    dd = cases.make_gdn(rng, [1] * 128, 128, slots=list(range(128)), baseline_style=True)
+    dev = DevGdn(dd)
+    pool_ref = dd.pool.copy()
+    for step in range(4):
+        step_data = cases.make_gdn(rng, [1] * 128, 128, slots=list(range(128)), baseline_style=True)
+        step_data.pool = pool_ref
+        want_o, pool_ref = cases.oracle_gdn(step_data)
+        dev.fused.copy_(to_dev(step_data.fused, True))
+        dev.g.copy_(to_dev(step_data.g))
+        dev.beta.copy_(to_dev(step_data.beta, True))
+        got_o, got_pool = run(session, dev, roost_amd.RECURRENT_VARIANT)
+        cases.assert_close(cases.bf16_values(got_o), cases.bf16_values(want_o), what=f"decode step {step}")
+    for s in range(128):
+        cases.assert_close(got_pool[s], pool_ref[s], max_abs=1.0, max_rel=cases.STATE_REL, what=f"decode state {s}")
+
+
+def test_rejections(session):
+    rng = np.random.default_rng(41)
+    d = cases.make_gdn(rng, [2, 3], 4, slots=[1, 3])
+    dev = DevGdn(d)
+    rec = session.lib.entry(roost_amd.RECURRENT_VARIANT)
+    chunk = session.lib.entry(roost_amd.CHUNK_VARIANT)
+
+    def status(entry, p, ws=None):
+        return session.run_raw(entry, p, ws)
+
+    p = dev.params(q_stride=ROW - 8)
+    assert status(rec, p) == abi.INVALID_ARGUMENT
+    p = dev.params()
+    p.v.length -= 1
+    assert status(rec, p) == abi.INVALID_ARGUMENT
+    assert status(rec, dev.params(k_heads=8, v_heads=8)) == abi.UNSUPPORTED
+    assert status(rec, dev.params(k_dim=64, v_dim=64)) == abi.UNSUPPORTED
+    assert status(rec, dev.params(l2_norm_qk=False)) == abi.UNSUPPORTED
+    p = dev.params()
+    p.beta.dtype = abi.DTYPE_F32
+    assert status(rec, p) == abi.UNSUPPORTED
+    p = dev.params()
+    p.g.address += 4
+    assert status(rec, p) == abi.INVALID_ARGUMENT
+    p = dev.params()
+    p.struct_size = 64
+    assert status(rec, p) == abi.ABI_MISMATCH
+    p = dev.params()
+    p.state.length = HEADS * DIM * DIM + 5
+    assert status(rec, p) == abi.INVALID_ARGUMENT
+    # Chunk variant: run() without plan() -> NOT_PLANNED; a short device workspace -> WORKSPACE_TOO_SMALL.
+    import ctypes as C
+
+    good = dev.params()
+    sizes = session.workspace_sizes(chunk, good)
+    import torch
+
+    buf = torch.empty(int(sizes.device_bytes) + 256, dtype=torch.uint8, device="cuda")
+    plan = C.create_string_buffer(int(sizes.plan_bytes))
+    ws = abi.new(abi.Workspace)
+    ws.device = (buf.data_ptr() + 255) // 256 * 256
+    ws.device_bytes = sizes.device_bytes
+    ws.plan, ws.plan_bytes = C.addressof(plan), sizes.plan_bytes
+    assert status(chunk, good, ws) == abi.NOT_PLANNED
+    ws.device_bytes = sizes.device_bytes - 256
+    assert status(chunk, good, ws) == abi.WORKSPACE_TOO_SMALL
+    torch.cuda.synchronize()

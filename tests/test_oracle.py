@@ -1,0 +1,348 @@
+"""Pins the CpuOps oracle (oracle/cpuops.c) before any GPU result is compared with it.
+
+Which check pins which oracle function:
+  to_bf16          -- bit patterns: ties to even, round-to-odd double rounding, NaN -> 0x7FC0, overflow -> inf
+                      (CpuElements.cs:128-160), and exhaustive agreement with float32 RNE for float32 inputs.
+  paged_attention  -- the reference's hand cases (AttentionTests.cs:135-228: two-key 7.0, bf16 mean [2, 3], window and
+                      no-pages zeros, out-of-range last page length refused), the reference's independent dense
+                      three-pass formulation over its 9 parameter rows at 1e-12 (AttentionTests.cs:8-133, restated
+                      here in numpy), and torch's float64 scaled_dot_product_attention on de-paged K/V.
+  cache_write      -- the hand case BasicOpsTests.cs:202-232 (NHD and HND) and a scatter/gather round trip.
+  gated_delta_rule -- the scalar hand case HybridTests.cs:7-24 (o = [1, 3], S = 1), the matrix formulation
+                      S' = (I - b k k^T) e^g S + b k v^T with grouped heads and slots (HybridTests.cs:32-172), two calls
+                      = one call and token-by-token decode (HybridTests.cs:174-220), scale 0 = 1/sqrt(k_dim), and
+                      strided views = contiguous copies (GatedDeltaRuleViewTests.cs).
+  plan_region      -- the closed form slot = block[pos / bs] * bs + pos % bs and the indptr prefix sums
+                      (PlanRegionWriter.cs:19-64) on hand-written plans.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import cases
+import oracle
+
+
+# ---- elements ----------------------------------------------------------------------------------------------------------
+
+def test_bf16_rounding_bit_patterns():
+    assert oracle.to_bf16(1.0) == 0x3F80
+    # Ties go to even: 1 + 2^-8 is halfway between 1 and 1 + 2^-7.
+    assert oracle.to_bf16(1.0 + 2 ** -8) == 0x3F80
+    assert oracle.to_bf16(1.0 + 3 * 2 ** -8) == 0x3F82
+    # Just above the tie rounds up: double rounding through float would lose this (1 + 2^-8 + 2^-40 -> float tie).
+    assert oracle.to_bf16(1.0 + 2 ** -8 + 2 ** -40) == 0x3F81
+    assert oracle.to_bf16(float("nan")) == 0x7FC0
+    assert oracle.to_bf16(float("inf")) == 0x7F80 and oracle.to_bf16(float("-inf")) == 0xFF80
+    assert oracle.to_bf16(3.5e38) == 0x7F80  # beyond the largest finite bf16
+    assert oracle.to_bf16(-0.0) == 0x8000
+
+
+def test_bf16_rounding_agrees_with_float32_rne():
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal(20000).astype(np.float32) * np.float32(10.0) ** rng.integers(-30, 30, 20000)
+    x = x.astype(np.float32)
+    want = oracle.f32_to_bf16_rne(x)
+    got = oracle.to_bf16(x.astype(np.float64))
+    assert np.array_equal(got, want)
+
+
+# ---- attention ---------------------------------------------------------------------------------------------------------
+
+def attention_f64(q, k_pool, v_pool, q_indptr, kv_indptr, kv_indices, last, *, batch, tokens, hq, hkv, hd, bs, hnd,
+                  scale=0.0, cap=0.0, window=-1, causal=True):
+    out = np.zeros((tokens, hq, hd))
+    oracle.paged_attention(np.ascontiguousarray(q, np.float64), out, np.ascontiguousarray(k_pool, np.float64),
+                           np.ascontiguousarray(v_pool, np.float64), np.asarray(q_indptr, np.int32),
+                           np.asarray(kv_indptr, np.int32), np.asarray(kv_indices, np.int32),
+                           np.asarray(last, np.int32), batch=batch, tokens=tokens, q_heads=hq, kv_heads=hkv,
+                           head_dim=hd, page_size=bs, hnd=hnd, scale=scale, soft_cap=cap, window_left=window,
+                           causal=causal, threads=1)
+    return out
+
+
+def test_two_key_hand_case():
+    # One head of width 1, scale 1: scores 0 and ln 3 -> weights 1/4, 3/4 -> 0.25 * 4 + 0.75 * 8 = 7.
+    out = attention_f64([[[1.0]]], [0.0, math.log(3)], [4.0, 8.0], [0, 1], [0, 1], [0], [2], batch=1, tokens=1, hq=1,
+                        hkv=1, hd=1, bs=2, hnd=False, scale=1.0)
+    assert abs(out[0, 0, 0] - 7.0) < 1e-13
+
+
+def test_bf16_cache_mean_hand_case():
+    q = cases.bf16_bits(np.array([[[1.0, 0.0]]], np.float32))
+    k = cases.bf16_bits(np.array([1, 0, 1, 0], np.float32))
+    v = cases.bf16_bits(np.array([1, 2, 3, 4], np.float32))
+    out = np.zeros_like(q)
+    oracle.paged_attention(q, out, k, v, np.array([0, 1], np.int32), np.array([0, 1], np.int32),
+                           np.array([0], np.int32), np.array([2], np.int32), batch=1, tokens=1, q_heads=1, kv_heads=1,
+                           head_dim=2, page_size=2, bf16=True)
+    assert list(cases.bf16_values(out).ravel()) == [2.0, 3.0]
+
+
+def test_window_of_one_and_no_pages_give_expected():
+    out = attention_f64([[[1.0]]], [1.0, 1.0], [5.0, 5.0], [0, 1], [0, 1], [0], [2], batch=1, tokens=1, hq=1, hkv=1,
+                        hd=1, bs=2, hnd=False, window=1)
+    assert abs(out[0, 0, 0] - 5.0) < 1e-13
+    out = attention_f64([[[1.0]]], [1.0, 1.0], [5.0, 5.0], [0, 1], [0, 0], [0], [2], batch=1, tokens=1, hq=1, hkv=1,
+                        hd=1, bs=2, hnd=False, causal=False)
+    assert out[0, 0, 0] == 0.0
+
+
+@pytest.mark.parametrize("last", [3, 0, -1])
+def test_out_of_range_last_page_length_is_refused_before_writing(last):
+    out = np.full((1, 1, 1), 99.0)
+    with pytest.raises(oracle.OracleError):
+        oracle.paged_attention(np.ones((1, 1, 1)), out, np.ones(2), np.full(2, 5.0), np.array([0, 1], np.int32),
+                               np.array([0, 1], np.int32), np.array([0], np.int32), np.array([last], np.int32),
+                               batch=1, tokens=1, q_heads=1, kv_heads=1, head_dim=1, page_size=2)
+    assert out[0, 0, 0] == 99.0
+    with pytest.raises(oracle.OracleError):  # WindowLeft 0 is an unbound field
+        oracle.paged_attention(np.ones((1, 1, 1)), out, np.ones(2), np.full(2, 5.0), np.array([0, 1], np.int32),
+                               np.array([0, 1], np.int32), np.array([0], np.int32), np.array([2], np.int32),
+                               batch=1, tokens=1, q_heads=1, kv_heads=1, head_dim=1, page_size=2, window_left=0)
+
+
+def dense_reference(q, k, v, q_lens, hq, hkv, hd, causal, window, scale, cap):
+    """Three-pass softmax over dense per-sequence K/V, no online rescaling (the reference's independent formulation,
+    AttentionTests.cs:8-56)."""
+    outs, qi = [], 0
+    for b, n in enumerate(q_lens):
+        kv_len = k[b].shape[0]
+        for i in range(n):
+            qpos = kv_len - n + i
+            for h in range(hq):
+                kvh = h // (hq // hkv)
+                ok = np.array([(not causal or j <= qpos) and (window < 0 or j >= qpos - window) for j in range(kv_len)])
+                s = k[b][:, kvh * hd:(kvh + 1) * hd] @ q[qi][h * hd:(h + 1) * hd] * scale
+                if cap != 0:
+                    s = cap * np.tanh(s / cap)
+                mx = s[ok].max() if ok.any() else 0.0
+                z = np.exp(s[ok] - mx).sum()
+                w = np.where(ok, np.exp(s - mx) / z, 0.0)
+                outs.append(w @ v[b][:, kvh * hd:(kvh + 1) * hd])
+            qi += 1
+    return np.array(outs).ravel()
+
+
+ROWS = [(False, False, -1, 0.0, 0.0), (True, False, -1, 0.0, 0.0), (False, True, -1, 0.0, 0.0),
+        (True, True, -1, 0.0, 0.0), (False, True, 3, 0.0, 0.0), (True, True, 3, 0.0, 0.0),
+        (False, True, -1, 0.0, 5.0), (True, True, 2, 0.37, 3.0), (False, False, 4, 0.0, 0.0)]
+
+
+@pytest.mark.parametrize("hnd,causal,window,scale_arg,cap", ROWS)
+def test_matches_dense_three_pass_through_shuffled_blocks(hnd, causal, window, scale_arg, cap):
+    hq, hkv, hd, bs = 4, 2, 8, 4
+    kv_lens, q_lens = [7, 10], [3, 1]
+    rng = np.random.default_rng(1234)
+    q = [rng.uniform(-1, 1, hq * hd) for _ in range(sum(q_lens))]
+    k = [rng.uniform(-1, 1, (n, hkv * hd)) for n in kv_lens]
+    v = [rng.uniform(-1, 1, (n, hkv * hd)) for n in kv_lens]
+    table = [[5, 2], [7, 0, 3]]
+    kp = np.zeros(8 * bs * hkv * hd)
+    vp = np.zeros_like(kp)
+    for b in range(2):
+        for j in range(kv_lens[b]):
+            blk, off = table[b][j // bs], j % bs
+            for h in range(hkv):
+                for d in range(hd):
+                    idx = (((blk * hkv + h) * bs + off) * hd + d) if hnd else (((blk * bs + off) * hkv + h) * hd + d)
+                    kp[idx] = k[b][j, h * hd + d]
+                    vp[idx] = v[b][j, h * hd + d]
+    out = attention_f64(np.array(q).reshape(4, hq, hd), kp, vp, [0, 3, 4], [0, 2, 5], [5, 2, 7, 0, 3], [3, 2],
+                        batch=2, tokens=4, hq=hq, hkv=hkv, hd=hd, bs=bs, hnd=hnd, scale=scale_arg, cap=cap,
+                        window=window, causal=causal)
+    scale = 1.0 / math.sqrt(hd) if scale_arg == 0 else float(np.float32(scale_arg))
+    want = dense_reference(q, k, v, q_lens, hq, hkv, hd, causal, window, scale, float(np.float32(cap)))
+    assert np.max(np.abs(out.ravel() - want)) < 1e-12
+
+
+def test_matches_torch_float64_sdpa():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(5)
+    b = cases.make_paged_batch(rng, [37, 100], [5, 100], page_size=16, bf16=False, d=32)
+    q = b.q.astype(np.float64)
+    kp = b.k_cache.astype(np.float64)
+    vp = b.v_cache.astype(np.float64)
+    out = attention_f64(q, kp, vp, b.q_indptr, b.kv_indptr, b.kv_indices, b.kv_last_page_len, batch=2,
+                        tokens=b.tokens, hq=8, hkv=2, hd=32, bs=16, hnd=False)
+    for s in range(2):
+        pages = b.kv_indices[b.kv_indptr[s]:b.kv_indptr[s + 1]]
+        k = torch.from_numpy(kp[pages].reshape(-1, 2, 32)[: b.kv_lens[s]]).repeat_interleave(4, dim=1)
+        v = torch.from_numpy(vp[pages].reshape(-1, 2, 32)[: b.kv_lens[s]]).repeat_interleave(4, dim=1)
+        qq = torch.from_numpy(q[b.q_indptr[s]:b.q_indptr[s + 1]])
+        n, kl = qq.shape[0], k.shape[0]
+        mask = torch.arange(kl)[None, :] <= torch.arange(kl - n, kl)[:, None]
+        ref = torch.nn.functional.scaled_dot_product_attention(qq.transpose(0, 1), k.transpose(0, 1),
+                                                               v.transpose(0, 1), attn_mask=mask)
+        assert np.max(np.abs(ref.transpose(0, 1).numpy() - out[b.q_indptr[s]:b.q_indptr[s + 1]])) < 1e-12
+
+
+# ---- cache write -------------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("hnd", [False, True])
+def test_cache_write_hand_case(hnd):
+    k = cases.bf16_bits(np.arange(1, 13, dtype=np.float32))
+    v = cases.bf16_bits(-np.arange(1, 13, dtype=np.float32))
+    kc = np.zeros(16, np.uint16)
+    vc = np.zeros(16, np.uint16)
+    oracle.cache_write(k, v, kc, vc, np.array([3, -1, 0], np.int64), tokens=3, kv_heads=2, head_dim=2, page_size=2,
+                       hnd=hnd, bf16=True)
+    expected = np.zeros(16)
+    for h in range(2):
+        for d in range(2):
+            idx = (lambda blk, off: ((blk * 2 + h) * 2 + off) * 2 + d) if hnd else \
+                (lambda blk, off: ((blk * 2 + off) * 2 + h) * 2 + d)
+            expected[idx(1, 1)] = h * 2 + d + 1
+            expected[idx(0, 0)] = 8 + h * 2 + d + 1
+    assert np.array_equal(cases.bf16_values(kc), expected)
+    assert np.array_equal(cases.bf16_values(vc), -expected)
+
+
+def test_cache_write_round_trip_and_skips():
+    rng = np.random.default_rng(2)
+    tokens, hkv, d, ps, pages = 50, 2, 8, 4, 20
+    k = rng.integers(0, 65536, (tokens, hkv, d), dtype=np.uint16)
+    kc = np.full((pages, ps, hkv, d), 0xABAB, np.uint16)
+    slots = rng.permutation(pages * ps)[:tokens].astype(np.int64)
+    slots[::5] = -1
+    oracle.cache_write(k, k, kc, kc.copy(), slots, tokens=tokens, kv_heads=hkv, head_dim=d, page_size=ps, bf16=True)
+    flat = kc.reshape(pages * ps, hkv, d)
+    for t in range(tokens):
+        if slots[t] >= 0:
+            assert np.array_equal(flat[slots[t]], k[t])
+    untouched = np.setdiff1d(np.arange(pages * ps), slots[slots >= 0])
+    assert np.all(flat[untouched] == 0xABAB)
+
+
+# ---- gated delta rule --------------------------------------------------------------------------------------------------
+
+def gdn_f64(q, k, v, g, beta, state, slots, cu, *, kh, vh, kd, vd, scale, init, l2, tokens, batch):
+    out = np.zeros((tokens, vh, vd))
+    oracle.gated_delta_rule(np.ascontiguousarray(q, np.float64), np.ascontiguousarray(k, np.float64),
+                            np.ascontiguousarray(v, np.float64), np.ascontiguousarray(g, np.float64),
+                            np.ascontiguousarray(beta, np.float64), out, state, np.asarray(slots, np.int32),
+                            np.asarray(cu, np.int32), batch=batch, tokens=tokens, k_heads=kh, v_heads=vh, k_dim=kd,
+                            v_dim=vd, use_initial_state=init, l2_norm_qk=l2, scale=scale, threads=1)
+    return out
+
+
+def test_gdn_scalar_hand_case():
+    # t0: S = 0, d = 0.5 * (2 - 0) = 1, S = 1, o = 1.  t1: S = 2, d = 1 * (1 - 2) = -1, S = 1, o = 3.
+    state = np.array([123.0], np.float32)
+    out = gdn_f64([1, 3], [1, 1], [2, 1], [0, math.log(2)], [0.5, 1], state, [0], [0, 2], kh=1, vh=1, kd=1, vd=1,
+                  scale=1.0, init=False, l2=False, tokens=2, batch=1)
+    assert np.max(np.abs(out.ravel() - [1.0, 3.0])) < 1e-14
+    assert state[0] == 1.0
+
+
+def matrix_form(q, k, v, g, beta, s0, scale, l2):
+    s = s0.copy()
+    outs = []
+    for t in range(len(q)):
+        qt, kt = np.array(q[t]), np.array(k[t])
+        if l2:
+            qt = qt / math.sqrt((qt ** 2).sum() + 1e-6)
+            kt = kt / math.sqrt((kt ** 2).sum() + 1e-6)
+        s = (np.eye(len(kt)) - beta[t] * np.outer(kt, kt)) @ (math.exp(g[t]) * s) + beta[t] * np.outer(kt, v[t])
+        outs.append(s.T @ (qt * scale))
+    return np.array(outs), s
+
+
+@pytest.mark.parametrize("l2", [False, True])
+def test_gdn_matches_matrix_formulation_with_grouped_heads_and_slots(l2):
+    kh, vh, kd, vd = 2, 4, 3, 2
+    rng = np.random.default_rng(77)
+    lens = [5, 3]
+    tokens = sum(lens)
+    q = rng.uniform(-1, 1, (tokens, kh, kd))
+    k = rng.uniform(-1, 1, (tokens, kh, kd))
+    v = rng.uniform(-1, 1, (tokens, vh, vd))
+    g = -rng.uniform(0, 1, (tokens, vh))
+    beta = rng.uniform(0, 1, (tokens, vh))
+    pool = rng.uniform(-1, 1, (4, vh, kd, vd)).astype(np.float32)
+    before = pool.copy()
+    scale = float(np.float32(0.7))
+    out = gdn_f64(q, k, v, g, beta, pool, [3, 1], [0, 5, 8], kh=kh, vh=vh, kd=kd, vd=vd, scale=0.7, init=True, l2=l2,
+                  tokens=tokens, batch=2)
+    t0 = 0
+    for b, slot in enumerate([3, 1]):
+        for h in range(vh):
+            khd = h // (vh // kh)
+            sl = slice(t0, t0 + lens[b])
+            exp_o, s_end = matrix_form(q[sl, khd], k[sl, khd], v[sl, h], g[sl, h], beta[sl, h],
+                                       before[slot, h].astype(np.float64), scale, l2)
+            assert np.max(np.abs(out[sl, h] - exp_o)) < 1e-12
+            assert np.max(np.abs(pool[slot, h] - s_end)) < 1e-6
+        t0 += lens[b]
+    assert np.array_equal(pool[0], before[0]) and np.array_equal(pool[2], before[2])
+
+
+def test_gdn_two_calls_equal_one_call_and_token_decode():
+    kd, vd, n = 4, 3, 9
+    rng = np.random.default_rng(11)
+    q, k, v = rng.uniform(-1, 1, (n, kd)), rng.uniform(-1, 1, (n, kd)), rng.uniform(-1, 1, (n, vd))
+    g, beta = -rng.uniform(0, 1, n), rng.uniform(0, 1, n)
+
+    def run(a, c, state, init):
+        return gdn_f64(q[a:a + c], k[a:a + c], v[a:a + c], g[a:a + c], beta[a:a + c], state, [0], [0, c], kh=1, vh=1,
+                       kd=kd, vd=vd, scale=0.5, init=init, l2=True, tokens=c, batch=1).ravel()
+
+    whole = np.zeros(kd * vd, np.float32)
+    full = run(0, n, whole, False)
+    split = np.zeros(kd * vd, np.float32)
+    two = np.concatenate([run(0, 4, split, False), run(4, 5, split, True)])
+    assert np.max(np.abs(full - two)) < 1e-6 and np.max(np.abs(whole - split)) < 1e-6
+    steps = np.zeros(kd * vd, np.float32)
+    dec = np.concatenate([run(t, 1, steps, t > 0) for t in range(n)])
+    assert np.max(np.abs(full - dec)) < 1e-5
+
+
+def test_gdn_scale_zero_means_inverse_root_kdim():
+    def run(scale):
+        return gdn_f64([1, 2, 3, 4], [0.5] * 4, [1], [0], [1], np.zeros(4, np.float32), [0], [0, 1], kh=1, vh=1, kd=4,
+                       vd=1, scale=scale, init=False, l2=False, tokens=1, batch=1)[0, 0, 0]
+
+    assert abs(run(0.5) - run(0.0)) < 1e-14
+
+
+def test_gdn_strided_views_equal_contiguous_copies():
+    rng = np.random.default_rng(3)
+    d = cases.make_gdn(rng, [7, 5], 4, slots=[2, 0])
+    out_s, pool_s = cases.oracle_gdn(d, threads=1)
+    # Contiguous copies of the three column slices through the same function.
+    out_c = np.zeros_like(out_s)
+    pool_c = d.pool.copy()
+    oracle.gated_delta_rule(d.view(0), d.view(1), d.view(2), d.g, d.beta, out_c, pool_c, d.slots, d.cu, batch=2,
+                            tokens=12, k_heads=16, v_heads=16, k_dim=128, v_dim=128, bf16=True, beta_bf16=True)
+    assert np.array_equal(out_s, out_c) and np.array_equal(pool_s, pool_c)
+
+
+def test_gdn_strided_call_reads_only_the_view():
+    """q_stride/k_stride/v_stride views of the fused buffer: the oracle given the fused buffer itself with strides
+    6144 and column offsets equals the contiguous call."""
+    rng = np.random.default_rng(8)
+    d = cases.make_gdn(rng, [6, 2], 3, slots=[1, 2])
+    out_c, pool_c = cases.oracle_gdn(d, threads=1)
+    out_s = np.zeros_like(out_c)
+    pool_s = d.pool.copy()
+    fused = d.fused
+    oracle.gated_delta_rule(fused, np.ascontiguousarray(fused[:, cases.ROW:]), np.ascontiguousarray(fused[:, 2 * cases.ROW:]),
+                            d.g, d.beta, out_s, pool_s, d.slots, d.cu, batch=2, tokens=8, k_heads=16, v_heads=16,
+                            k_dim=128, v_dim=128, q_stride=cases.FUSED, k_stride=cases.FUSED - cases.ROW,
+                            v_stride=cases.FUSED - 2 * cases.ROW, bf16=True, beta_bf16=True)
+    assert np.array_equal(out_s, out_c) and np.array_equal(pool_s, pool_c)
+
+
+# ---- plan region -------------------------------------------------------------------------------------------------------
+
+def test_plan_region_slot_mapping_closed_form():
+    seqs = [dict(token_start=0, token_count=3, position_offset=0, kv_length=3, blocks=[7]),
+            dict(token_start=3, token_count=1, position_offset=20, kv_length=21, blocks=[2, 9]),
+            dict(token_start=4, token_count=18, position_offset=14, kv_length=32, blocks=[4, 1])]
+    q_indptr, cu, kv_indptr, kv_indices, last, slots = oracle.plan_region(seqs, 16)
+    assert list(q_indptr) == [0, 3, 4, 22] and list(cu) == [0, 3, 4, 22]
+    assert list(kv_indptr) == [0, 1, 3, 5] and list(kv_indices) == [7, 2, 9, 4, 1]
+    assert list(last) == [3, 5, 16]
+    want = [7 * 16 + 0, 7 * 16 + 1, 7 * 16 + 2, 9 * 16 + 4] + [(4 if p < 16 else 1) * 16 + p % 16 for p in range(14, 32)]
+    assert list(slots) == want
