@@ -1,0 +1,271 @@
+"""Benchmark of the gfx950 Roost attention + Gated DeltaNet kernel library on one MI355X.
+
+Headline (BASELINE.json metric, `value`): paged bf16 decode attention at BASELINE config 2 -- Qwen3.5-0.8B shape,
+batch 64, contexts U(512, 8192), 8 query / 2 KV heads, head_dim 256, page 16, pool 1.25x tokens -- as achieved HBM
+GB/s over the algorithmic bytes (K and V of every context token, q read and o write, the page tables). A step is one
+run() of the PagedAttention entry point over the batch, inputs resident in HBM, plan() done beforehand (it is a host
+step, timed separately). The same JSON line carries config 3 causal chunked prefill (TFLOP/s vs bf16 dense MFMA peak),
+config 4 GDN chunked prefill and recurrent decode, the roofline of the dominant decode kernel, and the CpuOps oracle
+timed on the host as the CPU baseline.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+METRIC = "decode attn HBM GB/s (% peak) + prefill TFLOPS (% MFMA peak) vs CpuOps, 1 GPU"
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def bf16_bits(x):
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+class Paged:
+    """A seeded paged batch built directly on the device (host copies only of the small tables)."""
+
+    def __init__(self, torch, rng, kv_lens, q_lens, std=0.5, hq=8, hkv=2, d=256, ps=16, pool_factor=1.25):
+        self.kv_lens = np.asarray(kv_lens, np.int64)
+        self.q_lens = np.asarray(q_lens, np.int64)
+        pages = (self.kv_lens + ps - 1) // ps
+        total = int(pages.sum())
+        pool = int(np.ceil(total * pool_factor))
+        self.kv_indices_h = rng.permutation(pool)[:total].astype(np.int32)
+        self.q_indptr_h = np.concatenate([[0], np.cumsum(self.q_lens)]).astype(np.int32)
+        self.kv_indptr_h = np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)
+        self.last_h = (self.kv_lens - (pages - 1) * ps).astype(np.int32)
+        self.tokens = int(self.q_indptr_h[-1])
+        self.batch = len(kv_lens)
+        self.hq, self.hkv, self.d, self.ps, self.pages, self.pool = hq, hkv, d, ps, total, pool
+        g = torch.Generator(device="cuda").manual_seed(int(rng.integers(1 << 31)))
+        self.q = (torch.randn((self.tokens, hq, d), generator=g, device="cuda") * std).to(torch.bfloat16)
+        self.k = (torch.randn((pool, ps, hkv, d), generator=g, device="cuda") * std).to(torch.bfloat16)
+        self.v = (torch.randn((pool, ps, hkv, d), generator=g, device="cuda") * std).to(torch.bfloat16)
+        dev = lambda a: torch.from_numpy(a).cuda()  # noqa: E731
+        self.q_indptr, self.kv_indptr = dev(self.q_indptr_h), dev(self.kv_indptr_h)
+        self.kv_indices, self.last = dev(self.kv_indices_h), dev(self.last_h)
+        self.out = torch.empty_like(self.q)
+
+    def params(self, roost_amd, causal=True):
+        return roost_amd.paged_attention_params(
+            self.q, self.out, self.k, self.v, self.q_indptr, self.kv_indptr, self.kv_indices, self.last,
+            q_indptr_host=self.q_indptr_h, kv_indptr_host=self.kv_indptr_h, kv_last_page_len_host=self.last_h,
+            batch=self.batch, q_heads=self.hq, kv_heads=self.hkv, head_dim=self.d, page_size=self.ps, causal=causal)
+
+    def decode_bytes(self):
+        e = 2
+        kv = int(self.kv_lens.sum()) * self.hkv * self.d * 2 * e
+        qo = self.batch * self.hq * self.d * 2 * e
+        tables = 4 * (self.pages + 2 * self.batch + 1)
+        return kv + qo + tables
+
+    def prefill_flops(self):
+        n, p = self.q_lens, self.kv_lens - self.q_lens
+        return float(4 * self.hq * self.d * np.sum(n * p + n * (n + 1) / 2))
+
+
+def time_runs(torch, session, entry, params, ws, steps, warmup):
+    """Average run() duration in ms over `steps` launches, measured with events on the session's stream."""
+    for _ in range(warmup):
+        session.run(entry, params, ws)
+    session.stream.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(session.stream)
+    for _ in range(steps):
+        session.run(entry, params, ws)
+    end.record(session.stream)
+    end.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def planned(session, entry, params, key):
+    """Workspace + plan (host step), returning the workspace and the plan's wall time in ms."""
+    t0 = time.perf_counter()
+    session.launch(entry, params, key=key)  # plans and runs once
+    session.stream.synchronize()
+    plan_ms = (time.perf_counter() - t0) * 1e3
+    return session._ws[(entry.variant_id, key)][3], plan_ms
+
+
+def bench_decode(torch, roost_amd, session, steps, warmup):
+    rng = np.random.default_rng(2)
+    kv = rng.integers(512, 8193, size=64)
+    b = Paged(torch, rng, kv, np.ones(64, np.int64))
+    entry = session.lib.entry(roost_amd.ATTENTION_VARIANT)
+    p = b.params(roost_amd)
+    ws, plan_ms = planned(session, entry, p, "bench-decode")
+    ms = time_runs(torch, session, entry, p, ws, steps, warmup)
+    return b, ms, plan_ms
+
+
+def bench_prefill(torch, roost_amd, session, steps, warmup):
+    rng = np.random.default_rng(3)
+    n = rng.integers(256, 2049, size=8)
+    pre = rng.integers(0, 6145, size=8)
+    b = Paged(torch, rng, n + pre, n)
+    entry = session.lib.entry(roost_amd.ATTENTION_VARIANT)
+    p = b.params(roost_amd)
+    ws, plan_ms = planned(session, entry, p, "bench-prefill")
+    ms = time_runs(torch, session, entry, p, ws, max(steps // 2, 3), max(warmup // 2, 1))
+    return b, ms, plan_ms
+
+
+def bench_gdn(torch, roost_amd, session, steps, warmup):
+    H, D = 16, 128
+    g = torch.Generator(device="cuda").manual_seed(4)
+
+    def inputs(batch, lens):
+        tokens = int(sum(lens))
+        fused = torch.randn((tokens, 3 * H * D), generator=g, device="cuda").to(torch.bfloat16)
+        gg = -torch.nn.functional.softplus(torch.randn((tokens, H), generator=g, device="cuda"))
+        beta = torch.sigmoid(torch.randn((tokens, H), generator=g, device="cuda")).to(torch.bfloat16)
+        pool = torch.randn((batch, H, D, D), generator=g, device="cuda") * 0.01
+        slots = torch.arange(batch, dtype=torch.int32, device="cuda")
+        cu_h = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+        out = torch.empty((tokens, H, D), dtype=torch.bfloat16, device="cuda")
+        reach = (tokens - 1) * 3 * H * D + H * D
+        p = roost_amd.gated_delta_rule_params(
+            fused, fused, fused, gg, beta, out, pool, slots, torch.from_numpy(cu_h).cuda(), batch=batch,
+            tokens=tokens, q_stride=3 * H * D, k_stride=3 * H * D, v_stride=3 * H * D, q_len=reach, k_len=reach,
+            v_len=reach, q_offset=0, k_offset=H * D, v_offset=2 * H * D, cu_seqlens_host=cu_h)
+        return p, (fused, gg, beta, pool, slots, out)
+
+    res = {}
+    # Config 4: chunked prefill, 4 x 4096 tokens.
+    p, keep = inputs(4, [4096] * 4)
+    entry = session.lib.entry(roost_amd.CHUNK_VARIANT)
+    ws, _ = planned(session, entry, p, "bench-gdn-chunk")
+    ms = time_runs(torch, session, entry, p, ws, max(steps // 4, 3), 1)
+    T, B = 4 * 4096, 4
+    bytes_ = (3 * T * H * D + T * H * D) * 2 + T * H * 6 + 2 * B * H * D * D * 4
+    flops = (T // 64) * H * (2 * 64 * 64 * (3 * D + 2 * D) + 6 * 64 * D * D)
+    res["gdn_chunk"] = {"config": "4 x 4096 tokens, 16 heads x 128, chunk 64", "ms": ms,
+                        "hbm_gbs": bytes_ / ms / 1e6, "hbm_frac": bytes_ / ms / 1e6 / HBM_PEAK_GBS,
+                        "tflops": flops / ms / 1e9, "mfma_frac": flops / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS}
+    del keep
+    # Config 4 follow-on: one recurrent decode step on 128 states.
+    p, keep = inputs(128, [1] * 128)
+    entry = session.lib.entry(roost_amd.RECURRENT_VARIANT)
+    ms = time_runs(torch, session, entry, p, None, steps, warmup)
+    B = 128
+    bytes_ = 2 * B * H * D * D * 4 + B * (3 * H * D + H * D) * 2 + B * H * 6
+    res["gdn_recurrent"] = {"config": "128 states x 1 token, 16 heads x 128", "ms": ms,
+                            "hbm_gbs": bytes_ / ms / 1e6, "hbm_frac": bytes_ / ms / 1e6 / HBM_PEAK_GBS}
+    del keep
+    return res
+
+
+def cpu_baseline(b: Paged, sample_seqs: int):
+    """CpuOps oracle (single thread, double precision, the C restatement of CpuOps.PagedAttention) on the first
+    `sample_seqs` sequences of the decode batch; reported in the headline's unit (algorithmic GB/s)."""
+    import torch
+
+    import oracle
+
+    k = b.k.view(torch.int16).cpu().numpy().view(np.uint16)
+    v = b.v.view(torch.int16).cpu().numpy().view(np.uint16)
+    q = b.q[:sample_seqs].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    n = sample_seqs
+    kv_indptr = b.kv_indptr_h[: n + 1].copy()
+    out = np.zeros_like(q)
+    t0 = time.perf_counter()
+    oracle.paged_attention(q, out, k, v, np.arange(n + 1, dtype=np.int32), kv_indptr,
+                           b.kv_indices_h[: kv_indptr[-1]].copy(), b.last_h[:n].copy(), batch=n, tokens=n,
+                           q_heads=8, kv_heads=2, head_dim=256, page_size=16, bf16=True, threads=1)
+    secs = time.perf_counter() - t0
+    e = 2
+    bytes_ = int(b.kv_lens[:n].sum()) * 2 * 256 * 2 * e + n * 8 * 256 * 2 * e + 4 * (int(kv_indptr[-1]) + 2 * n + 1)
+    return {"value": bytes_ / secs / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"CpuOps restatement (oracle/cpuops.c, double, 1 thread) over the first {n} of the 64 config-2 "
+                      f"sequences ({int(b.kv_lens[:n].sum())} context tokens) in {secs:.2f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--cpu-sample", type=int, default=16)
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build runs the attention + GDN path on a single MI355X "
+              "(sharding is described in DESIGN.md, not launched).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import roost_amd
+
+    assert torch.cuda.is_available(), "bench.py needs the MI355X"
+    torch.cuda.set_device(0)
+    session = roost_amd.OpSession(device=0)
+    log("decode (config 2) ...")
+    b, dec_ms, dec_plan_ms = bench_decode(torch, roost_amd, session, args.steps, args.warmup)
+    dec_bytes = b.decode_bytes()
+    dec_gbs = dec_bytes / dec_ms / 1e6
+    log(f"  {dec_ms * 1e3:.1f} us/step, {dec_gbs:.0f} GB/s")
+    log("prefill (config 3) ...")
+    pb, pre_ms, pre_plan_ms = bench_prefill(torch, roost_amd, session, args.steps, args.warmup)
+    pre_tflops = pb.prefill_flops() / pre_ms / 1e9
+    log(f"  {pre_ms * 1e3:.1f} us/step, {pre_tflops:.0f} TFLOP/s")
+    log("gdn (config 4) ...")
+    gdn = bench_gdn(torch, roost_amd, session, args.steps, args.warmup)
+    log(f"  {json.dumps(gdn)}")
+    cpu = None
+    if not args.skip_cpu:
+        log("cpu baseline ...")
+        cpu = cpu_baseline(b, args.cpu_sample)
+        log(f"  {cpu}")
+    line = {
+        "metric": METRIC,
+        "value": round(dec_gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)*0.5 q/K/V, random disjoint page lists)",
+        "config": {"workload": "BASELINE config 2: paged decode, Qwen3.5-0.8B full-attention shape",
+                   "batch": 64, "ctx": "U(512, 8192)", "context_tokens": int(b.kv_lens.sum()), "q_heads": 8,
+                   "kv_heads": 2, "head_dim": 256, "page_size": 16, "pool_pages": b.pool},
+        "roofline": {"bound": "hbm", "achieved": round(dec_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": dec_bytes, "kernel": "DecodeKernel + DecodeMergeKernel (one run())"},
+        "plan_ms": {"decode": round(dec_plan_ms, 3), "prefill": round(pre_plan_ms, 3)},
+        "prefill": {"workload": "BASELINE config 3: 8 seqs, chunk U(256, 2048) on prefix U(0, 6144), causal",
+                    "ms": round(pre_ms, 4), "tflops": round(pre_tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+                    "frac": round(pre_tflops / MFMA_BF16_PEAK_TFLOPS, 4), "flops": pb.prefill_flops(),
+                    "query_tokens": pb.tokens},
+        "gdn": {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()} for k, v in gdn.items()},
+        "cpu_baseline": cpu,
+    }
+    session.close()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -379,7 +379,97 @@ struct DecodeCfg {
   static_assert(kNi * kGroup == kLpr, "each lane must end the reduce-scatter with one (token, head) score");
 };
 
+// One wavefront's running state: acc[h][e] is this lane's slice of sum_j p_j v_j for query head h, m[h] the running
+// max of the head (wave-uniform), l_lane this lane's share of the head-(r % 4) denominator.
 template <typename T, int D>
+struct DecodeState {
+  float acc[kGroup][DecodeCfg<T, D>::kVec];
+  float m[kGroup];
+  float l_lane;
+};
+
+// Folds one 16-token group (already in registers) into the state. valid: bit i set when load i of this lane holds a
+// real key.
+template <typename T, int D, typename QW>
+__device__ __forceinline__ void DecodeGroup(DecodeState<T, D>& st, const uint4* kr, const uint4* vr, uint32_t valid,
+                                            const QW (*qr)[DecodeCfg<T, D>::kQWords], float* p_row, int r, int ri,
+                                            int lane, float scale_log2) {
+  using C = DecodeCfg<T, D>;
+  constexpr int kVec = C::kVec, kLpr = C::kLpr, kNi = C::kNi;
+  // Partial scores s[i*4 + h] over this lane's 16-byte slice, then a reduce-scatter across the kLpr lanes of a row:
+  // afterwards lane r holds the complete score of index r (load r / 4, head r % 4).
+  float s[kLpr];
+#pragma unroll
+  for (int i = 0; i < kNi; ++i)
+#pragma unroll
+    for (int h = 0; h < (int)kGroup; ++h) s[i * kGroup + h] = Dot16(kr[i], qr[h], 0.0f);
+#pragma unroll
+  for (int mk = kLpr / 2; mk >= 1; mk >>= 1) {
+    const bool upper = (r & mk) != 0;
+#pragma unroll
+    for (int j = 0; j < mk; ++j) {
+      const float send = upper ? s[j] : s[j + mk];
+      const float keep = upper ? s[j + mk] : s[j];
+      s[j] = keep + ShflXor(send, mk);
+    }
+  }
+  const int my_head = r % kGroup;
+  const bool my_valid = (valid >> (r / kGroup)) & 1u;
+  const float sc = my_valid ? s[0] * scale_log2 : -INFINITY;
+  // Group max per head (lanes sharing r % 4), then every lane learns all 4.
+  float gm = sc;
+#pragma unroll
+  for (int mk = 4; mk < 64; mk <<= 1) gm = fmaxf(gm, ShflXor(gm, mk));
+  const float x1 = ShflXor(gm, 1), x2 = ShflXor(gm, 2), x3 = ShflXor(gm, 3);
+  float corr[kGroup];
+  bool rescale = false;
+#pragma unroll
+  for (int h = 0; h < (int)kGroup; ++h) {
+    const int dd = h ^ my_head;
+    const float hm = dd == 0 ? gm : (dd == 1 ? x1 : (dd == 2 ? x2 : x3));
+    const float mn = fmaxf(st.m[h], hm);
+    corr[h] = mn == -INFINITY ? 1.0f : exp2f(st.m[h] - mn);
+    rescale |= mn != st.m[h];
+    st.m[h] = mn;
+  }
+  const float pw = sc == -INFINITY ? 0.0f : exp2f(sc - Pick4(st.m, my_head));
+  st.l_lane = st.l_lane * Pick4(corr, my_head) + pw;
+  if (rescale) {
+#pragma unroll
+    for (int h = 0; h < (int)kGroup; ++h)
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) st.acc[h][e] *= corr[h];
+  }
+  // Weights through LDS: lane (ri, r) needs p of index i*4+h for its own row group ri.
+  p_row[lane] = pw;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float pv[kLpr];
+#pragma unroll
+  for (int i = 0; i < kLpr; i += 4) {
+    const float4 t4 = *reinterpret_cast<const float4*>(&p_row[ri * kLpr + i]);
+    pv[i] = t4.x; pv[i + 1] = t4.y; pv[i + 2] = t4.z; pv[i + 3] = t4.w;
+  }
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int i = 0; i < kNi; ++i) {
+    float vf[kVec];
+    Vec<T>::Widen(vr[i], vf);
+#pragma unroll
+    for (int h = 0; h < (int)kGroup; ++h) {
+      const float w = pv[i * kGroup + h];
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) st.acc[h][e] = fmaf(w, vf[e], st.acc[h][e]);
+    }
+  }
+}
+
+// Split-K paged decode. kFastPage: page_size is a multiple of 16, so a 16-token group (16-aligned within its
+// sequence) lies in one page and its page id is one wave-uniform scalar load; otherwise each lane looks its own
+// token's page up. Loads are branch-free (an absent key reads a valid address and is masked) and the next group's
+// K/V is fetched into a second register buffer while the current group is computed.
+template <typename T, int D, bool kFastPage>
 __global__ void __launch_bounds__(256) DecodeKernel(const T* __restrict__ q, T* __restrict__ out, float* __restrict__ lse,
                                                     KvView kv, const DecodeWork* __restrict__ work,
                                                     float* __restrict__ part_o, float* __restrict__ part_ml,
@@ -391,12 +481,13 @@ __global__ void __launch_bounds__(256) DecodeKernel(const T* __restrict__ q, T* 
   __shared__ float l_lds[4][kGroup];
   __shared__ float o_lds[4][kGroup][D];
 
-  const DecodeWork wk = work[blockIdx.x];
-  const uint32_t kvh = blockIdx.y;
+  // Both KV heads of a chunk are adjacent in launch order, so the two halves of each NHD page row are read together.
+  const DecodeWork wk = work[blockIdx.x / kv.kv_heads];
+  const uint32_t kvh = blockIdx.x % kv.kv_heads;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int r = lane % kLpr;    // which 16-byte slice of a row
-  const int ri = lane / kLpr;   // which row of a wave-wide load
+  const int r = lane % kLpr;   // which 16-byte slice of a row
+  const int ri = lane / kLpr;  // which row of a wave-wide load
   const T* kbase = static_cast<const T*>(kv.k);
   const T* vbase = static_cast<const T*>(kv.v);
 
@@ -405,7 +496,6 @@ __global__ void __launch_bounds__(256) DecodeKernel(const T* __restrict__ q, T* 
   const uint32_t t_begin = static_cast<uint32_t>(wk.token_begin);
   const uint32_t t_end = min(kv_len, t_begin + kDecodeChunkTokens);
 
-  // q slice of the 4 heads: for bf16 kept as packed pairs for v_dot2, for f32 as floats.
   using QW = typename std::conditional<sizeof(T) == 2, uint32_t, float>::type;
   QW qr[kGroup][C::kQWords];
   {
@@ -419,109 +509,61 @@ __global__ void __launch_bounds__(256) DecodeKernel(const T* __restrict__ q, T* 
     }
   }
 
-  float acc[kGroup][kVec];
+  DecodeState<T, D> st;
 #pragma unroll
-  for (int h = 0; h < (int)kGroup; ++h)
+  for (int h = 0; h < (int)kGroup; ++h) {
+    st.m[h] = -INFINITY;
 #pragma unroll
-    for (int e = 0; e < kVec; ++e) acc[h][e] = 0.0f;
-  float m[kGroup];
-#pragma unroll
-  for (int h = 0; h < (int)kGroup; ++h) m[h] = -INFINITY;
-  float l_lane = 0.0f;
-  const int my_head = r % kGroup;
+    for (int e = 0; e < kVec; ++e) st.acc[h][e] = 0.0f;
+  }
+  st.l_lane = 0.0f;
 
-  for (uint32_t g0 = t_begin + 16u * wave; g0 < t_end; g0 += 64u) {
-    uint4 kr[kNi], vr[kNi];
-    bool valid[kNi];
+  const uint64_t tok_stride = kv.hnd ? D : static_cast<uint64_t>(kv.kv_heads) * D;
+  auto load = [&](uint32_t g0, uint4* kr, uint4* vr, uint32_t& valid) {
+    valid = 0;
+    if constexpr (kFastPage) {
+      const uint32_t pi = __builtin_amdgcn_readfirstlane(g0 / kv.page_size);
+      const uint32_t off0 = g0 - pi * kv.page_size;
+      int32_t page = __builtin_amdgcn_readfirstlane(kv.kv_indices[p0 + pi]);
+      const bool page_ok = page >= 0 && static_cast<uint64_t>(page) < kv.pool_pages;
+      const uint64_t pg = page_ok ? static_cast<uint64_t>(page) : 0;
+      const uint64_t base = kv.hnd ? ((pg * kv.kv_heads + kvh) * kv.page_size + off0) * D
+                                   : ((pg * kv.page_size + off0) * kv.kv_heads + kvh) * D;
 #pragma unroll
-    for (int i = 0; i < kNi; ++i) {
-      const uint32_t j = g0 + i * kTpi + ri;
-      int64_t row = j < t_end ? KeyRow<D>(kv, p0, j, kvh) : -1;
-      valid[i] = row >= 0;
-      if (valid[i]) {
+      for (int i = 0; i < kNi; ++i) {
+        const uint32_t tt = i * kTpi + ri;
+        const bool ok = page_ok && g0 + tt < t_end;
+        const uint64_t at = base + (ok ? tt : 0) * tok_stride + r * kVec;
+        kr[i] = *reinterpret_cast<const uint4*>(kbase + at);
+        vr[i] = *reinterpret_cast<const uint4*>(vbase + at);
+        valid |= static_cast<uint32_t>(ok) << i;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kNi; ++i) {
+        bool ok;
+        const uint64_t row = KeyRowSafe<D>(kv, p0, static_cast<int32_t>(g0 + i * kTpi + ri),
+                                           static_cast<int32_t>(t_end), kvh, &ok);
         kr[i] = *reinterpret_cast<const uint4*>(kbase + row + r * kVec);
         vr[i] = *reinterpret_cast<const uint4*>(vbase + row + r * kVec);
-      } else {
-        kr[i] = make_uint4(0, 0, 0, 0);
-        vr[i] = make_uint4(0, 0, 0, 0);
+        valid |= static_cast<uint32_t>(ok) << i;
       }
     }
-    // Partial scores s[i*4 + h] over this lane's 16-byte slice.
-    float s[kLpr];
-#pragma unroll
-    for (int i = 0; i < kNi; ++i)
-#pragma unroll
-      for (int h = 0; h < (int)kGroup; ++h) s[i * kGroup + h] = Dot16(kr[i], qr[h], 0.0f);
-    // Reduce-scatter across the kLpr lanes of a row: afterwards lane r holds the full score of index r.
-#pragma unroll
-    for (int mk = kLpr / 2; mk >= 1; mk >>= 1) {
-      const bool upper = (r & mk) != 0;
-#pragma unroll
-      for (int j = 0; j < mk; ++j) {
-        const float send = upper ? s[j] : s[j + mk];
-        const float keep = upper ? s[j + mk] : s[j];
-        s[j] = keep + ShflXor(send, mk);
-      }
-    }
-    const int my_i = r / kGroup;  // load index of the token this lane's score belongs to
-    bool my_valid = false;
-#pragma unroll
-    for (int i = 0; i < kNi; ++i) my_valid = i == my_i ? valid[i] : my_valid;
-    const float sc = my_valid ? s[0] * scale_log2 : -INFINITY;
-    // Group max per head: lanes sharing r % 4.
-    float gm = sc;
-#pragma unroll
-    for (int mk = 4; mk < 64; mk <<= 1) gm = fmaxf(gm, ShflXor(gm, mk));
-    // Every lane learns the max of all 4 heads.
-    float hm[kGroup];
-    {
-      const float x1 = ShflXor(gm, 1), x2 = ShflXor(gm, 2), x3 = ShflXor(gm, 3);
-#pragma unroll
-      for (int h = 0; h < (int)kGroup; ++h) {
-        const int d = h ^ my_head;
-        hm[h] = d == 0 ? gm : (d == 1 ? x1 : (d == 2 ? x2 : x3));
-      }
-    }
-    float corr[kGroup];
-    bool rescale = false;
-#pragma unroll
-    for (int h = 0; h < (int)kGroup; ++h) {
-      const float mn = fmaxf(m[h], hm[h]);
-      corr[h] = mn == -INFINITY ? 1.0f : exp2f(m[h] - mn);
-      rescale |= mn != m[h];
-      m[h] = mn;
-    }
-    const float pw = sc == -INFINITY ? 0.0f : exp2f(sc - Pick4(m, my_head));
-    l_lane = l_lane * Pick4(corr, my_head) + pw;
-    if (rescale) {
-#pragma unroll
-      for (int h = 0; h < (int)kGroup; ++h)
-#pragma unroll
-        for (int e = 0; e < kVec; ++e) acc[h][e] *= corr[h];
-    }
-    // Exchange the weights: lane (ri, r) needs p of index i*4+h for its own row group ri.
-    p_lds[wave][lane] = pw;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    float pv[kLpr];
-#pragma unroll
-    for (int i = 0; i < kLpr; i += 4) {
-      const float4 t4 = *reinterpret_cast<const float4*>(&p_lds[wave][ri * kLpr + i]);
-      pv[i] = t4.x; pv[i + 1] = t4.y; pv[i + 2] = t4.z; pv[i + 3] = t4.w;
-    }
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int i = 0; i < kNi; ++i) {
-      float vf[kVec];
-      Vec<T>::Widen(vr[i], vf);
-#pragma unroll
-      for (int h = 0; h < (int)kGroup; ++h) {
-        const float w = pv[i * kGroup + h];
-#pragma unroll
-        for (int e = 0; e < kVec; ++e) acc[h][e] = fmaf(w, vf[e], acc[h][e]);
-      }
-    }
+  };
+
+  uint4 ka[kNi], va[kNi], kb[kNi], vb[kNi];
+  uint32_t valid_a = 0, valid_b = 0;
+  uint32_t g0 = t_begin + 16u * wave;
+  if (g0 < t_end) load(g0, ka, va, valid_a);
+  while (g0 < t_end) {
+    const uint32_t g1 = g0 + 64u;
+    if (g1 < t_end) load(g1, kb, vb, valid_b);
+    DecodeGroup<T, D, QW>(st, ka, va, valid_a, qr, p_lds[wave], r, ri, lane, scale_log2);
+    if (g1 >= t_end) break;
+    const uint32_t g2 = g1 + 64u;
+    if (g2 < t_end) load(g2, ka, va, valid_a);
+    DecodeGroup<T, D, QW>(st, kb, vb, valid_b, qr, p_lds[wave], r, ri, lane, scale_log2);
+    g0 = g2;
   }
 
   // Wave: fold the row groups (lanes sharing r) and total the per-lane denominators per head.
@@ -530,19 +572,19 @@ __global__ void __launch_bounds__(256) DecodeKernel(const T* __restrict__ q, T* 
 #pragma unroll
     for (int h = 0; h < (int)kGroup; ++h)
 #pragma unroll
-      for (int e = 0; e < kVec; ++e) acc[h][e] += ShflXor(acc[h][e], mk);
-  float lsum = l_lane;
+      for (int e = 0; e < kVec; ++e) st.acc[h][e] += ShflXor(st.acc[h][e], mk);
+  float lsum = st.l_lane;
 #pragma unroll
   for (int mk = 4; mk < 64; mk <<= 1) lsum += ShflXor(lsum, mk);
   if (lane < (int)kGroup) {
-    m_lds[wave][lane] = Pick4(m, lane);
+    m_lds[wave][lane] = Pick4(st.m, lane);
     l_lds[wave][lane] = lsum;  // lane h holds the total of head h (lanes with r % 4 == h)
   }
   if (ri == 0) {
 #pragma unroll
     for (int h = 0; h < (int)kGroup; ++h)
 #pragma unroll
-      for (int e = 0; e < kVec; ++e) o_lds[wave][h][r * kVec + e] = acc[h][e];
+      for (int e = 0; e < kVec; ++e) o_lds[wave][h][r * kVec + e] = st.acc[h][e];
   }
   __syncthreads();
 
@@ -832,9 +874,14 @@ RoostStatus LaunchDecode(const RoostPagedAttentionParams& p, const PlanRecord& r
   auto* out = static_cast<T*>(p.output.address);
   auto* lse = static_cast<float*>(p.lse.address);
   if (rec.work_items > 0) {
-    hipLaunchKernelGGL((DecodeKernel<T, D>), dim3(static_cast<uint32_t>(rec.work_items), p.kv_heads), dim3(256), 0,
-                       stream, static_cast<const T*>(p.q.address), out, lse, kv, items, part_o, part_ml, p.q_heads,
-                       scale_log2);
+    const dim3 grid(static_cast<uint32_t>(rec.work_items * p.kv_heads));
+    if (p.page_size % 16 == 0) {
+      hipLaunchKernelGGL((DecodeKernel<T, D, true>), grid, dim3(256), 0, stream, static_cast<const T*>(p.q.address), out,
+                         lse, kv, items, part_o, part_ml, p.q_heads, scale_log2);
+    } else {
+      hipLaunchKernelGGL((DecodeKernel<T, D, false>), grid, dim3(256), 0, stream, static_cast<const T*>(p.q.address),
+                         out, lse, kv, items, part_o, part_ml, p.q_heads, scale_log2);
+    }
     ROOST_TRY(roost::FromHip(hipGetLastError(), "PagedAttention decode launch"));
   }
   hipLaunchKernelGGL((DecodeMergeKernel<T, D>), dim3(p.batch, p.q_heads), dim3(D < 256 ? D : 256), 0, stream, out, lse,
