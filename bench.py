@@ -205,6 +205,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=16)
+    ap.add_argument("--only", choices=["decode", "prefill", "gdn"], default=None,
+                    help="run one workload only and print its timing (for profiler passes); no JSON line")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -219,6 +221,12 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs the MI355X"
     torch.cuda.set_device(0)
     session = roost_amd.OpSession(device=0)
+    if args.only is not None:
+        fn = {"decode": bench_decode, "prefill": bench_prefill, "gdn": bench_gdn}[args.only]
+        res = fn(torch, roost_amd, session, args.steps, args.warmup)
+        log(f"{args.only}: {res[1] if isinstance(res, tuple) else res} ms")
+        session.close()
+        return
     log("decode (config 2) ...")
     b, dec_ms, dec_plan_ms = bench_decode(torch, roost_amd, session, args.steps, args.warmup)
     dec_bytes = b.decode_bytes()

@@ -17,11 +17,12 @@
 #include "../../include/roost_amd.h"
 #include "../../include/roost_kernels.h"
 
-// Per-library, per-device state. The gfx950 kernels need no handles or loaded modules, so the context records the
-// device and the creation flags only.
+// Per-library, per-device state. The gfx950 kernels need no handles or loaded modules; the context records the
+// device, the creation flags and the device's compute-unit count (the decode planner sizes its grid to it).
 struct RoostContext {
   int32_t device;
   uint32_t flags;
+  uint32_t compute_units;
 };
 
 void roost_set_error(const char* message);

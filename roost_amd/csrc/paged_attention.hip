@@ -43,7 +43,8 @@ namespace {
 using namespace roost_dev;
 
 constexpr uint32_t kGroup = 4;                  // query heads per KV head (Qwen3.5: 8 over 2)
-constexpr uint32_t kDecodeChunkTokens = 512;    // split-K chunk
+constexpr uint32_t kDecodeWgsPerCu = 2;         // decode workgroups resident per CU (register-limited occupancy)
+constexpr uint32_t kMaxMergeSplits = 1024;      // partials one sequence may be split into
 constexpr uint32_t kPrefillTileQ = 32;          // query tokens per prefill workgroup
 constexpr uint32_t kPrefillTileK = 64;          // keys per LDS tile
 constexpr uint32_t kAlign = 256;
@@ -52,13 +53,15 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 struct DecodeWork {
   int32_t seq;
-  int32_t page_begin;  // first page entry of the chunk, relative to the sequence
-  int32_t token_begin; // first key of the chunk
-  int32_t split;       // partial slot, or -1 when the sequence has a single chunk
+  int32_t token_begin;  // first key of this piece (a multiple of 16)
+  int32_t token_end;    // one past its last key
+  int32_t slot;         // partial slot, or -1 when the piece is the whole sequence (written as the final row)
 };
-struct SeqSplits {
-  int32_t first;  // first partial slot
-  int32_t count;  // chunks of the sequence (0: no keys)
+struct DecodeMerge {
+  int32_t seq;
+  int32_t first;  // first partial slot; the sequence's pieces own slots first .. first + count - 1 in key order
+  int32_t count;
+  int32_t reserved;
 };
 struct PrefillWork {
   int32_t seq;
@@ -78,7 +81,11 @@ struct PlanRecord {
   uint32_t head_dim;
   uint32_t kv_heads;
   uint64_t pages;        // kv_indptr_host[batch]
-  uint64_t work_items;
+  uint64_t work_items;   // decode pieces or prefill tiles
+  uint64_t ranges;       // decode: workgroup ranges over the pieces
+  uint64_t merges;       // decode: sequences whose pieces are merged
+  uint64_t range_offset; // byte offsets in the int region
+  uint64_t merge_offset;
   uint64_t splits;       // decode partial slots
   uint64_t int_bytes;    // [work items | seq splits]
   uint64_t float_offset; // partials start here
@@ -87,8 +94,11 @@ struct PlanRecord {
 
 struct Layout {
   uint64_t work_items = 0;
+  uint64_t ranges = 0;
+  uint64_t merges = 0;
+  uint64_t range_offset = 0;
+  uint64_t merge_offset = 0;
   uint64_t splits = 0;
-  uint64_t seq_offset = 0;  // byte offset of SeqSplits in the int region
   uint64_t int_bytes = 0;
   uint64_t float_offset = 0;
   uint64_t float_bytes = 0;
@@ -182,14 +192,17 @@ RoostStatus Validate(const RoostPagedAttentionParams& p, bool for_run) {
 
 // ---- Host planning ---------------------------------------------------------------------------------------------------
 
-Layout MakeLayout(uint64_t work_items, uint64_t splits, uint64_t batch, uint32_t q_heads, uint32_t head_dim,
-                  uint32_t mode) {
+Layout MakeLayout(uint64_t work_items, uint64_t ranges, uint64_t merges, uint64_t splits, uint32_t q_heads,
+                  uint32_t head_dim, uint32_t mode) {
   Layout l;
   l.work_items = work_items;
+  l.ranges = ranges;
+  l.merges = merges;
   l.splits = splits;
   const uint64_t item_bytes = mode == ROOST_ATTENTION_DECODE ? sizeof(DecodeWork) : sizeof(PrefillWork);
-  l.seq_offset = roost::AlignUp(work_items * item_bytes, 16);
-  l.int_bytes = l.seq_offset + (mode == ROOST_ATTENTION_DECODE ? batch * sizeof(SeqSplits) : 0);
+  l.range_offset = roost::AlignUp(work_items * item_bytes, 16);
+  l.merge_offset = roost::AlignUp(l.range_offset + (ranges > 0 ? (ranges + 1) * sizeof(int32_t) : 0), 16);
+  l.int_bytes = l.merge_offset + merges * sizeof(DecodeMerge);
   l.float_offset = roost::AlignUp(l.int_bytes, kAlign);
   l.float_bytes = splits * q_heads * (static_cast<uint64_t>(head_dim) + 2) * sizeof(float);
   l.total = l.float_offset + l.float_bytes;
@@ -203,30 +216,62 @@ uint32_t KvLenHost(const RoostPagedAttentionParams& p, uint32_t b) {
   return static_cast<uint32_t>((pages - 1) * p.page_size + last);
 }
 
-// Decode: one work item per 512-token chunk. Writes items and per-sequence split tables into `host` when non-NULL.
-Layout PlanDecode(const RoostPagedAttentionParams& p, unsigned char* host) {
-  uint64_t items = 0, splits = 0;
-  std::vector<SeqSplits> seqs(p.batch);
+// Decode: the batch's 16-token groups are dealt out evenly to `ranges` workgroup ranges (one workgroup per range and
+// KV head, kDecodeWgsPerCu per CU), each range cut at sequence boundaries into pieces. Every workgroup then streams
+// the same number of bytes and the grid finishes together instead of in ragged rounds. A sequence cut into several
+// pieces owns consecutive partial slots and one DecodeMerge entry; a sequence without keys is one empty piece that
+// writes its zero rows. The split depends on the batch, so the variant is deterministic but not batch invariant.
+Layout PlanDecode(const RoostPagedAttentionParams& p, uint32_t cus, unsigned char* host) {
+  std::vector<uint64_t> groups(p.batch);
+  uint64_t total = 0;
+  for (uint32_t b = 0; b < p.batch; ++b) {
+    groups[b] = roost::CeilDiv(KvLenHost(p, b), 16);
+    total += groups[b];
+  }
+  const uint64_t slots_wanted = std::max<uint64_t>(1, static_cast<uint64_t>(cus) * kDecodeWgsPerCu / p.kv_heads);
+  const uint64_t ranges = std::max<uint64_t>(1, std::min<uint64_t>(slots_wanted, total));
+  const uint64_t per_range = std::max<uint64_t>(1, roost::CeilDiv(total, ranges));
+  // First pass: count pieces, merges and slots; second pass (host != NULL): write them.
+  std::vector<DecodeWork> items;
+  std::vector<int32_t> range_ptr;
+  std::vector<DecodeMerge> merges;
+  items.reserve(p.batch + ranges * 2);
+  range_ptr.reserve(ranges + 1);
+  range_ptr.push_back(0);
+  uint64_t room = per_range;  // groups left in the current range
+  int32_t slot = 0;
   for (uint32_t b = 0; b < p.batch; ++b) {
     const uint32_t kv = KvLenHost(p, b);
-    const uint32_t chunks = static_cast<uint32_t>(roost::CeilDiv(kv, kDecodeChunkTokens));
-    seqs[b].count = static_cast<int32_t>(chunks);
-    seqs[b].first = chunks > 1 ? static_cast<int32_t>(splits) : -1;
-    items += chunks;
-    if (chunks > 1) splits += chunks;
-  }
-  Layout l = MakeLayout(items, splits, p.batch, p.q_heads, p.head_dim, ROOST_ATTENTION_DECODE);
-  if (host != nullptr) {
-    auto* w = reinterpret_cast<DecodeWork*>(host);
-    uint64_t i = 0;
-    for (uint32_t b = 0; b < p.batch; ++b) {
-      for (int32_t c = 0; c < seqs[b].count; ++c) {
-        const int32_t tok = c * static_cast<int32_t>(kDecodeChunkTokens);
-        w[i++] = DecodeWork{static_cast<int32_t>(b), tok / static_cast<int32_t>(p.page_size), tok,
-                            seqs[b].count > 1 ? seqs[b].first + c : -1};
-      }
+    if (groups[b] == 0) {
+      items.push_back(DecodeWork{static_cast<int32_t>(b), 0, 0, -1});
+      continue;
     }
-    std::memcpy(host + l.seq_offset, seqs.data(), seqs.size() * sizeof(SeqSplits));
+    const size_t first_item = items.size();
+    uint64_t g = 0;
+    while (g < groups[b]) {
+      if (room == 0) {
+        range_ptr.push_back(static_cast<int32_t>(items.size()));
+        room = per_range;
+      }
+      const uint64_t take = std::min(room, groups[b] - g);
+      items.push_back(DecodeWork{static_cast<int32_t>(b), static_cast<int32_t>(g * 16),
+                                 static_cast<int32_t>(std::min<uint64_t>((g + take) * 16, kv)), -1});
+      g += take;
+      room -= take;
+    }
+    const size_t pieces = items.size() - first_item;
+    if (pieces > 1) {
+      merges.push_back(DecodeMerge{static_cast<int32_t>(b), slot, static_cast<int32_t>(pieces), 0});
+      for (size_t i = first_item; i < items.size(); ++i) items[i].slot = slot++;
+    }
+  }
+  range_ptr.push_back(static_cast<int32_t>(items.size()));
+  Layout l = MakeLayout(items.size(), range_ptr.size() - 1, merges.size(), static_cast<uint64_t>(slot), p.q_heads,
+                        p.head_dim, ROOST_ATTENTION_DECODE);
+  if (host != nullptr) {
+    std::memcpy(host, items.data(), items.size() * sizeof(DecodeWork));
+    std::memcpy(host + l.range_offset, range_ptr.data(), range_ptr.size() * sizeof(int32_t));
+    std::memcpy(host + l.merge_offset, merges.data(), merges.size() * sizeof(DecodeMerge));
   }
   return l;
 }
@@ -252,7 +297,7 @@ Layout PlanPrefill(const RoostPagedAttentionParams& p, unsigned char* host) {
     }
   }
   std::stable_sort(items.begin(), items.end(), [](const Item& a, const Item& b) { return a.cost > b.cost; });
-  Layout l = MakeLayout(items.size(), 0, p.batch, p.q_heads, p.head_dim, ROOST_ATTENTION_PREFILL);
+  Layout l = MakeLayout(items.size(), 0, 0, 0, p.q_heads, p.head_dim, ROOST_ATTENTION_PREFILL);
   if (host != nullptr) {
     auto* w = reinterpret_cast<PrefillWork*>(host);
     for (size_t i = 0; i < items.size(); ++i) w[i] = items[i].w;
@@ -260,8 +305,10 @@ Layout PlanPrefill(const RoostPagedAttentionParams& p, unsigned char* host) {
   return l;
 }
 
-Layout PlanLayout(const RoostPagedAttentionParams& p, unsigned char* host) {
-  return p.mode == ROOST_ATTENTION_DECODE ? PlanDecode(p, host) : PlanPrefill(p, host);
+uint32_t ComputeUnits(const RoostContext* ctx) { return ctx != nullptr && ctx->compute_units > 0 ? ctx->compute_units : 256; }
+
+Layout PlanLayout(const RoostPagedAttentionParams& p, uint32_t cus, unsigned char* host) {
+  return p.mode == ROOST_ATTENTION_DECODE ? PlanDecode(p, cus, host) : PlanPrefill(p, host);
 }
 
 // ---- Device helpers --------------------------------------------------------------------------------------------------
@@ -388,31 +435,29 @@ struct DecodeState {
   float l_lane;
 };
 
-// Folds one 16-token group (already in registers) into the state. valid: bit i set when load i of this lane holds a
-// real key.
+// Folds one 16-token group (already in registers) into the state.
+//
+// Lane (ri, r) holds, for K, the 16-byte slice r of token slot i ^ (r >> 2) in register i, and q of head h ^ (r & 3)
+// in register h; so its partial score register j = 4i + h stands for the logical (slot, head) index j ^ r. With that
+// permutation the reduce-scatter needs no selects: at distance mk the partner's register j + mk stands for the same
+// logical index as this lane's register j, so s[j] += partner.s[j + mk]; afterwards register 0 holds the complete score
+// of index r (slot r / 4, head r % 4). V register i holds slot i in natural order.
+// valid: bit s set when token slot s of this lane's row group is a real key.
 template <typename T, int D, typename QW>
 __device__ __forceinline__ void DecodeGroup(DecodeState<T, D>& st, const uint4* kr, const uint4* vr, uint32_t valid,
-                                            const QW (*qr)[DecodeCfg<T, D>::kQWords], float* p_row, int r, int ri,
+                                            const QW (*qr)[DecodeCfg<T, D>::kQWords], float* x_row, int r, int ri,
                                             int lane, float scale_log2) {
   using C = DecodeCfg<T, D>;
   constexpr int kVec = C::kVec, kLpr = C::kLpr, kNi = C::kNi;
-  // Partial scores s[i*4 + h] over this lane's 16-byte slice, then a reduce-scatter across the kLpr lanes of a row:
-  // afterwards lane r holds the complete score of index r (load r / 4, head r % 4).
   float s[kLpr];
 #pragma unroll
   for (int i = 0; i < kNi; ++i)
 #pragma unroll
     for (int h = 0; h < (int)kGroup; ++h) s[i * kGroup + h] = Dot16(kr[i], qr[h], 0.0f);
 #pragma unroll
-  for (int mk = kLpr / 2; mk >= 1; mk >>= 1) {
-    const bool upper = (r & mk) != 0;
+  for (int mk = kLpr / 2; mk >= 1; mk >>= 1)
 #pragma unroll
-    for (int j = 0; j < mk; ++j) {
-      const float send = upper ? s[j] : s[j + mk];
-      const float keep = upper ? s[j + mk] : s[j];
-      s[j] = keep + ShflXor(send, mk);
-    }
-  }
+    for (int j = 0; j < mk; ++j) s[j] += ShflXor(s[j + mk], mk);
   const int my_head = r % kGroup;
   const bool my_valid = (valid >> (r / kGroup)) & 1u;
   const float sc = my_valid ? s[0] * scale_log2 : -INFINITY;
@@ -440,27 +485,61 @@ __device__ __forceinline__ void DecodeGroup(DecodeState<T, D>& st, const uint4* 
 #pragma unroll
       for (int e = 0; e < kVec; ++e) st.acc[h][e] *= corr[h];
   }
-  // Weights through LDS: lane (ri, r) needs p of index i*4+h for its own row group ri.
-  p_row[lane] = pw;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  float pv[kLpr];
+  if constexpr (sizeof(T) == 2) {
+    // bf16: the weights of slots 2a and 2a+1 (lanes r and r ^ 4) travel as one packed bf16 pair per head, and P.V runs
+    // on v_dot2 over token pairs (P rounded to bf16 before the product, fp32 accumulation).
+    const float po = ShflXor(pw, 4);
+    auto* xw = reinterpret_cast<uint32_t*>(x_row);
+    if ((r & 4) == 0) xw[ri * (kLpr / 2) + (r >> 3) * kGroup + my_head] = PackBf16(pw, po);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    uint32_t pp[kNi / 2][kGroup];
 #pragma unroll
-  for (int i = 0; i < kLpr; i += 4) {
-    const float4 t4 = *reinterpret_cast<const float4*>(&p_row[ri * kLpr + i]);
-    pv[i] = t4.x; pv[i + 1] = t4.y; pv[i + 2] = t4.z; pv[i + 3] = t4.w;
-  }
-  __builtin_amdgcn_wave_barrier();
+    for (int a = 0; a < kNi / 2; ++a) {
+      const uint4 t4 = *reinterpret_cast<const uint4*>(&xw[ri * (kLpr / 2) + a * kGroup]);
+      pp[a][0] = t4.x; pp[a][1] = t4.y; pp[a][2] = t4.z; pp[a][3] = t4.w;
+    }
+    __builtin_amdgcn_wave_barrier();
 #pragma unroll
-  for (int i = 0; i < kNi; ++i) {
-    float vf[kVec];
-    Vec<T>::Widen(vr[i], vf);
+    for (int a = 0; a < kNi / 2; ++a) {
+      const uint32_t* v0 = reinterpret_cast<const uint32_t*>(&vr[2 * a]);
+      const uint32_t* v1 = reinterpret_cast<const uint32_t*>(&vr[2 * a + 1]);
 #pragma unroll
-    for (int h = 0; h < (int)kGroup; ++h) {
-      const float w = pv[i * kGroup + h];
+      for (int w = 0; w < kVec / 2; ++w) {
+        const uint32_t lo = __builtin_amdgcn_perm(v1[w], v0[w], 0x05040100u);  // (v[2a][2w], v[2a+1][2w])
+        const uint32_t hi = __builtin_amdgcn_perm(v1[w], v0[w], 0x07060302u);  // (v[2a][2w+1], v[2a+1][2w+1])
 #pragma unroll
-      for (int e = 0; e < kVec; ++e) st.acc[h][e] = fmaf(w, vf[e], st.acc[h][e]);
+        for (int h = 0; h < (int)kGroup; ++h) {
+          const bf16x2_t ph = __builtin_bit_cast(bf16x2_t, pp[a][h]);
+          st.acc[h][2 * w] = __builtin_amdgcn_fdot2_f32_bf16(ph, __builtin_bit_cast(bf16x2_t, lo), st.acc[h][2 * w], false);
+          st.acc[h][2 * w + 1] =
+              __builtin_amdgcn_fdot2_f32_bf16(ph, __builtin_bit_cast(bf16x2_t, hi), st.acc[h][2 * w + 1], false);
+        }
+      }
+    }
+  } else {
+    x_row[lane] = pw;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float pv[kLpr];
+#pragma unroll
+    for (int i = 0; i < kLpr; i += 4) {
+      const float4 t4 = *reinterpret_cast<const float4*>(&x_row[ri * kLpr + i]);
+      pv[i] = t4.x; pv[i + 1] = t4.y; pv[i + 2] = t4.z; pv[i + 3] = t4.w;
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 0; i < kNi; ++i) {
+      float vf[kVec];
+      Vec<T>::Widen(vr[i], vf);
+#pragma unroll
+      for (int h = 0; h < (int)kGroup; ++h) {
+        const float w = pv[i * kGroup + h];
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) st.acc[h][e] = fmaf(w, vf[e], st.acc[h][e]);
+      }
     }
   }
 }
@@ -468,33 +547,42 @@ __device__ __forceinline__ void DecodeGroup(DecodeState<T, D>& st, const uint4* 
 // Split-K paged decode. kFastPage: page_size is a multiple of 16, so a 16-token group (16-aligned within its
 // sequence) lies in one page and its page id is one wave-uniform scalar load; otherwise each lane looks its own
 // token's page up. Loads are branch-free (an absent key reads a valid address and is masked) and the next group's
-// K/V is fetched into a second register buffer while the current group is computed.
+// K/V is fetched into a second register buffer while the current group is computed. Workgroup (range, KV head)
+// processes the pieces of its range in turn; a piece that is not a whole sequence writes fp32 partials that
+// DecodeMergeKernel combines in key order.
 template <typename T, int D, bool kFastPage>
-__global__ void __launch_bounds__(256) DecodeKernel(const T* __restrict__ q, T* __restrict__ out, float* __restrict__ lse,
-                                                    KvView kv, const DecodeWork* __restrict__ work,
+__global__ void __launch_bounds__(256, 2) DecodeKernel(const T* __restrict__ q, T* __restrict__ out, float* __restrict__ lse,
+                                                    KvView kv, const int32_t* __restrict__ kv_indices,
+                                                    const DecodeWork* __restrict__ work,
+                                                    const int32_t* __restrict__ range_ptr,
                                                     float* __restrict__ part_o, float* __restrict__ part_ml,
                                                     uint32_t q_heads, float scale_log2) {
   using C = DecodeCfg<T, D>;
   constexpr int kVec = C::kVec, kLpr = C::kLpr, kTpi = C::kTpi, kNi = C::kNi;
-  __shared__ float p_lds[4][64];
+  __shared__ float x_lds[4][64];
   __shared__ float m_lds[4][kGroup];
   __shared__ float l_lds[4][kGroup];
   __shared__ float o_lds[4][kGroup][D];
 
-  // Both KV heads of a chunk are adjacent in launch order, so the two halves of each NHD page row are read together.
-  const DecodeWork wk = work[blockIdx.x / kv.kv_heads];
+  // Both KV heads of a range are adjacent in launch order, so the two halves of each NHD page row are read together.
+  const uint32_t range = blockIdx.x / kv.kv_heads;
   const uint32_t kvh = blockIdx.x % kv.kv_heads;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // The wavefront index is uniform within a wavefront; saying so lets the group's page id be a scalar load.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane % kLpr;   // which 16-byte slice of a row
   const int ri = lane / kLpr;  // which row of a wave-wide load
+  const int kperm = r / static_cast<int>(kGroup);  // this lane's token-slot permutation for K
   const T* kbase = static_cast<const T*>(kv.k);
   const T* vbase = static_cast<const T*>(kv.v);
 
+  const int32_t it_end = range_ptr[range + 1];
+  for (int32_t it = range_ptr[range]; it < it_end; ++it) {
+  const DecodeWork wk = work[it];
   int32_t p0 = 0;
   const uint32_t kv_len = SeqKvLen(kv, wk.seq, &p0);
   const uint32_t t_begin = static_cast<uint32_t>(wk.token_begin);
-  const uint32_t t_end = min(kv_len, t_begin + kDecodeChunkTokens);
+  const uint32_t t_end = min(kv_len, static_cast<uint32_t>(wk.token_end));
 
   using QW = typename std::conditional<sizeof(T) == 2, uint32_t, float>::type;
   QW qr[kGroup][C::kQWords];
@@ -502,7 +590,7 @@ __global__ void __launch_bounds__(256) DecodeKernel(const T* __restrict__ q, T* 
     const T* qrow = q + (static_cast<uint64_t>(wk.seq) * q_heads + kvh * kGroup) * D + r * kVec;
 #pragma unroll
     for (int h = 0; h < (int)kGroup; ++h) {
-      const uint4 v = *reinterpret_cast<const uint4*>(qrow + h * D);
+      const uint4 v = *reinterpret_cast<const uint4*>(qrow + (h ^ (r & 3)) * D);
       const QW* w = reinterpret_cast<const QW*>(&v);
 #pragma unroll
       for (int i = 0; i < C::kQWords; ++i) qr[h][i] = w[i];
@@ -518,52 +606,63 @@ __global__ void __launch_bounds__(256) DecodeKernel(const T* __restrict__ q, T* 
   }
   st.l_lane = 0.0f;
 
-  const uint64_t tok_stride = kv.hnd ? D : static_cast<uint64_t>(kv.kv_heads) * D;
-  auto load = [&](uint32_t g0, uint4* kr, uint4* vr, uint32_t& valid) {
+  // Byte stride between the rows of consecutive tokens of one KV head inside a page.
+  const uint32_t tok_bytes = (kv.hnd ? D : kv.kv_heads * D) * static_cast<uint32_t>(sizeof(T));
+  // Group gi (0-based, 16 tokens) of this wavefront: key g = t_begin + 16 * (wave + 4 * gi).
+  const uint32_t ngroups = (t_end > t_begin) ? (t_end - t_begin + 15) / 16 : 0;
+  const uint32_t nw = ngroups > static_cast<uint32_t>(wave) ? (ngroups - wave + 3) / 4 : 0;
+  // Every load is unconditional: a group index past the end is clamped to the wave's last group and its keys are
+  // masked, so the number of loads in flight is the same on every path and the compiler can wait for exactly the
+  // current group's data (vmcnt) while the next group's loads stay in flight.
+  auto load = [&](uint32_t gi, uint4* kr, uint4* vr, uint32_t& valid) {
     valid = 0;
+    const uint32_t g0 = t_begin + 16u * (wave + 4u * min(gi, nw - 1));
+    const bool live = gi < nw;
     if constexpr (kFastPage) {
-      const uint32_t pi = __builtin_amdgcn_readfirstlane(g0 / kv.page_size);
+      const uint32_t pi = g0 / kv.page_size;
       const uint32_t off0 = g0 - pi * kv.page_size;
-      int32_t page = __builtin_amdgcn_readfirstlane(kv.kv_indices[p0 + pi]);
+      const int32_t page = kv_indices[p0 + pi];  // uniform address: a scalar load
       const bool page_ok = page >= 0 && static_cast<uint64_t>(page) < kv.pool_pages;
       const uint64_t pg = page_ok ? static_cast<uint64_t>(page) : 0;
-      const uint64_t base = kv.hnd ? ((pg * kv.kv_heads + kvh) * kv.page_size + off0) * D
-                                   : ((pg * kv.page_size + off0) * kv.kv_heads + kvh) * D;
+      const uint64_t row0 = kv.hnd ? (pg * kv.kv_heads + kvh) * kv.page_size + off0
+                                   : (pg * kv.page_size + off0) * kv.kv_heads + kvh;
+      const char* kg = reinterpret_cast<const char*>(kbase + row0 * D);
+      const char* vg = reinterpret_cast<const char*>(vbase + row0 * D);
 #pragma unroll
       for (int i = 0; i < kNi; ++i) {
-        const uint32_t tt = i * kTpi + ri;
-        const bool ok = page_ok && g0 + tt < t_end;
-        const uint64_t at = base + (ok ? tt : 0) * tok_stride + r * kVec;
-        kr[i] = *reinterpret_cast<const uint4*>(kbase + at);
-        vr[i] = *reinterpret_cast<const uint4*>(vbase + at);
-        valid |= static_cast<uint32_t>(ok) << i;
+        const uint32_t tv = i * kTpi + ri;            // V register i: slot i
+        const uint32_t tk = (i ^ kperm) * kTpi + ri;  // K register i: slot i ^ kperm
+        const bool okv = live && page_ok && g0 + tv < t_end;
+        const bool okk = page_ok && g0 + tk < t_end;
+        kr[i] = *reinterpret_cast<const uint4*>(kg + ((okk ? tk : 0) * tok_bytes + r * 16));
+        vr[i] = *reinterpret_cast<const uint4*>(vg + ((okv ? tv : 0) * tok_bytes + r * 16));
+        valid |= static_cast<uint32_t>(okv) << i;
       }
     } else {
 #pragma unroll
       for (int i = 0; i < kNi; ++i) {
-        bool ok;
-        const uint64_t row = KeyRowSafe<D>(kv, p0, static_cast<int32_t>(g0 + i * kTpi + ri),
-                                           static_cast<int32_t>(t_end), kvh, &ok);
-        kr[i] = *reinterpret_cast<const uint4*>(kbase + row + r * kVec);
-        vr[i] = *reinterpret_cast<const uint4*>(vbase + row + r * kVec);
-        valid |= static_cast<uint32_t>(ok) << i;
+        bool okk, okv;
+        const uint64_t rowk = KeyRowSafe<D>(kv, p0, static_cast<int32_t>(g0 + (i ^ kperm) * kTpi + ri),
+                                            static_cast<int32_t>(t_end), kvh, &okk);
+        const uint64_t rowv = KeyRowSafe<D>(kv, p0, static_cast<int32_t>(g0 + i * kTpi + ri),
+                                            static_cast<int32_t>(t_end), kvh, &okv);
+        kr[i] = *reinterpret_cast<const uint4*>(kbase + rowk + r * kVec);
+        vr[i] = *reinterpret_cast<const uint4*>(vbase + rowv + r * kVec);
+        valid |= static_cast<uint32_t>(okv && live) << i;
       }
     }
   };
 
-  uint4 ka[kNi], va[kNi], kb[kNi], vb[kNi];
-  uint32_t valid_a = 0, valid_b = 0;
-  uint32_t g0 = t_begin + 16u * wave;
-  if (g0 < t_end) load(g0, ka, va, valid_a);
-  while (g0 < t_end) {
-    const uint32_t g1 = g0 + 64u;
-    if (g1 < t_end) load(g1, kb, vb, valid_b);
-    DecodeGroup<T, D, QW>(st, ka, va, valid_a, qr, p_lds[wave], r, ri, lane, scale_log2);
-    if (g1 >= t_end) break;
-    const uint32_t g2 = g1 + 64u;
-    if (g2 < t_end) load(g2, ka, va, valid_a);
-    DecodeGroup<T, D, QW>(st, kb, vb, valid_b, qr, p_lds[wave], r, ri, lane, scale_log2);
-    g0 = g2;
+  if (nw > 0) {
+    uint4 ka[kNi], va[kNi], kb[kNi], vb[kNi];
+    uint32_t valid_a = 0, valid_b = 0;
+    load(0, ka, va, valid_a);
+    for (uint32_t gi = 0; gi < nw; gi += 2) {
+      load(gi + 1, kb, vb, valid_b);
+      DecodeGroup<T, D, QW>(st, ka, va, valid_a, qr, x_lds[wave], r, ri, lane, scale_log2);
+      load(gi + 2, ka, va, valid_a);
+      if (gi + 1 < nw) DecodeGroup<T, D, QW>(st, kb, vb, valid_b, qr, x_lds[wave], r, ri, lane, scale_log2);
+    }
   }
 
   // Wave: fold the row groups (lanes sharing r) and total the per-lane denominators per head.
@@ -589,6 +688,7 @@ __global__ void __launch_bounds__(256) DecodeKernel(const T* __restrict__ q, T* 
   __syncthreads();
 
   // Workgroup: merge the 4 wavefronts, then write the final row or this chunk's partial.
+  const int split = wk.slot;
   for (int idx = threadIdx.x; idx < (int)(kGroup * D); idx += 256) {
     const int h = idx / D;
     const int d = idx - h * D;
@@ -603,12 +703,12 @@ __global__ void __launch_bounds__(256) DecodeKernel(const T* __restrict__ q, T* 
       L += l_lds[w][h] * f;
     }
     const uint32_t qh = kvh * kGroup + h;
-    if (wk.split < 0) {
+    if (split < 0) {
       const uint64_t row = static_cast<uint64_t>(wk.seq) * q_heads + qh;
       out[row * D + d] = Vec<T>::Narrow(L > 0.0f ? o / L : 0.0f);
       if (lse != nullptr && d == 0) lse[row] = L > 0.0f ? M + log2f(L) : -INFINITY;
     } else {
-      const uint64_t prow = static_cast<uint64_t>(wk.split) * q_heads + qh;
+      const uint64_t prow = static_cast<uint64_t>(split) * q_heads + qh;
       part_o[prow * D + d] = o;
       if (d == 0) {
         part_ml[prow * 2] = M;
@@ -616,37 +716,63 @@ __global__ void __launch_bounds__(256) DecodeKernel(const T* __restrict__ q, T* 
       }
     }
   }
+  __syncthreads();  // the next piece reuses the LDS merge buffers
+  }
 }
 
-// Combines the chunks of multi-chunk sequences in chunk order and zero-fills sequences without keys.
+// Combines the pieces of each split sequence in key order: one workgroup per (sequence, KV head); the per-piece
+// rescale factors are computed once into LDS, then every output element sums its pieces with independent loads.
 template <typename T, int D>
 __global__ void __launch_bounds__(256) DecodeMergeKernel(T* __restrict__ out, float* __restrict__ lse,
-                                                         const SeqSplits* __restrict__ seqs,
+                                                         const DecodeMerge* __restrict__ merges,
                                                          const float* __restrict__ part_o,
-                                                         const float* __restrict__ part_ml, uint32_t q_heads) {
-  const uint32_t b = blockIdx.x;
-  const uint32_t qh = blockIdx.y;
-  const SeqSplits s = seqs[b];
-  if (s.count == 1) return;
-  const uint64_t row = static_cast<uint64_t>(b) * q_heads + qh;
-  if (s.count == 0) {
-    for (int d = threadIdx.x; d < D; d += blockDim.x) out[row * D + d] = Vec<T>::Narrow(0.0f);
-    if (lse != nullptr && threadIdx.x == 0) lse[row] = -INFINITY;
-    return;
-  }
+                                                         const float* __restrict__ part_ml, uint32_t q_heads,
+                                                         uint32_t kv_heads) {
+  __shared__ float f_lds[kGroup][kMaxMergeSplits];
+  __shared__ float m_lds[kGroup][4];
+  __shared__ float inv_lds[kGroup];
+  __shared__ float lse_lds[kGroup];
+  const DecodeMerge mg = merges[blockIdx.x / kv_heads];
+  const uint32_t kvh = blockIdx.x % kv_heads;
+  const int n = min(mg.count, static_cast<int32_t>(kMaxMergeSplits));
+  const int lane = threadIdx.x & 63;
+  const int h = threadIdx.x >> 6;  // one wavefront per query head of the group
+  const uint32_t qh = kvh * kGroup + h;
+  // Max over pieces (wavefront reduction), then factors and the denominator.
   float M = -INFINITY;
-  for (int c = 0; c < s.count; ++c) M = fmaxf(M, part_ml[(static_cast<uint64_t>(s.first + c) * q_heads + qh) * 2]);
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float o = 0.0f, L = 0.0f;
-    for (int c = 0; c < s.count; ++c) {
-      const uint64_t prow = static_cast<uint64_t>(s.first + c) * q_heads + qh;
-      const float mc = part_ml[prow * 2];
-      const float f = mc == -INFINITY ? 0.0f : exp2f(mc - M);
-      o += part_o[prow * D + d] * f;
-      L += part_ml[prow * 2 + 1] * f;
+  for (int c = lane; c < n; c += 64) M = fmaxf(M, part_ml[(static_cast<uint64_t>(mg.first + c) * q_heads + qh) * 2]);
+  for (int mk = 32; mk >= 1; mk >>= 1) M = fmaxf(M, __shfl_xor(M, mk, 64));
+  float L = 0.0f;
+  for (int c = lane; c < n; c += 64) {
+    const uint64_t prow = static_cast<uint64_t>(mg.first + c) * q_heads + qh;
+    const float mc = part_ml[prow * 2];
+    const float f = mc == -INFINITY ? 0.0f : exp2f(mc - M);
+    f_lds[h][c] = f;
+    L += part_ml[prow * 2 + 1] * f;
+  }
+  for (int mk = 32; mk >= 1; mk >>= 1) L += __shfl_xor(L, mk, 64);
+  if (lane == 0) {
+    inv_lds[h] = L > 0.0f ? 1.0f / L : 0.0f;
+    lse_lds[h] = L > 0.0f ? M + log2f(L) : -INFINITY;
+    m_lds[h][0] = M;
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < (int)(kGroup * D); idx += 256) {
+    const int hh = idx / D;
+    const int d = idx - hh * D;
+    const uint32_t qq = kvh * kGroup + hh;
+    const float* po = part_o + (static_cast<uint64_t>(mg.first) * q_heads + qq) * D + d;
+    const uint64_t step = static_cast<uint64_t>(q_heads) * D;
+    float o0 = 0.0f, o1 = 0.0f;
+    int c = 0;
+    for (; c + 1 < n; c += 2) {
+      o0 = fmaf(po[c * step], f_lds[hh][c], o0);
+      o1 = fmaf(po[(c + 1) * step], f_lds[hh][c + 1], o1);
     }
-    out[row * D + d] = Vec<T>::Narrow(L > 0.0f ? o / L : 0.0f);
-    if (lse != nullptr && d == 0) lse[row] = L > 0.0f ? M + log2f(L) : -INFINITY;
+    if (c < n) o0 = fmaf(po[c * step], f_lds[hh][c], o0);
+    const uint64_t row = static_cast<uint64_t>(mg.seq) * q_heads + qq;
+    out[row * D + d] = Vec<T>::Narrow((o0 + o1) * inv_lds[hh]);
+    if (lse != nullptr && d == 0) lse[row] = lse_lds[hh];
   }
 }
 
@@ -868,30 +994,30 @@ template <typename T, int D>
 RoostStatus LaunchDecode(const RoostPagedAttentionParams& p, const PlanRecord& rec, unsigned char* dev, const KvView& kv,
                          float scale_log2, hipStream_t stream) {
   const auto* items = reinterpret_cast<const DecodeWork*>(dev);
-  const auto* seqs = reinterpret_cast<const SeqSplits*>(dev + roost::AlignUp(rec.work_items * sizeof(DecodeWork), 16));
+  const auto* range_ptr = reinterpret_cast<const int32_t*>(dev + rec.range_offset);
+  const auto* merges = reinterpret_cast<const DecodeMerge*>(dev + rec.merge_offset);
   auto* part_o = reinterpret_cast<float*>(dev + rec.float_offset);
   auto* part_ml = part_o + rec.splits * p.q_heads * D;
   auto* out = static_cast<T*>(p.output.address);
   auto* lse = static_cast<float*>(p.lse.address);
-  if (rec.work_items > 0) {
-    const dim3 grid(static_cast<uint32_t>(rec.work_items * p.kv_heads));
-    if (p.page_size % 16 == 0) {
-      hipLaunchKernelGGL((DecodeKernel<T, D, true>), grid, dim3(256), 0, stream, static_cast<const T*>(p.q.address), out,
-                         lse, kv, items, part_o, part_ml, p.q_heads, scale_log2);
-    } else {
-      hipLaunchKernelGGL((DecodeKernel<T, D, false>), grid, dim3(256), 0, stream, static_cast<const T*>(p.q.address),
-                         out, lse, kv, items, part_o, part_ml, p.q_heads, scale_log2);
-    }
-    ROOST_TRY(roost::FromHip(hipGetLastError(), "PagedAttention decode launch"));
+  const dim3 grid(static_cast<uint32_t>(rec.ranges * p.kv_heads));
+  if (p.page_size % 16 == 0) {
+    hipLaunchKernelGGL((DecodeKernel<T, D, true>), grid, dim3(256), 0, stream, static_cast<const T*>(p.q.address), out,
+                       lse, kv, kv.kv_indices, items, range_ptr, part_o, part_ml, p.q_heads, scale_log2);
+  } else {
+    hipLaunchKernelGGL((DecodeKernel<T, D, false>), grid, dim3(256), 0, stream, static_cast<const T*>(p.q.address), out,
+                       lse, kv, kv.kv_indices, items, range_ptr, part_o, part_ml, p.q_heads, scale_log2);
   }
-  hipLaunchKernelGGL((DecodeMergeKernel<T, D>), dim3(p.batch, p.q_heads), dim3(D < 256 ? D : 256), 0, stream, out, lse,
-                     seqs, part_o, part_ml, p.q_heads);
+  ROOST_TRY(roost::FromHip(hipGetLastError(), "PagedAttention decode launch"));
+  if (rec.merges == 0) return ROOST_STATUS_OK;
+  hipLaunchKernelGGL((DecodeMergeKernel<T, D>), dim3(static_cast<uint32_t>(rec.merges * p.kv_heads)), dim3(256), 0,
+                     stream, out, lse, merges, part_o, part_ml, p.q_heads, p.kv_heads);
   return roost::FromHip(hipGetLastError(), "PagedAttention merge launch");
 }
 
 }  // namespace
 
-extern "C" ROOST_API RoostStatus roost_paged_attention_workspace(RoostContext*, const void* params,
+extern "C" ROOST_API RoostStatus roost_paged_attention_workspace(RoostContext* ctx, const void* params,
                                                                  RoostWorkspaceSizes* sizes) {
   using namespace roost;
   ROOST_TRY(CheckHeader(params, sizeof(RoostPagedAttentionParams), "PagedAttention"));
@@ -899,7 +1025,7 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_workspace(RoostContext*, 
   const auto& p = *static_cast<const RoostPagedAttentionParams*>(params);
   return Guarded("PagedAttention", [&]() -> RoostStatus {
     ROOST_TRY(Validate(p, false));
-    const Layout l = PlanLayout(p, nullptr);
+    const Layout l = PlanLayout(p, ComputeUnits(ctx), nullptr);
     sizes->device_bytes = l.total;
     sizes->pinned_host_bytes = l.int_bytes;
     sizes->plan_bytes = sizeof(PlanRecord);
@@ -908,7 +1034,7 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_workspace(RoostContext*, 
   });
 }
 
-extern "C" ROOST_API RoostStatus roost_paged_attention_plan(RoostContext*, const void* params, const RoostWorkspace* ws,
+extern "C" ROOST_API RoostStatus roost_paged_attention_plan(RoostContext* ctx, const void* params, const RoostWorkspace* ws,
                                                             void* stream) {
   using namespace roost;
   ROOST_TRY(CheckHeader(params, sizeof(RoostPagedAttentionParams), "PagedAttention"));
@@ -918,7 +1044,8 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_plan(RoostContext*, const
     if (ws == nullptr || ws->plan == nullptr) {
       return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: plan needs a workspace with a plan record");
     }
-    const Layout l = PlanLayout(p, nullptr);
+    const uint32_t cus = ComputeUnits(ctx);
+    const Layout l = PlanLayout(p, cus, nullptr);
     if (ws->plan_bytes < sizeof(PlanRecord) || ws->device_bytes < l.total || ws->pinned_host_bytes < l.int_bytes ||
         (l.int_bytes > 0 && ws->pinned_host == nullptr) || (l.total > 0 && ws->device == nullptr) ||
         !Aligned(ws->device, kAlign)) {
@@ -927,7 +1054,7 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_plan(RoostContext*, const
     auto* host = static_cast<unsigned char*>(ws->pinned_host);
     if (l.int_bytes > 0) {
       std::memset(host, 0, l.int_bytes);
-      PlanLayout(p, host);
+      PlanLayout(p, cus, host);
       ROOST_TRY(FromHip(hipMemcpyAsync(ws->device, host, l.int_bytes, hipMemcpyHostToDevice, Stream(stream)),
                         "PagedAttention plan copy"));
     }
@@ -942,6 +1069,10 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_plan(RoostContext*, const
     rec.kv_heads = p.kv_heads;
     rec.pages = static_cast<uint64_t>(p.kv_indptr_host[p.batch]);
     rec.work_items = l.work_items;
+    rec.ranges = l.ranges;
+    rec.merges = l.merges;
+    rec.range_offset = l.range_offset;
+    rec.merge_offset = l.merge_offset;
     rec.splits = l.splits;
     rec.int_bytes = l.int_bytes;
     rec.float_offset = l.float_offset;

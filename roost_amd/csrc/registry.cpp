@@ -104,7 +104,7 @@ constexpr uint32_t kDet = ROOST_FLAG_DETERMINISTIC | ROOST_FLAG_BATCH_INVARIANT;
 
 const RoostOpEntry* Entries(uint32_t* count) {
   static const RoostOpEntry entries[] = {
-      Entry(ROOST_OP_PAGED_ATTENTION, kDet | ROOST_FLAG_NEEDS_PLAN, "paged-attention-gfx950",
+      Entry(ROOST_OP_PAGED_ATTENTION, ROOST_FLAG_DETERMINISTIC | ROOST_FLAG_NEEDS_PLAN, "paged-attention-gfx950",
             sizeof(RoostPagedAttentionParams), AttentionConstraints(), roost_paged_attention_run,
             roost_paged_attention_plan, roost_paged_attention_workspace),
       Entry(ROOST_OP_CACHE_WRITE, kDet | ROOST_FLAG_GRAPH_CAPTURABLE, "cache-write-gfx950", sizeof(RoostCacheWriteParams),
@@ -154,7 +154,13 @@ ROOST_API RoostStatus roost_context_create(const RoostContextCreateParams* param
     return roost::Fail(ROOST_STATUS_ABI_MISMATCH, "roost_context_create: params struct_size or abi_minor is not supported");
   }
   if (params->reserved0 != 0) return roost::Fail(ROOST_STATUS_INVALID_ARGUMENT, "roost_context_create: reserved0 must be zero");
-  *out = new (std::nothrow) RoostContext{params->device, params->flags};
+  // The compute-unit count sizes the decode grid; without a visible device (CPU-only validation) 256 is assumed.
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, params->device) != hipSuccess || cus <= 0) {
+    (void)hipGetLastError();
+    cus = 256;
+  }
+  *out = new (std::nothrow) RoostContext{params->device, params->flags, static_cast<uint32_t>(cus)};
   if (*out == nullptr) return roost::Fail(ROOST_STATUS_OUT_OF_MEMORY, "roost_context_create: out of host memory");
   return ROOST_STATUS_OK;
 }

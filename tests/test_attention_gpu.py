@@ -177,7 +177,11 @@ def test_config2_decode_full_size(session):
     check_against_oracle(got, b)
 
 
-def test_decode_batch_invariance(session):
+def test_decode_row_alone_equals_row_in_batch_within_tolerance(session):
+    """The decode plan deals the batch's keys out evenly over the workgroups, so how a sequence is split depends on the
+    rest of the batch: the variant is DETERMINISTIC (identical batch -> identical bits, checked in run_case) but not
+    BATCH_INVARIANT, like the reference's FlashInfer variant. A row computed alone and inside a batch agree to the
+    parity tolerance."""
     rng = np.random.default_rng(7)
     b = cases.make_paged_batch(rng, [3000, 17, 900], [1, 1, 1])
     many = run_case(session, b, check_nohost=False, check_determinism=False)
@@ -185,7 +189,9 @@ def test_decode_batch_invariance(session):
                            b.kv_indptr[:2].copy(), b.kv_indices[:b.kv_indptr[1]].copy(), b.kv_last_page_len[:1].copy(),
                            b.kv_lens[:1], [1], b.page_size, b.hnd, b.bf16)
     alone = run_case(session, one, check_nohost=False, check_determinism=False)
-    assert np.array_equal(alone, many[:1])
+    cases.assert_close(alone, many[:1], max_abs=2e-2, max_rel=1e-2, what="alone vs in batch")
+    entry = session.lib.entry(roost_amd.ATTENTION_VARIANT)
+    assert entry.flags & abi.FLAG_DETERMINISTIC and not entry.flags & abi.FLAG_BATCH_INVARIANT
 
 
 def test_decode_lse_is_base2_logsumexp(session):
