@@ -43,7 +43,14 @@ namespace {
 using namespace roost_dev;
 
 constexpr uint32_t kGroup = 4;                  // query heads per KV head (Qwen3.5: 8 over 2)
-constexpr uint32_t kDecodeWgsPerCu = 2;         // decode workgroups resident per CU (register-limited occupancy)
+#ifndef ROOST_DECODE_WGS_PER_CU
+#define ROOST_DECODE_WGS_PER_CU 2
+#endif
+#ifndef ROOST_DECODE_RING
+#define ROOST_DECODE_RING 2
+#endif
+constexpr uint32_t kDecodeWgsPerCu = ROOST_DECODE_WGS_PER_CU;  // decode workgroups resident per CU
+constexpr int kDecodeRing = ROOST_DECODE_RING;  // register ring depth: groups in flight per wavefront = ring - 1
 constexpr uint32_t kMaxMergeSplits = 1024;      // partials one sequence may be split into
 constexpr uint32_t kPrefillTileQ = 32;          // query tokens per prefill workgroup
 constexpr uint32_t kPrefillTileK = 64;          // keys per LDS tile
@@ -86,6 +93,7 @@ struct PlanRecord {
   uint64_t merges;       // decode: sequences whose pieces are merged
   uint64_t range_offset; // byte offsets in the int region
   uint64_t merge_offset;
+  uint64_t counter_offset;
   uint64_t splits;       // decode partial slots
   uint64_t int_bytes;    // [work items | seq splits]
   uint64_t float_offset; // partials start here
@@ -98,6 +106,7 @@ struct Layout {
   uint64_t merges = 0;
   uint64_t range_offset = 0;
   uint64_t merge_offset = 0;
+  uint64_t counter_offset = 0;
   uint64_t splits = 0;
   uint64_t int_bytes = 0;
   uint64_t float_offset = 0;
@@ -193,7 +202,7 @@ RoostStatus Validate(const RoostPagedAttentionParams& p, bool for_run) {
 // ---- Host planning ---------------------------------------------------------------------------------------------------
 
 Layout MakeLayout(uint64_t work_items, uint64_t ranges, uint64_t merges, uint64_t splits, uint32_t q_heads,
-                  uint32_t head_dim, uint32_t mode) {
+                  uint32_t kv_heads, uint32_t head_dim, uint32_t mode) {
   Layout l;
   l.work_items = work_items;
   l.ranges = ranges;
@@ -216,11 +225,15 @@ uint32_t KvLenHost(const RoostPagedAttentionParams& p, uint32_t b) {
   return static_cast<uint32_t>((pages - 1) * p.page_size + last);
 }
 
-// Decode: the batch's 16-token groups are dealt out evenly to `ranges` workgroup ranges (one workgroup per range and
-// KV head, kDecodeWgsPerCu per CU), each range cut at sequence boundaries into pieces. Every workgroup then streams
-// the same number of bytes and the grid finishes together instead of in ragged rounds. A sequence cut into several
-// pieces owns consecutive partial slots and one DecodeMerge entry; a sequence without keys is one empty piece that
-// writes its zero rows. The split depends on the batch, so the variant is deterministic but not batch invariant.
+// Decode: the batch's 16-token groups are dealt out evenly to `ranges` workgroup ranges (kDecodeWgsPerCu workgroups
+// per CU), each range cut at sequence boundaries into pieces. Every workgroup then streams the same number of bytes
+// and the grid finishes together instead of in ragged rounds. A sequence cut into several pieces owns consecutive
+// partial slots and one DecodeMerge entry (merged by DecodeMergeKernel); a sequence without keys is one empty piece
+// that writes its zero rows.
+// The split depends on the batch, so the variant is deterministic but not batch invariant.
+// KV heads one decode workgroup serves: 4, 2 or 1, whichever divides kv_heads first.
+uint32_t HeadsPerWorkgroup(uint32_t kv_heads) { return kv_heads % 4 == 0 ? 4 : (kv_heads % 2 == 0 ? 2 : 1); }
+
 Layout PlanDecode(const RoostPagedAttentionParams& p, uint32_t cus, unsigned char* host) {
   std::vector<uint64_t> groups(p.batch);
   uint64_t total = 0;
@@ -228,9 +241,13 @@ Layout PlanDecode(const RoostPagedAttentionParams& p, uint32_t cus, unsigned cha
     groups[b] = roost::CeilDiv(KvLenHost(p, b), 16);
     total += groups[b];
   }
-  const uint64_t slots_wanted = std::max<uint64_t>(1, static_cast<uint64_t>(cus) * kDecodeWgsPerCu / p.kv_heads);
+  const uint64_t slots_wanted = std::max<uint64_t>(
+      1, static_cast<uint64_t>(cus) * kDecodeWgsPerCu / (p.kv_heads / HeadsPerWorkgroup(p.kv_heads)));
   const uint64_t ranges = std::max<uint64_t>(1, std::min<uint64_t>(slots_wanted, total));
-  const uint64_t per_range = std::max<uint64_t>(1, roost::CeilDiv(total, ranges));
+  uint64_t per_range = std::max<uint64_t>(1, roost::CeilDiv(total, ranges));
+  // A sequence spans at most ceil(groups / per_range) + 1 pieces; keep that within what the merge kernel combines.
+  const uint64_t longest = groups.empty() ? 0 : *std::max_element(groups.begin(), groups.end());
+  per_range = std::max<uint64_t>(per_range, roost::CeilDiv(longest, kMaxMergeSplits - 2));
   // First pass: count pieces, merges and slots; second pass (host != NULL): write them.
   std::vector<DecodeWork> items;
   std::vector<int32_t> range_ptr;
@@ -267,7 +284,7 @@ Layout PlanDecode(const RoostPagedAttentionParams& p, uint32_t cus, unsigned cha
   }
   range_ptr.push_back(static_cast<int32_t>(items.size()));
   Layout l = MakeLayout(items.size(), range_ptr.size() - 1, merges.size(), static_cast<uint64_t>(slot), p.q_heads,
-                        p.head_dim, ROOST_ATTENTION_DECODE);
+                        p.kv_heads, p.head_dim, ROOST_ATTENTION_DECODE);
   if (host != nullptr) {
     std::memcpy(host, items.data(), items.size() * sizeof(DecodeWork));
     std::memcpy(host + l.range_offset, range_ptr.data(), range_ptr.size() * sizeof(int32_t));
@@ -297,7 +314,7 @@ Layout PlanPrefill(const RoostPagedAttentionParams& p, unsigned char* host) {
     }
   }
   std::stable_sort(items.begin(), items.end(), [](const Item& a, const Item& b) { return a.cost > b.cost; });
-  Layout l = MakeLayout(items.size(), 0, 0, 0, p.q_heads, p.head_dim, ROOST_ATTENTION_PREFILL);
+  Layout l = MakeLayout(items.size(), 0, 0, 0, p.q_heads, p.kv_heads, p.head_dim, ROOST_ATTENTION_PREFILL);
   if (host != nullptr) {
     auto* w = reinterpret_cast<PrefillWork*>(host);
     for (size_t i = 0; i < items.size(); ++i) w[i] = items[i].w;
@@ -389,6 +406,10 @@ struct Vec<float> {
 };
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 // Partial dot product of a 16-byte K vector with the matching 16 bytes of q (both bf16; q kept as packed pairs).
 __device__ __forceinline__ float Dot16(const uint4& k, const uint32_t* q, float acc) {
@@ -544,6 +565,103 @@ __device__ __forceinline__ void DecodeGroup(DecodeState<T, D>& st, const uint4* 
   }
 }
 
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// bf16 form of one 16-token group. q.k runs on v_mfma_f32_16x16x32_bf16 with the 16 tokens on M and the 4 query heads
+// (padded to 16 with zero columns) on N: K register kc of lane l holds token l % 16, dims 32*kc + 8*(l / 16) .. +8,
+// q register kc the same dims of head l % 16 (zero for l % 16 >= 4), and the result lane l holds the scores of tokens
+// 4*(l / 16) + j, j = 0..3, for head l % 16. No cross-lane reduction is needed for the scores; the per-head maximum is
+// two exchanges and four readlanes, so the running maxima are wave-uniform scalars. The weights go through 256 bytes of
+// LDS into the P.V layout (lane (ri, r): V register i = token kTpi*i + ri, 16-byte slice r), where P.V runs on v_dot2
+// over token pairs with P rounded to bf16 and fp32 accumulation.
+template <int D>
+__device__ __forceinline__ void DecodeGroupMfma(DecodeState<uint16_t, D>& st, const uint4* kr, const uint4* vr,
+                                                uint32_t validmask, const u32x4_t* qb, float* x_row, int r, int ri,
+                                                int lane, float scale_log2) {
+  using C = DecodeCfg<uint16_t, D>;
+  constexpr int kVec = C::kVec, kTpi = C::kTpi, kNi = C::kNi, kChunks = D / 32;
+  f32x4_t acc4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int kc = 0; kc < kChunks; ++kc) {
+    acc4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kr[kc]),
+                                                    __builtin_bit_cast(bf16x8_t, qb[kc]), acc4, 0, 0, 0);
+  }
+  const int col = lane & 15;
+  const int tok0 = (lane >> 4) * 4;
+  float sc[4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const bool ok = col < (int)kGroup && ((validmask >> (tok0 + j)) & 1u);
+    sc[j] = ok ? acc4[j] * scale_log2 : -INFINITY;
+    mx = fmaxf(mx, sc[j]);
+  }
+  mx = fmaxf(mx, ShflXor(mx, 16));
+  mx = fmaxf(mx, ShflXor(mx, 32));
+  float corr[kGroup];
+  bool rescale = false;
+#pragma unroll
+  for (int h = 0; h < (int)kGroup; ++h) {
+    const float hm = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), h));  // lane h holds head h
+    const float mn = fmaxf(st.m[h], hm);
+    corr[h] = mn == -INFINITY ? 1.0f : exp2f(st.m[h] - mn);
+    rescale |= mn != st.m[h];
+    st.m[h] = mn;
+  }
+  const float mine = Pick4(st.m, col & 3);
+  float pf[4];
+  float psum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    pf[j] = sc[j] == -INFINITY ? 0.0f : exp2f(sc[j] - mine);
+    psum += pf[j];
+  }
+  st.l_lane = st.l_lane * Pick4(corr, col & 3) + psum;
+  if (rescale) {
+#pragma unroll
+    for (int h = 0; h < (int)kGroup; ++h)
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) st.acc[h][e] *= corr[h];
+  }
+  // Weights to LDS as [token][head] floats, then each P.V lane packs the bf16 pairs it needs.
+  if (col < (int)kGroup) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x_row[(tok0 + j) * kGroup + col] = pf[j];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  uint32_t pp[kNi / 2][kGroup];
+#pragma unroll
+  for (int a = 0; a < kNi / 2; ++a) {
+    const float4 p0 = *reinterpret_cast<const float4*>(&x_row[(kTpi * (2 * a) + ri) * kGroup]);
+    const float4 p1 = *reinterpret_cast<const float4*>(&x_row[(kTpi * (2 * a + 1) + ri) * kGroup]);
+    pp[a][0] = PackBf16(p0.x, p1.x);
+    pp[a][1] = PackBf16(p0.y, p1.y);
+    pp[a][2] = PackBf16(p0.z, p1.z);
+    pp[a][3] = PackBf16(p0.w, p1.w);
+  }
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int a = 0; a < kNi / 2; ++a) {
+    const uint32_t* v0 = reinterpret_cast<const uint32_t*>(&vr[2 * a]);
+    const uint32_t* v1 = reinterpret_cast<const uint32_t*>(&vr[2 * a + 1]);
+#pragma unroll
+    for (int w = 0; w < kVec / 2; ++w) {
+      const uint32_t lo = __builtin_amdgcn_perm(v1[w], v0[w], 0x05040100u);
+      const uint32_t hi = __builtin_amdgcn_perm(v1[w], v0[w], 0x07060302u);
+#pragma unroll
+      for (int h = 0; h < (int)kGroup; ++h) {
+        const bf16x2_t ph = __builtin_bit_cast(bf16x2_t, pp[a][h]);
+        st.acc[h][2 * w] = __builtin_amdgcn_fdot2_f32_bf16(ph, __builtin_bit_cast(bf16x2_t, lo), st.acc[h][2 * w], false);
+        st.acc[h][2 * w + 1] =
+            __builtin_amdgcn_fdot2_f32_bf16(ph, __builtin_bit_cast(bf16x2_t, hi), st.acc[h][2 * w + 1], false);
+      }
+    }
+  }
+  (void)r;
+}
+
 // Split-K paged decode. kFastPage: page_size is a multiple of 16, so a 16-token group (16-aligned within its
 // sequence) lies in one page and its page id is one wave-uniform scalar load; otherwise each lane looks its own
 // token's page up. Loads are branch-free (an absent key reads a valid address and is masked) and the next group's
@@ -551,25 +669,32 @@ __device__ __forceinline__ void DecodeGroup(DecodeState<T, D>& st, const uint4* 
 // processes the pieces of its range in turn; a piece that is not a whole sequence writes fp32 partials that
 // DecodeMergeKernel combines in key order.
 template <typename T, int D, bool kFastPage>
-__global__ void __launch_bounds__(256, 2) DecodeKernel(const T* __restrict__ q, T* __restrict__ out, float* __restrict__ lse,
+__global__ void __launch_bounds__(256, ROOST_DECODE_WGS_PER_CU) DecodeKernel(const T* __restrict__ q, T* __restrict__ out, float* __restrict__ lse,
                                                     KvView kv, const int32_t* __restrict__ kv_indices,
                                                     const DecodeWork* __restrict__ work,
                                                     const int32_t* __restrict__ range_ptr,
+
                                                     float* __restrict__ part_o, float* __restrict__ part_ml,
-                                                    uint32_t q_heads, float scale_log2) {
+                                                    uint32_t q_heads, uint32_t heads_per_wg, float scale_log2) {
   using C = DecodeCfg<T, D>;
   constexpr int kVec = C::kVec, kLpr = C::kLpr, kTpi = C::kTpi, kNi = C::kNi;
+  constexpr bool kMfma = sizeof(T) == 2;  // bf16: q.k on MFMA; f32: the VALU reduce-scatter path
   __shared__ float x_lds[4][64];
   __shared__ float m_lds[4][kGroup];
   __shared__ float l_lds[4][kGroup];
   __shared__ float o_lds[4][kGroup][D];
 
   // Both KV heads of a range are adjacent in launch order, so the two halves of each NHD page row are read together.
-  const uint32_t range = blockIdx.x / kv.kv_heads;
-  const uint32_t kvh = blockIdx.x % kv.kv_heads;
+  // A workgroup serves heads_per_wg (1, 2 or 4) KV heads of one range, 4 / heads_per_wg wavefronts per head, so the
+  // KV heads of each page row (adjacent in an NHD pool) are read by one CU at the same time.
+  const uint32_t hblocks = kv.kv_heads / heads_per_wg;
+  const uint32_t range = blockIdx.x / hblocks;
   const int lane = threadIdx.x & 63;
   // The wavefront index is uniform within a wavefront; saying so lets the group's page id be a scalar load.
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave_id = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t kvh = (blockIdx.x % hblocks) * heads_per_wg + wave_id % heads_per_wg;
+  const int wave = wave_id / static_cast<int>(heads_per_wg);           // index among this head's wavefronts
+  const int waves_per_head = 4 / static_cast<int>(heads_per_wg);
   const int r = lane % kLpr;   // which 16-byte slice of a row
   const int ri = lane / kLpr;  // which row of a wave-wide load
   const int kperm = r / static_cast<int>(kGroup);  // this lane's token-slot permutation for K
@@ -585,8 +710,17 @@ __global__ void __launch_bounds__(256, 2) DecodeKernel(const T* __restrict__ q, 
   const uint32_t t_end = min(kv_len, static_cast<uint32_t>(wk.token_end));
 
   using QW = typename std::conditional<sizeof(T) == 2, uint32_t, float>::type;
-  QW qr[kGroup][C::kQWords];
-  {
+  QW qr[kGroup][C::kQWords];   // VALU path (f32)
+  u32x4_t qb[kMfma ? D / 32 : 1];  // MFMA path (bf16): B operand of q.k
+  if constexpr (kMfma) {
+    const int col = lane & 15;
+    const T* qrow = q + (static_cast<uint64_t>(wk.seq) * q_heads + kvh * kGroup + (col & 3)) * D + (lane >> 4) * 8;
+#pragma unroll
+    for (int kc = 0; kc < D / 32; ++kc) {
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(qrow + kc * 32);
+      qb[kc] = col < (int)kGroup ? v : u32x4_t{0, 0, 0, 0};
+    }
+  } else {
     const T* qrow = q + (static_cast<uint64_t>(wk.seq) * q_heads + kvh * kGroup) * D + r * kVec;
 #pragma unroll
     for (int h = 0; h < (int)kGroup; ++h) {
@@ -608,15 +742,16 @@ __global__ void __launch_bounds__(256, 2) DecodeKernel(const T* __restrict__ q, 
 
   // Byte stride between the rows of consecutive tokens of one KV head inside a page.
   const uint32_t tok_bytes = (kv.hnd ? D : kv.kv_heads * D) * static_cast<uint32_t>(sizeof(T));
-  // Group gi (0-based, 16 tokens) of this wavefront: key g = t_begin + 16 * (wave + 4 * gi).
+  // Group gi (0-based, 16 tokens) of this wavefront: key g = t_begin + 16 * (wave + waves_per_head * gi).
   const uint32_t ngroups = (t_end > t_begin) ? (t_end - t_begin + 15) / 16 : 0;
-  const uint32_t nw = ngroups > static_cast<uint32_t>(wave) ? (ngroups - wave + 3) / 4 : 0;
+  const uint32_t nw = ngroups > static_cast<uint32_t>(wave)
+                          ? (ngroups - wave + waves_per_head - 1) / waves_per_head : 0;
   // Every load is unconditional: a group index past the end is clamped to the wave's last group and its keys are
   // masked, so the number of loads in flight is the same on every path and the compiler can wait for exactly the
   // current group's data (vmcnt) while the next group's loads stay in flight.
   auto load = [&](uint32_t gi, uint4* kr, uint4* vr, uint32_t& valid) {
     valid = 0;
-    const uint32_t g0 = t_begin + 16u * (wave + 4u * min(gi, nw - 1));
+    const uint32_t g0 = t_begin + 16u * (wave + waves_per_head * min(gi, nw - 1));
     const bool live = gi < nw;
     if constexpr (kFastPage) {
       const uint32_t pi = g0 / kv.page_size;
@@ -630,38 +765,67 @@ __global__ void __launch_bounds__(256, 2) DecodeKernel(const T* __restrict__ q, 
       const char* vg = reinterpret_cast<const char*>(vbase + row0 * D);
 #pragma unroll
       for (int i = 0; i < kNi; ++i) {
-        const uint32_t tv = i * kTpi + ri;            // V register i: slot i
-        const uint32_t tk = (i ^ kperm) * kTpi + ri;  // K register i: slot i ^ kperm
+        const uint32_t tv = i * kTpi + ri;  // V register i: slot i
         const bool okv = live && page_ok && g0 + tv < t_end;
-        const bool okk = page_ok && g0 + tk < t_end;
-        kr[i] = *reinterpret_cast<const uint4*>(kg + ((okk ? tk : 0) * tok_bytes + r * 16));
         vr[i] = *reinterpret_cast<const uint4*>(vg + ((okv ? tv : 0) * tok_bytes + r * 16));
-        valid |= static_cast<uint32_t>(okv) << i;
+        if constexpr (kMfma) {
+          const uint32_t tk = lane & 15;  // K register i: dims 32 i + 8 (lane / 16) of token lane % 16
+          const bool okk = page_ok && g0 + tk < t_end;
+          kr[i] = *reinterpret_cast<const uint4*>(kg + ((okk ? tk : 0) * tok_bytes + i * 64 + (lane >> 4) * 16));
+        } else {
+          const uint32_t tk = (i ^ kperm) * kTpi + ri;  // K register i: slot i ^ kperm
+          const bool okk = page_ok && g0 + tk < t_end;
+          kr[i] = *reinterpret_cast<const uint4*>(kg + ((okk ? tk : 0) * tok_bytes + r * 16));
+          valid |= static_cast<uint32_t>(okv) << i;
+        }
+      }
+      if constexpr (kMfma) {
+        const uint32_t n = live && page_ok ? min(16u, t_end - g0) : 0u;
+        valid = (1u << n) - 1u;  // bit t: token t of the group is a real key
       }
     } else {
+      bool kok = false;
 #pragma unroll
       for (int i = 0; i < kNi; ++i) {
         bool okk, okv;
-        const uint64_t rowk = KeyRowSafe<D>(kv, p0, static_cast<int32_t>(g0 + (i ^ kperm) * kTpi + ri),
-                                            static_cast<int32_t>(t_end), kvh, &okk);
+        const int32_t tk = kMfma ? static_cast<int32_t>(g0 + (lane & 15))
+                                 : static_cast<int32_t>(g0 + (i ^ kperm) * kTpi + ri);
+        const uint64_t rowk = KeyRowSafe<D>(kv, p0, tk, static_cast<int32_t>(t_end), kvh, &okk);
         const uint64_t rowv = KeyRowSafe<D>(kv, p0, static_cast<int32_t>(g0 + i * kTpi + ri),
                                             static_cast<int32_t>(t_end), kvh, &okv);
-        kr[i] = *reinterpret_cast<const uint4*>(kbase + rowk + r * kVec);
+        kr[i] = *reinterpret_cast<const uint4*>(kMfma ? kbase + rowk + i * 32 + (lane >> 4) * 8 : kbase + rowk + r * kVec);
         vr[i] = *reinterpret_cast<const uint4*>(vbase + rowv + r * kVec);
-        valid |= static_cast<uint32_t>(okv && live) << i;
+        if constexpr (!kMfma) valid |= static_cast<uint32_t>(okv && live) << i;
+        kok = okk;
+      }
+      if constexpr (kMfma) {
+        // Lanes 0..15 hold tokens 0..15 of the group: their K validity is the key mask.
+        valid = static_cast<uint32_t>(__ballot(kok && live)) & 0xFFFFu;
       }
     }
   };
 
   if (nw > 0) {
-    uint4 ka[kNi], va[kNi], kb[kNi], vb[kNi];
-    uint32_t valid_a = 0, valid_b = 0;
-    load(0, ka, va, valid_a);
-    for (uint32_t gi = 0; gi < nw; gi += 2) {
-      load(gi + 1, kb, vb, valid_b);
-      DecodeGroup<T, D, QW>(st, ka, va, valid_a, qr, x_lds[wave], r, ri, lane, scale_log2);
-      load(gi + 2, ka, va, valid_a);
-      if (gi + 1 < nw) DecodeGroup<T, D, QW>(st, kb, vb, valid_b, qr, x_lds[wave], r, ri, lane, scale_log2);
+    // A ring of kDecodeRing register buffers: group gi is computed while groups gi+1 .. gi+kDecodeRing-1 are in
+    // flight (kDecodeRing - 1 groups of 16 loads stay below the 63 outstanding vector loads a wavefront can count).
+    uint4 kbuf[kDecodeRing][kNi], vbuf[kDecodeRing][kNi];
+    uint32_t valid[kDecodeRing];
+#pragma unroll
+    for (int s = 0; s < kDecodeRing - 1; ++s) load(s, kbuf[s], vbuf[s], valid[s]);
+    for (uint32_t gi = 0; gi < nw; gi += kDecodeRing) {
+#pragma unroll
+      for (int s = 0; s < kDecodeRing; ++s) {
+        constexpr int kLast = kDecodeRing - 1;
+        const int nxt = (s + kLast) % kDecodeRing;
+        load(gi + s + kLast, kbuf[nxt], vbuf[nxt], valid[nxt]);
+        if (gi + s < nw) {
+          if constexpr (kMfma) {
+            DecodeGroupMfma<D>(st, kbuf[s], vbuf[s], valid[s], qb, x_lds[wave_id], r, ri, lane, scale_log2);
+          } else {
+            DecodeGroup<T, D, QW>(st, kbuf[s], vbuf[s], valid[s], qr, x_lds[wave_id], r, ri, lane, scale_log2);
+          }
+        }
+      }
     }
   }
 
@@ -672,37 +836,37 @@ __global__ void __launch_bounds__(256, 2) DecodeKernel(const T* __restrict__ q, 
     for (int h = 0; h < (int)kGroup; ++h)
 #pragma unroll
       for (int e = 0; e < kVec; ++e) st.acc[h][e] += ShflXor(st.acc[h][e], mk);
+  // Per-lane denominators: VALU path, lanes with r % 4 == h hold head h; MFMA path, lanes with lane % 16 == h.
   float lsum = st.l_lane;
 #pragma unroll
-  for (int mk = 4; mk < 64; mk <<= 1) lsum += ShflXor(lsum, mk);
+  for (int mk = kMfma ? 16 : 4; mk < 64; mk <<= 1) lsum += ShflXor(lsum, mk);
   if (lane < (int)kGroup) {
-    m_lds[wave][lane] = Pick4(st.m, lane);
-    l_lds[wave][lane] = lsum;  // lane h holds the total of head h (lanes with r % 4 == h)
+    m_lds[wave_id][lane] = Pick4(st.m, lane);
+    l_lds[wave_id][lane] = lsum;  // lane h holds the total of head h
   }
   if (ri == 0) {
 #pragma unroll
     for (int h = 0; h < (int)kGroup; ++h)
 #pragma unroll
-      for (int e = 0; e < kVec; ++e) o_lds[wave][h][r * kVec + e] = st.acc[h][e];
+      for (int e = 0; e < kVec; ++e) o_lds[wave_id][h][r * kVec + e] = st.acc[h][e];
   }
   __syncthreads();
 
-  // Workgroup: merge the 4 wavefronts, then write the final row or this chunk's partial.
+  // Workgroup: merge the wavefronts of each KV head, then write the final row or this piece's partial.
   const int split = wk.slot;
-  for (int idx = threadIdx.x; idx < (int)(kGroup * D); idx += 256) {
-    const int h = idx / D;
-    const int d = idx - h * D;
+  for (int idx = threadIdx.x; idx < (int)(heads_per_wg * kGroup * D); idx += 256) {
+    const int hk = idx / (kGroup * D);  // local KV head: wavefronts hk, hk + heads_per_wg, ...
+    const int h = (idx / D) % kGroup;
+    const int d = idx % D;
     float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, m_lds[w][h]);
+    for (int w = hk; w < 4; w += heads_per_wg) M = fmaxf(M, m_lds[w][h]);
     float o = 0.0f, L = 0.0f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
+    for (int w = hk; w < 4; w += heads_per_wg) {
       const float f = m_lds[w][h] == -INFINITY ? 0.0f : exp2f(m_lds[w][h] - M);
       o += o_lds[w][h][d] * f;
       L += l_lds[w][h] * f;
     }
-    const uint32_t qh = kvh * kGroup + h;
+    const uint32_t qh = ((blockIdx.x % hblocks) * heads_per_wg + hk) * kGroup + h;
     if (split < 0) {
       const uint64_t row = static_cast<uint64_t>(wk.seq) * q_heads + qh;
       out[row * D + d] = Vec<T>::Narrow(L > 0.0f ? o / L : 0.0f);
@@ -720,68 +884,56 @@ __global__ void __launch_bounds__(256, 2) DecodeKernel(const T* __restrict__ q, 
   }
 }
 
-// Combines the pieces of each split sequence in key order: one workgroup per (sequence, KV head); the per-piece
-// rescale factors are computed once into LDS, then every output element sums its pieces with independent loads.
+// Combines the pieces of each split sequence in key order: one workgroup per (sequence, query head), D threads, one
+// output element each. Wavefront 0 computes the per-piece rescale factors into LDS (lanes over pieces), then every
+// thread sums its element over the pieces with independent loads.
 template <typename T, int D>
-__global__ void __launch_bounds__(256) DecodeMergeKernel(T* __restrict__ out, float* __restrict__ lse,
-                                                         const DecodeMerge* __restrict__ merges,
-                                                         const float* __restrict__ part_o,
-                                                         const float* __restrict__ part_ml, uint32_t q_heads,
-                                                         uint32_t kv_heads) {
-  __shared__ float f_lds[kGroup][kMaxMergeSplits];
-  __shared__ float m_lds[kGroup][4];
-  __shared__ float inv_lds[kGroup];
-  __shared__ float lse_lds[kGroup];
-  const DecodeMerge mg = merges[blockIdx.x / kv_heads];
-  const uint32_t kvh = blockIdx.x % kv_heads;
+__global__ void __launch_bounds__(D) DecodeMergeKernel(T* __restrict__ out, float* __restrict__ lse,
+                                                       const DecodeMerge* __restrict__ merges,
+                                                       const float* __restrict__ part_o,
+                                                       const float* __restrict__ part_ml, uint32_t q_heads) {
+  __shared__ float f_lds[kMaxMergeSplits];
+  __shared__ float inv_lds;
+  const DecodeMerge mg = merges[blockIdx.x / q_heads];
+  const uint32_t qh = blockIdx.x % q_heads;
   const int n = min(mg.count, static_cast<int32_t>(kMaxMergeSplits));
-  const int lane = threadIdx.x & 63;
-  const int h = threadIdx.x >> 6;  // one wavefront per query head of the group
-  const uint32_t qh = kvh * kGroup + h;
-  // Max over pieces (wavefront reduction), then factors and the denominator.
-  float M = -INFINITY;
-  for (int c = lane; c < n; c += 64) M = fmaxf(M, part_ml[(static_cast<uint64_t>(mg.first + c) * q_heads + qh) * 2]);
-  for (int mk = 32; mk >= 1; mk >>= 1) M = fmaxf(M, __shfl_xor(M, mk, 64));
-  float L = 0.0f;
-  for (int c = lane; c < n; c += 64) {
-    const uint64_t prow = static_cast<uint64_t>(mg.first + c) * q_heads + qh;
-    const float mc = part_ml[prow * 2];
-    const float f = mc == -INFINITY ? 0.0f : exp2f(mc - M);
-    f_lds[h][c] = f;
-    L += part_ml[prow * 2 + 1] * f;
-  }
-  for (int mk = 32; mk >= 1; mk >>= 1) L += __shfl_xor(L, mk, 64);
-  if (lane == 0) {
-    inv_lds[h] = L > 0.0f ? 1.0f / L : 0.0f;
-    lse_lds[h] = L > 0.0f ? M + log2f(L) : -INFINITY;
-    m_lds[h][0] = M;
+  const uint64_t base = static_cast<uint64_t>(mg.first) * q_heads + qh;  // partial row of piece c: base + c * q_heads
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    float M = -INFINITY;
+    for (int c = lane; c < n; c += 64) M = fmaxf(M, part_ml[(base + static_cast<uint64_t>(c) * q_heads) * 2]);
+    for (int mk = 32; mk >= 1; mk >>= 1) M = fmaxf(M, __shfl_xor(M, mk, 64));
+    float L = 0.0f;
+    for (int c = lane; c < n; c += 64) {
+      const uint64_t prow = base + static_cast<uint64_t>(c) * q_heads;
+      const float mc = part_ml[prow * 2];
+      const float f = mc == -INFINITY ? 0.0f : exp2f(mc - M);
+      f_lds[c] = f;
+      L += part_ml[prow * 2 + 1] * f;
+    }
+    for (int mk = 32; mk >= 1; mk >>= 1) L += __shfl_xor(L, mk, 64);
+    if (lane == 0) {
+      inv_lds = L > 0.0f ? 1.0f / L : 0.0f;
+      if (lse != nullptr) lse[static_cast<uint64_t>(mg.seq) * q_heads + qh] = L > 0.0f ? M + log2f(L) : -INFINITY;
+    }
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < (int)(kGroup * D); idx += 256) {
-    const int hh = idx / D;
-    const int d = idx - hh * D;
-    const uint32_t qq = kvh * kGroup + hh;
-    const float* po = part_o + (static_cast<uint64_t>(mg.first) * q_heads + qq) * D + d;
-    const uint64_t step = static_cast<uint64_t>(q_heads) * D;
-    float o0 = 0.0f, o1 = 0.0f;
-    int c = 0;
-    for (; c + 1 < n; c += 2) {
-      o0 = fmaf(po[c * step], f_lds[hh][c], o0);
-      o1 = fmaf(po[(c + 1) * step], f_lds[hh][c + 1], o1);
-    }
-    if (c < n) o0 = fmaf(po[c * step], f_lds[hh][c], o0);
-    const uint64_t row = static_cast<uint64_t>(mg.seq) * q_heads + qq;
-    out[row * D + d] = Vec<T>::Narrow((o0 + o1) * inv_lds[hh]);
-    if (lse != nullptr && d == 0) lse[row] = lse_lds[hh];
+  const int d = threadIdx.x;
+  const float* po = part_o + base * D + d;
+  const uint64_t step = static_cast<uint64_t>(q_heads) * D;
+  float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
+  int c = 0;
+  for (; c + 3 < n; c += 4) {
+    o0 = fmaf(po[(c + 0) * step], f_lds[c + 0], o0);
+    o1 = fmaf(po[(c + 1) * step], f_lds[c + 1], o1);
+    o2 = fmaf(po[(c + 2) * step], f_lds[c + 2], o2);
+    o3 = fmaf(po[(c + 3) * step], f_lds[c + 3], o3);
   }
+  for (; c < n; ++c) o0 = fmaf(po[c * step], f_lds[c], o0);
+  out[(static_cast<uint64_t>(mg.seq) * q_heads + qh) * D + d] = Vec<T>::Narrow(((o0 + o1) + (o2 + o3)) * inv_lds);
 }
 
 // ---- Prefill kernel (bf16, head_dim 256, MFMA) -----------------------------------------------------------------------
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kPD = 256;                 // head_dim
 constexpr int kKStride = kPD + 8;        // K tile row stride in LDS (elements): 528 bytes
@@ -1000,18 +1152,19 @@ RoostStatus LaunchDecode(const RoostPagedAttentionParams& p, const PlanRecord& r
   auto* part_ml = part_o + rec.splits * p.q_heads * D;
   auto* out = static_cast<T*>(p.output.address);
   auto* lse = static_cast<float*>(p.lse.address);
-  const dim3 grid(static_cast<uint32_t>(rec.ranges * p.kv_heads));
+  const uint32_t hpw = HeadsPerWorkgroup(p.kv_heads);
+  const dim3 grid(static_cast<uint32_t>(rec.ranges * (p.kv_heads / hpw)));
   if (p.page_size % 16 == 0) {
     hipLaunchKernelGGL((DecodeKernel<T, D, true>), grid, dim3(256), 0, stream, static_cast<const T*>(p.q.address), out,
-                       lse, kv, kv.kv_indices, items, range_ptr, part_o, part_ml, p.q_heads, scale_log2);
+                       lse, kv, kv.kv_indices, items, range_ptr, part_o, part_ml, p.q_heads, hpw, scale_log2);
   } else {
     hipLaunchKernelGGL((DecodeKernel<T, D, false>), grid, dim3(256), 0, stream, static_cast<const T*>(p.q.address), out,
-                       lse, kv, kv.kv_indices, items, range_ptr, part_o, part_ml, p.q_heads, scale_log2);
+                       lse, kv, kv.kv_indices, items, range_ptr, part_o, part_ml, p.q_heads, hpw, scale_log2);
   }
   ROOST_TRY(roost::FromHip(hipGetLastError(), "PagedAttention decode launch"));
   if (rec.merges == 0) return ROOST_STATUS_OK;
-  hipLaunchKernelGGL((DecodeMergeKernel<T, D>), dim3(static_cast<uint32_t>(rec.merges * p.kv_heads)), dim3(256), 0,
-                     stream, out, lse, merges, part_o, part_ml, p.q_heads, p.kv_heads);
+  hipLaunchKernelGGL((DecodeMergeKernel<T, D>), dim3(static_cast<uint32_t>(rec.merges * p.q_heads)), dim3(D), 0,
+                     stream, out, lse, merges, part_o, part_ml, p.q_heads);
   return roost::FromHip(hipGetLastError(), "PagedAttention merge launch");
 }
 
@@ -1073,6 +1226,7 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_plan(RoostContext* ctx, c
     rec.merges = l.merges;
     rec.range_offset = l.range_offset;
     rec.merge_offset = l.merge_offset;
+    rec.counter_offset = l.counter_offset;
     rec.splits = l.splits;
     rec.int_bytes = l.int_bytes;
     rec.float_offset = l.float_offset;
