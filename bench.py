@@ -198,6 +198,15 @@ def cpu_baseline(b: Paged, sample_seqs: int):
                       f"sequences ({int(b.kv_lens[:n].sum())} context tokens) in {secs:.2f} s"}
 
 
+def measured_traffic():
+    """HBM bytes per decode run() as measured by rocprofv3 FETCH_SIZE / WRITE_SIZE passes, scaled by a 1 GiB copy
+    (profiles/decode_config2_trace.md gives the commands); None when no measurement is committed."""
+    f = ROOT / "profiles" / "decode_config2_traffic.json"
+    if not f.exists():
+        return None
+    return int(json.loads(f.read_text())["traffic_bytes_per_run"])
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -261,7 +270,7 @@ def main():
                    "batch": 64, "ctx": "U(512, 8192)", "context_tokens": int(b.kv_lens.sum()), "q_heads": 8,
                    "kv_heads": 2, "head_dim": 256, "page_size": 16, "pool_pages": b.pool},
         "roofline": {"bound": "hbm", "achieved": round(dec_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "algorithmic_bytes": dec_bytes, "kernel": "DecodeKernel + DecodeMergeKernel (one run())"},
         "plan_ms": {"decode": round(dec_plan_ms, 3), "prefill": round(pre_plan_ms, 3)},
         "prefill": {"workload": "BASELINE config 3: 8 seqs, chunk U(256, 2048) on prefix U(0, 6144), causal",

@@ -61,6 +61,11 @@ def build(verbose: bool = True) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, LIB_PATH)
+    # The name Roost's loader derives for arch id 950 (libroost_kernels_sm<N>.so), pointing at the same file.
+    alias = HERE / "libroost_kernels_sm950.so"
+    if alias.is_symlink() or alias.exists():
+        alias.unlink()
+    alias.symlink_to(LIB_NAME)
     if verbose:
         print(f"built {LIB_PATH}")
     return LIB_PATH
