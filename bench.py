@@ -156,7 +156,9 @@ def bench_gdn(torch, roost_amd, session, steps, warmup):
     ms = time_runs(torch, session, entry, p, ws, max(steps // 4, 3), 1)
     T, B = 4 * 4096, 4
     bytes_ = (3 * T * H * D + T * H * D) * 2 + T * H * 6 + 2 * B * H * D * D * 4
-    flops = (T // 64) * H * (2 * 64 * 64 * (3 * D + 2 * D) + 6 * 64 * D * D)
+    # Algorithmic flops of the WY form per chunk of 64 and head: k.k^T, q.k^T, T.Y, P.V (2 C^2 D each) and
+    # k.S0, q.S0, k^T.V (2 C D^2 each); the bf16 hi/lo operand splits are not counted.
+    flops = (T // 64) * H * (2 * 64 * 64 * 4 * D + 6 * 64 * D * D)
     res["gdn_chunk"] = {"config": "4 x 4096 tokens, 16 heads x 128, chunk 64", "ms": ms,
                         "hbm_gbs": bytes_ / ms / 1e6, "hbm_frac": bytes_ / ms / 1e6 / HBM_PEAK_GBS,
                         "tflops": flops / ms / 1e9, "mfma_frac": flops / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS}

@@ -284,6 +284,9 @@ def paged_attention_params(q, output, k_cache, v_cache, q_indptr, kv_indptr, kv_
     p.q_heads, p.kv_heads, p.head_dim = q_heads, kv_heads, head_dim
     p.page_size, p.kv_layout = page_size, kv_layout
     p.sm_scale, p.logits_soft_cap, p.window_left, p.causal = sm_scale, soft_cap, window_left, int(causal)
+    # The struct holds raw addresses: keep every buffer it points at alive for as long as the struct is.
+    p._keep = (q, output, lse, k_cache, v_cache, q_indptr, kv_indptr, kv_indices, kv_last_page_len, q_indptr_host,
+               kv_indptr_host, kv_last_page_len_host)
     return p
 
 
@@ -299,6 +302,7 @@ def cache_write_params(k, v, k_cache, v_cache, slot_mapping, *, kv_heads, head_d
     p.tokens = k.shape[0]
     p.kv_heads, p.head_dim, p.page_size, p.kv_layout = kv_heads, head_dim, page_size, kv_layout
     p.k_scale = p.v_scale = 1.0
+    p._keep = (k, v, k_cache, v_cache, slot_mapping)
     return p
 
 
@@ -323,6 +327,7 @@ def gated_delta_rule_params(q, k, v, g, beta, output, state, state_slots, cu_seq
     p.k_heads, p.v_heads, p.k_dim, p.v_dim = k_heads, v_heads, k_dim, v_dim
     p.q_stride, p.k_stride, p.v_stride = q_stride, k_stride, v_stride
     p.use_initial_state, p.l2_norm_qk, p.scale = int(use_initial_state), int(l2_norm_qk), scale
+    p._keep = (q, k, v, g, beta, output, state, state_slots, cu_seqlens, cu_seqlens_host)
     return p
 
 

@@ -15,6 +15,7 @@
 // 4*(t/4)..+3 over 32 key rows 32*(t%4)..+31 of S in registers (128 floats), so the column sums S^T k and S^T q need
 // only a reduction over the 4 lanes of a quad, and consecutive lanes read consecutive 16-byte pieces of a state row.
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 
@@ -258,6 +259,517 @@ RoostStatus LaunchRecurrent(const RoostGatedDeltaRuleParams& p, hipStream_t stre
   return roost::FromHip(hipGetLastError(), "GatedDeltaRule recurrent launch");
 }
 
+// ---- Chunk variant: WY form on MFMA ---------------------------------------------------------------------------------
+//
+// A sequence is cut into chunks of 64 tokens from its first token (the last one may be shorter). Within a chunk with
+// start state S0, cumulative log-decay G_t = g_1 + .. + g_t, normalised k^_t = k_t * rk_t and q^_t = q_t * rq_t, the
+// token recurrence above is exactly
+//   A_tj = beta_t e^(G_t - G_j) k^_t . k^_j  (j < t),   T = (I + A)^-1,
+//   Y_t  = beta_t (v_t - e^G_t S0^T k^_t),              V = T Y              (the delta of every token),
+//   o_t  = e^G_t S0^T q^_t + sum_{j <= t} e^(G_t - G_j) (q^_t . k^_j) V_j,
+//   S    = e^G_n S0 + sum_j e^(G_n - G_j) k^_j V_j^T.
+// The prep kernel (one workgroup per chunk and head, all chunks in parallel) computes k.k and q.k on MFMA from the raw
+// bf16 rows (exact products, fp32 sums; the norms are applied afterwards in fp32), T by blocked forward substitution in
+// fp32, and stores T, P_tj = e^(G_t - G_j) q^_t . k^_j and the per-token factors in a per-(chunk, head) record. The scan
+// kernel walks the chunks of one (sequence, head, 32-column value block) in order with S in registers. Every product that
+// feeds the state runs with its fp32 operand split into bf16 hi + lo parts (raw k and q are exact in bf16 already):
+// K.S0 as 2 MFMAs, T.Y as 3, k^T.V as 2, which keeps the state within about 1e-5 of the double-precision recurrence
+// where single bf16 operands drift by a few 1e-3. The output terms, rounded to bf16 at the end, use single bf16 operands.
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kTilePitch = 136;  // bf16 per LDS row of a [64 tokens][128 dims] q/k tile (272 B: 16-byte aligned)
+constexpr int kTokPitch = 72;    // bf16 per LDS row of a [dim or column][64 tokens] tile (144 B)
+constexpr int kVBlock = 32;      // value columns per scan workgroup
+constexpr uint32_t kVBlocks = kDim / kVBlock;
+
+// Per-(chunk, head) record written by the prep kernel. T and P are stored as MFMA A operands of
+// v_mfma_f32_16x16x32_bf16: block (w, s) covers rows 16w..16w+15 and columns 32s..32s+31, lane l holding row
+// 16w + l % 16, columns 32s + 8 (l / 16) .. +7 as 16 bytes. Only the blocks with s <= w / 2 are on or below the
+// diagonal and are written.
+constexpr uint32_t kRecT = 0;          // [w 4][s 2][hi, lo][lane 64] x 16 B
+constexpr uint32_t kRecP = 16384;      // [w 4][s 2][lane 64] x 16 B
+constexpr uint32_t kRecScal = 24576;   // float [5][64]: e^G rk, beta, rq e^G, e^(Gn - G) rk, e^Gn (at [4][0])
+constexpr uint32_t kRecBytes = 25856;  // a multiple of 256
+
+struct ChunkArgs {
+  GdnArgs a;
+  const int4* chunks;  // [chunks] (sequence, first token, tokens, 0)
+  const int2* seqs;    // [batch] (first chunk, chunk count)
+  uint8_t* recs;       // [chunks][heads] records
+  uint32_t chains;     // batch * heads
+};
+
+__device__ __forceinline__ f32x4_t Mfma(uint4 a, uint4 b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                 0, 0, 0);
+}
+
+// Round-to-nearest-even pack of two floats (v_cvt_pk_bf16_f32); used for operands only, never for stored outputs.
+__device__ __forceinline__ uint32_t PackRne(float lo, float hi) {
+  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// x = hi + lo + O(2^-16 |x|): hi is x truncated to bf16, lo the remainder rounded to bf16. Two floats per word.
+__device__ __forceinline__ void Split2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+  const uint32_t u0 = __float_as_uint(x0) & 0xFFFF0000u;
+  const uint32_t u1 = __float_as_uint(x1) & 0xFFFF0000u;
+  hi = (u0 >> 16) | u1;
+  lo = PackRne(x0 - __uint_as_float(u0), x1 - __uint_as_float(u1));
+}
+
+template <bool kVec>
+__device__ __forceinline__ uint4 Load8(const uint16_t* p) {
+  if constexpr (kVec) {
+    return *reinterpret_cast<const uint4*>(p);
+  } else {
+    uint4 r;
+    r.x = p[0] | (static_cast<uint32_t>(p[1]) << 16);
+    r.y = p[2] | (static_cast<uint32_t>(p[3]) << 16);
+    r.z = p[4] | (static_cast<uint32_t>(p[5]) << 16);
+    r.w = p[6] | (static_cast<uint32_t>(p[7]) << 16);
+    return r;
+  }
+}
+
+__device__ __forceinline__ float SumSq8(uint4 v) {
+  float s = 0.0f;
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float a = Bf16LoToF32(w[i]), b = Bf16HiToF32(w[i]);
+    s = fmaf(a, a, s);
+    s = fmaf(b, b, s);
+  }
+  return s;
+}
+
+// Lower blocks (w, s), s <= w / 2, of a 64 x 64 matrix in 16 x 32 MFMA-operand blocks: item b = 0..5.
+__device__ __forceinline__ void LowerBlock(int b, int& w, int& s) {
+  w = b < 2 ? b : 2 + ((b - 2) >> 1);
+  s = b < 2 ? 0 : ((b - 2) & 1);
+}
+
+template <bool kVec>
+__global__ void __launch_bounds__(256, 2) ChunkPrepKernel(ChunkArgs ca) {
+  const GdnArgs& a = ca.a;
+  const int4 ch = ca.chunks[blockIdx.x];
+  const uint32_t h = blockIdx.y;
+  const int t0 = ch.y, n = ch.z;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, kq = lane >> 4;
+  uint8_t* rec = ca.recs + (static_cast<uint64_t>(blockIdx.x) * kHeads + h) * kRecBytes;
+
+  // region0 holds the raw q (tile 0) and k (tile 1) rows, then P and the substitution's partial products.
+  __shared__ __align__(16) uint8_t region0[2 * 64 * kTilePitch * 2];
+  __shared__ float a_lds[64][65];
+  __shared__ float t_lds[64][65];
+  __shared__ float g_lds[64], rk_lds[64], rq_lds[64], b_lds[64];
+  auto qk = reinterpret_cast<uint16_t(*)[64][kTilePitch]>(region0);
+  auto p_lds = reinterpret_cast<float(*)[65]>(region0);
+  auto tmp = reinterpret_cast<float(*)[65]>(region0 + 64 * 65 * 4);
+
+  {  // Raw rows into LDS (zero past the chunk's end) and their sums of squares.
+    const int row = tid >> 2, part = tid & 3;
+    const bool ok = row < n;
+    const uint64_t tok = static_cast<uint64_t>(t0 + (ok ? row : n - 1));
+    const uint16_t* kp = a.k + tok * a.k_stride + h * kDim + part * 32;
+    const uint16_t* qp = a.q + tok * a.q_stride + h * kDim + part * 32;
+    float kk = 0.0f, qq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint4 kv = Load8<kVec>(kp + 8 * i), qv = Load8<kVec>(qp + 8 * i);
+      if (!ok) kv = qv = make_uint4(0, 0, 0, 0);
+      kk += SumSq8(kv);
+      qq += SumSq8(qv);
+      *reinterpret_cast<uint4*>(&qk[1][row][part * 32 + 8 * i]) = kv;
+      *reinterpret_cast<uint4*>(&qk[0][row][part * 32 + 8 * i]) = qv;
+    }
+    kk = QuadSum(kk);
+    qq = QuadSum(qq);
+    if (part == 0) {
+      rk_lds[row] = 1.0f / sqrtf(kk + 1e-6f);
+      rq_lds[row] = a.scale / sqrtf(qq + 1e-6f);
+    }
+  }
+  if (w == 0) {  // cumulative log-decay (zero increments past the end) and beta
+    const uint64_t gi = static_cast<uint64_t>(t0 + lane) * kHeads + h;
+    float gv = lane < n ? a.g[gi] : 0.0f;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const float y = __shfl_up(gv, d, 64);
+      if (lane >= d) gv += y;
+    }
+    g_lds[lane] = gv;
+    b_lds[lane] = lane < n ? Bf16ToF32(a.beta[gi]) : 0.0f;
+  }
+  __syncthreads();
+
+  // k.k^T and q.k^T for row tile w, column tiles c <= w.
+  f32x4_t kk4[4], qk4[4];
+  {
+    uint4 ak[4], aq[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      ak[s] = *reinterpret_cast<const uint4*>(&qk[1][16 * w + r16][32 * s + 8 * kq]);
+      aq[s] = *reinterpret_cast<const uint4*>(&qk[0][16 * w + r16][32 * s + 8 * kq]);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      kk4[c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      qk4[c] = kk4[c];
+      if (c <= w) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const uint4 b = *reinterpret_cast<const uint4*>(&qk[1][16 * c + r16][32 * s + 8 * kq]);
+          kk4[c] = Mfma(ak[s], b, kk4[c]);
+          qk4[c] = Mfma(aq[s], b, qk4[c]);
+        }
+      }
+    }
+  }
+  __syncthreads();  // the q/k tiles are dead: region0 becomes P and the partial products
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 16 * w + 4 * kq + i, j = 16 * c + r16;
+      float av = 0.0f, pv = 0.0f;
+      if (j <= r) {
+        const float d = expf(g_lds[r] - g_lds[j]);
+        pv = qk4[c][i] * rq_lds[r] * rk_lds[j] * d;
+        if (j < r) av = b_lds[r] * d * kk4[c][i] * rk_lds[r] * rk_lds[j];
+      }
+      a_lds[r][j] = av;
+      p_lds[r][j] = pv;
+      if (c > w) t_lds[r][j] = 0.0f;
+    }
+  }
+  __syncthreads();
+
+  // T = (I + A)^-1. Diagonal 16 x 16 blocks by forward substitution (wave w, one column per lane), then the blocks
+  // below the diagonal by T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj in order of distance from the diagonal.
+  if (lane < 16) {
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float acc = i == lane ? 1.0f : 0.0f;
+#pragma unroll
+      for (int j = 0; j < i; ++j) acc = fmaf(-a_lds[16 * w + i][16 * w + j], x[j], acc);
+      x[i] = acc;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t_lds[16 * w + i][16 * w + lane] = x[i];
+  }
+  // P blocks out while the substitution proceeds (P is final).
+  for (int item = tid; item < 6 * 64; item += 256) {
+    int bw, bs;
+    LowerBlock(item >> 6, bw, bs);
+    const int l = item & 63;
+    const float* src = &p_lds[16 * bw + (l & 15)][32 * bs + 8 * (l >> 4)];
+    uint4 v;
+    v.x = PackRne(src[0], src[1]);
+    v.y = PackRne(src[2], src[3]);
+    v.z = PackRne(src[4], src[5]);
+    v.w = PackRne(src[6], src[7]);
+    *reinterpret_cast<uint4*>(rec + kRecP + ((bw * 2 + bs) * 64 + l) * 16) = v;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int d = 1; d < 4; ++d) {
+    const int items = (4 - d) * 256;
+    for (int e = tid; e < items; e += 256) {
+      const int j = e >> 8, i = j + d, r = (e >> 4) & 15, cc = e & 15;
+      float acc = 0.0f;
+      for (int k = j; k < i; ++k) {
+#pragma unroll
+        for (int m = 0; m < 16; ++m) acc = fmaf(a_lds[16 * i + r][16 * k + m], t_lds[16 * k + m][16 * j + cc], acc);
+      }
+      tmp[16 * i + r][16 * j + cc] = acc;
+    }
+    __syncthreads();
+    for (int e = tid; e < items; e += 256) {
+      const int j = e >> 8, i = j + d, r = (e >> 4) & 15, cc = e & 15;
+      float acc = 0.0f;
+#pragma unroll
+      for (int m = 0; m < 16; ++m) acc = fmaf(t_lds[16 * i + r][16 * i + m], tmp[16 * i + m][16 * j + cc], acc);
+      t_lds[16 * i + r][16 * j + cc] = -acc;
+    }
+    __syncthreads();
+  }
+  for (int item = tid; item < 6 * 64; item += 256) {
+    int bw, bs;
+    LowerBlock(item >> 6, bw, bs);
+    const int l = item & 63;
+    const float* src = &t_lds[16 * bw + (l & 15)][32 * bs + 8 * (l >> 4)];
+    uint4 hi, lo;
+    Split2(src[0], src[1], hi.x, lo.x);
+    Split2(src[2], src[3], hi.y, lo.y);
+    Split2(src[4], src[5], hi.z, lo.z);
+    Split2(src[6], src[7], hi.w, lo.w);
+    *reinterpret_cast<uint4*>(rec + kRecT + (((bw * 2 + bs) * 2 + 0) * 64 + l) * 16) = hi;
+    *reinterpret_cast<uint4*>(rec + kRecT + (((bw * 2 + bs) * 2 + 1) * 64 + l) * 16) = lo;
+  }
+  if (tid < 64) {
+    float* sc = reinterpret_cast<float*>(rec + kRecScal);
+    const float gt = g_lds[tid], gn = g_lds[63];
+    const float e = expf(gt);
+    sc[tid] = e * rk_lds[tid];
+    sc[64 + tid] = b_lds[tid];
+    sc[128 + tid] = rq_lds[tid] * e;
+    sc[192 + tid] = expf(gn - gt) * rk_lds[tid];
+    if (tid == 0) sc[256] = expf(gn);
+  }
+}
+
+// The registers one wave needs for one chunk: its 16 k and q rows (as MFMA A operands), its v values in the MFMA
+// result layout, its blocks of T and P, and the per-token factors.
+struct ChunkRegs {
+  uint4 kr[4], qr[4];
+  uint4 thi[2], tlo[2], pr[2];
+  float4 xs, beta, os, ws;
+  float vv[2][4];
+  float decay;
+  int t0, n;
+};
+
+template <bool kVec>
+__device__ __forceinline__ void LoadChunk(const ChunkArgs& ca, uint32_t chunk, uint32_t h, uint32_t vb, int w, int lane,
+                                          ChunkRegs& r) {
+  const GdnArgs& a = ca.a;
+  const int4 ch = ca.chunks[chunk];
+  r.t0 = ch.y;
+  r.n = ch.z;
+  const int r16 = lane & 15, kq = lane >> 4;
+  const int row = 16 * w + r16;
+  const bool ok = row < r.n;
+  const uint64_t tok = static_cast<uint64_t>(r.t0 + (ok ? row : r.n - 1));
+  const uint16_t* kp = a.k + tok * a.k_stride + h * kDim + 8 * kq;
+  const uint16_t* qp = a.q + tok * a.q_stride + h * kDim + 8 * kq;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const uint4 kv = Load8<kVec>(kp + 32 * s), qv = Load8<kVec>(qp + 32 * s);
+    r.kr[s] = ok ? kv : make_uint4(0, 0, 0, 0);
+    r.qr[s] = ok ? qv : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int rv = 16 * w + 4 * kq + i;
+    const bool okv = rv < r.n;
+    const uint16_t* vp = a.v + static_cast<uint64_t>(r.t0 + (okv ? rv : r.n - 1)) * a.v_stride + h * kDim +
+                         vb * kVBlock + r16;
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const float x = Bf16ToF32(vp[16 * nt]);
+      r.vv[nt][i] = okv ? x : 0.0f;
+    }
+  }
+  const uint8_t* rec = ca.recs + (static_cast<uint64_t>(chunk) * kHeads + h) * kRecBytes;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {  // blocks above the diagonal are loaded but never used
+    r.thi[s] = *reinterpret_cast<const uint4*>(rec + kRecT + (((w * 2 + s) * 2 + 0) * 64 + lane) * 16);
+    r.tlo[s] = *reinterpret_cast<const uint4*>(rec + kRecT + (((w * 2 + s) * 2 + 1) * 64 + lane) * 16);
+    r.pr[s] = *reinterpret_cast<const uint4*>(rec + kRecP + ((w * 2 + s) * 64 + lane) * 16);
+  }
+  const float* sc = reinterpret_cast<const float*>(rec + kRecScal) + 16 * w + 4 * kq;
+  r.xs = *reinterpret_cast<const float4*>(sc);
+  r.beta = *reinterpret_cast<const float4*>(sc + 64);
+  r.os = *reinterpret_cast<const float4*>(sc + 128);
+  r.ws = *reinterpret_cast<const float4*>(sc + 192);
+  r.decay = reinterpret_cast<const float*>(rec + kRecScal)[256];
+}
+
+__device__ __forceinline__ float F4(const float4& v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// One workgroup per (sequence, head, value block of 32 columns); wave w owns state rows 32w..32w+31 and, for the
+// token-side products, tokens 16w..16w+15 of each chunk. blockIdx -> (chain, block) keeps the four value blocks of a
+// chain on one XCD (workgroups are dealt to the 8 XCDs round-robin), so they share the chain's k, q and records in L2.
+template <bool kVec>
+__global__ void __launch_bounds__(256, 1) ChunkScanKernel(ChunkArgs ca) {
+  const GdnArgs& a = ca.a;
+  const uint32_t x = blockIdx.x;
+  const uint32_t chain = (x & 7) + 8 * (x >> 5);
+  const uint32_t vb = (x >> 3) & 3;
+  if (chain >= ca.chains) return;
+  const uint32_t seq = chain / kHeads, h = chain % kHeads;
+  const int2 sq = ca.seqs[seq];
+  if (sq.y == 0) return;  // an empty sequence leaves its slot untouched
+  const int32_t slot = a.slots[seq];
+  const bool has_slot = slot >= 0 && static_cast<uint64_t>(slot) < a.pool_slots;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, kq = lane >> 4;
+
+  __shared__ __align__(16) uint16_t s_lds[2][kVBlock][kTilePitch];  // S hi, lo as [column][dim]
+  __shared__ __align__(16) uint16_t kt_lds[2][kDim][kTokPitch];     // raw k^T [dim][token], double-buffered
+  __shared__ __align__(16) uint16_t y_lds[2][kVBlock][kTokPitch];   // Y hi, lo as [column][token]
+  __shared__ __align__(16) uint16_t vn_lds[3][kVBlock][kTokPitch];  // V (bf16), V * ws hi, lo as [column][token]
+
+  // st[mt][nt][i] = S[32w + 16mt + 4kq + i][32vb + 16nt + r16]
+  f32x4_t st[2][2];
+  float* sp = has_slot ? a.state + (static_cast<uint64_t>(slot) * kHeads + h) * kDim * kDim : nullptr;
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d = 32 * w + 16 * mt + 4 * kq + i, c = vb * kVBlock + 16 * nt + r16;
+        st[mt][nt][i] = (has_slot && a.use_initial_state) ? sp[d * kDim + c] : 0.0f;
+      }
+    }
+  }
+
+  ChunkRegs cur;
+  LoadChunk<kVec>(ca, sq.x, h, vb, w, lane, cur);
+  for (int c = 0; c < sq.y; ++c) {
+    ChunkRegs nxt;
+    LoadChunk<kVec>(ca, sq.x + min(c + 1, sq.y - 1), h, vb, w, lane, nxt);
+    const int buf = c & 1;
+    // (1) S as bf16 hi/lo B operands; raw k^T for the state update.
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        uint2 hi, lo;
+        Split2(st[mt][nt][0], st[mt][nt][1], hi.x, lo.x);
+        Split2(st[mt][nt][2], st[mt][nt][3], hi.y, lo.y);
+        const int d0 = 32 * w + 16 * mt + 4 * kq, col = 16 * nt + r16;
+        *reinterpret_cast<uint2*>(&s_lds[0][col][d0]) = hi;
+        *reinterpret_cast<uint2*>(&s_lds[1][col][d0]) = lo;
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const uint32_t wd[4] = {cur.kr[s].x, cur.kr[s].y, cur.kr[s].z, cur.kr[s].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        kt_lds[buf][32 * s + 8 * kq + 2 * e][16 * w + r16] = static_cast<uint16_t>(wd[e]);
+        kt_lds[buf][32 * s + 8 * kq + 2 * e + 1][16 * w + r16] = static_cast<uint16_t>(wd[e] >> 16);
+      }
+    }
+    __syncthreads();
+    // (2) X = k S0 (hi + lo) and q S0 (hi) for tokens 16w..16w+15; Y = beta (v - e^G rk X).
+    f32x4_t xs4[2], oq4[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) xs4[nt] = oq4[nt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const uint4 bh = *reinterpret_cast<const uint4*>(&s_lds[0][16 * nt + r16][32 * s + 8 * kq]);
+        const uint4 bl = *reinterpret_cast<const uint4*>(&s_lds[1][16 * nt + r16][32 * s + 8 * kq]);
+        xs4[nt] = Mfma(cur.kr[s], bh, xs4[nt]);
+        xs4[nt] = Mfma(cur.kr[s], bl, xs4[nt]);
+        oq4[nt] = Mfma(cur.qr[s], bh, oq4[nt]);
+      }
+    }
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      float y[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[i] = F4(cur.beta, i) * (cur.vv[nt][i] - F4(cur.xs, i) * xs4[nt][i]);
+      uint2 hi, lo;
+      Split2(y[0], y[1], hi.x, lo.x);
+      Split2(y[2], y[3], hi.y, lo.y);
+      const int col = 16 * nt + r16, t = 16 * w + 4 * kq;
+      *reinterpret_cast<uint2*>(&y_lds[0][col][t]) = hi;
+      *reinterpret_cast<uint2*>(&y_lds[1][col][t]) = lo;
+    }
+    __syncthreads();
+    // (3) V = T Y over the blocks on or below the diagonal (hi.hi + hi.lo + lo.hi).
+    f32x4_t vn4[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      if (s <= (w >> 1)) {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          const uint4 bh = *reinterpret_cast<const uint4*>(&y_lds[0][16 * nt + r16][32 * s + 8 * kq]);
+          const uint4 bl = *reinterpret_cast<const uint4*>(&y_lds[1][16 * nt + r16][32 * s + 8 * kq]);
+          vn4[nt] = Mfma(cur.thi[s], bh, vn4[nt]);
+          vn4[nt] = Mfma(cur.thi[s], bl, vn4[nt]);
+          vn4[nt] = Mfma(cur.tlo[s], bh, vn4[nt]);
+        }
+      }
+    }
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int col = 16 * nt + r16, t = 16 * w + 4 * kq;
+      uint2 v, hi, lo;
+      v.x = PackRne(vn4[nt][0], vn4[nt][1]);
+      v.y = PackRne(vn4[nt][2], vn4[nt][3]);
+      Split2(vn4[nt][0] * cur.ws.x, vn4[nt][1] * cur.ws.y, hi.x, lo.x);
+      Split2(vn4[nt][2] * cur.ws.z, vn4[nt][3] * cur.ws.w, hi.y, lo.y);
+      *reinterpret_cast<uint2*>(&vn_lds[0][col][t]) = v;
+      *reinterpret_cast<uint2*>(&vn_lds[1][col][t]) = hi;
+      *reinterpret_cast<uint2*>(&vn_lds[2][col][t]) = lo;
+    }
+    __syncthreads();
+    // (4) o = rq e^G q S0 + P V for tokens 16w..16w+15.
+    f32x4_t pv4[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      if (s <= (w >> 1)) {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          const uint4 b = *reinterpret_cast<const uint4*>(&vn_lds[0][16 * nt + r16][32 * s + 8 * kq]);
+          pv4[nt] = Mfma(cur.pr[s], b, pv4[nt]);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * w + 4 * kq + i;
+      if (t < cur.n) {
+        uint16_t* op = a.out + (static_cast<uint64_t>(cur.t0 + t) * kHeads + h) * kDim + vb * kVBlock + r16;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) op[16 * nt] = F32ToBf16(fmaf(F4(cur.os, i), oq4[nt][i], pv4[nt][i]));
+      }
+    }
+    // (5) S = e^Gn S0 + k^T (ws V) (hi + lo) for state rows 32w..32w+31.
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      uint4 ak[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        ak[s] = *reinterpret_cast<const uint4*>(&kt_lds[buf][32 * w + 16 * mt + r16][32 * s + 8 * kq]);
+      }
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        f32x4_t acc = st[mt][nt] * cur.decay;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          const uint4 bh = *reinterpret_cast<const uint4*>(&vn_lds[1][16 * nt + r16][32 * s + 8 * kq]);
+          const uint4 bl = *reinterpret_cast<const uint4*>(&vn_lds[2][16 * nt + r16][32 * s + 8 * kq]);
+          acc = Mfma(ak[s], bh, acc);
+          acc = Mfma(ak[s], bl, acc);
+        }
+        st[mt][nt] = acc;
+      }
+    }
+    cur = nxt;
+  }
+  if (has_slot) {
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d = 32 * w + 16 * mt + 4 * kq + i, c = vb * kVBlock + 16 * nt + r16;
+          sp[d * kDim + c] = st[mt][nt][i];
+        }
+      }
+    }
+  }
+}
+
 // ---- Chunk variant: plan tables ---------------------------------------------------------------------------------------
 
 struct PlanRecord {
@@ -268,8 +780,10 @@ struct PlanRecord {
 };
 
 struct ChunkLayout {
-  uint64_t chunk_table;  // [chunks] int2 (sequence, first token)
+  uint64_t chunk_table;  // [max_chunks] int4 (sequence, first token, tokens, 0)
+  uint64_t seq_table;    // [batch] int2 (first chunk, chunk count)
   uint64_t tables_bytes;
+  uint64_t records;      // [max_chunks][heads] records of kRecBytes
   uint64_t total;
   uint32_t max_chunks;
 };
@@ -278,9 +792,32 @@ ChunkLayout MakeChunkLayout(uint64_t tokens, uint64_t batch) {
   ChunkLayout l{};
   l.max_chunks = static_cast<uint32_t>(tokens / kChunk + batch);
   l.chunk_table = 0;
-  l.tables_bytes = roost::AlignUp(8ull * l.max_chunks, 256);
-  l.total = l.tables_bytes;
+  l.seq_table = roost::AlignUp(16ull * l.max_chunks, 256);
+  l.tables_bytes = roost::AlignUp(l.seq_table + 8ull * batch, 256);
+  l.records = l.tables_bytes;
+  l.total = l.records + uint64_t{l.max_chunks} * kHeads * kRecBytes;
   return l;
+}
+
+RoostStatus LaunchChunk(const RoostGatedDeltaRuleParams& p, const RoostWorkspace* ws, const ChunkLayout& l,
+                        uint32_t chunks, hipStream_t stream) {
+  ChunkArgs ca{};
+  ca.a = MakeArgs(p);
+  auto* base = static_cast<uint8_t*>(ws->device);
+  ca.chunks = reinterpret_cast<const int4*>(base + l.chunk_table);
+  ca.seqs = reinterpret_cast<const int2*>(base + l.seq_table);
+  ca.recs = base + l.records;
+  ca.chains = p.batch * kHeads;
+  const dim3 prep(chunks, kHeads);
+  const dim3 scan((ca.chains + 7) / 8 * 8 * kVBlocks);
+  if (Vec16(p)) {
+    hipLaunchKernelGGL(ChunkPrepKernel<true>, prep, dim3(256), 0, stream, ca);
+    hipLaunchKernelGGL(ChunkScanKernel<true>, scan, dim3(256), 0, stream, ca);
+  } else {
+    hipLaunchKernelGGL(ChunkPrepKernel<false>, prep, dim3(256), 0, stream, ca);
+    hipLaunchKernelGGL(ChunkScanKernel<false>, scan, dim3(256), 0, stream, ca);
+  }
+  return roost::FromHip(hipGetLastError(), "GatedDeltaRule chunk launch");
 }
 
 }  // namespace
@@ -361,18 +898,25 @@ extern "C" ROOST_API RoostStatus roost_gdn_chunk_plan(RoostContext* ctx, const v
     if (cu[0] != 0 || static_cast<uint32_t>(cu[p.batch]) != p.tokens) {
       return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRule plan: cu_seqlens_host must start at 0 and end at tokens");
     }
-    auto* table = static_cast<int32_t*>(ws->pinned_host);
+    auto* host = static_cast<uint8_t*>(ws->pinned_host);
+    auto* chunks = reinterpret_cast<int32_t*>(host + l.chunk_table);
+    auto* seqs = reinterpret_cast<int32_t*>(host + l.seq_table);
     uint32_t n = 0;
     for (uint32_t b = 0; b < p.batch; ++b) {
       if (cu[b + 1] < cu[b]) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRule plan: cu_seqlens_host decreases");
+      seqs[2 * b] = static_cast<int32_t>(n);
       for (int32_t t = cu[b]; t < cu[b + 1]; t += kChunk) {
-        table[2 * n] = static_cast<int32_t>(b);
-        table[2 * n + 1] = t;
+        chunks[4 * n] = static_cast<int32_t>(b);
+        chunks[4 * n + 1] = t;
+        chunks[4 * n + 2] = std::min<int32_t>(kChunk, cu[b + 1] - t);
+        chunks[4 * n + 3] = 0;
         ++n;
       }
+      seqs[2 * b + 1] = static_cast<int32_t>(n) - seqs[2 * b];
     }
     rec.chunks = n;
-    ROOST_TRY(FromHip(hipMemcpyAsync(ws->device, table, 8ull * n, hipMemcpyHostToDevice, Stream(stream)),
+    ROOST_TRY(FromHip(hipMemcpyAsync(ws->device, host, l.seq_table + 8ull * p.batch, hipMemcpyHostToDevice,
+                                     Stream(stream)),
                       "GatedDeltaRule plan copy"));
     std::memcpy(ws->plan, &rec, sizeof(rec));
     return ROOST_STATUS_OK;
@@ -396,6 +940,7 @@ extern "C" ROOST_API RoostStatus roost_gdn_chunk_run(RoostContext* ctx, const vo
     if (rec.magic != kPlanMagic || rec.batch != p.batch || rec.tokens != p.tokens || rec.chunks > l.max_chunks) {
       return Fail(ROOST_STATUS_NOT_PLANNED, "GatedDeltaRule: plan() has not run for these tokens and sequences");
     }
-    return LaunchRecurrent(p, Stream(stream));
+    if (rec.chunks == 0) return ROOST_STATUS_OK;
+    return LaunchChunk(p, ws, l, rec.chunks, Stream(stream));
   });
 }
