@@ -285,19 +285,19 @@ constexpr int kTokPitch = 72;    // bf16 per LDS row of a [dim or column][64 tok
 constexpr int kVBlock = 32;      // value columns per scan workgroup
 constexpr uint32_t kVBlocks = kDim / kVBlock;
 
-// Per-(chunk, head) record written by the prep kernel. T and P are stored as MFMA A operands of
-// v_mfma_f32_16x16x32_bf16: block (w, s) covers rows 16w..16w+15 and columns 32s..32s+31, lane l holding row
-// 16w + l % 16, columns 32s + 8 (l / 16) .. +7 as 16 bytes. Only the blocks with s <= w / 2 are on or below the
-// diagonal and are written.
-constexpr uint32_t kRecT = 0;          // [w 4][s 2][hi, lo][lane 64] x 16 B
-constexpr uint32_t kRecP = 16384;      // [w 4][s 2][lane 64] x 16 B
-constexpr uint32_t kRecScal = 24576;   // float [5][64]: e^G rk, beta, rq e^G, e^(Gn - G) rk, e^Gn (at [4][0])
-constexpr uint32_t kRecBytes = 25856;  // a multiple of 256
+// Per-(chunk, head) record written by the prep kernel, row-major bf16 matrices: T (hi and lo parts) and P as
+// [token t][token j], raw k transposed as [dim][token], then the per-token factors. The scan reads 16-byte pieces of
+// their rows as MFMA operands. Entries above the diagonal of T and P are written as zero.
+constexpr uint32_t kRecT = 0;          // T hi [64][64], then T lo [64][64]
+constexpr uint32_t kRecP = 16384;      // P [64][64]
+constexpr uint32_t kRecKT = 24576;     // k^T [128][64]
+constexpr uint32_t kRecScal = 40960;   // float [5][64]: e^G rk, beta, rq e^G, e^(Gn - G) rk, e^Gn (at [4][0])
+constexpr uint32_t kRecBytes = 42240;  // a multiple of 256
 
 struct ChunkArgs {
   GdnArgs a;
   const int4* chunks;  // [chunks] (sequence, first token, tokens, 0)
-  const int2* seqs;    // [batch] (first chunk, chunk count)
+  const int4* seqs;    // [batch] (first chunk, chunk count, first token, end token)
   uint8_t* recs;       // [chunks][heads] records
   uint32_t chains;     // batch * heads
 };
@@ -347,14 +347,15 @@ __device__ __forceinline__ float SumSq8(uint4 v) {
   return s;
 }
 
-// Lower blocks (w, s), s <= w / 2, of a 64 x 64 matrix in 16 x 32 MFMA-operand blocks: item b = 0..5.
-__device__ __forceinline__ void LowerBlock(int b, int& w, int& s) {
-  w = b < 2 ? b : 2 + ((b - 2) >> 1);
-  s = b < 2 ? 0 : ((b - 2) & 1);
+// fp32 16 x 16 x 4 MFMA: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16]; the result layout is that of the
+// bf16 16 x 16 products (lane l: rows 4 (l / 16) + i, column l % 16).
+__device__ __forceinline__ f32x4_t MfmaF32(float a, float b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// One workgroup per (chunk, head); wave w owns row tile w (tokens 16w..16w+15) of the 64 x 64 products.
 template <bool kVec>
-__global__ void __launch_bounds__(256, 2) ChunkPrepKernel(ChunkArgs ca) {
+__global__ void __launch_bounds__(256, 4) ChunkPrepKernel(ChunkArgs ca) {
   const GdnArgs& a = ca.a;
   const int4 ch = ca.chunks[blockIdx.x];
   const uint32_t h = blockIdx.y;
@@ -364,30 +365,38 @@ __global__ void __launch_bounds__(256, 2) ChunkPrepKernel(ChunkArgs ca) {
   const int r16 = lane & 15, kq = lane >> 4;
   uint8_t* rec = ca.recs + (static_cast<uint64_t>(blockIdx.x) * kHeads + h) * kRecBytes;
 
-  // region0 holds the raw q (tile 0) and k (tile 1) rows, then P and the substitution's partial products.
+  // region0 holds the raw q (tile 0) and k (tile 1) rows; once the products are formed it holds A and T (fp32).
   __shared__ __align__(16) uint8_t region0[2 * 64 * kTilePitch * 2];
-  __shared__ float a_lds[64][65];
-  __shared__ float t_lds[64][65];
   __shared__ float g_lds[64], rk_lds[64], rq_lds[64], b_lds[64];
   auto qk = reinterpret_cast<uint16_t(*)[64][kTilePitch]>(region0);
-  auto p_lds = reinterpret_cast<float(*)[65]>(region0);
-  auto tmp = reinterpret_cast<float(*)[65]>(region0 + 64 * 65 * 4);
+  auto a_lds = reinterpret_cast<float(*)[65]>(region0);
+  auto t_lds = reinterpret_cast<float(*)[65]>(region0 + 64 * 65 * 4);
 
-  {  // Raw rows into LDS (zero past the chunk's end) and their sums of squares.
+  {  // Raw rows into LDS (zero past the chunk's end) and their sums of squares. Every load is issued unconditionally
+     // from a clamped row and masked afterwards, so that all of them are in flight together.
     const int row = tid >> 2, part = tid & 3;
-    const bool ok = row < n;
-    const uint64_t tok = static_cast<uint64_t>(t0 + (ok ? row : n - 1));
+    const uint32_t keep = row < n ? ~0u : 0u;
+    const uint64_t tok = static_cast<uint64_t>(t0 + min(row, n - 1));
     const uint16_t* kp = a.k + tok * a.k_stride + h * kDim + part * 32;
     const uint16_t* qp = a.q + tok * a.q_stride + h * kDim + part * 32;
+    uint4 kv[4], qv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kv[i] = Load8<kVec>(kp + 8 * i);
+      qv[i] = Load8<kVec>(qp + 8 * i);
+    }
+    const uint64_t gi = static_cast<uint64_t>(t0 + min(lane, n - 1)) * kHeads + h;
+    const float graw = a.g[gi];
+    const uint16_t braw = a.beta[gi];
     float kk = 0.0f, qq = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      uint4 kv = Load8<kVec>(kp + 8 * i), qv = Load8<kVec>(qp + 8 * i);
-      if (!ok) kv = qv = make_uint4(0, 0, 0, 0);
-      kk += SumSq8(kv);
-      qq += SumSq8(qv);
-      *reinterpret_cast<uint4*>(&qk[1][row][part * 32 + 8 * i]) = kv;
-      *reinterpret_cast<uint4*>(&qk[0][row][part * 32 + 8 * i]) = qv;
+      kv[i] = make_uint4(kv[i].x & keep, kv[i].y & keep, kv[i].z & keep, kv[i].w & keep);
+      qv[i] = make_uint4(qv[i].x & keep, qv[i].y & keep, qv[i].z & keep, qv[i].w & keep);
+      kk += SumSq8(kv[i]);
+      qq += SumSq8(qv[i]);
+      *reinterpret_cast<uint4*>(&qk[1][row][part * 32 + 8 * i]) = kv[i];
+      *reinterpret_cast<uint4*>(&qk[0][row][part * 32 + 8 * i]) = qv[i];
     }
     kk = QuadSum(kk);
     qq = QuadSum(qq);
@@ -395,64 +404,84 @@ __global__ void __launch_bounds__(256, 2) ChunkPrepKernel(ChunkArgs ca) {
       rk_lds[row] = 1.0f / sqrtf(kk + 1e-6f);
       rq_lds[row] = a.scale / sqrtf(qq + 1e-6f);
     }
-  }
-  if (w == 0) {  // cumulative log-decay (zero increments past the end) and beta
-    const uint64_t gi = static_cast<uint64_t>(t0 + lane) * kHeads + h;
-    float gv = lane < n ? a.g[gi] : 0.0f;
+    if (w == 0) {  // cumulative log-decay (zero increments past the end) and beta
+      float gv = lane < n ? graw : 0.0f;
 #pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const float y = __shfl_up(gv, d, 64);
-      if (lane >= d) gv += y;
+      for (int d = 1; d < 64; d <<= 1) {
+        const float y = __shfl_up(gv, d, 64);
+        if (lane >= d) gv += y;
+      }
+      g_lds[lane] = gv;
+      b_lds[lane] = lane < n ? Bf16ToF32(braw) : 0.0f;
     }
-    g_lds[lane] = gv;
-    b_lds[lane] = lane < n ? Bf16ToF32(a.beta[gi]) : 0.0f;
   }
   __syncthreads();
 
-  // k.k^T and q.k^T for row tile w, column tiles c <= w.
-  f32x4_t kk4[4], qk4[4];
+  // kk4[c] = k.k^T at rows 16w.., columns 16c..; pt4[c] = k.q^T at rows 16c.. (key tokens j), columns 16w.. (query
+  // tokens t), i.e. P^T, whose result lanes hold four consecutive j of one t: one 8-byte piece of a row of P. A row-major
+  // 16 x 32 tile supplies the A and the B operand in the same lane layout, so the k rows of tile c serve as both.
+  f32x4_t kk4[4], pt4[4];
   {
-    uint4 ak[4], aq[4];
+    uint4 ak[4], bq[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       ak[s] = *reinterpret_cast<const uint4*>(&qk[1][16 * w + r16][32 * s + 8 * kq]);
-      aq[s] = *reinterpret_cast<const uint4*>(&qk[0][16 * w + r16][32 * s + 8 * kq]);
+      bq[s] = *reinterpret_cast<const uint4*>(&qk[0][16 * w + r16][32 * s + 8 * kq]);
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       kk4[c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-      qk4[c] = kk4[c];
+      pt4[c] = kk4[c];
       if (c <= w) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          const uint4 b = *reinterpret_cast<const uint4*>(&qk[1][16 * c + r16][32 * s + 8 * kq]);
-          kk4[c] = Mfma(ak[s], b, kk4[c]);
-          qk4[c] = Mfma(aq[s], b, qk4[c]);
+          const uint4 kc = *reinterpret_cast<const uint4*>(&qk[1][16 * c + r16][32 * s + 8 * kq]);
+          kk4[c] = Mfma(ak[s], kc, kk4[c]);
+          pt4[c] = Mfma(kc, bq[s], pt4[c]);
         }
       }
     }
   }
-  __syncthreads();  // the q/k tiles are dead: region0 becomes P and the partial products
+  // Raw k transposed: 16-byte pieces k^T[d][8g .. 8g + 7]; consecutive lanes read consecutive dims of a row.
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int piece = tid + 256 * m, d = piece & 127, g8 = piece >> 7;
+    uint32_t wd[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      wd[e] = static_cast<uint32_t>(qk[1][8 * g8 + 2 * e][d]) | (static_cast<uint32_t>(qk[1][8 * g8 + 2 * e + 1][d]) << 16);
+    }
+    *reinterpret_cast<uint4*>(rec + kRecKT + (d * 64 + 8 * g8) * 2) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+  }
+  __syncthreads();  // the q/k tiles are dead: region0 becomes A and T
+
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
+    uint2 pw = make_uint2(0, 0);
+    float pv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = 16 * w + 4 * kq + i, j = 16 * c + r16;
-      float av = 0.0f, pv = 0.0f;
-      if (j <= r) {
-        const float d = expf(g_lds[r] - g_lds[j]);
-        pv = qk4[c][i] * rq_lds[r] * rk_lds[j] * d;
-        if (j < r) av = b_lds[r] * d * kk4[c][i] * rk_lds[r] * rk_lds[j];
+      {  // A[r][j], r = 16w + 4kq + i, j = 16c + r16 (strictly lower); zero above the diagonal of A and T
+        const int r = 16 * w + 4 * kq + i, j = 16 * c + r16;
+        float av = 0.0f;
+        if (j < r) av = b_lds[r] * expf(g_lds[r] - g_lds[j]) * kk4[c][i] * rk_lds[r] * rk_lds[j];
+        a_lds[r][j] = av;
+        if (c > w) t_lds[r][j] = 0.0f;
       }
-      a_lds[r][j] = av;
-      p_lds[r][j] = pv;
-      if (c > w) t_lds[r][j] = 0.0f;
+      {  // P[t][j], t = 16w + r16, j = 16c + 4kq + i (on and below the diagonal)
+        const int t = 16 * w + r16, j = 16 * c + 4 * kq + i;
+        pv[i] = j <= t ? pt4[c][i] * rq_lds[t] * rk_lds[j] * expf(g_lds[t] - g_lds[j]) : 0.0f;
+      }
     }
+    if (c <= w) {
+      pw.x = PackRne(pv[0], pv[1]);
+      pw.y = PackRne(pv[2], pv[3]);
+    }
+    *reinterpret_cast<uint2*>(rec + kRecP + ((16 * w + r16) * 64 + 16 * c + 4 * kq) * 2) = pw;
   }
   __syncthreads();
 
-  // T = (I + A)^-1. Diagonal 16 x 16 blocks by forward substitution (wave w, one column per lane), then the blocks
-  // below the diagonal by T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj in order of distance from the diagonal.
+  // T = (I + A)^-1. Diagonal 16 x 16 blocks by forward substitution (wave w, one column per lane) ...
   if (lane < 16) {
     float x[16];
 #pragma unroll
@@ -465,54 +494,44 @@ __global__ void __launch_bounds__(256, 2) ChunkPrepKernel(ChunkArgs ca) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) t_lds[16 * w + i][16 * w + lane] = x[i];
   }
-  // P blocks out while the substitution proceeds (P is final).
-  for (int item = tid; item < 6 * 64; item += 256) {
-    int bw, bs;
-    LowerBlock(item >> 6, bw, bs);
-    const int l = item & 63;
-    const float* src = &p_lds[16 * bw + (l & 15)][32 * bs + 8 * (l >> 4)];
-    uint4 v;
-    v.x = PackRne(src[0], src[1]);
-    v.y = PackRne(src[2], src[3]);
-    v.z = PackRne(src[4], src[5]);
-    v.w = PackRne(src[6], src[7]);
-    *reinterpret_cast<uint4*>(rec + kRecP + ((bw * 2 + bs) * 64 + l) * 16) = v;
-  }
   __syncthreads();
+  // ... then the blocks below it, T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj, in order of distance d = i - j from the
+  // diagonal, one block per wave, on fp32 MFMA. The partial sum goes through the (unused) mirror block A[j][i].
 #pragma unroll
   for (int d = 1; d < 4; ++d) {
-    const int items = (4 - d) * 256;
-    for (int e = tid; e < items; e += 256) {
-      const int j = e >> 8, i = j + d, r = (e >> 4) & 15, cc = e & 15;
-      float acc = 0.0f;
+    if (w < 4 - d) {
+      const int j = w, i = w + d;
+      f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
       for (int k = j; k < i; ++k) {
 #pragma unroll
-        for (int m = 0; m < 16; ++m) acc = fmaf(a_lds[16 * i + r][16 * k + m], t_lds[16 * k + m][16 * j + cc], acc);
+        for (int kk = 0; kk < 4; ++kk) {
+          acc = MfmaF32(a_lds[16 * i + r16][16 * k + 4 * kk + kq], t_lds[16 * k + 4 * kk + kq][16 * j + r16], acc);
+        }
       }
-      tmp[16 * i + r][16 * j + cc] = acc;
-    }
-    __syncthreads();
-    for (int e = tid; e < items; e += 256) {
-      const int j = e >> 8, i = j + d, r = (e >> 4) & 15, cc = e & 15;
-      float acc = 0.0f;
 #pragma unroll
-      for (int m = 0; m < 16; ++m) acc = fmaf(t_lds[16 * i + r][16 * i + m], tmp[16 * i + m][16 * j + cc], acc);
-      t_lds[16 * i + r][16 * j + cc] = -acc;
+      for (int ii = 0; ii < 4; ++ii) a_lds[16 * j + 4 * kq + ii][16 * i + r16] = acc[ii];
+      f32x4_t tij = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        tij = MfmaF32(t_lds[16 * i + r16][16 * i + 4 * kk + kq], a_lds[16 * j + 4 * kk + kq][16 * i + r16], tij);
+      }
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) t_lds[16 * i + 4 * kq + ii][16 * j + r16] = -tij[ii];
     }
     __syncthreads();
   }
-  for (int item = tid; item < 6 * 64; item += 256) {
-    int bw, bs;
-    LowerBlock(item >> 6, bw, bs);
-    const int l = item & 63;
-    const float* src = &t_lds[16 * bw + (l & 15)][32 * bs + 8 * (l >> 4)];
+  // T rows as bf16 hi + lo, 8 columns per piece.
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    const int piece = tid + 256 * m, row = piece >> 3, c8 = piece & 7;
+    const float* src = &t_lds[row][8 * c8];
     uint4 hi, lo;
     Split2(src[0], src[1], hi.x, lo.x);
     Split2(src[2], src[3], hi.y, lo.y);
     Split2(src[4], src[5], hi.z, lo.z);
     Split2(src[6], src[7], hi.w, lo.w);
-    *reinterpret_cast<uint4*>(rec + kRecT + (((bw * 2 + bs) * 2 + 0) * 64 + l) * 16) = hi;
-    *reinterpret_cast<uint4*>(rec + kRecT + (((bw * 2 + bs) * 2 + 1) * 64 + l) * 16) = lo;
+    *reinterpret_cast<uint4*>(rec + kRecT + (row * 64 + 8 * c8) * 2) = hi;
+    *reinterpret_cast<uint4*>(rec + kRecT + 8192 + (row * 64 + 8 * c8) * 2) = lo;
   }
   if (tid < 64) {
     float* sc = reinterpret_cast<float*>(rec + kRecScal);
@@ -526,24 +545,58 @@ __global__ void __launch_bounds__(256, 2) ChunkPrepKernel(ChunkArgs ca) {
   }
 }
 
-// The registers one wave needs for one chunk: its 16 k and q rows (as MFMA A operands), its v values in the MFMA
-// result layout, its blocks of T and P, and the per-token factors.
+// Per wave and chunk, the record's rows that wave uses are copied into LDS by global_load_lds (no registers on the
+// way), double-buffered across chunks. 16-byte pieces are stored at swizzled positions so that the MFMA operand reads
+// (16 lanes reading the same piece index of 16 different rows) hit distinct banks.
+constexpr int kStageT = 0;         // T hi rows 16w..16w+15: [16][8 pieces of 16 B]
+constexpr int kStageTLo = 2048;    // T lo rows
+constexpr int kStageP = 4096;      // P rows
+constexpr int kStageKT = 6144;     // k^T rows 32w..32w+31: [32][8 pieces]
+constexpr int kStageScal = 10240;  // float [4][16]: e^G rk, beta, rq e^G, e^(Gn - G) rk of tokens 16w..16w+15
+constexpr int kStageBytes = 10496;
+
+// Position of 16-byte piece c8 of row r in a [rows][8 pieces] staging block.
+__device__ __forceinline__ int Swz(int r, int c8) { return r * 128 + 16 * (c8 ^ ((r >> 1) & 7)); }
+
+__device__ __forceinline__ uint32_t LdsAddr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
+}
+
+// global -> LDS copies (global_load_lds): lane l's bytes land at lds + size * l; lds must be wave-uniform. Issued from
+// inline assembly so that the compiler does not treat every later LDS access as waiting on them (it cannot tell which
+// LDS bytes they write); the scan waits for them itself, one chunk later. M0 carries the LDS address and is restored.
+__device__ __forceinline__ void Dma16(const void* g, uint32_t lds) {
+  uint32_t save;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(save) : "v"(g), "s"(lds));
+}
+__device__ __forceinline__ void Dma4(const void* g, uint32_t lds) {
+  uint32_t save;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(save) : "v"(g), "s"(lds));
+}
+
+// s_waitcnt vmcnt(0) alone (expcnt and lgkmcnt fields at their maxima).
+__device__ __forceinline__ void WaitVmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// The registers one wave needs for one chunk: its 16 raw k and q rows (MFMA A operands), its v values in the MFMA
+// result layout and the chunk's total decay.
 struct ChunkRegs {
   uint4 kr[4], qr[4];
-  uint4 thi[2], tlo[2], pr[2];
-  float4 xs, beta, os, ws;
   float vv[2][4];
   float decay;
   int t0, n;
 };
 
+// Chunk c of a sequence starts at token sq.z + 64c; its record is number sq.x + c. Loads the wave's registers and
+// starts the copy of its record rows into `stage` (this wave's block of one buffer).
 template <bool kVec>
-__device__ __forceinline__ void LoadChunk(const ChunkArgs& ca, uint32_t chunk, uint32_t h, uint32_t vb, int w, int lane,
-                                          ChunkRegs& r) {
+__device__ __forceinline__ void LoadChunk(const ChunkArgs& ca, const int4& sq, int c, uint32_t h, uint32_t vb, int w,
+                                          int lane, ChunkRegs& r, uint8_t* stage) {
   const GdnArgs& a = ca.a;
-  const int4 ch = ca.chunks[chunk];
-  r.t0 = ch.y;
-  r.n = ch.z;
+  const uint32_t chunk = static_cast<uint32_t>(sq.x + c);
+  r.t0 = sq.z + static_cast<int>(kChunk) * c;
+  r.n = min(static_cast<int>(kChunk), sq.w - r.t0);
   const int r16 = lane & 15, kq = lane >> 4;
   const int row = 16 * w + r16;
   const bool ok = row < r.n;
@@ -569,22 +622,196 @@ __device__ __forceinline__ void LoadChunk(const ChunkArgs& ca, uint32_t chunk, u
     }
   }
   const uint8_t* rec = ca.recs + (static_cast<uint64_t>(chunk) * kHeads + h) * kRecBytes;
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {  // blocks above the diagonal are loaded but never used
-    r.thi[s] = *reinterpret_cast<const uint4*>(rec + kRecT + (((w * 2 + s) * 2 + 0) * 64 + lane) * 16);
-    r.tlo[s] = *reinterpret_cast<const uint4*>(rec + kRecT + (((w * 2 + s) * 2 + 1) * 64 + lane) * 16);
-    r.pr[s] = *reinterpret_cast<const uint4*>(rec + kRecP + ((w * 2 + s) * 64 + lane) * 16);
-  }
-  const float* sc = reinterpret_cast<const float*>(rec + kRecScal) + 16 * w + 4 * kq;
-  r.xs = *reinterpret_cast<const float4*>(sc);
-  r.beta = *reinterpret_cast<const float4*>(sc + 64);
-  r.os = *reinterpret_cast<const float4*>(sc + 128);
-  r.ws = *reinterpret_cast<const float4*>(sc + 192);
   r.decay = reinterpret_cast<const float*>(rec + kRecScal)[256];
+  // Record rows into LDS: lane l fills byte 16 l of each 1 KB instruction block.
+  const uint32_t base = LdsAddr(stage);
+  const int rr = lane >> 3, pos = lane & 7;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int rw = 8 * i + rr, c8 = pos ^ ((rw >> 1) & 7);
+    const uint8_t* src = rec + ((16 * w + rw) * 64 + 8 * c8) * 2;
+    Dma16(src + kRecT, base + kStageT + 1024 * i);
+    Dma16(src + kRecT + 8192, base + kStageTLo + 1024 * i);
+    Dma16(src + kRecP, base + kStageP + 1024 * i);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int rw = 8 * i + rr, c8 = pos ^ ((rw >> 1) & 7);
+    Dma16(rec + kRecKT + ((32 * w + rw) * 64 + 8 * c8) * 2, base + kStageKT + 1024 * i);
+  }
+  Dma4(rec + kRecScal + ((lane >> 4) * 64 + 16 * w + r16) * 4, base + kStageScal);
+}
+
+// A chunk's output values of one lane, stored one chunk later (so that the wait at the top of a chunk never waits on
+// stores issued just before it).
+struct ChunkOut {
+  uint16_t o[2][4];
+  int t0, n;
+};
+
+__device__ __forceinline__ void StoreOut(const GdnArgs& a, const ChunkOut& r, uint32_t h, uint32_t vb, int w, int r16,
+                                         int kq) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = 16 * w + 4 * kq + i;
+    if (t < r.n) {
+      uint16_t* op = a.out + (static_cast<uint64_t>(r.t0 + t) * kHeads + h) * kDim + vb * kVBlock + r16;
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) op[16 * nt] = r.o[nt][i];
+    }
+  }
 }
 
 __device__ __forceinline__ float F4(const float4& v, int i) {
   return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+template <typename T>
+__device__ __forceinline__ T LdsRead(const uint8_t* p) {
+  return *reinterpret_cast<const T*>(p);
+}
+
+// One chunk of the scan (see ChunkScanKernel); `stage` is this wave's staged record block for the chunk.
+__device__ __forceinline__ void ScanStep(const GdnArgs& a, const ChunkRegs& cur, const uint8_t* stage,
+                                         f32x4_t (&st)[2][2], uint32_t h, uint32_t vb, int w, int r16, int kq,
+                                         uint16_t (&s_lds)[2][kVBlock][kTilePitch],
+                                         uint16_t (&y_lds)[2][kVBlock][kTokPitch],
+                                         uint16_t (&vn_lds)[3][kVBlock][kTokPitch], ChunkOut& out) {
+  // (1) S as bf16 hi/lo B operands.
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      uint2 hi, lo;
+      Split2(st[mt][nt][0], st[mt][nt][1], hi.x, lo.x);
+      Split2(st[mt][nt][2], st[mt][nt][3], hi.y, lo.y);
+      const int d0 = 32 * w + 16 * mt + 4 * kq, col = 16 * nt + r16;
+      *reinterpret_cast<uint2*>(&s_lds[0][col][d0]) = hi;
+      *reinterpret_cast<uint2*>(&s_lds[1][col][d0]) = lo;
+    }
+  }
+  __syncthreads();
+  // (2) X = k S0 (hi + lo) and q S0 (hi) for tokens 16w..16w+15; Y = beta (v - e^G rk X).
+  uint4 bh[4][2], bl[4][2];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      bh[s][nt] = *reinterpret_cast<const uint4*>(&s_lds[0][16 * nt + r16][32 * s + 8 * kq]);
+      bl[s][nt] = *reinterpret_cast<const uint4*>(&s_lds[1][16 * nt + r16][32 * s + 8 * kq]);
+    }
+  }
+  f32x4_t xs4[2], oq4[2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) xs4[nt] = oq4[nt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      xs4[nt] = Mfma(cur.kr[s], bh[s][nt], xs4[nt]);
+      oq4[nt] = Mfma(cur.qr[s], bh[s][nt], oq4[nt]);
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) xs4[nt] = Mfma(cur.kr[s], bl[s][nt], xs4[nt]);
+  }
+  const float4 xs = LdsRead<float4>(stage + kStageScal + 16 * kq);
+  const float4 beta = LdsRead<float4>(stage + kStageScal + 64 + 16 * kq);
+  const float4 os = LdsRead<float4>(stage + kStageScal + 128 + 16 * kq);
+  const float4 ws = LdsRead<float4>(stage + kStageScal + 192 + 16 * kq);
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    float y[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) y[i] = F4(beta, i) * (cur.vv[nt][i] - F4(xs, i) * xs4[nt][i]);
+    uint2 hi, lo;
+    Split2(y[0], y[1], hi.x, lo.x);
+    Split2(y[2], y[3], hi.y, lo.y);
+    const int col = 16 * nt + r16, t = 16 * w + 4 * kq;
+    *reinterpret_cast<uint2*>(&y_lds[0][col][t]) = hi;
+    *reinterpret_cast<uint2*>(&y_lds[1][col][t]) = lo;
+  }
+  __syncthreads();
+  // (3) V = T Y over the pieces on or below the diagonal (hi.hi + hi.lo + lo.hi).
+  f32x4_t vn4[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    if (s <= (w >> 1)) {
+      const uint4 th = LdsRead<uint4>(stage + kStageT + Swz(r16, 4 * s + kq));
+      const uint4 tl = LdsRead<uint4>(stage + kStageTLo + Swz(r16, 4 * s + kq));
+      uint4 yh[2], yl[2];
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        yh[nt] = *reinterpret_cast<const uint4*>(&y_lds[0][16 * nt + r16][32 * s + 8 * kq]);
+        yl[nt] = *reinterpret_cast<const uint4*>(&y_lds[1][16 * nt + r16][32 * s + 8 * kq]);
+      }
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        vn4[nt] = Mfma(th, yh[nt], vn4[nt]);
+        vn4[nt] = Mfma(th, yl[nt], vn4[nt]);
+        vn4[nt] = Mfma(tl, yh[nt], vn4[nt]);
+      }
+    }
+  }
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int col = 16 * nt + r16, t = 16 * w + 4 * kq;
+    uint2 v, hi, lo;
+    v.x = PackRne(vn4[nt][0], vn4[nt][1]);
+    v.y = PackRne(vn4[nt][2], vn4[nt][3]);
+    Split2(vn4[nt][0] * ws.x, vn4[nt][1] * ws.y, hi.x, lo.x);
+    Split2(vn4[nt][2] * ws.z, vn4[nt][3] * ws.w, hi.y, lo.y);
+    *reinterpret_cast<uint2*>(&vn_lds[0][col][t]) = v;
+    *reinterpret_cast<uint2*>(&vn_lds[1][col][t]) = hi;
+    *reinterpret_cast<uint2*>(&vn_lds[2][col][t]) = lo;
+  }
+  __syncthreads();
+  // (4) o = rq e^G q S0 + P V for tokens 16w..16w+15.
+  f32x4_t pv4[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    if (s <= (w >> 1)) {
+      const uint4 pr = LdsRead<uint4>(stage + kStageP + Swz(r16, 4 * s + kq));
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const uint4 b = *reinterpret_cast<const uint4*>(&vn_lds[0][16 * nt + r16][32 * s + 8 * kq]);
+        pv4[nt] = Mfma(pr, b, pv4[nt]);
+      }
+    }
+  }
+  out.t0 = cur.t0;
+  out.n = cur.n;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) out.o[nt][i] = F32ToBf16(fmaf(F4(os, i), oq4[nt][i], pv4[nt][i]));
+  }
+  // (5) S = e^Gn S0 + k^T (ws V) (hi + lo) for state rows 32w..32w+31.
+  uint4 vh[2][2], vl[2][2], ak[2][2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      vh[s][nt] = *reinterpret_cast<const uint4*>(&vn_lds[1][16 * nt + r16][32 * s + 8 * kq]);
+      vl[s][nt] = *reinterpret_cast<const uint4*>(&vn_lds[2][16 * nt + r16][32 * s + 8 * kq]);
+    }
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) ak[mt][s] = LdsRead<uint4>(stage + kStageKT + Swz(16 * mt + r16, 4 * s + kq));
+  }
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      f32x4_t acc = st[mt][nt] * cur.decay;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) acc = Mfma(ak[mt][s], vh[s][nt], acc);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) acc = Mfma(ak[mt][s], vl[s][nt], acc);
+      st[mt][nt] = acc;
+    }
+  }
 }
 
 // One workgroup per (sequence, head, value block of 32 columns); wave w owns state rows 32w..32w+31 and, for the
@@ -598,7 +825,7 @@ __global__ void __launch_bounds__(256, 1) ChunkScanKernel(ChunkArgs ca) {
   const uint32_t vb = (x >> 3) & 3;
   if (chain >= ca.chains) return;
   const uint32_t seq = chain / kHeads, h = chain % kHeads;
-  const int2 sq = ca.seqs[seq];
+  const int4 sq = ca.seqs[seq];
   if (sq.y == 0) return;  // an empty sequence leaves its slot untouched
   const int32_t slot = a.slots[seq];
   const bool has_slot = slot >= 0 && static_cast<uint64_t>(slot) < a.pool_slots;
@@ -607,9 +834,11 @@ __global__ void __launch_bounds__(256, 1) ChunkScanKernel(ChunkArgs ca) {
   const int r16 = lane & 15, kq = lane >> 4;
 
   __shared__ __align__(16) uint16_t s_lds[2][kVBlock][kTilePitch];  // S hi, lo as [column][dim]
-  __shared__ __align__(16) uint16_t kt_lds[2][kDim][kTokPitch];     // raw k^T [dim][token], double-buffered
   __shared__ __align__(16) uint16_t y_lds[2][kVBlock][kTokPitch];   // Y hi, lo as [column][token]
   __shared__ __align__(16) uint16_t vn_lds[3][kVBlock][kTokPitch];  // V (bf16), V * ws hi, lo as [column][token]
+  __shared__ __align__(16) uint8_t stage_lds[2][4][kStageBytes];    // [buffer][wave] staged record rows
+  uint8_t* stage0 = stage_lds[0][w];
+  uint8_t* stage1 = stage_lds[1][w];
 
   // st[mt][nt][i] = S[32w + 16mt + 4kq + i][32vb + 16nt + r16]
   f32x4_t st[2][2];
@@ -626,135 +855,29 @@ __global__ void __launch_bounds__(256, 1) ChunkScanKernel(ChunkArgs ca) {
     }
   }
 
-  ChunkRegs cur;
-  LoadChunk<kVec>(ca, sq.x, h, vb, w, lane, cur);
-  for (int c = 0; c < sq.y; ++c) {
-    ChunkRegs nxt;
-    LoadChunk<kVec>(ca, sq.x + min(c + 1, sq.y - 1), h, vb, w, lane, nxt);
-    const int buf = c & 1;
-    // (1) S as bf16 hi/lo B operands; raw k^T for the state update.
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        uint2 hi, lo;
-        Split2(st[mt][nt][0], st[mt][nt][1], hi.x, lo.x);
-        Split2(st[mt][nt][2], st[mt][nt][3], hi.y, lo.y);
-        const int d0 = 32 * w + 16 * mt + 4 * kq, col = 16 * nt + r16;
-        *reinterpret_cast<uint2*>(&s_lds[0][col][d0]) = hi;
-        *reinterpret_cast<uint2*>(&s_lds[1][col][d0]) = lo;
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const uint32_t wd[4] = {cur.kr[s].x, cur.kr[s].y, cur.kr[s].z, cur.kr[s].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        kt_lds[buf][32 * s + 8 * kq + 2 * e][16 * w + r16] = static_cast<uint16_t>(wd[e]);
-        kt_lds[buf][32 * s + 8 * kq + 2 * e + 1][16 * w + r16] = static_cast<uint16_t>(wd[e] >> 16);
-      }
-    }
-    __syncthreads();
-    // (2) X = k S0 (hi + lo) and q S0 (hi) for tokens 16w..16w+15; Y = beta (v - e^G rk X).
-    f32x4_t xs4[2], oq4[2];
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) xs4[nt] = oq4[nt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const uint4 bh = *reinterpret_cast<const uint4*>(&s_lds[0][16 * nt + r16][32 * s + 8 * kq]);
-        const uint4 bl = *reinterpret_cast<const uint4*>(&s_lds[1][16 * nt + r16][32 * s + 8 * kq]);
-        xs4[nt] = Mfma(cur.kr[s], bh, xs4[nt]);
-        xs4[nt] = Mfma(cur.kr[s], bl, xs4[nt]);
-        oq4[nt] = Mfma(cur.qr[s], bh, oq4[nt]);
-      }
-    }
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      float y[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) y[i] = F4(cur.beta, i) * (cur.vv[nt][i] - F4(cur.xs, i) * xs4[nt][i]);
-      uint2 hi, lo;
-      Split2(y[0], y[1], hi.x, lo.x);
-      Split2(y[2], y[3], hi.y, lo.y);
-      const int col = 16 * nt + r16, t = 16 * w + 4 * kq;
-      *reinterpret_cast<uint2*>(&y_lds[0][col][t]) = hi;
-      *reinterpret_cast<uint2*>(&y_lds[1][col][t]) = lo;
-    }
-    __syncthreads();
-    // (3) V = T Y over the blocks on or below the diagonal (hi.hi + hi.lo + lo.hi).
-    f32x4_t vn4[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      if (s <= (w >> 1)) {
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          const uint4 bh = *reinterpret_cast<const uint4*>(&y_lds[0][16 * nt + r16][32 * s + 8 * kq]);
-          const uint4 bl = *reinterpret_cast<const uint4*>(&y_lds[1][16 * nt + r16][32 * s + 8 * kq]);
-          vn4[nt] = Mfma(cur.thi[s], bh, vn4[nt]);
-          vn4[nt] = Mfma(cur.thi[s], bl, vn4[nt]);
-          vn4[nt] = Mfma(cur.tlo[s], bh, vn4[nt]);
-        }
-      }
-    }
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int col = 16 * nt + r16, t = 16 * w + 4 * kq;
-      uint2 v, hi, lo;
-      v.x = PackRne(vn4[nt][0], vn4[nt][1]);
-      v.y = PackRne(vn4[nt][2], vn4[nt][3]);
-      Split2(vn4[nt][0] * cur.ws.x, vn4[nt][1] * cur.ws.y, hi.x, lo.x);
-      Split2(vn4[nt][2] * cur.ws.z, vn4[nt][3] * cur.ws.w, hi.y, lo.y);
-      *reinterpret_cast<uint2*>(&vn_lds[0][col][t]) = v;
-      *reinterpret_cast<uint2*>(&vn_lds[1][col][t]) = hi;
-      *reinterpret_cast<uint2*>(&vn_lds[2][col][t]) = lo;
-    }
-    __syncthreads();
-    // (4) o = rq e^G q S0 + P V for tokens 16w..16w+15.
-    f32x4_t pv4[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      if (s <= (w >> 1)) {
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          const uint4 b = *reinterpret_cast<const uint4*>(&vn_lds[0][16 * nt + r16][32 * s + 8 * kq]);
-          pv4[nt] = Mfma(cur.pr[s], b, pv4[nt]);
-        }
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = 16 * w + 4 * kq + i;
-      if (t < cur.n) {
-        uint16_t* op = a.out + (static_cast<uint64_t>(cur.t0 + t) * kHeads + h) * kDim + vb * kVBlock + r16;
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) op[16 * nt] = F32ToBf16(fmaf(F4(cur.os, i), oq4[nt][i], pv4[nt][i]));
-      }
-    }
-    // (5) S = e^Gn S0 + k^T (ws V) (hi + lo) for state rows 32w..32w+31.
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      uint4 ak[2];
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        ak[s] = *reinterpret_cast<const uint4*>(&kt_lds[buf][32 * w + 16 * mt + r16][32 * s + 8 * kq]);
-      }
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        f32x4_t acc = st[mt][nt] * cur.decay;
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const uint4 bh = *reinterpret_cast<const uint4*>(&vn_lds[1][16 * nt + r16][32 * s + 8 * kq]);
-          const uint4 bl = *reinterpret_cast<const uint4*>(&vn_lds[2][16 * nt + r16][32 * s + 8 * kq]);
-          acc = Mfma(ak[s], bh, acc);
-          acc = Mfma(ak[s], bl, acc);
-        }
-        st[mt][nt] = acc;
-      }
-    }
-    cur = nxt;
+  // Two register sets and two staging buffers in turn: the loads of chunk c + 1 are in flight while chunk c is
+  // computed (the last chunk is loaded again past the end rather than branching around the load).
+  // Each step first waits for every vector memory operation issued one step earlier (the chunk's registers, its
+  // staged record rows, the previous chunk's outputs), then starts the loads of the next chunk.
+  ChunkRegs ra, rb;
+  ChunkOut out;
+  out.n = 0;
+  const int last = sq.y - 1;
+  LoadChunk<kVec>(ca, sq, 0, h, vb, w, lane, ra, stage0);
+  for (int c = 0;;) {
+    WaitVmem();
+    LoadChunk<kVec>(ca, sq, min(c + 1, last), h, vb, w, lane, rb, stage1);
+    StoreOut(a, out, h, vb, w, r16, kq);
+    ScanStep(a, ra, stage0, st, h, vb, w, r16, kq, s_lds, y_lds, vn_lds, out);
+    if (++c > last) break;
+    WaitVmem();
+    LoadChunk<kVec>(ca, sq, min(c + 1, last), h, vb, w, lane, ra, stage0);
+    StoreOut(a, out, h, vb, w, r16, kq);
+    ScanStep(a, rb, stage1, st, h, vb, w, r16, kq, s_lds, y_lds, vn_lds, out);
+    if (++c > last) break;
   }
+  StoreOut(a, out, h, vb, w, r16, kq);
+  WaitVmem();  // the copies of the re-loaded last chunk land before the workgroup's LDS is released
   if (has_slot) {
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
@@ -781,7 +904,7 @@ struct PlanRecord {
 
 struct ChunkLayout {
   uint64_t chunk_table;  // [max_chunks] int4 (sequence, first token, tokens, 0)
-  uint64_t seq_table;    // [batch] int2 (first chunk, chunk count)
+  uint64_t seq_table;    // [batch] int4 (first chunk, chunk count, first token, end token)
   uint64_t tables_bytes;
   uint64_t records;      // [max_chunks][heads] records of kRecBytes
   uint64_t total;
@@ -793,7 +916,7 @@ ChunkLayout MakeChunkLayout(uint64_t tokens, uint64_t batch) {
   l.max_chunks = static_cast<uint32_t>(tokens / kChunk + batch);
   l.chunk_table = 0;
   l.seq_table = roost::AlignUp(16ull * l.max_chunks, 256);
-  l.tables_bytes = roost::AlignUp(l.seq_table + 8ull * batch, 256);
+  l.tables_bytes = roost::AlignUp(l.seq_table + 16ull * batch, 256);
   l.records = l.tables_bytes;
   l.total = l.records + uint64_t{l.max_chunks} * kHeads * kRecBytes;
   return l;
@@ -805,7 +928,7 @@ RoostStatus LaunchChunk(const RoostGatedDeltaRuleParams& p, const RoostWorkspace
   ca.a = MakeArgs(p);
   auto* base = static_cast<uint8_t*>(ws->device);
   ca.chunks = reinterpret_cast<const int4*>(base + l.chunk_table);
-  ca.seqs = reinterpret_cast<const int2*>(base + l.seq_table);
+  ca.seqs = reinterpret_cast<const int4*>(base + l.seq_table);
   ca.recs = base + l.records;
   ca.chains = p.batch * kHeads;
   const dim3 prep(chunks, kHeads);
@@ -904,7 +1027,9 @@ extern "C" ROOST_API RoostStatus roost_gdn_chunk_plan(RoostContext* ctx, const v
     uint32_t n = 0;
     for (uint32_t b = 0; b < p.batch; ++b) {
       if (cu[b + 1] < cu[b]) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRule plan: cu_seqlens_host decreases");
-      seqs[2 * b] = static_cast<int32_t>(n);
+      seqs[4 * b] = static_cast<int32_t>(n);
+      seqs[4 * b + 2] = cu[b];
+      seqs[4 * b + 3] = cu[b + 1];
       for (int32_t t = cu[b]; t < cu[b + 1]; t += kChunk) {
         chunks[4 * n] = static_cast<int32_t>(b);
         chunks[4 * n + 1] = t;
@@ -912,10 +1037,10 @@ extern "C" ROOST_API RoostStatus roost_gdn_chunk_plan(RoostContext* ctx, const v
         chunks[4 * n + 3] = 0;
         ++n;
       }
-      seqs[2 * b + 1] = static_cast<int32_t>(n) - seqs[2 * b];
+      seqs[4 * b + 1] = static_cast<int32_t>(n) - seqs[4 * b];
     }
     rec.chunks = n;
-    ROOST_TRY(FromHip(hipMemcpyAsync(ws->device, host, l.seq_table + 8ull * p.batch, hipMemcpyHostToDevice,
+    ROOST_TRY(FromHip(hipMemcpyAsync(ws->device, host, l.seq_table + 16ull * p.batch, hipMemcpyHostToDevice,
                                      Stream(stream)),
                       "GatedDeltaRule plan copy"));
     std::memcpy(ws->plan, &rec, sizeof(rec));
