@@ -52,8 +52,11 @@ constexpr uint32_t kGroup = 4;                  // query heads per KV head (Qwen
 constexpr uint32_t kDecodeWgsPerCu = ROOST_DECODE_WGS_PER_CU;  // decode workgroups resident per CU
 constexpr int kDecodeRing = ROOST_DECODE_RING;  // register ring depth: groups in flight per wavefront = ring - 1
 constexpr uint32_t kMaxMergeSplits = 1024;      // partials one sequence may be split into
-constexpr uint32_t kPrefillTileQ = 32;          // query tokens per prefill workgroup
+constexpr uint32_t kPrefillTileQ = 32;          // query tokens per workgroup of the general-page-size prefill
 constexpr uint32_t kPrefillTileK = 64;          // keys per LDS tile
+constexpr uint32_t kPfTokens = 64;              // query tokens per workgroup of the prefill for page sizes % 16 == 0
+constexpr uint32_t kPfRows = kPfTokens * kGroup;  // query rows (token, head) of one such workgroup
+constexpr uint32_t kPfMinSplitTiles = 8;        // a split piece covers at least this many 64-key tiles
 constexpr uint32_t kAlign = 256;
 constexpr uint32_t kPlanMagic = 0x41504752;     // "RGPA"
 constexpr float kLog2e = 1.4426950408889634f;
@@ -70,11 +73,27 @@ struct DecodeMerge {
   int32_t count;
   int32_t reserved;
 };
+// A prefill work item: query tokens q0 .. q0 + rows - 1 of sequence seq (all kGroup query heads of one KV head)
+// against keys [kbeg, kend). slot >= 0 marks one piece of a split key range: it writes fp32 partials (unnormalised
+// output, running max and sum) that PrefillMergeKernel combines; slot -1 writes the final rows.
 struct PrefillWork {
   int32_t seq;
-  int32_t q0;  // first query of the tile, relative to the sequence
+  int32_t q0;
   int32_t kv_head;
+  int32_t rows;
+  int32_t kbeg;
+  int32_t kend;
+  int32_t slot;
   int32_t reserved;
+};
+struct PrefillMerge {
+  int32_t seq;
+  int32_t q0;
+  int32_t kv_head;
+  int32_t rows;
+  int32_t first;  // the pieces own partial slots first .. first + count - 1
+  int32_t count;
+  int32_t reserved[2];
 };
 
 // What plan() leaves for run(); trivially copyable, read back with memcpy.
@@ -201,19 +220,22 @@ RoostStatus Validate(const RoostPagedAttentionParams& p, bool for_run) {
 
 // ---- Host planning ---------------------------------------------------------------------------------------------------
 
-Layout MakeLayout(uint64_t work_items, uint64_t ranges, uint64_t merges, uint64_t splits, uint32_t q_heads,
-                  uint32_t kv_heads, uint32_t head_dim, uint32_t mode) {
+// rows_per_split: fp32 partial rows one split slot holds (decode: the query heads of a sequence; prefill: kPfRows).
+Layout MakeLayout(uint64_t work_items, uint64_t ranges, uint64_t merges, uint64_t splits, uint32_t rows_per_split,
+                  uint32_t head_dim, uint32_t mode) {
   Layout l;
   l.work_items = work_items;
   l.ranges = ranges;
   l.merges = merges;
   l.splits = splits;
-  const uint64_t item_bytes = mode == ROOST_ATTENTION_DECODE ? sizeof(DecodeWork) : sizeof(PrefillWork);
+  const bool decode = mode == ROOST_ATTENTION_DECODE;
+  const uint64_t item_bytes = decode ? sizeof(DecodeWork) : sizeof(PrefillWork);
+  const uint64_t merge_bytes = decode ? sizeof(DecodeMerge) : sizeof(PrefillMerge);
   l.range_offset = roost::AlignUp(work_items * item_bytes, 16);
   l.merge_offset = roost::AlignUp(l.range_offset + (ranges > 0 ? (ranges + 1) * sizeof(int32_t) : 0), 16);
-  l.int_bytes = l.merge_offset + merges * sizeof(DecodeMerge);
+  l.int_bytes = l.merge_offset + merges * merge_bytes;
   l.float_offset = roost::AlignUp(l.int_bytes, kAlign);
-  l.float_bytes = splits * q_heads * (static_cast<uint64_t>(head_dim) + 2) * sizeof(float);
+  l.float_bytes = splits * rows_per_split * (static_cast<uint64_t>(head_dim) + 2) * sizeof(float);
   l.total = l.float_offset + l.float_bytes;
   return l;
 }
@@ -284,7 +306,7 @@ Layout PlanDecode(const RoostPagedAttentionParams& p, uint32_t cus, unsigned cha
   }
   range_ptr.push_back(static_cast<int32_t>(items.size()));
   Layout l = MakeLayout(items.size(), range_ptr.size() - 1, merges.size(), static_cast<uint64_t>(slot), p.q_heads,
-                        p.kv_heads, p.head_dim, ROOST_ATTENTION_DECODE);
+                        p.head_dim, ROOST_ATTENTION_DECODE);
   if (host != nullptr) {
     std::memcpy(host, items.data(), items.size() * sizeof(DecodeWork));
     std::memcpy(host + l.range_offset, range_ptr.data(), range_ptr.size() * sizeof(int32_t));
@@ -293,31 +315,71 @@ Layout PlanDecode(const RoostPagedAttentionParams& p, uint32_t cus, unsigned cha
   return l;
 }
 
-// Prefill: one work item per (32-query tile, KV head), longest first.
-Layout PlanPrefill(const RoostPagedAttentionParams& p, unsigned char* host) {
+// Prefill work items: one per (query tile, KV head) -- 64-token tiles when the page size is a multiple of 16 (the
+// DMA-fed kernel), 32-token tiles otherwise. For the 64-token kernel the key range of an item longer than the average
+// load of a CU is cut into pieces of whole 64-key tiles (at least kPfMinSplitTiles each), so that the longest causal
+// tile does not set the makespan; the pieces write partials merged by PrefillMergeKernel. Items are ordered longest
+// first. The cuts depend on the whole batch, so the variant is deterministic but not batch invariant.
+bool PrefillFastPath(const RoostPagedAttentionParams& p) {
+  return p.page_size % 16 == 0 && (p.page_size & (p.page_size - 1)) == 0;
+}
+
+Layout PlanPrefill(const RoostPagedAttentionParams& p, uint32_t cus, unsigned char* host) {
+  const bool fast = PrefillFastPath(p);
+  const int64_t tile_q = fast ? kPfTokens : kPrefillTileQ;
   struct Item {
     PrefillWork w;
-    uint64_t cost;
+    int64_t cost;
   };
   std::vector<Item> items;
+  int64_t total_tiles = 0;
   for (uint32_t b = 0; b < p.batch; ++b) {
     const int64_t n = p.q_indptr_host[b + 1] - p.q_indptr_host[b];
     const int64_t kv = KvLenHost(p, b);
-    for (int64_t q0 = 0; q0 < n; q0 += kPrefillTileQ) {
-      const int64_t last = std::min<int64_t>(q0 + kPrefillTileQ, n) - 1;
-      int64_t keys = p.causal ? std::min<int64_t>(kv, kv - n + last + 1) : kv;
-      if (keys < 0) keys = 0;
+    for (int64_t q0 = 0; q0 < n; q0 += tile_q) {
+      const int64_t rows = std::min<int64_t>(tile_q, n - q0);
+      int64_t kend = p.causal ? std::min<int64_t>(kv, kv - n + q0 + rows) : kv;
+      if (kend < 0) kend = 0;
+      total_tiles += roost::CeilDiv(kend, 64) * p.kv_heads;
       for (uint32_t h = 0; h < p.kv_heads; ++h) {
-        items.push_back(Item{PrefillWork{static_cast<int32_t>(b), static_cast<int32_t>(q0), static_cast<int32_t>(h), 0},
-                             static_cast<uint64_t>(keys) + 64});
+        items.push_back(Item{PrefillWork{static_cast<int32_t>(b), static_cast<int32_t>(q0), static_cast<int32_t>(h),
+                                         static_cast<int32_t>(rows), 0, static_cast<int32_t>(kend), -1, 0},
+                             kend + 64});
       }
     }
   }
+  std::vector<PrefillMerge> merges;
+  int32_t slot = 0;
+  if (fast) {
+    const int64_t target = std::max<int64_t>(kPfMinSplitTiles, roost::CeilDiv(total_tiles, std::max<uint32_t>(cus, 1)));
+    std::vector<Item> cut;
+    cut.reserve(items.size());
+    for (const Item& it : items) {
+      const int64_t tiles = roost::CeilDiv(static_cast<int64_t>(it.w.kend), 64);
+      const int64_t pieces = std::min<int64_t>(roost::CeilDiv(tiles, target), kMaxMergeSplits);
+      if (pieces <= 1) {
+        cut.push_back(it);
+        continue;
+      }
+      merges.push_back(PrefillMerge{it.w.seq, it.w.q0, it.w.kv_head, it.w.rows, slot, static_cast<int32_t>(pieces), {0, 0}});
+      for (int64_t i = 0; i < pieces; ++i) {
+        const int64_t t0 = tiles * i / pieces, t1 = tiles * (i + 1) / pieces;
+        PrefillWork w = it.w;
+        w.kbeg = static_cast<int32_t>(t0 * 64);
+        w.kend = static_cast<int32_t>(std::min<int64_t>(t1 * 64, it.w.kend));
+        w.slot = slot++;
+        cut.push_back(Item{w, (t1 - t0) * 64 + 64});
+      }
+    }
+    items.swap(cut);
+  }
   std::stable_sort(items.begin(), items.end(), [](const Item& a, const Item& b) { return a.cost > b.cost; });
-  Layout l = MakeLayout(items.size(), 0, 0, 0, p.q_heads, p.kv_heads, p.head_dim, ROOST_ATTENTION_PREFILL);
+  Layout l = MakeLayout(items.size(), 0, merges.size(), static_cast<uint64_t>(slot), kPfRows, p.head_dim,
+                        ROOST_ATTENTION_PREFILL);
   if (host != nullptr) {
     auto* w = reinterpret_cast<PrefillWork*>(host);
     for (size_t i = 0; i < items.size(); ++i) w[i] = items[i].w;
+    std::memcpy(host + l.merge_offset, merges.data(), merges.size() * sizeof(PrefillMerge));
   }
   return l;
 }
@@ -325,7 +387,7 @@ Layout PlanPrefill(const RoostPagedAttentionParams& p, unsigned char* host) {
 uint32_t ComputeUnits(const RoostContext* ctx) { return ctx != nullptr && ctx->compute_units > 0 ? ctx->compute_units : 256; }
 
 Layout PlanLayout(const RoostPagedAttentionParams& p, uint32_t cus, unsigned char* host) {
-  return p.mode == ROOST_ATTENTION_DECODE ? PlanDecode(p, cus, host) : PlanPrefill(p, host);
+  return p.mode == ROOST_ATTENTION_DECODE ? PlanDecode(p, cus, host) : PlanPrefill(p, cus, host);
 }
 
 // ---- Device helpers --------------------------------------------------------------------------------------------------
@@ -967,7 +1029,7 @@ __global__ void __launch_bounds__(256, 1)
   const int32_t qbeg = q_indptr[wk.seq];
   const int32_t n = q_indptr[wk.seq + 1] - qbeg;
   const int32_t q0 = wk.q0;
-  const int32_t rows = min(static_cast<int32_t>(kPrefillTileQ), n - q0);
+  const int32_t rows = wk.rows;
   // Key position of this lane's query, and of the tile's first / last query.
   const int32_t base_pos = static_cast<int32_t>(kv_len) - n + q0;
   const int32_t my_pos = base_pos + col;
@@ -1142,6 +1204,306 @@ __global__ void __launch_bounds__(256, 1)
   }
 }
 
+// ---- Prefill kernel for page sizes that are multiples of 16 (bf16, head_dim 256, MFMA, DMA-fed) ---------------------
+//
+// One workgroup = 64 query tokens x the 4 query heads of one KV head, 8 wavefronts (two per SIMD, so one wavefront's
+// softmax runs under the other's MFMAs): wavefront w is query head 4 kvh + (w & 3) for tokens 32 (w >> 2) .. +31.
+// Per 64-key tile each wavefront copies 8 K rows and 8 V rows (inside one page: 16-aligned groups of rows never
+// straddle a page when the page size is a multiple of 16) from the paged cache straight into LDS with
+// global_load_lds, double-buffered, so the copy of tile t + 1 runs under the products of tile t. The tile is consumed
+// in two 32-key halves:
+//   S^T = K Q^T  (v_mfma_f32_32x32x16_bf16; K rows from LDS as the A operand, Q^T held in registers as B),
+//   online softmax per query (lane pair l, l ^ 32 holds one query's 32 scores; lazy rescaling: the running max only
+//   moves when a score exceeds it by more than 2^8, so P stays below 256),
+//   O^T += V^T P^T (V^T operands read from the row-major V tile with ds_read_b64_tr_b16, P^T from registers).
+// ds_read_b64_tr_b16 works within groups of 16 lanes: output lane 4a + b, element e, is element b of the 8 bytes that
+// lane 4e + a addressed. So when lane 4e + a of a group addresses keys k0 + e, dims d0 + 4a .. +3, output lane j of the
+// group receives V[k0 + e][d0 + j], e = 0..3: a V^T operand row.
+// LDS rows are 512 bytes with 16-byte pieces at swizzled positions: K piece p of row r at p ^ (r & 15) (the A-operand
+// reads of 16 consecutive rows hit 16 distinct bank groups), V piece p at p ^ 4 (r & 3) (the transposed reads of
+// 4 consecutive rows, 32 bytes each, hit distinct banks).
+
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) unsigned char lds_byte_t;
+
+__device__ __forceinline__ uint32_t LdsAddr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_byte_t*)p));
+}
+
+// global -> LDS copy of 16 bytes per lane (lane l lands at lds + 16 l; lds wave-uniform), from inline assembly so that
+// the compiler does not make every later LDS access wait on it; the kernel waits for it itself. M0 is restored.
+__device__ __forceinline__ void Dma16(const void* g, uint32_t lds) {
+  uint32_t save;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(save) : "v"(g), "s"(lds));
+}
+
+// The same with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane byte offset.
+__device__ __forceinline__ void Dma16(const void* sbase, uint32_t voff, uint32_t lds) {
+  uint32_t save;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+               : "=&s"(save) : "v"(voff), "s"(sbase), "s"(lds));
+}
+
+__device__ __forceinline__ void WaitVmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0) only
+
+__device__ __forceinline__ u32x2_t LdsTr16(const unsigned char* base, uint32_t off) {
+  auto* ptr = reinterpret_cast<__attribute__((address_space(3))) i16x4_t*>(
+      const_cast<lds_byte_t*>((const lds_byte_t*)base + off));
+  return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(ptr));
+}
+
+constexpr int kPfTileBytes = kPrefillTileK * kPD * 2;  // one 64-key K or V tile: 32 KB
+
+__global__ void __launch_bounds__(512, 1)
+    PrefillTileKernel(const uint16_t* __restrict__ q, uint16_t* __restrict__ out, float* __restrict__ lse, KvView kv,
+                      const int32_t* __restrict__ kv_indices, const int32_t* __restrict__ q_indptr,
+                      const PrefillWork* __restrict__ work, float* __restrict__ part_o, float* __restrict__ part_ml,
+                      uint32_t q_heads, uint32_t causal, uint32_t ps_shift, float scale_log2) {
+  __shared__ __attribute__((aligned(16))) unsigned char tiles[2][2][kPfTileBytes];  // [buffer][K, V]
+
+  const PrefillWork wk = work[blockIdx.x];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hq = w & 3;       // query head within the KV head's group
+  const int qt = w >> 2;      // 32-token half of the item
+  const int hl = lane >> 5;   // half of the wave: MFMA k-slot group
+  const int col = lane & 31;  // MFMA N index: this lane's query within the wavefront's 32
+  const uint32_t kvh = static_cast<uint32_t>(wk.kv_head);
+  const uint32_t head = kvh * kGroup + hq;
+  const uint16_t* kbase = static_cast<const uint16_t*>(kv.k);
+  const uint16_t* vbase = static_cast<const uint16_t*>(kv.v);
+  const uint32_t ps = kv.page_size;  // a power of two, 1 << ps_shift
+
+  int32_t p0 = 0;
+  const uint32_t kv_len = SeqKvLen(kv, wk.seq, &p0);
+  const int32_t qbeg = q_indptr[wk.seq];
+  const int32_t n = q_indptr[wk.seq + 1] - qbeg;
+  const int32_t r = 32 * qt + col;  // this lane's query within the item
+  const bool row_ok = r < wk.rows;
+  const int32_t my_pos = static_cast<int32_t>(kv_len) - n + wk.q0 + r;  // its key position
+  const int32_t last_pos = static_cast<int32_t>(kv_len) - n + wk.q0 + 32 * qt + 31;  // the wavefront's last query
+  const int32_t kbeg = wk.kbeg, kend = wk.kend;
+  const int ntiles = kend > kbeg ? (kend - kbeg + 63) / 64 : 0;
+
+  // Q^T operands: qreg[ks] = q[query r][dims 16 ks + 8 hl .. +8].
+  u32x4_t qreg[16];
+  {
+    const uint16_t* qrow = q + (static_cast<uint64_t>(qbeg + wk.q0 + (row_ok ? r : 0)) * q_heads + head) * kPD + hl * 8;
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) {
+      const u32x4_t x = *reinterpret_cast<const u32x4_t*>(qrow + ks * 16);
+      qreg[ks] = row_ok ? x : u32x4_t{0, 0, 0, 0};
+    }
+  }
+
+  // Page id of the 16 rows kb + 16 g .. +15 (clamped into the item's keys); false when it lies outside the pool.
+  auto group_page = [&](int32_t kb, int g, uint64_t* pg) -> bool {
+    const int32_t pos0 = min(kb + 16 * g, kend - 1);
+    const int32_t page = kv_indices[p0 + (pos0 >> ps_shift)];
+    const bool good = page >= 0 && static_cast<uint64_t>(page) < kv.pool_pages;
+    *pg = good ? static_cast<uint64_t>(page) : 0;
+    return good;
+  };
+  // Element offsets inside a page: a row at in-page position `within` starts at row_mul * within + row_add.
+  const uint32_t row_mul = kv.hnd ? kPD : kv.kv_heads * kPD;
+  const uint32_t row_add = kv.hnd ? kvh * ps * kPD : kvh * kPD;
+  const uint64_t page_elems = static_cast<uint64_t>(ps) * kv.kv_heads * kPD;
+  // This wavefront's share of the copy of tile t: rows 8w .. 8w + 7 of K and of V (two rows per instruction).
+  auto issue = [&](int t, int buf) {
+    const int32_t kb = kbeg + 64 * t;
+    const int32_t pos0 = kb + 8 * w;  // this wavefront's first row; all 8 lie in one page
+    uint64_t pg;
+    group_page(kb, w >> 1, &pg);
+    const int32_t page_first = min(pos0, kend - 1) & ~((1 << ps_shift) - 1);
+    const uint16_t* kpage = kbase + pg * page_elems + row_add;
+    const uint16_t* vpage = vbase + pg * page_elems + row_add;
+    const uint32_t kdst = LdsAddr(tiles[buf][0]) + 8 * w * 512, vdst = LdsAddr(tiles[buf][1]) + 8 * w * 512;
+    int c = col, hh = hl;
+    asm volatile("" : "+v"(c), "+v"(hh));  // recompute the lane offsets per call instead of holding eight of them
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rr = 2 * i + hh;  // row 8w + rr of the tile
+      const uint32_t within = static_cast<uint32_t>(min(pos0 + rr, kend - 1) - page_first);
+      const uint32_t off = 2 * row_mul * within;
+      const uint32_t kp = 16 * static_cast<uint32_t>(c ^ ((8 * w + rr) & 15));
+      const uint32_t vp = 16 * static_cast<uint32_t>(c ^ ((rr & 3) << 2));
+      Dma16(kpage, off + kp, kdst + 2 * i * 512);
+      Dma16(vpage, off + vp, vdst + 2 * i * 512);
+    }
+  };
+
+  f32x16_t o[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) o[dt][v] = 0.0f;
+  float m_run = -INFINITY;
+  float l_run = 0.0f;
+
+  // Lane-constant parts of the transposed V reads: in lane group g = lane / 16, lane j = lane % 16 addresses key
+  // +(j / 4) at dims +4 (j % 4), keys based at 32 half + 16 c + 4 (g >> 1) (+8 for the operand's second half), dims
+  // based at 32 dt + 16 (g & 1).
+  const int vj = lane & 15, vg = lane >> 4;
+  const int vkey = 4 * (vg >> 1) + (vj >> 2);
+  const int vdim = 16 * (vg & 1) + 4 * (vj & 3);
+  // With the swizzle, the V piece holding dims 32 dt + vdim of key vkey + 8 m sits at byte
+  // vkey * 512 + 8 m * 512 + (64 dt ^ vx) + vl: (4 (4 dt + pl)) ^ (16 * 4 e) splits into a dt part and a lane part.
+  int vrow = vkey * 512 + 16 * ((vdim >> 3) & 3) + 2 * (vdim & 7);
+  int vx = 64 * (vkey & 3);
+  int krow = col * 512;
+  int kx = 16 * (col & 15);
+
+  if (ntiles > 0) issue(0, 0);
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    WaitVmem();       // this wavefront's copies of tile t have landed
+    __syncthreads();  // ... and everyone's; everyone is also done reading the other buffer
+    if (t + 1 < ntiles) issue(t + 1, buf ^ 1);
+    const int32_t kb = kbeg + 64 * t;
+    // The lane-constant operand offsets are re-derived every tile rather than the ~64 offsets built from them being
+    // kept live across the loop (the register budget at two wavefronts per SIMD does not hold them).
+    asm volatile("" : "+v"(vrow), "+v"(vx), "+v"(krow), "+v"(kx));
+    uint32_t bad = 0;  // 16-key groups of this tile whose page id lies outside the pool
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      uint64_t pg;
+      bad |= group_page(kb, g, &pg) ? 0u : (1u << g);
+    }
+    const bool need_mask = kb + 64 > kend || (causal && kb + 63 > last_pos - 31) || bad != 0;
+    const unsigned char* ktile = tiles[buf][0];
+    const unsigned char* vtile = tiles[buf][1];
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      f32x16_t sc;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) sc[v] = 0.0f;
+      // K row 32 half + col, piece 2 ks + hl at position (2 ks + hl) ^ (col & 15) (32 half keeps row & 15 = col & 15).
+      const unsigned char* krow_p = ktile + 32 * half * 512 + krow;
+#pragma unroll
+      for (int ks = 0; ks < 16; ++ks) {
+        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(krow_p + ((16 * (2 * ks + hl)) ^ kx));
+        sc = Mfma32(a, qreg[ks], sc);
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int kk = 32 * half + (v >> 2) * 8 + hl * 4 + (v & 3);  // key within the tile
+        const int32_t key = kb + kk;
+        float x = sc[v] * scale_log2;
+        if (need_mask && (key >= kend || (causal && key > my_pos) || ((bad >> (kk >> 4)) & 1u))) x = -INFINITY;
+        sc[v] = x;
+        mx = fmaxf(mx, x);
+      }
+      mx = fmaxf(mx, ShflXor(mx, 32));
+      const bool grow = mx > m_run + 8.0f;
+      if (__any(grow)) {
+        const float m_new = grow ? mx : m_run;
+        const float corr = m_run == -INFINITY ? 0.0f : exp2f(m_run - m_new);
+        l_run *= corr;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) o[dt][v] *= corr;
+        m_run = m_new;
+      }
+      const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+      float psum = 0.0f;
+      u32x4_t pb[2];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        float pf[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pf[e] = exp2f(sc[(2 * c) * 4 + e] - m_use);
+          pf[4 + e] = exp2f(sc[(2 * c + 1) * 4 + e] - m_use);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) psum += pf[e];
+        pb[c] = u32x4_t{PackBf16(pf[0], pf[1]), PackBf16(pf[2], pf[3]), PackBf16(pf[4], pf[5]), PackBf16(pf[6], pf[7])};
+      }
+      l_run += psum;
+      // O^T += V^T P^T over this half's two 16-key steps.
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const uint32_t kbase1 = static_cast<uint32_t>((32 * half + 16 * c) * 512 + vrow);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          const uint32_t off1 = kbase1 + ((64 * dt) ^ vx);
+          const u32x2_t lo = LdsTr16(vtile, off1);
+          const u32x2_t hi = LdsTr16(vtile, off1 + 8 * 512);
+          o[dt] = Mfma32(u32x4_t{lo[0], lo[1], hi[0], hi[1]}, pb[c], o[dt]);
+        }
+      }
+    }
+  }
+
+  // Lane holds dims 32 dt + 8 i + 4 hl + jj of query r.
+  const float l_tot = l_run + ShflXor(l_run, 32);
+  if (!row_ok) return;
+  if (wk.slot >= 0) {
+    const uint64_t prow = static_cast<uint64_t>(wk.slot) * kPfRows + static_cast<uint64_t>(r) * kGroup + hq;
+    float* po = part_o + prow * kPD;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d = dt * 32 + i * 8 + hl * 4;
+        *reinterpret_cast<float4*>(po + d) = make_float4(o[dt][i * 4], o[dt][i * 4 + 1], o[dt][i * 4 + 2], o[dt][i * 4 + 3]);
+      }
+    if (hl == 0) {
+      part_ml[2 * prow] = m_run;
+      part_ml[2 * prow + 1] = l_tot;
+    }
+    return;
+  }
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  const uint64_t orow = (static_cast<uint64_t>(qbeg + wk.q0 + r) * q_heads + head) * kPD;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = dt * 32 + i * 8 + hl * 4;
+      const u32x2_t v{PackBf16(o[dt][i * 4] * inv, o[dt][i * 4 + 1] * inv),
+                      PackBf16(o[dt][i * 4 + 2] * inv, o[dt][i * 4 + 3] * inv)};
+      *reinterpret_cast<u32x2_t*>(out + orow + d) = v;
+    }
+  if (lse != nullptr && hl == 0) {
+    lse[static_cast<uint64_t>(qbeg + wk.q0 + r) * q_heads + head] = l_tot > 0.0f ? m_run + log2f(l_tot) : -INFINITY;
+  }
+}
+
+// Combines the pieces of a split prefill item: block (merge, token), thread = dim; the 4 query heads in turn.
+__global__ void __launch_bounds__(256)
+    PrefillMergeKernel(uint16_t* __restrict__ out, float* __restrict__ lse, const PrefillMerge* __restrict__ merges,
+                       const float* __restrict__ part_o, const float* __restrict__ part_ml,
+                       const int32_t* __restrict__ q_indptr, uint32_t q_heads) {
+  const PrefillMerge mg = merges[blockIdx.x];
+  const int r = blockIdx.y;
+  if (r >= mg.rows) return;
+  const int d = threadIdx.x;
+  const uint64_t token = static_cast<uint64_t>(q_indptr[mg.seq] + mg.q0 + r);
+  for (uint32_t hq = 0; hq < kGroup; ++hq) {
+    const uint64_t row = static_cast<uint64_t>(r) * kGroup + hq;
+    float mx = -INFINITY;
+    for (int i = 0; i < mg.count; ++i) mx = fmaxf(mx, part_ml[2 * ((mg.first + i) * uint64_t{kPfRows} + row)]);
+    float l = 0.0f, acc = 0.0f;
+    if (mx != -INFINITY) {
+      for (int i = 0; i < mg.count; ++i) {
+        const uint64_t prow = (mg.first + i) * uint64_t{kPfRows} + row;
+        const float m = part_ml[2 * prow];
+        const float f = m == -INFINITY ? 0.0f : exp2f(m - mx);
+        l += part_ml[2 * prow + 1] * f;
+        acc += part_o[prow * kPD + d] * f;
+      }
+    }
+    const uint32_t head = mg.kv_head * kGroup + hq;
+    out[(token * q_heads + head) * kPD + d] = F32ToBf16(l > 0.0f ? acc / l : 0.0f);
+    if (lse != nullptr && d == 0) lse[token * q_heads + head] = l > 0.0f ? mx + log2f(l) : -INFINITY;
+  }
+}
+
 template <typename T, int D>
 RoostStatus LaunchDecode(const RoostPagedAttentionParams& p, const PlanRecord& rec, unsigned char* dev, const KvView& kv,
                          float scale_log2, hipStream_t stream) {
@@ -1285,10 +1647,27 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_run(RoostContext*, const 
       }
     }
     if (rec.work_items == 0) return ROOST_STATUS_OK;
+    const auto* items = reinterpret_cast<const PrefillWork*>(dev);
+    const auto* q_indptr = static_cast<const int32_t*>(p.q_indptr.address);
+    auto* outp = static_cast<uint16_t*>(p.output.address);
+    auto* lsep = static_cast<float*>(p.lse.address);
+    if (PrefillFastPath(p)) {
+      auto* part_o = reinterpret_cast<float*>(dev + rec.float_offset);
+      auto* part_ml = part_o + rec.splits * kPfRows * kPD;
+      hipLaunchKernelGGL(PrefillTileKernel, dim3(static_cast<uint32_t>(rec.work_items)), dim3(512), 0, s,
+                         static_cast<const uint16_t*>(p.q.address), outp, lsep, kv, kv.kv_indices, q_indptr, items,
+                         part_o, part_ml, p.q_heads, p.causal, static_cast<uint32_t>(__builtin_ctz(p.page_size)),
+                         scale_log2);
+      ROOST_TRY(FromHip(hipGetLastError(), "PagedAttention prefill launch"));
+      if (rec.merges == 0) return ROOST_STATUS_OK;
+      hipLaunchKernelGGL(PrefillMergeKernel, dim3(static_cast<uint32_t>(rec.merges), kPfTokens), dim3(kPD), 0, s, outp,
+                         lsep, reinterpret_cast<const PrefillMerge*>(dev + rec.merge_offset), part_o, part_ml, q_indptr,
+                         p.q_heads);
+      return FromHip(hipGetLastError(), "PagedAttention prefill merge launch");
+    }
     hipLaunchKernelGGL(PrefillKernel, dim3(static_cast<uint32_t>(rec.work_items)), dim3(256), 0, s,
-                       static_cast<const uint16_t*>(p.q.address), static_cast<uint16_t*>(p.output.address),
-                       static_cast<float*>(p.lse.address), kv, static_cast<const int32_t*>(p.q_indptr.address),
-                       reinterpret_cast<const PrefillWork*>(dev), p.q_heads, p.causal, scale_log2);
+                       static_cast<const uint16_t*>(p.q.address), outp, lsep, kv, q_indptr, items, p.q_heads, p.causal,
+                       scale_log2);
     return FromHip(hipGetLastError(), "PagedAttention prefill launch");
   });
 }

@@ -230,6 +230,11 @@ PREFILL_CASES = [
     ("multi-seq", [(17, 17), (64, 300), (1, 50), (200, 200)], 16, False, True),
     ("non-causal-32-of-200", [(32, 200)], 16, False, False),
     ("partial-last-page", [(33, 33), (5, 21)], 16, False, True),
+    # page sizes that are not multiples of 16 take the general (register-staged) prefill kernel
+    ("chunk-100-of-300 ps8", [(100, 300)], 8, False, True),
+    ("fresh-40 ps1 HND", [(40, 40)], 1, True, True),
+    # a long causal chunk: its key range is cut into pieces that the merge kernel combines
+    ("chunk-512-of-4000 split", [(512, 4000), (3, 3)], 16, False, True),
 ]
 
 
