@@ -56,7 +56,7 @@ constexpr uint32_t kPrefillTileQ = 32;          // query tokens per workgroup of
 constexpr uint32_t kPrefillTileK = 64;          // keys per LDS tile
 constexpr uint32_t kPfTokens = 64;              // query tokens per workgroup of the prefill for page sizes % 16 == 0
 constexpr uint32_t kPfRows = kPfTokens * kGroup;  // query rows (token, head) of one such workgroup
-constexpr uint32_t kPfMinSplitTiles = 8;        // a split piece covers at least this many 64-key tiles
+constexpr uint32_t kPfMinSplitTiles = 16;       // a split piece covers at least this many 64-key tiles
 constexpr uint32_t kAlign = 256;
 constexpr uint32_t kPlanMagic = 0x41504752;     // "RGPA"
 constexpr float kLog2e = 1.4426950408889634f;
@@ -1253,6 +1253,12 @@ __device__ __forceinline__ u32x2_t LdsTr16(const unsigned char* base, uint32_t o
   return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(ptr));
 }
 
+// Round-to-nearest-even pack of two finite floats (v_cvt_pk_bf16_f32): the softmax weights, which lie in [0, 256].
+__device__ __forceinline__ uint32_t PackRne(float lo, float hi) {
+  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 constexpr int kPfTileBytes = kPrefillTileK * kPD * 2;  // one 64-key K or V tile: 32 KB
 
 __global__ void __launch_bounds__(512, 1)
@@ -1298,24 +1304,24 @@ __global__ void __launch_bounds__(512, 1)
     }
   }
 
-  // Page id of the 16 rows kb + 16 g .. +15 (clamped into the item's keys); false when it lies outside the pool.
-  auto group_page = [&](int32_t kb, int g, uint64_t* pg) -> bool {
-    const int32_t pos0 = min(kb + 16 * g, kend - 1);
-    const int32_t page = kv_indices[p0 + (pos0 >> ps_shift)];
-    const bool good = page >= 0 && static_cast<uint64_t>(page) < kv.pool_pages;
-    *pg = good ? static_cast<uint64_t>(page) : 0;
-    return good;
+  // Page ids of the four 16-row groups of tile t (rows clamped into the item's keys); loaded one tile before the
+  // copy that needs them, so the scalar loads never stall the loop.
+  auto load_ids = [&](int t, int32_t (&ids)[4]) {
+    const int32_t kb = kbeg + 64 * t;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) ids[g] = kv_indices[p0 + (min(kb + 16 * g, kend - 1) >> ps_shift)];
   };
+  auto good_page = [&](int32_t id) { return id >= 0 && static_cast<uint64_t>(id) < kv.pool_pages; };
   // Element offsets inside a page: a row at in-page position `within` starts at row_mul * within + row_add.
   const uint32_t row_mul = kv.hnd ? kPD : kv.kv_heads * kPD;
   const uint32_t row_add = kv.hnd ? kvh * ps * kPD : kvh * kPD;
   const uint64_t page_elems = static_cast<uint64_t>(ps) * kv.kv_heads * kPD;
   // This wavefront's share of the copy of tile t: rows 8w .. 8w + 7 of K and of V (two rows per instruction).
-  auto issue = [&](int t, int buf) {
+  auto issue = [&](int t, int buf, const int32_t (&ids)[4]) {
     const int32_t kb = kbeg + 64 * t;
     const int32_t pos0 = kb + 8 * w;  // this wavefront's first row; all 8 lie in one page
-    uint64_t pg;
-    group_page(kb, w >> 1, &pg);
+    const int32_t id = ids[w >> 1];
+    const uint64_t pg = good_page(id) ? static_cast<uint64_t>(id) : 0;  // a bad page's rows are masked, not read
     const int32_t page_first = min(pos0, kend - 1) & ~((1 << ps_shift) - 1);
     const uint16_t* kpage = kbase + pg * page_elems + row_add;
     const uint16_t* vpage = vbase + pg * page_elems + row_add;
@@ -1353,24 +1359,29 @@ __global__ void __launch_bounds__(512, 1)
   int vrow = vkey * 512 + 16 * ((vdim >> 3) & 3) + 2 * (vdim & 7);
   int vx = 64 * (vkey & 3);
   int krow = col * 512;
-  int kx = 16 * (col & 15);
+  int kx = 16 * (hl ^ (col & 15));
 
-  if (ntiles > 0) issue(0, 0);
+  int32_t ids_cur[4] = {0, 0, 0, 0}, ids_nxt[4] = {0, 0, 0, 0};
+  if (ntiles > 0) {
+    load_ids(0, ids_cur);
+    issue(0, 0, ids_cur);
+    load_ids(min(1, ntiles - 1), ids_nxt);
+  }
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
     WaitVmem();       // this wavefront's copies of tile t have landed
     __syncthreads();  // ... and everyone's; everyone is also done reading the other buffer
-    if (t + 1 < ntiles) issue(t + 1, buf ^ 1);
+    if (t + 1 < ntiles) issue(t + 1, buf ^ 1, ids_nxt);
+    uint32_t bad = 0;  // 16-key groups of this tile whose page id lies outside the pool
+#pragma unroll
+    for (int g = 0; g < 4; ++g) bad |= good_page(ids_cur[g]) ? 0u : (1u << g);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) ids_cur[g] = ids_nxt[g];
+    load_ids(min(t + 2, ntiles - 1), ids_nxt);
     const int32_t kb = kbeg + 64 * t;
     // The lane-constant operand offsets are re-derived every tile rather than the ~64 offsets built from them being
     // kept live across the loop (the register budget at two wavefronts per SIMD does not hold them).
     asm volatile("" : "+v"(vrow), "+v"(vx), "+v"(krow), "+v"(kx));
-    uint32_t bad = 0;  // 16-key groups of this tile whose page id lies outside the pool
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      uint64_t pg;
-      bad |= group_page(kb, g, &pg) ? 0u : (1u << g);
-    }
     const bool need_mask = kb + 64 > kend || (causal && kb + 63 > last_pos - 31) || bad != 0;
     const unsigned char* ktile = tiles[buf][0];
     const unsigned char* vtile = tiles[buf][1];
@@ -1379,11 +1390,14 @@ __global__ void __launch_bounds__(512, 1)
       f32x16_t sc;
 #pragma unroll
       for (int v = 0; v < 16; ++v) sc[v] = 0.0f;
-      // K row 32 half + col, piece 2 ks + hl at position (2 ks + hl) ^ (col & 15) (32 half keeps row & 15 = col & 15).
+      // K row 32 half + col, piece 2 ks + hl at position (2 ks + hl) ^ (col & 15) (32 half keeps row & 15 = col & 15);
+      // in bytes 16 ((2 ks + hl) ^ (col & 15)) = 32 ks ^ 16 (hl ^ (col & 15)).
       const unsigned char* krow_p = ktile + 32 * half * 512 + krow;
+      u32x4_t ka = *reinterpret_cast<const u32x4_t*>(krow_p + kx);
 #pragma unroll
-      for (int ks = 0; ks < 16; ++ks) {
-        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(krow_p + ((16 * (2 * ks + hl)) ^ kx));
+      for (int ks = 0; ks < 16; ++ks) {  // the operand of step ks + 1 is read while step ks multiplies
+        const u32x4_t a = ka;
+        if (ks + 1 < 16) ka = *reinterpret_cast<const u32x4_t*>(krow_p + ((32 * (ks + 1)) ^ kx));
         sc = Mfma32(a, qreg[ks], sc);
       }
       float mx = -INFINITY;
@@ -1416,12 +1430,12 @@ __global__ void __launch_bounds__(512, 1)
         float pf[8];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          pf[e] = exp2f(sc[(2 * c) * 4 + e] - m_use);
-          pf[4 + e] = exp2f(sc[(2 * c + 1) * 4 + e] - m_use);
+          pf[e] = __builtin_amdgcn_exp2f(sc[(2 * c) * 4 + e] - m_use);
+          pf[4 + e] = __builtin_amdgcn_exp2f(sc[(2 * c + 1) * 4 + e] - m_use);
         }
 #pragma unroll
         for (int e = 0; e < 8; ++e) psum += pf[e];
-        pb[c] = u32x4_t{PackBf16(pf[0], pf[1]), PackBf16(pf[2], pf[3]), PackBf16(pf[4], pf[5]), PackBf16(pf[6], pf[7])};
+        pb[c] = u32x4_t{PackRne(pf[0], pf[1]), PackRne(pf[2], pf[3]), PackRne(pf[4], pf[5]), PackRne(pf[6], pf[7])};
       }
       l_run += psum;
       // O^T += V^T P^T over this half's two 16-key steps.
@@ -1474,7 +1488,8 @@ __global__ void __launch_bounds__(512, 1)
   }
 }
 
-// Combines the pieces of a split prefill item: block (merge, token), thread = dim; the 4 query heads in turn.
+// Combines the pieces of a split prefill item: block (merge, token); thread t handles query head t / 64, dims
+// 4 (t % 64) .. +3.
 __global__ void __launch_bounds__(256)
     PrefillMergeKernel(uint16_t* __restrict__ out, float* __restrict__ lse, const PrefillMerge* __restrict__ merges,
                        const float* __restrict__ part_o, const float* __restrict__ part_ml,
@@ -1482,26 +1497,32 @@ __global__ void __launch_bounds__(256)
   const PrefillMerge mg = merges[blockIdx.x];
   const int r = blockIdx.y;
   if (r >= mg.rows) return;
-  const int d = threadIdx.x;
+  const int hq = threadIdx.x >> 6;
+  const int d = 4 * (threadIdx.x & 63);
   const uint64_t token = static_cast<uint64_t>(q_indptr[mg.seq] + mg.q0 + r);
-  for (uint32_t hq = 0; hq < kGroup; ++hq) {
-    const uint64_t row = static_cast<uint64_t>(r) * kGroup + hq;
-    float mx = -INFINITY;
-    for (int i = 0; i < mg.count; ++i) mx = fmaxf(mx, part_ml[2 * ((mg.first + i) * uint64_t{kPfRows} + row)]);
-    float l = 0.0f, acc = 0.0f;
-    if (mx != -INFINITY) {
-      for (int i = 0; i < mg.count; ++i) {
-        const uint64_t prow = (mg.first + i) * uint64_t{kPfRows} + row;
-        const float m = part_ml[2 * prow];
-        const float f = m == -INFINITY ? 0.0f : exp2f(m - mx);
-        l += part_ml[2 * prow + 1] * f;
-        acc += part_o[prow * kPD + d] * f;
-      }
+  const uint64_t row = static_cast<uint64_t>(r) * kGroup + hq;
+  float mx = -INFINITY;
+  for (int i = 0; i < mg.count; ++i) mx = fmaxf(mx, part_ml[2 * ((mg.first + i) * uint64_t{kPfRows} + row)]);
+  float l = 0.0f;
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (mx != -INFINITY) {
+    for (int i = 0; i < mg.count; ++i) {
+      const uint64_t prow = (mg.first + i) * uint64_t{kPfRows} + row;
+      const float m = part_ml[2 * prow];
+      const float f = m == -INFINITY ? 0.0f : exp2f(m - mx);
+      l += part_ml[2 * prow + 1] * f;
+      const float4 o = *reinterpret_cast<const float4*>(part_o + prow * kPD + d);
+      acc.x = fmaf(o.x, f, acc.x);
+      acc.y = fmaf(o.y, f, acc.y);
+      acc.z = fmaf(o.z, f, acc.z);
+      acc.w = fmaf(o.w, f, acc.w);
     }
-    const uint32_t head = mg.kv_head * kGroup + hq;
-    out[(token * q_heads + head) * kPD + d] = F32ToBf16(l > 0.0f ? acc / l : 0.0f);
-    if (lse != nullptr && d == 0) lse[token * q_heads + head] = l > 0.0f ? mx + log2f(l) : -INFINITY;
   }
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  const uint32_t head = mg.kv_head * kGroup + hq;
+  const u32x2_t v{PackBf16(acc.x * inv, acc.y * inv), PackBf16(acc.z * inv, acc.w * inv)};
+  *reinterpret_cast<u32x2_t*>(out + (token * q_heads + head) * kPD + d) = v;
+  if (lse != nullptr && d == 0) lse[token * q_heads + head] = l > 0.0f ? mx + log2f(l) : -INFINITY;
 }
 
 template <typename T, int D>
