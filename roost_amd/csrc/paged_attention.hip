@@ -1288,7 +1288,6 @@ __global__ void __launch_bounds__(512, 1)
   const int32_t n = q_indptr[wk.seq + 1] - qbeg;
   const int32_t r = 32 * qt + col;  // this lane's query within the item
   const bool row_ok = r < wk.rows;
-  const int32_t my_pos = static_cast<int32_t>(kv_len) - n + wk.q0 + r;  // its key position
   const int32_t last_pos = static_cast<int32_t>(kv_len) - n + wk.q0 + 32 * qt + 31;  // the wavefront's last query
   const int32_t kbeg = wk.kbeg, kend = wk.kend;
   const int ntiles = kend > kbeg ? (kend - kbeg + 63) / 64 : 0;
@@ -1317,7 +1316,7 @@ __global__ void __launch_bounds__(512, 1)
   const uint32_t row_add = kv.hnd ? kvh * ps * kPD : kvh * kPD;
   const uint64_t page_elems = static_cast<uint64_t>(ps) * kv.kv_heads * kPD;
   // This wavefront's share of the copy of tile t: rows 8w .. 8w + 7 of K and of V (two rows per instruction).
-  auto issue = [&](int t, int buf, const int32_t (&ids)[4]) {
+  auto issue = [&](int t, int buf, const int32_t (&ids)[4], int ln) {
     const int32_t kb = kbeg + 64 * t;
     const int32_t pos0 = kb + 8 * w;  // this wavefront's first row; all 8 lie in one page
     const int32_t id = ids[w >> 1];
@@ -1326,8 +1325,7 @@ __global__ void __launch_bounds__(512, 1)
     const uint16_t* kpage = kbase + pg * page_elems + row_add;
     const uint16_t* vpage = vbase + pg * page_elems + row_add;
     const uint32_t kdst = LdsAddr(tiles[buf][0]) + 8 * w * 512, vdst = LdsAddr(tiles[buf][1]) + 8 * w * 512;
-    int c = col, hh = hl;
-    asm volatile("" : "+v"(c), "+v"(hh));  // recompute the lane offsets per call instead of holding eight of them
+    const int c = ln & 31, hh = (ln >> 5) & 1;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int rr = 2 * i + hh;  // row 8w + rr of the tile
@@ -1348,30 +1346,22 @@ __global__ void __launch_bounds__(512, 1)
   float m_run = -INFINITY;
   float l_run = 0.0f;
 
-  // Lane-constant parts of the transposed V reads: in lane group g = lane / 16, lane j = lane % 16 addresses key
-  // +(j / 4) at dims +4 (j % 4), keys based at 32 half + 16 c + 4 (g >> 1) (+8 for the operand's second half), dims
-  // based at 32 dt + 16 (g & 1).
-  const int vj = lane & 15, vg = lane >> 4;
-  const int vkey = 4 * (vg >> 1) + (vj >> 2);
-  const int vdim = 16 * (vg & 1) + 4 * (vj & 3);
-  // With the swizzle, the V piece holding dims 32 dt + vdim of key vkey + 8 m sits at byte
-  // vkey * 512 + 8 m * 512 + (64 dt ^ vx) + vl: (4 (4 dt + pl)) ^ (16 * 4 e) splits into a dt part and a lane part.
-  int vrow = vkey * 512 + 16 * ((vdim >> 3) & 3) + 2 * (vdim & 7);
-  int vx = 64 * (vkey & 3);
-  int krow = col * 512;
-  int kx = 16 * (hl ^ (col & 15));
-
   int32_t ids_cur[4] = {0, 0, 0, 0}, ids_nxt[4] = {0, 0, 0, 0};
   if (ntiles > 0) {
     load_ids(0, ids_cur);
-    issue(0, 0, ids_cur);
+    issue(0, 0, ids_cur, lane);
     load_ids(min(1, ntiles - 1), ids_nxt);
   }
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
     WaitVmem();       // this wavefront's copies of tile t have landed
     __syncthreads();  // ... and everyone's; everyone is also done reading the other buffer
-    if (t + 1 < ntiles) issue(t + 1, buf ^ 1, ids_nxt);
+    // Every lane-dependent value the loop needs is re-derived here from the thread index, so that only the index
+    // stays live across the loop (the register budget at two wavefronts per SIMD holds nothing more).
+    int tx = static_cast<int>(threadIdx.x);
+    asm volatile("" : "+v"(tx));
+    const int ln = tx & 63, lc = ln & 31, lh = ln >> 5;
+    if (t + 1 < ntiles) issue(t + 1, buf ^ 1, ids_nxt, ln);
     uint32_t bad = 0;  // 16-key groups of this tile whose page id lies outside the pool
 #pragma unroll
     for (int g = 0; g < 4; ++g) bad |= good_page(ids_cur[g]) ? 0u : (1u << g);
@@ -1379,9 +1369,19 @@ __global__ void __launch_bounds__(512, 1)
     for (int g = 0; g < 4; ++g) ids_cur[g] = ids_nxt[g];
     load_ids(min(t + 2, ntiles - 1), ids_nxt);
     const int32_t kb = kbeg + 64 * t;
-    // The lane-constant operand offsets are re-derived every tile rather than the ~64 offsets built from them being
-    // kept live across the loop (the register budget at two wavefronts per SIMD does not hold them).
-    asm volatile("" : "+v"(vrow), "+v"(vx), "+v"(krow), "+v"(kx));
+    // K operand: row 32 half + lc, piece 2 ks + lh at position (2 ks + lh) ^ (lc & 15) (32 half keeps row & 15 =
+    // lc & 15); in bytes 16 ((2 ks + lh) ^ (lc & 15)) = 32 ks ^ 16 (lh ^ (lc & 15)).
+    const int krow = lc * 512, kx = 16 * (lh ^ (lc & 15));
+    // V^T operands, read transposed: in lane group g = ln / 16, lane j = ln % 16 addresses key +(j / 4) at dims
+    // +4 (j % 4), keys based at 32 half + 16 c + 4 (g >> 1) (+8 for the operand's second half), dims at
+    // 32 dt + 16 (g & 1). With the swizzle that piece sits at byte key * 512 + (64 dt ^ 64 (key & 3)) + the lane's
+    // offset inside the 64-byte group: (4 (4 dt + pl)) ^ (4 * 4 e) splits into a dt part and a lane part.
+    const int vj = ln & 15, vg = ln >> 4;
+    const int vkey = 4 * (vg >> 1) + (vj >> 2);
+    const int vdim = 16 * (vg & 1) + 4 * (vj & 3);
+    const int vrow = vkey * 512 + 16 * ((vdim >> 3) & 3) + 2 * (vdim & 7);
+    const int vx = 64 * (vkey & 3);
+    const int32_t qpos = static_cast<int32_t>(kv_len) - n + wk.q0 + 32 * qt + lc;  // this lane's query position
     const bool need_mask = kb + 64 > kend || (causal && kb + 63 > last_pos - 31) || bad != 0;
     const unsigned char* ktile = tiles[buf][0];
     const unsigned char* vtile = tiles[buf][1];
@@ -1390,26 +1390,31 @@ __global__ void __launch_bounds__(512, 1)
       f32x16_t sc;
 #pragma unroll
       for (int v = 0; v < 16; ++v) sc[v] = 0.0f;
-      // K row 32 half + col, piece 2 ks + hl at position (2 ks + hl) ^ (col & 15) (32 half keeps row & 15 = col & 15);
-      // in bytes 16 ((2 ks + hl) ^ (col & 15)) = 32 ks ^ 16 (hl ^ (col & 15)).
       const unsigned char* krow_p = ktile + 32 * half * 512 + krow;
-      u32x4_t ka = *reinterpret_cast<const u32x4_t*>(krow_p + kx);
+      constexpr int kRing = 2;  // K operands in flight ahead of the multiply that uses them
+      u32x4_t ka[kRing];
 #pragma unroll
-      for (int ks = 0; ks < 16; ++ks) {  // the operand of step ks + 1 is read while step ks multiplies
-        const u32x4_t a = ka;
-        if (ks + 1 < 16) ka = *reinterpret_cast<const u32x4_t*>(krow_p + ((32 * (ks + 1)) ^ kx));
+      for (int j = 0; j < kRing; ++j) ka[j] = *reinterpret_cast<const u32x4_t*>(krow_p + ((32 * j) ^ kx));
+#pragma unroll
+      for (int ks = 0; ks < 16; ++ks) {
+        const u32x4_t a = ka[ks % kRing];
+        if (ks + kRing < 16) ka[ks % kRing] = *reinterpret_cast<const u32x4_t*>(krow_p + ((32 * (ks + kRing)) ^ kx));
         sc = Mfma32(a, qreg[ks], sc);
+      }
+#pragma unroll
+      for (int v = 0; v < 16; ++v) sc[v] *= scale_log2;
+      if (need_mask) {  // one uniform branch around branch-free selects
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int kk = 32 * half + (v >> 2) * 8 + lh * 4 + (v & 3);  // key within the tile
+          const int32_t key = kb + kk;
+          const bool off = key >= kend || (causal && key > qpos) || ((bad >> (kk >> 4)) & 1u);
+          sc[v] = off ? -INFINITY : sc[v];
+        }
       }
       float mx = -INFINITY;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int kk = 32 * half + (v >> 2) * 8 + hl * 4 + (v & 3);  // key within the tile
-        const int32_t key = kb + kk;
-        float x = sc[v] * scale_log2;
-        if (need_mask && (key >= kend || (causal && key > my_pos) || ((bad >> (kk >> 4)) & 1u))) x = -INFINITY;
-        sc[v] = x;
-        mx = fmaxf(mx, x);
-      }
+      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sc[v]);
       mx = fmaxf(mx, ShflXor(mx, 32));
       const bool grow = mx > m_run + 8.0f;
       if (__any(grow)) {
@@ -1439,16 +1444,23 @@ __global__ void __launch_bounds__(512, 1)
       }
       l_run += psum;
       // O^T += V^T P^T over this half's two 16-key steps.
+      // V^T operands of the 16 multiplies (c, dt) in order, read kVRing ahead of use.
+      constexpr int kVRing = 2;
+      auto vread = [&](int j) {
+        const int c = j >> 3, dt = j & 7;
+        const uint32_t off = static_cast<uint32_t>((32 * half + 16 * c) * 512 + vrow) + ((64 * dt) ^ vx);
+        const u32x2_t lo = LdsTr16(vtile, off);
+        const u32x2_t hi = LdsTr16(vtile, off + 8 * 512);
+        return u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+      };
+      u32x4_t va[kVRing];
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const uint32_t kbase1 = static_cast<uint32_t>((32 * half + 16 * c) * 512 + vrow);
+      for (int j = 0; j < kVRing; ++j) va[j] = vread(j);
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-          const uint32_t off1 = kbase1 + ((64 * dt) ^ vx);
-          const u32x2_t lo = LdsTr16(vtile, off1);
-          const u32x2_t hi = LdsTr16(vtile, off1 + 8 * 512);
-          o[dt] = Mfma32(u32x4_t{lo[0], lo[1], hi[0], hi[1]}, pb[c], o[dt]);
-        }
+      for (int j = 0; j < 16; ++j) {
+        const u32x4_t av = va[j % kVRing];
+        if (j + kVRing < 16) va[j % kVRing] = vread(j + kVRing);
+        o[j & 7] = Mfma32(av, pb[j >> 3], o[j & 7]);
       }
     }
   }
