@@ -128,6 +128,18 @@ __device__ __forceinline__ void Load32(const uint16_t* src, float* dst) {
   }
 }
 
+typedef float f32x4v_t __attribute__((ext_vector_type(4)));
+
+// The recurrent step reads each state row once and writes it once, in whole 512-byte runs per wavefront: non-temporal
+// accesses keep that stream out of the caches.
+__device__ __forceinline__ float4 LoadStreamF4(const float* p) {
+  const f32x4v_t v = __builtin_nontemporal_load(reinterpret_cast<const f32x4v_t*>(p));
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void StoreStreamF4(float* p, const float4& x) {
+  __builtin_nontemporal_store(f32x4v_t{x.x, x.y, x.z, x.w}, reinterpret_cast<f32x4v_t*>(p));
+}
+
 __device__ __forceinline__ float QuadSum(float x) {
   x += __shfl_xor(x, 1, 64);
   x += __shfl_xor(x, 2, 64);
@@ -152,7 +164,7 @@ __global__ void __launch_bounds__(128) RecurrentKernel(GdnArgs a) {
   float* sp = has_slot ? a.state + (static_cast<uint64_t>(slot) * kHeads + h) * kDim * kDim : nullptr;
   if (has_slot && a.use_initial_state) {
 #pragma unroll
-    for (int i = 0; i < 32; ++i) s[i] = *reinterpret_cast<const float4*>(sp + (rq * 32 + i) * kDim + cg * 4);
+    for (int i = 0; i < 32; ++i) s[i] = LoadStreamF4(sp + (rq * 32 + i) * kDim + cg * 4);
   } else {
 #pragma unroll
     for (int i = 0; i < 32; ++i) s[i] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -217,7 +229,7 @@ __global__ void __launch_bounds__(128) RecurrentKernel(GdnArgs a) {
   }
   if (has_slot) {
 #pragma unroll
-    for (int i = 0; i < 32; ++i) *reinterpret_cast<float4*>(sp + (rq * 32 + i) * kDim + cg * 4) = s[i];
+    for (int i = 0; i < 32; ++i) StoreStreamF4(sp + (rq * 32 + i) * kDim + cg * 4, s[i]);
   }
 }
 
