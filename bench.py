@@ -102,7 +102,8 @@ def planned(session, entry, params, key):
     session.launch(entry, params, key=key)  # plans and runs once
     session.stream.synchronize()
     plan_ms = (time.perf_counter() - t0) * 1e3
-    return session._ws[(entry.variant_id, key)][3], plan_ms
+    slot = session._ws.get((entry.variant_id, key))
+    return (slot[3] if slot is not None else None), plan_ms
 
 
 def bench_decode(torch, roost_amd, session, steps, warmup):
@@ -166,13 +167,98 @@ def bench_gdn(torch, roost_amd, session, steps, warmup):
     # Config 4 follow-on: one recurrent decode step on 128 states.
     p, keep = inputs(128, [1] * 128)
     entry = session.lib.entry(roost_amd.RECURRENT_VARIANT)
-    ms = time_runs(torch, session, entry, p, None, steps, warmup)
+    ws, _ = planned(session, entry, p, "bench-gdn-recurrent")
+    ms = time_runs(torch, session, entry, p, ws, steps, warmup)
     B = 128
     bytes_ = 2 * B * H * D * D * 4 + B * (3 * H * D + H * D) * 2 + B * H * 6
     res["gdn_recurrent"] = {"config": "128 states x 1 token, 16 heads x 128", "ms": ms,
                             "hbm_gbs": bytes_ / ms / 1e6, "hbm_frac": bytes_ / ms / 1e6 / HBM_PEAK_GBS}
     del keep
     return res
+
+
+def bench_mixed(torch, roost_amd, session, steps, warmup):
+    """one worker step of a 3:1 GDN:attention layer group. 48 decode sequences (contexts
+    U(1024, 16384)) and 2 prefill chunks of 512 tokens on 4096-token prefixes share one paged KV pool and one state
+    pool. The step is CacheWrite of the 1072 new tokens, one PagedAttention call (prefill mode, as the worker issues a
+    mixed batch: tokens > batch) and three GatedDeltaRule calls on the recurrent variant (the one the worker names for
+    every length), each layer with its own state slots. Returns the step latency and the per-op breakdown."""
+    H, D = 16, 128
+    rng = np.random.default_rng(5)
+    dec = rng.integers(1024, 16385, size=48)
+    kv = np.concatenate([dec, [4096 + 512, 4096 + 512]])
+    n = np.concatenate([np.ones(48, np.int64), [512, 512]])
+    b = Paged(torch, rng, kv, n)
+    g = torch.Generator(device="cuda").manual_seed(6)
+    # Slot mapping of the new tokens (positions kv_len - n .. kv_len - 1 of each sequence), PlanRegionWriter's rule.
+    slots_h = []
+    for i in range(b.batch):
+        pages = b.kv_indices_h[b.kv_indptr_h[i]:b.kv_indptr_h[i + 1]].astype(np.int64)
+        pos = np.arange(kv[i] - n[i], kv[i])
+        slots_h.append(pages[pos // b.ps] * b.ps + pos % b.ps)
+    slot_mapping = torch.from_numpy(np.concatenate(slots_h)).cuda()
+    new_k = (torch.randn((b.tokens, b.hkv, b.d), generator=g, device="cuda") * 0.5).to(torch.bfloat16)
+    new_v = (torch.randn((b.tokens, b.hkv, b.d), generator=g, device="cuda") * 0.5).to(torch.bfloat16)
+    cw = roost_amd.cache_write_params(new_k, new_v, b.k, b.v, slot_mapping, kv_heads=b.hkv, head_dim=b.d,
+                                      page_size=b.ps)
+    att = b.params(roost_amd)
+    T, B = b.tokens, b.batch
+    fused = torch.randn((T, 3 * H * D), generator=g, device="cuda").to(torch.bfloat16)
+    gg = -torch.nn.functional.softplus(torch.randn((T, H), generator=g, device="cuda"))
+    beta = torch.sigmoid(torch.randn((T, H), generator=g, device="cuda")).to(torch.bfloat16)
+    pool = torch.randn((3 * B, H, D, D), generator=g, device="cuda") * 0.01
+    out = torch.empty((T, H, D), dtype=torch.bfloat16, device="cuda")
+    cu_h = b.q_indptr_h.copy()
+    cu = torch.from_numpy(cu_h).cuda()
+    reach = (T - 1) * 3 * H * D + H * D
+    gdn = []
+    for layer in range(3):
+        sl = torch.arange(layer * B, (layer + 1) * B, dtype=torch.int32, device="cuda")
+        gdn.append(roost_amd.gated_delta_rule_params(
+            fused, fused, fused, gg, beta, out, pool, sl, cu, batch=B, tokens=T, q_stride=3 * H * D,
+            k_stride=3 * H * D, v_stride=3 * H * D, q_len=reach, k_len=reach, v_len=reach, q_offset=0,
+            k_offset=H * D, v_offset=2 * H * D, cu_seqlens_host=cu_h))
+    e_cw = session.lib.entry(roost_amd.CACHE_WRITE_VARIANT)
+    e_att = session.lib.entry(roost_amd.ATTENTION_VARIANT)
+    e_gdn = session.lib.entry(roost_amd.RECURRENT_VARIANT)
+    ws_cw, _ = planned(session, e_cw, cw, "mixed-cw")
+    ws_att, plan_ms = planned(session, e_att, att, "mixed-att")
+    ws_gdn = []
+    for layer in range(3):
+        w, _ = planned(session, e_gdn, gdn[layer], f"mixed-gdn{layer}")
+        ws_gdn.append(w)
+
+    def step():
+        session.run(e_cw, cw, ws_cw)
+        session.run(e_att, att, ws_att)
+        for layer in range(3):
+            session.run(e_gdn, gdn[layer], ws_gdn[layer])
+
+    for _ in range(warmup):
+        step()
+    session.stream.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(session.stream)
+    for _ in range(steps):
+        step()
+    end.record(session.stream)
+    end.synchronize()
+    step_ms = start.elapsed_time(end) / steps
+    parts = {
+        "cache_write": time_runs(torch, session, e_cw, cw, ws_cw, steps, warmup),
+        "attention": time_runs(torch, session, e_att, att, ws_att, steps, warmup),
+        "gdn_layer": time_runs(torch, session, e_gdn, gdn[0], ws_gdn[0], steps, warmup),
+    }
+    # HBM floor of the step: K/V of every context token, the KV append, and per GDN layer the states read and
+    # written once plus q, k, v, g, beta and o of every token.
+    kv_bytes = int(kv.sum()) * b.hkv * b.d * 2 * 2 + 2 * T * b.hkv * b.d * 2 * 2
+    gdn_bytes = 3 * (2 * B * H * D * D * 4 + T * (4 * H * D * 2 + H * 6))
+    floor_ms = (kv_bytes + gdn_bytes) / (HBM_PEAK_GBS * 1e6)
+    return {"workload": "BASELINE config 5: 48 decode ctx U(1024, 16384) + 2 x 512-token chunks on 4096 prefixes; "
+                        "CacheWrite + PagedAttention + 3 GDN layers (recurrent variant)",
+            "step_ms": step_ms, "breakdown_ms": parts, "attention_plan_ms": plan_ms,
+            "hbm_floor_ms": floor_ms, "hbm_frac": floor_ms / step_ms, "context_tokens": int(kv.sum()),
+            "tokens": T}
 
 
 def cpu_baseline(b: Paged, sample_seqs: int):
@@ -209,6 +295,10 @@ def measured_traffic():
     return int(json.loads(f.read_text())["traffic_bytes_per_run"])
 
 
+def _rounded(d):
+    return {k: (round(v, 5) if isinstance(v, float) else _rounded(v) if isinstance(v, dict) else v) for k, v in d.items()}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -216,7 +306,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=16)
-    ap.add_argument("--only", choices=["decode", "prefill", "gdn"], default=None,
+    ap.add_argument("--only", choices=["decode", "prefill", "gdn", "mixed"], default=None,
                     help="run one workload only and print its timing (for profiler passes); no JSON line")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -233,7 +323,7 @@ def main():
     torch.cuda.set_device(0)
     session = roost_amd.OpSession(device=0)
     if args.only is not None:
-        fn = {"decode": bench_decode, "prefill": bench_prefill, "gdn": bench_gdn}[args.only]
+        fn = {"decode": bench_decode, "prefill": bench_prefill, "gdn": bench_gdn, "mixed": bench_mixed}[args.only]
         res = fn(torch, roost_amd, session, args.steps, args.warmup)
         log(f"{args.only}: {res[1] if isinstance(res, tuple) else res} ms")
         session.close()
@@ -250,6 +340,9 @@ def main():
     log("gdn (config 4) ...")
     gdn = bench_gdn(torch, roost_amd, session, args.steps, args.warmup)
     log(f"  {json.dumps(gdn)}")
+    log("mixed hybrid step (config 5) ...")
+    mixed = bench_mixed(torch, roost_amd, session, max(args.steps // 2, 3), max(args.warmup // 2, 1))
+    log(f"  {json.dumps(mixed)}")
     cpu = None
     if not args.skip_cpu:
         log("cpu baseline ...")
@@ -279,7 +372,8 @@ def main():
                     "ms": round(pre_ms, 4), "tflops": round(pre_tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                     "frac": round(pre_tflops / MFMA_BF16_PEAK_TFLOPS, 4), "flops": pb.prefill_flops(),
                     "query_tokens": pb.tokens},
-        "gdn": {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()} for k, v in gdn.items()},
+        "gdn": {k: _rounded(v) for k, v in gdn.items()},
+        "mixed_step": _rounded(mixed),
         "cpu_baseline": cpu,
     }
     session.close()

@@ -32,6 +32,9 @@ constexpr uint64_t kStateElems = uint64_t{kHeads} * kDim * kDim;
 constexpr uint64_t kMaxTokens = uint64_t{1} << 24;
 constexpr uint32_t kMaxBatch = 1u << 20;
 constexpr uint32_t kChunk = 64;
+// The recurrent variant hands a sequence of at least this many tokens to the chunk (WY) kernels: one token of the
+// token-serial recurrence costs about as much latency as a chunk step covering 64 tokens.
+constexpr uint32_t kRouteMinTokens = 16;
 constexpr uint32_t kPlanMagic = 0x50444752;  // "RGDP"
 
 uint32_t Stride(uint32_t s) { return s == 0 ? kRow : s; }
@@ -104,6 +107,8 @@ struct GdnArgs {
   float* state;
   const int32_t* slots;
   const int32_t* cu;
+  const int4* routed;  // when set: [batch] chunk-table entries; a sequence with a non-zero count is not the
+                       // recurrent kernel's
   uint64_t q_stride, k_stride, v_stride;
   uint64_t pool_slots;
   uint32_t use_initial_state;
@@ -154,6 +159,7 @@ __global__ void __launch_bounds__(128) RecurrentKernel(GdnArgs a) {
   const int32_t t0 = a.cu[b];
   const int32_t t1 = a.cu[b + 1];
   if (t1 <= t0) return;  // an empty sequence leaves its slot untouched
+  if (a.routed != nullptr && a.routed[b].y != 0) return;  // run by the chunk kernels
   const int32_t slot = a.slots[b];
   const bool has_slot = slot >= 0 && static_cast<uint64_t>(slot) < a.pool_slots;
   const int t = threadIdx.x;
@@ -260,8 +266,9 @@ bool Vec16(const RoostGatedDeltaRuleParams& p) {
          ks % 8 == 0 && vs % 4 == 0;
 }
 
-RoostStatus LaunchRecurrent(const RoostGatedDeltaRuleParams& p, hipStream_t stream) {
-  const GdnArgs a = MakeArgs(p);
+RoostStatus LaunchRecurrent(const RoostGatedDeltaRuleParams& p, hipStream_t stream, const int4* routed = nullptr) {
+  GdnArgs a = MakeArgs(p);
+  a.routed = routed;
   const dim3 grid(p.batch, kHeads);
   if (Vec16(p)) {
     hipLaunchKernelGGL(RecurrentKernel<true>, grid, dim3(128), 0, stream, a);
@@ -372,6 +379,7 @@ __global__ void __launch_bounds__(256, 4) ChunkPrepKernel(ChunkArgs ca) {
   const int4 ch = ca.chunks[blockIdx.x];
   const uint32_t h = blockIdx.y;
   const int t0 = ch.y, n = ch.z;
+  if (n <= 0) return;  // an unused entry of a table sized for the worst case
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, kq = lane >> 4;
@@ -923,15 +931,80 @@ struct ChunkLayout {
   uint32_t max_chunks;
 };
 
-ChunkLayout MakeChunkLayout(uint64_t tokens, uint64_t batch) {
+ChunkLayout MakeChunkLayoutFor(uint64_t max_chunks, uint64_t batch) {
   ChunkLayout l{};
-  l.max_chunks = static_cast<uint32_t>(tokens / kChunk + batch);
+  l.max_chunks = static_cast<uint32_t>(max_chunks);
   l.chunk_table = 0;
   l.seq_table = roost::AlignUp(16ull * l.max_chunks, 256);
   l.tables_bytes = roost::AlignUp(l.seq_table + 16ull * batch, 256);
   l.records = l.tables_bytes;
   l.total = l.records + uint64_t{l.max_chunks} * kHeads * kRecBytes;
   return l;
+}
+
+// Every sequence may be chunked (chunk variant): at most tokens / 64 + batch chunks.
+ChunkLayout MakeChunkLayout(uint64_t tokens, uint64_t batch) { return MakeChunkLayoutFor(tokens / kChunk + batch, batch); }
+
+// Only sequences of kRouteMinTokens or more are chunked (recurrent variant): sum ceil(len / 64) over them is at most
+// tokens / 64 plus their number, which is at most min(batch, tokens / kRouteMinTokens).
+ChunkLayout MakeRouteLayout(uint64_t tokens, uint64_t batch) {
+  return MakeChunkLayoutFor(tokens / kChunk + std::min<uint64_t>(batch, tokens / kRouteMinTokens), batch);
+}
+
+
+// Builds the chunk and sequence tables of the recurrent variant on the device from cu_seqlens, so that run() needs no
+// plan and no host copy: a sequence of kRouteMinTokens or more tokens gets ceil(len / 64) chunk entries and a non-zero
+// count in its sequence entry; every other sequence gets count 0 (the recurrent kernel runs it). Entries of the chunk
+// table past the last one written have 0 tokens, which the prep kernel skips. A sequence whose chunks would not fit
+// the table (only possible when cu_seqlens does not sum to the token count) stays with the recurrent kernel. One
+// workgroup walks the batch 1024 sequences at a time with a workgroup-wide prefix sum of the chunk counts.
+__global__ void __launch_bounds__(1024) RouteKernel(const int32_t* cu, uint32_t batch, uint32_t max_chunks,
+                                                    int4* chunks, int4* seqs) {
+  __shared__ uint32_t wave_sum[16];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (uint32_t i = tid; i < max_chunks; i += 1024) chunks[i] = make_int4(0, 0, 0, 0);
+  __syncthreads();  // the zero fill lands before any entry below is written over it
+  uint32_t base = 0;
+  for (uint32_t start = 0; start < batch; start += 1024) {
+    const uint32_t b = start + tid;
+    int32_t t0 = 0, t1 = 0;
+    uint32_t cnt = 0;
+    if (b < batch) {
+      t0 = cu[b];
+      t1 = cu[b + 1];
+      const int32_t len = t1 - t0;
+      cnt = len >= static_cast<int32_t>(kRouteMinTokens) ? (static_cast<uint32_t>(len) + kChunk - 1) / kChunk : 0;
+    }
+    uint32_t incl = cnt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_up(incl, o);
+      if (lane >= o) incl += y;
+    }
+    if (lane == 63) wave_sum[w] = incl;
+    __syncthreads();
+    uint32_t before = 0, total = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t x = wave_sum[i];
+      before += i < w ? x : 0;
+      total += x;
+    }
+    const uint64_t first = uint64_t{base} + before + incl - cnt;
+    if (b < batch) {
+      if (cnt != 0 && first + cnt <= max_chunks) {
+        seqs[b] = make_int4(static_cast<int32_t>(first), static_cast<int32_t>(cnt), t0, t1);
+        for (uint32_t c = 0; c < cnt; ++c) {
+          const int32_t tc = t0 + static_cast<int32_t>(c * kChunk);
+          chunks[first + c] = make_int4(static_cast<int32_t>(b), tc, min(static_cast<int32_t>(kChunk), t1 - tc), 0);
+        }
+      } else {
+        seqs[b] = make_int4(0, 0, t0, t1);
+      }
+    }
+    base = static_cast<uint32_t>(min<uint64_t>(uint64_t{base} + total, 0xFFFFFFFFull));
+    __syncthreads();  // wave_sum is rewritten by the next pass
+  }
 }
 
 RoostStatus LaunchChunk(const RoostGatedDeltaRuleParams& p, const RoostWorkspace* ws, const ChunkLayout& l,
@@ -970,14 +1043,16 @@ extern "C" ROOST_API RoostStatus roost_gdn_recurrent_workspace(RoostContext*, co
   if (p.tokens > kMaxTokens || p.batch > kMaxBatch) {
     return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRule: too many tokens or sequences for one call");
   }
-  sizes->device_bytes = 0;  // the views and the pool slots are read in place
+  // The views and the pool slots are read in place; a call that may hold a sequence of kRouteMinTokens or more
+  // tokens also gets the chunk tables and records for the sequences it hands to the chunk kernels.
+  sizes->device_bytes = p.tokens >= kRouteMinTokens ? MakeRouteLayout(p.tokens, p.batch).total : 0;
   sizes->pinned_host_bytes = 0;
   sizes->plan_bytes = 0;
   sizes->device_alignment = 256;
   return ROOST_STATUS_OK;
 }
 
-extern "C" ROOST_API RoostStatus roost_gdn_recurrent_run(RoostContext* ctx, const void* params, const RoostWorkspace*,
+extern "C" ROOST_API RoostStatus roost_gdn_recurrent_run(RoostContext* ctx, const void* params, const RoostWorkspace* ws,
                                                          void* stream) {
   using namespace roost;
   if (ctx == nullptr || params == nullptr) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRule: ctx or params is NULL");
@@ -985,7 +1060,21 @@ extern "C" ROOST_API RoostStatus roost_gdn_recurrent_run(RoostContext* ctx, cons
   return Guarded("GatedDeltaRule", [&]() -> RoostStatus {
     ROOST_TRY(Validate(p, false));
     if (p.batch == 0 || p.tokens == 0) return ROOST_STATUS_OK;
-    return LaunchRecurrent(p, Stream(stream));
+    if (p.tokens < kRouteMinTokens) return LaunchRecurrent(p, Stream(stream));
+    // Every launch size below follows from tokens and batch alone, so the call can be captured into a graph.
+    const ChunkLayout l = MakeRouteLayout(p.tokens, p.batch);
+    if (!DeviceWorkspaceOk(ws, l.total)) {
+      return Fail(ROOST_STATUS_WORKSPACE_TOO_SMALL,
+                  "GatedDeltaRule: workspace is missing or smaller than the workspace query said");
+    }
+    auto* base = static_cast<uint8_t*>(ws->device);
+    auto* chunks = reinterpret_cast<int4*>(base + l.chunk_table);
+    auto* seqs = reinterpret_cast<int4*>(base + l.seq_table);
+    hipLaunchKernelGGL(RouteKernel, dim3(1), dim3(1024), 0, Stream(stream), static_cast<const int32_t*>(p.cu_seqlens.address),
+                       p.batch, l.max_chunks, chunks, seqs);
+    ROOST_TRY(FromHip(hipGetLastError(), "GatedDeltaRule route launch"));
+    ROOST_TRY(LaunchRecurrent(p, Stream(stream), seqs));
+    return LaunchChunk(p, ws, l, l.max_chunks, Stream(stream));
   });
 }
 

@@ -183,6 +183,19 @@ def test_gdn_refusals_without_gpu(kernels):
     assert run(q) == abi.INVALID_ARGUMENT
     chunk = kernels.entry(roost_amd.CHUNK_VARIANT)
     assert chunk.run(ctx, C.addressof(p), None, None) == abi.WORKSPACE_TOO_SMALL
+    # The recurrent variant asks for no workspace while no sequence can reach 16 tokens, and for the chunk tables
+    # and records once one can; without them such a call is refused before any launch.
+    sizes = abi.new(abi.WorkspaceSizes)
+    assert rec.workspace(ctx, C.addressof(p), C.addressof(sizes)) == abi.OK and sizes.device_bytes == 0
+    long = abi.GatedDeltaRuleParams.from_buffer_copy(p)
+    long.tokens = 40
+    for name in ("q", "k", "v", "output"):
+        setattr(long, name, _fake(40 * 2048, abi.DTYPE_BF16))
+    long.g, long.beta = _fake(40 * 16, abi.DTYPE_F32), _fake(40 * 16, abi.DTYPE_BF16)
+    assert rec.workspace(ctx, C.addressof(long), C.addressof(sizes)) == abi.OK
+    # 40 tokens in one sequence: at most 40 // 64 + min(1, 40 // 16) = 1 chunk of 16 heads x 42240-byte records.
+    assert sizes.device_bytes == 256 + 256 + 16 * 42240 and sizes.pinned_host_bytes == 0 and sizes.plan_bytes == 0
+    assert run(long) == abi.WORKSPACE_TOO_SMALL
     kernels.destroy_context(ctx)
 
 

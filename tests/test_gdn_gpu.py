@@ -64,6 +64,9 @@ CASES = [
     ("one of 3 no init", [3], True, False, 0.2, 23),
     ("decode with empty [1,0,1]", [1, 0, 1], True, True, 0.2, 24),
     ("32 x 1 serving decode", [1] * 32, True, True, 0.2, 26),
+    # A mixed worker step: the recurrent variant hands sequences of 16 tokens or more to the chunk kernels.
+    ("hybrid step [1,15,16,1,600,0,64,2]", [1, 15, 16, 1, 600, 0, 64, 2], True, True, 0.2, 27),
+    ("hybrid step [17,1,1,1] no init", [17, 1, 1, 1], False, False, 0.2, 28),
 ]
 
 
@@ -181,6 +184,9 @@ def test_rejections(session):
     p = dev.params()
     p.state.length = HEADS * DIM * DIM + 5
     assert status(rec, p) == abi.INVALID_ARGUMENT
+    # A call that may hold a sequence of 16 tokens or more needs the recurrent variant's workspace.
+    long_dev = DevGdn(cases.make_gdn(rng, [20, 1], 4, slots=[0, 2]))
+    assert status(rec, long_dev.params()) == abi.WORKSPACE_TOO_SMALL
     # Chunk variant: run() without plan() -> NOT_PLANNED; a short device workspace -> WORKSPACE_TOO_SMALL.
     import ctypes as C
 
@@ -198,3 +204,40 @@ def test_rejections(session):
     ws.device_bytes = sizes.device_bytes - 256
     assert status(chunk, good, ws) == abi.WORKSPACE_TOO_SMALL
     torch.cuda.synchronize()
+
+
+def test_recurrent_variant_graph_replays():
+    """GRAPH_CAPTURABLE: a mixed call (chunk-routed and token-serial sequences) captured into a graph and replayed
+    three times, with eager work between the replays, gives the eager result bit for bit every time."""
+    import torch
+
+    rng = np.random.default_rng(29)
+    d = cases.make_gdn(rng, [1, 40, 1, 130, 3], 8, slots=[0, 2, 4, 6, 7])
+    stream = torch.cuda.Stream()
+    session = roost_amd.OpSession(stream=stream)
+    try:
+        dev = DevGdn(d)
+        p = dev.params()
+        entry = session.lib.entry(roost_amd.RECURRENT_VARIANT)
+        pool0 = dev.pool.clone()
+        with torch.cuda.stream(stream):
+            session.launch(entry, p, key="graph")  # allocates the workspace outside the capture
+        ws = session._ws[(entry.variant_id, "graph")][3]
+        stream.synchronize()
+        want_o, want_pool = dev.out.clone(), dev.pool.clone()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            session.run(entry, p, ws)
+        for replay in range(3):
+            with torch.cuda.stream(stream):
+                dev.pool.copy_(pool0)
+                dev.out.fill_(float("nan"))
+            graph.replay()
+            stream.synchronize()
+            assert torch.equal(dev.out.view(torch.int16), want_o.view(torch.int16)), f"replay {replay} output"
+            assert torch.equal(dev.pool, want_pool), f"replay {replay} state"
+        want_o_np, want_pool_np = cases.oracle_gdn(d)
+        cases.assert_close(cases.bf16_values(from_dev(dev.out, True)[: d.tokens]), cases.bf16_values(want_o_np),
+                           what="graph output")
+    finally:
+        session.close()
