@@ -107,8 +107,7 @@ struct GdnArgs {
   float* state;
   const int32_t* slots;
   const int32_t* cu;
-  const int4* routed;  // when set: [batch] chunk-table entries; a sequence with a non-zero count is not the
-                       // recurrent kernel's
+  int32_t route_min;   // > 0: sequences of this many tokens or more belong to the chunk kernels
   uint64_t q_stride, k_stride, v_stride;
   uint64_t pool_slots;
   uint32_t use_initial_state;
@@ -159,7 +158,7 @@ __global__ void __launch_bounds__(128) RecurrentKernel(GdnArgs a) {
   const int32_t t0 = a.cu[b];
   const int32_t t1 = a.cu[b + 1];
   if (t1 <= t0) return;  // an empty sequence leaves its slot untouched
-  if (a.routed != nullptr && a.routed[b].y != 0) return;  // run by the chunk kernels
+  if (a.route_min > 0 && t1 - t0 >= a.route_min) return;  // run by the chunk kernels
   const int32_t slot = a.slots[b];
   const bool has_slot = slot >= 0 && static_cast<uint64_t>(slot) < a.pool_slots;
   const int t = threadIdx.x;
@@ -266,9 +265,9 @@ bool Vec16(const RoostGatedDeltaRuleParams& p) {
          ks % 8 == 0 && vs % 4 == 0;
 }
 
-RoostStatus LaunchRecurrent(const RoostGatedDeltaRuleParams& p, hipStream_t stream, const int4* routed = nullptr) {
+RoostStatus LaunchRecurrent(const RoostGatedDeltaRuleParams& p, hipStream_t stream, int32_t route_min = 0) {
   GdnArgs a = MakeArgs(p);
-  a.routed = routed;
+  a.route_min = route_min;
   const dim3 grid(p.batch, kHeads);
   if (Vec16(p)) {
     hipLaunchKernelGGL(RecurrentKernel<true>, grid, dim3(128), 0, stream, a);
@@ -955,8 +954,9 @@ ChunkLayout MakeRouteLayout(uint64_t tokens, uint64_t batch) {
 // Builds the chunk and sequence tables of the recurrent variant on the device from cu_seqlens, so that run() needs no
 // plan and no host copy: a sequence of kRouteMinTokens or more tokens gets ceil(len / 64) chunk entries and a non-zero
 // count in its sequence entry; every other sequence gets count 0 (the recurrent kernel runs it). Entries of the chunk
-// table past the last one written have 0 tokens, which the prep kernel skips. A sequence whose chunks would not fit
-// the table (only possible when cu_seqlens does not sum to the token count) stays with the recurrent kernel. One
+// table past the last one written have 0 tokens, which the prep kernel skips. The table holds every chunk whenever
+// cu_seqlens ends at the call's token count; otherwise the sequences whose chunks do not fit get count 0 and no
+// output (device tables are not range-checked, as everywhere in this ABI), and nothing is written out of bounds. One
 // workgroup walks the batch 1024 sequences at a time with a workgroup-wide prefix sum of the chunk counts.
 __global__ void __launch_bounds__(1024) RouteKernel(const int32_t* cu, uint32_t batch, uint32_t max_chunks,
                                                     int4* chunks, int4* seqs) {
@@ -1070,11 +1070,15 @@ extern "C" ROOST_API RoostStatus roost_gdn_recurrent_run(RoostContext* ctx, cons
     auto* base = static_cast<uint8_t*>(ws->device);
     auto* chunks = reinterpret_cast<int4*>(base + l.chunk_table);
     auto* seqs = reinterpret_cast<int4*>(base + l.seq_table);
-    hipLaunchKernelGGL(RouteKernel, dim3(1), dim3(1024), 0, Stream(stream), static_cast<const int32_t*>(p.cu_seqlens.address),
+    // The long sequences on route -> prep -> scan, the short ones on the recurrent kernel, in that order on the
+    // caller's stream. (Running the two on two streams was slower: the short kernels lose more to sharing the chip
+    // than the overlap saves.) Two sequences of one call sharing a state slot leave the recurrent one's state.
+    hipStream_t s = Stream(stream);
+    hipLaunchKernelGGL(RouteKernel, dim3(1), dim3(1024), 0, s, static_cast<const int32_t*>(p.cu_seqlens.address),
                        p.batch, l.max_chunks, chunks, seqs);
     ROOST_TRY(FromHip(hipGetLastError(), "GatedDeltaRule route launch"));
-    ROOST_TRY(LaunchRecurrent(p, Stream(stream), seqs));
-    return LaunchChunk(p, ws, l, l.max_chunks, Stream(stream));
+    ROOST_TRY(LaunchChunk(p, ws, l, l.max_chunks, s));
+    return LaunchRecurrent(p, s, static_cast<int32_t>(kRouteMinTokens));
   });
 }
 

@@ -56,7 +56,7 @@ constexpr uint32_t kPrefillTileQ = 32;          // query tokens per workgroup of
 constexpr uint32_t kPrefillTileK = 64;          // keys per LDS tile
 constexpr uint32_t kPfTokens = 64;              // query tokens per workgroup of the prefill for page sizes % 16 == 0
 constexpr uint32_t kPfRows = kPfTokens * kGroup;  // query rows (token, head) of one such workgroup
-constexpr uint32_t kPfMinSplitTiles = 16;       // a split piece covers at least this many 64-key tiles
+constexpr uint32_t kPfMinSplitTiles = 8;        // a split piece covers at least this many 64-key tiles
 constexpr uint32_t kAlign = 256;
 constexpr uint32_t kPlanMagic = 0x41504752;     // "RGPA"
 constexpr float kLog2e = 1.4426950408889634f;
@@ -117,6 +117,9 @@ struct PlanRecord {
   uint64_t int_bytes;    // [work items | seq splits]
   uint64_t float_offset; // partials start here
   uint64_t float_bytes;
+  // Single-token sequences of a prefill call run as decode: their pieces, ranges, merges and partials.
+  uint64_t dec_items, dec_ranges, dec_merges, dec_splits;
+  uint64_t dec_item_offset, dec_range_offset, dec_merge_offset, dec_float_offset;
 };
 
 struct Layout {
@@ -131,6 +134,9 @@ struct Layout {
   uint64_t float_offset = 0;
   uint64_t float_bytes = 0;
   uint64_t total = 0;
+  // Decode region (decode calls: the whole plan; prefill calls: the single-token sequences).
+  uint64_t dec_items = 0, dec_ranges = 0, dec_merges = 0, dec_splits = 0;
+  uint64_t dec_item_offset = 0, dec_range_offset = 0, dec_merge_offset = 0, dec_float_offset = 0;
 };
 
 // ---- Validation (reference: kernels/src/paged_attention.cu:78-130) ------------------------------------------------
@@ -256,62 +262,108 @@ uint32_t KvLenHost(const RoostPagedAttentionParams& p, uint32_t b) {
 // KV heads one decode workgroup serves: 4, 2 or 1, whichever divides kv_heads first.
 uint32_t HeadsPerWorkgroup(uint32_t kv_heads) { return kv_heads % 4 == 0 ? 4 : (kv_heads % 2 == 0 ? 2 : 1); }
 
-Layout PlanDecode(const RoostPagedAttentionParams& p, uint32_t cus, unsigned char* host) {
-  std::vector<uint64_t> groups(p.batch);
-  uint64_t total = 0;
+struct DecodePlan {
+  std::vector<DecodeWork> items;
+  std::vector<int32_t> range_ptr;  // ranges + 1 entries; empty when no sequence is planned
+  std::vector<DecodeMerge> merges;
+  int32_t slots = 0;
+  uint64_t ranges() const { return range_ptr.empty() ? 0 : range_ptr.size() - 1; }
+};
+
+// Plans the sequences b with take(b) (all of them in a decode call, the single-token ones in a prefill call).
+template <typename Take>
+DecodePlan BuildDecode(const RoostPagedAttentionParams& p, uint32_t cus, Take take) {
+  DecodePlan d;
+  std::vector<uint64_t> groups(p.batch, 0);
+  uint64_t total = 0, planned = 0;
   for (uint32_t b = 0; b < p.batch; ++b) {
+    if (!take(b)) continue;
     groups[b] = roost::CeilDiv(KvLenHost(p, b), 16);
     total += groups[b];
+    ++planned;
   }
+  if (planned == 0) return d;
   const uint64_t slots_wanted = std::max<uint64_t>(
       1, static_cast<uint64_t>(cus) * kDecodeWgsPerCu / (p.kv_heads / HeadsPerWorkgroup(p.kv_heads)));
   const uint64_t ranges = std::max<uint64_t>(1, std::min<uint64_t>(slots_wanted, total));
   uint64_t per_range = std::max<uint64_t>(1, roost::CeilDiv(total, ranges));
   // A sequence spans at most ceil(groups / per_range) + 1 pieces; keep that within what the merge kernel combines.
-  const uint64_t longest = groups.empty() ? 0 : *std::max_element(groups.begin(), groups.end());
+  const uint64_t longest = *std::max_element(groups.begin(), groups.end());
   per_range = std::max<uint64_t>(per_range, roost::CeilDiv(longest, kMaxMergeSplits - 2));
-  // First pass: count pieces, merges and slots; second pass (host != NULL): write them.
-  std::vector<DecodeWork> items;
-  std::vector<int32_t> range_ptr;
-  std::vector<DecodeMerge> merges;
-  items.reserve(p.batch + ranges * 2);
-  range_ptr.reserve(ranges + 1);
-  range_ptr.push_back(0);
+  d.items.reserve(planned + ranges * 2);
+  d.range_ptr.reserve(ranges + 1);
+  d.range_ptr.push_back(0);
   uint64_t room = per_range;  // groups left in the current range
-  int32_t slot = 0;
   for (uint32_t b = 0; b < p.batch; ++b) {
+    if (!take(b)) continue;
     const uint32_t kv = KvLenHost(p, b);
     if (groups[b] == 0) {
-      items.push_back(DecodeWork{static_cast<int32_t>(b), 0, 0, -1});
+      d.items.push_back(DecodeWork{static_cast<int32_t>(b), 0, 0, -1});
       continue;
     }
-    const size_t first_item = items.size();
+    const size_t first_item = d.items.size();
     uint64_t g = 0;
     while (g < groups[b]) {
       if (room == 0) {
-        range_ptr.push_back(static_cast<int32_t>(items.size()));
+        d.range_ptr.push_back(static_cast<int32_t>(d.items.size()));
         room = per_range;
       }
-      const uint64_t take = std::min(room, groups[b] - g);
-      items.push_back(DecodeWork{static_cast<int32_t>(b), static_cast<int32_t>(g * 16),
-                                 static_cast<int32_t>(std::min<uint64_t>((g + take) * 16, kv)), -1});
-      g += take;
-      room -= take;
+      const uint64_t n = std::min(room, groups[b] - g);
+      d.items.push_back(DecodeWork{static_cast<int32_t>(b), static_cast<int32_t>(g * 16),
+                                   static_cast<int32_t>(std::min<uint64_t>((g + n) * 16, kv)), -1});
+      g += n;
+      room -= n;
     }
-    const size_t pieces = items.size() - first_item;
+    const size_t pieces = d.items.size() - first_item;
     if (pieces > 1) {
-      merges.push_back(DecodeMerge{static_cast<int32_t>(b), slot, static_cast<int32_t>(pieces), 0});
-      for (size_t i = first_item; i < items.size(); ++i) items[i].slot = slot++;
+      d.merges.push_back(DecodeMerge{static_cast<int32_t>(b), d.slots, static_cast<int32_t>(pieces), 0});
+      for (size_t i = first_item; i < d.items.size(); ++i) d.items[i].slot = d.slots++;
     }
   }
-  range_ptr.push_back(static_cast<int32_t>(items.size()));
-  Layout l = MakeLayout(items.size(), range_ptr.size() - 1, merges.size(), static_cast<uint64_t>(slot), p.q_heads,
-                        p.head_dim, ROOST_ATTENTION_DECODE);
+  d.range_ptr.push_back(static_cast<int32_t>(d.items.size()));
+  return d;
+}
+
+// Places a decode plan at the end of the int region [0, l.int_bytes) and its partials at the end of the float region
+// (which must not be laid out yet), then writes it to host when given.
+void AppendDecode(const RoostPagedAttentionParams& p, const DecodePlan& d, Layout& l, unsigned char* host) {
+  l.dec_items = d.items.size();
+  l.dec_ranges = d.ranges();
+  l.dec_merges = d.merges.size();
+  l.dec_splits = static_cast<uint64_t>(d.slots);
+  l.dec_item_offset = roost::AlignUp(l.int_bytes, 16);
+  l.dec_range_offset = roost::AlignUp(l.dec_item_offset + l.dec_items * sizeof(DecodeWork), 16);
+  l.dec_merge_offset = roost::AlignUp(l.dec_range_offset + d.range_ptr.size() * sizeof(int32_t), 16);
+  l.int_bytes = l.dec_merge_offset + l.dec_merges * sizeof(DecodeMerge);
   if (host != nullptr) {
-    std::memcpy(host, items.data(), items.size() * sizeof(DecodeWork));
-    std::memcpy(host + l.range_offset, range_ptr.data(), range_ptr.size() * sizeof(int32_t));
-    std::memcpy(host + l.merge_offset, merges.data(), merges.size() * sizeof(DecodeMerge));
+    std::memcpy(host + l.dec_item_offset, d.items.data(), d.items.size() * sizeof(DecodeWork));
+    std::memcpy(host + l.dec_range_offset, d.range_ptr.data(), d.range_ptr.size() * sizeof(int32_t));
+    std::memcpy(host + l.dec_merge_offset, d.merges.data(), d.merges.size() * sizeof(DecodeMerge));
   }
+  (void)p;
+}
+
+// Lays out the float region after the int region: the prefill partials (prefill_floats bytes), then the decode ones.
+void PlaceFloats(const RoostPagedAttentionParams& p, uint64_t prefill_floats, Layout& l) {
+  l.float_offset = roost::AlignUp(l.int_bytes, kAlign);
+  l.dec_float_offset = l.float_offset + roost::AlignUp(prefill_floats, kAlign);
+  l.float_bytes = (l.dec_float_offset - l.float_offset) +
+                  l.dec_splits * p.q_heads * (static_cast<uint64_t>(p.head_dim) + 2) * sizeof(float);
+  l.total = l.float_offset + l.float_bytes;
+}
+
+Layout PlanDecode(const RoostPagedAttentionParams& p, uint32_t cus, unsigned char* host) {
+  const DecodePlan d = BuildDecode(p, cus, [](uint32_t) { return true; });
+  Layout l;
+  AppendDecode(p, d, l, host);
+  PlaceFloats(p, 0, l);
+  // The decode call's record fields name the same region.
+  l.work_items = l.dec_items;
+  l.ranges = l.dec_ranges;
+  l.merges = l.dec_merges;
+  l.splits = l.dec_splits;
+  l.range_offset = l.dec_range_offset;
+  l.merge_offset = l.dec_merge_offset;
   return l;
 }
 
@@ -333,7 +385,11 @@ Layout PlanPrefill(const RoostPagedAttentionParams& p, uint32_t cus, unsigned ch
   };
   std::vector<Item> items;
   int64_t total_tiles = 0;
+  // A sequence with one query token (a decode row of a mixed step) sees every key whether causal or not: the decode
+  // kernel streams it at HBM speed instead of a 64-row MFMA tile holding one row.
+  auto single = [&](uint32_t b) { return p.q_indptr_host[b + 1] - p.q_indptr_host[b] == 1; };
   for (uint32_t b = 0; b < p.batch; ++b) {
+    if (single(b)) continue;
     const int64_t n = p.q_indptr_host[b + 1] - p.q_indptr_host[b];
     const int64_t kv = KvLenHost(p, b);
     for (int64_t q0 = 0; q0 < n; q0 += tile_q) {
@@ -381,6 +437,9 @@ Layout PlanPrefill(const RoostPagedAttentionParams& p, uint32_t cus, unsigned ch
     for (size_t i = 0; i < items.size(); ++i) w[i] = items[i].w;
     std::memcpy(host + l.merge_offset, merges.data(), merges.size() * sizeof(PrefillMerge));
   }
+  const uint64_t prefill_floats = l.float_bytes;
+  AppendDecode(p, BuildDecode(p, cus, single), l, host);
+  PlaceFloats(p, prefill_floats, l);
   return l;
 }
 
@@ -747,6 +806,7 @@ __global__ void __launch_bounds__(256, ROOST_DECODE_WGS_PER_CU) DecodeKernel(con
                                                     const int32_t* __restrict__ range_ptr,
 
                                                     float* __restrict__ part_o, float* __restrict__ part_ml,
+                                                    const int32_t* __restrict__ q_rows,
                                                     uint32_t q_heads, uint32_t heads_per_wg, float scale_log2) {
   using C = DecodeCfg<T, D>;
   constexpr int kVec = C::kVec, kLpr = C::kLpr, kTpi = C::kTpi, kNi = C::kNi;
@@ -778,6 +838,8 @@ __global__ void __launch_bounds__(256, ROOST_DECODE_WGS_PER_CU) DecodeKernel(con
   const DecodeWork wk = work[it];
   int32_t p0 = 0;
   const uint32_t kv_len = SeqKvLen(kv, wk.seq, &p0);
+  // The sequence's query token: its index in a decode call, q_indptr[seq] for a single-token sequence of a prefill call.
+  const uint64_t tok = q_rows != nullptr ? static_cast<uint64_t>(q_rows[wk.seq]) : static_cast<uint64_t>(wk.seq);
   const uint32_t t_begin = static_cast<uint32_t>(wk.token_begin);
   const uint32_t t_end = min(kv_len, static_cast<uint32_t>(wk.token_end));
 
@@ -786,14 +848,14 @@ __global__ void __launch_bounds__(256, ROOST_DECODE_WGS_PER_CU) DecodeKernel(con
   u32x4_t qb[kMfma ? D / 32 : 1];  // MFMA path (bf16): B operand of q.k
   if constexpr (kMfma) {
     const int col = lane & 15;
-    const T* qrow = q + (static_cast<uint64_t>(wk.seq) * q_heads + kvh * kGroup + (col & 3)) * D + (lane >> 4) * 8;
+    const T* qrow = q + (tok * q_heads + kvh * kGroup + (col & 3)) * D + (lane >> 4) * 8;
 #pragma unroll
     for (int kc = 0; kc < D / 32; ++kc) {
       const u32x4_t v = *reinterpret_cast<const u32x4_t*>(qrow + kc * 32);
       qb[kc] = col < (int)kGroup ? v : u32x4_t{0, 0, 0, 0};
     }
   } else {
-    const T* qrow = q + (static_cast<uint64_t>(wk.seq) * q_heads + kvh * kGroup) * D + r * kVec;
+    const T* qrow = q + (tok * q_heads + kvh * kGroup) * D + r * kVec;
 #pragma unroll
     for (int h = 0; h < (int)kGroup; ++h) {
       const uint4 v = *reinterpret_cast<const uint4*>(qrow + (h ^ (r & 3)) * D);
@@ -940,7 +1002,7 @@ __global__ void __launch_bounds__(256, ROOST_DECODE_WGS_PER_CU) DecodeKernel(con
     }
     const uint32_t qh = ((blockIdx.x % hblocks) * heads_per_wg + hk) * kGroup + h;
     if (split < 0) {
-      const uint64_t row = static_cast<uint64_t>(wk.seq) * q_heads + qh;
+      const uint64_t row = tok * q_heads + qh;
       out[row * D + d] = Vec<T>::Narrow(L > 0.0f ? o / L : 0.0f);
       if (lse != nullptr && d == 0) lse[row] = L > 0.0f ? M + log2f(L) : -INFINITY;
     } else {
@@ -963,10 +1025,12 @@ template <typename T, int D>
 __global__ void __launch_bounds__(D) DecodeMergeKernel(T* __restrict__ out, float* __restrict__ lse,
                                                        const DecodeMerge* __restrict__ merges,
                                                        const float* __restrict__ part_o,
-                                                       const float* __restrict__ part_ml, uint32_t q_heads) {
+                                                       const float* __restrict__ part_ml,
+                                                       const int32_t* __restrict__ q_rows, uint32_t q_heads) {
   __shared__ float f_lds[kMaxMergeSplits];
   __shared__ float inv_lds;
   const DecodeMerge mg = merges[blockIdx.x / q_heads];
+  const uint64_t tok = q_rows != nullptr ? static_cast<uint64_t>(q_rows[mg.seq]) : static_cast<uint64_t>(mg.seq);
   const uint32_t qh = blockIdx.x % q_heads;
   const int n = min(mg.count, static_cast<int32_t>(kMaxMergeSplits));
   const uint64_t base = static_cast<uint64_t>(mg.first) * q_heads + qh;  // partial row of piece c: base + c * q_heads
@@ -986,7 +1050,7 @@ __global__ void __launch_bounds__(D) DecodeMergeKernel(T* __restrict__ out, floa
     for (int mk = 32; mk >= 1; mk >>= 1) L += __shfl_xor(L, mk, 64);
     if (lane == 0) {
       inv_lds = L > 0.0f ? 1.0f / L : 0.0f;
-      if (lse != nullptr) lse[static_cast<uint64_t>(mg.seq) * q_heads + qh] = L > 0.0f ? M + log2f(L) : -INFINITY;
+      if (lse != nullptr) lse[tok * q_heads + qh] = L > 0.0f ? M + log2f(L) : -INFINITY;
     }
   }
   __syncthreads();
@@ -1002,7 +1066,7 @@ __global__ void __launch_bounds__(D) DecodeMergeKernel(T* __restrict__ out, floa
     o3 = fmaf(po[(c + 3) * step], f_lds[c + 3], o3);
   }
   for (; c < n; ++c) o0 = fmaf(po[c * step], f_lds[c], o0);
-  out[(static_cast<uint64_t>(mg.seq) * q_heads + qh) * D + d] = Vec<T>::Narrow(((o0 + o1) + (o2 + o3)) * inv_lds);
+  out[(tok * q_heads + qh) * D + d] = Vec<T>::Narrow(((o0 + o1) + (o2 + o3)) * inv_lds);
 }
 
 // ---- Prefill kernel (bf16, head_dim 256, MFMA) -----------------------------------------------------------------------
@@ -1550,27 +1614,59 @@ __global__ void __launch_bounds__(256)
 template <typename T, int D>
 RoostStatus LaunchDecode(const RoostPagedAttentionParams& p, const PlanRecord& rec, unsigned char* dev, const KvView& kv,
                          float scale_log2, hipStream_t stream) {
-  const auto* items = reinterpret_cast<const DecodeWork*>(dev);
-  const auto* range_ptr = reinterpret_cast<const int32_t*>(dev + rec.range_offset);
-  const auto* merges = reinterpret_cast<const DecodeMerge*>(dev + rec.merge_offset);
-  auto* part_o = reinterpret_cast<float*>(dev + rec.float_offset);
-  auto* part_ml = part_o + rec.splits * p.q_heads * D;
+  if (rec.dec_ranges == 0) return ROOST_STATUS_OK;
+  const auto* items = reinterpret_cast<const DecodeWork*>(dev + rec.dec_item_offset);
+  const auto* range_ptr = reinterpret_cast<const int32_t*>(dev + rec.dec_range_offset);
+  const auto* merges = reinterpret_cast<const DecodeMerge*>(dev + rec.dec_merge_offset);
+  auto* part_o = reinterpret_cast<float*>(dev + rec.dec_float_offset);
+  auto* part_ml = part_o + rec.dec_splits * p.q_heads * D;
+  // In a prefill call the decode pieces are its single-token sequences, whose query rows are q_indptr[seq].
+  const auto* q_rows =
+      p.mode == ROOST_ATTENTION_PREFILL ? static_cast<const int32_t*>(p.q_indptr.address) : nullptr;
   auto* out = static_cast<T*>(p.output.address);
   auto* lse = static_cast<float*>(p.lse.address);
   const uint32_t hpw = HeadsPerWorkgroup(p.kv_heads);
-  const dim3 grid(static_cast<uint32_t>(rec.ranges * (p.kv_heads / hpw)));
+  const dim3 grid(static_cast<uint32_t>(rec.dec_ranges * (p.kv_heads / hpw)));
   if (p.page_size % 16 == 0) {
     hipLaunchKernelGGL((DecodeKernel<T, D, true>), grid, dim3(256), 0, stream, static_cast<const T*>(p.q.address), out,
-                       lse, kv, kv.kv_indices, items, range_ptr, part_o, part_ml, p.q_heads, hpw, scale_log2);
+                       lse, kv, kv.kv_indices, items, range_ptr, part_o, part_ml, q_rows, p.q_heads, hpw, scale_log2);
   } else {
     hipLaunchKernelGGL((DecodeKernel<T, D, false>), grid, dim3(256), 0, stream, static_cast<const T*>(p.q.address), out,
-                       lse, kv, kv.kv_indices, items, range_ptr, part_o, part_ml, p.q_heads, hpw, scale_log2);
+                       lse, kv, kv.kv_indices, items, range_ptr, part_o, part_ml, q_rows, p.q_heads, hpw, scale_log2);
   }
   ROOST_TRY(roost::FromHip(hipGetLastError(), "PagedAttention decode launch"));
-  if (rec.merges == 0) return ROOST_STATUS_OK;
-  hipLaunchKernelGGL((DecodeMergeKernel<T, D>), dim3(static_cast<uint32_t>(rec.merges * p.q_heads)), dim3(D), 0,
-                     stream, out, lse, merges, part_o, part_ml, p.q_heads);
+  if (rec.dec_merges == 0) return ROOST_STATUS_OK;
+  hipLaunchKernelGGL((DecodeMergeKernel<T, D>), dim3(static_cast<uint32_t>(rec.dec_merges * p.q_heads)), dim3(D), 0,
+                     stream, out, lse, merges, part_o, part_ml, q_rows, p.q_heads);
   return roost::FromHip(hipGetLastError(), "PagedAttention merge launch");
+}
+
+RoostStatus LaunchPrefill(const RoostPagedAttentionParams& p, const PlanRecord& rec, unsigned char* dev, const KvView& kv,
+                          float scale_log2, hipStream_t stream) {
+  using roost::FromHip;
+  if (rec.work_items == 0) return ROOST_STATUS_OK;
+  const auto* items = reinterpret_cast<const PrefillWork*>(dev);
+  const auto* q_indptr = static_cast<const int32_t*>(p.q_indptr.address);
+  auto* outp = static_cast<uint16_t*>(p.output.address);
+  auto* lsep = static_cast<float*>(p.lse.address);
+  if (PrefillFastPath(p)) {
+    auto* part_o = reinterpret_cast<float*>(dev + rec.float_offset);
+    auto* part_ml = part_o + rec.splits * kPfRows * kPD;
+    hipLaunchKernelGGL(PrefillTileKernel, dim3(static_cast<uint32_t>(rec.work_items)), dim3(512), 0, stream,
+                       static_cast<const uint16_t*>(p.q.address), outp, lsep, kv, kv.kv_indices, q_indptr, items,
+                       part_o, part_ml, p.q_heads, p.causal, static_cast<uint32_t>(__builtin_ctz(p.page_size)),
+                       scale_log2);
+    ROOST_TRY(FromHip(hipGetLastError(), "PagedAttention prefill launch"));
+    if (rec.merges == 0) return ROOST_STATUS_OK;
+    hipLaunchKernelGGL(PrefillMergeKernel, dim3(static_cast<uint32_t>(rec.merges), kPfTokens), dim3(kPD), 0, stream, outp,
+                       lsep, reinterpret_cast<const PrefillMerge*>(dev + rec.merge_offset), part_o, part_ml, q_indptr,
+                       p.q_heads);
+    return FromHip(hipGetLastError(), "PagedAttention prefill merge launch");
+  }
+  hipLaunchKernelGGL(PrefillKernel, dim3(static_cast<uint32_t>(rec.work_items)), dim3(256), 0, stream,
+                     static_cast<const uint16_t*>(p.q.address), outp, lsep, kv, q_indptr, items, p.q_heads, p.causal,
+                     scale_log2);
+  return FromHip(hipGetLastError(), "PagedAttention prefill launch");
 }
 
 }  // namespace
@@ -1636,6 +1732,14 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_plan(RoostContext* ctx, c
     rec.int_bytes = l.int_bytes;
     rec.float_offset = l.float_offset;
     rec.float_bytes = l.float_bytes;
+    rec.dec_items = l.dec_items;
+    rec.dec_ranges = l.dec_ranges;
+    rec.dec_merges = l.dec_merges;
+    rec.dec_splits = l.dec_splits;
+    rec.dec_item_offset = l.dec_item_offset;
+    rec.dec_range_offset = l.dec_range_offset;
+    rec.dec_merge_offset = l.dec_merge_offset;
+    rec.dec_float_offset = l.dec_float_offset;
     std::memcpy(ws->plan, &rec, sizeof(rec));
     return ROOST_STATUS_OK;
   });
@@ -1689,28 +1793,10 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_run(RoostContext*, const 
                              : LaunchDecode<float, 256>(p, rec, dev, kv, scale_log2, s);
       }
     }
-    if (rec.work_items == 0) return ROOST_STATUS_OK;
-    const auto* items = reinterpret_cast<const PrefillWork*>(dev);
-    const auto* q_indptr = static_cast<const int32_t*>(p.q_indptr.address);
-    auto* outp = static_cast<uint16_t*>(p.output.address);
-    auto* lsep = static_cast<float*>(p.lse.address);
-    if (PrefillFastPath(p)) {
-      auto* part_o = reinterpret_cast<float*>(dev + rec.float_offset);
-      auto* part_ml = part_o + rec.splits * kPfRows * kPD;
-      hipLaunchKernelGGL(PrefillTileKernel, dim3(static_cast<uint32_t>(rec.work_items)), dim3(512), 0, s,
-                         static_cast<const uint16_t*>(p.q.address), outp, lsep, kv, kv.kv_indices, q_indptr, items,
-                         part_o, part_ml, p.q_heads, p.causal, static_cast<uint32_t>(__builtin_ctz(p.page_size)),
-                         scale_log2);
-      ROOST_TRY(FromHip(hipGetLastError(), "PagedAttention prefill launch"));
-      if (rec.merges == 0) return ROOST_STATUS_OK;
-      hipLaunchKernelGGL(PrefillMergeKernel, dim3(static_cast<uint32_t>(rec.merges), kPfTokens), dim3(kPD), 0, s, outp,
-                         lsep, reinterpret_cast<const PrefillMerge*>(dev + rec.merge_offset), part_o, part_ml, q_indptr,
-                         p.q_heads);
-      return FromHip(hipGetLastError(), "PagedAttention prefill merge launch");
-    }
-    hipLaunchKernelGGL(PrefillKernel, dim3(static_cast<uint32_t>(rec.work_items)), dim3(256), 0, s,
-                       static_cast<const uint16_t*>(p.q.address), outp, lsep, kv, q_indptr, items, p.q_heads, p.causal,
-                       scale_log2);
-    return FromHip(hipGetLastError(), "PagedAttention prefill launch");
+    // The multi-token sequences on the tile kernels, then the single-token ones on the decode kernels (bf16, head_dim
+    // 256 in prefill mode). Running the two side by side on two streams gains nothing: a tile workgroup needs two
+    // 256-register wavefronts per SIMD, so it cannot share a CU with resident decode workgroups.
+    ROOST_TRY(LaunchPrefill(p, rec, dev, kv, scale_log2, s));
+    return LaunchDecode<uint16_t, 256>(p, rec, dev, kv, scale_log2, s);
   });
 }

@@ -235,6 +235,13 @@ PREFILL_CASES = [
     ("fresh-40 ps1 HND", [(40, 40)], 1, True, True),
     # a long causal chunk: its key range is cut into pieces that the merge kernel combines
     ("chunk-512-of-4000 split", [(512, 4000), (3, 3)], 16, False, True),
+    # mixed worker steps: the single-token sequences of a prefill call run on the decode kernels
+    ("mixed step 6 decode + 2 chunks", [(1, 900), (1, 17), (200, 1200), (1, 3000), (1, 1), (64, 64), (1, 5000),
+                                        (1, 333)], 16, False, True),
+    ("mixed step HND ps64", [(1, 900), (130, 700), (1, 4000), (2, 2)], 64, True, True),
+    ("mixed step ps8", [(1, 900), (100, 300), (1, 45)], 8, False, True),
+    ("mixed non-causal with empty row", [(1, 0), (5, 40), (1, 7)], 16, False, False),
+    ("all single-token rows in prefill mode", [(1, 50), (1, 3000)], 16, False, True),
 ]
 
 
@@ -280,6 +287,42 @@ def test_config3_prefill_full_size(session):
                                [int(b.kv_lens[s])], [int(n[s])], 16, False, True)
         ref1 = cases.values(cases.oracle_attention(one), True)
         cases.assert_close(got[b.q_indptr[s]:b.q_indptr[s + 1]], ref1, what=f"config 3 seq {s} vs CpuOps")
+
+
+def test_config5_mixed_step_attention(session):
+    """BASELINE config 5's attention call: 48 decode rows (ctx U(1024, 16384)) and 2 chunks of 512 on 4096-token
+    prefixes in one prefill-mode call, as the worker issues a mixed step. The whole batch against a float32 torch
+    reference of the same math; three sampled sequences (two decode rows and one chunk) against the CpuOps oracle."""
+    t = torch()
+    rng = np.random.default_rng(5)
+    kv = np.concatenate([rng.integers(1024, 16385, size=48), [4608, 4608]])
+    n = np.concatenate([np.ones(48, np.int64), [512, 512]])
+    b = cases.make_paged_batch(rng, kv, n, std=0.5, pool_factor=1.25)
+    got = run_case(session, b, check_nohost=False, check_determinism=True)
+    qv = t.from_numpy(cases.values(b.q, True).astype(np.float32)).cuda()
+    kc = t.from_numpy(cases.values(b.k_cache, True).astype(np.float32)).cuda()
+    vc = t.from_numpy(cases.values(b.v_cache, True).astype(np.float32)).cuda()
+    ref = np.zeros_like(got)
+    for s in range(50):
+        pages = t.from_numpy(b.kv_indices[b.kv_indptr[s]:b.kv_indptr[s + 1]].astype(np.int64)).cuda()
+        kl = int(b.kv_lens[s])
+        k = kc[pages].reshape(-1, 2, 256)[:kl]
+        v = vc[pages].reshape(-1, 2, 256)[:kl]
+        q = qv[b.q_indptr[s]:b.q_indptr[s + 1]]
+        qpos = t.arange(kl - q.shape[0], kl, device="cuda")
+        mask = t.arange(kl, device="cuda")[None, :] <= qpos[:, None]
+        for h in range(8):
+            sc = (q[:, h, :] @ k[:, h // 4, :].T) / 16.0
+            sc = sc.masked_fill(~mask, float("-inf"))
+            ref[b.q_indptr[s]:b.q_indptr[s + 1], h] = (t.softmax(sc, dim=-1) @ v[:, h // 4, :]).cpu().numpy()
+    cases.assert_close(got, ref, what="config 5 attention vs fp32 torch")
+    for s in (int(np.argmin(kv[:48])), int(np.argmax(kv[:48])), 49):
+        one = cases.PagedBatch(b.q[b.q_indptr[s]:b.q_indptr[s + 1]].copy(), b.k_cache, b.v_cache,
+                               np.array([0, n[s]], np.int32), np.array([0, b.kv_indptr[s + 1] - b.kv_indptr[s]], np.int32),
+                               b.kv_indices[b.kv_indptr[s]:b.kv_indptr[s + 1]].copy(), b.kv_last_page_len[s:s + 1].copy(),
+                               [int(b.kv_lens[s])], [int(n[s])], 16, False, True)
+        ref1 = cases.values(cases.oracle_attention(one), True)
+        cases.assert_close(got[b.q_indptr[s]:b.q_indptr[s + 1]], ref1, what=f"config 5 seq {s} vs CpuOps")
 
 
 def test_prefill_batch_invariance(session):
