@@ -96,14 +96,28 @@ def time_runs(torch, session, entry, params, ws, steps, warmup):
     return start.elapsed_time(end) / steps
 
 
-def planned(session, entry, params, key):
-    """Workspace + plan (host step), returning the workspace and the plan's wall time in ms."""
-    t0 = time.perf_counter()
-    session.launch(entry, params, key=key)  # plans and runs once
+def planned(session, entry, params, key, reps=20):
+    """Workspace + plan, returning the workspace and the host cost of one step's planning in ms: the workspace query
+    and plan() (host tables, pinned staging, async copy) as the worker calls them every step, averaged over `reps`
+    once the buffers exist (the first launch also allocates them and is not counted)."""
+    import ctypes as C
+
+    session.launch(entry, params, key=key)  # allocates, plans and runs once
     session.stream.synchronize()
-    plan_ms = (time.perf_counter() - t0) * 1e3
     slot = session._ws.get((entry.variant_id, key))
-    return (slot[3] if slot is not None else None), plan_ms
+    if slot is None:
+        return None, 0.0
+    ws = slot[3]
+    if not entry.needs_plan:
+        return ws, 0.0
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        session.workspace_sizes(entry, params)
+        status = entry.plan(session.ctx, C.addressof(params), C.addressof(ws), C.c_void_p(session.stream_handle))
+        assert status == 0, status
+        session.stream.synchronize()  # the pinned staging buffer is reused by the next plan
+    plan_ms = (time.perf_counter() - t0) * 1e3 / reps
+    return ws, plan_ms
 
 
 def bench_decode(torch, roost_amd, session, steps, warmup):

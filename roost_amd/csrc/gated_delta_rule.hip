@@ -317,7 +317,8 @@ struct ChunkArgs {
   const int4* chunks;  // [chunks] (sequence, first token, tokens, 0)
   const int4* seqs;    // [batch] (first chunk, chunk count, first token, end token)
   uint8_t* recs;       // [chunks][heads] records
-  uint32_t chains;     // batch * heads
+  const int32_t* seq_list;  // when set: chain c runs sequence seq_list[c / heads] (-1: none)
+  uint32_t chains;     // batch * heads, or (length of seq_list) * heads
 };
 
 __device__ __forceinline__ f32x4_t Mfma(uint4 a, uint4 b, f32x4_t c) {
@@ -843,7 +844,9 @@ __global__ void __launch_bounds__(256, 1) ChunkScanKernel(ChunkArgs ca) {
   const uint32_t chain = (x & 7) + 8 * (x >> 5);
   const uint32_t vb = (x >> 3) & 3;
   if (chain >= ca.chains) return;
-  const uint32_t seq = chain / kHeads, h = chain % kHeads;
+  const int32_t listed = ca.seq_list != nullptr ? ca.seq_list[chain / kHeads] : static_cast<int32_t>(chain / kHeads);
+  if (listed < 0) return;
+  const uint32_t seq = static_cast<uint32_t>(listed), h = chain % kHeads;
   const int4 sq = ca.seqs[seq];
   if (sq.y == 0) return;  // an empty sequence leaves its slot untouched
   const int32_t slot = a.slots[seq];
@@ -924,18 +927,22 @@ struct PlanRecord {
 struct ChunkLayout {
   uint64_t chunk_table;  // [max_chunks] int4 (sequence, first token, tokens, 0)
   uint64_t seq_table;    // [batch] int4 (first chunk, chunk count, first token, end token)
+  uint64_t seq_list;     // [max_long] int32: the chunked sequences in order (recurrent variant only)
+  uint32_t max_long;
   uint64_t tables_bytes;
   uint64_t records;      // [max_chunks][heads] records of kRecBytes
   uint64_t total;
   uint32_t max_chunks;
 };
 
-ChunkLayout MakeChunkLayoutFor(uint64_t max_chunks, uint64_t batch) {
+ChunkLayout MakeChunkLayoutFor(uint64_t max_chunks, uint64_t batch, uint64_t max_long = 0) {
   ChunkLayout l{};
   l.max_chunks = static_cast<uint32_t>(max_chunks);
+  l.max_long = static_cast<uint32_t>(max_long);
   l.chunk_table = 0;
   l.seq_table = roost::AlignUp(16ull * l.max_chunks, 256);
-  l.tables_bytes = roost::AlignUp(l.seq_table + 16ull * batch, 256);
+  l.seq_list = l.seq_table + 16ull * batch;
+  l.tables_bytes = roost::AlignUp(l.seq_list + 4ull * max_long, 256);
   l.records = l.tables_bytes;
   l.total = l.records + uint64_t{l.max_chunks} * kHeads * kRecBytes;
   return l;
@@ -947,7 +954,8 @@ ChunkLayout MakeChunkLayout(uint64_t tokens, uint64_t batch) { return MakeChunkL
 // Only sequences of kRouteMinTokens or more are chunked (recurrent variant): sum ceil(len / 64) over them is at most
 // tokens / 64 plus their number, which is at most min(batch, tokens / kRouteMinTokens).
 ChunkLayout MakeRouteLayout(uint64_t tokens, uint64_t batch) {
-  return MakeChunkLayoutFor(tokens / kChunk + std::min<uint64_t>(batch, tokens / kRouteMinTokens), batch);
+  const uint64_t max_long = std::min<uint64_t>(batch, tokens / kRouteMinTokens);
+  return MakeChunkLayoutFor(tokens / kChunk + max_long, batch, max_long);
 }
 
 
@@ -959,12 +967,13 @@ ChunkLayout MakeRouteLayout(uint64_t tokens, uint64_t batch) {
 // output (device tables are not range-checked, as everywhere in this ABI), and nothing is written out of bounds. One
 // workgroup walks the batch 1024 sequences at a time with a workgroup-wide prefix sum of the chunk counts.
 __global__ void __launch_bounds__(1024) RouteKernel(const int32_t* cu, uint32_t batch, uint32_t max_chunks,
-                                                    int4* chunks, int4* seqs) {
-  __shared__ uint32_t wave_sum[16];
+                                                    int4* chunks, int4* seqs, int32_t* seq_list, uint32_t max_long) {
+  __shared__ uint32_t wave_sum[16], wave_long[16];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   for (uint32_t i = tid; i < max_chunks; i += 1024) chunks[i] = make_int4(0, 0, 0, 0);
-  __syncthreads();  // the zero fill lands before any entry below is written over it
-  uint32_t base = 0;
+  for (uint32_t i = tid; i < max_long; i += 1024) seq_list[i] = -1;
+  __syncthreads();  // the fills land before any entry below is written over them
+  uint32_t base = 0, long_base = 0;
   for (uint32_t start = 0; start < batch; start += 1024) {
     const uint32_t b = start + tid;
     int32_t t0 = 0, t1 = 0;
@@ -991,19 +1000,40 @@ __global__ void __launch_bounds__(1024) RouteKernel(const int32_t* cu, uint32_t 
       total += x;
     }
     const uint64_t first = uint64_t{base} + before + incl - cnt;
+    const bool routed = b < batch && cnt != 0 && first + cnt <= max_chunks;
+    // Second prefix sum: the position of each routed sequence in seq_list.
+    const uint32_t is_long = routed ? 1u : 0u;
+    uint32_t lincl = is_long;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_up(lincl, o);
+      if (lane >= o) lincl += y;
+    }
+    if (lane == 63) wave_long[w] = lincl;
+    __syncthreads();
+    uint32_t lbefore = 0, ltotal = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t x = wave_long[i];
+      lbefore += i < w ? x : 0;
+      ltotal += x;
+    }
     if (b < batch) {
-      if (cnt != 0 && first + cnt <= max_chunks) {
+      if (routed) {
         seqs[b] = make_int4(static_cast<int32_t>(first), static_cast<int32_t>(cnt), t0, t1);
         for (uint32_t c = 0; c < cnt; ++c) {
           const int32_t tc = t0 + static_cast<int32_t>(c * kChunk);
           chunks[first + c] = make_int4(static_cast<int32_t>(b), tc, min(static_cast<int32_t>(kChunk), t1 - tc), 0);
         }
+        const uint32_t li = long_base + lbefore + lincl - 1;
+        if (li < max_long) seq_list[li] = static_cast<int32_t>(b);
       } else {
         seqs[b] = make_int4(0, 0, t0, t1);
       }
     }
     base = static_cast<uint32_t>(min<uint64_t>(uint64_t{base} + total, 0xFFFFFFFFull));
-    __syncthreads();  // wave_sum is rewritten by the next pass
+    long_base += ltotal;
+    __syncthreads();  // wave_sum and wave_long are rewritten by the next pass
   }
 }
 
@@ -1015,7 +1045,9 @@ RoostStatus LaunchChunk(const RoostGatedDeltaRuleParams& p, const RoostWorkspace
   ca.chunks = reinterpret_cast<const int4*>(base + l.chunk_table);
   ca.seqs = reinterpret_cast<const int4*>(base + l.seq_table);
   ca.recs = base + l.records;
-  ca.chains = p.batch * kHeads;
+  // The recurrent variant's calls list their chunked sequences; the chunk variant's chains are every sequence.
+  ca.seq_list = l.max_long > 0 ? reinterpret_cast<const int32_t*>(base + l.seq_list) : nullptr;
+  ca.chains = (l.max_long > 0 ? l.max_long : p.batch) * kHeads;
   const dim3 prep(chunks, kHeads);
   const dim3 scan((ca.chains + 7) / 8 * 8 * kVBlocks);
   if (Vec16(p)) {
@@ -1061,6 +1093,15 @@ extern "C" ROOST_API RoostStatus roost_gdn_recurrent_run(RoostContext* ctx, cons
     ROOST_TRY(Validate(p, false));
     if (p.batch == 0 || p.tokens == 0) return ROOST_STATUS_OK;
     if (p.tokens < kRouteMinTokens) return LaunchRecurrent(p, Stream(stream));
+    if (p.cu_seqlens_host != nullptr) {
+      // The host copy says whether any sequence reaches kRouteMinTokens; if none does, the recurrent kernel runs every
+      // sequence (so a graph captured from this call stays correct whatever lengths it is replayed with).
+      bool any_long = false;
+      for (uint32_t b = 0; b < p.batch && !any_long; ++b) {
+        any_long = p.cu_seqlens_host[b + 1] - p.cu_seqlens_host[b] >= static_cast<int32_t>(kRouteMinTokens);
+      }
+      if (!any_long) return LaunchRecurrent(p, Stream(stream));
+    }
     // Every launch size below follows from tokens and batch alone, so the call can be captured into a graph.
     const ChunkLayout l = MakeRouteLayout(p.tokens, p.batch);
     if (!DeviceWorkspaceOk(ws, l.total)) {
@@ -1070,12 +1111,13 @@ extern "C" ROOST_API RoostStatus roost_gdn_recurrent_run(RoostContext* ctx, cons
     auto* base = static_cast<uint8_t*>(ws->device);
     auto* chunks = reinterpret_cast<int4*>(base + l.chunk_table);
     auto* seqs = reinterpret_cast<int4*>(base + l.seq_table);
+    auto* seq_list = reinterpret_cast<int32_t*>(base + l.seq_list);
     // The long sequences on route -> prep -> scan, the short ones on the recurrent kernel, in that order on the
     // caller's stream. (Running the two on two streams was slower: the short kernels lose more to sharing the chip
     // than the overlap saves.) Two sequences of one call sharing a state slot leave the recurrent one's state.
     hipStream_t s = Stream(stream);
     hipLaunchKernelGGL(RouteKernel, dim3(1), dim3(1024), 0, s, static_cast<const int32_t*>(p.cu_seqlens.address),
-                       p.batch, l.max_chunks, chunks, seqs);
+                       p.batch, l.max_chunks, chunks, seqs, seq_list, l.max_long);
     ROOST_TRY(FromHip(hipGetLastError(), "GatedDeltaRule route launch"));
     ROOST_TRY(LaunchChunk(p, ws, l, l.max_chunks, s));
     return LaunchRecurrent(p, s, static_cast<int32_t>(kRouteMinTokens));
