@@ -10,6 +10,11 @@ Functions and the reference code they restate:
   gated_delta_rule -- src/Starlings.Roost.Ops/CpuOps.Hybrid.cs:30-157
   plan_region      -- src/Starlings.Roost.Worker/Eager/PlanRegionWriter.cs:19-64
   to_bf16          -- src/Starlings.Roost.Ops/CpuElements.cs:128-160
+  gdn_gates        -- src/Starlings.Roost.Ops/CpuOps.Gating.cs:21-47
+  gated_rms_norm   -- src/Starlings.Roost.Ops/CpuOps.Gating.cs:57-86
+  sigmoid_mul      -- src/Starlings.Roost.Ops/CpuOps.Gating.cs:91-101
+  causal_conv1d    -- src/Starlings.Roost.Ops/CpuOps.Hybrid.cs:167-243
+  state_copy / state_snapshot -- src/Starlings.Roost.Ops/CpuOps.Hybrid.cs:251-263
 """
 from __future__ import annotations
 
@@ -125,6 +130,54 @@ def gated_delta_rule(q, k, v, g, beta, out, state, state_slots, cu_seqlens, *, b
         batch, tokens, k_heads, v_heads, k_dim, v_dim, ctypes.c_int64(q_stride), ctypes.c_int64(k_stride),
         ctypes.c_int64(v_stride), int(use_initial_state), int(l2_norm_qk), ctypes.c_float(scale), threads)
     _check(rc)
+
+
+def _dt(a: np.ndarray) -> int:
+    """Element type of an oracle array: uint16 bit arrays are bf16."""
+    return {np.dtype(np.float32): DT_F32, np.dtype(np.float64): DT_F64, np.dtype(np.uint16): DT_BF16}[a.dtype]
+
+
+def gdn_gates(a, b, a_log, dt_bias, g, beta, *, tokens, v_heads, a_stride=0, b_stride=0) -> None:
+    """CpuOps.GatedDeltaRuleGates. a and b share one element type; every other array is read or written in its own."""
+    assert a.dtype == b.dtype
+    _check(lib().oracle_gdn_gates(_ptr(a), _ptr(b), _dt(a), _ptr(a_log), _dt(a_log), _ptr(dt_bias), _dt(dt_bias),
+                                  _ptr(g), _dt(g), _ptr(beta), _dt(beta), tokens, v_heads, ctypes.c_int64(a_stride),
+                                  ctypes.c_int64(b_stride)))
+
+
+def gated_rms_norm(x, gate, weight, out, *, rows, dim, eps) -> None:
+    """CpuOps.GatedRmsNorm (norm before gate; the weight multiplies as stored)."""
+    _check(lib().oracle_gated_rms_norm(_ptr(x), _ptr(gate), _ptr(weight), _dt(weight), _ptr(out), _dt(x),
+                                       ctypes.c_int64(rows), dim, ctypes.c_float(eps)))
+
+
+def sigmoid_mul(x, gate, out) -> None:
+    """CpuOps.SigmoidMul over x.size elements."""
+    _check(lib().oracle_sigmoid_mul(_ptr(x), _ptr(gate), _ptr(out), _dt(x), ctypes.c_int64(x.size)))
+
+
+def causal_conv1d(x, weight, bias, out, state, state_slots, cu_seqlens, *, batch, tokens, channels, width,
+                  silu) -> None:
+    """CpuOps.CausalConv1d; state: the conv-state pool [slots, channels, width - 1], updated in place."""
+    _check(lib().oracle_causal_conv1d(_ptr(x), _ptr(weight), _ptr(bias), _ptr(out), _dt(x), _ptr(state), _dt(state),
+                                      ctypes.c_int64(state.size), _ptr(state_slots), _ptr(cu_seqlens), batch, tokens,
+                                      channels, width, int(silu)))
+
+
+def state_copy(pool: np.ndarray, pairs: np.ndarray, *, slot_bytes: int) -> None:
+    """CpuOps.RecurrentStateCopy: slot pairs[i, 0] -> slot pairs[i, 1] of pool, in pair order."""
+    raw = pool.view(np.uint8)
+    _check(lib().oracle_state_copy_pairs(_ptr(raw), ctypes.c_int64(raw.size), _ptr(raw), ctypes.c_int64(raw.size),
+                                         _ptr(pairs), pairs.size // 2, ctypes.c_int64(slot_bytes), 0))
+
+
+def state_snapshot(pool: np.ndarray, snapshots: np.ndarray, pairs: np.ndarray, *, slot_bytes: int,
+                   restore: bool) -> None:
+    """CpuOps.RecurrentStateSnapshot: pairs (slot, snapshot); restore copies snapshot -> slot."""
+    p, s = pool.view(np.uint8), snapshots.view(np.uint8)
+    src, dst = (s, p) if restore else (p, s)
+    _check(lib().oracle_state_copy_pairs(_ptr(src), ctypes.c_int64(src.size), _ptr(dst), ctypes.c_int64(dst.size),
+                                         _ptr(pairs), pairs.size // 2, ctypes.c_int64(slot_bytes), int(restore)))
 
 
 def plan_region(seqs, block_size: int):

@@ -310,3 +310,98 @@ int oracle_plan_region(int batch, const int32_t* token_start, const int32_t* tok
   kv_indptr[batch] = block_at;
   return 0;
 }
+
+/* ---- Gated DeltaNet layer neighbours (reference: src/Starlings.Roost.Ops/CpuOps.Gating.cs:21-110,
+ *      CpuOps.Hybrid.cs:160-263, CpuElements.cs:223) ---- */
+
+static double sigmoid_d(double x) { return 1.0 / (1.0 + exp(-x)); }
+static double silu_d(double x) { return x / (1.0 + exp(-x)); }
+
+/* GatedDeltaRuleGates (CpuOps.Gating.cs:21-47): a and b read as `dtype` at their row strides (0 = v_heads); a_log,
+ * dt_bias, g and beta in their own types. softplus(x) = x above 20, else log(1 + exp(x)). */
+int oracle_gdn_gates(const void* a, const void* b, int dtype, const void* a_log, int alog_dt, const void* dt_bias,
+                     int dtb_dt, void* g, int g_dt, void* beta, int beta_dt, int tokens, int v_heads, int64_t a_stride,
+                     int64_t b_stride) {
+  const int64_t as = a_stride == 0 ? v_heads : a_stride;
+  const int64_t bs = b_stride == 0 ? v_heads : b_stride;
+  if (as < v_heads || bs < v_heads) return fail("AStride and BStride must be 0 or at least VHeads");
+  for (int64_t t = 0; t < tokens; ++t) {
+    for (int h = 0; h < v_heads; ++h) {
+      const double x = load(a, dtype, t * as + h) + load(dt_bias, dtb_dt, h);
+      const double sp = x > 20.0 ? x : log(1.0 + exp(x));
+      store(g, g_dt, t * v_heads + h, -exp(load(a_log, alog_dt, h)) * sp);
+      store(beta, beta_dt, t * v_heads + h, sigmoid_d(load(b, dtype, t * bs + h)));
+    }
+  }
+  return 0;
+}
+
+/* GatedRmsNorm (CpuOps.Gating.cs:57-86): out = x / sqrt(sum(x^2) / dim + eps) * weight * silu(gate), per row. */
+int oracle_gated_rms_norm(const void* x, const void* gate, const void* weight, int w_dt, void* out, int dtype,
+                          int64_t rows, int dim, float eps) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const int64_t o = r * dim;
+    double ss = 0.0;
+    for (int i = 0; i < dim; ++i) {
+      const double v = load(x, dtype, o + i);
+      ss += v * v;
+    }
+    const double inv = 1.0 / sqrt(ss / dim + (double)eps);
+    for (int i = 0; i < dim; ++i) {
+      const double y = load(x, dtype, o + i) * inv * load(weight, w_dt, i) * silu_d(load(gate, dtype, o + i));
+      store(out, dtype, o + i, y);
+    }
+  }
+  return 0;
+}
+
+/* SigmoidMul (CpuOps.Gating.cs:91-101): out = x / (1 + exp(-gate)) elementwise. */
+int oracle_sigmoid_mul(const void* x, const void* gate, void* out, int dtype, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) store(out, dtype, i, load(x, dtype, i) * sigmoid_d(load(gate, dtype, i)));
+  return 0;
+}
+
+/* CausalConv1d (CpuOps.Hybrid.cs:167-243): y_t = bias + sum_j weight[c, j] * h_{t + j}, h = [state (width - 1, oldest
+ * first), inputs]; silu last when set; then the slot holds the last width - 1 entries of h. Weight and bias are read
+ * as `dtype`, the state as `state_dt`. A sequence of zero tokens leaves its slot untouched. */
+int oracle_causal_conv1d(const void* x, const void* weight, const void* bias, void* out, int dtype, void* state,
+                         int state_dt, int64_t state_len, const int32_t* slots, const int32_t* cu, int batch, int tokens,
+                         int channels, int width, int silu) {
+  if (width < 1 || width > 16) return fail("Width must be in [1, 16]");
+  const int sl = width - 1;
+  double next[16];
+  for (int b = 0; b < batch; ++b) {
+    const int64_t t0 = cu[b], t1 = cu[b + 1];
+    if (t0 < 0 || t1 < t0 || t1 > tokens) return fail("invalid CuSeqlens range");
+    const int64_t n = t1 - t0;
+    if (n == 0) continue;
+    for (int c = 0; c < channels; ++c) {
+      const int64_t so = ((int64_t)slots[b] * channels + c) * sl;
+      if (so < 0 || so + sl > state_len) return fail("conv state slot outside the pool");
+#define HIST(i) ((i) < sl ? load(state, state_dt, so + (i)) : load(x, dtype, (t0 + (i) - sl) * channels + c))
+      for (int64_t t = 0; t < n; ++t) {
+        double y = bias != NULL ? load(bias, dtype, c) : 0.0;
+        for (int j = 0; j < width; ++j) y += load(weight, dtype, (int64_t)c * width + j) * HIST(t + j);
+        store(out, dtype, (t0 + t) * channels + c, silu ? silu_d(y) : y);
+      }
+      for (int j = 0; j < sl; ++j) next[j] = HIST(n + j);
+#undef HIST
+      for (int j = 0; j < sl; ++j) store(state, state_dt, so + j, next[j]);
+    }
+  }
+  return 0;
+}
+
+/* RecurrentStateCopy / RecurrentStateSnapshot (CpuOps.Hybrid.cs:251-263): byte copies of slot_bytes, pair by pair in
+ * order. copy: src = dst = pool, pairs (from, to); snapshot: pairs (slot, snapshot), restore swaps the direction. */
+int oracle_state_copy_pairs(const uint8_t* src, int64_t src_bytes, uint8_t* dst, int64_t dst_bytes,
+                            const int32_t* pairs, int count, int64_t slot_bytes, int swap) {
+  for (int i = 0; i < count; ++i) {
+    const int64_t from = (int64_t)pairs[2 * i + swap], to = (int64_t)pairs[2 * i + 1 - swap];
+    if (from < 0 || to < 0 || (from + 1) * slot_bytes > src_bytes || (to + 1) * slot_bytes > dst_bytes) {
+      return fail("a slot lies outside its pool");
+    }
+    memmove(dst + to * slot_bytes, src + from * slot_bytes, (size_t)slot_bytes);
+  }
+  return 0;
+}

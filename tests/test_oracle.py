@@ -346,3 +346,202 @@ def test_plan_region_slot_mapping_closed_form():
     assert list(last) == [3, 5, 16]
     want = [7 * 16 + 0, 7 * 16 + 1, 7 * 16 + 2, 9 * 16 + 4] + [(4 if p < 16 else 1) * 16 + p % 16 for p in range(14, 32)]
     assert list(slots) == want
+
+
+# ---- Gated DeltaNet layer neighbours --------------------------------------------------------------------------------
+# Pinned by the reference's hand cases (tests/Starlings.Roost.Ops.Tests/GatingOpsTests.cs, HybridTests.cs:249-385) and by
+# transformers 5.20.1's own float32 tensors, which the reference's tests hold as a fixture
+# (Reference/qwen35-gating-cases.json, copied as data to tests/golden/qwen35_gating_cases.json).
+
+import json
+from pathlib import Path
+
+GOLDEN = json.loads((Path(__file__).resolve().parent / "golden" / "qwen35_gating_cases.json").read_text())
+LN2, LN3 = math.log(2), math.log(3)
+
+
+def _f64(*v):
+    return np.array(v, dtype=np.float64)
+
+
+def _fx(case, key, dtype=np.float32):
+    return np.array(GOLDEN[case][key], dtype=dtype)
+
+
+def _rel(got, want, rel):
+    """GatingReferenceTests.Rel: |got - want| <= rel * max(|want|, 1e-6) elementwise."""
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    assert (np.abs(got - want) <= rel * np.maximum(np.abs(want), 1e-6)).all()
+
+
+def test_golden_fixture_is_the_pinned_reference():
+    assert GOLDEN["transformers"] == "5.20.1"
+    assert GOLDEN["modeling_qwen3_5_sha256"].startswith("b48635f7")
+
+
+def test_gates_hand_case():
+    """GatingOpsTests.GatesHandComputed: x = a + dt_bias = 0, 25, -1, 20 (softplus returns x above 20 only)."""
+    a, b = _f64(1, 24, 0, 19), _f64(0, LN3, -LN3, 0)
+    g, beta = np.zeros(4), np.zeros(4)
+    oracle.gdn_gates(a, b, _f64(0, LN2), _f64(-1, 1), g, beta, tokens=2, v_heads=2)
+    np.testing.assert_allclose(g, [-LN2, -50.0, -math.log(1 + math.exp(-1)), -2 * math.log(1 + math.exp(20))],
+                               rtol=0, atol=1e-14)
+    np.testing.assert_allclose(beta, [0.5, 0.75, 0.25, 0.5], rtol=0, atol=1e-15)
+
+
+def test_gates_strided_views_and_output_types():
+    """GatingOpsTests.GatesReadStridedViewsAndWriteEachSpansType: a at column 0 and b at column 2 of [tokens, 5] rows;
+    g float32, beta bf16, a_log float32."""
+    fused = _f64(0, 0, 0, 0, 99, 0, 0, 0, 0, 99)
+    g, beta = np.zeros(4, np.float32), np.zeros(4, np.uint16)
+    oracle.gdn_gates(fused, np.ascontiguousarray(fused[2:]), np.array([0, LN2], np.float32), _f64(0, 0), g, beta,
+                     tokens=2, v_heads=2, a_stride=5, b_stride=5)
+    np.testing.assert_allclose(g, [-LN2, -2 * LN2, -LN2, -2 * LN2], rtol=1e-6)
+    assert list(oracle.bf16_to_f64(beta)) == [0.5] * 4
+    with pytest.raises(oracle.OracleError):
+        oracle.gdn_gates(fused, fused, _f64(0, 0), _f64(0, 0), np.zeros(4), np.zeros(4), tokens=2, v_heads=2,
+                         a_stride=1)
+
+
+def test_gates_match_transformers():
+    c = GOLDEN["linear"]
+    t, vh = c["tokens"], c["v_heads"]
+    g, beta = np.zeros(t * vh), np.zeros(t * vh)
+    oracle.gdn_gates(_fx("linear", "a"), _fx("linear", "b"), _fx("linear", "a_log"), _fx("linear", "dt_bias"), g, beta,
+                     tokens=t, v_heads=vh)
+    _rel(g, _fx("linear", "g"), 4e-7)
+    _rel(beta, _fx("linear", "beta"), 4e-7)
+    x = _fx("linear", "a", np.float64).reshape(t, vh)[:, 0] + c["dt_bias"][0]
+    assert (x > 20).any() and (x < -20).any() and ((x > 0) & (x < 20)).any()  # both sides of the threshold
+
+
+def test_gated_rms_norm_hand_cases():
+    """GatingOpsTests: rows [3, 4] and [-1, 2], eps 0, weight [1, 0.5] as stored; in place with eps 1; a float32
+    weight under bf16 activations."""
+    o = np.zeros(4)
+    oracle.gated_rms_norm(_f64(3, 4, -1, 2), _f64(0, LN3, LN3, LN3), _f64(1, 0.5), o, rows=2, dim=2, eps=0.0)
+    s3 = LN3 * 0.75
+    np.testing.assert_allclose(o, [0, 4 / math.sqrt(12.5) * 0.5 * s3, -1 / math.sqrt(2.5) * s3,
+                                   2 / math.sqrt(2.5) * 0.5 * s3], rtol=0, atol=1e-15)
+    x = _f64(1, 1)
+    oracle.gated_rms_norm(x, _f64(10, 10), _f64(2, 2), x, rows=1, dim=2, eps=1.0)
+    np.testing.assert_allclose(x, [2 / math.sqrt(2) * 10 / (1 + math.exp(-10))] * 2, rtol=0, atol=1e-14)
+    xb, gb = oracle.to_bf16([1, 1]), oracle.to_bf16([16, 16])
+    ob = np.zeros(2, np.uint16)
+    oracle.gated_rms_norm(xb, gb, np.array([1.5, 0.25], np.float32), ob, rows=1, dim=2, eps=0.0)
+    assert list(oracle.bf16_to_f64(ob)) == [24.0, 4.0]
+
+
+def test_gated_rms_norm_matches_transformers_and_discriminates():
+    c = GOLDEN["linear"]
+    rows, dim = c["tokens"] * c["v_heads"], c["v_dim"]
+    core, z, w = _fx("linear", "core"), _fx("linear", "z"), _fx("linear", "norm_weight")
+    o = np.zeros(rows * dim, np.float32)
+    oracle.gated_rms_norm(core, z, w, o, rows=rows, dim=dim, eps=c["eps"])
+    want = _fx("linear", "norm_out")
+    _rel(o, want, 4e-7)
+    wrong = np.zeros_like(o)  # a zero-centred weight (1 + w) is far off
+    oracle.gated_rms_norm(core, z, (1 + w).astype(np.float32), wrong, rows=rows, dim=dim, eps=c["eps"])
+    assert np.abs(wrong - want).max() > 0.1
+
+
+def test_sigmoid_mul_hand_case_in_place_and_transformers():
+    o = np.zeros(4)
+    x, gate = _f64(2, -4, 6, 1), _f64(0, LN3, -LN3, -800)
+    oracle.sigmoid_mul(x, gate, o)
+    np.testing.assert_allclose(o, [1, -3, 1.5, 0], rtol=0, atol=1e-15)
+    oracle.sigmoid_mul(x, gate, x)
+    np.testing.assert_allclose(x, [1, -3, 1.5, 0], rtol=0, atol=1e-15)
+    attn, gate = _fx("attention", "attn"), _fx("attention", "gate")
+    o = np.zeros_like(attn)
+    oracle.sigmoid_mul(attn, gate, o)
+    _rel(o, _fx("attention", "gated"), 4e-7)
+
+
+def test_gdn_oracle_matches_transformers_delta_rule():
+    """GatingReferenceTests.GatedDeltaRuleNormalisesQAndKInsideTheOp: transformers' q, k, v (before its l2 norm), g and
+    beta from a zero state give its core output; without the in-op norm the result is far off."""
+    c = GOLDEN["linear"]
+    t, kh, vh, kd, vd = c["tokens"], c["k_heads"], c["v_heads"], c["k_dim"], c["v_dim"]
+    core = _fx("linear", "core", np.float64)
+    tol = 1e-5 * np.abs(core).max()
+
+    def run(l2):
+        out = np.zeros(t * vh * vd, np.float32)
+        state = np.zeros(vh * kd * vd, np.float32)
+        oracle.gated_delta_rule(_fx("linear", "q"), _fx("linear", "k"), _fx("linear", "v"), _fx("linear", "g"),
+                                _fx("linear", "beta"), out, state, np.zeros(1, np.int32), np.array([0, t], np.int32),
+                                batch=1, tokens=t, k_heads=kh, v_heads=vh, k_dim=kd, v_dim=vd, use_initial_state=False,
+                                l2_norm_qk=l2)
+        return out.astype(np.float64)
+
+    assert np.abs(run(True) - core).max() <= tol
+    assert np.abs(run(False) - core).max() > 100 * tol
+
+
+def _conv(x, w, bias, state, slots, cu, *, batch, tokens, ch, width, silu):
+    y = np.zeros(tokens * ch)
+    oracle.causal_conv1d(x, w, bias, y, state, np.array(slots, np.int32), np.array(cu, np.int32), batch=batch,
+                         tokens=tokens, channels=ch, width=width, silu=silu)
+    return y
+
+
+def test_causal_conv1d_hand_cases():
+    """HybridTests.cs:249-277: width 3, state [1, 2], weights [1, 10, 100]; a one-token sequence with bias and silu."""
+    st = _f64(1, 2)
+    y = _conv(_f64(3, 4), _f64(1, 10, 100), None, st, [0], [0, 2], batch=1, tokens=2, ch=1, width=3, silu=False)
+    assert list(y) == [321.0, 432.0] and list(st) == [3.0, 4.0]
+    st = _f64(1, 2)
+    y = _conv(_f64(3), _f64(1, 10, 100), _f64(-5), st, [0], [0, 1], batch=1, tokens=1, ch=1, width=3, silu=True)
+    pre = 1 + 20 + 300 - 5
+    assert abs(y[0] - pre / (1 + math.exp(-pre))) < 1e-10 and list(st) == [2.0, 3.0]
+
+
+def test_causal_conv1d_one_call_equals_token_calls_and_independent_convolution():
+    """HybridTests.cs:280-359: one call = token-by-token calls, other slots untouched, final state = the last
+    width - 1 inputs; two packed sequences from zero states against a direct convolution in numpy."""
+    rng = np.random.default_rng(3)
+    ch, width, n = 3, 4, 7
+    xs, ws = rng.uniform(-1, 1, n * ch), rng.uniform(-1, 1, ch * width)
+    init = rng.uniform(-1, 1, 2 * ch * (width - 1))
+    st = init.copy()
+    y = _conv(xs, ws, None, st, [1], [0, n], batch=1, tokens=n, ch=ch, width=width, silu=True)
+    st2 = init.copy()
+    steps = [_conv(xs[t * ch:(t + 1) * ch].copy(), ws, None, st2, [1], [0, 1], batch=1, tokens=1, ch=ch, width=width,
+                   silu=True) for t in range(n)]
+    assert np.array_equal(y, np.concatenate(steps)) and np.array_equal(st, st2)
+    assert np.array_equal(st[:ch * (width - 1)], init[:ch * (width - 1)])
+    last = xs.reshape(n, ch)[n - (width - 1):].T  # [ch, width - 1], oldest first
+    assert np.array_equal(st[ch * (width - 1):].reshape(ch, width - 1), last)
+    # Two packed sequences from zero states.
+    ch, width, lens = 2, 3, [4, 2]
+    xs, ws = rng.uniform(-1, 1, 6 * ch), rng.uniform(-1, 1, ch * width)
+    y = _conv(xs, ws, None, np.zeros(2 * ch * (width - 1)), [0, 1], [0, 4, 6], batch=2, tokens=6, ch=ch, width=width,
+              silu=False)
+    x2, w2 = xs.reshape(6, ch), ws.reshape(ch, width)
+    start = 0
+    for ln in lens:
+        for t in range(ln):
+            for c in range(ch):
+                want = sum(w2[c, j] * x2[start + t - (width - 1) + j, c] for j in range(width)
+                           if t - (width - 1) + j >= 0)
+                assert abs(y[(start + t) * ch + c] - want) < 1e-13
+        start += ln
+
+
+def test_state_copy_and_snapshot_are_ordered_byte_copies():
+    """HybridTests.cs:362-385: slot 2 <- slot 0, then slot 0 <- slot 1 (NaN and -0 kept bit for bit); snapshot and
+    restore; a slot outside the pool is refused."""
+    pool = np.array([1.5, -0.0, np.nan, 4, 5, 6], np.float32)
+    oracle.state_copy(pool, np.array([0, 2, 1, 0], np.int32), slot_bytes=8)
+    bits = pool.view(np.uint32)
+    assert bits[0] == np.array([np.nan], np.float32).view(np.uint32)[0] and pool[1] == 4
+    assert pool[4] == 1.5 and bits[5] == 0x80000000
+    snaps = np.zeros(4, np.float32)
+    oracle.state_snapshot(pool, snaps, np.array([2, 1], np.int32), slot_bytes=8, restore=False)
+    assert list(snaps.view(np.uint32)) == [0, 0, np.float32(1.5).view(np.uint32), 0x80000000]
+    pool2 = np.zeros(6, np.float32)
+    oracle.state_snapshot(pool2, snaps, np.array([2, 1], np.int32), slot_bytes=8, restore=True)
+    assert list(pool2.view(np.uint32)) == [0, 0, 0, 0, np.float32(1.5).view(np.uint32), 0x80000000]
+    with pytest.raises(oracle.OracleError):
+        oracle.state_copy(pool, np.array([3, 0], np.int32), slot_bytes=8)
