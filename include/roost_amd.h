@@ -49,6 +49,30 @@ ROOST_API RoostStatus roost_gdn_recurrent_workspace(RoostContext* ctx, const voi
 ROOST_API RoostStatus roost_gdn_recurrent_run(RoostContext* ctx, const void* params, const RoostWorkspace* ws,
                                               void* stream);
 
+/* The Gated DeltaNet layer's neighbour ops, each flagged GRAPH_CAPTURABLE | DETERMINISTIC | BATCH_INVARIANT, no plan
+ * and no workspace:
+ * GatedDeltaRuleGates, variant "gated-delta-rule-gates-gfx950" -- replaces roost_gated_delta_rule_gates_run
+ *   (kernels/src/ops/gating.cu:110-177);
+ * GatedRmsNorm, variant "gated-rms-norm-gfx950" -- replaces roost_gated_rms_norm_run (gating.cu:179-229);
+ * SigmoidMul, variant "sigmoid-mul-gfx950" -- replaces roost_sigmoid_mul_run (gating.cu:231-269);
+ * CausalConv1d, variant "causal-conv1d-gfx950" -- replaces roost_causal_conv1d_run
+ *   (kernels/src/ops/causal_conv1d.cu:122-175);
+ * RecurrentStateCopy / RecurrentStateSnapshot, variants "recurrent-state-copy-gfx950" / "recurrent-state-snapshot-gfx950"
+ *   -- replace roost_recurrent_state_copy_run / _snapshot_run (kernels/src/ops/recurrent_state.cu:58-108).
+ * All are registered by kernels/src/ops/hybrid_entries.cu:75-148 in the reference. */
+ROOST_API RoostStatus roost_gated_delta_rule_gates_run(RoostContext* ctx, const void* params, const RoostWorkspace* ws,
+                                                       void* stream);
+ROOST_API RoostStatus roost_gated_rms_norm_run(RoostContext* ctx, const void* params, const RoostWorkspace* ws,
+                                               void* stream);
+ROOST_API RoostStatus roost_sigmoid_mul_run(RoostContext* ctx, const void* params, const RoostWorkspace* ws,
+                                            void* stream);
+ROOST_API RoostStatus roost_causal_conv1d_run(RoostContext* ctx, const void* params, const RoostWorkspace* ws,
+                                              void* stream);
+ROOST_API RoostStatus roost_recurrent_state_copy_run(RoostContext* ctx, const void* params, const RoostWorkspace* ws,
+                                                     void* stream);
+ROOST_API RoostStatus roost_recurrent_state_snapshot_run(RoostContext* ctx, const void* params,
+                                                         const RoostWorkspace* ws, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

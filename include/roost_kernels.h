@@ -291,6 +291,96 @@ typedef struct RoostGatedDeltaRuleParams {
   float scale; /* 0 = 1/sqrt(k_dim) */
 } RoostGatedDeltaRuleParams;
 
+/* Gates of a Gated DeltaNet layer from its raw a and b projections (ABI 1.2), per token t and value head h:
+ * g = -exp(a_log[h]) * softplus(a[t, h] + dt_bias[h]), softplus(x) = log(1 + exp(x)) and x itself above 20;
+ * beta = sigmoid(b[t, h]). a and b are row-strided views (0 = v_heads); every span is read or written in its own dtype
+ * (Qwen3.5: g f32, beta in the activation type). */
+typedef struct RoostGatedDeltaRuleGatesParams {
+  uint32_t struct_size;
+  uint32_t abi_minor;
+  RoostDeviceSpan a;       /* [tokens, v_heads] at a_stride */
+  RoostDeviceSpan b;       /* [tokens, v_heads] at b_stride */
+  RoostDeviceSpan a_log;   /* [v_heads] */
+  RoostDeviceSpan dt_bias; /* [v_heads] */
+  RoostDeviceSpan g;       /* [tokens, v_heads] output */
+  RoostDeviceSpan beta;    /* [tokens, v_heads] output */
+  uint32_t tokens;
+  uint32_t v_heads;
+  uint32_t a_stride;
+  uint32_t b_stride;
+} RoostGatedDeltaRuleGatesParams;
+
+/* Gated RMS norm, norm before gate (ABI 1.2): out = x * rsqrt(mean(x^2) + eps) * weight * silu(gate) per row of dim;
+ * the weight multiplies as stored and has its own dtype. input may alias output. */
+typedef struct RoostGatedRmsNormParams {
+  uint32_t struct_size;
+  uint32_t abi_minor;
+  RoostDeviceSpan input;  /* [rows, dim] */
+  RoostDeviceSpan gate;   /* [rows, dim] */
+  RoostDeviceSpan weight; /* [dim] */
+  RoostDeviceSpan output; /* [rows, dim] */
+  uint32_t rows;
+  uint32_t dim;
+  float eps;
+  uint32_t reserved0;
+} RoostGatedRmsNormParams;
+
+/* out = input * sigmoid(gate) elementwise over [rows, dim] (ABI 1.2). input may alias output. */
+typedef struct RoostSigmoidMulParams {
+  uint32_t struct_size;
+  uint32_t abi_minor;
+  RoostDeviceSpan input;  /* [rows, dim] */
+  RoostDeviceSpan gate;   /* [rows, dim] */
+  RoostDeviceSpan output; /* [rows, dim] */
+  uint32_t rows;
+  uint32_t dim;
+} RoostSigmoidMulParams;
+
+/* Depthwise causal convolution over packed sequences (ABI 1.2): y_t = bias + sum_{j < width} weight[c, j] *
+ * x_{t - (width - 1) + j}, the inputs before a sequence's start taken from its slot's conv_state (oldest first), SiLU
+ * last when silu is set; afterwards the slot holds the last width - 1 inputs of [state, sequence]. width <= 16. input
+ * and output must not overlap; a sequence of zero tokens leaves its slot untouched. */
+typedef struct RoostCausalConv1dParams {
+  uint32_t struct_size;
+  uint32_t abi_minor;
+  RoostDeviceSpan input;       /* [tokens, channels] */
+  RoostDeviceSpan weight;      /* [channels, width] */
+  RoostDeviceSpan bias;        /* optional [channels]; NULL address when unused */
+  RoostDeviceSpan output;      /* [tokens, channels] */
+  RoostDeviceSpan conv_state;  /* pool [slots, channels, width - 1] */
+  RoostDeviceSpan state_slots; /* [batch] int32 */
+  RoostDeviceSpan cu_seqlens;  /* [batch + 1] int32 */
+  uint32_t batch;
+  uint32_t tokens;
+  uint32_t channels;
+  uint32_t width;
+  uint32_t silu;
+  uint32_t reserved0;
+} RoostCausalConv1dParams;
+
+/* Byte copies of slot pairs[i, 0] to slot pairs[i, 1] of pool, slot_bytes each, in pair order (ABI 1.2). */
+typedef struct RoostRecurrentStateCopyParams {
+  uint32_t struct_size;
+  uint32_t abi_minor;
+  RoostDeviceSpan pool;
+  RoostDeviceSpan pairs; /* [count, 2] int32 */
+  uint64_t slot_bytes;
+  uint32_t count;
+  uint32_t reserved0;
+} RoostRecurrentStateCopyParams;
+
+/* pairs[i] = (pool slot, snapshot entry); restore == 0 copies slot to snapshot, else snapshot to slot (ABI 1.2). */
+typedef struct RoostRecurrentStateSnapshotParams {
+  uint32_t struct_size;
+  uint32_t abi_minor;
+  RoostDeviceSpan pool;
+  RoostDeviceSpan snapshots;
+  RoostDeviceSpan pairs; /* [count, 2] int32 */
+  uint64_t slot_bytes;
+  uint32_t count;
+  uint32_t restore;
+} RoostRecurrentStateSnapshotParams;
+
 /* ---- Exports (reference kernels/include/roost_kernels.h:699-711) ---- */
 ROOST_API uint32_t roost_abi_version(void);
 ROOST_API const char* roost_last_error(void); /* never NULL; valid until the next call on this thread */

@@ -32,6 +32,12 @@ RECURRENT_VARIANT = "gated-delta-rule-recurrent-aot"
 CHUNK_VARIANT = "gated-delta-rule-chunk-gfx950"
 ATTENTION_VARIANT = "paged-attention-gfx950"
 CACHE_WRITE_VARIANT = "cache-write-gfx950"
+GATES_VARIANT = "gated-delta-rule-gates-gfx950"
+GATED_RMS_NORM_VARIANT = "gated-rms-norm-gfx950"
+SIGMOID_MUL_VARIANT = "sigmoid-mul-gfx950"
+CAUSAL_CONV1D_VARIANT = "causal-conv1d-gfx950"
+STATE_COPY_VARIANT = "recurrent-state-copy-gfx950"
+STATE_SNAPSHOT_VARIANT = "recurrent-state-snapshot-gfx950"
 
 
 class KernelError(RuntimeError):
@@ -156,7 +162,8 @@ def _torch():
 def dtype_of(t) -> int:
     torch = _torch()
     return {torch.float32: abi.DTYPE_F32, torch.float16: abi.DTYPE_F16, torch.bfloat16: abi.DTYPE_BF16,
-            torch.float64: abi.DTYPE_F64, torch.int32: abi.DTYPE_I32, torch.int64: abi.DTYPE_I64}[t.dtype]
+            torch.float64: abi.DTYPE_F64, torch.int32: abi.DTYPE_I32, torch.int64: abi.DTYPE_I64,
+            torch.uint8: abi.DTYPE_U8}[t.dtype]
 
 
 def span(t, *, length: Optional[int] = None, dtype: Optional[int] = None, offset_elems: int = 0) -> abi.DeviceSpan:
@@ -335,3 +342,83 @@ def gated_delta_rule(session: OpSession, *args, variant: str = RECURRENT_VARIANT
     """CudaOps.GatedDeltaRule runs the recurrent variant for every length; the chunk variant is selectable."""
     p = gated_delta_rule_params(*args, **kwargs)
     session.launch(session.lib.entry(variant), p, key=(p.batch, p.tokens))
+
+
+# ---- the GDN layer's neighbour ops (CudaOps.GatedDeltaRuleGates / GatedRmsNorm / SigmoidMul / CausalConv1d and the
+# recurrent-state copies) ----------------------------------------------------------------------------------------------
+
+def gated_delta_rule_gates_params(a, b, a_log, dt_bias, g, beta, *, tokens, v_heads, a_stride=0, b_stride=0,
+                                  a_len=None, b_len=None, a_offset=0, b_offset=0):
+    """Fills RoostGatedDeltaRuleGatesParams; a and b may be column views of one projection (offset + stride)."""
+    p = abi.new(abi.GatedDeltaRuleGatesParams)
+    p.a = span(a, length=a_len, offset_elems=a_offset)
+    p.b = span(b, length=b_len, offset_elems=b_offset)
+    p.a_log, p.dt_bias, p.g, p.beta = span(a_log), span(dt_bias), span(g), span(beta)
+    p.tokens, p.v_heads, p.a_stride, p.b_stride = tokens, v_heads, a_stride, b_stride
+    p._keep = (a, b, a_log, dt_bias, g, beta)
+    return p
+
+
+def gated_rms_norm_params(x, gate, weight, out, *, rows, dim, eps):
+    p = abi.new(abi.GatedRmsNormParams)
+    p.input, p.gate, p.weight, p.output = span(x), span(gate), span(weight), span(out)
+    p.rows, p.dim, p.eps = rows, dim, eps
+    p._keep = (x, gate, weight, out)
+    return p
+
+
+def sigmoid_mul_params(x, gate, out, *, rows, dim):
+    p = abi.new(abi.SigmoidMulParams)
+    p.input, p.gate, p.output = span(x), span(gate), span(out)
+    p.rows, p.dim = rows, dim
+    p._keep = (x, gate, out)
+    return p
+
+
+def causal_conv1d_params(x, weight, bias, out, conv_state, state_slots, cu_seqlens, *, batch, tokens, channels, width,
+                         silu=True):
+    p = abi.new(abi.CausalConv1dParams)
+    p.input, p.weight, p.bias, p.output = span(x), span(weight), span(bias), span(out)
+    p.conv_state, p.state_slots, p.cu_seqlens = span(conv_state), span(state_slots), span(cu_seqlens)
+    p.batch, p.tokens, p.channels, p.width, p.silu = batch, tokens, channels, width, int(silu)
+    p._keep = (x, weight, bias, out, conv_state, state_slots, cu_seqlens)
+    return p
+
+
+def recurrent_state_copy_params(pool, pairs, *, slot_bytes, count):
+    p = abi.new(abi.RecurrentStateCopyParams)
+    p.pool, p.pairs, p.slot_bytes, p.count = span(pool), span(pairs), slot_bytes, count
+    p._keep = (pool, pairs)
+    return p
+
+
+def recurrent_state_snapshot_params(pool, snapshots, pairs, *, slot_bytes, count, restore):
+    p = abi.new(abi.RecurrentStateSnapshotParams)
+    p.pool, p.snapshots, p.pairs = span(pool), span(snapshots), span(pairs)
+    p.slot_bytes, p.count, p.restore = slot_bytes, count, int(restore)
+    p._keep = (pool, snapshots, pairs)
+    return p
+
+
+def gated_delta_rule_gates(session: OpSession, *args, **kwargs) -> None:
+    session.launch(session.lib.entry(GATES_VARIANT), gated_delta_rule_gates_params(*args, **kwargs))
+
+
+def gated_rms_norm(session: OpSession, *args, **kwargs) -> None:
+    session.launch(session.lib.entry(GATED_RMS_NORM_VARIANT), gated_rms_norm_params(*args, **kwargs))
+
+
+def sigmoid_mul(session: OpSession, *args, **kwargs) -> None:
+    session.launch(session.lib.entry(SIGMOID_MUL_VARIANT), sigmoid_mul_params(*args, **kwargs))
+
+
+def causal_conv1d(session: OpSession, *args, **kwargs) -> None:
+    session.launch(session.lib.entry(CAUSAL_CONV1D_VARIANT), causal_conv1d_params(*args, **kwargs))
+
+
+def recurrent_state_copy(session: OpSession, *args, **kwargs) -> None:
+    session.launch(session.lib.entry(STATE_COPY_VARIANT), recurrent_state_copy_params(*args, **kwargs))
+
+
+def recurrent_state_snapshot(session: OpSession, *args, **kwargs) -> None:
+    session.launch(session.lib.entry(STATE_SNAPSHOT_VARIANT), recurrent_state_snapshot_params(*args, **kwargs))

@@ -19,13 +19,15 @@ STATUS_NAMES = ["OK", "INVALID_ARGUMENT", "UNSUPPORTED", "CUDA_ERROR", "INTERNAL
 
 # Element types
 DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_F64 = 1, 2, 3, 4
-DTYPE_I32, DTYPE_I64 = 10, 12
+DTYPE_U8, DTYPE_I32, DTYPE_I64 = 8, 10, 12
 
 # Layouts
 LAYOUT_ROW_MAJOR, LAYOUT_PAGED_NHD, LAYOUT_PAGED_HND = 0, 2, 3
 
 # Op ids
 OP_PAGED_ATTENTION, OP_CACHE_WRITE, OP_GATED_DELTA_RULE = 4, 11, 128
+OP_CAUSAL_CONV1D, OP_RECURRENT_STATE_COPY, OP_RECURRENT_STATE_SNAPSHOT = 129, 130, 131
+OP_GATED_DELTA_RULE_GATES, OP_GATED_RMS_NORM, OP_SIGMOID_MUL = 133, 134, 135
 
 # Flags
 FLAG_GRAPH_CAPTURABLE, FLAG_DETERMINISTIC, FLAG_BATCH_INVARIANT, FLAG_NEEDS_PLAN, FLAG_PLAN_PER_SHAPE = \
@@ -109,11 +111,49 @@ class GatedDeltaRuleParams(C.Structure):
                 ("use_initial_state", C.c_uint32), ("l2_norm_qk", C.c_uint32), ("scale", C.c_float)]
 
 
+class GatedDeltaRuleGatesParams(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("abi_minor", C.c_uint32), ("a", DeviceSpan), ("b", DeviceSpan),
+                ("a_log", DeviceSpan), ("dt_bias", DeviceSpan), ("g", DeviceSpan), ("beta", DeviceSpan),
+                ("tokens", C.c_uint32), ("v_heads", C.c_uint32), ("a_stride", C.c_uint32), ("b_stride", C.c_uint32)]
+
+
+class GatedRmsNormParams(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("abi_minor", C.c_uint32), ("input", DeviceSpan), ("gate", DeviceSpan),
+                ("weight", DeviceSpan), ("output", DeviceSpan), ("rows", C.c_uint32), ("dim", C.c_uint32),
+                ("eps", C.c_float), ("reserved0", C.c_uint32)]
+
+
+class SigmoidMulParams(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("abi_minor", C.c_uint32), ("input", DeviceSpan), ("gate", DeviceSpan),
+                ("output", DeviceSpan), ("rows", C.c_uint32), ("dim", C.c_uint32)]
+
+
+class CausalConv1dParams(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("abi_minor", C.c_uint32), ("input", DeviceSpan), ("weight", DeviceSpan),
+                ("bias", DeviceSpan), ("output", DeviceSpan), ("conv_state", DeviceSpan), ("state_slots", DeviceSpan),
+                ("cu_seqlens", DeviceSpan), ("batch", C.c_uint32), ("tokens", C.c_uint32), ("channels", C.c_uint32),
+                ("width", C.c_uint32), ("silu", C.c_uint32), ("reserved0", C.c_uint32)]
+
+
+class RecurrentStateCopyParams(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("abi_minor", C.c_uint32), ("pool", DeviceSpan), ("pairs", DeviceSpan),
+                ("slot_bytes", C.c_uint64), ("count", C.c_uint32), ("reserved0", C.c_uint32)]
+
+
+class RecurrentStateSnapshotParams(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("abi_minor", C.c_uint32), ("pool", DeviceSpan), ("snapshots", DeviceSpan),
+                ("pairs", DeviceSpan), ("slot_bytes", C.c_uint64), ("count", C.c_uint32), ("restore", C.c_uint32)]
+
+
 ALL_STRUCTS = {
     "RoostDeviceSpan": DeviceSpan, "RoostWorkspaceSizes": WorkspaceSizes, "RoostWorkspace": Workspace,
     "RoostConstraints": Constraints, "RoostContextCreateParams": ContextCreateParams, "RoostOpEntry": OpEntry,
     "RoostOpTable": OpTable, "RoostPagedAttentionParams": PagedAttentionParams,
     "RoostCacheWriteParams": CacheWriteParams, "RoostGatedDeltaRuleParams": GatedDeltaRuleParams,
+    "RoostGatedDeltaRuleGatesParams": GatedDeltaRuleGatesParams, "RoostGatedRmsNormParams": GatedRmsNormParams,
+    "RoostSigmoidMulParams": SigmoidMulParams, "RoostCausalConv1dParams": CausalConv1dParams,
+    "RoostRecurrentStateCopyParams": RecurrentStateCopyParams,
+    "RoostRecurrentStateSnapshotParams": RecurrentStateSnapshotParams,
 }
 
 

@@ -1,0 +1,613 @@
+// The Gated DeltaNet layer's neighbour ops for gfx950: GatedDeltaRuleGates, GatedRmsNorm, SigmoidMul, CausalConv1d and
+// the recurrent-state copies (ROOST_OP_GATED_DELTA_RULE_GATES, _GATED_RMS_NORM, _SIGMOID_MUL, _CAUSAL_CONV1D,
+// _RECURRENT_STATE_COPY, _RECURRENT_STATE_SNAPSHOT).
+//
+// Semantics: src/Starlings.Roost.Ops/CpuOps.Gating.cs:21-101 and CpuOps.Hybrid.cs:160-263 (the formulas and element
+// types), with the reference entry points' refusal rules (kernels/src/ops/gating.cu:110-268, causal_conv1d.cu:122-175,
+// recurrent_state.cu:58-108). Every element is computed in fp32 and rounded once into its span's type.
+//
+// All of them are HBM-bound streams (a few flops per byte). The kernels read each input element once with 16-byte
+// vector loads where the layout allows, reduce in a fixed order (deterministic and batch invariant: no result depends
+// on another row, token or sequence), allocate nothing and use only the caller's stream (graph capturable).
+
+#include <cmath>
+
+#include "common.h"
+
+namespace {
+
+using namespace roost_dev;
+
+// An element of a span whose type (bf16 or f32) is chosen at run time; the branch is uniform across a launch.
+__device__ __forceinline__ float LoadF(const void* p, uint32_t dt, int64_t i) {
+  return dt == ROOST_DTYPE_BF16 ? Bf16ToF32(static_cast<const uint16_t*>(p)[i]) : static_cast<const float*>(p)[i];
+}
+__device__ __forceinline__ void StoreF(void* p, uint32_t dt, int64_t i, float v) {
+  if (dt == ROOST_DTYPE_BF16) {
+    static_cast<uint16_t*>(p)[i] = F32ToBf16(v);
+  } else {
+    static_cast<float*>(p)[i] = v;
+  }
+}
+
+__device__ __forceinline__ float SigmoidF(float x) { return 1.0f / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float SiluF(float x) { return x / (1.0f + __expf(-x)); }
+
+// ---- GatedDeltaRuleGates -------------------------------------------------------------------------------------------
+// g = -exp(a_log[h]) * softplus(a[t, h] + dt_bias[h]) (softplus(x) = x above 20), beta = sigmoid(b[t, h]). One thread per
+// (token, head); a and b are row-strided column views.
+__global__ void __launch_bounds__(256) GatesKernel(const void* a, const void* b, const void* a_log, const void* dt_bias,
+                                                   void* g, void* beta, uint32_t a_t, uint32_t b_t, uint32_t alog_t,
+                                                   uint32_t dtb_t, uint32_t g_t, uint32_t beta_t, uint64_t total,
+                                                   uint32_t v_heads, uint64_t a_stride, uint64_t b_stride) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const uint64_t t = i / v_heads;
+  const uint32_t h = static_cast<uint32_t>(i - t * v_heads);
+  const float x = LoadF(a, a_t, static_cast<int64_t>(t * a_stride + h)) + LoadF(dt_bias, dtb_t, h);
+  const float sp = x > 20.0f ? x : log1pf(__expf(x));
+  StoreF(g, g_t, static_cast<int64_t>(i), -__expf(LoadF(a_log, alog_t, h)) * sp);
+  StoreF(beta, beta_t, static_cast<int64_t>(i), SigmoidF(LoadF(b, b_t, static_cast<int64_t>(t * b_stride + h))));
+}
+
+// ---- GatedRmsNorm --------------------------------------------------------------------------------------------------
+// out = x * rsqrt(mean(x^2) + eps) * weight * silu(gate) per row. A row is served by G lanes (a power of two, G <= 64),
+// 64 / G rows per wavefront; each lane takes kV consecutive elements at a time (16-byte loads when kVec). The sum of
+// squares is reduced over the G lanes by a fixed xor butterfly.
+// kV consecutive elements of a bf16 or f32 row as floats: one 16-byte load when kVec.
+template <typename T, bool kVec>
+__device__ __forceinline__ void LoadRun(const T* p, uint64_t k, float* v) {
+  constexpr int kV = kVec ? 16 / static_cast<int>(sizeof(T)) : 1;
+  if constexpr (kVec) {
+    const uint4 q = *reinterpret_cast<const uint4*>(p + k);
+    const uint32_t* qw = reinterpret_cast<const uint32_t*>(&q);
+#pragma unroll
+    for (int e = 0; e < kV; ++e) {
+      v[e] = sizeof(T) == 2 ? ((e & 1) ? Bf16HiToF32(qw[e >> 1]) : Bf16LoToF32(qw[e >> 1])) : __uint_as_float(qw[e]);
+    }
+  } else {
+    v[0] = sizeof(T) == 2 ? Bf16ToF32(reinterpret_cast<const uint16_t*>(p)[k]) : reinterpret_cast<const float*>(p)[k];
+  }
+}
+
+template <typename T, bool kVec>
+__device__ __forceinline__ void StoreRun(T* p, uint64_t k, const float* v) {
+  constexpr int kV = kVec ? 16 / static_cast<int>(sizeof(T)) : 1;
+  if constexpr (kVec) {
+    uint4 q;
+    uint32_t* qw = reinterpret_cast<uint32_t*>(&q);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) qw[w] = sizeof(T) == 2 ? PackBf16(v[2 * w], v[2 * w + 1]) : __float_as_uint(v[w]);
+    *reinterpret_cast<uint4*>(p + k) = q;
+  } else if constexpr (sizeof(T) == 2) {
+    reinterpret_cast<uint16_t*>(p)[k] = F32ToBf16(v[0]);
+  } else {
+    reinterpret_cast<float*>(p)[k] = v[0];
+  }
+  (void)kV;
+}
+
+template <typename T, bool kVec>
+__global__ void __launch_bounds__(256) GatedRmsNormKernel(const T* __restrict__ x, const T* __restrict__ gate,
+                                                          const void* __restrict__ weight, uint32_t w_t,
+                                                          T* __restrict__ out, uint64_t rows, uint32_t dim,
+                                                          uint32_t lanes_per_row, float eps) {
+  constexpr int kV = kVec ? 16 / static_cast<int>(sizeof(T)) : 1;
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t sub = lane % lanes_per_row;
+  const uint64_t row = (static_cast<uint64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * (64 / lanes_per_row) +
+                       lane / lanes_per_row;
+  const bool live = row < rows;
+  const uint64_t base = (live ? row : 0) * dim;
+  float ss = 0.0f;
+  for (uint32_t i = sub * kV; i < dim; i += lanes_per_row * kV) {
+    float v[kV];
+    LoadRun<T, kVec>(x, base + i, v);
+#pragma unroll
+    for (int e = 0; e < kV; ++e) ss = fmaf(v[e], v[e], ss);
+  }
+  for (uint32_t m = 1; m < lanes_per_row; m <<= 1) ss += __shfl_xor(ss, static_cast<int>(m), 64);
+  if (!live) return;
+  const float inv = rsqrtf(ss / static_cast<float>(dim) + eps);
+  for (uint32_t i = sub * kV; i < dim; i += lanes_per_row * kV) {
+    float xv[kV], gv[kV], y[kV];
+    LoadRun<T, kVec>(x, base + i, xv);
+    LoadRun<T, kVec>(gate, base + i, gv);
+#pragma unroll
+    for (int e = 0; e < kV; ++e) y[e] = xv[e] * inv * LoadF(weight, w_t, i + e) * SiluF(gv[e]);
+    StoreRun<T, kVec>(out, base + i, y);
+  }
+}
+
+// ---- SigmoidMul ----------------------------------------------------------------------------------------------------
+// out = x * sigmoid(gate), kV elements per step (16-byte loads and stores when kVec), grid-stride.
+template <typename T, bool kVec>
+__global__ void __launch_bounds__(256) SigmoidMulKernel(const T* __restrict__ x, const T* __restrict__ gate,
+                                                        T* __restrict__ out, uint64_t n) {
+  constexpr int kV = kVec ? 16 / static_cast<int>(sizeof(T)) : 1;
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x * kV;
+  for (uint64_t i = (static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * kV; i < n; i += stride) {
+    if constexpr (kVec) {
+      const uint4 xv = *reinterpret_cast<const uint4*>(x + i);
+      const uint4 gv = *reinterpret_cast<const uint4*>(gate + i);
+      uint4 ov;
+      const uint32_t* xw = reinterpret_cast<const uint32_t*>(&xv);
+      const uint32_t* gw = reinterpret_cast<const uint32_t*>(&gv);
+      uint32_t* ow = reinterpret_cast<uint32_t*>(&ov);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        if constexpr (sizeof(T) == 2) {
+          ow[w] = PackBf16(Bf16LoToF32(xw[w]) * SigmoidF(Bf16LoToF32(gw[w])),
+                           Bf16HiToF32(xw[w]) * SigmoidF(Bf16HiToF32(gw[w])));
+        } else {
+          ow[w] = __float_as_uint(__uint_as_float(xw[w]) * SigmoidF(__uint_as_float(gw[w])));
+        }
+      }
+      *reinterpret_cast<uint4*>(out + i) = ov;
+    } else {
+      if constexpr (sizeof(T) == 2) {
+        const uint16_t xv = reinterpret_cast<const uint16_t*>(x)[i], gv = reinterpret_cast<const uint16_t*>(gate)[i];
+        reinterpret_cast<uint16_t*>(out)[i] = F32ToBf16(Bf16ToF32(xv) * SigmoidF(Bf16ToF32(gv)));
+      } else {
+        reinterpret_cast<float*>(out)[i] = reinterpret_cast<const float*>(x)[i] * SigmoidF(reinterpret_cast<const float*>(gate)[i]);
+      }
+    }
+  }
+}
+
+// ---- CausalConv1d --------------------------------------------------------------------------------------------------
+// y_t = bias + sum_j w[c, j] * h_{t + j} over h = [conv state (width - 1, oldest first), the sequence's inputs], SiLU
+// last when set. Workgroup column blockIdx.x is one token; its sequence is found by a binary search of cu_seqlens (uniform,
+// scalar loads). A thread computes kV consecutive channels (8 bf16 / 4 f32 from one 16-byte load per tap when kVec);
+// the taps re-read neighbouring tokens' inputs from cache. A slot outside the pool reads a zero history.
+struct ConvArgs {
+  const void* x;
+  const void* w;
+  const void* bias;  // NULL: none
+  void* y;
+  void* state;
+  const int32_t* slots;
+  const int32_t* cu;
+  uint32_t act_t, state_t;
+  uint32_t batch, tokens, channels, width, silu;
+  uint64_t pool_slots;
+};
+
+__device__ __forceinline__ int32_t SeqOfToken(const int32_t* cu, uint32_t batch, int32_t t) {
+  // The sequence b with cu[b] <= t < cu[b + 1] (empty sequences are skipped by the upper-bound search).
+  uint32_t lo = 0, hi = batch;  // invariant: cu[lo] <= t, answer in [lo, hi)
+  while (hi - lo > 1) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (cu[mid] <= t) lo = mid; else hi = mid;
+  }
+  return static_cast<int32_t>(lo);
+}
+
+template <typename T, bool kVec>
+__global__ void __launch_bounds__(256) ConvKernel(ConvArgs a) {
+  constexpr int kV = kVec ? 16 / static_cast<int>(sizeof(T)) : 1;
+  const int32_t t = static_cast<int32_t>(blockIdx.x);
+  const uint32_t c0 = (blockIdx.y * blockDim.x + threadIdx.x) * kV;
+  if (c0 >= a.channels) return;
+  const int32_t b = SeqOfToken(a.cu, a.batch, t);
+  const int32_t t0 = a.cu[b];
+  if (t < t0 || t >= a.cu[b + 1]) return;  // a token outside every sequence (cu does not cover it): no output
+  const int32_t slot = a.slots[b];
+  const bool has_state = slot >= 0 && static_cast<uint64_t>(slot) < a.pool_slots;
+  const int sl = static_cast<int>(a.width) - 1;
+  const T* x = static_cast<const T*>(a.x);
+  const T* w = static_cast<const T*>(a.w);
+  float acc[kV];
+#pragma unroll
+  for (int e = 0; e < kV; ++e) acc[e] = a.bias != nullptr ? LoadF(a.bias, a.act_t, c0 + e) : 0.0f;
+  const int32_t rel = t - t0;  // h index of this token's first tap is rel
+  for (int j = 0; j < static_cast<int>(a.width); ++j) {
+    const int32_t hi = rel + j;  // index into h = [state, inputs]
+    float hv[kV];
+    if (hi < sl) {
+      const uint64_t so = (static_cast<uint64_t>(has_state ? slot : 0) * a.channels) * sl;
+#pragma unroll
+      for (int e = 0; e < kV; ++e) hv[e] = has_state ? LoadF(a.state, a.state_t, so + (c0 + e) * sl + hi) : 0.0f;
+    } else {
+      const uint64_t xo = static_cast<uint64_t>(t0 + hi - sl) * a.channels + c0;
+      if constexpr (kVec) {
+        const uint4 v = *reinterpret_cast<const uint4*>(x + xo);
+        const uint32_t* vw = reinterpret_cast<const uint32_t*>(&v);
+#pragma unroll
+        for (int e = 0; e < kV; ++e) {
+          hv[e] = sizeof(T) == 2 ? ((e & 1) ? Bf16HiToF32(vw[e >> 1]) : Bf16LoToF32(vw[e >> 1])) : __uint_as_float(vw[e]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < kV; ++e) hv[e] = LoadF(x, a.act_t, xo + e);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < kV; ++e) acc[e] = fmaf(LoadF(w, a.act_t, static_cast<uint64_t>(c0 + e) * a.width + j), hv[e], acc[e]);
+  }
+  const uint64_t yo = static_cast<uint64_t>(t) * a.channels + c0;
+#pragma unroll
+  for (int e = 0; e < kV; ++e) StoreF(a.y, a.act_t, yo + e, a.silu ? SiluF(acc[e]) : acc[e]);
+}
+
+// After ConvKernel (stream order): each (sequence, channel) slot keeps the last width - 1 entries of h. A thread reads
+// them all (some may be old state entries) before writing any.
+__global__ void __launch_bounds__(256) ConvStateKernel(ConvArgs a) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= static_cast<uint64_t>(a.batch) * a.channels) return;
+  const uint32_t b = static_cast<uint32_t>(i / a.channels);
+  const uint32_t c = static_cast<uint32_t>(i - static_cast<uint64_t>(b) * a.channels);
+  const int32_t t0 = a.cu[b], t1 = a.cu[b + 1];
+  const int32_t n = t1 - t0;
+  const int32_t slot = a.slots[b];
+  if (n <= 0 || slot < 0 || static_cast<uint64_t>(slot) >= a.pool_slots) return;  // untouched
+  const int sl = static_cast<int>(a.width) - 1;
+  const uint64_t so = (static_cast<uint64_t>(slot) * a.channels + c) * sl;
+  float next[15];
+#pragma unroll
+  for (int j = 0; j < 15; ++j) {
+    if (j < sl) {
+      const int32_t hi = n + j;
+      next[j] = hi < sl ? LoadF(a.state, a.state_t, so + hi)
+                        : LoadF(a.x, a.act_t, static_cast<uint64_t>(t0 + hi - sl) * a.channels + c);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 15; ++j) {
+    if (j < sl) StoreF(a.state, a.state_t, so + j, next[j]);
+  }
+}
+
+// ---- Recurrent-state copies ----------------------------------------------------------------------------------------
+// Word w of every pair, pairs in order (so a later pair sees an earlier pair's write of the same word). from/to slots
+// outside their pool (when its size is known) are skipped.
+template <typename W>
+__global__ void __launch_bounds__(256) CopyPairsKernel(const unsigned char* src, unsigned char* dst, const int32_t* pairs,
+                                                       uint32_t count, uint64_t slot_bytes, uint32_t swap,
+                                                       uint64_t src_slots, uint64_t dst_slots) {
+  const uint64_t words = slot_bytes / sizeof(W);
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  for (uint64_t w = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; w < words; w += stride) {
+    for (uint32_t i = 0; i < count; ++i) {
+      const int32_t from = pairs[2 * i + swap], to = pairs[2 * i + 1 - swap];
+      if (from < 0 || to < 0 || static_cast<uint64_t>(from) >= src_slots || static_cast<uint64_t>(to) >= dst_slots) continue;
+      reinterpret_cast<W*>(dst + static_cast<uint64_t>(to) * slot_bytes)[w] =
+          reinterpret_cast<const W*>(src + static_cast<uint64_t>(from) * slot_bytes)[w];
+    }
+  }
+}
+
+bool FloatType(uint32_t dt) { return dt == ROOST_DTYPE_BF16 || dt == ROOST_DTYPE_F32; }
+uint64_t ElemBytes(uint32_t dt) { return dt == ROOST_DTYPE_BF16 ? 2 : 4; }
+bool Natural(const RoostDeviceSpan& s) { return roost::Aligned(s.address, ElemBytes(s.dtype)); }
+
+// A span used for `elems` elements of its own type: reserved zero, non-NULL when needed, long enough.
+bool SpanOkOwn(const RoostDeviceSpan& s, uint64_t elems) {
+  return s.reserved0 == 0 && s.length >= elems && (elems == 0 || s.address != nullptr);
+}
+bool SpanOkAs(const RoostDeviceSpan& s, uint32_t dt, uint64_t elems) { return s.dtype == dt && SpanOkOwn(s, elems); }
+
+uintptr_t Addr(const RoostDeviceSpan& s) { return reinterpret_cast<uintptr_t>(s.address); }
+bool AnyOverlap(const RoostDeviceSpan& x, uint64_t xn, const RoostDeviceSpan& y, uint64_t yn) {
+  return Addr(x) < Addr(y) + yn * ElemBytes(y.dtype) && Addr(y) < Addr(x) + xn * ElemBytes(x.dtype);
+}
+bool PartialOverlap(const RoostDeviceSpan& x, uint64_t xn, const RoostDeviceSpan& y, uint64_t yn) {
+  return Addr(x) != Addr(y) && AnyOverlap(x, xn, y, yn);
+}
+
+uint32_t Blocks(uint64_t items, uint32_t per_block) { return static_cast<uint32_t>(roost::CeilDiv(items, per_block)); }
+
+}  // namespace
+
+// ---- Entry points ---------------------------------------------------------------------------------------------------
+
+extern "C" ROOST_API RoostStatus roost_gated_delta_rule_gates_run(RoostContext* ctx, const void* params,
+                                                                   const RoostWorkspace*, void* stream) {
+  using namespace roost;
+  constexpr char kOp[] = "GatedDeltaRuleGates";
+  if (ctx == nullptr || params == nullptr) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRuleGates: ctx or params is NULL");
+  ROOST_TRY(CheckHeader(params, sizeof(RoostGatedDeltaRuleGatesParams), kOp));
+  const auto& p = *static_cast<const RoostGatedDeltaRuleGatesParams*>(params);
+  return Guarded(kOp, [&]() -> RoostStatus {
+    if (p.v_heads == 0 || p.v_heads > 0x7fffffffu) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRuleGates: v_heads must be in [1, 2^31 - 1]");
+    }
+    if (p.tokens == 0) return ROOST_STATUS_OK;
+    const uint64_t vh = p.v_heads;
+    const uint64_t as = p.a_stride == 0 ? vh : p.a_stride, bs = p.b_stride == 0 ? vh : p.b_stride;
+    if (as < vh || bs < vh) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRuleGates: a_stride or b_stride is below v_heads");
+    const RoostDeviceSpan* all[] = {&p.a, &p.b, &p.a_log, &p.dt_bias, &p.g, &p.beta};
+    for (const RoostDeviceSpan* s : all) {
+      if (!FloatType(s->dtype)) return Fail(ROOST_STATUS_UNSUPPORTED, "GatedDeltaRuleGates: every span must be bf16 or f32");
+    }
+    const uint64_t total = uint64_t{p.tokens} * vh;
+    const uint64_t a_reach = (p.tokens - 1ull) * as + vh, b_reach = (p.tokens - 1ull) * bs + vh;
+    if (!SpanOkOwn(p.a, a_reach) || !SpanOkOwn(p.b, b_reach) || !SpanOkOwn(p.a_log, vh) || !SpanOkOwn(p.dt_bias, vh) ||
+        !SpanOkOwn(p.g, total) || !SpanOkOwn(p.beta, total)) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRuleGates: a span is too short, has a NULL address or reserved0 set");
+    }
+    for (const RoostDeviceSpan* s : all) {
+      if (!Natural(*s)) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRuleGates: a span is not aligned to its element size");
+    }
+    // g and beta are outputs with no in-place form: they may overlap nothing (element sizes and strides can differ).
+    if (AnyOverlap(p.g, total, p.beta, total) || AnyOverlap(p.g, total, p.a, a_reach) || AnyOverlap(p.g, total, p.b, b_reach) ||
+        AnyOverlap(p.g, total, p.a_log, vh) || AnyOverlap(p.g, total, p.dt_bias, vh) ||
+        AnyOverlap(p.beta, total, p.a, a_reach) || AnyOverlap(p.beta, total, p.b, b_reach) ||
+        AnyOverlap(p.beta, total, p.a_log, vh) || AnyOverlap(p.beta, total, p.dt_bias, vh)) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT,
+                  "GatedDeltaRuleGates: g and beta must not overlap each other or any input (no in-place form, even from the same address)");
+    }
+    if (total > (uint64_t{1} << 40)) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRuleGates: too many elements for one call");
+    hipLaunchKernelGGL(GatesKernel, dim3(Blocks(total, 256)), dim3(256), 0, Stream(stream), p.a.address, p.b.address,
+                       p.a_log.address, p.dt_bias.address, p.g.address, p.beta.address, p.a.dtype, p.b.dtype,
+                       p.a_log.dtype, p.dt_bias.dtype, p.g.dtype, p.beta.dtype, total, p.v_heads, as, bs);
+    return FromHip(hipGetLastError(), "GatedDeltaRuleGates launch");
+  });
+}
+
+extern "C" ROOST_API RoostStatus roost_gated_rms_norm_run(RoostContext* ctx, const void* params, const RoostWorkspace*,
+                                                           void* stream) {
+  using namespace roost;
+  constexpr char kOp[] = "GatedRmsNorm";
+  if (ctx == nullptr || params == nullptr) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedRmsNorm: ctx or params is NULL");
+  ROOST_TRY(CheckHeader(params, sizeof(RoostGatedRmsNormParams), kOp));
+  const auto& p = *static_cast<const RoostGatedRmsNormParams*>(params);
+  return Guarded(kOp, [&]() -> RoostStatus {
+    if (p.reserved0 != 0) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedRmsNorm: reserved0 must be zero");
+    if (!std::isfinite(p.eps) || p.eps < 0.0f) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedRmsNorm: eps must be finite and non-negative");
+    }
+    if (p.dim == 0 || p.dim > 0x7fffffffu || p.rows > 0x7fffffffu) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedRmsNorm: dim must be in [1, 2^31 - 1] and rows at most 2^31 - 1");
+    }
+    if (p.rows == 0) return ROOST_STATUS_OK;
+    const uint32_t act = p.input.dtype;
+    if (!FloatType(act) || !FloatType(p.weight.dtype)) {
+      return Fail(ROOST_STATUS_UNSUPPORTED, "GatedRmsNorm: activations and weight must be bf16 or f32");
+    }
+    const uint64_t n = uint64_t{p.rows} * p.dim;
+    if (!SpanOkAs(p.input, act, n) || !SpanOkAs(p.gate, act, n) || !SpanOkAs(p.output, act, n) ||
+        !SpanOkOwn(p.weight, p.dim)) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT,
+                  "GatedRmsNorm: a span has the wrong dtype, is too short, has a NULL address or reserved0 set");
+    }
+    if (!Natural(p.input) || !Natural(p.gate) || !Natural(p.output) || !Natural(p.weight)) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedRmsNorm: a span is not aligned to its element size");
+    }
+    if (PartialOverlap(p.output, n, p.input, n) || PartialOverlap(p.output, n, p.gate, n)) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedRmsNorm: output may alias input or gate only from the same address");
+    }
+    const uint32_t v = 16 / static_cast<uint32_t>(ElemBytes(act));
+    const bool vec = p.dim % v == 0 && Aligned(p.input.address, 16) && Aligned(p.gate.address, 16) &&
+                     Aligned(p.output.address, 16);
+    // Lanes per row: enough for one vector each, a power of two up to 64.
+    const uint32_t per_lane = vec ? v : 1;
+    uint32_t lanes = 1;
+    while (lanes < 64 && lanes * per_lane < p.dim) lanes <<= 1;
+    const uint64_t rows_per_block = 4ull * (64 / lanes);
+    const dim3 grid(Blocks(p.rows, static_cast<uint32_t>(rows_per_block)));
+    hipStream_t s = Stream(stream);
+    if (act == ROOST_DTYPE_BF16) {
+      const auto* x = static_cast<const uint16_t*>(p.input.address);
+      const auto* g = static_cast<const uint16_t*>(p.gate.address);
+      auto* o = static_cast<uint16_t*>(p.output.address);
+      if (vec) {
+        hipLaunchKernelGGL((GatedRmsNormKernel<uint16_t, true>), grid, dim3(256), 0, s, x, g, p.weight.address,
+                           p.weight.dtype, o, uint64_t{p.rows}, p.dim, lanes, p.eps);
+      } else {
+        hipLaunchKernelGGL((GatedRmsNormKernel<uint16_t, false>), grid, dim3(256), 0, s, x, g, p.weight.address,
+                           p.weight.dtype, o, uint64_t{p.rows}, p.dim, lanes, p.eps);
+      }
+    } else {
+      const auto* x = static_cast<const float*>(p.input.address);
+      const auto* g = static_cast<const float*>(p.gate.address);
+      auto* o = static_cast<float*>(p.output.address);
+      if (vec) {
+        hipLaunchKernelGGL((GatedRmsNormKernel<float, true>), grid, dim3(256), 0, s, x, g, p.weight.address,
+                           p.weight.dtype, o, uint64_t{p.rows}, p.dim, lanes, p.eps);
+      } else {
+        hipLaunchKernelGGL((GatedRmsNormKernel<float, false>), grid, dim3(256), 0, s, x, g, p.weight.address,
+                           p.weight.dtype, o, uint64_t{p.rows}, p.dim, lanes, p.eps);
+      }
+    }
+    return FromHip(hipGetLastError(), "GatedRmsNorm launch");
+  });
+}
+
+extern "C" ROOST_API RoostStatus roost_sigmoid_mul_run(RoostContext* ctx, const void* params, const RoostWorkspace*,
+                                                        void* stream) {
+  using namespace roost;
+  constexpr char kOp[] = "SigmoidMul";
+  if (ctx == nullptr || params == nullptr) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "SigmoidMul: ctx or params is NULL");
+  ROOST_TRY(CheckHeader(params, sizeof(RoostSigmoidMulParams), kOp));
+  const auto& p = *static_cast<const RoostSigmoidMulParams*>(params);
+  return Guarded(kOp, [&]() -> RoostStatus {
+    const uint64_t n = uint64_t{p.rows} * p.dim;
+    if (n == 0) return ROOST_STATUS_OK;
+    const uint32_t act = p.input.dtype;
+    if (!FloatType(act)) return Fail(ROOST_STATUS_UNSUPPORTED, "SigmoidMul: activations must be bf16 or f32");
+    if (!SpanOkAs(p.input, act, n) || !SpanOkAs(p.gate, act, n) || !SpanOkAs(p.output, act, n)) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT,
+                  "SigmoidMul: a span has the wrong dtype, is too short, has a NULL address or reserved0 set");
+    }
+    if (!Natural(p.input) || !Natural(p.gate) || !Natural(p.output)) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "SigmoidMul: a span is not aligned to its element size");
+    }
+    if (PartialOverlap(p.output, n, p.input, n) || PartialOverlap(p.output, n, p.gate, n)) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "SigmoidMul: output may alias input or gate only from the same address");
+    }
+    const uint64_t v = 16 / ElemBytes(act);
+    const bool vec = n % v == 0 && Aligned(p.input.address, 16) && Aligned(p.gate.address, 16) && Aligned(p.output.address, 16);
+    const uint64_t steps = vec ? n / v : n;
+    const dim3 grid(static_cast<uint32_t>(std::min<uint64_t>(roost::CeilDiv(steps, 256), 65536)));
+    hipStream_t s = Stream(stream);
+    if (act == ROOST_DTYPE_BF16) {
+      const auto* x = static_cast<const uint16_t*>(p.input.address);
+      const auto* g = static_cast<const uint16_t*>(p.gate.address);
+      auto* o = static_cast<uint16_t*>(p.output.address);
+      if (vec) hipLaunchKernelGGL((SigmoidMulKernel<uint16_t, true>), grid, dim3(256), 0, s, x, g, o, n);
+      else hipLaunchKernelGGL((SigmoidMulKernel<uint16_t, false>), grid, dim3(256), 0, s, x, g, o, n);
+    } else {
+      const auto* x = static_cast<const float*>(p.input.address);
+      const auto* g = static_cast<const float*>(p.gate.address);
+      auto* o = static_cast<float*>(p.output.address);
+      if (vec) hipLaunchKernelGGL((SigmoidMulKernel<float, true>), grid, dim3(256), 0, s, x, g, o, n);
+      else hipLaunchKernelGGL((SigmoidMulKernel<float, false>), grid, dim3(256), 0, s, x, g, o, n);
+    }
+    return FromHip(hipGetLastError(), "SigmoidMul launch");
+  });
+}
+
+extern "C" ROOST_API RoostStatus roost_causal_conv1d_run(RoostContext* ctx, const void* params, const RoostWorkspace*,
+                                                          void* stream) {
+  using namespace roost;
+  constexpr char kOp[] = "CausalConv1d";
+  if (ctx == nullptr || params == nullptr) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "CausalConv1d: ctx or params is NULL");
+  ROOST_TRY(CheckHeader(params, sizeof(RoostCausalConv1dParams), kOp));
+  const auto& p = *static_cast<const RoostCausalConv1dParams*>(params);
+  return Guarded(kOp, [&]() -> RoostStatus {
+    if (p.reserved0 != 0) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "CausalConv1d: reserved0 must be zero");
+    if (p.width < 1 || p.width > 16 || p.channels == 0) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "CausalConv1d: width must be in [1, 16] and channels non-zero");
+    }
+    if (p.channels > 65535u * 128u || p.tokens > 0x7fffffffu || p.batch > 0x7fffffffu) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "CausalConv1d: too many channels, tokens or sequences for one call");
+    }
+    if (p.batch == 0 || p.tokens == 0) return ROOST_STATUS_OK;
+    const uint32_t act = p.input.dtype;
+    if (!FloatType(act)) return Fail(ROOST_STATUS_UNSUPPORTED, "CausalConv1d: activation dtype must be bf16 or f32");
+    const uint32_t st = p.conv_state.dtype == ROOST_DTYPE_UNDEFINED ? act : p.conv_state.dtype;
+    if (!FloatType(st)) return Fail(ROOST_STATUS_UNSUPPORTED, "CausalConv1d: conv state dtype must be bf16 or f32");
+    const uint64_t sl = p.width - 1ull;
+    const uint64_t n = uint64_t{p.tokens} * p.channels;
+    const bool has_bias = p.bias.address != nullptr;
+    if (!SpanOkAs(p.input, act, n) || !SpanOkAs(p.output, act, n) ||
+        !SpanOkAs(p.weight, act, uint64_t{p.channels} * p.width) || (has_bias && !SpanOkAs(p.bias, act, p.channels)) ||
+        !SpanOkAs(p.state_slots, ROOST_DTYPE_I32, p.batch) || !SpanOkAs(p.cu_seqlens, ROOST_DTYPE_I32, p.batch + 1ull)) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "CausalConv1d: a span has the wrong dtype, is too short or has a NULL address");
+    }
+    if (sl > 0 && (p.conv_state.reserved0 != 0 || p.conv_state.address == nullptr)) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "CausalConv1d: conv_state is NULL");
+    }
+    if (p.input.address == p.output.address || AnyOverlap(p.input, n, p.output, n)) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "CausalConv1d: input and output must not alias");
+    }
+    if (!Natural(p.input) || !Natural(p.output) || !Natural(p.weight) || (has_bias && !Natural(p.bias)) ||
+        (sl > 0 && !Aligned(p.conv_state.address, ElemBytes(st))) || !Aligned(p.state_slots.address, 4) ||
+        !Aligned(p.cu_seqlens.address, 4)) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "CausalConv1d: a span is not aligned to its element size");
+    }
+    ConvArgs a{};
+    a.x = p.input.address;
+    a.w = p.weight.address;
+    a.bias = has_bias ? p.bias.address : nullptr;
+    a.y = p.output.address;
+    a.state = p.conv_state.address;
+    a.slots = static_cast<const int32_t*>(p.state_slots.address);
+    a.cu = static_cast<const int32_t*>(p.cu_seqlens.address);
+    a.act_t = act;
+    a.state_t = st;
+    a.batch = p.batch;
+    a.tokens = p.tokens;
+    a.channels = p.channels;
+    a.width = p.width;
+    a.silu = p.silu != 0;
+    // Slots the pool holds; the state span's length is in its own elements (a zero length means no slot is valid).
+    a.pool_slots = sl == 0 ? 0 : p.conv_state.length / (uint64_t{p.channels} * sl);
+    const uint64_t v = 16 / ElemBytes(act);
+    const bool vec = p.channels % v == 0 && Aligned(p.input.address, 16);
+    const uint32_t per_thread = vec ? static_cast<uint32_t>(v) : 1u;
+    const dim3 grid(p.tokens, Blocks(roost::CeilDiv(p.channels, per_thread), 256));
+    hipStream_t s = Stream(stream);
+    if (act == ROOST_DTYPE_BF16) {
+      if (vec) hipLaunchKernelGGL((ConvKernel<uint16_t, true>), grid, dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((ConvKernel<uint16_t, false>), grid, dim3(256), 0, s, a);
+    } else {
+      if (vec) hipLaunchKernelGGL((ConvKernel<float, true>), grid, dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((ConvKernel<float, false>), grid, dim3(256), 0, s, a);
+    }
+    ROOST_TRY(FromHip(hipGetLastError(), "CausalConv1d launch"));
+    if (sl == 0) return ROOST_STATUS_OK;
+    hipLaunchKernelGGL(ConvStateKernel, dim3(Blocks(uint64_t{p.batch} * p.channels, 256)), dim3(256), 0, s, a);
+    return FromHip(hipGetLastError(), "CausalConv1d state launch");
+  });
+}
+
+namespace {
+
+RoostStatus LaunchCopyPairs(const void* src, uint64_t src_bytes, void* dst, uint64_t dst_bytes, const RoostDeviceSpan& pairs,
+                            uint64_t slot_bytes, uint32_t count, uint32_t swap, hipStream_t stream) {
+  using roost::Aligned;
+  const auto* s = static_cast<const unsigned char*>(src);
+  auto* d = static_cast<unsigned char*>(dst);
+  const auto* pr = static_cast<const int32_t*>(pairs.address);
+  // Pool sizes in slots; an unknown size (length 0) leaves the slots unchecked, as the reference does.
+  const uint64_t src_slots = src_bytes == 0 ? ~uint64_t{0} : src_bytes / slot_bytes;
+  const uint64_t dst_slots = dst_bytes == 0 ? ~uint64_t{0} : dst_bytes / slot_bytes;
+  const bool wide = slot_bytes % 16 == 0 && Aligned(s, 16) && Aligned(d, 16);
+  const bool word = slot_bytes % 4 == 0 && Aligned(s, 4) && Aligned(d, 4);
+  const uint64_t unit = wide ? 16 : (word ? 4 : 1);
+  const uint32_t blocks = static_cast<uint32_t>(std::min<uint64_t>(roost::CeilDiv(slot_bytes / unit, 256), 4096));
+  if (wide) {
+    hipLaunchKernelGGL(CopyPairsKernel<uint4>, dim3(blocks), dim3(256), 0, stream, s, d, pr, count, slot_bytes, swap,
+                       src_slots, dst_slots);
+  } else if (word) {
+    hipLaunchKernelGGL(CopyPairsKernel<uint32_t>, dim3(blocks), dim3(256), 0, stream, s, d, pr, count, slot_bytes, swap,
+                       src_slots, dst_slots);
+  } else {
+    hipLaunchKernelGGL(CopyPairsKernel<unsigned char>, dim3(blocks), dim3(256), 0, stream, s, d, pr, count, slot_bytes,
+                       swap, src_slots, dst_slots);
+  }
+  return roost::FromHip(hipGetLastError(), "recurrent-state copy launch");
+}
+
+uint64_t SpanBytes(const RoostDeviceSpan& s) {
+  const uint32_t eb = s.dtype == ROOST_DTYPE_UNDEFINED ? 1 : roost::DtypeBytes(s.dtype);
+  return s.length * eb;
+}
+
+bool PoolOk(const RoostDeviceSpan& s) { return s.reserved0 == 0 && s.address != nullptr; }
+
+}  // namespace
+
+extern "C" ROOST_API RoostStatus roost_recurrent_state_copy_run(RoostContext* ctx, const void* params,
+                                                                 const RoostWorkspace*, void* stream) {
+  using namespace roost;
+  constexpr char kOp[] = "RecurrentStateCopy";
+  if (ctx == nullptr || params == nullptr) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "RecurrentStateCopy: ctx or params is NULL");
+  ROOST_TRY(CheckHeader(params, sizeof(RoostRecurrentStateCopyParams), kOp));
+  const auto& p = *static_cast<const RoostRecurrentStateCopyParams*>(params);
+  return Guarded(kOp, [&]() -> RoostStatus {
+    if (p.reserved0 != 0) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "RecurrentStateCopy: reserved0 must be zero");
+    if (p.count == 0 || p.slot_bytes == 0) return ROOST_STATUS_OK;
+    if (!PoolOk(p.pool) || !SpanOkAs(p.pairs, ROOST_DTYPE_I32, uint64_t{p.count} * 2) || !Aligned(p.pairs.address, 4)) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "RecurrentStateCopy: pool is NULL, or pairs is not a long enough int32 span");
+    }
+    const uint64_t bytes = SpanBytes(p.pool);
+    return LaunchCopyPairs(p.pool.address, bytes, p.pool.address, bytes, p.pairs, p.slot_bytes, p.count, 0, Stream(stream));
+  });
+}
+
+extern "C" ROOST_API RoostStatus roost_recurrent_state_snapshot_run(RoostContext* ctx, const void* params,
+                                                                     const RoostWorkspace*, void* stream) {
+  using namespace roost;
+  constexpr char kOp[] = "RecurrentStateSnapshot";
+  if (ctx == nullptr || params == nullptr) {
+    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "RecurrentStateSnapshot: ctx or params is NULL");
+  }
+  ROOST_TRY(CheckHeader(params, sizeof(RoostRecurrentStateSnapshotParams), kOp));
+  const auto& p = *static_cast<const RoostRecurrentStateSnapshotParams*>(params);
+  return Guarded(kOp, [&]() -> RoostStatus {
+    if (p.count == 0 || p.slot_bytes == 0) return ROOST_STATUS_OK;
+    if (!PoolOk(p.pool) || !PoolOk(p.snapshots) || !SpanOkAs(p.pairs, ROOST_DTYPE_I32, uint64_t{p.count} * 2) ||
+        !Aligned(p.pairs.address, 4)) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT,
+                  "RecurrentStateSnapshot: pool or snapshots is NULL, or pairs is not a long enough int32 span");
+    }
+    const bool restore = p.restore != 0;
+    const RoostDeviceSpan& src = restore ? p.snapshots : p.pool;
+    const RoostDeviceSpan& dst = restore ? p.pool : p.snapshots;
+    return LaunchCopyPairs(src.address, SpanBytes(src), dst.address, SpanBytes(dst), p.pairs, p.slot_bytes, p.count,
+                           restore ? 1u : 0u, Stream(stream));
+  });
+}

@@ -35,6 +35,20 @@ static_assert(sizeof(RoostGatedDeltaRuleParams) == 280 && offsetof(RoostGatedDel
                   offsetof(RoostGatedDeltaRuleParams, scale) == 276,
               "RoostGatedDeltaRuleParams layout");
 
+static_assert(sizeof(RoostGatedDeltaRuleGatesParams) == 168 && offsetof(RoostGatedDeltaRuleGatesParams, tokens) == 152,
+              "RoostGatedDeltaRuleGatesParams layout");
+static_assert(sizeof(RoostGatedRmsNormParams) == 120 && offsetof(RoostGatedRmsNormParams, eps) == 112,
+              "RoostGatedRmsNormParams layout");
+static_assert(sizeof(RoostSigmoidMulParams) == 88 && offsetof(RoostSigmoidMulParams, rows) == 80, "RoostSigmoidMulParams layout");
+static_assert(sizeof(RoostCausalConv1dParams) == 200 && offsetof(RoostCausalConv1dParams, batch) == 176 &&
+                  offsetof(RoostCausalConv1dParams, silu) == 192,
+              "RoostCausalConv1dParams layout");
+static_assert(sizeof(RoostRecurrentStateCopyParams) == 72 && offsetof(RoostRecurrentStateCopyParams, slot_bytes) == 56,
+              "RoostRecurrentStateCopyParams layout");
+static_assert(sizeof(RoostRecurrentStateSnapshotParams) == 96 &&
+                  offsetof(RoostRecurrentStateSnapshotParams, restore) == 92,
+              "RoostRecurrentStateSnapshotParams layout");
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -85,6 +99,15 @@ RoostConstraints GdnConstraints() {
   return c;
 }
 
+// The GDN layer's elementwise and row ops: bf16 or f32 activations, row-major, element alignment.
+RoostConstraints PlainConstraints(uint64_t act_mask, uint32_t alignment) {
+  RoostConstraints c = BaseConstraints();
+  c.act_dtype_mask = act_mask;
+  c.layout_mask = 1u << ROOST_LAYOUT_ROW_MAJOR;
+  c.min_alignment = alignment;
+  return c;
+}
+
 RoostOpEntry Entry(uint32_t op, uint32_t flags, const char* id, uint32_t params_size, const RoostConstraints& c,
                    RoostRunFn run, RoostPlanFn plan, RoostWorkspaceFn workspace) {
   RoostOpEntry e{};
@@ -101,6 +124,7 @@ RoostOpEntry Entry(uint32_t op, uint32_t flags, const char* id, uint32_t params_
 }
 
 constexpr uint32_t kDet = ROOST_FLAG_DETERMINISTIC | ROOST_FLAG_BATCH_INVARIANT;
+constexpr uint64_t kBf16F32 = DtypeBit(ROOST_DTYPE_BF16) | DtypeBit(ROOST_DTYPE_F32);
 
 const RoostOpEntry* Entries(uint32_t* count) {
   static const RoostOpEntry entries[] = {
@@ -115,6 +139,21 @@ const RoostOpEntry* Entries(uint32_t* count) {
       Entry(ROOST_OP_GATED_DELTA_RULE, kDet | ROOST_FLAG_GRAPH_CAPTURABLE, "gated-delta-rule-recurrent-aot",
             sizeof(RoostGatedDeltaRuleParams), GdnConstraints(), roost_gdn_recurrent_run, nullptr,
             roost_gdn_recurrent_workspace),
+      Entry(ROOST_OP_CAUSAL_CONV1D, kDet | ROOST_FLAG_GRAPH_CAPTURABLE, "causal-conv1d-gfx950",
+            sizeof(RoostCausalConv1dParams), PlainConstraints(kBf16F32, 4), roost_causal_conv1d_run, nullptr, nullptr),
+      Entry(ROOST_OP_RECURRENT_STATE_COPY, kDet | ROOST_FLAG_GRAPH_CAPTURABLE, "recurrent-state-copy-gfx950",
+            sizeof(RoostRecurrentStateCopyParams), PlainConstraints(0, 1), roost_recurrent_state_copy_run, nullptr,
+            nullptr),
+      Entry(ROOST_OP_RECURRENT_STATE_SNAPSHOT, kDet | ROOST_FLAG_GRAPH_CAPTURABLE, "recurrent-state-snapshot-gfx950",
+            sizeof(RoostRecurrentStateSnapshotParams), PlainConstraints(0, 1), roost_recurrent_state_snapshot_run,
+            nullptr, nullptr),
+      Entry(ROOST_OP_GATED_DELTA_RULE_GATES, kDet | ROOST_FLAG_GRAPH_CAPTURABLE, "gated-delta-rule-gates-gfx950",
+            sizeof(RoostGatedDeltaRuleGatesParams), PlainConstraints(kBf16F32, 4), roost_gated_delta_rule_gates_run,
+            nullptr, nullptr),
+      Entry(ROOST_OP_GATED_RMS_NORM, kDet | ROOST_FLAG_GRAPH_CAPTURABLE, "gated-rms-norm-gfx950",
+            sizeof(RoostGatedRmsNormParams), PlainConstraints(kBf16F32, 4), roost_gated_rms_norm_run, nullptr, nullptr),
+      Entry(ROOST_OP_SIGMOID_MUL, kDet | ROOST_FLAG_GRAPH_CAPTURABLE, "sigmoid-mul-gfx950", sizeof(RoostSigmoidMulParams),
+            PlainConstraints(kBf16F32, 4), roost_sigmoid_mul_run, nullptr, nullptr),
   };
   *count = static_cast<uint32_t>(sizeof(entries) / sizeof(entries[0]));
   return entries;

@@ -53,7 +53,9 @@ def test_library_exports_every_declared_symbol(kernels):
     declared = declared_symbols()
     assert {"roost_abi_version", "roost_last_error", "roost_register", "roost_context_create",
             "roost_context_destroy", "roost_paged_attention_run", "roost_cache_write_run", "roost_gdn_chunk_run",
-            "roost_gdn_recurrent_run"} <= declared
+            "roost_gdn_recurrent_run", "roost_gated_delta_rule_gates_run", "roost_gated_rms_norm_run",
+            "roost_sigmoid_mul_run", "roost_causal_conv1d_run", "roost_recurrent_state_copy_run",
+            "roost_recurrent_state_snapshot_run"} <= declared
     assert declared <= exported, declared - exported
 
 
@@ -66,7 +68,20 @@ def test_abi_version_and_table(kernels):
     # The worker names the recurrent GDN variant by id (reference CudaOps.cs:28).
     assert roost_amd.RECURRENT_VARIANT == "gated-delta-rule-recurrent-aot"
     assert set(ids) == {roost_amd.ATTENTION_VARIANT, roost_amd.CACHE_WRITE_VARIANT, roost_amd.CHUNK_VARIANT,
-                        roost_amd.RECURRENT_VARIANT}
+                        roost_amd.RECURRENT_VARIANT, roost_amd.GATES_VARIANT, roost_amd.GATED_RMS_NORM_VARIANT,
+                        roost_amd.SIGMOID_MUL_VARIANT, roost_amd.CAUSAL_CONV1D_VARIANT, roost_amd.STATE_COPY_VARIANT,
+                        roost_amd.STATE_SNAPSHOT_VARIANT}
+    # The GDN layer's neighbour ops: graph capturable, deterministic, batch invariant, no plan, no workspace.
+    for vid, op, size in [(roost_amd.GATES_VARIANT, abi.OP_GATED_DELTA_RULE_GATES, 168),
+                          (roost_amd.GATED_RMS_NORM_VARIANT, abi.OP_GATED_RMS_NORM, 120),
+                          (roost_amd.SIGMOID_MUL_VARIANT, abi.OP_SIGMOID_MUL, 88),
+                          (roost_amd.CAUSAL_CONV1D_VARIANT, abi.OP_CAUSAL_CONV1D, 200),
+                          (roost_amd.STATE_COPY_VARIANT, abi.OP_RECURRENT_STATE_COPY, 72),
+                          (roost_amd.STATE_SNAPSHOT_VARIANT, abi.OP_RECURRENT_STATE_SNAPSHOT, 96)]:
+        e = ids[vid]
+        assert e.op == op and e.params_struct_size == size and e.plan is None and e.workspace is None
+        assert e.flags == abi.FLAG_GRAPH_CAPTURABLE | abi.FLAG_DETERMINISTIC | abi.FLAG_BATCH_INVARIANT
+        assert e.constraints.sm_min == 950
     att = ids[roost_amd.ATTENTION_VARIANT]
     assert att.op == abi.OP_PAGED_ATTENTION and att.needs_plan and att.params_struct_size == 296
     assert att.constraints.sm_min == 950 and att.constraints.group_size_mask == 1 << 3
