@@ -275,6 +275,55 @@ def bench_mixed(torch, roost_amd, session, steps, warmup):
             "tokens": T}
 
 
+def bench_layer_ops(torch, roost_amd, session, steps, warmup):
+    """The GDN layer's neighbour ops at Qwen3.5 shapes over config 4's 4 x 4096 tokens (HBM-bound; bytes are each op's
+    reads and writes once): CausalConv1d over the [tokens, 6144] q/k/v projection (width 4, SiLU, bf16 state),
+    GatedDeltaRuleGates (16 heads, a and b columns of a [tokens, 32] projection), GatedRmsNorm (16 x 128 per token,
+    f32 weight), SigmoidMul (the attention output gate, 8 x 256 per token) and RecurrentStateCopy (16 GDN state slots of
+    1 MiB)."""
+    T, B, CH, H, D = 4 * 4096, 4, 6144, 16, 128
+    g = torch.Generator(device="cuda").manual_seed(7)
+    bf = lambda *shape: torch.randn(shape, generator=g, device="cuda").to(torch.bfloat16)  # noqa: E731
+    res = {}
+
+    def timed(name, entry_id, params, nbytes):
+        entry = session.lib.entry(entry_id)
+        session.launch(entry, params)
+        ms = time_runs(torch, session, entry, params, None, steps, warmup)
+        res[name] = {"ms": ms, "gb_s": nbytes / ms / 1e6, "hbm_frac": nbytes / ms / 1e6 / HBM_PEAK_GBS}
+
+    x, w = bf(T, CH), bf(CH, 4)
+    y = torch.empty_like(x)
+    st = bf(B, CH, 3)
+    slots = torch.arange(B, dtype=torch.int32, device="cuda")
+    cu = torch.arange(0, T + 1, 4096, dtype=torch.int32, device="cuda")
+    p = roost_amd.causal_conv1d_params(x, w, None, y, st, slots, cu, batch=B, tokens=T, channels=CH, width=4, silu=True)
+    timed("causal_conv1d", roost_amd.CAUSAL_CONV1D_VARIANT, p, 2 * T * CH * 2 + CH * 4 * 2 + 2 * B * CH * 3 * 2)
+    ba = bf(T, 2 * H)
+    a_log = torch.randn(H, generator=g, device="cuda")
+    dt_bias = torch.randn(H, generator=g, device="cuda")
+    gg = torch.empty((T, H), dtype=torch.float32, device="cuda")
+    beta = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    reach = (T - 1) * 2 * H + H
+    p = roost_amd.gated_delta_rule_gates_params(ba, ba, a_log, dt_bias, gg, beta, tokens=T, v_heads=H, a_stride=2 * H,
+                                                b_stride=2 * H, a_len=reach, b_len=reach, a_offset=H, b_offset=0)
+    timed("gates", roost_amd.GATES_VARIANT, p, T * H * (2 + 2 + 4 + 2))
+    core, z = bf(T * H, D), bf(T * H, D)
+    nw = torch.randn(D, generator=g, device="cuda")
+    out = torch.empty_like(core)
+    p = roost_amd.gated_rms_norm_params(core, z, nw, out, rows=T * H, dim=D, eps=1e-6)
+    timed("gated_rms_norm", roost_amd.GATED_RMS_NORM_VARIANT, p, 3 * T * H * D * 2)
+    attn, gate = bf(T, 8 * 256), bf(T, 8 * 256)
+    o2 = torch.empty_like(attn)
+    p = roost_amd.sigmoid_mul_params(attn, gate, o2, rows=T, dim=8 * 256)
+    timed("sigmoid_mul", roost_amd.SIGMOID_MUL_VARIANT, p, 3 * T * 8 * 256 * 2)
+    pool = torch.zeros((32, H * D * D), dtype=torch.float32, device="cuda")
+    pairs = torch.tensor([[i, 16 + i] for i in range(16)], dtype=torch.int32, device="cuda").reshape(-1)
+    p = roost_amd.recurrent_state_copy_params(pool, pairs, slot_bytes=H * D * D * 4, count=16)
+    timed("recurrent_state_copy", roost_amd.STATE_COPY_VARIANT, p, 2 * 16 * H * D * D * 4)
+    return res
+
+
 def cpu_baseline(b: Paged, sample_seqs: int):
     """CpuOps oracle (single thread, double precision, the C restatement of CpuOps.PagedAttention) on the first
     `sample_seqs` sequences of the decode batch; reported in the headline's unit (algorithmic GB/s)."""
@@ -320,7 +369,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=16)
-    ap.add_argument("--only", choices=["decode", "prefill", "gdn", "mixed"], default=None,
+    ap.add_argument("--only", choices=["decode", "prefill", "gdn", "mixed", "layer"], default=None,
                     help="run one workload only and print its timing (for profiler passes); no JSON line")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -337,7 +386,8 @@ def main():
     torch.cuda.set_device(0)
     session = roost_amd.OpSession(device=0)
     if args.only is not None:
-        fn = {"decode": bench_decode, "prefill": bench_prefill, "gdn": bench_gdn, "mixed": bench_mixed}[args.only]
+        fn = {"decode": bench_decode, "prefill": bench_prefill, "gdn": bench_gdn, "mixed": bench_mixed,
+              "layer": bench_layer_ops}[args.only]
         res = fn(torch, roost_amd, session, args.steps, args.warmup)
         log(f"{args.only}: {res[1] if isinstance(res, tuple) else res} ms")
         session.close()
@@ -354,6 +404,9 @@ def main():
     log("gdn (config 4) ...")
     gdn = bench_gdn(torch, roost_amd, session, args.steps, args.warmup)
     log(f"  {json.dumps(gdn)}")
+    log("GDN layer neighbour ops ...")
+    layer = bench_layer_ops(torch, roost_amd, session, args.steps, args.warmup)
+    log(f"  {json.dumps(layer)}")
     log("mixed hybrid step (config 5) ...")
     mixed = bench_mixed(torch, roost_amd, session, max(args.steps // 2, 3), max(args.warmup // 2, 1))
     log(f"  {json.dumps(mixed)}")
@@ -388,6 +441,7 @@ def main():
                     "query_tokens": pb.tokens},
         "gdn": {k: _rounded(v) for k, v in gdn.items()},
         "mixed_step": _rounded(mixed),
+        "gdn_layer_ops": {k: _rounded(v) for k, v in layer.items()},
         "cpu_baseline": cpu,
     }
     session.close()

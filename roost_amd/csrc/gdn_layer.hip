@@ -30,8 +30,10 @@ __device__ __forceinline__ void StoreF(void* p, uint32_t dt, int64_t i, float v)
   }
 }
 
-__device__ __forceinline__ float SigmoidF(float x) { return 1.0f / (1.0f + __expf(-x)); }
-__device__ __forceinline__ float SiluF(float x) { return x / (1.0f + __expf(-x)); }
+// sigmoid and SiLU with the hardware reciprocal (v_rcp_f32, about 1 ulp) instead of a full-precision divide, which
+// would cost ten VALU instructions per element in these streaming kernels.
+__device__ __forceinline__ float SigmoidF(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+__device__ __forceinline__ float SiluF(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
 // ---- GatedDeltaRuleGates -------------------------------------------------------------------------------------------
 // g = -exp(a_log[h]) * softplus(a[t, h] + dt_bias[h]) (softplus(x) = x above 20), beta = sigmoid(b[t, h]). One thread per
@@ -183,6 +185,123 @@ __device__ __forceinline__ int32_t SeqOfToken(const int32_t* cu, uint32_t batch,
   return static_cast<int32_t>(lo);
 }
 
+// Tiled form for 16-byte channel vectors and a compile-time width: thread (tile of kTile tokens, kV channels) keeps the
+// last kW - 1 inputs of its channels in registers, so every input row is read once (plus a kW - 1 row halo per tile),
+// and loads its kV x kW weights once. A tile that crosses a sequence boundary takes a plain per-token loop instead.
+constexpr int kConvTile = 16;
+
+template <typename T, int kW>
+__global__ void __launch_bounds__(256) ConvTileKernel(ConvArgs a) {
+  constexpr int kV = 16 / static_cast<int>(sizeof(T));
+  const int32_t t_begin = static_cast<int32_t>(blockIdx.x) * kConvTile;
+  const uint32_t c0 = (blockIdx.y * blockDim.x + threadIdx.x) * kV;
+  if (c0 >= a.channels) return;
+  const int32_t t_end = min(t_begin + kConvTile, static_cast<int32_t>(a.tokens));
+  const T* x = static_cast<const T*>(a.x);
+  const T* wp = static_cast<const T*>(a.w);
+  auto unpack = [](const uint4& q, float* v) {
+    const uint32_t* qw = reinterpret_cast<const uint32_t*>(&q);
+#pragma unroll
+    for (int e = 0; e < kV; ++e) {
+      v[e] = sizeof(T) == 2 ? ((e & 1) ? Bf16HiToF32(qw[e >> 1]) : Bf16LoToF32(qw[e >> 1])) : __uint_as_float(qw[e]);
+    }
+  };
+  // Weights of channels c0 .. c0 + kV - 1: kV * kW consecutive elements, channel-major.
+  float w[kV][kW];
+  {
+    float flat[kV * kW];
+    const T* wrow = wp + static_cast<uint64_t>(c0) * kW;
+    if ((kV * kW * sizeof(T)) % 16 == 0 && (reinterpret_cast<uintptr_t>(wrow) & 15) == 0) {
+#pragma unroll
+      for (int q = 0; q < kV * kW / kV; ++q) unpack(reinterpret_cast<const uint4*>(wrow)[q], flat + q * kV);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kV * kW; ++i) flat[i] = LoadF(wrow, a.act_t, i);
+    }
+#pragma unroll
+    for (int e = 0; e < kV; ++e)
+#pragma unroll
+      for (int j = 0; j < kW; ++j) w[e][j] = flat[e * kW + j];
+  }
+  float bias[kV];
+#pragma unroll
+  for (int e = 0; e < kV; ++e) bias[e] = a.bias != nullptr ? LoadF(a.bias, a.act_t, c0 + e) : 0.0f;
+
+  const int32_t seq0 = SeqOfToken(a.cu, a.batch, t_begin);
+  const int32_t s0 = a.cu[seq0], s1 = a.cu[seq0 + 1];
+  // Entry i of [state (kW - 1), inputs] of sequence `seq` (first token `first`) for channels c0.., as floats.
+  auto history = [&](int32_t seq, int32_t first, int32_t i, float* v) {
+    if (i < kW - 1) {
+      const int32_t slot = a.slots[seq];
+      const bool ok = slot >= 0 && static_cast<uint64_t>(slot) < a.pool_slots;
+      const uint64_t so = static_cast<uint64_t>(ok ? slot : 0) * a.channels * (kW - 1);
+#pragma unroll
+      for (int e = 0; e < kV; ++e) v[e] = ok ? LoadF(a.state, a.state_t, so + (c0 + e) * (kW - 1) + i) : 0.0f;
+    } else {
+      unpack(*reinterpret_cast<const uint4*>(x + static_cast<uint64_t>(first + i - (kW - 1)) * a.channels + c0), v);
+    }
+  };
+  auto emit = [&](int32_t t, const float (*taps)[kV], const float* cur) {
+    float y[kV];
+#pragma unroll
+    for (int e = 0; e < kV; ++e) {
+      float acc = bias[e];
+#pragma unroll
+      for (int j = 0; j < kW - 1; ++j) acc = fmaf(w[e][j], taps[j][e], acc);
+      acc = fmaf(w[e][kW - 1], cur[e], acc);
+      y[e] = a.silu ? SiluF(acc) : acc;
+    }
+    StoreRun<T, true>(static_cast<T*>(a.y), static_cast<uint64_t>(t) * a.channels + c0, y);
+  };
+  float h[kW > 1 ? kW - 1 : 1][kV];  // the window: h[kW - 2] is the newest input
+
+  if (t_begin >= s0 && t_end <= s1) {
+    // The whole tile lies in one sequence (every tile but those at sequence boundaries): one window load, then a
+    // straight-line slide over the tile's rows, all of which are requested at once (one memory latency per tile).
+    uint4 rows[kConvTile];
+#pragma unroll
+    for (int i = 0; i < kConvTile; ++i) {
+      const int32_t t = min(t_begin + i, t_end - 1);
+      rows[i] = *reinterpret_cast<const uint4*>(x + static_cast<uint64_t>(t) * a.channels + c0);
+    }
+#pragma unroll
+    for (int j = 0; j < kW - 1; ++j) history(seq0, s0, t_begin - s0 + j, h[j]);
+#pragma unroll
+    for (int i = 0; i < kConvTile; ++i) {
+      const int32_t t = t_begin + i;
+      if (t >= t_end) break;
+      float cur[kV];
+      unpack(rows[i], cur);
+      emit(t, h, cur);
+#pragma unroll
+      for (int j = 0; j + 1 < kW - 1; ++j)
+#pragma unroll
+        for (int e = 0; e < kV; ++e) h[j][e] = h[j + 1][e];
+      if constexpr (kW > 1) {
+#pragma unroll
+        for (int e = 0; e < kV; ++e) h[kW - 2][e] = cur[e];
+      }
+    }
+    return;
+  }
+  // A tile that crosses a sequence boundary (or holds tokens outside every sequence): token by token, each tap read
+  // directly from the state or the inputs (the sequence is uniform across the workgroup: every thread shares the token).
+  int32_t seq = seq0;
+#pragma unroll 1
+  for (int32_t t = t_begin; t < t_end; ++t) {
+    while (seq + 1 < static_cast<int32_t>(a.batch) && a.cu[seq + 1] <= t) ++seq;
+    const int32_t first = a.cu[seq];
+    if (t < first || t >= a.cu[seq + 1]) continue;  // a token outside every sequence: no output
+    const int32_t rel = t - first;
+#pragma unroll
+    for (int j = 0; j < kW - 1; ++j) history(seq, first, rel + j, h[j]);
+    float cur[kV];
+    unpack(*reinterpret_cast<const uint4*>(x + static_cast<uint64_t>(t) * a.channels + c0), cur);
+    emit(t, h, cur);
+  }
+}
+
+// General form (any width, any channel count): one thread per (token, kV channels), taps loaded per output.
 template <typename T, bool kVec>
 __global__ void __launch_bounds__(256) ConvKernel(ConvArgs a) {
   constexpr int kV = kVec ? 16 / static_cast<int>(sizeof(T)) : 1;
@@ -515,16 +634,29 @@ extern "C" ROOST_API RoostStatus roost_causal_conv1d_run(RoostContext* ctx, cons
     // Slots the pool holds; the state span's length is in its own elements (a zero length means no slot is valid).
     a.pool_slots = sl == 0 ? 0 : p.conv_state.length / (uint64_t{p.channels} * sl);
     const uint64_t v = 16 / ElemBytes(act);
-    const bool vec = p.channels % v == 0 && Aligned(p.input.address, 16);
+    const bool vec = p.channels % v == 0 && Aligned(p.input.address, 16) && Aligned(p.output.address, 16);
     const uint32_t per_thread = vec ? static_cast<uint32_t>(v) : 1u;
-    const dim3 grid(p.tokens, Blocks(roost::CeilDiv(p.channels, per_thread), 256));
     hipStream_t s = Stream(stream);
-    if (act == ROOST_DTYPE_BF16) {
-      if (vec) hipLaunchKernelGGL((ConvKernel<uint16_t, true>), grid, dim3(256), 0, s, a);
-      else hipLaunchKernelGGL((ConvKernel<uint16_t, false>), grid, dim3(256), 0, s, a);
+    const dim3 tiled(Blocks(p.tokens, kConvTile), Blocks(roost::CeilDiv(p.channels, per_thread), 256));
+    const bool bf = act == ROOST_DTYPE_BF16;
+    if (vec && p.width >= 2 && p.width <= 4) {
+      switch (p.width * 2 + (bf ? 1 : 0)) {
+        case 5: hipLaunchKernelGGL((ConvTileKernel<uint16_t, 2>), tiled, dim3(256), 0, s, a); break;
+        case 7: hipLaunchKernelGGL((ConvTileKernel<uint16_t, 3>), tiled, dim3(256), 0, s, a); break;
+        case 9: hipLaunchKernelGGL((ConvTileKernel<uint16_t, 4>), tiled, dim3(256), 0, s, a); break;
+        case 4: hipLaunchKernelGGL((ConvTileKernel<float, 2>), tiled, dim3(256), 0, s, a); break;
+        case 6: hipLaunchKernelGGL((ConvTileKernel<float, 3>), tiled, dim3(256), 0, s, a); break;
+        default: hipLaunchKernelGGL((ConvTileKernel<float, 4>), tiled, dim3(256), 0, s, a); break;
+      }
     } else {
-      if (vec) hipLaunchKernelGGL((ConvKernel<float, true>), grid, dim3(256), 0, s, a);
-      else hipLaunchKernelGGL((ConvKernel<float, false>), grid, dim3(256), 0, s, a);
+      const dim3 grid(p.tokens, Blocks(roost::CeilDiv(p.channels, per_thread), 256));
+      if (bf) {
+        if (vec) hipLaunchKernelGGL((ConvKernel<uint16_t, true>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((ConvKernel<uint16_t, false>), grid, dim3(256), 0, s, a);
+      } else {
+        if (vec) hipLaunchKernelGGL((ConvKernel<float, true>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((ConvKernel<float, false>), grid, dim3(256), 0, s, a);
+      }
     }
     ROOST_TRY(FromHip(hipGetLastError(), "CausalConv1d launch"));
     if (sl == 0) return ROOST_STATUS_OK;

@@ -32,7 +32,9 @@ def assert_bf16_within_ulp(got_bits, want_bits, what):
 def assert_f32_rel(got, want, rel, what):
     got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
     scale = np.maximum(np.abs(want), 1e-6)
-    assert (np.abs(got - want) <= rel * scale).all(), f"{what}: max rel {(np.abs(got - want) / scale).max():.3e}"
+    r = np.abs(got - want) / scale
+    i = int(np.argmax(r))
+    assert (r <= rel).all(), f"{what}: max rel {r[i]:.3e} at element {i}: got {got[i]!r} want {want[i]!r}"
 
 
 def test_gates_qwen35_layout(session):
