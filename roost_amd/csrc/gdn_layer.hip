@@ -121,6 +121,67 @@ __global__ void __launch_bounds__(256) GatedRmsNormKernel(const T* __restrict__ 
   }
 }
 
+// Single-pass form for 16-byte vectors when one vector per lane covers the row (lanes_per_row * kV == dim, the Qwen
+// head dims): each thread serves kR rows spaced one block-row apart, issues all of their x and gate loads before any
+// arithmetic, keeps the row in registers (x is read once) and loads its kV weights once for all kR rows.
+constexpr int kRmsRows = 4;
+
+template <typename T, int kR>
+__global__ void __launch_bounds__(256) GatedRmsNormRowKernel(const T* __restrict__ x, const T* __restrict__ gate,
+                                                             const void* __restrict__ weight, uint32_t w_t,
+                                                             T* __restrict__ out, uint64_t rows, uint32_t dim,
+                                                             uint32_t lanes_per_row, float eps) {
+  constexpr int kV = 16 / static_cast<int>(sizeof(T));
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t sub = lane % lanes_per_row;
+  const uint64_t rows_per_pass = 4ull * (64 / lanes_per_row);  // rows one pass of the block covers
+  const uint64_t row0 = static_cast<uint64_t>(blockIdx.x) * rows_per_pass * kR +
+                        (threadIdx.x >> 6) * (64 / lanes_per_row) + lane / lanes_per_row;
+  const uint32_t col = sub * kV;
+  uint4 xq[kR], gq[kR];
+#pragma unroll
+  for (int r = 0; r < kR; ++r) {
+    const uint64_t row = row0 + r * rows_per_pass;
+    const uint64_t at = (row < rows ? row : 0) * dim + col;
+    xq[r] = *reinterpret_cast<const uint4*>(x + at);
+    gq[r] = *reinterpret_cast<const uint4*>(gate + at);
+  }
+  float wv[kV];
+  if (w_t == ROOST_DTYPE_F32 && (reinterpret_cast<uintptr_t>(weight) & 15) == 0) {
+    const float4* wp = reinterpret_cast<const float4*>(static_cast<const float*>(weight) + col);
+#pragma unroll
+    for (int q = 0; q < kV / 4; ++q) {
+      const float4 f = wp[q];
+      wv[4 * q] = f.x; wv[4 * q + 1] = f.y; wv[4 * q + 2] = f.z; wv[4 * q + 3] = f.w;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < kV; ++e) wv[e] = LoadF(weight, w_t, col + e);
+  }
+  auto unpack = [](const uint4& q, float* v) {
+    const uint32_t* qw = reinterpret_cast<const uint32_t*>(&q);
+#pragma unroll
+    for (int e = 0; e < kV; ++e) {
+      v[e] = sizeof(T) == 2 ? ((e & 1) ? Bf16HiToF32(qw[e >> 1]) : Bf16LoToF32(qw[e >> 1])) : __uint_as_float(qw[e]);
+    }
+  };
+#pragma unroll
+  for (int r = 0; r < kR; ++r) {
+    float xv[kV], gv[kV], y[kV];
+    unpack(xq[r], xv);
+    unpack(gq[r], gv);
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kV; ++e) ss = fmaf(xv[e], xv[e], ss);
+    for (uint32_t m = 1; m < lanes_per_row; m <<= 1) ss += __shfl_xor(ss, static_cast<int>(m), 64);
+    const float inv = rsqrtf(ss / static_cast<float>(dim) + eps);
+#pragma unroll
+    for (int e = 0; e < kV; ++e) y[e] = xv[e] * inv * wv[e] * SiluF(gv[e]);
+    const uint64_t row = row0 + r * rows_per_pass;
+    if (row < rows) StoreRun<T, true>(out, row * dim + col, y);
+  }
+}
+
 // ---- SigmoidMul ----------------------------------------------------------------------------------------------------
 // out = x * sigmoid(gate), kV elements per step (16-byte loads and stores when kVec), grid-stride.
 template <typename T, bool kVec>
@@ -505,12 +566,17 @@ extern "C" ROOST_API RoostStatus roost_gated_rms_norm_run(RoostContext* ctx, con
     while (lanes < 64 && lanes * per_lane < p.dim) lanes <<= 1;
     const uint64_t rows_per_block = 4ull * (64 / lanes);
     const dim3 grid(Blocks(p.rows, static_cast<uint32_t>(rows_per_block)));
+    const bool single = vec && lanes * per_lane == p.dim;
+    const dim3 row_grid(Blocks(p.rows, static_cast<uint32_t>(rows_per_block * kRmsRows)));
     hipStream_t s = Stream(stream);
     if (act == ROOST_DTYPE_BF16) {
       const auto* x = static_cast<const uint16_t*>(p.input.address);
       const auto* g = static_cast<const uint16_t*>(p.gate.address);
       auto* o = static_cast<uint16_t*>(p.output.address);
-      if (vec) {
+      if (single) {
+        hipLaunchKernelGGL((GatedRmsNormRowKernel<uint16_t, kRmsRows>), row_grid, dim3(256), 0, s, x, g,
+                           p.weight.address, p.weight.dtype, o, uint64_t{p.rows}, p.dim, lanes, p.eps);
+      } else if (vec) {
         hipLaunchKernelGGL((GatedRmsNormKernel<uint16_t, true>), grid, dim3(256), 0, s, x, g, p.weight.address,
                            p.weight.dtype, o, uint64_t{p.rows}, p.dim, lanes, p.eps);
       } else {
@@ -521,7 +587,10 @@ extern "C" ROOST_API RoostStatus roost_gated_rms_norm_run(RoostContext* ctx, con
       const auto* x = static_cast<const float*>(p.input.address);
       const auto* g = static_cast<const float*>(p.gate.address);
       auto* o = static_cast<float*>(p.output.address);
-      if (vec) {
+      if (single) {
+        hipLaunchKernelGGL((GatedRmsNormRowKernel<float, kRmsRows>), row_grid, dim3(256), 0, s, x, g,
+                           p.weight.address, p.weight.dtype, o, uint64_t{p.rows}, p.dim, lanes, p.eps);
+      } else if (vec) {
         hipLaunchKernelGGL((GatedRmsNormKernel<float, true>), grid, dim3(256), 0, s, x, g, p.weight.address,
                            p.weight.dtype, o, uint64_t{p.rows}, p.dim, lanes, p.eps);
       } else {

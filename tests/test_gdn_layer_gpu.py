@@ -82,7 +82,8 @@ def test_gates_match_transformers_fixture(session):
 
 @pytest.mark.parametrize("rows,dim,bf16,in_place", [(300 * 16, 128, True, False), (77, 128, True, True),
                                                      (40, 7, False, False), (9, 1000, False, True),
-                                                     (5, 4096, True, False)])
+                                                     (5, 4096, True, False), (33, 128, False, False),
+                                                     (10, 16, True, True)])
 def test_gated_rms_norm(session, rows, dim, bf16, in_place):
     import torch
 
