@@ -30,6 +30,14 @@ __device__ __forceinline__ void StoreF(void* p, uint32_t dt, int64_t i, float v)
   }
 }
 
+// Two floats to packed bf16 with gfx950's v_cvt_pk_bf16_f32: round to nearest, ties to even, as F32ToBf16 does, in one
+// instruction instead of a dozen. Only a NaN may come out with other NaN bits than F32ToBf16's 0x7FC0.
+__device__ __forceinline__ uint32_t PackBf16Rne(float lo, float hi) {
+  typedef float F2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 B2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((F2){lo, hi}, B2));
+}
+
 // sigmoid and SiLU with the hardware reciprocal (v_rcp_f32, about 1 ulp) instead of a full-precision divide, which
 // would cost ten VALU instructions per element in these streaming kernels.
 __device__ __forceinline__ float SigmoidF(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
@@ -79,7 +87,7 @@ __device__ __forceinline__ void StoreRun(T* p, uint64_t k, const float* v) {
     uint4 q;
     uint32_t* qw = reinterpret_cast<uint32_t*>(&q);
 #pragma unroll
-    for (int w = 0; w < 4; ++w) qw[w] = sizeof(T) == 2 ? PackBf16(v[2 * w], v[2 * w + 1]) : __float_as_uint(v[w]);
+    for (int w = 0; w < 4; ++w) qw[w] = sizeof(T) == 2 ? PackBf16Rne(v[2 * w], v[2 * w + 1]) : __float_as_uint(v[w]);
     *reinterpret_cast<uint4*>(p + k) = q;
   } else if constexpr (sizeof(T) == 2) {
     reinterpret_cast<uint16_t*>(p)[k] = F32ToBf16(v[0]);
@@ -200,7 +208,7 @@ __global__ void __launch_bounds__(256) SigmoidMulKernel(const T* __restrict__ x,
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         if constexpr (sizeof(T) == 2) {
-          ow[w] = PackBf16(Bf16LoToF32(xw[w]) * SigmoidF(Bf16LoToF32(gw[w])),
+          ow[w] = PackBf16Rne(Bf16LoToF32(xw[w]) * SigmoidF(Bf16LoToF32(gw[w])),
                            Bf16HiToF32(xw[w]) * SigmoidF(Bf16HiToF32(gw[w])));
         } else {
           ow[w] = __float_as_uint(__uint_as_float(xw[w]) * SigmoidF(__uint_as_float(gw[w])));
@@ -246,35 +254,78 @@ __device__ __forceinline__ int32_t SeqOfToken(const int32_t* cu, uint32_t batch,
   return static_cast<int32_t>(lo);
 }
 
-// Tiled form for 16-byte channel vectors and a compile-time width: thread (tile of kTile tokens, kV channels) keeps the
-// last kW - 1 inputs of its channels in registers, so every input row is read once (plus a kW - 1 row halo per tile),
-// and loads its kV x kW weights once. A tile that crosses a sequence boundary takes a plain per-token loop instead.
-constexpr int kConvTile = 16;
+// A run of kBytes / sizeof(T) consecutive channels: one 4-, 8- or 16-byte load or store.
+template <int kBytes>
+__device__ __forceinline__ void LoadWords(const void* p, uint32_t* w) {
+  if constexpr (kBytes == 16) {
+    const uint4 q = *static_cast<const uint4*>(p);
+    w[0] = q.x; w[1] = q.y; w[2] = q.z; w[3] = q.w;
+  } else if constexpr (kBytes == 8) {
+    const uint2 q = *static_cast<const uint2*>(p);
+    w[0] = q.x; w[1] = q.y;
+  } else {
+    w[0] = *static_cast<const uint32_t*>(p);
+  }
+}
+template <int kBytes>
+__device__ __forceinline__ void StoreWords(void* p, const uint32_t* w) {
+  if constexpr (kBytes == 16) {
+    *static_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  } else if constexpr (kBytes == 8) {
+    *static_cast<uint2*>(p) = make_uint2(w[0], w[1]);
+  } else {
+    *static_cast<uint32_t*>(p) = w[0];
+  }
+}
+template <typename T, int kWords>
+__device__ __forceinline__ void UnpackWords(const uint32_t* w, float* v) {
+  constexpr int kV = kWords * 4 / static_cast<int>(sizeof(T));
+#pragma unroll
+  for (int e = 0; e < kV; ++e) {
+    v[e] = sizeof(T) == 2 ? ((e & 1) ? Bf16HiToF32(w[e >> 1]) : Bf16LoToF32(w[e >> 1])) : __uint_as_float(w[e]);
+  }
+}
+template <typename T, int kWords>
+__device__ __forceinline__ void PackWords(const float* v, uint32_t* w) {
+#pragma unroll
+  for (int q = 0; q < kWords; ++q) w[q] = sizeof(T) == 2 ? PackBf16Rne(v[2 * q], v[2 * q + 1]) : __float_as_uint(v[q]);
+}
 
-template <typename T, int kW>
-__global__ void __launch_bounds__(256) ConvTileKernel(ConvArgs a) {
-  constexpr int kV = 16 / static_cast<int>(sizeof(T));
-  const int32_t t_begin = static_cast<int32_t>(blockIdx.x) * kConvTile;
-  const uint32_t c0 = (blockIdx.y * blockDim.x + threadIdx.x) * kV;
+// Tiled form for a compile-time width and channel vectors of kBytes (kV channels per thread). Workgroup b serves token
+// tile b / cblocks (kConvTile tokens) and channel block b % cblocks (consecutive workgroups cover one row). A thread keeps
+// the last kW - 1 inputs of its channels in registers, so every input row is read once plus a kW - 1 row halo per tile,
+// and loads its kV x kW weights once. Narrow vectors (8 bytes for bf16) keep the register count low enough for eight
+// waves per SIMD, which with long tiles keeps the halo small while the grid still fills the chip several times over.
+constexpr int kConvTile = 32;
+constexpr int kConvChunk = 4;  // rows requested ahead of the arithmetic
+
+template <typename T, int kW, int kBytes>
+__global__ void __launch_bounds__(256) ConvTileKernel(ConvArgs a, uint32_t cblocks) {
+  constexpr int kWords = kBytes / 4;
+  constexpr int kV = kBytes / static_cast<int>(sizeof(T));
+  const uint32_t tile = blockIdx.x / cblocks;
+  const int32_t t_begin = static_cast<int32_t>(tile) * kConvTile;
+  const uint32_t c0 = ((blockIdx.x - tile * cblocks) * blockDim.x + threadIdx.x) * kV;
   if (c0 >= a.channels) return;
   const int32_t t_end = min(t_begin + kConvTile, static_cast<int32_t>(a.tokens));
   const T* x = static_cast<const T*>(a.x);
-  const T* wp = static_cast<const T*>(a.w);
-  auto unpack = [](const uint4& q, float* v) {
-    const uint32_t* qw = reinterpret_cast<const uint32_t*>(&q);
-#pragma unroll
-    for (int e = 0; e < kV; ++e) {
-      v[e] = sizeof(T) == 2 ? ((e & 1) ? Bf16HiToF32(qw[e >> 1]) : Bf16LoToF32(qw[e >> 1])) : __uint_as_float(qw[e]);
-    }
+  auto row_at = [&](int32_t t, float* v) {
+    uint32_t q[kWords];
+    LoadWords<kBytes>(x + static_cast<uint64_t>(t) * a.channels + c0, q);
+    UnpackWords<T, kWords>(q, v);
   };
   // Weights of channels c0 .. c0 + kV - 1: kV * kW consecutive elements, channel-major.
   float w[kV][kW];
   {
     float flat[kV * kW];
-    const T* wrow = wp + static_cast<uint64_t>(c0) * kW;
-    if ((kV * kW * sizeof(T)) % 16 == 0 && (reinterpret_cast<uintptr_t>(wrow) & 15) == 0) {
+    const T* wrow = static_cast<const T*>(a.w) + static_cast<uint64_t>(c0) * kW;
+    if ((reinterpret_cast<uintptr_t>(wrow) & (kBytes - 1)) == 0) {
 #pragma unroll
-      for (int q = 0; q < kV * kW / kV; ++q) unpack(reinterpret_cast<const uint4*>(wrow)[q], flat + q * kV);
+      for (int q = 0; q < kW; ++q) {
+        uint32_t qw[kWords];
+        LoadWords<kBytes>(wrow + q * kV, qw);
+        UnpackWords<T, kWords>(qw, flat + q * kV);
+      }
     } else {
 #pragma unroll
       for (int i = 0; i < kV * kW; ++i) flat[i] = LoadF(wrow, a.act_t, i);
@@ -299,7 +350,7 @@ __global__ void __launch_bounds__(256) ConvTileKernel(ConvArgs a) {
 #pragma unroll
       for (int e = 0; e < kV; ++e) v[e] = ok ? LoadF(a.state, a.state_t, so + (c0 + e) * (kW - 1) + i) : 0.0f;
     } else {
-      unpack(*reinterpret_cast<const uint4*>(x + static_cast<uint64_t>(first + i - (kW - 1)) * a.channels + c0), v);
+      row_at(first + i - (kW - 1), v);
     }
   };
   auto emit = [&](int32_t t, const float (*taps)[kV], const float* cur) {
@@ -312,36 +363,46 @@ __global__ void __launch_bounds__(256) ConvTileKernel(ConvArgs a) {
       acc = fmaf(w[e][kW - 1], cur[e], acc);
       y[e] = a.silu ? SiluF(acc) : acc;
     }
-    StoreRun<T, true>(static_cast<T*>(a.y), static_cast<uint64_t>(t) * a.channels + c0, y);
+    uint32_t q[kWords];
+    PackWords<T, kWords>(y, q);
+    StoreWords<kBytes>(static_cast<T*>(a.y) + static_cast<uint64_t>(t) * a.channels + c0, q);
   };
-  float h[kW > 1 ? kW - 1 : 1][kV];  // the window: h[kW - 2] is the newest input
+  float h[kW - 1][kV];  // the window: h[kW - 2] is the newest input
 
   if (t_begin >= s0 && t_end <= s1) {
     // The whole tile lies in one sequence (every tile but those at sequence boundaries): one window load, then a
-    // straight-line slide over the tile's rows, all of which are requested at once (one memory latency per tile).
-    uint4 rows[kConvTile];
+    // straight-line slide over the tile's rows, the next kConvChunk rows requested before the current ones are computed.
+    auto fetch = [&](int32_t t0, uint32_t (*r)[kWords]) {
 #pragma unroll
-    for (int i = 0; i < kConvTile; ++i) {
-      const int32_t t = min(t_begin + i, t_end - 1);
-      rows[i] = *reinterpret_cast<const uint4*>(x + static_cast<uint64_t>(t) * a.channels + c0);
-    }
+      for (int i = 0; i < kConvChunk; ++i) {
+        LoadWords<kBytes>(x + static_cast<uint64_t>(min(t0 + i, t_end - 1)) * a.channels + c0, r[i]);
+      }
+    };
+    uint32_t rows[kConvChunk][kWords], next[kConvChunk][kWords];
+    fetch(t_begin, rows);
 #pragma unroll
     for (int j = 0; j < kW - 1; ++j) history(seq0, s0, t_begin - s0 + j, h[j]);
+#pragma unroll 1
+    for (int32_t tc = t_begin; tc < t_end; tc += kConvChunk) {
+      if (tc + kConvChunk < t_end) fetch(tc + kConvChunk, next);
 #pragma unroll
-    for (int i = 0; i < kConvTile; ++i) {
-      const int32_t t = t_begin + i;
-      if (t >= t_end) break;
-      float cur[kV];
-      unpack(rows[i], cur);
-      emit(t, h, cur);
+      for (int i = 0; i < kConvChunk; ++i) {
+        const int32_t t = tc + i;
+        if (t >= t_end) break;
+        float cur[kV];
+        UnpackWords<T, kWords>(rows[i], cur);
+        emit(t, h, cur);
 #pragma unroll
-      for (int j = 0; j + 1 < kW - 1; ++j)
+        for (int j = 0; j + 1 < kW - 1; ++j)
 #pragma unroll
-        for (int e = 0; e < kV; ++e) h[j][e] = h[j + 1][e];
-      if constexpr (kW > 1) {
+          for (int e = 0; e < kV; ++e) h[j][e] = h[j + 1][e];
 #pragma unroll
         for (int e = 0; e < kV; ++e) h[kW - 2][e] = cur[e];
       }
+#pragma unroll
+      for (int i = 0; i < kConvChunk; ++i)
+#pragma unroll
+        for (int q = 0; q < kWords; ++q) rows[i][q] = next[i][q];
     }
     return;
   }
@@ -357,7 +418,7 @@ __global__ void __launch_bounds__(256) ConvTileKernel(ConvArgs a) {
 #pragma unroll
     for (int j = 0; j < kW - 1; ++j) history(seq, first, rel + j, h[j]);
     float cur[kV];
-    unpack(*reinterpret_cast<const uint4*>(x + static_cast<uint64_t>(t) * a.channels + c0), cur);
+    row_at(t, cur);
     emit(t, h, cur);
   }
 }
@@ -706,16 +767,21 @@ extern "C" ROOST_API RoostStatus roost_causal_conv1d_run(RoostContext* ctx, cons
     const bool vec = p.channels % v == 0 && Aligned(p.input.address, 16) && Aligned(p.output.address, 16);
     const uint32_t per_thread = vec ? static_cast<uint32_t>(v) : 1u;
     hipStream_t s = Stream(stream);
-    const dim3 tiled(Blocks(p.tokens, kConvTile), Blocks(roost::CeilDiv(p.channels, per_thread), 256));
     const bool bf = act == ROOST_DTYPE_BF16;
-    if (vec && p.width >= 2 && p.width <= 4) {
+    // The tiled kernel takes 8-byte channel vectors (4 bf16 or 2 f32 channels) when the channel count and the
+    // buffers allow them.
+    const bool vec8 = p.channels % (8 / ElemBytes(act)) == 0 && Aligned(p.input.address, 8) && Aligned(p.output.address, 8);
+    const uint32_t cblocks = Blocks(p.channels / (8 / ElemBytes(act)), 256);
+    const uint64_t tiled_blocks = uint64_t{cblocks} * Blocks(p.tokens, kConvTile);
+    if (vec8 && p.width >= 2 && p.width <= 4 && tiled_blocks <= 0xFFFFFFFFull) {
+      const dim3 tiled(static_cast<uint32_t>(tiled_blocks));
       switch (p.width * 2 + (bf ? 1 : 0)) {
-        case 5: hipLaunchKernelGGL((ConvTileKernel<uint16_t, 2>), tiled, dim3(256), 0, s, a); break;
-        case 7: hipLaunchKernelGGL((ConvTileKernel<uint16_t, 3>), tiled, dim3(256), 0, s, a); break;
-        case 9: hipLaunchKernelGGL((ConvTileKernel<uint16_t, 4>), tiled, dim3(256), 0, s, a); break;
-        case 4: hipLaunchKernelGGL((ConvTileKernel<float, 2>), tiled, dim3(256), 0, s, a); break;
-        case 6: hipLaunchKernelGGL((ConvTileKernel<float, 3>), tiled, dim3(256), 0, s, a); break;
-        default: hipLaunchKernelGGL((ConvTileKernel<float, 4>), tiled, dim3(256), 0, s, a); break;
+        case 5: hipLaunchKernelGGL((ConvTileKernel<uint16_t, 2, 8>), tiled, dim3(256), 0, s, a, cblocks); break;
+        case 7: hipLaunchKernelGGL((ConvTileKernel<uint16_t, 3, 8>), tiled, dim3(256), 0, s, a, cblocks); break;
+        case 9: hipLaunchKernelGGL((ConvTileKernel<uint16_t, 4, 8>), tiled, dim3(256), 0, s, a, cblocks); break;
+        case 4: hipLaunchKernelGGL((ConvTileKernel<float, 2, 8>), tiled, dim3(256), 0, s, a, cblocks); break;
+        case 6: hipLaunchKernelGGL((ConvTileKernel<float, 3, 8>), tiled, dim3(256), 0, s, a, cblocks); break;
+        default: hipLaunchKernelGGL((ConvTileKernel<float, 4, 8>), tiled, dim3(256), 0, s, a, cblocks); break;
       }
     } else {
       const dim3 grid(p.tokens, Blocks(roost::CeilDiv(p.channels, per_thread), 256));

@@ -191,6 +191,7 @@ def _conv_case(session, lens, slots, pool_slots, channels, width, silu, bias, bf
     ("f32 with bias, width 3, f32 state", [7, 1, 20], [1, 0, 2], 3, 40, 3, False, True, False, True),
     ("width 1 (no state)", [3, 4], [0, 1], 2, 24, 1, True, True, False, True),
     ("odd channels scalar path", [9, 2], [1, 0], 2, 13, 4, True, False, True, True),
+    ("one sequence, ragged last tile", [45, 70], [1, 0], 2, 128, 4, True, True, True, False),
 ])
 def test_causal_conv1d(session, name, lens, slots, pool, channels, width, silu, bias, bf16, state_f32):
     got, want, got_state, want_state = _conv_case(session, lens, slots, pool, channels, width, silu, bias, bf16,
