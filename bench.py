@@ -324,6 +324,45 @@ def bench_layer_ops(torch, roost_amd, session, steps, warmup):
     return res
 
 
+def bench_attention_input(torch, roost_amd, session, steps, warmup):
+    """The attention layer's input ops at the Qwen3.5 full-attention shape (8 q heads, 2 KV heads, head dim 256,
+    16-token pages, theta 1e7): QkvQkNormRopeCacheWrite over a prefill of 8192 tokens and over a decode step of 64
+    tokens, and the unfused QkNorm and Rope over the 8192 tokens. Bytes are each op's reads and writes once: the fused
+    op reads the [q | k | v] rows and writes q plus the k and v cache rows."""
+    HQ, HK, D, BS = 8, 2, 256, 16
+    g = torch.Generator(device="cuda").manual_seed(11)
+    bf = lambda *shape: torch.randn(shape, generator=g, device="cuda").to(torch.bfloat16)  # noqa: E731
+    res = {}
+
+    def timed(name, entry_id, params, nbytes):
+        entry = session.lib.entry(entry_id)
+        session.launch(entry, params)
+        ms = time_runs(torch, session, entry, params, None, steps, warmup)
+        res[name] = {"ms": ms, "gb_s": nbytes / ms / 1e6, "hbm_frac": nbytes / ms / 1e6 / HBM_PEAK_GBS}
+
+    qw, kw = bf(D) * 0.1 + 1, bf(D) * 0.1 + 1
+    for name, T in (("qkv_prefill_8192", 8192), ("qkv_decode_64", 64)):
+        qkv = bf(T, (HQ + 2 * HK) * D)
+        q = torch.empty((T, HQ, D), dtype=torch.bfloat16, device="cuda")
+        pages = (T + BS - 1) // BS + 1
+        kc = torch.zeros((pages, BS, HK, D), dtype=torch.bfloat16, device="cuda")
+        vc = torch.zeros_like(kc)
+        pos = torch.arange(T, dtype=torch.int32, device="cuda") + 4096
+        slots = torch.randperm(pages * BS, generator=g, device="cuda")[:T].to(torch.int64)
+        p = roost_amd.qkv_qk_norm_rope_cache_write_params(qkv, q, qw, kw, pos, kc, vc, slots, tokens=T, q_heads=HQ,
+                                                          kv_heads=HK, head_dim=D, page_size=BS, eps=1e-6, theta=1e7)
+        nbytes = T * (HQ + 2 * HK) * D * 2 + T * (HQ + 2 * HK) * D * 2 + T * 12
+        timed(name, roost_amd.QKV_VARIANT, p, nbytes)
+    T = 8192
+    q, k = bf(T, HQ, D), bf(T, HK, D)
+    pos = torch.arange(T, dtype=torch.int32, device="cuda")
+    p = roost_amd.qk_norm_params(q, k, qw, kw, tokens=T, q_heads=HQ, kv_heads=HK, head_dim=D, eps=1e-6)
+    timed("qk_norm_8192", roost_amd.QK_NORM_VARIANT, p, 2 * T * (HQ + HK) * D * 2)
+    p = roost_amd.rope_params(q, k, pos, tokens=T, q_heads=HQ, kv_heads=HK, head_dim=D, theta=1e7, rotary_dim=64)
+    timed("rope_partial64_8192", roost_amd.ROPE_VARIANT, p, 2 * T * (HQ + HK) * D * 2)
+    return res
+
+
 def cpu_baseline(b: Paged, sample_seqs: int):
     """CpuOps oracle (single thread, double precision, the C restatement of CpuOps.PagedAttention) on the first
     `sample_seqs` sequences of the decode batch; reported in the headline's unit (algorithmic GB/s)."""
@@ -369,7 +408,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=16)
-    ap.add_argument("--only", choices=["decode", "prefill", "gdn", "mixed", "layer"], default=None,
+    ap.add_argument("--only", choices=["decode", "prefill", "gdn", "mixed", "layer", "attn_in"], default=None,
                     help="run one workload only and print its timing (for profiler passes); no JSON line")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -387,7 +426,7 @@ def main():
     session = roost_amd.OpSession(device=0)
     if args.only is not None:
         fn = {"decode": bench_decode, "prefill": bench_prefill, "gdn": bench_gdn, "mixed": bench_mixed,
-              "layer": bench_layer_ops}[args.only]
+              "layer": bench_layer_ops, "attn_in": bench_attention_input}[args.only]
         res = fn(torch, roost_amd, session, args.steps, args.warmup)
         log(f"{args.only}: {res[1] if isinstance(res, tuple) else res} ms")
         session.close()
@@ -407,6 +446,9 @@ def main():
     log("GDN layer neighbour ops ...")
     layer = bench_layer_ops(torch, roost_amd, session, args.steps, args.warmup)
     log(f"  {json.dumps(layer)}")
+    log("attention input ops ...")
+    attn_in = bench_attention_input(torch, roost_amd, session, args.steps, args.warmup)
+    log(f"  {json.dumps(attn_in)}")
     log("mixed hybrid step (config 5) ...")
     mixed = bench_mixed(torch, roost_amd, session, max(args.steps // 2, 3), max(args.warmup // 2, 1))
     log(f"  {json.dumps(mixed)}")
@@ -442,6 +484,7 @@ def main():
         "gdn": {k: _rounded(v) for k, v in gdn.items()},
         "mixed_step": _rounded(mixed),
         "gdn_layer_ops": {k: _rounded(v) for k, v in layer.items()},
+        "attention_input_ops": {k: _rounded(v) for k, v in attn_in.items()},
         "cpu_baseline": cpu,
     }
     session.close()

@@ -73,6 +73,46 @@ ROOST_API RoostStatus roost_recurrent_state_copy_run(RoostContext* ctx, const vo
 ROOST_API RoostStatus roost_recurrent_state_snapshot_run(RoostContext* ctx, const void* params,
                                                          const RoostWorkspace* ws, void* stream);
 
+/* The attention layer's input ops, each flagged GRAPH_CAPTURABLE | DETERMINISTIC | BATCH_INVARIANT, no plan and no
+ * workspace:
+ * QkNorm, variant "qk-norm-gfx950" -- replaces the reference's QkNormRun (kernels/src/m0_ops.cu:89-130, registered as
+ *   "qk-norm-flashinfer" at kernels/src/m0_registry.cu:77);
+ * Rope, variant "rope-gfx950" -- replaces RopeRun (kernels/src/m0_ops.cu:210-255, "rope-roost" at m0_registry.cu:79). */
+ROOST_API RoostStatus roost_qk_norm_run(RoostContext* ctx, const void* params, const RoostWorkspace* ws, void* stream);
+ROOST_API RoostStatus roost_rope_run(RoostContext* ctx, const void* params, const RoostWorkspace* ws, void* stream);
+
+/* QkvQkNormRopeCacheWrite (ROOST_OP_QKV_QK_NORM_ROPE_CACHE_WRITE, 67), variant "qkv-qk-norm-rope-cache-write-gfx950".
+ * The reference's C header names only the op id: the op exists in its CPU reference (src/Starlings.Roost.Ops/
+ * CpuOps.Fused.cs:37-95) with the argument struct QkvQkNormRopeCacheWriteArgs (src/Starlings.Roost.Ops/OpArgs.cs:
+ * 629-683), and no CUDA library implements it. This record carries those arguments field for field in the ABI's
+ * style; the activation type is qkv's dtype and the cache type k_cache's. Each [q | k | v] row of qkv is split: q
+ * heads are RmsNormed with q_weight, rotated (full rotary width, default frequencies, NeoX halves) and written to q;
+ * k heads are RmsNormed with k_weight, rotated and written into k_cache at slot_mapping[t] (NHD pools, unit scale);
+ * v heads are copied into v_cache there. A negative or out-of-pool slot writes no cache row; qkv is left as it was. */
+typedef struct RoostQkvQkNormRopeCacheWriteParams {
+  uint32_t struct_size;
+  uint32_t abi_minor;
+  RoostDeviceSpan qkv;          /* [tokens, (q_heads + 2 * kv_heads) * head_dim] */
+  RoostDeviceSpan q;            /* [tokens, q_heads, head_dim] output */
+  RoostDeviceSpan q_weight;     /* [head_dim] */
+  RoostDeviceSpan k_weight;     /* [head_dim] */
+  RoostDeviceSpan positions;    /* [tokens] int32 */
+  RoostDeviceSpan k_cache;      /* [pages, page_size, kv_heads, head_dim] */
+  RoostDeviceSpan v_cache;      /* same */
+  RoostDeviceSpan slot_mapping; /* [tokens] int64 */
+  uint32_t tokens;
+  uint32_t q_heads;
+  uint32_t kv_heads;
+  uint32_t head_dim;
+  uint32_t page_size;
+  float eps;
+  float theta;
+  uint32_t reserved0;
+} RoostQkvQkNormRopeCacheWriteParams;
+
+ROOST_API RoostStatus roost_qkv_qk_norm_rope_cache_write_run(RoostContext* ctx, const void* params,
+                                                             const RoostWorkspace* ws, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -325,6 +325,49 @@ typedef struct RoostGatedRmsNormParams {
   uint32_t reserved0;
 } RoostGatedRmsNormParams;
 
+/* Per-head RmsNorm of query and key heads, in place (reference kernels/include/roost_kernels.h:307-323). */
+typedef struct RoostQkNormParams {
+  uint32_t struct_size;
+  uint32_t abi_minor;
+  RoostDeviceSpan q;        /* [tokens, q_heads, head_dim] at q_stride */
+  RoostDeviceSpan k;        /* [tokens, kv_heads, head_dim] at k_stride */
+  RoostDeviceSpan q_weight; /* [head_dim] */
+  RoostDeviceSpan k_weight; /* [head_dim] */
+  uint32_t tokens;
+  uint32_t q_heads;
+  uint32_t kv_heads;
+  uint32_t head_dim;
+  uint32_t q_stride; /* elements between tokens; 0 means q_heads * head_dim */
+  uint32_t k_stride; /* 0 means kv_heads * head_dim */
+  float eps;
+  uint32_t reserved0;
+} RoostQkNormParams;
+
+#define ROOST_ROPE_DEFAULT 0
+#define ROOST_ROPE_LLAMA3 1
+
+/* Rotary position embedding of q and k, in place, NeoX (half-split) pairs unless interleaved is set (reference
+ * kernels/include/roost_kernels.h:328-347). */
+typedef struct RoostRopeParams {
+  uint32_t struct_size;
+  uint32_t abi_minor;
+  RoostDeviceSpan q;         /* [tokens, q_heads, head_dim] */
+  RoostDeviceSpan k;         /* [tokens, kv_heads, head_dim] */
+  RoostDeviceSpan positions; /* [tokens] int32 */
+  uint32_t tokens;
+  uint32_t q_heads;
+  uint32_t kv_heads;
+  uint32_t head_dim;
+  uint32_t rotary_dim; /* 0 means head_dim */
+  uint32_t kind;       /* ROOST_ROPE_* */
+  uint32_t interleaved;
+  float theta;
+  float llama3_factor;
+  float llama3_low_freq_factor;
+  float llama3_high_freq_factor;
+  uint32_t llama3_original_max_position;
+} RoostRopeParams;
+
 /* out = input * sigmoid(gate) elementwise over [rows, dim] (ABI 1.2). input may alias output. */
 typedef struct RoostSigmoidMulParams {
   uint32_t struct_size;

@@ -164,6 +164,44 @@ def causal_conv1d(x, weight, bias, out, state, state_slots, cu_seqlens, *, batch
                                       channels, width, int(silu)))
 
 
+def qk_norm(q, k, q_weight, k_weight, *, tokens, q_heads, kv_heads, head_dim, eps, q_stride=0, k_stride=0) -> None:
+    """CpuOps.QkNorm, in place (q_stride / k_stride: elements between tokens, 0 = contiguous)."""
+    assert q.dtype == k.dtype == q_weight.dtype == k_weight.dtype
+    _check(lib().oracle_qk_norm(_ptr(q), _ptr(k), _ptr(q_weight), _ptr(k_weight), _dt(q), tokens, q_heads, kv_heads,
+                                head_dim, q_stride, k_stride, ctypes.c_float(eps)))
+
+
+def rope(q, k, positions, *, tokens, q_heads, kv_heads, head_dim, theta, rotary_dim=0, interleaved=False,
+         llama3=None) -> None:
+    """CpuOps.Rope, in place. llama3: (factor, low_freq_factor, high_freq_factor, original_max_position) or None."""
+    assert q.dtype == k.dtype and positions.dtype == np.int32
+    kind, (fac, low, high, orig) = (1, llama3) if llama3 is not None else (0, (0.0, 0.0, 0.0, 0))
+    _check(lib().oracle_rope(_ptr(q), _ptr(k), _ptr(positions), _dt(q), tokens, q_heads, kv_heads, head_dim,
+                             rotary_dim, kind, int(interleaved), ctypes.c_float(theta), ctypes.c_float(fac),
+                             ctypes.c_float(low), ctypes.c_float(high), int(orig)))
+
+
+def qkv_qk_norm_rope_cache_write(qkv, q_out, q_weight, k_weight, positions, k_cache, v_cache, slot_mapping, *, tokens,
+                                 q_heads, kv_heads, head_dim, page_size, eps, theta) -> None:
+    """CpuOps.QkvQkNormRopeCacheWrite (CpuOps.Fused.cs:37-95): its unfused parts in order. q is copied out of each
+    [q | k | v] row into q_out and k, v into scratch; QkNorm of q and k; Rope (full rotary width, default kind, NeoX
+    halves) of q and k; CacheWrite of k and v into NHD pools. A cache element type wider than the activations (f32
+    pools under bf16 rows) takes the exact widening CpuOps' CopyConvert makes at unit scale."""
+    qw, kw = q_heads * head_dim, kv_heads * head_dim
+    rows = qkv.reshape(tokens, qw + 2 * kw)
+    q_out.reshape(tokens, qw)[:] = rows[:, :qw]
+    k = np.ascontiguousarray(rows[:, qw:qw + kw]).reshape(-1)
+    v = np.ascontiguousarray(rows[:, qw + kw:]).reshape(-1)
+    qk_norm(q_out, k, q_weight, k_weight, tokens=tokens, q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim, eps=eps)
+    rope(q_out, k, positions, tokens=tokens, q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim, theta=theta)
+    if k_cache.dtype != k.dtype:
+        assert k.dtype == np.uint16 and k_cache.dtype == np.float32, "only bf16 rows into f32 pools widen exactly"
+        k = (k.astype(np.uint32) << 16).view(np.float32)
+        v = (v.astype(np.uint32) << 16).view(np.float32)
+    cache_write(k, v, k_cache, v_cache, slot_mapping, tokens=tokens, kv_heads=kv_heads, head_dim=head_dim,
+                page_size=page_size, bf16=k.dtype == np.uint16)
+
+
 def state_copy(pool: np.ndarray, pairs: np.ndarray, *, slot_bytes: int) -> None:
     """CpuOps.RecurrentStateCopy: slot pairs[i, 0] -> slot pairs[i, 1] of pool, in pair order."""
     raw = pool.view(np.uint8)

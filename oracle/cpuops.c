@@ -10,6 +10,7 @@
  *
  * Parity pinning (which check pins which function) is listed in tests/test_oracle.py.
  */
+#define _GNU_SOURCE
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -191,6 +192,80 @@ int oracle_cache_write(const void* k, const void* v, void* k_cache, void* v_cach
       const int64_t src = t * per_token + (int64_t)h * head_dim;
       memcpy((char*)k_cache + dst * es, (const char*)k + src * es, (size_t)(head_dim * es));
       memcpy((char*)v_cache + dst * es, (const char*)v + src * es, (size_t)(head_dim * es));
+    }
+  }
+  return 0;
+}
+
+/* ---- QkNorm and Rope (reference: src/Starlings.Roost.Ops/CpuOps.cs:63-175) ---- */
+
+/* One head row: y = x / sqrt(sum(x^2) / dim + eps) * w, in double, rounded once (CpuOps.cs:89-103). */
+static void norm_row(void* x, int dt, int64_t o, const void* w, int dim, float eps) {
+  double ss = 0.0;
+  for (int i = 0; i < dim; ++i) {
+    const double v = load(x, dt, o + i);
+    ss += v * v;
+  }
+  const double inv = 1.0 / sqrt(ss / dim + (double)eps);
+  for (int i = 0; i < dim; ++i) store(x, dt, o + i, load(x, dt, o + i) * inv * load(w, dt, i));
+}
+
+/* QkNorm (CpuOps.cs:63-87), in place, every query head with q_weight and every key head with k_weight. q_stride and
+ * k_stride are the elements between tokens (0: heads * head_dim), as RoostQkNormParams carries them; CpuOps itself
+ * has contiguous rows only. */
+int oracle_qk_norm(void* q, void* k, const void* q_weight, const void* k_weight, int dtype, int tokens, int q_heads,
+                   int kv_heads, int head_dim, int q_stride, int k_stride, float eps) {
+  const int64_t qs = q_stride ? q_stride : (int64_t)q_heads * head_dim;
+  const int64_t ks = k_stride ? k_stride : (int64_t)kv_heads * head_dim;
+  for (int t = 0; t < tokens; ++t) {
+    for (int h = 0; h < q_heads; ++h) norm_row(q, dtype, t * qs + (int64_t)h * head_dim, q_weight, head_dim, eps);
+  }
+  for (int t = 0; t < tokens; ++t) {
+    for (int h = 0; h < kv_heads; ++h) norm_row(k, dtype, t * ks + (int64_t)h * head_dim, k_weight, head_dim, eps);
+  }
+  return 0;
+}
+
+/* Frequency i of R rotary dims (CpuOps.cs:141-163): theta^(-2i/R), Llama 3 scaled when kind is 1. */
+static double rope_frequency(int i, int rot, double theta, int kind, double factor, double low_ff, double high_ff,
+                             double orig) {
+  const double f = pow(theta, -2.0 * i / rot);
+  if (kind != 1) return f;
+  const double wavelen = 2.0 * M_PI / f;
+  const double low = orig / low_ff;
+  const double high = orig / high_ff;
+  if (wavelen < high) return f;
+  if (wavelen > low) return f / factor;
+  const double smooth = (orig / wavelen - low_ff) / (high_ff - low_ff);
+  return (1.0 - smooth) * f / factor + smooth * f;
+}
+
+/* Rope (CpuOps.cs:111-175), in place: angle = position * f_i; NeoX pairs (i, i + R/2) or interleaved (2i, 2i + 1)
+ * become (x1 cos - x2 sin, x2 cos + x1 sin); elements at and beyond R are unchanged. The float parameters are widened
+ * from float as the C# fields are. */
+int oracle_rope(void* q, void* k, const int32_t* positions, int dtype, int tokens, int q_heads, int kv_heads,
+                int head_dim, int rotary_dim, int kind, int interleaved, float theta, float factor, float low_ff,
+                float high_ff, int orig_max) {
+  const int rot = rotary_dim == 0 ? head_dim : rotary_dim;
+  if (rot < 0 || rot > head_dim || (rot & 1) != 0) return fail("Rope: RotaryDim must be even and at most HeadDim");
+  const int half = rot / 2;
+  for (int t = 0; t < tokens; ++t) {
+    const double pos = positions[t];
+    for (int i = 0; i < half; ++i) {
+      const double f = rope_frequency(i, rot, theta, kind, factor, low_ff, high_ff, orig_max);
+      const double c = cos(pos * f), s = sin(pos * f);
+      const int ia = interleaved ? 2 * i : i;
+      const int ib = interleaved ? 2 * i + 1 : i + half;
+      for (int pass = 0; pass < 2; ++pass) {
+        void* x = pass == 0 ? q : k;
+        const int heads = pass == 0 ? q_heads : kv_heads;
+        for (int h = 0; h < heads; ++h) {
+          const int64_t o = ((int64_t)t * heads + h) * head_dim;
+          const double x1 = load(x, dtype, o + ia), x2 = load(x, dtype, o + ib);
+          store(x, dtype, o + ia, x1 * c - x2 * s);
+          store(x, dtype, o + ib, x2 * c + x1 * s);
+        }
+      }
     }
   }
   return 0;

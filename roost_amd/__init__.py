@@ -38,6 +38,9 @@ SIGMOID_MUL_VARIANT = "sigmoid-mul-gfx950"
 CAUSAL_CONV1D_VARIANT = "causal-conv1d-gfx950"
 STATE_COPY_VARIANT = "recurrent-state-copy-gfx950"
 STATE_SNAPSHOT_VARIANT = "recurrent-state-snapshot-gfx950"
+QK_NORM_VARIANT = "qk-norm-gfx950"
+ROPE_VARIANT = "rope-gfx950"
+QKV_VARIANT = "qkv-qk-norm-rope-cache-write-gfx950"
 
 
 class KernelError(RuntimeError):
@@ -367,6 +370,43 @@ def gated_rms_norm_params(x, gate, weight, out, *, rows, dim, eps):
     return p
 
 
+def qk_norm_params(q, k, q_weight, k_weight, *, tokens, q_heads, kv_heads, head_dim, eps, q_stride=0, k_stride=0):
+    """RoostQkNormParams: per-head RmsNorm of q and k in place (q_stride / k_stride: elements between tokens)."""
+    p = abi.new(abi.QkNormParams)
+    p.q, p.k, p.q_weight, p.k_weight = span(q), span(k), span(q_weight), span(k_weight)
+    p.tokens, p.q_heads, p.kv_heads, p.head_dim = tokens, q_heads, kv_heads, head_dim
+    p.q_stride, p.k_stride, p.eps = q_stride, k_stride, eps
+    p._keep = (q, k, q_weight, k_weight)
+    return p
+
+
+def rope_params(q, k, positions, *, tokens, q_heads, kv_heads, head_dim, theta, rotary_dim=0, interleaved=False,
+                llama3=None):
+    """RoostRopeParams; llama3 = (factor, low_freq_factor, high_freq_factor, original_max_position) selects Llama 3."""
+    p = abi.new(abi.RopeParams)
+    p.q, p.k, p.positions = span(q), span(k), span(positions)
+    p.tokens, p.q_heads, p.kv_heads, p.head_dim = tokens, q_heads, kv_heads, head_dim
+    p.rotary_dim, p.interleaved, p.theta = rotary_dim, int(interleaved), theta
+    if llama3 is not None:
+        p.kind = abi.ROPE_LLAMA3
+        (p.llama3_factor, p.llama3_low_freq_factor, p.llama3_high_freq_factor,
+         p.llama3_original_max_position) = llama3
+    p._keep = (q, k, positions)
+    return p
+
+
+def qkv_qk_norm_rope_cache_write_params(qkv, q, q_weight, k_weight, positions, k_cache, v_cache, slot_mapping, *,
+                                        tokens, q_heads, kv_heads, head_dim, page_size, eps, theta):
+    """RoostQkvQkNormRopeCacheWriteParams (QkvQkNormRopeCacheWriteArgs of the reference's C# ops)."""
+    p = abi.new(abi.QkvQkNormRopeCacheWriteParams)
+    p.qkv, p.q, p.q_weight, p.k_weight, p.positions = span(qkv), span(q), span(q_weight), span(k_weight), span(positions)
+    p.k_cache, p.v_cache, p.slot_mapping = span(k_cache), span(v_cache), span(slot_mapping)
+    p.tokens, p.q_heads, p.kv_heads, p.head_dim, p.page_size = tokens, q_heads, kv_heads, head_dim, page_size
+    p.eps, p.theta = eps, theta
+    p._keep = (qkv, q, q_weight, k_weight, positions, k_cache, v_cache, slot_mapping)
+    return p
+
+
 def sigmoid_mul_params(x, gate, out, *, rows, dim):
     p = abi.new(abi.SigmoidMulParams)
     p.input, p.gate, p.output = span(x), span(gate), span(out)
@@ -414,6 +454,18 @@ def sigmoid_mul(session: OpSession, *args, **kwargs) -> None:
 
 def causal_conv1d(session: OpSession, *args, **kwargs) -> None:
     session.launch(session.lib.entry(CAUSAL_CONV1D_VARIANT), causal_conv1d_params(*args, **kwargs))
+
+
+def qk_norm(session: OpSession, *args, **kwargs) -> None:
+    session.launch(session.lib.entry(QK_NORM_VARIANT), qk_norm_params(*args, **kwargs))
+
+
+def rope(session: OpSession, *args, **kwargs) -> None:
+    session.launch(session.lib.entry(ROPE_VARIANT), rope_params(*args, **kwargs))
+
+
+def qkv_qk_norm_rope_cache_write(session: OpSession, *args, **kwargs) -> None:
+    session.launch(session.lib.entry(QKV_VARIANT), qkv_qk_norm_rope_cache_write_params(*args, **kwargs))
 
 
 def recurrent_state_copy(session: OpSession, *args, **kwargs) -> None:

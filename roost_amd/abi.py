@@ -28,6 +28,8 @@ LAYOUT_ROW_MAJOR, LAYOUT_PAGED_NHD, LAYOUT_PAGED_HND = 0, 2, 3
 OP_PAGED_ATTENTION, OP_CACHE_WRITE, OP_GATED_DELTA_RULE = 4, 11, 128
 OP_CAUSAL_CONV1D, OP_RECURRENT_STATE_COPY, OP_RECURRENT_STATE_SNAPSHOT = 129, 130, 131
 OP_GATED_DELTA_RULE_GATES, OP_GATED_RMS_NORM, OP_SIGMOID_MUL = 133, 134, 135
+OP_QK_NORM, OP_ROPE, OP_QKV_QK_NORM_ROPE_CACHE_WRITE = 2, 3, 67
+ROPE_DEFAULT, ROPE_LLAMA3 = 0, 1
 
 # Flags
 FLAG_GRAPH_CAPTURABLE, FLAG_DETERMINISTIC, FLAG_BATCH_INVARIANT, FLAG_NEEDS_PLAN, FLAG_PLAN_PER_SHAPE = \
@@ -123,6 +125,30 @@ class GatedRmsNormParams(C.Structure):
                 ("eps", C.c_float), ("reserved0", C.c_uint32)]
 
 
+class QkNormParams(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("abi_minor", C.c_uint32), ("q", DeviceSpan), ("k", DeviceSpan),
+                ("q_weight", DeviceSpan), ("k_weight", DeviceSpan), ("tokens", C.c_uint32), ("q_heads", C.c_uint32),
+                ("kv_heads", C.c_uint32), ("head_dim", C.c_uint32), ("q_stride", C.c_uint32), ("k_stride", C.c_uint32),
+                ("eps", C.c_float), ("reserved0", C.c_uint32)]
+
+
+class RopeParams(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("abi_minor", C.c_uint32), ("q", DeviceSpan), ("k", DeviceSpan),
+                ("positions", DeviceSpan), ("tokens", C.c_uint32), ("q_heads", C.c_uint32), ("kv_heads", C.c_uint32),
+                ("head_dim", C.c_uint32), ("rotary_dim", C.c_uint32), ("kind", C.c_uint32),
+                ("interleaved", C.c_uint32), ("theta", C.c_float), ("llama3_factor", C.c_float),
+                ("llama3_low_freq_factor", C.c_float), ("llama3_high_freq_factor", C.c_float),
+                ("llama3_original_max_position", C.c_uint32)]
+
+
+class QkvQkNormRopeCacheWriteParams(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("abi_minor", C.c_uint32), ("qkv", DeviceSpan), ("q", DeviceSpan),
+                ("q_weight", DeviceSpan), ("k_weight", DeviceSpan), ("positions", DeviceSpan), ("k_cache", DeviceSpan),
+                ("v_cache", DeviceSpan), ("slot_mapping", DeviceSpan), ("tokens", C.c_uint32),
+                ("q_heads", C.c_uint32), ("kv_heads", C.c_uint32), ("head_dim", C.c_uint32),
+                ("page_size", C.c_uint32), ("eps", C.c_float), ("theta", C.c_float), ("reserved0", C.c_uint32)]
+
+
 class SigmoidMulParams(C.Structure):
     _fields_ = [("struct_size", C.c_uint32), ("abi_minor", C.c_uint32), ("input", DeviceSpan), ("gate", DeviceSpan),
                 ("output", DeviceSpan), ("rows", C.c_uint32), ("dim", C.c_uint32)]
@@ -153,8 +179,12 @@ ALL_STRUCTS = {
     "RoostGatedDeltaRuleGatesParams": GatedDeltaRuleGatesParams, "RoostGatedRmsNormParams": GatedRmsNormParams,
     "RoostSigmoidMulParams": SigmoidMulParams, "RoostCausalConv1dParams": CausalConv1dParams,
     "RoostRecurrentStateCopyParams": RecurrentStateCopyParams,
-    "RoostRecurrentStateSnapshotParams": RecurrentStateSnapshotParams,
+    "RoostRecurrentStateSnapshotParams": RecurrentStateSnapshotParams, "RoostQkNormParams": QkNormParams,
+    "RoostRopeParams": RopeParams,
 }
+
+# Records of this library with no counterpart in the reference's C header (so not in its layout fixture).
+EXTENSION_STRUCTS = {"RoostQkvQkNormRopeCacheWriteParams": QkvQkNormRopeCacheWriteParams}
 
 
 def new(struct_type):

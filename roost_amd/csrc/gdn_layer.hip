@@ -30,14 +30,6 @@ __device__ __forceinline__ void StoreF(void* p, uint32_t dt, int64_t i, float v)
   }
 }
 
-// Two floats to packed bf16 with gfx950's v_cvt_pk_bf16_f32: round to nearest, ties to even, as F32ToBf16 does, in one
-// instruction instead of a dozen. Only a NaN may come out with other NaN bits than F32ToBf16's 0x7FC0.
-__device__ __forceinline__ uint32_t PackBf16Rne(float lo, float hi) {
-  typedef float F2 __attribute__((ext_vector_type(2)));
-  typedef __bf16 B2 __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((F2){lo, hi}, B2));
-}
-
 // sigmoid and SiLU with the hardware reciprocal (v_rcp_f32, about 1 ulp) instead of a full-precision divide, which
 // would cost ten VALU instructions per element in these streaming kernels.
 __device__ __forceinline__ float SigmoidF(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }

@@ -1,0 +1,829 @@
+// The attention layer's input ops for gfx950: QkNorm (ROOST_OP_QK_NORM), Rope (ROOST_OP_ROPE) and the fused
+// QkvQkNormRopeCacheWrite (ROOST_OP_QKV_QK_NORM_ROPE_CACHE_WRITE) that feeds PagedAttention.
+//
+// Semantics: src/Starlings.Roost.Ops/CpuOps.cs:63-175 (QkNorm, Rope) and CpuOps.Fused.cs:37-95 (the fused op, defined
+// as its unfused parts in order), with the refusal rules of the reference's QkNormRun and RopeRun
+// (kernels/src/m0_ops.cu:89-255). Every element is computed in fp32 and rounded into its span's type where CpuOps
+// stores it: the fused op rounds the normalised head before rotating it, as the unfused calls do.
+//
+// One (token, head) row is served by G lanes of a wavefront (G a power of two, 64 / G rows per wavefront); a lane
+// holds kJ chunks of kV consecutive elements (16-byte loads and stores when the rows allow them). The sum of squares
+// is reduced over the G lanes by a fixed xor butterfly. The rotation partner of each element (i +- R/2 for NeoX halves,
+// i ^ 1 for interleaved pairs) is read from a per-wavefront copy of the rounded row in LDS. Angles follow the
+// reference's own rope kernel: frequencies theta^(-2i/R) (Llama 3 scaled when asked) in double in an LDS table,
+// position * frequency in double reduced modulo 2 pi in double, then sincosf of the reduced angle.
+//
+// Nothing here allocates, synchronises the host or reads host memory; each call is one launch on the caller's stream.
+
+#include <cmath>
+
+#include "common.h"
+
+namespace {
+
+using namespace roost_dev;
+
+constexpr int kMaxHeadDim = 1024;
+constexpr int kMaxPairs = kMaxHeadDim / 2;
+
+template <typename T>
+__device__ __forceinline__ float LoadT(const T* p) {
+  if constexpr (sizeof(T) == 2) {
+    return Bf16ToF32(*reinterpret_cast<const uint16_t*>(p));
+  } else {
+    return *reinterpret_cast<const float*>(p);
+  }
+}
+template <typename T>
+__device__ __forceinline__ void StoreT(T* p, float v) {
+  if constexpr (sizeof(T) == 2) {
+    *reinterpret_cast<uint16_t*>(p) = static_cast<uint16_t>(PackBf16Rne(v, 0.0f));
+  } else {
+    *reinterpret_cast<float*>(p) = v;
+  }
+}
+// v rounded to T and widened back (what CpuOps reads after storing v in T).
+template <typename T>
+__device__ __forceinline__ float RoundT(float v) {
+  if constexpr (sizeof(T) == 2) {
+    return Bf16LoToF32(PackBf16Rne(v, 0.0f));
+  } else {
+    return v;
+  }
+}
+
+// Elements e and e + 1 of v rounded to T (bf16: one v_cvt_pk_bf16_f32, round to nearest even).
+template <typename T>
+__device__ __forceinline__ void RoundPairT(float* v) {
+  if constexpr (sizeof(T) == 2) {
+    const uint32_t w = PackBf16Rne(v[0], v[1]);
+    v[0] = Bf16LoToF32(w);
+    v[1] = Bf16HiToF32(w);
+  }
+}
+
+// kV consecutive elements at p as floats (one 16-byte load when kV * sizeof(T) == 16).
+template <typename T, int kV>
+__device__ __forceinline__ void LoadChunk(const T* p, float* v) {
+  if constexpr (kV * sizeof(T) == 16) {
+    const uint4 q = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int e = 0; e < kV; ++e) {
+      v[e] = sizeof(T) == 2 ? ((e & 1) ? Bf16HiToF32(w[e >> 1]) : Bf16LoToF32(w[e >> 1])) : __uint_as_float(w[e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < kV; ++e) v[e] = LoadT(p + e);
+  }
+}
+template <typename T, int kV>
+__device__ __forceinline__ void StoreChunk(T* p, const float* v) {
+  if constexpr (kV * sizeof(T) == 16) {
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) w[q] = sizeof(T) == 2 ? PackBf16Rne(v[2 * q], v[2 * q + 1]) : __float_as_uint(v[q]);
+    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < kV; ++e) StoreT(p + e, v[e]);
+  }
+}
+
+// What a rope launch needs besides the rows.
+struct RopeSpec {
+  const int32_t* positions;
+  uint32_t rot;  // rotated dims R (even, <= head_dim)
+  uint32_t interleaved;
+  uint32_t llama3;
+  float theta, factor, low_ff, high_ff;
+  uint32_t original_max;
+  uint32_t chunk_pairs;  // every pair lies within one chunk (interleaved) or pairs whole chunks (NeoX)
+};
+
+// Frequency i of R rotary dims (CpuOps.cs:141-163): theta^(-2i/R), Llama 3 scaled when asked; in double.
+__device__ double Frequency(const RopeSpec& r, uint32_t i) {
+  double f = pow(static_cast<double>(r.theta), -2.0 * i / r.rot);
+  if (r.llama3) {
+    const double orig = r.original_max;
+    const double wavelen = 2.0 * 3.14159265358979323846 / f;
+    const double low = orig / static_cast<double>(r.low_ff), high = orig / static_cast<double>(r.high_ff);
+    if (wavelen < high) {
+      // kept
+    } else if (wavelen > low) {
+      f = f / static_cast<double>(r.factor);
+    } else {
+      const double smooth = (orig / wavelen - static_cast<double>(r.low_ff)) /
+                            (static_cast<double>(r.high_ff) - static_cast<double>(r.low_ff));
+      f = (1.0 - smooth) * f / static_cast<double>(r.factor) + smooth * f;
+    }
+  }
+  return f;
+}
+
+// The workgroup's angle table: cs[t * R/2 + i] = (cos, sin) of positions[t0 + t] * f_i for its tokens t < count. The
+// angle is formed and reduced to [-pi, pi] in double, then sincosf of the reduced angle. Every head of a token reads
+// the same entries, so each is computed once per token. Two barriers: frequencies, then angles.
+__device__ void BuildAngles(const RopeSpec& r, uint64_t t0, uint32_t count, double* freq, float2* cs) {
+  constexpr double kTwoPi = 6.283185307179586476925286766559;
+  constexpr double kInvTwoPi = 0.15915494309189533576888376337251;
+  const uint32_t half = r.rot / 2;
+  for (uint32_t i = threadIdx.x; i < half; i += blockDim.x) freq[i] = Frequency(r, i);
+  __syncthreads();
+  for (uint32_t idx = threadIdx.x; idx < count * half; idx += blockDim.x) {
+    const uint32_t t = idx / half, i = idx - t * half;
+    const double a = static_cast<double>(r.positions[t0 + t]) * freq[i];
+    const double red = fma(-kTwoPi, rint(a * kInvTwoPi), a);
+    float sn, c;
+    sincosf(static_cast<float>(red), &sn, &c);
+    cs[idx] = make_float2(c, sn);
+  }
+  __syncthreads();
+}
+
+// One row's values held by the G lanes serving it: chunk c = sub + G * j of kV elements for j < kJ.
+template <int kV, int kJ>
+struct RowRegs {
+  float v[kJ][kV];
+};
+
+// RmsNorm of the row in place: v * rsqrt(mean(v^2) + eps) * w, then rounded to T (CpuOps.cs:89-103). Lanes whose
+// chunks lie beyond head_dim hold zeros and contribute nothing.
+template <typename T, int kV, int kJ>
+__device__ __forceinline__ void NormRow(RowRegs<kV, kJ>& r, const T* w, uint32_t sub, uint32_t g, uint32_t chunks,
+                                        uint32_t head_dim, float eps) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kJ; ++j)
+#pragma unroll
+    for (int e = 0; e < kV; ++e) ss = fmaf(r.v[j][e], r.v[j][e], ss);
+  for (uint32_t m = 1; m < g; m <<= 1) ss += __shfl_xor(ss, static_cast<int>(m), 64);
+  const float inv = rsqrtf(ss / static_cast<float>(head_dim) + eps);
+#pragma unroll
+  for (int j = 0; j < kJ; ++j) {
+    const uint32_t c = sub + g * j;
+    if (c < chunks) {
+      float wv[kV];
+      LoadChunk<T, kV>(w + c * kV, wv);
+#pragma unroll
+      for (int e = 0; e < kV; ++e) r.v[j][e] = r.v[j][e] * inv * wv[e];
+      if constexpr (kV % 2 == 0) {
+#pragma unroll
+        for (int e = 0; e < kV; e += 2) RoundPairT<T>(&r.v[j][e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < kV; ++e) r.v[j][e] = RoundT<T>(r.v[j][e]);
+      }
+    }
+  }
+}
+
+// The rotation with whole chunks (vector rows, host-checked layout): interleaved pairs lie inside a chunk; NeoX pairs
+// chunk c with chunk c +- R/(2 kV), read from the row's LDS copy as vectors. Same arithmetic, element for element, as
+// the general form below.
+template <typename T, int kV, int kJ>
+__device__ __forceinline__ void RopeRowChunks(RowRegs<kV, kJ>& r, float* row, const float2* cs, const RopeSpec& rs,
+                                              uint32_t sub, uint32_t g, uint32_t chunks) {
+  static_assert(kV % 4 == 0, "vector chunks hold 4 or 8 elements");
+  if (rs.interleaved) {
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+      const uint32_t c = sub + g * j, i0 = c * kV;
+      if (c >= chunks || i0 >= rs.rot) continue;
+      const float4* a4 = reinterpret_cast<const float4*>(cs + i0 / 2);
+#pragma unroll
+      for (int q = 0; q < kV / 4; ++q) {
+        const float4 a = a4[q];  // pairs (2q, 2q + 1) of the chunk: (cos, sin) twice
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int e = 4 * q + 2 * h;
+          const float c0 = h ? a.z : a.x, s0 = h ? a.w : a.y;
+          const float x1 = r.v[j][e], x2 = r.v[j][e + 1];
+          r.v[j][e] = fmaf(x1, c0, -(x2 * s0));
+          r.v[j][e + 1] = fmaf(x2, c0, x1 * s0);
+          RoundPairT<T>(&r.v[j][e]);
+        }
+      }
+    }
+    return;
+  }
+  const uint32_t half = rs.rot / 2;
+#pragma unroll
+  for (int j = 0; j < kJ; ++j) {
+    const uint32_t c = sub + g * j;
+    if (c < chunks && c * kV < rs.rot) {
+#pragma unroll
+      for (int q = 0; q < kV / 4; ++q) {
+        reinterpret_cast<float4*>(row + c * kV)[q] =
+            make_float4(r.v[j][4 * q], r.v[j][4 * q + 1], r.v[j][4 * q + 2], r.v[j][4 * q + 3]);
+      }
+    }
+  }
+  __builtin_amdgcn_wave_barrier();  // the row's lanes are all in this wavefront: LDS order within it is program order
+#pragma unroll
+  for (int j = 0; j < kJ; ++j) {
+    const uint32_t c = sub + g * j, i0 = c * kV;
+    if (c >= chunks || i0 >= rs.rot) continue;
+    const bool first = i0 < half;
+    const uint32_t p0 = first ? i0 + half : i0 - half, k0 = first ? i0 : i0 - half;
+    float xp[kV];
+    float2 a[kV];
+#pragma unroll
+    for (int q = 0; q < kV / 4; ++q) {
+      const float4 v = reinterpret_cast<const float4*>(row + p0)[q];
+      xp[4 * q] = v.x; xp[4 * q + 1] = v.y; xp[4 * q + 2] = v.z; xp[4 * q + 3] = v.w;
+    }
+#pragma unroll
+    for (int q = 0; q < kV / 2; ++q) {
+      const float4 v = reinterpret_cast<const float4*>(cs + k0)[q];
+      a[2 * q] = make_float2(v.x, v.y);
+      a[2 * q + 1] = make_float2(v.z, v.w);
+    }
+#pragma unroll
+    for (int e = 0; e < kV; ++e) {
+      const float x = r.v[j][e];
+      r.v[j][e] = first ? fmaf(x, a[e].x, -(xp[e] * a[e].y)) : fmaf(x, a[e].x, xp[e] * a[e].y);
+    }
+#pragma unroll
+    for (int e = 0; e < kV; e += 2) RoundPairT<T>(&r.v[j][e]);
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
+// Rotation of the row in place (CpuOps.cs:111-139, 165-175): pair (x1, x2) -> (x1 c - x2 s, x2 c + x1 s), NeoX
+// partners i +- R/2 or interleaved i ^ 1, elements at and beyond R kept; rounded to T. `row` is this row's LDS copy.
+template <typename T, int kV, int kJ>
+__device__ __forceinline__ void RopeRow(RowRegs<kV, kJ>& r, float* row, const float2* cs, const RopeSpec& rs,
+                                        uint32_t sub, uint32_t g, uint32_t chunks) {
+  if constexpr (kV > 1) {
+    if (rs.chunk_pairs) {
+      RopeRowChunks<T, kV, kJ>(r, row, cs, rs, sub, g, chunks);
+      return;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kJ; ++j) {
+    const uint32_t c = sub + g * j;
+    if (c < chunks) {
+#pragma unroll
+      for (int e = 0; e < kV; ++e) row[c * kV + e] = r.v[j][e];
+    }
+  }
+  __builtin_amdgcn_wave_barrier();  // the row's lanes are all in this wavefront: LDS order within it is program order
+  const uint32_t half = rs.rot / 2;
+#pragma unroll
+  for (int j = 0; j < kJ; ++j) {
+    const uint32_t c = sub + g * j;
+    if (c >= chunks) continue;
+#pragma unroll
+    for (int e = 0; e < kV; ++e) {
+      const uint32_t i = c * kV + e;
+      if (i >= rs.rot) continue;
+      uint32_t pair, partner;
+      bool first;
+      if (rs.interleaved) {
+        pair = i >> 1;
+        partner = i ^ 1u;
+        first = (i & 1u) == 0;
+      } else {
+        first = i < half;
+        pair = first ? i : i - half;
+        partner = first ? i + half : i - half;
+      }
+      const float2 a = cs[pair];
+      const float x = r.v[j][e], xp = row[partner];
+      // Explicit fused multiply-adds: every kernel that rotates a row rounds it the same way.
+      r.v[j][e] = RoundT<T>(first ? fmaf(x, a.x, -(xp * a.y)) : fmaf(x, a.x, xp * a.y));
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
+template <typename T, int kV, int kJ>
+__device__ __forceinline__ void LoadRow(RowRegs<kV, kJ>& r, const T* src, uint32_t sub, uint32_t g, uint32_t chunks,
+                                        bool live) {
+#pragma unroll
+  for (int j = 0; j < kJ; ++j) {
+    const uint32_t c = sub + g * j;
+    if (live && c < chunks) {
+      LoadChunk<T, kV>(src + c * kV, r.v[j]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < kV; ++e) r.v[j][e] = 0.0f;
+    }
+  }
+}
+template <typename T, int kV, int kJ>
+__device__ __forceinline__ void StoreRow(const RowRegs<kV, kJ>& r, T* dst, uint32_t sub, uint32_t g, uint32_t chunks) {
+#pragma unroll
+  for (int j = 0; j < kJ; ++j) {
+    const uint32_t c = sub + g * j;
+    if (c < chunks) StoreChunk<T, kV>(dst + c * kV, r.v[j]);
+  }
+}
+
+// The lane's place: row index (over the whole launch), lane within the row.
+struct Lane {
+  uint64_t row;
+  uint32_t sub;
+};
+__device__ __forceinline__ Lane Place(uint32_t g) {
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  Lane l;
+  l.sub = lane % g;
+  l.row = (static_cast<uint64_t>(blockIdx.x) * (blockDim.x >> 6) + wave) * (64 / g) + lane / g;
+  return l;
+}
+
+// Rope launches: workgroup b serves tokens [b * tpb, b * tpb + tpb) (tpb tokens per block), all of their head rows;
+// wavefront w takes row groups w, w + 4, ... of 64 / g rows each. Dynamic LDS, sized by RopeLdsBytes: the frequency
+// table (R/2 doubles), the angle table (tpb x R/2 (cos, sin) pairs) and each wavefront's row copies (64 / g rows).
+constexpr uint32_t kMaxTpb = 8;
+
+__host__ __device__ constexpr uint64_t RopeLdsBytes(uint32_t half, uint32_t tpb, uint32_t g, uint32_t head_dim) {
+  return uint64_t{half} * 8 + uint64_t{tpb} * half * 8 + uint64_t{4} * (64 / g) * head_dim * 4;
+}
+__device__ __forceinline__ void CarveLds(uint32_t half, uint32_t tpb, uint32_t g, uint32_t head_dim, double** freq,
+                                         float2** cs, float** rows) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  *freq = reinterpret_cast<double*>(lds_raw);
+  *cs = reinterpret_cast<float2*>(lds_raw + uint64_t{half} * 8);
+  *rows = reinterpret_cast<float*>(lds_raw + uint64_t{half} * 8 + uint64_t{tpb} * half * 8);
+  (void)g;
+  (void)head_dim;
+}
+
+struct TokenRows {
+  uint64_t t0;     // first token of the workgroup
+  uint32_t count;  // its tokens
+  uint32_t rows;   // count * heads
+};
+__device__ __forceinline__ TokenRows BlockTokens(uint32_t tokens, uint32_t tpb, uint32_t heads) {
+  TokenRows tr;
+  tr.t0 = static_cast<uint64_t>(blockIdx.x) * tpb;
+  tr.count = static_cast<uint32_t>(min(static_cast<uint64_t>(tpb), tokens - tr.t0));
+  tr.rows = tr.count * heads;
+  return tr;
+}
+
+// ---- QkNorm: rows are (token, head) over q heads then k heads, in place. --------------------------------------------
+template <typename T, int kV, int kJ>
+__global__ void __launch_bounds__(256) QkNormKernel(T* q, T* k, const T* qw, const T* kw, uint32_t tokens,
+                                                    uint32_t q_heads, uint32_t kv_heads, uint32_t head_dim,
+                                                    uint64_t q_stride, uint64_t k_stride, float eps, uint32_t g) {
+  const Lane l = Place(g);
+  const uint32_t heads = q_heads + kv_heads;
+  const uint64_t rows = static_cast<uint64_t>(tokens) * heads;
+  const bool live = l.row < rows;
+  const uint64_t t = live ? l.row / heads : 0;
+  const uint32_t h = live ? static_cast<uint32_t>(l.row - t * heads) : 0;
+  const bool is_q = h < q_heads;
+  T* x = is_q ? q + t * q_stride + static_cast<uint64_t>(h) * head_dim
+              : k + t * k_stride + static_cast<uint64_t>(h - q_heads) * head_dim;
+  const uint32_t chunks = head_dim / kV;
+  RowRegs<kV, kJ> r;
+  LoadRow<T, kV, kJ>(r, x, l.sub, g, chunks, live);
+  NormRow<T, kV, kJ>(r, is_q ? qw : kw, l.sub, g, chunks, head_dim, eps);
+  if (live) StoreRow<T, kV, kJ>(r, x, l.sub, g, chunks);
+}
+
+// ---- Rope: rows are (token, head) over q heads then k heads, contiguous [tokens, heads, head_dim], in place. --------
+template <typename T, int kV, int kJ>
+__global__ void __launch_bounds__(256) RopeKernel(T* q, T* k, RopeSpec rs, uint32_t tokens, uint32_t q_heads,
+                                                  uint32_t kv_heads, uint32_t head_dim, uint32_t g, uint32_t tpb) {
+  const uint32_t heads = q_heads + kv_heads;
+  const TokenRows tr = BlockTokens(tokens, tpb, heads);
+  double* freq;
+  float2* cs;
+  float* lds;
+  CarveLds(rs.rot / 2, tpb, g, head_dim, &freq, &cs, &lds);
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, per = 64 / g, sub = lane % g;
+  const uint32_t chunks = head_dim / kV, half = rs.rot / 2;
+  float* row_lds = lds + (wave * per + lane / g) * head_dim;
+  // Row r of the workgroup: its address, and whether this lane's row exists.
+  auto row_at = [&](uint32_t grp, bool* live, uint32_t* lt) -> T* {
+    const uint32_t r = grp * per + lane / g;
+    *live = r < tr.rows;
+    *lt = *live ? r / heads : 0;
+    const uint32_t h = *live ? r - *lt * heads : 0;
+    const uint64_t t = tr.t0 + *lt;
+    return h < q_heads ? q + (t * q_heads + h) * head_dim : k + (t * kv_heads + (h - q_heads)) * head_dim;
+  };
+  // Software pipeline: the first group's rows are requested before the angle table is built, and each group's
+  // successor before the group is computed.
+  bool live;
+  uint32_t lt;
+  T* x = row_at(wave, &live, &lt);
+  RowRegs<kV, kJ> cur;
+  LoadRow<T, kV, kJ>(cur, x, sub, g, chunks, live);
+  BuildAngles(rs, tr.t0, tr.count, freq, cs);
+  for (uint32_t grp = wave; grp * per < tr.rows; grp += 4) {
+    bool live_n;
+    uint32_t lt_n;
+    T* x_n = row_at(grp + 4, &live_n, &lt_n);
+    RowRegs<kV, kJ> nxt;
+    LoadRow<T, kV, kJ>(nxt, x_n, sub, g, chunks, live_n);
+    RopeRow<T, kV, kJ>(cur, row_lds, cs + lt * half, rs, sub, g, chunks);
+    if (live) StoreRow<T, kV, kJ>(cur, x, sub, g, chunks);
+    cur = nxt;
+    x = x_n;
+    live = live_n;
+    lt = lt_n;
+  }
+}
+
+// ---- QkvQkNormRopeCacheWrite: rows are (token, head) over q, k and v heads of each [q | k | v] row. ----------------
+struct QkvArgs {
+  const void* qkv;
+  void* q;
+  const void* qw;
+  const void* kw;
+  void* k_cache;
+  void* v_cache;
+  const int64_t* slots;
+  uint64_t pool_rows;  // (page, offset) rows both pools hold
+  uint32_t tokens, q_heads, kv_heads, head_dim;
+  float eps;
+};
+
+// A v row goes to the cache as stored (CacheWrite copies it; a wider cache type widens it exactly).
+template <typename T, typename C, int kV, int kJ>
+__device__ __forceinline__ void CopyVRow(const T* src, C* dst, uint32_t sub, uint32_t g, uint32_t chunks) {
+#pragma unroll
+  for (int j = 0; j < kJ; ++j) {
+    const uint32_t c = sub + g * j;
+    if (c >= chunks) continue;
+    if constexpr (sizeof(C) == sizeof(T) && kV * sizeof(T) == 16) {
+      *reinterpret_cast<uint4*>(dst + c * kV) = *reinterpret_cast<const uint4*>(src + c * kV);
+    } else if constexpr (sizeof(C) == sizeof(T)) {
+#pragma unroll
+      for (int e = 0; e < kV; ++e) dst[c * kV + e] = src[c * kV + e];
+    } else {
+      float v[kV];
+      LoadChunk<T, kV>(src + c * kV, v);
+#pragma unroll
+      for (int e = 0; e < kV; ++e) StoreT(dst + c * kV + e, v[e]);
+    }
+  }
+}
+
+// Workgroup b serves tokens [b * tpb, b * tpb + tpb). Its wavefronts first take the v rows (plain copies), then the q
+// and k rows (norm, rounding, rotation), so a wavefront's rows share one path.
+template <typename T, typename C, int kV, int kJ>
+__global__ void __launch_bounds__(256) QkvKernel(QkvArgs a, RopeSpec rs, uint32_t g, uint32_t tpb) {
+  double* freq;
+  float2* cs;
+  float* lds;
+  CarveLds(rs.rot / 2, tpb, g, a.head_dim, &freq, &cs, &lds);
+  const uint32_t qk_heads = a.q_heads + a.kv_heads, heads = qk_heads + a.kv_heads;
+  const TokenRows tr = BlockTokens(a.tokens, tpb, heads);
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, per = 64 / g, sub = lane % g;
+  const uint32_t chunks = a.head_dim / kV, half = rs.rot / 2;
+  const T* qkv = static_cast<const T*>(a.qkv);
+  // v rows (no angles needed): tr.count * kv_heads of them.
+  const uint32_t v_rows = tr.count * a.kv_heads;
+  for (uint32_t grp = wave; grp * per < v_rows; grp += 4) {
+    const uint32_t r = grp * per + lane / g;
+    if (r >= v_rows) continue;
+    const uint32_t lt = r / a.kv_heads, h = r - lt * a.kv_heads;
+    const uint64_t t = tr.t0 + lt;
+    const int64_t slot = a.slots[t];
+    if (slot < 0 || static_cast<uint64_t>(slot) >= a.pool_rows) continue;
+    CopyVRow<T, C, kV, kJ>(qkv + (t * heads + qk_heads + h) * a.head_dim,
+                           static_cast<C*>(a.v_cache) + (static_cast<uint64_t>(slot) * a.kv_heads + h) * a.head_dim,
+                           sub, g, chunks);
+  }
+  float* row_lds = lds + (wave * per + lane / g) * a.head_dim;
+  const uint32_t qk_rows = tr.count * qk_heads;
+  struct RowAt {
+    bool live, is_q;
+    uint32_t lt, h;
+  };
+  auto row_at = [&](uint32_t grp) {
+    RowAt w;
+    const uint32_t r = grp * per + lane / g;
+    w.live = r < qk_rows;
+    w.lt = w.live ? r / qk_heads : 0;
+    w.h = w.live ? r - w.lt * qk_heads : 0;
+    w.is_q = w.h < a.q_heads;
+    return w;
+  };
+  auto src_of = [&](const RowAt& w) { return qkv + ((tr.t0 + w.lt) * heads + w.h) * a.head_dim; };
+  // Software pipeline: the first group's rows are requested before the angle table is built, and each group's
+  // successor before the group is computed.
+  RowAt w = row_at(wave);
+  RowRegs<kV, kJ> cur;
+  LoadRow<T, kV, kJ>(cur, src_of(w), sub, g, chunks, w.live);
+  BuildAngles(rs, tr.t0, tr.count, freq, cs);
+  for (uint32_t grp = wave; grp * per < qk_rows; grp += 4) {
+    const RowAt wn = row_at(grp + 4);
+    RowRegs<kV, kJ> nxt;
+    LoadRow<T, kV, kJ>(nxt, src_of(wn), sub, g, chunks, wn.live);
+    NormRow<T, kV, kJ>(cur, static_cast<const T*>(w.is_q ? a.qw : a.kw), sub, g, chunks, a.head_dim, a.eps);
+    RopeRow<T, kV, kJ>(cur, row_lds, cs + w.lt * half, rs, sub, g, chunks);
+    const uint64_t t = tr.t0 + w.lt;
+    if (w.live && w.is_q) {
+      StoreRow<T, kV, kJ>(cur, static_cast<T*>(a.q) + (t * a.q_heads + w.h) * a.head_dim, sub, g, chunks);
+    } else if (w.live) {
+      const int64_t slot = a.slots[t];
+      if (slot >= 0 && static_cast<uint64_t>(slot) < a.pool_rows) {
+        C* dst = static_cast<C*>(a.k_cache) + (static_cast<uint64_t>(slot) * a.kv_heads + (w.h - a.q_heads)) * a.head_dim;
+        if constexpr (sizeof(C) == sizeof(T)) {
+          StoreRow<T, kV, kJ>(cur, reinterpret_cast<T*>(dst), sub, g, chunks);
+        } else {
+#pragma unroll
+          for (int j = 0; j < kJ; ++j) {
+            const uint32_t c = sub + g * j;
+            if (c < chunks) {
+#pragma unroll
+              for (int e = 0; e < kV; ++e) StoreT(dst + c * kV + e, cur.v[j][e]);
+            }
+          }
+        }
+      }
+    }
+    cur = nxt;
+    w = wn;
+  }
+}
+
+// ---- Host side ------------------------------------------------------------------------------------------------------
+
+uint64_t ElemBytes(uint32_t dt) { return dt == ROOST_DTYPE_BF16 ? 2 : 4; }
+bool ActType(uint32_t dt) { return dt == ROOST_DTYPE_BF16 || dt == ROOST_DTYPE_F32; }
+bool SpanOk(const RoostDeviceSpan& s, uint32_t dt, uint64_t elems) {
+  return s.reserved0 == 0 && s.dtype == dt && s.length >= elems && (elems == 0 || s.address != nullptr);
+}
+uintptr_t Addr(const void* p) { return reinterpret_cast<uintptr_t>(p); }
+bool Overlap(const RoostDeviceSpan& x, uint64_t xn, const RoostDeviceSpan& y, uint64_t yn) {
+  return Addr(x.address) < Addr(y.address) + yn * ElemBytes(y.dtype) &&
+         Addr(y.address) < Addr(x.address) + xn * ElemBytes(x.dtype);
+}
+
+// How a row of head_dim elements maps onto lanes: kV elements per chunk (16 / element bytes when every row start is
+// 16-byte aligned, else 1), kJ chunks per lane, g lanes per row.
+struct RowShape {
+  bool vec;
+  int kj;  // 1, 2 (vector) or 1, 16 (scalar)
+  uint32_t g;
+};
+uint32_t Pow2AtLeast(uint32_t n) {
+  uint32_t p = 1;
+  while (p < n) p <<= 1;
+  return p;
+}
+RowShape ShapeFor(uint32_t head_dim, uint32_t elem_bytes, bool aligned16) {
+  const uint32_t v = 16 / elem_bytes;
+  RowShape s{};
+  s.vec = aligned16 && head_dim % v == 0 && head_dim / v <= 128;  // two 16-byte chunks per lane at most
+  const uint32_t chunks = s.vec ? head_dim / v : head_dim;
+  if (chunks <= 64) {
+    s.kj = 1;
+    s.g = Pow2AtLeast(chunks);
+  } else {
+    s.kj = s.vec ? 2 : 16;
+    s.g = 64;
+  }
+  return s;
+}
+// Every row start base + t * stride + h * head_dim (elements) is 16-byte aligned when these are.
+bool RowsAligned16(const void* base, uint64_t stride, uint32_t head_dim, uint32_t elem_bytes) {
+  return roost::Aligned(base, 16) && (stride * elem_bytes) % 16 == 0 && (uint64_t{head_dim} * elem_bytes) % 16 == 0;
+}
+// Whether the rotation can take whole chunks (vector rows only): interleaved pairs never straddle a chunk when R is a
+// multiple of the chunk, NeoX halves pair whole chunks when R/2 is.
+uint32_t ChunkPairs(const RowShape& s, uint32_t elem_bytes, uint32_t rot, bool interleaved) {
+  const uint32_t v = 16 / elem_bytes;
+  if (!s.vec) return 0u;
+  return (interleaved ? rot % v == 0 : (rot / 2) % v == 0) ? 1u : 0u;
+}
+uint32_t Blocks(uint64_t items, uint32_t per) { return static_cast<uint32_t>(roost::CeilDiv(items, per)); }
+// Tokens per rope workgroup: about a thousand workgroups for large calls, one token each for small ones.
+uint32_t TokensPerBlock(uint32_t tokens) { return std::min<uint32_t>(kMaxTpb, std::max<uint32_t>(1, tokens / 1024)); }
+uint32_t GridFor(uint64_t rows, uint32_t g) {
+  return static_cast<uint32_t>(roost::CeilDiv(rows, uint64_t{4} * (64 / g)));
+}
+
+// Instantiates `launch` for (T, kV, kJ) from the dtype and the row shape.
+template <typename F>
+void DispatchShape(uint32_t dt, const RowShape& s, F&& launch) {
+  auto by_kj = [&](auto t_tag, auto kv_tag) {
+    using T = decltype(t_tag);
+    constexpr int kV = decltype(kv_tag)::value;
+    if constexpr (kV == 1) {
+      if (s.kj == 1) launch(T{}, std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
+      else launch(T{}, std::integral_constant<int, 1>{}, std::integral_constant<int, 16>{});
+    } else {
+      if (s.kj == 1) launch(T{}, std::integral_constant<int, kV>{}, std::integral_constant<int, 1>{});
+      else launch(T{}, std::integral_constant<int, kV>{}, std::integral_constant<int, 2>{});
+    }
+  };
+  if (dt == ROOST_DTYPE_BF16) {
+    if (s.vec) by_kj(uint16_t{}, std::integral_constant<int, 8>{});
+    else by_kj(uint16_t{}, std::integral_constant<int, 1>{});
+  } else {
+    if (s.vec) by_kj(float{}, std::integral_constant<int, 4>{});
+    else by_kj(float{}, std::integral_constant<int, 1>{});
+  }
+}
+
+RoostStatus CheckRopeSpec(const char* op, uint32_t head_dim, uint32_t rot, uint32_t kind, float theta, float factor,
+                          float low, float high, uint32_t orig) {
+  using roost::Fail;
+  if (kind != ROOST_ROPE_DEFAULT && kind != ROOST_ROPE_LLAMA3) {
+    return Fail(ROOST_STATUS_INVALID_ARGUMENT, std::string(op) + ": kind must be DEFAULT or LLAMA3");
+  }
+  if (rot > head_dim || (rot & 1u) != 0 || rot == 0) {
+    return Fail(ROOST_STATUS_INVALID_ARGUMENT, std::string(op) + ": rotary_dim must be even and at most head_dim");
+  }
+  if (!(theta > 0.0f)) return Fail(ROOST_STATUS_INVALID_ARGUMENT, std::string(op) + ": theta must be positive");
+  if (kind == ROOST_ROPE_LLAMA3 && (!(factor > 0.0f) || !(low > 0.0f) || !(high > low) || orig == 0)) {
+    return Fail(ROOST_STATUS_INVALID_ARGUMENT,
+                std::string(op) + ": llama3 needs factor > 0, 0 < low < high and a positive max");
+  }
+  return ROOST_STATUS_OK;
+}
+
+}  // namespace
+
+// ---- Entry points ---------------------------------------------------------------------------------------------------
+
+extern "C" ROOST_API RoostStatus roost_qk_norm_run(RoostContext* ctx, const void* params, const RoostWorkspace*,
+                                                   void* stream) {
+  using namespace roost;
+  constexpr char kOp[] = "QkNorm";
+  if (ctx == nullptr || params == nullptr) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "QkNorm: ctx or params is NULL");
+  ROOST_TRY(CheckHeader(params, sizeof(RoostQkNormParams), kOp));
+  const auto& p = *static_cast<const RoostQkNormParams*>(params);
+  return Guarded(kOp, [&]() -> RoostStatus {
+    if (p.reserved0 != 0) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "QkNorm: reserved0 must be zero");
+    if (p.head_dim == 0 || p.q_heads == 0 || p.kv_heads == 0) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "QkNorm: head_dim, q_heads and kv_heads must be non-zero");
+    }
+    const uint64_t qrow = uint64_t{p.q_heads} * p.head_dim, krow = uint64_t{p.kv_heads} * p.head_dim;
+    const uint64_t qs = p.q_stride == 0 ? qrow : p.q_stride, ks = p.k_stride == 0 ? krow : p.k_stride;
+    if (qs < qrow || ks < krow) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "QkNorm: a token stride is smaller than heads * head_dim");
+    }
+    if (p.tokens == 0) return ROOST_STATUS_OK;
+    const uint32_t dt = p.q.dtype;
+    if (!ActType(dt)) return Fail(ROOST_STATUS_UNSUPPORTED, "QkNorm: dtype must be bf16 or f32");
+    if (p.head_dim > kMaxHeadDim) return Fail(ROOST_STATUS_UNSUPPORTED, "QkNorm: head_dim above 1024 is not built");
+    const uint64_t q_len = (p.tokens - 1ull) * qs + qrow, k_len = (p.tokens - 1ull) * ks + krow;
+    if (!SpanOk(p.q, dt, q_len) || !SpanOk(p.k, dt, k_len) || !SpanOk(p.q_weight, dt, p.head_dim) ||
+        !SpanOk(p.k_weight, dt, p.head_dim)) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT,
+                  "QkNorm: a span has the wrong dtype, is too short, has a NULL address or reserved0 set");
+    }
+    const uint32_t eb = static_cast<uint32_t>(ElemBytes(dt));
+    const void* all[] = {p.q.address, p.k.address, p.q_weight.address, p.k_weight.address};
+    for (const void* a : all) {
+      if (!Aligned(a, eb)) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "QkNorm: a span is not aligned to its element size");
+    }
+    const uint64_t rows = uint64_t{p.tokens} * (p.q_heads + p.kv_heads);
+    if (rows > (uint64_t{1} << 40)) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "QkNorm: too many rows for one call");
+    const bool a16 = RowsAligned16(p.q.address, qs, p.head_dim, eb) && RowsAligned16(p.k.address, ks, p.head_dim, eb) &&
+                     Aligned(p.q_weight.address, 16) && Aligned(p.k_weight.address, 16);
+    const RowShape s = ShapeFor(p.head_dim, eb, a16);
+    DispatchShape(dt, s, [&](auto t_tag, auto kv, auto kj) {
+      using T = decltype(t_tag);
+      hipLaunchKernelGGL((QkNormKernel<T, decltype(kv)::value, decltype(kj)::value>), dim3(GridFor(rows, s.g)),
+                         dim3(256), 0, Stream(stream), static_cast<T*>(p.q.address), static_cast<T*>(p.k.address),
+                         static_cast<const T*>(p.q_weight.address), static_cast<const T*>(p.k_weight.address),
+                         p.tokens, p.q_heads, p.kv_heads, p.head_dim, qs, ks, p.eps, s.g);
+    });
+    return FromHip(hipGetLastError(), "QkNorm launch");
+  });
+}
+
+extern "C" ROOST_API RoostStatus roost_rope_run(RoostContext* ctx, const void* params, const RoostWorkspace*,
+                                                void* stream) {
+  using namespace roost;
+  constexpr char kOp[] = "Rope";
+  if (ctx == nullptr || params == nullptr) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "Rope: ctx or params is NULL");
+  ROOST_TRY(CheckHeader(params, sizeof(RoostRopeParams), kOp));
+  const auto& p = *static_cast<const RoostRopeParams*>(params);
+  return Guarded(kOp, [&]() -> RoostStatus {
+    if (p.head_dim == 0 || p.q_heads == 0 || p.kv_heads == 0) {
+      if (p.kind != ROOST_ROPE_DEFAULT && p.kind != ROOST_ROPE_LLAMA3) {
+        return Fail(ROOST_STATUS_INVALID_ARGUMENT, "Rope: kind must be DEFAULT or LLAMA3");
+      }
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "Rope: head_dim, q_heads and kv_heads must be non-zero");
+    }
+    const uint32_t rot = p.rotary_dim == 0 ? p.head_dim : p.rotary_dim;
+    ROOST_TRY(CheckRopeSpec(kOp, p.head_dim, rot, p.kind, p.theta, p.llama3_factor, p.llama3_low_freq_factor,
+                            p.llama3_high_freq_factor, p.llama3_original_max_position));
+    if (p.head_dim > kMaxHeadDim) return Fail(ROOST_STATUS_UNSUPPORTED, "Rope: head_dim above 1024 is not built");
+    if (p.tokens == 0) return ROOST_STATUS_OK;
+    const uint32_t dt = p.q.dtype;
+    if (!ActType(dt)) return Fail(ROOST_STATUS_UNSUPPORTED, "Rope: dtype must be bf16 or f32");
+    const uint64_t q_len = uint64_t{p.tokens} * p.q_heads * p.head_dim;
+    const uint64_t k_len = uint64_t{p.tokens} * p.kv_heads * p.head_dim;
+    if (!SpanOk(p.q, dt, q_len) || !SpanOk(p.k, dt, k_len) || !SpanOk(p.positions, ROOST_DTYPE_I32, p.tokens)) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT,
+                  "Rope: a span has the wrong dtype, is too short, has a NULL address or reserved0 set");
+    }
+    const uint32_t eb = static_cast<uint32_t>(ElemBytes(dt));
+    if (!Aligned(p.q.address, eb) || !Aligned(p.k.address, eb) || !Aligned(p.positions.address, 4)) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "Rope: a span is not aligned to its element size");
+    }
+    const uint64_t rows = uint64_t{p.tokens} * (p.q_heads + p.kv_heads);
+    if (rows > (uint64_t{1} << 40)) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "Rope: too many rows for one call");
+    RopeSpec rs{static_cast<const int32_t*>(p.positions.address), rot, p.interleaved != 0u,
+                p.kind == ROOST_ROPE_LLAMA3, p.theta, p.llama3_factor, p.llama3_low_freq_factor,
+                p.llama3_high_freq_factor, p.llama3_original_max_position, 0u};
+    const bool a16 = RowsAligned16(p.q.address, uint64_t{p.q_heads} * p.head_dim, p.head_dim, eb) &&
+                     RowsAligned16(p.k.address, uint64_t{p.kv_heads} * p.head_dim, p.head_dim, eb);
+    const RowShape s = ShapeFor(p.head_dim, eb, a16);
+    rs.chunk_pairs = ChunkPairs(s, eb, rot, p.interleaved != 0u);
+    const uint32_t tpb = TokensPerBlock(p.tokens);
+    DispatchShape(dt, s, [&](auto t_tag, auto kv, auto kj) {
+      using T = decltype(t_tag);
+      hipLaunchKernelGGL((RopeKernel<T, decltype(kv)::value, decltype(kj)::value>), dim3(Blocks(p.tokens, tpb)),
+                         dim3(256), RopeLdsBytes(rot / 2, tpb, s.g, p.head_dim), Stream(stream),
+                         static_cast<T*>(p.q.address), static_cast<T*>(p.k.address), rs, p.tokens, p.q_heads,
+                         p.kv_heads, p.head_dim, s.g, tpb);
+    });
+    return FromHip(hipGetLastError(), "Rope launch");
+  });
+}
+
+extern "C" ROOST_API RoostStatus roost_qkv_qk_norm_rope_cache_write_run(RoostContext* ctx, const void* params,
+                                                                        const RoostWorkspace*, void* stream) {
+  using namespace roost;
+  constexpr char kOp[] = "QkvQkNormRopeCacheWrite";
+  if (ctx == nullptr || params == nullptr) {
+    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "QkvQkNormRopeCacheWrite: ctx or params is NULL");
+  }
+  ROOST_TRY(CheckHeader(params, sizeof(RoostQkvQkNormRopeCacheWriteParams), kOp));
+  const auto& p = *static_cast<const RoostQkvQkNormRopeCacheWriteParams*>(params);
+  return Guarded(kOp, [&]() -> RoostStatus {
+    if (p.reserved0 != 0) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "QkvQkNormRopeCacheWrite: reserved0 must be zero");
+    if (p.head_dim == 0 || p.q_heads == 0 || p.kv_heads == 0 || p.page_size == 0) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT,
+                  "QkvQkNormRopeCacheWrite: head_dim, q_heads, kv_heads and page_size must be non-zero");
+    }
+    ROOST_TRY(CheckRopeSpec(kOp, p.head_dim, p.head_dim, ROOST_ROPE_DEFAULT, p.theta, 0.0f, 0.0f, 0.0f, 0));
+    if (p.tokens == 0) return ROOST_STATUS_OK;
+    const uint32_t dt = p.qkv.dtype, ct = p.k_cache.dtype;
+    if (!ActType(dt)) return Fail(ROOST_STATUS_UNSUPPORTED, "QkvQkNormRopeCacheWrite: activation dtype must be bf16 or f32");
+    if (!(ct == dt || (dt == ROOST_DTYPE_BF16 && ct == ROOST_DTYPE_F32))) {
+      return Fail(ROOST_STATUS_UNSUPPORTED,
+                  "QkvQkNormRopeCacheWrite: the cache dtype must equal the activation dtype, or be f32 under bf16");
+    }
+    if (p.head_dim > kMaxHeadDim) {
+      return Fail(ROOST_STATUS_UNSUPPORTED, "QkvQkNormRopeCacheWrite: head_dim above 1024 is not built");
+    }
+    const uint64_t qw = uint64_t{p.q_heads} * p.head_dim, kw = uint64_t{p.kv_heads} * p.head_dim;
+    const uint64_t row = qw + 2 * kw, tokens = p.tokens;
+    if (!SpanOk(p.qkv, dt, tokens * row) || !SpanOk(p.q, dt, tokens * qw) || !SpanOk(p.q_weight, dt, p.head_dim) ||
+        !SpanOk(p.k_weight, dt, p.head_dim) || !SpanOk(p.positions, ROOST_DTYPE_I32, tokens) ||
+        !SpanOk(p.slot_mapping, ROOST_DTYPE_I64, tokens) || !SpanOk(p.k_cache, ct, kw) || !SpanOk(p.v_cache, ct, kw)) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT,
+                  "QkvQkNormRopeCacheWrite: a span has the wrong dtype, is too short, has a NULL address or reserved0 set");
+    }
+    const uint32_t eb = static_cast<uint32_t>(ElemBytes(dt)), cb = static_cast<uint32_t>(ElemBytes(ct));
+    if (!Aligned(p.qkv.address, eb) || !Aligned(p.q.address, eb) || !Aligned(p.q_weight.address, eb) ||
+        !Aligned(p.k_weight.address, eb) || !Aligned(p.positions.address, 4) || !Aligned(p.slot_mapping.address, 8) ||
+        !Aligned(p.k_cache.address, cb) || !Aligned(p.v_cache.address, cb)) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "QkvQkNormRopeCacheWrite: a span is not aligned to its element size");
+    }
+    const uint64_t kc_len = p.k_cache.length, vc_len = p.v_cache.length;
+    if (Overlap(p.q, tokens * qw, p.qkv, tokens * row) || Overlap(p.q, tokens * qw, p.k_cache, kc_len) ||
+        Overlap(p.q, tokens * qw, p.v_cache, vc_len) || Overlap(p.qkv, tokens * row, p.k_cache, kc_len) ||
+        Overlap(p.qkv, tokens * row, p.v_cache, vc_len) || Overlap(p.k_cache, kc_len, p.v_cache, vc_len)) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "QkvQkNormRopeCacheWrite: q, qkv and the two pools must not overlap");
+    }
+    const uint64_t rows = tokens * (p.q_heads + 2ull * p.kv_heads);
+    if (rows > (uint64_t{1} << 40)) {
+      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "QkvQkNormRopeCacheWrite: too many rows for one call");
+    }
+    QkvArgs a{p.qkv.address, p.q.address, p.q_weight.address, p.k_weight.address, p.k_cache.address,
+              p.v_cache.address, static_cast<const int64_t*>(p.slot_mapping.address), std::min(kc_len, vc_len) / kw,
+              p.tokens, p.q_heads, p.kv_heads, p.head_dim, p.eps};
+    RopeSpec rs{static_cast<const int32_t*>(p.positions.address), p.head_dim, 0u, 0u, p.theta, 0.0f, 0.0f, 0.0f, 0u, 0u};
+    // 16-byte rows need every row start aligned: qkv rows, q rows, cache rows and the weights.
+    const bool a16 = RowsAligned16(p.qkv.address, row, p.head_dim, eb) && RowsAligned16(p.q.address, qw, p.head_dim, eb) &&
+                     RowsAligned16(p.k_cache.address, kw, p.head_dim, cb) &&
+                     RowsAligned16(p.v_cache.address, kw, p.head_dim, cb) && Aligned(p.q_weight.address, 16) &&
+                     Aligned(p.k_weight.address, 16);
+    const RowShape s = ShapeFor(p.head_dim, eb, a16);
+    rs.chunk_pairs = ChunkPairs(s, eb, p.head_dim, false);
+    const bool widen = ct != dt;
+    const uint32_t tpb = TokensPerBlock(p.tokens);
+    const dim3 grid(Blocks(p.tokens, tpb));
+    const uint64_t lds = RopeLdsBytes(p.head_dim / 2, tpb, s.g, p.head_dim);
+    DispatchShape(dt, s, [&](auto t_tag, auto kv, auto kj) {
+      using T = decltype(t_tag);
+      constexpr int kV = decltype(kv)::value, kJ = decltype(kj)::value;
+      if (widen) {
+        if constexpr (sizeof(T) == 2) {
+          hipLaunchKernelGGL((QkvKernel<T, float, kV, kJ>), grid, dim3(256), lds, Stream(stream), a, rs, s.g, tpb);
+        }
+      } else {
+        hipLaunchKernelGGL((QkvKernel<T, T, kV, kJ>), grid, dim3(256), lds, Stream(stream), a, rs, s.g, tpb);
+      }
+    });
+    return FromHip(hipGetLastError(), "QkvQkNormRopeCacheWrite launch");
+  });
+}

@@ -43,6 +43,16 @@ static_assert(sizeof(RoostSigmoidMulParams) == 88 && offsetof(RoostSigmoidMulPar
 static_assert(sizeof(RoostCausalConv1dParams) == 200 && offsetof(RoostCausalConv1dParams, batch) == 176 &&
                   offsetof(RoostCausalConv1dParams, silu) == 192,
               "RoostCausalConv1dParams layout");
+static_assert(sizeof(RoostQkNormParams) == 136 && offsetof(RoostQkNormParams, tokens) == 104 &&
+                  offsetof(RoostQkNormParams, eps) == 128, "RoostQkNormParams layout");
+static_assert(sizeof(RoostRopeParams) == 128 && offsetof(RoostRopeParams, tokens) == 80 &&
+                  offsetof(RoostRopeParams, theta) == 108 && offsetof(RoostRopeParams, llama3_original_max_position) == 124,
+              "RoostRopeParams layout");
+static_assert(sizeof(RoostQkvQkNormRopeCacheWriteParams) == 232 &&
+                  offsetof(RoostQkvQkNormRopeCacheWriteParams, slot_mapping) == 176 &&
+                  offsetof(RoostQkvQkNormRopeCacheWriteParams, tokens) == 200 &&
+                  offsetof(RoostQkvQkNormRopeCacheWriteParams, theta) == 224,
+              "RoostQkvQkNormRopeCacheWriteParams layout");
 static_assert(sizeof(RoostRecurrentStateCopyParams) == 72 && offsetof(RoostRecurrentStateCopyParams, slot_bytes) == 56,
               "RoostRecurrentStateCopyParams layout");
 static_assert(sizeof(RoostRecurrentStateSnapshotParams) == 96 &&
@@ -108,6 +118,22 @@ RoostConstraints PlainConstraints(uint64_t act_mask, uint32_t alignment) {
   return c;
 }
 
+// QkNorm and Rope: bf16 or f32 heads of any even width up to 1024, element alignment (16-byte rows take vector loads).
+RoostConstraints HeadConstraints() {
+  RoostConstraints c = PlainConstraints(DtypeBit(ROOST_DTYPE_BF16) | DtypeBit(ROOST_DTYPE_F32), 2);
+  c.head_dim_mask = ~uint64_t{0};
+  return c;
+}
+
+// The fused QKV op writes NHD pages of the activation type, or f32 pages under bf16 activations.
+RoostConstraints QkvConstraints() {
+  RoostConstraints c = HeadConstraints();
+  c.kv_dtype_mask = DtypeBit(ROOST_DTYPE_BF16) | DtypeBit(ROOST_DTYPE_F32);
+  c.layout_mask = 1u << ROOST_LAYOUT_PAGED_NHD;
+  c.page_size_mask = kAnyPageSize;
+  return c;
+}
+
 RoostOpEntry Entry(uint32_t op, uint32_t flags, const char* id, uint32_t params_size, const RoostConstraints& c,
                    RoostRunFn run, RoostPlanFn plan, RoostWorkspaceFn workspace) {
   RoostOpEntry e{};
@@ -154,6 +180,13 @@ const RoostOpEntry* Entries(uint32_t* count) {
             sizeof(RoostGatedRmsNormParams), PlainConstraints(kBf16F32, 4), roost_gated_rms_norm_run, nullptr, nullptr),
       Entry(ROOST_OP_SIGMOID_MUL, kDet | ROOST_FLAG_GRAPH_CAPTURABLE, "sigmoid-mul-gfx950", sizeof(RoostSigmoidMulParams),
             PlainConstraints(kBf16F32, 4), roost_sigmoid_mul_run, nullptr, nullptr),
+      Entry(ROOST_OP_QK_NORM, kDet | ROOST_FLAG_GRAPH_CAPTURABLE, "qk-norm-gfx950", sizeof(RoostQkNormParams),
+            HeadConstraints(), roost_qk_norm_run, nullptr, nullptr),
+      Entry(ROOST_OP_ROPE, kDet | ROOST_FLAG_GRAPH_CAPTURABLE, "rope-gfx950", sizeof(RoostRopeParams), HeadConstraints(),
+            roost_rope_run, nullptr, nullptr),
+      Entry(ROOST_OP_QKV_QK_NORM_ROPE_CACHE_WRITE, kDet | ROOST_FLAG_GRAPH_CAPTURABLE,
+            "qkv-qk-norm-rope-cache-write-gfx950", sizeof(RoostQkvQkNormRopeCacheWriteParams), QkvConstraints(),
+            roost_qkv_qk_norm_rope_cache_write_run, nullptr, nullptr),
   };
   *count = static_cast<uint32_t>(sizeof(entries) / sizeof(entries[0]));
   return entries;

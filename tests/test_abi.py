@@ -39,6 +39,16 @@ def test_layouts_match_reference_fixture():
         assert fields == g["fields"], name
 
 
+def test_extension_layouts_match_the_header():
+    """RoostQkvQkNormRopeCacheWriteParams has no reference layout: its ctypes mirror must match the C header's
+    offsets, which registry.cpp pins with static_asserts (232 bytes, slot_mapping at 176, tokens at 200, theta at 224)."""
+    st = abi.EXTENSION_STRUCTS["RoostQkvQkNormRopeCacheWriteParams"]
+    assert C.sizeof(st) == 232
+    assert (st.slot_mapping.offset, st.tokens.offset, st.theta.offset) == (176, 200, 224)
+    spans = [f[0] for f in st._fields_ if f[1] is abi.DeviceSpan]
+    assert spans == ["qkv", "q", "q_weight", "k_weight", "positions", "k_cache", "v_cache", "slot_mapping"]
+
+
 def declared_symbols():
     syms = set()
     for h in (ROOT / "include").glob("*.h"):
@@ -55,7 +65,8 @@ def test_library_exports_every_declared_symbol(kernels):
             "roost_context_destroy", "roost_paged_attention_run", "roost_cache_write_run", "roost_gdn_chunk_run",
             "roost_gdn_recurrent_run", "roost_gated_delta_rule_gates_run", "roost_gated_rms_norm_run",
             "roost_sigmoid_mul_run", "roost_causal_conv1d_run", "roost_recurrent_state_copy_run",
-            "roost_recurrent_state_snapshot_run"} <= declared
+            "roost_recurrent_state_snapshot_run", "roost_qk_norm_run", "roost_rope_run",
+            "roost_qkv_qk_norm_rope_cache_write_run"} <= declared
     assert declared <= exported, declared - exported
 
 
@@ -70,14 +81,17 @@ def test_abi_version_and_table(kernels):
     assert set(ids) == {roost_amd.ATTENTION_VARIANT, roost_amd.CACHE_WRITE_VARIANT, roost_amd.CHUNK_VARIANT,
                         roost_amd.RECURRENT_VARIANT, roost_amd.GATES_VARIANT, roost_amd.GATED_RMS_NORM_VARIANT,
                         roost_amd.SIGMOID_MUL_VARIANT, roost_amd.CAUSAL_CONV1D_VARIANT, roost_amd.STATE_COPY_VARIANT,
-                        roost_amd.STATE_SNAPSHOT_VARIANT}
-    # The GDN layer's neighbour ops: graph capturable, deterministic, batch invariant, no plan, no workspace.
+                        roost_amd.STATE_SNAPSHOT_VARIANT, roost_amd.QK_NORM_VARIANT, roost_amd.ROPE_VARIANT,
+                        roost_amd.QKV_VARIANT}
+    # The GDN layer's neighbour ops and the attention input ops: graph capturable, deterministic, batch invariant, no plan, no workspace.
     for vid, op, size in [(roost_amd.GATES_VARIANT, abi.OP_GATED_DELTA_RULE_GATES, 168),
                           (roost_amd.GATED_RMS_NORM_VARIANT, abi.OP_GATED_RMS_NORM, 120),
                           (roost_amd.SIGMOID_MUL_VARIANT, abi.OP_SIGMOID_MUL, 88),
                           (roost_amd.CAUSAL_CONV1D_VARIANT, abi.OP_CAUSAL_CONV1D, 200),
                           (roost_amd.STATE_COPY_VARIANT, abi.OP_RECURRENT_STATE_COPY, 72),
-                          (roost_amd.STATE_SNAPSHOT_VARIANT, abi.OP_RECURRENT_STATE_SNAPSHOT, 96)]:
+                          (roost_amd.STATE_SNAPSHOT_VARIANT, abi.OP_RECURRENT_STATE_SNAPSHOT, 96),
+                          (roost_amd.QK_NORM_VARIANT, abi.OP_QK_NORM, 136), (roost_amd.ROPE_VARIANT, abi.OP_ROPE, 128),
+                          (roost_amd.QKV_VARIANT, abi.OP_QKV_QK_NORM_ROPE_CACHE_WRITE, 232)]:
         e = ids[vid]
         assert e.op == op and e.params_struct_size == size and e.plan is None and e.workspace is None
         assert e.flags == abi.FLAG_GRAPH_CAPTURABLE | abi.FLAG_DETERMINISTIC | abi.FLAG_BATCH_INVARIANT

@@ -12,6 +12,12 @@ Which check pins which oracle function:
                       S' = (I - b k k^T) e^g S + b k v^T with grouped heads and slots (HybridTests.cs:32-172), two calls
                       = one call and token-by-token decode (HybridTests.cs:174-220), scale 0 = 1/sqrt(k_dim), and
                       strided views = contiguous copies (GatedDeltaRuleViewTests.cs).
+  qk_norm          -- the hand case BasicOpsTests.cs:35-46 (two query heads, one key head, each with its own weight),
+                      per-token strides = contiguous copies, and the mean square of a unit-weight row being 1.
+  rope             -- the hand cases BasicOpsTests.cs:65-116 (NeoX halves, interleaved pairs, partial rotary width,
+                      position 0, Llama 3 low-frequency scaling at 1e-11), transformers 5.20.1's Llama 3 cos/sin rows
+                      (the reference fixture, RopeScalingTests.cs:105-127), and the rotation laws: pair norms kept,
+                      rope(p1) then rope(p2) = rope(p1 + p2).
   plan_region      -- the closed form slot = block[pos / bs] * bs + pos % bs and the indptr prefix sums
                       (PlanRegionWriter.cs:19-64) on hand-written plans.
 """
@@ -545,3 +551,131 @@ def test_state_copy_and_snapshot_are_ordered_byte_copies():
     assert list(pool2.view(np.uint32)) == [0, 0, 0, 0, np.float32(1.5).view(np.uint32), 0x80000000]
     with pytest.raises(oracle.OracleError):
         oracle.state_copy(pool, np.array([3, 0], np.int32), slot_bytes=8)
+
+
+# ---- QkNorm, Rope and the fused QkvQkNormRopeCacheWrite (CpuOps.cs:63-175, CpuOps.Fused.cs:37-95) ----
+
+ROPE_GOLDEN = json.loads((Path(__file__).resolve().parent / "golden" / "rope_llama3_cases.json").read_text())
+
+
+def test_qk_norm_hand_case_and_strides():
+    """BasicOpsTests.cs:35-46: one token, q heads [3, 4] and [6, 8] with weight 1, k head [0, 5] with weight [2, 3]."""
+    q, k = np.array([3.0, 4, 6, 8]), np.array([0.0, 5])
+    oracle.qk_norm(q, k, np.ones(2), np.array([2.0, 3]), tokens=1, q_heads=2, kv_heads=1, head_dim=2, eps=0.0)
+    r, r2 = 1 / math.sqrt(12.5), 1 / math.sqrt(50)
+    np.testing.assert_allclose(q, [3 * r, 4 * r, 6 * r2, 8 * r2], rtol=1e-15)
+    np.testing.assert_allclose(k, [0.0, 5 / math.sqrt(12.5) * 3], rtol=1e-15)
+    # Rows at a token stride (q heads inside a wider row) give what the contiguous rows give; padding is untouched.
+    rng = np.random.default_rng(3)
+    t, hq, hk, hd = 3, 2, 1, 8
+    qs, ks = rng.standard_normal(t * 24), rng.standard_normal(t * 12)
+    qc = qs.reshape(t, 24)[:, :hq * hd].copy().reshape(-1)
+    kc = ks.reshape(t, 12)[:, :hk * hd].copy().reshape(-1)
+    qw, kw = rng.standard_normal(hd), rng.standard_normal(hd)
+    pad_q, pad_k = qs.reshape(t, 24)[:, hq * hd:].copy(), ks.reshape(t, 12)[:, hk * hd:].copy()
+    oracle.qk_norm(qs, ks, qw, kw, tokens=t, q_heads=hq, kv_heads=hk, head_dim=hd, eps=1e-6, q_stride=24, k_stride=12)
+    oracle.qk_norm(qc, kc, qw, kw, tokens=t, q_heads=hq, kv_heads=hk, head_dim=hd, eps=1e-6)
+    assert np.array_equal(qs.reshape(t, 24)[:, :hq * hd].reshape(-1), qc)
+    assert np.array_equal(ks.reshape(t, 12)[:, :hk * hd].reshape(-1), kc)
+    assert np.array_equal(qs.reshape(t, 24)[:, hq * hd:], pad_q) and np.array_equal(ks.reshape(t, 12)[:, hk * hd:], pad_k)
+    # With unit weights and eps 0 every normalised head has mean square 1.
+    x = rng.standard_normal(5 * 16)
+    oracle.qk_norm(x, np.zeros(16), np.ones(16), np.ones(16), tokens=5, q_heads=1, kv_heads=1, head_dim=16, eps=0.0)
+    np.testing.assert_allclose((x.reshape(5, 16) ** 2).mean(axis=1), 1.0, rtol=1e-14)
+
+
+def _rope1(x, pos, hd, rot=0, interleaved=False, theta=100.0, llama3=None):
+    q, k = np.array(x, np.float64), np.array(x, np.float64)
+    oracle.rope(q, k, np.array([pos], np.int32), tokens=1, q_heads=1, kv_heads=1, head_dim=hd, rotary_dim=rot,
+                interleaved=interleaved, theta=theta, llama3=llama3)
+    assert np.array_equal(q, k)
+    return q
+
+
+def test_rope_hand_cases():
+    """BasicOpsTests.cs:65-116."""
+    a0, a1 = 2.0, 0.2  # head dim 4, theta 100: frequencies 1 and 0.1; position 2
+    np.testing.assert_allclose(_rope1([1, 2, 3, 4], 2, 4),
+                               [math.cos(a0) - 3 * math.sin(a0), 2 * math.cos(a1) - 4 * math.sin(a1),
+                                3 * math.cos(a0) + math.sin(a0), 4 * math.cos(a1) + 2 * math.sin(a1)], rtol=1e-14)
+    np.testing.assert_allclose(_rope1([1, 2, 3, 4], 2, 4, interleaved=True),
+                               [math.cos(a0) - 2 * math.sin(a0), 2 * math.cos(a0) + math.sin(a0),
+                                3 * math.cos(a1) - 4 * math.sin(a1), 4 * math.cos(a1) + 3 * math.sin(a1)], rtol=1e-14)
+    y = _rope1([1, 2, 3, 4], 1, 4, rot=2)
+    assert y[2] == 3.0 and y[3] == 4.0 and abs(y[0] - (math.cos(1.0) - 2 * math.sin(1.0))) < 1e-14
+    assert list(_rope1([1, 2, 3, 4], 0, 4)) == [1.0, 2.0, 3.0, 4.0]
+    # Llama 3: head dim 8, theta 1e6, original 8192, low 1, high 4, factor 8.
+    y = _rope1([1, 1, 1, 1, 0, 0, 0, 0], 1000, 8, theta=1e6, llama3=(8.0, 1.0, 4.0, 8192))
+    f = [float(np.float32(1e6)) ** (-2.0 * i / 8) for i in range(4)]
+    smooth = (8192.0 / (2 * math.pi / f[2]) - 1) / (4 - 1)
+    scaled = [f[0], f[1], (1 - smooth) * f[2] / 8 + smooth * f[2], f[3] / 8]
+    for i in range(4):
+        assert abs(math.cos(1000 * scaled[i]) - y[i]) < 1e-11 and abs(math.sin(1000 * scaled[i]) - y[i + 4]) < 1e-11
+    with pytest.raises(oracle.OracleError):
+        _rope1([1, 2, 3, 4], 1, 4, rot=3)
+
+
+@pytest.mark.parametrize("case", ROPE_GOLDEN["cases"], ids=lambda c: c["name"])
+def test_rope_llama3_matches_transformers(case):
+    """RopeScalingTests.cs:105-127: a head of ones then zeros comes out as [cos, sin] of its position's angles, against
+    transformers' own rows."""
+    hd, pos, p = case["head_dim"], np.array(case["positions"], np.int32), case["params"]
+    q = np.array([1.0 if i % hd < hd // 2 else 0.0 for i in range(len(pos) * hd)])
+    k = np.zeros(len(pos) * hd)
+    oracle.rope(q, k, pos, tokens=len(pos), q_heads=1, kv_heads=1, head_dim=hd, theta=case["theta"],
+                llama3=(p["factor"], p["low_freq_factor"], p["high_freq_factor"], p["original_max_position_embeddings"]))
+    np.testing.assert_allclose(q, case["cos_sin_rows"], rtol=0, atol=1e-9)
+
+
+def test_rope_rotation_laws():
+    """Each pair keeps its norm, and rotating by p1 then by p2 equals rotating by p1 + p2 (NeoX and interleaved,
+    partial width)."""
+    rng = np.random.default_rng(11)
+    hd, rot = 16, 12
+    for inter in (False, True):
+        x = rng.standard_normal(hd)
+        a = _rope1(x, 37, hd, rot=rot, interleaved=inter, theta=1e4)
+        b = _rope1(_rope1(x, 30, hd, rot=rot, interleaved=inter, theta=1e4), 7, hd, rot=rot, interleaved=inter,
+                   theta=1e4)
+        np.testing.assert_allclose(a, b, rtol=0, atol=1e-13)
+        pairs = [(2 * i, 2 * i + 1) for i in range(rot // 2)] if inter else [(i, i + rot // 2) for i in range(rot // 2)]
+        for i, j in pairs:
+            assert abs(math.hypot(a[i], a[j]) - math.hypot(x[i], x[j])) < 1e-13
+        assert np.array_equal(a[rot:], x[rot:])
+
+
+def test_fused_qkv_is_its_parts_and_leaves_qkv_alone():
+    """FusedOpsTests.cs:48-97 on the oracle: the fused call equals QkNorm, Rope and CacheWrite called in order, a -1 slot
+    writes nothing, the qkv rows are left as they were; bf16 rows widen exactly into an f32 pool."""
+    rng = np.random.default_rng(9)
+    tokens, hq, hk, hd, bs, blocks = 5, 4, 2, 8, 4, 4
+    qw, kw = hq * hd, hk * hd
+    row = qw + 2 * kw
+    qkv = cases.bf16_bits(rng.uniform(-1, 1, tokens * row).astype(np.float32))
+    qn, kn = (cases.bf16_bits(rng.uniform(0.9, 1.1, hd).astype(np.float32)) for _ in range(2))
+    pos = np.array([7, 8, 9, 0, 1], np.int32)
+    slots = np.array([3, 12, -1, 5, 6], np.int64)
+    before = qkv.copy()
+    q_out = np.zeros(tokens * qw, np.uint16)
+    kc, vc = np.zeros(blocks * bs * kw, np.uint16), np.zeros(blocks * bs * kw, np.uint16)
+    oracle.qkv_qk_norm_rope_cache_write(qkv, q_out, qn, kn, pos, kc, vc, slots, tokens=tokens, q_heads=hq,
+                                        kv_heads=hk, head_dim=hd, page_size=bs, eps=1e-6, theta=1e6)
+    assert np.array_equal(qkv, before)
+    rows = qkv.reshape(tokens, row)
+    q = rows[:, :qw].copy().reshape(-1)
+    k = rows[:, qw:qw + kw].copy().reshape(-1)
+    v = rows[:, qw + kw:].copy().reshape(-1)
+    oracle.qk_norm(q, k, qn, kn, tokens=tokens, q_heads=hq, kv_heads=hk, head_dim=hd, eps=1e-6)
+    oracle.rope(q, k, pos, tokens=tokens, q_heads=hq, kv_heads=hk, head_dim=hd, theta=1e6)
+    assert np.array_equal(q_out, q)
+    kr, vr = kc.reshape(-1, kw), vc.reshape(-1, kw)
+    for t, s in enumerate(slots):
+        if s >= 0:
+            assert np.array_equal(kr[s], k.reshape(tokens, kw)[t]) and np.array_equal(vr[s], v.reshape(tokens, kw)[t])
+    written = {int(s) for s in slots if s >= 0}
+    assert all(not kr[r].any() and not vr[r].any() for r in range(blocks * bs) if r not in written)
+    kc32, vc32 = np.zeros(blocks * bs * kw, np.float32), np.zeros(blocks * bs * kw, np.float32)
+    oracle.qkv_qk_norm_rope_cache_write(qkv, q_out, qn, kn, pos, kc32, vc32, slots, tokens=tokens, q_heads=hq,
+                                        kv_heads=hk, head_dim=hd, page_size=bs, eps=1e-6, theta=1e6)
+    assert np.array_equal(kc32.view(np.uint32) >> 16, kc.astype(np.uint32))
+    assert np.array_equal(vc32.view(np.uint32) >> 16, vc.astype(np.uint32))
