@@ -167,6 +167,9 @@ def causal_conv1d(x, weight, bias, out, state, state_slots, cu_seqlens, *, batch
 def qk_norm(q, k, q_weight, k_weight, *, tokens, q_heads, kv_heads, head_dim, eps, q_stride=0, k_stride=0) -> None:
     """CpuOps.QkNorm, in place (q_stride / k_stride: elements between tokens, 0 = contiguous)."""
     assert q.dtype == k.dtype == q_weight.dtype == k_weight.dtype
+    qs, ks = q_stride or q_heads * head_dim, k_stride or kv_heads * head_dim
+    assert q.size >= (tokens - 1) * qs + q_heads * head_dim and k.size >= (tokens - 1) * ks + kv_heads * head_dim
+    assert q_weight.size >= head_dim and k_weight.size >= head_dim
     _check(lib().oracle_qk_norm(_ptr(q), _ptr(k), _ptr(q_weight), _ptr(k_weight), _dt(q), tokens, q_heads, kv_heads,
                                 head_dim, q_stride, k_stride, ctypes.c_float(eps)))
 
@@ -175,6 +178,7 @@ def rope(q, k, positions, *, tokens, q_heads, kv_heads, head_dim, theta, rotary_
          llama3=None) -> None:
     """CpuOps.Rope, in place. llama3: (factor, low_freq_factor, high_freq_factor, original_max_position) or None."""
     assert q.dtype == k.dtype and positions.dtype == np.int32
+    assert q.size >= tokens * q_heads * head_dim and k.size >= tokens * kv_heads * head_dim and positions.size >= tokens
     kind, (fac, low, high, orig) = (1, llama3) if llama3 is not None else (0, (0.0, 0.0, 0.0, 0))
     _check(lib().oracle_rope(_ptr(q), _ptr(k), _ptr(positions), _dt(q), tokens, q_heads, kv_heads, head_dim,
                              rotary_dim, kind, int(interleaved), ctypes.c_float(theta), ctypes.c_float(fac),

@@ -580,7 +580,8 @@ def test_qk_norm_hand_case_and_strides():
     assert np.array_equal(qs.reshape(t, 24)[:, hq * hd:], pad_q) and np.array_equal(ks.reshape(t, 12)[:, hk * hd:], pad_k)
     # With unit weights and eps 0 every normalised head has mean square 1.
     x = rng.standard_normal(5 * 16)
-    oracle.qk_norm(x, np.zeros(16), np.ones(16), np.ones(16), tokens=5, q_heads=1, kv_heads=1, head_dim=16, eps=0.0)
+    oracle.qk_norm(x, np.zeros(5 * 16), np.ones(16), np.ones(16), tokens=5, q_heads=1, kv_heads=1, head_dim=16,
+                   eps=0.0)
     np.testing.assert_allclose((x.reshape(5, 16) ** 2).mean(axis=1), 1.0, rtol=1e-14)
 
 
