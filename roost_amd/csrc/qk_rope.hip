@@ -147,26 +147,41 @@ struct RowRegs {
   float v[kJ][kV];
 };
 
+// v of lane (lane ^ M): ds_swizzle's bit-mask mode within each 32 lanes for M < 32 (one instruction, no address), a
+// full-wave permute for M = 32.
+template <int M>
+__device__ __forceinline__ float XorLanes(float v) {
+  if constexpr (M < 32) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (M << 10) | 0x1F));
+  } else {
+    return __shfl_xor(v, M, 64);
+  }
+}
+
 // RmsNorm of the row in place: v * rsqrt(mean(v^2) + eps) * w, then rounded to T (CpuOps.cs:89-103). Lanes whose
-// chunks lie beyond head_dim hold zeros and contribute nothing.
+// chunks lie beyond head_dim hold zeros and contribute nothing; w holds the lane's chunks of the weight. The sum of
+// squares is reduced over the g lanes of the row by an xor butterfly with constant masks (DPP / swizzle moves).
 template <typename T, int kV, int kJ>
-__device__ __forceinline__ void NormRow(RowRegs<kV, kJ>& r, const T* w, uint32_t sub, uint32_t g, uint32_t chunks,
-                                        uint32_t head_dim, float eps) {
+__device__ __forceinline__ void NormRow(RowRegs<kV, kJ>& r, const RowRegs<kV, kJ>& w, uint32_t sub, uint32_t g,
+                                        uint32_t chunks, float inv_dim, float eps) {
   float ss = 0.0f;
 #pragma unroll
   for (int j = 0; j < kJ; ++j)
 #pragma unroll
     for (int e = 0; e < kV; ++e) ss = fmaf(r.v[j][e], r.v[j][e], ss);
-  for (uint32_t m = 1; m < g; m <<= 1) ss += __shfl_xor(ss, static_cast<int>(m), 64);
-  const float inv = rsqrtf(ss / static_cast<float>(head_dim) + eps);
+  if (g > 1) ss += XorLanes<1>(ss);
+  if (g > 2) ss += XorLanes<2>(ss);
+  if (g > 4) ss += XorLanes<4>(ss);
+  if (g > 8) ss += XorLanes<8>(ss);
+  if (g > 16) ss += XorLanes<16>(ss);
+  if (g > 32) ss += XorLanes<32>(ss);
+  const float inv = rsqrtf(ss * inv_dim + eps);
 #pragma unroll
   for (int j = 0; j < kJ; ++j) {
     const uint32_t c = sub + g * j;
     if (c < chunks) {
-      float wv[kV];
-      LoadChunk<T, kV>(w + c * kV, wv);
 #pragma unroll
-      for (int e = 0; e < kV; ++e) r.v[j][e] = r.v[j][e] * inv * wv[e];
+      for (int e = 0; e < kV; ++e) r.v[j][e] = r.v[j][e] * inv * w.v[j][e];
       if constexpr (kV % 2 == 0) {
 #pragma unroll
         for (int e = 0; e < kV; e += 2) RoundPairT<T>(&r.v[j][e]);
@@ -313,6 +328,50 @@ __device__ __forceinline__ void LoadRow(RowRegs<kV, kJ>& r, const T* src, uint32
     }
   }
 }
+// A lane's chunks of one row as fetched: the 16-byte words of vector rows (unpacked only when the row is used, so a
+// fetched row stays in flight while the previous one is computed), or the floats of scalar rows.
+template <typename T, int kV, int kJ>
+struct RowRaw {
+  static constexpr bool kVec = kV * sizeof(T) == 16;
+  uint4 w[kVec ? kJ : 1];
+  RowRegs<kV, kVec ? 1 : kJ> f;
+};
+// Fetches the row at src (when live) or, for lanes without a row or past head_dim, the harmless address `safe`
+// (their values are zeroed on unpacking).
+template <typename T, int kV, int kJ>
+__device__ __forceinline__ void FetchRow(RowRaw<T, kV, kJ>& raw, const T* src, const T* safe, uint32_t sub, uint32_t g,
+                                         uint32_t chunks, bool live) {
+  if constexpr (RowRaw<T, kV, kJ>::kVec) {
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+      const uint32_t c = sub + g * j;
+      const bool ok = live && c < chunks;
+      raw.w[j] = *reinterpret_cast<const uint4*>(ok ? src + c * kV : safe);
+    }
+  } else {
+    LoadRow<T, kV, kJ>(raw.f, src, sub, g, chunks, live);
+  }
+}
+template <typename T, int kV, int kJ>
+__device__ __forceinline__ void UnpackRow(const RowRaw<T, kV, kJ>& raw, RowRegs<kV, kJ>& r, uint32_t sub, uint32_t g,
+                                          uint32_t chunks, bool live) {
+  if constexpr (RowRaw<T, kV, kJ>::kVec) {
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+      const bool ok = live && sub + g * j < chunks;
+      const uint32_t wd[4] = {raw.w[j].x, raw.w[j].y, raw.w[j].z, raw.w[j].w};
+#pragma unroll
+      for (int e = 0; e < kV; ++e) {
+        const float v = sizeof(T) == 2 ? ((e & 1) ? Bf16HiToF32(wd[e >> 1]) : Bf16LoToF32(wd[e >> 1]))
+                                       : __uint_as_float(wd[e]);
+        r.v[j][e] = ok ? v : 0.0f;
+      }
+    }
+  } else {
+    r = raw.f;
+  }
+}
+
 template <typename T, int kV, int kJ>
 __device__ __forceinline__ void StoreRow(const RowRegs<kV, kJ>& r, T* dst, uint32_t sub, uint32_t g, uint32_t chunks) {
 #pragma unroll
@@ -381,9 +440,10 @@ __global__ void __launch_bounds__(256) QkNormKernel(T* q, T* k, const T* qw, con
   T* x = is_q ? q + t * q_stride + static_cast<uint64_t>(h) * head_dim
               : k + t * k_stride + static_cast<uint64_t>(h - q_heads) * head_dim;
   const uint32_t chunks = head_dim / kV;
-  RowRegs<kV, kJ> r;
+  RowRegs<kV, kJ> r, w;
   LoadRow<T, kV, kJ>(r, x, l.sub, g, chunks, live);
-  NormRow<T, kV, kJ>(r, is_q ? qw : kw, l.sub, g, chunks, head_dim, eps);
+  LoadRow<T, kV, kJ>(w, is_q ? qw : kw, l.sub, g, chunks, true);
+  NormRow<T, kV, kJ>(r, w, l.sub, g, chunks, 1.0f / static_cast<float>(head_dim), eps);
   if (live) StoreRow<T, kV, kJ>(r, x, l.sub, g, chunks);
 }
 
@@ -414,18 +474,18 @@ __global__ void __launch_bounds__(256) RopeKernel(T* q, T* k, RopeSpec rs, uint3
   bool live;
   uint32_t lt;
   T* x = row_at(wave, &live, &lt);
-  RowRegs<kV, kJ> cur;
-  LoadRow<T, kV, kJ>(cur, x, sub, g, chunks, live);
+  RowRaw<T, kV, kJ> raw;
+  FetchRow<T, kV, kJ>(raw, x, q, sub, g, chunks, live);
   BuildAngles(rs, tr.t0, tr.count, freq, cs);
   for (uint32_t grp = wave; grp * per < tr.rows; grp += 4) {
+    RowRegs<kV, kJ> cur;
+    UnpackRow<T, kV, kJ>(raw, cur, sub, g, chunks, live);
     bool live_n;
     uint32_t lt_n;
     T* x_n = row_at(grp + 4, &live_n, &lt_n);
-    RowRegs<kV, kJ> nxt;
-    LoadRow<T, kV, kJ>(nxt, x_n, sub, g, chunks, live_n);
+    FetchRow<T, kV, kJ>(raw, x_n, q, sub, g, chunks, live_n);
     RopeRow<T, kV, kJ>(cur, row_lds, cs + lt * half, rs, sub, g, chunks);
     if (live) StoreRow<T, kV, kJ>(cur, x, sub, g, chunks);
-    cur = nxt;
     x = x_n;
     live = live_n;
     lt = lt_n;
@@ -480,6 +540,9 @@ __global__ void __launch_bounds__(256) QkvKernel(QkvArgs a, RopeSpec rs, uint32_
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, per = 64 / g, sub = lane % g;
   const uint32_t chunks = a.head_dim / kV, half = rs.rot / 2;
   const T* qkv = static_cast<const T*>(a.qkv);
+  RowRaw<T, kV, kJ> wq, wk;  // this lane's chunks of the two norm weights, fetched once
+  FetchRow<T, kV, kJ>(wq, static_cast<const T*>(a.qw), static_cast<const T*>(a.qw), sub, g, chunks, true);
+  FetchRow<T, kV, kJ>(wk, static_cast<const T*>(a.kw), static_cast<const T*>(a.kw), sub, g, chunks, true);
   // v rows (no angles needed): tr.count * kv_heads of them.
   const uint32_t v_rows = tr.count * a.kv_heads;
   for (uint32_t grp = wave; grp * per < v_rows; grp += 4) {
@@ -498,6 +561,7 @@ __global__ void __launch_bounds__(256) QkvKernel(QkvArgs a, RopeSpec rs, uint32_
   struct RowAt {
     bool live, is_q;
     uint32_t lt, h;
+    int64_t slot;  // k rows: the token's cache slot, read with the row (one iteration ahead)
   };
   auto row_at = [&](uint32_t grp) {
     RowAt w;
@@ -506,26 +570,31 @@ __global__ void __launch_bounds__(256) QkvKernel(QkvArgs a, RopeSpec rs, uint32_
     w.lt = w.live ? r / qk_heads : 0;
     w.h = w.live ? r - w.lt * qk_heads : 0;
     w.is_q = w.h < a.q_heads;
+    w.slot = a.slots[tr.t0 + w.lt];
     return w;
   };
   auto src_of = [&](const RowAt& w) { return qkv + ((tr.t0 + w.lt) * heads + w.h) * a.head_dim; };
   // Software pipeline: the first group's rows are requested before the angle table is built, and each group's
   // successor before the group is computed.
   RowAt w = row_at(wave);
-  RowRegs<kV, kJ> cur;
-  LoadRow<T, kV, kJ>(cur, src_of(w), sub, g, chunks, w.live);
+  RowRaw<T, kV, kJ> raw;
+  FetchRow<T, kV, kJ>(raw, src_of(w), qkv, sub, g, chunks, w.live);
   BuildAngles(rs, tr.t0, tr.count, freq, cs);
+  const float inv_dim = 1.0f / static_cast<float>(a.head_dim);
   for (uint32_t grp = wave; grp * per < qk_rows; grp += 4) {
+    RowRegs<kV, kJ> cur;
+    UnpackRow<T, kV, kJ>(raw, cur, sub, g, chunks, w.live);
     const RowAt wn = row_at(grp + 4);
-    RowRegs<kV, kJ> nxt;
-    LoadRow<T, kV, kJ>(nxt, src_of(wn), sub, g, chunks, wn.live);
-    NormRow<T, kV, kJ>(cur, static_cast<const T*>(w.is_q ? a.qw : a.kw), sub, g, chunks, a.head_dim, a.eps);
+    FetchRow<T, kV, kJ>(raw, src_of(wn), qkv, sub, g, chunks, wn.live);
+    RowRegs<kV, kJ> wt;
+    UnpackRow<T, kV, kJ>(w.is_q ? wq : wk, wt, sub, g, chunks, true);
+    NormRow<T, kV, kJ>(cur, wt, sub, g, chunks, inv_dim, a.eps);
     RopeRow<T, kV, kJ>(cur, row_lds, cs + w.lt * half, rs, sub, g, chunks);
     const uint64_t t = tr.t0 + w.lt;
     if (w.live && w.is_q) {
       StoreRow<T, kV, kJ>(cur, static_cast<T*>(a.q) + (t * a.q_heads + w.h) * a.head_dim, sub, g, chunks);
     } else if (w.live) {
-      const int64_t slot = a.slots[t];
+      const int64_t slot = w.slot;
       if (slot >= 0 && static_cast<uint64_t>(slot) < a.pool_rows) {
         C* dst = static_cast<C*>(a.k_cache) + (static_cast<uint64_t>(slot) * a.kv_heads + (w.h - a.q_heads)) * a.head_dim;
         if constexpr (sizeof(C) == sizeof(T)) {
@@ -542,7 +611,6 @@ __global__ void __launch_bounds__(256) QkvKernel(QkvArgs a, RopeSpec rs, uint32_
         }
       }
     }
-    cur = nxt;
     w = wn;
   }
 }
