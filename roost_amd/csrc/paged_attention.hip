@@ -106,6 +106,8 @@ struct PlanRecord {
   uint32_t kv_layout;
   uint32_t head_dim;
   uint32_t kv_heads;
+  int32_t window;        // WindowOf(params): the pieces start at the window
+  uint32_t reserved0;
   uint64_t pages;        // kv_indptr_host[batch]
   uint64_t work_items;   // decode pieces or prefill tiles
   uint64_t ranges;       // decode: workgroup ranges over the pieces
@@ -156,8 +158,9 @@ RoostStatus Validate(const RoostPagedAttentionParams& p, bool for_run) {
   if (p.kv_heads == 0 || p.q_heads != p.kv_heads * kGroup) {
     return Fail(ROOST_STATUS_UNSUPPORTED, "PagedAttention: only 4 query heads per KV head are built");
   }
-  if (p.window_left != -1) {
-    return Fail(ROOST_STATUS_UNSUPPORTED, "PagedAttention: sliding window is not built (window_left must be -1)");
+  if (p.window_left == 0) {
+    // CpuOps refuses a window of 0 (reference CpuOps.cs:180-186): bind -1 for no window.
+    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: window_left 0 is refused (-1 means no window)");
   }
   if (p.logits_soft_cap != 0.0f) return Fail(ROOST_STATUS_UNSUPPORTED, "PagedAttention: logit soft capping is not built");
   if (p.kv_layout != ROOST_LAYOUT_PAGED_NHD && p.kv_layout != ROOST_LAYOUT_PAGED_HND) {
@@ -253,6 +256,12 @@ uint32_t KvLenHost(const RoostPagedAttentionParams& p, uint32_t b) {
   return static_cast<uint32_t>((pages - 1) * p.page_size + last);
 }
 
+// The sliding window: query position pos sees keys j >= pos - window (reference CpuOps.cs:180-197, 245-252); -1 (any
+// negative window_left) means no window.
+int32_t WindowOf(const RoostPagedAttentionParams& p) { return p.window_left < 0 ? -1 : p.window_left; }
+// First key a decode query (position kv - 1) sees.
+int64_t DecodeFirstKey(int64_t kv, int32_t window) { return window < 0 ? 0 : std::max<int64_t>(0, kv - 1 - window); }
+
 // Decode: the batch's 16-token groups are dealt out evenly to `ranges` workgroup ranges (kDecodeWgsPerCu workgroups
 // per CU), each range cut at sequence boundaries into pieces. Every workgroup then streams the same number of bytes
 // and the grid finishes together instead of in ragged rounds. A sequence cut into several pieces owns consecutive
@@ -274,11 +283,16 @@ struct DecodePlan {
 template <typename Take>
 DecodePlan BuildDecode(const RoostPagedAttentionParams& p, uint32_t cus, Take take) {
   DecodePlan d;
-  std::vector<uint64_t> groups(p.batch, 0);
+  std::vector<uint64_t> groups(p.batch, 0), first_group(p.batch, 0);
   uint64_t total = 0, planned = 0;
+  const int32_t window = WindowOf(p);
   for (uint32_t b = 0; b < p.batch; ++b) {
     if (!take(b)) continue;
-    groups[b] = roost::CeilDiv(KvLenHost(p, b), 16);
+    const uint32_t kv = KvLenHost(p, b);
+    // Keys before the window are never read (their pages may have been released); the first group keeps its
+    // 16-alignment and the kernel masks its keys below the window.
+    first_group[b] = static_cast<uint64_t>(DecodeFirstKey(kv, window)) / 16;
+    groups[b] = roost::CeilDiv(kv, 16) - first_group[b];
     total += groups[b];
     ++planned;
   }
@@ -309,8 +323,8 @@ DecodePlan BuildDecode(const RoostPagedAttentionParams& p, uint32_t cus, Take ta
         room = per_range;
       }
       const uint64_t n = std::min(room, groups[b] - g);
-      d.items.push_back(DecodeWork{static_cast<int32_t>(b), static_cast<int32_t>(g * 16),
-                                   static_cast<int32_t>(std::min<uint64_t>((g + n) * 16, kv)), -1});
+      d.items.push_back(DecodeWork{static_cast<int32_t>(b), static_cast<int32_t>((first_group[b] + g) * 16),
+                                   static_cast<int32_t>(std::min<uint64_t>((first_group[b] + g + n) * 16, kv)), -1});
       g += n;
       room -= n;
     }
@@ -385,6 +399,7 @@ Layout PlanPrefill(const RoostPagedAttentionParams& p, uint32_t cus, unsigned ch
   };
   std::vector<Item> items;
   int64_t total_tiles = 0;
+  const int32_t window = WindowOf(p);
   // A sequence with one query token (a decode row of a mixed step) sees every key whether causal or not: the decode
   // kernel streams it at HBM speed instead of a 64-row MFMA tile holding one row.
   auto single = [&](uint32_t b) { return p.q_indptr_host[b + 1] - p.q_indptr_host[b] == 1; };
@@ -396,11 +411,17 @@ Layout PlanPrefill(const RoostPagedAttentionParams& p, uint32_t cus, unsigned ch
       const int64_t rows = std::min<int64_t>(tile_q, n - q0);
       int64_t kend = p.causal ? std::min<int64_t>(kv, kv - n + q0 + rows) : kv;
       if (kend < 0) kend = 0;
-      total_tiles += roost::CeilDiv(kend, 64) * p.kv_heads;
+      // With a window the item's first query (position kv - n + q0) sees keys from kv - n + q0 - window on; the
+      // range starts at that key rounded down to 16 (a 16-row group never straddles a page), and keys before it are
+      // never read.
+      int64_t kbeg = window < 0 ? 0 : std::max<int64_t>(0, kv - n + q0 - window) / 16 * 16;
+      if (kbeg > kend) kbeg = kend;
+      total_tiles += roost::CeilDiv(kend - kbeg, 64) * p.kv_heads;
       for (uint32_t h = 0; h < p.kv_heads; ++h) {
         items.push_back(Item{PrefillWork{static_cast<int32_t>(b), static_cast<int32_t>(q0), static_cast<int32_t>(h),
-                                         static_cast<int32_t>(rows), 0, static_cast<int32_t>(kend), -1, 0},
-                             kend + 64});
+                                         static_cast<int32_t>(rows), static_cast<int32_t>(kbeg),
+                                         static_cast<int32_t>(kend), -1, 0},
+                             kend - kbeg + 64});
       }
     }
   }
@@ -411,7 +432,7 @@ Layout PlanPrefill(const RoostPagedAttentionParams& p, uint32_t cus, unsigned ch
     std::vector<Item> cut;
     cut.reserve(items.size());
     for (const Item& it : items) {
-      const int64_t tiles = roost::CeilDiv(static_cast<int64_t>(it.w.kend), 64);
+      const int64_t tiles = roost::CeilDiv(static_cast<int64_t>(it.w.kend - it.w.kbeg), 64);
       const int64_t pieces = std::min<int64_t>(roost::CeilDiv(tiles, target), kMaxMergeSplits);
       if (pieces <= 1) {
         cut.push_back(it);
@@ -421,8 +442,8 @@ Layout PlanPrefill(const RoostPagedAttentionParams& p, uint32_t cus, unsigned ch
       for (int64_t i = 0; i < pieces; ++i) {
         const int64_t t0 = tiles * i / pieces, t1 = tiles * (i + 1) / pieces;
         PrefillWork w = it.w;
-        w.kbeg = static_cast<int32_t>(t0 * 64);
-        w.kend = static_cast<int32_t>(std::min<int64_t>(t1 * 64, it.w.kend));
+        w.kbeg = static_cast<int32_t>(it.w.kbeg + t0 * 64);
+        w.kend = static_cast<int32_t>(std::min<int64_t>(it.w.kbeg + t1 * 64, it.w.kend));
         w.slot = slot++;
         cut.push_back(Item{w, (t1 - t0) * 64 + 64});
       }
@@ -807,7 +828,8 @@ __global__ void __launch_bounds__(256, ROOST_DECODE_WGS_PER_CU) DecodeKernel(con
 
                                                     float* __restrict__ part_o, float* __restrict__ part_ml,
                                                     const int32_t* __restrict__ q_rows,
-                                                    uint32_t q_heads, uint32_t heads_per_wg, float scale_log2) {
+                                                    uint32_t q_heads, uint32_t heads_per_wg, float scale_log2,
+                                                    int32_t window) {
   using C = DecodeCfg<T, D>;
   constexpr int kVec = C::kVec, kLpr = C::kLpr, kTpi = C::kTpi, kNi = C::kNi;
   constexpr bool kMfma = sizeof(T) == 2;  // bf16: q.k on MFMA; f32: the VALU reduce-scatter path
@@ -842,6 +864,9 @@ __global__ void __launch_bounds__(256, ROOST_DECODE_WGS_PER_CU) DecodeKernel(con
   const uint64_t tok = q_rows != nullptr ? static_cast<uint64_t>(q_rows[wk.seq]) : static_cast<uint64_t>(wk.seq);
   const uint32_t t_begin = static_cast<uint32_t>(wk.token_begin);
   const uint32_t t_end = min(kv_len, static_cast<uint32_t>(wk.token_end));
+  // The sliding window's first visible key (the query sits at position kv_len - 1); the piece may start up to 15
+  // keys before it, which are masked.
+  const uint32_t lo = window < 0 || kv_len == 0 ? 0u : static_cast<uint32_t>(max(0, static_cast<int32_t>(kv_len) - 1 - window));
 
   using QW = typename std::conditional<sizeof(T) == 2, uint32_t, float>::type;
   QW qr[kGroup][C::kQWords];   // VALU path (f32)
@@ -900,7 +925,7 @@ __global__ void __launch_bounds__(256, ROOST_DECODE_WGS_PER_CU) DecodeKernel(con
 #pragma unroll
       for (int i = 0; i < kNi; ++i) {
         const uint32_t tv = i * kTpi + ri;  // V register i: slot i
-        const bool okv = live && page_ok && g0 + tv < t_end;
+        const bool okv = live && page_ok && g0 + tv < t_end && g0 + tv >= lo;
         vr[i] = LoadStream16(vg + ((okv ? tv : 0) * tok_bytes + r * 16));
         if constexpr (kMfma) {
           const uint32_t tk = lane & 15;  // K register i: dims 32 i + 8 (lane / 16) of token lane % 16
@@ -916,6 +941,7 @@ __global__ void __launch_bounds__(256, ROOST_DECODE_WGS_PER_CU) DecodeKernel(con
       if constexpr (kMfma) {
         const uint32_t n = live && page_ok ? min(16u, t_end - g0) : 0u;
         valid = (1u << n) - 1u;  // bit t: token t of the group is a real key
+        if (g0 < lo) valid &= ~((1u << min(16u, lo - g0)) - 1u);  // before the window
       }
     } else {
       bool kok = false;
@@ -927,6 +953,8 @@ __global__ void __launch_bounds__(256, ROOST_DECODE_WGS_PER_CU) DecodeKernel(con
         const uint64_t rowk = KeyRowSafe<D>(kv, p0, tk, static_cast<int32_t>(t_end), kvh, &okk);
         const uint64_t rowv = KeyRowSafe<D>(kv, p0, static_cast<int32_t>(g0 + i * kTpi + ri),
                                             static_cast<int32_t>(t_end), kvh, &okv);
+        okk = okk && tk >= static_cast<int32_t>(lo);
+        okv = okv && g0 + i * kTpi + ri >= lo;
         kr[i] = *reinterpret_cast<const uint4*>(kMfma ? kbase + rowk + i * 32 + (lane >> 4) * 8 : kbase + rowk + r * kVec);
         vr[i] = LoadStream16(vbase + rowv + r * kVec);
         if constexpr (!kMfma) valid |= static_cast<uint32_t>(okv && live) << i;
@@ -1083,7 +1111,7 @@ __device__ __forceinline__ f32x16_t Mfma32(const u32x4_t& a, const u32x4_t& b, c
 __global__ void __launch_bounds__(256, 1)
     PrefillKernel(const uint16_t* __restrict__ q, uint16_t* __restrict__ out, float* __restrict__ lse, KvView kv,
                   const int32_t* __restrict__ q_indptr, const PrefillWork* __restrict__ work, uint32_t q_heads,
-                  uint32_t causal, float scale_log2) {
+                  uint32_t causal, float scale_log2, int32_t window) {
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[kPrefillTileK * kKStride];
   __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kPD * kVtStride];
 
@@ -1155,9 +1183,12 @@ __global__ void __launch_bounds__(256, 1)
       }
     }
   };
-  if (key_end > 0) fetch(0);
+  // With a window the tile's first query (position base_pos) sees keys from base_pos - window on; keys before that
+  // are never read.
+  const int32_t key_beg = window < 0 ? 0 : min(max(0, base_pos - window), key_end);
+  if (key_end > key_beg) fetch(key_beg);
 
-  for (int32_t kb = 0; kb < key_end; kb += kPrefillTileK) {
+  for (int32_t kb = key_beg; kb < key_end; kb += kPrefillTileK) {
     __syncthreads();  // every wavefront is done reading the previous tile
     // K row-major; V transposed: 4 keys x 8 dims become 8 rows (dims) of 4 keys.
 #pragma unroll
@@ -1201,7 +1232,8 @@ __global__ void __launch_bounds__(256, 1)
     }
     // Scale, mask, online softmax for this lane's query.
     const bool need_mask = (kb + static_cast<int32_t>(kPrefillTileK) > key_end) ||
-                           (causal && kb + static_cast<int32_t>(kPrefillTileK) - 1 > base_pos);
+                           (causal && kb + static_cast<int32_t>(kPrefillTileK) - 1 > base_pos) ||
+                           (window >= 0 && kb < base_pos + rows - 1 - window);
     float mx = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
@@ -1209,7 +1241,9 @@ __global__ void __launch_bounds__(256, 1)
       for (int v = 0; v < 16; ++v) {
         const int32_t key = kb + kt * 32 + (v >> 2) * 8 + hl * 4 + (v & 3);
         float x = s[kt][v] * scale_log2;
-        if (need_mask && (key >= key_end || (causal && key > my_pos))) x = -INFINITY;
+        if (need_mask && (key >= key_end || (causal && key > my_pos) || (window >= 0 && key < my_pos - window))) {
+          x = -INFINITY;
+        }
         s[kt][v] = x;
         mx = fmaxf(mx, x);
       }
@@ -1340,7 +1374,7 @@ __global__ void __launch_bounds__(512, 1)
     PrefillTileKernel(const uint16_t* __restrict__ q, uint16_t* __restrict__ out, float* __restrict__ lse, KvView kv,
                       const int32_t* __restrict__ kv_indices, const int32_t* __restrict__ q_indptr,
                       const PrefillWork* __restrict__ work, float* __restrict__ part_o, float* __restrict__ part_ml,
-                      uint32_t q_heads, uint32_t causal, uint32_t ps_shift, float scale_log2) {
+                      uint32_t q_heads, uint32_t causal, uint32_t ps_shift, float scale_log2, int32_t window) {
   __shared__ __attribute__((aligned(16))) unsigned char tiles[2][2][kPfTileBytes];  // [buffer][K, V]
 
   const PrefillWork wk = work[blockIdx.x];
@@ -1457,7 +1491,8 @@ __global__ void __launch_bounds__(512, 1)
     const int vrow = vkey * 512 + 16 * ((vdim >> 3) & 3) + 2 * (vdim & 7);
     const int vx = (64 * (vkey & 3)) ^ (128 * ((vkey >> 2) & 1));
     const int32_t qpos = static_cast<int32_t>(kv_len) - n + wk.q0 + 32 * qt + lc;  // this lane's query position
-    const bool need_mask = kb + 64 > kend || (causal && kb + 63 > last_pos - 31) || bad != 0;
+    const bool need_mask = kb + 64 > kend || (causal && kb + 63 > last_pos - 31) || bad != 0 ||
+                           (window >= 0 && kb < last_pos - window);
     const unsigned char* ktile = tiles[buf][0];
     const unsigned char* vtile = tiles[buf][1];
 #pragma unroll
@@ -1483,7 +1518,8 @@ __global__ void __launch_bounds__(512, 1)
         for (int v = 0; v < 16; ++v) {
           const int kk = 32 * half + (v >> 2) * 8 + lh * 4 + (v & 3);  // key within the tile
           const int32_t key = kb + kk;
-          const bool off = key >= kend || (causal && key > qpos) || ((bad >> (kk >> 4)) & 1u);
+          const bool off = key >= kend || (causal && key > qpos) || ((bad >> (kk >> 4)) & 1u) ||
+                           (window >= 0 && key < qpos - window);
           sc[v] = off ? -INFINITY : sc[v];
         }
       }
@@ -1630,10 +1666,12 @@ RoostStatus LaunchDecode(const RoostPagedAttentionParams& p, const PlanRecord& r
   const dim3 grid(static_cast<uint32_t>(rec.dec_ranges * (p.kv_heads / hpw)));
   if (p.page_size % 16 == 0) {
     hipLaunchKernelGGL((DecodeKernel<T, D, true>), grid, dim3(256), 0, stream, static_cast<const T*>(p.q.address), out,
-                       lse, kv, kv.kv_indices, items, range_ptr, part_o, part_ml, q_rows, p.q_heads, hpw, scale_log2);
+                       lse, kv, kv.kv_indices, items, range_ptr, part_o, part_ml, q_rows, p.q_heads, hpw, scale_log2,
+                       WindowOf(p));
   } else {
     hipLaunchKernelGGL((DecodeKernel<T, D, false>), grid, dim3(256), 0, stream, static_cast<const T*>(p.q.address), out,
-                       lse, kv, kv.kv_indices, items, range_ptr, part_o, part_ml, q_rows, p.q_heads, hpw, scale_log2);
+                       lse, kv, kv.kv_indices, items, range_ptr, part_o, part_ml, q_rows, p.q_heads, hpw, scale_log2,
+                       WindowOf(p));
   }
   ROOST_TRY(roost::FromHip(hipGetLastError(), "PagedAttention decode launch"));
   if (rec.dec_merges == 0) return ROOST_STATUS_OK;
@@ -1656,7 +1694,7 @@ RoostStatus LaunchPrefill(const RoostPagedAttentionParams& p, const PlanRecord& 
     hipLaunchKernelGGL(PrefillTileKernel, dim3(static_cast<uint32_t>(rec.work_items)), dim3(512), 0, stream,
                        static_cast<const uint16_t*>(p.q.address), outp, lsep, kv, kv.kv_indices, q_indptr, items,
                        part_o, part_ml, p.q_heads, p.causal, static_cast<uint32_t>(__builtin_ctz(p.page_size)),
-                       scale_log2);
+                       scale_log2, WindowOf(p));
     ROOST_TRY(FromHip(hipGetLastError(), "PagedAttention prefill launch"));
     if (rec.merges == 0) return ROOST_STATUS_OK;
     hipLaunchKernelGGL(PrefillMergeKernel, dim3(static_cast<uint32_t>(rec.merges), kPfTokens), dim3(kPD), 0, stream, outp,
@@ -1666,7 +1704,7 @@ RoostStatus LaunchPrefill(const RoostPagedAttentionParams& p, const PlanRecord& 
   }
   hipLaunchKernelGGL(PrefillKernel, dim3(static_cast<uint32_t>(rec.work_items)), dim3(256), 0, stream,
                      static_cast<const uint16_t*>(p.q.address), outp, lsep, kv, q_indptr, items, p.q_heads, p.causal,
-                     scale_log2);
+                     scale_log2, WindowOf(p));
   return FromHip(hipGetLastError(), "PagedAttention prefill launch");
 }
 
@@ -1722,6 +1760,7 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_plan(RoostContext* ctx, c
     rec.kv_layout = p.kv_layout;
     rec.head_dim = p.head_dim;
     rec.kv_heads = p.kv_heads;
+    rec.window = WindowOf(p);
     rec.pages = static_cast<uint64_t>(p.kv_indptr_host[p.batch]);
     rec.work_items = l.work_items;
     rec.ranges = l.ranges;
@@ -1760,7 +1799,8 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_run(RoostContext*, const 
     std::memcpy(&rec, ws->plan, sizeof(rec));
     if (rec.magic != kPlanMagic) return Fail(ROOST_STATUS_NOT_PLANNED, "PagedAttention: no plan was made in this workspace");
     if (rec.mode != p.mode || rec.batch != p.batch || rec.tokens != p.tokens || rec.page_size != p.page_size ||
-        rec.kv_layout != p.kv_layout || rec.head_dim != p.head_dim || rec.kv_heads != p.kv_heads) {
+        rec.kv_layout != p.kv_layout || rec.head_dim != p.head_dim || rec.kv_heads != p.kv_heads ||
+        rec.window != WindowOf(p)) {
       return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: the plan was made for another batch shape");
     }
     ROOST_TRY(CheckSpan(p.kv_indices, ROOST_DTYPE_I32, rec.pages, "PagedAttention", "kv_indices"));

@@ -39,7 +39,7 @@ def from_dev(x, bf16=False):
 class Dev:
     """A PagedBatch on the device plus its params."""
 
-    def __init__(self, b: cases.PagedBatch, causal=True, with_lse=False):
+    def __init__(self, b: cases.PagedBatch, causal=True, with_lse=False, window_left=-1):
         self.b = b
         self.q = to_dev(b.q, b.bf16)
         self.k = to_dev(b.k_cache, b.bf16)
@@ -51,13 +51,15 @@ class Dev:
         self.out = torch().full_like(self.q, float("nan"))
         self.lse = torch().zeros((b.tokens, b.hq), dtype=torch().float32, device="cuda") if with_lse else None
         self.causal = causal
+        self.window_left = window_left
 
     def params(self, host=True, **over):
         b = self.b
         kw = dict(q_indptr_host=b.q_indptr if host else None, kv_indptr_host=b.kv_indptr if host else None,
                   kv_last_page_len_host=b.kv_last_page_len if host else None, batch=b.batch, q_heads=b.hq,
                   kv_heads=b.hkv, head_dim=b.d, page_size=b.page_size,
-                  kv_layout=abi.LAYOUT_PAGED_HND if b.hnd else abi.LAYOUT_PAGED_NHD, causal=self.causal, lse=self.lse)
+                  kv_layout=abi.LAYOUT_PAGED_HND if b.hnd else abi.LAYOUT_PAGED_NHD, causal=self.causal, lse=self.lse,
+                  window_left=self.window_left)
         kw.update(over)
         return roost_amd.paged_attention_params(self.q, self.out, self.k, self.v, self.q_indptr, self.kv_indptr,
                                                 self.kv_indices, self.last, **kw)
@@ -66,8 +68,8 @@ class Dev:
         return cases.values(from_dev(self.out, self.b.bf16), self.b.bf16)
 
 
-def run_case(session, b: cases.PagedBatch, causal=True, check_nohost=True, check_determinism=True):
-    d = Dev(b, causal)
+def run_case(session, b: cases.PagedBatch, causal=True, check_nohost=True, check_determinism=True, window_left=-1):
+    d = Dev(b, causal, window_left=window_left)
     entry = session.lib.entry(roost_amd.ATTENTION_VARIANT)
     p = d.params()
     # Run before plan: NOT_PLANNED (a fresh, zeroed plan record).
@@ -90,8 +92,8 @@ def run_case(session, b: cases.PagedBatch, causal=True, check_nohost=True, check
     return cases.values(got, b.bf16)
 
 
-def check_against_oracle(got, b, causal=True):
-    ref = cases.values(cases.oracle_attention(b, causal), b.bf16)
+def check_against_oracle(got, b, causal=True, window_left=-1):
+    ref = cases.values(cases.oracle_attention(b, causal, window_left=window_left), b.bf16)
     a, r = cases.assert_close(got, ref, what="attention")
     if b.bf16:
         cases.assert_attention_class(got, ref, float(np.abs(cases.values(b.v_cache, True)).max()), what="attention")
@@ -351,7 +353,7 @@ def test_rejections(session):
 
     assert status(head_dim=96) == abi.UNSUPPORTED
     assert status(q_heads=16) == abi.UNSUPPORTED
-    assert status(window_left=128) == abi.UNSUPPORTED
+    assert status(window_left=0) == abi.INVALID_ARGUMENT  # CpuOps refuses a window of 0; -1 means none
     assert status(soft_cap=30.0) == abi.UNSUPPORTED
     p = d.params()
     p.tokens = 3
@@ -379,3 +381,82 @@ def test_rejections(session):
     assert entry.plan(session.ctx, C.addressof(good), C.addressof(small), C.c_void_p(session.stream_handle)) == \
         abi.WORKSPACE_TOO_SMALL
     torch().cuda.synchronize()
+
+
+# ---- Sliding window (CpuOps.cs:180-197, 245-252): query position pos sees keys j >= pos - window_left ---------------
+
+
+def _release_before_window(b: cases.PagedBatch, window, causal=True):
+    """Marks every page that no query of its sequence can see as released (-1), as the block manager does for blocks
+    that left a sliding window (R-028): the kernels must neither read them nor fault on them."""
+    idx = b.kv_indices.copy()
+    for s in range(b.batch):
+        n = int(b.q_indptr[s + 1] - b.q_indptr[s])
+        first = max(0, int(b.kv_lens[s]) - n - window)  # the first query's first visible key
+        for pi in range(int(b.kv_indptr[s]), int(b.kv_indptr[s + 1])):
+            page = pi - int(b.kv_indptr[s])
+            if (page + 1) * b.page_size <= first:
+                idx[pi] = -1
+    b.kv_indices = idx
+    return b
+
+
+WINDOW_DECODE_CASES = [
+    ("decode w1", [5, 37, 130, 16], 16, False, 1),
+    ("decode w40 ps16", [900, 17, 1, 2048, 333, 64, 1024, 777], 16, False, 40),
+    ("decode w100 HND ps64", [900, 17, 1, 2048, 333, 64, 1024, 777], 64, True, 100),
+    ("decode w4096 longer than most", [900, 6000, 5000, 40], 16, False, 4096),
+    ("decode w33 ps7 general pages", [5, 37, 130, 1000], 7, False, 33),
+]
+
+
+@pytest.mark.parametrize("name,kv_lens,ps,hnd,window", WINDOW_DECODE_CASES, ids=[c[0] for c in WINDOW_DECODE_CASES])
+def test_decode_sliding_window(session, name, kv_lens, ps, hnd, window):
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    b = _release_before_window(cases.make_paged_batch(rng, kv_lens, [1] * len(kv_lens), page_size=ps, hnd=hnd),
+                               window)
+    got = run_case(session, b, window_left=window)
+    check_against_oracle(got, b, window_left=window)
+
+
+def test_decode_sliding_window_f32(session):
+    """The f32 decode path (config 1's types) with a window and released pages."""
+    rng = np.random.default_rng(41)
+    b = _release_before_window(cases.make_paged_batch(rng, [17, 300, 120, 64], [1] * 4, bf16=False, d=64), 50)
+    got = run_case(session, b, window_left=50)
+    ref = cases.values(cases.oracle_attention(b, window_left=50), False)
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
+
+
+WINDOW_PREFILL_CASES = [
+    ("prefill w128 fresh-700", [(700, 700)], 16, False, True, 128),
+    ("prefill w1000 chunk-512-of-4000 split", [(512, 4000), (3, 3)], 16, False, True, 1000),
+    ("prefill w64 multi-seq HND ps32", [(17, 17), (64, 300), (200, 200)], 32, True, True, 64),
+    ("prefill w50 ps8 general", [(100, 300)], 8, False, True, 50),
+    ("prefill w200 non-causal", [(32, 400)], 16, False, False, 200),
+    ("prefill w300 mixed step", [(1, 900), (1, 17), (200, 1200), (1, 3000), (64, 64)], 16, False, True, 300),
+    ("prefill w5000 wider than every context", [(128, 1000), (40, 40)], 16, False, True, 5000),
+]
+
+
+@pytest.mark.parametrize("name,seqs,ps,hnd,causal,window", WINDOW_PREFILL_CASES,
+                         ids=[c[0] for c in WINDOW_PREFILL_CASES])
+def test_prefill_sliding_window(session, name, seqs, ps, hnd, causal, window):
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    b = cases.make_paged_batch(rng, [s[1] for s in seqs], [s[0] for s in seqs], page_size=ps, hnd=hnd)
+    if causal:
+        b = _release_before_window(b, window)
+    got = run_case(session, b, causal=causal, window_left=window)
+    check_against_oracle(got, b, causal=causal, window_left=window)
+
+
+def test_sliding_window_plan_must_match_run(session):
+    """A plan made for one window is refused by a run with another (the pieces start at the window)."""
+    rng = np.random.default_rng(77)
+    b = cases.make_paged_batch(rng, [300, 40], [1, 1])
+    d = Dev(b, window_left=64)
+    entry = session.lib.entry(roost_amd.ATTENTION_VARIANT)
+    session.launch(entry, d.params(), key="window")
+    ws = session._ws[(entry.variant_id, "window")][3]
+    d.window_left = -1
+    assert session.run_raw(entry, d.params(), ws) == abi.INVALID_ARGUMENT
