@@ -157,7 +157,7 @@ def test_attention_refusals_without_gpu(kernels):
     run = lambda q: e.run(ctx, C.addressof(q), None, None)  # noqa: E731
     assert run(p) == abi.NOT_PLANNED  # valid params, no plan record
     for field, value, want in [("head_dim", 96, abi.UNSUPPORTED), ("q_heads", 16, abi.UNSUPPORTED),
-                               ("window_left", 128, abi.UNSUPPORTED), ("logits_soft_cap", 30.0, abi.UNSUPPORTED),
+                               ("window_left", 0, abi.INVALID_ARGUMENT), ("logits_soft_cap", 30.0, abi.UNSUPPORTED),
                                ("tokens", 3, abi.INVALID_ARGUMENT), ("mode", 7, abi.INVALID_ARGUMENT),
                                ("kv_layout", 0, abi.INVALID_ARGUMENT), ("batch", 0, abi.INVALID_ARGUMENT),
                                ("struct_size", 64, abi.ABI_MISMATCH), ("abi_minor", 4, abi.ABI_MISMATCH)]:
