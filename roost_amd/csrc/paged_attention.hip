@@ -1511,8 +1511,6 @@ __global__ void __launch_bounds__(512, 1)
         if (ks + kRing < 16) ka[ks % kRing] = *reinterpret_cast<const u32x4_t*>(krow_p + ((32 * (ks + kRing)) ^ kx));
         sc = Mfma32(a, qreg[ks], sc);
       }
-#pragma unroll
-      for (int v = 0; v < 16; ++v) sc[v] *= scale_log2;
       if (need_mask) {  // one uniform branch around branch-free selects
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
@@ -1527,6 +1525,7 @@ __global__ void __launch_bounds__(512, 1)
 #pragma unroll
       for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sc[v]);
       mx = fmaxf(mx, ShflXor(mx, 32));
+      mx *= scale_log2;  // scores stay unscaled until the exponent: the scale is positive, so this is the scaled max
       const bool grow = mx > m_run + 8.0f;
       if (__any(grow)) {
         const float m_new = grow ? mx : m_run;
@@ -1546,8 +1545,8 @@ __global__ void __launch_bounds__(512, 1)
         float pf[8];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          pf[e] = __builtin_amdgcn_exp2f(sc[(2 * c) * 4 + e] - m_use);
-          pf[4 + e] = __builtin_amdgcn_exp2f(sc[(2 * c + 1) * 4 + e] - m_use);
+          pf[e] = __builtin_amdgcn_exp2f(fmaf(sc[(2 * c) * 4 + e], scale_log2, -m_use));
+          pf[4 + e] = __builtin_amdgcn_exp2f(fmaf(sc[(2 * c + 1) * 4 + e], scale_log2, -m_use));
         }
 #pragma unroll
         for (int e = 0; e < 8; ++e) psum += pf[e];
