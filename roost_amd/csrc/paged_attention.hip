@@ -1062,13 +1062,30 @@ __global__ void __launch_bounds__(D) DecodeMergeKernel(T* __restrict__ out, floa
   const uint32_t qh = blockIdx.x % q_heads;
   const int n = min(mg.count, static_cast<int32_t>(kMaxMergeSplits));
   const uint64_t base = static_cast<uint64_t>(mg.first) * q_heads + qh;  // partial row of piece c: base + c * q_heads
+  // This thread's partial outputs of the first kPre pieces are requested first, so that they arrive while the pieces'
+  // weights are being computed (a sequence is usually cut into fewer than kPre pieces).
+  constexpr int kPre = 16;
+  const int d = threadIdx.x;
+  const float* po = part_o + base * D + d;
+  const uint64_t step = static_cast<uint64_t>(q_heads) * D;
+  float pre[kPre];
+#pragma unroll
+  for (int c = 0; c < kPre; ++c) pre[c] = c < n ? po[c * step] : 0.0f;
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
-    float M = -INFINITY;
-    for (int c = lane; c < n; c += 64) M = fmaxf(M, part_ml[(base + static_cast<uint64_t>(c) * q_heads) * 2]);
+    // Piece `lane` (and lane + 64, ... for longer splits): its max and sum, read once.
+    const float m0 = lane < n ? part_ml[(base + static_cast<uint64_t>(lane) * q_heads) * 2] : -INFINITY;
+    const float l0 = lane < n ? part_ml[(base + static_cast<uint64_t>(lane) * q_heads) * 2 + 1] : 0.0f;
+    float M = m0;
+    for (int c = lane + 64; c < n; c += 64) M = fmaxf(M, part_ml[(base + static_cast<uint64_t>(c) * q_heads) * 2]);
     for (int mk = 32; mk >= 1; mk >>= 1) M = fmaxf(M, __shfl_xor(M, mk, 64));
     float L = 0.0f;
-    for (int c = lane; c < n; c += 64) {
+    if (lane < n) {
+      const float f = m0 == -INFINITY ? 0.0f : exp2f(m0 - M);
+      f_lds[lane] = f;
+      L = l0 * f;
+    }
+    for (int c = lane + 64; c < n; c += 64) {
       const uint64_t prow = base + static_cast<uint64_t>(c) * q_heads;
       const float mc = part_ml[prow * 2];
       const float f = mc == -INFINITY ? 0.0f : exp2f(mc - M);
@@ -1082,18 +1099,14 @@ __global__ void __launch_bounds__(D) DecodeMergeKernel(T* __restrict__ out, floa
     }
   }
   __syncthreads();
-  const int d = threadIdx.x;
-  const float* po = part_o + base * D + d;
-  const uint64_t step = static_cast<uint64_t>(q_heads) * D;
-  float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
-  int c = 0;
-  for (; c + 3 < n; c += 4) {
-    o0 = fmaf(po[(c + 0) * step], f_lds[c + 0], o0);
-    o1 = fmaf(po[(c + 1) * step], f_lds[c + 1], o1);
-    o2 = fmaf(po[(c + 2) * step], f_lds[c + 2], o2);
-    o3 = fmaf(po[(c + 3) * step], f_lds[c + 3], o3);
+  // Pieces in key order, piece c into accumulator c % 4 (a fixed order: deterministic).
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int c = 0; c < kPre; ++c) {
+    if (c < n) acc[c & 3] = fmaf(pre[c], f_lds[c], acc[c & 3]);
   }
-  for (; c < n; ++c) o0 = fmaf(po[c * step], f_lds[c], o0);
+  for (int c = kPre; c < n; ++c) acc[c & 3] = fmaf(po[c * step], f_lds[c], acc[c & 3]);
+  const float o0 = acc[0], o1 = acc[1], o2 = acc[2], o3 = acc[3];
   out[(tok * q_heads + qh) * D + d] = Vec<T>::Narrow(((o0 + o1) + (o2 + o3)) * inv_lds);
 }
 
