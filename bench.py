@@ -131,11 +131,12 @@ def bench_decode(torch, roost_amd, session, steps, warmup):
     return b, ms, plan_ms
 
 
-def bench_prefill(torch, roost_amd, session, steps, warmup):
+def bench_prefill(torch, roost_amd, session, steps, warmup, d=256):
+    """Config 3's draw (seed 3); d=128 runs the same batch at head dim 128 (the second tile-kernel instantiation)."""
     rng = np.random.default_rng(3)
     n = rng.integers(256, 2049, size=8)
     pre = rng.integers(0, 6145, size=8)
-    b = Paged(torch, rng, n + pre, n)
+    b = Paged(torch, rng, n + pre, n, d=d)
     entry = session.lib.entry(roost_amd.ATTENTION_VARIANT)
     p = b.params(roost_amd)
     ws, plan_ms = planned(session, entry, p, "bench-prefill")
@@ -408,7 +409,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=16)
-    ap.add_argument("--only", choices=["decode", "prefill", "gdn", "mixed", "layer", "attn_in"], default=None,
+    ap.add_argument("--only", choices=["decode", "prefill", "prefill128", "gdn", "mixed", "layer", "attn_in"], default=None,
                     help="run one workload only and print its timing (for profiler passes); no JSON line")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -426,7 +427,8 @@ def main():
     session = roost_amd.OpSession(device=0)
     if args.only is not None:
         fn = {"decode": bench_decode, "prefill": bench_prefill, "gdn": bench_gdn, "mixed": bench_mixed,
-              "layer": bench_layer_ops, "attn_in": bench_attention_input}[args.only]
+              "layer": bench_layer_ops, "attn_in": bench_attention_input,
+              "prefill128": lambda *a: bench_prefill(*a, d=128)}[args.only]
         res = fn(torch, roost_amd, session, args.steps, args.warmup)
         log(f"{args.only}: {res[1] if isinstance(res, tuple) else res} ms")
         session.close()
@@ -440,6 +442,9 @@ def main():
     pb, pre_ms, pre_plan_ms = bench_prefill(torch, roost_amd, session, args.steps, args.warmup)
     pre_tflops = pb.prefill_flops() / pre_ms / 1e9
     log(f"  {pre_ms * 1e3:.1f} us/step, {pre_tflops:.0f} TFLOP/s")
+    _, pre128_ms, _ = bench_prefill(torch, roost_amd, session, args.steps, args.warmup, d=128)
+    pre128_flops = pb.prefill_flops() / 2
+    log(f"  head dim 128: {pre128_ms * 1e3:.1f} us/step, {pre128_flops / pre128_ms / 1e9:.0f} TFLOP/s")
     log("gdn (config 4) ...")
     gdn = bench_gdn(torch, roost_amd, session, args.steps, args.warmup)
     log(f"  {json.dumps(gdn)}")
@@ -480,7 +485,10 @@ def main():
         "prefill": {"workload": "BASELINE config 3: 8 seqs, chunk U(256, 2048) on prefix U(0, 6144), causal",
                     "ms": round(pre_ms, 4), "tflops": round(pre_tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                     "frac": round(pre_tflops / MFMA_BF16_PEAK_TFLOPS, 4), "flops": pb.prefill_flops(),
-                    "query_tokens": pb.tokens},
+                    "query_tokens": pb.tokens,
+                    "head_dim_128": {"ms": round(pre128_ms, 4), "tflops": round(pre128_flops / pre128_ms / 1e9, 1),
+                                     "frac": round(pre128_flops / pre128_ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
+                                     "note": "the same draw at head dim 128 (not a BASELINE config)"}},
         "gdn": {k: _rounded(v) for k, v in gdn.items()},
         "mixed_step": _rounded(mixed),
         "gdn_layer_ops": {k: _rounded(v) for k, v in layer.items()},

@@ -152,8 +152,11 @@ RoostStatus Validate(const RoostPagedAttentionParams& p, bool for_run) {
   if (p.head_dim != 64 && p.head_dim != 128 && p.head_dim != 256) {
     return Fail(ROOST_STATUS_UNSUPPORTED, "PagedAttention: head_dim must be 64, 128 or 256");
   }
-  if (p.mode == ROOST_ATTENTION_PREFILL && p.head_dim != 256) {
-    return Fail(ROOST_STATUS_UNSUPPORTED, "PagedAttention: prefill is built for head_dim 256");
+  if (p.mode == ROOST_ATTENTION_PREFILL && p.head_dim != 256 &&
+      !(p.head_dim == 128 && p.page_size % 16 == 0 && (p.page_size & (p.page_size - 1)) == 0)) {
+    return Fail(ROOST_STATUS_UNSUPPORTED,
+                "PagedAttention: prefill is built for head_dim 256, and for 128 with page sizes that are powers of two "
+                "and multiples of 16");
   }
   if (p.kv_heads == 0 || p.q_heads != p.kv_heads * kGroup) {
     return Fail(ROOST_STATUS_UNSUPPORTED, "PagedAttention: only 4 query heads per KV head are built");
@@ -1381,14 +1384,22 @@ __device__ __forceinline__ uint32_t PackRne(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-constexpr int kPfTileBytes = kPrefillTileK * kPD * 2;  // one 64-key K or V tile: 32 KB
-
+// Head dims 256 and 128: a row is 2 D bytes = D / 8 16-byte pieces (32 or 16), and every swizzle term below (at most
+// 15 for K, 12 for V) stays inside the row.
+template <int D>
 __global__ void __launch_bounds__(512, 1)
     PrefillTileKernel(const uint16_t* __restrict__ q, uint16_t* __restrict__ out, float* __restrict__ lse, KvView kv,
                       const int32_t* __restrict__ kv_indices, const int32_t* __restrict__ q_indptr,
                       const PrefillWork* __restrict__ work, float* __restrict__ part_o, float* __restrict__ part_ml,
                       uint32_t q_heads, uint32_t causal, uint32_t ps_shift, float scale_log2, int32_t window) {
-  __shared__ __attribute__((aligned(16))) unsigned char tiles[2][2][kPfTileBytes];  // [buffer][K, V]
+  static_assert(D == 128 || D == 256, "the tile kernel is built for head dims 128 and 256");
+  constexpr int kRowB = 2 * D;                  // bytes of one K or V row in LDS
+  constexpr int kPieces = D / 8;                // 16-byte pieces per row
+  constexpr int kRowsPerDma = 1024 / kRowB;     // rows one 64-lane global_load_lds_dwordx4 fills
+  constexpr int kKs = D / 16;                   // K = 16 steps of S^T = K Q^T
+  constexpr int kDt = D / 32;                   // 32-dim blocks of O^T
+  constexpr int kTileBytes = kPrefillTileK * kRowB;  // one 64-key K or V tile
+  __shared__ __attribute__((aligned(16))) unsigned char tiles[2][2][kTileBytes];  // [buffer][K, V]
 
   const PrefillWork wk = work[blockIdx.x];
   const int tid = threadIdx.x;
@@ -1415,11 +1426,11 @@ __global__ void __launch_bounds__(512, 1)
   const int ntiles = kend > kbeg ? (kend - kbeg + 63) / 64 : 0;
 
   // Q^T operands: qreg[ks] = q[query r][dims 16 ks + 8 hl .. +8].
-  u32x4_t qreg[16];
+  u32x4_t qreg[kKs];
   {
-    const uint16_t* qrow = q + (static_cast<uint64_t>(qbeg + wk.q0 + (row_ok ? r : 0)) * q_heads + head) * kPD + hl * 8;
+    const uint16_t* qrow = q + (static_cast<uint64_t>(qbeg + wk.q0 + (row_ok ? r : 0)) * q_heads + head) * D + hl * 8;
 #pragma unroll
-    for (int ks = 0; ks < 16; ++ks) {
+    for (int ks = 0; ks < kKs; ++ks) {
       const u32x4_t x = *reinterpret_cast<const u32x4_t*>(qrow + ks * 16);
       qreg[ks] = row_ok ? x : u32x4_t{0, 0, 0, 0};
     }
@@ -1434,10 +1445,10 @@ __global__ void __launch_bounds__(512, 1)
   };
   auto good_page = [&](int32_t id) { return id >= 0 && static_cast<uint64_t>(id) < kv.pool_pages; };
   // Element offsets inside a page: a row at in-page position `within` starts at row_mul * within + row_add.
-  const uint32_t row_mul = kv.hnd ? kPD : kv.kv_heads * kPD;
-  const uint32_t row_add = kv.hnd ? kvh * ps * kPD : kvh * kPD;
-  const uint64_t page_elems = static_cast<uint64_t>(ps) * kv.kv_heads * kPD;
-  // This wavefront's share of the copy of tile t: rows 8w .. 8w + 7 of K and of V (two rows per instruction).
+  const uint32_t row_mul = kv.hnd ? D : kv.kv_heads * D;
+  const uint32_t row_add = kv.hnd ? kvh * ps * D : kvh * D;
+  const uint64_t page_elems = static_cast<uint64_t>(ps) * kv.kv_heads * D;
+  // This wavefront's share of the copy of tile t: rows 8w .. 8w + 7 of K and of V (kRowsPerDma rows per instruction).
   auto issue = [&](int t, int buf, const int32_t (&ids)[4], int ln) {
     const int32_t kb = kbeg + 64 * t;
     const int32_t pos0 = kb + 8 * w;  // this wavefront's first row; all 8 lie in one page
@@ -1446,23 +1457,23 @@ __global__ void __launch_bounds__(512, 1)
     const int32_t page_first = min(pos0, kend - 1) & ~((1 << ps_shift) - 1);
     const uint16_t* kpage = kbase + pg * page_elems + row_add;
     const uint16_t* vpage = vbase + pg * page_elems + row_add;
-    const uint32_t kdst = LdsAddr(tiles[buf][0]) + 8 * w * 512, vdst = LdsAddr(tiles[buf][1]) + 8 * w * 512;
-    const int c = ln & 31, hh = (ln >> 5) & 1;
+    const uint32_t kdst = LdsAddr(tiles[buf][0]) + 8 * w * kRowB, vdst = LdsAddr(tiles[buf][1]) + 8 * w * kRowB;
+    const int c = ln % kPieces, hh = ln / kPieces;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int rr = 2 * i + hh;  // row 8w + rr of the tile
+    for (int i = 0; i < 8 / kRowsPerDma; ++i) {
+      const int rr = kRowsPerDma * i + hh;  // row 8w + rr of the tile
       const uint32_t within = static_cast<uint32_t>(min(pos0 + rr, kend - 1) - page_first);
       const uint32_t off = 2 * row_mul * within;
       const uint32_t kp = 16 * static_cast<uint32_t>(c ^ ((8 * w + rr) & 15));
       const uint32_t vp = 16 * static_cast<uint32_t>(c ^ ((rr & 3) << 2) ^ (((rr >> 2) & 1) << 3));
-      Dma16(kpage, off + kp, kdst + 2 * i * 512);
-      Dma16(vpage, off + vp, vdst + 2 * i * 512);
+      Dma16(kpage, off + kp, kdst + i * 1024);
+      Dma16(vpage, off + vp, vdst + i * 1024);
     }
   };
 
-  f32x16_t o[8];
+  f32x16_t o[kDt];
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
+  for (int dt = 0; dt < kDt; ++dt)
 #pragma unroll
     for (int v = 0; v < 16; ++v) o[dt][v] = 0.0f;
   float m_run = -INFINITY;
@@ -1493,15 +1504,15 @@ __global__ void __launch_bounds__(512, 1)
     const int32_t kb = kbeg + 64 * t;
     // K operand: row 32 half + lc, piece 2 ks + lh at position (2 ks + lh) ^ (lc & 15) (32 half keeps row & 15 =
     // lc & 15); in bytes 16 ((2 ks + lh) ^ (lc & 15)) = 32 ks ^ 16 (lh ^ (lc & 15)).
-    const int krow = lc * 512, kx = 16 * (lh ^ (lc & 15));
+    const int krow = lc * kRowB, kx = 16 * (lh ^ (lc & 15));
     // V^T operands, read transposed: in lane group g = ln / 16, lane j = ln % 16 addresses key +(j / 4) at dims
     // +4 (j % 4), keys based at 32 half + 16 c + 4 (g >> 1) (+8 for the operand's second half), dims at
-    // 32 dt + 16 (g & 1). With the swizzle that piece sits at byte key * 512 + (64 dt ^ vx) + the lane's offset inside
+    // 32 dt + 16 (g & 1). With the swizzle that piece sits at byte key * kRowB + (64 dt ^ vx) + the lane's offset inside
     // the 64-byte group, vx = 64 (key & 3) ^ 128 ((key >> 2) & 1) (key & 7 = vkey here).
     const int vj = ln & 15, vg = ln >> 4;
     const int vkey = 4 * (vg >> 1) + (vj >> 2);
     const int vdim = 16 * (vg & 1) + 4 * (vj & 3);
-    const int vrow = vkey * 512 + 16 * ((vdim >> 3) & 3) + 2 * (vdim & 7);
+    const int vrow = vkey * kRowB + 16 * ((vdim >> 3) & 3) + 2 * (vdim & 7);
     const int vx = (64 * (vkey & 3)) ^ (128 * ((vkey >> 2) & 1));
     const int32_t qpos = static_cast<int32_t>(kv_len) - n + wk.q0 + 32 * qt + lc;  // this lane's query position
     const bool need_mask = kb + 64 > kend || (causal && kb + 63 > last_pos - 31) || bad != 0 ||
@@ -1513,15 +1524,15 @@ __global__ void __launch_bounds__(512, 1)
       f32x16_t sc;
 #pragma unroll
       for (int v = 0; v < 16; ++v) sc[v] = 0.0f;
-      const unsigned char* krow_p = ktile + 32 * half * 512 + krow;
+      const unsigned char* krow_p = ktile + 32 * half * kRowB + krow;
       constexpr int kRing = 2;  // K operands in flight ahead of the multiply that uses them
       u32x4_t ka[kRing];
 #pragma unroll
       for (int j = 0; j < kRing; ++j) ka[j] = *reinterpret_cast<const u32x4_t*>(krow_p + ((32 * j) ^ kx));
 #pragma unroll
-      for (int ks = 0; ks < 16; ++ks) {
+      for (int ks = 0; ks < kKs; ++ks) {
         const u32x4_t a = ka[ks % kRing];
-        if (ks + kRing < 16) ka[ks % kRing] = *reinterpret_cast<const u32x4_t*>(krow_p + ((32 * (ks + kRing)) ^ kx));
+        if (ks + kRing < kKs) ka[ks % kRing] = *reinterpret_cast<const u32x4_t*>(krow_p + ((32 * (ks + kRing)) ^ kx));
         sc = Mfma32(a, qreg[ks], sc);
       }
       if (need_mask) {  // one uniform branch around branch-free selects
@@ -1545,7 +1556,7 @@ __global__ void __launch_bounds__(512, 1)
         const float corr = m_run == -INFINITY ? 0.0f : exp2f(m_run - m_new);
         l_run *= corr;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
+        for (int dt = 0; dt < kDt; ++dt)
 #pragma unroll
           for (int v = 0; v < 16; ++v) o[dt][v] *= corr;
         m_run = m_new;
@@ -1570,20 +1581,20 @@ __global__ void __launch_bounds__(512, 1)
       // V^T operands of the 16 multiplies (c, dt) in order, read kVRing ahead of use.
       constexpr int kVRing = 2;
       auto vread = [&](int j) {
-        const int c = j >> 3, dt = j & 7;
-        const uint32_t off = static_cast<uint32_t>((32 * half + 16 * c) * 512 + vrow) + ((64 * dt) ^ vx);
+        const int c = j / kDt, dt = j % kDt;
+        const uint32_t off = static_cast<uint32_t>((32 * half + 16 * c) * kRowB + vrow) + ((64 * dt) ^ vx);
         const u32x2_t lo = LdsTr16(vtile, off);
-        const u32x2_t hi = LdsTr16(vtile, off + 8 * 512);
+        const u32x2_t hi = LdsTr16(vtile, off + 8 * kRowB);
         return u32x4_t{lo[0], lo[1], hi[0], hi[1]};
       };
       u32x4_t va[kVRing];
 #pragma unroll
       for (int j = 0; j < kVRing; ++j) va[j] = vread(j);
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
+      for (int j = 0; j < 2 * kDt; ++j) {
         const u32x4_t av = va[j % kVRing];
-        if (j + kVRing < 16) va[j % kVRing] = vread(j + kVRing);
-        o[j & 7] = Mfma32(av, pb[j >> 3], o[j & 7]);
+        if (j + kVRing < 2 * kDt) va[j % kVRing] = vread(j + kVRing);
+        o[j % kDt] = Mfma32(av, pb[j / kDt], o[j % kDt]);
       }
     }
   }
@@ -1593,9 +1604,9 @@ __global__ void __launch_bounds__(512, 1)
   if (!row_ok) return;
   if (wk.slot >= 0) {
     const uint64_t prow = static_cast<uint64_t>(wk.slot) * kPfRows + static_cast<uint64_t>(r) * kGroup + hq;
-    float* po = part_o + prow * kPD;
+    float* po = part_o + prow * D;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
+    for (int dt = 0; dt < kDt; ++dt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int d = dt * 32 + i * 8 + hl * 4;
@@ -1608,9 +1619,9 @@ __global__ void __launch_bounds__(512, 1)
     return;
   }
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  const uint64_t orow = (static_cast<uint64_t>(qbeg + wk.q0 + r) * q_heads + head) * kPD;
+  const uint64_t orow = (static_cast<uint64_t>(qbeg + wk.q0 + r) * q_heads + head) * D;
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
+  for (int dt = 0; dt < kDt; ++dt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int d = dt * 32 + i * 8 + hl * 4;
@@ -1623,8 +1634,9 @@ __global__ void __launch_bounds__(512, 1)
   }
 }
 
-// Combines the pieces of a split prefill item: block (merge, token); thread t handles query head t / 64, dims
-// 4 (t % 64) .. +3.
+// Combines the pieces of a split prefill item: block (merge, token) of D threads; thread t handles query head
+// t / (D / 4), dims 4 (t % (D / 4)) .. +3.
+template <int D>
 __global__ void __launch_bounds__(256)
     PrefillMergeKernel(uint16_t* __restrict__ out, float* __restrict__ lse, const PrefillMerge* __restrict__ merges,
                        const float* __restrict__ part_o, const float* __restrict__ part_ml,
@@ -1632,8 +1644,8 @@ __global__ void __launch_bounds__(256)
   const PrefillMerge mg = merges[blockIdx.x];
   const int r = blockIdx.y;
   if (r >= mg.rows) return;
-  const int hq = threadIdx.x >> 6;
-  const int d = 4 * (threadIdx.x & 63);
+  const int hq = threadIdx.x / (D / 4);
+  const int d = 4 * (threadIdx.x % (D / 4));
   const uint64_t token = static_cast<uint64_t>(q_indptr[mg.seq] + mg.q0 + r);
   const uint64_t row = static_cast<uint64_t>(r) * kGroup + hq;
   float mx = -INFINITY;
@@ -1646,7 +1658,7 @@ __global__ void __launch_bounds__(256)
       const float m = part_ml[2 * prow];
       const float f = m == -INFINITY ? 0.0f : exp2f(m - mx);
       l += part_ml[2 * prow + 1] * f;
-      const float4 o = *reinterpret_cast<const float4*>(part_o + prow * kPD + d);
+      const float4 o = *reinterpret_cast<const float4*>(part_o + prow * D + d);
       acc.x = fmaf(o.x, f, acc.x);
       acc.y = fmaf(o.y, f, acc.y);
       acc.z = fmaf(o.z, f, acc.z);
@@ -1656,7 +1668,7 @@ __global__ void __launch_bounds__(256)
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
   const uint32_t head = mg.kv_head * kGroup + hq;
   const u32x2_t v{PackBf16(acc.x * inv, acc.y * inv), PackBf16(acc.z * inv, acc.w * inv)};
-  *reinterpret_cast<u32x2_t*>(out + (token * q_heads + head) * kPD + d) = v;
+  *reinterpret_cast<u32x2_t*>(out + (token * q_heads + head) * D + d) = v;
   if (lse != nullptr && d == 0) lse[token * q_heads + head] = l > 0.0f ? mx + log2f(l) : -INFINITY;
 }
 
@@ -1702,16 +1714,28 @@ RoostStatus LaunchPrefill(const RoostPagedAttentionParams& p, const PlanRecord& 
   auto* lsep = static_cast<float*>(p.lse.address);
   if (PrefillFastPath(p)) {
     auto* part_o = reinterpret_cast<float*>(dev + rec.float_offset);
-    auto* part_ml = part_o + rec.splits * kPfRows * kPD;
-    hipLaunchKernelGGL(PrefillTileKernel, dim3(static_cast<uint32_t>(rec.work_items)), dim3(512), 0, stream,
-                       static_cast<const uint16_t*>(p.q.address), outp, lsep, kv, kv.kv_indices, q_indptr, items,
-                       part_o, part_ml, p.q_heads, p.causal, static_cast<uint32_t>(__builtin_ctz(p.page_size)),
-                       scale_log2, WindowOf(p));
+    auto* part_ml = part_o + rec.splits * kPfRows * p.head_dim;
+    const dim3 grid(static_cast<uint32_t>(rec.work_items));
+    const auto* q16 = static_cast<const uint16_t*>(p.q.address);
+    const uint32_t ps_shift = static_cast<uint32_t>(__builtin_ctz(p.page_size));
+    if (p.head_dim == 128) {
+      hipLaunchKernelGGL(PrefillTileKernel<128>, grid, dim3(512), 0, stream, q16, outp, lsep, kv, kv.kv_indices,
+                         q_indptr, items, part_o, part_ml, p.q_heads, p.causal, ps_shift, scale_log2, WindowOf(p));
+    } else {
+      hipLaunchKernelGGL(PrefillTileKernel<256>, grid, dim3(512), 0, stream, q16, outp, lsep, kv, kv.kv_indices,
+                         q_indptr, items, part_o, part_ml, p.q_heads, p.causal, ps_shift, scale_log2, WindowOf(p));
+    }
     ROOST_TRY(FromHip(hipGetLastError(), "PagedAttention prefill launch"));
     if (rec.merges == 0) return ROOST_STATUS_OK;
-    hipLaunchKernelGGL(PrefillMergeKernel, dim3(static_cast<uint32_t>(rec.merges), kPfTokens), dim3(kPD), 0, stream, outp,
-                       lsep, reinterpret_cast<const PrefillMerge*>(dev + rec.merge_offset), part_o, part_ml, q_indptr,
-                       p.q_heads);
+    const dim3 mgrid(static_cast<uint32_t>(rec.merges), kPfTokens);
+    const auto* mg = reinterpret_cast<const PrefillMerge*>(dev + rec.merge_offset);
+    if (p.head_dim == 128) {
+      hipLaunchKernelGGL(PrefillMergeKernel<128>, mgrid, dim3(kGroup * 128 / 4), 0, stream, outp, lsep, mg, part_o,
+                         part_ml, q_indptr, p.q_heads);
+    } else {
+      hipLaunchKernelGGL(PrefillMergeKernel<256>, mgrid, dim3(kGroup * 256 / 4), 0, stream, outp, lsep, mg, part_o,
+                         part_ml, q_indptr, p.q_heads);
+    }
     return FromHip(hipGetLastError(), "PagedAttention prefill merge launch");
   }
   hipLaunchKernelGGL(PrefillKernel, dim3(static_cast<uint32_t>(rec.work_items)), dim3(256), 0, stream,
@@ -1850,6 +1874,7 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_run(RoostContext*, const 
     // 256 in prefill mode). Running the two side by side on two streams gains nothing: a tile workgroup needs two
     // 256-register wavefronts per SIMD, so it cannot share a CU with resident decode workgroups.
     ROOST_TRY(LaunchPrefill(p, rec, dev, kv, scale_log2, s));
-    return LaunchDecode<uint16_t, 256>(p, rec, dev, kv, scale_log2, s);
+    return p.head_dim == 128 ? LaunchDecode<uint16_t, 128>(p, rec, dev, kv, scale_log2, s)
+                             : LaunchDecode<uint16_t, 256>(p, rec, dev, kv, scale_log2, s);
   });
 }

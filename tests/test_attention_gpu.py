@@ -460,3 +460,34 @@ def test_sliding_window_plan_must_match_run(session):
     ws = session._ws[(entry.variant_id, "window")][3]
     d.window_left = -1
     assert session.run_raw(entry, d.params(), ws) == abi.INVALID_ARGUMENT
+
+
+# ---- Prefill at head_dim 128 (the tile kernel templated on the head dim; decode already serves 64/128/256) ---------
+
+HD128_PREFILL_CASES = [
+    ("hd128 fresh-300", [(300, 300)], 16, False, True, -1),
+    ("hd128 chunk-128-of-1000 HND ps32", [(128, 1000)], 32, True, True, -1),
+    ("hd128 chunk-512-of-4000 split", [(512, 4000), (3, 3)], 16, False, True, -1),
+    ("hd128 mixed step", [(1, 900), (1, 17), (200, 1200), (1, 3000), (64, 64)], 64, False, True, -1),
+    ("hd128 non-causal-32-of-200", [(32, 200)], 16, False, False, -1),
+    ("hd128 window 100", [(700, 700), (40, 900)], 16, False, True, 100),
+]
+
+
+@pytest.mark.parametrize("name,seqs,ps,hnd,causal,window", HD128_PREFILL_CASES, ids=[c[0] for c in HD128_PREFILL_CASES])
+def test_prefill_head_dim_128(session, name, seqs, ps, hnd, causal, window):
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    b = cases.make_paged_batch(rng, [s[1] for s in seqs], [s[0] for s in seqs], page_size=ps, hnd=hnd, d=128)
+    got = run_case(session, b, causal=causal, window_left=window)
+    check_against_oracle(got, b, causal=causal, window_left=window)
+
+
+def test_prefill_head_dim_128_needs_a_dma_page_size(session):
+    """Head dim 128 prefill is built on the DMA-fed tile kernel only: page sizes that are powers of two and multiples
+    of 16. Page size 8 is refused as UNSUPPORTED before any launch."""
+    rng = np.random.default_rng(5)
+    b = cases.make_paged_batch(rng, [100], [50], page_size=8, d=128)
+    d = Dev(b)
+    entry = session.lib.entry(roost_amd.ATTENTION_VARIANT)
+    sizes = abi.new(abi.WorkspaceSizes)
+    assert entry.workspace(session.ctx, C.addressof(d.params()), C.addressof(sizes)) == abi.UNSUPPORTED
