@@ -143,6 +143,15 @@ struct Layout {
 
 // ---- Validation (reference: kernels/src/paged_attention.cu:78-130) ------------------------------------------------
 
+// Query heads per KV head the kernels serve: groups of kGroup = 4, or 8, 16 and 32 as 2, 4 and 8 groups of 4 that read
+// the same KV rows (the reference builds 4 only).
+bool GroupBuilt(uint32_t g) { return g == 4 || g == 8 || g == 16 || g == 32; }
+// Groups of kGroup query heads ("virtual" KV heads) and the log2 of how many of them share one real KV head.
+uint32_t VirtualHeads(const RoostPagedAttentionParams& p) { return p.q_heads / kGroup; }
+uint32_t HeadShift(const RoostPagedAttentionParams& p) {
+  return static_cast<uint32_t>(__builtin_ctz(p.q_heads / (p.kv_heads * kGroup)));
+}
+
 RoostStatus Validate(const RoostPagedAttentionParams& p, bool for_run) {
   using roost::Fail;
   constexpr char kOp[] = "PagedAttention";
@@ -158,8 +167,8 @@ RoostStatus Validate(const RoostPagedAttentionParams& p, bool for_run) {
                 "PagedAttention: prefill is built for head_dim 256, and for 128 with page sizes that are powers of two "
                 "and multiples of 16");
   }
-  if (p.kv_heads == 0 || p.q_heads != p.kv_heads * kGroup) {
-    return Fail(ROOST_STATUS_UNSUPPORTED, "PagedAttention: only 4 query heads per KV head are built");
+  if (p.kv_heads == 0 || p.q_heads % p.kv_heads != 0 || !GroupBuilt(p.q_heads / p.kv_heads)) {
+    return Fail(ROOST_STATUS_UNSUPPORTED, "PagedAttention: 4, 8, 16 or 32 query heads per KV head are built");
   }
   if (p.window_left == 0) {
     // CpuOps refuses a window of 0 (reference CpuOps.cs:180-186): bind -1 for no window.
@@ -301,7 +310,7 @@ DecodePlan BuildDecode(const RoostPagedAttentionParams& p, uint32_t cus, Take ta
   }
   if (planned == 0) return d;
   const uint64_t slots_wanted = std::max<uint64_t>(
-      1, static_cast<uint64_t>(cus) * kDecodeWgsPerCu / (p.kv_heads / HeadsPerWorkgroup(p.kv_heads)));
+      1, static_cast<uint64_t>(cus) * kDecodeWgsPerCu / (VirtualHeads(p) / HeadsPerWorkgroup(VirtualHeads(p))));
   const uint64_t ranges = std::max<uint64_t>(1, std::min<uint64_t>(slots_wanted, total));
   uint64_t per_range = std::max<uint64_t>(1, roost::CeilDiv(total, ranges));
   // A sequence spans at most ceil(groups / per_range) + 1 pieces; keep that within what the merge kernel combines.
@@ -419,8 +428,8 @@ Layout PlanPrefill(const RoostPagedAttentionParams& p, uint32_t cus, unsigned ch
       // never read.
       int64_t kbeg = window < 0 ? 0 : std::max<int64_t>(0, kv - n + q0 - window) / 16 * 16;
       if (kbeg > kend) kbeg = kend;
-      total_tiles += roost::CeilDiv(kend - kbeg, 64) * p.kv_heads;
-      for (uint32_t h = 0; h < p.kv_heads; ++h) {
+      total_tiles += roost::CeilDiv(kend - kbeg, 64) * VirtualHeads(p);
+      for (uint32_t h = 0; h < VirtualHeads(p); ++h) {  // item per group of kGroup query heads
         items.push_back(Item{PrefillWork{static_cast<int32_t>(b), static_cast<int32_t>(q0), static_cast<int32_t>(h),
                                          static_cast<int32_t>(rows), static_cast<int32_t>(kbeg),
                                          static_cast<int32_t>(kend), -1, 0},
@@ -483,8 +492,11 @@ struct KvView {
   const int32_t* last_len;
   uint64_t pool_pages;  // pages the pools hold; page ids outside [0, pool_pages) are skipped
   uint32_t page_size;
-  uint32_t kv_heads;
+  uint32_t kv_heads;    // real KV heads of the pools (their row strides)
   uint32_t hnd;
+  uint32_t head_shift;  // the kernels work on groups of kGroup query heads ("virtual" KV heads, q_heads / kGroup of
+                        // them); virtual head v reads the K/V rows of real head v >> head_shift
+  uint32_t vheads;      // q_heads / kGroup
 };
 
 __device__ __forceinline__ uint32_t SeqKvLen(const KvView& kv, int32_t b, int32_t* p0) {
@@ -507,7 +519,8 @@ __device__ __forceinline__ int64_t KeyRow(const KvView& kv, int32_t p0, uint32_t
   const int32_t page = kv.kv_indices[p0 + pi];
   if (page < 0 || static_cast<uint64_t>(page) >= kv.pool_pages) return -1;
   const uint64_t pg = static_cast<uint64_t>(page);
-  const uint64_t row = kv.hnd ? (pg * kv.kv_heads + h) * kv.page_size + off : (pg * kv.page_size + off) * kv.kv_heads + h;
+  const uint32_t hr = h >> kv.head_shift;
+  const uint64_t row = kv.hnd ? (pg * kv.kv_heads + hr) * kv.page_size + off : (pg * kv.page_size + off) * kv.kv_heads + hr;
   return static_cast<int64_t>(row * D);
 }
 
@@ -523,7 +536,8 @@ __device__ __forceinline__ uint64_t KeyRowSafe(const KvView& kv, int32_t p0, int
   const bool good = j < key_end && page >= 0 && static_cast<uint64_t>(page) < kv.pool_pages;
   *ok = good;
   const uint64_t pg = good ? static_cast<uint64_t>(page) : 0;
-  const uint64_t row = kv.hnd ? (pg * kv.kv_heads + h) * kv.page_size + off : (pg * kv.page_size + off) * kv.kv_heads + h;
+  const uint32_t hr = h >> kv.head_shift;
+  const uint64_t row = kv.hnd ? (pg * kv.kv_heads + hr) * kv.page_size + off : (pg * kv.page_size + off) * kv.kv_heads + hr;
   return good ? row * D : 0;
 }
 
@@ -844,7 +858,7 @@ __global__ void __launch_bounds__(256, ROOST_DECODE_WGS_PER_CU) DecodeKernel(con
   // Both KV heads of a range are adjacent in launch order, so the two halves of each NHD page row are read together.
   // A workgroup serves heads_per_wg (1, 2 or 4) KV heads of one range, 4 / heads_per_wg wavefronts per head, so the
   // KV heads of each page row (adjacent in an NHD pool) are read by one CU at the same time.
-  const uint32_t hblocks = kv.kv_heads / heads_per_wg;
+  const uint32_t hblocks = kv.vheads / heads_per_wg;
   const uint32_t range = blockIdx.x / hblocks;
   const int lane = threadIdx.x & 63;
   // The wavefront index is uniform within a wavefront; saying so lets the group's page id be a scalar load.
@@ -921,8 +935,9 @@ __global__ void __launch_bounds__(256, ROOST_DECODE_WGS_PER_CU) DecodeKernel(con
       const int32_t page = kv_indices[p0 + pi];  // uniform address: a scalar load
       const bool page_ok = page >= 0 && static_cast<uint64_t>(page) < kv.pool_pages;
       const uint64_t pg = page_ok ? static_cast<uint64_t>(page) : 0;
-      const uint64_t row0 = kv.hnd ? (pg * kv.kv_heads + kvh) * kv.page_size + off0
-                                   : (pg * kv.page_size + off0) * kv.kv_heads + kvh;
+      const uint32_t kvr = kvh >> kv.head_shift;  // the real KV head this group of query heads reads
+      const uint64_t row0 = kv.hnd ? (pg * kv.kv_heads + kvr) * kv.page_size + off0
+                                   : (pg * kv.page_size + off0) * kv.kv_heads + kvr;
       const char* kg = reinterpret_cast<const char*>(kbase + row0 * D);
       const char* vg = reinterpret_cast<const char*>(vbase + row0 * D);
 #pragma unroll
@@ -1446,7 +1461,8 @@ __global__ void __launch_bounds__(512, 1)
   auto good_page = [&](int32_t id) { return id >= 0 && static_cast<uint64_t>(id) < kv.pool_pages; };
   // Element offsets inside a page: a row at in-page position `within` starts at row_mul * within + row_add.
   const uint32_t row_mul = kv.hnd ? D : kv.kv_heads * D;
-  const uint32_t row_add = kv.hnd ? kvh * ps * D : kvh * D;
+  const uint32_t kvr = kvh >> kv.head_shift;  // the real KV head the item's query heads read
+  const uint32_t row_add = kv.hnd ? kvr * ps * D : kvr * D;
   const uint64_t page_elems = static_cast<uint64_t>(ps) * kv.kv_heads * D;
   // This wavefront's share of the copy of tile t: rows 8w .. 8w + 7 of K and of V (kRowsPerDma rows per instruction).
   auto issue = [&](int t, int buf, const int32_t (&ids)[4], int ln) {
@@ -1686,8 +1702,8 @@ RoostStatus LaunchDecode(const RoostPagedAttentionParams& p, const PlanRecord& r
       p.mode == ROOST_ATTENTION_PREFILL ? static_cast<const int32_t*>(p.q_indptr.address) : nullptr;
   auto* out = static_cast<T*>(p.output.address);
   auto* lse = static_cast<float*>(p.lse.address);
-  const uint32_t hpw = HeadsPerWorkgroup(p.kv_heads);
-  const dim3 grid(static_cast<uint32_t>(rec.dec_ranges * (p.kv_heads / hpw)));
+  const uint32_t hpw = HeadsPerWorkgroup(VirtualHeads(p));
+  const dim3 grid(static_cast<uint32_t>(rec.dec_ranges * (VirtualHeads(p) / hpw)));
   if (p.page_size % 16 == 0) {
     hipLaunchKernelGGL((DecodeKernel<T, D, true>), grid, dim3(256), 0, stream, static_cast<const T*>(p.q.address), out,
                        lse, kv, kv.kv_indices, items, range_ptr, part_o, part_ml, q_rows, p.q_heads, hpw, scale_log2,
@@ -1856,6 +1872,8 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_run(RoostContext*, const 
     kv.pool_pages = std::min(p.k_cache.length, p.v_cache.length) / page_elems;
     kv.page_size = p.page_size;
     kv.kv_heads = p.kv_heads;
+    kv.head_shift = HeadShift(p);
+    kv.vheads = VirtualHeads(p);
     kv.hnd = p.kv_layout == ROOST_LAYOUT_PAGED_HND ? 1u : 0u;
     auto* dev = static_cast<unsigned char*>(ws->device);
     hipStream_t s = Stream(stream);

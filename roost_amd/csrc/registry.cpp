@@ -68,7 +68,8 @@ using roost::DtypeBit;
 constexpr uint64_t HeadDimBit(uint32_t d) { return uint64_t{1} << (d / 16 - 1); }
 constexpr uint32_t kPaged = (1u << ROOST_LAYOUT_PAGED_NHD) | (1u << ROOST_LAYOUT_PAGED_HND);
 constexpr uint32_t kAnyPageSize = 0xFFu;  // bit i = page size 2^i: 1 .. 128 tokens
-constexpr uint32_t kGroup4 = 1u << 3;     // 4 query heads per KV head
+constexpr uint32_t kGroup4 = 1u << 3;     // 4 query heads per KV head (bit g - 1: group size g)
+constexpr uint32_t kGroups = kGroup4 | (1u << 7) | (1u << 15) | (1u << 31);  // 4, 8, 16 and 32
 
 RoostConstraints BaseConstraints() {
   RoostConstraints c{};
@@ -84,7 +85,7 @@ RoostConstraints AttentionConstraints() {
   c.layout_mask = kPaged;
   c.page_size_mask = kAnyPageSize;
   c.min_alignment = 16;
-  c.group_size_mask = kGroup4;
+  c.group_size_mask = kGroups;
   return c;
 }
 

@@ -98,7 +98,7 @@ def test_abi_version_and_table(kernels):
         assert e.constraints.sm_min == 950
     att = ids[roost_amd.ATTENTION_VARIANT]
     assert att.op == abi.OP_PAGED_ATTENTION and att.needs_plan and att.params_struct_size == 296
-    assert att.constraints.sm_min == 950 and att.constraints.group_size_mask == 1 << 3
+    assert att.constraints.sm_min == 950 and att.constraints.group_size_mask == (1 << 3) | (1 << 7) | (1 << 15) | (1 << 31)
     assert att.constraints.head_dim_mask & (1 << (256 // 16 - 1))
     cw = ids[roost_amd.CACHE_WRITE_VARIANT]
     assert cw.op == abi.OP_CACHE_WRITE and cw.plan is None and cw.params_struct_size == 160
@@ -156,7 +156,7 @@ def test_attention_refusals_without_gpu(kernels):
     ctx = kernels.create_context(0)
     run = lambda q: e.run(ctx, C.addressof(q), None, None)  # noqa: E731
     assert run(p) == abi.NOT_PLANNED  # valid params, no plan record
-    for field, value, want in [("head_dim", 96, abi.UNSUPPORTED), ("q_heads", 16, abi.UNSUPPORTED),
+    for field, value, want in [("head_dim", 96, abi.UNSUPPORTED), ("q_heads", 12, abi.UNSUPPORTED),
                                ("window_left", 0, abi.INVALID_ARGUMENT), ("logits_soft_cap", 30.0, abi.UNSUPPORTED),
                                ("tokens", 3, abi.INVALID_ARGUMENT), ("mode", 7, abi.INVALID_ARGUMENT),
                                ("kv_layout", 0, abi.INVALID_ARGUMENT), ("batch", 0, abi.INVALID_ARGUMENT),

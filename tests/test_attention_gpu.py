@@ -352,7 +352,7 @@ def test_rejections(session):
         return session.run_raw(entry, d.params(**over), ws)
 
     assert status(head_dim=96) == abi.UNSUPPORTED
-    assert status(q_heads=16) == abi.UNSUPPORTED
+    assert status(q_heads=12) == abi.UNSUPPORTED  # a group of 6 (4, 8, 16 and 32 are built)
     assert status(window_left=0) == abi.INVALID_ARGUMENT  # CpuOps refuses a window of 0; -1 means none
     assert status(soft_cap=30.0) == abi.UNSUPPORTED
     p = d.params()
@@ -491,3 +491,27 @@ def test_prefill_head_dim_128_needs_a_dma_page_size(session):
     entry = session.lib.entry(roost_amd.ATTENTION_VARIANT)
     sizes = abi.new(abi.WorkspaceSizes)
     assert entry.workspace(session.ctx, C.addressof(d.params()), C.addressof(sizes)) == abi.UNSUPPORTED
+
+
+# ---- Groups of 8, 16 and 32 query heads per KV head: 2, 4 or 8 groups of 4 reading the same KV rows -----------------
+
+GROUP_CASES = [
+    ("decode group 8", "decode", [900, 17, 1, 2048, 333, 64], 16, False, 16, 2, 256),
+    ("decode group 16 HND ps64", "decode", [900, 17, 2048, 64], 64, True, 32, 2, 128),
+    ("decode group 8 ps7 general pages", "decode", [5, 37, 130, 1000], 7, False, 8, 1, 128),
+    ("prefill group 8", "prefill", [(300, 300), (64, 700)], 16, False, 16, 2, 256),
+    ("prefill group 32 hd128", "prefill", [(200, 1200)], 32, False, 32, 1, 128),
+    ("prefill group 8 mixed step", "prefill", [(1, 900), (130, 700), (1, 40)], 16, False, 16, 2, 256),
+]
+
+
+@pytest.mark.parametrize("name,mode,lens,ps,hnd,hq,hkv,d", GROUP_CASES, ids=[c[0] for c in GROUP_CASES])
+def test_query_head_groups(session, name, mode, lens, ps, hnd, hq, hkv, d):
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    if mode == "decode":
+        b = cases.make_paged_batch(rng, lens, [1] * len(lens), page_size=ps, hnd=hnd, hq=hq, hkv=hkv, d=d)
+    else:
+        b = cases.make_paged_batch(rng, [s[1] for s in lens], [s[0] for s in lens], page_size=ps, hnd=hnd, hq=hq,
+                                   hkv=hkv, d=d)
+    got = run_case(session, b)
+    check_against_oracle(got, b)
