@@ -364,6 +364,40 @@ def bench_attention_input(torch, roost_amd, session, steps, warmup):
     return res
 
 
+def bench_dense_vs_sdpa(torch, roost_amd, session, steps, warmup):
+    """A dense-equivalent causal prefill (4 fresh sequences of 4096 tokens, 8 query / 2 KV heads, head dims 256 and
+    128) through this library's paged kernels, beside torch's own scaled_dot_product_attention (the ROCm build's flash
+    backend) on the same shape with contiguous K/V -- the platform's stock attention as a point of comparison."""
+    import torch.nn.functional as F
+
+    res = {}
+    for d in (256, 128):
+        rng = np.random.default_rng(1)
+        b = Paged(torch, rng, [4096] * 4, [4096] * 4, d=d)
+        entry = session.lib.entry(roost_amd.ATTENTION_VARIANT)
+        p = b.params(roost_amd)
+        ws, _ = planned(session, entry, p, f"bench-dense-{d}")
+        ms = time_runs(torch, session, entry, p, ws, max(steps // 4, 3), 2)
+        flops = b.prefill_flops()
+        q = torch.randn(4, 8, 4096, d, device="cuda", dtype=torch.bfloat16) * 0.5
+        k = torch.randn(4, 2, 4096, d, device="cuda", dtype=torch.bfloat16) * 0.5
+        v = torch.randn(4, 2, 4096, d, device="cuda", dtype=torch.bfloat16) * 0.5
+        sdpa = lambda: F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True)  # noqa: E731
+        for _ in range(2):
+            sdpa()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(5):
+            sdpa()
+        e1.record()
+        torch.cuda.synchronize()
+        sdpa_ms = e0.elapsed_time(e1) / 5
+        res[f"head_dim_{d}"] = {"ms": ms, "tflops": flops / ms / 1e9, "frac": flops / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS,
+                                "torch_sdpa_ms": sdpa_ms, "torch_sdpa_tflops": flops / sdpa_ms / 1e9}
+    return res
+
+
 def cpu_baseline(b: Paged, sample_seqs: int):
     """CpuOps oracle (single thread, double precision, the C restatement of CpuOps.PagedAttention) on the first
     `sample_seqs` sequences of the decode batch; reported in the headline's unit (algorithmic GB/s)."""
@@ -409,7 +443,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=16)
-    ap.add_argument("--only", choices=["decode", "prefill", "prefill128", "gdn", "mixed", "layer", "attn_in"], default=None,
+    ap.add_argument("--only", choices=["decode", "prefill", "prefill128", "dense", "gdn", "mixed", "layer", "attn_in"], default=None,
                     help="run one workload only and print its timing (for profiler passes); no JSON line")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -428,7 +462,7 @@ def main():
     if args.only is not None:
         fn = {"decode": bench_decode, "prefill": bench_prefill, "gdn": bench_gdn, "mixed": bench_mixed,
               "layer": bench_layer_ops, "attn_in": bench_attention_input,
-              "prefill128": lambda *a: bench_prefill(*a, d=128)}[args.only]
+              "prefill128": lambda *a: bench_prefill(*a, d=128), "dense": bench_dense_vs_sdpa}[args.only]
         res = fn(torch, roost_amd, session, args.steps, args.warmup)
         log(f"{args.only}: {res[1] if isinstance(res, tuple) else res} ms")
         session.close()
@@ -445,6 +479,8 @@ def main():
     _, pre128_ms, _ = bench_prefill(torch, roost_amd, session, args.steps, args.warmup, d=128)
     pre128_flops = pb.prefill_flops() / 2
     log(f"  head dim 128: {pre128_ms * 1e3:.1f} us/step, {pre128_flops / pre128_ms / 1e9:.0f} TFLOP/s")
+    dense = bench_dense_vs_sdpa(torch, roost_amd, session, args.steps, args.warmup)
+    log(f"  dense 4 x 4096 vs torch SDPA: {json.dumps(_rounded(dense))}")
     log("gdn (config 4) ...")
     gdn = bench_gdn(torch, roost_amd, session, args.steps, args.warmup)
     log(f"  {json.dumps(gdn)}")
@@ -488,7 +524,8 @@ def main():
                     "query_tokens": pb.tokens,
                     "head_dim_128": {"ms": round(pre128_ms, 4), "tflops": round(pre128_flops / pre128_ms / 1e9, 1),
                                      "frac": round(pre128_flops / pre128_ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
-                                     "note": "the same draw at head dim 128 (not a BASELINE config)"}},
+                                     "note": "the same draw at head dim 128 (not a BASELINE config)"},
+                    "dense_4x4096_vs_torch_sdpa": _rounded(dense)},
         "gdn": {k: _rounded(v) for k, v in gdn.items()},
         "mixed_step": _rounded(mixed),
         "gdn_layer_ops": {k: _rounded(v) for k, v in layer.items()},
