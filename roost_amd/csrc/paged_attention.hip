@@ -598,6 +598,17 @@ __device__ __forceinline__ float Dot16(const uint4& k, const float* q, float acc
 
 __device__ __forceinline__ float ShflXor(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
+// A lane's value combined with that of lane ^ 32 through v_permlane32_swap (registers only, no LDS round trip): the
+// swap leaves each lane holding both values, so max and sum need no select and both lanes get the same bits.
+__device__ __forceinline__ float MaxXor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float SumXor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // x[i] for a runtime i in [0, 4) without indexing a register array (which would spill it to scratch).
 __device__ __forceinline__ float Pick4(const float* x, int i) {
   return i == 0 ? x[0] : (i == 1 ? x[1] : (i == 2 ? x[2] : x[3]));
@@ -766,7 +777,7 @@ __device__ __forceinline__ void DecodeGroupMfma(DecodeState<uint16_t, D>& st, co
     mx = fmaxf(mx, sc[j]);
   }
   mx = fmaxf(mx, ShflXor(mx, 16));
-  mx = fmaxf(mx, ShflXor(mx, 32));
+  mx = MaxXor32(mx);
   float corr[kGroup];
   bool rescale = false;
 #pragma unroll
@@ -1278,7 +1289,7 @@ __global__ void __launch_bounds__(256, 1)
         s[kt][v] = x;
         mx = fmaxf(mx, x);
       }
-    mx = fmaxf(mx, ShflXor(mx, 32));
+    mx = MaxXor32(mx);
     // Lazy rescaling: the running max only moves when a score exceeds it by more than 2^8, so P stays below 256 (safe
     // in fp32 and bf16) and the O accumulators are rescaled on a handful of tiles instead of every tile.
     const bool grow = mx > m_run + 8.0f;
@@ -1324,7 +1335,7 @@ __global__ void __launch_bounds__(256, 1)
   }
 
   // Normalise and write: lane holds dims dt*32 + 8i + 4hl + jj of query col.
-  const float l_tot = l_run + ShflXor(l_run, 32);
+  const float l_tot = SumXor32(l_run);
   if (col < rows) {
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     const uint64_t orow = (static_cast<uint64_t>(qbeg + q0 + col) * q_heads + head) * kPD;
@@ -1347,21 +1358,23 @@ __global__ void __launch_bounds__(256, 1)
 //
 // One workgroup = 64 query tokens x the 4 query heads of one KV head, 8 wavefronts (two per SIMD, so one wavefront's
 // softmax runs under the other's MFMAs): wavefront w is query head 4 kvh + (w & 3) for tokens 32 (w >> 2) .. +31.
-// Per 64-key tile each wavefront copies 8 K rows and 8 V rows (inside one page: 16-aligned groups of rows never
-// straddle a page when the page size is a multiple of 16) from the paged cache straight into LDS with
-// global_load_lds, double-buffered, so the copy of tile t + 1 runs under the products of tile t. The tile is consumed
-// in two 32-key halves:
+// Per 64-key tile each wavefront copies 8 K rows and a quarter of the V tile (16-aligned groups of rows never straddle
+// a page when the page size is a multiple of 16) from the paged cache straight into LDS with global_load_lds,
+// double-buffered, so the copy of tile t + 1 runs under the products of tile t. The tile is consumed in two 32-key
+// halves:
 //   S^T = K Q^T  (v_mfma_f32_32x32x16_bf16; K rows from LDS as the A operand, Q^T held in registers as B),
 //   online softmax per query (lane pair l, l ^ 32 holds one query's 32 scores; lazy rescaling: the running max only
 //   moves when a score exceeds it by more than 2^8, so P stays below 256),
-//   O^T += V^T P^T (V^T operands read from the row-major V tile with ds_read_b64_tr_b16, P^T from registers).
+//   O^T += V^T P^T (V^T operands read from the V tile with ds_read_b64_tr_b16, P^T from registers).
 // ds_read_b64_tr_b16 works within groups of 16 lanes: output lane 4a + b, element e, is element b of the 8 bytes that
 // lane 4e + a addressed. So when lane 4e + a of a group addresses keys k0 + e, dims d0 + 4a .. +3, output lane j of the
 // group receives V[k0 + e][d0 + j], e = 0..3: a V^T operand row.
-// LDS rows are 512 bytes with 16-byte pieces at swizzled positions: K piece p of row r at p ^ (r & 15) (the A-operand
-// reads of 16 consecutive rows hit 16 distinct bank groups), V piece p at p ^ 4 (r & 3) ^ 8 ((r >> 2) & 1) (the
-// transposed reads of 4 consecutive rows, 32 bytes each, hit distinct banks, and the wavefront's two 4-row sets land
-// 128 bytes apart: measured 2.6 cycles per read instruction against 3.1 without the second term).
+// K rows are 512 bytes in LDS with 16-byte pieces at swizzled positions: piece p of row r at p ^ (r & 15) (the A-operand
+// reads of 16 consecutive rows hit 16 distinct bank groups). The V tile is stored in the order the transposed reads
+// consume it: 1 KB block (c16, dt) holds keys 16 c16 .. +15 x dims 32 dt .. +31, each read instruction takes one
+// contiguous 512-byte half of a block (conflict-free, and every read is one base register plus an immediate). Each
+// copy instruction then fetches 16 rows x 64 bytes; storing K the same way (32 rows x 32 bytes per copy) was measured
+// 8% slower overall, the copy's wider spread of cache lines costing more than the cheaper reads gain.
 
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) unsigned char lds_byte_t;
@@ -1383,6 +1396,23 @@ __device__ __forceinline__ void Dma16(const void* sbase, uint32_t voff, uint32_t
   uint32_t save;
   asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
                : "=&s"(save) : "v"(voff), "s"(sbase), "s"(lds));
+}
+
+// Both copies again with an immediate byte offset kOff (below 4096) on the global address. The instruction adds its
+// offset to the LDS address as well, so M0 is set to lds - kOff and the 16 bytes of lane l still land at lds + 16 l.
+template <int kOff>
+__device__ __forceinline__ void Dma16At(const void* sbase, uint32_t voff, uint32_t lds) {
+  uint32_t save;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\tglobal_load_lds_dwordx4 %1, %2 offset:%4\n\ts_mov_b32 m0, %0"
+               : "=&s"(save) : "v"(voff), "s"(sbase), "s"(lds - kOff), "i"(kOff));
+}
+
+template <int kN, typename F>
+__device__ __forceinline__ void StaticFor(F&& f) {
+  if constexpr (kN > 0) {
+    StaticFor<kN - 1>(f);
+    f(std::integral_constant<int, kN - 1>{});
+  }
 }
 
 __device__ __forceinline__ void WaitVmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0) only
@@ -1414,6 +1444,7 @@ __global__ void __launch_bounds__(512, 1)
   constexpr int kKs = D / 16;                   // K = 16 steps of S^T = K Q^T
   constexpr int kDt = D / 32;                   // 32-dim blocks of O^T
   constexpr int kTileBytes = kPrefillTileK * kRowB;  // one 64-key K or V tile
+  constexpr int kNv = kDt / 2;                  // V blocks each wavefront copies per tile (4 kDt blocks / 8)
   __shared__ __attribute__((aligned(16))) unsigned char tiles[2][2][kTileBytes];  // [buffer][K, V]
 
   const PrefillWork wk = work[blockIdx.x];
@@ -1464,7 +1495,8 @@ __global__ void __launch_bounds__(512, 1)
   const uint32_t kvr = kvh >> kv.head_shift;  // the real KV head the item's query heads read
   const uint32_t row_add = kv.hnd ? kvr * ps * D : kvr * D;
   const uint64_t page_elems = static_cast<uint64_t>(ps) * kv.kv_heads * D;
-  // This wavefront's share of the copy of tile t: rows 8w .. 8w + 7 of K and of V (kRowsPerDma rows per instruction).
+  // This wavefront's share of the copy of tile t: K rows 8w .. 8w + 7 (kRowsPerDma rows per instruction) and kNv
+  // blocks of V.
   auto issue = [&](int t, int buf, const int32_t (&ids)[4], int ln) {
     const int32_t kb = kbeg + 64 * t;
     const int32_t pos0 = kb + 8 * w;  // this wavefront's first row; all 8 lie in one page
@@ -1472,8 +1504,7 @@ __global__ void __launch_bounds__(512, 1)
     const uint64_t pg = good_page(id) ? static_cast<uint64_t>(id) : 0;  // a bad page's rows are masked, not read
     const int32_t page_first = min(pos0, kend - 1) & ~((1 << ps_shift) - 1);
     const uint16_t* kpage = kbase + pg * page_elems + row_add;
-    const uint16_t* vpage = vbase + pg * page_elems + row_add;
-    const uint32_t kdst = LdsAddr(tiles[buf][0]) + 8 * w * kRowB, vdst = LdsAddr(tiles[buf][1]) + 8 * w * kRowB;
+    const uint32_t kdst = LdsAddr(tiles[buf][0]) + 8 * w * kRowB;
     const int c = ln % kPieces, hh = ln / kPieces;
 #pragma unroll
     for (int i = 0; i < 8 / kRowsPerDma; ++i) {
@@ -1481,9 +1512,19 @@ __global__ void __launch_bounds__(512, 1)
       const uint32_t within = static_cast<uint32_t>(min(pos0 + rr, kend - 1) - page_first);
       const uint32_t off = 2 * row_mul * within;
       const uint32_t kp = 16 * static_cast<uint32_t>(c ^ ((8 * w + rr) & 15));
-      const uint32_t vp = 16 * static_cast<uint32_t>(c ^ ((rr & 3) << 2) ^ (((rr >> 2) & 1) << 3));
       Dma16(kpage, off + kp, kdst + i * 1024);
-      Dma16(vpage, off + vp, vdst + i * 1024);
+    }
+    {  // V blocks (c16, dt0 + i): lane ln fetches key 16 c16 + 8 hi + 4 ((mm >> 4) & 1) + ((mm & 7) >> 1),
+       // dims 32 (dt0 + i) + 16 ((mm >> 3) & 1) + 8 (mm & 1); the block's 16 keys lie in one page
+      const int mm = ln & 31, hi = ln >> 5;
+      const int c16 = w >> 1, dt0 = (w & 1) * kNv;
+      const int32_t vid = ids[c16];
+      const uint16_t* vpage = vbase + (good_page(vid) ? static_cast<uint64_t>(vid) : 0) * page_elems + row_add;
+      const int key = 16 * c16 + 8 * hi + 4 * ((mm >> 4) & 1) + ((mm & 7) >> 1);
+      const uint32_t within = static_cast<uint32_t>(min(kb + key, kend - 1)) & ((1u << ps_shift) - 1);
+      const uint32_t voff = 2 * (row_mul * within + 32 * dt0 + 16 * ((mm >> 3) & 1) + 8 * (mm & 1));
+      const uint32_t dst = LdsAddr(tiles[buf][1]) + 1024 * (c16 * kDt + dt0);
+      StaticFor<kNv>([&](auto i) { Dma16At<64 * i.value>(vpage, voff, dst + 1024 * i.value); });
     }
   };
 
@@ -1522,19 +1563,14 @@ __global__ void __launch_bounds__(512, 1)
     // lc & 15); in bytes 16 ((2 ks + lh) ^ (lc & 15)) = 32 ks ^ 16 (lh ^ (lc & 15)).
     const int krow = lc * kRowB, kx = 16 * (lh ^ (lc & 15));
     // V^T operands, read transposed: in lane group g = ln / 16, lane j = ln % 16 addresses key +(j / 4) at dims
-    // +4 (j % 4), keys based at 32 half + 16 c + 4 (g >> 1) (+8 for the operand's second half), dims at
-    // 32 dt + 16 (g & 1). With the swizzle that piece sits at byte key * kRowB + (64 dt ^ vx) + the lane's offset inside
-    // the 64-byte group, vx = 64 (key & 3) ^ 128 ((key >> 2) & 1) (key & 7 = vkey here).
-    const int vj = ln & 15, vg = ln >> 4;
-    const int vkey = 4 * (vg >> 1) + (vj >> 2);
-    const int vdim = 16 * (vg & 1) + 4 * (vj & 3);
-    const int vrow = vkey * kRowB + 16 * ((vdim >> 3) & 3) + 2 * (vdim & 7);
-    const int vx = (64 * (vkey & 3)) ^ (128 * ((vkey >> 2) & 1));
+    // +4 (j % 4), keys based at 16 c16 + 4 (g >> 1) (+8 for the operand's second half), dims at 32 dt + 16 (g & 1);
+    // block (c16, dt) of the V tile holds exactly those 8 bytes at 8 ln (and the second half's at 512 + 8 ln).
     const int32_t qpos = static_cast<int32_t>(kv_len) - n + wk.q0 + 32 * qt + lc;  // this lane's query position
     const bool need_mask = kb + 64 > kend || (causal && kb + 63 > last_pos - 31) || bad != 0 ||
                            (window >= 0 && kb < last_pos - window);
     const unsigned char* ktile = tiles[buf][0];
     const unsigned char* vtile = tiles[buf][1];
+    const unsigned char* vl = vtile + 8 * ln;
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       f32x16_t sc;
@@ -1564,7 +1600,7 @@ __global__ void __launch_bounds__(512, 1)
       float mx = -INFINITY;
 #pragma unroll
       for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sc[v]);
-      mx = fmaxf(mx, ShflXor(mx, 32));
+      mx = MaxXor32(mx);
       mx *= scale_log2;  // scores stay unscaled until the exponent: the scale is positive, so this is the scaled max
       const bool grow = mx > m_run + 8.0f;
       if (__any(grow)) {
@@ -1598,9 +1634,9 @@ __global__ void __launch_bounds__(512, 1)
       constexpr int kVRing = 2;
       auto vread = [&](int j) {
         const int c = j / kDt, dt = j % kDt;
-        const uint32_t off = static_cast<uint32_t>((32 * half + 16 * c) * kRowB + vrow) + ((64 * dt) ^ vx);
-        const u32x2_t lo = LdsTr16(vtile, off);
-        const u32x2_t hi = LdsTr16(vtile, off + 8 * kRowB);
+        const uint32_t off = 1024 * ((2 * half + c) * kDt + dt);
+        const u32x2_t lo = LdsTr16(vl, off);
+        const u32x2_t hi = LdsTr16(vl, off + 512);
         return u32x4_t{lo[0], lo[1], hi[0], hi[1]};
       };
       u32x4_t va[kVRing];
@@ -1616,7 +1652,7 @@ __global__ void __launch_bounds__(512, 1)
   }
 
   // Lane holds dims 32 dt + 8 i + 4 hl + jj of query r.
-  const float l_tot = l_run + ShflXor(l_run, 32);
+  const float l_tot = SumXor32(l_run);
   if (!row_ok) return;
   if (wk.slot >= 0) {
     const uint64_t prow = static_cast<uint64_t>(wk.slot) * kPfRows + static_cast<uint64_t>(r) * kGroup + hq;
