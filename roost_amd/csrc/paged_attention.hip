@@ -74,8 +74,9 @@ struct DecodeMerge {
   int32_t reserved;
 };
 // A prefill work item: query tokens q0 .. q0 + rows - 1 of sequence seq (all kGroup query heads of one KV head)
-// against keys [kbeg, kend). slot >= 0 marks one piece of a split key range: it writes fp32 partials (unnormalised
-// output, running max and sum) that PrefillMergeKernel combines; slot -1 writes the final rows.
+// against keys [kbeg, kend). slot >= 0 marks one piece of a split key range: it writes partials (its output divided
+// by its own sum, in bf16, and its fp32 running max and sum) that PrefillMergeKernel combines; slot -1 writes the final
+// rows.
 struct PrefillWork {
   int32_t seq;
   int32_t q0;
@@ -241,7 +242,7 @@ RoostStatus Validate(const RoostPagedAttentionParams& p, bool for_run) {
 
 // ---- Host planning ---------------------------------------------------------------------------------------------------
 
-// rows_per_split: fp32 partial rows one split slot holds (decode: the query heads of a sequence; prefill: kPfRows).
+// rows_per_split: partial rows one split slot holds (decode: the query heads of a sequence; prefill: kPfRows).
 Layout MakeLayout(uint64_t work_items, uint64_t ranges, uint64_t merges, uint64_t splits, uint32_t rows_per_split,
                   uint32_t head_dim, uint32_t mode) {
   Layout l;
@@ -256,7 +257,9 @@ Layout MakeLayout(uint64_t work_items, uint64_t ranges, uint64_t merges, uint64_
   l.merge_offset = roost::AlignUp(l.range_offset + (ranges > 0 ? (ranges + 1) * sizeof(int32_t) : 0), 16);
   l.int_bytes = l.merge_offset + merges * merge_bytes;
   l.float_offset = roost::AlignUp(l.int_bytes, kAlign);
-  l.float_bytes = splits * rows_per_split * (static_cast<uint64_t>(head_dim) + 2) * sizeof(float);
+  // decode partials: fp32 rows then (max, sum); prefill partials: bf16 rows then (max, sum)
+  l.float_bytes = splits * rows_per_split *
+                  (decode ? (static_cast<uint64_t>(head_dim) + 2) * sizeof(float) : 2 * static_cast<uint64_t>(head_dim) + 8);
   l.total = l.float_offset + l.float_bytes;
   return l;
 }
@@ -1435,7 +1438,7 @@ template <int D>
 __global__ void __launch_bounds__(512, 1)
     PrefillTileKernel(const uint16_t* __restrict__ q, uint16_t* __restrict__ out, float* __restrict__ lse, KvView kv,
                       const int32_t* __restrict__ kv_indices, const int32_t* __restrict__ q_indptr,
-                      const PrefillWork* __restrict__ work, float* __restrict__ part_o, float* __restrict__ part_ml,
+                      const PrefillWork* __restrict__ work, uint16_t* __restrict__ part_o, float* __restrict__ part_ml,
                       uint32_t q_heads, uint32_t causal, uint32_t ps_shift, float scale_log2, int32_t window) {
   static_assert(D == 128 || D == 256, "the tile kernel is built for head dims 128 and 256");
   constexpr int kRowB = 2 * D;                  // bytes of one K or V row in LDS
@@ -1654,15 +1657,18 @@ __global__ void __launch_bounds__(512, 1)
   // Lane holds dims 32 dt + 8 i + 4 hl + jj of query r.
   const float l_tot = SumXor32(l_run);
   if (!row_ok) return;
-  if (wk.slot >= 0) {
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  if (wk.slot >= 0) {  // a piece of a split item: its normalised output in bf16 and its (max, sum)
     const uint64_t prow = static_cast<uint64_t>(wk.slot) * kPfRows + static_cast<uint64_t>(r) * kGroup + hq;
-    float* po = part_o + prow * D;
+    uint16_t* po = part_o + prow * D;
 #pragma unroll
     for (int dt = 0; dt < kDt; ++dt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int d = dt * 32 + i * 8 + hl * 4;
-        *reinterpret_cast<float4*>(po + d) = make_float4(o[dt][i * 4], o[dt][i * 4 + 1], o[dt][i * 4 + 2], o[dt][i * 4 + 3]);
+        const u32x2_t v{PackBf16(o[dt][i * 4] * inv, o[dt][i * 4 + 1] * inv),
+                        PackBf16(o[dt][i * 4 + 2] * inv, o[dt][i * 4 + 3] * inv)};
+        *reinterpret_cast<u32x2_t*>(po + d) = v;
       }
     if (hl == 0) {
       part_ml[2 * prow] = m_run;
@@ -1670,7 +1676,6 @@ __global__ void __launch_bounds__(512, 1)
     }
     return;
   }
-  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
   const uint64_t orow = (static_cast<uint64_t>(qbeg + wk.q0 + r) * q_heads + head) * D;
 #pragma unroll
   for (int dt = 0; dt < kDt; ++dt)
@@ -1691,7 +1696,7 @@ __global__ void __launch_bounds__(512, 1)
 template <int D>
 __global__ void __launch_bounds__(256)
     PrefillMergeKernel(uint16_t* __restrict__ out, float* __restrict__ lse, const PrefillMerge* __restrict__ merges,
-                       const float* __restrict__ part_o, const float* __restrict__ part_ml,
+                       const uint16_t* __restrict__ part_o, const float* __restrict__ part_ml,
                        const int32_t* __restrict__ q_indptr, uint32_t q_heads) {
   const PrefillMerge mg = merges[blockIdx.x];
   const int r = blockIdx.y;
@@ -1700,21 +1705,27 @@ __global__ void __launch_bounds__(256)
   const int d = 4 * (threadIdx.x % (D / 4));
   const uint64_t token = static_cast<uint64_t>(q_indptr[mg.seq] + mg.q0 + r);
   const uint64_t row = static_cast<uint64_t>(r) * kGroup + hq;
+  // Both loops are unrolled so that the loads of several pieces are in flight at once (a rolled loop waits out one
+  // memory round trip per piece).
   float mx = -INFINITY;
+#pragma unroll 8
   for (int i = 0; i < mg.count; ++i) mx = fmaxf(mx, part_ml[2 * ((mg.first + i) * uint64_t{kPfRows} + row)]);
   float l = 0.0f;
   float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   if (mx != -INFINITY) {
+#pragma unroll 4
     for (int i = 0; i < mg.count; ++i) {
       const uint64_t prow = (mg.first + i) * uint64_t{kPfRows} + row;
-      const float m = part_ml[2 * prow];
-      const float f = m == -INFINITY ? 0.0f : exp2f(m - mx);
-      l += part_ml[2 * prow + 1] * f;
-      const float4 o = *reinterpret_cast<const float4*>(part_o + prow * D + d);
-      acc.x = fmaf(o.x, f, acc.x);
-      acc.y = fmaf(o.y, f, acc.y);
-      acc.z = fmaf(o.z, f, acc.z);
-      acc.w = fmaf(o.w, f, acc.w);
+      const float2 ml = *reinterpret_cast<const float2*>(part_ml + 2 * prow);
+      // The piece's weight is its sum rescaled to the common max (mx is finite here, so a piece without keys, max
+      // -inf, gets exp2(-inf) = 0); its output row is already divided by that sum.
+      const float f = ml.y * exp2f(ml.x - mx);
+      l += f;
+      const u32x2_t raw = *reinterpret_cast<const u32x2_t*>(part_o + prow * D + d);
+      acc.x = fmaf(__uint_as_float(raw[0] << 16), f, acc.x);
+      acc.y = fmaf(__uint_as_float(raw[0] & 0xFFFF0000u), f, acc.y);
+      acc.z = fmaf(__uint_as_float(raw[1] << 16), f, acc.z);
+      acc.w = fmaf(__uint_as_float(raw[1] & 0xFFFF0000u), f, acc.w);
     }
   }
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
@@ -1765,8 +1776,9 @@ RoostStatus LaunchPrefill(const RoostPagedAttentionParams& p, const PlanRecord& 
   auto* outp = static_cast<uint16_t*>(p.output.address);
   auto* lsep = static_cast<float*>(p.lse.address);
   if (PrefillFastPath(p)) {
-    auto* part_o = reinterpret_cast<float*>(dev + rec.float_offset);
-    auto* part_ml = part_o + rec.splits * kPfRows * p.head_dim;
+    // Partials: bf16 rows of the pieces' normalised outputs, then their fp32 (max, sum) pairs.
+    auto* part_o = reinterpret_cast<uint16_t*>(dev + rec.float_offset);
+    auto* part_ml = reinterpret_cast<float*>(part_o + rec.splits * kPfRows * p.head_dim);
     const dim3 grid(static_cast<uint32_t>(rec.work_items));
     const auto* q16 = static_cast<const uint16_t*>(p.q.address);
     const uint32_t ps_shift = static_cast<uint32_t>(__builtin_ctz(p.page_size));
