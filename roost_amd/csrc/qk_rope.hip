@@ -24,7 +24,6 @@ namespace {
 using namespace roost_dev;
 
 constexpr int kMaxHeadDim = 1024;
-constexpr int kMaxPairs = kMaxHeadDim / 2;
 
 template <typename T>
 __device__ __forceinline__ float LoadT(const T* p) {
