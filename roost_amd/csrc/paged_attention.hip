@@ -1691,48 +1691,95 @@ __global__ void __launch_bounds__(512, 1)
   }
 }
 
-// Combines the pieces of a split prefill item: block (merge, token) of D threads; thread t handles query head
-// t / (D / 4), dims 4 (t % (D / 4)) .. +3.
+// Combines the pieces of a split prefill item: block (merge, group of kPfMergeRows tokens) of kGroup * D / 4 threads;
+// thread t handles query head t / (D / 4), dims 4 (t % (D / 4)) .. +3 of each of the group's tokens. Pieces are
+// combined in key order (deterministic): the common case of two pieces issues every load of the group's rows before
+// combining any; other counts go row by row with the piece loops unrolled.
+constexpr int kPfMergeRows = 8;
+
+template <int D>
+__device__ __forceinline__ void MergeWrite(uint16_t* __restrict__ out, float* __restrict__ lse, uint64_t token,
+                                           uint32_t q_heads, uint32_t head, int d, float4 acc, float l, float mx) {
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  const u32x2_t v{PackBf16(acc.x * inv, acc.y * inv), PackBf16(acc.z * inv, acc.w * inv)};
+  *reinterpret_cast<u32x2_t*>(out + (token * q_heads + head) * D + d) = v;
+  if (lse != nullptr && d == 0) lse[token * q_heads + head] = l > 0.0f ? mx + log2f(l) : -INFINITY;
+}
+
+// acc += o * f for one piece's bf16 output slice (already divided by the piece's own sum).
+__device__ __forceinline__ void MergeAdd(float4& acc, u32x2_t raw, float f) {
+  acc.x = fmaf(__uint_as_float(raw[0] << 16), f, acc.x);
+  acc.y = fmaf(__uint_as_float(raw[0] & 0xFFFF0000u), f, acc.y);
+  acc.z = fmaf(__uint_as_float(raw[1] << 16), f, acc.z);
+  acc.w = fmaf(__uint_as_float(raw[1] & 0xFFFF0000u), f, acc.w);
+}
+
 template <int D>
 __global__ void __launch_bounds__(256)
     PrefillMergeKernel(uint16_t* __restrict__ out, float* __restrict__ lse, const PrefillMerge* __restrict__ merges,
                        const uint16_t* __restrict__ part_o, const float* __restrict__ part_ml,
                        const int32_t* __restrict__ q_indptr, uint32_t q_heads) {
   const PrefillMerge mg = merges[blockIdx.x];
-  const int r = blockIdx.y;
-  if (r >= mg.rows) return;
+  const int r0 = static_cast<int>(blockIdx.y) * kPfMergeRows;
+  if (r0 >= mg.rows) return;
   const int hq = threadIdx.x / (D / 4);
   const int d = 4 * (threadIdx.x % (D / 4));
-  const uint64_t token = static_cast<uint64_t>(q_indptr[mg.seq] + mg.q0 + r);
-  const uint64_t row = static_cast<uint64_t>(r) * kGroup + hq;
-  // Both loops are unrolled so that the loads of several pieces are in flight at once (a rolled loop waits out one
-  // memory round trip per piece).
-  float mx = -INFINITY;
-#pragma unroll 8
-  for (int i = 0; i < mg.count; ++i) mx = fmaxf(mx, part_ml[2 * ((mg.first + i) * uint64_t{kPfRows} + row)]);
-  float l = 0.0f;
-  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  if (mx != -INFINITY) {
-#pragma unroll 4
-    for (int i = 0; i < mg.count; ++i) {
-      const uint64_t prow = (mg.first + i) * uint64_t{kPfRows} + row;
-      const float2 ml = *reinterpret_cast<const float2*>(part_ml + 2 * prow);
-      // The piece's weight is its sum rescaled to the common max (mx is finite here, so a piece without keys, max
-      // -inf, gets exp2(-inf) = 0); its output row is already divided by that sum.
-      const float f = ml.y * exp2f(ml.x - mx);
-      l += f;
-      const u32x2_t raw = *reinterpret_cast<const u32x2_t*>(part_o + prow * D + d);
-      acc.x = fmaf(__uint_as_float(raw[0] << 16), f, acc.x);
-      acc.y = fmaf(__uint_as_float(raw[0] & 0xFFFF0000u), f, acc.y);
-      acc.z = fmaf(__uint_as_float(raw[1] << 16), f, acc.z);
-      acc.w = fmaf(__uint_as_float(raw[1] & 0xFFFF0000u), f, acc.w);
-    }
-  }
-  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
   const uint32_t head = mg.kv_head * kGroup + hq;
-  const u32x2_t v{PackBf16(acc.x * inv, acc.y * inv), PackBf16(acc.z * inv, acc.w * inv)};
-  *reinterpret_cast<u32x2_t*>(out + (token * q_heads + head) * D + d) = v;
-  if (lse != nullptr && d == 0) lse[token * q_heads + head] = l > 0.0f ? mx + log2f(l) : -INFINITY;
+  const uint64_t tok0 = static_cast<uint64_t>(q_indptr[mg.seq] + mg.q0);
+  // Partial row of piece i for token row r: (first + i) * kPfRows + r * kGroup + hq.
+  auto prow = [&](int i, int r) {
+    return (static_cast<uint64_t>(mg.first) + i) * kPfRows + static_cast<uint64_t>(r) * kGroup + hq;
+  };
+  if (mg.count == 2) {
+    float2 ml[kPfMergeRows][2];
+    u32x2_t o[kPfMergeRows][2];
+#pragma unroll
+    for (int j = 0; j < kPfMergeRows; ++j) {
+      const int r = min(r0 + j, mg.rows - 1);  // rows past the item's end re-read its last row and are not written
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        ml[j][i] = *reinterpret_cast<const float2*>(part_ml + 2 * prow(i, r));
+        o[j][i] = *reinterpret_cast<const u32x2_t*>(part_o + prow(i, r) * D + d);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kPfMergeRows; ++j) {
+      if (r0 + j >= mg.rows) break;
+      const float mx = fmaxf(ml[j][0].x, ml[j][1].x);
+      float l = 0.0f;
+      float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (mx != -INFINITY) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          // The piece's weight is its sum rescaled to the common max (mx is finite here, so a piece without keys,
+          // max -inf, gets exp2(-inf) = 0).
+          const float f = ml[j][i].y * exp2f(ml[j][i].x - mx);
+          l += f;
+          MergeAdd(acc, o[j][i], f);
+        }
+      }
+      MergeWrite<D>(out, lse, tok0 + r0 + j, q_heads, head, d, acc, l, mx);
+    }
+    return;
+  }
+  for (int j = 0; j < kPfMergeRows && r0 + j < mg.rows; ++j) {
+    const int r = r0 + j;
+    float mx = -INFINITY;
+#pragma unroll 8
+    for (int i = 0; i < mg.count; ++i) mx = fmaxf(mx, part_ml[2 * prow(i, r)]);
+    float l = 0.0f;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (mx != -INFINITY) {
+#pragma unroll 4
+      for (int i = 0; i < mg.count; ++i) {
+        const float2 m = *reinterpret_cast<const float2*>(part_ml + 2 * prow(i, r));
+        const float f = m.y * exp2f(m.x - mx);
+        l += f;
+        MergeAdd(acc, *reinterpret_cast<const u32x2_t*>(part_o + prow(i, r) * D + d), f);
+      }
+    }
+    MergeWrite<D>(out, lse, tok0 + r, q_heads, head, d, acc, l, mx);
+  }
 }
 
 template <typename T, int D>
@@ -1791,7 +1838,7 @@ RoostStatus LaunchPrefill(const RoostPagedAttentionParams& p, const PlanRecord& 
     }
     ROOST_TRY(FromHip(hipGetLastError(), "PagedAttention prefill launch"));
     if (rec.merges == 0) return ROOST_STATUS_OK;
-    const dim3 mgrid(static_cast<uint32_t>(rec.merges), kPfTokens);
+    const dim3 mgrid(static_cast<uint32_t>(rec.merges), kPfTokens / kPfMergeRows);
     const auto* mg = reinterpret_cast<const PrefillMerge*>(dev + rec.merge_offset);
     if (p.head_dim == 128) {
       hipLaunchKernelGGL(PrefillMergeKernel<128>, mgrid, dim3(kGroup * 128 / 4), 0, stream, outp, lsep, mg, part_o,
