@@ -1590,6 +1590,15 @@ __global__ void __launch_bounds__(512, 1)
         if (ks + kRing < kKs) ka[ks % kRing] = *reinterpret_cast<const u32x4_t*>(krow_p + ((32 * (ks + kRing)) ^ kx));
         sc = Mfma32(a, qreg[ks], sc);
       }
+      // Keep kRing operand reads in flight (left alone, the compiler waits out every read before its multiply at this
+      // register budget): the reads of the first kRing steps, then one multiply and one read in turn.
+      __builtin_amdgcn_sched_group_barrier(0x100, kRing, 0);
+#pragma unroll
+      for (int ks = 0; ks < kKs - kRing; ++ks) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, kRing, 0);
       if (need_mask) {  // one uniform branch around branch-free selects
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
