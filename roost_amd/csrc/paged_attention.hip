@@ -108,7 +108,7 @@ struct PlanRecord {
   uint32_t head_dim;
   uint32_t kv_heads;
   int32_t window;        // WindowOf(params): the pieces start at the window
-  uint32_t reserved0;
+  uint32_t merges_two;   // prefill: the leading merge entries of exactly two pieces
   uint64_t pages;        // kv_indptr_host[batch]
   uint64_t work_items;   // decode pieces or prefill tiles
   uint64_t ranges;       // decode: workgroup ranges over the pieces
@@ -129,6 +129,7 @@ struct Layout {
   uint64_t work_items = 0;
   uint64_t ranges = 0;
   uint64_t merges = 0;
+  uint64_t merges_two = 0;  // prefill: leading merge entries of two pieces
   uint64_t range_offset = 0;
   uint64_t merge_offset = 0;
   uint64_t counter_offset = 0;
@@ -466,8 +467,12 @@ Layout PlanPrefill(const RoostPagedAttentionParams& p, uint32_t cus, unsigned ch
     items.swap(cut);
   }
   std::stable_sort(items.begin(), items.end(), [](const Item& a, const Item& b) { return a.cost > b.cost; });
+  // Merges of exactly two pieces first: they run on the 8-rows-per-block form of the merge kernel.
+  std::stable_partition(merges.begin(), merges.end(), [](const PrefillMerge& m) { return m.count == 2; });
   Layout l = MakeLayout(items.size(), 0, merges.size(), static_cast<uint64_t>(slot), kPfRows, p.head_dim,
                         ROOST_ATTENTION_PREFILL);
+  l.merges_two = static_cast<uint64_t>(
+      std::count_if(merges.begin(), merges.end(), [](const PrefillMerge& m) { return m.count == 2; }));
   if (host != nullptr) {
     auto* w = reinterpret_cast<PrefillWork*>(host);
     for (size_t i = 0; i < items.size(); ++i) w[i] = items[i].w;
@@ -1700,10 +1705,10 @@ __global__ void __launch_bounds__(512, 1)
   }
 }
 
-// Combines the pieces of a split prefill item: block (merge, group of kPfMergeRows tokens) of kGroup * D / 4 threads;
-// thread t handles query head t / (D / 4), dims 4 (t % (D / 4)) .. +3 of each of the group's tokens. Pieces are
-// combined in key order (deterministic): the common case of two pieces issues every load of the group's rows before
-// combining any; other counts go row by row with the piece loops unrolled.
+// Combines the pieces of a split prefill item: block (merge, group of kRows tokens) of kGroup * D / 4 threads; thread t
+// handles query head t / (D / 4), dims 4 (t % (D / 4)) .. +3 of each of the group's tokens. Pieces are combined in
+// key order (deterministic). Merges of two pieces (the plan puts them first) run 8 tokens per block with every load
+// issued before any is combined; the others one token per block.
 constexpr int kPfMergeRows = 8;
 
 template <int D>
@@ -1723,13 +1728,13 @@ __device__ __forceinline__ void MergeAdd(float4& acc, u32x2_t raw, float f) {
   acc.w = fmaf(__uint_as_float(raw[1] & 0xFFFF0000u), f, acc.w);
 }
 
-template <int D>
+template <int D, int kRows>
 __global__ void __launch_bounds__(256)
     PrefillMergeKernel(uint16_t* __restrict__ out, float* __restrict__ lse, const PrefillMerge* __restrict__ merges,
                        const uint16_t* __restrict__ part_o, const float* __restrict__ part_ml,
                        const int32_t* __restrict__ q_indptr, uint32_t q_heads) {
   const PrefillMerge mg = merges[blockIdx.x];
-  const int r0 = static_cast<int>(blockIdx.y) * kPfMergeRows;
+  const int r0 = static_cast<int>(blockIdx.y) * kRows;
   if (r0 >= mg.rows) return;
   const int hq = threadIdx.x / (D / 4);
   const int d = 4 * (threadIdx.x % (D / 4));
@@ -1739,11 +1744,11 @@ __global__ void __launch_bounds__(256)
   auto prow = [&](int i, int r) {
     return (static_cast<uint64_t>(mg.first) + i) * kPfRows + static_cast<uint64_t>(r) * kGroup + hq;
   };
-  if (mg.count == 2) {
-    float2 ml[kPfMergeRows][2];
-    u32x2_t o[kPfMergeRows][2];
+  if constexpr (kRows > 1) {  // merges of exactly two pieces
+    float2 ml[kRows][2];
+    u32x2_t o[kRows][2];
 #pragma unroll
-    for (int j = 0; j < kPfMergeRows; ++j) {
+    for (int j = 0; j < kRows; ++j) {
       const int r = min(r0 + j, mg.rows - 1);  // rows past the item's end re-read its last row and are not written
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
@@ -1752,7 +1757,7 @@ __global__ void __launch_bounds__(256)
       }
     }
 #pragma unroll
-    for (int j = 0; j < kPfMergeRows; ++j) {
+    for (int j = 0; j < kRows; ++j) {
       if (r0 + j >= mg.rows) break;
       const float mx = fmaxf(ml[j][0].x, ml[j][1].x);
       float l = 0.0f;
@@ -1769,25 +1774,22 @@ __global__ void __launch_bounds__(256)
       }
       MergeWrite<D>(out, lse, tok0 + r0 + j, q_heads, head, d, acc, l, mx);
     }
-    return;
-  }
-  for (int j = 0; j < kPfMergeRows && r0 + j < mg.rows; ++j) {
-    const int r = r0 + j;
+  } else {  // any count, one token row per block; the piece loops are unrolled so several pieces' loads are in flight
     float mx = -INFINITY;
 #pragma unroll 8
-    for (int i = 0; i < mg.count; ++i) mx = fmaxf(mx, part_ml[2 * prow(i, r)]);
+    for (int i = 0; i < mg.count; ++i) mx = fmaxf(mx, part_ml[2 * prow(i, r0)]);
     float l = 0.0f;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (mx != -INFINITY) {
 #pragma unroll 4
       for (int i = 0; i < mg.count; ++i) {
-        const float2 m = *reinterpret_cast<const float2*>(part_ml + 2 * prow(i, r));
+        const float2 m = *reinterpret_cast<const float2*>(part_ml + 2 * prow(i, r0));
         const float f = m.y * exp2f(m.x - mx);
         l += f;
-        MergeAdd(acc, *reinterpret_cast<const u32x2_t*>(part_o + prow(i, r) * D + d), f);
+        MergeAdd(acc, *reinterpret_cast<const u32x2_t*>(part_o + prow(i, r0) * D + d), f);
       }
     }
-    MergeWrite<D>(out, lse, tok0 + r, q_heads, head, d, acc, l, mx);
+    MergeWrite<D>(out, lse, tok0 + r0, q_heads, head, d, acc, l, mx);
   }
 }
 
@@ -1847,14 +1849,28 @@ RoostStatus LaunchPrefill(const RoostPagedAttentionParams& p, const PlanRecord& 
     }
     ROOST_TRY(FromHip(hipGetLastError(), "PagedAttention prefill launch"));
     if (rec.merges == 0) return ROOST_STATUS_OK;
-    const dim3 mgrid(static_cast<uint32_t>(rec.merges), kPfTokens / kPfMergeRows);
     const auto* mg = reinterpret_cast<const PrefillMerge*>(dev + rec.merge_offset);
-    if (p.head_dim == 128) {
-      hipLaunchKernelGGL(PrefillMergeKernel<128>, mgrid, dim3(kGroup * 128 / 4), 0, stream, outp, lsep, mg, part_o,
-                         part_ml, q_indptr, p.q_heads);
-    } else {
-      hipLaunchKernelGGL(PrefillMergeKernel<256>, mgrid, dim3(kGroup * 256 / 4), 0, stream, outp, lsep, mg, part_o,
-                         part_ml, q_indptr, p.q_heads);
+    const uint32_t two = rec.merges_two, rest = static_cast<uint32_t>(rec.merges) - rec.merges_two;
+    const dim3 block(kGroup * p.head_dim / 4);
+    if (two > 0) {
+      const dim3 g(two, kPfTokens / kPfMergeRows);
+      if (p.head_dim == 128) {
+        hipLaunchKernelGGL((PrefillMergeKernel<128, kPfMergeRows>), g, block, 0, stream, outp, lsep, mg, part_o, part_ml,
+                           q_indptr, p.q_heads);
+      } else {
+        hipLaunchKernelGGL((PrefillMergeKernel<256, kPfMergeRows>), g, block, 0, stream, outp, lsep, mg, part_o, part_ml,
+                           q_indptr, p.q_heads);
+      }
+    }
+    if (rest > 0) {
+      const dim3 g(rest, kPfTokens);
+      if (p.head_dim == 128) {
+        hipLaunchKernelGGL((PrefillMergeKernel<128, 1>), g, block, 0, stream, outp, lsep, mg + two, part_o, part_ml,
+                           q_indptr, p.q_heads);
+      } else {
+        hipLaunchKernelGGL((PrefillMergeKernel<256, 1>), g, block, 0, stream, outp, lsep, mg + two, part_o, part_ml,
+                           q_indptr, p.q_heads);
+      }
     }
     return FromHip(hipGetLastError(), "PagedAttention prefill merge launch");
   }
@@ -1921,6 +1937,7 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_plan(RoostContext* ctx, c
     rec.work_items = l.work_items;
     rec.ranges = l.ranges;
     rec.merges = l.merges;
+    rec.merges_two = static_cast<uint32_t>(l.merges_two);
     rec.range_offset = l.range_offset;
     rec.merge_offset = l.merge_offset;
     rec.counter_offset = l.counter_offset;
