@@ -10,25 +10,24 @@
 // written a plan record for this batch shape. The optional lse output is the base-2 log-sum-exp of the scaled scores,
 // log2(sum_j 2^(s_j * log2 e)), which is the convention of the FlashInfer kernels the reference wraps.
 //
-// Decode (mode DECODE) -- bandwidth bound, no MFMA:
-//   * split-K over fixed 512-token chunks of each sequence; the chunk size depends only on the sequence's own length,
-//     so a row's result does not depend on the rest of the batch (BATCH_INVARIANT) and the fixed merge order makes it
-//     DETERMINISTIC;
-//   * one workgroup = one (chunk, KV head); its 4 wavefronts take 16-token groups in turn; every K/V byte is loaded once
-//     with 16-byte coalesced reads (a 512-byte bf16 row per 32 lanes) straight into registers and shared by the 4 query
-//     heads of the GQA group;
-//   * q.k uses v_dot2 bf16 dot products; the per-(token, head) partial sums are reduce-scattered across the lanes of a
-//     row so that each lane ends with exactly one score; the online-softmax max is a wavefront max-reduction; the
-//     weights are exchanged through a 256-byte LDS slot per wavefront; P.V accumulates in fp32 registers;
-//   * the 4 wavefronts merge through LDS; a sequence with several chunks writes fp32 partials (o, m, l) that a small
-//     merge kernel combines in chunk order.
-// Prefill (mode PREFILL) -- MFMA bound:
-//   * one workgroup = 32 query tokens x the 4 query heads of one KV head (one wavefront per head), all sharing each
-//     64-key K and V tile staged in LDS (K row-major, V transposed so both MFMA operands read contiguous LDS);
-//   * S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_32x32x16_bf16 with fp32 accumulation; with queries on the MFMA N axis
-//     the softmax statistics of a query live in one lane pair, so the online softmax needs one cross-lane exchange per
-//     tile; P is rounded to bf16 before the P.V product (as FlashAttention-2 does);
-//   * plan() orders the (tile, KV head) work items longest-first so the ragged causal tail does not set the makespan.
+// Decode (mode DECODE) -- HBM bound (DecodeKernel, DecodeMergeKernel):
+//   * plan() deals the batch's 16-token groups out evenly to one range per resident workgroup slot and cuts sequences
+//     at range boundaries (so the variant is DETERMINISTIC but not BATCH_INVARIANT); a workgroup serves the KV heads
+//     of its range, its wavefronts take alternate groups;
+//   * K and V rows are loaded branch-free into a register double buffer (the next group in flight while the current
+//     one is computed), each K/V byte once, shared by the query heads of the GQA group;
+//   * bf16: q.k on v_mfma_f32_16x16x32_bf16 (tokens on M, the group's query heads on N), P.V on v_dot2 with P rounded
+//     to bf16; f32: q.k as VALU products reduce-scattered across the lanes of a row;
+//   * the wavefronts merge through LDS; a sequence cut into pieces writes fp32 partials (o, m, l) that
+//     DecodeMergeKernel combines in key order.
+// Prefill (mode PREFILL) -- MFMA bound (PrefillTileKernel + PrefillMergeKernel for page sizes that are powers of two
+// and multiples of 16; PrefillKernel otherwise):
+//   * one workgroup = 64 query tokens x the 4 query heads of one (virtual) KV head, 8 wavefronts; 64-key K and V
+//     tiles are copied from the paged cache straight into LDS (global_load_lds), double-buffered;
+//   * S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_32x32x16_bf16 with fp32 accumulation; the softmax statistics of a
+//     query live in one lane pair; P is rounded to bf16 before the P.V product (as FlashAttention-2 does);
+//   * plan() cuts items longer than the average CU load into pieces (bf16 partials merged in key order) and orders the
+//     work longest-first so the ragged causal tail does not set the makespan.
 
 #include <algorithm>
 #include <cmath>
