@@ -237,6 +237,8 @@ PREFILL_CASES = [
     ("fresh-40 ps1 HND", [(40, 40)], 1, True, True),
     # a long causal chunk: its key range is cut into pieces that the merge kernel combines
     ("chunk-512-of-4000 split", [(512, 4000), (3, 3)], 16, False, True),
+    # merges of two pieces (8 tokens per merge block) and of 3 and 24 pieces (one token per block) in one call
+    ("two- and many-piece merges", [(64, 12064), (256, 1156)], 16, False, True),
     # mixed worker steps: the single-token sequences of a prefill call run on the decode kernels
     ("mixed step 6 decode + 2 chunks", [(1, 900), (1, 17), (200, 1200), (1, 3000), (1, 1), (64, 64), (1, 5000),
                                         (1, 333)], 16, False, True),
