@@ -39,58 +39,69 @@ constexpr uint32_t kPlanMagic = 0x50444752;  // "RGDP"
 
 uint32_t Stride(uint32_t s) { return s == 0 ? kRow : s; }
 
-// Checks shared by both variants (reference: kernels/src/ops/gated_delta_rule.cu:231-278), same statuses.
-RoostStatus Validate(const RoostGatedDeltaRuleParams& p, bool need_host_cu) {
-  using roost::Aligned;
-  using roost::Fail;
-  if (p.struct_size < sizeof(RoostGatedDeltaRuleParams) || p.abi_minor > ROOST_ABI_MINOR) {
-    return Fail(ROOST_STATUS_ABI_MISMATCH, "GatedDeltaRule: params struct_size or abi_minor is not supported by this library");
-  }
-  if (p.k_heads != kHeads || p.v_heads != kHeads || p.k_dim != kDim || p.v_dim != kDim) {
-    return Fail(ROOST_STATUS_UNSUPPORTED,
-                "GatedDeltaRule: built for 16 key heads, 16 value heads and head size 128 (Qwen3.5-0.8B)");
-  }
-  if (p.l2_norm_qk == 0) return Fail(ROOST_STATUS_UNSUPPORTED, "GatedDeltaRule: only l2_norm_qk != 0 is built");
-  if (p.tokens > kMaxTokens || p.batch > kMaxBatch) {
-    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRule: too many tokens or sequences for one call");
-  }
+constexpr char kOp[] = "gated_delta_rule";
+
+// The call's rules, shared by both variants. The statuses are the contract's (the reference refuses the same shapes:
+// kernels/src/ops/gated_delta_rule.cu:231-278); `planning` adds plan()'s need for the host cu_seqlens copy.
+RoostStatus Admit(const RoostGatedDeltaRuleParams& p, bool planning) {
+  roost::Gate gate(kOp);
+  gate.Header(&p, sizeof(RoostGatedDeltaRuleParams))
+      .Expect(p.k_heads == kHeads && p.v_heads == kHeads && p.k_dim == kDim && p.v_dim == kDim,
+              ROOST_STATUS_UNSUPPORTED, "heads %u/%u of dims %u/%u (key/value): the kernels are built for the "
+              "Qwen3.5-0.8B shape, 16/16 heads of 128", p.k_heads, p.v_heads, p.k_dim, p.v_dim)
+      .Expect(p.l2_norm_qk != 0, ROOST_STATUS_UNSUPPORTED, "l2_norm_qk = 0: the kernels always normalise q and k")
+      .Expect(p.tokens <= kMaxTokens && p.batch <= kMaxBatch, ROOST_STATUS_INVALID_ARGUMENT,
+              "%u tokens in %u sequences exceeds one call's limits (%llu tokens, %u sequences)", p.tokens, p.batch,
+              static_cast<unsigned long long>(kMaxTokens), kMaxBatch);
+  ROOST_GATE_RETURN(gate);
   const uint64_t qs = Stride(p.q_stride), ks = Stride(p.k_stride), vs = Stride(p.v_stride);
-  if (qs < kRow || ks < kRow || vs < kRow) {
-    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRule: a q, k or v stride is smaller than the row width");
-  }
-  auto span_ok = [](const RoostDeviceSpan& s, uint32_t dtype, uint64_t n) {
-    return s.reserved0 == 0 && s.dtype == dtype && s.length >= n && (n == 0 || s.address != nullptr);
-  };
+  gate.Expect(qs >= kRow && ks >= kRow && vs >= kRow, ROOST_STATUS_INVALID_ARGUMENT,
+              "row strides q %llu, k %llu, v %llu: each view row holds %u elements", static_cast<unsigned long long>(qs),
+              static_cast<unsigned long long>(ks), static_cast<unsigned long long>(vs), kRow);
+  ROOST_GATE_RETURN(gate);
+  // A strided view reaches (tokens - 1) * stride + one row.
   const uint64_t t = p.tokens;
-  const uint64_t tail = t == 0 ? 0 : t - 1;
-  if (!span_ok(p.q, ROOST_DTYPE_BF16, t == 0 ? 0 : tail * qs + kRow) ||
-      !span_ok(p.k, ROOST_DTYPE_BF16, t == 0 ? 0 : tail * ks + kRow) ||
-      !span_ok(p.v, ROOST_DTYPE_BF16, t == 0 ? 0 : tail * vs + kRow)) {
-    return Fail(ROOST_STATUS_INVALID_ARGUMENT,
-                "GatedDeltaRule: q, k and v must be bf16 spans reaching (tokens - 1) * stride + 2048 elements");
-  }
-  if (!span_ok(p.g, ROOST_DTYPE_F32, t * kHeads) || !span_ok(p.beta, ROOST_DTYPE_BF16, t * kHeads) ||
-      !span_ok(p.output, ROOST_DTYPE_BF16, t * kRow)) {
-    return Fail(ROOST_STATUS_UNSUPPORTED, "GatedDeltaRule: g must be float32, beta and output bf16, each long enough");
-  }
-  if (!span_ok(p.state, ROOST_DTYPE_F32, kStateElems) || p.state.length % kStateElems != 0) {
-    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRule: state must be a float32 pool of whole [16, 128, 128] slots");
-  }
-  if (!span_ok(p.state_slots, ROOST_DTYPE_I32, p.batch) || !span_ok(p.cu_seqlens, ROOST_DTYPE_I32, uint64_t{p.batch} + 1)) {
-    return Fail(ROOST_STATUS_INVALID_ARGUMENT,
-                "GatedDeltaRule: state_slots and cu_seqlens must be int32 spans of batch and batch + 1");
-  }
-  if (!Aligned(p.g.address, 16) || !Aligned(p.beta.address, 16) || !Aligned(p.output.address, 16) ||
-      !Aligned(p.state.address, 16)) {
-    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRule: g, beta, output and state must be 16-byte aligned");
-  }
-  if (!Aligned(p.q.address, 2) || !Aligned(p.k.address, 2) || !Aligned(p.v.address, 2)) {
-    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRule: q, k and v must be 2-byte aligned");
-  }
-  if (need_host_cu && p.cu_seqlens_host == nullptr && p.batch > 0 && p.tokens > 0) {
-    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRule plan: cu_seqlens_host is required");
-  }
-  return ROOST_STATUS_OK;
+  auto reach = [t](uint64_t stride) { return t == 0 ? 0 : (t - 1) * stride + kRow; };
+  gate.Tensor("q", p.q, ROOST_DTYPE_BF16, reach(qs))
+      .Tensor("k", p.k, ROOST_DTYPE_BF16, reach(ks))
+      .Tensor("v", p.v, ROOST_DTYPE_BF16, reach(vs));
+  ROOST_GATE_RETURN(gate);
+  // g, beta and output of another type are shapes the kernels do not cover (UNSUPPORTED, as the contract has it).
+  gate.Expect(p.g.dtype == ROOST_DTYPE_F32 && p.beta.dtype == ROOST_DTYPE_BF16 && p.output.dtype == ROOST_DTYPE_BF16,
+              ROOST_STATUS_UNSUPPORTED, "g %s, beta %s, output %s: built for f32 g with bf16 beta and output",
+              roost::Describe(p.g.dtype).name, roost::Describe(p.beta.dtype).name, roost::Describe(p.output.dtype).name);
+  ROOST_GATE_RETURN(gate);
+  gate.Tensor("g", p.g, ROOST_DTYPE_F32, t * kHeads)
+      .Tensor("beta", p.beta, ROOST_DTYPE_BF16, t * kHeads)
+      .Tensor("output", p.output, ROOST_DTYPE_BF16, t * kRow)
+      .Tensor("state", p.state, ROOST_DTYPE_F32, kStateElems)
+      .Expect(p.state.length % kStateElems == 0, ROOST_STATUS_INVALID_ARGUMENT,
+              "state pool of %llu floats is not a whole number of [16, 128, 128] slots",
+              static_cast<unsigned long long>(p.state.length))
+      .Tensor("state_slots", p.state_slots, ROOST_DTYPE_I32, p.batch)
+      .Tensor("cu_seqlens", p.cu_seqlens, ROOST_DTYPE_I32, uint64_t{p.batch} + 1)
+      .Aligned("g", p.g.address, 16)
+      .Aligned("beta", p.beta.address, 16)
+      .Aligned("output", p.output.address, 16)
+      .Aligned("state", p.state.address, 16)
+      .Aligned("q", p.q.address, 2)
+      .Aligned("k", p.k.address, 2)
+      .Aligned("v", p.v.address, 2)
+      .Expect(!planning || p.cu_seqlens_host != nullptr || p.batch == 0 || p.tokens == 0,
+              ROOST_STATUS_INVALID_ARGUMENT, "plan() reads cu_seqlens_host, which is NULL");
+  return gate.status();
+}
+
+// workspace() only sizes the call: the header and the token / sequence limits.
+RoostStatus AdmitForSizing(const void* params, const RoostWorkspaceSizes* sizes) {
+  roost::Gate gate(kOp);
+  gate.Expect(sizes != nullptr, ROOST_STATUS_INVALID_ARGUMENT, "the sizes out-pointer is NULL")
+      .Header(params, sizeof(RoostGatedDeltaRuleParams));
+  ROOST_GATE_RETURN(gate);
+  const auto& p = *static_cast<const RoostGatedDeltaRuleParams*>(params);
+  gate.Expect(p.tokens <= kMaxTokens && p.batch <= kMaxBatch, ROOST_STATUS_INVALID_ARGUMENT,
+              "%u tokens in %u sequences exceeds one call's limits", p.tokens, p.batch);
+  return gate.status();
 }
 
 float Scale(const RoostGatedDeltaRuleParams& p) {
@@ -259,7 +270,7 @@ GdnArgs MakeArgs(const RoostGatedDeltaRuleParams& p) {
 }
 
 bool Vec16(const RoostGatedDeltaRuleParams& p) {
-  using roost::Aligned;
+  auto Aligned = [](const void* a, uint64_t n) { return roost::IsAligned(a, n); };
   const uint64_t qs = Stride(p.q_stride), ks = Stride(p.k_stride), vs = Stride(p.v_stride);
   return Aligned(p.q.address, 16) && Aligned(p.k.address, 16) && Aligned(p.v.address, 8) && qs % 8 == 0 &&
          ks % 8 == 0 && vs % 4 == 0;
@@ -274,7 +285,7 @@ RoostStatus LaunchRecurrent(const RoostGatedDeltaRuleParams& p, hipStream_t stre
   } else {
     hipLaunchKernelGGL(RecurrentKernel<false>, grid, dim3(128), 0, stream, a);
   }
-  return roost::FromHip(hipGetLastError(), "GatedDeltaRule recurrent launch");
+  return roost::HipStatus(hipGetLastError(), kOp, "recurrent launch");
 }
 
 // ---- Chunk variant: WY form on MFMA ---------------------------------------------------------------------------------
@@ -917,14 +928,14 @@ __global__ void __launch_bounds__(256, 1) ChunkScanKernel(ChunkArgs ca) {
 
 // ---- Chunk variant: plan tables ---------------------------------------------------------------------------------------
 
-struct PlanRecord {
+struct ChunkStamp {  // what plan() leaves in ws->plan for run()
   uint32_t magic;
   uint32_t batch;
   uint32_t tokens;
   uint32_t chunks;
 };
 
-struct ChunkLayout {
+struct ChunkArena {
   uint64_t chunk_table;  // [max_chunks] int4 (sequence, first token, tokens, 0)
   uint64_t seq_table;    // [batch] int4 (first chunk, chunk count, first token, end token)
   uint64_t seq_list;     // [max_long] int32: the chunked sequences in order (recurrent variant only)
@@ -935,27 +946,27 @@ struct ChunkLayout {
   uint32_t max_chunks;
 };
 
-ChunkLayout MakeChunkLayoutFor(uint64_t max_chunks, uint64_t batch, uint64_t max_long = 0) {
-  ChunkLayout l{};
+ChunkArena MakeArena(uint64_t max_chunks, uint64_t batch, uint64_t max_long = 0) {
+  ChunkArena l{};
   l.max_chunks = static_cast<uint32_t>(max_chunks);
   l.max_long = static_cast<uint32_t>(max_long);
   l.chunk_table = 0;
-  l.seq_table = roost::AlignUp(16ull * l.max_chunks, 256);
+  l.seq_table = roost::RoundUp(16ull * l.max_chunks, 256);
   l.seq_list = l.seq_table + 16ull * batch;
-  l.tables_bytes = roost::AlignUp(l.seq_list + 4ull * max_long, 256);
+  l.tables_bytes = roost::RoundUp(l.seq_list + 4ull * max_long, 256);
   l.records = l.tables_bytes;
   l.total = l.records + uint64_t{l.max_chunks} * kHeads * kRecBytes;
   return l;
 }
 
 // Every sequence may be chunked (chunk variant): at most tokens / 64 + batch chunks.
-ChunkLayout MakeChunkLayout(uint64_t tokens, uint64_t batch) { return MakeChunkLayoutFor(tokens / kChunk + batch, batch); }
+ChunkArena MakeChunkArena(uint64_t tokens, uint64_t batch) { return MakeArena(tokens / kChunk + batch, batch); }
 
 // Only sequences of kRouteMinTokens or more are chunked (recurrent variant): sum ceil(len / 64) over them is at most
 // tokens / 64 plus their number, which is at most min(batch, tokens / kRouteMinTokens).
-ChunkLayout MakeRouteLayout(uint64_t tokens, uint64_t batch) {
+ChunkArena MakeRouteArena(uint64_t tokens, uint64_t batch) {
   const uint64_t max_long = std::min<uint64_t>(batch, tokens / kRouteMinTokens);
-  return MakeChunkLayoutFor(tokens / kChunk + max_long, batch, max_long);
+  return MakeArena(tokens / kChunk + max_long, batch, max_long);
 }
 
 
@@ -1037,7 +1048,7 @@ __global__ void __launch_bounds__(1024) RouteKernel(const int32_t* cu, uint32_t 
   }
 }
 
-RoostStatus LaunchChunk(const RoostGatedDeltaRuleParams& p, const RoostWorkspace* ws, const ChunkLayout& l,
+RoostStatus LaunchChunk(const RoostGatedDeltaRuleParams& p, const RoostWorkspace* ws, const ChunkArena& l,
                         uint32_t chunks, hipStream_t stream) {
   ChunkArgs ca{};
   ca.a = MakeArgs(p);
@@ -1057,7 +1068,25 @@ RoostStatus LaunchChunk(const RoostGatedDeltaRuleParams& p, const RoostWorkspace
     hipLaunchKernelGGL(ChunkPrepKernel<false>, prep, dim3(256), 0, stream, ca);
     hipLaunchKernelGGL(ChunkScanKernel<false>, scan, dim3(256), 0, stream, ca);
   }
-  return roost::FromHip(hipGetLastError(), "GatedDeltaRule chunk launch");
+  return roost::HipStatus(hipGetLastError(), kOp, "chunk launch");
+}
+
+// The recurrent variant's routed path over a device region laid out as `l`: RouteKernel writes the chunk tables of the
+// sequences of kRouteMinTokens or more tokens from the device cu_seqlens, the chunk kernels run those sequences and the
+// recurrent kernel the rest, in that order on one stream. (Two streams were slower: the short kernels lose more to
+// sharing the chip than the overlap saves.) Two sequences of one call sharing a state slot leave the recurrent one's
+// state.
+RoostStatus LaunchRouted(const RoostGatedDeltaRuleParams& p, uint8_t* base, const ChunkArena& l, hipStream_t s) {
+  hipLaunchKernelGGL(RouteKernel, dim3(1), dim3(1024), 0, s, static_cast<const int32_t*>(p.cu_seqlens.address),
+                     p.batch, l.max_chunks, reinterpret_cast<int4*>(base + l.chunk_table),
+                     reinterpret_cast<int4*>(base + l.seq_table), reinterpret_cast<int32_t*>(base + l.seq_list),
+                     l.max_long);
+  ROOST_RETURN_IF_FAILED(roost::HipStatus(hipGetLastError(), kOp, "route launch"));
+  RoostWorkspace ws{};
+  ws.device = base;
+  ws.device_bytes = l.total;
+  ROOST_RETURN_IF_FAILED(LaunchChunk(p, &ws, l, l.max_chunks, s));
+  return LaunchRecurrent(p, s, static_cast<int32_t>(kRouteMinTokens));
 }
 
 }  // namespace
@@ -1066,33 +1095,27 @@ RoostStatus LaunchChunk(const RoostGatedDeltaRuleParams& p, const RoostWorkspace
 
 extern "C" ROOST_API RoostStatus roost_gdn_recurrent_workspace(RoostContext*, const void* params,
                                                                RoostWorkspaceSizes* sizes) {
-  using namespace roost;
-  if (params == nullptr || sizes == nullptr) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRule: params or sizes is NULL");
+  ROOST_RETURN_IF_FAILED(AdmitForSizing(params, sizes));
   const auto& p = *static_cast<const RoostGatedDeltaRuleParams*>(params);
-  if (p.struct_size < sizeof(RoostGatedDeltaRuleParams) || p.abi_minor > ROOST_ABI_MINOR) {
-    return Fail(ROOST_STATUS_ABI_MISMATCH, "GatedDeltaRule: params struct_size or abi_minor is not supported by this library");
-  }
-  if (p.tokens > kMaxTokens || p.batch > kMaxBatch) {
-    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRule: too many tokens or sequences for one call");
-  }
   // The views and the pool slots are read in place; a call that may hold a sequence of kRouteMinTokens or more
   // tokens also gets the chunk tables and records for the sequences it hands to the chunk kernels.
-  sizes->device_bytes = p.tokens >= kRouteMinTokens ? MakeRouteLayout(p.tokens, p.batch).total : 0;
-  sizes->pinned_host_bytes = 0;
-  sizes->plan_bytes = 0;
+  *sizes = RoostWorkspaceSizes{};
+  sizes->device_bytes = p.tokens >= kRouteMinTokens ? MakeRouteArena(p.tokens, p.batch).total : 0;
   sizes->device_alignment = 256;
   return ROOST_STATUS_OK;
 }
 
 extern "C" ROOST_API RoostStatus roost_gdn_recurrent_run(RoostContext* ctx, const void* params, const RoostWorkspace* ws,
                                                          void* stream) {
-  using namespace roost;
-  if (ctx == nullptr || params == nullptr) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRule: ctx or params is NULL");
+  roost::Gate gate(kOp);
+  gate.Expect(ctx != nullptr && params != nullptr, ROOST_STATUS_INVALID_ARGUMENT, "a context and params are required");
+  ROOST_GATE_RETURN(gate);
   const auto& p = *static_cast<const RoostGatedDeltaRuleParams*>(params);
-  return Guarded("GatedDeltaRule", [&]() -> RoostStatus {
-    ROOST_TRY(Validate(p, false));
+  return roost::CatchAll(kOp, [&]() -> RoostStatus {
+    ROOST_RETURN_IF_FAILED(Admit(p, false));
     if (p.batch == 0 || p.tokens == 0) return ROOST_STATUS_OK;
-    if (p.tokens < kRouteMinTokens) return LaunchRecurrent(p, Stream(stream));
+    hipStream_t s = roost::Stream(stream);
+    if (p.tokens < kRouteMinTokens) return LaunchRecurrent(p, s);
     if (p.cu_seqlens_host != nullptr) {
       // The host copy says whether any sequence reaches kRouteMinTokens; if none does, the recurrent kernel runs every
       // sequence (so a graph captured from this call stays correct whatever lengths it is replayed with).
@@ -1100,119 +1123,110 @@ extern "C" ROOST_API RoostStatus roost_gdn_recurrent_run(RoostContext* ctx, cons
       for (uint32_t b = 0; b < p.batch && !any_long; ++b) {
         any_long = p.cu_seqlens_host[b + 1] - p.cu_seqlens_host[b] >= static_cast<int32_t>(kRouteMinTokens);
       }
-      if (!any_long) return LaunchRecurrent(p, Stream(stream));
+      if (!any_long) return LaunchRecurrent(p, s);
     }
     // Every launch size below follows from tokens and batch alone, so the call can be captured into a graph.
-    const ChunkLayout l = MakeRouteLayout(p.tokens, p.batch);
-    if (!DeviceWorkspaceOk(ws, l.total)) {
-      return Fail(ROOST_STATUS_WORKSPACE_TOO_SMALL,
-                  "GatedDeltaRule: workspace is missing or smaller than the workspace query said");
-    }
-    auto* base = static_cast<uint8_t*>(ws->device);
-    auto* chunks = reinterpret_cast<int4*>(base + l.chunk_table);
-    auto* seqs = reinterpret_cast<int4*>(base + l.seq_table);
-    auto* seq_list = reinterpret_cast<int32_t*>(base + l.seq_list);
-    // The long sequences on route -> prep -> scan, the short ones on the recurrent kernel, in that order on the
-    // caller's stream. (Running the two on two streams was slower: the short kernels lose more to sharing the chip
-    // than the overlap saves.) Two sequences of one call sharing a state slot leave the recurrent one's state.
-    hipStream_t s = Stream(stream);
-    hipLaunchKernelGGL(RouteKernel, dim3(1), dim3(1024), 0, s, static_cast<const int32_t*>(p.cu_seqlens.address),
-                       p.batch, l.max_chunks, chunks, seqs, seq_list, l.max_long);
-    ROOST_TRY(FromHip(hipGetLastError(), "GatedDeltaRule route launch"));
-    ROOST_TRY(LaunchChunk(p, ws, l, l.max_chunks, s));
-    return LaunchRecurrent(p, s, static_cast<int32_t>(kRouteMinTokens));
+    const ChunkArena l = MakeRouteArena(p.tokens, p.batch);
+    gate.Expect(roost::HasDeviceRegion(ws, l.total), ROOST_STATUS_WORKSPACE_TOO_SMALL,
+                "%u tokens may route sequences to the chunk kernels, which need %llu device workspace bytes",
+                p.tokens, static_cast<unsigned long long>(l.total));
+    ROOST_GATE_RETURN(gate);
+    return LaunchRouted(p, static_cast<uint8_t*>(ws->device), l, s);
   });
 }
 
 // ---- Chunk entry points ---------------------------------------------------------------------------------------------
 
 extern "C" ROOST_API RoostStatus roost_gdn_chunk_workspace(RoostContext*, const void* params, RoostWorkspaceSizes* sizes) {
-  using namespace roost;
-  if (params == nullptr || sizes == nullptr) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRule: params or sizes is NULL");
+  ROOST_RETURN_IF_FAILED(AdmitForSizing(params, sizes));
   const auto& p = *static_cast<const RoostGatedDeltaRuleParams*>(params);
-  if (p.struct_size < sizeof(RoostGatedDeltaRuleParams) || p.abi_minor > ROOST_ABI_MINOR) {
-    return Fail(ROOST_STATUS_ABI_MISMATCH, "GatedDeltaRule: params struct_size or abi_minor is not supported by this library");
-  }
-  if (p.tokens > kMaxTokens || p.batch > kMaxBatch) {
-    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRule: too many tokens or sequences for one call");
-  }
-  const ChunkLayout l = MakeChunkLayout(p.tokens, p.batch);
+  const ChunkArena l = MakeChunkArena(p.tokens, p.batch);
+  *sizes = RoostWorkspaceSizes{};
   sizes->device_bytes = l.total;
   sizes->pinned_host_bytes = l.tables_bytes;
-  sizes->plan_bytes = sizeof(PlanRecord);
+  sizes->plan_bytes = sizeof(ChunkStamp);
   sizes->device_alignment = 256;
   return ROOST_STATUS_OK;
 }
 
+// Writes the chunk table (sequence, first token, tokens) of every 64-token chunk and the per-sequence table (first
+// chunk, count, token range) into `host`; returns the chunk count, or -1 when cu_seqlens goes backwards at `*bad`.
+static int64_t FillChunkTables(const int32_t* cu, uint32_t batch, const ChunkArena& l, uint8_t* host, uint32_t* bad) {
+  auto* chunks = reinterpret_cast<int4*>(host + l.chunk_table);
+  auto* seqs = reinterpret_cast<int4*>(host + l.seq_table);
+  int32_t n = 0;
+  for (uint32_t b = 0; b < batch; ++b) {
+    const int32_t lo = cu[b], hi = cu[b + 1];
+    if (hi < lo) {
+      *bad = b;
+      return -1;
+    }
+    const int32_t first = n;
+    for (int32_t t = lo; t < hi; t += kChunk) chunks[n++] = int4{static_cast<int32_t>(b), t, std::min<int32_t>(kChunk, hi - t), 0};
+    seqs[b] = int4{first, n - first, lo, hi};
+  }
+  return n;
+}
+
 extern "C" ROOST_API RoostStatus roost_gdn_chunk_plan(RoostContext* ctx, const void* params, const RoostWorkspace* ws,
                                                       void* stream) {
-  using namespace roost;
-  if (ctx == nullptr || params == nullptr || ws == nullptr) {
-    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRule plan: ctx, params or workspace is NULL");
-  }
+  roost::Gate gate(kOp);
+  gate.Expect(ctx != nullptr && params != nullptr && ws != nullptr, ROOST_STATUS_INVALID_ARGUMENT,
+              "plan() needs a context, params and a workspace");
+  ROOST_GATE_RETURN(gate);
   const auto& p = *static_cast<const RoostGatedDeltaRuleParams*>(params);
-  return Guarded("GatedDeltaRule", [&]() -> RoostStatus {
-    ROOST_TRY(Validate(p, true));
-    const ChunkLayout l = MakeChunkLayout(p.tokens, p.batch);
-    if (!DeviceWorkspaceOk(ws, l.total) || ws->pinned_host == nullptr || ws->pinned_host_bytes < l.tables_bytes ||
-        ws->plan == nullptr || ws->plan_bytes < sizeof(PlanRecord)) {
-      return Fail(ROOST_STATUS_WORKSPACE_TOO_SMALL,
-                  "GatedDeltaRule plan: workspace is missing or smaller than the workspace query said");
+  return roost::CatchAll(kOp, [&]() -> RoostStatus {
+    ROOST_RETURN_IF_FAILED(Admit(p, true));
+    const ChunkArena l = MakeChunkArena(p.tokens, p.batch);
+    gate.Expect(roost::HasDeviceRegion(ws, l.total) && ws->pinned_host != nullptr &&
+                    ws->pinned_host_bytes >= l.tables_bytes && ws->plan != nullptr &&
+                    ws->plan_bytes >= sizeof(ChunkStamp),
+                ROOST_STATUS_WORKSPACE_TOO_SMALL,
+                "the call needs %llu device bytes, %llu pinned bytes and a %zu-byte plan record",
+                static_cast<unsigned long long>(l.total), static_cast<unsigned long long>(l.tables_bytes),
+                sizeof(ChunkStamp));
+    ROOST_GATE_RETURN(gate);
+    ChunkStamp stamp{kPlanMagic, p.batch, p.tokens, 0};
+    if (p.batch > 0 && p.tokens > 0) {
+      const int32_t* cu = p.cu_seqlens_host;
+      gate.Expect(cu[0] == 0 && static_cast<uint32_t>(cu[p.batch]) == p.tokens, ROOST_STATUS_INVALID_ARGUMENT,
+                  "cu_seqlens_host runs from %d to %d; it must run from 0 to tokens = %u", cu[0], cu[p.batch], p.tokens);
+      ROOST_GATE_RETURN(gate);
+      uint32_t bad = 0;
+      const int64_t n = FillChunkTables(cu, p.batch, l, static_cast<uint8_t*>(ws->pinned_host), &bad);
+      gate.Expect(n >= 0, ROOST_STATUS_INVALID_ARGUMENT, "cu_seqlens_host goes backwards at sequence %u", bad);
+      ROOST_GATE_RETURN(gate);
+      stamp.chunks = static_cast<uint32_t>(n);
+      ROOST_RETURN_IF_FAILED(roost::HipStatus(hipMemcpyAsync(ws->device, ws->pinned_host, l.seq_table + 16ull * p.batch,
+                                                             hipMemcpyHostToDevice, roost::Stream(stream)),
+                                              kOp, "copy of the chunk tables to the device"));
     }
-    PlanRecord rec{kPlanMagic, p.batch, p.tokens, 0};
-    if (p.batch == 0 || p.tokens == 0) {
-      std::memcpy(ws->plan, &rec, sizeof(rec));
-      return ROOST_STATUS_OK;
-    }
-    const int32_t* cu = p.cu_seqlens_host;
-    if (cu[0] != 0 || static_cast<uint32_t>(cu[p.batch]) != p.tokens) {
-      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRule plan: cu_seqlens_host must start at 0 and end at tokens");
-    }
-    auto* host = static_cast<uint8_t*>(ws->pinned_host);
-    auto* chunks = reinterpret_cast<int32_t*>(host + l.chunk_table);
-    auto* seqs = reinterpret_cast<int32_t*>(host + l.seq_table);
-    uint32_t n = 0;
-    for (uint32_t b = 0; b < p.batch; ++b) {
-      if (cu[b + 1] < cu[b]) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRule plan: cu_seqlens_host decreases");
-      seqs[4 * b] = static_cast<int32_t>(n);
-      seqs[4 * b + 2] = cu[b];
-      seqs[4 * b + 3] = cu[b + 1];
-      for (int32_t t = cu[b]; t < cu[b + 1]; t += kChunk) {
-        chunks[4 * n] = static_cast<int32_t>(b);
-        chunks[4 * n + 1] = t;
-        chunks[4 * n + 2] = std::min<int32_t>(kChunk, cu[b + 1] - t);
-        chunks[4 * n + 3] = 0;
-        ++n;
-      }
-      seqs[4 * b + 1] = static_cast<int32_t>(n) - seqs[4 * b];
-    }
-    rec.chunks = n;
-    ROOST_TRY(FromHip(hipMemcpyAsync(ws->device, host, l.seq_table + 16ull * p.batch, hipMemcpyHostToDevice,
-                                     Stream(stream)),
-                      "GatedDeltaRule plan copy"));
-    std::memcpy(ws->plan, &rec, sizeof(rec));
+    std::memcpy(ws->plan, &stamp, sizeof(stamp));
     return ROOST_STATUS_OK;
   });
 }
 
 extern "C" ROOST_API RoostStatus roost_gdn_chunk_run(RoostContext* ctx, const void* params, const RoostWorkspace* ws,
                                                      void* stream) {
-  using namespace roost;
-  if (ctx == nullptr || params == nullptr) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "GatedDeltaRule: ctx or params is NULL");
+  roost::Gate gate(kOp);
+  gate.Expect(ctx != nullptr && params != nullptr, ROOST_STATUS_INVALID_ARGUMENT, "a context and params are required");
+  ROOST_GATE_RETURN(gate);
   const auto& p = *static_cast<const RoostGatedDeltaRuleParams*>(params);
-  return Guarded("GatedDeltaRule", [&]() -> RoostStatus {
-    ROOST_TRY(Validate(p, false));
+  return roost::CatchAll(kOp, [&]() -> RoostStatus {
+    ROOST_RETURN_IF_FAILED(Admit(p, false));
     if (p.batch == 0 || p.tokens == 0) return ROOST_STATUS_OK;
-    const ChunkLayout l = MakeChunkLayout(p.tokens, p.batch);
-    if (!DeviceWorkspaceOk(ws, l.total) || ws->plan == nullptr || ws->plan_bytes < sizeof(PlanRecord)) {
-      return Fail(ROOST_STATUS_WORKSPACE_TOO_SMALL, "GatedDeltaRule: workspace or plan is missing or too small");
+    const ChunkArena l = MakeChunkArena(p.tokens, p.batch);
+    gate.Expect(roost::HasDeviceRegion(ws, l.total) && ws->plan != nullptr && ws->plan_bytes >= sizeof(ChunkStamp),
+                ROOST_STATUS_WORKSPACE_TOO_SMALL, "the call needs %llu device bytes and its plan record",
+                static_cast<unsigned long long>(l.total));
+    ROOST_GATE_RETURN(gate);
+    ChunkStamp stamp;
+    std::memcpy(&stamp, ws->plan, sizeof(stamp));
+    if (stamp.magic != kPlanMagic || stamp.batch != p.batch || stamp.tokens != p.tokens || stamp.chunks > l.max_chunks) {
+      return roost::Report(ROOST_STATUS_NOT_PLANNED, kOp, "no plan() for %u tokens in %u sequences in this workspace",
+                           p.tokens, p.batch);
     }
-    PlanRecord rec;
-    std::memcpy(&rec, ws->plan, sizeof(rec));
-    if (rec.magic != kPlanMagic || rec.batch != p.batch || rec.tokens != p.tokens || rec.chunks > l.max_chunks) {
-      return Fail(ROOST_STATUS_NOT_PLANNED, "GatedDeltaRule: plan() has not run for these tokens and sequences");
-    }
-    if (rec.chunks == 0) return ROOST_STATUS_OK;
-    return LaunchChunk(p, ws, l, rec.chunks, Stream(stream));
+    if (stamp.chunks == 0) return ROOST_STATUS_OK;
+    return LaunchChunk(p, ws, l, stamp.chunks, roost::Stream(stream));
   });
 }

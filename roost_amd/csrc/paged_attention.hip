@@ -84,8 +84,13 @@ struct PrefillWork {
   int32_t kbeg;
   int32_t kend;
   int32_t slot;
-  int32_t reserved;
+  int32_t ends;  // kPieceFirst | kPieceLast: whether this piece starts / ends its item's key range
 };
+// The kernels re-derive an item's outer key bounds from the device's kv_last_page_len (plan() may have assumed full
+// last pages when kv_last_page_len_host was NULL, or the lengths may have changed since): the first piece of an item
+// starts at the device's first visible key and the last piece ends at the device's last one.
+constexpr int32_t kPieceFirst = 1;
+constexpr int32_t kPieceLast = 2;
 struct PrefillMerge {
   int32_t seq;
   int32_t q0;
@@ -142,7 +147,7 @@ struct Layout {
   uint64_t dec_item_offset = 0, dec_range_offset = 0, dec_merge_offset = 0, dec_float_offset = 0;
 };
 
-// ---- Validation (reference: kernels/src/paged_attention.cu:78-130) ------------------------------------------------
+// ---- Admission ---------------------------------------------------------------------------------------------------
 
 // Query heads per KV head the kernels serve: groups of kGroup = 4, or 8, 16 and 32 as 2, 4 and 8 groups of 4 that read
 // the same KV rows (the reference builds 4 only).
@@ -153,91 +158,94 @@ uint32_t HeadShift(const RoostPagedAttentionParams& p) {
   return static_cast<uint32_t>(__builtin_ctz(p.q_heads / (p.kv_heads * kGroup)));
 }
 
-RoostStatus Validate(const RoostPagedAttentionParams& p, bool for_run) {
-  using roost::Fail;
-  constexpr char kOp[] = "PagedAttention";
-  if (p.mode != ROOST_ATTENTION_DECODE && p.mode != ROOST_ATTENTION_PREFILL) {
-    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: mode must be DECODE or PREFILL");
+// Shapes with a kernel here, per mode: head dims 64/128/256 decode; prefill on the tile kernel at 128 and 256
+// (128 needs page sizes that are powers of two and multiples of 16), on the general kernel at 256.
+bool PrefillShapeBuilt(const RoostPagedAttentionParams& p) {
+  if (p.head_dim == 256) return true;
+  return p.head_dim == 128 && p.page_size % 16 == 0 && roost::IsPow2(p.page_size);
+}
+
+// The host batch tables, as workspace() and plan() read them: q_indptr over [0, tokens], both indptrs
+// non-decreasing, last-page lengths in [1, page_size] for sequences that have pages, and (CpuOps.cs:326-329) a causal
+// prefill sequence holding at least as many keys as queries.
+void AdmitHostTables(const RoostPagedAttentionParams& p, roost::Gate& gate) {
+  gate.Expect(p.q_indptr_host != nullptr && p.kv_indptr_host != nullptr, ROOST_STATUS_INVALID_ARGUMENT,
+              "plan and workspace read q_indptr_host and kv_indptr_host; %s is NULL",
+              p.q_indptr_host == nullptr ? "q_indptr_host" : "kv_indptr_host");
+  if (!gate.ok()) return;
+  const int32_t* qi = p.q_indptr_host;
+  const int32_t* ki = p.kv_indptr_host;
+  gate.Expect(qi[0] == 0 && qi[p.batch] == static_cast<int32_t>(p.tokens), ROOST_STATUS_INVALID_ARGUMENT,
+              "q_indptr_host runs from %d to %d; it must run from 0 to tokens = %u", qi[0], qi[p.batch], p.tokens)
+      .Expect(ki[0] == 0, ROOST_STATUS_INVALID_ARGUMENT, "kv_indptr_host[0] = %d, must be 0", ki[0]);
+  for (uint32_t b = 0; b < p.batch && gate.ok(); ++b) {
+    gate.Expect(qi[b + 1] >= qi[b] && ki[b + 1] >= ki[b], ROOST_STATUS_INVALID_ARGUMENT,
+                "sequence %u: q_indptr_host or kv_indptr_host goes backwards", b);
+    const int64_t pages = ki[b + 1] - ki[b];
+    if (p.kv_last_page_len_host == nullptr || pages <= 0 || !gate.ok()) continue;
+    const int32_t last = p.kv_last_page_len_host[b];
+    gate.Expect(last >= 1 && last <= static_cast<int32_t>(p.page_size), ROOST_STATUS_INVALID_ARGUMENT,
+                "sequence %u: kv_last_page_len_host = %d outside 1..page_size (%u)", b, last, p.page_size);
+    if (p.mode == ROOST_ATTENTION_PREFILL && p.causal) {
+      const int64_t keys = (pages - 1) * p.page_size + last;
+      gate.Expect(keys >= qi[b + 1] - qi[b], ROOST_STATUS_INVALID_ARGUMENT,
+                  "sequence %u: causal prefill of %d queries over only %lld keys", b, qi[b + 1] - qi[b],
+                  static_cast<long long>(keys));
+    }
   }
-  if (p.head_dim != 64 && p.head_dim != 128 && p.head_dim != 256) {
-    return Fail(ROOST_STATUS_UNSUPPORTED, "PagedAttention: head_dim must be 64, 128 or 256");
-  }
-  if (p.mode == ROOST_ATTENTION_PREFILL && p.head_dim != 256 &&
-      !(p.head_dim == 128 && p.page_size % 16 == 0 && (p.page_size & (p.page_size - 1)) == 0)) {
-    return Fail(ROOST_STATUS_UNSUPPORTED,
-                "PagedAttention: prefill is built for head_dim 256, and for 128 with page sizes that are powers of two "
-                "and multiples of 16");
-  }
-  if (p.kv_heads == 0 || p.q_heads % p.kv_heads != 0 || !GroupBuilt(p.q_heads / p.kv_heads)) {
-    return Fail(ROOST_STATUS_UNSUPPORTED, "PagedAttention: 4, 8, 16 or 32 query heads per KV head are built");
-  }
-  if (p.window_left == 0) {
-    // CpuOps refuses a window of 0 (reference CpuOps.cs:180-186): bind -1 for no window.
-    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: window_left 0 is refused (-1 means no window)");
-  }
-  if (p.logits_soft_cap != 0.0f) return Fail(ROOST_STATUS_UNSUPPORTED, "PagedAttention: logit soft capping is not built");
-  if (p.kv_layout != ROOST_LAYOUT_PAGED_NHD && p.kv_layout != ROOST_LAYOUT_PAGED_HND) {
-    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: kv_layout must be PAGED_NHD or PAGED_HND");
-  }
-  if (p.batch == 0 || p.page_size == 0) {
-    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: batch and page_size must be non-zero");
-  }
-  if (p.mode == ROOST_ATTENTION_DECODE && p.tokens != p.batch) {
-    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: decode takes exactly one query token per sequence");
-  }
+}
+
+// The call's rules (the reference refuses a subset of these shapes: kernels/src/paged_attention.cu:78-130). `for_run`
+// checks the device spans; otherwise (workspace, plan) the host tables.
+RoostStatus Admit(const RoostPagedAttentionParams& p, bool for_run) {
+  roost::Gate gate("paged_attention");
+  const bool prefill = p.mode == ROOST_ATTENTION_PREFILL;
+  gate.Expect(p.mode == ROOST_ATTENTION_DECODE || prefill, ROOST_STATUS_INVALID_ARGUMENT,
+              "mode = %u is neither DECODE nor PREFILL", p.mode)
+      .Expect(p.head_dim == 64 || p.head_dim == 128 || p.head_dim == 256, ROOST_STATUS_UNSUPPORTED,
+              "head_dim = %u has no kernel here (built: 64, 128, 256)", p.head_dim)
+      .Expect(!prefill || PrefillShapeBuilt(p), ROOST_STATUS_UNSUPPORTED,
+              "prefill at head_dim = %u, page_size = %u has no kernel here (built: 256 at any page size; 128 at "
+              "power-of-two page sizes that are multiples of 16)", p.head_dim, p.page_size)
+      .Expect(p.kv_heads > 0 && p.q_heads % p.kv_heads == 0 && GroupBuilt(p.q_heads / std::max(p.kv_heads, 1u)),
+              ROOST_STATUS_UNSUPPORTED, "q_heads = %u over kv_heads = %u: built for groups of 4, 8, 16 or 32 query "
+              "heads per KV head", p.q_heads, p.kv_heads)
+      // CpuOps.cs:180-186: a window of 0 keys is an error; -1 (any negative value) means no window.
+      .Expect(p.window_left != 0, ROOST_STATUS_INVALID_ARGUMENT, "window_left = 0 is not a window; pass -1 for none")
+      .Expect(p.logits_soft_cap == 0.0f, ROOST_STATUS_UNSUPPORTED, "logits_soft_cap = %g: capping has no kernel here",
+              p.logits_soft_cap)
+      .Expect(p.kv_layout == ROOST_LAYOUT_PAGED_NHD || p.kv_layout == ROOST_LAYOUT_PAGED_HND,
+              ROOST_STATUS_INVALID_ARGUMENT, "kv_layout = %u is not a paged layout (NHD or HND)", p.kv_layout)
+      .Expect(p.batch > 0 && p.page_size > 0, ROOST_STATUS_INVALID_ARGUMENT,
+              "batch = %u, page_size = %u: both must be positive", p.batch, p.page_size)
+      .Expect(prefill || p.tokens == p.batch, ROOST_STATUS_INVALID_ARGUMENT,
+              "decode of %u tokens over %u sequences; decode is one query token per sequence", p.tokens, p.batch);
+  ROOST_GATE_RETURN(gate);
   if (!for_run) {
-    if (p.q_indptr_host == nullptr || p.kv_indptr_host == nullptr) {
-      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: q_indptr_host and kv_indptr_host are required");
-    }
-    if (p.q_indptr_host[0] != 0 || p.q_indptr_host[p.batch] != static_cast<int32_t>(p.tokens)) {
-      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: q_indptr_host must start at 0 and end at tokens");
-    }
-    if (p.kv_indptr_host[0] != 0) {
-      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: kv_indptr_host must start at 0 and not decrease");
-    }
-    for (uint32_t b = 0; b < p.batch; ++b) {
-      if (p.q_indptr_host[b + 1] < p.q_indptr_host[b] || p.kv_indptr_host[b + 1] < p.kv_indptr_host[b]) {
-        return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: q_indptr_host and kv_indptr_host must not decrease");
-      }
-      if (p.kv_last_page_len_host != nullptr && p.kv_indptr_host[b + 1] > p.kv_indptr_host[b]) {
-        const int32_t last = p.kv_last_page_len_host[b];
-        if (last < 1 || last > static_cast<int32_t>(p.page_size)) {
-          return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: kv_last_page_len_host outside [1, page_size]");
-        }
-      }
-      if (p.mode == ROOST_ATTENTION_PREFILL && p.causal && p.kv_last_page_len_host != nullptr) {
-        // CpuOps refuses a causal sequence with fewer keys than queries (reference CpuOps.cs:326-329).
-        const int64_t pages = p.kv_indptr_host[b + 1] - p.kv_indptr_host[b];
-        const int64_t kv = pages == 0 ? 0 : (pages - 1) * p.page_size + p.kv_last_page_len_host[b];
-        if (kv < p.q_indptr_host[b + 1] - p.q_indptr_host[b]) {
-          return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: a causal sequence has fewer keys than queries");
-        }
-      }
-    }
-    return ROOST_STATUS_OK;
+    AdmitHostTables(p, gate);
+    return gate.status();
   }
   const uint32_t dt = p.q.dtype;
-  if (dt != ROOST_DTYPE_BF16 && dt != ROOST_DTYPE_F32) {
-    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: q must be bf16 (or f32 for decode)");
-  }
-  if (dt == ROOST_DTYPE_F32 && p.mode == ROOST_ATTENTION_PREFILL) {
-    return Fail(ROOST_STATUS_UNSUPPORTED, "PagedAttention: f32 prefill is not built (bf16 MFMA only)");
-  }
+  gate.Expect(dt == ROOST_DTYPE_BF16 || dt == ROOST_DTYPE_F32, ROOST_STATUS_INVALID_ARGUMENT,
+              "q is %s; attention reads bf16 (or f32 in decode)", roost::Describe(dt).name)
+      .Expect(dt == ROOST_DTYPE_BF16 || !prefill, ROOST_STATUS_UNSUPPORTED,
+              "an f32 prefill has no kernel here (prefill runs on bf16 MFMA)");
+  ROOST_GATE_RETURN(gate);
   const uint64_t q_elems = static_cast<uint64_t>(p.tokens) * p.q_heads * p.head_dim;
-  ROOST_TRY(roost::CheckSpan(p.q, dt, q_elems, kOp, "q"));
-  ROOST_TRY(roost::CheckSpan(p.output, dt, q_elems, kOp, "output"));
-  ROOST_TRY(roost::CheckSpan(p.lse, ROOST_DTYPE_F32, static_cast<uint64_t>(p.tokens) * p.q_heads, kOp, "lse", true));
   const uint64_t page_elems = static_cast<uint64_t>(p.page_size) * p.kv_heads * p.head_dim;
-  ROOST_TRY(roost::CheckSpan(p.k_cache, dt, page_elems, kOp, "k_cache"));
-  ROOST_TRY(roost::CheckSpan(p.v_cache, dt, page_elems, kOp, "v_cache"));
-  ROOST_TRY(roost::CheckSpan(p.q_indptr, ROOST_DTYPE_I32, p.batch + 1ull, kOp, "q_indptr"));
-  ROOST_TRY(roost::CheckSpan(p.kv_indptr, ROOST_DTYPE_I32, p.batch + 1ull, kOp, "kv_indptr"));
-  ROOST_TRY(roost::CheckSpan(p.kv_last_page_len, ROOST_DTYPE_I32, p.batch, kOp, "kv_last_page_len"));
-  if (!roost::Aligned(p.q.address, 16) || !roost::Aligned(p.output.address, 16) ||
-      !roost::Aligned(p.k_cache.address, 16) || !roost::Aligned(p.v_cache.address, 16)) {
-    return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: q, output and the KV pools must be 16-byte aligned");
-  }
-  return ROOST_STATUS_OK;
+  gate.Tensor("q", p.q, dt, q_elems)
+      .Tensor("output", p.output, dt, q_elems)
+      .OptionalTensor("lse", p.lse, ROOST_DTYPE_F32, static_cast<uint64_t>(p.tokens) * p.q_heads)
+      .Tensor("k_cache", p.k_cache, dt, page_elems)
+      .Tensor("v_cache", p.v_cache, dt, page_elems)
+      .Tensor("q_indptr", p.q_indptr, ROOST_DTYPE_I32, p.batch + 1ull)
+      .Tensor("kv_indptr", p.kv_indptr, ROOST_DTYPE_I32, p.batch + 1ull)
+      .Tensor("kv_last_page_len", p.kv_last_page_len, ROOST_DTYPE_I32, p.batch)
+      .Aligned("q", p.q.address, 16)
+      .Aligned("output", p.output.address, 16)
+      .Aligned("k_cache", p.k_cache.address, 16)
+      .Aligned("v_cache", p.v_cache.address, 16);
+  return gate.status();
 }
 
 // ---- Host planning ---------------------------------------------------------------------------------------------------
@@ -253,10 +261,10 @@ Layout MakeLayout(uint64_t work_items, uint64_t ranges, uint64_t merges, uint64_
   const bool decode = mode == ROOST_ATTENTION_DECODE;
   const uint64_t item_bytes = decode ? sizeof(DecodeWork) : sizeof(PrefillWork);
   const uint64_t merge_bytes = decode ? sizeof(DecodeMerge) : sizeof(PrefillMerge);
-  l.range_offset = roost::AlignUp(work_items * item_bytes, 16);
-  l.merge_offset = roost::AlignUp(l.range_offset + (ranges > 0 ? (ranges + 1) * sizeof(int32_t) : 0), 16);
+  l.range_offset = roost::RoundUp(work_items * item_bytes, 16);
+  l.merge_offset = roost::RoundUp(l.range_offset + (ranges > 0 ? (ranges + 1) * sizeof(int32_t) : 0), 16);
   l.int_bytes = l.merge_offset + merges * merge_bytes;
-  l.float_offset = roost::AlignUp(l.int_bytes, kAlign);
+  l.float_offset = roost::RoundUp(l.int_bytes, kAlign);
   // decode partials: fp32 rows then (max, sum); prefill partials: bf16 rows then (max, sum)
   l.float_bytes = splits * rows_per_split *
                   (decode ? (static_cast<uint64_t>(head_dim) + 2) * sizeof(float) : 2 * static_cast<uint64_t>(head_dim) + 8);
@@ -360,9 +368,9 @@ void AppendDecode(const RoostPagedAttentionParams& p, const DecodePlan& d, Layou
   l.dec_ranges = d.ranges();
   l.dec_merges = d.merges.size();
   l.dec_splits = static_cast<uint64_t>(d.slots);
-  l.dec_item_offset = roost::AlignUp(l.int_bytes, 16);
-  l.dec_range_offset = roost::AlignUp(l.dec_item_offset + l.dec_items * sizeof(DecodeWork), 16);
-  l.dec_merge_offset = roost::AlignUp(l.dec_range_offset + d.range_ptr.size() * sizeof(int32_t), 16);
+  l.dec_item_offset = roost::RoundUp(l.int_bytes, 16);
+  l.dec_range_offset = roost::RoundUp(l.dec_item_offset + l.dec_items * sizeof(DecodeWork), 16);
+  l.dec_merge_offset = roost::RoundUp(l.dec_range_offset + d.range_ptr.size() * sizeof(int32_t), 16);
   l.int_bytes = l.dec_merge_offset + l.dec_merges * sizeof(DecodeMerge);
   if (host != nullptr) {
     std::memcpy(host + l.dec_item_offset, d.items.data(), d.items.size() * sizeof(DecodeWork));
@@ -374,8 +382,8 @@ void AppendDecode(const RoostPagedAttentionParams& p, const DecodePlan& d, Layou
 
 // Lays out the float region after the int region: the prefill partials (prefill_floats bytes), then the decode ones.
 void PlaceFloats(const RoostPagedAttentionParams& p, uint64_t prefill_floats, Layout& l) {
-  l.float_offset = roost::AlignUp(l.int_bytes, kAlign);
-  l.dec_float_offset = l.float_offset + roost::AlignUp(prefill_floats, kAlign);
+  l.float_offset = roost::RoundUp(l.int_bytes, kAlign);
+  l.dec_float_offset = l.float_offset + roost::RoundUp(prefill_floats, kAlign);
   l.float_bytes = (l.dec_float_offset - l.float_offset) +
                   l.dec_splits * p.q_heads * (static_cast<uint64_t>(p.head_dim) + 2) * sizeof(float);
   l.total = l.float_offset + l.float_bytes;
@@ -435,7 +443,7 @@ Layout PlanPrefill(const RoostPagedAttentionParams& p, uint32_t cus, unsigned ch
       for (uint32_t h = 0; h < VirtualHeads(p); ++h) {  // item per group of kGroup query heads
         items.push_back(Item{PrefillWork{static_cast<int32_t>(b), static_cast<int32_t>(q0), static_cast<int32_t>(h),
                                          static_cast<int32_t>(rows), static_cast<int32_t>(kbeg),
-                                         static_cast<int32_t>(kend), -1, 0},
+                                         static_cast<int32_t>(kend), -1, kPieceFirst | kPieceLast},
                              kend - kbeg + 64});
       }
     }
@@ -460,6 +468,7 @@ Layout PlanPrefill(const RoostPagedAttentionParams& p, uint32_t cus, unsigned ch
         w.kbeg = static_cast<int32_t>(it.w.kbeg + t0 * 64);
         w.kend = static_cast<int32_t>(std::min<int64_t>(it.w.kbeg + t1 * 64, it.w.kend));
         w.slot = slot++;
+        w.ends = (i == 0 ? kPieceFirst : 0) | (i == pieces - 1 ? kPieceLast : 0);
         cut.push_back(Item{w, (t1 - t0) * 64 + 64});
       }
     }
@@ -1475,7 +1484,14 @@ __global__ void __launch_bounds__(512, 1)
   const int32_t r = 32 * qt + col;  // this lane's query within the item
   const bool row_ok = r < wk.rows;
   const int32_t last_pos = static_cast<int32_t>(kv_len) - n + wk.q0 + 32 * qt + 31;  // the wavefront's last query
-  const int32_t kbeg = wk.kbeg, kend = wk.kend;
+  // The item's key range by the device's lengths: keys up to its last query (causal) or all keys, from its first
+  // query's window start rounded down to 16. The plan's cuts between pieces stay; the outer bounds follow the device.
+  const int32_t dev_first = static_cast<int32_t>(kv_len) - n + wk.q0;  // the item's first query position
+  const int32_t dev_end = max(0, causal ? min(static_cast<int32_t>(kv_len), dev_first + wk.rows)
+                                        : static_cast<int32_t>(kv_len));
+  const int32_t dev_beg = window < 0 ? 0 : (max(0, dev_first - window) & ~15);
+  const int32_t kbeg = (wk.ends & kPieceFirst) ? dev_beg : wk.kbeg;
+  const int32_t kend = (wk.ends & kPieceLast) ? dev_end : min(wk.kend, dev_end);
   const int ntiles = kend > kbeg ? (kend - kbeg + 63) / 64 : 0;
 
   // Q^T operands: qreg[ks] = q[query r][dims 16 ks + 8 hl .. +8].
@@ -1817,16 +1833,15 @@ RoostStatus LaunchDecode(const RoostPagedAttentionParams& p, const PlanRecord& r
                        lse, kv, kv.kv_indices, items, range_ptr, part_o, part_ml, q_rows, p.q_heads, hpw, scale_log2,
                        WindowOf(p));
   }
-  ROOST_TRY(roost::FromHip(hipGetLastError(), "PagedAttention decode launch"));
+  ROOST_RETURN_IF_FAILED(roost::HipStatus(hipGetLastError(), "paged_attention", "decode launch"));
   if (rec.dec_merges == 0) return ROOST_STATUS_OK;
   hipLaunchKernelGGL((DecodeMergeKernel<T, D>), dim3(static_cast<uint32_t>(rec.dec_merges * p.q_heads)), dim3(D), 0,
                      stream, out, lse, merges, part_o, part_ml, q_rows, p.q_heads);
-  return roost::FromHip(hipGetLastError(), "PagedAttention merge launch");
+  return roost::HipStatus(hipGetLastError(), "paged_attention", "decode merge launch");
 }
 
 RoostStatus LaunchPrefill(const RoostPagedAttentionParams& p, const PlanRecord& rec, unsigned char* dev, const KvView& kv,
                           float scale_log2, hipStream_t stream) {
-  using roost::FromHip;
   if (rec.work_items == 0) return ROOST_STATUS_OK;
   const auto* items = reinterpret_cast<const PrefillWork*>(dev);
   const auto* q_indptr = static_cast<const int32_t*>(p.q_indptr.address);
@@ -1846,7 +1861,7 @@ RoostStatus LaunchPrefill(const RoostPagedAttentionParams& p, const PlanRecord& 
       hipLaunchKernelGGL(PrefillTileKernel<256>, grid, dim3(512), 0, stream, q16, outp, lsep, kv, kv.kv_indices,
                          q_indptr, items, part_o, part_ml, p.q_heads, p.causal, ps_shift, scale_log2, WindowOf(p));
     }
-    ROOST_TRY(FromHip(hipGetLastError(), "PagedAttention prefill launch"));
+    ROOST_RETURN_IF_FAILED(roost::HipStatus(hipGetLastError(), "paged_attention", "prefill launch"));
     if (rec.merges == 0) return ROOST_STATUS_OK;
     const auto* mg = reinterpret_cast<const PrefillMerge*>(dev + rec.merge_offset);
     const uint32_t two = rec.merges_two, rest = static_cast<uint32_t>(rec.merges) - rec.merges_two;
@@ -1871,25 +1886,74 @@ RoostStatus LaunchPrefill(const RoostPagedAttentionParams& p, const PlanRecord& 
                            q_indptr, p.q_heads);
       }
     }
-    return FromHip(hipGetLastError(), "PagedAttention prefill merge launch");
+    return roost::HipStatus(hipGetLastError(), "paged_attention", "prefill merge launch");
   }
   hipLaunchKernelGGL(PrefillKernel, dim3(static_cast<uint32_t>(rec.work_items)), dim3(256), 0, stream,
                      static_cast<const uint16_t*>(p.q.address), outp, lsep, kv, q_indptr, items, p.q_heads, p.causal,
                      scale_log2, WindowOf(p));
-  return FromHip(hipGetLastError(), "PagedAttention prefill launch");
+  return roost::HipStatus(hipGetLastError(), "paged_attention", "prefill launch");
+}
+
+
+constexpr char kOp[] = "paged_attention";
+
+const RoostPagedAttentionParams* Params(const void* params) {
+  return static_cast<const RoostPagedAttentionParams*>(params);
+}
+
+// The plan record plan() leaves for run(): the batch shape it was made for and where its tables sit.
+PlanRecord MakeRecord(const RoostPagedAttentionParams& p, const Layout& l) {
+  PlanRecord r{};
+  r.magic = kPlanMagic;
+  r.mode = p.mode;
+  r.batch = p.batch;
+  r.tokens = p.tokens;
+  r.page_size = p.page_size;
+  r.kv_layout = p.kv_layout;
+  r.head_dim = p.head_dim;
+  r.kv_heads = p.kv_heads;
+  r.window = WindowOf(p);
+  r.merges_two = static_cast<uint32_t>(l.merges_two);
+  r.pages = static_cast<uint64_t>(p.kv_indptr_host[p.batch]);
+  r.work_items = l.work_items;
+  r.ranges = l.ranges;
+  r.merges = l.merges;
+  r.range_offset = l.range_offset;
+  r.merge_offset = l.merge_offset;
+  r.counter_offset = l.counter_offset;
+  r.splits = l.splits;
+  r.int_bytes = l.int_bytes;
+  r.float_offset = l.float_offset;
+  r.float_bytes = l.float_bytes;
+  r.dec_items = l.dec_items;
+  r.dec_ranges = l.dec_ranges;
+  r.dec_merges = l.dec_merges;
+  r.dec_splits = l.dec_splits;
+  r.dec_item_offset = l.dec_item_offset;
+  r.dec_range_offset = l.dec_range_offset;
+  r.dec_merge_offset = l.dec_merge_offset;
+  r.dec_float_offset = l.dec_float_offset;
+  return r;
+}
+
+bool RecordFits(const PlanRecord& r, const RoostPagedAttentionParams& p) {
+  return r.mode == p.mode && r.batch == p.batch && r.tokens == p.tokens && r.page_size == p.page_size &&
+         r.kv_layout == p.kv_layout && r.head_dim == p.head_dim && r.kv_heads == p.kv_heads && r.window == WindowOf(p);
 }
 
 }  // namespace
 
 extern "C" ROOST_API RoostStatus roost_paged_attention_workspace(RoostContext* ctx, const void* params,
                                                                  RoostWorkspaceSizes* sizes) {
-  using namespace roost;
-  ROOST_TRY(CheckHeader(params, sizeof(RoostPagedAttentionParams), "PagedAttention"));
-  if (sizes == nullptr) return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: sizes is NULL");
-  const auto& p = *static_cast<const RoostPagedAttentionParams*>(params);
-  return Guarded("PagedAttention", [&]() -> RoostStatus {
-    ROOST_TRY(Validate(p, false));
+  roost::Gate gate(kOp);
+  gate.Header(params, sizeof(RoostPagedAttentionParams))
+      .Expect(sizes != nullptr, ROOST_STATUS_INVALID_ARGUMENT, "the sizes out-pointer is NULL");
+  ROOST_GATE_RETURN(gate);
+  const auto& p = *Params(params);
+  return roost::CatchAll(kOp, [&]() -> RoostStatus {
+    ROOST_RETURN_IF_FAILED(Admit(p, false));
     const Layout l = PlanLayout(p, ComputeUnits(ctx), nullptr);
+    *sizes = RoostWorkspaceSizes{};
     sizes->device_bytes = l.total;
     sizes->pinned_host_bytes = l.int_bytes;
     sizes->plan_bytes = sizeof(PlanRecord);
@@ -1900,58 +1964,34 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_workspace(RoostContext* c
 
 extern "C" ROOST_API RoostStatus roost_paged_attention_plan(RoostContext* ctx, const void* params, const RoostWorkspace* ws,
                                                             void* stream) {
-  using namespace roost;
-  ROOST_TRY(CheckHeader(params, sizeof(RoostPagedAttentionParams), "PagedAttention"));
-  const auto& p = *static_cast<const RoostPagedAttentionParams*>(params);
-  return Guarded("PagedAttention", [&]() -> RoostStatus {
-    ROOST_TRY(Validate(p, false));
-    if (ws == nullptr || ws->plan == nullptr) {
-      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: plan needs a workspace with a plan record");
-    }
+  roost::Gate gate(kOp);
+  ROOST_GATE_RETURN(gate.Header(params, sizeof(RoostPagedAttentionParams)));
+  const auto& p = *Params(params);
+  return roost::CatchAll(kOp, [&]() -> RoostStatus {
+    ROOST_RETURN_IF_FAILED(Admit(p, false));
+    gate.Expect(ws != nullptr && ws->plan != nullptr, ROOST_STATUS_INVALID_ARGUMENT,
+                "plan() writes its record into ws->plan, which is missing");
+    ROOST_GATE_RETURN(gate);
     const uint32_t cus = ComputeUnits(ctx);
     const Layout l = PlanLayout(p, cus, nullptr);
-    if (ws->plan_bytes < sizeof(PlanRecord) || ws->device_bytes < l.total || ws->pinned_host_bytes < l.int_bytes ||
-        (l.int_bytes > 0 && ws->pinned_host == nullptr) || (l.total > 0 && ws->device == nullptr) ||
-        !Aligned(ws->device, kAlign)) {
-      return Fail(ROOST_STATUS_WORKSPACE_TOO_SMALL, "PagedAttention: workspace is smaller than the query reported");
-    }
-    auto* host = static_cast<unsigned char*>(ws->pinned_host);
+    const bool fits = ws->plan_bytes >= sizeof(PlanRecord) && ws->pinned_host_bytes >= l.int_bytes &&
+                      (l.int_bytes == 0 || ws->pinned_host != nullptr) && roost::HasDeviceRegion(ws, l.total, kAlign);
+    gate.Expect(fits, ROOST_STATUS_WORKSPACE_TOO_SMALL,
+                "this batch needs %llu device bytes (%u-aligned), %llu pinned bytes and a %zu-byte plan record; the "
+                "workspace has %llu, %llu and %llu", static_cast<unsigned long long>(l.total), kAlign,
+                static_cast<unsigned long long>(l.int_bytes), sizeof(PlanRecord),
+                static_cast<unsigned long long>(ws->device_bytes), static_cast<unsigned long long>(ws->pinned_host_bytes),
+                static_cast<unsigned long long>(ws->plan_bytes));
+    ROOST_GATE_RETURN(gate);
     if (l.int_bytes > 0) {
+      auto* host = static_cast<unsigned char*>(ws->pinned_host);
       std::memset(host, 0, l.int_bytes);
       PlanLayout(p, cus, host);
-      ROOST_TRY(FromHip(hipMemcpyAsync(ws->device, host, l.int_bytes, hipMemcpyHostToDevice, Stream(stream)),
-                        "PagedAttention plan copy"));
+      ROOST_RETURN_IF_FAILED(roost::HipStatus(
+          hipMemcpyAsync(ws->device, host, l.int_bytes, hipMemcpyHostToDevice, roost::Stream(stream)), kOp,
+          "copy of the work tables to the device"));
     }
-    PlanRecord rec{};
-    rec.magic = kPlanMagic;
-    rec.mode = p.mode;
-    rec.batch = p.batch;
-    rec.tokens = p.tokens;
-    rec.page_size = p.page_size;
-    rec.kv_layout = p.kv_layout;
-    rec.head_dim = p.head_dim;
-    rec.kv_heads = p.kv_heads;
-    rec.window = WindowOf(p);
-    rec.pages = static_cast<uint64_t>(p.kv_indptr_host[p.batch]);
-    rec.work_items = l.work_items;
-    rec.ranges = l.ranges;
-    rec.merges = l.merges;
-    rec.merges_two = static_cast<uint32_t>(l.merges_two);
-    rec.range_offset = l.range_offset;
-    rec.merge_offset = l.merge_offset;
-    rec.counter_offset = l.counter_offset;
-    rec.splits = l.splits;
-    rec.int_bytes = l.int_bytes;
-    rec.float_offset = l.float_offset;
-    rec.float_bytes = l.float_bytes;
-    rec.dec_items = l.dec_items;
-    rec.dec_ranges = l.dec_ranges;
-    rec.dec_merges = l.dec_merges;
-    rec.dec_splits = l.dec_splits;
-    rec.dec_item_offset = l.dec_item_offset;
-    rec.dec_range_offset = l.dec_range_offset;
-    rec.dec_merge_offset = l.dec_merge_offset;
-    rec.dec_float_offset = l.dec_float_offset;
+    const PlanRecord rec = MakeRecord(p, l);
     std::memcpy(ws->plan, &rec, sizeof(rec));
     return ROOST_STATUS_OK;
   });
@@ -1960,26 +2000,30 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_plan(RoostContext* ctx, c
 extern "C" ROOST_API RoostStatus roost_paged_attention_run(RoostContext*, const void* params, const RoostWorkspace* ws,
                                                            void* stream) {
   using namespace roost;
-  ROOST_TRY(CheckHeader(params, sizeof(RoostPagedAttentionParams), "PagedAttention"));
-  const auto& p = *static_cast<const RoostPagedAttentionParams*>(params);
-  return Guarded("PagedAttention", [&]() -> RoostStatus {
-    ROOST_TRY(Validate(p, true));
+  Gate gate(kOp);
+  ROOST_GATE_RETURN(gate.Header(params, sizeof(RoostPagedAttentionParams)));
+  const auto& p = *Params(params);
+  return CatchAll(kOp, [&]() -> RoostStatus {
+    ROOST_RETURN_IF_FAILED(Admit(p, true));
+    // C1: run() before plan() in this workspace is NOT_PLANNED (the caller then plans and runs again).
     if (ws == nullptr || ws->plan == nullptr || ws->plan_bytes < sizeof(PlanRecord)) {
-      return Fail(ROOST_STATUS_NOT_PLANNED, "PagedAttention: no plan record in the workspace");
+      return Report(ROOST_STATUS_NOT_PLANNED, kOp, "the workspace carries no plan record; call plan() first");
     }
     PlanRecord rec;
     std::memcpy(&rec, ws->plan, sizeof(rec));
-    if (rec.magic != kPlanMagic) return Fail(ROOST_STATUS_NOT_PLANNED, "PagedAttention: no plan was made in this workspace");
-    if (rec.mode != p.mode || rec.batch != p.batch || rec.tokens != p.tokens || rec.page_size != p.page_size ||
-        rec.kv_layout != p.kv_layout || rec.head_dim != p.head_dim || rec.kv_heads != p.kv_heads ||
-        rec.window != WindowOf(p)) {
-      return Fail(ROOST_STATUS_INVALID_ARGUMENT, "PagedAttention: the plan was made for another batch shape");
+    if (rec.magic != kPlanMagic) {
+      return Report(ROOST_STATUS_NOT_PLANNED, kOp, "the plan record is blank; call plan() first");
     }
-    ROOST_TRY(CheckSpan(p.kv_indices, ROOST_DTYPE_I32, rec.pages, "PagedAttention", "kv_indices"));
-    const uint64_t total = rec.float_offset + rec.float_bytes;
-    if (!DeviceWorkspaceOk(ws, total, kAlign)) {
-      return Fail(ROOST_STATUS_WORKSPACE_TOO_SMALL, "PagedAttention: device workspace is smaller than the plan");
-    }
+    gate.Expect(RecordFits(rec, p), ROOST_STATUS_INVALID_ARGUMENT,
+                "the plan record describes batch %u / tokens %u / mode %u / window %d; this call is batch %u / tokens "
+                "%u / mode %u / window %d (or its page size, layout, head shape differ)", rec.batch, rec.tokens,
+                rec.mode, rec.window, p.batch, p.tokens, p.mode, WindowOf(p))
+        .Tensor("kv_indices", p.kv_indices, ROOST_DTYPE_I32, rec.pages)
+        .Expect(HasDeviceRegion(ws, rec.float_offset + rec.float_bytes, kAlign), ROOST_STATUS_WORKSPACE_TOO_SMALL,
+                "the plan placed %llu bytes in the device workspace, which holds %llu",
+                static_cast<unsigned long long>(rec.float_offset + rec.float_bytes),
+                static_cast<unsigned long long>(ws->device_bytes));
+    ROOST_GATE_RETURN(gate);
     const float scale = p.sm_scale != 0.0f ? p.sm_scale : 1.0f / std::sqrt(static_cast<float>(p.head_dim));
     const float scale_log2 = scale * kLog2e;
     KvView kv{};
@@ -2011,7 +2055,7 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_run(RoostContext*, const 
     // The multi-token sequences on the tile kernels, then the single-token ones on the decode kernels (bf16, head_dim
     // 256 in prefill mode). Running the two side by side on two streams gains nothing: a tile workgroup needs two
     // 256-register wavefronts per SIMD, so it cannot share a CU with resident decode workgroups.
-    ROOST_TRY(LaunchPrefill(p, rec, dev, kv, scale_log2, s));
+    ROOST_RETURN_IF_FAILED(LaunchPrefill(p, rec, dev, kv, scale_log2, s));
     return p.head_dim == 128 ? LaunchDecode<uint16_t, 128>(p, rec, dev, kv, scale_log2, s)
                              : LaunchDecode<uint16_t, 256>(p, rec, dev, kv, scale_log2, s);
   });

@@ -63,7 +63,7 @@ namespace {
 
 thread_local std::string g_last_error;
 
-using roost::DtypeBit;
+using roost::DtypeMask;
 
 constexpr uint64_t HeadDimBit(uint32_t d) { return uint64_t{1} << (d / 16 - 1); }
 constexpr uint32_t kPaged = (1u << ROOST_LAYOUT_PAGED_NHD) | (1u << ROOST_LAYOUT_PAGED_HND);
@@ -79,8 +79,8 @@ RoostConstraints BaseConstraints() {
 
 RoostConstraints AttentionConstraints() {
   RoostConstraints c = BaseConstraints();
-  c.act_dtype_mask = DtypeBit(ROOST_DTYPE_BF16) | DtypeBit(ROOST_DTYPE_F32);
-  c.kv_dtype_mask = DtypeBit(ROOST_DTYPE_BF16) | DtypeBit(ROOST_DTYPE_F32);
+  c.act_dtype_mask = DtypeMask(ROOST_DTYPE_BF16) | DtypeMask(ROOST_DTYPE_F32);
+  c.kv_dtype_mask = DtypeMask(ROOST_DTYPE_BF16) | DtypeMask(ROOST_DTYPE_F32);
   c.head_dim_mask = HeadDimBit(64) | HeadDimBit(128) | HeadDimBit(256);
   c.layout_mask = kPaged;
   c.page_size_mask = kAnyPageSize;
@@ -91,7 +91,7 @@ RoostConstraints AttentionConstraints() {
 
 RoostConstraints CacheWriteConstraints() {
   RoostConstraints c = BaseConstraints();
-  c.act_dtype_mask = DtypeBit(ROOST_DTYPE_BF16) | DtypeBit(ROOST_DTYPE_F16) | DtypeBit(ROOST_DTYPE_F32);
+  c.act_dtype_mask = DtypeMask(ROOST_DTYPE_BF16) | DtypeMask(ROOST_DTYPE_F16) | DtypeMask(ROOST_DTYPE_F32);
   c.kv_dtype_mask = c.act_dtype_mask;
   c.head_dim_mask = ~uint64_t{0};
   c.layout_mask = kPaged;
@@ -102,7 +102,7 @@ RoostConstraints CacheWriteConstraints() {
 
 RoostConstraints GdnConstraints() {
   RoostConstraints c = BaseConstraints();
-  c.act_dtype_mask = DtypeBit(ROOST_DTYPE_BF16);
+  c.act_dtype_mask = DtypeMask(ROOST_DTYPE_BF16);
   c.head_dim_mask = HeadDimBit(128);
   c.layout_mask = 1u << ROOST_LAYOUT_ROW_MAJOR;
   c.min_alignment = 16;
@@ -121,7 +121,7 @@ RoostConstraints PlainConstraints(uint64_t act_mask, uint32_t alignment) {
 
 // QkNorm and Rope: bf16 or f32 heads of any even width up to 1024, element alignment (16-byte rows take vector loads).
 RoostConstraints HeadConstraints() {
-  RoostConstraints c = PlainConstraints(DtypeBit(ROOST_DTYPE_BF16) | DtypeBit(ROOST_DTYPE_F32), 2);
+  RoostConstraints c = PlainConstraints(DtypeMask(ROOST_DTYPE_BF16) | DtypeMask(ROOST_DTYPE_F32), 2);
   c.head_dim_mask = ~uint64_t{0};
   return c;
 }
@@ -129,7 +129,7 @@ RoostConstraints HeadConstraints() {
 // The fused QKV op writes NHD pages of the activation type, or f32 pages under bf16 activations.
 RoostConstraints QkvConstraints() {
   RoostConstraints c = HeadConstraints();
-  c.kv_dtype_mask = DtypeBit(ROOST_DTYPE_BF16) | DtypeBit(ROOST_DTYPE_F32);
+  c.kv_dtype_mask = DtypeMask(ROOST_DTYPE_BF16) | DtypeMask(ROOST_DTYPE_F32);
   c.layout_mask = 1u << ROOST_LAYOUT_PAGED_NHD;
   c.page_size_mask = kAnyPageSize;
   return c;
@@ -151,7 +151,7 @@ RoostOpEntry Entry(uint32_t op, uint32_t flags, const char* id, uint32_t params_
 }
 
 constexpr uint32_t kDet = ROOST_FLAG_DETERMINISTIC | ROOST_FLAG_BATCH_INVARIANT;
-constexpr uint64_t kBf16F32 = DtypeBit(ROOST_DTYPE_BF16) | DtypeBit(ROOST_DTYPE_F32);
+constexpr uint64_t kBf16F32 = DtypeMask(ROOST_DTYPE_BF16) | DtypeMask(ROOST_DTYPE_F32);
 
 const RoostOpEntry* Entries(uint32_t* count) {
   static const RoostOpEntry entries[] = {
@@ -204,10 +204,13 @@ ROOST_API uint32_t roost_abi_version(void) { return ROOST_ABI_VERSION; }
 ROOST_API const char* roost_last_error(void) { return g_last_error.c_str(); }
 
 ROOST_API RoostStatus roost_register(RoostOpTable* table) {
-  if (table == nullptr) return roost::Fail(ROOST_STATUS_INVALID_ARGUMENT, "roost_register: table is NULL");
-  if (table->struct_size < sizeof(RoostOpTable) || table->abi_minor > ROOST_ABI_MINOR) {
-    return roost::Fail(ROOST_STATUS_ABI_MISMATCH, "roost_register: table struct_size or abi_minor is not supported");
-  }
+  roost::Gate gate("register");
+  gate.Expect(table != nullptr, ROOST_STATUS_INVALID_ARGUMENT, "no op table to fill was passed");
+  ROOST_GATE_RETURN(gate);
+  gate.Expect(table->struct_size >= sizeof(RoostOpTable) && table->abi_minor <= ROOST_ABI_MINOR,
+              ROOST_STATUS_ABI_MISMATCH, "op table of %u bytes at ABI minor %u; this library fills %zu bytes at minor <= %u",
+              table->struct_size, table->abi_minor, sizeof(RoostOpTable), static_cast<uint32_t>(ROOST_ABI_MINOR));
+  ROOST_GATE_RETURN(gate);
   uint32_t count = 0;
   const RoostOpEntry* entries = Entries(&count);
   table->entry_size = static_cast<uint32_t>(sizeof(RoostOpEntry));
@@ -220,13 +223,13 @@ ROOST_API RoostStatus roost_register(RoostOpTable* table) {
 }
 
 ROOST_API RoostStatus roost_context_create(const RoostContextCreateParams* params, RoostContext** out) {
-  if (params == nullptr || out == nullptr) {
-    return roost::Fail(ROOST_STATUS_INVALID_ARGUMENT, "roost_context_create: params or out is NULL");
-  }
-  if (params->struct_size < sizeof(RoostContextCreateParams) || params->abi_minor > ROOST_ABI_MINOR) {
-    return roost::Fail(ROOST_STATUS_ABI_MISMATCH, "roost_context_create: params struct_size or abi_minor is not supported");
-  }
-  if (params->reserved0 != 0) return roost::Fail(ROOST_STATUS_INVALID_ARGUMENT, "roost_context_create: reserved0 must be zero");
+  roost::Gate gate("context_create");
+  gate.Expect(params != nullptr && out != nullptr, ROOST_STATUS_INVALID_ARGUMENT,
+              "both the create params and the out-pointer are required");
+  ROOST_GATE_RETURN(gate);
+  gate.Header(params, sizeof(RoostContextCreateParams))
+      .Expect(params->reserved0 == 0, ROOST_STATUS_INVALID_ARGUMENT, "reserved0 = %llu, must be 0", static_cast<unsigned long long>(params->reserved0));
+  ROOST_GATE_RETURN(gate);
   // The compute-unit count sizes the decode grid; without a visible device (CPU-only validation) 256 is assumed.
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, params->device) != hipSuccess || cus <= 0) {
@@ -234,8 +237,8 @@ ROOST_API RoostStatus roost_context_create(const RoostContextCreateParams* param
     cus = 256;
   }
   *out = new (std::nothrow) RoostContext{params->device, params->flags, static_cast<uint32_t>(cus)};
-  if (*out == nullptr) return roost::Fail(ROOST_STATUS_OUT_OF_MEMORY, "roost_context_create: out of host memory");
-  return ROOST_STATUS_OK;
+  gate.Expect(*out != nullptr, ROOST_STATUS_OUT_OF_MEMORY, "no host memory left for a context");
+  return gate.status();
 }
 
 ROOST_API RoostStatus roost_context_destroy(RoostContext* ctx) {

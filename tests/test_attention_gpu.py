@@ -517,3 +517,32 @@ def test_query_head_groups(session, name, mode, lens, ps, hnd, hq, hkv, d):
                                    hkv=hkv, d=d)
     got = run_case(session, b)
     check_against_oracle(got, b)
+
+
+# ---- plan() without kv_last_page_len_host ---------------------------------------------------------------------------
+# The reference's plan() needs only the q and kv indptr host tables (kernels/src/paged_attention.cu:107); the kernels
+# must then take every sequence's key count from the device's kv_last_page_len. With partial last pages the plan's
+# assumption (full pages) is wrong by up to page_size - 1 keys.
+
+NOLAST_CASES = [
+    ("non-causal hd256", [(32, 203), (70, 1001)], 16, False, False, -1, 256),
+    ("non-causal hd256 split", [(512, 4001), (3, 9)], 16, False, False, -1, 256),
+    ("causal hd256 split", [(512, 4001), (100, 233)], 16, False, True, -1, 256),
+    ("windowed hd256", [(300, 1201), (64, 77)], 16, False, True, 100, 256),
+    ("windowed hd256 split", [(512, 4001)], 16, False, True, 1500, 256),
+    ("windowed non-causal hd256 ps32", [(40, 505)], 32, False, False, 200, 256),
+    ("non-causal hd128", [(32, 203), (70, 1001)], 16, False, False, -1, 128),
+    ("windowed hd128 HND split", [(512, 4001), (64, 77)], 16, True, True, 1000, 128),
+    ("mixed step with decode rows", [(1, 901), (130, 705), (1, 4003)], 16, False, True, -1, 256),
+]
+
+
+@pytest.mark.parametrize("name,seqs,ps,hnd,causal,window,d", NOLAST_CASES, ids=[c[0] for c in NOLAST_CASES])
+def test_prefill_plan_without_last_page_len_host(session, name, seqs, ps, hnd, causal, window, d):
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    b = cases.make_paged_batch(rng, [s[1] for s in seqs], [s[0] for s in seqs], page_size=ps, hnd=hnd, d=d)
+    assert any(int(x) < ps for x in b.kv_last_page_len), "the case needs a partial last page"
+    dv = Dev(b, causal, window_left=window)
+    entry = session.lib.entry(roost_amd.ATTENTION_VARIANT)
+    session.launch(entry, dv.params(kv_last_page_len_host=None), key=("nolast", name))
+    check_against_oracle(dv.result(), b, causal=causal, window_left=window)
