@@ -92,6 +92,31 @@ def run_case(session, b: cases.PagedBatch, causal=True, check_nohost=True, check
     return cases.values(got, b.bf16)
 
 
+def torch_reference(b: cases.PagedBatch, causal=True) -> np.ndarray:
+    """The same attention in float32 torch on the GPU over de-paged K/V (NHD bf16 pools): the whole-batch check for
+    shapes too large for the double-precision CpuOps oracle."""
+    t = torch()
+    qv = t.from_numpy(cases.values(b.q, True).astype(np.float32)).cuda()
+    kc = t.from_numpy(cases.values(b.k_cache, True).astype(np.float32)).cuda()
+    vc = t.from_numpy(cases.values(b.v_cache, True).astype(np.float32)).cuda()
+    ref = np.zeros(b.q.shape, np.float64)
+    group = b.hq // b.hkv
+    for s in range(b.batch):
+        pages = t.from_numpy(b.kv_indices[b.kv_indptr[s]:b.kv_indptr[s + 1]].astype(np.int64)).cuda()
+        kl = int(b.kv_lens[s])
+        k = kc[pages].reshape(-1, b.hkv, b.d)[:kl]
+        v = vc[pages].reshape(-1, b.hkv, b.d)[:kl]
+        q = qv[b.q_indptr[s]:b.q_indptr[s + 1]]
+        qpos = t.arange(kl - q.shape[0], kl, device="cuda")
+        mask = t.arange(kl, device="cuda")[None, :] <= qpos[:, None]
+        for h in range(b.hq):
+            sc = (q[:, h, :] @ k[:, h // group, :].T) / float(np.sqrt(b.d))
+            if causal:
+                sc = sc.masked_fill(~mask, float("-inf"))
+            ref[b.q_indptr[s]:b.q_indptr[s + 1], h] = (t.softmax(sc, dim=-1) @ v[:, h // group, :]).cpu().numpy()
+    return ref
+
+
 def check_against_oracle(got, b, causal=True, window_left=-1):
     ref = cases.values(cases.oracle_attention(b, causal, window_left=window_left), b.bf16)
     a, r = cases.assert_close(got, ref, what="attention")
@@ -266,23 +291,7 @@ def test_config3_prefill_full_size(session):
     pre = rng.integers(0, 6145, size=8)
     b = cases.make_paged_batch(rng, n + pre, n, std=0.5, pool_factor=1.25)
     got = run_case(session, b, check_nohost=False, check_determinism=False)
-    qv = t.from_numpy(cases.values(b.q, True).astype(np.float32)).cuda()
-    kc = t.from_numpy(cases.values(b.k_cache, True).astype(np.float32)).cuda()
-    vc = t.from_numpy(cases.values(b.v_cache, True).astype(np.float32)).cuda()
-    ref = np.zeros_like(got)
-    for s in range(8):
-        pages = t.from_numpy(b.kv_indices[b.kv_indptr[s]:b.kv_indptr[s + 1]].astype(np.int64)).cuda()
-        kl = int(b.kv_lens[s])
-        k = kc[pages].reshape(-1, 2, 256)[:kl]
-        v = vc[pages].reshape(-1, 2, 256)[:kl]
-        q = qv[b.q_indptr[s]:b.q_indptr[s + 1]]
-        nq = q.shape[0]
-        qpos = t.arange(kl - nq, kl, device="cuda")
-        mask = t.arange(kl, device="cuda")[None, :] <= qpos[:, None]
-        for h in range(8):
-            sc = (q[:, h, :] @ k[:, h // 4, :].T) / 16.0
-            sc = sc.masked_fill(~mask, float("-inf"))
-            ref[b.q_indptr[s]:b.q_indptr[s + 1], h] = (t.softmax(sc, dim=-1) @ v[:, h // 4, :]).cpu().numpy()
+    ref = torch_reference(b)
     cases.assert_close(got, ref, what="config 3 vs fp32 torch")
     for s in (int(np.argmin(n + pre)), 3):
         one = cases.PagedBatch(b.q[b.q_indptr[s]:b.q_indptr[s + 1]].copy(), b.k_cache, b.v_cache,
@@ -303,22 +312,7 @@ def test_config5_mixed_step_attention(session):
     n = np.concatenate([np.ones(48, np.int64), [512, 512]])
     b = cases.make_paged_batch(rng, kv, n, std=0.5, pool_factor=1.25)
     got = run_case(session, b, check_nohost=False, check_determinism=True)
-    qv = t.from_numpy(cases.values(b.q, True).astype(np.float32)).cuda()
-    kc = t.from_numpy(cases.values(b.k_cache, True).astype(np.float32)).cuda()
-    vc = t.from_numpy(cases.values(b.v_cache, True).astype(np.float32)).cuda()
-    ref = np.zeros_like(got)
-    for s in range(50):
-        pages = t.from_numpy(b.kv_indices[b.kv_indptr[s]:b.kv_indptr[s + 1]].astype(np.int64)).cuda()
-        kl = int(b.kv_lens[s])
-        k = kc[pages].reshape(-1, 2, 256)[:kl]
-        v = vc[pages].reshape(-1, 2, 256)[:kl]
-        q = qv[b.q_indptr[s]:b.q_indptr[s + 1]]
-        qpos = t.arange(kl - q.shape[0], kl, device="cuda")
-        mask = t.arange(kl, device="cuda")[None, :] <= qpos[:, None]
-        for h in range(8):
-            sc = (q[:, h, :] @ k[:, h // 4, :].T) / 16.0
-            sc = sc.masked_fill(~mask, float("-inf"))
-            ref[b.q_indptr[s]:b.q_indptr[s + 1], h] = (t.softmax(sc, dim=-1) @ v[:, h // 4, :]).cpu().numpy()
+    ref = torch_reference(b)
     cases.assert_close(got, ref, what="config 5 attention vs fp32 torch")
     for s in (int(np.argmin(kv[:48])), int(np.argmax(kv[:48])), 49):
         one = cases.PagedBatch(b.q[b.q_indptr[s]:b.q_indptr[s + 1]].copy(), b.k_cache, b.v_cache,

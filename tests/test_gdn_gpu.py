@@ -137,21 +137,42 @@ def test_config4_chunked_prefill_then_recurrent_decode(session):
     cases.assert_close(cases.bf16_values(got_o), cases.bf16_values(want_o), what="config 4 chunk output")
     for s in range(4):
         cases.assert_close(got_pool[s], want_pool[s], max_abs=1.0, max_rel=cases.STATE_REL, what=f"config 4 state {s}")
-    # Decode: 128 states, 4 steps of one token each through the recurrent variant, chained through the pool.
-    dd = cases.make_gdn(rng, [1] * 128, 128, slots=list(range(128)), baseline_style=True)
+    _recurrent_chain(session, rng, states=128, steps=128)
+
+
+def _recurrent_chain(session, rng, states, steps):
+    """`steps` recurrent decode calls of one token per sequence on `states` states, chained through the pool; every
+    call's output is checked, and the final states after the last call. The CpuOps reference runs the whole chain as
+    one call of `steps`-token sequences (one call over n tokens = n one-token calls: HybridTests.cs:174-220)."""
+    dd = cases.make_gdn(rng, [1] * states, states, slots=list(range(states)), baseline_style=True)
+    fused = np.empty((steps, states, FUSED), np.uint16)
+    g = np.empty((steps, states, HEADS), np.float32)
+    beta = np.empty((steps, states, HEADS), np.uint16)
+    for t in range(steps):
+        sd = cases.make_gdn(rng, [1] * states, states, slots=list(range(states)), baseline_style=True)
+        fused[t], g[t], beta[t] = sd.fused, sd.g, sd.beta
+    # Sequence-major copy for the one-call reference: sequence b's tokens are steps 0..steps-1 of state b.
+    whole = cases.GdnData(np.ascontiguousarray(fused.transpose(1, 0, 2).reshape(-1, FUSED)),
+                          np.ascontiguousarray(g.transpose(1, 0, 2).reshape(-1, HEADS)),
+                          np.ascontiguousarray(beta.transpose(1, 0, 2).reshape(-1, HEADS)), dd.pool.copy(),
+                          np.arange(states, dtype=np.int32),
+                          (np.arange(states + 1) * steps).astype(np.int32), [steps] * states)
+    want_o, want_pool = cases.oracle_gdn(whole)
+    want_o = want_o.reshape(states, steps, HEADS, DIM)
     dev = DevGdn(dd)
-    pool_ref = dd.pool.copy()
-    for step in range(4):
-        step_data = cases.make_gdn(rng, [1] * 128, 128, slots=list(range(128)), baseline_style=True)
-        step_data.pool = pool_ref
-        want_o, pool_ref = cases.oracle_gdn(step_data)
-        dev.fused.copy_(to_dev(step_data.fused, True))
-        dev.g.copy_(to_dev(step_data.g))
-        dev.beta.copy_(to_dev(step_data.beta, True))
-        got_o, got_pool = run(session, dev, roost_amd.RECURRENT_VARIANT)
-        cases.assert_close(cases.bf16_values(got_o), cases.bf16_values(want_o), what=f"decode step {step}")
-    for s in range(128):
-        cases.assert_close(got_pool[s], pool_ref[s], max_abs=1.0, max_rel=cases.STATE_REL, what=f"decode state {s}")
+    for t in range(steps):
+        dev.fused.copy_(to_dev(fused[t], True))
+        dev.g.copy_(to_dev(g[t]))
+        dev.beta.copy_(to_dev(beta[t], True))
+        p = dev.params()
+        session.launch(session.lib.entry(roost_amd.RECURRENT_VARIANT), p, key=("chain", states))
+        if t % 16 == 0 or t == steps - 1:
+            got_o = from_dev(dev.out, True)[:states]
+            cases.assert_close(cases.bf16_values(got_o), cases.bf16_values(want_o[:, t]), what=f"decode step {t}")
+    got_pool = from_dev(dev.pool)
+    for s in range(states):
+        cases.assert_close(got_pool[s], want_pool[s], max_abs=1.0, max_rel=cases.STATE_REL,
+                           what=f"state {s} after {steps} steps")
 
 
 def test_rejections(session):
