@@ -18,6 +18,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 
 #include "common.h"
 
@@ -1228,5 +1229,71 @@ extern "C" ROOST_API RoostStatus roost_gdn_chunk_run(RoostContext* ctx, const vo
     }
     if (stamp.chunks == 0) return ROOST_STATUS_OK;
     return LaunchChunk(p, ws, l, stamp.chunks, roost::Stream(stream));
+  });
+}
+
+// ---- Allocation-free recurrent entry point -------------------------------------------------------------------------
+//
+// The recurrent variant with its routing scratch (chunk tables and per-(chunk, head) records of the sequences it hands
+// to the chunk kernels) in a file-scope device array instead of a caller workspace, for callers that cannot allocate.
+// Every call on a device shares that device's array, which keeps the last call's contents; RouteKernel rewrites every
+// table entry the chunk kernels read, and the prep kernel writes every record before the scan reads it, so nothing
+// has to start at zero. Calls that overlap on one device (two streams, two threads) race on the array.
+
+namespace {
+
+constexpr uint64_t kStaticScratchBytes = 48ull << 20;  // 48 MiB per device, held until the process ends
+constexpr int kMaxDevices = 64;
+
+__device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+std::mutex g_scratch_mutex;
+uint8_t* g_scratch_ptr[kMaxDevices] = {};  // device address of `scratch` on each device, once looked up
+
+// The device address of this device's `scratch`, looked up once per device with that device current. The array's
+// name is a host-side stand-in in host code; only this address may be handed to kernels.
+RoostStatus ScratchFor(int device, uint8_t** out) {
+  if (device < 0 || device >= kMaxDevices) {
+    return roost::Report(ROOST_STATUS_INVALID_ARGUMENT, kOp, "device %d is outside the %d devices this path tracks",
+                         device, kMaxDevices);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[device] == nullptr) {
+    void* ptr = nullptr;
+    ROOST_RETURN_IF_FAILED(
+        roost::HipStatus(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), kOp, "lookup of the static scratch array"));
+    g_scratch_ptr[device] = static_cast<uint8_t*>(ptr);
+  }
+  *out = g_scratch_ptr[device];
+  return ROOST_STATUS_OK;
+}
+
+}  // namespace
+
+extern "C" ROOST_API RoostStatus roost_amd_gdn_recurrent_run_noalloc(RoostContext* ctx, const void* params,
+                                                                     void* stream) {
+  roost::Gate gate(kOp);
+  gate.Expect(ctx != nullptr && params != nullptr, ROOST_STATUS_INVALID_ARGUMENT, "a context and params are required");
+  ROOST_GATE_RETURN(gate);
+  const auto& p = *static_cast<const RoostGatedDeltaRuleParams*>(params);
+  return roost::CatchAll(kOp, [&]() -> RoostStatus {
+    ROOST_RETURN_IF_FAILED(Admit(p, false));
+    if (p.batch == 0 || p.tokens == 0) return ROOST_STATUS_OK;
+    hipStream_t s = roost::Stream(stream);
+    if (p.tokens < kRouteMinTokens) return LaunchRecurrent(p, s);
+    const ChunkArena l = MakeRouteArena(p.tokens, p.batch);
+    gate.Expect(l.total <= kStaticScratchBytes, ROOST_STATUS_INVALID_ARGUMENT,
+                "%u tokens in %u sequences need %llu bytes of routing scratch; the allocation-free path holds %llu",
+                p.tokens, p.batch, static_cast<unsigned long long>(l.total),
+                static_cast<unsigned long long>(kStaticScratchBytes));
+    ROOST_GATE_RETURN(gate);
+    int current = -1;
+    ROOST_RETURN_IF_FAILED(roost::HipStatus(hipGetDevice(&current), kOp, "query of the current device"));
+    gate.Expect(current == ctx->device, ROOST_STATUS_INVALID_ARGUMENT,
+                "the context is for device %d but device %d is current", ctx->device, current);
+    ROOST_GATE_RETURN(gate);
+    uint8_t* base = nullptr;
+    ROOST_RETURN_IF_FAILED(ScratchFor(current, &base));
+    return LaunchRouted(p, base, l, s);
   });
 }
