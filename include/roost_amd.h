@@ -52,9 +52,9 @@ ROOST_API RoostStatus roost_gdn_recurrent_run(RoostContext* ctx, const void* par
 /* GatedDeltaRule recurrent variant without a workspace argument. This entry point has no counterpart in the reference:
  * it is for callers that cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc). It computes exactly what roost_gdn_recurrent_run computes, with the routing scratch (chunk
- * tables and per-(chunk, head) records of the sequences of 16+ tokens) in a static 48 MiB device array per GPU instead
+ * tables and per-(chunk, head) records of the sequences of 16+ tokens) in a static 24 MiB device array per GPU instead
  * of ws->device. A call whose routing could need more than the array (the workspace query of the recurrent variant
- * reports above 48 MiB: room for 74 chunks of 64 tokens x 16 heads, e.g. one 4,600-token sequence, or a worker step of
+ * reports above 24 MiB: room for 76 chunks of 64 tokens x 16 heads, e.g. one 4,700-token sequence, or a worker step of
  * 1,072 tokens over 50 sequences) is refused with ROOST_STATUS_INVALID_ARGUMENT before any launch. The context's device must be
  * current. Calls that overlap on one GPU race on its array. It calls no hipMalloc/hipFree. */
 ROOST_API RoostStatus roost_amd_gdn_recurrent_run_noalloc(RoostContext* ctx, const void* params, void* stream);

@@ -18,6 +18,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <cstddef>
 #include <mutex>
 
 #include "common.h"
@@ -273,8 +274,8 @@ GdnArgs MakeArgs(const RoostGatedDeltaRuleParams& p) {
 bool Vec16(const RoostGatedDeltaRuleParams& p) {
   auto Aligned = [](const void* a, uint64_t n) { return roost::IsAligned(a, n); };
   const uint64_t qs = Stride(p.q_stride), ks = Stride(p.k_stride), vs = Stride(p.v_stride);
-  return Aligned(p.q.address, 16) && Aligned(p.k.address, 16) && Aligned(p.v.address, 8) && qs % 8 == 0 &&
-         ks % 8 == 0 && vs % 4 == 0;
+  return Aligned(p.q.address, 16) && Aligned(p.k.address, 16) && Aligned(p.v.address, 16) && qs % 8 == 0 &&
+         ks % 8 == 0 && vs % 8 == 0;
 }
 
 RoostStatus LaunchRecurrent(const RoostGatedDeltaRuleParams& p, hipStream_t stream, int32_t route_min = 0) {
@@ -311,18 +312,8 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kTilePitch = 136;  // bf16 per LDS row of a [64 tokens][128 dims] q/k tile (272 B: 16-byte aligned)
-constexpr int kTokPitch = 72;    // bf16 per LDS row of a [dim or column][64 tokens] tile (144 B)
 constexpr int kVBlock = 32;      // value columns per scan workgroup
 constexpr uint32_t kVBlocks = kDim / kVBlock;
-
-// Per-(chunk, head) record written by the prep kernel, row-major bf16 matrices: T (hi and lo parts) and P as
-// [token t][token j], raw k transposed as [dim][token], then the per-token factors. The scan reads 16-byte pieces of
-// their rows as MFMA operands. Entries above the diagonal of T and P are written as zero.
-constexpr uint32_t kRecT = 0;          // T hi [64][64], then T lo [64][64]
-constexpr uint32_t kRecP = 16384;      // P [64][64]
-constexpr uint32_t kRecKT = 24576;     // k^T [128][64]
-constexpr uint32_t kRecScal = 40960;   // float [5][64]: e^G rk, beta, rq e^G, e^(Gn - G) rk, e^Gn (at [4][0])
-constexpr uint32_t kRecBytes = 42240;  // a multiple of 256
 
 struct ChunkArgs {
   GdnArgs a;
@@ -384,9 +375,79 @@ __device__ __forceinline__ f32x4_t MfmaF32(float a, float b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// One workgroup per (chunk, head); wave w owns row tile w (tokens 16w..16w+15) of the 64 x 64 products.
+__device__ __forceinline__ uint32_t LdsAddr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
+}
+
+// global -> LDS copies (global_load_lds): lane l's bytes land at lds + size * l; lds must be wave-uniform. Issued from
+// inline assembly so that the compiler does not treat every later LDS access as waiting on them (it cannot tell which
+// LDS bytes they write); the scan waits for them itself, one chunk later. M0 carries the LDS address and is restored.
+__device__ __forceinline__ void Dma16(const void* g, uint32_t lds) {
+  uint32_t save;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(save) : "v"(g), "s"(lds));
+}
+// s_waitcnt vmcnt(0) alone (expcnt and lgkmcnt fields at their maxima).
+__device__ __forceinline__ void WaitVmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+__device__ __forceinline__ float F4(const float4& v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// ---- Chunk variant: operand records and the WY scan ----------------------------------------------------------------
+//
+// WyPrepKernel (one workgroup per chunk and head, all in parallel) turns a chunk's raw rows into one 20 KB record of
+// ready-made MFMA operands: T = (I + A)^-1 split into bf16 hi and lo parts, P, and the per-token factors. WyScanKernel
+// (one workgroup of two wavefronts per sequence, head and 32-column value block) walks the chunks in order with the
+// state in registers: per chunk it copies the record and the raw k, q and v rows into LDS (global_load_lds, one chunk
+// ahead), and each wavefront advances its 16 state columns with no exchange between wavefronts.
+//
+// Operand layouts (v_mfma_f32_16x16x32_bf16: A lane l = row l%16, k-slots 8(l/16)..+7; B lane l = column l%16, same
+// k-slots; C lane l = column l%16, rows 4(l/16)+i). A product's C tiles feed the next product's B operand without any
+// exchange by ordering its k-slots to match: slot 8g + 4h + i of k-step s stands for row 32s + 16h + 4g + i of the C
+// tiles 2s (h = 0) and 2s + 1 (h = 1). The state S [128 x 16] lives in eight C tiles m = 2s + h whose row 4g + i is
+// state row 32s + 8g + 4h + i, so that the k-slots of S's B operand are 8 consecutive state rows and the k rows of
+// X = k S are plain 16-byte LDS reads; the transposed k operand of the state update is read with ds_read_b64_tr_b16 in
+// the same row order.
+
+namespace wy {
+
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kPairs = 6;                 // (token tile r, k-step s') on and below the diagonal: s' <= r / 2
+constexpr int kRecTHi = 0;                // [pair][64 lanes] uint4: T hi operands
+constexpr int kRecTLo = kPairs * 1024;    // T lo operands
+constexpr int kRecP = 2 * kPairs * 1024;  // P operands
+constexpr int kRecScal = 3 * kPairs * 1024;  // float [4][64] xs, beta, os, ws; then the chunk's decay
+constexpr int kRecBytes = 20 * 1024;      // 19.25 KB used, copied as 20 1 KB blocks
+__host__ __device__ constexpr int Pair(int r, int sp) { return r < 2 ? r : 2 * r - 2 + sp; }
+
+// 16-byte piece c (0..15) of row r of a 256-byte-row tile sits at piece c ^ Hsw(r): the 16 rows of a row tile then
+// spread a same-piece read over all banks, and so do the transposed reads (4 rows x 4 pieces).
+__device__ __forceinline__ int Hsw(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+__device__ __forceinline__ int T16(int r, int c) { return r * 256 + 16 * (c ^ Hsw(r)); }
+
+template <typename T>
+__device__ __forceinline__ T Lds(const uint8_t* base, int off) {
+  return *reinterpret_cast<const T*>(base + off);
+}
+
+__device__ __forceinline__ u32x2_t TrRead(const uint8_t* p) {
+  typedef short i16x4_t __attribute__((ext_vector_type(4)));
+  auto* ptr = reinterpret_cast<__attribute__((address_space(3))) i16x4_t*>(
+      const_cast<__attribute__((address_space(3))) char*>((const __attribute__((address_space(3))) char*)p));
+  return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(ptr));
+}
+
+}  // namespace wy
+
+// One workgroup per (chunk, head); wave w owns token tile w (tokens 16w .. 16w + 15) of the 64 x 64 products. The
+// arithmetic is the prep of the WY form: k.k^T and k.q^T on bf16 MFMA from the raw rows (exact products; the norms are
+// applied afterwards in fp32), T by blocked substitution in fp32 (16 x 16 diagonal blocks by forward substitution, the
+// blocks below on v_mfma_f32_16x16x4f32).
 template <bool kVec>
-__global__ void __launch_bounds__(256, 4) ChunkPrepKernel(ChunkArgs ca) {
+__global__ void __launch_bounds__(256, 4) WyPrepKernel(ChunkArgs ca) {
+  using namespace wy;
   const GdnArgs& a = ca.a;
   const int4 ch = ca.chunks[blockIdx.x];
   const uint32_t h = blockIdx.y;
@@ -450,8 +511,8 @@ __global__ void __launch_bounds__(256, 4) ChunkPrepKernel(ChunkArgs ca) {
   __syncthreads();
 
   // kk4[c] = k.k^T at rows 16w.., columns 16c..; pt4[c] = k.q^T at rows 16c.. (key tokens j), columns 16w.. (query
-  // tokens t), i.e. P^T, whose result lanes hold four consecutive j of one t: one 8-byte piece of a row of P. A row-major
-  // 16 x 32 tile supplies the A and the B operand in the same lane layout, so the k rows of tile c serve as both.
+  // tokens t), i.e. P^T, whose result lanes hold four consecutive j of one t. A row-major 16 x 32 tile supplies the A and
+  // the B operand in the same lane layout, so the k rows of tile c serve as both.
   f32x4_t kk4[4], pt4[4];
   {
     uint4 ak[4], bq[4];
@@ -474,42 +535,41 @@ __global__ void __launch_bounds__(256, 4) ChunkPrepKernel(ChunkArgs ca) {
       }
     }
   }
-  // Raw k transposed: 16-byte pieces k^T[d][8g .. 8g + 7]; consecutive lanes read consecutive dims of a row.
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const int piece = tid + 256 * m, d = piece & 127, g8 = piece >> 7;
-    uint32_t wd[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      wd[e] = static_cast<uint32_t>(qk[1][8 * g8 + 2 * e][d]) | (static_cast<uint32_t>(qk[1][8 * g8 + 2 * e + 1][d]) << 16);
-    }
-    *reinterpret_cast<uint4*>(rec + kRecKT + (d * 64 + 8 * g8) * 2) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
-  }
   __syncthreads();  // the q/k tiles are dead: region0 becomes A and T
 
+  // P operands of wave w's token tile: lane (kq, r16) holds P[t = 16w + r16][j = 16c + 4kq + i] in pt4[c], which is
+  // exactly its share of the operand of pair (w, s') for c = 2s' (slots 8kq..8kq+3) and c = 2s' + 1 (slots +4..+7).
+  {
+    float pv[4][4];
+    const int t = 16 * w + r16;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int j = 16 * c + 4 * kq + i;
+        pv[c][i] = (c <= w && j <= t) ? pt4[c][i] * rq_lds[t] * rk_lds[j] * expf(g_lds[t] - g_lds[j]) : 0.0f;
+      }
+#pragma unroll
+    for (int sp = 0; sp < 2; ++sp) {
+      if (sp <= w / 2) {
+        const uint4 op = make_uint4(PackRne(pv[2 * sp][0], pv[2 * sp][1]), PackRne(pv[2 * sp][2], pv[2 * sp][3]),
+                                    PackRne(pv[2 * sp + 1][0], pv[2 * sp + 1][1]),
+                                    PackRne(pv[2 * sp + 1][2], pv[2 * sp + 1][3]));
+        *reinterpret_cast<uint4*>(rec + kRecP + Pair(w, sp) * 1024 + 16 * lane) = op;
+      }
+    }
+  }
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    uint2 pw = make_uint2(0, 0);
-    float pv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      {  // A[r][j], r = 16w + 4kq + i, j = 16c + r16 (strictly lower); zero above the diagonal of A and T
-        const int r = 16 * w + 4 * kq + i, j = 16 * c + r16;
-        float av = 0.0f;
-        if (j < r) av = b_lds[r] * expf(g_lds[r] - g_lds[j]) * kk4[c][i] * rk_lds[r] * rk_lds[j];
-        a_lds[r][j] = av;
-        if (c > w) t_lds[r][j] = 0.0f;
-      }
-      {  // P[t][j], t = 16w + r16, j = 16c + 4kq + i (on and below the diagonal)
-        const int t = 16 * w + r16, j = 16 * c + 4 * kq + i;
-        pv[i] = j <= t ? pt4[c][i] * rq_lds[t] * rk_lds[j] * expf(g_lds[t] - g_lds[j]) : 0.0f;
-      }
+      // A[r][j], r = 16w + 4kq + i, j = 16c + r16 (strictly lower); zero above the diagonal of A and T
+      const int r = 16 * w + 4 * kq + i, j = 16 * c + r16;
+      float av = 0.0f;
+      if (j < r) av = b_lds[r] * expf(g_lds[r] - g_lds[j]) * kk4[c][i] * rk_lds[r] * rk_lds[j];
+      a_lds[r][j] = av;
+      if (c > w) t_lds[r][j] = 0.0f;
     }
-    if (c <= w) {
-      pw.x = PackRne(pv[0], pv[1]);
-      pw.y = PackRne(pv[2], pv[3]);
-    }
-    *reinterpret_cast<uint2*>(rec + kRecP + ((16 * w + r16) * 64 + 16 * c + 4 * kq) * 2) = pw;
   }
   __syncthreads();
 
@@ -552,18 +612,19 @@ __global__ void __launch_bounds__(256, 4) ChunkPrepKernel(ChunkArgs ca) {
     }
     __syncthreads();
   }
-  // T rows as bf16 hi + lo, 8 columns per piece.
+  // T operands, hi and lo, of wave w's token tile: lane (kq, r16) holds T[16w + r16][32s' + 16hh + 4kq + i].
 #pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    const int piece = tid + 256 * m, row = piece >> 3, c8 = piece & 7;
-    const float* src = &t_lds[row][8 * c8];
-    uint4 hi, lo;
-    Split2(src[0], src[1], hi.x, lo.x);
-    Split2(src[2], src[3], hi.y, lo.y);
-    Split2(src[4], src[5], hi.z, lo.z);
-    Split2(src[6], src[7], hi.w, lo.w);
-    *reinterpret_cast<uint4*>(rec + kRecT + (row * 64 + 8 * c8) * 2) = hi;
-    *reinterpret_cast<uint4*>(rec + kRecT + 8192 + (row * 64 + 8 * c8) * 2) = lo;
+  for (int sp = 0; sp < 2; ++sp) {
+    if (sp <= w / 2) {
+      const float* row = &t_lds[16 * w + r16][32 * sp + 4 * kq];
+      uint4 hi, lo;
+      Split2(row[0], row[1], hi.x, lo.x);
+      Split2(row[2], row[3], hi.y, lo.y);
+      Split2(row[16], row[17], hi.z, lo.z);
+      Split2(row[18], row[19], hi.w, lo.w);
+      *reinterpret_cast<uint4*>(rec + kRecTHi + Pair(w, sp) * 1024 + 16 * lane) = hi;
+      *reinterpret_cast<uint4*>(rec + kRecTLo + Pair(w, sp) * 1024 + 16 * lane) = lo;
+    }
   }
   if (tid < 64) {
     float* sc = reinterpret_cast<float*>(rec + kRecScal);
@@ -572,285 +633,290 @@ __global__ void __launch_bounds__(256, 4) ChunkPrepKernel(ChunkArgs ca) {
     sc[tid] = e * rk_lds[tid];
     sc[64 + tid] = b_lds[tid];
     sc[128 + tid] = rq_lds[tid] * e;
-    sc[192 + tid] = expf(gn - gt) * rk_lds[tid];
+    sc[192 + tid] = tid < n ? expf(gn - gt) * rk_lds[tid] : 0.0f;
     if (tid == 0) sc[256] = expf(gn);
   }
 }
 
-// Per wave and chunk, the record's rows that wave uses are copied into LDS by global_load_lds (no registers on the
-// way), double-buffered across chunks. 16-byte pieces are stored at swizzled positions so that the MFMA operand reads
-// (16 lanes reading the same piece index of 16 different rows) hit distinct banks.
-constexpr int kStageT = 0;         // T hi rows 16w..16w+15: [16][8 pieces of 16 B]
-constexpr int kStageTLo = 2048;    // T lo rows
-constexpr int kStageP = 4096;      // P rows
-constexpr int kStageKT = 6144;     // k^T rows 32w..32w+31: [32][8 pieces]
-constexpr int kStageScal = 10240;  // float [4][16]: e^G rk, beta, rq e^G, e^(Gn - G) rk of tokens 16w..16w+15
-constexpr int kStageBytes = 10496;
+namespace wy {
 
-// Position of 16-byte piece c8 of row r in a [rows][8 pieces] staging block.
-__device__ __forceinline__ int Swz(int r, int c8) { return r * 128 + 16 * (c8 ^ ((r >> 1) & 7)); }
-
-__device__ __forceinline__ uint32_t LdsAddr(const void* p) {
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
-}
-
-// global -> LDS copies (global_load_lds): lane l's bytes land at lds + size * l; lds must be wave-uniform. Issued from
-// inline assembly so that the compiler does not treat every later LDS access as waiting on them (it cannot tell which
-// LDS bytes they write); the scan waits for them itself, one chunk later. M0 carries the LDS address and is restored.
-__device__ __forceinline__ void Dma16(const void* g, uint32_t lds) {
-  uint32_t save;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
-               : "=&s"(save) : "v"(g), "s"(lds));
-}
-__device__ __forceinline__ void Dma4(const void* g, uint32_t lds) {
-  uint32_t save;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
-               : "=&s"(save) : "v"(g), "s"(lds));
-}
-
-// s_waitcnt vmcnt(0) alone (expcnt and lgkmcnt fields at their maxima).
-__device__ __forceinline__ void WaitVmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
-// The registers one wave needs for one chunk: its 16 raw k and q rows (MFMA A operands), its v values in the MFMA
-// result layout and the chunk's total decay.
-struct ChunkRegs {
-  uint4 kr[4], qr[4];
-  float vv[2][4];
-  float decay;
-  int t0, n;
+// One chunk's LDS stage: its record, the raw k and q rows (swizzled 16-byte pieces) and the v block.
+struct Stage {
+  uint8_t rec[kRecBytes];
+  uint8_t kt[64 * 256];
+  uint8_t qt[64 * 256];
+  uint8_t vt[64 * 64];  // [64 tokens][32 columns] bf16
+  uint8_t ob[64 * 64];  // the chunk's outputs [64 tokens][32 columns] bf16, written by the compute wavefronts
 };
 
-// Chunk c of a sequence starts at token sq.z + 64c; its record is number sq.x + c. Loads the wave's registers and
-// starts the copy of its record rows into `stage` (this wave's block of one buffer).
+// Starts the copies of chunk (t0, n)'s record and rows into `st`; wave 0 copies the record and v, wave 1 k and q.
+// Rows past the chunk's end repeat its last row (their factors are zero).
+// global -> LDS copy with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane byte offset: lane l's 16 bytes land
+// at lds + 16 l. M0 carries the LDS address and is restored.
+__device__ __forceinline__ void DmaS(const void* sbase, uint32_t voff, uint32_t lds) {
+  uint32_t save;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+               : "=&s"(save) : "v"(voff), "s"(sbase), "s"(lds));
+}
+
+__device__ __forceinline__ uint32_t Uniform(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// Per-lane byte offsets of a full chunk's copies, fixed for the whole scan. Instruction i of the k (or q) copy fills
+// rows 4i .. 4i + 3: lane l takes row 4i + l / 16 and fetches the piece that lands at position l % 16, which is
+// (l % 16) ^ Hsw(row) = (l % 16) ^ 4 (l / 16) ^ (i % 4); the row part 4i * stride is wave-uniform and goes into the base.
+struct CopyOffsets {
+  uint32_t k[4], q[4];  // by i % 4
+  uint32_t v;           // v block: instruction i copies tokens 16i .. 16i + 15, 4 lanes x 16 bytes per token
+  uint32_t rec;         // 16 bytes per lane of each 1 KB record block
+};
+
+__device__ __forceinline__ CopyOffsets MakeCopyOffsets(const GdnArgs& a, uint32_t h, uint32_t vb, int lane) {
+  CopyOffsets o;
+  const uint32_t rr = static_cast<uint32_t>(lane) >> 4, pos = static_cast<uint32_t>(lane) & 15;
+#pragma unroll
+  for (uint32_t j = 0; j < 4; ++j) {
+    const uint32_t piece = pos ^ (rr << 2) ^ j;
+    o.k[j] = static_cast<uint32_t>(rr * a.k_stride * 2) + h * 256 + 16 * piece;
+    o.q[j] = static_cast<uint32_t>(rr * a.q_stride * 2) + h * 256 + 16 * piece;
+  }
+  o.v = static_cast<uint32_t>((static_cast<uint32_t>(lane) >> 2) * a.v_stride * 2) + h * 256 + vb * 64 +
+        16 * (static_cast<uint32_t>(lane) & 3);
+  o.rec = 16 * static_cast<uint32_t>(lane);
+  return o;
+}
+
+// Views that are not 16-byte aligned (kVec false) are read into registers and written to LDS instead; so are the rows
+// of a chunk shorter than 64 tokens, whose rows past the end repeat its last row (their factors are zero).
 template <bool kVec>
-__device__ __forceinline__ void LoadChunk(const ChunkArgs& ca, const int4& sq, int c, uint32_t h, uint32_t vb, int w,
-                                          int lane, ChunkRegs& r, uint8_t* stage) {
-  const GdnArgs& a = ca.a;
-  const uint32_t chunk = static_cast<uint32_t>(sq.x + c);
-  r.t0 = sq.z + static_cast<int>(kChunk) * c;
-  r.n = min(static_cast<int>(kChunk), sq.w - r.t0);
-  const int r16 = lane & 15, kq = lane >> 4;
-  const int row = 16 * w + r16;
-  const bool ok = row < r.n;
-  const uint64_t tok = static_cast<uint64_t>(r.t0 + (ok ? row : r.n - 1));
-  const uint16_t* kp = a.k + tok * a.k_stride + h * kDim + 8 * kq;
-  const uint16_t* qp = a.q + tok * a.q_stride + h * kDim + 8 * kq;
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const uint4 kv = Load8<kVec>(kp + 32 * s), qv = Load8<kVec>(qp + 32 * s);
-    r.kr[s] = ok ? kv : make_uint4(0, 0, 0, 0);
-    r.qr[s] = ok ? qv : make_uint4(0, 0, 0, 0);
+__device__ __forceinline__ void Copy16(const uint16_t* src, uint8_t* tile, uint32_t tile_lds, int block, int lane) {
+  if constexpr (kVec) {
+    Dma16(src, tile_lds + 1024 * block);
+  } else {
+    *reinterpret_cast<uint4*>(tile + 1024 * block + 16 * lane) = Load8<false>(src);
   }
+}
+
+// Copies chunk (t0, n)'s record and rows into `st`: copier 0 the record and the v block, copier 1 the k and q rows.
+// `lds` is the LDS byte address of `st` (computed once, outside the loop, from the stage array).
+template <bool kVec>
+__device__ __forceinline__ void Fetch(const GdnArgs& a, const CopyOffsets& co, const uint8_t* recp, int t0, int n,
+                                      uint32_t h, uint32_t vb, int copier, int lane, Stage& st, uint32_t lds) {
+  const bool full = kVec && n == 64;
+  const uint32_t l_rec = lds + offsetof(Stage, rec), l_kt = lds + offsetof(Stage, kt), l_qt = lds + offsetof(Stage, qt),
+                 l_vt = lds + offsetof(Stage, vt);
+  if (copier == 0) {
+#pragma unroll
+    for (int b = 0; b < kRecBytes / 1024; ++b) DmaS(recp + 1024 * b, co.rec, l_rec + 1024 * b);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // 16 tokens of 4 x 16 bytes per instruction
+      if (full) {
+        const auto* vbase = reinterpret_cast<const uint8_t*>(a.v) + static_cast<uint64_t>(t0 + 16 * i) * a.v_stride * 2;
+        DmaS(vbase, co.v, l_vt + 1024 * i);
+      } else {
+        const int row = 16 * i + (lane >> 2);
+        const uint16_t* src = a.v + static_cast<uint64_t>(t0 + min(row, n - 1)) * a.v_stride + h * kDim + vb * 32 +
+                              8 * (lane & 3);
+        Copy16<kVec>(src, st.vt, l_vt, i, lane);
+      }
+    }
+  } else if (full) {
+    const auto* kb = reinterpret_cast<const uint8_t*>(a.k) + static_cast<uint64_t>(t0) * a.k_stride * 2;
+    const auto* qb = reinterpret_cast<const uint8_t*>(a.q) + static_cast<uint64_t>(t0) * a.q_stride * 2;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      DmaS(kb + 4ull * i * a.k_stride * 2, co.k[i & 3], l_kt + 1024 * i);
+      DmaS(qb + 4ull * i * a.q_stride * 2, co.q[i & 3], l_qt + 1024 * i);
+    }
+  } else {
+    const int rr = lane >> 4, pos = lane & 15;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int row = 4 * i + rr;
+      const int piece = pos ^ Hsw(row);
+      const uint64_t tok = static_cast<uint64_t>(t0 + min(row, n - 1));
+      Copy16<kVec>(a.k + tok * a.k_stride + h * kDim + 8 * piece, st.kt, l_kt, i, lane);
+      Copy16<kVec>(a.q + tok * a.q_stride + h * kDim + 8 * piece, st.qt, l_qt, i, lane);
+    }
+  }
+}
+
+// Writes a chunk's outputs from its LDS block to the output rows (copier 0): 16 tokens of 4 x 16 bytes per instruction.
+__device__ __forceinline__ void StoreOut(const GdnArgs& a, const Stage& st, int t0, int n, uint32_t h, uint32_t vb,
+                                         int lane) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int rv = 16 * w + 4 * kq + i;
-    const bool okv = rv < r.n;
-    const uint16_t* vp = a.v + static_cast<uint64_t>(r.t0 + (okv ? rv : r.n - 1)) * a.v_stride + h * kDim +
-                         vb * kVBlock + r16;
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const float x = Bf16ToF32(vp[16 * nt]);
-      r.vv[nt][i] = okv ? x : 0.0f;
-    }
-  }
-  const uint8_t* rec = ca.recs + (static_cast<uint64_t>(chunk) * kHeads + h) * kRecBytes;
-  r.decay = reinterpret_cast<const float*>(rec + kRecScal)[256];
-  // Record rows into LDS: lane l fills byte 16 l of each 1 KB instruction block.
-  const uint32_t base = LdsAddr(stage);
-  const int rr = lane >> 3, pos = lane & 7;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int rw = 8 * i + rr, c8 = pos ^ ((rw >> 1) & 7);
-    const uint8_t* src = rec + ((16 * w + rw) * 64 + 8 * c8) * 2;
-    Dma16(src + kRecT, base + kStageT + 1024 * i);
-    Dma16(src + kRecT + 8192, base + kStageTLo + 1024 * i);
-    Dma16(src + kRecP, base + kStageP + 1024 * i);
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int rw = 8 * i + rr, c8 = pos ^ ((rw >> 1) & 7);
-    Dma16(rec + kRecKT + ((32 * w + rw) * 64 + 8 * c8) * 2, base + kStageKT + 1024 * i);
-  }
-  Dma4(rec + kRecScal + ((lane >> 4) * 64 + 16 * w + r16) * 4, base + kStageScal);
-}
-
-// A chunk's output values of one lane, stored one chunk later (so that the wait at the top of a chunk never waits on
-// stores issued just before it).
-struct ChunkOut {
-  uint16_t o[2][4];
-  int t0, n;
-};
-
-__device__ __forceinline__ void StoreOut(const GdnArgs& a, const ChunkOut& r, uint32_t h, uint32_t vb, int w, int r16,
-                                         int kq) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int t = 16 * w + 4 * kq + i;
-    if (t < r.n) {
-      uint16_t* op = a.out + (static_cast<uint64_t>(r.t0 + t) * kHeads + h) * kDim + vb * kVBlock + r16;
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) op[16 * nt] = r.o[nt][i];
+    const int t = 16 * i + (lane >> 2);
+    const uint4 v = *reinterpret_cast<const uint4*>(st.ob + t * 64 + 16 * (lane & 3));
+    if (t < n) {
+      *reinterpret_cast<uint4*>(a.out + (static_cast<uint64_t>(t0 + t) * kHeads + h) * kDim + vb * 32 + 8 * (lane & 3)) = v;
     }
   }
 }
 
-__device__ __forceinline__ float F4(const float4& v, int i) {
-  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
-}
+// One chunk of the scan for one wavefront's 16 state columns. With one wavefront per SIMD nothing hides an LDS read's
+// latency but the wavefront's own work, so every phase keeps its operand reads a few multiplies ahead (register rings
+// whose order sched_group_barrier pins) and loads the next phase's factors while the current one multiplies.
+__device__ __forceinline__ void Advance(Stage& sg, f32x4_t (&st)[8], int w, int lane) {
+  const int g = lane >> 4, m = lane & 15;
+  const float* sc = reinterpret_cast<const float*>(sg.rec + kRecScal);
+  // Per-lane LDS offsets of the k / q operand of (row tile r, k-step s): row 16r + m, piece 4s + g.
+  auto kq_off = [&](int r, int s) { return T16(16 * r + m, 4 * s + g); };
 
-template <typename T>
-__device__ __forceinline__ T LdsRead(const uint8_t* p) {
-  return *reinterpret_cast<const T*>(p);
-}
-
-// One chunk of the scan (see ChunkScanKernel); `stage` is this wave's staged record block for the chunk.
-__device__ __forceinline__ void ScanStep(const GdnArgs& a, const ChunkRegs& cur, const uint8_t* stage,
-                                         f32x4_t (&st)[2][2], uint32_t h, uint32_t vb, int w, int r16, int kq,
-                                         uint16_t (&s_lds)[2][kVBlock][kTilePitch],
-                                         uint16_t (&y_lds)[2][kVBlock][kTokPitch],
-                                         uint16_t (&vn_lds)[3][kVBlock][kTokPitch], ChunkOut& out) {
-  // (1) S as bf16 hi/lo B operands.
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      uint2 hi, lo;
-      Split2(st[mt][nt][0], st[mt][nt][1], hi.x, lo.x);
-      Split2(st[mt][nt][2], st[mt][nt][3], hi.y, lo.y);
-      const int d0 = 32 * w + 16 * mt + 4 * kq, col = 16 * nt + r16;
-      *reinterpret_cast<uint2*>(&s_lds[0][col][d0]) = hi;
-      *reinterpret_cast<uint2*>(&s_lds[1][col][d0]) = lo;
-    }
-  }
-  __syncthreads();
-  // (2) X = k S0 (hi + lo) and q S0 (hi) for tokens 16w..16w+15; Y = beta (v - e^G rk X).
-  uint4 bh[4][2], bl[4][2];
+  // (1) S as bf16 hi / lo B operands: k-step s covers state rows 32s .. 32s + 31.
+  uint4 sh[4], sl[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
+    Split2(st[2 * s][0], st[2 * s][1], sh[s].x, sl[s].x);
+    Split2(st[2 * s][2], st[2 * s][3], sh[s].y, sl[s].y);
+    Split2(st[2 * s + 1][0], st[2 * s + 1][1], sh[s].z, sl[s].z);
+    Split2(st[2 * s + 1][2], st[2 * s + 1][3], sh[s].w, sl[s].w);
+  }
+  // (2) X = k S as hi and lo partial sums and q S (hi), over (s, r) in s-major order so that consecutive multiplies
+  // hit different accumulators; a ring keeps the k / q reads kRing steps ahead.
+  constexpr int kRing = 3;
+  f32x4_t xh[4], xl[4], oq[4];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      bh[s][nt] = *reinterpret_cast<const uint4*>(&s_lds[0][16 * nt + r16][32 * s + 8 * kq]);
-      bl[s][nt] = *reinterpret_cast<const uint4*>(&s_lds[1][16 * nt + r16][32 * s + 8 * kq]);
+  for (int r = 0; r < 4; ++r) xh[r] = xl[r] = oq[r] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  uint4 rk[kRing], rq[kRing];
+#pragma unroll
+  for (int j = 0; j < kRing; ++j) {
+    rk[j] = Lds<uint4>(sg.kt, kq_off(j & 3, j >> 2));
+    rq[j] = Lds<uint4>(sg.qt, kq_off(j & 3, j >> 2));
+  }
+  // The factors of phase (3) and the v block, read while the multiplies run.
+  float4 xf[4], bf[4];
+  u32x2_t vr[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    xf[r] = *reinterpret_cast<const float4*>(sc + 16 * r + 4 * g);
+    bf[r] = *reinterpret_cast<const float4*>(sc + 64 + 16 * r + 4 * g);
+    vr[r] = TrRead(sg.vt + (16 * r + 4 * g + (m >> 2)) * 64 + 32 * w + 8 * (m & 3));
+  }
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int r = j & 3, s = j >> 2;
+    const uint4 ak = rk[j % kRing], aq = rq[j % kRing];
+    if (j + kRing < 16) {
+      rk[j % kRing] = Lds<uint4>(sg.kt, kq_off((j + kRing) & 3, (j + kRing) >> 2));
+      rq[j % kRing] = Lds<uint4>(sg.qt, kq_off((j + kRing) & 3, (j + kRing) >> 2));
     }
+    xh[r] = Mfma(ak, sh[s], xh[r]);
+    xl[r] = Mfma(ak, sl[s], xl[r]);
+    oq[r] = Mfma(sh[s], aq, oq[r]);  // (q S)^T: lane (g, m) gets columns 4g .. 4g + 3 of token 16r + m
   }
-  f32x4_t xs4[2], oq4[2];
+
+  // T operands of phase (4), read while phase (3)'s arithmetic runs.
+  uint4 th[kPairs], tl[kPairs];
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) xs4[nt] = oq4[nt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      xs4[nt] = Mfma(cur.kr[s], bh[s][nt], xs4[nt]);
-      oq4[nt] = Mfma(cur.qr[s], bh[s][nt], oq4[nt]);
-    }
+  for (int q = 0; q < kPairs; ++q) {
+    th[q] = Lds<uint4>(sg.rec, kRecTHi + q * 1024 + 16 * lane);
+    tl[q] = Lds<uint4>(sg.rec, kRecTLo + q * 1024 + 16 * lane);
   }
+  // (3) Y = beta (v - e^G rk X) as hi / lo B operands of k-steps s' (tokens 32s' ..).
+  uint4 yh[2], yl[2];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) xs4[nt] = Mfma(cur.kr[s], bl[s][nt], xs4[nt]);
-  }
-  const float4 xs = LdsRead<float4>(stage + kStageScal + 16 * kq);
-  const float4 beta = LdsRead<float4>(stage + kStageScal + 64 + 16 * kq);
-  const float4 os = LdsRead<float4>(stage + kStageScal + 128 + 16 * kq);
-  const float4 ws = LdsRead<float4>(stage + kStageScal + 192 + 16 * kq);
-#pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
+  for (int r = 0; r < 4; ++r) {
+    const float v4[4] = {Bf16LoToF32(vr[r][0]), Bf16HiToF32(vr[r][0]), Bf16LoToF32(vr[r][1]), Bf16HiToF32(vr[r][1])};
     float y[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) y[i] = F4(beta, i) * (cur.vv[nt][i] - F4(xs, i) * xs4[nt][i]);
-    uint2 hi, lo;
-    Split2(y[0], y[1], hi.x, lo.x);
-    Split2(y[2], y[3], hi.y, lo.y);
-    const int col = 16 * nt + r16, t = 16 * w + 4 * kq;
-    *reinterpret_cast<uint2*>(&y_lds[0][col][t]) = hi;
-    *reinterpret_cast<uint2*>(&y_lds[1][col][t]) = lo;
+    for (int i = 0; i < 4; ++i) y[i] = F4(bf[r], i) * (v4[i] - F4(xf[r], i) * (xh[r][i] + xl[r][i]));
+    uint32_t* dh = reinterpret_cast<uint32_t*>(&yh[r >> 1]) + 2 * (r & 1);
+    uint32_t* dl = reinterpret_cast<uint32_t*>(&yl[r >> 1]) + 2 * (r & 1);
+    Split2(y[0], y[1], dh[0], dl[0]);
+    Split2(y[2], y[3], dh[1], dl[1]);
   }
-  __syncthreads();
-  // (3) V = T Y over the pieces on or below the diagonal (hi.hi + hi.lo + lo.hi).
-  f32x4_t vn4[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};
+  // Factors of phases (5) and (7); the output is transposed, so lane (g, m) scales token 16r + m.
+  float4 wf[4];
+  float of[4];
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    if (s <= (w >> 1)) {
-      const uint4 th = LdsRead<uint4>(stage + kStageT + Swz(r16, 4 * s + kq));
-      const uint4 tl = LdsRead<uint4>(stage + kStageTLo + Swz(r16, 4 * s + kq));
-      uint4 yh[2], yl[2];
+  for (int r = 0; r < 4; ++r) {
+    wf[r] = *reinterpret_cast<const float4*>(sc + 192 + 16 * r + 4 * g);
+    of[r] = sc[128 + 16 * r + m];
+  }
+  const float decay = sc[256];
+  // (4) V = T Y on and below the diagonal (hi.hi + hi.lo + lo.hi), pairs in an order that alternates accumulators.
+  f32x4_t vn[4];
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        yh[nt] = *reinterpret_cast<const uint4*>(&y_lds[0][16 * nt + r16][32 * s + 8 * kq]);
-        yl[nt] = *reinterpret_cast<const uint4*>(&y_lds[1][16 * nt + r16][32 * s + 8 * kq]);
+  for (int r = 0; r < 4; ++r) vn[r] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int term = 0; term < 3; ++term) {
+#pragma unroll
+    for (int q = 0; q < kPairs; ++q) {
+      const int r = q < 2 ? q : 2 + (q - 2) / 2, sp = q < 2 ? 0 : (q - 2) % 2;
+      const uint4 ta = term == 2 ? tl[q] : th[q];
+      const uint4 yb = term == 1 ? yl[sp] : yh[sp];
+      vn[r] = Mfma(ta, yb, vn[r]);
+    }
+  }
+  // The transposed k operands of phase (6): tiles mt = 2s + hf, k-steps s' (two 8-byte reads each).
+  const int e = m >> 2, q4 = m & 3;
+  auto kt_op = [&](int mt, int sp) {
+    const int s = mt >> 1, hf = mt & 1;
+    const u32x2_t lo = TrRead(sg.kt + T16(32 * sp + 4 * g + e, 4 * s + q4) + 8 * hf);
+    const u32x2_t hi = TrRead(sg.kt + T16(32 * sp + 16 + 4 * g + e, 4 * s + q4) + 8 * hf);
+    return make_uint4(lo[0], lo[1], hi[0], hi[1]);
+  };
+  constexpr int kKtRing = 4;  // (mt, s') operands in flight
+  uint4 kr[kKtRing];
+#pragma unroll
+  for (int j = 0; j < kKtRing; ++j) kr[j] = kt_op(j >> 1, j & 1);
+  // (5) V as single bf16 operands for P V, and ws V as hi / lo for the state update.
+  uint4 vb[2], wh[2], wl[2];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    uint32_t* db = reinterpret_cast<uint32_t*>(&vb[r >> 1]) + 2 * (r & 1);
+    uint32_t* dh = reinterpret_cast<uint32_t*>(&wh[r >> 1]) + 2 * (r & 1);
+    uint32_t* dl = reinterpret_cast<uint32_t*>(&wl[r >> 1]) + 2 * (r & 1);
+    db[0] = PackRne(vn[r][0], vn[r][1]);
+    db[1] = PackRne(vn[r][2], vn[r][3]);
+    Split2(vn[r][0] * wf[r].x, vn[r][1] * wf[r].y, dh[0], dl[0]);
+    Split2(vn[r][2] * wf[r].z, vn[r][3] * wf[r].w, dh[1], dl[1]);
+  }
+  // (6) S = e^Gn S + k^T (ws V), hi + lo, over (mt, s') with the transposed reads kKtRing operands ahead; two state
+  // tiles are advanced side by side so that consecutive multiplies hit different accumulators.
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt) st[mt] = st[mt] * decay;
+#pragma unroll
+  for (int pr = 0; pr < 4; ++pr) {  // state tiles 2pr and 2pr + 1
+#pragma unroll
+    for (int sp = 0; sp < 2; ++sp) {
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const int mt = 2 * pr + hf, j = 4 * pr + 2 * hf + sp;  // operand index in (mt, s') order: j = 2 mt + s'
+        const uint4 ak = kr[j % kKtRing];
+        if (j + kKtRing < 16) kr[j % kKtRing] = kt_op((j + kKtRing) >> 1, (j + kKtRing) & 1);
+        st[mt] = Mfma(ak, wh[sp], st[mt]);
+        st[mt] = Mfma(ak, wl[sp], st[mt]);
       }
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        vn4[nt] = Mfma(th, yh[nt], vn4[nt]);
-        vn4[nt] = Mfma(th, yl[nt], vn4[nt]);
-        vn4[nt] = Mfma(tl, yh[nt], vn4[nt]);
-      }
     }
   }
+  // (7) o^T = rq e^G (q S0)^T + V^T P^T, rounded to bf16 (round to nearest even); written to the chunk's LDS output block.
+  // The C layout of V is the A layout of V^T and P's A operand is the B layout of P^T, so the operands are the same
+  // registers as P V's with their roles swapped; lane (g, m) ends up with 4 consecutive columns of token 16r + m.
+  uint4 pa[kPairs];
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const int col = 16 * nt + r16, t = 16 * w + 4 * kq;
-    uint2 v, hi, lo;
-    v.x = PackRne(vn4[nt][0], vn4[nt][1]);
-    v.y = PackRne(vn4[nt][2], vn4[nt][3]);
-    Split2(vn4[nt][0] * ws.x, vn4[nt][1] * ws.y, hi.x, lo.x);
-    Split2(vn4[nt][2] * ws.z, vn4[nt][3] * ws.w, hi.y, lo.y);
-    *reinterpret_cast<uint2*>(&vn_lds[0][col][t]) = v;
-    *reinterpret_cast<uint2*>(&vn_lds[1][col][t]) = hi;
-    *reinterpret_cast<uint2*>(&vn_lds[2][col][t]) = lo;
-  }
-  __syncthreads();
-  // (4) o = rq e^G q S0 + P V for tokens 16w..16w+15.
-  f32x4_t pv4[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};
+  for (int q = 0; q < kPairs; ++q) pa[q] = Lds<uint4>(sg.rec, kRecP + q * 1024 + 16 * lane);
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    if (s <= (w >> 1)) {
-      const uint4 pr = LdsRead<uint4>(stage + kStageP + Swz(r16, 4 * s + kq));
+  for (int r = 0; r < 4; ++r) {
+    f32x4_t o = oq[r] * of[r];
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const uint4 b = *reinterpret_cast<const uint4*>(&vn_lds[0][16 * nt + r16][32 * s + 8 * kq]);
-        pv4[nt] = Mfma(pr, b, pv4[nt]);
-      }
-    }
-  }
-  out.t0 = cur.t0;
-  out.n = cur.n;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) out.o[nt][i] = F32ToBf16(fmaf(F4(os, i), oq4[nt][i], pv4[nt][i]));
-  }
-  // (5) S = e^Gn S0 + k^T (ws V) (hi + lo) for state rows 32w..32w+31.
-  uint4 vh[2][2], vl[2][2], ak[2][2];
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      vh[s][nt] = *reinterpret_cast<const uint4*>(&vn_lds[1][16 * nt + r16][32 * s + 8 * kq]);
-      vl[s][nt] = *reinterpret_cast<const uint4*>(&vn_lds[2][16 * nt + r16][32 * s + 8 * kq]);
-    }
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) ak[mt][s] = LdsRead<uint4>(stage + kStageKT + Swz(16 * mt + r16, 4 * s + kq));
-  }
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      f32x4_t acc = st[mt][nt] * cur.decay;
-#pragma unroll
-      for (int s = 0; s < 2; ++s) acc = Mfma(ak[mt][s], vh[s][nt], acc);
-#pragma unroll
-      for (int s = 0; s < 2; ++s) acc = Mfma(ak[mt][s], vl[s][nt], acc);
-      st[mt][nt] = acc;
-    }
+    for (int sp = 0; sp <= r / 2; ++sp) o = Mfma(vb[sp], pa[Pair(r, sp)], o);
+    *reinterpret_cast<uint2*>(sg.ob + (16 * r + m) * 64 + 2 * (16 * w + 4 * g)) =
+        make_uint2(PackRne(o[0], o[1]), PackRne(o[2], o[3]));
   }
 }
 
-// One workgroup per (sequence, head, value block of 32 columns); wave w owns state rows 32w..32w+31 and, for the
-// token-side products, tokens 16w..16w+15 of each chunk. blockIdx -> (chain, block) keeps the four value blocks of a
-// chain on one XCD (workgroups are dealt to the 8 XCDs round-robin), so they share the chain's k, q and records in L2.
+}  // namespace wy
+
+// One workgroup of four wavefronts per (sequence, head, value block of 32 columns): wavefronts 0 and 1 compute
+// (columns 16w .. 16w + 15 of the block each) and never touch global memory inside the loop; wavefronts 2 and 3 copy
+// the next chunk into LDS (and 2 stores the previous chunk's outputs) while they compute, so that the copies, which are
+// bound by HBM, never hold the compute wavefronts at the memory pipeline. blockIdx -> (chain, block) keeps the four
+// value blocks of a chain on one XCD (workgroups are dealt to the 8 XCDs round-robin): they share the chain's rows and
+// records in L2.
 template <bool kVec>
-__global__ void __launch_bounds__(256, 1) ChunkScanKernel(ChunkArgs ca) {
+__global__ void __launch_bounds__(256, 1) WyScanKernel(ChunkArgs ca) {
+  using namespace wy;
   const GdnArgs& a = ca.a;
   const uint32_t x = blockIdx.x;
   const uint32_t chain = (x & 7) + 8 * (x >> 5);
@@ -860,70 +926,66 @@ __global__ void __launch_bounds__(256, 1) ChunkScanKernel(ChunkArgs ca) {
   if (listed < 0) return;
   const uint32_t seq = static_cast<uint32_t>(listed), h = chain % kHeads;
   const int4 sq = ca.seqs[seq];
-  if (sq.y == 0) return;  // an empty sequence leaves its slot untouched
-  const int32_t slot = a.slots[seq];
-  const bool has_slot = slot >= 0 && static_cast<uint64_t>(slot) < a.pool_slots;
+  const int chunks = sq.y;
+  if (chunks == 0) return;  // an empty (or unrouted) sequence leaves its slot untouched
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r16 = lane & 15, kq = lane >> 4;
+  const int g = lane >> 4, m = lane & 15;
+  __shared__ __align__(16) Stage stage[2];
 
-  __shared__ __align__(16) uint16_t s_lds[2][kVBlock][kTilePitch];  // S hi, lo as [column][dim]
-  __shared__ __align__(16) uint16_t y_lds[2][kVBlock][kTokPitch];   // Y hi, lo as [column][token]
-  __shared__ __align__(16) uint16_t vn_lds[3][kVBlock][kTokPitch];  // V (bf16), V * ws hi, lo as [column][token]
-  __shared__ __align__(16) uint8_t stage_lds[2][4][kStageBytes];    // [buffer][wave] staged record rows
-  uint8_t* stage0 = stage_lds[0][w];
-  uint8_t* stage1 = stage_lds[1][w];
+  auto t0_of = [&](int c) { return sq.z + 64 * c; };
+  auto n_of = [&](int c) { return min(64, sq.w - t0_of(c)); };
+  auto rec_of = [&](int c) {
+    return ca.recs + (static_cast<uint64_t>(sq.x + c) * kHeads + h) * kRecBytes;
+  };
 
-  // st[mt][nt][i] = S[32w + 16mt + 4kq + i][32vb + 16nt + r16]
-  f32x4_t st[2][2];
-  float* sp = has_slot ? a.state + (static_cast<uint64_t>(slot) * kHeads + h) * kDim * kDim : nullptr;
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int d = 32 * w + 16 * mt + 4 * kq + i, c = vb * kVBlock + 16 * nt + r16;
-        st[mt][nt][i] = (has_slot && a.use_initial_state) ? sp[d * kDim + c] : 0.0f;
+  const uint32_t lds0 = Uniform(LdsAddr(&stage[0]));  // LDS byte address of stage[0]; stage[1] follows it
+  if (w >= 2) {  // copiers
+    const int copier = w - 2;
+    const CopyOffsets co = MakeCopyOffsets(a, h, vb, lane);
+    Fetch<kVec>(a, co, rec_of(0), t0_of(0), n_of(0), h, vb, copier, lane, stage[0], lds0);
+    WaitVmem();
+    __syncthreads();
+    for (int c = 0; c < chunks; ++c) {
+      if (copier == 0 && c > 0) StoreOut(a, stage[(c - 1) & 1], t0_of(c - 1), n_of(c - 1), h, vb, lane);
+      if (c + 1 < chunks) {
+        const int nb = (c + 1) & 1;
+        Fetch<kVec>(a, co, rec_of(c + 1), t0_of(c + 1), n_of(c + 1), h, vb, copier, lane, stage[nb],
+                    lds0 + nb * static_cast<uint32_t>(sizeof(Stage)));
       }
+      WaitVmem();
+      __syncthreads();
     }
+    if (copier == 0) StoreOut(a, stage[(chunks - 1) & 1], t0_of(chunks - 1), n_of(chunks - 1), h, vb, lane);
+    return;
   }
 
-  // Two register sets and two staging buffers in turn: the loads of chunk c + 1 are in flight while chunk c is
-  // computed (the last chunk is loaded again past the end rather than branching around the load).
-  // Each step first waits for every vector memory operation issued one step earlier (the chunk's registers, its
-  // staged record rows, the previous chunk's outputs), then starts the loads of the next chunk.
-  ChunkRegs ra, rb;
-  ChunkOut out;
-  out.n = 0;
-  const int last = sq.y - 1;
-  LoadChunk<kVec>(ca, sq, 0, h, vb, w, lane, ra, stage0);
-  for (int c = 0;;) {
-    WaitVmem();
-    LoadChunk<kVec>(ca, sq, min(c + 1, last), h, vb, w, lane, rb, stage1);
-    StoreOut(a, out, h, vb, w, r16, kq);
-    ScanStep(a, ra, stage0, st, h, vb, w, r16, kq, s_lds, y_lds, vn_lds, out);
-    if (++c > last) break;
-    WaitVmem();
-    LoadChunk<kVec>(ca, sq, min(c + 1, last), h, vb, w, lane, ra, stage0);
-    StoreOut(a, out, h, vb, w, r16, kq);
-    ScanStep(a, rb, stage1, st, h, vb, w, r16, kq, s_lds, y_lds, vn_lds, out);
-    if (++c > last) break;
+  const int32_t slot = a.slots[seq];
+  const bool has_slot = slot >= 0 && static_cast<uint64_t>(slot) < a.pool_slots;
+  const uint32_t col = vb * 32 + 16 * w + m;
+  float* sp = has_slot ? a.state + (static_cast<uint64_t>(slot) * kHeads + h) * kDim * kDim : nullptr;
+  // st[mt][i] = S[32 (mt >> 1) + 8g + 4 (mt & 1) + i][col]
+  f32x4_t st[8];
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = 32 * (mt >> 1) + 8 * g + 4 * (mt & 1) + i;
+      st[mt][i] = (has_slot && a.use_initial_state) ? sp[d * kDim + col] : 0.0f;
+    }
+  __syncthreads();
+  for (int c = 0; c < chunks; ++c) {
+    Advance(stage[c & 1], st, w, lane);
+    __syncthreads();
   }
-  StoreOut(a, out, h, vb, w, r16, kq);
-  WaitVmem();  // the copies of the re-loaded last chunk land before the workgroup's LDS is released
   if (has_slot) {
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+    for (int mt = 0; mt < 8; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int d = 32 * w + 16 * mt + 4 * kq + i, c = vb * kVBlock + 16 * nt + r16;
-          sp[d * kDim + c] = st[mt][nt][i];
-        }
+      for (int i = 0; i < 4; ++i) {
+        const int d = 32 * (mt >> 1) + 8 * g + 4 * (mt & 1) + i;
+        sp[d * kDim + col] = st[mt][i];
       }
-    }
   }
 }
 
@@ -956,7 +1018,7 @@ ChunkArena MakeArena(uint64_t max_chunks, uint64_t batch, uint64_t max_long = 0)
   l.seq_list = l.seq_table + 16ull * batch;
   l.tables_bytes = roost::RoundUp(l.seq_list + 4ull * max_long, 256);
   l.records = l.tables_bytes;
-  l.total = l.records + uint64_t{l.max_chunks} * kHeads * kRecBytes;
+  l.total = l.records + uint64_t{l.max_chunks} * kHeads * wy::kRecBytes;
   return l;
 }
 
@@ -1063,11 +1125,11 @@ RoostStatus LaunchChunk(const RoostGatedDeltaRuleParams& p, const RoostWorkspace
   const dim3 prep(chunks, kHeads);
   const dim3 scan((ca.chains + 7) / 8 * 8 * kVBlocks);
   if (Vec16(p)) {
-    hipLaunchKernelGGL(ChunkPrepKernel<true>, prep, dim3(256), 0, stream, ca);
-    hipLaunchKernelGGL(ChunkScanKernel<true>, scan, dim3(256), 0, stream, ca);
+    hipLaunchKernelGGL(WyPrepKernel<true>, prep, dim3(256), 0, stream, ca);
+    hipLaunchKernelGGL(WyScanKernel<true>, scan, dim3(256), 0, stream, ca);
   } else {
-    hipLaunchKernelGGL(ChunkPrepKernel<false>, prep, dim3(256), 0, stream, ca);
-    hipLaunchKernelGGL(ChunkScanKernel<false>, scan, dim3(256), 0, stream, ca);
+    hipLaunchKernelGGL(WyPrepKernel<false>, prep, dim3(256), 0, stream, ca);
+    hipLaunchKernelGGL(WyScanKernel<false>, scan, dim3(256), 0, stream, ca);
   }
   return roost::HipStatus(hipGetLastError(), kOp, "chunk launch");
 }
@@ -1242,7 +1304,7 @@ extern "C" ROOST_API RoostStatus roost_gdn_chunk_run(RoostContext* ctx, const vo
 
 namespace {
 
-constexpr uint64_t kStaticScratchBytes = 48ull << 20;  // 48 MiB per device, held until the process ends
+constexpr uint64_t kStaticScratchBytes = 24ull << 20;  // 24 MiB per device, held until the process ends
 constexpr int kMaxDevices = 64;
 
 __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
@@ -1297,3 +1359,5 @@ extern "C" ROOST_API RoostStatus roost_amd_gdn_recurrent_run_noalloc(RoostContex
     return LaunchRouted(p, base, l, s);
   });
 }
+
+

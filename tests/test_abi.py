@@ -222,8 +222,8 @@ def test_gdn_refusals_without_gpu(kernels):
         setattr(long, name, _fake(40 * 2048, abi.DTYPE_BF16))
     long.g, long.beta = _fake(40 * 16, abi.DTYPE_F32), _fake(40 * 16, abi.DTYPE_BF16)
     assert rec.workspace(ctx, C.addressof(long), C.addressof(sizes)) == abi.OK
-    # 40 tokens in one sequence: at most 40 // 64 + min(1, 40 // 16) = 1 chunk of 16 heads x 42240-byte records.
-    assert sizes.device_bytes == 256 + 256 + 16 * 42240 and sizes.pinned_host_bytes == 0 and sizes.plan_bytes == 0
+    # 40 tokens in one sequence: at most 40 // 64 + min(1, 40 // 16) = 1 chunk of 16 heads x 20480-byte records.
+    assert sizes.device_bytes == 256 + 256 + 16 * 20480 and sizes.pinned_host_bytes == 0 and sizes.plan_bytes == 0
     assert run(long) == abi.WORKSPACE_TOO_SMALL
     kernels.destroy_context(ctx)
 
