@@ -37,10 +37,16 @@ def hipcc() -> str:
     return path
 
 
+# Per-source code-generation options. The GDN scan keeps its MFMA accumulators in architectural VGPRs (its
+# compute wavefronts read them with VALU every chunk; the AGPR form costs a copy per read).
+SOURCE_FLAGS = {"gated_delta_rule.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _compile(src: str) -> Path:
     obj = BUILD / (Path(src).stem + ".o")
     lang = ["-x", "hip"] if src.endswith(".cpp") else []
-    cmd = [hipcc(), *HIPCC_FLAGS, *lang, "-I", str(ROOT / "include"), "-c", str(CSRC / src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(src, []), *lang, "-I", str(ROOT / "include"), "-c", str(CSRC / src),
+           "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{res.stderr}")

@@ -771,8 +771,9 @@ __device__ __forceinline__ void Advance(Stage& sg, f32x4_t (&st)[8], int w, int 
     Split2(st[2 * s + 1][0], st[2 * s + 1][1], sh[s].z, sl[s].z);
     Split2(st[2 * s + 1][2], st[2 * s + 1][3], sh[s].w, sl[s].w);
   }
-  // (2) X = k S as hi and lo partial sums and q S (hi), over (s, r) in s-major order so that consecutive multiplies
-  // hit different accumulators; a ring keeps the k / q reads kRing steps ahead.
+  // (2) X = k S as hi and lo partial sums and (q S)^T, token tile by token tile (r-major), so that (3) for tile r can
+  // run while tile r + 1 multiplies; within a tile the three accumulators alternate. A ring keeps the k / q reads kRing
+  // steps ahead.
   constexpr int kRing = 3;
   f32x4_t xh[4], xl[4], oq[4];
 #pragma unroll
@@ -780,10 +781,10 @@ __device__ __forceinline__ void Advance(Stage& sg, f32x4_t (&st)[8], int w, int 
   uint4 rk[kRing], rq[kRing];
 #pragma unroll
   for (int j = 0; j < kRing; ++j) {
-    rk[j] = Lds<uint4>(sg.kt, kq_off(j & 3, j >> 2));
-    rq[j] = Lds<uint4>(sg.qt, kq_off(j & 3, j >> 2));
+    rk[j] = Lds<uint4>(sg.kt, kq_off(j >> 2, j & 3));
+    rq[j] = Lds<uint4>(sg.qt, kq_off(j >> 2, j & 3));
   }
-  // The factors of phase (3) and the v block, read while the multiplies run.
+  // The factors of phase (3), the v block and the T operands of phase (4), read while the multiplies run.
   float4 xf[4], bf[4];
   u32x2_t vr[4];
 #pragma unroll
@@ -792,20 +793,6 @@ __device__ __forceinline__ void Advance(Stage& sg, f32x4_t (&st)[8], int w, int 
     bf[r] = *reinterpret_cast<const float4*>(sc + 64 + 16 * r + 4 * g);
     vr[r] = TrRead(sg.vt + (16 * r + 4 * g + (m >> 2)) * 64 + 32 * w + 8 * (m & 3));
   }
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const int r = j & 3, s = j >> 2;
-    const uint4 ak = rk[j % kRing], aq = rq[j % kRing];
-    if (j + kRing < 16) {
-      rk[j % kRing] = Lds<uint4>(sg.kt, kq_off((j + kRing) & 3, (j + kRing) >> 2));
-      rq[j % kRing] = Lds<uint4>(sg.qt, kq_off((j + kRing) & 3, (j + kRing) >> 2));
-    }
-    xh[r] = Mfma(ak, sh[s], xh[r]);
-    xl[r] = Mfma(ak, sl[s], xl[r]);
-    oq[r] = Mfma(sh[s], aq, oq[r]);  // (q S)^T: lane (g, m) gets columns 4g .. 4g + 3 of token 16r + m
-  }
-
-  // T operands of phase (4), read while phase (3)'s arithmetic runs.
   uint4 th[kPairs], tl[kPairs];
 #pragma unroll
   for (int q = 0; q < kPairs; ++q) {
@@ -815,15 +802,27 @@ __device__ __forceinline__ void Advance(Stage& sg, f32x4_t (&st)[8], int w, int 
   // (3) Y = beta (v - e^G rk X) as hi / lo B operands of k-steps s' (tokens 32s' ..).
   uint4 yh[2], yl[2];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const float v4[4] = {Bf16LoToF32(vr[r][0]), Bf16HiToF32(vr[r][0]), Bf16LoToF32(vr[r][1]), Bf16HiToF32(vr[r][1])};
-    float y[4];
+  for (int j = 0; j < 16; ++j) {
+    const int r = j >> 2, s = j & 3;
+    const uint4 ak = rk[j % kRing], aq = rq[j % kRing];
+    if (j + kRing < 16) {
+      rk[j % kRing] = Lds<uint4>(sg.kt, kq_off((j + kRing) >> 2, (j + kRing) & 3));
+      rq[j % kRing] = Lds<uint4>(sg.qt, kq_off((j + kRing) >> 2, (j + kRing) & 3));
+    }
+    xh[r] = Mfma(ak, sh[s], xh[r]);
+    xl[r] = Mfma(ak, sl[s], xl[r]);
+    oq[r] = Mfma(sh[s], aq, oq[r]);  // (q S)^T: lane (g, m) gets columns 4g .. 4g + 3 of token 16r + m
+    if (s == 3) {
+      const float v4[4] = {Bf16LoToF32(vr[r][0]), Bf16HiToF32(vr[r][0]), Bf16LoToF32(vr[r][1]),
+                           Bf16HiToF32(vr[r][1])};
+      float y[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) y[i] = F4(bf[r], i) * (v4[i] - F4(xf[r], i) * (xh[r][i] + xl[r][i]));
-    uint32_t* dh = reinterpret_cast<uint32_t*>(&yh[r >> 1]) + 2 * (r & 1);
-    uint32_t* dl = reinterpret_cast<uint32_t*>(&yl[r >> 1]) + 2 * (r & 1);
-    Split2(y[0], y[1], dh[0], dl[0]);
-    Split2(y[2], y[3], dh[1], dl[1]);
+      for (int i = 0; i < 4; ++i) y[i] = F4(bf[r], i) * (v4[i] - F4(xf[r], i) * (xh[r][i] + xl[r][i]));
+      uint32_t* dh = reinterpret_cast<uint32_t*>(&yh[r >> 1]) + 2 * (r & 1);
+      uint32_t* dl = reinterpret_cast<uint32_t*>(&yl[r >> 1]) + 2 * (r & 1);
+      Split2(y[0], y[1], dh[0], dl[0]);
+      Split2(y[2], y[3], dh[1], dl[1]);
+    }
   }
   // Factors of phases (5) and (7); the output is transposed, so lane (g, m) scales token 16r + m.
   float4 wf[4];
@@ -1359,5 +1358,6 @@ extern "C" ROOST_API RoostStatus roost_amd_gdn_recurrent_run_noalloc(RoostContex
     return LaunchRouted(p, base, l, s);
   });
 }
+
 
 
