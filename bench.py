@@ -27,6 +27,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 METRIC = "decode attn HBM GB/s (% peak) + prefill TFLOPS (% MFMA peak) vs CpuOps, 1 GPU"
+FLUSH = None  # the cache-flush buffer (set in main)
 
 
 def log(msg):
@@ -96,6 +97,50 @@ def time_runs(torch, session, entry, params, ws, steps, warmup):
     return start.elapsed_time(end) / steps
 
 
+class Flush:
+    """A 512 MiB device buffer read between timed launches: it evicts the 256 MB MALL and the L2s with clean lines,
+    so a cold launch reads its inputs from HBM (a written buffer would instead leave dirty lines whose write-back
+    lands inside the timed launch)."""
+
+    def __init__(self, torch):
+        self.buf = torch.ones(128 << 20, dtype=torch.int32, device="cuda")
+
+    def __call__(self, stream):
+        import torch
+
+        with torch.cuda.stream(stream):
+            self.sink = self.buf.sum()
+
+
+def time_cold(torch, session, flush, fn, reps):
+    """Median duration in ms of `fn` (launches on the session's stream), each launch timed alone with events after a
+    cache flush."""
+    times = []
+    for _ in range(reps):
+        flush(session.stream)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(session.stream)
+        fn()
+        e1.record(session.stream)
+        e1.synchronize()
+        times.append(e0.elapsed_time(e1))
+    return float(np.median(times))
+
+
+def time_each(torch, session, fn, reps, warmup=2):
+    """Median duration in ms of `fn` launched back to back (warm caches), each launch between its own events."""
+    for _ in range(warmup):
+        fn()
+    session.stream.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for e0, e1 in evs:
+        e0.record(session.stream)
+        fn()
+        e1.record(session.stream)
+    evs[-1][1].synchronize()
+    return float(np.median([e0.elapsed_time(e1) for e0, e1 in evs]))
+
+
 def planned(session, entry, params, key, reps=20):
     """Workspace + plan, returning the workspace and the host cost of one step's planning in ms: the workspace query
     and plan() (host tables, pinned staging, async copy) as the worker calls them every step, averaged over `reps`
@@ -128,6 +173,8 @@ def bench_decode(torch, roost_amd, session, steps, warmup):
     p = b.params(roost_amd)
     ws, plan_ms = planned(session, entry, p, "bench-decode")
     ms = time_runs(torch, session, entry, p, ws, steps, warmup)
+    if FLUSH is not None:
+        b.cold_ms = time_cold(torch, session, FLUSH, lambda: session.run(entry, p, ws), 10)
     return b, ms, plan_ms
 
 
@@ -140,7 +187,27 @@ def bench_prefill(torch, roost_amd, session, steps, warmup, d=256):
     entry = session.lib.entry(roost_amd.ATTENTION_VARIANT)
     p = b.params(roost_amd)
     ws, plan_ms = planned(session, entry, p, "bench-prefill")
-    ms = time_runs(torch, session, entry, p, ws, max(steps // 2, 3), max(warmup // 2, 1))
+    reps = max(steps // 2, 20)
+    ms = time_each(torch, session, lambda: session.run(entry, p, ws), reps)
+    # The config's step also writes the chunks' new K/V rows into their (freshly allocated, random) pages first:
+    # CacheWrite at the plan-region slots, then the attention call.
+    slots_h = []
+    for i in range(b.batch):
+        pages = b.kv_indices_h[b.kv_indptr_h[i]:b.kv_indptr_h[i + 1]].astype(np.int64)
+        pos = np.arange(b.kv_lens[i] - b.q_lens[i], b.kv_lens[i])
+        slots_h.append(pages[pos // b.ps] * b.ps + pos % b.ps)
+    g = torch.Generator(device="cuda").manual_seed(33)
+    new_k = (torch.randn((b.tokens, b.hkv, b.d), generator=g, device="cuda") * 0.5).to(torch.bfloat16)
+    new_v = (torch.randn((b.tokens, b.hkv, b.d), generator=g, device="cuda") * 0.5).to(torch.bfloat16)
+    cw = roost_amd.cache_write_params(new_k, new_v, b.k, b.v, torch.from_numpy(np.concatenate(slots_h)).cuda(),
+                                      kv_heads=b.hkv, head_dim=b.d, page_size=b.ps)
+    e_cw = session.lib.entry(roost_amd.CACHE_WRITE_VARIANT)
+
+    def step():
+        session.run(e_cw, cw, None)
+        session.run(entry, p, ws)
+
+    b.append_ms = time_each(torch, session, step, reps)
     return b, ms, plan_ms
 
 
@@ -169,25 +236,30 @@ def bench_gdn(torch, roost_amd, session, steps, warmup):
     p, keep = inputs(4, [4096] * 4)
     entry = session.lib.entry(roost_amd.CHUNK_VARIANT)
     ws, _ = planned(session, entry, p, "bench-gdn-chunk")
-    ms = time_runs(torch, session, entry, p, ws, max(steps // 4, 3), 1)
-    T, B = 4 * 4096, 4
+    run = lambda: session.run(entry, p, ws)  # noqa: E731
+    ms = time_each(torch, session, run, max(steps // 2, 10))
+    cold = time_cold(torch, session, FLUSH, run, 10) if FLUSH is not None else None
+    T, B, C = 4 * 4096, 4, 64
     bytes_ = (3 * T * H * D + T * H * D) * 2 + T * H * 6 + 2 * B * H * D * D * 4
-    # Algorithmic flops of the WY form per chunk of 64 and head: k.k^T, q.k^T, T.Y, P.V (2 C^2 D each) and
-    # k.S0, q.S0, k^T.V (2 C D^2 each); the bf16 hi/lo operand splits are not counted.
-    flops = (T // 64) * H * (2 * 64 * 64 * 4 * D + 6 * 64 * D * D)
-    res["gdn_chunk"] = {"config": "4 x 4096 tokens, 16 heads x 128, chunk 64", "ms": ms,
+    # Algorithmic flops of the WY form per chunk of C = 64 tokens and head: 2 C^2 (3 dk + 2 dv) + 6 C dk dv
+    # (11.53 MFLOP; the bf16 hi / lo operand splits are not counted).
+    flops = (T // C) * H * (2 * C * C * (3 * D + 2 * D) + 6 * C * D * D)
+    res["gdn_chunk"] = {"config": "4 x 4096 tokens, 16 heads x 128, chunk 64", "ms": ms, "cold_ms": cold,
                         "hbm_gbs": bytes_ / ms / 1e6, "hbm_frac": bytes_ / ms / 1e6 / HBM_PEAK_GBS,
-                        "tflops": flops / ms / 1e9, "mfma_frac": flops / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS}
+                        "tflops": flops / ms / 1e9, "mfma_frac": flops / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS,
+                        "flops": flops, "algorithmic_bytes": bytes_}
     del keep
     # Config 4 follow-on: one recurrent decode step on 128 states.
     p, keep = inputs(128, [1] * 128)
     entry = session.lib.entry(roost_amd.RECURRENT_VARIANT)
     ws, _ = planned(session, entry, p, "bench-gdn-recurrent")
     ms = time_runs(torch, session, entry, p, ws, steps, warmup)
+    cold = time_cold(torch, session, FLUSH, lambda: session.run(entry, p, ws), 10) if FLUSH is not None else None
     B = 128
     bytes_ = 2 * B * H * D * D * 4 + B * (3 * H * D + H * D) * 2 + B * H * 6
-    res["gdn_recurrent"] = {"config": "128 states x 1 token, 16 heads x 128", "ms": ms,
-                            "hbm_gbs": bytes_ / ms / 1e6, "hbm_frac": bytes_ / ms / 1e6 / HBM_PEAK_GBS}
+    res["gdn_recurrent"] = {"config": "128 states x 1 token, 16 heads x 128", "ms": ms, "cold_ms": cold,
+                            "hbm_gbs": bytes_ / ms / 1e6, "hbm_frac": bytes_ / ms / 1e6 / HBM_PEAK_GBS,
+                            "cold_hbm_frac": bytes_ / cold / 1e6 / HBM_PEAK_GBS if cold else None}
     del keep
     return res
 
@@ -259,6 +331,7 @@ def bench_mixed(torch, roost_amd, session, steps, warmup):
     end.record(session.stream)
     end.synchronize()
     step_ms = start.elapsed_time(end) / steps
+    cold_ms = time_cold(torch, session, FLUSH, step, 10) if FLUSH is not None else None
     parts = {
         "cache_write": time_runs(torch, session, e_cw, cw, ws_cw, steps, warmup),
         "attention": time_runs(torch, session, e_att, att, ws_att, steps, warmup),
@@ -271,7 +344,7 @@ def bench_mixed(torch, roost_amd, session, steps, warmup):
     floor_ms = (kv_bytes + gdn_bytes) / (HBM_PEAK_GBS * 1e6)
     return {"workload": "BASELINE config 5: 48 decode ctx U(1024, 16384) + 2 x 512-token chunks on 4096 prefixes; "
                         "CacheWrite + PagedAttention + 3 GDN layers (recurrent variant)",
-            "step_ms": step_ms, "breakdown_ms": parts, "attention_plan_ms": plan_ms,
+            "step_ms": step_ms, "cold_step_ms": cold_ms, "breakdown_ms": parts, "attention_plan_ms": plan_ms,
             "hbm_floor_ms": floor_ms, "hbm_frac": floor_ms / step_ms, "context_tokens": int(kv.sum()),
             "tokens": T}
 
@@ -292,6 +365,9 @@ def bench_layer_ops(torch, roost_amd, session, steps, warmup):
         session.launch(entry, params)
         ms = time_runs(torch, session, entry, params, None, steps, warmup)
         res[name] = {"ms": ms, "gb_s": nbytes / ms / 1e6, "hbm_frac": nbytes / ms / 1e6 / HBM_PEAK_GBS}
+        if FLUSH is not None:
+            cold = time_cold(torch, session, FLUSH, lambda: session.run(entry, params, None), 10)
+            res[name].update(cold_ms=cold, cold_hbm_frac=nbytes / cold / 1e6 / HBM_PEAK_GBS)
 
     x, w = bf(T, CH), bf(CH, 4)
     y = torch.empty_like(x)
@@ -398,29 +474,109 @@ def bench_dense_vs_sdpa(torch, roost_amd, session, steps, warmup):
     return res
 
 
-def cpu_baseline(b: Paged, sample_seqs: int):
-    """CpuOps oracle (single thread, double precision, the C restatement of CpuOps.PagedAttention) on the first
-    `sample_seqs` sequences of the decode batch; reported in the headline's unit (algorithmic GB/s)."""
+def _host_info():
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    model = "unknown"
+    try:
+        for ln in Path("/proc/cpuinfo").read_text().splitlines():
+            if ln.startswith("model name"):
+                model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "threads_available": threads, "cpu_model": model}
+
+
+def _timed(fn):
+    t0 = time.perf_counter()
+    fn()
+    return time.perf_counter() - t0
+
+
+def cpu_baselines(b: Paged, pb: Paged):
+    """The CpuOps restatement (oracle/cpuops.c: double precision, one rounding per output) timed on this host on the
+    same inputs as the GPU rows: one thread (CpuOps itself is single-threaded) and OpenMP over (sequence, head) on every
+    available core. Decode config 2 runs in full; prefill config 3 and GDN config 4 run on stated subsets and are
+    scaled by the exact work ratio (flops, or tokens for the token-serial GDN recurrence), labelled as extrapolated.
+    Returns (host info, table, the headline baseline in the headline's unit)."""
     import torch
 
     import oracle
 
-    k = b.k.view(torch.int16).cpu().numpy().view(np.uint16)
-    v = b.v.view(torch.int16).cpu().numpy().view(np.uint16)
-    q = b.q[:sample_seqs].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
-    n = sample_seqs
-    kv_indptr = b.kv_indptr_h[: n + 1].copy()
+    info = _host_info()
+    nthr = info["threads_available"]
+    host = lambda t: t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)  # noqa: E731
+    rows = {}
+    # Decode, config 2 (whole batch).
+    k, v, q = host(b.k), host(b.v), host(b.q)
     out = np.zeros_like(q)
-    t0 = time.perf_counter()
-    oracle.paged_attention(q, out, k, v, np.arange(n + 1, dtype=np.int32), kv_indptr,
-                           b.kv_indices_h[: kv_indptr[-1]].copy(), b.last_h[:n].copy(), batch=n, tokens=n,
-                           q_heads=8, kv_heads=2, head_dim=256, page_size=16, bf16=True, threads=1)
-    secs = time.perf_counter() - t0
-    e = 2
-    bytes_ = int(b.kv_lens[:n].sum()) * 2 * 256 * 2 * e + n * 8 * 256 * 2 * e + 4 * (int(kv_indptr[-1]) + 2 * n + 1)
-    return {"value": bytes_ / secs / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"CpuOps restatement (oracle/cpuops.c, double, 1 thread) over the first {n} of the 64 config-2 "
-                      f"sequences ({int(b.kv_lens[:n].sum())} context tokens) in {secs:.2f} s"}
+    dec_bytes = b.decode_bytes()
+
+    def decode(threads):
+        oracle.paged_attention(q, out, k, v, b.q_indptr_h, b.kv_indptr_h, b.kv_indices_h, b.last_h, batch=b.batch,
+                               tokens=b.tokens, q_heads=8, kv_heads=2, head_dim=256, page_size=16, bf16=True,
+                               threads=threads)
+
+    for name, threads in (("1_thread", 1), ("openmp", nthr)):
+        secs = _timed(lambda: decode(threads))
+        rows[f"decode_config2_{name}"] = {"threads": threads, "seconds": secs, "gb_s": dec_bytes / secs / 1e9,
+                                          "sample": "all 64 sequences"}
+    del k, v
+    # Prefill, config 3: sequence subsets, scaled by flops.
+    pk, pv, pq = host(pb.k), host(pb.v), host(pb.q)
+    n, pre = pb.q_lens, pb.kv_lens - pb.q_lens
+    seq_flops = 4 * 8 * 256 * (n * pre + n * (n + 1) / 2)
+    total = float(seq_flops.sum())
+
+    def prefill(seqs, threads):
+        qi = np.concatenate([[0], np.cumsum(n[seqs])]).astype(np.int32)
+        pages = [pb.kv_indices_h[pb.kv_indptr_h[i]:pb.kv_indptr_h[i + 1]] for i in seqs]
+        ki = np.concatenate([[0], np.cumsum([len(x) for x in pages])]).astype(np.int32)
+        qq = np.concatenate([pq[pb.q_indptr_h[i]:pb.q_indptr_h[i + 1]] for i in seqs])
+        oo = np.zeros_like(qq)
+        return _timed(lambda: oracle.paged_attention(
+            qq, oo, pk, pv, qi, ki, np.concatenate(pages).astype(np.int32), pb.last_h[seqs].copy(),
+            batch=len(seqs), tokens=int(qi[-1]), q_heads=8, kv_heads=2, head_dim=256, page_size=16, bf16=True,
+            threads=threads))
+
+    order = np.argsort(seq_flops)
+    for name, seqs, threads in (("1_thread", order[:1], 1), ("openmp", order[:3], nthr)):
+        part = float(seq_flops[seqs].sum())
+        secs = prefill(list(seqs), threads)
+        rows[f"prefill_config3_{name}"] = {
+            "threads": threads, "seconds_for_sample": secs, "seconds_extrapolated": secs * total / part,
+            "tflops": part / secs / 1e12, "sample": f"sequences {sorted(int(x) for x in seqs)} "
+            f"({part / 1e9:.1f} of {total / 1e9:.1f} GFLOP), scaled by the flop ratio"}
+    # GDN, config 4 (recurrent form, 4 x 4096 tokens): one sequence on one thread, all four on every core.
+    rng = np.random.default_rng(4)
+    H, D, T1 = 16, 128, 4096
+
+    def gdn(nseq, threads):
+        T = nseq * T1
+        rows_ = lambda: bf16_bits(rng.standard_normal((T, H * D), dtype=np.float32))  # noqa: E731
+        qg, kg, vg = rows_(), rows_(), rows_()
+        gg = (-np.logaddexp(0.0, rng.standard_normal((T, H)))).astype(np.float32)
+        bb = bf16_bits(1.0 / (1.0 + np.exp(-rng.standard_normal((T, H)))))
+        pool = (rng.standard_normal((nseq, H, D, D), dtype=np.float32) * 0.01).astype(np.float32)
+        oo = np.zeros((T, H, D), np.uint16)
+        cu = (np.arange(nseq + 1) * T1).astype(np.int32)
+        return _timed(lambda: oracle.gated_delta_rule(
+            qg, kg, vg, gg, bb, oo, pool, np.arange(nseq, dtype=np.int32), cu, batch=nseq, tokens=T, k_heads=H,
+            v_heads=H, k_dim=D, v_dim=D, bf16=True, beta_bf16=True, threads=threads))
+
+    gdn_flops = 4 * T1 * H * 6 * D * D  # the recurrence: 6 dk dv per token and head
+    for name, nseq, threads in (("1_thread", 1, 1), ("openmp", 4, nthr)):
+        secs = gdn(nseq, threads)
+        rows[f"gdn_config4_{name}"] = {"threads": threads, "seconds_for_sample": secs,
+                                       "seconds_extrapolated": secs * 4 / nseq,
+                                       "gflops": gdn_flops * nseq / 4 / secs / 1e9,
+                                       "sample": f"{nseq} of 4 sequences of 4096 tokens (scaled by tokens)"}
+    r = rows["decode_config2_1_thread"]
+    headline = {"value": r["gb_s"], "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"CpuOps restatement (oracle/cpuops.c, double, 1 thread) over the whole config-2 decode "
+                          f"batch ({int(b.kv_lens.sum())} context tokens) in {r['seconds']:.2f} s on "
+                          f"{info['cpu_model']}"}
+    return info, rows, headline
 
 
 def measured_traffic():
@@ -442,7 +598,6 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--cpu-sample", type=int, default=16)
     ap.add_argument("--only", choices=["decode", "prefill", "prefill128", "dense", "gdn", "mixed", "layer", "attn_in"], default=None,
                     help="run one workload only and print its timing (for profiler passes); no JSON line")
     args = ap.parse_args()
@@ -459,6 +614,8 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs the MI355X"
     torch.cuda.set_device(0)
     session = roost_amd.OpSession(device=0)
+    global FLUSH
+    FLUSH = Flush(torch)
     if args.only is not None:
         fn = {"decode": bench_decode, "prefill": bench_prefill, "gdn": bench_gdn, "mixed": bench_mixed,
               "layer": bench_layer_ops, "attn_in": bench_attention_input,
@@ -493,11 +650,11 @@ def main():
     log("mixed hybrid step (config 5) ...")
     mixed = bench_mixed(torch, roost_amd, session, max(args.steps // 2, 3), max(args.warmup // 2, 1))
     log(f"  {json.dumps(mixed)}")
-    cpu = None
+    cpu = cpu_host = cpu_rows = None
     if not args.skip_cpu:
-        log("cpu baseline ...")
-        cpu = cpu_baseline(b, args.cpu_sample)
-        log(f"  {cpu}")
+        log("cpu baselines ...")
+        cpu_host, cpu_rows, cpu = cpu_baselines(b, pb)
+        log(f"  {cpu_host} {json.dumps(_rounded(cpu_rows))}")
     line = {
         "metric": METRIC,
         "value": round(dec_gbs, 1),
@@ -514,6 +671,8 @@ def main():
         "config": {"workload": "BASELINE config 2: paged decode, Qwen3.5-0.8B full-attention shape",
                    "batch": 64, "ctx": "U(512, 8192)", "context_tokens": int(b.kv_lens.sum()), "q_heads": 8,
                    "kv_heads": 2, "head_dim": 256, "page_size": 16, "pool_pages": b.pool},
+        "cold": {"ms_per_step": round(b.cold_ms, 5), "gb_s": round(dec_bytes / b.cold_ms / 1e6, 1),
+                 "note": "median of 10 launches, each after reading a 512 MiB buffer (evicts the 256 MB MALL)"},
         "roofline": {"bound": "hbm", "achieved": round(dec_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "algorithmic_bytes": dec_bytes, "kernel": "DecodeKernel + DecodeMergeKernel (one run())"},
@@ -521,7 +680,9 @@ def main():
         "prefill": {"workload": "BASELINE config 3: 8 seqs, chunk U(256, 2048) on prefix U(0, 6144), causal",
                     "ms": round(pre_ms, 4), "tflops": round(pre_tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                     "frac": round(pre_tflops / MFMA_BF16_PEAK_TFLOPS, 4), "flops": pb.prefill_flops(),
-                    "query_tokens": pb.tokens,
+                    "query_tokens": pb.tokens, "stat": "median of back-to-back launches, attention call only",
+                    "append_plus_attention_ms": round(pb.append_ms, 4),
+                    "append_plus_attention_tflops": round(pb.prefill_flops() / pb.append_ms / 1e9, 1),
                     "head_dim_128": {"ms": round(pre128_ms, 4), "tflops": round(pre128_flops / pre128_ms / 1e9, 1),
                                      "frac": round(pre128_flops / pre128_ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
                                      "note": "the same draw at head dim 128 (not a BASELINE config)"},
@@ -531,6 +692,7 @@ def main():
         "gdn_layer_ops": {k: _rounded(v) for k, v in layer.items()},
         "attention_input_ops": {k: _rounded(v) for k, v in attn_in.items()},
         "cpu_baseline": cpu,
+        "cpu_baselines": {"host": cpu_host, "rows": _rounded(cpu_rows) if cpu_rows else None},
     }
     session.close()
     print(json.dumps(line), flush=True)
