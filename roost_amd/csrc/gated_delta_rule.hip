@@ -27,10 +27,9 @@ namespace {
 
 using namespace roost_dev;
 
-constexpr uint32_t kHeads = 16;
-constexpr uint32_t kDim = 128;
-constexpr uint32_t kRow = kHeads * kDim;
-constexpr uint64_t kStateElems = uint64_t{kHeads} * kDim * kDim;
+constexpr uint32_t kDim = 128;          // key and value head size (Qwen3.5)
+constexpr uint32_t kMaxHeads = 128;     // value heads of one call
+constexpr uint32_t kMaxGroup = 8;       // value heads per key head
 constexpr uint64_t kMaxTokens = uint64_t{1} << 24;
 constexpr uint32_t kMaxBatch = 1u << 20;
 constexpr uint32_t kChunk = 64;
@@ -39,7 +38,12 @@ constexpr uint32_t kChunk = 64;
 constexpr uint32_t kRouteMinTokens = 16;
 constexpr uint32_t kPlanMagic = 0x50444752;  // "RGDP"
 
-uint32_t Stride(uint32_t s) { return s == 0 ? kRow : s; }
+// Row widths of the views (elements): q and k rows hold k_heads heads, v and output rows v_heads heads; a stride of 0
+// means rows packed at their width. A state slot is [v_heads, 128, 128] fp32.
+uint64_t KRow(const RoostGatedDeltaRuleParams& p) { return uint64_t{p.k_heads} * kDim; }
+uint64_t VRow(const RoostGatedDeltaRuleParams& p) { return uint64_t{p.v_heads} * kDim; }
+uint64_t StateElems(const RoostGatedDeltaRuleParams& p) { return uint64_t{p.v_heads} * kDim * kDim; }
+uint64_t Stride(uint32_t s, uint64_t row) { return s == 0 ? row : s; }
 
 constexpr char kOp[] = "gated_delta_rule";
 
@@ -48,38 +52,44 @@ constexpr char kOp[] = "gated_delta_rule";
 RoostStatus Admit(const RoostGatedDeltaRuleParams& p, bool planning) {
   roost::Gate gate(kOp);
   gate.Header(&p, sizeof(RoostGatedDeltaRuleParams))
-      .Expect(p.k_heads == kHeads && p.v_heads == kHeads && p.k_dim == kDim && p.v_dim == kDim,
-              ROOST_STATUS_UNSUPPORTED, "heads %u/%u of dims %u/%u (key/value): the kernels are built for the "
-              "Qwen3.5-0.8B shape, 16/16 heads of 128", p.k_heads, p.v_heads, p.k_dim, p.v_dim)
+      .Expect(p.k_dim == kDim && p.v_dim == kDim, ROOST_STATUS_UNSUPPORTED,
+              "head sizes %u / %u (key / value): the kernels are built for 128 (Qwen3.5)", p.k_dim, p.v_dim)
+      .Expect(p.k_heads >= 1 && p.v_heads % std::max(p.k_heads, 1u) == 0 && p.v_heads / std::max(p.k_heads, 1u) >= 1 &&
+                  p.v_heads / std::max(p.k_heads, 1u) <= kMaxGroup && p.v_heads <= kMaxHeads,
+              ROOST_STATUS_UNSUPPORTED, "%u value heads over %u key heads: built for 1 to %u value heads per key head, "
+              "at most %u value heads", p.v_heads, p.k_heads, kMaxGroup, kMaxHeads)
       .Expect(p.l2_norm_qk != 0, ROOST_STATUS_UNSUPPORTED, "l2_norm_qk = 0: the kernels always normalise q and k")
       .Expect(p.tokens <= kMaxTokens && p.batch <= kMaxBatch, ROOST_STATUS_INVALID_ARGUMENT,
               "%u tokens in %u sequences exceeds one call's limits (%llu tokens, %u sequences)", p.tokens, p.batch,
               static_cast<unsigned long long>(kMaxTokens), kMaxBatch);
   ROOST_GATE_RETURN(gate);
-  const uint64_t qs = Stride(p.q_stride), ks = Stride(p.k_stride), vs = Stride(p.v_stride);
-  gate.Expect(qs >= kRow && ks >= kRow && vs >= kRow, ROOST_STATUS_INVALID_ARGUMENT,
-              "row strides q %llu, k %llu, v %llu: each view row holds %u elements", static_cast<unsigned long long>(qs),
-              static_cast<unsigned long long>(ks), static_cast<unsigned long long>(vs), kRow);
+  const uint64_t krow = KRow(p), vrow = VRow(p);
+  const uint64_t qs = Stride(p.q_stride, krow), ks = Stride(p.k_stride, krow), vs = Stride(p.v_stride, vrow);
+  gate.Expect(qs >= krow && ks >= krow && vs >= vrow, ROOST_STATUS_INVALID_ARGUMENT,
+              "row strides q %llu, k %llu, v %llu: q and k rows hold %llu elements, v rows %llu",
+              static_cast<unsigned long long>(qs), static_cast<unsigned long long>(ks),
+              static_cast<unsigned long long>(vs), static_cast<unsigned long long>(krow),
+              static_cast<unsigned long long>(vrow));
   ROOST_GATE_RETURN(gate);
   // A strided view reaches (tokens - 1) * stride + one row.
   const uint64_t t = p.tokens;
-  auto reach = [t](uint64_t stride) { return t == 0 ? 0 : (t - 1) * stride + kRow; };
-  gate.Tensor("q", p.q, ROOST_DTYPE_BF16, reach(qs))
-      .Tensor("k", p.k, ROOST_DTYPE_BF16, reach(ks))
-      .Tensor("v", p.v, ROOST_DTYPE_BF16, reach(vs));
+  auto reach = [t](uint64_t stride, uint64_t row) { return t == 0 ? 0 : (t - 1) * stride + row; };
+  gate.Tensor("q", p.q, ROOST_DTYPE_BF16, reach(qs, krow))
+      .Tensor("k", p.k, ROOST_DTYPE_BF16, reach(ks, krow))
+      .Tensor("v", p.v, ROOST_DTYPE_BF16, reach(vs, vrow));
   ROOST_GATE_RETURN(gate);
   // g, beta and output of another type are shapes the kernels do not cover (UNSUPPORTED, as the contract has it).
   gate.Expect(p.g.dtype == ROOST_DTYPE_F32 && p.beta.dtype == ROOST_DTYPE_BF16 && p.output.dtype == ROOST_DTYPE_BF16,
               ROOST_STATUS_UNSUPPORTED, "g %s, beta %s, output %s: built for f32 g with bf16 beta and output",
               roost::Describe(p.g.dtype).name, roost::Describe(p.beta.dtype).name, roost::Describe(p.output.dtype).name);
   ROOST_GATE_RETURN(gate);
-  gate.Tensor("g", p.g, ROOST_DTYPE_F32, t * kHeads)
-      .Tensor("beta", p.beta, ROOST_DTYPE_BF16, t * kHeads)
-      .Tensor("output", p.output, ROOST_DTYPE_BF16, t * kRow)
-      .Tensor("state", p.state, ROOST_DTYPE_F32, kStateElems)
-      .Expect(p.state.length % kStateElems == 0, ROOST_STATUS_INVALID_ARGUMENT,
-              "state pool of %llu floats is not a whole number of [16, 128, 128] slots",
-              static_cast<unsigned long long>(p.state.length))
+  gate.Tensor("g", p.g, ROOST_DTYPE_F32, t * p.v_heads)
+      .Tensor("beta", p.beta, ROOST_DTYPE_BF16, t * p.v_heads)
+      .Tensor("output", p.output, ROOST_DTYPE_BF16, t * vrow)
+      .Tensor("state", p.state, ROOST_DTYPE_F32, StateElems(p))
+      .Expect(p.state.length % StateElems(p) == 0, ROOST_STATUS_INVALID_ARGUMENT,
+              "state pool of %llu floats is not a whole number of [%u, 128, 128] slots",
+              static_cast<unsigned long long>(p.state.length), p.v_heads)
       .Tensor("state_slots", p.state_slots, ROOST_DTYPE_I32, p.batch)
       .Tensor("cu_seqlens", p.cu_seqlens, ROOST_DTYPE_I32, uint64_t{p.batch} + 1)
       .Aligned("g", p.g.address, 16)
@@ -102,7 +112,9 @@ RoostStatus AdmitForSizing(const void* params, const RoostWorkspaceSizes* sizes)
   ROOST_GATE_RETURN(gate);
   const auto& p = *static_cast<const RoostGatedDeltaRuleParams*>(params);
   gate.Expect(p.tokens <= kMaxTokens && p.batch <= kMaxBatch, ROOST_STATUS_INVALID_ARGUMENT,
-              "%u tokens in %u sequences exceeds one call's limits", p.tokens, p.batch);
+              "%u tokens in %u sequences exceeds one call's limits", p.tokens, p.batch)
+      .Expect(p.v_heads >= 1 && p.v_heads <= kMaxHeads, ROOST_STATUS_UNSUPPORTED,
+              "%u value heads: built for 1 to %u", p.v_heads, kMaxHeads);
   return gate.status();
 }
 
@@ -125,6 +137,8 @@ struct GdnArgs {
   uint64_t pool_slots;
   uint32_t use_initial_state;
   float scale;
+  uint32_t vh;     // value heads (the rows of v, output, g and beta, the heads of a state slot)
+  uint32_t group;  // value heads per key head: value head h reads q / k head h / group
 };
 
 // Loads 32 consecutive bf16 of a row as floats: 16-byte loads when the view is 16-byte aligned, else 2-byte loads.
@@ -177,9 +191,9 @@ __global__ void __launch_bounds__(128) RecurrentKernel(GdnArgs a) {
   const int t = threadIdx.x;
   const int rq = t & 3;   // key rows 32*rq .. +31
   const int cg = t >> 2;  // value columns 4*cg .. +3
-  const uint32_t kh = h;  // one value head per key head
+  const uint32_t kh = h / a.group;
   float4 s[32];
-  float* sp = has_slot ? a.state + (static_cast<uint64_t>(slot) * kHeads + h) * kDim * kDim : nullptr;
+  float* sp = has_slot ? a.state + (static_cast<uint64_t>(slot) * a.vh + h) * kDim * kDim : nullptr;
   if (has_slot && a.use_initial_state) {
 #pragma unroll
     for (int i = 0; i < 32; ++i) s[i] = LoadStreamF4(sp + (rq * 32 + i) * kDim + cg * 4);
@@ -201,7 +215,7 @@ __global__ void __launch_bounds__(128) RecurrentKernel(GdnArgs a) {
     kk = QuadSum(kk);
     const float qn = a.scale / sqrtf(qq + 1e-6f);
     const float kn = 1.0f / sqrtf(kk + 1e-6f);
-    const uint64_t gi = static_cast<uint64_t>(tok) * kHeads + h;
+    const uint64_t gi = static_cast<uint64_t>(tok) * a.vh + h;
     const float decay = expf(a.g[gi]);
     const float beta = Bf16ToF32(a.beta[gi]);
     const uint16_t* vrow = a.v + static_cast<uint64_t>(tok) * a.v_stride + h * kDim + cg * 4;
@@ -242,7 +256,7 @@ __global__ void __launch_bounds__(128) RecurrentKernel(GdnArgs a) {
       uint2 w;
       w.x = PackBf16(o[0], o[1]);
       w.y = PackBf16(o[2], o[3]);
-      *reinterpret_cast<uint2*>(a.out + (static_cast<uint64_t>(tok) * kHeads + h) * kDim + cg * 4) = w;
+      *reinterpret_cast<uint2*>(a.out + (static_cast<uint64_t>(tok) * a.vh + h) * kDim + cg * 4) = w;
     }
   }
   if (has_slot) {
@@ -262,10 +276,12 @@ GdnArgs MakeArgs(const RoostGatedDeltaRuleParams& p) {
   a.state = static_cast<float*>(p.state.address);
   a.slots = static_cast<const int32_t*>(p.state_slots.address);
   a.cu = static_cast<const int32_t*>(p.cu_seqlens.address);
-  a.q_stride = Stride(p.q_stride);
-  a.k_stride = Stride(p.k_stride);
-  a.v_stride = Stride(p.v_stride);
-  a.pool_slots = p.state.length / kStateElems;
+  a.q_stride = Stride(p.q_stride, KRow(p));
+  a.k_stride = Stride(p.k_stride, KRow(p));
+  a.v_stride = Stride(p.v_stride, VRow(p));
+  a.pool_slots = p.state.length / StateElems(p);
+  a.vh = p.v_heads;
+  a.group = p.v_heads / p.k_heads;
   a.use_initial_state = p.use_initial_state;
   a.scale = Scale(p);
   return a;
@@ -273,7 +289,7 @@ GdnArgs MakeArgs(const RoostGatedDeltaRuleParams& p) {
 
 bool Vec16(const RoostGatedDeltaRuleParams& p) {
   auto Aligned = [](const void* a, uint64_t n) { return roost::IsAligned(a, n); };
-  const uint64_t qs = Stride(p.q_stride), ks = Stride(p.k_stride), vs = Stride(p.v_stride);
+  const uint64_t qs = Stride(p.q_stride, KRow(p)), ks = Stride(p.k_stride, KRow(p)), vs = Stride(p.v_stride, VRow(p));
   return Aligned(p.q.address, 16) && Aligned(p.k.address, 16) && Aligned(p.v.address, 16) && qs % 8 == 0 &&
          ks % 8 == 0 && vs % 8 == 0;
 }
@@ -281,7 +297,7 @@ bool Vec16(const RoostGatedDeltaRuleParams& p) {
 RoostStatus LaunchRecurrent(const RoostGatedDeltaRuleParams& p, hipStream_t stream, int32_t route_min = 0) {
   GdnArgs a = MakeArgs(p);
   a.route_min = route_min;
-  const dim3 grid(p.batch, kHeads);
+  const dim3 grid(p.batch, p.v_heads);
   if (Vec16(p)) {
     hipLaunchKernelGGL(RecurrentKernel<true>, grid, dim3(128), 0, stream, a);
   } else {
@@ -456,7 +472,8 @@ __global__ void __launch_bounds__(256, 4) WyPrepKernel(ChunkArgs ca) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, kq = lane >> 4;
-  uint8_t* rec = ca.recs + (static_cast<uint64_t>(blockIdx.x) * kHeads + h) * kRecBytes;
+  const uint32_t kh = h / a.group;
+  uint8_t* rec = ca.recs + (static_cast<uint64_t>(blockIdx.x) * a.vh + h) * kRecBytes;
 
   // region0 holds the raw q (tile 0) and k (tile 1) rows; once the products are formed it holds A and T (fp32).
   __shared__ __align__(16) uint8_t region0[2 * 64 * kTilePitch * 2];
@@ -470,15 +487,15 @@ __global__ void __launch_bounds__(256, 4) WyPrepKernel(ChunkArgs ca) {
     const int row = tid >> 2, part = tid & 3;
     const uint32_t keep = row < n ? ~0u : 0u;
     const uint64_t tok = static_cast<uint64_t>(t0 + min(row, n - 1));
-    const uint16_t* kp = a.k + tok * a.k_stride + h * kDim + part * 32;
-    const uint16_t* qp = a.q + tok * a.q_stride + h * kDim + part * 32;
+    const uint16_t* kp = a.k + tok * a.k_stride + kh * kDim + part * 32;
+    const uint16_t* qp = a.q + tok * a.q_stride + kh * kDim + part * 32;
     uint4 kv[4], qv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       kv[i] = Load8<kVec>(kp + 8 * i);
       qv[i] = Load8<kVec>(qp + 8 * i);
     }
-    const uint64_t gi = static_cast<uint64_t>(t0 + min(lane, n - 1)) * kHeads + h;
+    const uint64_t gi = static_cast<uint64_t>(t0 + min(lane, n - 1)) * a.vh + h;
     const float graw = a.g[gi];
     const uint16_t braw = a.beta[gi];
     float kk = 0.0f, qq = 0.0f;
@@ -676,8 +693,8 @@ __device__ __forceinline__ CopyOffsets MakeCopyOffsets(const GdnArgs& a, uint32_
 #pragma unroll
   for (uint32_t j = 0; j < 4; ++j) {
     const uint32_t piece = pos ^ (rr << 2) ^ j;
-    o.k[j] = static_cast<uint32_t>(rr * a.k_stride * 2) + h * 256 + 16 * piece;
-    o.q[j] = static_cast<uint32_t>(rr * a.q_stride * 2) + h * 256 + 16 * piece;
+    o.k[j] = static_cast<uint32_t>(rr * a.k_stride * 2) + (h / a.group) * 256 + 16 * piece;
+    o.q[j] = static_cast<uint32_t>(rr * a.q_stride * 2) + (h / a.group) * 256 + 16 * piece;
   }
   o.v = static_cast<uint32_t>((static_cast<uint32_t>(lane) >> 2) * a.v_stride * 2) + h * 256 + vb * 64 +
         16 * (static_cast<uint32_t>(lane) & 3);
@@ -734,8 +751,8 @@ __device__ __forceinline__ void Fetch(const GdnArgs& a, const CopyOffsets& co, c
       const int row = 4 * i + rr;
       const int piece = pos ^ Hsw(row);
       const uint64_t tok = static_cast<uint64_t>(t0 + min(row, n - 1));
-      Copy16<kVec>(a.k + tok * a.k_stride + h * kDim + 8 * piece, st.kt, l_kt, i, lane);
-      Copy16<kVec>(a.q + tok * a.q_stride + h * kDim + 8 * piece, st.qt, l_qt, i, lane);
+      Copy16<kVec>(a.k + tok * a.k_stride + (h / a.group) * kDim + 8 * piece, st.kt, l_kt, i, lane);
+      Copy16<kVec>(a.q + tok * a.q_stride + (h / a.group) * kDim + 8 * piece, st.qt, l_qt, i, lane);
     }
   }
 }
@@ -748,7 +765,7 @@ __device__ __forceinline__ void StoreOut(const GdnArgs& a, const Stage& st, int 
     const int t = 16 * i + (lane >> 2);
     const uint4 v = *reinterpret_cast<const uint4*>(st.ob + t * 64 + 16 * (lane & 3));
     if (t < n) {
-      *reinterpret_cast<uint4*>(a.out + (static_cast<uint64_t>(t0 + t) * kHeads + h) * kDim + vb * 32 + 8 * (lane & 3)) = v;
+      *reinterpret_cast<uint4*>(a.out + (static_cast<uint64_t>(t0 + t) * a.vh + h) * kDim + vb * 32 + 8 * (lane & 3)) = v;
     }
   }
 }
@@ -921,9 +938,9 @@ __global__ void __launch_bounds__(256, 1) WyScanKernel(ChunkArgs ca) {
   const uint32_t chain = (x & 7) + 8 * (x >> 5);
   const uint32_t vb = (x >> 3) & 3;
   if (chain >= ca.chains) return;
-  const int32_t listed = ca.seq_list != nullptr ? ca.seq_list[chain / kHeads] : static_cast<int32_t>(chain / kHeads);
+  const int32_t listed = ca.seq_list != nullptr ? ca.seq_list[chain / a.vh] : static_cast<int32_t>(chain / a.vh);
   if (listed < 0) return;
-  const uint32_t seq = static_cast<uint32_t>(listed), h = chain % kHeads;
+  const uint32_t seq = static_cast<uint32_t>(listed), h = chain % a.vh;
   const int4 sq = ca.seqs[seq];
   const int chunks = sq.y;
   if (chunks == 0) return;  // an empty (or unrouted) sequence leaves its slot untouched
@@ -935,7 +952,7 @@ __global__ void __launch_bounds__(256, 1) WyScanKernel(ChunkArgs ca) {
   auto t0_of = [&](int c) { return sq.z + 64 * c; };
   auto n_of = [&](int c) { return min(64, sq.w - t0_of(c)); };
   auto rec_of = [&](int c) {
-    return ca.recs + (static_cast<uint64_t>(sq.x + c) * kHeads + h) * kRecBytes;
+    return ca.recs + (static_cast<uint64_t>(sq.x + c) * a.vh + h) * kRecBytes;
   };
 
   const uint32_t lds0 = Uniform(LdsAddr(&stage[0]));  // LDS byte address of stage[0]; stage[1] follows it
@@ -962,7 +979,7 @@ __global__ void __launch_bounds__(256, 1) WyScanKernel(ChunkArgs ca) {
   const int32_t slot = a.slots[seq];
   const bool has_slot = slot >= 0 && static_cast<uint64_t>(slot) < a.pool_slots;
   const uint32_t col = vb * 32 + 16 * w + m;
-  float* sp = has_slot ? a.state + (static_cast<uint64_t>(slot) * kHeads + h) * kDim * kDim : nullptr;
+  float* sp = has_slot ? a.state + (static_cast<uint64_t>(slot) * a.vh + h) * kDim * kDim : nullptr;
   // st[mt][i] = S[32 (mt >> 1) + 8g + 4 (mt & 1) + i][col]
   f32x4_t st[8];
 #pragma unroll
@@ -1008,7 +1025,7 @@ struct ChunkArena {
   uint32_t max_chunks;
 };
 
-ChunkArena MakeArena(uint64_t max_chunks, uint64_t batch, uint64_t max_long = 0) {
+ChunkArena MakeArena(uint64_t max_chunks, uint64_t batch, uint64_t heads, uint64_t max_long = 0) {
   ChunkArena l{};
   l.max_chunks = static_cast<uint32_t>(max_chunks);
   l.max_long = static_cast<uint32_t>(max_long);
@@ -1017,18 +1034,20 @@ ChunkArena MakeArena(uint64_t max_chunks, uint64_t batch, uint64_t max_long = 0)
   l.seq_list = l.seq_table + 16ull * batch;
   l.tables_bytes = roost::RoundUp(l.seq_list + 4ull * max_long, 256);
   l.records = l.tables_bytes;
-  l.total = l.records + uint64_t{l.max_chunks} * kHeads * wy::kRecBytes;
+  l.total = l.records + uint64_t{l.max_chunks} * heads * wy::kRecBytes;
   return l;
 }
 
 // Every sequence may be chunked (chunk variant): at most tokens / 64 + batch chunks.
-ChunkArena MakeChunkArena(uint64_t tokens, uint64_t batch) { return MakeArena(tokens / kChunk + batch, batch); }
+ChunkArena MakeChunkArena(uint64_t tokens, uint64_t batch, uint64_t heads) {
+  return MakeArena(tokens / kChunk + batch, batch, heads);
+}
 
 // Only sequences of kRouteMinTokens or more are chunked (recurrent variant): sum ceil(len / 64) over them is at most
 // tokens / 64 plus their number, which is at most min(batch, tokens / kRouteMinTokens).
-ChunkArena MakeRouteArena(uint64_t tokens, uint64_t batch) {
+ChunkArena MakeRouteArena(uint64_t tokens, uint64_t batch, uint64_t heads) {
   const uint64_t max_long = std::min<uint64_t>(batch, tokens / kRouteMinTokens);
-  return MakeArena(tokens / kChunk + max_long, batch, max_long);
+  return MakeArena(tokens / kChunk + max_long, batch, heads, max_long);
 }
 
 
@@ -1120,8 +1139,8 @@ RoostStatus LaunchChunk(const RoostGatedDeltaRuleParams& p, const RoostWorkspace
   ca.recs = base + l.records;
   // The recurrent variant's calls list their chunked sequences; the chunk variant's chains are every sequence.
   ca.seq_list = l.max_long > 0 ? reinterpret_cast<const int32_t*>(base + l.seq_list) : nullptr;
-  ca.chains = (l.max_long > 0 ? l.max_long : p.batch) * kHeads;
-  const dim3 prep(chunks, kHeads);
+  ca.chains = (l.max_long > 0 ? l.max_long : p.batch) * p.v_heads;
+  const dim3 prep(chunks, p.v_heads);
   const dim3 scan((ca.chains + 7) / 8 * 8 * kVBlocks);
   if (Vec16(p)) {
     hipLaunchKernelGGL(WyPrepKernel<true>, prep, dim3(256), 0, stream, ca);
@@ -1162,7 +1181,7 @@ extern "C" ROOST_API RoostStatus roost_gdn_recurrent_workspace(RoostContext*, co
   // The views and the pool slots are read in place; a call that may hold a sequence of kRouteMinTokens or more
   // tokens also gets the chunk tables and records for the sequences it hands to the chunk kernels.
   *sizes = RoostWorkspaceSizes{};
-  sizes->device_bytes = p.tokens >= kRouteMinTokens ? MakeRouteArena(p.tokens, p.batch).total : 0;
+  sizes->device_bytes = p.tokens >= kRouteMinTokens ? MakeRouteArena(p.tokens, p.batch, p.v_heads).total : 0;
   sizes->device_alignment = 256;
   return ROOST_STATUS_OK;
 }
@@ -1188,7 +1207,7 @@ extern "C" ROOST_API RoostStatus roost_gdn_recurrent_run(RoostContext* ctx, cons
       if (!any_long) return LaunchRecurrent(p, s);
     }
     // Every launch size below follows from tokens and batch alone, so the call can be captured into a graph.
-    const ChunkArena l = MakeRouteArena(p.tokens, p.batch);
+    const ChunkArena l = MakeRouteArena(p.tokens, p.batch, p.v_heads);
     gate.Expect(roost::HasDeviceRegion(ws, l.total), ROOST_STATUS_WORKSPACE_TOO_SMALL,
                 "%u tokens may route sequences to the chunk kernels, which need %llu device workspace bytes",
                 p.tokens, static_cast<unsigned long long>(l.total));
@@ -1202,7 +1221,7 @@ extern "C" ROOST_API RoostStatus roost_gdn_recurrent_run(RoostContext* ctx, cons
 extern "C" ROOST_API RoostStatus roost_gdn_chunk_workspace(RoostContext*, const void* params, RoostWorkspaceSizes* sizes) {
   ROOST_RETURN_IF_FAILED(AdmitForSizing(params, sizes));
   const auto& p = *static_cast<const RoostGatedDeltaRuleParams*>(params);
-  const ChunkArena l = MakeChunkArena(p.tokens, p.batch);
+  const ChunkArena l = MakeChunkArena(p.tokens, p.batch, p.v_heads);
   *sizes = RoostWorkspaceSizes{};
   sizes->device_bytes = l.total;
   sizes->pinned_host_bytes = l.tables_bytes;
@@ -1239,7 +1258,7 @@ extern "C" ROOST_API RoostStatus roost_gdn_chunk_plan(RoostContext* ctx, const v
   const auto& p = *static_cast<const RoostGatedDeltaRuleParams*>(params);
   return roost::CatchAll(kOp, [&]() -> RoostStatus {
     ROOST_RETURN_IF_FAILED(Admit(p, true));
-    const ChunkArena l = MakeChunkArena(p.tokens, p.batch);
+    const ChunkArena l = MakeChunkArena(p.tokens, p.batch, p.v_heads);
     gate.Expect(roost::HasDeviceRegion(ws, l.total) && ws->pinned_host != nullptr &&
                     ws->pinned_host_bytes >= l.tables_bytes && ws->plan != nullptr &&
                     ws->plan_bytes >= sizeof(ChunkStamp),
@@ -1277,7 +1296,7 @@ extern "C" ROOST_API RoostStatus roost_gdn_chunk_run(RoostContext* ctx, const vo
   return roost::CatchAll(kOp, [&]() -> RoostStatus {
     ROOST_RETURN_IF_FAILED(Admit(p, false));
     if (p.batch == 0 || p.tokens == 0) return ROOST_STATUS_OK;
-    const ChunkArena l = MakeChunkArena(p.tokens, p.batch);
+    const ChunkArena l = MakeChunkArena(p.tokens, p.batch, p.v_heads);
     gate.Expect(roost::HasDeviceRegion(ws, l.total) && ws->plan != nullptr && ws->plan_bytes >= sizeof(ChunkStamp),
                 ROOST_STATUS_WORKSPACE_TOO_SMALL, "the call needs %llu device bytes and its plan record",
                 static_cast<unsigned long long>(l.total));
@@ -1342,7 +1361,7 @@ extern "C" ROOST_API RoostStatus roost_amd_gdn_recurrent_run_noalloc(RoostContex
     if (p.batch == 0 || p.tokens == 0) return ROOST_STATUS_OK;
     hipStream_t s = roost::Stream(stream);
     if (p.tokens < kRouteMinTokens) return LaunchRecurrent(p, s);
-    const ChunkArena l = MakeRouteArena(p.tokens, p.batch);
+    const ChunkArena l = MakeRouteArena(p.tokens, p.batch, p.v_heads);
     gate.Expect(l.total <= kStaticScratchBytes, ROOST_STATUS_INVALID_ARGUMENT,
                 "%u tokens in %u sequences need %llu bytes of routing scratch; the allocation-free path holds %llu",
                 p.tokens, p.batch, static_cast<unsigned long long>(l.total),

@@ -60,6 +60,17 @@ constexpr uint32_t kAlign = 256;
 constexpr uint32_t kPlanMagic = 0x41504752;     // "RGPA"
 constexpr float kLog2e = 1.4426950408889634f;
 
+// Logit soft capping (CpuOps.cs:276: s -> cap tanh(s / cap) after the scale), applied to scores in log2 units:
+// y -> capl tanh(y / capl) with capl = |cap| log2(e), through tanh(u) = 1 - 2 / (1 + e^(2u)) = 1 - 2 / (1 + 2^(y k)),
+// k = 2 log2(e) / capl. capl = 0 turns it off. Masked scores are set to -inf after capping.
+struct SoftCap {
+  float capl;
+  float k;
+};
+__device__ __forceinline__ float Capped(float y, SoftCap c) {
+  return c.capl - 2.0f * c.capl * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(y * c.k));
+}
+
 struct DecodeWork {
   int32_t seq;
   int32_t token_begin;  // first key of this piece (a multiple of 16)
@@ -212,8 +223,8 @@ RoostStatus Admit(const RoostPagedAttentionParams& p, bool for_run) {
               "heads per KV head", p.q_heads, p.kv_heads)
       // CpuOps.cs:180-186: a window of 0 keys is an error; -1 (any negative value) means no window.
       .Expect(p.window_left != 0, ROOST_STATUS_INVALID_ARGUMENT, "window_left = 0 is not a window; pass -1 for none")
-      .Expect(p.logits_soft_cap == 0.0f, ROOST_STATUS_UNSUPPORTED, "logits_soft_cap = %g: capping has no kernel here",
-              p.logits_soft_cap)
+      .Expect(std::isfinite(p.logits_soft_cap), ROOST_STATUS_INVALID_ARGUMENT,
+              "logits_soft_cap = %g; a finite cap (0 for none) is required", p.logits_soft_cap)
       .Expect(p.kv_layout == ROOST_LAYOUT_PAGED_NHD || p.kv_layout == ROOST_LAYOUT_PAGED_HND,
               ROOST_STATUS_INVALID_ARGUMENT, "kv_layout = %u is not a paged layout (NHD or HND)", p.kv_layout)
       .Expect(p.batch > 0 && p.page_size > 0, ROOST_STATUS_INVALID_ARGUMENT,
@@ -282,6 +293,14 @@ uint32_t KvLenHost(const RoostPagedAttentionParams& p, uint32_t b) {
 // The sliding window: query position pos sees keys j >= pos - window (reference CpuOps.cs:180-197, 245-252); -1 (any
 // negative window_left) means no window.
 int32_t WindowOf(const RoostPagedAttentionParams& p) { return p.window_left < 0 ? -1 : p.window_left; }
+// The soft cap as the kernels apply it (in log2 units); a cap of 0 is off and the sign of the cap does not matter
+// (cap tanh(s / cap) is even in cap).
+SoftCap CapOf(const RoostPagedAttentionParams& p) {
+  const float cap = std::fabs(p.logits_soft_cap);
+  if (cap == 0.0f) return SoftCap{0.0f, 0.0f};
+  const float capl = cap * kLog2e;
+  return SoftCap{capl, 2.0f * kLog2e / capl};
+}
 // First key a decode query (position kv - 1) sees.
 int64_t DecodeFirstKey(int64_t kv, int32_t window) { return window < 0 ? 0 : std::max<int64_t>(0, kv - 1 - window); }
 
@@ -663,7 +682,7 @@ struct DecodeState {
 template <typename T, int D, typename QW>
 __device__ __forceinline__ void DecodeGroup(DecodeState<T, D>& st, const uint4* kr, const uint4* vr, uint32_t valid,
                                             const QW (*qr)[DecodeCfg<T, D>::kQWords], float* x_row, int r, int ri,
-                                            int lane, float scale_log2) {
+                                            int lane, float scale_log2, SoftCap cap) {
   using C = DecodeCfg<T, D>;
   constexpr int kVec = C::kVec, kLpr = C::kLpr, kNi = C::kNi;
   float s[kLpr];
@@ -677,7 +696,9 @@ __device__ __forceinline__ void DecodeGroup(DecodeState<T, D>& st, const uint4* 
     for (int j = 0; j < mk; ++j) s[j] += ShflXor(s[j + mk], mk);
   const int my_head = r % kGroup;
   const bool my_valid = (valid >> (r / kGroup)) & 1u;
-  const float sc = my_valid ? s[0] * scale_log2 : -INFINITY;
+  float y = s[0] * scale_log2;
+  if (cap.capl != 0.0f) y = Capped(y, cap);
+  const float sc = my_valid ? y : -INFINITY;
   // Group max per head (lanes sharing r % 4), then every lane learns all 4.
   float gm = sc;
 #pragma unroll
@@ -773,7 +794,7 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 template <int D>
 __device__ __forceinline__ void DecodeGroupMfma(DecodeState<uint16_t, D>& st, const uint4* kr, const uint4* vr,
                                                 uint32_t validmask, const u32x4_t* qb, float* x_row, int r, int ri,
-                                                int lane, float scale_log2) {
+                                                int lane, float scale_log2, SoftCap cap) {
   using C = DecodeCfg<uint16_t, D>;
   constexpr int kVec = C::kVec, kTpi = C::kTpi, kNi = C::kNi, kChunks = D / 32;
   f32x4_t acc4 = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -789,7 +810,9 @@ __device__ __forceinline__ void DecodeGroupMfma(DecodeState<uint16_t, D>& st, co
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const bool ok = col < (int)kGroup && ((validmask >> (tok0 + j)) & 1u);
-    sc[j] = ok ? acc4[j] * scale_log2 : -INFINITY;
+    float y = acc4[j] * scale_log2;
+    if (cap.capl != 0.0f) y = Capped(y, cap);
+    sc[j] = ok ? y : -INFINITY;
     mx = fmaxf(mx, sc[j]);
   }
   mx = fmaxf(mx, ShflXor(mx, 16));
@@ -873,7 +896,7 @@ __global__ void __launch_bounds__(256, ROOST_DECODE_WGS_PER_CU) DecodeKernel(con
                                                     float* __restrict__ part_o, float* __restrict__ part_ml,
                                                     const int32_t* __restrict__ q_rows,
                                                     uint32_t q_heads, uint32_t heads_per_wg, float scale_log2,
-                                                    int32_t window) {
+                                                    int32_t window, SoftCap cap) {
   using C = DecodeCfg<T, D>;
   constexpr int kVec = C::kVec, kLpr = C::kLpr, kTpi = C::kTpi, kNi = C::kNi;
   constexpr bool kMfma = sizeof(T) == 2;  // bf16: q.k on MFMA; f32: the VALU reduce-scatter path
@@ -1027,9 +1050,9 @@ __global__ void __launch_bounds__(256, ROOST_DECODE_WGS_PER_CU) DecodeKernel(con
         load(gi + s + kLast, kbuf[nxt], vbuf[nxt], valid[nxt]);
         if (gi + s < nw) {
           if constexpr (kMfma) {
-            DecodeGroupMfma<D>(st, kbuf[s], vbuf[s], valid[s], qb, x_lds[wave_id], r, ri, lane, scale_log2);
+            DecodeGroupMfma<D>(st, kbuf[s], vbuf[s], valid[s], qb, x_lds[wave_id], r, ri, lane, scale_log2, cap);
           } else {
-            DecodeGroup<T, D, QW>(st, kbuf[s], vbuf[s], valid[s], qr, x_lds[wave_id], r, ri, lane, scale_log2);
+            DecodeGroup<T, D, QW>(st, kbuf[s], vbuf[s], valid[s], qr, x_lds[wave_id], r, ri, lane, scale_log2, cap);
           }
         }
       }
@@ -1169,7 +1192,7 @@ __device__ __forceinline__ f32x16_t Mfma32(const u32x4_t& a, const u32x4_t& b, c
 __global__ void __launch_bounds__(256, 1)
     PrefillKernel(const uint16_t* __restrict__ q, uint16_t* __restrict__ out, float* __restrict__ lse, KvView kv,
                   const int32_t* __restrict__ q_indptr, const PrefillWork* __restrict__ work, uint32_t q_heads,
-                  uint32_t causal, float scale_log2, int32_t window) {
+                  uint32_t causal, float scale_log2, int32_t window, SoftCap cap) {
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[kPrefillTileK * kKStride];
   __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kPD * kVtStride];
 
@@ -1299,6 +1322,7 @@ __global__ void __launch_bounds__(256, 1)
       for (int v = 0; v < 16; ++v) {
         const int32_t key = kb + kt * 32 + (v >> 2) * 8 + hl * 4 + (v & 3);
         float x = s[kt][v] * scale_log2;
+        if (cap.capl != 0.0f) x = Capped(x, cap);
         if (need_mask && (key >= key_end || (causal && key > my_pos) || (window >= 0 && key < my_pos - window))) {
           x = -INFINITY;
         }
@@ -1452,7 +1476,8 @@ __global__ void __launch_bounds__(512, 1)
     PrefillTileKernel(const uint16_t* __restrict__ q, uint16_t* __restrict__ out, float* __restrict__ lse, KvView kv,
                       const int32_t* __restrict__ kv_indices, const int32_t* __restrict__ q_indptr,
                       const PrefillWork* __restrict__ work, uint16_t* __restrict__ part_o, float* __restrict__ part_ml,
-                      uint32_t q_heads, uint32_t causal, uint32_t ps_shift, float scale_log2, int32_t window) {
+                      uint32_t q_heads, uint32_t causal, uint32_t ps_shift, float scale_log2, int32_t window,
+                      SoftCap cap) {
   static_assert(D == 128 || D == 256, "the tile kernel is built for head dims 128 and 256");
   constexpr int kRowB = 2 * D;                  // bytes of one K or V row in LDS
   constexpr int kPieces = D / 8;                // 16-byte pieces per row
@@ -1619,6 +1644,10 @@ __global__ void __launch_bounds__(512, 1)
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
       __builtin_amdgcn_sched_group_barrier(0x008, kRing, 0);
+      if (cap.capl != 0.0f) {  // capped in log2 units, then kept unscaled like the uncapped scores
+#pragma unroll
+        for (int v = 0; v < 16; ++v) sc[v] = Capped(sc[v] * scale_log2, cap) / scale_log2;
+      }
       if (need_mask) {  // one uniform branch around branch-free selects
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
@@ -1827,11 +1856,11 @@ RoostStatus LaunchDecode(const RoostPagedAttentionParams& p, const PlanRecord& r
   if (p.page_size % 16 == 0) {
     hipLaunchKernelGGL((DecodeKernel<T, D, true>), grid, dim3(256), 0, stream, static_cast<const T*>(p.q.address), out,
                        lse, kv, kv.kv_indices, items, range_ptr, part_o, part_ml, q_rows, p.q_heads, hpw, scale_log2,
-                       WindowOf(p));
+                       WindowOf(p), CapOf(p));
   } else {
     hipLaunchKernelGGL((DecodeKernel<T, D, false>), grid, dim3(256), 0, stream, static_cast<const T*>(p.q.address), out,
                        lse, kv, kv.kv_indices, items, range_ptr, part_o, part_ml, q_rows, p.q_heads, hpw, scale_log2,
-                       WindowOf(p));
+                       WindowOf(p), CapOf(p));
   }
   ROOST_RETURN_IF_FAILED(roost::HipStatus(hipGetLastError(), "paged_attention", "decode launch"));
   if (rec.dec_merges == 0) return ROOST_STATUS_OK;
@@ -1856,10 +1885,10 @@ RoostStatus LaunchPrefill(const RoostPagedAttentionParams& p, const PlanRecord& 
     const uint32_t ps_shift = static_cast<uint32_t>(__builtin_ctz(p.page_size));
     if (p.head_dim == 128) {
       hipLaunchKernelGGL(PrefillTileKernel<128>, grid, dim3(512), 0, stream, q16, outp, lsep, kv, kv.kv_indices,
-                         q_indptr, items, part_o, part_ml, p.q_heads, p.causal, ps_shift, scale_log2, WindowOf(p));
+                         q_indptr, items, part_o, part_ml, p.q_heads, p.causal, ps_shift, scale_log2, WindowOf(p), CapOf(p));
     } else {
       hipLaunchKernelGGL(PrefillTileKernel<256>, grid, dim3(512), 0, stream, q16, outp, lsep, kv, kv.kv_indices,
-                         q_indptr, items, part_o, part_ml, p.q_heads, p.causal, ps_shift, scale_log2, WindowOf(p));
+                         q_indptr, items, part_o, part_ml, p.q_heads, p.causal, ps_shift, scale_log2, WindowOf(p), CapOf(p));
     }
     ROOST_RETURN_IF_FAILED(roost::HipStatus(hipGetLastError(), "paged_attention", "prefill launch"));
     if (rec.merges == 0) return ROOST_STATUS_OK;
@@ -1890,7 +1919,7 @@ RoostStatus LaunchPrefill(const RoostPagedAttentionParams& p, const PlanRecord& 
   }
   hipLaunchKernelGGL(PrefillKernel, dim3(static_cast<uint32_t>(rec.work_items)), dim3(256), 0, stream,
                      static_cast<const uint16_t*>(p.q.address), outp, lsep, kv, q_indptr, items, p.q_heads, p.causal,
-                     scale_log2, WindowOf(p));
+                     scale_log2, WindowOf(p), CapOf(p));
   return roost::HipStatus(hipGetLastError(), "paged_attention", "prefill launch");
 }
 

@@ -106,7 +106,7 @@ RoostConstraints GdnConstraints() {
   c.head_dim_mask = HeadDimBit(128);
   c.layout_mask = 1u << ROOST_LAYOUT_ROW_MAJOR;
   c.min_alignment = 16;
-  c.group_size_mask = 1u;  // one value head per key head (16 over 16)
+  c.group_size_mask = 0xFFu;  // 1 to 8 value heads per key head
   return c;
 }
 

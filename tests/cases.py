@@ -106,9 +106,10 @@ def make_paged_batch(rng: np.random.Generator, kv_lens, q_lens, page_size=16, hn
     return PagedBatch(q, k, v, q_indptr, kv_indptr, kv_indices, last, kv_lens, q_lens, page_size, hnd, bf16, hq, hkv, d)
 
 
-def oracle_attention(b: PagedBatch, causal=True, threads=None, window_left=-1) -> np.ndarray:
+def oracle_attention(b: PagedBatch, causal=True, threads=None, window_left=-1, soft_cap=0.0) -> np.ndarray:
     out = np.zeros_like(b.q)
     oracle.paged_attention(b.q, out, b.k_cache, b.v_cache, b.q_indptr, b.kv_indptr, b.kv_indices, b.kv_last_page_len,
+                           soft_cap=soft_cap,
                            batch=b.batch, tokens=b.tokens, q_heads=b.hq, kv_heads=b.hkv, head_dim=b.d,
                            page_size=b.page_size, hnd=b.hnd, causal=causal, bf16=b.bf16, window_left=window_left,
                            threads=threads or oracle.host_threads())

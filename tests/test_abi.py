@@ -157,7 +157,7 @@ def test_attention_refusals_without_gpu(kernels):
     run = lambda q: e.run(ctx, C.addressof(q), None, None)  # noqa: E731
     assert run(p) == abi.NOT_PLANNED  # valid params, no plan record
     for field, value, want in [("head_dim", 96, abi.UNSUPPORTED), ("q_heads", 12, abi.UNSUPPORTED),
-                               ("window_left", 0, abi.INVALID_ARGUMENT), ("logits_soft_cap", 30.0, abi.UNSUPPORTED),
+                               ("window_left", 0, abi.INVALID_ARGUMENT), ("logits_soft_cap", float("nan"), abi.INVALID_ARGUMENT),
                                ("tokens", 3, abi.INVALID_ARGUMENT), ("mode", 7, abi.INVALID_ARGUMENT),
                                ("kv_layout", 0, abi.INVALID_ARGUMENT), ("batch", 0, abi.INVALID_ARGUMENT),
                                ("struct_size", 64, abi.ABI_MISMATCH), ("abi_minor", 4, abi.ABI_MISMATCH)]:
@@ -195,7 +195,7 @@ def test_gdn_refusals_without_gpu(kernels):
     p.cu_seqlens = _fake(2, abi.DTYPE_I32)
     ctx = kernels.create_context(0)
     run = lambda q: rec.run(ctx, C.addressof(q), None, None)  # noqa: E731
-    for field, value, want in [("k_heads", 8, abi.UNSUPPORTED), ("k_dim", 64, abi.UNSUPPORTED),
+    for field, value, want in [("k_heads", 3, abi.UNSUPPORTED), ("k_heads", 1, abi.UNSUPPORTED), ("k_dim", 64, abi.UNSUPPORTED),
                                ("l2_norm_qk", 0, abi.UNSUPPORTED), ("q_stride", 2040, abi.INVALID_ARGUMENT),
                                ("struct_size", 64, abi.ABI_MISMATCH)]:
         q = abi.GatedDeltaRuleParams.from_buffer_copy(p)

@@ -39,7 +39,7 @@ def from_dev(x, bf16=False):
 class Dev:
     """A PagedBatch on the device plus its params."""
 
-    def __init__(self, b: cases.PagedBatch, causal=True, with_lse=False, window_left=-1):
+    def __init__(self, b: cases.PagedBatch, causal=True, with_lse=False, window_left=-1, soft_cap=0.0):
         self.b = b
         self.q = to_dev(b.q, b.bf16)
         self.k = to_dev(b.k_cache, b.bf16)
@@ -52,6 +52,7 @@ class Dev:
         self.lse = torch().zeros((b.tokens, b.hq), dtype=torch().float32, device="cuda") if with_lse else None
         self.causal = causal
         self.window_left = window_left
+        self.soft_cap = soft_cap
 
     def params(self, host=True, **over):
         b = self.b
@@ -59,7 +60,7 @@ class Dev:
                   kv_last_page_len_host=b.kv_last_page_len if host else None, batch=b.batch, q_heads=b.hq,
                   kv_heads=b.hkv, head_dim=b.d, page_size=b.page_size,
                   kv_layout=abi.LAYOUT_PAGED_HND if b.hnd else abi.LAYOUT_PAGED_NHD, causal=self.causal, lse=self.lse,
-                  window_left=self.window_left)
+                  window_left=self.window_left, soft_cap=self.soft_cap)
         kw.update(over)
         return roost_amd.paged_attention_params(self.q, self.out, self.k, self.v, self.q_indptr, self.kv_indptr,
                                                 self.kv_indices, self.last, **kw)
@@ -350,7 +351,7 @@ def test_rejections(session):
     assert status(head_dim=96) == abi.UNSUPPORTED
     assert status(q_heads=12) == abi.UNSUPPORTED  # a group of 6 (4, 8, 16 and 32 are built)
     assert status(window_left=0) == abi.INVALID_ARGUMENT  # CpuOps refuses a window of 0; -1 means none
-    assert status(soft_cap=30.0) == abi.UNSUPPORTED
+    assert status(soft_cap=float("inf")) == abi.INVALID_ARGUMENT
     p = d.params()
     p.tokens = 3
     assert session.run_raw(entry, p, ws) == abi.INVALID_ARGUMENT
@@ -540,3 +541,39 @@ def test_prefill_plan_without_last_page_len_host(session, name, seqs, ps, hnd, c
     entry = session.lib.entry(roost_amd.ATTENTION_VARIANT)
     session.launch(entry, dv.params(kv_last_page_len_host=None), key=("nolast", name))
     check_against_oracle(dv.result(), b, causal=causal, window_left=window)
+
+
+# ---- Logit soft capping (CpuOps.cs:276; the reference GPU library refuses it, kernels/src/paged_attention.cu:92-94) --
+
+SOFTCAP_CASES = [
+    ("decode bf16 hd256", [(1, 700), (1, 33), (1, 1500)], 16, False, True, 256, True, 5.0),
+    ("decode bf16 hd64 HND ps64", [(1, 300), (1, 901)], 64, True, True, 64, True, 3.0),
+    ("decode bf16 hd128 split", [(1, 6000)], 16, False, True, 128, True, 8.0),
+    ("decode f32 hd64", [(1, 200), (1, 77)], 16, False, True, 64, False, 4.0),
+    ("prefill hd256 split", [(512, 4000), (3, 3)], 16, False, True, 256, True, 5.0),
+    ("prefill hd128 non-causal", [(40, 300)], 16, False, False, 128, True, 2.0),
+    ("prefill ps8 general", [(100, 300)], 8, False, True, 256, True, 5.0),
+    ("mixed step", [(1, 900), (200, 1200), (1, 3000), (64, 64)], 16, False, True, 256, True, 30.0),
+]
+
+
+@pytest.mark.parametrize("name,seqs,ps,hnd,causal,d,bf16,cap", SOFTCAP_CASES, ids=[c[0] for c in SOFTCAP_CASES])
+def test_logit_soft_cap(session, name, seqs, ps, hnd, causal, d, bf16, cap):
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    # std 2 puts the scaled scores at a few units, where a cap of 2-8 bends them; a negative cap caps alike.
+    b = cases.make_paged_batch(rng, [s[1] for s in seqs], [s[0] for s in seqs], page_size=ps, hnd=hnd, d=d,
+                               bf16=bf16, std=2.0)
+    dv = Dev(b, causal, soft_cap=-cap if "HND" in name else cap)
+    entry = session.lib.entry(roost_amd.ATTENTION_VARIANT)
+    session.launch(entry, dv.params(), key=("softcap", name))
+    got = dv.result()
+    ref = cases.values(cases.oracle_attention(b, causal, soft_cap=cap), b.bf16)
+    if bf16:
+        # V is drawn at std 2 as well, so outputs and their bf16 steps are twice the std-1 cases': the absolute
+        # tolerance scales with them.
+        cases.assert_close(got, ref, max_abs=2 * cases.MAX_ABS, what=f"soft cap {name}")
+    else:
+        np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
+    # The cap changes the result (the case exercises it).
+    uncapped = cases.values(cases.oracle_attention(b, causal), b.bf16)
+    assert np.abs(uncapped - ref).max() > 1e-2

@@ -5,6 +5,7 @@ import numpy as np
 import pytest
 
 import cases
+import oracle
 import roost_amd
 from cases import DIM, FUSED, HEADS, ROW
 from roost_amd import abi
@@ -190,7 +191,9 @@ def test_rejections(session):
     p = dev.params()
     p.v.length -= 1
     assert status(rec, p) == abi.INVALID_ARGUMENT
-    assert status(rec, dev.params(k_heads=8, v_heads=8)) == abi.UNSUPPORTED
+    # Value heads must be 1 to 8 whole groups of the key heads.
+    assert status(rec, dev.params(k_heads=3, v_heads=16)) == abi.UNSUPPORTED
+    assert status(rec, dev.params(k_heads=1, v_heads=16)) == abi.UNSUPPORTED
     assert status(rec, dev.params(k_dim=64, v_dim=64)) == abi.UNSUPPORTED
     assert status(rec, dev.params(l2_norm_qk=False)) == abi.UNSUPPORTED
     p = dev.params()
@@ -262,3 +265,50 @@ def test_recurrent_variant_graph_replays():
                            what="graph output")
     finally:
         session.close()
+
+
+# ---- Grouped value heads: v_heads = g * k_heads (CpuOps.Hybrid.cs:31-34, 95: value head h reads key head h / g) ------
+
+GROUP_CASES = [
+    ("8 key / 16 value heads", 8, 16, [300, 1, 77, 40, 1]),
+    ("4 key / 16 value heads", 4, 16, [130, 1, 1, 64]),
+    ("16 key / 32 value heads", 16, 32, [200, 1, 1, 20]),
+    ("2 key / 16 value heads decode", 2, 16, [1, 1, 1, 1, 1]),
+]
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
+@pytest.mark.parametrize("name,kh,vh,lens", GROUP_CASES, ids=[c[0] for c in GROUP_CASES])
+def test_grouped_value_heads(session, variant, name, kh, vh, lens):
+    import torch
+
+    rng = np.random.default_rng(kh * 100 + vh)
+    T, B = int(sum(lens)), len(lens)
+    qk_row, v_row = kh * DIM, vh * DIM
+    width = 2 * qk_row + v_row  # one fused [q | k | v] row per token, read through strided views
+    fused = cases.bf16_bits(rng.standard_normal((T, width), dtype=np.float32))
+    g = (-np.logaddexp(0.0, rng.standard_normal((T, vh)))).astype(np.float32)
+    beta = cases.bf16_bits(1.0 / (1.0 + np.exp(-rng.standard_normal((T, vh)))))
+    slots_n = B + 2
+    pool = (rng.standard_normal((slots_n, vh, DIM, DIM), dtype=np.float32) * 0.05).astype(np.float32)
+    slots = rng.permutation(slots_n)[:B].astype(np.int32)  # distinct: sequences of one call never share a slot
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    want_o = np.zeros((T, vh, DIM), np.uint16)
+    want_pool = pool.copy()
+    q, k, v = (np.ascontiguousarray(fused[:, a:b]) for a, b in
+               ((0, qk_row), (qk_row, 2 * qk_row), (2 * qk_row, width)))
+    oracle.gated_delta_rule(q, k, v, g, beta, want_o, want_pool, slots, cu, batch=B, tokens=T, k_heads=kh, v_heads=vh,
+                            k_dim=DIM, v_dim=DIM, l2_norm_qk=True, bf16=True, beta_bf16=True,
+                            threads=oracle.host_threads())
+    dfused, dpool = to_dev(fused, True), to_dev(pool)
+    out = torch.full((T, vh, DIM), float("nan"), dtype=torch.bfloat16, device="cuda")
+    reach_qk, reach_v = (T - 1) * width + qk_row, (T - 1) * width + v_row
+    p = roost_amd.gated_delta_rule_params(
+        dfused, dfused, dfused, to_dev(g), to_dev(beta, True), out, dpool, to_dev(slots), to_dev(cu), batch=B, tokens=T,
+        k_heads=kh, v_heads=vh, q_stride=width, k_stride=width, v_stride=width, q_len=reach_qk, k_len=reach_qk,
+        v_len=reach_v, q_offset=0, k_offset=qk_row, v_offset=2 * qk_row, cu_seqlens_host=cu)
+    session.launch(session.lib.entry(variant), p, key=("group", kh, vh, T))
+    got_o, got_pool = from_dev(out, True), from_dev(dpool)
+    cases.assert_close(cases.bf16_values(got_o), cases.bf16_values(want_o), what=f"{name} output")
+    for s in slots:
+        cases.assert_close(got_pool[s], want_pool[s], max_abs=1.0, max_rel=cases.STATE_REL, what=f"{name} state {s}")
