@@ -169,11 +169,11 @@ uint32_t HeadShift(const RoostPagedAttentionParams& p) {
   return static_cast<uint32_t>(__builtin_ctz(p.q_heads / (p.kv_heads * kGroup)));
 }
 
-// Shapes with a kernel here, per mode: head dims 64/128/256 decode; prefill on the tile kernel at 128 and 256
-// (128 needs page sizes that are powers of two and multiples of 16), on the general kernel at 256.
+// Shapes with a kernel here, per mode: head dims 64/128/256 decode; prefill on the tile kernel at 64, 128 and 256
+// (64 and 128 need page sizes that are powers of two and multiples of 16), on the general kernel at 256.
 bool PrefillShapeBuilt(const RoostPagedAttentionParams& p) {
   if (p.head_dim == 256) return true;
-  return p.head_dim == 128 && p.page_size % 16 == 0 && roost::IsPow2(p.page_size);
+  return (p.head_dim == 128 || p.head_dim == 64) && p.page_size % 16 == 0 && roost::IsPow2(p.page_size);
 }
 
 // The host batch tables, as workspace() and plan() read them: q_indptr over [0, tokens], both indptrs
@@ -216,8 +216,8 @@ RoostStatus Admit(const RoostPagedAttentionParams& p, bool for_run) {
       .Expect(p.head_dim == 64 || p.head_dim == 128 || p.head_dim == 256, ROOST_STATUS_UNSUPPORTED,
               "head_dim = %u has no kernel here (built: 64, 128, 256)", p.head_dim)
       .Expect(!prefill || PrefillShapeBuilt(p), ROOST_STATUS_UNSUPPORTED,
-              "prefill at head_dim = %u, page_size = %u has no kernel here (built: 256 at any page size; 128 at "
-              "power-of-two page sizes that are multiples of 16)", p.head_dim, p.page_size)
+              "prefill at head_dim = %u, page_size = %u has no kernel here (built: 256 at any page size; 64 and 128 "
+              "at power-of-two page sizes that are multiples of 16)", p.head_dim, p.page_size)
       .Expect(p.kv_heads > 0 && p.q_heads % p.kv_heads == 0 && GroupBuilt(p.q_heads / std::max(p.kv_heads, 1u)),
               ROOST_STATUS_UNSUPPORTED, "q_heads = %u over kv_heads = %u: built for groups of 4, 8, 16 or 32 query "
               "heads per KV head", p.q_heads, p.kv_heads)
@@ -1394,7 +1394,7 @@ __global__ void __launch_bounds__(256, 1)
   }
 }
 
-// ---- Prefill kernel for page sizes that are multiples of 16 (bf16, head_dim 256, MFMA, DMA-fed) ---------------------
+// ---- Prefill kernel for page sizes that are multiples of 16 (bf16, head_dim 64/128/256, MFMA, DMA-fed) --------------
 //
 // One workgroup = 64 query tokens x the 4 query heads of one KV head, 8 wavefronts (two per SIMD, so one wavefront's
 // softmax runs under the other's MFMAs): wavefront w is query head 4 kvh + (w & 3) for tokens 32 (w >> 2) .. +31.
@@ -1469,8 +1469,9 @@ __device__ __forceinline__ uint32_t PackRne(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// Head dims 256 and 128: a row is 2 D bytes = D / 8 16-byte pieces (32 or 16), and every swizzle term below (at most
-// 15 for K, 12 for V) stays inside the row.
+// Head dims 256, 128 and 64: a row is 2 D bytes = D / 8 16-byte pieces (32, 16 or 8). K pieces are swizzled by the
+// row index modulo min(16, D / 8), which keeps every swizzled piece inside its row and any 8 consecutive rows (the
+// lanes one LDS read cycle serves) on distinct 16-byte bank groups; the V offsets (at most 12 pieces) stay inside a row.
 template <int D>
 __global__ void __launch_bounds__(512, 1)
     PrefillTileKernel(const uint16_t* __restrict__ q, uint16_t* __restrict__ out, float* __restrict__ lse, KvView kv,
@@ -1478,7 +1479,7 @@ __global__ void __launch_bounds__(512, 1)
                       const PrefillWork* __restrict__ work, uint16_t* __restrict__ part_o, float* __restrict__ part_ml,
                       uint32_t q_heads, uint32_t causal, uint32_t ps_shift, float scale_log2, int32_t window,
                       SoftCap cap) {
-  static_assert(D == 128 || D == 256, "the tile kernel is built for head dims 128 and 256");
+  static_assert(D == 64 || D == 128 || D == 256, "the tile kernel is built for head dims 64, 128 and 256");
   constexpr int kRowB = 2 * D;                  // bytes of one K or V row in LDS
   constexpr int kPieces = D / 8;                // 16-byte pieces per row
   constexpr int kRowsPerDma = 1024 / kRowB;     // rows one 64-lane global_load_lds_dwordx4 fills
@@ -1486,6 +1487,7 @@ __global__ void __launch_bounds__(512, 1)
   constexpr int kDt = D / 32;                   // 32-dim blocks of O^T
   constexpr int kTileBytes = kPrefillTileK * kRowB;  // one 64-key K or V tile
   constexpr int kNv = kDt / 2;                  // V blocks each wavefront copies per tile (4 kDt blocks / 8)
+  constexpr int kSw = (kPieces < 16 ? kPieces : 16) - 1;  // K swizzle mask
   __shared__ __attribute__((aligned(16))) unsigned char tiles[2][2][kTileBytes];  // [buffer][K, V]
 
   const PrefillWork wk = work[blockIdx.x];
@@ -1559,7 +1561,7 @@ __global__ void __launch_bounds__(512, 1)
       const int rr = kRowsPerDma * i + hh;  // row 8w + rr of the tile
       const uint32_t within = static_cast<uint32_t>(min(pos0 + rr, kend - 1) - page_first);
       const uint32_t off = 2 * row_mul * within;
-      const uint32_t kp = 16 * static_cast<uint32_t>(c ^ ((8 * w + rr) & 15));
+      const uint32_t kp = 16 * static_cast<uint32_t>(c ^ ((8 * w + rr) & kSw));
       Dma16(kpage, off + kp, kdst + i * 1024);
     }
     {  // V blocks (c16, dt0 + i): lane ln fetches key 16 c16 + 8 hi + 4 ((mm >> 4) & 1) + ((mm & 7) >> 1),
@@ -1607,9 +1609,9 @@ __global__ void __launch_bounds__(512, 1)
     for (int g = 0; g < 4; ++g) ids_cur[g] = ids_nxt[g];
     load_ids(min(t + 2, ntiles - 1), ids_nxt);
     const int32_t kb = kbeg + 64 * t;
-    // K operand: row 32 half + lc, piece 2 ks + lh at position (2 ks + lh) ^ (lc & 15) (32 half keeps row & 15 =
-    // lc & 15); in bytes 16 ((2 ks + lh) ^ (lc & 15)) = 32 ks ^ 16 (lh ^ (lc & 15)).
-    const int krow = lc * kRowB, kx = 16 * (lh ^ (lc & 15));
+    // K operand: row 32 half + lc, piece 2 ks + lh at position (2 ks + lh) ^ (lc & kSw) (32 half keeps row & kSw =
+    // lc & kSw); in bytes 16 ((2 ks + lh) ^ (lc & kSw)) = 32 ks ^ 16 (lh ^ (lc & kSw)).
+    const int krow = lc * kRowB, kx = 16 * (lh ^ (lc & kSw));
     // V^T operands, read transposed: in lane group g = ln / 16, lane j = ln % 16 addresses key +(j / 4) at dims
     // +4 (j % 4), keys based at 16 c16 + 4 (g >> 1) (+8 for the operand's second half), dims at 32 dt + 16 (g & 1);
     // block (c16, dt) of the V tile holds exactly those 8 bytes at 8 ln (and the second half's at 512 + 8 ln).
@@ -1883,7 +1885,10 @@ RoostStatus LaunchPrefill(const RoostPagedAttentionParams& p, const PlanRecord& 
     const dim3 grid(static_cast<uint32_t>(rec.work_items));
     const auto* q16 = static_cast<const uint16_t*>(p.q.address);
     const uint32_t ps_shift = static_cast<uint32_t>(__builtin_ctz(p.page_size));
-    if (p.head_dim == 128) {
+    if (p.head_dim == 64) {
+      hipLaunchKernelGGL(PrefillTileKernel<64>, grid, dim3(512), 0, stream, q16, outp, lsep, kv, kv.kv_indices,
+                         q_indptr, items, part_o, part_ml, p.q_heads, p.causal, ps_shift, scale_log2, WindowOf(p), CapOf(p));
+    } else if (p.head_dim == 128) {
       hipLaunchKernelGGL(PrefillTileKernel<128>, grid, dim3(512), 0, stream, q16, outp, lsep, kv, kv.kv_indices,
                          q_indptr, items, part_o, part_ml, p.q_heads, p.causal, ps_shift, scale_log2, WindowOf(p), CapOf(p));
     } else {
@@ -1897,7 +1902,10 @@ RoostStatus LaunchPrefill(const RoostPagedAttentionParams& p, const PlanRecord& 
     const dim3 block(kGroup * p.head_dim / 4);
     if (two > 0) {
       const dim3 g(two, kPfTokens / kPfMergeRows);
-      if (p.head_dim == 128) {
+      if (p.head_dim == 64) {
+        hipLaunchKernelGGL((PrefillMergeKernel<64, kPfMergeRows>), g, block, 0, stream, outp, lsep, mg, part_o, part_ml,
+                           q_indptr, p.q_heads);
+      } else if (p.head_dim == 128) {
         hipLaunchKernelGGL((PrefillMergeKernel<128, kPfMergeRows>), g, block, 0, stream, outp, lsep, mg, part_o, part_ml,
                            q_indptr, p.q_heads);
       } else {
@@ -1907,7 +1915,10 @@ RoostStatus LaunchPrefill(const RoostPagedAttentionParams& p, const PlanRecord& 
     }
     if (rest > 0) {
       const dim3 g(rest, kPfTokens);
-      if (p.head_dim == 128) {
+      if (p.head_dim == 64) {
+        hipLaunchKernelGGL((PrefillMergeKernel<64, 1>), g, block, 0, stream, outp, lsep, mg + two, part_o, part_ml,
+                           q_indptr, p.q_heads);
+      } else if (p.head_dim == 128) {
         hipLaunchKernelGGL((PrefillMergeKernel<128, 1>), g, block, 0, stream, outp, lsep, mg + two, part_o, part_ml,
                            q_indptr, p.q_heads);
       } else {
@@ -2081,11 +2092,14 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_run(RoostContext*, const 
                              : LaunchDecode<float, 256>(p, rec, dev, kv, scale_log2, s);
       }
     }
-    // The multi-token sequences on the tile kernels, then the single-token ones on the decode kernels (bf16, head_dim
-    // 256 in prefill mode). Running the two side by side on two streams gains nothing: a tile workgroup needs two
-    // 256-register wavefronts per SIMD, so it cannot share a CU with resident decode workgroups.
+    // The multi-token sequences on the tile kernels, then the single-token ones on the decode kernels (bf16 in prefill
+    // mode, at the call's head dim). Running the two side by side on two streams gains nothing: a tile workgroup needs
+    // two 256-register wavefronts per SIMD, so it cannot share a CU with resident decode workgroups.
     ROOST_RETURN_IF_FAILED(LaunchPrefill(p, rec, dev, kv, scale_log2, s));
-    return p.head_dim == 128 ? LaunchDecode<uint16_t, 128>(p, rec, dev, kv, scale_log2, s)
-                             : LaunchDecode<uint16_t, 256>(p, rec, dev, kv, scale_log2, s);
+    switch (p.head_dim) {
+      case 64: return LaunchDecode<uint16_t, 64>(p, rec, dev, kv, scale_log2, s);
+      case 128: return LaunchDecode<uint16_t, 128>(p, rec, dev, kv, scale_log2, s);
+      default: return LaunchDecode<uint16_t, 256>(p, rec, dev, kv, scale_log2, s);
+    }
   });
 }

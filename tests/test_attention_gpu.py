@@ -479,6 +479,26 @@ def test_prefill_head_dim_128(session, name, seqs, ps, hnd, causal, window):
     check_against_oracle(got, b, causal=causal, window_left=window)
 
 
+HD64_PREFILL_CASES = [
+    ("hd64 fresh-300", [(300, 300)], 16, False, True, -1, 4),
+    ("hd64 chunk-128-of-1000 HND ps32", [(128, 1000)], 32, True, True, -1, 4),
+    ("hd64 chunk-512-of-4000 split", [(512, 4000), (3, 3)], 16, False, True, -1, 4),
+    ("hd64 mixed step group 8", [(1, 900), (1, 17), (200, 1200), (1, 3000), (64, 64)], 64, False, True, -1, 8),
+    ("hd64 non-causal-32-of-200", [(32, 200)], 16, False, False, -1, 4),
+    ("hd64 window 100", [(700, 700), (40, 900)], 16, False, True, 100, 4),
+]
+
+
+@pytest.mark.parametrize("name,seqs,ps,hnd,causal,window,group", HD64_PREFILL_CASES,
+                         ids=[c[0] for c in HD64_PREFILL_CASES])
+def test_prefill_head_dim_64(session, name, seqs, ps, hnd, causal, window, group):
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    b = cases.make_paged_batch(rng, [s[1] for s in seqs], [s[0] for s in seqs], page_size=ps, hnd=hnd, d=64,
+                               hq=2 * group, hkv=2)
+    got = run_case(session, b, causal=causal, window_left=window)
+    check_against_oracle(got, b, causal=causal, window_left=window)
+
+
 def test_prefill_head_dim_128_needs_a_dma_page_size(session):
     """Head dim 128 prefill is built on the DMA-fed tile kernel only: page sizes that are powers of two and multiples
     of 16. Page size 8 is refused as UNSUPPORTED before any launch."""
