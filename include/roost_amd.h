@@ -123,6 +123,49 @@ typedef struct RoostQkvQkNormRopeCacheWriteParams {
 ROOST_API RoostStatus roost_qkv_qk_norm_rope_cache_write_run(RoostContext* ctx, const void* params,
                                                              const RoostWorkspace* ws, void* stream);
 
+/* The plan region: the batch tables and slot mapping of one worker step, from its sequences. Replaces the worker's
+ * PlanRegionWriter.Fill (reference src/Starlings.Roost.Worker/Eager/PlanRegionWriter.cs:19-64), which the reference runs
+ * in C# on a host mirror of the region before one host-to-device copy. For sequence b (in order):
+ *   q_indptr[b] = cu_seqlens[b] = token_start[b]; kv_indptr[b] = blocks listed before b;
+ *   kv_indices[kv_indptr[b] + i] = its block i; kv_last_page_len[b] = kv_length[b] - (its blocks - 1) * block_size;
+ *   state_slots[b] = recurrent_slot[b];
+ *   for t < token_count[b], at index = token_start[b] + t and position = position_offset[b] + t:
+ *     positions[index] = position; slot_mapping[index] = block[position / block_size] * block_size + position % block_size;
+ * and the [batch] entries of q_indptr and cu_seqlens are the last sequence's token_start + token_count, of kv_indptr
+ * the number of blocks. The region's token ids and sampling rows (embedding and sampler inputs) are not written here.
+ * state_slots / recurrent_slot and positions may be NULL (not written). Entries no sequence writes are left alone. */
+typedef struct RoostAmdPlanRegion {
+  uint32_t batch;                 /* sequences */
+  uint32_t tokens;                /* entries of positions and slot_mapping */
+  uint32_t block_size;            /* tokens per KV page, > 0 */
+  uint32_t reserved0;             /* 0 */
+  const int32_t* token_start;     /* [batch] */
+  const int32_t* token_count;     /* [batch] */
+  const int32_t* position_offset; /* [batch]: position of the sequence's first token of this step */
+  const int32_t* kv_length;       /* [batch]: keys after this step */
+  const int32_t* block_indptr;    /* [batch + 1], from 0: sequence b's blocks are blocks[block_indptr[b] ..) */
+  const int32_t* blocks;          /* [block_indptr[batch]] */
+  const int32_t* recurrent_slot;  /* [batch] or NULL */
+  int32_t* q_indptr;              /* [batch + 1] */
+  int32_t* cu_seqlens;            /* [batch + 1] */
+  int32_t* kv_indptr;             /* [batch + 1] */
+  int32_t* kv_indices;            /* [block_indptr[batch]] */
+  int32_t* kv_last_page_len;      /* [batch] */
+  int32_t* state_slots;           /* [batch] or NULL */
+  int32_t* positions;             /* [tokens] or NULL */
+  int64_t* slot_mapping;          /* [tokens] */
+} RoostAmdPlanRegion;
+
+/* Host memory: fills the tables on the calling thread. A sequence whose tokens fall outside [0, tokens), whose
+ * positions reach past its blocks, or whose block_indptr goes backwards is refused with ROOST_STATUS_INVALID_ARGUMENT
+ * (the reference's Fill throws on the same plans) and nothing is written. */
+ROOST_API RoostStatus roost_amd_plan_region_fill(const RoostAmdPlanRegion* region);
+
+/* Device memory: one launch on `stream` writes the same tables on the GPU from the device copies of the sequences'
+ * fields, so a step's per-token work never crosses PCIe. The device arrays are not validated on the host: a token
+ * index outside [0, tokens) is skipped and a position past its sequence's blocks gets slot -1 (CacheWrite skips it). */
+ROOST_API RoostStatus roost_amd_plan_region_run(RoostContext* ctx, const RoostAmdPlanRegion* region, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -97,6 +97,10 @@ class KernelLibrary:
         self.dll.roost_context_create.restype = C.c_int32
         self.dll.roost_context_destroy.argtypes = [C.c_void_p]
         self.dll.roost_context_destroy.restype = C.c_int32
+        self.dll.roost_amd_plan_region_fill.argtypes = [C.POINTER(abi.PlanRegion)]
+        self.dll.roost_amd_plan_region_fill.restype = C.c_int32
+        self.dll.roost_amd_plan_region_run.argtypes = [C.c_void_p, C.POINTER(abi.PlanRegion), C.c_void_p]
+        self.dll.roost_amd_plan_region_run.restype = C.c_int32
         version = self.dll.roost_abi_version()
         if version >> 16 != abi.ABI_MAJOR or (version & 0xFFFF) < abi.ABI_MINOR:
             raise RuntimeError(f"{path}: ABI {version >> 16}.{version & 0xFFFF} is not {abi.ABI_MAJOR}.{abi.ABI_MINOR}")
@@ -474,3 +478,46 @@ def recurrent_state_copy(session: OpSession, *args, **kwargs) -> None:
 
 def recurrent_state_snapshot(session: OpSession, *args, **kwargs) -> None:
     session.launch(session.lib.entry(STATE_SNAPSHOT_VARIANT), recurrent_state_snapshot_params(*args, **kwargs))
+
+
+# ---- plan region (PlanRegionWriter.Fill) ------------------------------------------------------------------------------
+
+PLAN_REGION_INPUTS = ("token_start", "token_count", "position_offset", "kv_length", "block_indptr", "blocks",
+                      "recurrent_slot")
+PLAN_REGION_OUTPUTS = ("q_indptr", "cu_seqlens", "kv_indptr", "kv_indices", "kv_last_page_len", "state_slots",
+                       "positions", "slot_mapping")
+
+
+def _address(a) -> Optional[int]:
+    if a is None:
+        return None
+    if hasattr(a, "data_ptr"):
+        return a.data_ptr()
+    return a.ctypes.data
+
+
+def plan_region_struct(*, batch: int, tokens: int, block_size: int, **arrays) -> abi.PlanRegion:
+    """RoostAmdPlanRegion over numpy arrays (host) or torch tensors (device); absent names are NULL."""
+    r = abi.PlanRegion()
+    r.batch, r.tokens, r.block_size = batch, tokens, block_size
+    for name, a in arrays.items():
+        if name not in PLAN_REGION_INPUTS + PLAN_REGION_OUTPUTS:
+            raise TypeError(f"unknown plan region array {name}")
+        setattr(r, name, _address(a))
+    return r
+
+
+def plan_region_fill(lib: KernelLibrary, **kwargs) -> None:
+    """roost_amd_plan_region_fill on host arrays; raises KernelError on a refused plan."""
+    r = plan_region_struct(**kwargs)
+    status = lib.dll.roost_amd_plan_region_fill(C.byref(r))
+    if status != abi.OK:
+        raise KernelError("plan_region_fill", status, lib.last_error())
+
+
+def plan_region_run(session: OpSession, **kwargs) -> None:
+    """roost_amd_plan_region_run on device tensors, on the session's stream."""
+    r = plan_region_struct(**kwargs)
+    status = session.lib.dll.roost_amd_plan_region_run(session.ctx, C.byref(r), C.c_void_p(session.stream_handle))
+    if status != abi.OK:
+        raise KernelError("plan_region_run", status, session.lib.last_error())

@@ -171,6 +171,14 @@ class RecurrentStateSnapshotParams(C.Structure):
                 ("pairs", DeviceSpan), ("slot_bytes", C.c_uint64), ("count", C.c_uint32), ("restore", C.c_uint32)]
 
 
+class PlanRegion(C.Structure):
+    """RoostAmdPlanRegion: plain pointers (host memory for roost_amd_plan_region_fill, device memory for _run)."""
+    _fields_ = [("batch", C.c_uint32), ("tokens", C.c_uint32), ("block_size", C.c_uint32), ("reserved0", C.c_uint32)] + [
+        (name, C.c_void_p) for name in ("token_start", "token_count", "position_offset", "kv_length", "block_indptr",
+                                        "blocks", "recurrent_slot", "q_indptr", "cu_seqlens", "kv_indptr", "kv_indices",
+                                        "kv_last_page_len", "state_slots", "positions", "slot_mapping")]
+
+
 ALL_STRUCTS = {
     "RoostDeviceSpan": DeviceSpan, "RoostWorkspaceSizes": WorkspaceSizes, "RoostWorkspace": Workspace,
     "RoostConstraints": Constraints, "RoostContextCreateParams": ContextCreateParams, "RoostOpEntry": OpEntry,

@@ -19,7 +19,7 @@ CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 LIB_NAME = "libroost_kernels_gfx950.so"
 LIB_PATH = HERE / LIB_NAME
-SOURCES = ["registry.cpp", "cache_write.hip", "paged_attention.hip", "gated_delta_rule.hip", "gdn_layer.hip", "qk_rope.hip"]
+SOURCES = ["registry.cpp", "cache_write.hip", "paged_attention.hip", "gated_delta_rule.hip", "gdn_layer.hip", "qk_rope.hip", "plan_region.hip"]
 
 # Packed-FP32 instructions are kept out of every HIP object (the compiler would otherwise form v_pk_* from scalar
 # float code); the host pass of hipcc warns that it does not know the feature, which is harmless.

@@ -354,6 +354,16 @@ def test_plan_region_slot_mapping_closed_form():
     assert list(slots) == want
 
 
+
+def test_plan_region_reference_hand_case():
+    """PlanAndResultTests.cs:25-45: a 3-token prefill on block 5 and a 1-token decode at position 17 on blocks [2, 7]."""
+    seqs = [dict(token_start=0, token_count=3, position_offset=0, kv_length=3, blocks=[5]),
+            dict(token_start=3, token_count=1, position_offset=17, kv_length=18, blocks=[2, 7])]
+    q_indptr, cu, kv_indptr, kv_indices, last, slots = oracle.plan_region(seqs, 16)
+    assert list(slots) == [80, 81, 82, 7 * 16 + 1]
+    assert list(q_indptr) == [0, 3, 4] and list(cu) == [0, 3, 4]
+    assert list(kv_indptr) == [0, 1, 3] and list(kv_indices) == [5, 2, 7] and list(last) == [3, 2]
+
 # ---- Gated DeltaNet layer neighbours --------------------------------------------------------------------------------
 # Pinned by the reference's hand cases (tests/Starlings.Roost.Ops.Tests/GatingOpsTests.cs, HybridTests.cs:249-385) and by
 # transformers 5.20.1's own float32 tensors, which the reference's tests hold as a fixture
