@@ -326,8 +326,10 @@ def bench_mixed(torch, roost_amd, session, steps, warmup):
     session.stream.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(session.stream)
+    t_issue = time.perf_counter()
     for _ in range(steps):
         step()
+    issue_ms = (time.perf_counter() - t_issue) * 1e3 / steps
     end.record(session.stream)
     end.synchronize()
     step_ms = start.elapsed_time(end) / steps
@@ -344,7 +346,8 @@ def bench_mixed(torch, roost_amd, session, steps, warmup):
     floor_ms = (kv_bytes + gdn_bytes) / (HBM_PEAK_GBS * 1e6)
     return {"workload": "BASELINE config 5: 48 decode ctx U(1024, 16384) + 2 x 512-token chunks on 4096 prefixes; "
                         "CacheWrite + PagedAttention + 3 GDN layers (recurrent variant)",
-            "step_ms": step_ms, "cold_step_ms": cold_ms, "breakdown_ms": parts, "attention_plan_ms": plan_ms,
+            "step_ms": step_ms, "cold_step_ms": cold_ms, "host_issue_ms": issue_ms, "breakdown_ms": parts,
+            "attention_plan_ms": plan_ms,
             "hbm_floor_ms": floor_ms, "hbm_frac": floor_ms / step_ms, "context_tokens": int(kv.sum()),
             "tokens": T}
 

@@ -414,9 +414,10 @@ __device__ __forceinline__ float F4(const float4& v, int i) {
 //
 // WyPrepKernel (one workgroup per chunk and head, all in parallel) turns a chunk's raw rows into one 20 KB record of
 // ready-made MFMA operands: T = (I + A)^-1 split into bf16 hi and lo parts, P, and the per-token factors. WyScanKernel
-// (one workgroup of two wavefronts per sequence, head and 32-column value block) walks the chunks in order with the
-// state in registers: per chunk it copies the record and the raw k, q and v rows into LDS (global_load_lds, one chunk
-// ahead), and each wavefront advances its 16 state columns with no exchange between wavefronts.
+// (one workgroup per sequence, head and 32-column value block: two compute and two copier wavefronts) walks the chunks
+// in order with the state in registers: per chunk the copiers bring the record and the raw k, q and v rows into LDS
+// (global_load_lds, one chunk ahead), and each compute wavefront advances its 16 state columns with no exchange between
+// wavefronts.
 //
 // Operand layouts (v_mfma_f32_16x16x32_bf16: A lane l = row l%16, k-slots 8(l/16)..+7; B lane l = column l%16, same
 // k-slots; C lane l = column l%16, rows 4(l/16)+i). A product's C tiles feed the next product's B operand without any
@@ -666,7 +667,7 @@ struct Stage {
   uint8_t ob[64 * 64];  // the chunk's outputs [64 tokens][32 columns] bf16, written by the compute wavefronts
 };
 
-// Starts the copies of chunk (t0, n)'s record and rows into `st`; wave 0 copies the record and v, wave 1 k and q.
+// Starts the copies of chunk (t0, n)'s record and rows into `st`; copier 0 copies the record and v, copier 1 k and q.
 // Rows past the chunk's end repeat its last row (their factors are zero).
 // global -> LDS copy with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane byte offset: lane l's 16 bytes land
 // at lds + 16 l. M0 carries the LDS address and is restored.
@@ -1154,10 +1155,20 @@ RoostStatus LaunchChunk(const RoostGatedDeltaRuleParams& p, const RoostWorkspace
 
 // The recurrent variant's routed path over a device region laid out as `l`: RouteKernel writes the chunk tables of the
 // sequences of kRouteMinTokens or more tokens from the device cu_seqlens, the chunk kernels run those sequences and the
-// recurrent kernel the rest, in that order on one stream. (Two streams were slower: the short kernels lose more to
-// sharing the chip than the overlap saves.) Two sequences of one call sharing a state slot leave the recurrent one's
-// state.
-RoostStatus LaunchRouted(const RoostGatedDeltaRuleParams& p, uint8_t* base, const ChunkArena& l, hipStream_t s) {
+// recurrent kernel the rest. The recurrent kernel is forked onto the context's side stream (after everything the
+// caller queued before this call) and joined back before the call returns, so it runs beside the chunk kernels: their
+// chains leave most of the chip idle (one workgroup per chain and value block) and a recurrent workgroup (237 VGPRs,
+// no LDS) fits beside a scan workgroup on one CU. Without a side stream the three run in order on the caller's
+// stream. Sequences of one call must use distinct state slots: two that share one race (they may run at the same time
+// on either path), as they do in the reference's gather / scatter of the slots.
+RoostStatus LaunchRouted(const RoostContext& ctx, const RoostGatedDeltaRuleParams& p, uint8_t* base, const ChunkArena& l,
+                         hipStream_t s) {
+  const bool fork = ctx.side != nullptr;
+  if (fork) {
+    ROOST_RETURN_IF_FAILED(roost::HipStatus(hipEventRecord(ctx.fork, s), kOp, "fork event"));
+    ROOST_RETURN_IF_FAILED(roost::HipStatus(hipStreamWaitEvent(ctx.side, ctx.fork, 0), kOp, "fork wait"));
+    ROOST_RETURN_IF_FAILED(LaunchRecurrent(p, ctx.side, static_cast<int32_t>(kRouteMinTokens)));
+  }
   hipLaunchKernelGGL(RouteKernel, dim3(1), dim3(1024), 0, s, static_cast<const int32_t*>(p.cu_seqlens.address),
                      p.batch, l.max_chunks, reinterpret_cast<int4*>(base + l.chunk_table),
                      reinterpret_cast<int4*>(base + l.seq_table), reinterpret_cast<int32_t*>(base + l.seq_list),
@@ -1167,7 +1178,9 @@ RoostStatus LaunchRouted(const RoostGatedDeltaRuleParams& p, uint8_t* base, cons
   ws.device = base;
   ws.device_bytes = l.total;
   ROOST_RETURN_IF_FAILED(LaunchChunk(p, &ws, l, l.max_chunks, s));
-  return LaunchRecurrent(p, s, static_cast<int32_t>(kRouteMinTokens));
+  if (!fork) return LaunchRecurrent(p, s, static_cast<int32_t>(kRouteMinTokens));
+  ROOST_RETURN_IF_FAILED(roost::HipStatus(hipEventRecord(ctx.join, ctx.side), kOp, "join event"));
+  return roost::HipStatus(hipStreamWaitEvent(s, ctx.join, 0), kOp, "join wait");
 }
 
 }  // namespace
@@ -1212,7 +1225,7 @@ extern "C" ROOST_API RoostStatus roost_gdn_recurrent_run(RoostContext* ctx, cons
                 "%u tokens may route sequences to the chunk kernels, which need %llu device workspace bytes",
                 p.tokens, static_cast<unsigned long long>(l.total));
     ROOST_GATE_RETURN(gate);
-    return LaunchRouted(p, static_cast<uint8_t*>(ws->device), l, s);
+    return LaunchRouted(*ctx, p, static_cast<uint8_t*>(ws->device), l, s);
   });
 }
 
@@ -1374,7 +1387,7 @@ extern "C" ROOST_API RoostStatus roost_amd_gdn_recurrent_run_noalloc(RoostContex
     ROOST_GATE_RETURN(gate);
     uint8_t* base = nullptr;
     ROOST_RETURN_IF_FAILED(ScratchFor(current, &base));
-    return LaunchRouted(p, base, l, s);
+    return LaunchRouted(*ctx, p, base, l, s);
   });
 }
 
