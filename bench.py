@@ -83,7 +83,9 @@ class Paged:
 
 
 def time_runs(torch, session, entry, params, ws, steps, warmup):
-    """Average run() duration in ms over `steps` launches, measured with events on the session's stream."""
+    """Average run() duration in ms over `steps` launches, measured with events on the session's stream, after
+    settling the GPU on the same call."""
+    settle(session, lambda: session.run(entry, params, ws))
     for _ in range(warmup):
         session.run(entry, params, ws)
     session.stream.synchronize()
@@ -127,8 +129,19 @@ def time_cold(torch, session, flush, fn, reps):
     return float(np.median(times))
 
 
+def settle(session, fn, seconds=0.3):
+    """Runs `fn` back to back for `seconds` so that clocks and caches reach their steady state before a timing."""
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            fn()
+        session.stream.synchronize()
+
+
 def time_each(torch, session, fn, reps, warmup=2):
-    """Median duration in ms of `fn` launched back to back (warm caches), each launch between its own events."""
+    """Median duration in ms of `fn` launched back to back (warm caches), each launch between its own events, after
+    settling the GPU on it."""
+    settle(session, fn)
     for _ in range(warmup):
         fn()
     session.stream.synchronize()
@@ -321,6 +334,7 @@ def bench_mixed(torch, roost_amd, session, steps, warmup):
         for layer in range(3):
             session.run(e_gdn, gdn[layer], ws_gdn[layer])
 
+    settle(session, step)
     for _ in range(warmup):
         step()
     session.stream.synchronize()
