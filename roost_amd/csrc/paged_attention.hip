@@ -32,6 +32,8 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <functional>
+#include <queue>
 #include <type_traits>
 #include <vector>
 
@@ -432,6 +434,70 @@ bool PrefillFastPath(const RoostPagedAttentionParams& p) {
   return p.page_size % 16 == 0 && (p.page_size & (p.page_size - 1)) == 0;
 }
 
+// Tiles of a work item (its key range in 64-key tiles), and of the pieces it is cut into with at most `target` each.
+int64_t ItemTiles(const PrefillWork& w) { return roost::CeilDiv(static_cast<int64_t>(w.kend - w.kbeg), 64); }
+int64_t Pieces(int64_t tiles, int64_t target) { return std::min<int64_t>(roost::CeilDiv(tiles, target), kMaxMergeSplits); }
+
+// The longest-first dispatch of the items cut at `target` onto `cus` workgroup slots, each piece costing its tiles
+// plus kPfPieceCost (its set-up and epilogue): the finishing time of the last slot, in tiles.
+constexpr int64_t kPfPieceCost = 2;
+template <typename Items>
+int64_t PrefillMakespan(const Items& items, int64_t target, uint32_t cus) {
+  std::vector<int64_t> cost;
+  for (const auto& it : items) {
+    const int64_t tiles = ItemTiles(it.w), n = Pieces(tiles, target);
+    for (int64_t i = 0; i < n; ++i) cost.push_back(tiles * (i + 1) / n - tiles * i / n + kPfPieceCost);
+  }
+  std::sort(cost.begin(), cost.end(), std::greater<int64_t>());
+  std::priority_queue<int64_t, std::vector<int64_t>, std::greater<int64_t>> slots;
+  for (uint32_t c = 0; c < cus; ++c) slots.push(0);
+  int64_t end = 0;
+  for (const int64_t c : cost) {
+    const int64_t t = slots.top() + c;
+    slots.pop();
+    slots.push(t);
+    end = std::max(end, t);
+  }
+  return end;
+}
+
+// The piece size (in tiles, at least kPfMinSplitTiles) the 64-token kernel cuts key ranges at. Candidates: 3/4 of the
+// average CU load (config 3: 0.213 ms against 0.219 with the whole average and 0.242 with half), and the smallest
+// sizes whose pieces fill the CUs exactly once or twice (config 5's two 512-token chunks: 256 pieces of 9 tiles
+// instead of 288 of 8, whose last 32 ran in a second round); the one whose longest-first dispatch ends first wins.
+template <typename Items>
+int64_t PrefillPieceTiles(const Items& items, int64_t total_tiles, uint32_t cus) {
+  const uint32_t slots = std::max<uint32_t>(cus, 1);
+  std::vector<int64_t> cand{std::max<int64_t>(kPfMinSplitTiles, roost::CeilDiv(total_tiles * 3, 4 * int64_t{slots}))};
+  int64_t longest = 0;
+  for (const auto& it : items) longest = std::max(longest, ItemTiles(it.w));
+  for (int64_t rounds = 1; rounds <= 2; ++rounds) {
+    if (static_cast<int64_t>(items.size()) > rounds * slots) break;
+    // Smallest target whose pieces number at most rounds x slots (the count only falls as the target grows).
+    int64_t lo = kPfMinSplitTiles, hi = std::max<int64_t>(longest, kPfMinSplitTiles);
+    auto count = [&](int64_t t) {
+      int64_t n = 0;
+      for (const auto& it : items) n += Pieces(ItemTiles(it.w), t);
+      return n;
+    };
+    if (count(hi) > rounds * slots) continue;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) / 2;
+      if (count(mid) <= rounds * slots) hi = mid; else lo = mid + 1;
+    }
+    cand.push_back(lo);
+  }
+  int64_t best = cand[0], best_end = PrefillMakespan(items, cand[0], slots);
+  for (size_t i = 1; i < cand.size(); ++i) {
+    const int64_t end = PrefillMakespan(items, cand[i], slots);
+    if (end < best_end || (end == best_end && cand[i] > best)) {
+      best = cand[i];
+      best_end = end;
+    }
+  }
+  return best;
+}
+
 Layout PlanPrefill(const RoostPagedAttentionParams& p, uint32_t cus, unsigned char* host) {
   const bool fast = PrefillFastPath(p);
   const int64_t tile_q = fast ? kPfTokens : kPrefillTileQ;
@@ -470,10 +536,7 @@ Layout PlanPrefill(const RoostPagedAttentionParams& p, uint32_t cus, unsigned ch
   std::vector<PrefillMerge> merges;
   int32_t slot = 0;
   if (fast) {
-    // Pieces of at most 3/4 of the average CU load: the longest-first dispatch then ends closer to the average
-    // (config 3: 0.213 against 0.219 ms with the whole average; half of it took 0.242 ms, the merges costing more).
-    const int64_t target =
-        std::max<int64_t>(kPfMinSplitTiles, roost::CeilDiv(total_tiles * 3, 4 * std::max<uint32_t>(cus, 1)));
+    const int64_t target = PrefillPieceTiles(items, total_tiles, cus);
     std::vector<Item> cut;
     cut.reserve(items.size());
     for (const Item& it : items) {
