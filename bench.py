@@ -129,8 +129,13 @@ def time_cold(torch, session, flush, fn, reps):
     return float(np.median(times))
 
 
-def settle(session, fn, seconds=0.3):
-    """Runs `fn` back to back for `seconds` so that clocks and caches reach their steady state before a timing."""
+SETTLE_S = 0.3  # --settle
+
+
+def settle(session, fn, seconds=None):
+    """Runs `fn` back to back for `seconds` (default --settle) so that clocks and caches reach their steady state before
+    a timing."""
+    seconds = SETTLE_S if seconds is None else seconds
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < seconds:
         for _ in range(8):
@@ -615,9 +620,13 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--settle", type=float, default=0.3,
+                    help="seconds each timed call is run back to back before its timing (0 for profiler passes)")
     ap.add_argument("--only", choices=["decode", "prefill", "prefill128", "dense", "gdn", "mixed", "layer", "attn_in"], default=None,
                     help="run one workload only and print its timing (for profiler passes); no JSON line")
     args = ap.parse_args()
+    global SETTLE_S
+    SETTLE_S = args.settle
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU only: this build runs the attention + GDN path on a single MI355X "
