@@ -359,6 +359,11 @@ __device__ __forceinline__ void Split2(float x0, float x1, uint32_t& hi, uint32_
   lo = PackRne(x0 - __uint_as_float(u0), x1 - __uint_as_float(u1));
 }
 
+constexpr float kLog2e = 1.4426950408889634f;
+// 2^x on the hardware's v_exp_f32 (about 1 ulp; results below 2^-126 flush to zero, which only ever multiplies
+// factors that are already negligible).
+__device__ __forceinline__ float Exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 template <bool kVec>
 __device__ __forceinline__ uint4 Load8(const uint16_t* p) {
   if constexpr (kVec) {
@@ -463,7 +468,7 @@ __device__ __forceinline__ u32x2_t TrRead(const uint8_t* p) {
 // applied afterwards in fp32), T by blocked substitution in fp32 (16 x 16 diagonal blocks by forward substitution, the
 // blocks below on v_mfma_f32_16x16x4f32).
 template <bool kVec>
-__global__ void __launch_bounds__(256, 4) WyPrepKernel(ChunkArgs ca) {
+__global__ void __launch_bounds__(256, 6) WyPrepKernel(ChunkArgs ca) {
   using namespace wy;
   const GdnArgs& a = ca.a;
   const int4 ch = ca.chunks[blockIdx.x];
@@ -476,25 +481,42 @@ __global__ void __launch_bounds__(256, 4) WyPrepKernel(ChunkArgs ca) {
   const uint32_t kh = h / a.group;
   uint8_t* rec = ca.recs + (static_cast<uint64_t>(blockIdx.x) * a.vh + h) * kRecBytes;
 
-  // region0 holds the raw q (tile 0) and k (tile 1) rows; once the products are formed it holds A and T (fp32).
-  __shared__ __align__(16) uint8_t region0[2 * 64 * kTilePitch * 2];
+  // region0 holds the raw k rows (a [64][kTilePitch] bf16 tile; each wavefront keeps its own 16 q rows in registers).
+  // Once the products are formed it holds A and T (fp32) as their 10 lower-triangular 16 x 16 blocks each, and one
+  // 16 x 16 block of partial sums per wavefront: 24 KB in all, so that 6 workgroups share a CU.
+  constexpr int kBlk = 256;  // floats per 16 x 16 block
+  __shared__ __align__(16) uint8_t region0[(2 * 10 + 4) * kBlk * 4];
+  static_assert(sizeof(region0) >= 64 * kTilePitch * 2, "the k tile fits the region");
   __shared__ float g_lds[64], rk_lds[64], rq_lds[64], b_lds[64];
-  auto qk = reinterpret_cast<uint16_t(*)[64][kTilePitch]>(region0);
-  auto a_lds = reinterpret_cast<float(*)[65]>(region0);
-  auto t_lds = reinterpret_cast<float(*)[65]>(region0 + 64 * 65 * 4);
+  auto kt = reinterpret_cast<uint16_t(*)[kTilePitch]>(region0);
+  float* const a_mem = reinterpret_cast<float*>(region0);
+  float* const t_mem = a_mem + 10 * kBlk;
+  float* const p_mem = t_mem + 10 * kBlk;
+  // Element (r, c) of a block sits at 16 (r % 16) + ((c % 16) ^ 4 ((r % 16) / 4)): the MFMA operand reads (16 rows x 4
+  // columns, or 4 rows x 16 columns, per instruction) fall on 64 distinct banks, and column pairs (2c, 2c + 1) stay
+  // adjacent. Block (bi, bj), bj <= bi, is block bi (bi + 1) / 2 + bj of its matrix.
+  auto in_blk = [](int r, int c) { return (r & 15) * 16 + ((c & 15) ^ (4 * ((r & 15) >> 2))); };
+  auto tri = [](int r, int c) { return ((r >> 4) * ((r >> 4) + 1) / 2 + (c >> 4)) * kBlk; };
+  auto a_lds = [=](int r, int c) -> float& { return a_mem[tri(r, c) + in_blk(r, c)]; };
+  auto t_lds = [=](int r, int c) -> float& { return t_mem[tri(r, c) + in_blk(r, c)]; };
+  auto p_lds = [=](int r, int c) -> float& { return p_mem[w * kBlk + in_blk(r, c)]; };  // this wavefront's block
 
-  {  // Raw rows into LDS (zero past the chunk's end) and their sums of squares. Every load is issued unconditionally
-     // from a clamped row and masked afterwards, so that all of them are in flight together.
+  // Q operands of this wavefront's token tile: bq[s] = q[16w + r16][32s + 8kq .. +8], zero past the chunk's end.
+  uint4 bq[4];
+  {  // Raw k rows into LDS, q rows into registers (zero past the chunk's end), and their sums of squares. Every load
+     // is issued unconditionally from a clamped row and masked afterwards, so that all of them are in flight together.
     const int row = tid >> 2, part = tid & 3;
     const uint32_t keep = row < n ? ~0u : 0u;
     const uint64_t tok = static_cast<uint64_t>(t0 + min(row, n - 1));
     const uint16_t* kp = a.k + tok * a.k_stride + kh * kDim + part * 32;
-    const uint16_t* qp = a.q + tok * a.q_stride + kh * kDim + part * 32;
-    uint4 kv[4], qv[4];
+    const int qrow = 16 * w + r16;
+    const uint32_t qkeep = qrow < n ? ~0u : 0u;
+    const uint16_t* qp = a.q + static_cast<uint64_t>(t0 + min(qrow, n - 1)) * a.q_stride + kh * kDim + 8 * kq;
+    uint4 kv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       kv[i] = Load8<kVec>(kp + 8 * i);
-      qv[i] = Load8<kVec>(qp + 8 * i);
+      bq[i] = Load8<kVec>(qp + 32 * i);
     }
     const uint64_t gi = static_cast<uint64_t>(t0 + min(lane, n - 1)) * a.vh + h;
     const float graw = a.g[gi];
@@ -503,18 +525,16 @@ __global__ void __launch_bounds__(256, 4) WyPrepKernel(ChunkArgs ca) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       kv[i] = make_uint4(kv[i].x & keep, kv[i].y & keep, kv[i].z & keep, kv[i].w & keep);
-      qv[i] = make_uint4(qv[i].x & keep, qv[i].y & keep, qv[i].z & keep, qv[i].w & keep);
+      bq[i] = make_uint4(bq[i].x & qkeep, bq[i].y & qkeep, bq[i].z & qkeep, bq[i].w & qkeep);
       kk += SumSq8(kv[i]);
-      qq += SumSq8(qv[i]);
-      *reinterpret_cast<uint4*>(&qk[1][row][part * 32 + 8 * i]) = kv[i];
-      *reinterpret_cast<uint4*>(&qk[0][row][part * 32 + 8 * i]) = qv[i];
+      qq += SumSq8(bq[i]);
+      *reinterpret_cast<uint4*>(&kt[row][part * 32 + 8 * i]) = kv[i];
     }
     kk = QuadSum(kk);
-    qq = QuadSum(qq);
-    if (part == 0) {
-      rk_lds[row] = 1.0f / sqrtf(kk + 1e-6f);
-      rq_lds[row] = a.scale / sqrtf(qq + 1e-6f);
-    }
+    qq += __shfl_xor(qq, 16, 64);  // the 4 lanes r16 + 16kq hold disjoint quarters of q row 16w + r16
+    qq += __shfl_xor(qq, 32, 64);
+    if (part == 0) rk_lds[row] = 1.0f / sqrtf(kk + 1e-6f);
+    if (kq == 0) rq_lds[qrow] = a.scale / sqrtf(qq + 1e-6f);
     if (w == 0) {  // cumulative log-decay (zero increments past the end) and beta
       float gv = lane < n ? graw : 0.0f;
 #pragma unroll
@@ -522,7 +542,7 @@ __global__ void __launch_bounds__(256, 4) WyPrepKernel(ChunkArgs ca) {
         const float y = __shfl_up(gv, d, 64);
         if (lane >= d) gv += y;
       }
-      g_lds[lane] = gv;
+      g_lds[lane] = gv * kLog2e;  // cumulative log-decay in log2 units: every factor below is one exp2
       b_lds[lane] = lane < n ? Bf16ToF32(braw) : 0.0f;
     }
   }
@@ -533,12 +553,9 @@ __global__ void __launch_bounds__(256, 4) WyPrepKernel(ChunkArgs ca) {
   // the B operand in the same lane layout, so the k rows of tile c serve as both.
   f32x4_t kk4[4], pt4[4];
   {
-    uint4 ak[4], bq[4];
+    uint4 ak[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      ak[s] = *reinterpret_cast<const uint4*>(&qk[1][16 * w + r16][32 * s + 8 * kq]);
-      bq[s] = *reinterpret_cast<const uint4*>(&qk[0][16 * w + r16][32 * s + 8 * kq]);
-    }
+    for (int s = 0; s < 4; ++s) ak[s] = *reinterpret_cast<const uint4*>(&kt[16 * w + r16][32 * s + 8 * kq]);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       kk4[c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -546,14 +563,14 @@ __global__ void __launch_bounds__(256, 4) WyPrepKernel(ChunkArgs ca) {
       if (c <= w) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          const uint4 kc = *reinterpret_cast<const uint4*>(&qk[1][16 * c + r16][32 * s + 8 * kq]);
+          const uint4 kc = *reinterpret_cast<const uint4*>(&kt[16 * c + r16][32 * s + 8 * kq]);
           kk4[c] = Mfma(ak[s], kc, kk4[c]);
           pt4[c] = Mfma(kc, bq[s], pt4[c]);
         }
       }
     }
   }
-  __syncthreads();  // the q/k tiles are dead: region0 becomes A and T
+  __syncthreads();  // the k tile is dead: region0 becomes A and T
 
   // P operands of wave w's token tile: lane (kq, r16) holds P[t = 16w + r16][j = 16c + 4kq + i] in pt4[c], which is
   // exactly its share of the operand of pair (w, s') for c = 2s' (slots 8kq..8kq+3) and c = 2s' + 1 (slots +4..+7).
@@ -565,7 +582,7 @@ __global__ void __launch_bounds__(256, 4) WyPrepKernel(ChunkArgs ca) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int j = 16 * c + 4 * kq + i;
-        pv[c][i] = (c <= w && j <= t) ? pt4[c][i] * rq_lds[t] * rk_lds[j] * expf(g_lds[t] - g_lds[j]) : 0.0f;
+        pv[c][i] = (c <= w && j <= t) ? pt4[c][i] * rq_lds[t] * rk_lds[j] * Exp2(g_lds[t] - g_lds[j]) : 0.0f;
       }
 #pragma unroll
     for (int sp = 0; sp < 2; ++sp) {
@@ -579,14 +596,14 @@ __global__ void __launch_bounds__(256, 4) WyPrepKernel(ChunkArgs ca) {
   }
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
+    if (c > w) continue;  // blocks above the diagonal are not stored
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      // A[r][j], r = 16w + 4kq + i, j = 16c + r16 (strictly lower); zero above the diagonal of A and T
+      // A[r][j], r = 16w + 4kq + i, j = 16c + r16 (strictly lower; zero above the diagonal of the diagonal block)
       const int r = 16 * w + 4 * kq + i, j = 16 * c + r16;
       float av = 0.0f;
-      if (j < r) av = b_lds[r] * expf(g_lds[r] - g_lds[j]) * kk4[c][i] * rk_lds[r] * rk_lds[j];
-      a_lds[r][j] = av;
-      if (c > w) t_lds[r][j] = 0.0f;
+      if (j < r) av = b_lds[r] * Exp2(g_lds[r] - g_lds[j]) * kk4[c][i] * rk_lds[r] * rk_lds[j];
+      a_lds(r, j) = av;
     }
   }
   __syncthreads();
@@ -598,15 +615,15 @@ __global__ void __launch_bounds__(256, 4) WyPrepKernel(ChunkArgs ca) {
     for (int i = 0; i < 16; ++i) {
       float acc = i == lane ? 1.0f : 0.0f;
 #pragma unroll
-      for (int j = 0; j < i; ++j) acc = fmaf(-a_lds[16 * w + i][16 * w + j], x[j], acc);
+      for (int j = 0; j < i; ++j) acc = fmaf(-a_lds(16 * w + i, 16 * w + j), x[j], acc);
       x[i] = acc;
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) t_lds[16 * w + i][16 * w + lane] = x[i];
+    for (int i = 0; i < 16; ++i) t_lds(16 * w + i, 16 * w + lane) = x[i];
   }
   __syncthreads();
   // ... then the blocks below it, T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj, in order of distance d = i - j from the
-  // diagonal, one block per wave, on fp32 MFMA. The partial sum goes through the (unused) mirror block A[j][i].
+  // diagonal, one block per wave, on fp32 MFMA. The partial sum goes through the wavefront's own block of LDS.
 #pragma unroll
   for (int d = 1; d < 4; ++d) {
     if (w < 4 - d) {
@@ -615,18 +632,18 @@ __global__ void __launch_bounds__(256, 4) WyPrepKernel(ChunkArgs ca) {
       for (int k = j; k < i; ++k) {
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-          acc = MfmaF32(a_lds[16 * i + r16][16 * k + 4 * kk + kq], t_lds[16 * k + 4 * kk + kq][16 * j + r16], acc);
+          acc = MfmaF32(a_lds(16 * i + r16, 16 * k + 4 * kk + kq), t_lds(16 * k + 4 * kk + kq, 16 * j + r16), acc);
         }
       }
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii) a_lds[16 * j + 4 * kq + ii][16 * i + r16] = acc[ii];
+      for (int ii = 0; ii < 4; ++ii) p_lds(4 * kq + ii, r16) = acc[ii];
       f32x4_t tij = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        tij = MfmaF32(t_lds[16 * i + r16][16 * i + 4 * kk + kq], a_lds[16 * j + 4 * kk + kq][16 * i + r16], tij);
+        tij = MfmaF32(t_lds(16 * i + r16, 16 * i + 4 * kk + kq), p_lds(4 * kk + kq, r16), tij);
       }
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii) t_lds[16 * i + 4 * kq + ii][16 * j + r16] = -tij[ii];
+      for (int ii = 0; ii < 4; ++ii) t_lds(16 * i + 4 * kq + ii, 16 * j + r16) = -tij[ii];
     }
     __syncthreads();
   }
@@ -634,12 +651,14 @@ __global__ void __launch_bounds__(256, 4) WyPrepKernel(ChunkArgs ca) {
 #pragma unroll
   for (int sp = 0; sp < 2; ++sp) {
     if (sp <= w / 2) {
-      const float* row = &t_lds[16 * w + r16][32 * sp + 4 * kq];
+      const int tr = 16 * w + r16, tc = 32 * sp + 4 * kq;
+      // T is zero above its diagonal blocks, which are not stored.
+      auto tv = [&](int c) { return (c >> 4) > w ? 0.0f : t_lds(tr, c); };
       uint4 hi, lo;
-      Split2(row[0], row[1], hi.x, lo.x);
-      Split2(row[2], row[3], hi.y, lo.y);
-      Split2(row[16], row[17], hi.z, lo.z);
-      Split2(row[18], row[19], hi.w, lo.w);
+      Split2(tv(tc), tv(tc + 1), hi.x, lo.x);
+      Split2(tv(tc + 2), tv(tc + 3), hi.y, lo.y);
+      Split2(tv(tc + 16), tv(tc + 17), hi.z, lo.z);
+      Split2(tv(tc + 18), tv(tc + 19), hi.w, lo.w);
       *reinterpret_cast<uint4*>(rec + kRecTHi + Pair(w, sp) * 1024 + 16 * lane) = hi;
       *reinterpret_cast<uint4*>(rec + kRecTLo + Pair(w, sp) * 1024 + 16 * lane) = lo;
     }
@@ -647,12 +666,12 @@ __global__ void __launch_bounds__(256, 4) WyPrepKernel(ChunkArgs ca) {
   if (tid < 64) {
     float* sc = reinterpret_cast<float*>(rec + kRecScal);
     const float gt = g_lds[tid], gn = g_lds[63];
-    const float e = expf(gt);
+    const float e = Exp2(gt);
     sc[tid] = e * rk_lds[tid];
     sc[64 + tid] = b_lds[tid];
     sc[128 + tid] = rq_lds[tid] * e;
-    sc[192 + tid] = tid < n ? expf(gn - gt) * rk_lds[tid] : 0.0f;
-    if (tid == 0) sc[256] = expf(gn);
+    sc[192 + tid] = tid < n ? Exp2(gn - gt) * rk_lds[tid] : 0.0f;
+    if (tid == 0) sc[256] = Exp2(gn);
   }
 }
 
