@@ -777,15 +777,29 @@ __device__ __forceinline__ void Fetch(const GdnArgs& a, const CopyOffsets& co, c
   }
 }
 
-// Writes a chunk's outputs from its LDS block to the output rows (copier 0): 16 tokens of 4 x 16 bytes per instruction.
+// The workgroup barrier of the storer wavefront. `__syncthreads()` releases at workgroup scope, which waits for every
+// global store of the wavefront to complete (`vmcnt(0)`): a store's round trip at every chunk. Nothing in the workgroup
+// reads the outputs, so the storer only waits for its LDS reads (the block it read may be overwritten after the
+// barrier); the empty asm's memory clobber keeps the compiler from moving memory operations across it.
+__device__ __forceinline__ void BarrierAfterLdsReads() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left at their maxima
+  asm volatile("s_barrier" ::: "memory");
+}
+
+// Writes a chunk's outputs from its LDS block to the output rows (the storer): 16 tokens of 4 x 16 bytes per
+// instruction.
 __device__ __forceinline__ void StoreOut(const GdnArgs& a, const Stage& st, int t0, int n, uint32_t h, uint32_t vb,
                                          int lane) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int t = 16 * i + (lane >> 2);
     const uint4 v = *reinterpret_cast<const uint4*>(st.ob + t * 64 + 16 * (lane & 3));
-    if (t < n) {
-      *reinterpret_cast<uint4*>(a.out + (static_cast<uint64_t>(t0 + t) * a.vh + h) * kDim + vb * 32 + 8 * (lane & 3)) = v;
+    if (t < n) {  // non-temporal: the outputs are not read here again, and kept out of L2 they leave the chain's
+                  // shared k, q and record lines there (config 4: 0.167 against 0.176 ms)
+      typedef uint32_t u32x4_nt __attribute__((ext_vector_type(4)));
+      __builtin_nontemporal_store(u32x4_nt{v.x, v.y, v.z, v.w},
+                                  reinterpret_cast<u32x4_nt*>(a.out + (static_cast<uint64_t>(t0 + t) * a.vh + h) * kDim +
+                                                              vb * 32 + 8 * (lane & 3)));
     }
   }
 }
@@ -944,14 +958,16 @@ __device__ __forceinline__ void Advance(Stage& sg, f32x4_t (&st)[8], int w, int 
 
 }  // namespace wy
 
-// One workgroup of four wavefronts per (sequence, head, value block of 32 columns): wavefronts 0 and 1 compute
+// One workgroup of five wavefronts per (sequence, head, value block of 32 columns): wavefronts 0 and 1 compute
 // (columns 16w .. 16w + 15 of the block each) and never touch global memory inside the loop; wavefronts 2 and 3 copy
-// the next chunk into LDS (and 2 stores the previous chunk's outputs) while they compute, so that the copies, which are
-// bound by HBM, never hold the compute wavefronts at the memory pipeline. blockIdx -> (chain, block) keeps the four
+// the next chunk into LDS while they compute, so that the copies, which are bound by HBM, never hold the compute
+// wavefronts at the memory pipeline; wavefront 4 stores the previous chunk's outputs. The storer passes its barriers
+// without waiting for its stores: with the stores on a copier, the wait for them came back at every chunk
+// (config 4: 0.176 ms against 0.165 with the storer and non-temporal stores). blockIdx -> (chain, block) keeps the four
 // value blocks of a chain on one XCD (workgroups are dealt to the 8 XCDs round-robin): they share the chain's rows and
 // records in L2.
 template <bool kVec>
-__global__ void __launch_bounds__(256, 1) WyScanKernel(ChunkArgs ca) {
+__global__ void __launch_bounds__(320, 1) WyScanKernel(ChunkArgs ca) {
   using namespace wy;
   const GdnArgs& a = ca.a;
   const uint32_t x = blockIdx.x;
@@ -976,6 +992,15 @@ __global__ void __launch_bounds__(256, 1) WyScanKernel(ChunkArgs ca) {
   };
 
   const uint32_t lds0 = Uniform(LdsAddr(&stage[0]));  // LDS byte address of stage[0]; stage[1] follows it
+  if (w == 4) {  // storer: the previous chunk's outputs, from LDS, while the next chunk is computed
+    __syncthreads();
+    for (int c = 0; c < chunks; ++c) {
+      if (c > 0) StoreOut(a, stage[(c - 1) & 1], t0_of(c - 1), n_of(c - 1), h, vb, lane);
+      BarrierAfterLdsReads();
+    }
+    StoreOut(a, stage[(chunks - 1) & 1], t0_of(chunks - 1), n_of(chunks - 1), h, vb, lane);
+    return;
+  }
   if (w >= 2) {  // copiers
     const int copier = w - 2;
     const CopyOffsets co = MakeCopyOffsets(a, h, vb, lane);
@@ -983,7 +1008,6 @@ __global__ void __launch_bounds__(256, 1) WyScanKernel(ChunkArgs ca) {
     WaitVmem();
     __syncthreads();
     for (int c = 0; c < chunks; ++c) {
-      if (copier == 0 && c > 0) StoreOut(a, stage[(c - 1) & 1], t0_of(c - 1), n_of(c - 1), h, vb, lane);
       if (c + 1 < chunks) {
         const int nb = (c + 1) & 1;
         Fetch<kVec>(a, co, rec_of(c + 1), t0_of(c + 1), n_of(c + 1), h, vb, copier, lane, stage[nb],
@@ -992,7 +1016,6 @@ __global__ void __launch_bounds__(256, 1) WyScanKernel(ChunkArgs ca) {
       WaitVmem();
       __syncthreads();
     }
-    if (copier == 0) StoreOut(a, stage[(chunks - 1) & 1], t0_of(chunks - 1), n_of(chunks - 1), h, vb, lane);
     return;
   }
 
@@ -1164,10 +1187,10 @@ RoostStatus LaunchChunk(const RoostGatedDeltaRuleParams& p, const RoostWorkspace
   const dim3 scan((ca.chains + 7) / 8 * 8 * kVBlocks);
   if (Vec16(p)) {
     hipLaunchKernelGGL(WyPrepKernel<true>, prep, dim3(256), 0, stream, ca);
-    hipLaunchKernelGGL(WyScanKernel<true>, scan, dim3(256), 0, stream, ca);
+    hipLaunchKernelGGL(WyScanKernel<true>, scan, dim3(320), 0, stream, ca);
   } else {
     hipLaunchKernelGGL(WyPrepKernel<false>, prep, dim3(256), 0, stream, ca);
-    hipLaunchKernelGGL(WyScanKernel<false>, scan, dim3(256), 0, stream, ca);
+    hipLaunchKernelGGL(WyScanKernel<false>, scan, dim3(320), 0, stream, ca);
   }
   return roost::HipStatus(hipGetLastError(), kOp, "chunk launch");
 }

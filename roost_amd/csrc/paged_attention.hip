@@ -947,6 +947,15 @@ __device__ __forceinline__ void DecodeGroupMfma(DecodeState<uint16_t, D>& st, co
   (void)r;
 }
 
+// A workgroup barrier that orders LDS only: the wavefront's LDS operations complete, global loads and stores stay in
+// flight. `__syncthreads()` also waits for every outstanding global access (`vmcnt(0)`); at a piece's end that is the
+// round trip of its output stores and of the ring's loads past the piece's last group, none of which the barrier
+// protects. The empty asm's memory clobber keeps the compiler from moving memory operations across it.
+__device__ __forceinline__ void LdsBarrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left at their maxima
+  asm volatile("s_barrier" ::: "memory");
+}
+
 // Split-K paged decode. kFastPage: page_size is a multiple of 16, so a 16-token group (16-aligned within its
 // sequence) lies in one page and its page id is one wave-uniform scalar load; otherwise each lane looks its own
 // token's page up. Loads are branch-free (an absent key reads a valid address and is masked) and the next group's
@@ -1146,7 +1155,7 @@ __global__ void __launch_bounds__(256, ROOST_DECODE_WGS_PER_CU) DecodeKernel(con
 #pragma unroll
       for (int e = 0; e < kVec; ++e) o_lds[wave_id][h][r * kVec + e] = st.acc[h][e];
   }
-  __syncthreads();
+  LdsBarrier();
 
   // Workgroup: merge the wavefronts of each KV head, then write the final row or this piece's partial.
   const int split = wk.slot;
@@ -1176,7 +1185,7 @@ __global__ void __launch_bounds__(256, ROOST_DECODE_WGS_PER_CU) DecodeKernel(con
       }
     }
   }
-  __syncthreads();  // the next piece reuses the LDS merge buffers
+  LdsBarrier();  // the next piece reuses the LDS merge buffers
   }
 }
 
