@@ -696,6 +696,15 @@ __device__ __forceinline__ void DmaS(const void* sbase, uint32_t voff, uint32_t 
                : "=&s"(save) : "v"(voff), "s"(sbase), "s"(lds));
 }
 
+// The same copy with the non-temporal hint, for rows one workgroup alone reads (its v block): kept out of L2, they leave
+// room there for the k, q and record lines the chain's four value-block workgroups share (config 4: 0.160 against
+// 0.166 ms).
+__device__ __forceinline__ void DmaSNt(const void* sbase, uint32_t voff, uint32_t lds) {
+  uint32_t save;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\tglobal_load_lds_dwordx4 %1, %2 nt\n\ts_mov_b32 m0, %0"
+               : "=&s"(save) : "v"(voff), "s"(sbase), "s"(lds));
+}
+
 __device__ __forceinline__ uint32_t Uniform(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
 
 // Per-lane byte offsets of a full chunk's copies, fixed for the whole scan. Instruction i of the k (or q) copy fills
@@ -748,7 +757,7 @@ __device__ __forceinline__ void Fetch(const GdnArgs& a, const CopyOffsets& co, c
     for (int i = 0; i < 4; ++i) {  // 16 tokens of 4 x 16 bytes per instruction
       if (full) {
         const auto* vbase = reinterpret_cast<const uint8_t*>(a.v) + static_cast<uint64_t>(t0 + 16 * i) * a.v_stride * 2;
-        DmaS(vbase, co.v, l_vt + 1024 * i);
+        DmaSNt(vbase, co.v, l_vt + 1024 * i);
       } else {
         const int row = 16 * i + (lane >> 2);
         const uint16_t* src = a.v + static_cast<uint64_t>(t0 + min(row, n - 1)) * a.v_stride + h * kDim + vb * 32 +
