@@ -1547,7 +1547,10 @@ __device__ __forceinline__ uint32_t PackRne(float lo, float hi) {
 // Head dims 256, 128 and 64: a row is 2 D bytes = D / 8 16-byte pieces (32, 16 or 8). K pieces are swizzled by the
 // row index modulo min(16, D / 8), which keeps every swizzled piece inside its row and any 8 consecutive rows (the
 // lanes one LDS read cycle serves) on distinct 16-byte bank groups; the V offsets (at most 12 pieces) stay inside a row.
-template <int D>
+// kCap: the call caps its logits; `cap` is then the cap in the kernel's unscaled score units (the log2-unit cap divided
+// by scale_log2, its slope multiplied by it), so that a capped score stays unscaled like an uncapped one. A separate
+// instantiation keeps the cap's registers out of the uncapped kernel, which otherwise spills at head dim 256.
+template <int D, bool kCap>
 __global__ void __launch_bounds__(512, 1)
     PrefillTileKernel(const uint16_t* __restrict__ q, uint16_t* __restrict__ out, float* __restrict__ lse, KvView kv,
                       const int32_t* __restrict__ kv_indices, const int32_t* __restrict__ q_indptr,
@@ -1721,9 +1724,9 @@ __global__ void __launch_bounds__(512, 1)
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
       __builtin_amdgcn_sched_group_barrier(0x008, kRing, 0);
-      if (cap.capl != 0.0f) {  // capped in log2 units, then kept unscaled like the uncapped scores
+      if constexpr (kCap) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) sc[v] = Capped(sc[v] * scale_log2, cap) / scale_log2;
+        for (int v = 0; v < 16; ++v) sc[v] = Capped(sc[v], cap);
       }
       if (need_mask) {  // one uniform branch around branch-free selects
 #pragma unroll
@@ -1960,15 +1963,20 @@ RoostStatus LaunchPrefill(const RoostPagedAttentionParams& p, const PlanRecord& 
     const dim3 grid(static_cast<uint32_t>(rec.work_items));
     const auto* q16 = static_cast<const uint16_t*>(p.q.address);
     const uint32_t ps_shift = static_cast<uint32_t>(__builtin_ctz(p.page_size));
+    // The cap in unscaled score units: Capped(s * scale_log2, cap) / scale_log2 == Capped(s, raw).
+    const SoftCap cap = CapOf(p);
+    const SoftCap raw{cap.capl / scale_log2, cap.k * scale_log2};
+    const bool capped = cap.capl != 0.0f;
+    auto launch = [&](auto kernel) {
+      hipLaunchKernelGGL(kernel, grid, dim3(512), 0, stream, q16, outp, lsep, kv, kv.kv_indices, q_indptr, items,
+                         part_o, part_ml, p.q_heads, p.causal, ps_shift, scale_log2, WindowOf(p), raw);
+    };
     if (p.head_dim == 64) {
-      hipLaunchKernelGGL(PrefillTileKernel<64>, grid, dim3(512), 0, stream, q16, outp, lsep, kv, kv.kv_indices,
-                         q_indptr, items, part_o, part_ml, p.q_heads, p.causal, ps_shift, scale_log2, WindowOf(p), CapOf(p));
+      capped ? launch(PrefillTileKernel<64, true>) : launch(PrefillTileKernel<64, false>);
     } else if (p.head_dim == 128) {
-      hipLaunchKernelGGL(PrefillTileKernel<128>, grid, dim3(512), 0, stream, q16, outp, lsep, kv, kv.kv_indices,
-                         q_indptr, items, part_o, part_ml, p.q_heads, p.causal, ps_shift, scale_log2, WindowOf(p), CapOf(p));
+      capped ? launch(PrefillTileKernel<128, true>) : launch(PrefillTileKernel<128, false>);
     } else {
-      hipLaunchKernelGGL(PrefillTileKernel<256>, grid, dim3(512), 0, stream, q16, outp, lsep, kv, kv.kv_indices,
-                         q_indptr, items, part_o, part_ml, p.q_heads, p.causal, ps_shift, scale_log2, WindowOf(p), CapOf(p));
+      capped ? launch(PrefillTileKernel<256, true>) : launch(PrefillTileKernel<256, false>);
     }
     ROOST_RETURN_IF_FAILED(roost::HipStatus(hipGetLastError(), "paged_attention", "prefill launch"));
     if (rec.merges == 0) return ROOST_STATUS_OK;
