@@ -338,7 +338,16 @@ struct ChunkArgs {
   uint8_t* recs;       // [chunks][heads] records
   const int32_t* seq_list;  // when set: chain c runs sequence seq_list[c / heads] (-1: none)
   uint32_t chains;     // batch * heads, or (length of seq_list) * heads
+  // When set (the recurrent variant's routed calls of at most kFoldBatch sequences), the prep launch routes itself:
+  // each workgroup finds its chunk from cu_seqlens, and workgroup (0, 0) writes the sequence table and the list of
+  // routed sequences (fold_seqs, fold_list) that the scan reads; no chunk table is used.
+  const int32_t* fold_cu;
+  int4* fold_seqs;
+  int32_t* fold_list;
+  uint32_t fold_batch, fold_max_chunks, fold_max_long;
 };
+
+constexpr uint32_t kFoldBatch = 1024;  // sequences one prep workgroup routes (4 per thread)
 
 __device__ __forceinline__ f32x4_t Mfma(uint4 a, uint4 b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
@@ -467,11 +476,90 @@ __device__ __forceinline__ u32x2_t TrRead(const uint8_t* p) {
 // arithmetic is the prep of the WY form: k.k^T and k.q^T on bf16 MFMA from the raw rows (exact products; the norms are
 // applied afterwards in fp32), T by blocked substitution in fp32 (16 x 16 diagonal blocks by forward substitution, the
 // blocks below on v_mfma_f32_16x16x4f32).
+// RouteKernel's rule for one chunk, computed by the prep workgroup that preps it: sequences of kRouteMinTokens or more
+// tokens get ceil(len / 64) chunks, numbered in sequence order, as long as they fit max_chunks. Returns chunk x's
+// (sequence, first token, tokens), or tokens 0 past the routed chunks. The writer (workgroup (0, 0)) also writes the
+// per-sequence table (first chunk, count, first token, end token) and the routed sequences' list, -1 past its end.
+__device__ int4 FoldRoute(const ChunkArgs& ca, uint32_t x, bool writer) {
+  __shared__ uint32_t wave_cnt[4], wave_long[4];
+  __shared__ int4 found;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const uint32_t batch = ca.fold_batch;
+  int32_t t0[4], t1[4];
+  uint32_t cnt[4], mine = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t b = 4 * tid + i;
+    t0[i] = b < batch ? ca.fold_cu[b] : 0;
+    t1[i] = b < batch ? ca.fold_cu[b + 1] : 0;
+    const int32_t len = t1[i] - t0[i];
+    cnt[i] = len >= static_cast<int32_t>(kRouteMinTokens) ? (static_cast<uint32_t>(len) + kChunk - 1) / kChunk : 0;
+    mine += cnt[i];
+  }
+  // Exclusive prefix of the chunk counts over the threads (sequence order is thread order, then i).
+  uint32_t incl = mine;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(incl, o);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) wave_cnt[w] = incl;
+  if (tid == 0) found = make_int4(0, 0, 0, 0);
+  __syncthreads();
+  uint64_t first = incl - mine;
+  for (int i = 0; i < w; ++i) first += wave_cnt[i];
+  bool routed[4];
+  uint32_t mine_long = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    routed[i] = cnt[i] != 0 && first + cnt[i] <= ca.fold_max_chunks;
+    if (routed[i] && x >= first && x < first + cnt[i]) {
+      const int32_t c0 = t0[i] + static_cast<int32_t>(kChunk * (x - first));
+      found = make_int4(static_cast<int32_t>(4 * tid + i), c0, min(static_cast<int32_t>(kChunk), t1[i] - c0), 0);
+    }
+    mine_long += routed[i] ? 1u : 0u;
+    first += cnt[i];
+  }
+  if (writer) {  // the scan's tables: a second prefix over the routed sequences gives each its place in the list
+    uint32_t lincl = mine_long;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_up(lincl, o);
+      if (lane >= o) lincl += y;
+    }
+    if (lane == 63) wave_long[w] = lincl;
+    __syncthreads();
+    uint32_t li = lincl - mine_long, total_long = 0;
+    for (int i = 0; i < 4; ++i) {
+      li += i < w ? wave_long[i] : 0;
+      total_long += wave_long[i];
+    }
+    uint64_t f = first;
+#pragma unroll
+    for (int i = 3; i >= 0; --i) f -= cnt[i];  // back to this thread's first chunk
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t b = 4 * tid + i;
+      if (b < batch) {
+        ca.fold_seqs[b] = routed[i] ? make_int4(static_cast<int32_t>(f), static_cast<int32_t>(cnt[i]), t0[i], t1[i])
+                                    : make_int4(0, 0, t0[i], t1[i]);
+        if (routed[i] && li < ca.fold_max_long) ca.fold_list[li] = static_cast<int32_t>(b);
+      }
+      li += routed[i] ? 1u : 0u;
+      f += cnt[i];
+    }
+    for (uint32_t i = total_long + tid; i < ca.fold_max_long; i += 256) ca.fold_list[i] = -1;
+  }
+  __syncthreads();
+  return found;
+}
+
 template <bool kVec>
 __global__ void __launch_bounds__(256, 6) WyPrepKernel(ChunkArgs ca) {
   using namespace wy;
   const GdnArgs& a = ca.a;
-  const int4 ch = ca.chunks[blockIdx.x];
+  const int4 ch = ca.fold_cu != nullptr ? FoldRoute(ca, blockIdx.x, blockIdx.x == 0 && blockIdx.y == 0)
+                                        : ca.chunks[blockIdx.x];
   const uint32_t h = blockIdx.y;
   const int t0 = ch.y, n = ch.z;
   if (n <= 0) return;  // an unused entry of a table sized for the worst case
@@ -1182,7 +1270,7 @@ __global__ void __launch_bounds__(1024) RouteKernel(const int32_t* cu, uint32_t 
 }
 
 RoostStatus LaunchChunk(const RoostGatedDeltaRuleParams& p, const RoostWorkspace* ws, const ChunkArena& l,
-                        uint32_t chunks, hipStream_t stream) {
+                        uint32_t chunks, hipStream_t stream, bool fold = false) {
   ChunkArgs ca{};
   ca.a = MakeArgs(p);
   auto* base = static_cast<uint8_t*>(ws->device);
@@ -1192,6 +1280,14 @@ RoostStatus LaunchChunk(const RoostGatedDeltaRuleParams& p, const RoostWorkspace
   // The recurrent variant's calls list their chunked sequences; the chunk variant's chains are every sequence.
   ca.seq_list = l.max_long > 0 ? reinterpret_cast<const int32_t*>(base + l.seq_list) : nullptr;
   ca.chains = (l.max_long > 0 ? l.max_long : p.batch) * p.v_heads;
+  if (fold) {
+    ca.fold_cu = static_cast<const int32_t*>(p.cu_seqlens.address);
+    ca.fold_seqs = reinterpret_cast<int4*>(base + l.seq_table);
+    ca.fold_list = reinterpret_cast<int32_t*>(base + l.seq_list);
+    ca.fold_batch = p.batch;
+    ca.fold_max_chunks = l.max_chunks;
+    ca.fold_max_long = l.max_long;
+  }
   const dim3 prep(chunks, p.v_heads);
   const dim3 scan((ca.chains + 7) / 8 * 8 * kVBlocks);
   if (Vec16(p)) {
@@ -1220,15 +1316,20 @@ RoostStatus LaunchRouted(const RoostContext& ctx, const RoostGatedDeltaRuleParam
     ROOST_RETURN_IF_FAILED(roost::HipStatus(hipStreamWaitEvent(ctx.side, ctx.fork, 0), kOp, "fork wait"));
     ROOST_RETURN_IF_FAILED(LaunchRecurrent(p, ctx.side, static_cast<int32_t>(kRouteMinTokens)));
   }
-  hipLaunchKernelGGL(RouteKernel, dim3(1), dim3(1024), 0, s, static_cast<const int32_t*>(p.cu_seqlens.address),
-                     p.batch, l.max_chunks, reinterpret_cast<int4*>(base + l.chunk_table),
-                     reinterpret_cast<int4*>(base + l.seq_table), reinterpret_cast<int32_t*>(base + l.seq_list),
-                     l.max_long);
-  ROOST_RETURN_IF_FAILED(roost::HipStatus(hipGetLastError(), kOp, "route launch"));
+  // Up to kFoldBatch sequences the prep launch routes itself (one launch less per call); larger batches keep the
+  // separate one-workgroup RouteKernel.
+  const bool fold = p.batch <= kFoldBatch;
+  if (!fold) {
+    hipLaunchKernelGGL(RouteKernel, dim3(1), dim3(1024), 0, s, static_cast<const int32_t*>(p.cu_seqlens.address),
+                       p.batch, l.max_chunks, reinterpret_cast<int4*>(base + l.chunk_table),
+                       reinterpret_cast<int4*>(base + l.seq_table), reinterpret_cast<int32_t*>(base + l.seq_list),
+                       l.max_long);
+    ROOST_RETURN_IF_FAILED(roost::HipStatus(hipGetLastError(), kOp, "route launch"));
+  }
   RoostWorkspace ws{};
   ws.device = base;
   ws.device_bytes = l.total;
-  ROOST_RETURN_IF_FAILED(LaunchChunk(p, &ws, l, l.max_chunks, s));
+  ROOST_RETURN_IF_FAILED(LaunchChunk(p, &ws, l, l.max_chunks, s, fold));
   if (!fork) return LaunchRecurrent(p, s, static_cast<int32_t>(kRouteMinTokens));
   ROOST_RETURN_IF_FAILED(roost::HipStatus(hipEventRecord(ctx.join, ctx.side), kOp, "join event"));
   return roost::HipStatus(hipStreamWaitEvent(s, ctx.join, 0), kOp, "join wait");

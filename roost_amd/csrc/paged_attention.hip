@@ -1538,7 +1538,9 @@ __device__ __forceinline__ u32x2_t LdsTr16(const unsigned char* base, uint32_t o
   return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(ptr));
 }
 
-// Round-to-nearest-even pack of two finite floats (v_cvt_pk_bf16_f32): the softmax weights, which lie in [0, 256].
+// Round-to-nearest-even pack of two floats (v_cvt_pk_bf16_f32): the softmax weights, which lie in [0, 256], and the
+// tile kernel's outputs (the same rounding as PackBf16 for every finite value; only a NaN, which finite inputs never
+// produce here, may keep another NaN pattern than 0x7FC0).
 __device__ __forceinline__ uint32_t PackRne(float lo, float hi) {
   const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
   return __builtin_bit_cast(uint32_t, v);
@@ -1694,8 +1696,11 @@ __global__ void __launch_bounds__(512, 1)
     // +4 (j % 4), keys based at 16 c16 + 4 (g >> 1) (+8 for the operand's second half), dims at 32 dt + 16 (g & 1);
     // block (c16, dt) of the V tile holds exactly those 8 bytes at 8 ln (and the second half's at 512 + 8 ln).
     const int32_t qpos = static_cast<int32_t>(kv_len) - n + wk.q0 + 32 * qt + lc;  // this lane's query position
-    const bool need_mask = kb + 64 > kend || (causal && kb + 63 > last_pos - 31) || bad != 0 ||
-                           (window >= 0 && kb < last_pos - window);
+    // Every term is wave-uniform; readfirstlane says so, so that the masking below is skipped by a scalar branch
+    // instead of running under an empty exec mask on every tile.
+    const bool need_mask = __builtin_amdgcn_readfirstlane(
+        static_cast<int>((kb + 64 > kend) | (causal && kb + 63 > last_pos - 31) | (bad != 0) |
+                         (window >= 0 && kb < last_pos - window))) != 0;
     const unsigned char* ktile = tiles[buf][0];
     const unsigned char* vtile = tiles[buf][1];
     const unsigned char* vl = vtile + 8 * ln;
@@ -1733,8 +1738,9 @@ __global__ void __launch_bounds__(512, 1)
         for (int v = 0; v < 16; ++v) {
           const int kk = 32 * half + (v >> 2) * 8 + lh * 4 + (v & 3);  // key within the tile
           const int32_t key = kb + kk;
-          const bool off = key >= kend || (causal && key > qpos) || ((bad >> (kk >> 4)) & 1u) ||
-                           (window >= 0 && key < qpos - window);
+          // Bitwise ors: no short-circuit branches (each would be an exec-mask change per score).
+          const bool off = (key >= kend) | ((causal != 0) & (key > qpos)) | (((bad >> (kk >> 4)) & 1u) != 0) |
+                           ((window >= 0) & (key < qpos - window));
           sc[v] = off ? -INFINITY : sc[v];
         }
       }
@@ -1804,8 +1810,8 @@ __global__ void __launch_bounds__(512, 1)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int d = dt * 32 + i * 8 + hl * 4;
-        const u32x2_t v{PackBf16(o[dt][i * 4] * inv, o[dt][i * 4 + 1] * inv),
-                        PackBf16(o[dt][i * 4 + 2] * inv, o[dt][i * 4 + 3] * inv)};
+        const u32x2_t v{PackRne(o[dt][i * 4] * inv, o[dt][i * 4 + 1] * inv),
+                        PackRne(o[dt][i * 4 + 2] * inv, o[dt][i * 4 + 3] * inv)};
         *reinterpret_cast<u32x2_t*>(po + d) = v;
       }
     if (hl == 0) {
@@ -1820,8 +1826,8 @@ __global__ void __launch_bounds__(512, 1)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int d = dt * 32 + i * 8 + hl * 4;
-      const u32x2_t v{PackBf16(o[dt][i * 4] * inv, o[dt][i * 4 + 1] * inv),
-                      PackBf16(o[dt][i * 4 + 2] * inv, o[dt][i * 4 + 3] * inv)};
+      const u32x2_t v{PackRne(o[dt][i * 4] * inv, o[dt][i * 4 + 1] * inv),
+                      PackRne(o[dt][i * 4 + 2] * inv, o[dt][i * 4 + 3] * inv)};
       *reinterpret_cast<u32x2_t*>(out + orow + d) = v;
     }
   if (lse != nullptr && hl == 0) {
