@@ -65,6 +65,16 @@ constexpr float kLog2e = 1.4426950408889634f;
 // Logit soft capping (CpuOps.cs:276: s -> cap tanh(s / cap) after the scale), applied to scores in log2 units:
 // y -> capl tanh(y / capl) with capl = |cap| log2(e), through tanh(u) = 1 - 2 / (1 + e^(2u)) = 1 - 2 / (1 + 2^(y k)),
 // k = 2 log2(e) / capl. capl = 0 turns it off. Masked scores are set to -inf after capping.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Round-to-nearest-even pack of two floats (v_cvt_pk_bf16_f32): the softmax weights, which lie in [0, 256], and the
+// tile kernel's outputs (the same rounding as PackBf16 for every finite value; only a NaN, which finite inputs never
+// produce here, may keep another NaN pattern than 0x7FC0).
+__device__ __forceinline__ uint32_t PackRne(float lo, float hi) {
+  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 struct SoftCap {
   float capl;
   float k;
@@ -665,7 +675,6 @@ struct Vec<float> {
   __device__ static float Narrow(float x) { return x; }
 };
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
@@ -921,10 +930,10 @@ __device__ __forceinline__ void DecodeGroupMfma(DecodeState<uint16_t, D>& st, co
   for (int a = 0; a < kNi / 2; ++a) {
     const float4 p0 = *reinterpret_cast<const float4*>(&x_row[(kTpi * (2 * a) + ri) * kGroup]);
     const float4 p1 = *reinterpret_cast<const float4*>(&x_row[(kTpi * (2 * a + 1) + ri) * kGroup]);
-    pp[a][0] = PackBf16(p0.x, p1.x);
-    pp[a][1] = PackBf16(p0.y, p1.y);
-    pp[a][2] = PackBf16(p0.z, p1.z);
-    pp[a][3] = PackBf16(p0.w, p1.w);
+    pp[a][0] = PackRne(p0.x, p1.x);
+    pp[a][1] = PackRne(p0.y, p1.y);
+    pp[a][2] = PackRne(p0.z, p1.z);
+    pp[a][3] = PackRne(p0.w, p1.w);
   }
   __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -1538,13 +1547,6 @@ __device__ __forceinline__ u32x2_t LdsTr16(const unsigned char* base, uint32_t o
   return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(ptr));
 }
 
-// Round-to-nearest-even pack of two floats (v_cvt_pk_bf16_f32): the softmax weights, which lie in [0, 256], and the
-// tile kernel's outputs (the same rounding as PackBf16 for every finite value; only a NaN, which finite inputs never
-// produce here, may keep another NaN pattern than 0x7FC0).
-__device__ __forceinline__ uint32_t PackRne(float lo, float hi) {
-  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
-  return __builtin_bit_cast(uint32_t, v);
-}
 
 // Head dims 256, 128 and 64: a row is 2 D bytes = D / 8 16-byte pieces (32, 16 or 8). K pieces are swizzled by the
 // row index modulo min(16, D / 8), which keeps every swizzled piece inside its row and any 8 consecutive rows (the
