@@ -141,24 +141,6 @@ struct GdnArgs {
   uint32_t group;  // value heads per key head: value head h reads q / k head h / group
 };
 
-// Loads 32 consecutive bf16 of a row as floats: 16-byte loads when the view is 16-byte aligned, else 2-byte loads.
-template <bool kVec>
-__device__ __forceinline__ void Load32(const uint16_t* src, float* dst) {
-  if constexpr (kVec) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint4 w = reinterpret_cast<const uint4*>(src)[i];
-      dst[8 * i + 0] = Bf16LoToF32(w.x); dst[8 * i + 1] = Bf16HiToF32(w.x);
-      dst[8 * i + 2] = Bf16LoToF32(w.y); dst[8 * i + 3] = Bf16HiToF32(w.y);
-      dst[8 * i + 4] = Bf16LoToF32(w.z); dst[8 * i + 5] = Bf16HiToF32(w.z);
-      dst[8 * i + 6] = Bf16LoToF32(w.w); dst[8 * i + 7] = Bf16HiToF32(w.w);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 32; ++i) dst[i] = Bf16ToF32(src[i]);
-  }
-}
-
 typedef float f32x4v_t __attribute__((ext_vector_type(4)));
 
 // The recurrent step reads each state row once and writes it once, in whole 512-byte runs per wavefront: non-temporal
@@ -171,76 +153,120 @@ __device__ __forceinline__ void StoreStreamF4(float* p, const float4& x) {
   __builtin_nontemporal_store(f32x4v_t{x.x, x.y, x.z, x.w}, reinterpret_cast<f32x4v_t*>(p));
 }
 
+// Sum over the 8 lanes of a row group (lanes 8m .. 8m + 7).
+__device__ __forceinline__ float OctSum(float x) {
+  x += __shfl_xor(x, 1, 64);
+  x += __shfl_xor(x, 2, 64);
+  x += __shfl_xor(x, 4, 64);
+  return x;
+}
+
 __device__ __forceinline__ float QuadSum(float x) {
   x += __shfl_xor(x, 1, 64);
   x += __shfl_xor(x, 2, 64);
   return x;
 }
 
-// One workgroup per (sequence, value head): the token-serial recurrence with S held in registers.
+// The value columns of a state are independent in the recurrence (column c reads only S[:, c], k, q and v[c]), so each
+// (sequence, value head) is split over kRecQuarters workgroups of 32 columns. Within one, wavefront w holds rows
+// 32 w .. + 31 and lane l rows 32 w + 4 (l % 8) .. + 3 of columns 4 (l / 8) .. + 3 (16 floats): a state-row access by a
+// wavefront is eight whole 128-byte lines, and the dot products over rows reduce over the 8 lanes of a row group and
+// then over the 4 wavefronts through LDS. At 16 floats of state per lane the workgroups of a whole decode step are
+// resident at once, beside the prep workgroups when both share a launch.
+constexpr uint32_t kRecQuarters = 4;
+constexpr uint32_t kRecThreads = 256;
+
+// Workgroup (sequence b, value head h, column quarter): the token-serial recurrence with its share of S in registers.
 template <bool kVec>
-__global__ void __launch_bounds__(128) RecurrentKernel(GdnArgs a) {
-  const uint32_t b = blockIdx.x;
-  const uint32_t h = blockIdx.y;
+__device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint32_t h, uint32_t quarter) {
+  __shared__ float red_sk[4][32], red_o[4][32];
   const int32_t t0 = a.cu[b];
   const int32_t t1 = a.cu[b + 1];
   if (t1 <= t0) return;  // an empty sequence leaves its slot untouched
   if (a.route_min > 0 && t1 - t0 >= a.route_min) return;  // run by the chunk kernels
   const int32_t slot = a.slots[b];
   const bool has_slot = slot >= 0 && static_cast<uint64_t>(slot) < a.pool_slots;
-  const int t = threadIdx.x;
-  const int rq = t & 3;   // key rows 32*rq .. +31
-  const int cg = t >> 2;  // value columns 4*cg .. +3
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int rg = lane & 7;  // key rows 32 w + 4 rg .. + 3
+  const int cg = lane >> 3;  // value columns 32 quarter + 4 cg .. + 3
+  const int row0 = 32 * w + 4 * rg;
+  const uint32_t col = 32 * quarter + 4 * cg;
   const uint32_t kh = h / a.group;
-  float4 s[32];
-  float* sp = has_slot ? a.state + (static_cast<uint64_t>(slot) * a.vh + h) * kDim * kDim : nullptr;
+  float4 s[4];
+  float* sp = has_slot ? a.state + (static_cast<uint64_t>(slot) * a.vh + h) * kDim * kDim + col : nullptr;
   if (has_slot && a.use_initial_state) {
 #pragma unroll
-    for (int i = 0; i < 32; ++i) s[i] = LoadStreamF4(sp + (rq * 32 + i) * kDim + cg * 4);
+    for (int i = 0; i < 4; ++i) s[i] = LoadStreamF4(sp + (row0 + i) * kDim);
   } else {
 #pragma unroll
-    for (int i = 0; i < 32; ++i) s[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = 0; i < 4; ++i) s[i] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   for (int32_t tok = t0; tok < t1; ++tok) {
-    float qv[32], kv[32];
-    Load32<kVec>(a.q + static_cast<uint64_t>(tok) * a.q_stride + kh * kDim + rq * 32, qv);
-    Load32<kVec>(a.k + static_cast<uint64_t>(tok) * a.k_stride + kh * kDim + rq * 32, kv);
-    float qq = 0.f, kk = 0.f;
+    const uint16_t* qrow = a.q + static_cast<uint64_t>(tok) * a.q_stride + kh * kDim;
+    const uint16_t* krow = a.k + static_cast<uint64_t>(tok) * a.k_stride + kh * kDim;
+    // The norms: lane l squares elements 2l, 2l + 1 and the wavefront reduces, so that every wavefront has them whole.
+    float q2[2], k2[2], q4[4], k4[4], vv[4];
+    const uint16_t* vrow = a.v + static_cast<uint64_t>(tok) * a.v_stride + h * kDim + col;
+    if constexpr (kVec) {
+      const uint32_t qw = *reinterpret_cast<const uint32_t*>(qrow + 2 * lane);
+      const uint32_t kw = *reinterpret_cast<const uint32_t*>(krow + 2 * lane);
+      const uint2 qr = *reinterpret_cast<const uint2*>(qrow + row0), kr = *reinterpret_cast<const uint2*>(krow + row0);
+      const uint2 vw = *reinterpret_cast<const uint2*>(vrow);
+      q2[0] = Bf16LoToF32(qw); q2[1] = Bf16HiToF32(qw);
+      k2[0] = Bf16LoToF32(kw); k2[1] = Bf16HiToF32(kw);
+      q4[0] = Bf16LoToF32(qr.x); q4[1] = Bf16HiToF32(qr.x); q4[2] = Bf16LoToF32(qr.y); q4[3] = Bf16HiToF32(qr.y);
+      k4[0] = Bf16LoToF32(kr.x); k4[1] = Bf16HiToF32(kr.x); k4[2] = Bf16LoToF32(kr.y); k4[3] = Bf16HiToF32(kr.y);
+      vv[0] = Bf16LoToF32(vw.x); vv[1] = Bf16HiToF32(vw.x); vv[2] = Bf16LoToF32(vw.y); vv[3] = Bf16HiToF32(vw.y);
+    } else {
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      qq = fmaf(qv[i], qv[i], qq);
-      kk = fmaf(kv[i], kv[i], kk);
+      for (int i = 0; i < 2; ++i) {
+        q2[i] = Bf16ToF32(qrow[2 * lane + i]);
+        k2[i] = Bf16ToF32(krow[2 * lane + i]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        q4[i] = Bf16ToF32(qrow[row0 + i]);
+        k4[i] = Bf16ToF32(krow[row0 + i]);
+        vv[i] = Bf16ToF32(vrow[i]);
+      }
     }
-    qq = QuadSum(qq);
-    kk = QuadSum(kk);
-    const float qn = a.scale / sqrtf(qq + 1e-6f);
-    const float kn = 1.0f / sqrtf(kk + 1e-6f);
     const uint64_t gi = static_cast<uint64_t>(tok) * a.vh + h;
     const float decay = expf(a.g[gi]);
     const float beta = Bf16ToF32(a.beta[gi]);
-    const uint16_t* vrow = a.v + static_cast<uint64_t>(tok) * a.v_stride + h * kDim + cg * 4;
-    float vv[4];
+    float qq = fmaf(q2[0], q2[0], q2[1] * q2[1]), kk = fmaf(k2[0], k2[0], k2[1] * k2[1]);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) vv[c] = Bf16ToF32(vrow[c]);
-    // S^T k over this thread's rows, then across the quad.
+    for (int o = 1; o < 64; o <<= 1) {
+      qq += __shfl_xor(qq, o, 64);
+      kk += __shfl_xor(kk, o, 64);
+    }
+    const float qn = a.scale / sqrtf(qq + 1e-6f);
+    const float kn = 1.0f / sqrtf(kk + 1e-6f);
+    // S^T k: this lane's 4 rows, the row group's 32, then the workgroup's 128 through LDS.
     float sk[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      const float ki = kv[i] * kn;
-      kv[i] = ki;
-      sk[0] = fmaf(s[i].x, ki, sk[0]);
-      sk[1] = fmaf(s[i].y, ki, sk[1]);
-      sk[2] = fmaf(s[i].z, ki, sk[2]);
-      sk[3] = fmaf(s[i].w, ki, sk[3]);
+    for (int i = 0; i < 4; ++i) {
+      k4[i] *= kn;
+      sk[0] = fmaf(s[i].x, k4[i], sk[0]);
+      sk[1] = fmaf(s[i].y, k4[i], sk[1]);
+      sk[2] = fmaf(s[i].z, k4[i], sk[2]);
+      sk[3] = fmaf(s[i].w, k4[i], sk[3]);
     }
-    float d[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) d[c] = beta * (vv[c] - decay * QuadSum(sk[c]));
+    for (int c = 0; c < 4; ++c) sk[c] = OctSum(sk[c]);
+    if (rg == 0) *reinterpret_cast<float4*>(&red_sk[w][4 * cg]) = make_float4(sk[0], sk[1], sk[2], sk[3]);
+    __syncthreads();
+    float4 tot = *reinterpret_cast<const float4*>(&red_sk[0][4 * cg]);
+#pragma unroll
+    for (int ww = 1; ww < 4; ++ww) {
+      const float4 x = *reinterpret_cast<const float4*>(&red_sk[ww][4 * cg]);
+      tot = make_float4(tot.x + x.x, tot.y + x.y, tot.z + x.z, tot.w + x.w);
+    }
+    const float d[4] = {beta * (vv[0] - decay * tot.x), beta * (vv[1] - decay * tot.y),
+                        beta * (vv[2] - decay * tot.z), beta * (vv[3] - decay * tot.w)};
     float o[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      const float ki = kv[i];
-      const float qi = qv[i] * qn;
+    for (int i = 0; i < 4; ++i) {
+      const float ki = k4[i], qi = q4[i] * qn;
       s[i].x = fmaf(s[i].x, decay, ki * d[0]);
       s[i].y = fmaf(s[i].y, decay, ki * d[1]);
       s[i].z = fmaf(s[i].z, decay, ki * d[2]);
@@ -251,18 +277,31 @@ __global__ void __launch_bounds__(128) RecurrentKernel(GdnArgs a) {
       o[3] = fmaf(s[i].w, qi, o[3]);
     }
 #pragma unroll
-    for (int c = 0; c < 4; ++c) o[c] = QuadSum(o[c]);
-    if (rq == 0) {
-      uint2 w;
-      w.x = PackBf16(o[0], o[1]);
-      w.y = PackBf16(o[2], o[3]);
-      *reinterpret_cast<uint2*>(a.out + (static_cast<uint64_t>(tok) * a.vh + h) * kDim + cg * 4) = w;
+    for (int c = 0; c < 4; ++c) o[c] = OctSum(o[c]);
+    if (rg == 0) *reinterpret_cast<float4*>(&red_o[w][4 * cg]) = make_float4(o[0], o[1], o[2], o[3]);
+    __syncthreads();
+    if (w == 0 && rg == 0) {
+      float4 ot = *reinterpret_cast<const float4*>(&red_o[0][4 * cg]);
+#pragma unroll
+      for (int ww = 1; ww < 4; ++ww) {
+        const float4 x = *reinterpret_cast<const float4*>(&red_o[ww][4 * cg]);
+        ot = make_float4(ot.x + x.x, ot.y + x.y, ot.z + x.z, ot.w + x.w);
+      }
+      uint2 pw;
+      pw.x = PackBf16(ot.x, ot.y);
+      pw.y = PackBf16(ot.z, ot.w);
+      *reinterpret_cast<uint2*>(a.out + (static_cast<uint64_t>(tok) * a.vh + h) * kDim + col) = pw;
     }
   }
   if (has_slot) {
 #pragma unroll
-    for (int i = 0; i < 32; ++i) StoreStreamF4(sp + (rq * 32 + i) * kDim + cg * 4, s[i]);
+    for (int i = 0; i < 4; ++i) StoreStreamF4(sp + (row0 + i) * kDim, s[i]);
   }
+}
+
+template <bool kVec>
+__global__ void __launch_bounds__(kRecThreads) RecurrentKernel(GdnArgs a) {
+  RecurrentUnit<kVec>(a, blockIdx.x, blockIdx.y / kRecQuarters, blockIdx.y % kRecQuarters);
 }
 
 GdnArgs MakeArgs(const RoostGatedDeltaRuleParams& p) {
@@ -297,11 +336,11 @@ bool Vec16(const RoostGatedDeltaRuleParams& p) {
 RoostStatus LaunchRecurrent(const RoostGatedDeltaRuleParams& p, hipStream_t stream, int32_t route_min = 0) {
   GdnArgs a = MakeArgs(p);
   a.route_min = route_min;
-  const dim3 grid(p.batch, p.v_heads);
+  const dim3 grid(p.batch, p.v_heads * kRecQuarters);
   if (Vec16(p)) {
-    hipLaunchKernelGGL(RecurrentKernel<true>, grid, dim3(128), 0, stream, a);
+    hipLaunchKernelGGL(RecurrentKernel<true>, grid, dim3(kRecThreads), 0, stream, a);
   } else {
-    hipLaunchKernelGGL(RecurrentKernel<false>, grid, dim3(128), 0, stream, a);
+    hipLaunchKernelGGL(RecurrentKernel<false>, grid, dim3(kRecThreads), 0, stream, a);
   }
   return roost::HipStatus(hipGetLastError(), kOp, "recurrent launch");
 }
@@ -345,6 +384,7 @@ struct ChunkArgs {
   int4* fold_seqs;
   int32_t* fold_list;
   uint32_t fold_batch, fold_max_chunks, fold_max_long;
+  uint32_t prep_x;  // WyPrepRecurrentKernel: workgroup columns that prep chunks (the rest run recurrent sequences)
 };
 
 constexpr uint32_t kFoldBatch = 1024;  // sequences one prep workgroup routes (4 per thread)
@@ -555,19 +595,17 @@ __device__ int4 FoldRoute(const ChunkArgs& ca, uint32_t x, bool writer) {
 }
 
 template <bool kVec>
-__global__ void __launch_bounds__(256, 6) WyPrepKernel(ChunkArgs ca) {
+__device__ __forceinline__ void WyPrepChunk(const ChunkArgs& ca, uint32_t x, uint32_t h) {
   using namespace wy;
   const GdnArgs& a = ca.a;
-  const int4 ch = ca.fold_cu != nullptr ? FoldRoute(ca, blockIdx.x, blockIdx.x == 0 && blockIdx.y == 0)
-                                        : ca.chunks[blockIdx.x];
-  const uint32_t h = blockIdx.y;
+  const int4 ch = ca.fold_cu != nullptr ? FoldRoute(ca, x, x == 0 && h == 0) : ca.chunks[x];
   const int t0 = ch.y, n = ch.z;
   if (n <= 0) return;  // an unused entry of a table sized for the worst case
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, kq = lane >> 4;
   const uint32_t kh = h / a.group;
-  uint8_t* rec = ca.recs + (static_cast<uint64_t>(blockIdx.x) * a.vh + h) * kRecBytes;
+  uint8_t* rec = ca.recs + (static_cast<uint64_t>(x) * a.vh + h) * kRecBytes;
 
   // region0 holds the raw k rows (a [64][kTilePitch] bf16 tile; each wavefront keeps its own 16 q rows in registers).
   // Once the products are formed it holds A and T (fp32) as their 10 lower-triangular 16 x 16 blocks each, and one
@@ -760,6 +798,28 @@ __global__ void __launch_bounds__(256, 6) WyPrepKernel(ChunkArgs ca) {
     sc[128 + tid] = rq_lds[tid] * e;
     sc[192 + tid] = tid < n ? Exp2(gn - gt) * rk_lds[tid] : 0.0f;
     if (tid == 0) sc[256] = Exp2(gn);
+  }
+}
+
+template <bool kVec>
+__global__ void __launch_bounds__(256, 6) WyPrepKernel(ChunkArgs ca) {
+  WyPrepChunk<kVec>(ca, blockIdx.x, blockIdx.y);
+}
+
+// The recurrent variant's routed calls: the prep workgroups (the first prep_x x heads of a 1-D grid, every head of a
+// chunk in turn) and, behind them, one workgroup per (sequence, value head, column quarter) for the recurrence of the
+// sequences shorter than a.route_min. One launch instead of two streams: the recurrent work fills the CUs the prep
+// leaves idle, and the scan that follows has the chip to itself. The prep workgroups come first in dispatch order, so
+// that none of them waits behind recurrent ones for a slot.
+template <bool kVec>
+__global__ void __launch_bounds__(256) WyPrepRecurrentKernel(ChunkArgs ca) {
+  static_assert(kRecThreads == 256, "the prep and recurrent workgroups share one size");
+  const uint32_t vh = ca.a.vh, i = blockIdx.x, preps = ca.prep_x * vh;
+  if (i < preps) {
+    WyPrepChunk<kVec>(ca, i / vh, i % vh);
+  } else {
+    const uint32_t j = i - preps, per_seq = vh * kRecQuarters;
+    RecurrentUnit<kVec>(ca.a, j / per_seq, (j % per_seq) / kRecQuarters, j % kRecQuarters);
   }
 }
 
@@ -1269,8 +1329,9 @@ __global__ void __launch_bounds__(1024) RouteKernel(const int32_t* cu, uint32_t 
   }
 }
 
+// with_recurrent: the prep launch also runs the recurrence of the sequences shorter than kRouteMinTokens.
 RoostStatus LaunchChunk(const RoostGatedDeltaRuleParams& p, const RoostWorkspace* ws, const ChunkArena& l,
-                        uint32_t chunks, hipStream_t stream, bool fold = false) {
+                        uint32_t chunks, hipStream_t stream, bool fold = false, bool with_recurrent = false) {
   ChunkArgs ca{};
   ca.a = MakeArgs(p);
   auto* base = static_cast<uint8_t*>(ws->device);
@@ -1290,7 +1351,18 @@ RoostStatus LaunchChunk(const RoostGatedDeltaRuleParams& p, const RoostWorkspace
   }
   const dim3 prep(chunks, p.v_heads);
   const dim3 scan((ca.chains + 7) / 8 * 8 * kVBlocks);
-  if (Vec16(p)) {
+  if (with_recurrent) {
+    ca.a.route_min = static_cast<int32_t>(kRouteMinTokens);
+    ca.prep_x = chunks;
+    const dim3 both((chunks + p.batch * kRecQuarters) * p.v_heads);
+    if (Vec16(p)) {
+      hipLaunchKernelGGL(WyPrepRecurrentKernel<true>, both, dim3(256), 0, stream, ca);
+      hipLaunchKernelGGL(WyScanKernel<true>, scan, dim3(320), 0, stream, ca);
+    } else {
+      hipLaunchKernelGGL(WyPrepRecurrentKernel<false>, both, dim3(256), 0, stream, ca);
+      hipLaunchKernelGGL(WyScanKernel<false>, scan, dim3(320), 0, stream, ca);
+    }
+  } else if (Vec16(p)) {
     hipLaunchKernelGGL(WyPrepKernel<true>, prep, dim3(256), 0, stream, ca);
     hipLaunchKernelGGL(WyScanKernel<true>, scan, dim3(320), 0, stream, ca);
   } else {
@@ -1300,24 +1372,13 @@ RoostStatus LaunchChunk(const RoostGatedDeltaRuleParams& p, const RoostWorkspace
   return roost::HipStatus(hipGetLastError(), kOp, "chunk launch");
 }
 
-// The recurrent variant's routed path over a device region laid out as `l`: RouteKernel writes the chunk tables of the
-// sequences of kRouteMinTokens or more tokens from the device cu_seqlens, the chunk kernels run those sequences and the
-// recurrent kernel the rest. The recurrent kernel is forked onto the context's side stream (after everything the
-// caller queued before this call) and joined back before the call returns, so it runs beside the chunk kernels: their
-// chains leave most of the chip idle (one workgroup per chain and value block) and a recurrent workgroup (237 VGPRs,
-// no LDS) fits beside a scan workgroup on one CU. Without a side stream the three run in order on the caller's
-// stream. Sequences of one call must use distinct state slots: two that share one race (they may run at the same time
-// on either path), as they do in the reference's gather / scatter of the slots.
-RoostStatus LaunchRouted(const RoostContext& ctx, const RoostGatedDeltaRuleParams& p, uint8_t* base, const ChunkArena& l,
-                         hipStream_t s) {
-  const bool fork = ctx.side != nullptr;
-  if (fork) {
-    ROOST_RETURN_IF_FAILED(roost::HipStatus(hipEventRecord(ctx.fork, s), kOp, "fork event"));
-    ROOST_RETURN_IF_FAILED(roost::HipStatus(hipStreamWaitEvent(ctx.side, ctx.fork, 0), kOp, "fork wait"));
-    ROOST_RETURN_IF_FAILED(LaunchRecurrent(p, ctx.side, static_cast<int32_t>(kRouteMinTokens)));
-  }
-  // Up to kFoldBatch sequences the prep launch routes itself (one launch less per call); larger batches keep the
-  // separate one-workgroup RouteKernel.
+// The recurrent variant's routed path over a device region laid out as `l`: the sequences of kRouteMinTokens or more
+// tokens are cut into chunks (by the prep launch itself up to kFoldBatch sequences, else by RouteKernel from the device
+// cu_seqlens), and the prep launch also runs the recurrence of the shorter ones in workgroups of its own, beside the
+// prep workgroups: the chunks' chains leave most of the chip idle. The scan follows on the same stream. Sequences of
+// one call must use distinct state slots: two that share one race (they may run at the same time), as they do in the
+// reference's gather / scatter of the slots.
+RoostStatus LaunchRouted(const RoostGatedDeltaRuleParams& p, uint8_t* base, const ChunkArena& l, hipStream_t s) {
   const bool fold = p.batch <= kFoldBatch;
   if (!fold) {
     hipLaunchKernelGGL(RouteKernel, dim3(1), dim3(1024), 0, s, static_cast<const int32_t*>(p.cu_seqlens.address),
@@ -1329,10 +1390,7 @@ RoostStatus LaunchRouted(const RoostContext& ctx, const RoostGatedDeltaRuleParam
   RoostWorkspace ws{};
   ws.device = base;
   ws.device_bytes = l.total;
-  ROOST_RETURN_IF_FAILED(LaunchChunk(p, &ws, l, l.max_chunks, s, fold));
-  if (!fork) return LaunchRecurrent(p, s, static_cast<int32_t>(kRouteMinTokens));
-  ROOST_RETURN_IF_FAILED(roost::HipStatus(hipEventRecord(ctx.join, ctx.side), kOp, "join event"));
-  return roost::HipStatus(hipStreamWaitEvent(s, ctx.join, 0), kOp, "join wait");
+  return LaunchChunk(p, &ws, l, l.max_chunks, s, fold, /*with_recurrent=*/true);
 }
 
 }  // namespace
@@ -1377,7 +1435,7 @@ extern "C" ROOST_API RoostStatus roost_gdn_recurrent_run(RoostContext* ctx, cons
                 "%u tokens may route sequences to the chunk kernels, which need %llu device workspace bytes",
                 p.tokens, static_cast<unsigned long long>(l.total));
     ROOST_GATE_RETURN(gate);
-    return LaunchRouted(*ctx, p, static_cast<uint8_t*>(ws->device), l, s);
+    return LaunchRouted(p, static_cast<uint8_t*>(ws->device), l, s);
   });
 }
 
@@ -1539,7 +1597,7 @@ extern "C" ROOST_API RoostStatus roost_amd_gdn_recurrent_run_noalloc(RoostContex
     ROOST_GATE_RETURN(gate);
     uint8_t* base = nullptr;
     ROOST_RETURN_IF_FAILED(ScratchFor(current, &base));
-    return LaunchRouted(*ctx, p, base, l, s);
+    return LaunchRouted(p, base, l, s);
   });
 }
 
