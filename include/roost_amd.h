@@ -166,6 +166,41 @@ ROOST_API RoostStatus roost_amd_plan_region_fill(const RoostAmdPlanRegion* regio
  * index outside [0, tokens) is skipped and a position past its sequence's blocks gets slot -1 (CacheWrite skips it). */
 ROOST_API RoostStatus roost_amd_plan_region_run(RoostContext* ctx, const RoostAmdPlanRegion* region, void* stream);
 
+/* The same tables read straight from a C2 step plan: the shared buffer the engine writes (RoostStepPlanHeader and its
+ * tables, reference kernels/include/roost_worker_shm.h:57-141), in place of the worker's StepPlanReader.Read +
+ * PlanRegionWriter.Fill (src/Starlings.Roost.Worker/Eager/StepPlanReader.cs:195-345, PlanRegionWriter.cs:19-64).
+ * Sequence b's KV blocks are the first ceil((position_offset + token_count) / block_size) ids of its group_blocks entry
+ * b * group_count + attention_group; its keys after the step are position_offset + token_count. Besides the tables of
+ * roost_amd_plan_region_fill it writes ids[index] = token_ids[index] and, for each sequence with the sample flag
+ * (0x2) in plan order, rows[r] = its last token index. The plan is checked as the reader checks the fields used here
+ * (magic, table bounds and counts, contiguous non-empty token ranges, consecutive positions, group_blocks_start ==
+ * b * group_count, enough blocks listed); a plan that fails, or outputs shorter than it needs, is refused with
+ * ROOST_STATUS_INVALID_ARGUMENT and nothing is written. Host memory only. */
+typedef struct RoostAmdStepTables {
+  uint32_t attention_group;  /* the state group whose block lists hold the attention KV blocks */
+  uint32_t block_size;       /* tokens per KV page, > 0 */
+  uint32_t max_batch;        /* sequences the per-sequence outputs hold (indptr arrays hold max_batch + 1) */
+  uint32_t max_tokens;       /* entries of ids, positions and slot_mapping */
+  uint32_t max_blocks;       /* entries of kv_indices */
+  uint32_t batch;            /* out: sequences */
+  uint32_t tokens;           /* out: tokens */
+  uint32_t blocks;           /* out: kv_indices entries written */
+  uint32_t rows_written;     /* out: sampling rows written */
+  uint32_t reserved0;        /* 0 */
+  int32_t* q_indptr;         /* [batch + 1] */
+  int32_t* cu_seqlens;       /* [batch + 1] */
+  int32_t* kv_indptr;        /* [batch + 1] */
+  int32_t* kv_indices;       /* [blocks] */
+  int32_t* kv_last_page_len; /* [batch] */
+  int32_t* state_slots;      /* [batch] or NULL */
+  int32_t* ids;              /* [tokens] or NULL */
+  int32_t* positions;        /* [tokens] or NULL */
+  int64_t* slot_mapping;     /* [tokens] */
+  int32_t* rows;             /* [max_batch] or NULL */
+} RoostAmdStepTables;
+
+ROOST_API RoostStatus roost_amd_plan_region_from_step(const void* plan, uint64_t plan_bytes, RoostAmdStepTables* tables);
+
 #ifdef __cplusplus
 }
 #endif

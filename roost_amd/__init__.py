@@ -101,6 +101,8 @@ class KernelLibrary:
         self.dll.roost_amd_plan_region_fill.restype = C.c_int32
         self.dll.roost_amd_plan_region_run.argtypes = [C.c_void_p, C.POINTER(abi.PlanRegion), C.c_void_p]
         self.dll.roost_amd_plan_region_run.restype = C.c_int32
+        self.dll.roost_amd_plan_region_from_step.argtypes = [C.c_void_p, C.c_uint64, C.POINTER(abi.StepTables)]
+        self.dll.roost_amd_plan_region_from_step.restype = C.c_int32
         version = self.dll.roost_abi_version()
         if version >> 16 != abi.ABI_MAJOR or (version & 0xFFFF) < abi.ABI_MINOR:
             raise RuntimeError(f"{path}: ABI {version >> 16}.{version & 0xFFFF} is not {abi.ABI_MAJOR}.{abi.ABI_MINOR}")
@@ -521,3 +523,33 @@ def plan_region_run(session: OpSession, **kwargs) -> None:
     status = session.lib.dll.roost_amd_plan_region_run(session.ctx, C.byref(r), C.c_void_p(session.stream_handle))
     if status != abi.OK:
         raise KernelError("plan_region_run", status, session.lib.last_error())
+
+
+def plan_region_from_step(lib: KernelLibrary, plan, *, attention_group: int, block_size: int, max_batch: int,
+                          max_tokens: int, max_blocks: int) -> dict:
+    """roost_amd_plan_region_from_step over a C2 step-plan buffer (bytes or a uint8 numpy array). Returns the tables as
+    numpy arrays cut to what was written; raises KernelError on a refused plan."""
+    import numpy as np
+
+    buf = np.frombuffer(bytes(plan), dtype=np.uint8).copy() if not isinstance(plan, np.ndarray) else plan
+    out = {
+        "q_indptr": np.full(max_batch + 1, -7, np.int32), "cu_seqlens": np.full(max_batch + 1, -7, np.int32),
+        "kv_indptr": np.full(max_batch + 1, -7, np.int32), "kv_indices": np.full(max(max_blocks, 1), -7, np.int32),
+        "kv_last_page_len": np.full(max(max_batch, 1), -7, np.int32), "state_slots": np.full(max(max_batch, 1), -7, np.int32),
+        "ids": np.full(max(max_tokens, 1), -7, np.int32), "positions": np.full(max(max_tokens, 1), -7, np.int32),
+        "slot_mapping": np.full(max(max_tokens, 1), -7, np.int64), "rows": np.full(max(max_batch, 1), -7, np.int32),
+    }
+    t = abi.StepTables()
+    t.attention_group, t.block_size = attention_group, block_size
+    t.max_batch, t.max_tokens, t.max_blocks = max_batch, max_tokens, max_blocks
+    for name, a in out.items():
+        setattr(t, name, a.ctypes.data)
+    status = lib.dll.roost_amd_plan_region_from_step(C.c_void_p(buf.ctypes.data), buf.size, C.byref(t))
+    if status != abi.OK:
+        raise KernelError("plan_region_from_step", status, lib.last_error())
+    n, m, k, r = t.batch, t.tokens, t.blocks, t.rows_written
+    return {"q_indptr": out["q_indptr"][:n + 1], "cu_seqlens": out["cu_seqlens"][:n + 1],
+            "kv_indptr": out["kv_indptr"][:n + 1], "kv_indices": out["kv_indices"][:k],
+            "kv_last_page_len": out["kv_last_page_len"][:n], "state_slots": out["state_slots"][:n],
+            "ids": out["ids"][:m], "positions": out["positions"][:m], "slot_mapping": out["slot_mapping"][:m],
+            "rows": out["rows"][:r]}

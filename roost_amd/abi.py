@@ -179,6 +179,52 @@ class PlanRegion(C.Structure):
                                         "kv_last_page_len", "state_slots", "positions", "slot_mapping")]
 
 
+class StepTables(C.Structure):
+    """RoostAmdStepTables: the outputs of roost_amd_plan_region_from_step (host pointers)."""
+    _fields_ = [(name, C.c_uint32) for name in ("attention_group", "block_size", "max_batch", "max_tokens", "max_blocks",
+                                                "batch", "tokens", "blocks", "rows_written", "reserved0")] + [
+        (name, C.c_void_p) for name in ("q_indptr", "cu_seqlens", "kv_indptr", "kv_indices", "kv_last_page_len",
+                                        "state_slots", "ids", "positions", "slot_mapping", "rows")]
+
+
+# ---- The C2 step plan (reference kernels/include/roost_worker_shm.h:41-141), for building plan buffers ------------------
+
+class TableRef(C.Structure):
+    _fields_ = [("offset", C.c_uint64), ("count", C.c_uint32), ("stride", C.c_uint32)]
+
+
+class StepPlanHeader(C.Structure):
+    _fields_ = ([(n, C.c_uint32) for n in ("magic", "layout_version", "header_size", "flags")]
+                + [("step_id", C.c_uint64), ("total_bytes", C.c_uint64)]
+                + [(n, C.c_uint32) for n in ("shape_bucket", "math_mode", "sequence_count", "token_count", "group_count",
+                                             "rank", "mesh_id", "reserved0")]
+                + [(n, TableRef) for n in ("sequences", "token_ids", "positions", "group_blocks", "block_ids", "sampling",
+                                           "cache_ops", "embedding_inputs", "stop_token_ids", "spec_tree_parents",
+                                           "spec_tree_masks", "moe_expert_counts", "moe_expert_placement",
+                                           "kv_transfers", "head_rows", "encoder_outputs")]
+                + [(n, C.c_uint64) for n in ("reserved1", "reserved2", "input_step_id")])
+
+
+class PlanSequence(C.Structure):
+    _fields_ = ([("sequence_handle", C.c_uint64)]
+                + [(n, C.c_uint32) for n in ("token_start", "token_count", "position_offset", "group_blocks_start")]
+                + [(n, C.c_int32) for n in ("recurrent_slot", "lora_slot", "grammar_slot", "embedding_slot")]
+                + [(n, C.c_uint32) for n in ("sampling_index", "draft_count", "flags", "stop_start", "stop_count",
+                                             "max_new_tokens_left", "spec_tree_start", "spec_tree_count")]
+                + [(n, C.c_int32) for n in ("head_row", "encoder_output")])
+
+
+class PlanGroupBlocks(C.Structure):
+    _fields_ = [("block_start", C.c_uint32), ("block_count", C.c_uint32)]
+
+
+SHM_STRUCTS = {"RoostTableRef": TableRef, "RoostStepPlanHeader": StepPlanHeader, "RoostPlanSequence": PlanSequence,
+               "RoostPlanGroupBlocks": PlanGroupBlocks}
+SHM_MAGIC_PLAN = 0x4C505352  # "RSPL"
+SHM_LAYOUT_VERSION = 3
+SEQ_FLAG_PREFILL, SEQ_FLAG_SAMPLE = 0x1, 0x2
+
+
 ALL_STRUCTS = {
     "RoostDeviceSpan": DeviceSpan, "RoostWorkspaceSizes": WorkspaceSizes, "RoostWorkspace": Workspace,
     "RoostConstraints": Constraints, "RoostContextCreateParams": ContextCreateParams, "RoostOpEntry": OpEntry,

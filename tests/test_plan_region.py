@@ -1,6 +1,8 @@
 """The plan region (roost_amd_plan_region_fill on the host, roost_amd_plan_region_run on the GPU) against the reference's
 hand case (tests/Starlings.Roost.Worker.Tests/PlanAndResultTests.cs:25-45) and the restated PlanRegionWriter.Fill
 (src/Starlings.Roost.Worker/Eager/PlanRegionWriter.cs:19-64, oracle.plan_region), bit for bit."""
+from pathlib import Path
+
 import numpy as np
 import pytest
 
@@ -135,6 +137,172 @@ def test_host_fill_refusals_write_nothing(kernels, change):
     assert kernels.dll.roost_amd_plan_region_fill(C.byref(r)) == abi.INVALID_ARGUMENT
     assert kernels.last_error().startswith("plan_region: ")
     assert all((a == -7).all() for a in out.values())
+
+
+# ---- C2 step plans (roost_amd_plan_region_from_step) ------------------------------------------------------------------
+
+SHM_GOLDEN = Path(__file__).resolve().parent / "golden" / "shm_layout.golden.txt"
+
+
+def test_step_plan_layouts_match_reference_fixture():
+    """The ctypes mirrors the buffers below are built with have the reference's own layout (its fixture, kept as data);
+    plan_region.hip pins the same offsets with static_asserts."""
+    import ctypes as C
+
+    golden, cur = {}, None
+    for line in SHM_GOLDEN.read_text().splitlines():
+        if line.startswith("#") or not line.strip():
+            continue
+        if line.startswith("struct "):
+            _, cur, size, _align = line.split()
+            golden[cur] = {"size": int(size.split("=")[1]), "fields": []}
+            continue
+        name, off, size, _type = line.split()
+        golden[cur]["fields"].append((name, int(off), int(size)))
+    assert set(golden) == set(abi.SHM_STRUCTS)
+    for name, st in abi.SHM_STRUCTS.items():
+        assert C.sizeof(st) == golden[name]["size"], name
+        assert [(f[0], getattr(st, f[0]).offset, getattr(st, f[0]).size) for f in st._fields_] == golden[name]["fields"]
+
+
+def _step_plan(seqs, *, group_count=3, attention_group=1, sample=None, token_ids=None, seq_stride=80, extra_blocks=2,
+               gap=24):
+    """A C2 step-plan buffer: header, then the sequence, token-id, position, group-block and block-id tables (each
+    after `gap` bytes of 0xEE filler, the sequence table at `seq_stride` bytes per entry). Every sequence lists
+    `extra_blocks` blocks more than it needs in the attention group, and decoy lists in the other groups."""
+    import ctypes as C
+
+    b = len(seqs)
+    tokens = sum(s["token_count"] for s in seqs)
+    token_ids = np.arange(tokens, dtype=np.int32) * 7 + 3 if token_ids is None else token_ids
+    sample = [i % 2 == 0 for i in range(b)] if sample is None else sample
+    block_ids, groups = [], []
+    for i, s in enumerate(seqs):
+        for g in range(group_count):
+            if g == attention_group:
+                lst = list(s["blocks"]) + [900000 + i * 10 + j for j in range(extra_blocks)]
+            else:
+                lst = [800000 + i * 10 + g]
+            groups.append((len(block_ids), len(lst)))
+            block_ids += lst
+    parts, at = [], C.sizeof(abi.StepPlanHeader)
+
+    def place(raw):
+        nonlocal at
+        at += gap
+        parts.append((at, raw))
+        off = at
+        at += len(raw)
+        return off
+
+    seq_raw = bytearray()
+    for i, s in enumerate(seqs):
+        ps = abi.PlanSequence(sequence_handle=1000 + i, token_start=s["token_start"], token_count=s["token_count"],
+                              position_offset=s["position_offset"], group_blocks_start=i * group_count,
+                              recurrent_slot=5 * i + 2, lora_slot=-1, grammar_slot=-1, embedding_slot=-1,
+                              flags=abi.SEQ_FLAG_SAMPLE if sample[i] else 0, head_row=-1, encoder_output=-1)
+        seq_raw += bytes(ps) + b"\xEE" * (seq_stride - C.sizeof(ps))
+    positions = (np.concatenate([np.arange(s["token_count"]) + s["position_offset"] for s in seqs]).astype(np.int32)
+                 if b else np.zeros(0, np.int32))
+    gb_raw = b"".join(bytes(abi.PlanGroupBlocks(a, n)) for a, n in groups)
+    h = abi.StepPlanHeader(magic=abi.SHM_MAGIC_PLAN, layout_version=abi.SHM_LAYOUT_VERSION,
+                           header_size=C.sizeof(abi.StepPlanHeader), step_id=11, sequence_count=b, token_count=tokens,
+                           group_count=group_count)
+    h.sequences = abi.TableRef(place(bytes(seq_raw)), b, seq_stride)
+    h.token_ids = abi.TableRef(place(np.asarray(token_ids, np.int32).tobytes()), tokens, 4)
+    h.positions = abi.TableRef(place(positions.tobytes()), tokens, 4)
+    h.group_blocks = abi.TableRef(place(gb_raw), b * group_count, 8)
+    h.block_ids = abi.TableRef(place(np.asarray(block_ids, np.int32).tobytes()), len(block_ids), 4)
+    h.total_bytes = at
+    buf = bytearray(b"\xEE" * at)
+    buf[: C.sizeof(h)] = bytes(h)
+    for off, raw in parts:
+        buf[off:off + len(raw)] = raw
+    return np.frombuffer(bytes(buf), dtype=np.uint8).copy(), token_ids, sample
+
+
+def _from_step(kernels, buf, seqs, bs, **kw):
+    tokens = sum(s["token_count"] for s in seqs)
+    nblocks = sum(len(s["blocks"]) for s in seqs)
+    args = dict(attention_group=1, block_size=bs, max_batch=len(seqs), max_tokens=tokens, max_blocks=nblocks)
+    args.update(kw)
+    return roost_amd.plan_region_from_step(kernels, buf, **args)
+
+
+@pytest.mark.parametrize("name,q_lens,kv_lens,bs", PLANS, ids=[p[0] for p in PLANS])
+def test_step_plan_matches_plan_region_writer(kernels, name, q_lens, kv_lens, bs):
+    rng = np.random.default_rng(len(name) + 100)
+    q_lens, kv_lens = _plan_case(rng, q_lens, kv_lens)
+    seqs = _plan(rng, q_lens, kv_lens, bs)
+    buf, ids, sample = _step_plan(seqs, seq_stride=96 if bs == 7 else 80)
+    out = _from_step(kernels, buf, seqs, bs)
+    q_indptr, cu, kv_indptr, kv_indices, last, slots = oracle.plan_region(seqs, bs)
+    assert np.array_equal(out["q_indptr"], q_indptr) and np.array_equal(out["cu_seqlens"], cu)
+    assert np.array_equal(out["kv_indptr"], kv_indptr) and np.array_equal(out["kv_indices"], kv_indices)
+    assert np.array_equal(out["kv_last_page_len"], last) and np.array_equal(out["slot_mapping"], slots)
+    assert np.array_equal(out["positions"], np.concatenate([np.arange(s["token_count"]) + s["position_offset"]
+                                                            for s in seqs]))
+    assert np.array_equal(out["ids"], ids)
+    assert np.array_equal(out["state_slots"], [5 * i + 2 for i in range(len(seqs))])
+    want_rows = [s["token_start"] + s["token_count"] - 1 for s, smp in zip(seqs, sample) if smp]
+    assert list(out["rows"]) == want_rows
+
+
+def test_step_plan_reference_hand_case(kernels):
+    """PlanAndResultTests.cs:25-45's plan: a 3-token prefill from position 0 and a decode at position 17."""
+    buf, _, _ = _step_plan(HAND, sample=[False, True], token_ids=np.array([11, 12, 13, 14], np.int32))
+    out = _from_step(kernels, buf, HAND, 16)
+    assert list(out["slot_mapping"]) == [80, 81, 82, 7 * 16 + 1] and list(out["positions"]) == [0, 1, 2, 17]
+    assert list(out["kv_indptr"]) == [0, 1, 3] and list(out["kv_indices"]) == [5, 2, 7]
+    assert list(out["kv_last_page_len"]) == [3, 2] and list(out["ids"]) == [11, 12, 13, 14] and list(out["rows"]) == [3]
+
+
+def test_step_plan_empty(kernels):
+    buf, _, _ = _step_plan([])
+    out = roost_amd.plan_region_from_step(kernels, buf, attention_group=1, block_size=16, max_batch=0, max_tokens=0,
+                                          max_blocks=0)
+    assert list(out["q_indptr"]) == [0] and list(out["kv_indptr"]) == [0] and out["rows"].size == 0
+
+
+@pytest.mark.parametrize("change", ["magic", "short buffer", "table past the end", "tokens not contiguous",
+                                   "positions skip", "too few blocks", "group_blocks_start", "attention group",
+                                   "outputs too small", "token count"])
+def test_step_plan_refusals(kernels, change):
+    import ctypes as C
+
+    seqs = [dict(s, blocks=list(s["blocks"])) for s in HAND]
+    kw = dict(extra_blocks=0)
+    call = {}
+    buf, _, _ = _step_plan(seqs, **kw)
+    h = abi.StepPlanHeader.from_buffer_copy(bytes(buf[:C.sizeof(abi.StepPlanHeader)]))
+    seq_at = lambda i: int(h.sequences.offset) + i * int(h.sequences.stride)  # noqa: E731
+    if change == "magic":
+        buf[0] ^= 1
+    elif change == "short buffer":
+        buf = buf[:-1]
+    elif change == "table past the end":
+        h.block_ids.offset = h.total_bytes - 4
+        buf[:C.sizeof(h)] = np.frombuffer(bytes(h), np.uint8)
+    elif change == "tokens not contiguous":
+        buf[seq_at(1) + 8] += 1  # token_start 3 -> 4
+    elif change == "positions skip":
+        pos_at = int(h.positions.offset) + 4
+        buf[pos_at] += 1
+    elif change == "too few blocks":
+        seqs[1]["position_offset"] = 40  # 41 keys need 3 blocks of 16; 2 are listed
+        buf, _, _ = _step_plan(seqs, **kw)
+    elif change == "group_blocks_start":
+        buf[seq_at(1) + 20] += 1
+    elif change == "attention group":
+        call["attention_group"] = 3
+    elif change == "outputs too small":
+        call["max_tokens"] = 3
+    elif change == "token count":
+        h.token_count += 1
+        buf[:C.sizeof(h)] = np.frombuffer(bytes(h), np.uint8)
+    with pytest.raises(roost_amd.KernelError) as err:
+        _from_step(kernels, buf, HAND, 16, **call)
+    assert err.value.status == abi.INVALID_ARGUMENT and "plan_region: " in str(err.value)
 
 
 # ---- device path -------------------------------------------------------------------------------------------------------
