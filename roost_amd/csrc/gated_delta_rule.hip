@@ -498,6 +498,11 @@ __host__ __device__ constexpr int Pair(int r, int sp) { return r < 2 ? r : 2 * r
 __device__ __forceinline__ int Hsw(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 __device__ __forceinline__ int T16(int r, int c) { return r * 256 + 16 * (c ^ Hsw(r)); }
 
+// 16-byte piece c (0..3) of row r of a 64-byte-row tile (the v block and the output block) sits at piece c ^ ((r / 4) %
+// 4): rows r, r + 4, r + 8 and r + 12, which start on the same bank, then spread the transposed v reads and the 8-byte
+// output writes over all banks.
+__host__ __device__ __forceinline__ uint32_t VSw(uint32_t r, uint32_t c) { return c ^ ((r >> 2) & 3); }
+
 template <typename T>
 __device__ __forceinline__ T Lds(const uint8_t* base, int off) {
   return *reinterpret_cast<const T*>(base + off);
@@ -874,7 +879,7 @@ __device__ __forceinline__ CopyOffsets MakeCopyOffsets(const GdnArgs& a, uint32_
     o.q[j] = static_cast<uint32_t>(rr * a.q_stride * 2) + (h / a.group) * 256 + 16 * piece;
   }
   o.v = static_cast<uint32_t>((static_cast<uint32_t>(lane) >> 2) * a.v_stride * 2) + h * 256 + vb * 64 +
-        16 * (static_cast<uint32_t>(lane) & 3);
+        16 * VSw(static_cast<uint32_t>(lane) >> 2, static_cast<uint32_t>(lane) & 3);
   o.rec = 16 * static_cast<uint32_t>(lane);
   return o;
 }
@@ -909,7 +914,7 @@ __device__ __forceinline__ void Fetch(const GdnArgs& a, const CopyOffsets& co, c
       } else {
         const int row = 16 * i + (lane >> 2);
         const uint16_t* src = a.v + static_cast<uint64_t>(t0 + min(row, n - 1)) * a.v_stride + h * kDim + vb * 32 +
-                              8 * (lane & 3);
+                              8 * VSw(row, lane & 3);
         Copy16<kVec>(src, st.vt, l_vt, i, lane);
       }
     }
@@ -950,7 +955,7 @@ __device__ __forceinline__ void StoreOut(const GdnArgs& a, const Stage& st, int 
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int t = 16 * i + (lane >> 2);
-    const uint4 v = *reinterpret_cast<const uint4*>(st.ob + t * 64 + 16 * (lane & 3));
+    const uint4 v = *reinterpret_cast<const uint4*>(st.ob + t * 64 + 16 * VSw(t, lane & 3));
     if (t < n) {  // non-temporal: the outputs are not read here again, and kept out of L2 they leave the chain's
                   // shared k, q and record lines there (config 4: 0.167 against 0.176 ms)
       typedef uint32_t u32x4_nt __attribute__((ext_vector_type(4)));
@@ -999,7 +1004,8 @@ __device__ __forceinline__ void Advance(Stage& sg, f32x4_t (&st)[8], int w, int 
   for (int r = 0; r < 4; ++r) {
     xf[r] = *reinterpret_cast<const float4*>(sc + 16 * r + 4 * g);
     bf[r] = *reinterpret_cast<const float4*>(sc + 64 + 16 * r + 4 * g);
-    vr[r] = TrRead(sg.vt + (16 * r + 4 * g + (m >> 2)) * 64 + 32 * w + 8 * (m & 3));
+    vr[r] = TrRead(sg.vt + (16 * r + 4 * g + (m >> 2)) * 64 + 16 * VSw(16 * r + 4 * g + (m >> 2), 2 * w + ((m & 3) >> 1)) +
+                   8 * (m & 1));
   }
   uint4 th[kPairs], tl[kPairs];
 #pragma unroll
@@ -1108,7 +1114,7 @@ __device__ __forceinline__ void Advance(Stage& sg, f32x4_t (&st)[8], int w, int 
     f32x4_t o = oq[r] * of[r];
 #pragma unroll
     for (int sp = 0; sp <= r / 2; ++sp) o = Mfma(vb[sp], pa[Pair(r, sp)], o);
-    *reinterpret_cast<uint2*>(sg.ob + (16 * r + m) * 64 + 2 * (16 * w + 4 * g)) =
+    *reinterpret_cast<uint2*>(sg.ob + (16 * r + m) * 64 + 16 * VSw(16 * r + m, 2 * w + (g >> 1)) + 8 * (g & 1)) =
         make_uint2(PackRne(o[0], o[1]), PackRne(o[2], o[3]));
   }
 }
