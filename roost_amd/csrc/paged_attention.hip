@@ -136,6 +136,8 @@ struct PlanRecord {
   uint32_t kv_heads;
   int32_t window;        // WindowOf(params): the pieces start at the window
   uint32_t merges_two;   // prefill: the leading merge entries of exactly two pieces
+  uint32_t overlap;      // prefill with single-token sequences: tile and decode kernels run side by side
+  uint32_t reserved1;
   uint64_t pages;        // kv_indptr_host[batch]
   uint64_t work_items;   // decode pieces or prefill tiles
   uint64_t ranges;       // decode: workgroup ranges over the pieces
@@ -157,6 +159,7 @@ struct Layout {
   uint64_t ranges = 0;
   uint64_t merges = 0;
   uint64_t merges_two = 0;  // prefill: leading merge entries of two pieces
+  uint32_t overlap = 0;     // prefill: tile and decode kernels on two streams (ChooseOverlap)
   uint64_t range_offset = 0;
   uint64_t merge_offset = 0;
   uint64_t counter_offset = 0;
@@ -508,6 +511,65 @@ int64_t PrefillPieceTiles(const Items& items, int64_t total_tiles, uint32_t cus)
   return best;
 }
 
+// Side by side or one after the other. A prefill call that also holds single-token sequences (a mixed worker step)
+// runs MFMA-bound tile kernels and HBM-bound decode kernels. A tile workgroup needs a whole CU (two 256-register
+// wavefronts per SIMD and 128 KB of LDS), so the two kinds cannot share CUs; but when the tile kernel is cut into fewer,
+// longer pieces it holds only as many CUs as it has pieces, and the decode kernel, launched right after it on a second
+// stream with its ranges sized for the remaining CUs, streams K/V on those. ChooseOverlap estimates both schedules with
+// rates measured on the MI355X -- a 64-key tile at head dim 256 takes ~3.7 us of a CU (less at smaller head dims), the
+// decode stream reaches 5.6 TB/s on 256 CUs and falls off as (CUs / 256)^0.26 (5.2 TB/s on 192), and a fork and join
+// cost ~18 us -- and keeps the cheaper. Config 5 (48 decode rows over 831 MB of K/V, two 512-token chunks): 64 pieces
+// of 36 tiles beside decode ranges for 192 CUs, 183 against 211 us one after the other.
+struct OverlapChoice {
+  bool use = false;
+  int64_t target = 0;    // piece size (tiles) of the tile kernel
+  uint32_t dec_cus = 0;  // CUs the decode ranges are sized for
+};
+
+constexpr double kTileUsD256 = 3.7;
+constexpr double kDecodeBytesPerUs = 5.6e6;
+constexpr double kForkJoinUs = 18.0;
+
+double TileUs(uint32_t head_dim) { return kTileUsD256 * (0.25 + 0.75 * head_dim / 256.0); }
+double DecodeUs(double bytes, uint32_t cus_used, uint32_t cus) {
+  return bytes / (kDecodeBytesPerUs * std::pow(static_cast<double>(cus_used) / cus, 0.26));
+}
+
+template <typename Items, typename Single>
+OverlapChoice ChooseOverlap(const RoostPagedAttentionParams& p, const Items& items, int64_t serial_target, uint32_t cus,
+                            Single single) {
+  OverlapChoice best;
+  double dec_bytes = 0.0;
+  for (uint32_t b = 0; b < p.batch; ++b) {
+    if (single(b)) dec_bytes += static_cast<double>(KvLenHost(p, b)) * VirtualHeads(p) * p.head_dim * 2.0 * 2.0;
+  }
+  if (dec_bytes == 0.0 || items.empty() || cus < 2) return best;
+  int64_t longest = 0;
+  for (const auto& it : items) longest = std::max(longest, ItemTiles(it.w));
+  const double tile_us = TileUs(p.head_dim);
+  double best_us = PrefillMakespan(items, serial_target, cus) * tile_us + DecodeUs(dec_bytes, cus, cus);
+  for (int64_t k = 1; k <= 16; ++k) {
+    const int64_t target = std::max<int64_t>(1, roost::CeilDiv(longest, k));
+    int64_t pieces = 0, piece_max = 0;
+    for (const auto& it : items) {
+      const int64_t tiles = ItemTiles(it.w), n = Pieces(tiles, target);
+      pieces += n;
+      piece_max = std::max<int64_t>(piece_max, roost::CeilDiv(tiles, n));
+    }
+    if (pieces >= static_cast<int64_t>(cus)) break;
+    const uint32_t left = cus - static_cast<uint32_t>(pieces);
+    const double us = std::max(static_cast<double>(piece_max + kPfPieceCost) * tile_us, DecodeUs(dec_bytes, left, cus)) +
+                      kForkJoinUs;
+    if (us < best_us) {
+      best_us = us;
+      best.use = true;
+      best.target = target;
+      best.dec_cus = left;
+    }
+  }
+  return best;
+}
+
 Layout PlanPrefill(const RoostPagedAttentionParams& p, uint32_t cus, unsigned char* host) {
   const bool fast = PrefillFastPath(p);
   const int64_t tile_q = fast ? kPfTokens : kPrefillTileQ;
@@ -545,8 +607,11 @@ Layout PlanPrefill(const RoostPagedAttentionParams& p, uint32_t cus, unsigned ch
   }
   std::vector<PrefillMerge> merges;
   int32_t slot = 0;
+  OverlapChoice overlap;
   if (fast) {
-    const int64_t target = PrefillPieceTiles(items, total_tiles, cus);
+    int64_t target = PrefillPieceTiles(items, total_tiles, cus);
+    overlap = ChooseOverlap(p, items, target, cus, single);
+    if (overlap.use) target = overlap.target;
     std::vector<Item> cut;
     cut.reserve(items.size());
     for (const Item& it : items) {
@@ -582,7 +647,8 @@ Layout PlanPrefill(const RoostPagedAttentionParams& p, uint32_t cus, unsigned ch
     std::memcpy(host + l.merge_offset, merges.data(), merges.size() * sizeof(PrefillMerge));
   }
   const uint64_t prefill_floats = l.float_bytes;
-  AppendDecode(p, BuildDecode(p, cus, single), l, host);
+  l.overlap = overlap.use ? 1u : 0u;
+  AppendDecode(p, BuildDecode(p, overlap.use ? overlap.dec_cus : cus, single), l, host);
   PlaceFloats(p, prefill_floats, l);
   return l;
 }
@@ -2045,6 +2111,7 @@ PlanRecord MakeRecord(const RoostPagedAttentionParams& p, const Layout& l) {
   r.kv_heads = p.kv_heads;
   r.window = WindowOf(p);
   r.merges_two = static_cast<uint32_t>(l.merges_two);
+  r.overlap = l.overlap;
   r.pages = static_cast<uint64_t>(p.kv_indptr_host[p.batch]);
   r.work_items = l.work_items;
   r.ranges = l.ranges;
@@ -2128,8 +2195,8 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_plan(RoostContext* ctx, c
   });
 }
 
-extern "C" ROOST_API RoostStatus roost_paged_attention_run(RoostContext*, const void* params, const RoostWorkspace* ws,
-                                                           void* stream) {
+extern "C" ROOST_API RoostStatus roost_paged_attention_run(RoostContext* ctx, const void* params,
+                                                           const RoostWorkspace* ws, void* stream) {
   using namespace roost;
   Gate gate(kOp);
   ROOST_GATE_RETURN(gate.Header(params, sizeof(RoostPagedAttentionParams)));
@@ -2184,13 +2251,23 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_run(RoostContext*, const 
       }
     }
     // The multi-token sequences on the tile kernels, then the single-token ones on the decode kernels (bf16 in prefill
-    // mode, at the call's head dim). Running the two side by side on two streams gains nothing: a tile workgroup needs
-    // two 256-register wavefronts per SIMD, so it cannot share a CU with resident decode workgroups.
+    // mode, at the call's head dim). When the plan chose to overlap them (ChooseOverlap), the decode kernels run on
+    // the context's side stream, forked after the caller's earlier work and joined back before returning; the tile
+    // kernel is issued first so that its workgroups hold their CUs before the decode ranges fill the rest.
+    const bool side = rec.overlap != 0 && ctx != nullptr && ctx->side != nullptr;
+    hipStream_t ds = side ? ctx->side : s;
+    if (side) ROOST_RETURN_IF_FAILED(HipStatus(hipEventRecord(ctx->fork, s), kOp, "fork event"));
     ROOST_RETURN_IF_FAILED(LaunchPrefill(p, rec, dev, kv, scale_log2, s));
+    if (side) ROOST_RETURN_IF_FAILED(HipStatus(hipStreamWaitEvent(ds, ctx->fork, 0), kOp, "fork wait"));
+    RoostStatus st;
     switch (p.head_dim) {
-      case 64: return LaunchDecode<uint16_t, 64>(p, rec, dev, kv, scale_log2, s);
-      case 128: return LaunchDecode<uint16_t, 128>(p, rec, dev, kv, scale_log2, s);
-      default: return LaunchDecode<uint16_t, 256>(p, rec, dev, kv, scale_log2, s);
+      case 64: st = LaunchDecode<uint16_t, 64>(p, rec, dev, kv, scale_log2, ds); break;
+      case 128: st = LaunchDecode<uint16_t, 128>(p, rec, dev, kv, scale_log2, ds); break;
+      default: st = LaunchDecode<uint16_t, 256>(p, rec, dev, kv, scale_log2, ds); break;
     }
+    ROOST_RETURN_IF_FAILED(st);
+    if (!side) return ROOST_STATUS_OK;
+    ROOST_RETURN_IF_FAILED(HipStatus(hipEventRecord(ctx->join, ds), kOp, "join event"));
+    return HipStatus(hipStreamWaitEvent(s, ctx->join, 0), kOp, "join wait");
   });
 }
