@@ -83,17 +83,20 @@ __device__ __forceinline__ float Capped(float y, SoftCap c) {
   return c.capl - 2.0f * c.capl * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(y * c.k));
 }
 
+// A decode row is one query token: the last token of its sequence (q_back 0: decode calls and the single-token
+// sequences of a prefill call) or, in an f32 prefill, any token, q_back tokens before the sequence's last.
 struct DecodeWork {
   int32_t seq;
   int32_t token_begin;  // first key of this piece (a multiple of 16)
   int32_t token_end;    // one past its last key
-  int32_t slot;         // partial slot, or -1 when the piece is the whole sequence (written as the final row)
+  int32_t slot;         // partial slot, or -1 when the piece is the whole row (written as the final row)
+  int32_t q_back;       // the row's query token sits q_back tokens before its sequence's last token
 };
 struct DecodeMerge {
   int32_t seq;
-  int32_t first;  // first partial slot; the sequence's pieces own slots first .. first + count - 1 in key order
+  int32_t first;  // first partial slot; the row's pieces own slots first .. first + count - 1 in key order
   int32_t count;
-  int32_t reserved;
+  int32_t q_back;
 };
 // A prefill work item: query tokens q0 .. q0 + rows - 1 of sequence seq (all kGroup query heads of one KV head)
 // against keys [kbeg, kend). slot >= 0 marks one piece of a split key range: it writes partials (its output divided
@@ -187,7 +190,8 @@ uint32_t HeadShift(const RoostPagedAttentionParams& p) {
 // Shapes with a kernel here, per mode: head dims 64/128/256 decode; prefill on the tile kernel at 64, 128 and 256
 // (64 and 128 need page sizes that are powers of two and multiples of 16), on the general kernel at 256.
 bool PrefillShapeBuilt(const RoostPagedAttentionParams& p) {
-  if (p.head_dim == 256) return true;
+  // f32 prefills run on the decode kernels (any page size); bf16 ones on the tile kernels.
+  if (p.head_dim == 256 || p.q.dtype == ROOST_DTYPE_F32) return true;
   return (p.head_dim == 128 || p.head_dim == 64) && p.page_size % 16 == 0 && roost::IsPow2(p.page_size);
 }
 
@@ -231,7 +235,7 @@ RoostStatus Admit(const RoostPagedAttentionParams& p, bool for_run) {
       .Expect(p.head_dim == 64 || p.head_dim == 128 || p.head_dim == 256, ROOST_STATUS_UNSUPPORTED,
               "head_dim = %u has no kernel here (built: 64, 128, 256)", p.head_dim)
       .Expect(!prefill || PrefillShapeBuilt(p), ROOST_STATUS_UNSUPPORTED,
-              "prefill at head_dim = %u, page_size = %u has no kernel here (built: 256 at any page size; 64 and 128 "
+              "bf16 prefill at head_dim = %u, page_size = %u has no kernel here (built: 256 at any page size; 64 and 128 "
               "at power-of-two page sizes that are multiples of 16)", p.head_dim, p.page_size)
       .Expect(p.kv_heads > 0 && p.q_heads % p.kv_heads == 0 && GroupBuilt(p.q_heads / std::max(p.kv_heads, 1u)),
               ROOST_STATUS_UNSUPPORTED, "q_heads = %u over kv_heads = %u: built for groups of 4, 8, 16 or 32 query "
@@ -253,9 +257,7 @@ RoostStatus Admit(const RoostPagedAttentionParams& p, bool for_run) {
   }
   const uint32_t dt = p.q.dtype;
   gate.Expect(dt == ROOST_DTYPE_BF16 || dt == ROOST_DTYPE_F32, ROOST_STATUS_INVALID_ARGUMENT,
-              "q is %s; attention reads bf16 (or f32 in decode)", roost::Describe(dt).name)
-      .Expect(dt == ROOST_DTYPE_BF16 || !prefill, ROOST_STATUS_UNSUPPORTED,
-              "an f32 prefill has no kernel here (prefill runs on bf16 MFMA)");
+              "q is %s; attention reads bf16 or f32", roost::Describe(dt).name);
   ROOST_GATE_RETURN(gate);
   const uint64_t q_elems = static_cast<uint64_t>(p.tokens) * p.q_heads * p.head_dim;
   const uint64_t page_elems = static_cast<uint64_t>(p.page_size) * p.kv_heads * p.head_dim;
@@ -336,63 +338,103 @@ struct DecodePlan {
   uint64_t ranges() const { return range_ptr.empty() ? 0 : range_ptr.size() - 1; }
 };
 
-// Plans the sequences b with take(b) (all of them in a decode call, the single-token ones in a prefill call).
-template <typename Take>
-DecodePlan BuildDecode(const RoostPagedAttentionParams& p, uint32_t cus, Take take) {
+// One decode row: query token q_back tokens before the last of sequence seq, reading keys [first, end) (host lengths;
+// the kernel clamps to the device's).
+struct DecodeRow {
+  uint32_t seq;
+  int32_t q_back;
+  int64_t first;
+  int64_t end;
+};
+
+// Cuts the rows' keys into 16-token groups and the groups into ranges of about equal length, one range per workgroup
+// slot (kDecodeWgsPerCu per CU); a row cut across ranges gets partial slots and a DecodeMerge entry.
+DecodePlan BuildDecodeRows(const RoostPagedAttentionParams& p, uint32_t cus, const std::vector<DecodeRow>& rows) {
   DecodePlan d;
-  std::vector<uint64_t> groups(p.batch, 0), first_group(p.batch, 0);
-  uint64_t total = 0, planned = 0;
-  const int32_t window = WindowOf(p);
-  for (uint32_t b = 0; b < p.batch; ++b) {
-    if (!take(b)) continue;
-    const uint32_t kv = KvLenHost(p, b);
+  if (rows.empty()) return d;
+  std::vector<uint64_t> groups(rows.size()), first_group(rows.size());
+  uint64_t total = 0;
+  for (size_t r = 0; r < rows.size(); ++r) {
     // Keys before the window are never read (their pages may have been released); the first group keeps its
     // 16-alignment and the kernel masks its keys below the window.
-    first_group[b] = static_cast<uint64_t>(DecodeFirstKey(kv, window)) / 16;
-    groups[b] = roost::CeilDiv(kv, 16) - first_group[b];
-    total += groups[b];
-    ++planned;
+    first_group[r] = static_cast<uint64_t>(rows[r].first) / 16;
+    groups[r] = rows[r].end > rows[r].first ? roost::CeilDiv(static_cast<uint64_t>(rows[r].end), 16) - first_group[r] : 0;
+    total += groups[r];
   }
-  if (planned == 0) return d;
   const uint64_t slots_wanted = std::max<uint64_t>(
       1, static_cast<uint64_t>(cus) * kDecodeWgsPerCu / (VirtualHeads(p) / HeadsPerWorkgroup(VirtualHeads(p))));
   const uint64_t ranges = std::max<uint64_t>(1, std::min<uint64_t>(slots_wanted, total));
   uint64_t per_range = std::max<uint64_t>(1, roost::CeilDiv(total, ranges));
-  // A sequence spans at most ceil(groups / per_range) + 1 pieces; keep that within what the merge kernel combines.
+  // A row spans at most ceil(groups / per_range) + 1 pieces; keep that within what the merge kernel combines.
   const uint64_t longest = *std::max_element(groups.begin(), groups.end());
   per_range = std::max<uint64_t>(per_range, roost::CeilDiv(longest, kMaxMergeSplits - 2));
-  d.items.reserve(planned + ranges * 2);
+  d.items.reserve(rows.size() + ranges * 2);
   d.range_ptr.reserve(ranges + 1);
   d.range_ptr.push_back(0);
   uint64_t room = per_range;  // groups left in the current range
-  for (uint32_t b = 0; b < p.batch; ++b) {
-    if (!take(b)) continue;
-    const uint32_t kv = KvLenHost(p, b);
-    if (groups[b] == 0) {
-      d.items.push_back(DecodeWork{static_cast<int32_t>(b), 0, 0, -1});
+  for (size_t r = 0; r < rows.size(); ++r) {
+    const auto seq = static_cast<int32_t>(rows[r].seq);
+    const int32_t back = rows[r].q_back;
+    if (groups[r] == 0) {
+      d.items.push_back(DecodeWork{seq, 0, 0, -1, back});
       continue;
     }
     const size_t first_item = d.items.size();
     uint64_t g = 0;
-    while (g < groups[b]) {
+    while (g < groups[r]) {
       if (room == 0) {
         d.range_ptr.push_back(static_cast<int32_t>(d.items.size()));
         room = per_range;
       }
-      const uint64_t n = std::min(room, groups[b] - g);
-      d.items.push_back(DecodeWork{static_cast<int32_t>(b), static_cast<int32_t>((first_group[b] + g) * 16),
-                                   static_cast<int32_t>(std::min<uint64_t>((first_group[b] + g + n) * 16, kv)), -1});
+      const uint64_t n = std::min(room, groups[r] - g);
+      d.items.push_back(DecodeWork{seq, static_cast<int32_t>((first_group[r] + g) * 16),
+                                   static_cast<int32_t>(std::min<uint64_t>((first_group[r] + g + n) * 16,
+                                                                           static_cast<uint64_t>(rows[r].end))),
+                                   -1, back});
       g += n;
       room -= n;
     }
     const size_t pieces = d.items.size() - first_item;
     if (pieces > 1) {
-      d.merges.push_back(DecodeMerge{static_cast<int32_t>(b), d.slots, static_cast<int32_t>(pieces), 0});
+      d.merges.push_back(DecodeMerge{seq, d.slots, static_cast<int32_t>(pieces), back});
       for (size_t i = first_item; i < d.items.size(); ++i) d.items[i].slot = d.slots++;
     }
   }
   d.range_ptr.push_back(static_cast<int32_t>(d.items.size()));
   return d;
+}
+
+// The last-token rows of the sequences b with take(b) (all of them in a decode call, the single-token ones in a
+// prefill call).
+template <typename Take>
+DecodePlan BuildDecode(const RoostPagedAttentionParams& p, uint32_t cus, Take take) {
+  std::vector<DecodeRow> rows;
+  const int32_t window = WindowOf(p);
+  for (uint32_t b = 0; b < p.batch; ++b) {
+    if (!take(b)) continue;
+    const int64_t kv = KvLenHost(p, b);
+    rows.push_back(DecodeRow{b, 0, DecodeFirstKey(kv, window), kv});
+  }
+  return BuildDecodeRows(p, cus, rows);
+}
+
+// Every query token of every sequence as its own row (the f32 prefill, which runs on the VALU decode kernel): token i
+// of a sequence of n tokens and kv keys sits at position kv - n + i and reads keys from its window start to itself
+// (causal) or to the end.
+DecodePlan BuildDecodeAllTokens(const RoostPagedAttentionParams& p, uint32_t cus) {
+  std::vector<DecodeRow> rows;
+  const int32_t window = WindowOf(p);
+  for (uint32_t b = 0; b < p.batch; ++b) {
+    const int64_t n = p.q_indptr_host[b + 1] - p.q_indptr_host[b];
+    const int64_t kv = KvLenHost(p, b);
+    for (int64_t i = 0; i < n; ++i) {
+      const int64_t pos = kv - n + i;
+      const int64_t end = p.causal ? std::max<int64_t>(0, pos + 1) : kv;
+      const int64_t first = window < 0 ? 0 : std::max<int64_t>(0, pos - window);
+      rows.push_back(DecodeRow{b, static_cast<int32_t>(n - 1 - i), std::min(first, end), end});
+    }
+  }
+  return BuildDecodeRows(p, cus, rows);
 }
 
 // Places a decode plan at the end of the int region [0, l.int_bytes) and its partials at the end of the float region
@@ -571,6 +613,12 @@ OverlapChoice ChooseOverlap(const RoostPagedAttentionParams& p, const Items& ite
 }
 
 Layout PlanPrefill(const RoostPagedAttentionParams& p, uint32_t cus, unsigned char* host) {
+  if (p.q.dtype == ROOST_DTYPE_F32) {  // no f32 MFMA tile kernel: every query token is a row of the f32 decode kernel
+    Layout l = MakeLayout(0, 0, 0, 0, kPfRows, p.head_dim, ROOST_ATTENTION_PREFILL);
+    AppendDecode(p, BuildDecodeAllTokens(p, cus), l, host);
+    PlaceFloats(p, 0, l);
+    return l;
+  }
   const bool fast = PrefillFastPath(p);
   const int64_t tile_q = fast ? kPfTokens : kPrefillTileQ;
   struct Item {
@@ -1046,7 +1094,7 @@ __global__ void __launch_bounds__(256, ROOST_DECODE_WGS_PER_CU) DecodeKernel(con
                                                     float* __restrict__ part_o, float* __restrict__ part_ml,
                                                     const int32_t* __restrict__ q_rows,
                                                     uint32_t q_heads, uint32_t heads_per_wg, float scale_log2,
-                                                    int32_t window, SoftCap cap) {
+                                                    int32_t window, uint32_t causal, SoftCap cap) {
   using C = DecodeCfg<T, D>;
   constexpr int kVec = C::kVec, kLpr = C::kLpr, kTpi = C::kTpi, kNi = C::kNi;
   constexpr bool kMfma = sizeof(T) == 2;  // bf16: q.k on MFMA; f32: the VALU reduce-scatter path
@@ -1077,13 +1125,19 @@ __global__ void __launch_bounds__(256, ROOST_DECODE_WGS_PER_CU) DecodeKernel(con
   const DecodeWork wk = work[it];
   int32_t p0 = 0;
   const uint32_t kv_len = SeqKvLen(kv, wk.seq, &p0);
-  // The sequence's query token: its index in a decode call, q_indptr[seq] for a single-token sequence of a prefill call.
-  const uint64_t tok = q_rows != nullptr ? static_cast<uint64_t>(q_rows[wk.seq]) : static_cast<uint64_t>(wk.seq);
+  // The row's query token: its sequence's index in a decode call; in a prefill call q_back tokens before the
+  // sequence's last, q_indptr[seq + 1] - 1 (the last token; the only one of a single-token sequence).
+  // (Clamped into the sequence's own rows, so that device tables that disagree with the plan cannot move it outside.)
+  const uint64_t tok = q_rows != nullptr
+                           ? static_cast<uint64_t>(max(q_rows[wk.seq], q_rows[wk.seq + 1] - 1 - wk.q_back))
+                           : static_cast<uint64_t>(wk.seq);
+  // The query's position; it sees keys up to itself (causal) or all of them, and from its window start on.
+  const int32_t qpos = static_cast<int32_t>(kv_len) - 1 - wk.q_back;
   const uint32_t t_begin = static_cast<uint32_t>(wk.token_begin);
-  const uint32_t t_end = min(kv_len, static_cast<uint32_t>(wk.token_end));
-  // The sliding window's first visible key (the query sits at position kv_len - 1); the piece may start up to 15
-  // keys before it, which are masked.
-  const uint32_t lo = window < 0 || kv_len == 0 ? 0u : static_cast<uint32_t>(max(0, static_cast<int32_t>(kv_len) - 1 - window));
+  uint32_t t_end = min(kv_len, static_cast<uint32_t>(wk.token_end));
+  if (causal) t_end = min(t_end, static_cast<uint32_t>(max(0, qpos + 1)));
+  // The sliding window's first visible key; the piece may start up to 15 keys before it, which are masked.
+  const uint32_t lo = window < 0 || kv_len == 0 ? 0u : static_cast<uint32_t>(max(0, qpos - window));
 
   using QW = typename std::conditional<sizeof(T) == 2, uint32_t, float>::type;
   QW qr[kGroup][C::kQWords];   // VALU path (f32)
@@ -1276,7 +1330,9 @@ __global__ void __launch_bounds__(D) DecodeMergeKernel(T* __restrict__ out, floa
   __shared__ float f_lds[kMaxMergeSplits];
   __shared__ float inv_lds;
   const DecodeMerge mg = merges[blockIdx.x / q_heads];
-  const uint64_t tok = q_rows != nullptr ? static_cast<uint64_t>(q_rows[mg.seq]) : static_cast<uint64_t>(mg.seq);
+  const uint64_t tok = q_rows != nullptr
+                           ? static_cast<uint64_t>(max(q_rows[mg.seq], q_rows[mg.seq + 1] - 1 - mg.q_back))
+                           : static_cast<uint64_t>(mg.seq);
   const uint32_t qh = blockIdx.x % q_heads;
   const int n = min(mg.count, static_cast<int32_t>(kMaxMergeSplits));
   const uint64_t base = static_cast<uint64_t>(mg.first) * q_heads + qh;  // partial row of piece c: base + c * q_heads
@@ -2010,11 +2066,11 @@ RoostStatus LaunchDecode(const RoostPagedAttentionParams& p, const PlanRecord& r
   if (p.page_size % 16 == 0) {
     hipLaunchKernelGGL((DecodeKernel<T, D, true>), grid, dim3(256), 0, stream, static_cast<const T*>(p.q.address), out,
                        lse, kv, kv.kv_indices, items, range_ptr, part_o, part_ml, q_rows, p.q_heads, hpw, scale_log2,
-                       WindowOf(p), CapOf(p));
+                       WindowOf(p), p.causal, CapOf(p));
   } else {
     hipLaunchKernelGGL((DecodeKernel<T, D, false>), grid, dim3(256), 0, stream, static_cast<const T*>(p.q.address), out,
                        lse, kv, kv.kv_indices, items, range_ptr, part_o, part_ml, q_rows, p.q_heads, hpw, scale_log2,
-                       WindowOf(p), CapOf(p));
+                       WindowOf(p), p.causal, CapOf(p));
   }
   ROOST_RETURN_IF_FAILED(roost::HipStatus(hipGetLastError(), "paged_attention", "decode launch"));
   if (rec.dec_merges == 0) return ROOST_STATUS_OK;
@@ -2254,6 +2310,13 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_run(RoostContext* ctx, co
     // mode, at the call's head dim). When the plan chose to overlap them (ChooseOverlap), the decode kernels run on
     // the context's side stream, forked after the caller's earlier work and joined back before returning; the tile
     // kernel is issued first so that its workgroups hold their CUs before the decode ranges fill the rest.
+    if (p.q.dtype == ROOST_DTYPE_F32) {  // every query token is a row of the f32 decode kernel
+      switch (p.head_dim) {
+        case 64: return LaunchDecode<float, 64>(p, rec, dev, kv, scale_log2, s);
+        case 128: return LaunchDecode<float, 128>(p, rec, dev, kv, scale_log2, s);
+        default: return LaunchDecode<float, 256>(p, rec, dev, kv, scale_log2, s);
+      }
+    }
     const bool side = rec.overlap != 0 && ctx != nullptr && ctx->side != nullptr;
     hipStream_t ds = side ? ctx->side : s;
     if (side) ROOST_RETURN_IF_FAILED(HipStatus(hipEventRecord(ctx->fork, s), kOp, "fork event"));

@@ -574,6 +574,7 @@ SOFTCAP_CASES = [
     ("prefill hd128 non-causal", [(40, 300)], 16, False, False, 128, True, 2.0),
     ("prefill ps8 general", [(100, 300)], 8, False, True, 256, True, 5.0),
     ("mixed step", [(1, 900), (200, 1200), (1, 3000), (64, 64)], 16, False, True, 256, True, 30.0),
+    ("prefill f32 hd128", [(30, 200), (1, 50)], 16, False, True, 128, False, 4.0),
 ]
 
 
@@ -597,3 +598,28 @@ def test_logit_soft_cap(session, name, seqs, ps, hnd, causal, d, bf16, cap):
     # The cap changes the result (the case exercises it).
     uncapped = cases.values(cases.oracle_attention(b, causal), b.bf16)
     assert np.abs(uncapped - ref).max() > 1e-2
+
+
+# ---- f32 prefill (CpuOps.cs:198-298 computes in any dtype; the reference GPU library refuses it) ----------------------
+#
+# No f32 MFMA tile kernel: every query token becomes a row of the f32 decode kernel (its position, causal end and
+# window start), rows longer than a range are split and merged like decode rows. Checked against CpuOps at f32's own
+# accuracy (fp32 accumulation against the oracle's double).
+
+F32_PREFILL_CASES = [
+    ("causal hd256 mixed lengths", [(37, 300), (1, 90), (64, 64)], 16, False, True, -1, 256),
+    ("non-causal hd128 HND", [(20, 180), (5, 33)], 16, True, False, -1, 128),
+    ("window hd64 page size 7", [(50, 400), (1, 77)], 7, False, True, 100, 64),
+    ("non-causal window hd256 ps32", [(30, 500)], 32, False, False, 64, 256),
+    ("long rows split and merged", [(6, 9000), (3, 40)], 16, False, True, -1, 256),
+]
+
+
+@pytest.mark.parametrize("name,seqs,ps,hnd,causal,window,d", F32_PREFILL_CASES, ids=[c[0] for c in F32_PREFILL_CASES])
+def test_prefill_f32_matches_cpuops(session, name, seqs, ps, hnd, causal, window, d):
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    b = cases.make_paged_batch(rng, [s[1] for s in seqs], [s[0] for s in seqs], page_size=ps, hnd=hnd, d=d,
+                               bf16=False)
+    got = run_case(session, b, causal, window_left=window)
+    ref = cases.values(cases.oracle_attention(b, causal, window_left=window), False)
+    np.testing.assert_allclose(got, ref, rtol=2e-5, atol=2e-5)
