@@ -1983,12 +1983,10 @@ __device__ __forceinline__ void MergeAdd(float4& acc, u32x2_t raw, float f) {
 }
 
 template <int D, int kRows>
-__global__ void __launch_bounds__(256)
-    PrefillMergeKernel(uint16_t* __restrict__ out, float* __restrict__ lse, const PrefillMerge* __restrict__ merges,
-                       const uint16_t* __restrict__ part_o, const float* __restrict__ part_ml,
-                       const int32_t* __restrict__ q_indptr, uint32_t q_heads) {
-  const PrefillMerge mg = merges[blockIdx.x];
-  const int r0 = static_cast<int>(blockIdx.y) * kRows;
+__device__ __forceinline__ void PrefillMergeRows(uint16_t* __restrict__ out, float* __restrict__ lse,
+                                                 const PrefillMerge& mg, int r0, const uint16_t* __restrict__ part_o,
+                                                 const float* __restrict__ part_ml,
+                                                 const int32_t* __restrict__ q_indptr, uint32_t q_heads) {
   if (r0 >= mg.rows) return;
   const int hq = threadIdx.x / (D / 4);
   const int d = 4 * (threadIdx.x % (D / 4));
@@ -2044,6 +2042,25 @@ __global__ void __launch_bounds__(256)
       }
     }
     MergeWrite<D>(out, lse, tok0 + r0, q_heads, head, d, acc, l, mx);
+  }
+}
+
+// One launch for both forms: the first `two` merges (exactly two pieces) as blocks of kPfMergeRows token rows, the
+// rest one token row per block (two merge launches one after the other cost a second launch's latency).
+template <int D>
+__global__ void __launch_bounds__(256)
+    PrefillMergeKernel(uint16_t* __restrict__ out, float* __restrict__ lse, const PrefillMerge* __restrict__ merges,
+                       const uint16_t* __restrict__ part_o, const float* __restrict__ part_ml,
+                       const int32_t* __restrict__ q_indptr, uint32_t q_heads, uint32_t two) {
+  constexpr uint32_t kTwoBlocks = kPfTokens / kPfMergeRows;  // blocks per two-piece merge
+  const uint32_t b = blockIdx.x;
+  if (b < two * kTwoBlocks) {
+    PrefillMergeRows<D, kPfMergeRows>(out, lse, merges[b / kTwoBlocks], static_cast<int>(b % kTwoBlocks) * kPfMergeRows,
+                                      part_o, part_ml, q_indptr, q_heads);
+  } else {
+    const uint32_t k = b - two * kTwoBlocks;
+    PrefillMergeRows<D, 1>(out, lse, merges[two + k / kPfTokens], static_cast<int>(k % kPfTokens), part_o, part_ml,
+                           q_indptr, q_heads);
   }
 }
 
@@ -2113,31 +2130,16 @@ RoostStatus LaunchPrefill(const RoostPagedAttentionParams& p, const PlanRecord& 
     const auto* mg = reinterpret_cast<const PrefillMerge*>(dev + rec.merge_offset);
     const uint32_t two = rec.merges_two, rest = static_cast<uint32_t>(rec.merges) - rec.merges_two;
     const dim3 block(kGroup * p.head_dim / 4);
-    if (two > 0) {
-      const dim3 g(two, kPfTokens / kPfMergeRows);
-      if (p.head_dim == 64) {
-        hipLaunchKernelGGL((PrefillMergeKernel<64, kPfMergeRows>), g, block, 0, stream, outp, lsep, mg, part_o, part_ml,
-                           q_indptr, p.q_heads);
-      } else if (p.head_dim == 128) {
-        hipLaunchKernelGGL((PrefillMergeKernel<128, kPfMergeRows>), g, block, 0, stream, outp, lsep, mg, part_o, part_ml,
-                           q_indptr, p.q_heads);
-      } else {
-        hipLaunchKernelGGL((PrefillMergeKernel<256, kPfMergeRows>), g, block, 0, stream, outp, lsep, mg, part_o, part_ml,
-                           q_indptr, p.q_heads);
-      }
-    }
-    if (rest > 0) {
-      const dim3 g(rest, kPfTokens);
-      if (p.head_dim == 64) {
-        hipLaunchKernelGGL((PrefillMergeKernel<64, 1>), g, block, 0, stream, outp, lsep, mg + two, part_o, part_ml,
-                           q_indptr, p.q_heads);
-      } else if (p.head_dim == 128) {
-        hipLaunchKernelGGL((PrefillMergeKernel<128, 1>), g, block, 0, stream, outp, lsep, mg + two, part_o, part_ml,
-                           q_indptr, p.q_heads);
-      } else {
-        hipLaunchKernelGGL((PrefillMergeKernel<256, 1>), g, block, 0, stream, outp, lsep, mg + two, part_o, part_ml,
-                           q_indptr, p.q_heads);
-      }
+    const dim3 g(two * (kPfTokens / kPfMergeRows) + rest * kPfTokens);
+    if (p.head_dim == 64) {
+      hipLaunchKernelGGL(PrefillMergeKernel<64>, g, block, 0, stream, outp, lsep, mg, part_o, part_ml, q_indptr,
+                         p.q_heads, two);
+    } else if (p.head_dim == 128) {
+      hipLaunchKernelGGL(PrefillMergeKernel<128>, g, block, 0, stream, outp, lsep, mg, part_o, part_ml, q_indptr,
+                         p.q_heads, two);
+    } else {
+      hipLaunchKernelGGL(PrefillMergeKernel<256>, g, block, 0, stream, outp, lsep, mg, part_o, part_ml, q_indptr,
+                         p.q_heads, two);
     }
     return roost::HipStatus(hipGetLastError(), "paged_attention", "prefill merge launch");
   }
