@@ -59,6 +59,17 @@ ROOST_API RoostStatus roost_gdn_recurrent_run(RoostContext* ctx, const void* par
  * current. Calls that overlap on one GPU race on its array. It calls no hipMalloc/hipFree. */
 ROOST_API RoostStatus roost_amd_gdn_recurrent_run_noalloc(RoostContext* ctx, const void* params, void* stream);
 
+/* GatedDeltaRuleGates folded into the recurrent GatedDeltaRule variant. No counterpart in the reference, whose Qwen3.5
+ * layer runs roost_gated_delta_rule_gates_run (g, beta from a, b, a_log, dt_bias) and then the recurrent variant on
+ * them (CpuOps.Gating.cs:21-58, CpuOps.Hybrid.cs:30-157). This call computes the same outputs and states bit for bit
+ * without writing or reading g and beta: each kernel that reads a token's gates computes them from the gates' inputs
+ * with the gates op's own arithmetic (beta rounded to bf16, as that op's bf16 output holds it). `params` is a
+ * RoostGatedDeltaRuleParams whose g and beta spans are not read; `gates` a RoostGatedDeltaRuleGatesParams (tokens and
+ * v_heads equal to the GDN call's; a and b bf16 or f32 row-strided views, a_log and dt_bias bf16 or f32) whose g and
+ * beta spans are not read. Workspace as roost_gdn_recurrent_workspace sizes it. */
+ROOST_API RoostStatus roost_amd_gdn_recurrent_gated_run(RoostContext* ctx, const void* params, const void* gates,
+                                                         const RoostWorkspace* ws, void* stream);
+
 /* The Gated DeltaNet layer's neighbour ops, each flagged GRAPH_CAPTURABLE | DETERMINISTIC | BATCH_INVARIANT, no plan
  * and no workspace:
  * GatedDeltaRuleGates, variant "gated-delta-rule-gates-gfx950" -- replaces roost_gated_delta_rule_gates_run

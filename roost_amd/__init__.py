@@ -101,6 +101,9 @@ class KernelLibrary:
         self.dll.roost_amd_plan_region_fill.restype = C.c_int32
         self.dll.roost_amd_plan_region_run.argtypes = [C.c_void_p, C.POINTER(abi.PlanRegion), C.c_void_p]
         self.dll.roost_amd_plan_region_run.restype = C.c_int32
+        self.dll.roost_amd_gdn_recurrent_gated_run.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                                               C.c_void_p]
+        self.dll.roost_amd_gdn_recurrent_gated_run.restype = C.c_int32
         self.dll.roost_amd_plan_region_from_step.argtypes = [C.c_void_p, C.c_uint64, C.POINTER(abi.StepTables)]
         self.dll.roost_amd_plan_region_from_step.restype = C.c_int32
         version = self.dll.roost_abi_version()
@@ -448,6 +451,18 @@ def recurrent_state_snapshot_params(pool, snapshots, pairs, *, slot_bytes, count
 
 def gated_delta_rule_gates(session: OpSession, *args, **kwargs) -> None:
     session.launch(session.lib.entry(GATES_VARIANT), gated_delta_rule_gates_params(*args, **kwargs))
+
+
+def gdn_recurrent_gated(session: OpSession, gdn_params, gates_params, key="gated") -> None:
+    """roost_amd_gdn_recurrent_gated_run: the recurrent GatedDeltaRule with the gates computed in its kernels, in the
+    recurrent variant's workspace (sized and kept by the session under `key`)."""
+    entry = session.lib.entry(RECURRENT_VARIANT)
+    ws = session._workspace(entry, gdn_params, key)[3]
+    status = session.lib.dll.roost_amd_gdn_recurrent_gated_run(session.ctx, C.addressof(gdn_params),
+                                                               C.addressof(gates_params), C.addressof(ws),
+                                                               C.c_void_p(session.stream_handle))
+    if status != abi.OK:
+        raise KernelError("gdn_recurrent_gated", status, session.lib.last_error())
 
 
 def gated_rms_norm(session: OpSession, *args, **kwargs) -> None:

@@ -53,6 +53,24 @@ __device__ __forceinline__ uint32_t PackBf16Rne(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((F2){lo, hi}, B2));
 }
 
+// An element of a span whose type (bf16 or f32) is chosen at run time; the branch is uniform across a launch.
+__device__ __forceinline__ float LoadF(const void* p, uint32_t dt, int64_t i) {
+  return dt == ROOST_DTYPE_BF16 ? Bf16ToF32(static_cast<const uint16_t*>(p)[i]) : static_cast<const float*>(p)[i];
+}
+
+// sigmoid with the hardware reciprocal (v_rcp_f32, about 1 ulp) instead of a full-precision divide.
+__device__ __forceinline__ float SigmoidF(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+
+// GatedDeltaRuleGates for one (token, value head) (CpuOps.Gating.cs): g = -exp(a_log) * softplus(a + dt_bias), with
+// softplus(x) = x above 20, and beta = sigmoid(b), in fp32. The gates op stores these; the GDN kernels' fused-gates
+// path uses them directly, so both paths compute bit-identical values.
+__device__ __forceinline__ void GateValues(float a, float dt_bias, float a_log, float b, float& g, float& beta) {
+  const float x = a + dt_bias;
+  const float sp = x > 20.0f ? x : log1pf(__expf(x));
+  g = -__expf(a_log) * sp;
+  beta = SigmoidF(b);
+}
+
 }  // namespace roost_dev
 
 #endif  // ROOST_AMD_COMMON_H_

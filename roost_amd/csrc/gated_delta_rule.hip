@@ -49,7 +49,8 @@ constexpr char kOp[] = "gated_delta_rule";
 
 // The call's rules, shared by both variants. The statuses are the contract's (the reference refuses the same shapes:
 // kernels/src/ops/gated_delta_rule.cu:231-278); `planning` adds plan()'s need for the host cu_seqlens copy.
-RoostStatus Admit(const RoostGatedDeltaRuleParams& p, bool planning) {
+// fused_gates: g and beta come from the call's GatedDeltaRuleGates inputs, so their spans are not read.
+RoostStatus Admit(const RoostGatedDeltaRuleParams& p, bool planning, bool fused_gates = false) {
   roost::Gate gate(kOp);
   gate.Header(&p, sizeof(RoostGatedDeltaRuleParams))
       .Expect(p.k_dim == kDim && p.v_dim == kDim, ROOST_STATUS_UNSUPPORTED,
@@ -79,21 +80,25 @@ RoostStatus Admit(const RoostGatedDeltaRuleParams& p, bool planning) {
       .Tensor("v", p.v, ROOST_DTYPE_BF16, reach(vs, vrow));
   ROOST_GATE_RETURN(gate);
   // g, beta and output of another type are shapes the kernels do not cover (UNSUPPORTED, as the contract has it).
-  gate.Expect(p.g.dtype == ROOST_DTYPE_F32 && p.beta.dtype == ROOST_DTYPE_BF16 && p.output.dtype == ROOST_DTYPE_BF16,
-              ROOST_STATUS_UNSUPPORTED, "g %s, beta %s, output %s: built for f32 g with bf16 beta and output",
-              roost::Describe(p.g.dtype).name, roost::Describe(p.beta.dtype).name, roost::Describe(p.output.dtype).name);
+  gate.Expect(fused_gates || (p.g.dtype == ROOST_DTYPE_F32 && p.beta.dtype == ROOST_DTYPE_BF16),
+              ROOST_STATUS_UNSUPPORTED, "g %s, beta %s: built for f32 g with bf16 beta", roost::Describe(p.g.dtype).name,
+              roost::Describe(p.beta.dtype).name)
+      .Expect(p.output.dtype == ROOST_DTYPE_BF16, ROOST_STATUS_UNSUPPORTED, "output %s: built for bf16 output",
+              roost::Describe(p.output.dtype).name);
   ROOST_GATE_RETURN(gate);
-  gate.Tensor("g", p.g, ROOST_DTYPE_F32, t * p.v_heads)
-      .Tensor("beta", p.beta, ROOST_DTYPE_BF16, t * p.v_heads)
-      .Tensor("output", p.output, ROOST_DTYPE_BF16, t * vrow)
+  if (!fused_gates) {
+    gate.Tensor("g", p.g, ROOST_DTYPE_F32, t * p.v_heads)
+        .Tensor("beta", p.beta, ROOST_DTYPE_BF16, t * p.v_heads)
+        .Aligned("g", p.g.address, 16)
+        .Aligned("beta", p.beta.address, 16);
+  }
+  gate.Tensor("output", p.output, ROOST_DTYPE_BF16, t * vrow)
       .Tensor("state", p.state, ROOST_DTYPE_F32, StateElems(p))
       .Expect(p.state.length % StateElems(p) == 0, ROOST_STATUS_INVALID_ARGUMENT,
               "state pool of %llu floats is not a whole number of [%u, 128, 128] slots",
               static_cast<unsigned long long>(p.state.length), p.v_heads)
       .Tensor("state_slots", p.state_slots, ROOST_DTYPE_I32, p.batch)
       .Tensor("cu_seqlens", p.cu_seqlens, ROOST_DTYPE_I32, uint64_t{p.batch} + 1)
-      .Aligned("g", p.g.address, 16)
-      .Aligned("beta", p.beta.address, 16)
       .Aligned("output", p.output.address, 16)
       .Aligned("state", p.state.address, 16)
       .Aligned("q", p.q.address, 2)
@@ -122,6 +127,16 @@ float Scale(const RoostGatedDeltaRuleParams& p) {
   return p.scale != 0.0f ? p.scale : 1.0f / std::sqrt(static_cast<float>(kDim));
 }
 
+// The GatedDeltaRuleGates inputs of a call that folds the gates in (roost_amd_gdn_recurrent_gated_run).
+struct GateSource {
+  const void* a = nullptr;  // [tokens, v_heads] at a_stride
+  const void* b = nullptr;  // [tokens, v_heads] at b_stride
+  const void* a_log = nullptr;
+  const void* dt_bias = nullptr;
+  uint32_t a_t = 0, b_t = 0, alog_t = 0, dtb_t = 0;  // dtypes (bf16 or f32)
+  uint64_t a_stride = 0, b_stride = 0;
+};
+
 struct GdnArgs {
   const uint16_t* q;
   const uint16_t* k;
@@ -139,7 +154,24 @@ struct GdnArgs {
   float scale;
   uint32_t vh;     // value heads (the rows of v, output, g and beta, the heads of a state slot)
   uint32_t group;  // value heads per key head: value head h reads q / k head h / group
+  GateSource gs;   // when gs.a is set, g and beta are computed from these instead of read from g and beta
 };
+
+// g and beta of (token, value head): read from the call's g and beta, or computed from the gates' inputs exactly as
+// the GatedDeltaRuleGates op computes and stores them (beta rounded to bf16, as its bf16 output holds it).
+__device__ __forceinline__ void GateAt(const GdnArgs& a, uint64_t tok, uint32_t h, float& g, float& beta) {
+  if (a.gs.a != nullptr) {
+    float bv;
+    GateValues(LoadF(a.gs.a, a.gs.a_t, static_cast<int64_t>(tok * a.gs.a_stride + h)),
+               LoadF(a.gs.dt_bias, a.gs.dtb_t, h), LoadF(a.gs.a_log, a.gs.alog_t, h),
+               LoadF(a.gs.b, a.gs.b_t, static_cast<int64_t>(tok * a.gs.b_stride + h)), g, bv);
+    beta = Bf16ToF32(F32ToBf16(bv));
+  } else {
+    const uint64_t gi = tok * a.vh + h;
+    g = a.g[gi];
+    beta = Bf16ToF32(a.beta[gi]);
+  }
+}
 
 typedef float f32x4v_t __attribute__((ext_vector_type(4)));
 
@@ -230,9 +262,9 @@ __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint
         vv[i] = Bf16ToF32(vrow[i]);
       }
     }
-    const uint64_t gi = static_cast<uint64_t>(tok) * a.vh + h;
-    const float decay = expf(a.g[gi]);
-    const float beta = Bf16ToF32(a.beta[gi]);
+    float graw, beta;
+    GateAt(a, static_cast<uint64_t>(tok), h, graw, beta);
+    const float decay = expf(graw);
     float qq = fmaf(q2[0], q2[0], q2[1] * q2[1]), kk = fmaf(k2[0], k2[0], k2[1] * k2[1]);
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -304,8 +336,9 @@ __global__ void __launch_bounds__(kRecThreads) RecurrentKernel(GdnArgs a) {
   RecurrentUnit<kVec>(a, blockIdx.x, blockIdx.y / kRecQuarters, blockIdx.y % kRecQuarters);
 }
 
-GdnArgs MakeArgs(const RoostGatedDeltaRuleParams& p) {
+GdnArgs MakeArgs(const RoostGatedDeltaRuleParams& p, const GateSource& gs = GateSource{}) {
   GdnArgs a{};
+  a.gs = gs;
   a.q = static_cast<const uint16_t*>(p.q.address);
   a.k = static_cast<const uint16_t*>(p.k.address);
   a.v = static_cast<const uint16_t*>(p.v.address);
@@ -333,8 +366,9 @@ bool Vec16(const RoostGatedDeltaRuleParams& p) {
          ks % 8 == 0 && vs % 8 == 0;
 }
 
-RoostStatus LaunchRecurrent(const RoostGatedDeltaRuleParams& p, hipStream_t stream, int32_t route_min = 0) {
-  GdnArgs a = MakeArgs(p);
+RoostStatus LaunchRecurrent(const RoostGatedDeltaRuleParams& p, hipStream_t stream, int32_t route_min = 0,
+                            const GateSource& gs = GateSource{}) {
+  GdnArgs a = MakeArgs(p, gs);
   a.route_min = route_min;
   const dim3 grid(p.batch, p.v_heads * kRecQuarters);
   if (Vec16(p)) {
@@ -649,9 +683,8 @@ __device__ __forceinline__ void WyPrepChunk(const ChunkArgs& ca, uint32_t x, uin
       kv[i] = Load8<kVec>(kp + 8 * i);
       bq[i] = Load8<kVec>(qp + 32 * i);
     }
-    const uint64_t gi = static_cast<uint64_t>(t0 + min(lane, n - 1)) * a.vh + h;
-    const float graw = a.g[gi];
-    const uint16_t braw = a.beta[gi];
+    float graw, braw;
+    GateAt(a, static_cast<uint64_t>(t0 + min(lane, n - 1)), h, graw, braw);
     float kk = 0.0f, qq = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -674,7 +707,7 @@ __device__ __forceinline__ void WyPrepChunk(const ChunkArgs& ca, uint32_t x, uin
         if (lane >= d) gv += y;
       }
       g_lds[lane] = gv * kLog2e;  // cumulative log-decay in log2 units: every factor below is one exp2
-      b_lds[lane] = lane < n ? Bf16ToF32(braw) : 0.0f;
+      b_lds[lane] = lane < n ? braw : 0.0f;
     }
   }
   __syncthreads();
@@ -1337,9 +1370,10 @@ __global__ void __launch_bounds__(1024) RouteKernel(const int32_t* cu, uint32_t 
 
 // with_recurrent: the prep launch also runs the recurrence of the sequences shorter than kRouteMinTokens.
 RoostStatus LaunchChunk(const RoostGatedDeltaRuleParams& p, const RoostWorkspace* ws, const ChunkArena& l,
-                        uint32_t chunks, hipStream_t stream, bool fold = false, bool with_recurrent = false) {
+                        uint32_t chunks, hipStream_t stream, bool fold = false, bool with_recurrent = false,
+                        const GateSource& gs = GateSource{}) {
   ChunkArgs ca{};
-  ca.a = MakeArgs(p);
+  ca.a = MakeArgs(p, gs);
   auto* base = static_cast<uint8_t*>(ws->device);
   ca.chunks = reinterpret_cast<const int4*>(base + l.chunk_table);
   ca.seqs = reinterpret_cast<const int4*>(base + l.seq_table);
@@ -1384,7 +1418,8 @@ RoostStatus LaunchChunk(const RoostGatedDeltaRuleParams& p, const RoostWorkspace
 // prep workgroups: the chunks' chains leave most of the chip idle. The scan follows on the same stream. Sequences of
 // one call must use distinct state slots: two that share one race (they may run at the same time), as they do in the
 // reference's gather / scatter of the slots.
-RoostStatus LaunchRouted(const RoostGatedDeltaRuleParams& p, uint8_t* base, const ChunkArena& l, hipStream_t s) {
+RoostStatus LaunchRouted(const RoostGatedDeltaRuleParams& p, uint8_t* base, const ChunkArena& l, hipStream_t s,
+                         const GateSource& gs = GateSource{}) {
   const bool fold = p.batch <= kFoldBatch;
   if (!fold) {
     hipLaunchKernelGGL(RouteKernel, dim3(1), dim3(1024), 0, s, static_cast<const int32_t*>(p.cu_seqlens.address),
@@ -1396,7 +1431,31 @@ RoostStatus LaunchRouted(const RoostGatedDeltaRuleParams& p, uint8_t* base, cons
   RoostWorkspace ws{};
   ws.device = base;
   ws.device_bytes = l.total;
-  return LaunchChunk(p, &ws, l, l.max_chunks, s, fold, /*with_recurrent=*/true);
+  return LaunchChunk(p, &ws, l, l.max_chunks, s, fold, /*with_recurrent=*/true, gs);
+}
+
+// The recurrent variant's run() over its admitted call, with g and beta read from the call or computed from gs.
+RoostStatus RecurrentRun(const RoostGatedDeltaRuleParams& p, const RoostWorkspace* ws, hipStream_t s,
+                         const GateSource& gs) {
+  roost::Gate gate(kOp);
+  if (p.batch == 0 || p.tokens == 0) return ROOST_STATUS_OK;
+  if (p.tokens < kRouteMinTokens) return LaunchRecurrent(p, s, 0, gs);
+  if (p.cu_seqlens_host != nullptr) {
+    // The host copy says whether any sequence reaches kRouteMinTokens; if none does, the recurrent kernel runs every
+    // sequence (so a graph captured from this call stays correct whatever lengths it is replayed with).
+    bool any_long = false;
+    for (uint32_t b = 0; b < p.batch && !any_long; ++b) {
+      any_long = p.cu_seqlens_host[b + 1] - p.cu_seqlens_host[b] >= static_cast<int32_t>(kRouteMinTokens);
+    }
+    if (!any_long) return LaunchRecurrent(p, s, 0, gs);
+  }
+  // Every launch size below follows from tokens and batch alone, so the call can be captured into a graph.
+  const ChunkArena l = MakeRouteArena(p.tokens, p.batch, p.v_heads);
+  gate.Expect(roost::HasDeviceRegion(ws, l.total), ROOST_STATUS_WORKSPACE_TOO_SMALL,
+              "%u tokens may route sequences to the chunk kernels, which need %llu device workspace bytes", p.tokens,
+              static_cast<unsigned long long>(l.total));
+  ROOST_GATE_RETURN(gate);
+  return LaunchRouted(p, static_cast<uint8_t*>(ws->device), l, s, gs);
 }
 
 }  // namespace
@@ -1423,25 +1482,54 @@ extern "C" ROOST_API RoostStatus roost_gdn_recurrent_run(RoostContext* ctx, cons
   const auto& p = *static_cast<const RoostGatedDeltaRuleParams*>(params);
   return roost::CatchAll(kOp, [&]() -> RoostStatus {
     ROOST_RETURN_IF_FAILED(Admit(p, false));
-    if (p.batch == 0 || p.tokens == 0) return ROOST_STATUS_OK;
-    hipStream_t s = roost::Stream(stream);
-    if (p.tokens < kRouteMinTokens) return LaunchRecurrent(p, s);
-    if (p.cu_seqlens_host != nullptr) {
-      // The host copy says whether any sequence reaches kRouteMinTokens; if none does, the recurrent kernel runs every
-      // sequence (so a graph captured from this call stays correct whatever lengths it is replayed with).
-      bool any_long = false;
-      for (uint32_t b = 0; b < p.batch && !any_long; ++b) {
-        any_long = p.cu_seqlens_host[b + 1] - p.cu_seqlens_host[b] >= static_cast<int32_t>(kRouteMinTokens);
-      }
-      if (!any_long) return LaunchRecurrent(p, s);
-    }
-    // Every launch size below follows from tokens and batch alone, so the call can be captured into a graph.
-    const ChunkArena l = MakeRouteArena(p.tokens, p.batch, p.v_heads);
-    gate.Expect(roost::HasDeviceRegion(ws, l.total), ROOST_STATUS_WORKSPACE_TOO_SMALL,
-                "%u tokens may route sequences to the chunk kernels, which need %llu device workspace bytes",
-                p.tokens, static_cast<unsigned long long>(l.total));
+    return RecurrentRun(p, ws, roost::Stream(stream), GateSource{});
+  });
+}
+
+extern "C" ROOST_API RoostStatus roost_amd_gdn_recurrent_gated_run(RoostContext* ctx, const void* params,
+                                                                   const void* gates, const RoostWorkspace* ws,
+                                                                   void* stream) {
+  roost::Gate gate(kOp);
+  gate.Expect(ctx != nullptr && params != nullptr && gates != nullptr, ROOST_STATUS_INVALID_ARGUMENT,
+              "a context, the GDN params and the gates params are required");
+  ROOST_GATE_RETURN(gate);
+  ROOST_GATE_RETURN(gate.Header(gates, sizeof(RoostGatedDeltaRuleGatesParams)));
+  const auto& p = *static_cast<const RoostGatedDeltaRuleParams*>(params);
+  const auto& gp = *static_cast<const RoostGatedDeltaRuleGatesParams*>(gates);
+  return roost::CatchAll(kOp, [&]() -> RoostStatus {
+    ROOST_RETURN_IF_FAILED(Admit(p, false, /*fused_gates=*/true));
+    gate.Expect(gp.tokens == p.tokens && gp.v_heads == p.v_heads, ROOST_STATUS_INVALID_ARGUMENT,
+                "the gates cover %u tokens x %u heads; the call has %u x %u", gp.tokens, gp.v_heads, p.tokens,
+                p.v_heads);
     ROOST_GATE_RETURN(gate);
-    return LaunchRouted(p, static_cast<uint8_t*>(ws->device), l, s);
+    auto float_span = [&](const char* name, const RoostDeviceSpan& sp, uint64_t elements) {
+      gate.Expect(sp.dtype == ROOST_DTYPE_BF16 || sp.dtype == ROOST_DTYPE_F32, ROOST_STATUS_UNSUPPORTED,
+                  "%s is %s; the gates read bf16 or f32", name, roost::Describe(sp.dtype).name);
+      if (gate.ok()) gate.Tensor(name, sp, sp.dtype, elements).Aligned(name, sp.address, roost::ElementBytes(sp.dtype));
+    };
+    const uint64_t as = gp.a_stride == 0 ? gp.v_heads : gp.a_stride, bs = gp.b_stride == 0 ? gp.v_heads : gp.b_stride;
+    gate.Expect(as >= gp.v_heads && bs >= gp.v_heads, ROOST_STATUS_INVALID_ARGUMENT,
+                "a_stride %llu, b_stride %llu: rows hold %u heads", static_cast<unsigned long long>(as),
+                static_cast<unsigned long long>(bs), gp.v_heads);
+    const uint64_t t = gp.tokens;
+    float_span("a", gp.a, t == 0 ? 0 : (t - 1) * as + gp.v_heads);
+    float_span("b", gp.b, t == 0 ? 0 : (t - 1) * bs + gp.v_heads);
+    float_span("a_log", gp.a_log, gp.v_heads);
+    float_span("dt_bias", gp.dt_bias, gp.v_heads);
+    ROOST_GATE_RETURN(gate);
+    GateSource gs;
+    gs.a = gp.a.address;
+    gs.b = gp.b.address;
+    gs.a_log = gp.a_log.address;
+    gs.dt_bias = gp.dt_bias.address;
+    gs.a_t = gp.a.dtype;
+    gs.b_t = gp.b.dtype;
+    gs.alog_t = gp.a_log.dtype;
+    gs.dtb_t = gp.dt_bias.dtype;
+    gs.a_stride = as;
+    gs.b_stride = bs;
+    if (t > 0 && gs.a == nullptr) return roost::Report(ROOST_STATUS_INVALID_ARGUMENT, kOp, "a: address is NULL");
+    return RecurrentRun(p, ws, roost::Stream(stream), gs);
   });
 }
 

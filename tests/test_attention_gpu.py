@@ -507,7 +507,8 @@ def test_prefill_head_dim_128_needs_a_dma_page_size(session):
     d = Dev(b)
     entry = session.lib.entry(roost_amd.ATTENTION_VARIANT)
     sizes = abi.new(abi.WorkspaceSizes)
-    assert entry.workspace(session.ctx, C.addressof(d.params()), C.addressof(sizes)) == abi.UNSUPPORTED
+    params = d.params()  # held here: the call reads it through a raw address
+    assert entry.workspace(session.ctx, C.addressof(params), C.addressof(sizes)) == abi.UNSUPPORTED
 
 
 # ---- Groups of 8, 16 and 32 query heads per KV head: 2, 4 or 8 groups of 4 reading the same KV rows -----------------

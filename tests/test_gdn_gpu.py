@@ -1,6 +1,8 @@
 """GatedDeltaRule (chunk and recurrent variants) on the GPU through the C ABI vs the CpuOps oracle (reference harness:
 kernels/tests/hybrid-conformance/GdnCases.cs:31-471). Tolerances: output max-abs 2e-2 and max-rel 1e-2; final state
 max-rel 1e-3 (relative to |ref_i| + max|ref|), per BASELINE.json."""
+import zlib
+
 import numpy as np
 import pytest
 
@@ -313,3 +315,86 @@ def test_grouped_value_heads(session, variant, name, kh, vh, lens):
     cases.assert_close(cases.bf16_values(got_o), cases.bf16_values(want_o), what=f"{name} output")
     for s in slots:
         cases.assert_close(got_pool[s], want_pool[s], max_abs=1.0, max_rel=cases.STATE_REL, what=f"{name} state {s}")
+
+
+# ---- GatedDeltaRuleGates folded into the recurrent variant (roost_amd_gdn_recurrent_gated_run) ------------------------
+
+GATED_CASES = [
+    ("decode 48 x 1", [1] * 48),
+    ("routed step 1, 40, 1, 600, 3", [1, 40, 1, 600, 3]),
+    ("short continuations", [5, 9, 15, 1]),
+]
+
+
+@pytest.mark.parametrize("name,lens", GATED_CASES, ids=[c[0] for c in GATED_CASES])
+def test_recurrent_with_gates_folded_in_equals_gates_then_recurrent(session, name, lens):
+    """The fused call against the two calls it replaces, bit for bit (outputs and every state slot): the gates op
+    writes g (f32) and beta (bf16) from a [tokens, 64] projection (b at column 0, a at 16, Qwen3.5's layout), then the
+    recurrent variant reads them; the fused call reads the projection itself. One case is also checked against CpuOps."""
+    import torch
+
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    d = cases.make_gdn(rng, lens, len(lens) + 3, slots=list(rng.permutation(len(lens) + 3)[: len(lens)]),
+                       baseline_style=True)
+    T, row = d.tokens, 64
+    proj = cases.bf16_bits(rng.standard_normal((T, row)).astype(np.float32) * 4.0)
+    a_log = (rng.standard_normal(HEADS) * 0.5).astype(np.float32)
+    dt_bias = (rng.standard_normal(HEADS) * 2.0).astype(np.float32)
+    d_proj, d_alog, d_dtb = to_dev(proj, True), to_dev(a_log), to_dev(dt_bias)
+    reach = (T - 1) * row + HEADS
+    gkw = dict(tokens=T, v_heads=HEADS, a_stride=row, b_stride=row, a_len=reach, b_len=reach, a_offset=16, b_offset=0)
+
+    # The two calls: gates into g / beta, then the recurrent variant on them.
+    two = DevGdn(d)
+    two.g = torch.full((T, HEADS), float("nan"), dtype=torch.float32, device="cuda")
+    two.beta = torch.zeros((T, HEADS), dtype=torch.bfloat16, device="cuda")
+    roost_amd.gated_delta_rule_gates(session, d_proj, d_proj, d_alog, d_dtb, two.g, two.beta, **gkw)
+    session.launch(session.lib.entry(roost_amd.RECURRENT_VARIANT), two.params(), key=("gated-two", T))
+    torch.cuda.synchronize()
+    want_o, want_pool = from_dev(two.out, True)[:T], from_dev(two.pool)
+
+    # The fused call: g and beta spans left empty.
+    one = DevGdn(d)
+    one.g = None
+    one.beta = None
+    gates = roost_amd.gated_delta_rule_gates_params(d_proj, d_proj, d_alog, d_dtb, None, None, **gkw)
+    roost_amd.gdn_recurrent_gated(session, one.params(), gates, key=("gated-one", T))
+    torch.cuda.synchronize()
+    assert np.array_equal(from_dev(one.out, True)[:T], want_o), "outputs differ from gates + recurrent"
+    assert np.array_equal(from_dev(one.pool), want_pool), "states differ from gates + recurrent"
+
+    if name.startswith("routed"):
+        d.g = np.ascontiguousarray(from_dev(two.g).reshape(T, HEADS))
+        d.beta = np.ascontiguousarray(from_dev(two.beta, True).reshape(T, HEADS))
+        want_o_cpu, want_pool_cpu = cases.oracle_gdn(d)
+        cases.assert_close(cases.bf16_values(want_o), cases.bf16_values(want_o_cpu), what="fused gates vs CpuOps")
+        for s in d.slots:
+            cases.assert_close(want_pool[s], want_pool_cpu[s], max_abs=1.0, max_rel=cases.STATE_REL, what=f"slot {s}")
+
+
+def test_recurrent_with_gates_refusals(session):
+    rng = np.random.default_rng(5)
+    d = cases.make_gdn(rng, [1, 1], 2)
+    dev = DevGdn(d)
+    proj = to_dev(cases.bf16_bits(rng.standard_normal((2, 64)).astype(np.float32)), True)
+    vec = to_dev(np.zeros(HEADS, np.float32))
+    entry_fn = session.lib.dll.roost_amd_gdn_recurrent_gated_run
+    ws = abi.new(abi.Workspace)
+
+    def status(gates, **over):
+        import ctypes as C
+
+        params = dev.params(**over)  # held here: the call reads it through a raw address
+        return entry_fn(session.ctx, C.addressof(params), C.addressof(gates) if gates is not None else None,
+                        C.addressof(ws), C.c_void_p(session.stream_handle))
+
+    good = roost_amd.gated_delta_rule_gates_params(proj, proj, vec, vec, None, None, tokens=2, v_heads=HEADS,
+                                                   a_stride=64, b_stride=64, a_offset=16)
+    assert status(None) == abi.INVALID_ARGUMENT
+    bad = roost_amd.gated_delta_rule_gates_params(proj, proj, vec, vec, None, None, tokens=3, v_heads=HEADS,
+                                                  a_stride=64, b_stride=64, a_offset=16)
+    assert status(bad) == abi.INVALID_ARGUMENT  # the gates cover another token count
+    short = roost_amd.gated_delta_rule_gates_params(proj, proj, vec, vec, None, None, tokens=2, v_heads=HEADS,
+                                                    a_stride=64, b_stride=64, a_offset=16, a_len=10)
+    assert status(short) == abi.INVALID_ARGUMENT  # a shorter than its view
+    assert status(good) == abi.OK
