@@ -358,6 +358,26 @@ def bench_mixed(torch, roost_amd, session, steps, warmup):
         "attention": time_runs(torch, session, e_att, att, ws_att, steps, warmup),
         "gdn_layer": time_runs(torch, session, e_gdn, gdn[0], ws_gdn[0], steps, warmup),
     }
+    # The gates folded into the GDN call (roost_amd_gdn_recurrent_gated_run) against the two calls it replaces (the
+    # GatedDeltaRuleGates op writing g and beta from a Qwen3.5 [tokens, 64] b|a projection, then the recurrent variant):
+    # not part of config 5's step, reported beside it.
+    proj = (torch.randn((T, 64), generator=g, device="cuda") * 4).to(torch.bfloat16)
+    a_log = torch.randn((H,), generator=g, device="cuda") * 0.5
+    dt_bias = torch.randn((H,), generator=g, device="cuda")
+    reach_g = (T - 1) * 64 + H
+    gkw = dict(tokens=T, v_heads=H, a_stride=64, b_stride=64, a_len=reach_g, b_len=reach_g, a_offset=16, b_offset=0)
+    gates_sep = roost_amd.gated_delta_rule_gates_params(proj, proj, a_log, dt_bias, gg, beta, **gkw)
+    gates_fused = roost_amd.gated_delta_rule_gates_params(proj, proj, a_log, dt_bias, None, None, **gkw)
+    e_gates = session.lib.entry(roost_amd.GATES_VARIANT)
+    ws_gates, _ = planned(session, e_gates, gates_sep, "mixed-gates")
+
+    def gates_then_gdn():
+        session.run(e_gates, gates_sep, ws_gates)
+        session.run(e_gdn, gdn[0], ws_gdn[0])
+
+    parts["gates_then_gdn_layer"] = time_each(torch, session, gates_then_gdn, steps)
+    parts["gdn_layer_gates_fused"] = time_each(
+        torch, session, lambda: roost_amd.gdn_recurrent_gated(session, gdn[0], gates_fused, key="mixed-gated"), steps)
     # HBM floor of the step: K/V of every context token, the KV append, and per GDN layer the states read and
     # written once plus q, k, v, g, beta and o of every token.
     kv_bytes = int(kv.sum()) * b.hkv * b.d * 2 * 2 + 2 * T * b.hkv * b.d * 2 * 2
