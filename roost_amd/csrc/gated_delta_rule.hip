@@ -11,9 +11,10 @@
 // back (slots are device data and are never range-checked on the host).
 //
 // Recurrent variant -- HBM bound (the state is read once and written once per call; the views are read in place, with
-// no gather or state copy): one 128-thread workgroup per (sequence, value head). Thread t owns the 4 value columns
-// 4*(t/4)..+3 over 32 key rows 32*(t%4)..+31 of S in registers (128 floats), so the column sums S^T k and S^T q need
-// only a reduction over the 4 lanes of a quad, and consecutive lanes read consecutive 16-byte pieces of a state row.
+// no gather or state copy): four 256-thread workgroups per (sequence, value head), one per quarter of the value columns,
+// each lane holding 16 floats of S in registers (RecurrentUnit). Sequences of 16 or more tokens go to the chunk (WY)
+// kernels instead; their prep workgroups share one launch with the recurrent ones (WyPrepRecurrentKernel). The gates
+// may be folded in (roost_amd_gdn_recurrent_gated_run): g and beta are then computed where they are read.
 
 #include <algorithm>
 #include <cmath>

@@ -27,7 +27,10 @@
 //   * S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_32x32x16_bf16 with fp32 accumulation; the softmax statistics of a
 //     query live in one lane pair; P is rounded to bf16 before the P.V product (as FlashAttention-2 does);
 //   * plan() cuts items longer than the average CU load into pieces (bf16 partials merged in key order) and orders the
-//     work longest-first so the ragged causal tail does not set the makespan.
+//     work longest-first so the ragged causal tail does not set the makespan;
+//   * single-token sequences of a prefill call run on the decode kernels, beside the tile kernel on the context's
+//     second stream when plan() finds that cheaper (ChooseOverlap); an f32 prefill runs every query token as a row of
+//     the f32 decode kernel.
 
 #include <algorithm>
 #include <cmath>
