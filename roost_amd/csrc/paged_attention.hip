@@ -1741,12 +1741,25 @@ __global__ void __launch_bounds__(512, 1)
 
   // Page ids of the four 16-row groups of tile t (rows clamped into the item's keys); loaded one tile before the
   // copy that needs them, so the scalar loads never stall the loop.
+  // With 16-token pages, a tile wholly inside the key range takes its four ids as one 16-byte scalar load of
+  // consecutive page-table entries (all of them exist: the sequence has a page for every key below kend).
   auto load_ids = [&](int t, int32_t (&ids)[4]) {
     const int32_t kb = kbeg + 64 * t;
+    if (ps_shift == 4 && kb + 64 <= kend) {
+      int4 v;
+      __builtin_memcpy(&v, kv_indices + p0 + (kb >> 4), sizeof(v));
+      ids[0] = v.x;
+      ids[1] = v.y;
+      ids[2] = v.z;
+      ids[3] = v.w;
+    } else {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) ids[g] = kv_indices[p0 + (min(kb + 16 * g, kend - 1) >> ps_shift)];
+      for (int g = 0; g < 4; ++g) ids[g] = kv_indices[p0 + (min(kb + 16 * g, kend - 1) >> ps_shift)];
+    }
   };
-  auto good_page = [&](int32_t id) { return id >= 0 && static_cast<uint64_t>(id) < kv.pool_pages; };
+  // id in [0, pool_pages) as one unsigned 32-bit compare (pool page counts above 2^31 - 1 are clamped: ids are int32).
+  const uint32_t pool32 = static_cast<uint32_t>(min(kv.pool_pages, static_cast<uint64_t>(0x7FFFFFFF)));
+  auto good_page = [&](int32_t id) { return static_cast<uint32_t>(id) < pool32; };
   // Element offsets inside a page: a row at in-page position `within` starts at row_mul * within + row_add.
   const uint32_t row_mul = kv.hnd ? D : kv.kv_heads * D;
   const uint32_t kvr = kvh >> kv.head_shift;  // the real KV head the item's query heads read
