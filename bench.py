@@ -378,6 +378,28 @@ def bench_mixed(torch, roost_amd, session, steps, warmup):
     parts["gates_then_gdn_layer"] = time_each(torch, session, gates_then_gdn, steps)
     parts["gdn_layer_gates_fused"] = time_each(
         torch, session, lambda: roost_amd.gdn_recurrent_gated(session, gdn[0], gates_fused, key="mixed-gated"), steps)
+    # Qwen3.5's attention output gate (SigmoidMul on the attention output) folded into the attention call
+    # (roost_amd_paged_attention_gated_run) against the two calls it replaces: not part of config 5's step either.
+    out_gate = (torch.randn((T, b.hq * b.d), generator=g, device="cuda") * 2).to(torch.bfloat16)
+    sm = roost_amd.sigmoid_mul_params(b.out, out_gate, b.out, rows=T, dim=b.hq * b.d)
+    e_sm = session.lib.entry(roost_amd.SIGMOID_MUL_VARIANT)
+
+    def attention_then_gate():
+        session.run(e_att, att, ws_att)
+        session.run(e_sm, sm, None)
+
+    roost_amd.paged_attention_gated(session, att, sm, key="mixed-att-gated")
+    ws_att_gated = session._ws[(e_att.variant_id, "mixed-att-gated")][3]
+
+    def attention_gated():
+        import ctypes as C
+
+        st = session.lib.dll.roost_amd_paged_attention_gated_run(session.ctx, C.addressof(att), C.addressof(sm),
+                                                               C.addressof(ws_att_gated), C.c_void_p(session.stream_handle))
+        assert st == 0, session.lib.last_error()
+
+    parts["attention_then_sigmoid_mul"] = time_each(torch, session, attention_then_gate, steps)
+    parts["attention_gate_fused"] = time_each(torch, session, attention_gated, steps)
     # HBM floor of the step: K/V of every context token, the KV append, and per GDN layer the states read and
     # written once plus q, k, v, g, beta and o of every token.
     kv_bytes = int(kv.sum()) * b.hkv * b.d * 2 * 2 + 2 * T * b.hkv * b.d * 2 * 2

@@ -28,6 +28,18 @@ ROOST_API RoostStatus roost_paged_attention_plan(RoostContext* ctx, const void* 
 ROOST_API RoostStatus roost_paged_attention_run(RoostContext* ctx, const void* params, const RoostWorkspace* ws,
                                                 void* stream);
 
+/* PagedAttention with Qwen3.5's attention output gate (SigmoidMul, out = out * sigmoid(gate)) folded into the kernels
+ * that write the output. No counterpart in the reference, whose Qwen3.5 worker runs roost_paged_attention_run and then
+ * roost_sigmoid_mul_run on its output (Qwen35EagerModel.cs:94-97 lists both kernels; semantics CpuOps.Gating.cs:84-96).
+ * This call computes the same output bit for bit and writes it once: each output element, rounded to the output type,
+ * is multiplied by sigmoid(gate) with the SigmoidMul op's own arithmetic where the decode, tile and merge kernels store
+ * it. `params` is a planned RoostPagedAttentionParams (plan() and the workspace as for roost_paged_attention_run);
+ * `gate_params` a RoostSigmoidMulParams whose input and output are both the attention output (the gate applies in
+ * place), rows = tokens, dim = q_heads * head_dim, and whose gate (same dtype as the output, 8-byte aligned) does not
+ * overlap the output. The lse output, when requested, is that of the ungated attention. */
+ROOST_API RoostStatus roost_amd_paged_attention_gated_run(RoostContext* ctx, const void* params, const void* gate_params,
+                                                          const RoostWorkspace* ws, void* stream);
+
 /* CacheWrite, variant "cache-write-gfx950" (GRAPH_CAPTURABLE | DETERMINISTIC | BATCH_INVARIANT), no workspace.
  * Replaces roost_cache_write_run (kernels/src/m0_ops.cu:388-429; declared in kernels/src/roost_internal.h:42). */
 ROOST_API RoostStatus roost_cache_write_run(RoostContext* ctx, const void* params, const RoostWorkspace* ws,

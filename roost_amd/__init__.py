@@ -104,6 +104,9 @@ class KernelLibrary:
         self.dll.roost_amd_gdn_recurrent_gated_run.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                                                C.c_void_p]
         self.dll.roost_amd_gdn_recurrent_gated_run.restype = C.c_int32
+        self.dll.roost_amd_paged_attention_gated_run.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                                                 C.c_void_p]
+        self.dll.roost_amd_paged_attention_gated_run.restype = C.c_int32
         self.dll.roost_amd_plan_region_from_step.argtypes = [C.c_void_p, C.c_uint64, C.POINTER(abi.StepTables)]
         self.dll.roost_amd_plan_region_from_step.restype = C.c_int32
         version = self.dll.roost_abi_version()
@@ -463,6 +466,28 @@ def gdn_recurrent_gated(session: OpSession, gdn_params, gates_params, key="gated
                                                                C.c_void_p(session.stream_handle))
     if status != abi.OK:
         raise KernelError("gdn_recurrent_gated", status, session.lib.last_error())
+
+
+def paged_attention_gated(session: OpSession, attn_params, gate_params, key="gated", plan: bool = True) -> None:
+    """roost_amd_paged_attention_gated_run: PagedAttention with the SigmoidMul output gate folded into its kernels, in
+    the attention variant's workspace (planned here unless plan is False; sized and kept by the session under key)."""
+    entry = session.lib.entry(ATTENTION_VARIANT)
+    slot = session._workspace(entry, attn_params, key)
+    ws = slot[3]
+    if plan:
+        if slot[4] is not None:
+            slot[4].synchronize()
+        status = entry.plan(session.ctx, C.addressof(attn_params), C.addressof(ws), C.c_void_p(session.stream_handle))
+        if status != abi.OK:
+            raise KernelError(f"{entry.variant_id} plan", status, session.lib.last_error())
+        ev = _torch().cuda.Event()
+        ev.record(session.stream)
+        slot[4] = ev
+    status = session.lib.dll.roost_amd_paged_attention_gated_run(session.ctx, C.addressof(attn_params),
+                                                                 C.addressof(gate_params), C.addressof(ws),
+                                                                 C.c_void_p(session.stream_handle))
+    if status != abi.OK:
+        raise KernelError("paged_attention_gated", status, session.lib.last_error())
 
 
 def gated_rms_norm(session: OpSession, *args, **kwargs) -> None:

@@ -61,6 +61,17 @@ __device__ __forceinline__ float LoadF(const void* p, uint32_t dt, int64_t i) {
 // sigmoid with the hardware reciprocal (v_rcp_f32, about 1 ulp) instead of a full-precision divide.
 __device__ __forceinline__ float SigmoidF(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
+// SigmoidMul's arithmetic (CpuOps.Gating.cs, out = x * sigmoid(gate)): each element in fp32, rounded once to the
+// element type. The SigmoidMul op and the attention kernels' gated epilogue both use these, so the fused and the
+// separate calls agree bit for bit.
+__device__ __forceinline__ uint32_t GateMulBf16x2(uint32_t x, uint32_t g) {
+  return PackBf16Rne(Bf16LoToF32(x) * SigmoidF(Bf16LoToF32(g)), Bf16HiToF32(x) * SigmoidF(Bf16HiToF32(g)));
+}
+__device__ __forceinline__ uint16_t GateMul(uint16_t x, uint16_t g) {
+  return static_cast<uint16_t>(GateMulBf16x2(x, g));
+}
+__device__ __forceinline__ float GateMul(float x, float g) { return x * SigmoidF(g); }
+
 // GatedDeltaRuleGates for one (token, value head) (CpuOps.Gating.cs): g = -exp(a_log) * softplus(a + dt_bias), with
 // softplus(x) = x above 20, and beta = sigmoid(b), in fp32. The gates op stores these; the GDN kernels' fused-gates
 // path uses them directly, so both paths compute bit-identical values.

@@ -31,6 +31,9 @@
 //   * single-token sequences of a prefill call run on the decode kernels, beside the tile kernel on the context's
 //     second stream when plan() finds that cheaper (ChooseOverlap); an f32 prefill runs every query token as a row of
 //     the f32 decode kernel.
+// Output gate (roost_amd_paged_attention_gated_run): Qwen3.5's SigmoidMul on the attention output, applied by every
+// kernel that stores an output element (decode, both prefill kernels, both merges) to the element already rounded to
+// the output type, with the SigmoidMul op's arithmetic (GateMul in common.h), so it equals run() then SigmoidMul.
 
 #include <algorithm>
 #include <cmath>
@@ -725,6 +728,7 @@ struct KvView {
   uint32_t head_shift;  // the kernels work on groups of kGroup query heads ("virtual" KV heads, q_heads / kGroup of
                         // them); virtual head v reads the K/V rows of real head v >> head_shift
   uint32_t vheads;      // q_heads / kGroup
+  const void* out_gate;  // the output gate ([tokens, q_heads * head_dim] in the output's type), or NULL for none
 };
 
 __device__ __forceinline__ uint32_t SeqKvLen(const KvView& kv, int32_t b, int32_t* p0) {
@@ -796,6 +800,18 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// The output gate (SigmoidMul folded into the epilogue): output element e, already rounded to the output type, times
+// sigmoid(gate[e]) with SigmoidMul's own arithmetic; unchanged without a gate. GateOut2 takes two packed bf16 pairs.
+__device__ __forceinline__ u32x2_t GateOut2(const void* gate, uint64_t e, u32x2_t v) {
+  if (gate == nullptr) return v;
+  const u32x2_t g = *reinterpret_cast<const u32x2_t*>(static_cast<const uint16_t*>(gate) + e);
+  return u32x2_t{GateMulBf16x2(v[0], g[0]), GateMulBf16x2(v[1], g[1])};
+}
+template <typename T>
+__device__ __forceinline__ T GateOut(const void* gate, uint64_t e, T v) {
+  return gate == nullptr ? v : GateMul(v, static_cast<const T*>(gate)[e]);
+}
 
 // 16-byte load with the non-temporal hint, for data read exactly once in whole cache lines per instruction (decode V:
 // 2 tokens x 512 contiguous bytes per wavefront load). Keeping such a stream out of the caches raises the rate of a
@@ -1306,7 +1322,7 @@ __global__ void __launch_bounds__(256, ROOST_DECODE_WGS_PER_CU) DecodeKernel(con
     const uint32_t qh = ((blockIdx.x % hblocks) * heads_per_wg + hk) * kGroup + h;
     if (split < 0) {
       const uint64_t row = tok * q_heads + qh;
-      out[row * D + d] = Vec<T>::Narrow(L > 0.0f ? o / L : 0.0f);
+      out[row * D + d] = GateOut<T>(kv.out_gate, row * D + d, Vec<T>::Narrow(L > 0.0f ? o / L : 0.0f));
       if (lse != nullptr && d == 0) lse[row] = L > 0.0f ? M + log2f(L) : -INFINITY;
     } else {
       const uint64_t prow = static_cast<uint64_t>(split) * q_heads + qh;
@@ -1329,7 +1345,8 @@ __global__ void __launch_bounds__(D) DecodeMergeKernel(T* __restrict__ out, floa
                                                        const DecodeMerge* __restrict__ merges,
                                                        const float* __restrict__ part_o,
                                                        const float* __restrict__ part_ml,
-                                                       const int32_t* __restrict__ q_rows, uint32_t q_heads) {
+                                                       const int32_t* __restrict__ q_rows, uint32_t q_heads,
+                                                       const void* out_gate) {
   __shared__ float f_lds[kMaxMergeSplits];
   __shared__ float inv_lds;
   const DecodeMerge mg = merges[blockIdx.x / q_heads];
@@ -1384,7 +1401,8 @@ __global__ void __launch_bounds__(D) DecodeMergeKernel(T* __restrict__ out, floa
   }
   for (int c = kPre; c < n; ++c) acc[c & 3] = fmaf(po[c * step], f_lds[c], acc[c & 3]);
   const float o0 = acc[0], o1 = acc[1], o2 = acc[2], o3 = acc[3];
-  out[(tok * q_heads + qh) * D + d] = Vec<T>::Narrow(((o0 + o1) + (o2 + o3)) * inv_lds);
+  const uint64_t e = (tok * q_heads + qh) * D + d;
+  out[e] = GateOut<T>(out_gate, e, Vec<T>::Narrow(((o0 + o1) + (o2 + o3)) * inv_lds));
 }
 
 // ---- Prefill kernel (bf16, head_dim 256, MFMA) -----------------------------------------------------------------------
@@ -1595,7 +1613,7 @@ __global__ void __launch_bounds__(256, 1)
         const int d = dt * 32 + i * 8 + hl * 4;
         const u32x2_t w{PackBf16(o[dt][i * 4] * inv, o[dt][i * 4 + 1] * inv),
                         PackBf16(o[dt][i * 4 + 2] * inv, o[dt][i * 4 + 3] * inv)};
-        *reinterpret_cast<u32x2_t*>(out + orow + d) = w;
+        *reinterpret_cast<u32x2_t*>(out + orow + d) = GateOut2(kv.out_gate, orow + d, w);
       }
     if (lse != nullptr && hl == 0) {
       lse[static_cast<uint64_t>(qbeg + q0 + col) * q_heads + head] = l_tot > 0.0f ? m_run + log2f(l_tot) : -INFINITY;
@@ -1968,7 +1986,7 @@ __global__ void __launch_bounds__(512, 1)
       const int d = dt * 32 + i * 8 + hl * 4;
       const u32x2_t v{PackRne(o[dt][i * 4] * inv, o[dt][i * 4 + 1] * inv),
                       PackRne(o[dt][i * 4 + 2] * inv, o[dt][i * 4 + 3] * inv)};
-      *reinterpret_cast<u32x2_t*>(out + orow + d) = v;
+      *reinterpret_cast<u32x2_t*>(out + orow + d) = GateOut2(kv.out_gate, orow + d, v);
     }
   if (lse != nullptr && hl == 0) {
     lse[static_cast<uint64_t>(qbeg + wk.q0 + r) * q_heads + head] = l_tot > 0.0f ? m_run + log2f(l_tot) : -INFINITY;
@@ -1982,11 +2000,13 @@ __global__ void __launch_bounds__(512, 1)
 constexpr int kPfMergeRows = 8;
 
 template <int D>
-__device__ __forceinline__ void MergeWrite(uint16_t* __restrict__ out, float* __restrict__ lse, uint64_t token,
-                                           uint32_t q_heads, uint32_t head, int d, float4 acc, float l, float mx) {
+__device__ __forceinline__ void MergeWrite(uint16_t* __restrict__ out, float* __restrict__ lse, const void* gate,
+                                           uint64_t token, uint32_t q_heads, uint32_t head, int d, float4 acc, float l,
+                                           float mx) {
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
   const u32x2_t v{PackBf16(acc.x * inv, acc.y * inv), PackBf16(acc.z * inv, acc.w * inv)};
-  *reinterpret_cast<u32x2_t*>(out + (token * q_heads + head) * D + d) = v;
+  const uint64_t e = (token * q_heads + head) * D + d;
+  *reinterpret_cast<u32x2_t*>(out + e) = GateOut2(gate, e, v);
   if (lse != nullptr && d == 0) lse[token * q_heads + head] = l > 0.0f ? mx + log2f(l) : -INFINITY;
 }
 
@@ -2002,7 +2022,8 @@ template <int D, int kRows>
 __device__ __forceinline__ void PrefillMergeRows(uint16_t* __restrict__ out, float* __restrict__ lse,
                                                  const PrefillMerge& mg, int r0, const uint16_t* __restrict__ part_o,
                                                  const float* __restrict__ part_ml,
-                                                 const int32_t* __restrict__ q_indptr, uint32_t q_heads) {
+                                                 const int32_t* __restrict__ q_indptr, uint32_t q_heads,
+                                                 const void* gate) {
   if (r0 >= mg.rows) return;
   const int hq = threadIdx.x / (D / 4);
   const int d = 4 * (threadIdx.x % (D / 4));
@@ -2040,7 +2061,7 @@ __device__ __forceinline__ void PrefillMergeRows(uint16_t* __restrict__ out, flo
           MergeAdd(acc, o[j][i], f);
         }
       }
-      MergeWrite<D>(out, lse, tok0 + r0 + j, q_heads, head, d, acc, l, mx);
+      MergeWrite<D>(out, lse, gate, tok0 + r0 + j, q_heads, head, d, acc, l, mx);
     }
   } else {  // any count, one token row per block; the piece loops are unrolled so several pieces' loads are in flight
     float mx = -INFINITY;
@@ -2057,7 +2078,7 @@ __device__ __forceinline__ void PrefillMergeRows(uint16_t* __restrict__ out, flo
         MergeAdd(acc, *reinterpret_cast<const u32x2_t*>(part_o + prow(i, r0) * D + d), f);
       }
     }
-    MergeWrite<D>(out, lse, tok0 + r0, q_heads, head, d, acc, l, mx);
+    MergeWrite<D>(out, lse, gate, tok0 + r0, q_heads, head, d, acc, l, mx);
   }
 }
 
@@ -2067,16 +2088,16 @@ template <int D>
 __global__ void __launch_bounds__(256)
     PrefillMergeKernel(uint16_t* __restrict__ out, float* __restrict__ lse, const PrefillMerge* __restrict__ merges,
                        const uint16_t* __restrict__ part_o, const float* __restrict__ part_ml,
-                       const int32_t* __restrict__ q_indptr, uint32_t q_heads, uint32_t two) {
+                       const int32_t* __restrict__ q_indptr, uint32_t q_heads, uint32_t two, const void* gate) {
   constexpr uint32_t kTwoBlocks = kPfTokens / kPfMergeRows;  // blocks per two-piece merge
   const uint32_t b = blockIdx.x;
   if (b < two * kTwoBlocks) {
     PrefillMergeRows<D, kPfMergeRows>(out, lse, merges[b / kTwoBlocks], static_cast<int>(b % kTwoBlocks) * kPfMergeRows,
-                                      part_o, part_ml, q_indptr, q_heads);
+                                      part_o, part_ml, q_indptr, q_heads, gate);
   } else {
     const uint32_t k = b - two * kTwoBlocks;
     PrefillMergeRows<D, 1>(out, lse, merges[two + k / kPfTokens], static_cast<int>(k % kPfTokens), part_o, part_ml,
-                           q_indptr, q_heads);
+                           q_indptr, q_heads, gate);
   }
 }
 
@@ -2108,7 +2129,7 @@ RoostStatus LaunchDecode(const RoostPagedAttentionParams& p, const PlanRecord& r
   ROOST_RETURN_IF_FAILED(roost::HipStatus(hipGetLastError(), "paged_attention", "decode launch"));
   if (rec.dec_merges == 0) return ROOST_STATUS_OK;
   hipLaunchKernelGGL((DecodeMergeKernel<T, D>), dim3(static_cast<uint32_t>(rec.dec_merges * p.q_heads)), dim3(D), 0,
-                     stream, out, lse, merges, part_o, part_ml, q_rows, p.q_heads);
+                     stream, out, lse, merges, part_o, part_ml, q_rows, p.q_heads, kv.out_gate);
   return roost::HipStatus(hipGetLastError(), "paged_attention", "decode merge launch");
 }
 
@@ -2149,13 +2170,13 @@ RoostStatus LaunchPrefill(const RoostPagedAttentionParams& p, const PlanRecord& 
     const dim3 g(two * (kPfTokens / kPfMergeRows) + rest * kPfTokens);
     if (p.head_dim == 64) {
       hipLaunchKernelGGL(PrefillMergeKernel<64>, g, block, 0, stream, outp, lsep, mg, part_o, part_ml, q_indptr,
-                         p.q_heads, two);
+                         p.q_heads, two, kv.out_gate);
     } else if (p.head_dim == 128) {
       hipLaunchKernelGGL(PrefillMergeKernel<128>, g, block, 0, stream, outp, lsep, mg, part_o, part_ml, q_indptr,
-                         p.q_heads, two);
+                         p.q_heads, two, kv.out_gate);
     } else {
       hipLaunchKernelGGL(PrefillMergeKernel<256>, g, block, 0, stream, outp, lsep, mg, part_o, part_ml, q_indptr,
-                         p.q_heads, two);
+                         p.q_heads, two, kv.out_gate);
     }
     return roost::HipStatus(hipGetLastError(), "paged_attention", "prefill merge launch");
   }
@@ -2269,8 +2290,12 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_plan(RoostContext* ctx, c
   });
 }
 
-extern "C" ROOST_API RoostStatus roost_paged_attention_run(RoostContext* ctx, const void* params,
-                                                           const RoostWorkspace* ws, void* stream) {
+namespace {
+
+// run() of an admitted-or-not call; out_gate (NULL for none) folds SigmoidMul into every kernel that writes an output
+// row.
+RoostStatus RunAttention(RoostContext* ctx, const void* params, const RoostWorkspace* ws, void* stream,
+                         const void* out_gate) {
   using namespace roost;
   Gate gate(kOp);
   ROOST_GATE_RETURN(gate.Header(params, sizeof(RoostPagedAttentionParams)));
@@ -2311,6 +2336,7 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_run(RoostContext* ctx, co
     kv.head_shift = HeadShift(p);
     kv.vheads = VirtualHeads(p);
     kv.hnd = p.kv_layout == ROOST_LAYOUT_PAGED_HND ? 1u : 0u;
+    kv.out_gate = out_gate;
     auto* dev = static_cast<unsigned char*>(ws->device);
     hipStream_t s = Stream(stream);
     if (p.mode == ROOST_ATTENTION_DECODE) {
@@ -2350,5 +2376,52 @@ extern "C" ROOST_API RoostStatus roost_paged_attention_run(RoostContext* ctx, co
     if (!side) return ROOST_STATUS_OK;
     ROOST_RETURN_IF_FAILED(HipStatus(hipEventRecord(ctx->join, ds), kOp, "join event"));
     return HipStatus(hipStreamWaitEvent(s, ctx->join, 0), kOp, "join wait");
+  });
+}
+
+}  // namespace
+
+extern "C" ROOST_API RoostStatus roost_paged_attention_run(RoostContext* ctx, const void* params,
+                                                           const RoostWorkspace* ws, void* stream) {
+  return RunAttention(ctx, params, ws, stream, nullptr);
+}
+
+// PagedAttention followed by SigmoidMul on its output, in one call: the gate multiplies each output element where the
+// kernels write it (the tile, decode and merge kernels' epilogues), with SigmoidMul's arithmetic on the output already
+// rounded to its type, so the result equals run() then roost_sigmoid_mul_run bit for bit and the output is written once.
+extern "C" ROOST_API RoostStatus roost_amd_paged_attention_gated_run(RoostContext* ctx, const void* params,
+                                                                     const void* gate_params, const RoostWorkspace* ws,
+                                                                     void* stream) {
+  using namespace roost;
+  Gate gate(kOp);
+  ROOST_GATE_RETURN(gate.Header(params, sizeof(RoostPagedAttentionParams)));
+  gate.Expect(gate_params != nullptr, ROOST_STATUS_INVALID_ARGUMENT, "no SigmoidMul params struct was passed");
+  ROOST_GATE_RETURN(gate);
+  ROOST_GATE_RETURN(gate.Header(gate_params, sizeof(RoostSigmoidMulParams)));
+  const auto& p = *Params(params);
+  const auto& sm = *static_cast<const RoostSigmoidMulParams*>(gate_params);
+  return CatchAll(kOp, [&]() -> RoostStatus {
+    ROOST_RETURN_IF_FAILED(Admit(p, true));
+    const uint32_t dt = p.output.dtype;
+    const uint64_t dim = static_cast<uint64_t>(p.q_heads) * p.head_dim, n = dim * p.tokens;
+    gate.Expect(sm.rows == p.tokens && sm.dim == dim, ROOST_STATUS_INVALID_ARGUMENT,
+                "the gate covers %u rows x %u; the attention output is %u tokens x %llu", sm.rows, sm.dim, p.tokens,
+                static_cast<unsigned long long>(dim))
+        .Expect(sm.input.address == p.output.address && sm.output.address == p.output.address,
+                ROOST_STATUS_INVALID_ARGUMENT,
+                "the gate applies in place: its input and output must both be the attention output (%p), not %p and %p",
+                p.output.address, sm.input.address, sm.output.address)
+        .Tensor("gate input", sm.input, dt, n)
+        .Tensor("gate output", sm.output, dt, n)
+        .Tensor("gate", sm.gate, dt, n)
+        .Aligned("gate", sm.gate.address, 8);
+    ROOST_GATE_RETURN(gate);
+    const auto g0 = reinterpret_cast<uintptr_t>(sm.gate.address), o0 = reinterpret_cast<uintptr_t>(p.output.address);
+    const uint64_t bytes = n * ElementBytes(dt);
+    gate.Expect(n == 0 || g0 + bytes <= o0 || o0 + bytes <= g0, ROOST_STATUS_INVALID_ARGUMENT,
+                "the gate (%p) overlaps the output (%p, %llu bytes)", sm.gate.address, p.output.address,
+                static_cast<unsigned long long>(bytes));
+    ROOST_GATE_RETURN(gate);
+    return RunAttention(ctx, params, ws, stream, sm.gate.address);
   });
 }
