@@ -82,6 +82,22 @@ ROOST_API RoostStatus roost_amd_gdn_recurrent_run_noalloc(RoostContext* ctx, con
 ROOST_API RoostStatus roost_amd_gdn_recurrent_gated_run(RoostContext* ctx, const void* params, const void* gates,
                                                          const RoostWorkspace* ws, void* stream);
 
+/* One decode step of a Gated DeltaNet layer in one call: CausalConv1d, GatedDeltaRuleGates, the recurrent GatedDeltaRule
+ * and GatedRmsNorm. No counterpart in the reference, whose Qwen3.5 worker runs the four ops one after another
+ * (Qwen35EagerModel.cs:89-92 lists them; semantics CpuOps.Hybrid.cs:30-157, 160-263 and CpuOps.Gating.cs:21-83). The
+ * norm's output, the recurrent states and the convolution states equal the four calls' bit for bit; the convolution's
+ * output and the GDN output are not written (their spans are only checked). `conv_params` is a RoostCausalConv1dParams
+ * over bf16 activations with at most 4 taps and the GDN call's batch, tokens and cu_seqlens; `gdn_params` a
+ * RoostGatedDeltaRuleParams whose q, k and v are column views of the convolution's output (row stride = channels) and
+ * whose cu_seqlens_host is given: every sequence must be shorter than 16 tokens (longer ones run on the chunk kernels in
+ * the recurrent variant), else UNSUPPORTED; `gates_params` a RoostGatedDeltaRuleGatesParams as for
+ * roost_amd_gdn_recurrent_gated_run, or NULL to read g and beta from the GDN params; `norm_params` a
+ * RoostGatedRmsNormParams of bf16 rows = tokens x v_heads, dim = 128, whose input is the GDN output, with input, gate and
+ * output 16-byte aligned, and whose output overlaps none of the layer's other inputs or states. No workspace. */
+ROOST_API RoostStatus roost_amd_gdn_decode_layer_run(RoostContext* ctx, const void* conv_params,
+                                                      const void* gates_params, const void* gdn_params,
+                                                      const void* norm_params, void* stream);
+
 /* The Gated DeltaNet layer's neighbour ops, each flagged GRAPH_CAPTURABLE | DETERMINISTIC | BATCH_INVARIANT, no plan
  * and no workspace:
  * GatedDeltaRuleGates, variant "gated-delta-rule-gates-gfx950" -- replaces roost_gated_delta_rule_gates_run

@@ -107,6 +107,8 @@ class KernelLibrary:
         self.dll.roost_amd_paged_attention_gated_run.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                                                  C.c_void_p]
         self.dll.roost_amd_paged_attention_gated_run.restype = C.c_int32
+        self.dll.roost_amd_gdn_decode_layer_run.argtypes = [C.c_void_p] * 6
+        self.dll.roost_amd_gdn_decode_layer_run.restype = C.c_int32
         self.dll.roost_amd_plan_region_from_step.argtypes = [C.c_void_p, C.c_uint64, C.POINTER(abi.StepTables)]
         self.dll.roost_amd_plan_region_from_step.restype = C.c_int32
         version = self.dll.roost_abi_version()
@@ -488,6 +490,16 @@ def paged_attention_gated(session: OpSession, attn_params, gate_params, key="gat
                                                                  C.c_void_p(session.stream_handle))
     if status != abi.OK:
         raise KernelError("paged_attention_gated", status, session.lib.last_error())
+
+
+def gdn_decode_layer(session: OpSession, conv_params, gates_params, gdn_params, norm_params) -> None:
+    """roost_amd_gdn_decode_layer_run: CausalConv1d, GatedDeltaRuleGates (gates_params may be None: g and beta are then
+    read from gdn_params), the recurrent GatedDeltaRule and GatedRmsNorm of one decode step in one call."""
+    status = session.lib.dll.roost_amd_gdn_decode_layer_run(
+        session.ctx, C.addressof(conv_params), C.addressof(gates_params) if gates_params is not None else None,
+        C.addressof(gdn_params), C.addressof(norm_params), C.c_void_p(session.stream_handle))
+    if status != abi.OK:
+        raise KernelError("gdn_decode_layer", status, session.lib.last_error())
 
 
 def gated_rms_norm(session: OpSession, *args, **kwargs) -> None:

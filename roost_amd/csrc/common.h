@@ -60,6 +60,8 @@ __device__ __forceinline__ float LoadF(const void* p, uint32_t dt, int64_t i) {
 
 // sigmoid with the hardware reciprocal (v_rcp_f32, about 1 ulp) instead of a full-precision divide.
 __device__ __forceinline__ float SigmoidF(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+// SiLU, x * sigmoid(x), with the same reciprocal; the conv and gated-norm kernels and the fused GDN layer share it.
+__device__ __forceinline__ float SiluF(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
 // SigmoidMul's arithmetic (CpuOps.Gating.cs, out = x * sigmoid(gate)): each element in fp32, rounded once to the
 // element type. The SigmoidMul op and the attention kernels' gated epilogue both use these, so the fused and the

@@ -23,6 +23,7 @@
 #include <mutex>
 
 #include "common.h"
+#include "gdn_layer.h"
 
 namespace {
 
@@ -209,6 +210,120 @@ __device__ __forceinline__ float QuadSum(float x) {
 constexpr uint32_t kRecQuarters = 4;
 constexpr uint32_t kRecThreads = 256;
 
+// One token of the recurrence for one thread's share of a (sequence, value head): rows row0 .. + 3 and kC value
+// columns of S, in groups of 4: group m of lane cg is columns 32 m + 4 cg .. + 3 (so the 8 lanes of a row group cover
+// whole 128-byte rows of S per access), from the token's q and k elements
+// 2 lane, 2 lane + 1 (the norms), rows row0 .. + 3 of q and k, the kC columns of v and the token's gates; red_sk and
+// red_o are the [4 wavefronts][8 kC] LDS reduction arrays of the columns' workgroup (two workgroup barriers). Lanes with
+// w == 0 and rg == 0 receive their kC output columns. Every column sees the same operations in the same order whatever
+// kC is, so the recurrent kernel (kC = 4) and the decode-layer kernel (kC = 16) agree bit for bit.
+template <int kC>
+__device__ __forceinline__ void RecurrentStep(float (&s)[4][kC], const float (&q2)[2], const float (&k2)[2],
+                                              const float (&q4)[4], float (&k4)[4], const float (&vv)[kC], float graw,
+                                              float beta, float scale, int w, int rg, int cg, float (*red_sk)[8 * kC],
+                                              float (*red_o)[8 * kC], float (&ot)[kC]) {
+  static_assert(kC % 4 == 0, "columns go through LDS as float4");
+  const float decay = expf(graw);
+  float qq = fmaf(q2[0], q2[0], q2[1] * q2[1]), kk = fmaf(k2[0], k2[0], k2[1] * k2[1]);
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    qq += __shfl_xor(qq, o, 64);
+    kk += __shfl_xor(kk, o, 64);
+  }
+  const float qn = scale / sqrtf(qq + 1e-6f);
+  const float kn = 1.0f / sqrtf(kk + 1e-6f);
+  // S^T k: this lane's 4 rows, the row group's 32, then the workgroup's 128 through LDS.
+  float sk[kC];
+#pragma unroll
+  for (int c = 0; c < kC; ++c) sk[c] = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    k4[i] *= kn;
+#pragma unroll
+    for (int c = 0; c < kC; ++c) sk[c] = fmaf(s[i][c], k4[i], sk[c]);
+  }
+#pragma unroll
+  for (int c = 0; c < kC; ++c) sk[c] = OctSum(sk[c]);
+  if (rg == 0) {
+#pragma unroll
+    for (int c = 0; c < kC; c += 4)
+      *reinterpret_cast<float4*>(&red_sk[w][8 * c + 4 * cg]) = make_float4(sk[c], sk[c + 1], sk[c + 2], sk[c + 3]);
+  }
+  __syncthreads();
+  float d[kC];
+#pragma unroll
+  for (int c = 0; c < kC; c += 4) {
+    float4 tot = *reinterpret_cast<const float4*>(&red_sk[0][8 * c + 4 * cg]);
+#pragma unroll
+    for (int ww = 1; ww < 4; ++ww) {
+      const float4 x = *reinterpret_cast<const float4*>(&red_sk[ww][8 * c + 4 * cg]);
+      tot = make_float4(tot.x + x.x, tot.y + x.y, tot.z + x.z, tot.w + x.w);
+    }
+    d[c] = beta * (vv[c] - decay * tot.x);
+    d[c + 1] = beta * (vv[c + 1] - decay * tot.y);
+    d[c + 2] = beta * (vv[c + 2] - decay * tot.z);
+    d[c + 3] = beta * (vv[c + 3] - decay * tot.w);
+  }
+  float o[kC];
+#pragma unroll
+  for (int c = 0; c < kC; ++c) o[c] = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float ki = k4[i], qi = q4[i] * qn;
+#pragma unroll
+    for (int c = 0; c < kC; ++c) s[i][c] = fmaf(s[i][c], decay, ki * d[c]);
+#pragma unroll
+    for (int c = 0; c < kC; ++c) o[c] = fmaf(s[i][c], qi, o[c]);
+  }
+#pragma unroll
+  for (int c = 0; c < kC; ++c) o[c] = OctSum(o[c]);
+  if (rg == 0) {
+#pragma unroll
+    for (int c = 0; c < kC; c += 4)
+      *reinterpret_cast<float4*>(&red_o[w][8 * c + 4 * cg]) = make_float4(o[c], o[c + 1], o[c + 2], o[c + 3]);
+  }
+  __syncthreads();
+  if (w == 0 && rg == 0) {
+#pragma unroll
+    for (int c = 0; c < kC; c += 4) {
+      float4 t = *reinterpret_cast<const float4*>(&red_o[0][8 * c + 4 * cg]);
+#pragma unroll
+      for (int ww = 1; ww < 4; ++ww) {
+        const float4 x = *reinterpret_cast<const float4*>(&red_o[ww][8 * c + 4 * cg]);
+        t = make_float4(t.x + x.x, t.y + x.y, t.z + x.z, t.w + x.w);
+      }
+      ot[c] = t.x;
+      ot[c + 1] = t.y;
+      ot[c + 2] = t.z;
+      ot[c + 3] = t.w;
+    }
+  }
+}
+
+// The state rows row0 .. + 3 of a lane's kC columns (groups of 4 at sp + 32 m, row stride kDim), as fp32 streams that
+// skip the caches.
+template <int kC>
+__device__ __forceinline__ void LoadStateRows(const float* sp, int row0, float (&s)[4][kC]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int c = 0; c < kC; c += 4) {
+      const float4 v = LoadStreamF4(sp + (row0 + i) * kDim + 8 * c);
+      s[i][c] = v.x;
+      s[i][c + 1] = v.y;
+      s[i][c + 2] = v.z;
+      s[i][c + 3] = v.w;
+    }
+}
+template <int kC>
+__device__ __forceinline__ void StoreStateRows(float* sp, int row0, const float (&s)[4][kC]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int c = 0; c < kC; c += 4)
+      StoreStreamF4(sp + (row0 + i) * kDim + 8 * c, make_float4(s[i][c], s[i][c + 1], s[i][c + 2], s[i][c + 3]));
+}
+
 // Workgroup (sequence b, value head h, column quarter): the token-serial recurrence with its share of S in registers.
 template <bool kVec>
 __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint32_t h, uint32_t quarter) {
@@ -225,14 +340,15 @@ __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint
   const int row0 = 32 * w + 4 * rg;
   const uint32_t col = 32 * quarter + 4 * cg;
   const uint32_t kh = h / a.group;
-  float4 s[4];
+  float s[4][4];
   float* sp = has_slot ? a.state + (static_cast<uint64_t>(slot) * a.vh + h) * kDim * kDim + col : nullptr;
   if (has_slot && a.use_initial_state) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) s[i] = LoadStreamF4(sp + (row0 + i) * kDim);
+    LoadStateRows<4>(sp, row0, s);
   } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) s[i][c] = 0.f;
   }
   for (int32_t tok = t0; tok < t1; ++tok) {
     const uint16_t* qrow = a.q + static_cast<uint64_t>(tok) * a.q_stride + kh * kDim;
@@ -265,71 +381,16 @@ __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint
     }
     float graw, beta;
     GateAt(a, static_cast<uint64_t>(tok), h, graw, beta);
-    const float decay = expf(graw);
-    float qq = fmaf(q2[0], q2[0], q2[1] * q2[1]), kk = fmaf(k2[0], k2[0], k2[1] * k2[1]);
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      qq += __shfl_xor(qq, o, 64);
-      kk += __shfl_xor(kk, o, 64);
-    }
-    const float qn = a.scale / sqrtf(qq + 1e-6f);
-    const float kn = 1.0f / sqrtf(kk + 1e-6f);
-    // S^T k: this lane's 4 rows, the row group's 32, then the workgroup's 128 through LDS.
-    float sk[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      k4[i] *= kn;
-      sk[0] = fmaf(s[i].x, k4[i], sk[0]);
-      sk[1] = fmaf(s[i].y, k4[i], sk[1]);
-      sk[2] = fmaf(s[i].z, k4[i], sk[2]);
-      sk[3] = fmaf(s[i].w, k4[i], sk[3]);
-    }
-#pragma unroll
-    for (int c = 0; c < 4; ++c) sk[c] = OctSum(sk[c]);
-    if (rg == 0) *reinterpret_cast<float4*>(&red_sk[w][4 * cg]) = make_float4(sk[0], sk[1], sk[2], sk[3]);
-    __syncthreads();
-    float4 tot = *reinterpret_cast<const float4*>(&red_sk[0][4 * cg]);
-#pragma unroll
-    for (int ww = 1; ww < 4; ++ww) {
-      const float4 x = *reinterpret_cast<const float4*>(&red_sk[ww][4 * cg]);
-      tot = make_float4(tot.x + x.x, tot.y + x.y, tot.z + x.z, tot.w + x.w);
-    }
-    const float d[4] = {beta * (vv[0] - decay * tot.x), beta * (vv[1] - decay * tot.y),
-                        beta * (vv[2] - decay * tot.z), beta * (vv[3] - decay * tot.w)};
-    float o[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float ki = k4[i], qi = q4[i] * qn;
-      s[i].x = fmaf(s[i].x, decay, ki * d[0]);
-      s[i].y = fmaf(s[i].y, decay, ki * d[1]);
-      s[i].z = fmaf(s[i].z, decay, ki * d[2]);
-      s[i].w = fmaf(s[i].w, decay, ki * d[3]);
-      o[0] = fmaf(s[i].x, qi, o[0]);
-      o[1] = fmaf(s[i].y, qi, o[1]);
-      o[2] = fmaf(s[i].z, qi, o[2]);
-      o[3] = fmaf(s[i].w, qi, o[3]);
-    }
-#pragma unroll
-    for (int c = 0; c < 4; ++c) o[c] = OctSum(o[c]);
-    if (rg == 0) *reinterpret_cast<float4*>(&red_o[w][4 * cg]) = make_float4(o[0], o[1], o[2], o[3]);
-    __syncthreads();
+    float ot[4];
+    RecurrentStep<4>(s, q2, k2, q4, k4, vv, graw, beta, a.scale, w, rg, cg, red_sk, red_o, ot);
     if (w == 0 && rg == 0) {
-      float4 ot = *reinterpret_cast<const float4*>(&red_o[0][4 * cg]);
-#pragma unroll
-      for (int ww = 1; ww < 4; ++ww) {
-        const float4 x = *reinterpret_cast<const float4*>(&red_o[ww][4 * cg]);
-        ot = make_float4(ot.x + x.x, ot.y + x.y, ot.z + x.z, ot.w + x.w);
-      }
       uint2 pw;
-      pw.x = PackBf16(ot.x, ot.y);
-      pw.y = PackBf16(ot.z, ot.w);
+      pw.x = PackBf16(ot[0], ot[1]);
+      pw.y = PackBf16(ot[2], ot[3]);
       *reinterpret_cast<uint2*>(a.out + (static_cast<uint64_t>(tok) * a.vh + h) * kDim + col) = pw;
     }
   }
-  if (has_slot) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) StoreStreamF4(sp + (row0 + i) * kDim, s[i]);
-  }
+  if (has_slot) StoreStateRows<4>(sp, row0, s);
 }
 
 template <bool kVec>
@@ -378,6 +439,195 @@ RoostStatus LaunchRecurrent(const RoostGatedDeltaRuleParams& p, hipStream_t stre
     hipLaunchKernelGGL(RecurrentKernel<false>, grid, dim3(kRecThreads), 0, stream, a);
   }
   return roost::HipStatus(hipGetLastError(), kOp, "recurrent launch");
+}
+
+// ---- Decode layer: CausalConv1d + gates + recurrence + GatedRmsNorm in one kernel ------------------------------------
+//
+// One workgroup of 256 threads per (sequence, value head): lane (rg, cg) of wavefront w holds state rows
+// 32 w + 4 rg .. + 3 of columns 32 m + 4 cg .. + 3, m = 0 .. 3 (64 floats), and runs RecurrentStep<16>, which treats each column exactly
+// as the recurrent kernel's RecurrentStep<4> does. The workgroup convolves the token's q, k and v itself from the
+// layer's projection (CausalConv1d's arithmetic: bias, then the taps oldest first with fmaf, SiLU, rounded to bf16),
+// computes the gates where they are read, and normalises the token's 128 outputs (rounded to bf16, as the GDN op
+// stores them) on 16 lanes with GatedRmsNorm's single-pass arithmetic (8 columns per lane, squares summed in column
+// order, then over the lanes by xor 1, 2, 4, 8). The results equal the four ops' bit for bit; neither the
+// convolution's nor the GDN op's output is written. With one value head per key head a workgroup owns the channels it
+// convolves and updates their convolution state itself at the end, as the conv op's state kernel does; with more,
+// value heads share q and k channels, and that state kernel runs afterwards instead.
+struct LayerArgs {
+  GdnArgs a;                  // the recurrence; its q, k, v and out are not used
+  const uint16_t* x;          // the convolution's input [tokens, channels] (bf16)
+  const uint16_t* conv_w;     // [channels, width]
+  const uint16_t* conv_b;     // [channels], or NULL
+  void* conv_state;           // [slots, channels, width - 1]
+  const int32_t* conv_slots;  // [batch]
+  uint64_t conv_pool_slots;
+  uint32_t conv_state_t, channels, width, silu;
+  uint32_t conv_state_update;  // nonzero: the workgroup updates its channels' convolution state
+  uint32_t cq, ck, cv;        // the channels of element 0 of q, k and v head 0
+  const uint16_t* z;          // GatedRmsNorm's gate [tokens * v_heads, 128]
+  const void* norm_w;         // [128]
+  uint32_t norm_w_t;
+  float eps;
+  uint16_t* y;                // GatedRmsNorm's output [tokens * v_heads, 128]
+};
+
+constexpr uint32_t kLayerThreads = 256;
+constexpr int kLayerCols = 16;            // state columns per lane
+constexpr uint32_t kLayerMaxWidth = 4;
+constexpr int kLayerConvPerThread = 2;    // 3 x 128 channels over 256 threads
+
+__global__ void __launch_bounds__(kLayerThreads) GdnDecodeLayerKernel(LayerArgs L) {
+  const GdnArgs& a = L.a;
+  __shared__ float red_sk[4][8 * kLayerCols], red_o[4][8 * kLayerCols];
+  __shared__ __align__(16) uint16_t xin[3 * kDim];  // this token's q, k and v, as the convolution rounds them
+  __shared__ __align__(16) uint16_t ob[kDim];       // its outputs, as the GDN op rounds them
+  const uint32_t b = blockIdx.x, h = blockIdx.y;
+  const int32_t t0 = a.cu[b], t1 = a.cu[b + 1];
+  if (t1 <= t0) return;  // an empty sequence leaves its slots untouched
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int rg = lane & 7, cg = lane >> 3;
+  const int row0 = 32 * w + 4 * rg;
+  const int col = 4 * cg;  // the lane's first column; group m starts at col + 32 m
+  const uint32_t kh = h / a.group;
+  const int32_t slot = a.slots[b];
+  const bool has_slot = slot >= 0 && static_cast<uint64_t>(slot) < a.pool_slots;
+  float s[4][kLayerCols] = {};
+  float* sp = has_slot ? a.state + (static_cast<uint64_t>(slot) * a.vh + h) * kDim * kDim + col : nullptr;
+  if (has_slot && a.use_initial_state) LoadStateRows<kLayerCols>(sp, row0, s);
+  // Channel j (0 .. 383) of the token: element j % 128 of q (key head kh), k (key head kh) or v (value head h);
+  // thread tid convolves channels tid and tid + 256.
+  const int sl = static_cast<int>(L.width) - 1;
+  const int32_t cslot = L.conv_slots[b];
+  const bool cslot_ok = cslot >= 0 && static_cast<uint64_t>(cslot) < L.conv_pool_slots;
+  uint32_t cc[kLayerConvPerThread];
+  float cw[kLayerConvPerThread][kLayerMaxWidth] = {}, cb[kLayerConvPerThread] = {};
+#pragma unroll
+  for (int u = 0; u < kLayerConvPerThread; ++u) {
+    const int j = tid + u * static_cast<int>(kLayerThreads), part = j / static_cast<int>(kDim);
+    cc[u] = (part == 0 ? L.cq + kh * kDim : part == 1 ? L.ck + kh * kDim : L.cv + h * kDim) + j % kDim;
+    if (j < 3 * static_cast<int>(kDim)) {
+#pragma unroll
+      for (int k = 0; k < static_cast<int>(kLayerMaxWidth); ++k)
+        if (k < static_cast<int>(L.width)) cw[u][k] = Bf16ToF32(L.conv_w[static_cast<uint64_t>(cc[u]) * L.width + k]);
+      if (L.conv_b != nullptr) cb[u] = Bf16ToF32(L.conv_b[cc[u]]);
+    }
+  }
+  for (int32_t tok = t0; tok < t1; ++tok) {
+    const int32_t rel = tok - t0;  // entry rel + k of [state, sequence] is tap k of this token
+#pragma unroll
+    for (int u = 0; u < kLayerConvPerThread; ++u) {
+      const int j = tid + u * static_cast<int>(kLayerThreads);
+      if (j < 3 * static_cast<int>(kDim)) {
+        float acc = cb[u];
+#pragma unroll
+        for (int k = 0; k < static_cast<int>(kLayerMaxWidth); ++k) {
+          if (k < static_cast<int>(L.width)) {
+            const int32_t hi = rel + k;
+            float tap;
+            if (hi < sl) {
+              tap = cslot_ok ? LoadF(L.conv_state, L.conv_state_t,
+                                     static_cast<int64_t>((static_cast<uint64_t>(cslot) * L.channels + cc[u]) * sl + hi))
+                             : 0.0f;
+            } else {
+              tap = Bf16ToF32(L.x[static_cast<uint64_t>(t0 + hi - sl) * L.channels + cc[u]]);
+            }
+            acc = fmaf(cw[u][k], tap, acc);
+          }
+        }
+        xin[j] = F32ToBf16(L.silu ? SiluF(acc) : acc);
+      }
+    }
+    // The norm's gate for this token, requested before the recurrence runs.
+    uint4 zq = make_uint4(0, 0, 0, 0);
+    const uint64_t row = static_cast<uint64_t>(tok) * a.vh + h;
+    if (tid < 16) zq = *reinterpret_cast<const uint4*>(L.z + row * kDim + 8 * tid);
+    __syncthreads();
+    const uint16_t* qv = xin;
+    const uint16_t* kv = xin + kDim;
+    const uint16_t* vv16 = xin + 2 * kDim;
+    float q2[2], k2[2], q4[4], k4[4], vv[kLayerCols];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      q2[i] = Bf16ToF32(qv[2 * lane + i]);
+      k2[i] = Bf16ToF32(kv[2 * lane + i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      q4[i] = Bf16ToF32(qv[row0 + i]);
+      k4[i] = Bf16ToF32(kv[row0 + i]);
+    }
+#pragma unroll
+    for (int c = 0; c < kLayerCols; ++c) vv[c] = Bf16ToF32(vv16[col + 8 * (c & ~3) + (c & 3)]);
+    float graw, beta;
+    GateAt(a, static_cast<uint64_t>(tok), h, graw, beta);
+    float ot[kLayerCols];
+    RecurrentStep<kLayerCols>(s, q2, k2, q4, k4, vv, graw, beta, a.scale, w, rg, cg, red_sk, red_o, ot);
+    if (w == 0 && rg == 0) {
+#pragma unroll
+      for (int c = 0; c < kLayerCols; c += 4) {
+        *reinterpret_cast<uint2*>(&ob[col + 8 * c]) =
+            make_uint2(PackBf16(ot[c], ot[c + 1]), PackBf16(ot[c + 2], ot[c + 3]));
+      }
+    }
+    __syncthreads();
+    if (tid < 16) {  // the norm of row (tok, h): lane tid holds columns 8 tid .. 8 tid + 7
+      const int c0 = 8 * tid;
+      const uint4 xq = *reinterpret_cast<const uint4*>(&ob[c0]);
+      const uint32_t* xw = reinterpret_cast<const uint32_t*>(&xq);
+      const uint32_t* zw = reinterpret_cast<const uint32_t*>(&zq);
+      float xv[8], gv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        xv[e] = (e & 1) ? Bf16HiToF32(xw[e >> 1]) : Bf16LoToF32(xw[e >> 1]);
+        gv[e] = (e & 1) ? Bf16HiToF32(zw[e >> 1]) : Bf16LoToF32(zw[e >> 1]);
+      }
+      float ss = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(xv[e], xv[e], ss);
+#pragma unroll
+      for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, 64);
+      const float inv = rsqrtf(ss / static_cast<float>(kDim) + L.eps);
+      uint32_t yw[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float y0 = xv[2 * q] * inv * LoadF(L.norm_w, L.norm_w_t, c0 + 2 * q) * SiluF(gv[2 * q]);
+        const float y1 = xv[2 * q + 1] * inv * LoadF(L.norm_w, L.norm_w_t, c0 + 2 * q + 1) * SiluF(gv[2 * q + 1]);
+        yw[q] = PackBf16Rne(y0, y1);
+      }
+      *reinterpret_cast<uint4*>(L.y + row * kDim + c0) = make_uint4(yw[0], yw[1], yw[2], yw[3]);
+    }
+  }
+  if (has_slot) StoreStateRows<kLayerCols>(sp, row0, s);
+  if (L.conv_state_update != 0 && cslot_ok && sl > 0) {
+    // The slot keeps the last width - 1 entries of [state, sequence]: all of a channel's entries are read (some may
+    // be old state entries) before any is written, by the one thread that owns the channel.
+    const int32_t n = t1 - t0;
+#pragma unroll
+    for (int u = 0; u < kLayerConvPerThread; ++u) {
+      const int j = tid + u * static_cast<int>(kLayerThreads);
+      if (j >= 3 * static_cast<int>(kDim)) continue;
+      const uint64_t so = (static_cast<uint64_t>(cslot) * L.channels + cc[u]) * sl;
+      float next[kLayerMaxWidth - 1];
+#pragma unroll
+      for (int e = 0; e < static_cast<int>(kLayerMaxWidth) - 1; ++e) {
+        if (e < sl) {
+          const int32_t hi = n + e;
+          next[e] = hi < sl ? LoadF(L.conv_state, L.conv_state_t, static_cast<int64_t>(so + hi))
+                            : Bf16ToF32(L.x[static_cast<uint64_t>(t0 + hi - sl) * L.channels + cc[u]]);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < static_cast<int>(kLayerMaxWidth) - 1; ++e) {
+        if (e < sl) {
+          if (L.conv_state_t == ROOST_DTYPE_BF16) {
+            static_cast<uint16_t*>(L.conv_state)[so + e] = F32ToBf16(next[e]);
+          } else {
+            static_cast<float*>(L.conv_state)[so + e] = next[e];
+          }
+        }
+      }
+    }
+  }
 }
 
 // ---- Chunk variant: WY form on MFMA ---------------------------------------------------------------------------------
@@ -1435,6 +1685,41 @@ RoostStatus LaunchRouted(const RoostGatedDeltaRuleParams& p, uint8_t* base, cons
   return LaunchChunk(p, &ws, l, l.max_chunks, s, fold, /*with_recurrent=*/true, gs);
 }
 
+// The GatedDeltaRuleGates inputs of a call that folds the gates in, checked against the (admitted) GDN call.
+RoostStatus GateSourceOf(const RoostGatedDeltaRuleGatesParams& gp, const RoostGatedDeltaRuleParams& p, GateSource* gs) {
+  roost::Gate gate(kOp);
+  gate.Expect(gp.tokens == p.tokens && gp.v_heads == p.v_heads, ROOST_STATUS_INVALID_ARGUMENT,
+              "the gates cover %u tokens x %u heads; the call has %u x %u", gp.tokens, gp.v_heads, p.tokens, p.v_heads);
+  ROOST_GATE_RETURN(gate);
+  auto float_span = [&](const char* name, const RoostDeviceSpan& sp, uint64_t elements) {
+    gate.Expect(sp.dtype == ROOST_DTYPE_BF16 || sp.dtype == ROOST_DTYPE_F32, ROOST_STATUS_UNSUPPORTED,
+                "%s is %s; the gates read bf16 or f32", name, roost::Describe(sp.dtype).name);
+    if (gate.ok()) gate.Tensor(name, sp, sp.dtype, elements).Aligned(name, sp.address, roost::ElementBytes(sp.dtype));
+  };
+  const uint64_t as = gp.a_stride == 0 ? gp.v_heads : gp.a_stride, bs = gp.b_stride == 0 ? gp.v_heads : gp.b_stride;
+  gate.Expect(as >= gp.v_heads && bs >= gp.v_heads, ROOST_STATUS_INVALID_ARGUMENT,
+              "a_stride %llu, b_stride %llu: rows hold %u heads", static_cast<unsigned long long>(as),
+              static_cast<unsigned long long>(bs), gp.v_heads);
+  const uint64_t t = gp.tokens;
+  float_span("a", gp.a, t == 0 ? 0 : (t - 1) * as + gp.v_heads);
+  float_span("b", gp.b, t == 0 ? 0 : (t - 1) * bs + gp.v_heads);
+  float_span("a_log", gp.a_log, gp.v_heads);
+  float_span("dt_bias", gp.dt_bias, gp.v_heads);
+  ROOST_GATE_RETURN(gate);
+  gs->a = gp.a.address;
+  gs->b = gp.b.address;
+  gs->a_log = gp.a_log.address;
+  gs->dt_bias = gp.dt_bias.address;
+  gs->a_t = gp.a.dtype;
+  gs->b_t = gp.b.dtype;
+  gs->alog_t = gp.a_log.dtype;
+  gs->dtb_t = gp.dt_bias.dtype;
+  gs->a_stride = as;
+  gs->b_stride = bs;
+  if (t > 0 && gs->a == nullptr) return roost::Report(ROOST_STATUS_INVALID_ARGUMENT, kOp, "a: address is NULL");
+  return ROOST_STATUS_OK;
+}
+
 // The recurrent variant's run() over its admitted call, with g and beta read from the call or computed from gs.
 RoostStatus RecurrentRun(const RoostGatedDeltaRuleParams& p, const RoostWorkspace* ws, hipStream_t s,
                          const GateSource& gs) {
@@ -1499,38 +1784,135 @@ extern "C" ROOST_API RoostStatus roost_amd_gdn_recurrent_gated_run(RoostContext*
   const auto& gp = *static_cast<const RoostGatedDeltaRuleGatesParams*>(gates);
   return roost::CatchAll(kOp, [&]() -> RoostStatus {
     ROOST_RETURN_IF_FAILED(Admit(p, false, /*fused_gates=*/true));
-    gate.Expect(gp.tokens == p.tokens && gp.v_heads == p.v_heads, ROOST_STATUS_INVALID_ARGUMENT,
-                "the gates cover %u tokens x %u heads; the call has %u x %u", gp.tokens, gp.v_heads, p.tokens,
-                p.v_heads);
-    ROOST_GATE_RETURN(gate);
-    auto float_span = [&](const char* name, const RoostDeviceSpan& sp, uint64_t elements) {
-      gate.Expect(sp.dtype == ROOST_DTYPE_BF16 || sp.dtype == ROOST_DTYPE_F32, ROOST_STATUS_UNSUPPORTED,
-                  "%s is %s; the gates read bf16 or f32", name, roost::Describe(sp.dtype).name);
-      if (gate.ok()) gate.Tensor(name, sp, sp.dtype, elements).Aligned(name, sp.address, roost::ElementBytes(sp.dtype));
-    };
-    const uint64_t as = gp.a_stride == 0 ? gp.v_heads : gp.a_stride, bs = gp.b_stride == 0 ? gp.v_heads : gp.b_stride;
-    gate.Expect(as >= gp.v_heads && bs >= gp.v_heads, ROOST_STATUS_INVALID_ARGUMENT,
-                "a_stride %llu, b_stride %llu: rows hold %u heads", static_cast<unsigned long long>(as),
-                static_cast<unsigned long long>(bs), gp.v_heads);
-    const uint64_t t = gp.tokens;
-    float_span("a", gp.a, t == 0 ? 0 : (t - 1) * as + gp.v_heads);
-    float_span("b", gp.b, t == 0 ? 0 : (t - 1) * bs + gp.v_heads);
-    float_span("a_log", gp.a_log, gp.v_heads);
-    float_span("dt_bias", gp.dt_bias, gp.v_heads);
-    ROOST_GATE_RETURN(gate);
     GateSource gs;
-    gs.a = gp.a.address;
-    gs.b = gp.b.address;
-    gs.a_log = gp.a_log.address;
-    gs.dt_bias = gp.dt_bias.address;
-    gs.a_t = gp.a.dtype;
-    gs.b_t = gp.b.dtype;
-    gs.alog_t = gp.a_log.dtype;
-    gs.dtb_t = gp.dt_bias.dtype;
-    gs.a_stride = as;
-    gs.b_stride = bs;
-    if (t > 0 && gs.a == nullptr) return roost::Report(ROOST_STATUS_INVALID_ARGUMENT, kOp, "a: address is NULL");
+    ROOST_RETURN_IF_FAILED(GateSourceOf(gp, p, &gs));
     return RecurrentRun(p, ws, roost::Stream(stream), gs);
+  });
+}
+
+// CausalConv1d + GatedDeltaRuleGates + the recurrent GatedDeltaRule + GatedRmsNorm of one decode step in two launches
+// (GdnDecodeLayerKernel, then the convolution's state update): the four ops' results bit for bit.
+extern "C" ROOST_API RoostStatus roost_amd_gdn_decode_layer_run(RoostContext* ctx, const void* conv_params,
+                                                                const void* gates_params, const void* gdn_params,
+                                                                const void* norm_params, void* stream) {
+  constexpr char kLayerOp[] = "gdn_decode_layer";
+  roost::Gate gate(kLayerOp);
+  gate.Expect(ctx != nullptr && conv_params != nullptr && gdn_params != nullptr && norm_params != nullptr,
+              ROOST_STATUS_INVALID_ARGUMENT, "a context and the conv, GDN and norm params are required (the gates "
+              "params may be NULL: g and beta are then read from the GDN params)");
+  ROOST_GATE_RETURN(gate);
+  gate.Header(conv_params, sizeof(RoostCausalConv1dParams))
+      .Header(gdn_params, sizeof(RoostGatedDeltaRuleParams))
+      .Header(norm_params, sizeof(RoostGatedRmsNormParams));
+  if (gates_params != nullptr) gate.Header(gates_params, sizeof(RoostGatedDeltaRuleGatesParams));
+  ROOST_GATE_RETURN(gate);
+  const auto& cp = *static_cast<const RoostCausalConv1dParams*>(conv_params);
+  const auto& p = *static_cast<const RoostGatedDeltaRuleParams*>(gdn_params);
+  const auto& np = *static_cast<const RoostGatedRmsNormParams*>(norm_params);
+  return roost::CatchAll(kLayerOp, [&]() -> RoostStatus {
+    ROOST_RETURN_IF_FAILED(Admit(p, false, /*fused_gates=*/gates_params != nullptr));
+    GateSource gs;
+    if (gates_params != nullptr) {
+      ROOST_RETURN_IF_FAILED(GateSourceOf(*static_cast<const RoostGatedDeltaRuleGatesParams*>(gates_params), p, &gs));
+    }
+    ROOST_RETURN_IF_FAILED(roost_layer::AdmitConv(cp, kLayerOp));
+    bool row_form = false;
+    ROOST_RETURN_IF_FAILED(roost_layer::AdmitNorm(np, kLayerOp, &row_form));
+    // Every sequence on the token-serial recurrence: longer ones are the chunk kernels' in the recurrent variant.
+    gate.Expect(p.batch == 0 || p.cu_seqlens_host != nullptr, ROOST_STATUS_INVALID_ARGUMENT,
+                "the decode layer checks the sequence lengths in cu_seqlens_host, which is NULL");
+    ROOST_GATE_RETURN(gate);
+    for (uint32_t b = 0; b < p.batch; ++b) {
+      const int64_t n = int64_t{p.cu_seqlens_host[b + 1]} - p.cu_seqlens_host[b];
+      gate.Expect(n < static_cast<int64_t>(kRouteMinTokens), ROOST_STATUS_UNSUPPORTED,
+                  "sequence %u has %lld tokens; sequences of %u or more run on the chunk kernels, so this call covers "
+                  "decode steps only (run the four ops one by one)", b, static_cast<long long>(n), kRouteMinTokens);
+      if (!gate.ok()) return gate.status();
+    }
+    // The convolution: the GDN call's batch, bf16, at most kLayerMaxWidth taps, and q, k and v column views of its
+    // output (the GDN op reads them there).
+    const uint64_t ch = cp.channels;
+    gate.Expect(cp.batch == p.batch && cp.tokens == p.tokens && cp.cu_seqlens.address == p.cu_seqlens.address,
+                ROOST_STATUS_INVALID_ARGUMENT,
+                "the convolution covers %u sequences / %u tokens (cu_seqlens %p); the GDN call %u / %u (%p)", cp.batch,
+                cp.tokens, cp.cu_seqlens.address, p.batch, p.tokens, p.cu_seqlens.address)
+        .Expect(cp.input.dtype == ROOST_DTYPE_BF16 && cp.width <= kLayerMaxWidth, ROOST_STATUS_UNSUPPORTED,
+                "convolution of %s with %u taps: the decode layer is built for bf16 and up to %u taps",
+                roost::Describe(cp.input.dtype).name, cp.width, kLayerMaxWidth);
+    ROOST_GATE_RETURN(gate);
+    auto view = [&](const char* name, const RoostDeviceSpan& sp, uint32_t stride, uint64_t heads, uint32_t* first) {
+      const auto at = reinterpret_cast<intptr_t>(sp.address) - reinterpret_cast<intptr_t>(cp.output.address);
+      const uint64_t width = heads * kDim;
+      const bool ok = at >= 0 && at % 2 == 0 && static_cast<uint64_t>(at / 2) + width <= ch && Stride(stride, width) == ch;
+      gate.Expect(ok, ROOST_STATUS_INVALID_ARGUMENT,
+                  "%s is not a column view of the convolution's output (offset %lld bytes, row stride %llu; rows of "
+                  "%llu channels)", name, static_cast<long long>(at),
+                  static_cast<unsigned long long>(Stride(stride, width)), static_cast<unsigned long long>(ch));
+      *first = ok ? static_cast<uint32_t>(at / 2) : 0;
+    };
+    LayerArgs L{};
+    view("q", p.q, p.q_stride, p.k_heads, &L.cq);
+    view("k", p.k, p.k_stride, p.k_heads, &L.ck);
+    view("v", p.v, p.v_stride, p.v_heads, &L.cv);
+    ROOST_GATE_RETURN(gate);
+    // The norm: GatedRmsNorm of the GDN output over 128-column rows, in its single-pass form.
+    gate.Expect(np.input.address == p.output.address && np.rows == uint64_t{p.tokens} * p.v_heads && np.dim == kDim,
+                ROOST_STATUS_INVALID_ARGUMENT,
+                "the norm reads %u rows x %u at %p; the GDN output is %llu rows x %u at %p", np.rows, np.dim,
+                np.input.address, static_cast<unsigned long long>(uint64_t{p.tokens} * p.v_heads), kDim,
+                p.output.address)
+        .Expect(np.rows == 0 || (np.input.dtype == ROOST_DTYPE_BF16 && row_form), ROOST_STATUS_UNSUPPORTED,
+                "the decode layer's norm is GatedRmsNorm's single-pass bf16 form: 16-byte aligned input, gate and "
+                "output of bf16");
+    ROOST_GATE_RETURN(gate);
+    // What the kernel reads may not be what it writes: the norm's output against the layer's other inputs and states.
+    auto range = [](const void* a, uint64_t bytes) {
+      const auto x = reinterpret_cast<uintptr_t>(a);
+      return std::pair<uintptr_t, uintptr_t>{x, x + bytes};
+    };
+    const auto out = range(np.output.address, np.rows * uint64_t{kDim} * 2);
+    auto clear = [&](const char* name, const void* a, uint64_t bytes) {
+      const auto r = range(a, bytes);
+      gate.Expect(a == nullptr || bytes == 0 || r.second <= out.first || out.second <= r.first,
+                  ROOST_STATUS_INVALID_ARGUMENT, "the norm's output overlaps %s", name);
+    };
+    const uint64_t sl = cp.width - 1ull;
+    clear("the convolution's input", cp.input.address, uint64_t{cp.tokens} * ch * 2);
+    clear("the convolution's weights", cp.weight.address, ch * cp.width * 2);
+    clear("the convolution's bias", cp.bias.address, ch * 2);
+    clear("the convolution's state", sl == 0 ? nullptr : cp.conv_state.address,
+          cp.conv_state.length * roost::ElementBytes(cp.conv_state.dtype == ROOST_DTYPE_UNDEFINED ? cp.input.dtype
+                                                                                              : cp.conv_state.dtype));
+    clear("the recurrent state", p.state.address, p.state.length * 4);
+    ROOST_GATE_RETURN(gate);
+    if (p.batch == 0 || p.tokens == 0) return ROOST_STATUS_OK;
+    L.a = MakeArgs(p, gs);
+    L.x = static_cast<const uint16_t*>(cp.input.address);
+    L.conv_w = static_cast<const uint16_t*>(cp.weight.address);
+    L.conv_b = static_cast<const uint16_t*>(cp.bias.address);
+    L.conv_state = cp.conv_state.address;
+    L.conv_slots = static_cast<const int32_t*>(cp.state_slots.address);
+    L.conv_state_t = cp.conv_state.dtype == ROOST_DTYPE_UNDEFINED ? cp.input.dtype : cp.conv_state.dtype;
+    L.conv_pool_slots = sl == 0 ? 0 : cp.conv_state.length / (ch * sl);
+    L.channels = cp.channels;
+    L.width = cp.width;
+    L.silu = cp.silu != 0 ? 1u : 0u;
+    // One value head per key head, and q, k and v tiling the channels without overlap: each channel belongs to exactly
+    // one workgroup, which updates its state itself. Otherwise the conv op's state kernel runs afterwards.
+    const uint64_t qk = uint64_t{p.k_heads} * kDim, vw = uint64_t{p.v_heads} * kDim;
+    auto apart = [](uint64_t a, uint64_t na, uint64_t b, uint64_t nb) { return a + na <= b || b + nb <= a; };
+    const bool tiled = apart(L.cq, qk, L.ck, qk) && apart(L.cq, qk, L.cv, vw) && apart(L.ck, qk, L.cv, vw) &&
+                       2 * qk + vw == ch;
+    L.conv_state_update = p.v_heads == p.k_heads && tiled ? 1u : 0u;
+    L.z = static_cast<const uint16_t*>(np.gate.address);
+    L.norm_w = np.weight.address;
+    L.norm_w_t = np.weight.dtype;
+    L.eps = np.eps;
+    L.y = static_cast<uint16_t*>(np.output.address);
+    hipStream_t s = roost::Stream(stream);
+    hipLaunchKernelGGL(GdnDecodeLayerKernel, dim3(p.batch, p.v_heads), dim3(kLayerThreads), 0, s, L);
+    ROOST_RETURN_IF_FAILED(roost::HipStatus(hipGetLastError(), kLayerOp, "layer launch"));
+    return L.conv_state_update != 0 ? ROOST_STATUS_OK : roost_layer::ConvStateUpdate(cp, s, kLayerOp);
   });
 }
 
