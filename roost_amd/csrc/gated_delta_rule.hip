@@ -215,8 +215,9 @@ constexpr uint32_t kRecThreads = 256;
 // whole 128-byte rows of S per access), from the token's q and k elements
 // 2 lane, 2 lane + 1 (the norms), rows row0 .. + 3 of q and k, the kC columns of v and the token's gates; red_sk and
 // red_o are the [4 wavefronts][8 kC] LDS reduction arrays of the columns' workgroup (two workgroup barriers). Lanes with
-// w == 0 and rg == 0 receive their kC output columns. Every column sees the same operations in the same order whatever
-// kC is, so the recurrent kernel (kC = 4) and the decode-layer kernel (kC = 16) agree bit for bit.
+// w == 0 and rg == 0 receive their kC output columns. Every column sees the operations RecurrentUnit applies to it, in
+// the same order (RecurrentUnit keeps its own copy, 4 columns per lane, for its register allocation), so the decode-layer
+// kernel (kC = 16) and the recurrent kernels agree bit for bit.
 template <int kC>
 __device__ __forceinline__ void RecurrentStep(float (&s)[4][kC], const float (&q2)[2], const float (&k2)[2],
                                               const float (&q4)[4], float (&k4)[4], const float (&vv)[kC], float graw,
@@ -340,15 +341,14 @@ __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint
   const int row0 = 32 * w + 4 * rg;
   const uint32_t col = 32 * quarter + 4 * cg;
   const uint32_t kh = h / a.group;
-  float s[4][4];
+  float4 s[4];
   float* sp = has_slot ? a.state + (static_cast<uint64_t>(slot) * a.vh + h) * kDim * kDim + col : nullptr;
   if (has_slot && a.use_initial_state) {
-    LoadStateRows<4>(sp, row0, s);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[i] = LoadStreamF4(sp + (row0 + i) * kDim);
   } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) s[i][c] = 0.f;
+    for (int i = 0; i < 4; ++i) s[i] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   for (int32_t tok = t0; tok < t1; ++tok) {
     const uint16_t* qrow = a.q + static_cast<uint64_t>(tok) * a.q_stride + kh * kDim;
@@ -381,16 +381,71 @@ __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint
     }
     float graw, beta;
     GateAt(a, static_cast<uint64_t>(tok), h, graw, beta);
-    float ot[4];
-    RecurrentStep<4>(s, q2, k2, q4, k4, vv, graw, beta, a.scale, w, rg, cg, red_sk, red_o, ot);
+    const float decay = expf(graw);
+    float qq = fmaf(q2[0], q2[0], q2[1] * q2[1]), kk = fmaf(k2[0], k2[0], k2[1] * k2[1]);
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      qq += __shfl_xor(qq, o, 64);
+      kk += __shfl_xor(kk, o, 64);
+    }
+    const float qn = a.scale / sqrtf(qq + 1e-6f);
+    const float kn = 1.0f / sqrtf(kk + 1e-6f);
+    // S^T k: this lane's 4 rows, the row group's 32, then the workgroup's 128 through LDS.
+    float sk[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      k4[i] *= kn;
+      sk[0] = fmaf(s[i].x, k4[i], sk[0]);
+      sk[1] = fmaf(s[i].y, k4[i], sk[1]);
+      sk[2] = fmaf(s[i].z, k4[i], sk[2]);
+      sk[3] = fmaf(s[i].w, k4[i], sk[3]);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) sk[c] = OctSum(sk[c]);
+    if (rg == 0) *reinterpret_cast<float4*>(&red_sk[w][4 * cg]) = make_float4(sk[0], sk[1], sk[2], sk[3]);
+    __syncthreads();
+    float4 tot = *reinterpret_cast<const float4*>(&red_sk[0][4 * cg]);
+#pragma unroll
+    for (int ww = 1; ww < 4; ++ww) {
+      const float4 x = *reinterpret_cast<const float4*>(&red_sk[ww][4 * cg]);
+      tot = make_float4(tot.x + x.x, tot.y + x.y, tot.z + x.z, tot.w + x.w);
+    }
+    const float d[4] = {beta * (vv[0] - decay * tot.x), beta * (vv[1] - decay * tot.y),
+                        beta * (vv[2] - decay * tot.z), beta * (vv[3] - decay * tot.w)};
+    float o[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float ki = k4[i], qi = q4[i] * qn;
+      s[i].x = fmaf(s[i].x, decay, ki * d[0]);
+      s[i].y = fmaf(s[i].y, decay, ki * d[1]);
+      s[i].z = fmaf(s[i].z, decay, ki * d[2]);
+      s[i].w = fmaf(s[i].w, decay, ki * d[3]);
+      o[0] = fmaf(s[i].x, qi, o[0]);
+      o[1] = fmaf(s[i].y, qi, o[1]);
+      o[2] = fmaf(s[i].z, qi, o[2]);
+      o[3] = fmaf(s[i].w, qi, o[3]);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] = OctSum(o[c]);
+    if (rg == 0) *reinterpret_cast<float4*>(&red_o[w][4 * cg]) = make_float4(o[0], o[1], o[2], o[3]);
+    __syncthreads();
     if (w == 0 && rg == 0) {
+      float4 ot = *reinterpret_cast<const float4*>(&red_o[0][4 * cg]);
+#pragma unroll
+      for (int ww = 1; ww < 4; ++ww) {
+        const float4 x = *reinterpret_cast<const float4*>(&red_o[ww][4 * cg]);
+        ot = make_float4(ot.x + x.x, ot.y + x.y, ot.z + x.z, ot.w + x.w);
+      }
       uint2 pw;
-      pw.x = PackBf16(ot[0], ot[1]);
-      pw.y = PackBf16(ot[2], ot[3]);
+      pw.x = PackBf16(ot.x, ot.y);
+      pw.y = PackBf16(ot.z, ot.w);
       *reinterpret_cast<uint2*>(a.out + (static_cast<uint64_t>(tok) * a.vh + h) * kDim + col) = pw;
     }
   }
-  if (has_slot) StoreStateRows<4>(sp, row0, s);
+  if (has_slot) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) StoreStreamF4(sp + (row0 + i) * kDim, s[i]);
+  }
 }
 
 template <bool kVec>
