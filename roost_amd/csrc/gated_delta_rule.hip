@@ -14,7 +14,9 @@
 // no gather or state copy): four 256-thread workgroups per (sequence, value head), one per quarter of the value columns,
 // each lane holding 16 floats of S in registers (RecurrentUnit). Sequences of 16 or more tokens go to the chunk (WY)
 // kernels instead; their prep workgroups share one launch with the recurrent ones (WyPrepRecurrentKernel). The gates
-// may be folded in (roost_amd_gdn_recurrent_gated_run): g and beta are then computed where they are read.
+// may be folded in (roost_amd_gdn_recurrent_gated_run): g and beta are then computed where they are read. A decode
+// step of the whole layer -- CausalConv1d, the gates, the recurrence and GatedRmsNorm -- runs as one kernel
+// (GdnDecodeLayerKernel, roost_amd_gdn_decode_layer_run).
 
 #include <algorithm>
 #include <cmath>
