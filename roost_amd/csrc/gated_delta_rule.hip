@@ -1875,6 +1875,7 @@ extern "C" ROOST_API RoostStatus roost_amd_gdn_decode_layer_run(RoostContext* ct
     ROOST_RETURN_IF_FAILED(roost_layer::AdmitConv(cp, kLayerOp));
     bool row_form = false;
     ROOST_RETURN_IF_FAILED(roost_layer::AdmitNorm(np, kLayerOp, &row_form));
+    if (p.batch == 0 || p.tokens == 0) return ROOST_STATUS_OK;  // nothing to read or write, as for the four ops
     // Every sequence on the token-serial recurrence: longer ones are the chunk kernels' in the recurrent variant.
     gate.Expect(p.batch == 0 || p.cu_seqlens_host != nullptr, ROOST_STATUS_INVALID_ARGUMENT,
                 "the decode layer checks the sequence lengths in cu_seqlens_host, which is NULL");
@@ -1942,7 +1943,6 @@ extern "C" ROOST_API RoostStatus roost_amd_gdn_decode_layer_run(RoostContext* ct
                                                                                               : cp.conv_state.dtype));
     clear("the recurrent state", p.state.address, p.state.length * 4);
     ROOST_GATE_RETURN(gate);
-    if (p.batch == 0 || p.tokens == 0) return ROOST_STATUS_OK;
     L.a = MakeArgs(p, gs);
     L.x = static_cast<const uint16_t*>(cp.input.address);
     L.conv_w = static_cast<const uint16_t*>(cp.weight.address);

@@ -172,3 +172,12 @@ def test_decode_layer_refusals(session):
     assert e.value.status == abi.UNSUPPORTED
     # Nothing was written by the refused calls.
     assert np.array_equal(from_dev(lst), from_dev(long.state))
+
+
+def test_decode_layer_empty_step(session):
+    """A step whose sequences are all empty reads and writes nothing, as the four ops do."""
+    rng = np.random.default_rng(23)
+    layer = Layer(rng, [0, 0], 16, 16, 4, True, "bf16", True, None, None)
+    out, cs, st = layer.fused(session)
+    assert np.array_equal(cs, from_dev(layer.conv_state, True))
+    assert np.array_equal(st, from_dev(layer.state))
