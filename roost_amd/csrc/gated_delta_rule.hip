@@ -500,8 +500,9 @@ RoostStatus LaunchRecurrent(const RoostGatedDeltaRuleParams& p, hipStream_t stre
 
 // ---- Decode layer: CausalConv1d + gates + recurrence + GatedRmsNorm in one kernel ------------------------------------
 //
-// One workgroup of 256 threads per (sequence, value head): lane (rg, cg) of wavefront w holds state rows
-// 32 w + 4 rg .. + 3 of columns 32 m + 4 cg .. + 3, m = 0 .. 3 (64 floats), and runs RecurrentStep<16>, which treats each column exactly
+// One workgroup of 512 threads per (sequence, value head), two halves of 4 wavefronts: lane (rg, cg) of wavefront w
+// of half hf holds state rows 32 w + 4 rg .. + 3 of columns 64 hf + 32 m + 4 cg .. + 3, m = 0, 1 (32 floats), and runs
+// RecurrentStep<8> with its half's reduction arrays, which treats each column exactly
 // as the recurrent kernel's RecurrentStep<4> does. The workgroup convolves the token's q, k and v itself from the
 // layer's projection (CausalConv1d's arithmetic: bias, then the taps oldest first with fmaf, SiLU, rounded to bf16),
 // computes the gates where they are read, and normalises the token's 128 outputs (rounded to bf16, as the GDN op
@@ -528,23 +529,23 @@ struct LayerArgs {
   uint16_t* y;                // GatedRmsNorm's output [tokens * v_heads, 128]
 };
 
-constexpr uint32_t kLayerThreads = 256;
-constexpr int kLayerCols = 16;            // state columns per lane
+constexpr uint32_t kLayerThreads = 512;
+constexpr int kLayerCols = 8;             // state columns per lane
 constexpr uint32_t kLayerMaxWidth = 4;
-constexpr int kLayerConvPerThread = 2;    // 3 x 128 channels over 256 threads
+constexpr int kLayerConvPerThread = 1;    // 3 x 128 channels over 512 threads
 
 __global__ void __launch_bounds__(kLayerThreads) GdnDecodeLayerKernel(LayerArgs L) {
   const GdnArgs& a = L.a;
-  __shared__ float red_sk[4][8 * kLayerCols], red_o[4][8 * kLayerCols];
+  __shared__ float red_sk[2][4][8 * kLayerCols], red_o[2][4][8 * kLayerCols];
   __shared__ __align__(16) uint16_t xin[3 * kDim];  // this token's q, k and v, as the convolution rounds them
   __shared__ __align__(16) uint16_t ob[kDim];       // its outputs, as the GDN op rounds them
   const uint32_t b = blockIdx.x, h = blockIdx.y;
   const int32_t t0 = a.cu[b], t1 = a.cu[b + 1];
   if (t1 <= t0) return;  // an empty sequence leaves its slots untouched
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = (tid >> 6) & 3, hf = tid >> 8;
   const int rg = lane & 7, cg = lane >> 3;
   const int row0 = 32 * w + 4 * rg;
-  const int col = 4 * cg;  // the lane's first column; group m starts at col + 32 m
+  const int col = 64 * hf + 4 * cg;  // the lane's first column; group m starts at col + 32 m
   const uint32_t kh = h / a.group;
   const int32_t slot = a.slots[b];
   const bool has_slot = slot >= 0 && static_cast<uint64_t>(slot) < a.pool_slots;
@@ -618,7 +619,7 @@ __global__ void __launch_bounds__(kLayerThreads) GdnDecodeLayerKernel(LayerArgs 
     float graw, beta;
     GateAt(a, static_cast<uint64_t>(tok), h, graw, beta);
     float ot[kLayerCols];
-    RecurrentStep<kLayerCols>(s, q2, k2, q4, k4, vv, graw, beta, a.scale, w, rg, cg, red_sk, red_o, ot);
+    RecurrentStep<kLayerCols>(s, q2, k2, q4, k4, vv, graw, beta, a.scale, w, rg, cg, red_sk[hf], red_o[hf], ot);
     if (w == 0 && rg == 0) {
 #pragma unroll
       for (int c = 0; c < kLayerCols; c += 4) {
