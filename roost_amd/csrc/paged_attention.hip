@@ -504,22 +504,30 @@ int64_t Pieces(int64_t tiles, int64_t target) { return std::min<int64_t>(roost::
 constexpr int64_t kPfPieceCost = 2;
 template <typename Items>
 int64_t PrefillMakespan(const Items& items, int64_t target, uint32_t cus) {
-  std::vector<int64_t> cost;
+  // Piece costs by counting (they are small integers), then longest first onto the least loaded slot.
+  std::vector<uint32_t> count;
   for (const auto& it : items) {
     const int64_t tiles = ItemTiles(it.w), n = Pieces(tiles, target);
-    for (int64_t i = 0; i < n; ++i) cost.push_back(tiles * (i + 1) / n - tiles * i / n + kPfPieceCost);
+    for (int64_t i = 0; i < n; ++i) {
+      const auto c = static_cast<size_t>(tiles * (i + 1) / n - tiles * i / n + kPfPieceCost);
+      if (c >= count.size()) count.resize(c + 1, 0);
+      ++count[c];
+    }
   }
-  std::sort(cost.begin(), cost.end(), std::greater<int64_t>());
-  std::priority_queue<int64_t, std::vector<int64_t>, std::greater<int64_t>> slots;
-  for (uint32_t c = 0; c < cus; ++c) slots.push(0);
-  int64_t end = 0;
-  for (const int64_t c : cost) {
-    const int64_t t = slots.top() + c;
-    slots.pop();
-    slots.push(t);
-    end = std::max(end, t);
+  // Slots by load (at[L]: how many slots carry L tiles); loads only grow, so the least loaded level only moves up.
+  std::vector<uint32_t> at(1, std::max<uint32_t>(cus, 1));
+  size_t lo = 0, end = 0;
+  for (size_t c = count.size(); c-- > 0;) {
+    for (uint32_t k = 0; k < count[c]; ++k) {
+      while (at[lo] == 0) ++lo;
+      --at[lo];
+      const size_t load = lo + c;
+      if (load >= at.size()) at.resize(load + 1, 0);
+      ++at[load];
+      end = std::max(end, load);
+    }
   }
-  return end;
+  return static_cast<int64_t>(end);
 }
 
 // The piece size (in tiles, at least kPfMinSplitTiles) the 64-token kernel cuts key ranges at. Candidates: 3/4 of the
