@@ -192,6 +192,9 @@ def _conv_case(session, lens, slots, pool_slots, channels, width, silu, bias, bf
     ("width 1 (no state)", [3, 4], [0, 1], 2, 24, 1, True, True, False, True),
     ("odd channels scalar path", [9, 2], [1, 0], 2, 13, 4, True, False, True, True),
     ("one sequence, ragged last tile", [45, 70], [1, 0], 2, 128, 4, True, True, True, False),
+    # decode-shaped batches (fewer tokens than sequences x 32: the one-token-per-thread short form)
+    ("decode 64 x 1, width 3, bias, f32 state", [1] * 64, list(range(63, -1, -1)), 64, 1024, 3, True, True, True, True),
+    ("short rows, width 2, unslotted row", [2, 1, 3, 0, 1], [0, -1, 2, 3, 1], 4, 512, 2, False, True, True, False),
 ])
 def test_causal_conv1d(session, name, lens, slots, pool, channels, width, silu, bias, bf16, state_f32):
     got, want, got_state, want_state = _conv_case(session, lens, slots, pool, channels, width, silu, bias, bf16,
