@@ -256,10 +256,10 @@ def test_recurrent_variant_graph_replays():
         with torch.cuda.graph(graph, stream=stream):
             session.run(entry, p, ws)
         for replay in range(3):
-            with torch.cuda.stream(stream):
+            with torch.cuda.stream(stream):  # the replay too: replay() launches on the current stream
                 dev.pool.copy_(pool0)
                 dev.out.fill_(float("nan"))
-            graph.replay()
+                graph.replay()
             stream.synchronize()
             assert torch.equal(dev.out.view(torch.int16), want_o.view(torch.int16)), f"replay {replay} output"
             assert torch.equal(dev.pool, want_pool), f"replay {replay} state"

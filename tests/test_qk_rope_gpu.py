@@ -210,11 +210,11 @@ def test_fused_qkv_replays_in_a_graph(session):  # the fixture skips without a G
         with torch.cuda.graph(graph, stream=stream):
             session.run(entry, p, None)
         for replay in range(3):
-            with torch.cuda.stream(stream):
+            with torch.cuda.stream(stream):  # the replay too: replay() launches on the current stream
                 q.fill_(float("nan"))
                 kc.zero_()
                 vc.zero_()
-            graph.replay()
+                graph.replay()
             stream.synchronize()
             for got, exp in zip((q, kc, vc), want):
                 assert torch.equal(got.view(torch.int16), exp.view(torch.int16)), f"replay {replay}"
