@@ -530,14 +530,18 @@ int64_t PrefillMakespan(const Items& items, int64_t target, uint32_t cus) {
   return static_cast<int64_t>(end);
 }
 
-// The piece size (in tiles, at least kPfMinSplitTiles) the 64-token kernel cuts key ranges at. Candidates: 3/4 of the
-// average CU load (config 3: 0.213 ms against 0.219 with the whole average and 0.242 with half), and the smallest
-// sizes whose pieces fill the CUs exactly once or twice (config 5's two 512-token chunks: 256 pieces of 9 tiles
-// instead of 288 of 8, whose last 32 ran in a second round); the one whose longest-first dispatch ends first wins.
+// The piece size (in tiles, at least kPfMinSplitTiles) the 64-token kernel cuts key ranges at. Candidates: 3/4, 17/20
+// and the whole of the average CU load, and the smallest sizes whose pieces fill the CUs exactly once or twice
+// (config 5's two 512-token chunks: 256 pieces of 9 tiles instead of 288 of 8, whose last 32 ran in a second round);
+// the one whose longest-first dispatch ends first wins. Config 3 keeps 3/4 (0.197 ms, against 0.203 at 17/20 and
+// 0.234 at 13/20); a dense 4 x 4096 batch takes the whole average (1,095 against 950 TFLOP/s at 3/4).
 template <typename Items>
 int64_t PrefillPieceTiles(const Items& items, int64_t total_tiles, uint32_t cus) {
   const uint32_t slots = std::max<uint32_t>(cus, 1);
-  std::vector<int64_t> cand{std::max<int64_t>(kPfMinSplitTiles, roost::CeilDiv(total_tiles * 3, 4 * int64_t{slots}))};
+  auto of_avg = [&](int64_t num, int64_t den) {
+    return std::max<int64_t>(kPfMinSplitTiles, roost::CeilDiv(total_tiles * num, den * int64_t{slots}));
+  };
+  std::vector<int64_t> cand{of_avg(3, 4), of_avg(17, 20), of_avg(1, 1)};
   int64_t longest = 0;
   for (const auto& it : items) longest = std::max(longest, ItemTiles(it.w));
   for (int64_t rounds = 1; rounds <= 2; ++rounds) {
