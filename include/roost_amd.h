@@ -225,7 +225,7 @@ typedef struct RoostAmdStepTables {
   uint32_t tokens;           /* out: tokens */
   uint32_t blocks;           /* out: kv_indices entries written */
   uint32_t rows_written;     /* out: sampling rows written */
-  uint32_t reserved0;        /* 0 */
+  uint32_t attention_blocks; /* blocks in the attention KV pool, > 0: block ids outside [0, attention_blocks) are refused */
   int32_t* q_indptr;         /* [batch + 1] */
   int32_t* cu_seqlens;       /* [batch + 1] */
   int32_t* kv_indptr;        /* [batch + 1] */

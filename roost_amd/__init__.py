@@ -577,8 +577,8 @@ def plan_region_run(session: OpSession, **kwargs) -> None:
         raise KernelError("plan_region_run", status, session.lib.last_error())
 
 
-def plan_region_from_step(lib: KernelLibrary, plan, *, attention_group: int, block_size: int, max_batch: int,
-                          max_tokens: int, max_blocks: int) -> dict:
+def plan_region_from_step(lib: KernelLibrary, plan, *, attention_group: int, block_size: int, attention_blocks: int,
+                          max_batch: int, max_tokens: int, max_blocks: int) -> dict:
     """roost_amd_plan_region_from_step over a C2 step-plan buffer (bytes or a uint8 numpy array). Returns the tables as
     numpy arrays cut to what was written; raises KernelError on a refused plan."""
     import numpy as np
@@ -592,7 +592,7 @@ def plan_region_from_step(lib: KernelLibrary, plan, *, attention_group: int, blo
         "slot_mapping": np.full(max(max_tokens, 1), -7, np.int64), "rows": np.full(max(max_batch, 1), -7, np.int32),
     }
     t = abi.StepTables()
-    t.attention_group, t.block_size = attention_group, block_size
+    t.attention_group, t.block_size, t.attention_blocks = attention_group, block_size, attention_blocks
     t.max_batch, t.max_tokens, t.max_blocks = max_batch, max_tokens, max_blocks
     for name, a in out.items():
         setattr(t, name, a.ctypes.data)

@@ -182,7 +182,7 @@ class PlanRegion(C.Structure):
 class StepTables(C.Structure):
     """RoostAmdStepTables: the outputs of roost_amd_plan_region_from_step (host pointers)."""
     _fields_ = [(name, C.c_uint32) for name in ("attention_group", "block_size", "max_batch", "max_tokens", "max_blocks",
-                                                "batch", "tokens", "blocks", "rows_written", "reserved0")] + [
+                                                "batch", "tokens", "blocks", "rows_written", "attention_blocks")] + [
         (name, C.c_void_p) for name in ("q_indptr", "cu_seqlens", "kv_indptr", "kv_indices", "kv_last_page_len",
                                         "state_slots", "ids", "positions", "slot_mapping", "rows")]
 

@@ -2119,7 +2119,22 @@ extern "C" ROOST_API RoostStatus roost_amd_gdn_recurrent_run_noalloc(RoostContex
     if (p.batch == 0 || p.tokens == 0) return ROOST_STATUS_OK;
     hipStream_t s = roost::Stream(stream);
     if (p.tokens < kRouteMinTokens) return LaunchRecurrent(p, s);
-    const ChunkArena l = MakeRouteArena(p.tokens, p.batch, p.v_heads);
+    ChunkArena l = MakeRouteArena(p.tokens, p.batch, p.v_heads);
+    if (p.cu_seqlens_host != nullptr) {
+      // The host copy bounds the routing exactly: its long sequences and their chunks (a decode batch has none and
+      // runs on the recurrent kernel alone, whatever its size).
+      uint64_t long_seqs = 0, chunks = 0;
+      for (uint32_t b = 0; b < p.batch; ++b) {
+        const int64_t len = int64_t{p.cu_seqlens_host[b + 1]} - p.cu_seqlens_host[b];
+        if (len >= static_cast<int64_t>(kRouteMinTokens)) {
+          ++long_seqs;
+          chunks += roost::CeilDiv(static_cast<uint64_t>(len), uint64_t{kChunk});
+        }
+      }
+      if (long_seqs == 0) return LaunchRecurrent(p, s);
+      l = MakeArena(std::min<uint64_t>(chunks, l.max_chunks), p.batch, p.v_heads,
+                    std::min<uint64_t>(long_seqs, l.max_long));
+    }
     gate.Expect(l.total <= kStaticScratchBytes, ROOST_STATUS_INVALID_ARGUMENT,
                 "%u tokens in %u sequences need %llu bytes of routing scratch; the allocation-free path holds %llu",
                 p.tokens, p.batch, static_cast<unsigned long long>(l.total),

@@ -641,20 +641,46 @@ __global__ void __launch_bounds__(256) ConvStateVecKernel(ConvArgs a) {
 }
 
 // ---- Recurrent-state copies ----------------------------------------------------------------------------------------
-// Word w of every pair, pairs in order (so a later pair sees an earlier pair's write of the same word). from/to slots
-// outside their pool (when its size is known) are skipped.
-template <typename W>
-__global__ void __launch_bounds__(256) CopyPairsKernel(const unsigned char* src, unsigned char* dst, const int32_t* pairs,
-                                                       uint32_t count, uint64_t slot_bytes, uint32_t swap,
-                                                       uint64_t src_slots, uint64_t dst_slots) {
-  const uint64_t words = slot_bytes / sizeof(W);
-  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
-  for (uint64_t w = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; w < words; w += stride) {
-    for (uint32_t i = 0; i < count; ++i) {
-      const int32_t from = pairs[2 * i + swap], to = pairs[2 * i + 1 - swap];
-      if (from < 0 || to < 0 || static_cast<uint64_t>(from) >= src_slots || static_cast<uint64_t>(to) >= dst_slots) continue;
-      reinterpret_cast<W*>(dst + static_cast<uint64_t>(to) * slot_bytes)[w] =
-          reinterpret_cast<const W*>(src + static_cast<uint64_t>(from) * slot_bytes)[w];
+// A slot is cut into units (16 bytes when sizes and addresses allow, else single bytes). Each unit belongs to one
+// thread, which applies the pairs to it in list order, so a pair that reads a slot an earlier pair wrote sees that
+// write. The workgroup first resolves a batch of pairs into byte offsets in LDS (-1: a slot outside its pool, skipped)
+// so that the pair list is read once per workgroup rather than once per unit.
+constexpr uint32_t kPairBatch = 512;
+constexpr uint32_t kUnitsPerThread = 4;
+
+template <bool kVec>
+__global__ void __launch_bounds__(256) SlotPairCopyKernel(const unsigned char* __restrict__ src, unsigned char* dst,
+                                                          const int32_t* __restrict__ pairs, uint32_t count,
+                                                          uint64_t slot_bytes, uint32_t from_col, uint64_t src_slots,
+                                                          uint64_t dst_slots) {
+  __shared__ int64_t offs[2][kPairBatch];
+  const uint64_t units = kVec ? slot_bytes / 16 : slot_bytes;
+  const uint64_t per_wg = static_cast<uint64_t>(blockDim.x) * kUnitsPerThread;
+  const uint64_t first = static_cast<uint64_t>(blockIdx.x) * per_wg + threadIdx.x;
+  for (uint32_t base = 0; base < count; base += kPairBatch) {
+    const uint32_t n = min(kPairBatch, count - base);
+    __syncthreads();  // the previous batch's offsets are no longer read
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+      const int32_t from = pairs[2 * (base + i) + from_col], to = pairs[2 * (base + i) + 1 - from_col];
+      const bool ok = from >= 0 && to >= 0 && static_cast<uint64_t>(from) < src_slots &&
+                      static_cast<uint64_t>(to) < dst_slots;
+      offs[0][i] = ok ? static_cast<int64_t>(from) * static_cast<int64_t>(slot_bytes) : -1;
+      offs[1][i] = ok ? static_cast<int64_t>(to) * static_cast<int64_t>(slot_bytes) : -1;
+    }
+    __syncthreads();
+    for (uint32_t i = 0; i < n; ++i) {
+      const int64_t f = offs[0][i], t = offs[1][i];
+      if (f < 0) continue;
+#pragma unroll
+      for (uint32_t j = 0; j < kUnitsPerThread; ++j) {
+        const uint64_t u = first + static_cast<uint64_t>(j) * blockDim.x;
+        if (u >= units) break;
+        if constexpr (kVec) {
+          *reinterpret_cast<uint4*>(dst + t + 16 * u) = *reinterpret_cast<const uint4*>(src + f + 16 * u);
+        } else {
+          dst[t + u] = src[f + u];
+        }
+      }
     }
   }
 }
@@ -1034,28 +1060,19 @@ extern "C" ROOST_API RoostStatus roost_causal_conv1d_run(RoostContext* ctx, cons
 namespace {
 
 RoostStatus LaunchCopyPairs(const char* op, const void* src, uint64_t src_bytes, void* dst, uint64_t dst_bytes,
-                            const RoostDeviceSpan& pairs, uint64_t slot_bytes, uint32_t count, uint32_t swap,
+                            const RoostDeviceSpan& pairs, uint64_t slot_bytes, uint32_t count, uint32_t from_col,
                             hipStream_t stream) {
-  const auto* s = static_cast<const unsigned char*>(src);
-  auto* d = static_cast<unsigned char*>(dst);
-  const auto* pr = static_cast<const int32_t*>(pairs.address);
-  // Pool sizes in slots; an unknown size (length 0) leaves the slots unchecked, as the reference does.
-  const uint64_t src_slots = src_bytes == 0 ? ~uint64_t{0} : src_bytes / slot_bytes;
-  const uint64_t dst_slots = dst_bytes == 0 ? ~uint64_t{0} : dst_bytes / slot_bytes;
-  const bool wide = slot_bytes % 16 == 0 && roost::IsAligned(s, 16) && roost::IsAligned(d, 16);
-  const bool word = slot_bytes % 4 == 0 && roost::IsAligned(s, 4) && roost::IsAligned(d, 4);
-  const uint64_t unit = wide ? 16 : (word ? 4 : 1);
-  const uint32_t blocks = static_cast<uint32_t>(std::min<uint64_t>(roost::CeilDiv(slot_bytes / unit, 256), 4096));
-  if (wide) {
-    hipLaunchKernelGGL(CopyPairsKernel<uint4>, dim3(blocks), dim3(256), 0, stream, s, d, pr, count, slot_bytes, swap,
-                       src_slots, dst_slots);
-  } else if (word) {
-    hipLaunchKernelGGL(CopyPairsKernel<uint32_t>, dim3(blocks), dim3(256), 0, stream, s, d, pr, count, slot_bytes, swap,
-                       src_slots, dst_slots);
-  } else {
-    hipLaunchKernelGGL(CopyPairsKernel<unsigned char>, dim3(blocks), dim3(256), 0, stream, s, d, pr, count, slot_bytes,
-                       swap, src_slots, dst_slots);
-  }
+  // Pool sizes in slots; a pool of unknown size (length 0) leaves its slots unchecked, as the reference does.
+  const uint64_t src_slots = src_bytes == 0 ? UINT64_MAX : src_bytes / slot_bytes;
+  const uint64_t dst_slots = dst_bytes == 0 ? UINT64_MAX : dst_bytes / slot_bytes;
+  const bool vec = slot_bytes % 16 == 0 && roost::IsAligned(src, 16) && roost::IsAligned(dst, 16);
+  const uint64_t units = vec ? slot_bytes / 16 : slot_bytes;
+  const uint64_t grid = roost::CeilDiv(units, uint64_t{256} * kUnitsPerThread);
+  if (grid > 0x7fffffff) return roost::Report(ROOST_STATUS_INVALID_ARGUMENT, op, "slot_bytes %llu is too large", static_cast<unsigned long long>(slot_bytes));
+  auto* kernel = vec ? SlotPairCopyKernel<true> : SlotPairCopyKernel<false>;
+  hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(grid)), dim3(256), 0, stream,
+                     static_cast<const unsigned char*>(src), static_cast<unsigned char*>(dst),
+                     static_cast<const int32_t*>(pairs.address), count, slot_bytes, from_col, src_slots, dst_slots);
   return roost::HipStatus(hipGetLastError(), op, "slot copy launch");
 }
 

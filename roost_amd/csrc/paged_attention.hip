@@ -50,14 +50,8 @@ namespace {
 using namespace roost_dev;
 
 constexpr uint32_t kGroup = 4;                  // query heads per KV head (Qwen3.5: 8 over 2)
-#ifndef ROOST_DECODE_WGS_PER_CU
-#define ROOST_DECODE_WGS_PER_CU 2
-#endif
-#ifndef ROOST_DECODE_RING
-#define ROOST_DECODE_RING 2
-#endif
-constexpr uint32_t kDecodeWgsPerCu = ROOST_DECODE_WGS_PER_CU;  // decode workgroups resident per CU
-constexpr int kDecodeRing = ROOST_DECODE_RING;  // register ring depth: groups in flight per wavefront = ring - 1
+constexpr uint32_t kDecodeWgsPerCu = 2;        // decode workgroups resident per CU
+constexpr int kDecodeRing = 2;                  // register ring depth: groups in flight per wavefront = ring - 1
 constexpr uint32_t kMaxMergeSplits = 1024;      // partials one sequence may be split into
 constexpr uint32_t kPrefillTileQ = 32;          // query tokens per workgroup of the general-page-size prefill
 constexpr uint32_t kPrefillTileK = 64;          // keys per LDS tile
@@ -1117,7 +1111,7 @@ __device__ __forceinline__ void LdsBarrier() {
 // processes the pieces of its range in turn; a piece that is not a whole sequence writes fp32 partials that
 // DecodeMergeKernel combines in key order.
 template <typename T, int D, bool kFastPage>
-__global__ void __launch_bounds__(256, ROOST_DECODE_WGS_PER_CU) DecodeKernel(const T* __restrict__ q, T* __restrict__ out, float* __restrict__ lse,
+__global__ void __launch_bounds__(256, kDecodeWgsPerCu) DecodeKernel(const T* __restrict__ q, T* __restrict__ out, float* __restrict__ lse,
                                                     KvView kv, const int32_t* __restrict__ kv_indices,
                                                     const DecodeWork* __restrict__ work,
                                                     const int32_t* __restrict__ range_ptr,

@@ -212,8 +212,8 @@ RoostStatus ReadStepPlan(const unsigned char* plan, uint64_t plan_bytes, RoostAm
       .Expect(h.header_size >= sizeof(shm::PlanHead) && h.total_bytes <= plan_bytes && h.header_size <= h.total_bytes,
               ROOST_STATUS_INVALID_ARGUMENT, "header of %u bytes in a plan of %llu bytes (%llu given)", h.header_size,
               static_cast<unsigned long long>(h.total_bytes), static_cast<unsigned long long>(plan_bytes))
-      .Expect(out.block_size > 0 && out.reserved0 == 0, ROOST_STATUS_INVALID_ARGUMENT,
-              "block_size = %u, reserved0 = %u", out.block_size, out.reserved0)
+      .Expect(out.block_size > 0 && out.attention_blocks > 0, ROOST_STATUS_INVALID_ARGUMENT,
+              "block_size = %u, attention_blocks = %u", out.block_size, out.attention_blocks)
       .Expect(out.attention_group < h.group_count, ROOST_STATUS_INVALID_ARGUMENT,
               "attention_group %u of a plan with %u groups", out.attention_group, h.group_count);
   ROOST_GATE_RETURN(gate);
@@ -271,7 +271,16 @@ RoostStatus ReadStepPlan(const unsigned char* plan, uint64_t plan_bytes, RoostAm
     offset[b] = static_cast<int32_t>(s.position_offset);
     kv_length[b] = static_cast<int32_t>(kv);
     slot[b] = s.recurrent_slot;
-    for (uint64_t i = 0; i < pages; ++i) blocks.push_back(Entry<int32_t>(plan, h.block_ids, g.block_start + i));
+    for (uint64_t i = 0; i < pages && gate.ok(); ++i) {
+      // A block id outside the pool would send attention reads and KV writes out of the pool: refused here, before
+      // anything is written, as the worker's plan reader does (StepPlanReader.cs:322-328).
+      const int32_t id = Entry<int32_t>(plan, h.block_ids, g.block_start + i);
+      gate.Expect(id >= 0 && static_cast<uint32_t>(id) < out.attention_blocks, ROOST_STATUS_INVALID_ARGUMENT,
+                  "sequence %llu: block id %d is outside [0, %u)", static_cast<unsigned long long>(b), id,
+                  out.attention_blocks);
+      blocks.push_back(id);
+    }
+    if (!gate.ok()) break;
     indptr[b + 1] = static_cast<int32_t>(blocks.size());
     if (s.flags & shm::kSeqSample) rows.push_back(static_cast<int32_t>(end - 1));
     next = end;

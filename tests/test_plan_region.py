@@ -224,7 +224,9 @@ def _step_plan(seqs, *, group_count=3, attention_group=1, sample=None, token_ids
 def _from_step(kernels, buf, seqs, bs, **kw):
     tokens = sum(s["token_count"] for s in seqs)
     nblocks = sum(len(s["blocks"]) for s in seqs)
-    args = dict(attention_group=1, block_size=bs, max_batch=len(seqs), max_tokens=tokens, max_blocks=nblocks)
+    pool = 1 + max((b for s in seqs for b in s["blocks"]), default=0)
+    args = dict(attention_group=1, block_size=bs, attention_blocks=pool, max_batch=len(seqs), max_tokens=tokens,
+                max_blocks=nblocks)
     args.update(kw)
     return roost_amd.plan_region_from_step(kernels, buf, **args)
 
@@ -259,14 +261,15 @@ def test_step_plan_reference_hand_case(kernels):
 
 def test_step_plan_empty(kernels):
     buf, _, _ = _step_plan([])
-    out = roost_amd.plan_region_from_step(kernels, buf, attention_group=1, block_size=16, max_batch=0, max_tokens=0,
-                                          max_blocks=0)
+    out = roost_amd.plan_region_from_step(kernels, buf, attention_group=1, block_size=16, attention_blocks=1,
+                                          max_batch=0, max_tokens=0, max_blocks=0)
     assert list(out["q_indptr"]) == [0] and list(out["kv_indptr"]) == [0] and out["rows"].size == 0
 
 
 @pytest.mark.parametrize("change", ["magic", "short buffer", "table past the end", "tokens not contiguous",
                                    "positions skip", "too few blocks", "group_blocks_start", "attention group",
-                                   "outputs too small", "token count"])
+                                   "outputs too small", "token count", "block id past the pool",
+                                   "negative block id", "no pool size"])
 def test_step_plan_refusals(kernels, change):
     import ctypes as C
 
@@ -297,6 +300,14 @@ def test_step_plan_refusals(kernels, change):
         call["attention_group"] = 3
     elif change == "outputs too small":
         call["max_tokens"] = 3
+    elif change == "block id past the pool":
+        call["attention_blocks"] = 7  # the hand case lists block 7
+    elif change == "negative block id":
+        seqs[1]["blocks"][0] = -1
+        buf, _, _ = _step_plan(seqs, **kw)
+        call["attention_blocks"] = 8
+    elif change == "no pool size":
+        call["attention_blocks"] = 0
     elif change == "token count":
         h.token_count += 1
         buf[:C.sizeof(h)] = np.frombuffer(bytes(h), np.uint8)

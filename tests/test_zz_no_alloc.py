@@ -58,3 +58,15 @@ def test_noalloc_refuses_calls_beyond_its_scratch(session):
     assert _noalloc(session)(session.ctx, C.addressof(p), C.c_void_p(session.stream_handle)) == abi.INVALID_ARGUMENT
     assert "scratch" in session.lib.last_error()
     assert np.array_equal(from_dev(dev.pool), before)
+
+
+@pytest.mark.parametrize("lens", [[1] * 1024, [1] * 1023 + [600]], ids=["decode-1024", "decode-1023-plus-600"])
+def test_noalloc_large_batches_bounded_by_the_host_lengths(session, lens):
+    """1,024 sequences over 16 value heads: sized from tokens and batch alone these would need more than the static
+    scratch holds; the host copy of cu_seqlens bounds the routing to what the batch really chunks (none for a decode
+    step, 10 chunks for one 600-token row), so both run, equal to the workspace entry point bit for bit."""
+    rng = np.random.default_rng(len(lens))
+    d = cases.make_gdn(rng, lens, len(lens), slots=list(range(len(lens))), baseline_style=True)
+    (ro, rp), (go, gp) = _both(session, d)
+    assert np.array_equal(ro, go)
+    assert np.array_equal(rp, gp)
