@@ -72,8 +72,13 @@ def build(verbose: bool = True) -> Path:
     if alias.is_symlink() or alias.exists():
         alias.unlink()
     alias.symlink_to(LIB_NAME)
+    # The gfx950 manifest entries (variants, flags, constraints, the file's size and digest) follow every build.
+    from . import manifest
+    from . import KernelLibrary
+
+    manifest.write(KernelLibrary(LIB_PATH), LIB_PATH)
     if verbose:
-        print(f"built {LIB_PATH}")
+        print(f"built {LIB_PATH} and {manifest.MANIFEST_PATH.name}")
     return LIB_PATH
 
 
