@@ -273,6 +273,77 @@ int oracle_rope(void* q, void* k, const int32_t* positions, int dtype, int token
 
 /* ---- GatedDeltaRule (reference: src/Starlings.Roost.Ops/CpuOps.Hybrid.cs:30-157, 233-241) ---- */
 
+/* One (sequence, value head) of GatedDeltaRule: CpuOps' loop body (CpuOps.Hybrid.cs:82-149). */
+typedef struct GdnCall {
+  const void *q, *k, *v, *g, *beta;
+  void* out;
+  float* state;
+  const int32_t *slots, *cu;
+  int g_dtype, beta_dtype, dtype, v_heads, kd, vd, group, use_initial_state, l2_norm_qk;
+  int64_t qs, ks, vs, state_elems;
+  double scale;
+} GdnCall;
+
+static void gdn_unit(const GdnCall* c, int b, int h) {
+  const void *q = c->q, *k = c->k, *v = c->v, *g = c->g, *beta = c->beta;
+  void* out = c->out;
+  const int32_t *slots = c->slots, *cu = c->cu;
+  const int g_dtype = c->g_dtype, beta_dtype = c->beta_dtype, dtype = c->dtype, v_heads = c->v_heads;
+  const int kd = c->kd, vd = c->vd, group = c->group, use_initial_state = c->use_initial_state;
+  const int l2_norm_qk = c->l2_norm_qk;
+  const int64_t qs = c->qs, ks = c->ks, vs = c->vs, state_elems = c->state_elems;
+  const double scale = c->scale;
+  float* state = c->state;
+  const int64_t t0 = cu[b], t1 = cu[b + 1];
+  if (t1 == t0) return;
+  double* s = (double*)malloc(sizeof(double) * (size_t)(state_elems + 2 * kd + vd));
+  double* qv = s + state_elems;
+  double* kv = qv + kd;
+  double* dv = kv + kd;
+  float* st = state + ((int64_t)slots[b] * v_heads + h) * state_elems;
+  for (int64_t i = 0; i < state_elems; ++i) s[i] = use_initial_state ? (double)st[i] : 0.0;
+  const int kh = h / group;
+  for (int64_t t = t0; t < t1; ++t) {
+    const int64_t qo = t * qs + (int64_t)kh * kd;
+    const int64_t ko = t * ks + (int64_t)kh * kd;
+    double qq = 0.0, kk = 0.0;
+    for (int i = 0; i < kd; ++i) {
+      qv[i] = load(q, dtype, qo + i);
+      kv[i] = load(k, dtype, ko + i);
+      qq += qv[i] * qv[i];
+      kk += kv[i] * kv[i];
+    }
+    const double qn = l2_norm_qk ? 1.0 / sqrt(qq + 1e-6) : 1.0;
+    const double kn = l2_norm_qk ? 1.0 / sqrt(kk + 1e-6) : 1.0;
+    for (int i = 0; i < kd; ++i) {
+      qv[i] *= qn * scale;
+      kv[i] *= kn;
+    }
+    const double decay = exp(load(g, g_dtype, t * v_heads + h));
+    const double bt = load(beta, beta_dtype, t * v_heads + h);
+    const int64_t vo = t * vs + (int64_t)h * vd;
+    const int64_t oo = (t * v_heads + h) * (int64_t)vd;
+    for (int j = 0; j < vd; ++j) {
+      double kvs = 0.0;
+      for (int i = 0; i < kd; ++i) {
+        s[(int64_t)i * vd + j] *= decay;
+        kvs += s[(int64_t)i * vd + j] * kv[i];
+      }
+      dv[j] = bt * (load(v, dtype, vo + j) - kvs);
+    }
+    for (int j = 0; j < vd; ++j) {
+      double o = 0.0;
+      for (int i = 0; i < kd; ++i) {
+        s[(int64_t)i * vd + j] += kv[i] * dv[j];
+        o += s[(int64_t)i * vd + j] * qv[i];
+      }
+      store(out, dtype, oo + j, o);
+    }
+  }
+  for (int64_t i = 0; i < state_elems; ++i) st[i] = (float)s[i];
+  free(s);
+}
+
 int oracle_gated_delta_rule(const void* q, const void* k, const void* v, const void* g, int g_dtype,
                             const void* beta, int beta_dtype, void* out, float* state, int64_t state_len,
                             const int32_t* slots, const int32_t* cu, int dtype, int batch, int tokens, int k_heads,
@@ -296,62 +367,30 @@ int oracle_gated_delta_rule(const void* q, const void* k, const void* v, const v
       if (so < 0 || so + (int64_t)v_heads * state_elems > state_len) return fail("state slot outside the pool");
     }
   }
+  const GdnCall call = {q, k, v, g, beta, out, state, slots, cu, g_dtype, beta_dtype, dtype, v_heads, kd, vd, group,
+                        use_initial_state, l2_norm_qk, qs, ks, vs, state_elems, scale};
+  /* CpuOps walks the batch in order, so sequences that share a slot see each other's writes. When any do, the
+   * parallel loop runs over heads only, each head walking the batch in order; otherwise over (sequence, head). */
+  int shared = 0;
+  for (int b = 0; b < batch && !shared; ++b) {
+    for (int c2 = b + 1; c2 < batch && !shared; ++c2) {
+      shared = slots[b] == slots[c2] && cu[b + 1] > cu[b] && cu[c2 + 1] > cu[c2];
+    }
+  }
+  if (shared) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads > 0 ? threads : 1)
+#endif
+    for (int h = 0; h < v_heads; ++h) {
+      for (int b = 0; b < batch; ++b) gdn_unit(&call, b, h);
+    }
+    return 0;
+  }
   const int64_t work = (int64_t)batch * v_heads;
 #ifdef _OPENMP
 #pragma omp parallel for schedule(dynamic, 1) num_threads(threads > 0 ? threads : 1)
 #endif
-  for (int64_t bh = 0; bh < work; ++bh) {
-    const int b = (int)(bh / v_heads);
-    const int h = (int)(bh % v_heads);
-    const int64_t t0 = cu[b], t1 = cu[b + 1];
-    if (t1 == t0) continue;
-    double* s = (double*)malloc(sizeof(double) * (size_t)(state_elems + 2 * kd + vd));
-    double* qv = s + state_elems;
-    double* kv = qv + kd;
-    double* dv = kv + kd;
-    float* st = state + ((int64_t)slots[b] * v_heads + h) * state_elems;
-    for (int64_t i = 0; i < state_elems; ++i) s[i] = use_initial_state ? (double)st[i] : 0.0;
-    const int kh = h / group;
-    for (int64_t t = t0; t < t1; ++t) {
-      const int64_t qo = t * qs + (int64_t)kh * kd;
-      const int64_t ko = t * ks + (int64_t)kh * kd;
-      double qq = 0.0, kk = 0.0;
-      for (int i = 0; i < kd; ++i) {
-        qv[i] = load(q, dtype, qo + i);
-        kv[i] = load(k, dtype, ko + i);
-        qq += qv[i] * qv[i];
-        kk += kv[i] * kv[i];
-      }
-      const double qn = l2_norm_qk ? 1.0 / sqrt(qq + 1e-6) : 1.0;
-      const double kn = l2_norm_qk ? 1.0 / sqrt(kk + 1e-6) : 1.0;
-      for (int i = 0; i < kd; ++i) {
-        qv[i] *= qn * scale;
-        kv[i] *= kn;
-      }
-      const double decay = exp(load(g, g_dtype, t * v_heads + h));
-      const double bt = load(beta, beta_dtype, t * v_heads + h);
-      const int64_t vo = t * vs + (int64_t)h * vd;
-      const int64_t oo = (t * v_heads + h) * (int64_t)vd;
-      for (int j = 0; j < vd; ++j) {
-        double kvs = 0.0;
-        for (int i = 0; i < kd; ++i) {
-          s[(int64_t)i * vd + j] *= decay;
-          kvs += s[(int64_t)i * vd + j] * kv[i];
-        }
-        dv[j] = bt * (load(v, dtype, vo + j) - kvs);
-      }
-      for (int j = 0; j < vd; ++j) {
-        double o = 0.0;
-        for (int i = 0; i < kd; ++i) {
-          s[(int64_t)i * vd + j] += kv[i] * dv[j];
-          o += s[(int64_t)i * vd + j] * qv[i];
-        }
-        store(out, dtype, oo + j, o);
-      }
-    }
-    for (int64_t i = 0; i < state_elems; ++i) st[i] = (float)s[i];
-    free(s);
-  }
+  for (int64_t bh = 0; bh < work; ++bh) gdn_unit(&call, (int)(bh / v_heads), (int)(bh % v_heads));
   return 0;
 }
 

@@ -158,6 +158,7 @@ struct GdnArgs {
   float scale;
   uint32_t vh;     // value heads (the rows of v, output, g and beta, the heads of a state slot)
   uint32_t group;  // value heads per key head: value head h reads q / k head h / group
+  uint32_t batch;  // sequences of the call (the length of slots)
   GateSource gs;   // when gs.a is set, g and beta are computed from these instead of read from g and beta
 };
 
@@ -327,17 +328,36 @@ __device__ __forceinline__ void StoreStateRows(float* sp, int row0, const float 
       StoreStreamF4(sp + (row0 + i) * kDim + 8 * c, make_float4(s[i][c], s[i][c + 1], s[i][c + 2], s[i][c + 3]));
 }
 
+// Whether sequence j runs on the recurrent kernel with state slot `slot`: non-empty, not routed to the chunk kernels.
+__device__ __forceinline__ bool ChainMember(const GdnArgs& a, uint32_t j, int32_t slot) {
+  if (a.slots[j] != slot) return false;
+  const int32_t u0 = a.cu[j], u1 = a.cu[j + 1];
+  return u1 > u0 && (a.route_min <= 0 || u1 - u0 < a.route_min);
+}
+
 // Workgroup (sequence b, value head h, column quarter): the token-serial recurrence with its share of S in registers.
 template <bool kVec>
 __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint32_t h, uint32_t quarter) {
   __shared__ float red_sk[4][32], red_o[4][32];
-  const int32_t t0 = a.cu[b];
-  const int32_t t1 = a.cu[b + 1];
+  int32_t t0 = a.cu[b];
+  int32_t t1 = a.cu[b + 1];
   if (t1 <= t0) return;  // an empty sequence leaves its slot untouched
   if (a.route_min > 0 && t1 - t0 >= a.route_min) return;  // run by the chunk kernels
   const int32_t slot = a.slots[b];
   const bool has_slot = slot >= 0 && static_cast<uint64_t>(slot) < a.pool_slots;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // Sequences of one call that share a slot run in batch order, as CpuOps runs them: each starts from the state the
+  // one before it left (or from zero without use_initial_state). The workgroup of the first such sequence carries
+  // the state through all of them in registers and writes it once; the others' workgroups leave.
+  bool chained = false;
+  if (has_slot) {
+    int earlier = 0, later = 0;
+    for (uint32_t j = tid; j < a.batch; j += blockDim.x) {
+      if (j != b && ChainMember(a, j, slot)) (j < b ? earlier : later) = 1;
+    }
+    if (__syncthreads_or(earlier)) return;
+    chained = __syncthreads_or(later) != 0;
+  }
   const int rg = lane & 7;  // key rows 32 w + 4 rg .. + 3
   const int cg = lane >> 3;  // value columns 32 quarter + 4 cg .. + 3
   const int row0 = 32 * w + 4 * rg;
@@ -352,6 +372,7 @@ __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint
 #pragma unroll
     for (int i = 0; i < 4; ++i) s[i] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
+  for (uint32_t cur = b;;) {
   for (int32_t tok = t0; tok < t1; ++tok) {
     const uint16_t* qrow = a.q + static_cast<uint64_t>(tok) * a.q_stride + kh * kDim;
     const uint16_t* krow = a.k + static_cast<uint64_t>(tok) * a.k_stride + kh * kDim;
@@ -444,6 +465,19 @@ __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint
       *reinterpret_cast<uint2*>(a.out + (static_cast<uint64_t>(tok) * a.vh + h) * kDim + col) = pw;
     }
   }
+  if (!chained) break;
+  // The next sequence of the chain, if any (a uniform walk: every lane reads the same entries).
+  uint32_t next = cur + 1;
+  while (next < a.batch && !ChainMember(a, next, slot)) ++next;
+  if (next >= a.batch) break;
+  cur = next;
+  t0 = a.cu[cur];
+  t1 = a.cu[cur + 1];
+  if (!a.use_initial_state) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  }
   if (has_slot) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) StoreStreamF4(sp + (row0 + i) * kDim, s[i]);
@@ -473,6 +507,7 @@ GdnArgs MakeArgs(const RoostGatedDeltaRuleParams& p, const GateSource& gs = Gate
   a.pool_slots = p.state.length / StateElems(p);
   a.vh = p.v_heads;
   a.group = p.v_heads / p.k_heads;
+  a.batch = p.batch;
   a.use_initial_state = p.use_initial_state;
   a.scale = Scale(p);
   return a;
@@ -1724,9 +1759,9 @@ RoostStatus LaunchChunk(const RoostGatedDeltaRuleParams& p, const RoostWorkspace
 // The recurrent variant's routed path over a device region laid out as `l`: the sequences of kRouteMinTokens or more
 // tokens are cut into chunks (by the prep launch itself up to kFoldBatch sequences, else by RouteKernel from the device
 // cu_seqlens), and the prep launch also runs the recurrence of the shorter ones in workgroups of its own, beside the
-// prep workgroups: the chunks' chains leave most of the chip idle. The scan follows on the same stream. Sequences of
-// one call must use distinct state slots: two that share one race (they may run at the same time), as they do in the
-// reference's gather / scatter of the slots.
+// prep workgroups: the chunks' chains leave most of the chip idle. The scan follows on the same stream. Short
+// sequences that share a slot run in batch order (RecurrentUnit); a chunked sequence must have its slot to itself:
+// otherwise the two race (they may run at the same time), as they do in the reference's gather / scatter of the slots.
 RoostStatus LaunchRouted(const RoostGatedDeltaRuleParams& p, uint8_t* base, const ChunkArena& l, hipStream_t s,
                          const GateSource& gs = GateSource{}) {
   const bool fold = p.batch <= kFoldBatch;

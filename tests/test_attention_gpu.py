@@ -239,6 +239,69 @@ def test_decode_lse_is_base2_logsumexp(session):
             assert abs(lse[s, h] - want) < 1e-3
 
 
+def lse_reference(b: cases.PagedBatch, causal=True, window_left=-1) -> np.ndarray:
+    """[tokens, hq] base-2 log-sum-exp of each query row's visible scaled scores, in float64 from the de-paged
+    K (NaN for a row that sees no key). The library's convention for the optional lse output (FlashInfer's): log2 of
+    sum_j exp(s_j) with s_j = q.k_j / sqrt(d)."""
+    qv = cases.values(b.q, b.bf16).astype(np.float64)
+    kc = cases.values(b.k_cache, b.bf16).astype(np.float64)
+    out = np.full((b.tokens, b.hq), np.nan)
+    group = b.hq // b.hkv
+    for s in range(b.batch):
+        pages = b.kv_indices[b.kv_indptr[s]:b.kv_indptr[s + 1]]
+        kl = int(b.kv_lens[s])
+        if b.hnd:
+            keys = kc[pages].transpose(0, 2, 1, 3).reshape(-1, b.hkv, b.d)[:kl]
+        else:
+            keys = kc[pages].reshape(-1, b.hkv, b.d)[:kl]
+        q0, q1 = int(b.q_indptr[s]), int(b.q_indptr[s + 1])
+        for i in range(q1 - q0):
+            pos = kl - (q1 - q0) + i
+            hi = pos + 1 if causal or q1 - q0 == 1 else kl
+            lo = max(0, pos - window_left) if window_left >= 0 else 0
+            if hi <= lo:
+                continue
+            for h in range(b.hq):
+                sc = keys[lo:hi, h // group, :] @ qv[q0 + i, h] / np.sqrt(b.d)
+                m = sc.max()
+                out[q0 + i, h] = (m + np.log(np.exp(sc - m).sum())) / np.log(2.0)
+    return out
+
+
+LSE_PREFILL_CASES = [
+    # tile kernel: a 64-token chunk split into many pieces (one-token merge blocks) and a 256-token chunk in two
+    # pieces (the 8-token merge form), in one call
+    ("tile split, both merge forms", [(64, 12064), (256, 1156)], 16, False, True, -1, 256, True),
+    ("tile hd128 HND window", [(300, 2000), (17, 17)], 32, True, True, 200, 128, True),
+    ("tile non-causal", [(40, 700)], 16, False, False, -1, 256, True),
+    ("general kernel ps8", [(100, 300), (5, 40)], 8, False, True, -1, 256, True),
+    ("mixed step: decode rows beside chunks", [(1, 900), (200, 1200), (1, 3000), (1, 17)], 16, False, True, -1, 256,
+     True),
+    ("f32 prefill rows, split", [(6, 9000), (37, 300)], 16, False, True, -1, 256, False),
+]
+
+
+@pytest.mark.parametrize("name,seqs,ps,hnd,causal,window,d,bf16", LSE_PREFILL_CASES,
+                         ids=[c[0] for c in LSE_PREFILL_CASES])
+def test_prefill_lse_is_base2_logsumexp(session, name, seqs, ps, hnd, causal, window, d, bf16):
+    """The optional lse output of prefill calls (roost_kernels.h: PagedAttention's lse span) on every kernel that writes
+    it: the tile kernel and both merge forms, the general kernel, the decode rows of a mixed call and f32 prefill
+    rows, against float64 log-sum-exp. Bar: 2e-3 absolute (fp32 scores and sums over up to 12k keys)."""
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    b = cases.make_paged_batch(rng, [s[1] for s in seqs], [s[0] for s in seqs], page_size=ps, hnd=hnd, d=d, bf16=bf16)
+    dv = Dev(b, causal=causal, with_lse=True, window_left=window)
+    dv.lse.fill_(float("nan"))
+    session.launch(session.lib.entry(roost_amd.ATTENTION_VARIANT), dv.params(), key=("lse", name))
+    got = from_dev(dv.lse)
+    want = lse_reference(b, causal, window)
+    seen = ~np.isnan(want)
+    assert seen.any() and np.isfinite(got[seen]).all(), name
+    err = np.abs(got[seen] - want[seen]).max()
+    assert err < 2e-3, f"{name}: lse off by {err}"
+    # the output rows are unchanged by asking for lse
+    check_against_oracle(dv.result(), b, causal=causal, window_left=window) if bf16 else None
+
+
 def test_decode_zero_length_sequence_outputs_zeros(session):
     rng = np.random.default_rng(5)
     b = cases.make_paged_batch(rng, [40, 0, 17], [1, 1, 1])

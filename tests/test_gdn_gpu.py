@@ -131,6 +131,32 @@ def test_deterministic(session, variant):
     assert o1.tobytes() == o2.tobytes() and p1.tobytes() == p2.tobytes()
 
 
+SHARED_SLOT_CASES = [
+    ("decode, three rows on slot 3", [1, 1, 1, 1, 1], [3, 1, 3, 3, 0], True),
+    ("short rows, empty member, no init", [5, 7, 1, 0, 3], [2, 2, 4, 2, 2], False),
+    ("routed call, short rows share a slot", [100, 5, 3, 1], [0, 1, 1, 2], True),
+]
+
+
+@pytest.mark.parametrize("name,lens,slots,init", SHARED_SLOT_CASES, ids=[c[0] for c in SHARED_SLOT_CASES])
+def test_recurrent_shared_slots_run_in_batch_order(session, name, lens, slots, init):
+    """Sequences of one recurrent call that share a state slot (and run on the recurrent kernel: shorter than 16
+    tokens) run in batch order, as CpuOps runs them (CpuOps.Hybrid.cs:67-149): each starts from the state the one
+    before it wrote, or from zero without use_initial_state. Against the oracle, and bit-identical on a second run
+    (the variant registers DETERMINISTIC)."""
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    d = cases.make_gdn(rng, lens, 6, slots=slots)
+    want_o, want_pool = cases.oracle_gdn(d, use_initial_state=init)
+    o1, p1 = run(session, DevGdn(d), roost_amd.RECURRENT_VARIANT, init)
+    o2, p2 = run(session, DevGdn(d), roost_amd.RECURRENT_VARIANT, init)
+    assert o1.tobytes() == o2.tobytes() and p1.tobytes() == p2.tobytes()
+    cases.assert_close(cases.bf16_values(o1), cases.bf16_values(want_o), what=f"{name} output")
+    for s in set(slots):
+        cases.assert_close(p1[s], want_pool[s], max_abs=1.0, max_rel=cases.STATE_REL, what=f"{name} slot {s}")
+    for s in set(range(6)) - set(slots):
+        assert p1[s].tobytes() == d.pool[s].tobytes()
+
+
 def test_config4_chunked_prefill_then_recurrent_decode(session):
     """4 x 4096 tokens, 16 heads x 128, beta = sigmoid(N(0,1)), g = -softplus(N(0,1)),
     S0 ~ N(0, 0.01); chunked prefill vs CpuOps; then recurrent decode steps on 128 states vs CpuOps."""

@@ -304,6 +304,25 @@ def test_gdn_two_calls_equal_one_call_and_token_decode():
     assert np.max(np.abs(full - dec)) < 1e-5
 
 
+@pytest.mark.parametrize("init", [True, False])
+def test_gdn_shared_slots_run_in_batch_order(init):
+    """Sequences of one call that share a slot run in batch order (CpuOps.Hybrid.cs:67-149 is one sequential loop):
+    the multi-threaded call equals one single-sequence call per sequence, made one after another on the same pool."""
+    rng = np.random.default_rng(17)
+    lens, slots = [5, 7, 1, 0, 3], [2, 2, 4, 2, 2]
+    d = cases.make_gdn(rng, lens, 6, slots=slots)
+    out, pool = cases.oracle_gdn(d, use_initial_state=init, threads=8)
+    seq_pool = d.pool.copy()
+    seq_out = np.zeros_like(out)
+    for b, n in enumerate(lens):
+        t0 = int(d.cu[b])
+        one = cases.GdnData(d.fused[t0:t0 + n].copy(), d.g[t0:t0 + n].copy(), d.beta[t0:t0 + n].copy(), seq_pool,
+                            np.array([slots[b]], np.int32), np.array([0, n], np.int32), [n])
+        o, seq_pool = cases.oracle_gdn(one, use_initial_state=init, threads=1)
+        seq_out[t0:t0 + n] = o
+    assert np.array_equal(out, seq_out) and np.array_equal(pool, seq_pool)
+
+
 def test_gdn_scale_zero_means_inverse_root_kdim():
     def run(scale):
         return gdn_f64([1, 2, 3, 4], [0.5] * 4, [1], [0], [1], np.zeros(4, np.float32), [0], [0, 1], kh=1, vh=1, kd=4,
