@@ -569,7 +569,7 @@ constexpr int kLayerCols = 8;             // state columns per lane
 constexpr uint32_t kLayerMaxWidth = 4;
 constexpr int kLayerConvPerThread = 1;    // 3 x 128 channels over 512 threads
 
-__global__ void __launch_bounds__(kLayerThreads) GdnDecodeLayerKernel(LayerArgs L) {
+__global__ void __launch_bounds__(kLayerThreads, 4) GdnDecodeLayerKernel(LayerArgs L) {
   const GdnArgs& a = L.a;
   __shared__ float red_sk[2][4][8 * kLayerCols], red_o[2][4][8 * kLayerCols];
   __shared__ __align__(16) uint16_t xin[3 * kDim];  // this token's q, k and v, as the convolution rounds them
@@ -605,6 +605,12 @@ __global__ void __launch_bounds__(kLayerThreads) GdnDecodeLayerKernel(LayerArgs 
       if (L.conv_b != nullptr) cb[u] = Bf16ToF32(L.conv_b[cc[u]]);
     }
   }
+  // The norm's weights, requested now (into LDS: registers are at the two-workgroups-per-CU limit) so that their
+  // latency is not paid after the recurrence; the token loop's first barrier publishes them.
+  __shared__ float nws[kDim];
+  if (tid < static_cast<int>(kDim)) nws[tid] = LoadF(L.norm_w, L.norm_w_t, tid);
+  // Taps 1 .. width - 1 of the latest token: after the last one, the channel's new convolution state.
+  float taps[kLayerConvPerThread][kLayerMaxWidth - 1] = {};
   for (int32_t tok = t0; tok < t1; ++tok) {
     const int32_t rel = tok - t0;  // entry rel + k of [state, sequence] is tap k of this token
 #pragma unroll
@@ -624,6 +630,7 @@ __global__ void __launch_bounds__(kLayerThreads) GdnDecodeLayerKernel(LayerArgs 
             } else {
               tap = Bf16ToF32(L.x[static_cast<uint64_t>(t0 + hi - sl) * L.channels + cc[u]]);
             }
+            if (k > 0) taps[u][k - 1] = tap;
             acc = fmaf(cw[u][k], tap, acc);
           }
         }
@@ -655,6 +662,8 @@ __global__ void __launch_bounds__(kLayerThreads) GdnDecodeLayerKernel(LayerArgs 
     GateAt(a, static_cast<uint64_t>(tok), h, graw, beta);
     float ot[kLayerCols];
     RecurrentStep<kLayerCols>(s, q2, k2, q4, k4, vv, graw, beta, a.scale, w, rg, cg, red_sk[hf], red_o[hf], ot);
+    // After the last token the state is final: its stores go out now, in flight during the norm.
+    if (has_slot && tok + 1 == t1) StoreStateRows<kLayerCols>(sp, row0, s);
     if (w == 0 && rg == 0) {
 #pragma unroll
       for (int c = 0; c < kLayerCols; c += 4) {
@@ -683,39 +692,29 @@ __global__ void __launch_bounds__(kLayerThreads) GdnDecodeLayerKernel(LayerArgs 
       uint32_t yw[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const float y0 = xv[2 * q] * inv * LoadF(L.norm_w, L.norm_w_t, c0 + 2 * q) * SiluF(gv[2 * q]);
-        const float y1 = xv[2 * q + 1] * inv * LoadF(L.norm_w, L.norm_w_t, c0 + 2 * q + 1) * SiluF(gv[2 * q + 1]);
+        const float y0 = xv[2 * q] * inv * nws[c0 + 2 * q] * SiluF(gv[2 * q]);
+        const float y1 = xv[2 * q + 1] * inv * nws[c0 + 2 * q + 1] * SiluF(gv[2 * q + 1]);
         yw[q] = PackBf16Rne(y0, y1);
       }
       *reinterpret_cast<uint4*>(L.y + row * kDim + c0) = make_uint4(yw[0], yw[1], yw[2], yw[3]);
     }
   }
-  if (has_slot) StoreStateRows<kLayerCols>(sp, row0, s);
   if (L.conv_state_update != 0 && cslot_ok && sl > 0) {
-    // The slot keeps the last width - 1 entries of [state, sequence]: all of a channel's entries are read (some may
-    // be old state entries) before any is written, by the one thread that owns the channel.
-    const int32_t n = t1 - t0;
+    // The slot keeps the last width - 1 entries of [state, sequence], entries n .. n + width - 2: taps 1 .. width - 1
+    // of the last token, already in registers (values as read: bf16 inputs and state entries widen exactly). The one
+    // thread that owns the channel read every old entry before this write.
 #pragma unroll
     for (int u = 0; u < kLayerConvPerThread; ++u) {
       const int j = tid + u * static_cast<int>(kLayerThreads);
       if (j >= 3 * static_cast<int>(kDim)) continue;
       const uint64_t so = (static_cast<uint64_t>(cslot) * L.channels + cc[u]) * sl;
-      float next[kLayerMaxWidth - 1];
-#pragma unroll
-      for (int e = 0; e < static_cast<int>(kLayerMaxWidth) - 1; ++e) {
-        if (e < sl) {
-          const int32_t hi = n + e;
-          next[e] = hi < sl ? LoadF(L.conv_state, L.conv_state_t, static_cast<int64_t>(so + hi))
-                            : Bf16ToF32(L.x[static_cast<uint64_t>(t0 + hi - sl) * L.channels + cc[u]]);
-        }
-      }
 #pragma unroll
       for (int e = 0; e < static_cast<int>(kLayerMaxWidth) - 1; ++e) {
         if (e < sl) {
           if (L.conv_state_t == ROOST_DTYPE_BF16) {
-            static_cast<uint16_t*>(L.conv_state)[so + e] = F32ToBf16(next[e]);
+            static_cast<uint16_t*>(L.conv_state)[so + e] = F32ToBf16(taps[u][e]);
           } else {
-            static_cast<float*>(L.conv_state)[so + e] = next[e];
+            static_cast<float*>(L.conv_state)[so + e] = taps[u][e];
           }
         }
       }
