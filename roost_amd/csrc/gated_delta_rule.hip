@@ -346,23 +346,20 @@ __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint
   const int32_t slot = a.slots[b];
   const bool has_slot = slot >= 0 && static_cast<uint64_t>(slot) < a.pool_slots;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  // Sequences of one call that share a slot run in batch order, as CpuOps runs them: each starts from the state the
-  // one before it left (or from zero without use_initial_state). The workgroup of the first such sequence carries
-  // the state through all of them in registers and writes it once; the others' workgroups leave.
-  bool chained = false;
-  if (has_slot) {
-    int earlier = 0, later = 0;
-    for (uint32_t j = tid; j < a.batch; j += blockDim.x) {
-      if (j != b && ChainMember(a, j, slot)) (j < b ? earlier : later) = 1;
-    }
-    if (__syncthreads_or(earlier)) return;
-    chained = __syncthreads_or(later) != 0;
-  }
   const int rg = lane & 7;  // key rows 32 w + 4 rg .. + 3
   const int cg = lane >> 3;  // value columns 32 quarter + 4 cg .. + 3
   const int row0 = 32 * w + 4 * rg;
   const uint32_t col = 32 * quarter + 4 * cg;
   const uint32_t kh = h / a.group;
+  // Wavefront 0 scans the slot table for sequences sharing this one's slot (below). Its first kScanNow entries per
+  // lane are requested first of all: the memory counter retires in order, so waiting for them later does not wait
+  // for the state loads issued after them.
+  constexpr int kScanNow = 2;  // slot entries per lane requested up front (128 sequences)
+  int32_t sj[kScanNow] = {};
+  if (has_slot && w == 0) {
+#pragma unroll
+    for (int i = 0; i < kScanNow; ++i) sj[i] = a.slots[min(static_cast<uint32_t>(lane + 64 * i), a.batch - 1)];
+  }
   float4 s[4];
   float* sp = has_slot ? a.state + (static_cast<uint64_t>(slot) * a.vh + h) * kDim * kDim + col : nullptr;
   if (has_slot && a.use_initial_state) {
@@ -372,8 +369,15 @@ __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint
 #pragma unroll
     for (int i = 0; i < 4; ++i) s[i] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  for (uint32_t cur = b;;) {
-  for (int32_t tok = t0; tok < t1; ++tok) {
+  // Sequences of one call that share a slot run in batch order, as CpuOps runs them: each starts from the state the
+  // one before it left (or from zero without use_initial_state). The workgroup of the first such sequence carries
+  // the state through all of them in registers and writes it once; the others' workgroups leave.
+  // The scan runs in the first token step, after that step's loads are issued; its verdict reaches the other
+  // wavefronts through LDS at the step's first barrier.
+  __shared__ uint32_t chain_flags;  // bit 0: an earlier sequence shares the slot; bit 1: a later one does
+  bool scan_pending = has_slot, chained = false;
+  uint32_t cur = b;  // the sequence whose tokens run now (later members of a chain follow in turn)
+  for (int32_t tok = t0;;) {
     const uint16_t* qrow = a.q + static_cast<uint64_t>(tok) * a.q_stride + kh * kDim;
     const uint16_t* krow = a.k + static_cast<uint64_t>(tok) * a.k_stride + kh * kDim;
     // The norms: lane l squares elements 2l, 2l + 1 and the wavefront reduces, so that every wavefront has them whole.
@@ -411,6 +415,28 @@ __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint
       qq += __shfl_xor(qq, o, 64);
       kk += __shfl_xor(kk, o, 64);
     }
+    if (scan_pending && w == 0) {  // (the loads above have landed: the slot entries, requested earlier, have too)
+      // Tied to the norms, so that the compiler cannot move the scan above this step's loads.
+#pragma unroll
+      for (int i = 0; i < kScanNow; ++i) asm volatile("" : "+v"(sj[i]) : "v"(qq), "v"(kk));
+      bool earlier = false, later = false;
+#pragma unroll
+      for (int i = 0; i < kScanNow; ++i) {
+        const uint32_t jj = static_cast<uint32_t>(lane + 64 * i);
+        if (jj < a.batch && jj != b && sj[i] == slot && ChainMember(a, jj, slot)) {
+          earlier |= jj < b;
+          later |= jj > b;
+        }
+      }
+      for (uint32_t jj = static_cast<uint32_t>(lane + 64 * kScanNow); jj < a.batch; jj += 64) {
+        if (jj != b && ChainMember(a, jj, slot)) {
+          earlier |= jj < b;
+          later |= jj > b;
+        }
+      }
+      const uint32_t f = (__any(earlier) ? 1u : 0u) | (__any(later) ? 2u : 0u);  // whole-wavefront ballots
+      if (lane == 0) chain_flags = f;
+    }
     const float qn = a.scale / sqrtf(qq + 1e-6f);
     const float kn = 1.0f / sqrtf(kk + 1e-6f);
     // S^T k: this lane's 4 rows, the row group's 32, then the workgroup's 128 through LDS.
@@ -427,6 +453,12 @@ __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint
     for (int c = 0; c < 4; ++c) sk[c] = OctSum(sk[c]);
     if (rg == 0) *reinterpret_cast<float4*>(&red_sk[w][4 * cg]) = make_float4(sk[0], sk[1], sk[2], sk[3]);
     __syncthreads();
+    if (scan_pending) {
+      scan_pending = false;
+      const uint32_t f = chain_flags;
+      if (f & 1u) return;  // nothing written yet; every wavefront of the workgroup leaves here
+      chained = (f & 2u) != 0;
+    }
     float4 tot = *reinterpret_cast<const float4*>(&red_sk[0][4 * cg]);
 #pragma unroll
     for (int ww = 1; ww < 4; ++ww) {
@@ -464,19 +496,19 @@ __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint
       pw.y = PackBf16(ot.z, ot.w);
       *reinterpret_cast<uint2*>(a.out + (static_cast<uint64_t>(tok) * a.vh + h) * kDim + col) = pw;
     }
-  }
-  if (!chained) break;
-  // The next sequence of the chain, if any (a uniform walk: every lane reads the same entries).
-  uint32_t next = cur + 1;
-  while (next < a.batch && !ChainMember(a, next, slot)) ++next;
-  if (next >= a.batch) break;
-  cur = next;
-  t0 = a.cu[cur];
-  t1 = a.cu[cur + 1];
-  if (!a.use_initial_state) {
+    if (++tok < t1) continue;
+    if (!chained) break;
+    // The next sequence of the chain, if any (a uniform walk: every lane reads the same entries; rare).
+    uint32_t next = cur + 1;
+    while (next < a.batch && !ChainMember(a, next, slot)) ++next;
+    if (next >= a.batch) break;
+    cur = next;
+    tok = a.cu[cur];
+    t1 = a.cu[cur + 1];
+    if (!a.use_initial_state) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
+      for (int i = 0; i < 4; ++i) s[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
   }
   if (has_slot) {
 #pragma unroll
@@ -1193,7 +1225,7 @@ __global__ void __launch_bounds__(256, 6) WyPrepKernel(ChunkArgs ca) {
 // leaves idle, and the scan that follows has the chip to itself. The prep workgroups come first in dispatch order, so
 // that none of them waits behind recurrent ones for a slot.
 template <bool kVec>
-__global__ void __launch_bounds__(256) WyPrepRecurrentKernel(ChunkArgs ca) {
+__global__ void __launch_bounds__(256, 6) WyPrepRecurrentKernel(ChunkArgs ca) {
   static_assert(kRecThreads == 256, "the prep and recurrent workgroups share one size");
   const uint32_t vh = ca.a.vh, i = blockIdx.x, preps = ca.prep_x * vh;
   if (i < preps) {
