@@ -17,11 +17,6 @@ struct RoostContext {
   int32_t device;
   uint32_t flags;
   uint32_t compute_units;
-  // A second stream of the context's device (default priority, non-blocking) and the two events that fork work onto
-  // it from a caller's stream and join it back; all null when the device could not be opened at creation.
-  hipStream_t side = nullptr;
-  hipEvent_t fork = nullptr;
-  hipEvent_t join = nullptr;
 };
 
 // ---- Device-side helpers -------------------------------------------------------------------------------------------

@@ -51,6 +51,7 @@ using namespace roost_dev;
 
 constexpr uint32_t kGroup = 4;                  // query heads per KV head (Qwen3.5: 8 over 2)
 constexpr uint32_t kDecodeWgsPerCu = 2;        // decode workgroups resident per CU
+constexpr int kMixedDecodeWaves = 8;           // wavefronts of a decode workgroup in the one-launch mixed step
 constexpr int kDecodeRing = 2;                  // register ring depth: groups in flight per wavefront = ring - 1
 constexpr uint32_t kMaxMergeSplits = 1024;      // partials one sequence may be split into
 constexpr uint32_t kPrefillTileQ = 32;          // query tokens per workgroup of the general-page-size prefill
@@ -566,14 +567,15 @@ int64_t PrefillPieceTiles(const Items& items, int64_t total_tiles, uint32_t cus)
 }
 
 // Side by side or one after the other. A prefill call that also holds single-token sequences (a mixed worker step)
-// runs MFMA-bound tile kernels and HBM-bound decode kernels. A tile workgroup needs a whole CU (two 256-register
-// wavefronts per SIMD and 128 KB of LDS), so the two kinds cannot share CUs; but when the tile kernel is cut into fewer,
-// longer pieces it holds only as many CUs as it has pieces, and the decode kernel, launched right after it on a second
-// stream with its ranges sized for the remaining CUs, streams K/V on those. ChooseOverlap estimates both schedules with
-// rates measured on the MI355X -- a 64-key tile at head dim 256 takes ~3.7 us of a CU (less at smaller head dims), the
-// decode stream reaches 5.6 TB/s on 256 CUs and falls off as (CUs / 256)^0.26 (5.2 TB/s on 192), and a fork and join
-// cost ~18 us -- and keeps the cheaper. Config 5 (48 decode rows over 831 MB of K/V, two 512-token chunks): 64 pieces
-// of 36 tiles beside decode ranges for 192 CUs, 183 against 211 us one after the other.
+// runs MFMA-bound tile pieces and HBM-bound decode ranges. A tile workgroup needs a whole CU (two 256-register
+// wavefronts per SIMD and 128 KB of LDS), so the two kinds cannot share CUs; but when the tile items are cut into fewer,
+// longer pieces they hold only as many CUs as there are pieces, and decode ranges sized for the remaining CUs stream
+// K/V on those, both in one launch (MixedAttentionKernel). ChooseOverlap estimates both schedules with rates measured
+// on the MI355X -- a 64-key tile at head dim 256 takes ~3.7 us of a CU (less at smaller head dims), the decode stream
+// reaches 5.6 TB/s on 256 CUs and falls off as (CUs / 256)^0.26 (5.2 TB/s on 192), and the merged launch costs ~3 us
+// more than its longer side -- and keeps the cheaper. Config 5 (48 decode rows over 831 MB of K/V, two 512-token
+// chunks): 64 pieces beside decode ranges for the other 191 CUs. The decode side needs page sizes that are multiples
+// of 16 (its fast-page form).
 struct OverlapChoice {
   bool use = false;
   int64_t target = 0;    // piece size (tiles) of the tile kernel
@@ -582,7 +584,7 @@ struct OverlapChoice {
 
 constexpr double kTileUsD256 = 3.7;
 constexpr double kDecodeBytesPerUs = 5.6e6;
-constexpr double kForkJoinUs = 18.0;
+constexpr double kMixedLaunchUs = 3.0;
 
 double TileUs(uint32_t head_dim) { return kTileUsD256 * (0.25 + 0.75 * head_dim / 256.0); }
 double DecodeUs(double bytes, uint32_t cus_used, uint32_t cus) {
@@ -597,7 +599,7 @@ OverlapChoice ChooseOverlap(const RoostPagedAttentionParams& p, const Items& ite
   for (uint32_t b = 0; b < p.batch; ++b) {
     if (single(b)) dec_bytes += static_cast<double>(KvLenHost(p, b)) * VirtualHeads(p) * p.head_dim * 2.0 * 2.0;
   }
-  if (dec_bytes == 0.0 || items.empty() || cus < 2) return best;
+  if (dec_bytes == 0.0 || items.empty() || cus < 2 || p.page_size % 16 != 0) return best;
   int64_t longest = 0;
   for (const auto& it : items) longest = std::max(longest, ItemTiles(it.w));
   const double tile_us = TileUs(p.head_dim);
@@ -613,7 +615,7 @@ OverlapChoice ChooseOverlap(const RoostPagedAttentionParams& p, const Items& ite
     if (pieces >= static_cast<int64_t>(cus)) break;
     const uint32_t left = cus - static_cast<uint32_t>(pieces);
     const double us = std::max(static_cast<double>(piece_max + kPfPieceCost) * tile_us, DecodeUs(dec_bytes, left, cus)) +
-                      kForkJoinUs;
+                      kMixedLaunchUs;
     if (us < best_us) {
       best_us = us;
       best.use = true;
@@ -708,7 +710,9 @@ Layout PlanPrefill(const RoostPagedAttentionParams& p, uint32_t cus, unsigned ch
   }
   const uint64_t prefill_floats = l.float_bytes;
   l.overlap = overlap.use ? 1u : 0u;
-  AppendDecode(p, BuildDecode(p, overlap.use ? overlap.dec_cus : cus, single), l, host);
+  // Side by side, a decode workgroup has 8 wavefronts and a CU to itself: ranges for dec_cus / 2 CUs at
+  // kDecodeWgsPerCu 4-wavefront workgroups each are one range per free CU.
+  AppendDecode(p, BuildDecode(p, overlap.use ? std::max(1u, overlap.dec_cus / kDecodeWgsPerCu) : cus, single), l, host);
   PlaceFloats(p, prefill_floats, l);
   return l;
 }
@@ -1110,35 +1114,30 @@ __device__ __forceinline__ void LdsBarrier() {
 // K/V is fetched into a second register buffer while the current group is computed. Workgroup (range, KV head)
 // processes the pieces of its range in turn; a piece that is not a whole sequence writes fp32 partials that
 // DecodeMergeKernel combines in key order.
-template <typename T, int D, bool kFastPage>
-__global__ void __launch_bounds__(256, kDecodeWgsPerCu) DecodeKernel(const T* __restrict__ q, T* __restrict__ out, float* __restrict__ lse,
-                                                    KvView kv, const int32_t* __restrict__ kv_indices,
-                                                    const DecodeWork* __restrict__ work,
-                                                    const int32_t* __restrict__ range_ptr,
-
-                                                    float* __restrict__ part_o, float* __restrict__ part_ml,
-                                                    const int32_t* __restrict__ q_rows,
-                                                    uint32_t q_heads, uint32_t heads_per_wg, float scale_log2,
-                                                    int32_t window, uint32_t causal, SoftCap cap) {
+template <typename T, int D, bool kFastPage, int kWaves>
+__device__ __forceinline__ void DecodeBody(const T* __restrict__ q, T* __restrict__ out, float* __restrict__ lse,
+                                           KvView kv, const int32_t* __restrict__ kv_indices,
+                                           const DecodeWork* __restrict__ work, const int32_t* __restrict__ range_ptr,
+                                           float* __restrict__ part_o, float* __restrict__ part_ml,
+                                           const int32_t* __restrict__ q_rows, uint32_t q_heads, uint32_t heads_per_wg,
+                                           float scale_log2, int32_t window, uint32_t causal, SoftCap cap,
+                                           uint32_t block, float* x_lds, float* m_lds, float* l_lds, float* o_lds) {
+  // LDS (the caller's): x_lds [kWaves][64], m_lds and l_lds [kWaves][kGroup], o_lds [kWaves][kGroup][D] floats.
   using C = DecodeCfg<T, D>;
   constexpr int kVec = C::kVec, kLpr = C::kLpr, kTpi = C::kTpi, kNi = C::kNi;
   constexpr bool kMfma = sizeof(T) == 2;  // bf16: q.k on MFMA; f32: the VALU reduce-scatter path
-  __shared__ float x_lds[4][64];
-  __shared__ float m_lds[4][kGroup];
-  __shared__ float l_lds[4][kGroup];
-  __shared__ float o_lds[4][kGroup][D];
 
   // Both KV heads of a range are adjacent in launch order, so the two halves of each NHD page row are read together.
   // A workgroup serves heads_per_wg (1, 2 or 4) KV heads of one range, 4 / heads_per_wg wavefronts per head, so the
   // KV heads of each page row (adjacent in an NHD pool) are read by one CU at the same time.
   const uint32_t hblocks = kv.vheads / heads_per_wg;
-  const uint32_t range = blockIdx.x / hblocks;
+  const uint32_t range = block / hblocks;
   const int lane = threadIdx.x & 63;
   // The wavefront index is uniform within a wavefront; saying so lets the group's page id be a scalar load.
   const int wave_id = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t kvh = (blockIdx.x % hblocks) * heads_per_wg + wave_id % heads_per_wg;
+  const uint32_t kvh = (block % hblocks) * heads_per_wg + wave_id % heads_per_wg;
   const int wave = wave_id / static_cast<int>(heads_per_wg);           // index among this head's wavefronts
-  const int waves_per_head = 4 / static_cast<int>(heads_per_wg);
+  const int waves_per_head = kWaves / static_cast<int>(heads_per_wg);
   const int r = lane % kLpr;   // which 16-byte slice of a row
   const int ri = lane / kLpr;  // which row of a wave-wide load
   const int kperm = r / static_cast<int>(kGroup);  // this lane's token-slot permutation for K
@@ -1279,9 +1278,9 @@ __global__ void __launch_bounds__(256, kDecodeWgsPerCu) DecodeKernel(const T* __
         load(gi + s + kLast, kbuf[nxt], vbuf[nxt], valid[nxt]);
         if (gi + s < nw) {
           if constexpr (kMfma) {
-            DecodeGroupMfma<D>(st, kbuf[s], vbuf[s], valid[s], qb, x_lds[wave_id], r, ri, lane, scale_log2, cap);
+            DecodeGroupMfma<D>(st, kbuf[s], vbuf[s], valid[s], qb, x_lds + 64 * wave_id, r, ri, lane, scale_log2, cap);
           } else {
-            DecodeGroup<T, D, QW>(st, kbuf[s], vbuf[s], valid[s], qr, x_lds[wave_id], r, ri, lane, scale_log2, cap);
+            DecodeGroup<T, D, QW>(st, kbuf[s], vbuf[s], valid[s], qr, x_lds + 64 * wave_id, r, ri, lane, scale_log2, cap);
           }
         }
       }
@@ -1300,32 +1299,32 @@ __global__ void __launch_bounds__(256, kDecodeWgsPerCu) DecodeKernel(const T* __
 #pragma unroll
   for (int mk = kMfma ? 16 : 4; mk < 64; mk <<= 1) lsum += ShflXor(lsum, mk);
   if (lane < (int)kGroup) {
-    m_lds[wave_id][lane] = Pick4(st.m, lane);
-    l_lds[wave_id][lane] = lsum;  // lane h holds the total of head h
+    m_lds[wave_id * kGroup + lane] = Pick4(st.m, lane);
+    l_lds[wave_id * kGroup + lane] = lsum;  // lane h holds the total of head h
   }
   if (ri == 0) {
 #pragma unroll
     for (int h = 0; h < (int)kGroup; ++h)
 #pragma unroll
-      for (int e = 0; e < kVec; ++e) o_lds[wave_id][h][r * kVec + e] = st.acc[h][e];
+      for (int e = 0; e < kVec; ++e) o_lds[(wave_id * kGroup + h) * D + r * kVec + e] = st.acc[h][e];
   }
   LdsBarrier();
 
   // Workgroup: merge the wavefronts of each KV head, then write the final row or this piece's partial.
   const int split = wk.slot;
-  for (int idx = threadIdx.x; idx < (int)(heads_per_wg * kGroup * D); idx += 256) {
+  for (int idx = threadIdx.x; idx < (int)(heads_per_wg * kGroup * D); idx += 64 * kWaves) {
     const int hk = idx / (kGroup * D);  // local KV head: wavefronts hk, hk + heads_per_wg, ...
     const int h = (idx / D) % kGroup;
     const int d = idx % D;
     float M = -INFINITY;
-    for (int w = hk; w < 4; w += heads_per_wg) M = fmaxf(M, m_lds[w][h]);
+    for (int w = hk; w < kWaves; w += heads_per_wg) M = fmaxf(M, m_lds[w * kGroup + h]);
     float o = 0.0f, L = 0.0f;
-    for (int w = hk; w < 4; w += heads_per_wg) {
-      const float f = m_lds[w][h] == -INFINITY ? 0.0f : exp2f(m_lds[w][h] - M);
-      o += o_lds[w][h][d] * f;
-      L += l_lds[w][h] * f;
+    for (int w = hk; w < kWaves; w += heads_per_wg) {
+      const float f = m_lds[w * kGroup + h] == -INFINITY ? 0.0f : exp2f(m_lds[w * kGroup + h] - M);
+      o += o_lds[(w * kGroup + h) * D + d] * f;
+      L += l_lds[w * kGroup + h] * f;
     }
-    const uint32_t qh = ((blockIdx.x % hblocks) * heads_per_wg + hk) * kGroup + h;
+    const uint32_t qh = ((block % hblocks) * heads_per_wg + hk) * kGroup + h;
     if (split < 0) {
       const uint64_t row = tok * q_heads + qh;
       out[row * D + d] = GateOut<T>(kv.out_gate, row * D + d, Vec<T>::Narrow(L > 0.0f ? o / L : 0.0f));
@@ -1341,6 +1340,26 @@ __global__ void __launch_bounds__(256, kDecodeWgsPerCu) DecodeKernel(const T* __
   }
   LdsBarrier();  // the next piece reuses the LDS merge buffers
   }
+}
+
+
+// Split-K paged decode, one workgroup of 4 wavefronts per (range, head block): DecodeBody with LDS of its own.
+template <typename T, int D, bool kFastPage>
+__global__ void __launch_bounds__(256, kDecodeWgsPerCu) DecodeKernel(const T* __restrict__ q, T* __restrict__ out, float* __restrict__ lse,
+                                                    KvView kv, const int32_t* __restrict__ kv_indices,
+                                                    const DecodeWork* __restrict__ work,
+                                                    const int32_t* __restrict__ range_ptr,
+                                                    float* __restrict__ part_o, float* __restrict__ part_ml,
+                                                    const int32_t* __restrict__ q_rows,
+                                                    uint32_t q_heads, uint32_t heads_per_wg, float scale_log2,
+                                                    int32_t window, uint32_t causal, SoftCap cap) {
+  __shared__ float x_lds[4][64];
+  __shared__ float m_lds[4][kGroup];
+  __shared__ float l_lds[4][kGroup];
+  __shared__ float o_lds[4][kGroup][D];
+  DecodeBody<T, D, kFastPage, 4>(q, out, lse, kv, kv_indices, work, range_ptr, part_o, part_ml, q_rows, q_heads,
+                                 heads_per_wg, scale_log2, window, causal, cap, blockIdx.x, &x_lds[0][0], &m_lds[0][0],
+                                 &l_lds[0][0], &o_lds[0][0][0]);
 }
 
 // Combines the pieces of each split sequence in key order: one workgroup per (sequence, query head), D threads, one
@@ -1703,25 +1722,29 @@ __device__ __forceinline__ u32x2_t LdsTr16(const unsigned char* base, uint32_t o
 // kCap: the call caps its logits; `cap` is then the cap in the kernel's unscaled score units (the log2-unit cap divided
 // by scale_log2, its slope multiplied by it), so that a capped score stays unscaled like an uncapped one. A separate
 // instantiation keeps the cap's registers out of the uncapped kernel, which otherwise spills at head dim 256.
+template <int D>
+constexpr int kPfTileBytes = kPrefillTileK * 2 * D;  // one 64-key K or V tile in LDS
+
+// The tile kernel's work for item `item`; `tiles` is the caller's LDS, [2 buffers][K, V][kPfTileBytes<D>].
 template <int D, bool kCap>
-__global__ void __launch_bounds__(512, 1)
-    PrefillTileKernel(const uint16_t* __restrict__ q, uint16_t* __restrict__ out, float* __restrict__ lse, KvView kv,
-                      const int32_t* __restrict__ kv_indices, const int32_t* __restrict__ q_indptr,
-                      const PrefillWork* __restrict__ work, uint16_t* __restrict__ part_o, float* __restrict__ part_ml,
-                      uint32_t q_heads, uint32_t causal, uint32_t ps_shift, float scale_log2, int32_t window,
-                      SoftCap cap) {
+__device__ __forceinline__ void PrefillTileBody(const uint16_t* __restrict__ q, uint16_t* __restrict__ out,
+                                                float* __restrict__ lse, KvView kv,
+                                                const int32_t* __restrict__ kv_indices,
+                                                const int32_t* __restrict__ q_indptr,
+                                                const PrefillWork* __restrict__ work, uint16_t* __restrict__ part_o,
+                                                float* __restrict__ part_ml, uint32_t q_heads, uint32_t causal,
+                                                uint32_t ps_shift, float scale_log2, int32_t window, SoftCap cap,
+                                                uint32_t item, unsigned char (*tiles)[2][kPfTileBytes<D>]) {
   static_assert(D == 64 || D == 128 || D == 256, "the tile kernel is built for head dims 64, 128 and 256");
   constexpr int kRowB = 2 * D;                  // bytes of one K or V row in LDS
   constexpr int kPieces = D / 8;                // 16-byte pieces per row
   constexpr int kRowsPerDma = 1024 / kRowB;     // rows one 64-lane global_load_lds_dwordx4 fills
   constexpr int kKs = D / 16;                   // K = 16 steps of S^T = K Q^T
   constexpr int kDt = D / 32;                   // 32-dim blocks of O^T
-  constexpr int kTileBytes = kPrefillTileK * kRowB;  // one 64-key K or V tile
   constexpr int kNv = kDt / 2;                  // V blocks each wavefront copies per tile (4 kDt blocks / 8)
   constexpr int kSw = (kPieces < 16 ? kPieces : 16) - 1;  // K swizzle mask
-  __shared__ __attribute__((aligned(16))) unsigned char tiles[2][2][kTileBytes];  // [buffer][K, V]
 
-  const PrefillWork wk = work[blockIdx.x];
+  const PrefillWork wk = work[item];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1999,6 +2022,56 @@ __global__ void __launch_bounds__(512, 1)
   }
 }
 
+
+template <int D, bool kCap>
+__global__ void __launch_bounds__(512, 1)
+    PrefillTileKernel(const uint16_t* __restrict__ q, uint16_t* __restrict__ out, float* __restrict__ lse, KvView kv,
+                      const int32_t* __restrict__ kv_indices, const int32_t* __restrict__ q_indptr,
+                      const PrefillWork* __restrict__ work, uint16_t* __restrict__ part_o, float* __restrict__ part_ml,
+                      uint32_t q_heads, uint32_t causal, uint32_t ps_shift, float scale_log2, int32_t window,
+                      SoftCap cap) {
+  __shared__ __attribute__((aligned(16))) unsigned char tiles[2][2][kPfTileBytes<D>];  // [buffer][K, V]
+  PrefillTileBody<D, kCap>(q, out, lse, kv, kv_indices, q_indptr, work, part_o, part_ml, q_heads, causal, ps_shift,
+                           scale_log2, window, cap, blockIdx.x, tiles);
+}
+
+// A mixed step's attention in one launch: workgroups [0, items) run the tile pieces, the rest the decode ranges with 8
+// wavefronts each (one range of one KV-head block per CU, 8 / heads_per_wg wavefronts per head). Tile workgroups come
+// first in launch order, so they take their CUs before the decode ranges fill the others. Both kinds use the one LDS
+// buffer in their own layout (a decode workgroup needs far less than a tile one, and neither shares its CU).
+template <int D>
+constexpr int kMixedDecodeLds = 4 * (kMixedDecodeWaves * 64 + 2 * kMixedDecodeWaves * kGroup +
+                                     kMixedDecodeWaves * kGroup * D);
+
+template <int D, bool kCap>
+__global__ void __launch_bounds__(512, 1)
+    MixedAttentionKernel(const uint16_t* __restrict__ q, uint16_t* __restrict__ out, float* __restrict__ lse,
+                         KvView kv, const int32_t* __restrict__ kv_indices, const int32_t* __restrict__ q_indptr,
+                         const PrefillWork* __restrict__ work, uint16_t* __restrict__ part_o,
+                         float* __restrict__ part_ml, uint32_t q_heads, uint32_t causal, uint32_t ps_shift,
+                         float scale_log2, int32_t window, SoftCap raw_cap, uint32_t items,
+                         const DecodeWork* __restrict__ dec_work, const int32_t* __restrict__ dec_range_ptr,
+                         float* __restrict__ dec_part_o, float* __restrict__ dec_part_ml, uint32_t heads_per_wg,
+                         SoftCap cap) {
+  constexpr int kTileLds = 2 * 2 * kPfTileBytes<D>;
+  constexpr int kLds = kTileLds > kMixedDecodeLds<D> ? kTileLds : kMixedDecodeLds<D>;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kLds];
+  if (blockIdx.x < items) {
+    PrefillTileBody<D, kCap>(q, out, lse, kv, kv_indices, q_indptr, work, part_o, part_ml, q_heads, causal, ps_shift,
+                             scale_log2, window, raw_cap, blockIdx.x,
+                             reinterpret_cast<unsigned char (*)[2][kPfTileBytes<D>]>(lds));
+    return;
+  }
+  constexpr int W = kMixedDecodeWaves;
+  float* x_lds = reinterpret_cast<float*>(lds);
+  float* m_lds = x_lds + W * 64;
+  float* l_lds = m_lds + W * kGroup;
+  float* o_lds = l_lds + W * kGroup;
+  DecodeBody<uint16_t, D, true, W>(q, out, lse, kv, kv_indices, dec_work, dec_range_ptr, dec_part_o, dec_part_ml,
+                                   q_indptr, q_heads, heads_per_wg, scale_log2, window, causal, cap,
+                                   blockIdx.x - items, x_lds, m_lds, l_lds, o_lds);
+}
+
 // Combines the pieces of a split prefill item: block (merge, group of kRows tokens) of kGroup * D / 4 threads; thread t
 // handles query head t / (D / 4), dims 4 (t % (D / 4)) .. +3 of each of the group's tokens. Pieces are combined in
 // key order (deterministic). Merges of two pieces (the plan puts them first) run 8 tokens per block with every load
@@ -2107,13 +2180,28 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// The decode pieces' partials: fp32 rows (dec_splits x q_heads x D), then their (max, sum) pairs.
+template <typename T, int D>
+RoostStatus LaunchDecodeMerge(const RoostPagedAttentionParams& p, const PlanRecord& rec, unsigned char* dev,
+                              const KvView& kv, hipStream_t stream) {
+  if (rec.dec_merges == 0) return ROOST_STATUS_OK;
+  const auto* merges = reinterpret_cast<const DecodeMerge*>(dev + rec.dec_merge_offset);
+  auto* part_o = reinterpret_cast<float*>(dev + rec.dec_float_offset);
+  auto* part_ml = part_o + rec.dec_splits * p.q_heads * D;
+  const auto* q_rows =
+      p.mode == ROOST_ATTENTION_PREFILL ? static_cast<const int32_t*>(p.q_indptr.address) : nullptr;
+  hipLaunchKernelGGL((DecodeMergeKernel<T, D>), dim3(static_cast<uint32_t>(rec.dec_merges * p.q_heads)), dim3(D), 0,
+                     stream, static_cast<T*>(p.output.address), static_cast<float*>(p.lse.address), merges, part_o,
+                     part_ml, q_rows, p.q_heads, kv.out_gate);
+  return roost::HipStatus(hipGetLastError(), "paged_attention", "decode merge launch");
+}
+
 template <typename T, int D>
 RoostStatus LaunchDecode(const RoostPagedAttentionParams& p, const PlanRecord& rec, unsigned char* dev, const KvView& kv,
                          float scale_log2, hipStream_t stream) {
   if (rec.dec_ranges == 0) return ROOST_STATUS_OK;
   const auto* items = reinterpret_cast<const DecodeWork*>(dev + rec.dec_item_offset);
   const auto* range_ptr = reinterpret_cast<const int32_t*>(dev + rec.dec_range_offset);
-  const auto* merges = reinterpret_cast<const DecodeMerge*>(dev + rec.dec_merge_offset);
   auto* part_o = reinterpret_cast<float*>(dev + rec.dec_float_offset);
   auto* part_ml = part_o + rec.dec_splits * p.q_heads * D;
   // In a prefill call the decode pieces are its single-token sequences, whose query rows are q_indptr[seq].
@@ -2133,10 +2221,81 @@ RoostStatus LaunchDecode(const RoostPagedAttentionParams& p, const PlanRecord& r
                        WindowOf(p), p.causal, CapOf(p));
   }
   ROOST_RETURN_IF_FAILED(roost::HipStatus(hipGetLastError(), "paged_attention", "decode launch"));
-  if (rec.dec_merges == 0) return ROOST_STATUS_OK;
-  hipLaunchKernelGGL((DecodeMergeKernel<T, D>), dim3(static_cast<uint32_t>(rec.dec_merges * p.q_heads)), dim3(D), 0,
-                     stream, out, lse, merges, part_o, part_ml, q_rows, p.q_heads, kv.out_gate);
-  return roost::HipStatus(hipGetLastError(), "paged_attention", "decode merge launch");
+  return LaunchDecodeMerge<T, D>(p, rec, dev, kv, stream);
+}
+
+// Partials of the tile pieces: bf16 rows of the pieces' normalised outputs, then their fp32 (max, sum) pairs.
+uint16_t* PrefillPartO(const RoostPagedAttentionParams& p, const PlanRecord& rec, unsigned char* dev) {
+  return reinterpret_cast<uint16_t*>(dev + rec.float_offset);
+}
+float* PrefillPartMl(const RoostPagedAttentionParams& p, const PlanRecord& rec, unsigned char* dev) {
+  return reinterpret_cast<float*>(PrefillPartO(p, rec, dev) + rec.splits * kPfRows * p.head_dim);
+}
+
+RoostStatus LaunchPrefillMerge(const RoostPagedAttentionParams& p, const PlanRecord& rec, unsigned char* dev,
+                               const KvView& kv, hipStream_t stream) {
+  if (rec.merges == 0) return ROOST_STATUS_OK;
+  const auto* q_indptr = static_cast<const int32_t*>(p.q_indptr.address);
+  auto* outp = static_cast<uint16_t*>(p.output.address);
+  auto* lsep = static_cast<float*>(p.lse.address);
+  uint16_t* part_o = PrefillPartO(p, rec, dev);
+  float* part_ml = PrefillPartMl(p, rec, dev);
+  const auto* mg = reinterpret_cast<const PrefillMerge*>(dev + rec.merge_offset);
+  const uint32_t two = rec.merges_two, rest = static_cast<uint32_t>(rec.merges) - rec.merges_two;
+  const dim3 block(kGroup * p.head_dim / 4);
+  const dim3 g(two * (kPfTokens / kPfMergeRows) + rest * kPfTokens);
+  if (p.head_dim == 64) {
+    hipLaunchKernelGGL(PrefillMergeKernel<64>, g, block, 0, stream, outp, lsep, mg, part_o, part_ml, q_indptr,
+                       p.q_heads, two, kv.out_gate);
+  } else if (p.head_dim == 128) {
+    hipLaunchKernelGGL(PrefillMergeKernel<128>, g, block, 0, stream, outp, lsep, mg, part_o, part_ml, q_indptr,
+                       p.q_heads, two, kv.out_gate);
+  } else {
+    hipLaunchKernelGGL(PrefillMergeKernel<256>, g, block, 0, stream, outp, lsep, mg, part_o, part_ml, q_indptr,
+                       p.q_heads, two, kv.out_gate);
+  }
+  return roost::HipStatus(hipGetLastError(), "paged_attention", "prefill merge launch");
+}
+
+// A mixed step the plan chose to run in one launch (PlanRecord::overlap): the tile pieces and decode ranges on
+// MixedAttentionKernel, then both merge kernels, all on the caller's stream.
+RoostStatus LaunchMixed(const RoostPagedAttentionParams& p, const PlanRecord& rec, unsigned char* dev, const KvView& kv,
+                        float scale_log2, hipStream_t stream) {
+  const auto* q16 = static_cast<const uint16_t*>(p.q.address);
+  const auto* q_indptr = static_cast<const int32_t*>(p.q_indptr.address);
+  auto* outp = static_cast<uint16_t*>(p.output.address);
+  auto* lsep = static_cast<float*>(p.lse.address);
+  const auto* items = reinterpret_cast<const PrefillWork*>(dev);
+  const uint32_t ps_shift = static_cast<uint32_t>(__builtin_ctz(p.page_size));
+  const SoftCap cap = CapOf(p);
+  const SoftCap raw{cap.capl / scale_log2, cap.k * scale_log2};
+  const bool capped = cap.capl != 0.0f;
+  const uint32_t hpw = HeadsPerWorkgroup(VirtualHeads(p));
+  const uint32_t n_items = static_cast<uint32_t>(rec.work_items);
+  const dim3 grid(n_items + static_cast<uint32_t>(rec.dec_ranges * (VirtualHeads(p) / hpw)));
+  const auto* dec_items = reinterpret_cast<const DecodeWork*>(dev + rec.dec_item_offset);
+  const auto* dec_ranges = reinterpret_cast<const int32_t*>(dev + rec.dec_range_offset);
+  auto* dec_o = reinterpret_cast<float*>(dev + rec.dec_float_offset);
+  auto* dec_ml = dec_o + rec.dec_splits * p.q_heads * p.head_dim;
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, dim3(512), 0, stream, q16, outp, lsep, kv, kv.kv_indices, q_indptr, items,
+                       PrefillPartO(p, rec, dev), PrefillPartMl(p, rec, dev), p.q_heads, p.causal, ps_shift,
+                       scale_log2, WindowOf(p), raw, n_items, dec_items, dec_ranges, dec_o, dec_ml, hpw, cap);
+  };
+  if (p.head_dim == 64) {
+    capped ? launch(MixedAttentionKernel<64, true>) : launch(MixedAttentionKernel<64, false>);
+  } else if (p.head_dim == 128) {
+    capped ? launch(MixedAttentionKernel<128, true>) : launch(MixedAttentionKernel<128, false>);
+  } else {
+    capped ? launch(MixedAttentionKernel<256, true>) : launch(MixedAttentionKernel<256, false>);
+  }
+  ROOST_RETURN_IF_FAILED(roost::HipStatus(hipGetLastError(), "paged_attention", "mixed attention launch"));
+  ROOST_RETURN_IF_FAILED(LaunchPrefillMerge(p, rec, dev, kv, stream));
+  switch (p.head_dim) {
+    case 64: return LaunchDecodeMerge<uint16_t, 64>(p, rec, dev, kv, stream);
+    case 128: return LaunchDecodeMerge<uint16_t, 128>(p, rec, dev, kv, stream);
+    default: return LaunchDecodeMerge<uint16_t, 256>(p, rec, dev, kv, stream);
+  }
 }
 
 RoostStatus LaunchPrefill(const RoostPagedAttentionParams& p, const PlanRecord& rec, unsigned char* dev, const KvView& kv,
@@ -2147,9 +2306,8 @@ RoostStatus LaunchPrefill(const RoostPagedAttentionParams& p, const PlanRecord& 
   auto* outp = static_cast<uint16_t*>(p.output.address);
   auto* lsep = static_cast<float*>(p.lse.address);
   if (PrefillFastPath(p)) {
-    // Partials: bf16 rows of the pieces' normalised outputs, then their fp32 (max, sum) pairs.
-    auto* part_o = reinterpret_cast<uint16_t*>(dev + rec.float_offset);
-    auto* part_ml = reinterpret_cast<float*>(part_o + rec.splits * kPfRows * p.head_dim);
+    uint16_t* part_o = PrefillPartO(p, rec, dev);
+    float* part_ml = PrefillPartMl(p, rec, dev);
     const dim3 grid(static_cast<uint32_t>(rec.work_items));
     const auto* q16 = static_cast<const uint16_t*>(p.q.address);
     const uint32_t ps_shift = static_cast<uint32_t>(__builtin_ctz(p.page_size));
@@ -2169,22 +2327,7 @@ RoostStatus LaunchPrefill(const RoostPagedAttentionParams& p, const PlanRecord& 
       capped ? launch(PrefillTileKernel<256, true>) : launch(PrefillTileKernel<256, false>);
     }
     ROOST_RETURN_IF_FAILED(roost::HipStatus(hipGetLastError(), "paged_attention", "prefill launch"));
-    if (rec.merges == 0) return ROOST_STATUS_OK;
-    const auto* mg = reinterpret_cast<const PrefillMerge*>(dev + rec.merge_offset);
-    const uint32_t two = rec.merges_two, rest = static_cast<uint32_t>(rec.merges) - rec.merges_two;
-    const dim3 block(kGroup * p.head_dim / 4);
-    const dim3 g(two * (kPfTokens / kPfMergeRows) + rest * kPfTokens);
-    if (p.head_dim == 64) {
-      hipLaunchKernelGGL(PrefillMergeKernel<64>, g, block, 0, stream, outp, lsep, mg, part_o, part_ml, q_indptr,
-                         p.q_heads, two, kv.out_gate);
-    } else if (p.head_dim == 128) {
-      hipLaunchKernelGGL(PrefillMergeKernel<128>, g, block, 0, stream, outp, lsep, mg, part_o, part_ml, q_indptr,
-                         p.q_heads, two, kv.out_gate);
-    } else {
-      hipLaunchKernelGGL(PrefillMergeKernel<256>, g, block, 0, stream, outp, lsep, mg, part_o, part_ml, q_indptr,
-                         p.q_heads, two, kv.out_gate);
-    }
-    return roost::HipStatus(hipGetLastError(), "paged_attention", "prefill merge launch");
+    return LaunchPrefillMerge(p, rec, dev, kv, stream);
   }
   hipLaunchKernelGGL(PrefillKernel, dim3(static_cast<uint32_t>(rec.work_items)), dim3(256), 0, stream,
                      static_cast<const uint16_t*>(p.q.address), outp, lsep, kv, q_indptr, items, p.q_heads, p.causal,
@@ -2357,9 +2500,7 @@ RoostStatus RunAttention(RoostContext* ctx, const void* params, const RoostWorks
       }
     }
     // The multi-token sequences on the tile kernels, then the single-token ones on the decode kernels (bf16 in prefill
-    // mode, at the call's head dim). When the plan chose to overlap them (ChooseOverlap), the decode kernels run on
-    // the context's side stream, forked after the caller's earlier work and joined back before returning; the tile
-    // kernel is issued first so that its workgroups hold their CUs before the decode ranges fill the rest.
+    // mode, at the call's head dim), or both in one launch when the plan chose that (ChooseOverlap).
     if (p.q.dtype == ROOST_DTYPE_F32) {  // every query token is a row of the f32 decode kernel
       switch (p.head_dim) {
         case 64: return LaunchDecode<float, 64>(p, rec, dev, kv, scale_log2, s);
@@ -2367,21 +2508,13 @@ RoostStatus RunAttention(RoostContext* ctx, const void* params, const RoostWorks
         default: return LaunchDecode<float, 256>(p, rec, dev, kv, scale_log2, s);
       }
     }
-    const bool side = rec.overlap != 0 && ctx != nullptr && ctx->side != nullptr;
-    hipStream_t ds = side ? ctx->side : s;
-    if (side) ROOST_RETURN_IF_FAILED(HipStatus(hipEventRecord(ctx->fork, s), kOp, "fork event"));
+    if (rec.overlap != 0) return LaunchMixed(p, rec, dev, kv, scale_log2, s);
     ROOST_RETURN_IF_FAILED(LaunchPrefill(p, rec, dev, kv, scale_log2, s));
-    if (side) ROOST_RETURN_IF_FAILED(HipStatus(hipStreamWaitEvent(ds, ctx->fork, 0), kOp, "fork wait"));
-    RoostStatus st;
     switch (p.head_dim) {
-      case 64: st = LaunchDecode<uint16_t, 64>(p, rec, dev, kv, scale_log2, ds); break;
-      case 128: st = LaunchDecode<uint16_t, 128>(p, rec, dev, kv, scale_log2, ds); break;
-      default: st = LaunchDecode<uint16_t, 256>(p, rec, dev, kv, scale_log2, ds); break;
+      case 64: return LaunchDecode<uint16_t, 64>(p, rec, dev, kv, scale_log2, s);
+      case 128: return LaunchDecode<uint16_t, 128>(p, rec, dev, kv, scale_log2, s);
+      default: return LaunchDecode<uint16_t, 256>(p, rec, dev, kv, scale_log2, s);
     }
-    ROOST_RETURN_IF_FAILED(st);
-    if (!side) return ROOST_STATUS_OK;
-    ROOST_RETURN_IF_FAILED(HipStatus(hipEventRecord(ctx->join, ds), kOp, "join event"));
-    return HipStatus(hipStreamWaitEvent(s, ctx->join, 0), kOp, "join wait");
   });
 }
 

@@ -224,40 +224,6 @@ ROOST_API RoostStatus roost_register(RoostOpTable* table) {
 
 }  // extern "C"
 
-namespace {
-
-void CloseSideStream(RoostContext& c) {
-  if (c.fork != nullptr) (void)hipEventDestroy(c.fork);
-  if (c.join != nullptr) (void)hipEventDestroy(c.join);
-  if (c.side != nullptr) (void)hipStreamDestroy(c.side);
-  c.side = nullptr;
-  c.fork = c.join = nullptr;
-}
-
-// The fork / join events order work between two streams of one device and are never waited on by the host: no timing
-// and no system-scope fence (a device-scope release is what the waiting stream needs; config 5's attention call took
-// 183.5 us with the system fence and 179 us without).
-constexpr unsigned kSyncEvent = hipEventDisableTiming | hipEventDisableSystemFence;
-
-// The side stream and its fork/join events, made on the context's device with the caller's current device restored.
-// Without a usable device (CPU-only validation) the context has none and the ops run everything on the caller's stream.
-void OpenSideStream(RoostContext& c) {
-  int previous = -1;
-  if (hipGetDevice(&previous) != hipSuccess || hipSetDevice(c.device) != hipSuccess) {
-    (void)hipGetLastError();
-    return;
-  }
-  const bool made = hipStreamCreateWithFlags(&c.side, hipStreamNonBlocking) == hipSuccess &&
-                    hipEventCreateWithFlags(&c.fork, kSyncEvent) == hipSuccess &&
-                    hipEventCreateWithFlags(&c.join, kSyncEvent) == hipSuccess;
-  if (!made) {
-    (void)hipGetLastError();
-    CloseSideStream(c);
-  }
-  (void)hipSetDevice(previous);
-}
-
-}  // namespace
 
 extern "C" {
 
@@ -277,12 +243,10 @@ ROOST_API RoostStatus roost_context_create(const RoostContextCreateParams* param
   }
   *out = new (std::nothrow) RoostContext{params->device, params->flags, static_cast<uint32_t>(cus)};
   gate.Expect(*out != nullptr, ROOST_STATUS_OUT_OF_MEMORY, "no host memory left for a context");
-  if (gate.ok()) OpenSideStream(**out);
   return gate.status();
 }
 
 ROOST_API RoostStatus roost_context_destroy(RoostContext* ctx) {
-  if (ctx != nullptr) CloseSideStream(*ctx);
   delete ctx;
   return ROOST_STATUS_OK;
 }

@@ -3,7 +3,7 @@ folded into the kernels that write the output. The reference's worker runs the t
 (Qwen35EagerModel.cs:94-97); the fused call must give the same bits, which each case checks against run() followed by
 the SigmoidMul op on the GPU, for every kernel that writes output rows: decode (bf16 and f32, whole rows and split rows
 merged), the prefill tile kernel (whole items and split pieces merged in both merge forms), the general prefill kernel
-(page size 7), the f32 prefill rows, and config 5's mixed step, whose decode rows run on the context's side stream.
+(page size 7), the f32 prefill rows, and config 5's mixed step, whose decode rows run in the same launch as its tile pieces.
 The ungated attention itself is checked against the oracle elsewhere; here the gate is also shown to change the output,
 and the lse output to be the ungated one."""
 import zlib
@@ -75,7 +75,7 @@ def test_gated_equals_attention_then_sigmoid_mul(session, name, seqs, ps, hnd, c
 
 
 def test_config5_mixed_step_gated(session):
-    """Config 5's attention call (48 decode rows beside two 512-token chunks, the decode rows on the side stream) with
+    """Config 5's attention call (48 decode rows beside two 512-token chunks, the decode rows in the tile pieces' launch) with
     the output gate folded in."""
     rng = np.random.default_rng(5)
     kv = np.concatenate([rng.integers(1024, 16385, size=48), [4608, 4608]])
