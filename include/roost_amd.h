@@ -98,6 +98,23 @@ ROOST_API RoostStatus roost_amd_gdn_decode_layer_run(RoostContext* ctx, const vo
                                                       const void* gates_params, const void* gdn_params,
                                                       const void* norm_params, void* stream);
 
+/* One prefill pass of a Gated DeltaNet layer over the chunk variant in one call: CausalConv1d, GatedDeltaRuleGates, the
+ * chunked GatedDeltaRule and GatedRmsNorm. No counterpart in the reference (the same four calls as above, one after
+ * another). The chunk kernels compute g and beta from the gates' inputs where they read them (the gates op's
+ * arithmetic), so g and beta never reach memory. The convolution's output, the GDN output, the norm's output, the
+ * recurrent states and the convolution states equal the four calls' bit for bit. Params as for
+ * roost_amd_gdn_decode_layer_run, except that the sequences may have any lengths (cu_seqlens_host may be NULL at run)
+ * and the norm may take any form roost_gated_rms_norm_run takes. `ws` is the chunk variant's workspace, sized by
+ * roost_gdn_chunk_workspace and planned by roost_amd_gdn_chunk_layer_plan for the same gates and GDN params (else
+ * NOT_PLANNED). */
+ROOST_API RoostStatus roost_amd_gdn_chunk_layer_run(RoostContext* ctx, const void* conv_params,
+                                                     const void* gates_params, const void* gdn_params,
+                                                     const void* norm_params, const RoostWorkspace* ws, void* stream);
+/* plan() of roost_amd_gdn_chunk_layer_run: roost_gdn_chunk_plan of `gdn_params` (host chunk tables from cu_seqlens_host,
+ * copied to ws on the stream), except that with `gates_params` given the GDN params' g and beta are not read. */
+ROOST_API RoostStatus roost_amd_gdn_chunk_layer_plan(RoostContext* ctx, const void* gates_params, const void* gdn_params,
+                                                      const RoostWorkspace* ws, void* stream);
+
 /* The Gated DeltaNet layer's neighbour ops, each flagged GRAPH_CAPTURABLE | DETERMINISTIC | BATCH_INVARIANT, no plan
  * and no workspace:
  * GatedDeltaRuleGates, variant "gated-delta-rule-gates-gfx950" -- replaces roost_gated_delta_rule_gates_run

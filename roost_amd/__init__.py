@@ -109,6 +109,10 @@ class KernelLibrary:
         self.dll.roost_amd_paged_attention_gated_run.restype = C.c_int32
         self.dll.roost_amd_gdn_decode_layer_run.argtypes = [C.c_void_p] * 6
         self.dll.roost_amd_gdn_decode_layer_run.restype = C.c_int32
+        self.dll.roost_amd_gdn_chunk_layer_run.argtypes = [C.c_void_p] * 7
+        self.dll.roost_amd_gdn_chunk_layer_run.restype = C.c_int32
+        self.dll.roost_amd_gdn_chunk_layer_plan.argtypes = [C.c_void_p] * 5
+        self.dll.roost_amd_gdn_chunk_layer_plan.restype = C.c_int32
         self.dll.roost_amd_plan_region_from_step.argtypes = [C.c_void_p, C.c_uint64, C.POINTER(abi.StepTables)]
         self.dll.roost_amd_plan_region_from_step.restype = C.c_int32
         version = self.dll.roost_abi_version()
@@ -252,11 +256,10 @@ class OpSession:
             self._ws[(entry.variant_id, key)] = slot
         return slot
 
-    def launch(self, entry: Entry, params, key=0, plan: bool = True) -> None:
-        """Workspace -> (plan) -> run on the session stream."""
+    def prepare(self, entry: Entry, params, key=0, plan: bool = True) -> Optional[abi.Workspace]:
+        """Workspace -> (plan) on the session stream; the workspace a run() of these params takes (None: none)."""
         if entry.workspace is None:
-            self.run(entry, params, None)
-            return
+            return None
         slot = self._workspace(entry, params, key)
         ws = slot[3]
         if entry.needs_plan and plan:
@@ -268,7 +271,11 @@ class OpSession:
             ev = _torch().cuda.Event()
             ev.record(self.stream)
             slot[4] = ev
-        self.run(entry, params, ws)
+        return ws
+
+    def launch(self, entry: Entry, params, key=0, plan: bool = True) -> None:
+        """Workspace -> (plan) -> run on the session stream."""
+        self.run(entry, params, self.prepare(entry, params, key, plan))
 
     def run(self, entry: Entry, params, ws: Optional[abi.Workspace]) -> None:
         status = self.run_raw(entry, params, ws)
@@ -500,6 +507,27 @@ def gdn_decode_layer(session: OpSession, conv_params, gates_params, gdn_params, 
         C.addressof(gdn_params), C.addressof(norm_params), C.c_void_p(session.stream_handle))
     if status != abi.OK:
         raise KernelError("gdn_decode_layer", status, session.lib.last_error())
+
+
+def gdn_chunk_layer(session: OpSession, conv_params, gates_params, gdn_params, norm_params, key=0,
+                    plan: bool = True) -> None:
+    """roost_amd_gdn_chunk_layer_run: CausalConv1d (folded into the chunk prep), GatedDeltaRuleGates (gates_params may
+    be None), the chunked GatedDeltaRule and GatedRmsNorm of one prefill pass, in the chunk variant's workspace
+    (planned here by roost_amd_gdn_chunk_layer_plan unless plan is False)."""
+    chunk = session.lib.entry(CHUNK_VARIANT)
+    ws = session.prepare(chunk, gdn_params, ("chunk-layer", key), plan=False)  # the workspace: the chunk variant's
+    if plan:
+        status = session.lib.dll.roost_amd_gdn_chunk_layer_plan(
+            session.ctx, C.addressof(gates_params) if gates_params is not None else None, C.addressof(gdn_params),
+            C.addressof(ws), C.c_void_p(session.stream_handle))
+        if status != abi.OK:
+            raise KernelError("gdn_chunk_layer plan", status, session.lib.last_error())
+        session.stream.synchronize()  # the pinned tables are reused by the next plan
+    status = session.lib.dll.roost_amd_gdn_chunk_layer_run(
+        session.ctx, C.addressof(conv_params), C.addressof(gates_params) if gates_params is not None else None,
+        C.addressof(gdn_params), C.addressof(norm_params), C.addressof(ws), C.c_void_p(session.stream_handle))
+    if status != abi.OK:
+        raise KernelError("gdn_chunk_layer", status, session.lib.last_error())
 
 
 def gated_rms_norm(session: OpSession, *args, **kwargs) -> None:

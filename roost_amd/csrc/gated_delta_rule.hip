@@ -1916,6 +1916,91 @@ extern "C" ROOST_API RoostStatus roost_amd_gdn_recurrent_gated_run(RoostContext*
 
 // CausalConv1d + GatedDeltaRuleGates + the recurrent GatedDeltaRule + GatedRmsNorm of one decode step in two launches
 // (GdnDecodeLayerKernel, then the convolution's state update): the four ops' results bit for bit.
+namespace {
+
+// What the two layer calls (decode and chunk) read from their four params structs once admitted.
+struct LayerViews {
+  GateSource gs;
+  uint32_t cq = 0, ck = 0, cv = 0;  // first channel of the q, k and v columns in the convolution's output rows
+  bool tiled = false;               // q, k and v tile the channels without overlap
+  bool row_form = false;            // the norm runs on GatedRmsNorm's single-pass bf16 form
+  bool empty = false;               // no sequence has a token: nothing is read or written
+};
+
+// The rules the layer calls share: each op's own admission; the convolution over the GDN call's batch, bf16, at most
+// kLayerMaxWidth taps, and q, k and v column views of its output (where the GDN op reads them); the norm over the GDN
+// output's 128-column rows; and the norm's output apart from every input and state the layer reads.
+RoostStatus AdmitLayer(const char* op, const RoostCausalConv1dParams& cp, const void* gates_params,
+                       const RoostGatedDeltaRuleParams& p, const RoostGatedRmsNormParams& np, LayerViews* v) {
+  roost::Gate gate(op);
+  ROOST_RETURN_IF_FAILED(Admit(p, false, /*fused_gates=*/gates_params != nullptr));
+  if (gates_params != nullptr) {
+    ROOST_RETURN_IF_FAILED(GateSourceOf(*static_cast<const RoostGatedDeltaRuleGatesParams*>(gates_params), p, &v->gs));
+  }
+  ROOST_RETURN_IF_FAILED(roost_layer::AdmitConv(cp, op));
+  ROOST_RETURN_IF_FAILED(roost_layer::AdmitNorm(np, op, &v->row_form));
+  if (p.batch == 0 || p.tokens == 0) {  // nothing to read or write, as for the four ops
+    v->empty = true;
+    return ROOST_STATUS_OK;
+  }
+  const uint64_t ch = cp.channels;
+  gate.Expect(cp.batch == p.batch && cp.tokens == p.tokens && cp.cu_seqlens.address == p.cu_seqlens.address,
+              ROOST_STATUS_INVALID_ARGUMENT,
+              "the convolution covers %u sequences / %u tokens (cu_seqlens %p); the GDN call %u / %u (%p)", cp.batch,
+              cp.tokens, cp.cu_seqlens.address, p.batch, p.tokens, p.cu_seqlens.address)
+      .Expect(cp.input.dtype == ROOST_DTYPE_BF16 && cp.width <= kLayerMaxWidth, ROOST_STATUS_UNSUPPORTED,
+              "convolution of %s with %u taps: the layer calls are built for bf16 and up to %u taps",
+              roost::Describe(cp.input.dtype).name, cp.width, kLayerMaxWidth);
+  ROOST_GATE_RETURN(gate);
+  auto view = [&](const char* name, const RoostDeviceSpan& sp, uint32_t stride, uint64_t heads, uint32_t* first) {
+    const auto at = reinterpret_cast<intptr_t>(sp.address) - reinterpret_cast<intptr_t>(cp.output.address);
+    const uint64_t width = heads * kDim;
+    const bool ok = at >= 0 && at % 2 == 0 && static_cast<uint64_t>(at / 2) + width <= ch && Stride(stride, width) == ch;
+    gate.Expect(ok, ROOST_STATUS_INVALID_ARGUMENT,
+                "%s is not a column view of the convolution's output (offset %lld bytes, row stride %llu; rows of "
+                "%llu channels)", name, static_cast<long long>(at),
+                static_cast<unsigned long long>(Stride(stride, width)), static_cast<unsigned long long>(ch));
+    *first = ok ? static_cast<uint32_t>(at / 2) : 0;
+  };
+  view("q", p.q, p.q_stride, p.k_heads, &v->cq);
+  view("k", p.k, p.k_stride, p.k_heads, &v->ck);
+  view("v", p.v, p.v_stride, p.v_heads, &v->cv);
+  ROOST_GATE_RETURN(gate);
+  gate.Expect(np.input.address == p.output.address && np.rows == uint64_t{p.tokens} * p.v_heads && np.dim == kDim,
+              ROOST_STATUS_INVALID_ARGUMENT,
+              "the norm reads %u rows x %u at %p; the GDN output is %llu rows x %u at %p", np.rows, np.dim,
+              np.input.address, static_cast<unsigned long long>(uint64_t{p.tokens} * p.v_heads), kDim,
+              p.output.address);
+  ROOST_GATE_RETURN(gate);
+  // What the kernels read may not be what they write: the norm's output against the layer's other inputs and states.
+  auto range = [](const void* a, uint64_t bytes) {
+    const auto x = reinterpret_cast<uintptr_t>(a);
+    return std::pair<uintptr_t, uintptr_t>{x, x + bytes};
+  };
+  const auto out = range(np.output.address, np.rows * uint64_t{kDim} * 2);
+  auto clear = [&](const char* name, const void* a, uint64_t bytes) {
+    const auto r = range(a, bytes);
+    gate.Expect(a == nullptr || bytes == 0 || r.second <= out.first || out.second <= r.first,
+                ROOST_STATUS_INVALID_ARGUMENT, "the norm's output overlaps %s", name);
+  };
+  const uint64_t sl = cp.width - 1ull;
+  clear("the convolution's input", cp.input.address, uint64_t{cp.tokens} * ch * 2);
+  clear("the convolution's weights", cp.weight.address, ch * cp.width * 2);
+  clear("the convolution's bias", cp.bias.address, ch * 2);
+  clear("the convolution's state", sl == 0 ? nullptr : cp.conv_state.address,
+        cp.conv_state.length * roost::ElementBytes(cp.conv_state.dtype == ROOST_DTYPE_UNDEFINED ? cp.input.dtype
+                                                                                            : cp.conv_state.dtype));
+  clear("the recurrent state", p.state.address, p.state.length * 4);
+  ROOST_GATE_RETURN(gate);
+  const uint64_t qk = uint64_t{p.k_heads} * kDim, vw = uint64_t{p.v_heads} * kDim;
+  auto apart = [](uint64_t a, uint64_t na, uint64_t b, uint64_t nb) { return a + na <= b || b + nb <= a; };
+  v->tiled = apart(v->cq, qk, v->ck, qk) && apart(v->cq, qk, v->cv, vw) && apart(v->ck, qk, v->cv, vw) &&
+             2 * qk + vw == ch;
+  return ROOST_STATUS_OK;
+}
+
+}  // namespace
+
 extern "C" ROOST_API RoostStatus roost_amd_gdn_decode_layer_run(RoostContext* ctx, const void* conv_params,
                                                                 const void* gates_params, const void* gdn_params,
                                                                 const void* norm_params, void* stream) {
@@ -1934,100 +2019,44 @@ extern "C" ROOST_API RoostStatus roost_amd_gdn_decode_layer_run(RoostContext* ct
   const auto& p = *static_cast<const RoostGatedDeltaRuleParams*>(gdn_params);
   const auto& np = *static_cast<const RoostGatedRmsNormParams*>(norm_params);
   return roost::CatchAll(kLayerOp, [&]() -> RoostStatus {
-    ROOST_RETURN_IF_FAILED(Admit(p, false, /*fused_gates=*/gates_params != nullptr));
-    GateSource gs;
-    if (gates_params != nullptr) {
-      ROOST_RETURN_IF_FAILED(GateSourceOf(*static_cast<const RoostGatedDeltaRuleGatesParams*>(gates_params), p, &gs));
-    }
-    ROOST_RETURN_IF_FAILED(roost_layer::AdmitConv(cp, kLayerOp));
-    bool row_form = false;
-    ROOST_RETURN_IF_FAILED(roost_layer::AdmitNorm(np, kLayerOp, &row_form));
-    if (p.batch == 0 || p.tokens == 0) return ROOST_STATUS_OK;  // nothing to read or write, as for the four ops
+    LayerViews lv;
+    ROOST_RETURN_IF_FAILED(AdmitLayer(kLayerOp, cp, gates_params, p, np, &lv));
+    if (lv.empty) return ROOST_STATUS_OK;
     // Every sequence on the token-serial recurrence: longer ones are the chunk kernels' in the recurrent variant.
-    gate.Expect(p.batch == 0 || p.cu_seqlens_host != nullptr, ROOST_STATUS_INVALID_ARGUMENT,
+    gate.Expect(p.cu_seqlens_host != nullptr, ROOST_STATUS_INVALID_ARGUMENT,
                 "the decode layer checks the sequence lengths in cu_seqlens_host, which is NULL");
     ROOST_GATE_RETURN(gate);
     for (uint32_t b = 0; b < p.batch; ++b) {
       const int64_t n = int64_t{p.cu_seqlens_host[b + 1]} - p.cu_seqlens_host[b];
       gate.Expect(n < static_cast<int64_t>(kRouteMinTokens), ROOST_STATUS_UNSUPPORTED,
                   "sequence %u has %lld tokens; sequences of %u or more run on the chunk kernels, so this call covers "
-                  "decode steps only (run the four ops one by one)", b, static_cast<long long>(n), kRouteMinTokens);
+                  "decode steps only (run the four ops one by one, or the chunk layer call)", b,
+                  static_cast<long long>(n), kRouteMinTokens);
       if (!gate.ok()) return gate.status();
     }
-    // The convolution: the GDN call's batch, bf16, at most kLayerMaxWidth taps, and q, k and v column views of its
-    // output (the GDN op reads them there).
-    const uint64_t ch = cp.channels;
-    gate.Expect(cp.batch == p.batch && cp.tokens == p.tokens && cp.cu_seqlens.address == p.cu_seqlens.address,
-                ROOST_STATUS_INVALID_ARGUMENT,
-                "the convolution covers %u sequences / %u tokens (cu_seqlens %p); the GDN call %u / %u (%p)", cp.batch,
-                cp.tokens, cp.cu_seqlens.address, p.batch, p.tokens, p.cu_seqlens.address)
-        .Expect(cp.input.dtype == ROOST_DTYPE_BF16 && cp.width <= kLayerMaxWidth, ROOST_STATUS_UNSUPPORTED,
-                "convolution of %s with %u taps: the decode layer is built for bf16 and up to %u taps",
-                roost::Describe(cp.input.dtype).name, cp.width, kLayerMaxWidth);
-    ROOST_GATE_RETURN(gate);
-    auto view = [&](const char* name, const RoostDeviceSpan& sp, uint32_t stride, uint64_t heads, uint32_t* first) {
-      const auto at = reinterpret_cast<intptr_t>(sp.address) - reinterpret_cast<intptr_t>(cp.output.address);
-      const uint64_t width = heads * kDim;
-      const bool ok = at >= 0 && at % 2 == 0 && static_cast<uint64_t>(at / 2) + width <= ch && Stride(stride, width) == ch;
-      gate.Expect(ok, ROOST_STATUS_INVALID_ARGUMENT,
-                  "%s is not a column view of the convolution's output (offset %lld bytes, row stride %llu; rows of "
-                  "%llu channels)", name, static_cast<long long>(at),
-                  static_cast<unsigned long long>(Stride(stride, width)), static_cast<unsigned long long>(ch));
-      *first = ok ? static_cast<uint32_t>(at / 2) : 0;
-    };
-    LayerArgs L{};
-    view("q", p.q, p.q_stride, p.k_heads, &L.cq);
-    view("k", p.k, p.k_stride, p.k_heads, &L.ck);
-    view("v", p.v, p.v_stride, p.v_heads, &L.cv);
-    ROOST_GATE_RETURN(gate);
-    // The norm: GatedRmsNorm of the GDN output over 128-column rows, in its single-pass form.
-    gate.Expect(np.input.address == p.output.address && np.rows == uint64_t{p.tokens} * p.v_heads && np.dim == kDim,
-                ROOST_STATUS_INVALID_ARGUMENT,
-                "the norm reads %u rows x %u at %p; the GDN output is %llu rows x %u at %p", np.rows, np.dim,
-                np.input.address, static_cast<unsigned long long>(uint64_t{p.tokens} * p.v_heads), kDim,
-                p.output.address)
-        .Expect(np.rows == 0 || (np.input.dtype == ROOST_DTYPE_BF16 && row_form), ROOST_STATUS_UNSUPPORTED,
+    gate.Expect(np.rows == 0 || (np.input.dtype == ROOST_DTYPE_BF16 && lv.row_form), ROOST_STATUS_UNSUPPORTED,
                 "the decode layer's norm is GatedRmsNorm's single-pass bf16 form: 16-byte aligned input, gate and "
                 "output of bf16");
     ROOST_GATE_RETURN(gate);
-    // What the kernel reads may not be what it writes: the norm's output against the layer's other inputs and states.
-    auto range = [](const void* a, uint64_t bytes) {
-      const auto x = reinterpret_cast<uintptr_t>(a);
-      return std::pair<uintptr_t, uintptr_t>{x, x + bytes};
-    };
-    const auto out = range(np.output.address, np.rows * uint64_t{kDim} * 2);
-    auto clear = [&](const char* name, const void* a, uint64_t bytes) {
-      const auto r = range(a, bytes);
-      gate.Expect(a == nullptr || bytes == 0 || r.second <= out.first || out.second <= r.first,
-                  ROOST_STATUS_INVALID_ARGUMENT, "the norm's output overlaps %s", name);
-    };
     const uint64_t sl = cp.width - 1ull;
-    clear("the convolution's input", cp.input.address, uint64_t{cp.tokens} * ch * 2);
-    clear("the convolution's weights", cp.weight.address, ch * cp.width * 2);
-    clear("the convolution's bias", cp.bias.address, ch * 2);
-    clear("the convolution's state", sl == 0 ? nullptr : cp.conv_state.address,
-          cp.conv_state.length * roost::ElementBytes(cp.conv_state.dtype == ROOST_DTYPE_UNDEFINED ? cp.input.dtype
-                                                                                              : cp.conv_state.dtype));
-    clear("the recurrent state", p.state.address, p.state.length * 4);
-    ROOST_GATE_RETURN(gate);
-    L.a = MakeArgs(p, gs);
+    LayerArgs L{};
+    L.cq = lv.cq;
+    L.ck = lv.ck;
+    L.cv = lv.cv;
+    L.a = MakeArgs(p, lv.gs);
     L.x = static_cast<const uint16_t*>(cp.input.address);
     L.conv_w = static_cast<const uint16_t*>(cp.weight.address);
     L.conv_b = static_cast<const uint16_t*>(cp.bias.address);
     L.conv_state = cp.conv_state.address;
     L.conv_slots = static_cast<const int32_t*>(cp.state_slots.address);
     L.conv_state_t = cp.conv_state.dtype == ROOST_DTYPE_UNDEFINED ? cp.input.dtype : cp.conv_state.dtype;
-    L.conv_pool_slots = sl == 0 ? 0 : cp.conv_state.length / (ch * sl);
+    L.conv_pool_slots = sl == 0 ? 0 : cp.conv_state.length / (uint64_t{cp.channels} * sl);
     L.channels = cp.channels;
     L.width = cp.width;
     L.silu = cp.silu != 0 ? 1u : 0u;
     // One value head per key head, and q, k and v tiling the channels without overlap: each channel belongs to exactly
     // one workgroup, which updates its state itself. Otherwise the conv op's state kernel runs afterwards.
-    const uint64_t qk = uint64_t{p.k_heads} * kDim, vw = uint64_t{p.v_heads} * kDim;
-    auto apart = [](uint64_t a, uint64_t na, uint64_t b, uint64_t nb) { return a + na <= b || b + nb <= a; };
-    const bool tiled = apart(L.cq, qk, L.ck, qk) && apart(L.cq, qk, L.cv, vw) && apart(L.ck, qk, L.cv, vw) &&
-                       2 * qk + vw == ch;
-    L.conv_state_update = p.v_heads == p.k_heads && tiled ? 1u : 0u;
+    L.conv_state_update = p.v_heads == p.k_heads && lv.tiled ? 1u : 0u;
     L.z = static_cast<const uint16_t*>(np.gate.address);
     L.norm_w = np.weight.address;
     L.norm_w_t = np.weight.dtype;
@@ -2073,6 +2102,43 @@ static int64_t FillChunkTables(const int32_t* cu, uint32_t batch, const ChunkAre
   return n;
 }
 
+namespace {
+
+// plan() of the chunk variant: the chunk and sequence tables from cu_seqlens_host, copied to the workspace on the
+// stream, and the stamp run() checks. With fused_gates the GDN params' g and beta are not read (a layer call computes
+// them from the gates' inputs).
+RoostStatus ChunkPlan(const RoostGatedDeltaRuleParams& p, const RoostWorkspace* ws, void* stream, bool fused_gates) {
+  roost::Gate gate(kOp);
+  ROOST_RETURN_IF_FAILED(Admit(p, true, fused_gates));
+  const ChunkArena l = MakeChunkArena(p.tokens, p.batch, p.v_heads);
+  gate.Expect(roost::HasDeviceRegion(ws, l.total) && ws->pinned_host != nullptr &&
+                  ws->pinned_host_bytes >= l.tables_bytes && ws->plan != nullptr && ws->plan_bytes >= sizeof(ChunkStamp),
+              ROOST_STATUS_WORKSPACE_TOO_SMALL,
+              "the call needs %llu device bytes, %llu pinned bytes and a %zu-byte plan record",
+              static_cast<unsigned long long>(l.total), static_cast<unsigned long long>(l.tables_bytes),
+              sizeof(ChunkStamp));
+  ROOST_GATE_RETURN(gate);
+  ChunkStamp stamp{kPlanMagic, p.batch, p.tokens, 0};
+  if (p.batch > 0 && p.tokens > 0) {
+    const int32_t* cu = p.cu_seqlens_host;
+    gate.Expect(cu[0] == 0 && static_cast<uint32_t>(cu[p.batch]) == p.tokens, ROOST_STATUS_INVALID_ARGUMENT,
+                "cu_seqlens_host runs from %d to %d; it must run from 0 to tokens = %u", cu[0], cu[p.batch], p.tokens);
+    ROOST_GATE_RETURN(gate);
+    uint32_t bad = 0;
+    const int64_t n = FillChunkTables(cu, p.batch, l, static_cast<uint8_t*>(ws->pinned_host), &bad);
+    gate.Expect(n >= 0, ROOST_STATUS_INVALID_ARGUMENT, "cu_seqlens_host goes backwards at sequence %u", bad);
+    ROOST_GATE_RETURN(gate);
+    stamp.chunks = static_cast<uint32_t>(n);
+    ROOST_RETURN_IF_FAILED(roost::HipStatus(hipMemcpyAsync(ws->device, ws->pinned_host, l.seq_table + 16ull * p.batch,
+                                                           hipMemcpyHostToDevice, roost::Stream(stream)),
+                                            kOp, "copy of the chunk tables to the device"));
+  }
+  std::memcpy(ws->plan, &stamp, sizeof(stamp));
+  return ROOST_STATUS_OK;
+}
+
+}  // namespace
+
 extern "C" ROOST_API RoostStatus roost_gdn_chunk_plan(RoostContext* ctx, const void* params, const RoostWorkspace* ws,
                                                       void* stream) {
   roost::Gate gate(kOp);
@@ -2080,34 +2146,28 @@ extern "C" ROOST_API RoostStatus roost_gdn_chunk_plan(RoostContext* ctx, const v
               "plan() needs a context, params and a workspace");
   ROOST_GATE_RETURN(gate);
   const auto& p = *static_cast<const RoostGatedDeltaRuleParams*>(params);
+  return roost::CatchAll(kOp, [&]() -> RoostStatus { return ChunkPlan(p, ws, stream, false); });
+}
+
+// plan() for roost_amd_gdn_chunk_layer_run: the chunk variant's plan of the GDN params, whose g and beta are not read
+// when the gates params are given (the layer computes them).
+extern "C" ROOST_API RoostStatus roost_amd_gdn_chunk_layer_plan(RoostContext* ctx, const void* gates_params,
+                                                                const void* gdn_params, const RoostWorkspace* ws,
+                                                                void* stream) {
+  roost::Gate gate(kOp);
+  gate.Expect(ctx != nullptr && gdn_params != nullptr && ws != nullptr, ROOST_STATUS_INVALID_ARGUMENT,
+              "plan() needs a context, the GDN params and a workspace");
+  ROOST_GATE_RETURN(gate);
+  if (gates_params != nullptr) gate.Header(gates_params, sizeof(RoostGatedDeltaRuleGatesParams));
+  ROOST_GATE_RETURN(gate);
+  const auto& p = *static_cast<const RoostGatedDeltaRuleParams*>(gdn_params);
   return roost::CatchAll(kOp, [&]() -> RoostStatus {
-    ROOST_RETURN_IF_FAILED(Admit(p, true));
-    const ChunkArena l = MakeChunkArena(p.tokens, p.batch, p.v_heads);
-    gate.Expect(roost::HasDeviceRegion(ws, l.total) && ws->pinned_host != nullptr &&
-                    ws->pinned_host_bytes >= l.tables_bytes && ws->plan != nullptr &&
-                    ws->plan_bytes >= sizeof(ChunkStamp),
-                ROOST_STATUS_WORKSPACE_TOO_SMALL,
-                "the call needs %llu device bytes, %llu pinned bytes and a %zu-byte plan record",
-                static_cast<unsigned long long>(l.total), static_cast<unsigned long long>(l.tables_bytes),
-                sizeof(ChunkStamp));
-    ROOST_GATE_RETURN(gate);
-    ChunkStamp stamp{kPlanMagic, p.batch, p.tokens, 0};
-    if (p.batch > 0 && p.tokens > 0) {
-      const int32_t* cu = p.cu_seqlens_host;
-      gate.Expect(cu[0] == 0 && static_cast<uint32_t>(cu[p.batch]) == p.tokens, ROOST_STATUS_INVALID_ARGUMENT,
-                  "cu_seqlens_host runs from %d to %d; it must run from 0 to tokens = %u", cu[0], cu[p.batch], p.tokens);
-      ROOST_GATE_RETURN(gate);
-      uint32_t bad = 0;
-      const int64_t n = FillChunkTables(cu, p.batch, l, static_cast<uint8_t*>(ws->pinned_host), &bad);
-      gate.Expect(n >= 0, ROOST_STATUS_INVALID_ARGUMENT, "cu_seqlens_host goes backwards at sequence %u", bad);
-      ROOST_GATE_RETURN(gate);
-      stamp.chunks = static_cast<uint32_t>(n);
-      ROOST_RETURN_IF_FAILED(roost::HipStatus(hipMemcpyAsync(ws->device, ws->pinned_host, l.seq_table + 16ull * p.batch,
-                                                             hipMemcpyHostToDevice, roost::Stream(stream)),
-                                              kOp, "copy of the chunk tables to the device"));
+    if (gates_params != nullptr) {
+      ROOST_RETURN_IF_FAILED(Admit(p, true, true));
+      GateSource gs;
+      ROOST_RETURN_IF_FAILED(GateSourceOf(*static_cast<const RoostGatedDeltaRuleGatesParams*>(gates_params), p, &gs));
     }
-    std::memcpy(ws->plan, &stamp, sizeof(stamp));
-    return ROOST_STATUS_OK;
+    return ChunkPlan(p, ws, stream, gates_params != nullptr);
   });
 }
 
@@ -2133,6 +2193,53 @@ extern "C" ROOST_API RoostStatus roost_gdn_chunk_run(RoostContext* ctx, const vo
     }
     if (stamp.chunks == 0) return ROOST_STATUS_OK;
     return LaunchChunk(p, ws, l, stamp.chunks, roost::Stream(stream));
+  });
+}
+
+// One prefill pass of a GDN layer over the chunk variant (no reference counterpart; the Qwen3.5 worker runs
+// CausalConv1d, GatedDeltaRuleGates, GatedDeltaRule and GatedRmsNorm one after another, Qwen35EagerModel.cs:89-92) in
+// one call: the convolution, the chunk kernels computing g and beta where they read them (the gates op's arithmetic,
+// so g and beta never reach memory), and the norm. The workspace is the chunk variant's (roost_gdn_chunk_workspace),
+// planned by roost_amd_gdn_chunk_layer_plan.
+extern "C" ROOST_API RoostStatus roost_amd_gdn_chunk_layer_run(RoostContext* ctx, const void* conv_params,
+                                                               const void* gates_params, const void* gdn_params,
+                                                               const void* norm_params, const RoostWorkspace* ws,
+                                                               void* stream) {
+  constexpr char kLayerOp[] = "gdn_chunk_layer";
+  roost::Gate gate(kLayerOp);
+  gate.Expect(ctx != nullptr && conv_params != nullptr && gdn_params != nullptr && norm_params != nullptr,
+              ROOST_STATUS_INVALID_ARGUMENT, "a context and the conv, GDN and norm params are required (the gates "
+              "params may be NULL: g and beta are then read from the GDN params)");
+  ROOST_GATE_RETURN(gate);
+  gate.Header(conv_params, sizeof(RoostCausalConv1dParams))
+      .Header(gdn_params, sizeof(RoostGatedDeltaRuleParams))
+      .Header(norm_params, sizeof(RoostGatedRmsNormParams));
+  if (gates_params != nullptr) gate.Header(gates_params, sizeof(RoostGatedDeltaRuleGatesParams));
+  ROOST_GATE_RETURN(gate);
+  const auto& cp = *static_cast<const RoostCausalConv1dParams*>(conv_params);
+  const auto& p = *static_cast<const RoostGatedDeltaRuleParams*>(gdn_params);
+  const auto& np = *static_cast<const RoostGatedRmsNormParams*>(norm_params);
+  return roost::CatchAll(kLayerOp, [&]() -> RoostStatus {
+    LayerViews lv;
+    ROOST_RETURN_IF_FAILED(AdmitLayer(kLayerOp, cp, gates_params, p, np, &lv));
+    if (lv.empty) return ROOST_STATUS_OK;
+    const ChunkArena l = MakeChunkArena(p.tokens, p.batch, p.v_heads);
+    gate.Expect(roost::HasDeviceRegion(ws, l.total) && ws->plan != nullptr && ws->plan_bytes >= sizeof(ChunkStamp),
+                ROOST_STATUS_WORKSPACE_TOO_SMALL, "the call needs %llu device bytes and its plan record",
+                static_cast<unsigned long long>(l.total));
+    ROOST_GATE_RETURN(gate);
+    ChunkStamp stamp;
+    std::memcpy(&stamp, ws->plan, sizeof(stamp));
+    if (stamp.magic != kPlanMagic || stamp.batch != p.batch || stamp.tokens != p.tokens || stamp.chunks > l.max_chunks) {
+      return roost::Report(ROOST_STATUS_NOT_PLANNED, kLayerOp,
+                           "no roost_amd_gdn_chunk_layer_plan() for %u tokens in %u sequences in this workspace", p.tokens,
+                           p.batch);
+    }
+    // The convolution (with its state update; the GDN kernels do not read the convolution's state), the chunk kernels
+    // with the gates computed where they are read, then the norm, all on the caller's stream.
+    ROOST_RETURN_IF_FAILED(roost_causal_conv1d_run(ctx, conv_params, nullptr, stream));
+    if (stamp.chunks > 0) ROOST_RETURN_IF_FAILED(LaunchChunk(p, ws, l, stamp.chunks, roost::Stream(stream), false, false, lv.gs));
+    return roost_gated_rms_norm_run(ctx, norm_params, nullptr, stream);
   });
 }
 
