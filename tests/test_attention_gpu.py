@@ -387,6 +387,41 @@ def test_config5_mixed_step_attention(session):
         cases.assert_close(got[b.q_indptr[s]:b.q_indptr[s + 1]], ref1, what=f"config 5 seq {s} vs CpuOps")
 
 
+def _plan_overlap(session, key) -> int:
+    """The plan record's `overlap` word (its 11th 32-bit field): the decode workgroups a mixed call launches beside its
+    tile pieces in one MixedAttentionKernel launch, 0 when the plan runs them one after the other."""
+    plan = session._ws[(roost_amd.ATTENTION_VARIANT, key)][2]
+    return int(np.frombuffer(bytes(plan)[40:44], np.uint32)[0])
+
+
+@pytest.mark.parametrize("d,cap", [(128, 0.0), (64, 0.0), (256, 30.0)], ids=["hd128", "hd64", "hd256 soft cap"])
+def test_mixed_launch_head_dims_and_soft_cap(session, d, cap):
+    """Config 5's shape (48 decode rows of U(1024, 16384) contexts beside two 512-token chunks on 4096-token prefixes)
+    at the other head dims and with a logit soft cap: the plan takes the one-launch form (checked in the plan record),
+    and the result matches a float32 torch reference of the whole batch (uncapped) and the CpuOps oracle on a short
+    and a long decode row and one chunk."""
+    rng = np.random.default_rng(50 + d + int(cap))
+    kv = np.concatenate([rng.integers(1024, 16385, size=48), [4608, 4608]])
+    n = np.concatenate([np.ones(48, np.int64), [512, 512]])
+    b = cases.make_paged_batch(rng, kv, n, d=d, std=2.0 if cap else 0.5, pool_factor=1.25)
+    dv = Dev(b, soft_cap=cap)
+    key = ("mixed-launch", d, cap)
+    session.launch(session.lib.entry(roost_amd.ATTENTION_VARIANT), dv.params(), key=key)
+    assert _plan_overlap(session, key) > 0, "the plan did not take the one-launch form"
+    got = dv.result()
+    assert not np.isnan(got).any()
+    if not cap:
+        cases.assert_close(got, torch_reference(b), what=f"hd{d} mixed launch vs fp32 torch")
+    for s in (int(np.argmin(kv[:48])), int(np.argmax(kv[:48])), 49):
+        one = cases.PagedBatch(b.q[b.q_indptr[s]:b.q_indptr[s + 1]].copy(), b.k_cache, b.v_cache,
+                               np.array([0, n[s]], np.int32), np.array([0, b.kv_indptr[s + 1] - b.kv_indptr[s]], np.int32),
+                               b.kv_indices[b.kv_indptr[s]:b.kv_indptr[s + 1]].copy(), b.kv_last_page_len[s:s + 1].copy(),
+                               [int(b.kv_lens[s])], [int(n[s])], 16, False, True, d=d)
+        ref1 = cases.values(cases.oracle_attention(one, soft_cap=cap), True)
+        cases.assert_close(got[b.q_indptr[s]:b.q_indptr[s + 1]], ref1, max_abs=(2 if cap else 1) * cases.MAX_ABS,
+                           what=f"hd{d} cap {cap} seq {s} vs CpuOps")
+
+
 def test_prefill_batch_invariance(session):
     rng = np.random.default_rng(9)
     b = cases.make_paged_batch(rng, [333, 500, 129], [333, 100, 129])
