@@ -722,3 +722,35 @@ def test_prefill_f32_matches_cpuops(session, name, seqs, ps, hnd, causal, window
     got = run_case(session, b, causal, window_left=window)
     ref = cases.values(cases.oracle_attention(b, causal, window_left=window), False)
     np.testing.assert_allclose(got, ref, rtol=2e-5, atol=2e-5)
+
+
+def test_decode_large_batch(session):
+    """8,192 decode rows of 1 to 64 keys (far more sequences than ranges) against a float32 torch reference."""
+    rng = np.random.default_rng(77)
+    kv = rng.integers(1, 65, size=8192)
+    b = cases.make_paged_batch(rng, kv, np.ones(8192, np.int64), std=0.5)
+    got = run_case(session, b, check_nohost=False, check_determinism=False)
+    cases.assert_close(got, torch_reference(b), what="8192-row decode vs fp32 torch")
+
+
+def test_prefill_long_sequence_sampled_rows(session):
+    """One causal prefill of 32,768 tokens (hundreds of pieces and merges at head dim 256): sampled query rows -- the
+    first, tile and piece edges, the last -- against a float64 numpy evaluation of those rows alone."""
+    rng = np.random.default_rng(78)
+    L = 32768
+    b = cases.make_paged_batch(rng, [L], [L], std=0.5)
+    got = run_case(session, b, check_nohost=False, check_determinism=False)
+    vals = lambda a: cases.values(a, True).astype(np.float64)  # noqa: E731
+    q, kc, vc = vals(b.q), vals(b.k_cache), vals(b.v_cache)
+    pos = np.arange(L)
+    page, slot = b.kv_indices[pos // b.page_size], pos % b.page_size
+    k = kc[page, slot]  # [L, hkv, d]
+    v = vc[page, slot]
+    scale = 1.0 / np.sqrt(b.d)
+    group = b.hq // b.hkv
+    for t in (0, 63, 64, 1000, 4095, 4096, 20000, L - 1):
+        for h in range(b.hq):
+            s = (k[: t + 1, h // group] @ q[t, h]) * scale
+            p = np.exp(s - s.max())
+            ref = (p @ v[: t + 1, h // group]) / p.sum()
+            cases.assert_close(got[t, h][None], ref[None], what=f"32k prefill row {t} head {h}")

@@ -424,3 +424,54 @@ def test_recurrent_with_gates_refusals(session):
                                                     a_stride=64, b_stride=64, a_offset=16, a_len=10)
     assert status(short) == abi.INVALID_ARGUMENT  # a shorter than its view
     assert status(good) == abi.OK
+
+
+def test_chunk_long_sequence_two_calls_equal_one(session):
+    """A size-independent property at a length the oracle cannot reach in a test (two sequences of 131,072 tokens on
+    the chunk variant): running each sequence's first half and then its second half in a second call that starts from
+    the state the first wrote gives the same outputs and final states, bit for bit, as one call over the whole
+    sequences (the halves end on chunk boundaries, so both runs do the same arithmetic). The reference states the same
+    invariant on short sequences (HybridTests.cs:174-200)."""
+    import torch
+
+    H, D, L, B = 4, DIM, 1 << 17, 2
+    g_ = torch.Generator(device="cuda").manual_seed(31)
+    fused = (torch.randn((B * L, 3 * H * D), generator=g_, device="cuda") * 0.5).to(torch.bfloat16)
+    gg = -torch.nn.functional.softplus(torch.randn((B * L, H), generator=g_, device="cuda")) * 0.05
+    beta = torch.sigmoid(torch.randn((B * L, H), generator=g_, device="cuda")).to(torch.bfloat16)
+    s0 = torch.randn((B, H, D, D), generator=g_, device="cuda") * 0.01
+    slots = torch.arange(B, dtype=torch.int32, device="cuda")
+    entry = session.lib.entry(roost_amd.CHUNK_VARIANT)
+
+    def call(rows, lens, pool, out, key):
+        cu_h = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+        tokens = int(cu_h[-1])
+        x = fused[rows]
+        reach = (tokens - 1) * 3 * H * D + H * D
+        p = roost_amd.gated_delta_rule_params(
+            x, x, x, gg[rows], beta[rows], out, pool, slots, torch.from_numpy(cu_h).cuda(), batch=B, tokens=tokens,
+            k_heads=H, v_heads=H, q_stride=3 * H * D, k_stride=3 * H * D, v_stride=3 * H * D, q_len=reach,
+            k_len=reach, v_len=reach, q_offset=0, k_offset=H * D, v_offset=2 * H * D, cu_seqlens_host=cu_h)
+        session.launch(entry, p, key=key)
+
+    # One call: sequence b is rows [b L, (b + 1) L).
+    pool_one = s0.clone()
+    out_one = torch.full((B * L, H, D), float("nan"), dtype=torch.bfloat16, device="cuda")
+    call(slice(None), [L, L], pool_one, out_one, "long-one")
+    # Two calls: the first halves of both sequences, then the second halves (rows gathered so each call's sequences
+    # are contiguous).
+    half = L // 2
+    first = torch.cat([torch.arange(b * L, b * L + half) for b in range(B)]).cuda()
+    second = torch.cat([torch.arange(b * L + half, (b + 1) * L) for b in range(B)]).cuda()
+    pool_two = s0.clone()
+    out_a = torch.full((B * half, H, D), float("nan"), dtype=torch.bfloat16, device="cuda")
+    out_b = torch.full((B * half, H, D), float("nan"), dtype=torch.bfloat16, device="cuda")
+    call(first, [half, half], pool_two, out_a, "long-a")
+    call(second, [half, half], pool_two, out_b, "long-b")
+    torch.cuda.synchronize()
+    out_two = torch.empty_like(out_one)
+    out_two[first] = out_a
+    out_two[second] = out_b
+    assert not torch.isnan(out_one.float()).any()
+    assert torch.equal(pool_one, pool_two), "final states differ between one call and two"
+    assert torch.equal(out_one.view(torch.int16), out_two.view(torch.int16)), "outputs differ between one call and two"
