@@ -281,7 +281,69 @@ def bench_gdn(torch, roost_amd, session, steps, warmup):
     del keep
     res["gdn_decode_layer"] = bench_decode_layer(torch, roost_amd, session, steps, g)
     res["gdn_chunk_layer"] = bench_chunk_layer(torch, roost_amd, session, steps, g)
+    res["gdn_step_layer"] = bench_step_layer(torch, roost_amd, session, steps, g)
     return res
+
+
+def bench_step_layer(torch, roost_amd, session, steps, g):
+    """Config 5's GDN layer as a whole Qwen3.5 layer (CausalConv1d of width 4 over the 6,144-channel projection,
+    GatedDeltaRuleGates, the recurrent GatedDeltaRule routing the two 512-token chunks to the chunk kernels,
+    GatedRmsNorm; 48 one-token sequences and 2 x 512 tokens): the four ops one after another against
+    roost_amd_gdn_layer_run."""
+    H, D, W = 16, 128, 4
+    lens = np.array([1] * 48 + [512, 512])
+    B, T, ch = len(lens), int(lens.sum()), 3 * H * D
+    bf = lambda t: t.to(torch.bfloat16)  # noqa: E731
+    x = bf(torch.randn((T, ch), generator=g, device="cuda"))
+    w = bf(torch.randn((ch, W), generator=g, device="cuda") * 0.5)
+    bias = bf(torch.randn((ch,), generator=g, device="cuda") * 0.3)
+    conv_state = bf(torch.randn((B, ch, W - 1), generator=g, device="cuda"))
+    slots = torch.arange(B, dtype=torch.int32, device="cuda")
+    cu_h = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    cu = torch.from_numpy(cu_h).cuda()
+    y = torch.empty((T, ch), dtype=torch.bfloat16, device="cuda")
+    proj = bf(torch.randn((T, 2 * H), generator=g, device="cuda") * 3)
+    a_log = torch.randn((H,), generator=g, device="cuda") * 0.5
+    dt_bias = torch.randn((H,), generator=g, device="cuda")
+    gg = torch.empty((T, H), dtype=torch.float32, device="cuda")
+    beta = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    pool = torch.randn((B, H, D, D), generator=g, device="cuda") * 0.01
+    o = torch.empty((T, H, D), dtype=torch.bfloat16, device="cuda")
+    z = bf(torch.randn((T * H, D), generator=g, device="cuda"))
+    nw = 1 + torch.randn((D,), generator=g, device="cuda") * 0.2
+    out = torch.empty((T * H, D), dtype=torch.bfloat16, device="cuda")
+    conv = roost_amd.causal_conv1d_params(x, w, bias, y, conv_state, slots, cu, batch=B, tokens=T, channels=ch, width=W)
+    gkw = dict(tokens=T, v_heads=H, a_stride=2 * H, b_stride=2 * H, a_len=(T - 1) * 2 * H + H,
+               b_len=(T - 1) * 2 * H + H, a_offset=H, b_offset=0)
+    gates = roost_amd.gated_delta_rule_gates_params(proj, proj, a_log, dt_bias, gg, beta, **gkw)
+    gates_in = roost_amd.gated_delta_rule_gates_params(proj, proj, a_log, dt_bias, None, None, **gkw)
+    reach = (T - 1) * ch + H * D
+
+    def gdn_params(gv, bv):
+        return roost_amd.gated_delta_rule_params(
+            y, y, y, gv, bv, o, pool, slots, cu, batch=B, tokens=T, q_stride=ch, k_stride=ch, v_stride=ch, q_len=reach,
+            k_len=reach, v_len=reach, q_offset=0, k_offset=H * D, v_offset=2 * H * D, cu_seqlens_host=cu_h)
+
+    gdn, gdn_in = gdn_params(gg, beta), gdn_params(None, None)
+    norm = roost_amd.gated_rms_norm_params(o, z, nw, out, rows=T * H, dim=D, eps=1e-6)
+    e_conv = session.lib.entry(roost_amd.CAUSAL_CONV1D_VARIANT)
+    e_gates = session.lib.entry(roost_amd.GATES_VARIANT)
+    e_gdn = session.lib.entry(roost_amd.RECURRENT_VARIANT)
+    e_norm = session.lib.entry(roost_amd.GATED_RMS_NORM_VARIANT)
+    ws_gdn, _ = planned(session, e_gdn, gdn, "bench-step-layer-gdn")
+
+    def four():
+        session.run(e_conv, conv, None)
+        session.run(e_gates, gates, None)
+        session.run(e_gdn, gdn, ws_gdn)
+        session.run(e_norm, norm, None)
+
+    def fused():
+        roost_amd.gdn_layer(session, conv, gates_in, gdn_in, norm, key="bench-step")
+
+    return {"config": "config 5's GDN layer: 48 x 1 + 2 x 512 tokens, Qwen3.5 layer (conv width 4, gates, recurrent "
+                      "variant, gated norm)",
+            "four_ops_ms": time_each(torch, session, four, steps), "fused_ms": time_each(torch, session, fused, steps)}
 
 
 def bench_chunk_layer(torch, roost_amd, session, steps, g):

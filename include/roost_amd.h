@@ -98,6 +98,20 @@ ROOST_API RoostStatus roost_amd_gdn_decode_layer_run(RoostContext* ctx, const vo
                                                       const void* gates_params, const void* gdn_params,
                                                       const void* norm_params, void* stream);
 
+/* One Gated DeltaNet layer of any step (decode, prefill or mixed) over the recurrent variant in one call: CausalConv1d,
+ * GatedDeltaRuleGates, GatedDeltaRule and GatedRmsNorm. No counterpart in the reference (the same four calls, one after
+ * another; the worker names the recurrent variant for every length, CudaOps.cs:28). A step whose sequences are all
+ * shorter than 16 tokens (known from tokens < 16 or from cu_seqlens_host) with the norm in its single-pass bf16 form
+ * runs as roost_amd_gdn_decode_layer_run does; any other step runs the convolution, the recurrent variant with g and
+ * beta computed from the gates' inputs (its sequences of 16+ tokens on the chunk kernels) and the norm. The norm's
+ * output, the recurrent states and the convolution states equal the four calls' bit for bit (the convolution's and
+ * the GDN output are written on the second path only). Params as for roost_amd_gdn_decode_layer_run, without its
+ * length limit; `ws` is the recurrent variant's workspace (roost_gdn_recurrent_workspace of `gdn_params`; NULL is
+ * enough when it reports zero bytes). */
+ROOST_API RoostStatus roost_amd_gdn_layer_run(RoostContext* ctx, const void* conv_params, const void* gates_params,
+                                              const void* gdn_params, const void* norm_params, const RoostWorkspace* ws,
+                                              void* stream);
+
 /* One prefill pass of a Gated DeltaNet layer over the chunk variant in one call: CausalConv1d, GatedDeltaRuleGates, the
  * chunked GatedDeltaRule and GatedRmsNorm. No counterpart in the reference (the same four calls as above, one after
  * another). The chunk kernels compute g and beta from the gates' inputs where they read them (the gates op's

@@ -112,6 +112,8 @@ class KernelLibrary:
         self.dll.roost_amd_gdn_chunk_layer_run.argtypes = [C.c_void_p] * 7
         self.dll.roost_amd_gdn_chunk_layer_run.restype = C.c_int32
         self.dll.roost_amd_gdn_chunk_layer_plan.argtypes = [C.c_void_p] * 5
+        self.dll.roost_amd_gdn_layer_run.argtypes = [C.c_void_p] * 7
+        self.dll.roost_amd_gdn_layer_run.restype = C.c_int32
         self.dll.roost_amd_gdn_chunk_layer_plan.restype = C.c_int32
         self.dll.roost_amd_plan_region_from_step.argtypes = [C.c_void_p, C.c_uint64, C.POINTER(abi.StepTables)]
         self.dll.roost_amd_plan_region_from_step.restype = C.c_int32
@@ -507,6 +509,18 @@ def gdn_decode_layer(session: OpSession, conv_params, gates_params, gdn_params, 
         C.addressof(gdn_params), C.addressof(norm_params), C.c_void_p(session.stream_handle))
     if status != abi.OK:
         raise KernelError("gdn_decode_layer", status, session.lib.last_error())
+
+
+def gdn_layer(session: OpSession, conv_params, gates_params, gdn_params, norm_params, key=0) -> None:
+    """roost_amd_gdn_layer_run: CausalConv1d, GatedDeltaRuleGates (gates_params may be None), the recurrent
+    GatedDeltaRule and GatedRmsNorm of any step in one call, in the recurrent variant's workspace."""
+    ws = session.prepare(session.lib.entry(RECURRENT_VARIANT), gdn_params, ("layer", key), plan=False)
+    status = session.lib.dll.roost_amd_gdn_layer_run(
+        session.ctx, C.addressof(conv_params), C.addressof(gates_params) if gates_params is not None else None,
+        C.addressof(gdn_params), C.addressof(norm_params), C.addressof(ws) if ws is not None else None,
+        C.c_void_p(session.stream_handle))
+    if status != abi.OK:
+        raise KernelError("gdn_layer", status, session.lib.last_error())
 
 
 def gdn_chunk_layer(session: OpSession, conv_params, gates_params, gdn_params, norm_params, key=0,

@@ -1927,6 +1927,22 @@ struct LayerViews {
   bool empty = false;               // no sequence has a token: nothing is read or written
 };
 
+// The layer calls' pointers and struct headers: a context and the conv, GDN and norm params are required; the gates
+// params may be NULL (g and beta are then read from the GDN params).
+RoostStatus LayerHeaders(const char* op, const RoostContext* ctx, const void* conv_params, const void* gates_params,
+                         const void* gdn_params, const void* norm_params) {
+  roost::Gate gate(op);
+  gate.Expect(ctx != nullptr && conv_params != nullptr && gdn_params != nullptr && norm_params != nullptr,
+              ROOST_STATUS_INVALID_ARGUMENT, "a context and the conv, GDN and norm params are required (the gates "
+              "params may be NULL: g and beta are then read from the GDN params)");
+  ROOST_GATE_RETURN(gate);
+  gate.Header(conv_params, sizeof(RoostCausalConv1dParams))
+      .Header(gdn_params, sizeof(RoostGatedDeltaRuleParams))
+      .Header(norm_params, sizeof(RoostGatedRmsNormParams));
+  if (gates_params != nullptr) gate.Header(gates_params, sizeof(RoostGatedDeltaRuleGatesParams));
+  return gate.status();
+}
+
 // The rules the layer calls share: each op's own admission; the convolution over the GDN call's batch, bf16, at most
 // kLayerMaxWidth taps, and q, k and v column views of its output (where the GDN op reads them); the norm over the GDN
 // output's 128-column rows; and the norm's output apart from every input and state the layer reads.
@@ -1999,6 +2015,40 @@ RoostStatus AdmitLayer(const char* op, const RoostCausalConv1dParams& cp, const 
   return ROOST_STATUS_OK;
 }
 
+// The decode layer's launch for an admitted call whose sequences are all shorter than kRouteMinTokens and whose norm
+// is the single-pass bf16 form: GdnDecodeLayerKernel, then the convolution's state kernel unless the workgroups
+// updated their channels' state themselves.
+RoostStatus LaunchDecodeLayer(const char* op, const RoostCausalConv1dParams& cp, const RoostGatedDeltaRuleParams& p,
+                              const RoostGatedRmsNormParams& np, const LayerViews& lv, hipStream_t s) {
+  const uint64_t sl = cp.width - 1ull;
+  LayerArgs L{};
+  L.cq = lv.cq;
+  L.ck = lv.ck;
+  L.cv = lv.cv;
+  L.a = MakeArgs(p, lv.gs);
+  L.x = static_cast<const uint16_t*>(cp.input.address);
+  L.conv_w = static_cast<const uint16_t*>(cp.weight.address);
+  L.conv_b = static_cast<const uint16_t*>(cp.bias.address);
+  L.conv_state = cp.conv_state.address;
+  L.conv_slots = static_cast<const int32_t*>(cp.state_slots.address);
+  L.conv_state_t = cp.conv_state.dtype == ROOST_DTYPE_UNDEFINED ? cp.input.dtype : cp.conv_state.dtype;
+  L.conv_pool_slots = sl == 0 ? 0 : cp.conv_state.length / (uint64_t{cp.channels} * sl);
+  L.channels = cp.channels;
+  L.width = cp.width;
+  L.silu = cp.silu != 0 ? 1u : 0u;
+  // One value head per key head, and q, k and v tiling the channels without overlap: each channel belongs to exactly
+  // one workgroup, which updates its state itself. Otherwise the conv op's state kernel runs afterwards.
+  L.conv_state_update = p.v_heads == p.k_heads && lv.tiled ? 1u : 0u;
+  L.z = static_cast<const uint16_t*>(np.gate.address);
+  L.norm_w = np.weight.address;
+  L.norm_w_t = np.weight.dtype;
+  L.eps = np.eps;
+  L.y = static_cast<uint16_t*>(np.output.address);
+  hipLaunchKernelGGL(GdnDecodeLayerKernel, dim3(p.batch, p.v_heads), dim3(kLayerThreads), 0, s, L);
+  ROOST_RETURN_IF_FAILED(roost::HipStatus(hipGetLastError(), op, "layer launch"));
+  return L.conv_state_update != 0 ? ROOST_STATUS_OK : roost_layer::ConvStateUpdate(cp, s, op);
+}
+
 }  // namespace
 
 extern "C" ROOST_API RoostStatus roost_amd_gdn_decode_layer_run(RoostContext* ctx, const void* conv_params,
@@ -2006,15 +2056,7 @@ extern "C" ROOST_API RoostStatus roost_amd_gdn_decode_layer_run(RoostContext* ct
                                                                 const void* norm_params, void* stream) {
   constexpr char kLayerOp[] = "gdn_decode_layer";
   roost::Gate gate(kLayerOp);
-  gate.Expect(ctx != nullptr && conv_params != nullptr && gdn_params != nullptr && norm_params != nullptr,
-              ROOST_STATUS_INVALID_ARGUMENT, "a context and the conv, GDN and norm params are required (the gates "
-              "params may be NULL: g and beta are then read from the GDN params)");
-  ROOST_GATE_RETURN(gate);
-  gate.Header(conv_params, sizeof(RoostCausalConv1dParams))
-      .Header(gdn_params, sizeof(RoostGatedDeltaRuleParams))
-      .Header(norm_params, sizeof(RoostGatedRmsNormParams));
-  if (gates_params != nullptr) gate.Header(gates_params, sizeof(RoostGatedDeltaRuleGatesParams));
-  ROOST_GATE_RETURN(gate);
+  ROOST_RETURN_IF_FAILED(LayerHeaders(kLayerOp, ctx, conv_params, gates_params, gdn_params, norm_params));
   const auto& cp = *static_cast<const RoostCausalConv1dParams*>(conv_params);
   const auto& p = *static_cast<const RoostGatedDeltaRuleParams*>(gdn_params);
   const auto& np = *static_cast<const RoostGatedRmsNormParams*>(norm_params);
@@ -2038,34 +2080,44 @@ extern "C" ROOST_API RoostStatus roost_amd_gdn_decode_layer_run(RoostContext* ct
                 "the decode layer's norm is GatedRmsNorm's single-pass bf16 form: 16-byte aligned input, gate and "
                 "output of bf16");
     ROOST_GATE_RETURN(gate);
-    const uint64_t sl = cp.width - 1ull;
-    LayerArgs L{};
-    L.cq = lv.cq;
-    L.ck = lv.ck;
-    L.cv = lv.cv;
-    L.a = MakeArgs(p, lv.gs);
-    L.x = static_cast<const uint16_t*>(cp.input.address);
-    L.conv_w = static_cast<const uint16_t*>(cp.weight.address);
-    L.conv_b = static_cast<const uint16_t*>(cp.bias.address);
-    L.conv_state = cp.conv_state.address;
-    L.conv_slots = static_cast<const int32_t*>(cp.state_slots.address);
-    L.conv_state_t = cp.conv_state.dtype == ROOST_DTYPE_UNDEFINED ? cp.input.dtype : cp.conv_state.dtype;
-    L.conv_pool_slots = sl == 0 ? 0 : cp.conv_state.length / (uint64_t{cp.channels} * sl);
-    L.channels = cp.channels;
-    L.width = cp.width;
-    L.silu = cp.silu != 0 ? 1u : 0u;
-    // One value head per key head, and q, k and v tiling the channels without overlap: each channel belongs to exactly
-    // one workgroup, which updates its state itself. Otherwise the conv op's state kernel runs afterwards.
-    L.conv_state_update = p.v_heads == p.k_heads && lv.tiled ? 1u : 0u;
-    L.z = static_cast<const uint16_t*>(np.gate.address);
-    L.norm_w = np.weight.address;
-    L.norm_w_t = np.weight.dtype;
-    L.eps = np.eps;
-    L.y = static_cast<uint16_t*>(np.output.address);
+    return LaunchDecodeLayer(kLayerOp, cp, p, np, lv, roost::Stream(stream));
+  });
+}
+
+// One GDN layer over the recurrent variant for any step (no reference counterpart; the Qwen3.5 worker runs the four
+// ops one after another, Qwen35EagerModel.cs:89-92, and names the recurrent variant for every length): a step whose
+// sequences are all shorter than kRouteMinTokens, with the norm in its single-pass bf16 form, runs as the decode
+// layer (GdnDecodeLayerKernel); any other step runs the conv op, the recurrent variant with the gates computed where
+// they are read (its longer sequences on the chunk kernels, in `ws`), and the norm op. Either way the results equal
+// the four ops'.
+extern "C" ROOST_API RoostStatus roost_amd_gdn_layer_run(RoostContext* ctx, const void* conv_params,
+                                                         const void* gates_params, const void* gdn_params,
+                                                         const void* norm_params, const RoostWorkspace* ws,
+                                                         void* stream) {
+  constexpr char kLayerOp[] = "gdn_layer";
+  ROOST_RETURN_IF_FAILED(LayerHeaders(kLayerOp, ctx, conv_params, gates_params, gdn_params, norm_params));
+  const auto& cp = *static_cast<const RoostCausalConv1dParams*>(conv_params);
+  const auto& p = *static_cast<const RoostGatedDeltaRuleParams*>(gdn_params);
+  const auto& np = *static_cast<const RoostGatedRmsNormParams*>(norm_params);
+  return roost::CatchAll(kLayerOp, [&]() -> RoostStatus {
+    LayerViews lv;
+    ROOST_RETURN_IF_FAILED(AdmitLayer(kLayerOp, cp, gates_params, p, np, &lv));
+    if (lv.empty) return ROOST_STATUS_OK;
+    // Short sequences only: known from the token count, or from the host copy of cu_seqlens.
+    bool short_only = p.tokens < kRouteMinTokens;
+    if (!short_only && p.cu_seqlens_host != nullptr) {
+      short_only = true;
+      for (uint32_t b = 0; b < p.batch && short_only; ++b) {
+        short_only = p.cu_seqlens_host[b + 1] - p.cu_seqlens_host[b] < static_cast<int32_t>(kRouteMinTokens);
+      }
+    }
     hipStream_t s = roost::Stream(stream);
-    hipLaunchKernelGGL(GdnDecodeLayerKernel, dim3(p.batch, p.v_heads), dim3(kLayerThreads), 0, s, L);
-    ROOST_RETURN_IF_FAILED(roost::HipStatus(hipGetLastError(), kLayerOp, "layer launch"));
-    return L.conv_state_update != 0 ? ROOST_STATUS_OK : roost_layer::ConvStateUpdate(cp, s, kLayerOp);
+    if (short_only && np.input.dtype == ROOST_DTYPE_BF16 && lv.row_form) {
+      return LaunchDecodeLayer(kLayerOp, cp, p, np, lv, s);
+    }
+    ROOST_RETURN_IF_FAILED(roost_causal_conv1d_run(ctx, conv_params, nullptr, stream));
+    ROOST_RETURN_IF_FAILED(RecurrentRun(p, ws, s, lv.gs));
+    return roost_gated_rms_norm_run(ctx, norm_params, nullptr, stream);
   });
 }
 
@@ -2207,15 +2259,7 @@ extern "C" ROOST_API RoostStatus roost_amd_gdn_chunk_layer_run(RoostContext* ctx
                                                                void* stream) {
   constexpr char kLayerOp[] = "gdn_chunk_layer";
   roost::Gate gate(kLayerOp);
-  gate.Expect(ctx != nullptr && conv_params != nullptr && gdn_params != nullptr && norm_params != nullptr,
-              ROOST_STATUS_INVALID_ARGUMENT, "a context and the conv, GDN and norm params are required (the gates "
-              "params may be NULL: g and beta are then read from the GDN params)");
-  ROOST_GATE_RETURN(gate);
-  gate.Header(conv_params, sizeof(RoostCausalConv1dParams))
-      .Header(gdn_params, sizeof(RoostGatedDeltaRuleParams))
-      .Header(norm_params, sizeof(RoostGatedRmsNormParams));
-  if (gates_params != nullptr) gate.Header(gates_params, sizeof(RoostGatedDeltaRuleGatesParams));
-  ROOST_GATE_RETURN(gate);
+  ROOST_RETURN_IF_FAILED(LayerHeaders(kLayerOp, ctx, conv_params, gates_params, gdn_params, norm_params));
   const auto& cp = *static_cast<const RoostCausalConv1dParams*>(conv_params);
   const auto& p = *static_cast<const RoostGatedDeltaRuleParams*>(gdn_params);
   const auto& np = *static_cast<const RoostGatedRmsNormParams*>(norm_params);

@@ -181,3 +181,32 @@ def test_decode_layer_empty_step(session):
     out, cs, st = layer.fused(session)
     assert np.array_equal(cs, from_dev(layer.conv_state, True))
     assert np.array_equal(st, from_dev(layer.state))
+
+
+# roost_amd_gdn_layer_run: the same layer for any step over the recurrent variant (the decode-layer kernel when every
+# sequence is short, else the conv op, the recurrent variant with the gates folded in and the norm op).
+ANY_LAYER_CASES = [
+    ("decode 16 x 1 (decode-layer kernel)", [1] * 16, 16, 16, 4, True, "bf16", True, True),
+    ("mixed step: prefills beside decode rows", [1, 600, 17, 0, 3, 1, 64], 16, 16, 4, True, "bf16", True, True),
+    ("mixed step, group 2, width 3, f32 state, g and beta read", [200, 1, 1, 40], 8, 16, 3, False, "f32", False, True),
+    ("no host lengths (device routing)", [1, 30, 2, 16], 4, 4, 4, True, "bf16", True, False),
+]
+
+
+@pytest.mark.parametrize("name,lens,kh,vh,width,bias,sdt,fg,cu_host", ANY_LAYER_CASES,
+                         ids=[c[0] for c in ANY_LAYER_CASES])
+def test_any_step_layer_equals_the_four_ops(session, name, lens, kh, vh, width, bias, sdt, fg, cu_host):
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    layer = Layer(rng, lens, kh, vh, width, bias, sdt, fg, None, None)
+    want_out, want_cs, want_st = layer.four_ops(session)
+    t = layer.t
+    y, o, out, cs, st = layer.buffers()
+    gates = layer.gates_params(None, None) if fg else None
+    gdn = layer.gdn_params(y, o, st, None if fg else layer.g, None if fg else layer.beta, cu_host=cu_host)
+    roost_amd.gdn_layer(session, layer.conv_params(y, cs), gates, gdn, layer.norm_params(o, out), key=name)
+    t.cuda.synchronize()
+    T = layer.T * vh
+    assert np.array_equal(from_dev(out, True)[:T], want_out[:T]), "norm output differs from the four ops"
+    assert np.array_equal(from_dev(cs, cs.dtype == t.bfloat16), want_cs), "convolution states differ from the four ops"
+    assert np.array_equal(from_dev(st), want_st), "recurrent states differ from the four ops"
+    assert not np.isnan(cases.bf16_values(from_dev(out, True)[:T])).any()
