@@ -164,18 +164,32 @@ struct GdnArgs {
 
 // g and beta of (token, value head): read from the call's g and beta, or computed from the gates' inputs exactly as
 // the GatedDeltaRuleGates op computes and stores them (beta rounded to bf16, as its bf16 output holds it).
-__device__ __forceinline__ void GateAt(const GdnArgs& a, uint64_t tok, uint32_t h, float& g, float& beta) {
+// In two steps, so that a kernel can request a token's gate inputs early and compute from them later: GateLoad reads
+// (a, dt_bias, a_log, b), or (g, beta) when the gates are not folded in; GateFrom computes.
+struct GateIn {
+  float x0, x1, x2, x3;
+};
+__device__ __forceinline__ GateIn GateLoad(const GdnArgs& a, uint64_t tok, uint32_t h) {
+  if (a.gs.a != nullptr) {
+    return GateIn{LoadF(a.gs.a, a.gs.a_t, static_cast<int64_t>(tok * a.gs.a_stride + h)),
+                  LoadF(a.gs.dt_bias, a.gs.dtb_t, h), LoadF(a.gs.a_log, a.gs.alog_t, h),
+                  LoadF(a.gs.b, a.gs.b_t, static_cast<int64_t>(tok * a.gs.b_stride + h))};
+  }
+  const uint64_t gi = tok * a.vh + h;
+  return GateIn{a.g[gi], Bf16ToF32(a.beta[gi]), 0.0f, 0.0f};
+}
+__device__ __forceinline__ void GateFrom(const GdnArgs& a, const GateIn& in, float& g, float& beta) {
   if (a.gs.a != nullptr) {
     float bv;
-    GateValues(LoadF(a.gs.a, a.gs.a_t, static_cast<int64_t>(tok * a.gs.a_stride + h)),
-               LoadF(a.gs.dt_bias, a.gs.dtb_t, h), LoadF(a.gs.a_log, a.gs.alog_t, h),
-               LoadF(a.gs.b, a.gs.b_t, static_cast<int64_t>(tok * a.gs.b_stride + h)), g, bv);
+    GateValues(in.x0, in.x1, in.x2, in.x3, g, bv);
     beta = Bf16ToF32(F32ToBf16(bv));
   } else {
-    const uint64_t gi = tok * a.vh + h;
-    g = a.g[gi];
-    beta = Bf16ToF32(a.beta[gi]);
+    g = in.x0;
+    beta = in.x1;
   }
+}
+__device__ __forceinline__ void GateAt(const GdnArgs& a, uint64_t tok, uint32_t h, float& g, float& beta) {
+  GateFrom(a, GateLoad(a, tok, h), g, beta);
 }
 
 typedef float f32x4v_t __attribute__((ext_vector_type(4)));
@@ -336,7 +350,7 @@ __device__ __forceinline__ bool ChainMember(const GdnArgs& a, uint32_t j, int32_
 }
 
 // Workgroup (sequence b, value head h, column quarter): the token-serial recurrence with its share of S in registers.
-template <bool kVec>
+template <bool kVec, bool kPreload = false>
 __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint32_t h, uint32_t quarter) {
   __shared__ float red_sk[4][32], red_o[4][32];
   int32_t t0 = a.cu[b];
@@ -360,6 +374,30 @@ __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint
 #pragma unroll
     for (int i = 0; i < kScanNow; ++i) sj[i] = a.slots[min(static_cast<uint32_t>(lane + 64 * i), a.batch - 1)];
   }
+  // With kPreload the first token's q, k and v words and gate inputs are requested before the state too: its norms
+  // and gates then wait only for themselves and are computed while the state is in flight (RecurrentKernel: 48.4
+  // against 49.5 us at 128 states; inside the prep launch's 80-register bound the extra live registers spill, and it
+  // keeps the loads in the step).
+  uint32_t qw = 0, kw = 0;
+  uint2 qr = make_uint2(0, 0), kr = qr, vw = qr;
+  auto load_rows = [&](int32_t tok) {
+    if constexpr (kVec) {
+      const uint16_t* qrow = a.q + static_cast<uint64_t>(tok) * a.q_stride + kh * kDim;
+      const uint16_t* krow = a.k + static_cast<uint64_t>(tok) * a.k_stride + kh * kDim;
+      const uint16_t* vrow = a.v + static_cast<uint64_t>(tok) * a.v_stride + h * kDim + col;
+      qw = *reinterpret_cast<const uint32_t*>(qrow + 2 * lane);
+      kw = *reinterpret_cast<const uint32_t*>(krow + 2 * lane);
+      qr = *reinterpret_cast<const uint2*>(qrow + row0);
+      kr = *reinterpret_cast<const uint2*>(krow + row0);
+      vw = *reinterpret_cast<const uint2*>(vrow);
+    }
+  };
+  GateIn gin{};
+  if constexpr (kPreload) {
+    load_rows(t0);
+    gin = GateLoad(a, static_cast<uint64_t>(t0), h);
+  }
+  bool first_step = kPreload;
   float4 s[4];
   float* sp = has_slot ? a.state + (static_cast<uint64_t>(slot) * a.vh + h) * kDim * kDim + col : nullptr;
   if (has_slot && a.use_initial_state) {
@@ -384,10 +422,7 @@ __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint
     float q2[2], k2[2], q4[4], k4[4], vv[4];
     const uint16_t* vrow = a.v + static_cast<uint64_t>(tok) * a.v_stride + h * kDim + col;
     if constexpr (kVec) {
-      const uint32_t qw = *reinterpret_cast<const uint32_t*>(qrow + 2 * lane);
-      const uint32_t kw = *reinterpret_cast<const uint32_t*>(krow + 2 * lane);
-      const uint2 qr = *reinterpret_cast<const uint2*>(qrow + row0), kr = *reinterpret_cast<const uint2*>(krow + row0);
-      const uint2 vw = *reinterpret_cast<const uint2*>(vrow);
+      if (!first_step) load_rows(tok);
       q2[0] = Bf16LoToF32(qw); q2[1] = Bf16HiToF32(qw);
       k2[0] = Bf16LoToF32(kw); k2[1] = Bf16HiToF32(kw);
       q4[0] = Bf16LoToF32(qr.x); q4[1] = Bf16HiToF32(qr.x); q4[2] = Bf16LoToF32(qr.y); q4[3] = Bf16HiToF32(qr.y);
@@ -406,8 +441,10 @@ __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint
         vv[i] = Bf16ToF32(vrow[i]);
       }
     }
+    if (!first_step) gin = GateLoad(a, static_cast<uint64_t>(tok), h);
+    first_step = false;
     float graw, beta;
-    GateAt(a, static_cast<uint64_t>(tok), h, graw, beta);
+    GateFrom(a, gin, graw, beta);
     const float decay = expf(graw);
     float qq = fmaf(q2[0], q2[0], q2[1] * q2[1]), kk = fmaf(k2[0], k2[0], k2[1] * k2[1]);
 #pragma unroll
@@ -518,7 +555,7 @@ __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint
 
 template <bool kVec>
 __global__ void __launch_bounds__(kRecThreads) RecurrentKernel(GdnArgs a) {
-  RecurrentUnit<kVec>(a, blockIdx.x, blockIdx.y / kRecQuarters, blockIdx.y % kRecQuarters);
+  RecurrentUnit<kVec, true>(a, blockIdx.x, blockIdx.y / kRecQuarters, blockIdx.y % kRecQuarters);
 }
 
 GdnArgs MakeArgs(const RoostGatedDeltaRuleParams& p, const GateSource& gs = GateSource{}) {
