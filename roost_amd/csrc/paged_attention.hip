@@ -1365,20 +1365,26 @@ __global__ void __launch_bounds__(256, kDecodeWgsPerCu) DecodeKernel(const T* __
 // Combines the pieces of each split sequence in key order: one workgroup per (sequence, query head), D threads, one
 // output element each. Wavefront 0 computes the per-piece rescale factors into LDS (lanes over pieces), then every
 // thread sums its element over the pieces with independent loads.
+struct DecodeMergeArgs {
+  const DecodeMerge* merges;
+  const float* part_o;
+  const float* part_ml;
+  const int32_t* q_rows;  // the call's q_indptr in a prefill call, NULL in a decode call
+};
+
 template <typename T, int D>
-__global__ void __launch_bounds__(D) DecodeMergeKernel(T* __restrict__ out, float* __restrict__ lse,
-                                                       const DecodeMerge* __restrict__ merges,
-                                                       const float* __restrict__ part_o,
-                                                       const float* __restrict__ part_ml,
-                                                       const int32_t* __restrict__ q_rows, uint32_t q_heads,
-                                                       const void* out_gate) {
+__device__ __forceinline__ void DecodeMergeBody(T* __restrict__ out, float* __restrict__ lse, const DecodeMergeArgs& m,
+                                                uint32_t q_heads, const void* out_gate, uint32_t bx) {
   __shared__ float f_lds[kMaxMergeSplits];
   __shared__ float inv_lds;
-  const DecodeMerge mg = merges[blockIdx.x / q_heads];
+  const float* __restrict__ part_o = m.part_o;
+  const float* __restrict__ part_ml = m.part_ml;
+  const int32_t* __restrict__ q_rows = m.q_rows;
+  const DecodeMerge mg = m.merges[bx / q_heads];
   const uint64_t tok = q_rows != nullptr
                            ? static_cast<uint64_t>(max(q_rows[mg.seq], q_rows[mg.seq + 1] - 1 - mg.q_back))
                            : static_cast<uint64_t>(mg.seq);
-  const uint32_t qh = blockIdx.x % q_heads;
+  const uint32_t qh = bx % q_heads;
   const int n = min(mg.count, static_cast<int32_t>(kMaxMergeSplits));
   const uint64_t base = static_cast<uint64_t>(mg.first) * q_heads + qh;  // partial row of piece c: base + c * q_heads
   // This thread's partial outputs of the first kPre pieces are requested first, so that they arrive while the pieces'
@@ -1428,6 +1434,12 @@ __global__ void __launch_bounds__(D) DecodeMergeKernel(T* __restrict__ out, floa
   const float o0 = acc[0], o1 = acc[1], o2 = acc[2], o3 = acc[3];
   const uint64_t e = (tok * q_heads + qh) * D + d;
   out[e] = GateOut<T>(out_gate, e, Vec<T>::Narrow(((o0 + o1) + (o2 + o3)) * inv_lds));
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(D) DecodeMergeKernel(T* __restrict__ out, float* __restrict__ lse, DecodeMergeArgs m,
+                                                       uint32_t q_heads, const void* out_gate) {
+  DecodeMergeBody<T, D>(out, lse, m, q_heads, out_gate, blockIdx.x);
 }
 
 // ---- Prefill kernel (bf16, head_dim 256, MFMA) -----------------------------------------------------------------------
@@ -2163,13 +2175,25 @@ __device__ __forceinline__ void PrefillMergeRows(uint16_t* __restrict__ out, flo
 
 // One launch for both forms: the first `two` merges (exactly two pieces) as blocks of kPfMergeRows token rows, the
 // rest one token row per block (two merge launches one after the other cost a second launch's latency).
+struct PrefillMergeArgs {
+  const PrefillMerge* merges;
+  const uint16_t* part_o;
+  const float* part_ml;
+  const int32_t* q_indptr;
+  uint32_t two;     // merges of exactly two pieces, listed first
+  uint32_t blocks;  // blocks of the launch's prefill share
+};
+
 template <int D>
-__global__ void __launch_bounds__(256)
-    PrefillMergeKernel(uint16_t* __restrict__ out, float* __restrict__ lse, const PrefillMerge* __restrict__ merges,
-                       const uint16_t* __restrict__ part_o, const float* __restrict__ part_ml,
-                       const int32_t* __restrict__ q_indptr, uint32_t q_heads, uint32_t two, const void* gate) {
+__device__ __forceinline__ void PrefillMergeBody(uint16_t* __restrict__ out, float* __restrict__ lse,
+                                                 const PrefillMergeArgs& m, uint32_t q_heads, const void* gate,
+                                                 uint32_t b) {
   constexpr uint32_t kTwoBlocks = kPfTokens / kPfMergeRows;  // blocks per two-piece merge
-  const uint32_t b = blockIdx.x;
+  const PrefillMerge* __restrict__ merges = m.merges;
+  const uint16_t* __restrict__ part_o = m.part_o;
+  const float* __restrict__ part_ml = m.part_ml;
+  const int32_t* __restrict__ q_indptr = m.q_indptr;
+  const uint32_t two = m.two;
   if (b < two * kTwoBlocks) {
     PrefillMergeRows<D, kPfMergeRows>(out, lse, merges[b / kTwoBlocks], static_cast<int>(b % kTwoBlocks) * kPfMergeRows,
                                       part_o, part_ml, q_indptr, q_heads, gate);
@@ -2180,19 +2204,44 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+template <int D>
+__global__ void __launch_bounds__(256) PrefillMergeKernel(uint16_t* __restrict__ out, float* __restrict__ lse,
+                                                          PrefillMergeArgs m, uint32_t q_heads, const void* gate) {
+  PrefillMergeBody<D>(out, lse, m, q_heads, gate, blockIdx.x);
+}
+
+// A mixed step's two merges in one launch (both take D threads per block): the tile pieces' merge blocks first, then
+// the decode ranges'. One launch instead of two saves the second's latency.
+template <int D>
+__global__ void __launch_bounds__(D) MixedMergeKernel(uint16_t* __restrict__ out, float* __restrict__ lse,
+                                                      PrefillMergeArgs pm, DecodeMergeArgs dm, uint32_t q_heads,
+                                                      const void* gate) {
+  static_assert(kGroup * D / 4 == D, "a prefill merge block has D threads");
+  if (blockIdx.x < pm.blocks) {
+    PrefillMergeBody<D>(out, lse, pm, q_heads, gate, blockIdx.x);
+  } else {
+    DecodeMergeBody<uint16_t, D>(out, lse, dm, q_heads, gate, blockIdx.x - pm.blocks);
+  }
+}
+
 // The decode pieces' partials: fp32 rows (dec_splits x q_heads x D), then their (max, sum) pairs.
+DecodeMergeArgs DecodeMergeArgsOf(const RoostPagedAttentionParams& p, const PlanRecord& rec, unsigned char* dev,
+                                  uint32_t d) {
+  DecodeMergeArgs m{};
+  m.merges = reinterpret_cast<const DecodeMerge*>(dev + rec.dec_merge_offset);
+  m.part_o = reinterpret_cast<const float*>(dev + rec.dec_float_offset);
+  m.part_ml = m.part_o + rec.dec_splits * p.q_heads * d;
+  m.q_rows = p.mode == ROOST_ATTENTION_PREFILL ? static_cast<const int32_t*>(p.q_indptr.address) : nullptr;
+  return m;
+}
+
 template <typename T, int D>
 RoostStatus LaunchDecodeMerge(const RoostPagedAttentionParams& p, const PlanRecord& rec, unsigned char* dev,
                               const KvView& kv, hipStream_t stream) {
   if (rec.dec_merges == 0) return ROOST_STATUS_OK;
-  const auto* merges = reinterpret_cast<const DecodeMerge*>(dev + rec.dec_merge_offset);
-  auto* part_o = reinterpret_cast<float*>(dev + rec.dec_float_offset);
-  auto* part_ml = part_o + rec.dec_splits * p.q_heads * D;
-  const auto* q_rows =
-      p.mode == ROOST_ATTENTION_PREFILL ? static_cast<const int32_t*>(p.q_indptr.address) : nullptr;
   hipLaunchKernelGGL((DecodeMergeKernel<T, D>), dim3(static_cast<uint32_t>(rec.dec_merges * p.q_heads)), dim3(D), 0,
-                     stream, static_cast<T*>(p.output.address), static_cast<float*>(p.lse.address), merges, part_o,
-                     part_ml, q_rows, p.q_heads, kv.out_gate);
+                     stream, static_cast<T*>(p.output.address), static_cast<float*>(p.lse.address),
+                     DecodeMergeArgsOf(p, rec, dev, D), p.q_heads, kv.out_gate);
   return roost::HipStatus(hipGetLastError(), "paged_attention", "decode merge launch");
 }
 
@@ -2232,33 +2281,36 @@ float* PrefillPartMl(const RoostPagedAttentionParams& p, const PlanRecord& rec, 
   return reinterpret_cast<float*>(PrefillPartO(p, rec, dev) + rec.splits * kPfRows * p.head_dim);
 }
 
+PrefillMergeArgs PrefillMergeArgsOf(const RoostPagedAttentionParams& p, const PlanRecord& rec, unsigned char* dev) {
+  PrefillMergeArgs m{};
+  m.merges = reinterpret_cast<const PrefillMerge*>(dev + rec.merge_offset);
+  m.part_o = PrefillPartO(p, rec, dev);
+  m.part_ml = PrefillPartMl(p, rec, dev);
+  m.q_indptr = static_cast<const int32_t*>(p.q_indptr.address);
+  m.two = static_cast<uint32_t>(rec.merges_two);
+  m.blocks = m.two * (kPfTokens / kPfMergeRows) + (static_cast<uint32_t>(rec.merges) - m.two) * kPfTokens;
+  return m;
+}
+
 RoostStatus LaunchPrefillMerge(const RoostPagedAttentionParams& p, const PlanRecord& rec, unsigned char* dev,
                                const KvView& kv, hipStream_t stream) {
   if (rec.merges == 0) return ROOST_STATUS_OK;
-  const auto* q_indptr = static_cast<const int32_t*>(p.q_indptr.address);
   auto* outp = static_cast<uint16_t*>(p.output.address);
   auto* lsep = static_cast<float*>(p.lse.address);
-  uint16_t* part_o = PrefillPartO(p, rec, dev);
-  float* part_ml = PrefillPartMl(p, rec, dev);
-  const auto* mg = reinterpret_cast<const PrefillMerge*>(dev + rec.merge_offset);
-  const uint32_t two = rec.merges_two, rest = static_cast<uint32_t>(rec.merges) - rec.merges_two;
-  const dim3 block(kGroup * p.head_dim / 4);
-  const dim3 g(two * (kPfTokens / kPfMergeRows) + rest * kPfTokens);
+  const PrefillMergeArgs m = PrefillMergeArgsOf(p, rec, dev);
+  const dim3 block(kGroup * p.head_dim / 4), g(m.blocks);
   if (p.head_dim == 64) {
-    hipLaunchKernelGGL(PrefillMergeKernel<64>, g, block, 0, stream, outp, lsep, mg, part_o, part_ml, q_indptr,
-                       p.q_heads, two, kv.out_gate);
+    hipLaunchKernelGGL(PrefillMergeKernel<64>, g, block, 0, stream, outp, lsep, m, p.q_heads, kv.out_gate);
   } else if (p.head_dim == 128) {
-    hipLaunchKernelGGL(PrefillMergeKernel<128>, g, block, 0, stream, outp, lsep, mg, part_o, part_ml, q_indptr,
-                       p.q_heads, two, kv.out_gate);
+    hipLaunchKernelGGL(PrefillMergeKernel<128>, g, block, 0, stream, outp, lsep, m, p.q_heads, kv.out_gate);
   } else {
-    hipLaunchKernelGGL(PrefillMergeKernel<256>, g, block, 0, stream, outp, lsep, mg, part_o, part_ml, q_indptr,
-                       p.q_heads, two, kv.out_gate);
+    hipLaunchKernelGGL(PrefillMergeKernel<256>, g, block, 0, stream, outp, lsep, m, p.q_heads, kv.out_gate);
   }
   return roost::HipStatus(hipGetLastError(), "paged_attention", "prefill merge launch");
 }
 
 // A mixed step the plan chose to run in one launch (PlanRecord::overlap): the tile pieces and decode ranges on
-// MixedAttentionKernel, then both merge kernels, all on the caller's stream.
+// MixedAttentionKernel, then both merges in one MixedMergeKernel launch, all on the caller's stream.
 RoostStatus LaunchMixed(const RoostPagedAttentionParams& p, const PlanRecord& rec, unsigned char* dev, const KvView& kv,
                         float scale_log2, hipStream_t stream) {
   const auto* q16 = static_cast<const uint16_t*>(p.q.address);
@@ -2290,12 +2342,17 @@ RoostStatus LaunchMixed(const RoostPagedAttentionParams& p, const PlanRecord& re
     capped ? launch(MixedAttentionKernel<256, true>) : launch(MixedAttentionKernel<256, false>);
   }
   ROOST_RETURN_IF_FAILED(roost::HipStatus(hipGetLastError(), "paged_attention", "mixed attention launch"));
-  ROOST_RETURN_IF_FAILED(LaunchPrefillMerge(p, rec, dev, kv, stream));
+  const PrefillMergeArgs pm = rec.merges != 0 ? PrefillMergeArgsOf(p, rec, dev) : PrefillMergeArgs{};
+  const DecodeMergeArgs dm = DecodeMergeArgsOf(p, rec, dev, p.head_dim);
+  const uint64_t blocks = uint64_t{pm.blocks} + rec.dec_merges * p.q_heads;
+  if (blocks == 0) return ROOST_STATUS_OK;
+  const dim3 g(static_cast<uint32_t>(blocks)), block(p.head_dim);
   switch (p.head_dim) {
-    case 64: return LaunchDecodeMerge<uint16_t, 64>(p, rec, dev, kv, stream);
-    case 128: return LaunchDecodeMerge<uint16_t, 128>(p, rec, dev, kv, stream);
-    default: return LaunchDecodeMerge<uint16_t, 256>(p, rec, dev, kv, stream);
+    case 64: hipLaunchKernelGGL(MixedMergeKernel<64>, g, block, 0, stream, outp, lsep, pm, dm, p.q_heads, kv.out_gate); break;
+    case 128: hipLaunchKernelGGL(MixedMergeKernel<128>, g, block, 0, stream, outp, lsep, pm, dm, p.q_heads, kv.out_gate); break;
+    default: hipLaunchKernelGGL(MixedMergeKernel<256>, g, block, 0, stream, outp, lsep, pm, dm, p.q_heads, kv.out_gate); break;
   }
+  return roost::HipStatus(hipGetLastError(), "paged_attention", "mixed merge launch");
 }
 
 RoostStatus LaunchPrefill(const RoostPagedAttentionParams& p, const PlanRecord& rec, unsigned char* dev, const KvView& kv,
