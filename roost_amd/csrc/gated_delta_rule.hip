@@ -350,7 +350,7 @@ __device__ __forceinline__ bool ChainMember(const GdnArgs& a, uint32_t j, int32_
 }
 
 // Workgroup (sequence b, value head h, column quarter): the token-serial recurrence with its share of S in registers.
-template <bool kVec, bool kPreload = false>
+template <bool kVec, bool kPreload = false, bool kPreGate = kPreload>
 __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint32_t h, uint32_t quarter) {
   __shared__ float red_sk[4][32], red_o[4][32];
   int32_t t0 = a.cu[b];
@@ -377,7 +377,9 @@ __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint
   // With kPreload the first token's q, k and v words and gate inputs are requested before the state too: its norms
   // and gates then wait only for themselves and are computed while the state is in flight (RecurrentKernel: 48.4
   // against 49.5 us at 128 states; inside the prep launch's 80-register bound the extra live registers spill, and it
-  // keeps the loads in the step).
+  // keeps the loads in the step). kPreGate requests only the gate inputs early: the prep launch does so when it
+  // computes the gates itself (four inputs and the gate arithmetic per token: config 5's GDN layer 0.0446 against
+  // 0.0460 ms), not when it reads g and beta (0.0415 against 0.0412 ms).
   uint32_t qw = 0, kw = 0;
   uint2 qr = make_uint2(0, 0), kr = qr, vw = qr;
   auto load_rows = [&](int32_t tok) {
@@ -393,11 +395,9 @@ __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint
     }
   };
   GateIn gin{};
-  if constexpr (kPreload) {
-    load_rows(t0);
-    gin = GateLoad(a, static_cast<uint64_t>(t0), h);
-  }
-  bool first_step = kPreload;
+  if constexpr (kPreload) load_rows(t0);
+  if constexpr (kPreGate) gin = GateLoad(a, static_cast<uint64_t>(t0), h);
+  bool first_step = kPreload, first_gate = kPreGate;
   float4 s[4];
   float* sp = has_slot ? a.state + (static_cast<uint64_t>(slot) * a.vh + h) * kDim * kDim + col : nullptr;
   if (has_slot && a.use_initial_state) {
@@ -441,8 +441,9 @@ __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint
         vv[i] = Bf16ToF32(vrow[i]);
       }
     }
-    if (!first_step) gin = GateLoad(a, static_cast<uint64_t>(tok), h);
+    if (!first_gate) gin = GateLoad(a, static_cast<uint64_t>(tok), h);
     first_step = false;
+    first_gate = false;
     float graw, beta;
     GateFrom(a, gin, graw, beta);
     const float decay = expf(graw);
@@ -1261,7 +1262,7 @@ __global__ void __launch_bounds__(256, 6) WyPrepKernel(ChunkArgs ca) {
 // sequences shorter than a.route_min. One launch instead of two streams: the recurrent work fills the CUs the prep
 // leaves idle, and the scan that follows has the chip to itself. The prep workgroups come first in dispatch order, so
 // that none of them waits behind recurrent ones for a slot.
-template <bool kVec>
+template <bool kVec, bool kPreGate>
 __global__ void __launch_bounds__(256, 6) WyPrepRecurrentKernel(ChunkArgs ca) {
   static_assert(kRecThreads == 256, "the prep and recurrent workgroups share one size");
   const uint32_t vh = ca.a.vh, i = blockIdx.x, preps = ca.prep_x * vh;
@@ -1269,7 +1270,7 @@ __global__ void __launch_bounds__(256, 6) WyPrepRecurrentKernel(ChunkArgs ca) {
     WyPrepChunk<kVec>(ca, i / vh, i % vh);
   } else {
     const uint32_t j = i - preps, per_seq = vh * kRecQuarters;
-    RecurrentUnit<kVec>(ca.a, j / per_seq, (j % per_seq) / kRecQuarters, j % kRecQuarters);
+    RecurrentUnit<kVec, false, kPreGate>(ca.a, j / per_seq, (j % per_seq) / kRecQuarters, j % kRecQuarters);
   }
 }
 
@@ -1807,11 +1808,15 @@ RoostStatus LaunchChunk(const RoostGatedDeltaRuleParams& p, const RoostWorkspace
     ca.a.route_min = static_cast<int32_t>(kRouteMinTokens);
     ca.prep_x = chunks;
     const dim3 both((chunks + p.batch * kRecQuarters) * p.v_heads);
+    // The gate inputs are requested before the state when the launch computes the gates itself.
+    const bool pre_gate = gs.a != nullptr;
     if (Vec16(p)) {
-      hipLaunchKernelGGL(WyPrepRecurrentKernel<true>, both, dim3(256), 0, stream, ca);
+      auto* prep = pre_gate ? WyPrepRecurrentKernel<true, true> : WyPrepRecurrentKernel<true, false>;
+      hipLaunchKernelGGL(prep, both, dim3(256), 0, stream, ca);
       hipLaunchKernelGGL(WyScanKernel<true>, scan, dim3(320), 0, stream, ca);
     } else {
-      hipLaunchKernelGGL(WyPrepRecurrentKernel<false>, both, dim3(256), 0, stream, ca);
+      auto* prep = pre_gate ? WyPrepRecurrentKernel<false, true> : WyPrepRecurrentKernel<false, false>;
+      hipLaunchKernelGGL(prep, both, dim3(256), 0, stream, ca);
       hipLaunchKernelGGL(WyScanKernel<false>, scan, dim3(320), 0, stream, ca);
     }
   } else if (Vec16(p)) {
