@@ -822,6 +822,22 @@ template <typename T>
 __device__ __forceinline__ T GateOut(const void* gate, uint64_t e, T v) {
   return gate == nullptr ? v : GateMul(v, static_cast<const T*>(gate)[e]);
 }
+// The same in two steps, for epilogues that request the gate before their own loads land: the raw gate words of
+// element e (zero without a gate), then the product.
+__device__ __forceinline__ u32x2_t GateFetch2(const void* gate, uint64_t e) {
+  return gate == nullptr ? u32x2_t{0, 0} : *reinterpret_cast<const u32x2_t*>(static_cast<const uint16_t*>(gate) + e);
+}
+__device__ __forceinline__ u32x2_t GateApply2(const void* gate, u32x2_t g, u32x2_t v) {
+  return gate == nullptr ? v : u32x2_t{GateMulBf16x2(v[0], g[0]), GateMulBf16x2(v[1], g[1])};
+}
+template <typename T>
+__device__ __forceinline__ T GateFetch(const void* gate, uint64_t e) {
+  return gate == nullptr ? T{} : static_cast<const T*>(gate)[e];
+}
+template <typename T>
+__device__ __forceinline__ T GateApply(const void* gate, T g, T v) {
+  return gate == nullptr ? v : GateMul(v, g);
+}
 
 // 16-byte load with the non-temporal hint, for data read exactly once in whole cache lines per instruction (decode V:
 // 2 tokens x 512 contiguous bytes per wavefront load). Keeping such a stream out of the caches raises the rate of a
@@ -1393,6 +1409,8 @@ __device__ __forceinline__ void DecodeMergeBody(T* __restrict__ out, float* __re
   const int d = threadIdx.x;
   const float* po = part_o + base * D + d;
   const uint64_t step = static_cast<uint64_t>(q_heads) * D;
+  const uint64_t e = (tok * q_heads + qh) * D + d;
+  const T gv = GateFetch<T>(out_gate, e);  // requested with the partials, applied at the end
   float pre[kPre];
 #pragma unroll
   for (int c = 0; c < kPre; ++c) pre[c] = c < n ? po[c * step] : 0.0f;
@@ -1432,8 +1450,7 @@ __device__ __forceinline__ void DecodeMergeBody(T* __restrict__ out, float* __re
   }
   for (int c = kPre; c < n; ++c) acc[c & 3] = fmaf(po[c * step], f_lds[c], acc[c & 3]);
   const float o0 = acc[0], o1 = acc[1], o2 = acc[2], o3 = acc[3];
-  const uint64_t e = (tok * q_heads + qh) * D + d;
-  out[e] = GateOut<T>(out_gate, e, Vec<T>::Narrow(((o0 + o1) + (o2 + o3)) * inv_lds));
+  out[e] = GateApply<T>(out_gate, gv, Vec<T>::Narrow(((o0 + o1) + (o2 + o3)) * inv_lds));
 }
 
 template <typename T, int D>
@@ -2092,12 +2109,12 @@ constexpr int kPfMergeRows = 8;
 
 template <int D>
 __device__ __forceinline__ void MergeWrite(uint16_t* __restrict__ out, float* __restrict__ lse, const void* gate,
-                                           uint64_t token, uint32_t q_heads, uint32_t head, int d, float4 acc, float l,
-                                           float mx) {
+                                           u32x2_t g, uint64_t token, uint32_t q_heads, uint32_t head, int d,
+                                           float4 acc, float l, float mx) {
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
   const u32x2_t v{PackBf16(acc.x * inv, acc.y * inv), PackBf16(acc.z * inv, acc.w * inv)};
   const uint64_t e = (token * q_heads + head) * D + d;
-  *reinterpret_cast<u32x2_t*>(out + e) = GateOut2(gate, e, v);
+  *reinterpret_cast<u32x2_t*>(out + e) = GateApply2(gate, g, v);
   if (lse != nullptr && d == 0) lse[token * q_heads + head] = l > 0.0f ? mx + log2f(l) : -INFINITY;
 }
 
@@ -2126,10 +2143,11 @@ __device__ __forceinline__ void PrefillMergeRows(uint16_t* __restrict__ out, flo
   };
   if constexpr (kRows > 1) {  // merges of exactly two pieces
     float2 ml[kRows][2];
-    u32x2_t o[kRows][2];
+    u32x2_t o[kRows][2], gw[kRows];
 #pragma unroll
     for (int j = 0; j < kRows; ++j) {
       const int r = min(r0 + j, mg.rows - 1);  // rows past the item's end re-read its last row and are not written
+      gw[j] = GateFetch2(gate, ((tok0 + r) * q_heads + head) * D + d);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         ml[j][i] = *reinterpret_cast<const float2*>(part_ml + 2 * prow(i, r));
@@ -2152,9 +2170,10 @@ __device__ __forceinline__ void PrefillMergeRows(uint16_t* __restrict__ out, flo
           MergeAdd(acc, o[j][i], f);
         }
       }
-      MergeWrite<D>(out, lse, gate, tok0 + r0 + j, q_heads, head, d, acc, l, mx);
+      MergeWrite<D>(out, lse, gate, gw[j], tok0 + r0 + j, q_heads, head, d, acc, l, mx);
     }
   } else {  // any count, one token row per block; the piece loops are unrolled so several pieces' loads are in flight
+    const u32x2_t gw = GateFetch2(gate, ((tok0 + r0) * q_heads + head) * D + d);
     float mx = -INFINITY;
 #pragma unroll 8
     for (int i = 0; i < mg.count; ++i) mx = fmaxf(mx, part_ml[2 * prow(i, r0)]);
@@ -2169,7 +2188,7 @@ __device__ __forceinline__ void PrefillMergeRows(uint16_t* __restrict__ out, flo
         MergeAdd(acc, *reinterpret_cast<const u32x2_t*>(part_o + prow(i, r0) * D + d), f);
       }
     }
-    MergeWrite<D>(out, lse, gate, tok0 + r0, q_heads, head, d, acc, l, mx);
+    MergeWrite<D>(out, lse, gate, gw, tok0 + r0, q_heads, head, d, acc, l, mx);
   }
 }
 
