@@ -254,6 +254,21 @@ __device__ __forceinline__ void LoadWords(const void* p, uint32_t* w) {
     w[0] = *static_cast<const uint32_t*>(p);
   }
 }
+// The same with the non-temporal hint, for rows read once in whole lines (the tiled convolution's input stream).
+template <int kBytes>
+__device__ __forceinline__ void LoadWordsNt(const void* p, uint32_t* w) {
+  typedef uint32_t v4 __attribute__((ext_vector_type(4)));
+  typedef uint32_t v2 __attribute__((ext_vector_type(2)));
+  if constexpr (kBytes == 16) {
+    const v4 q = __builtin_nontemporal_load(static_cast<const v4*>(p));
+    w[0] = q[0]; w[1] = q[1]; w[2] = q[2]; w[3] = q[3];
+  } else if constexpr (kBytes == 8) {
+    const v2 q = __builtin_nontemporal_load(static_cast<const v2*>(p));
+    w[0] = q[0]; w[1] = q[1];
+  } else {
+    w[0] = __builtin_nontemporal_load(static_cast<const uint32_t*>(p));
+  }
+}
 template <int kBytes>
 __device__ __forceinline__ void StoreWords(void* p, const uint32_t* w) {
   if constexpr (kBytes == 16) {
@@ -359,10 +374,12 @@ __global__ void __launch_bounds__(256) ConvTileKernel(ConvArgs a, uint32_t cbloc
   if (t_begin >= s0 && t_end <= s1) {
     // The whole tile lies in one sequence (every tile but those at sequence boundaries): one window load, then a
     // straight-line slide over the tile's rows, the next kConvChunk rows requested before the current ones are computed.
+    // The rows stream in with the non-temporal hint (Qwen3.5's [16384, 6144] projection: 74.6 against 86.0 us); the
+    // window's halo rows, which the tile before also reads, keep plain loads.
     auto fetch = [&](int32_t t0, uint32_t (*r)[kWords]) {
 #pragma unroll
       for (int i = 0; i < kConvChunk; ++i) {
-        LoadWords<kBytes>(x + static_cast<uint64_t>(min(t0 + i, t_end - 1)) * a.channels + c0, r[i]);
+        LoadWordsNt<kBytes>(x + static_cast<uint64_t>(min(t0 + i, t_end - 1)) * a.channels + c0, r[i]);
       }
     };
     uint32_t rows[kConvChunk][kWords], next[kConvChunk][kWords];
