@@ -19,6 +19,10 @@ RoostStatus ConvStateUpdate(const RoostCausalConv1dParams& p, hipStream_t s, con
 // the call with its single-pass kernel (one 16-byte vector per lane covers a row).
 RoostStatus AdmitNorm(const RoostGatedRmsNormParams& p, const char* op, bool* row_form);
 
+// The launches of an admitted GatedRmsNorm call, reported under `op`. stream_input: the single-pass kernel reads its
+// input and gate rows with the non-temporal hint (the chunk layer, whose norm input the scan stored past the caches).
+RoostStatus RunNorm(const RoostGatedRmsNormParams& p, hipStream_t s, bool stream_input, const char* op);
+
 }  // namespace roost_layer
 
 #endif  // ROOST_AMD_GDN_LAYER_H_

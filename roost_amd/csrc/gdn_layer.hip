@@ -119,7 +119,22 @@ __global__ void __launch_bounds__(256) GatedRmsNormKernel(const T* __restrict__ 
 // arithmetic, keeps the row in registers (x is read once) and loads its kV weights once for all kR rows.
 constexpr int kRmsRows = 4;
 
-template <typename T, int kR>
+// The same with the non-temporal hint, for rows read once in whole lines (the tiled convolution's input stream).
+template <int kBytes>
+__device__ __forceinline__ void LoadWordsNt(const void* p, uint32_t* w) {
+  typedef uint32_t v4 __attribute__((ext_vector_type(4)));
+  typedef uint32_t v2 __attribute__((ext_vector_type(2)));
+  if constexpr (kBytes == 16) {
+    const v4 q = __builtin_nontemporal_load(static_cast<const v4*>(p));
+    w[0] = q[0]; w[1] = q[1]; w[2] = q[2]; w[3] = q[3];
+  } else if constexpr (kBytes == 8) {
+    const v2 q = __builtin_nontemporal_load(static_cast<const v2*>(p));
+    w[0] = q[0]; w[1] = q[1];
+  } else {
+    w[0] = __builtin_nontemporal_load(static_cast<const uint32_t*>(p));
+  }
+}
+template <typename T, int kR, bool kStream = false>
 __global__ void __launch_bounds__(256) GatedRmsNormRowKernel(const T* __restrict__ x, const T* __restrict__ gate,
                                                              const void* __restrict__ weight, uint32_t w_t,
                                                              T* __restrict__ out, uint64_t rows, uint32_t dim,
@@ -136,8 +151,16 @@ __global__ void __launch_bounds__(256) GatedRmsNormRowKernel(const T* __restrict
   for (int r = 0; r < kR; ++r) {
     const uint64_t row = row0 + r * rows_per_pass;
     const uint64_t at = (row < rows ? row : 0) * dim + col;
-    xq[r] = *reinterpret_cast<const uint4*>(x + at);
-    gq[r] = *reinterpret_cast<const uint4*>(gate + at);
+    if constexpr (kStream) {  // both streams read once, past the caches
+      uint32_t t[4];
+      LoadWordsNt<16>(x + at, t);
+      xq[r] = make_uint4(t[0], t[1], t[2], t[3]);
+      LoadWordsNt<16>(gate + at, t);
+      gq[r] = make_uint4(t[0], t[1], t[2], t[3]);
+    } else {
+      xq[r] = *reinterpret_cast<const uint4*>(x + at);
+      gq[r] = *reinterpret_cast<const uint4*>(gate + at);
+    }
   }
   float wv[kV];
   if (w_t == ROOST_DTYPE_F32 && (reinterpret_cast<uintptr_t>(weight) & 15) == 0) {
@@ -252,21 +275,6 @@ __device__ __forceinline__ void LoadWords(const void* p, uint32_t* w) {
     w[0] = q.x; w[1] = q.y;
   } else {
     w[0] = *static_cast<const uint32_t*>(p);
-  }
-}
-// The same with the non-temporal hint, for rows read once in whole lines (the tiled convolution's input stream).
-template <int kBytes>
-__device__ __forceinline__ void LoadWordsNt(const void* p, uint32_t* w) {
-  typedef uint32_t v4 __attribute__((ext_vector_type(4)));
-  typedef uint32_t v2 __attribute__((ext_vector_type(2)));
-  if constexpr (kBytes == 16) {
-    const v4 q = __builtin_nontemporal_load(static_cast<const v4*>(p));
-    w[0] = q[0]; w[1] = q[1]; w[2] = q[2]; w[3] = q[3];
-  } else if constexpr (kBytes == 8) {
-    const v2 q = __builtin_nontemporal_load(static_cast<const v2*>(p));
-    w[0] = q[0]; w[1] = q[1];
-  } else {
-    w[0] = __builtin_nontemporal_load(static_cast<const uint32_t*>(p));
   }
 }
 template <int kBytes>
@@ -829,6 +837,53 @@ RoostStatus roost_layer::AdmitNorm(const RoostGatedRmsNormParams& p, const char*
   return ROOST_STATUS_OK;
 }
 
+namespace roost_layer {
+
+RoostStatus RunNorm(const RoostGatedRmsNormParams& p, hipStream_t s, bool stream_input, const char* kOp) {
+  if (p.rows == 0) return ROOST_STATUS_OK;
+  const uint32_t act = p.input.dtype;
+  const NormShape f = NormForm(p);
+  const bool vec = f.vec, single = f.single;
+  const uint32_t lanes = f.lanes;
+  const uint64_t rows_per_block = 4ull * (64 / lanes);
+  const dim3 grid(Blocks(p.rows, static_cast<uint32_t>(rows_per_block)));
+  const dim3 row_grid(Blocks(p.rows, static_cast<uint32_t>(rows_per_block * kRmsRows)));
+  if (act == ROOST_DTYPE_BF16) {
+    const auto* x = static_cast<const uint16_t*>(p.input.address);
+    const auto* g = static_cast<const uint16_t*>(p.gate.address);
+    auto* o = static_cast<uint16_t*>(p.output.address);
+    if (single) {
+      auto* k = stream_input ? GatedRmsNormRowKernel<uint16_t, kRmsRows, true>
+                             : GatedRmsNormRowKernel<uint16_t, kRmsRows, false>;
+      hipLaunchKernelGGL(k, row_grid, dim3(256), 0, s, x, g, p.weight.address, p.weight.dtype, o, uint64_t{p.rows},
+                         p.dim, lanes, p.eps);
+    } else if (vec) {
+      hipLaunchKernelGGL((GatedRmsNormKernel<uint16_t, true>), grid, dim3(256), 0, s, x, g, p.weight.address,
+                         p.weight.dtype, o, uint64_t{p.rows}, p.dim, lanes, p.eps);
+    } else {
+      hipLaunchKernelGGL((GatedRmsNormKernel<uint16_t, false>), grid, dim3(256), 0, s, x, g, p.weight.address,
+                         p.weight.dtype, o, uint64_t{p.rows}, p.dim, lanes, p.eps);
+    }
+  } else {
+    const auto* x = static_cast<const float*>(p.input.address);
+    const auto* g = static_cast<const float*>(p.gate.address);
+    auto* o = static_cast<float*>(p.output.address);
+    if (single) {
+      hipLaunchKernelGGL((GatedRmsNormRowKernel<float, kRmsRows>), row_grid, dim3(256), 0, s, x, g,
+                         p.weight.address, p.weight.dtype, o, uint64_t{p.rows}, p.dim, lanes, p.eps);
+    } else if (vec) {
+      hipLaunchKernelGGL((GatedRmsNormKernel<float, true>), grid, dim3(256), 0, s, x, g, p.weight.address,
+                         p.weight.dtype, o, uint64_t{p.rows}, p.dim, lanes, p.eps);
+    } else {
+      hipLaunchKernelGGL((GatedRmsNormKernel<float, false>), grid, dim3(256), 0, s, x, g, p.weight.address,
+                         p.weight.dtype, o, uint64_t{p.rows}, p.dim, lanes, p.eps);
+    }
+  }
+  return roost::HipStatus(hipGetLastError(), kOp, "kernel launch");
+}
+
+}  // namespace roost_layer
+
 extern "C" ROOST_API RoostStatus roost_gated_rms_norm_run(RoostContext* ctx, const void* params, const RoostWorkspace*,
                                                            void* stream) {
   constexpr char kOp[] = "gated_rms_norm";
@@ -838,45 +893,7 @@ extern "C" ROOST_API RoostStatus roost_gated_rms_norm_run(RoostContext* ctx, con
   const auto& p = *pp;
   return roost::CatchAll(kOp, [&]() -> RoostStatus {
     ROOST_RETURN_IF_FAILED(roost_layer::AdmitNorm(p, kOp, nullptr));
-    if (p.rows == 0) return ROOST_STATUS_OK;
-    const uint32_t act = p.input.dtype;
-    const NormShape f = NormForm(p);
-    const bool vec = f.vec, single = f.single;
-    const uint32_t lanes = f.lanes;
-    const uint64_t rows_per_block = 4ull * (64 / lanes);
-    const dim3 grid(Blocks(p.rows, static_cast<uint32_t>(rows_per_block)));
-    const dim3 row_grid(Blocks(p.rows, static_cast<uint32_t>(rows_per_block * kRmsRows)));
-    hipStream_t s = roost::Stream(stream);
-    if (act == ROOST_DTYPE_BF16) {
-      const auto* x = static_cast<const uint16_t*>(p.input.address);
-      const auto* g = static_cast<const uint16_t*>(p.gate.address);
-      auto* o = static_cast<uint16_t*>(p.output.address);
-      if (single) {
-        hipLaunchKernelGGL((GatedRmsNormRowKernel<uint16_t, kRmsRows>), row_grid, dim3(256), 0, s, x, g,
-                           p.weight.address, p.weight.dtype, o, uint64_t{p.rows}, p.dim, lanes, p.eps);
-      } else if (vec) {
-        hipLaunchKernelGGL((GatedRmsNormKernel<uint16_t, true>), grid, dim3(256), 0, s, x, g, p.weight.address,
-                           p.weight.dtype, o, uint64_t{p.rows}, p.dim, lanes, p.eps);
-      } else {
-        hipLaunchKernelGGL((GatedRmsNormKernel<uint16_t, false>), grid, dim3(256), 0, s, x, g, p.weight.address,
-                           p.weight.dtype, o, uint64_t{p.rows}, p.dim, lanes, p.eps);
-      }
-    } else {
-      const auto* x = static_cast<const float*>(p.input.address);
-      const auto* g = static_cast<const float*>(p.gate.address);
-      auto* o = static_cast<float*>(p.output.address);
-      if (single) {
-        hipLaunchKernelGGL((GatedRmsNormRowKernel<float, kRmsRows>), row_grid, dim3(256), 0, s, x, g,
-                           p.weight.address, p.weight.dtype, o, uint64_t{p.rows}, p.dim, lanes, p.eps);
-      } else if (vec) {
-        hipLaunchKernelGGL((GatedRmsNormKernel<float, true>), grid, dim3(256), 0, s, x, g, p.weight.address,
-                           p.weight.dtype, o, uint64_t{p.rows}, p.dim, lanes, p.eps);
-      } else {
-        hipLaunchKernelGGL((GatedRmsNormKernel<float, false>), grid, dim3(256), 0, s, x, g, p.weight.address,
-                           p.weight.dtype, o, uint64_t{p.rows}, p.dim, lanes, p.eps);
-      }
-    }
-    return roost::HipStatus(hipGetLastError(), kOp, "kernel launch");
+    return roost_layer::RunNorm(p, roost::Stream(stream), false, kOp);
   });
 }
 
