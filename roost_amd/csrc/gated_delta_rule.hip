@@ -2324,10 +2324,12 @@ extern "C" ROOST_API RoostStatus roost_amd_gdn_chunk_layer_run(RoostContext* ctx
     // The convolution (with its state update; the GDN kernels do not read the convolution's state), the chunk kernels
     // with the gates computed where they are read, then the norm, all on the caller's stream.
     ROOST_RETURN_IF_FAILED(roost_causal_conv1d_run(ctx, conv_params, nullptr, stream));
-    if (stamp.chunks > 0) ROOST_RETURN_IF_FAILED(LaunchChunk(p, ws, l, stamp.chunks, roost::Stream(stream), false, false, lv.gs));
+    if (stamp.chunks > 0) {
+      ROOST_RETURN_IF_FAILED(LaunchChunk(p, ws, l, stamp.chunks, roost::Stream(stream), false, false, lv.gs));
+    }
     // The norm's input is normally the scan's output, which the scan stores past the caches: the norm streams it and
-    // its gate in the same way (config 4's layer: 0.286-0.287 against 0.289 ms; the standalone op keeps plain loads, which
-    // are faster when its inputs are still cached).
+    // its gate in the same way (config 4's layer: 0.286-0.287 against 0.289 ms; the standalone op keeps plain loads,
+    // which are faster when its inputs are still cached).
     return roost_layer::RunNorm(np, roost::Stream(stream), true, kLayerOp);
   });
 }
