@@ -2366,11 +2366,8 @@ RoostStatus LaunchMixed(const RoostPagedAttentionParams& p, const PlanRecord& re
   const uint64_t blocks = uint64_t{pm.blocks} + rec.dec_merges * p.q_heads;
   if (blocks == 0) return ROOST_STATUS_OK;
   const dim3 g(static_cast<uint32_t>(blocks)), block(p.head_dim);
-  switch (p.head_dim) {
-    case 64: hipLaunchKernelGGL(MixedMergeKernel<64>, g, block, 0, stream, outp, lsep, pm, dm, p.q_heads, kv.out_gate); break;
-    case 128: hipLaunchKernelGGL(MixedMergeKernel<128>, g, block, 0, stream, outp, lsep, pm, dm, p.q_heads, kv.out_gate); break;
-    default: hipLaunchKernelGGL(MixedMergeKernel<256>, g, block, 0, stream, outp, lsep, pm, dm, p.q_heads, kv.out_gate); break;
-  }
+  auto* merge = p.head_dim == 64 ? MixedMergeKernel<64> : p.head_dim == 128 ? MixedMergeKernel<128> : MixedMergeKernel<256>;
+  hipLaunchKernelGGL(merge, g, block, 0, stream, outp, lsep, pm, dm, p.q_heads, kv.out_gate);
   return roost::HipStatus(hipGetLastError(), "paged_attention", "mixed merge launch");
 }
 
