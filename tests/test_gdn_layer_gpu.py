@@ -235,6 +235,21 @@ def test_causal_conv1d_one_call_equals_token_calls(session):
     assert np.array_equal(from_dev(st_a, True)[:ch * (width - 1)], init[:ch * (width - 1)])  # slot 0 untouched
 
 
+@pytest.mark.parametrize("slot_bytes,count", [(65536, 40), (4096, 600), (6, 40)])
+def test_state_copy_long_chains_match_oracle(session, slot_bytes, count):
+    """Many pairs over few slots: chains where a pair reads what an earlier one (adjacent or not) wrote and self
+    copies, against the oracle's in-order byte copies; 600 pairs cross the kernel's 512-pair batch."""
+    rng = np.random.default_rng(count + slot_bytes)
+    slots = 6
+    pool = rng.integers(0, 256, slots * slot_bytes, dtype=np.uint8)
+    pairs = rng.integers(0, slots, 2 * count).astype(np.int32)
+    want = pool.copy()
+    oracle.state_copy(want, pairs, slot_bytes=slot_bytes)
+    d = to_dev(pool)
+    roost_amd.recurrent_state_copy(session, d, to_dev(pairs), slot_bytes=slot_bytes, count=count)
+    assert np.array_equal(from_dev(d), want)
+
+
 @pytest.mark.parametrize("slot_bytes", [8, 6, 65536])
 def test_state_copy_and_snapshot_bit_exact(session, slot_bytes):
     """Ordered pair copies (a later pair sees an earlier pair's write), NaN and -0 bit patterns kept; 16-byte, word and
