@@ -119,7 +119,8 @@ __global__ void __launch_bounds__(256) GatedRmsNormKernel(const T* __restrict__ 
 // arithmetic, keeps the row in registers (x is read once) and loads its kV weights once for all kR rows.
 constexpr int kRmsRows = 4;
 
-// The same with the non-temporal hint, for rows read once in whole lines (the tiled convolution's input stream).
+// LoadWords with the non-temporal hint, for rows read once in whole lines (the tiled convolution's input rows, the
+// chunk layer's norm inputs).
 template <int kBytes>
 __device__ __forceinline__ void LoadWordsNt(const void* p, uint32_t* w) {
   typedef uint32_t v4 __attribute__((ext_vector_type(4)));
@@ -839,7 +840,7 @@ RoostStatus roost_layer::AdmitNorm(const RoostGatedRmsNormParams& p, const char*
 
 namespace roost_layer {
 
-RoostStatus RunNorm(const RoostGatedRmsNormParams& p, hipStream_t s, bool stream_input, const char* kOp) {
+RoostStatus RunNorm(const RoostGatedRmsNormParams& p, hipStream_t s, bool stream_input, const char* op) {
   if (p.rows == 0) return ROOST_STATUS_OK;
   const uint32_t act = p.input.dtype;
   const NormShape f = NormForm(p);
@@ -869,8 +870,10 @@ RoostStatus RunNorm(const RoostGatedRmsNormParams& p, hipStream_t s, bool stream
     const auto* g = static_cast<const float*>(p.gate.address);
     auto* o = static_cast<float*>(p.output.address);
     if (single) {
-      hipLaunchKernelGGL((GatedRmsNormRowKernel<float, kRmsRows>), row_grid, dim3(256), 0, s, x, g,
-                         p.weight.address, p.weight.dtype, o, uint64_t{p.rows}, p.dim, lanes, p.eps);
+      auto* k = stream_input ? GatedRmsNormRowKernel<float, kRmsRows, true>
+                             : GatedRmsNormRowKernel<float, kRmsRows, false>;
+      hipLaunchKernelGGL(k, row_grid, dim3(256), 0, s, x, g, p.weight.address, p.weight.dtype, o, uint64_t{p.rows},
+                         p.dim, lanes, p.eps);
     } else if (vec) {
       hipLaunchKernelGGL((GatedRmsNormKernel<float, true>), grid, dim3(256), 0, s, x, g, p.weight.address,
                          p.weight.dtype, o, uint64_t{p.rows}, p.dim, lanes, p.eps);
@@ -879,7 +882,7 @@ RoostStatus RunNorm(const RoostGatedRmsNormParams& p, hipStream_t s, bool stream
                          p.weight.dtype, o, uint64_t{p.rows}, p.dim, lanes, p.eps);
     }
   }
-  return roost::HipStatus(hipGetLastError(), kOp, "kernel launch");
+  return roost::HipStatus(hipGetLastError(), op, "kernel launch");
 }
 
 }  // namespace roost_layer
