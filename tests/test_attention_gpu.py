@@ -754,3 +754,37 @@ def test_prefill_long_sequence_sampled_rows(session):
             p = np.exp(s - s.max())
             ref = (p @ v[: t + 1, h // group]) / p.sum()
             cases.assert_close(got[t, h][None], ref[None], what=f"32k prefill row {t} head {h}")
+
+
+def _random_case(rng):
+    """One random paged call: batch 1-6, decode rows (one token) mixed with prefill chunks on random prefixes, head
+    dims 64/128/256, page sizes 7/16/32/64, NHD or HND, causal or not, with or without a window and a soft cap."""
+    d = int(rng.choice([64, 128, 256]))
+    ps = int(rng.choice([16, 32, 64] + ([7] if d == 256 else [])))  # head dims 64 and 128 prefill need the DMA pages
+    batch = int(rng.integers(1, 7))
+    decode = rng.random() < 0.3
+    q_lens = [1 if decode or rng.random() < 0.3 else int(rng.integers(2, 300)) for _ in range(batch)]
+    kv_lens = [q + int(rng.integers(0, 900)) for q in q_lens]
+    causal = bool(rng.random() < 0.7)
+    window = -1 if rng.random() < 0.6 else int(rng.integers(30, 500))
+    cap = 0.0 if rng.random() < 0.7 else float(rng.choice([5.0, 20.0]))
+    return dict(d=d, ps=ps, q_lens=q_lens, kv_lens=kv_lens, hnd=bool(rng.random() < 0.5), causal=causal,
+                window=window, cap=cap)
+
+
+@pytest.mark.parametrize("seed", range(64))
+def test_random_attention_calls_match_cpuops(session, seed):
+    """Random combinations of the call's features (decode and prefill rows in one batch, head dims, page sizes, layouts,
+    causal or not, window, soft cap) against CpuOps, with the same bf16 tolerance as the fixed cases."""
+    rng = np.random.default_rng(1000 + seed)
+    c = _random_case(rng)
+    b = cases.make_paged_batch(rng, c["kv_lens"], c["q_lens"], page_size=c["ps"], hnd=c["hnd"], d=c["d"], std=0.5)
+    mode = abi.ATTENTION_DECODE if all(q == 1 for q in c["q_lens"]) else abi.ATTENTION_PREFILL
+    dev = Dev(b, c["causal"], window_left=c["window"], soft_cap=c["cap"])
+    print(f"seed {seed}: {c}", flush=True)
+    session.launch(session.lib.entry(roost_amd.ATTENTION_VARIANT), dev.params(mode=mode), key=("random", seed))
+    got = dev.result()
+    ref = cases.values(cases.oracle_attention(b, c["causal"], window_left=c["window"], soft_cap=c["cap"]), True)
+    cases.assert_close(got, ref, what=f"random attention {seed}")
+    cases.assert_attention_class(got, ref, float(np.abs(cases.values(b.v_cache, True)).max()),
+                                 what=f"random attention {seed}")
