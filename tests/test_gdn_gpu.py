@@ -475,3 +475,81 @@ def test_chunk_long_sequence_two_calls_equal_one(session):
     assert not torch.isnan(out_one.float()).any()
     assert torch.equal(pool_one, pool_two), "final states differ between one call and two"
     assert torch.equal(out_one.view(torch.int16), out_two.view(torch.int16)), "outputs differ between one call and two"
+
+
+# ---- seeded random calls -------------------------------------------------------------------------------------------
+
+def _random_gdn_case(rng):
+    """One call's shape: head counts and groups, fused or separate rows, lengths mixing empty, decode, the 16-token
+    routing edge, chunk edges and long sequences, init, scale, decay distribution and, for the recurrent variant,
+    whether the host copy of cu_seqlens is given (without it the device routes the call itself)."""
+    kh = int(rng.choice([2, 4, 8, 16]))
+    vh = kh * int(rng.choice([1, 2, 4]))
+    pool_lens = [0, 1, 1, 1, 2, 7, 15, 16, 17, 33, 63, 64, 65, 127, 128, 129, 200, 300, 511]
+    lens = [int(rng.choice(pool_lens)) for _ in range(int(rng.integers(1, 9)))]
+    if rng.random() < 0.3:
+        lens = [1] * int(rng.integers(1, 80))  # a decode step
+    c = dict(kh=kh, vh=vh, lens=lens, fused=bool(rng.random() < 0.6), init=bool(rng.random() < 0.8),
+             scale=float(rng.choice([0.0, 0.0, 0.05, 0.3])), baseline_style=bool(rng.random() < 0.5),
+             host_cu=bool(rng.random() < 0.7), variant=VARIANTS[int(rng.integers(0, 2))])
+    if c["variant"] == roost_amd.CHUNK_VARIANT:
+        c["host_cu"] = True  # the chunk variant's plan() reads the host copy
+    return c
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_random_gdn_calls_match_cpuops(session, seed):
+    """Seeded random calls of either variant against CpuOps' GatedDeltaRule (CpuOps.Hybrid.cs:30-157): outputs to the
+    bf16 bar, every owned state slot to the 1e-3 state bar, every other slot untouched."""
+    import torch
+
+    rng = np.random.default_rng(5000 + seed)
+    c = _random_gdn_case(rng)
+    kh, vh, lens = c["kh"], c["vh"], c["lens"]
+    T, B = int(sum(lens)), len(lens)
+    qk_row, v_row = kh * DIM, vh * DIM
+    width = 2 * qk_row + v_row
+    fused = cases.bf16_bits(rng.standard_normal((max(T, 1), width), dtype=np.float32))
+    if c["baseline_style"]:
+        g = (-np.logaddexp(0.0, rng.standard_normal((max(T, 1), vh)))).astype(np.float32)
+        beta = cases.bf16_bits(1.0 / (1.0 + np.exp(-rng.standard_normal((max(T, 1), vh)))))
+    else:
+        g = (-rng.random((max(T, 1), vh)) * 0.2).astype(np.float32)
+        beta = cases.bf16_bits(rng.random((max(T, 1), vh)).astype(np.float32))
+    slots_n = B + 3
+    pool = (rng.standard_normal((slots_n, vh, DIM, DIM), dtype=np.float32) * 0.05).astype(np.float32)
+    slots = rng.permutation(slots_n)[:B].astype(np.int32)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    q, k, v = (np.ascontiguousarray(fused[:, a:b]) for a, b in
+               ((0, qk_row), (qk_row, 2 * qk_row), (2 * qk_row, width)))
+    want_o = np.zeros((max(T, 1), vh, DIM), np.uint16)
+    want_pool = pool.copy()
+    oracle.gated_delta_rule(q, k, v, g, beta, want_o, want_pool, slots, cu, batch=B, tokens=T, k_heads=kh, v_heads=vh,
+                            k_dim=DIM, v_dim=DIM, use_initial_state=c["init"], l2_norm_qk=True, scale=c["scale"],
+                            bf16=True, beta_bf16=True, threads=oracle.host_threads())
+    dpool = to_dev(pool)
+    out = torch.full((max(T, 1), vh, DIM), float("nan"), dtype=torch.bfloat16, device="cuda")
+    common = dict(batch=B, tokens=T, k_heads=kh, v_heads=vh, use_initial_state=c["init"], scale=c["scale"],
+                  cu_seqlens_host=cu if c["host_cu"] else None)
+    if c["fused"]:
+        dfused = to_dev(fused, True)
+        reach_qk = 0 if T == 0 else (T - 1) * width + qk_row
+        reach_v = 0 if T == 0 else (T - 1) * width + v_row
+        p = roost_amd.gated_delta_rule_params(
+            dfused, dfused, dfused, to_dev(g), to_dev(beta, True), out, dpool, to_dev(slots), to_dev(cu),
+            q_stride=width, k_stride=width, v_stride=width, q_len=reach_qk, k_len=reach_qk, v_len=reach_v,
+            q_offset=0, k_offset=qk_row, v_offset=2 * qk_row, **common)
+    else:
+        p = roost_amd.gated_delta_rule_params(to_dev(q, True), to_dev(k, True), to_dev(v, True), to_dev(g),
+                                              to_dev(beta, True), out, dpool, to_dev(slots), to_dev(cu), **common)
+    print(f"seed {seed}: {c}", flush=True)
+    session.launch(session.lib.entry(c["variant"]), p, key=("random", seed))
+    got_o, got_pool = from_dev(out, True)[:T], from_dev(dpool)
+    cases.assert_close(cases.bf16_values(got_o), cases.bf16_values(want_o[:T]), what=f"seed {seed} output")
+    owned = {int(slots[b]) for b in range(B) if lens[b] > 0}
+    for s in range(slots_n):
+        if s in owned:
+            cases.assert_close(got_pool[s], want_pool[s], max_abs=1.0, max_rel=cases.STATE_REL,
+                               what=f"seed {seed} state {s}")
+        else:
+            assert got_pool[s].tobytes() == pool[s].tobytes(), f"seed {seed}: slot {s} was touched"
