@@ -85,8 +85,9 @@ ROOST_API RoostStatus roost_amd_gdn_recurrent_gated_run(RoostContext* ctx, const
 /* One decode step of a Gated DeltaNet layer in one call: CausalConv1d, GatedDeltaRuleGates, the recurrent GatedDeltaRule
  * and GatedRmsNorm. No counterpart in the reference, whose Qwen3.5 worker runs the four ops one after another
  * (Qwen35EagerModel.cs:89-92 lists them; semantics CpuOps.Hybrid.cs:30-157, 160-263 and CpuOps.Gating.cs:21-83). The
- * norm's output, the recurrent states and the convolution states equal the four calls' bit for bit; the convolution's
- * output and the GDN output are not written (their spans are only checked). `conv_params` is a RoostCausalConv1dParams
+ * norm's output, the GDN output, the recurrent states and the convolution states equal the four calls' bit for bit
+ * (sequences that share a state slot run in batch order, as the recurrent variant runs them); the convolution's output
+ * is not written (its span is only checked). `conv_params` is a RoostCausalConv1dParams
  * over bf16 activations with at most 4 taps and the GDN call's batch, tokens and cu_seqlens; `gdn_params` a
  * RoostGatedDeltaRuleParams whose q, k and v are column views of the convolution's output (row stride = channels) and
  * whose cu_seqlens_host is given: every sequence must be shorter than 16 tokens (longer ones run on the chunk kernels in
@@ -104,8 +105,8 @@ ROOST_API RoostStatus roost_amd_gdn_decode_layer_run(RoostContext* ctx, const vo
  * shorter than 16 tokens (known from tokens < 16 or from cu_seqlens_host) with the norm in its single-pass bf16 form
  * runs as roost_amd_gdn_decode_layer_run does; any other step runs the convolution, the recurrent variant with g and
  * beta computed from the gates' inputs (its sequences of 16+ tokens on the chunk kernels) and the norm. The norm's
- * output, the recurrent states and the convolution states equal the four calls' bit for bit (the convolution's and
- * the GDN output are written on the second path only). Params as for roost_amd_gdn_decode_layer_run, without its
+ * output, the recurrent states and the convolution states equal the four calls' bit for bit (the convolution's output
+ * is written on the second path only). Params as for roost_amd_gdn_decode_layer_run, without its
  * length limit; `ws` is the recurrent variant's workspace (roost_gdn_recurrent_workspace of `gdn_params`; NULL is
  * enough when it reports zero bytes). */
 ROOST_API RoostStatus roost_amd_gdn_layer_run(RoostContext* ctx, const void* conv_params, const void* gates_params,

@@ -15,8 +15,8 @@
 // each lane holding 16 floats of S in registers (RecurrentUnit). Sequences of 16 or more tokens go to the chunk (WY)
 // kernels instead; their prep workgroups share one launch with the recurrent ones (WyPrepRecurrentKernel). The gates
 // may be folded in (roost_amd_gdn_recurrent_gated_run): g and beta are then computed where they are read. A decode
-// step of the whole layer -- CausalConv1d, the gates, the recurrence and GatedRmsNorm -- runs as one kernel
-// (GdnDecodeLayerKernel, roost_amd_gdn_decode_layer_run).
+// step of the whole layer -- CausalConv1d, the gates, the recurrence and GatedRmsNorm -- runs as two launches
+// (ConvRecurrentKernel, then the norm with the convolution's state update; roost_amd_gdn_decode_layer_run).
 
 #include <algorithm>
 #include <cmath>
@@ -233,8 +233,8 @@ constexpr uint32_t kRecThreads = 256;
 // 2 lane, 2 lane + 1 (the norms), rows row0 .. + 3 of q and k, the kC columns of v and the token's gates; red_sk and
 // red_o are the [4 wavefronts][8 kC] LDS reduction arrays of the columns' workgroup (two workgroup barriers). Lanes with
 // w == 0 and rg == 0 receive their kC output columns. Every column sees the operations RecurrentUnit applies to it, in
-// the same order (RecurrentUnit keeps its own copy, 4 columns per lane, for its register allocation), so the decode-layer
-// kernel (kC = 16) and the recurrent kernels agree bit for bit.
+// the same order (RecurrentUnit keeps its own copy, for its register allocation), so the decode layer's
+// ConvRecurrentKernel (kC = 4) and the recurrent kernels agree bit for bit.
 template <int kC>
 __device__ __forceinline__ void RecurrentStep(float (&s)[4][kC], const float (&q2)[2], const float (&k2)[2],
                                               const float (&q4)[4], float (&k4)[4], const float (&vv)[kC], float graw,
@@ -603,119 +603,196 @@ RoostStatus LaunchRecurrent(const RoostGatedDeltaRuleParams& p, hipStream_t stre
   return roost::HipStatus(hipGetLastError(), kOp, "recurrent launch");
 }
 
-// ---- Decode layer: CausalConv1d + gates + recurrence + GatedRmsNorm in one kernel ------------------------------------
+// ---- Decode layer: CausalConv1d + gates + recurrence in one kernel, then GatedRmsNorm + the convolution's state ---
 //
-// One workgroup of 512 threads per (sequence, value head), two halves of 4 wavefronts: lane (rg, cg) of wavefront w
-// of half hf holds state rows 32 w + 4 rg .. + 3 of columns 64 hf + 32 m + 4 cg .. + 3, m = 0, 1 (32 floats), and runs
-// RecurrentStep<8> with its half's reduction arrays, which treats each column exactly
-// as the recurrent kernel's RecurrentStep<4> does. The workgroup convolves the token's q, k and v itself from the
-// layer's projection (CausalConv1d's arithmetic: bias, then the taps oldest first with fmaf, SiLU, rounded to bf16),
-// computes the gates where they are read, and normalises the token's 128 outputs (rounded to bf16, as the GDN op
-// stores them) on 16 lanes with GatedRmsNorm's single-pass arithmetic (8 columns per lane, squares summed in column
-// order, then over the lanes by xor 1, 2, 4, 8). The results equal the four ops' bit for bit; neither the
-// convolution's nor the GDN op's output is written. With one value head per key head a workgroup owns the channels it
-// convolves and updates their convolution state itself at the end, as the conv op's state kernel does; with more,
-// value heads share q and k channels, and that state kernel runs afterwards instead.
+// ConvRecurrentKernel (below) runs the recurrent kernel's quarter workgroups with the convolution and the gates
+// computed where the recurrence reads them; one more launch (RunNormAndConvState) normalises the GDN output rows and
+// writes the convolution states. The convolution's output, g and beta never reach memory.
 struct LayerArgs {
-  GdnArgs a;                  // the recurrence; its q, k, v and out are not used
+  GdnArgs a;                  // the recurrence; its q, k and v are not used (the workgroups convolve them)
   const uint16_t* x;          // the convolution's input [tokens, channels] (bf16)
   const uint16_t* conv_w;     // [channels, width]
   const uint16_t* conv_b;     // [channels], or NULL
-  void* conv_state;           // [slots, channels, width - 1]
+  const void* conv_state;     // [slots, channels, width - 1]
   const int32_t* conv_slots;  // [batch]
   uint64_t conv_pool_slots;
   uint32_t conv_state_t, channels, width, silu;
-  uint32_t conv_state_update;  // nonzero: the workgroup updates its channels' convolution state
   uint32_t cq, ck, cv;        // the channels of element 0 of q, k and v head 0
-  const uint16_t* z;          // GatedRmsNorm's gate [tokens * v_heads, 128]
-  const void* norm_w;         // [128]
-  uint32_t norm_w_t;
-  float eps;
-  uint16_t* y;                // GatedRmsNorm's output [tokens * v_heads, 128]
 };
 
-constexpr uint32_t kLayerThreads = 512;
-constexpr int kLayerCols = 8;             // state columns per lane
 constexpr uint32_t kLayerMaxWidth = 4;
-constexpr int kLayerConvPerThread = 1;    // 3 x 128 channels over 512 threads
 
-__global__ void __launch_bounds__(kLayerThreads, 4) GdnDecodeLayerKernel(LayerArgs L) {
+// A float input of dtype bf16 or f32 in two steps, so that the load can be issued early and its value used late: the
+// request keeps the loaded bits as they are (no use of them inside the dtype branch, which would make the request wait
+// for everything in flight before it), and RawToF widens them where they are needed. LoadF's values, bit for bit.
+__device__ __forceinline__ uint32_t RawLoad(const void* p, uint32_t dt, int64_t i) {
+  return dt == ROOST_DTYPE_BF16 ? static_cast<uint32_t>(static_cast<const uint16_t*>(p)[i])
+                                : static_cast<const uint32_t*>(p)[i];
+}
+__device__ __forceinline__ float RawToF(uint32_t r, uint32_t dt) {
+  return dt == ROOST_DTYPE_BF16 ? __uint_as_float(r << 16) : __uint_as_float(r);
+}
+
+// Zeros in device memory: the stand-in a kernel reads for an absent operand, so that its request needs no branch.
+__device__ __align__(16) uint32_t kZeroTaps[4] = {0u, 0u, 0u, 0u};
+
+// GateLoad / GateFrom in the same two steps.
+struct GateRaw {
+  uint32_t r0, r1, r2, r3;
+};
+__device__ __forceinline__ GateRaw GateRequest(const GdnArgs& a, uint64_t tok, uint32_t h) {
+  if (a.gs.a != nullptr) {
+    return GateRaw{RawLoad(a.gs.a, a.gs.a_t, static_cast<int64_t>(tok * a.gs.a_stride + h)),
+                   RawLoad(a.gs.dt_bias, a.gs.dtb_t, h), RawLoad(a.gs.a_log, a.gs.alog_t, h),
+                   RawLoad(a.gs.b, a.gs.b_t, static_cast<int64_t>(tok * a.gs.b_stride + h))};
+  }
+  const uint64_t gi = tok * a.vh + h;
+  return GateRaw{__float_as_uint(a.g[gi]), static_cast<uint32_t>(a.beta[gi]), 0u, 0u};
+}
+__device__ __forceinline__ GateIn GateWiden(const GdnArgs& a, const GateRaw& r) {
+  if (a.gs.a != nullptr) {
+    return GateIn{RawToF(r.r0, a.gs.a_t), RawToF(r.r1, a.gs.dtb_t), RawToF(r.r2, a.gs.alog_t), RawToF(r.r3, a.gs.b_t)};
+  }
+  return GateIn{__uint_as_float(r.r0), __uint_as_float(r.r1 << 16), 0.0f, 0.0f};
+}
+
+// The decode layer's recurrence on the recurrent kernel's quarter workgroups (sequence b, value head h, 32 value
+// columns), with the convolution folded in: per token the workgroup convolves the 288 channels it reads (the key head's
+// 128 q and 128 k channels and its 32 v channels; CausalConv1d's arithmetic: bias, then the taps oldest first with
+// fmaf, SiLU, rounded to bf16) into LDS, then runs RecurrentStep<4> (the recurrent kernel's arithmetic) and writes its
+// 32 output columns as the GDN op rounds them. Sequences sharing a state slot run in batch order, carried by the first one's workgroup, as in RecurrentUnit.
+// Every workgroup reads the old convolution state (the four ops' convolution reads it before its state kernel runs), so
+// the state update and the gated norm run afterwards as their own launches. kW is the convolution's width and CS its
+// state's element type (uint16_t: bf16, or float).
+//
+// A workgroup lives for a few memory round trips, so the first token's operands (taps, weights, bias, gate inputs,
+// the slot-table entries of the sharing scan) are all requested before the state, without a use of any of them in
+// between: the memory counter retires in order, so waiting for one of them then leaves the state's loads in flight.
+template <int kW, typename CS>
+__global__ void __launch_bounds__(kRecThreads) ConvRecurrentKernel(LayerArgs L) {
   const GdnArgs& a = L.a;
-  __shared__ float red_sk[2][4][8 * kLayerCols], red_o[2][4][8 * kLayerCols];
-  __shared__ __align__(16) uint16_t xin[3 * kDim];  // this token's q, k and v, as the convolution rounds them
-  __shared__ __align__(16) uint16_t ob[kDim];       // its outputs, as the GDN op rounds them
-  const uint32_t b = blockIdx.x, h = blockIdx.y;
-  const int32_t t0 = a.cu[b], t1 = a.cu[b + 1];
-  if (t1 <= t0) return;  // an empty sequence leaves its slots untouched
-  const int tid = threadIdx.x, lane = tid & 63, w = (tid >> 6) & 3, hf = tid >> 8;
+  constexpr int kSl = kW - 1;                 // state taps
+  constexpr int kSt = kSl > 0 ? kSl : 1;
+  constexpr int kChans = 2 * kDim + 32;       // channels a workgroup convolves
+  constexpr bool kBf16State = sizeof(CS) == 2;
+  __shared__ float red_sk[4][32], red_o[4][32];
+  __shared__ __align__(16) uint16_t xin[kChans];  // this token's q, k and v columns, as the convolution rounds them
+  __shared__ uint32_t chain_flags;  // bit 0: an earlier sequence shares the slot; bit 1: a later one does
+  const uint32_t b = blockIdx.x, h = blockIdx.y / kRecQuarters, quarter = blockIdx.y % kRecQuarters;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int rg = lane & 7, cg = lane >> 3;
   const int row0 = 32 * w + 4 * rg;
-  const int col = 64 * hf + 4 * cg;  // the lane's first column; group m starts at col + 32 m
+  const uint32_t col = 32 * quarter + 4 * cg;
   const uint32_t kh = h / a.group;
+  int32_t t0 = a.cu[b];
+  int32_t t1 = a.cu[b + 1];
+  if (t1 <= t0) return;  // an empty sequence leaves its slots untouched
   const int32_t slot = a.slots[b];
   const bool has_slot = slot >= 0 && static_cast<uint64_t>(slot) < a.pool_slots;
-  float s[4][kLayerCols] = {};
-  float* sp = has_slot ? a.state + (static_cast<uint64_t>(slot) * a.vh + h) * kDim * kDim + col : nullptr;
-  if (has_slot && a.use_initial_state) LoadStateRows<kLayerCols>(sp, row0, s);
-  // Channel j (0 .. 383) of the token: element j % 128 of q (key head kh), k (key head kh) or v (value head h);
-  // thread tid convolves channels tid and tid + 256.
-  const int sl = static_cast<int>(L.width) - 1;
-  const int32_t cslot = L.conv_slots[b];
-  const bool cslot_ok = cslot >= 0 && static_cast<uint64_t>(cslot) < L.conv_pool_slots;
-  uint32_t cc[kLayerConvPerThread];
-  float cw[kLayerConvPerThread][kLayerMaxWidth] = {}, cb[kLayerConvPerThread] = {};
+  const int32_t cslot0 = L.conv_slots[b];
+  const GateRaw graw0 = GateRequest(a, static_cast<uint64_t>(t0), h);
+  // Channel j of the token: q element j (j < 128), k element j - 128 (j < 256), v column 32 quarter + j - 256; thread
+  // tid convolves channel tid and, for tid < 32, channel 256 + tid (the other threads' second channel repeats their
+  // first, so that every request is in bounds; its result is not stored).
+  uint32_t cc[2];
 #pragma unroll
-  for (int u = 0; u < kLayerConvPerThread; ++u) {
-    const int j = tid + u * static_cast<int>(kLayerThreads), part = j / static_cast<int>(kDim);
-    cc[u] = (part == 0 ? L.cq + kh * kDim : part == 1 ? L.ck + kh * kDim : L.cv + h * kDim) + j % kDim;
-    if (j < 3 * static_cast<int>(kDim)) {
-#pragma unroll
-      for (int k = 0; k < static_cast<int>(kLayerMaxWidth); ++k)
-        if (k < static_cast<int>(L.width)) cw[u][k] = Bf16ToF32(L.conv_w[static_cast<uint64_t>(cc[u]) * L.width + k]);
-      if (L.conv_b != nullptr) cb[u] = Bf16ToF32(L.conv_b[cc[u]]);
-    }
+  for (int u = 0; u < 2; ++u) {
+    const int j = tid < 32 ? tid + 256 * u : tid;
+    cc[u] = j < static_cast<int>(kDim)      ? L.cq + kh * kDim + j
+            : j < 2 * static_cast<int>(kDim) ? L.ck + kh * kDim + (j - kDim)
+                                             : L.cv + h * kDim + 32 * quarter + (j - 2 * kDim);
   }
-  // The norm's weights, requested now (into LDS: registers are at the two-workgroups-per-CU limit) so that their
-  // latency is not paid after the recurrence; the token loop's first barrier publishes them.
-  __shared__ float nws[kDim];
-  if (tid < static_cast<int>(kDim)) nws[tid] = LoadF(L.norm_w, L.norm_w_t, tid);
-  // Taps 1 .. width - 1 of the latest token: after the last one, the channel's new convolution state.
-  float taps[kLayerConvPerThread][kLayerMaxWidth - 1] = {};
-  for (int32_t tok = t0; tok < t1; ++tok) {
-    const int32_t rel = tok - t0;  // entry rel + k of [state, sequence] is tap k of this token
+  // The first token's taps (entry k of [state, sequence] for k < kW: the state's kSl entries, then the token itself).
+  const bool cslot0_ok = cslot0 >= 0 && static_cast<uint64_t>(cslot0) < L.conv_pool_slots;
+  // Absent operands (no bias, a slot outside the pool) are read from kZeroTaps, so that no request sits in a branch.
+  uint16_t rw[2][kW], rb[2], rx[2];
+  CS rs[2][kSt];
 #pragma unroll
-    for (int u = 0; u < kLayerConvPerThread; ++u) {
-      const int j = tid + u * static_cast<int>(kLayerThreads);
-      if (j < 3 * static_cast<int>(kDim)) {
-        float acc = cb[u];
+  for (int u = 0; u < 2; ++u) {
 #pragma unroll
-        for (int k = 0; k < static_cast<int>(kLayerMaxWidth); ++k) {
-          if (k < static_cast<int>(L.width)) {
-            const int32_t hi = rel + k;
-            float tap;
-            if (hi < sl) {
-              tap = cslot_ok ? LoadF(L.conv_state, L.conv_state_t,
-                                     static_cast<int64_t>((static_cast<uint64_t>(cslot) * L.channels + cc[u]) * sl + hi))
-                             : 0.0f;
-            } else {
-              tap = Bf16ToF32(L.x[static_cast<uint64_t>(t0 + hi - sl) * L.channels + cc[u]]);
-            }
-            if (k > 0) taps[u][k - 1] = tap;
-            acc = fmaf(cw[u][k], tap, acc);
+    for (int k = 0; k < kW; ++k) rw[u][k] = L.conv_w[static_cast<uint64_t>(cc[u]) * kW + k];
+    rb[u] = *(L.conv_b != nullptr ? L.conv_b + cc[u] : reinterpret_cast<const uint16_t*>(kZeroTaps));
+    const CS* st = cslot0_ok ? static_cast<const CS*>(L.conv_state) +
+                                   (static_cast<uint64_t>(cslot0) * L.channels + cc[u]) * kSl
+                             : reinterpret_cast<const CS*>(kZeroTaps);
+#pragma unroll
+    for (int k = 0; k < kSl; ++k) rs[u][k] = st[k];
+    rx[u] = L.x[static_cast<uint64_t>(t0) * L.channels + cc[u]];
+  }
+  constexpr int kScanNow = 2;  // slot entries per lane requested up front (128 sequences)
+  int32_t sj[kScanNow];
+#pragma unroll
+  for (int i = 0; i < kScanNow; ++i) sj[i] = a.slots[min(static_cast<uint32_t>(lane + 64 * i), a.batch - 1)];
+  float s[4][4] = {};
+  float* sp = has_slot ? a.state + (static_cast<uint64_t>(slot) * a.vh + h) * kDim * kDim + col : nullptr;
+  if (has_slot && a.use_initial_state) LoadStateRows<4>(sp, row0, s);
+  auto state_tap = [&](CS v) { return kBf16State ? Bf16ToF32(static_cast<uint16_t>(v)) : static_cast<float>(v); };
+  bool scan_pending = has_slot, chained = false, first = true;
+  uint32_t cur = b;  // the sequence whose tokens run now (later members of a chain follow in turn)
+  int32_t cur_t0 = t0;
+  for (int32_t tok = t0;;) {
+    if (first) {  // from the requests above
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        float acc = Bf16ToF32(rb[u]);
+#pragma unroll
+        for (int k = 0; k < kSl; ++k) acc = fmaf(Bf16ToF32(rw[u][k]), state_tap(rs[u][k]), acc);
+        acc = fmaf(Bf16ToF32(rw[u][kSl]), Bf16ToF32(rx[u]), acc);
+        if (u == 0 || tid < 32) xin[tid + 256 * u] = F32ToBf16(L.silu ? SiluF(acc) : acc);
+      }
+    } else {  // a later token, or a later sequence of a chain: entry rel + k of [state, sequence] is tap k (the
+              // weights and bias read again rather than held in registers through the step)
+      const int32_t rel = tok - cur_t0;
+      const int32_t cslot = L.conv_slots[cur];
+      const bool cslot_ok = cslot >= 0 && static_cast<uint64_t>(cslot) < L.conv_pool_slots;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        float acc = L.conv_b != nullptr ? Bf16ToF32(L.conv_b[cc[u]]) : 0.0f;
+#pragma unroll
+        for (int k = 0; k < kW; ++k) {
+          const int32_t hi = rel + k;
+          float tap;
+          if (hi < kSl) {
+            tap = cslot_ok ? state_tap(static_cast<const CS*>(L.conv_state)[(static_cast<uint64_t>(cslot) * L.channels +
+                                                                              cc[u]) * kSl + hi])
+                           : 0.0f;
+          } else {
+            tap = Bf16ToF32(L.x[static_cast<uint64_t>(cur_t0 + hi - kSl) * L.channels + cc[u]]);
           }
+          acc = fmaf(Bf16ToF32(L.conv_w[static_cast<uint64_t>(cc[u]) * kW + k]), tap, acc);
         }
-        xin[j] = F32ToBf16(L.silu ? SiluF(acc) : acc);
+        if (u == 0 || tid < 32) xin[tid + 256 * u] = F32ToBf16(L.silu ? SiluF(acc) : acc);
       }
     }
-    // The norm's gate for this token, requested before the recurrence runs.
-    uint4 zq = make_uint4(0, 0, 0, 0);
-    const uint64_t row = static_cast<uint64_t>(tok) * a.vh + h;
-    if (tid < 16) zq = *reinterpret_cast<const uint4*>(L.z + row * kDim + 8 * tid);
+    if (scan_pending && w == 0) {  // sequences sharing this one's slot (RecurrentUnit's rule), once
+      bool earlier = false, later = false;
+#pragma unroll
+      for (int i = 0; i < kScanNow; ++i) {
+        const uint32_t jj = static_cast<uint32_t>(lane + 64 * i);
+        if (jj < a.batch && jj != b && sj[i] == slot && ChainMember(a, jj, slot)) {
+          earlier |= jj < b;
+          later |= jj > b;
+        }
+      }
+      for (uint32_t jj = static_cast<uint32_t>(lane + 64 * kScanNow); jj < a.batch; jj += 64) {
+        if (jj != b && ChainMember(a, jj, slot)) {
+          earlier |= jj < b;
+          later |= jj > b;
+        }
+      }
+      const uint32_t f = (__any(earlier) ? 1u : 0u) | (__any(later) ? 2u : 0u);
+      if (lane == 0) chain_flags = f;
+    }
     __syncthreads();
+    if (scan_pending) {
+      scan_pending = false;
+      const uint32_t f = chain_flags;
+      if (f & 1u) return;  // nothing written yet; every wavefront of the workgroup leaves here
+      chained = (f & 2u) != 0;
+    }
     const uint16_t* qv = xin;
     const uint16_t* kv = xin + kDim;
-    const uint16_t* vv16 = xin + 2 * kDim;
-    float q2[2], k2[2], q4[4], k4[4], vv[kLayerCols];
+    float q2[2], k2[2], q4[4], k4[4], vv[4];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       q2[i] = Bf16ToF32(qv[2 * lane + i]);
@@ -725,71 +802,36 @@ __global__ void __launch_bounds__(kLayerThreads, 4) GdnDecodeLayerKernel(LayerAr
     for (int i = 0; i < 4; ++i) {
       q4[i] = Bf16ToF32(qv[row0 + i]);
       k4[i] = Bf16ToF32(kv[row0 + i]);
+      vv[i] = Bf16ToF32(xin[2 * kDim + 4 * cg + i]);
     }
-#pragma unroll
-    for (int c = 0; c < kLayerCols; ++c) vv[c] = Bf16ToF32(vv16[col + 8 * (c & ~3) + (c & 3)]);
+    const GateIn gin = GateWiden(a, first ? graw0 : GateRequest(a, static_cast<uint64_t>(tok), h));
+    first = false;
     float graw, beta;
-    GateAt(a, static_cast<uint64_t>(tok), h, graw, beta);
-    float ot[kLayerCols];
-    RecurrentStep<kLayerCols>(s, q2, k2, q4, k4, vv, graw, beta, a.scale, w, rg, cg, red_sk[hf], red_o[hf], ot);
-    // After the last token the state is final: its stores go out now, in flight during the norm.
-    if (has_slot && tok + 1 == t1) StoreStateRows<kLayerCols>(sp, row0, s);
+    GateFrom(a, gin, graw, beta);
+    float ot[4];
+    RecurrentStep<4>(s, q2, k2, q4, k4, vv, graw, beta, a.scale, w, rg, cg, red_sk, red_o, ot);
     if (w == 0 && rg == 0) {
-#pragma unroll
-      for (int c = 0; c < kLayerCols; c += 4) {
-        *reinterpret_cast<uint2*>(&ob[col + 8 * c]) =
-            make_uint2(PackBf16(ot[c], ot[c + 1]), PackBf16(ot[c + 2], ot[c + 3]));
-      }
+      uint2 pw;
+      pw.x = PackBf16(ot[0], ot[1]);
+      pw.y = PackBf16(ot[2], ot[3]);
+      *reinterpret_cast<uint2*>(a.out + (static_cast<uint64_t>(tok) * a.vh + h) * kDim + col) = pw;
     }
-    __syncthreads();
-    if (tid < 16) {  // the norm of row (tok, h): lane tid holds columns 8 tid .. 8 tid + 7
-      const int c0 = 8 * tid;
-      const uint4 xq = *reinterpret_cast<const uint4*>(&ob[c0]);
-      const uint32_t* xw = reinterpret_cast<const uint32_t*>(&xq);
-      const uint32_t* zw = reinterpret_cast<const uint32_t*>(&zq);
-      float xv[8], gv[8];
+    if (++tok < t1) continue;
+    if (!chained) break;
+    uint32_t next = cur + 1;
+    while (next < a.batch && !ChainMember(a, next, slot)) ++next;
+    if (next >= a.batch) break;
+    cur = next;
+    cur_t0 = tok = a.cu[cur];
+    t1 = a.cu[cur + 1];
+    if (!a.use_initial_state) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        xv[e] = (e & 1) ? Bf16HiToF32(xw[e >> 1]) : Bf16LoToF32(xw[e >> 1]);
-        gv[e] = (e & 1) ? Bf16HiToF32(zw[e >> 1]) : Bf16LoToF32(zw[e >> 1]);
-      }
-      float ss = 0.0f;
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ss = fmaf(xv[e], xv[e], ss);
-#pragma unroll
-      for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, 64);
-      const float inv = rsqrtf(ss / static_cast<float>(kDim) + L.eps);
-      uint32_t yw[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float y0 = xv[2 * q] * inv * nws[c0 + 2 * q] * SiluF(gv[2 * q]);
-        const float y1 = xv[2 * q + 1] * inv * nws[c0 + 2 * q + 1] * SiluF(gv[2 * q + 1]);
-        yw[q] = PackBf16Rne(y0, y1);
-      }
-      *reinterpret_cast<uint4*>(L.y + row * kDim + c0) = make_uint4(yw[0], yw[1], yw[2], yw[3]);
+        for (int c = 0; c < 4; ++c) s[i][c] = 0.f;
     }
   }
-  if (L.conv_state_update != 0 && cslot_ok && sl > 0) {
-    // The slot keeps the last width - 1 entries of [state, sequence], entries n .. n + width - 2: taps 1 .. width - 1
-    // of the last token, already in registers (values as read: bf16 inputs and state entries widen exactly). The one
-    // thread that owns the channel read every old entry before this write.
-#pragma unroll
-    for (int u = 0; u < kLayerConvPerThread; ++u) {
-      const int j = tid + u * static_cast<int>(kLayerThreads);
-      if (j >= 3 * static_cast<int>(kDim)) continue;
-      const uint64_t so = (static_cast<uint64_t>(cslot) * L.channels + cc[u]) * sl;
-#pragma unroll
-      for (int e = 0; e < static_cast<int>(kLayerMaxWidth) - 1; ++e) {
-        if (e < sl) {
-          if (L.conv_state_t == ROOST_DTYPE_BF16) {
-            static_cast<uint16_t*>(L.conv_state)[so + e] = F32ToBf16(taps[u][e]);
-          } else {
-            static_cast<float*>(L.conv_state)[so + e] = taps[u][e];
-          }
-        }
-      }
-    }
-  }
+  if (has_slot) StoreStateRows<4>(sp, row0, s);
 }
 
 // ---- Chunk variant: WY form on MFMA ---------------------------------------------------------------------------------
@@ -1957,14 +1999,13 @@ extern "C" ROOST_API RoostStatus roost_amd_gdn_recurrent_gated_run(RoostContext*
 }
 
 // CausalConv1d + GatedDeltaRuleGates + the recurrent GatedDeltaRule + GatedRmsNorm of one decode step in two launches
-// (GdnDecodeLayerKernel, then the convolution's state update): the four ops' results bit for bit.
+// (ConvRecurrentKernel, then the norm with the convolution's state update): the four ops' results bit for bit.
 namespace {
 
 // What the two layer calls (decode and chunk) read from their four params structs once admitted.
 struct LayerViews {
   GateSource gs;
   uint32_t cq = 0, ck = 0, cv = 0;  // first channel of the q, k and v columns in the convolution's output rows
-  bool tiled = false;               // q, k and v tile the channels without overlap
   bool row_form = false;            // the norm runs on GatedRmsNorm's single-pass bf16 form
   bool empty = false;               // no sequence has a token: nothing is read or written
 };
@@ -2050,16 +2091,11 @@ RoostStatus AdmitLayer(const char* op, const RoostCausalConv1dParams& cp, const 
                                                                                             : cp.conv_state.dtype));
   clear("the recurrent state", p.state.address, p.state.length * 4);
   ROOST_GATE_RETURN(gate);
-  const uint64_t qk = uint64_t{p.k_heads} * kDim, vw = uint64_t{p.v_heads} * kDim;
-  auto apart = [](uint64_t a, uint64_t na, uint64_t b, uint64_t nb) { return a + na <= b || b + nb <= a; };
-  v->tiled = apart(v->cq, qk, v->ck, qk) && apart(v->cq, qk, v->cv, vw) && apart(v->ck, qk, v->cv, vw) &&
-             2 * qk + vw == ch;
   return ROOST_STATUS_OK;
 }
 
 // The decode layer's launch for an admitted call whose sequences are all shorter than kRouteMinTokens and whose norm
-// is the single-pass bf16 form: GdnDecodeLayerKernel, then the convolution's state kernel unless the workgroups
-// updated their channels' state themselves.
+// is the single-pass bf16 form: ConvRecurrentKernel, then the norm and the convolution's state update.
 RoostStatus LaunchDecodeLayer(const char* op, const RoostCausalConv1dParams& cp, const RoostGatedDeltaRuleParams& p,
                               const RoostGatedRmsNormParams& np, const LayerViews& lv, hipStream_t s) {
   const uint64_t sl = cp.width - 1ull;
@@ -2078,17 +2114,20 @@ RoostStatus LaunchDecodeLayer(const char* op, const RoostCausalConv1dParams& cp,
   L.channels = cp.channels;
   L.width = cp.width;
   L.silu = cp.silu != 0 ? 1u : 0u;
-  // One value head per key head, and q, k and v tiling the channels without overlap: each channel belongs to exactly
-  // one workgroup, which updates its state itself. Otherwise the conv op's state kernel runs afterwards.
-  L.conv_state_update = p.v_heads == p.k_heads && lv.tiled ? 1u : 0u;
-  L.z = static_cast<const uint16_t*>(np.gate.address);
-  L.norm_w = np.weight.address;
-  L.norm_w_t = np.weight.dtype;
-  L.eps = np.eps;
-  L.y = static_cast<uint16_t*>(np.output.address);
-  hipLaunchKernelGGL(GdnDecodeLayerKernel, dim3(p.batch, p.v_heads), dim3(kLayerThreads), 0, s, L);
+  const dim3 grid(p.batch, p.v_heads * kRecQuarters);
+  const bool bf16_state = L.conv_state_t == ROOST_DTYPE_BF16;
+  switch (cp.width * 2 + (bf16_state ? 1 : 0)) {
+    case 3: hipLaunchKernelGGL((ConvRecurrentKernel<1, uint16_t>), grid, dim3(kRecThreads), 0, s, L); break;
+    case 2: hipLaunchKernelGGL((ConvRecurrentKernel<1, float>), grid, dim3(kRecThreads), 0, s, L); break;
+    case 5: hipLaunchKernelGGL((ConvRecurrentKernel<2, uint16_t>), grid, dim3(kRecThreads), 0, s, L); break;
+    case 4: hipLaunchKernelGGL((ConvRecurrentKernel<2, float>), grid, dim3(kRecThreads), 0, s, L); break;
+    case 7: hipLaunchKernelGGL((ConvRecurrentKernel<3, uint16_t>), grid, dim3(kRecThreads), 0, s, L); break;
+    case 6: hipLaunchKernelGGL((ConvRecurrentKernel<3, float>), grid, dim3(kRecThreads), 0, s, L); break;
+    case 9: hipLaunchKernelGGL((ConvRecurrentKernel<4, uint16_t>), grid, dim3(kRecThreads), 0, s, L); break;
+    default: hipLaunchKernelGGL((ConvRecurrentKernel<4, float>), grid, dim3(kRecThreads), 0, s, L); break;
+  }
   ROOST_RETURN_IF_FAILED(roost::HipStatus(hipGetLastError(), op, "layer launch"));
-  return L.conv_state_update != 0 ? ROOST_STATUS_OK : roost_layer::ConvStateUpdate(cp, s, op);
+  return roost_layer::RunNormAndConvState(np, cp, s, op);
 }
 
 }  // namespace
@@ -2129,7 +2168,7 @@ extern "C" ROOST_API RoostStatus roost_amd_gdn_decode_layer_run(RoostContext* ct
 // One GDN layer over the recurrent variant for any step (no reference counterpart; the Qwen3.5 worker runs the four
 // ops one after another, Qwen35EagerModel.cs:89-92, and names the recurrent variant for every length): a step whose
 // sequences are all shorter than kRouteMinTokens, with the norm in its single-pass bf16 form, runs as the decode
-// layer (GdnDecodeLayerKernel); any other step runs the conv op, the recurrent variant with the gates computed where
+// layer (ConvRecurrentKernel, then the norm and the convolution's state); any other step runs the conv op, the recurrent variant with the gates computed where
 // they are read (its longer sequences on the chunk kernels, in `ws`), and the norm op. Either way the results equal
 // the four ops'.
 extern "C" ROOST_API RoostStatus roost_amd_gdn_layer_run(RoostContext* ctx, const void* conv_params,

@@ -23,6 +23,11 @@ RoostStatus AdmitNorm(const RoostGatedRmsNormParams& p, const char* op, bool* ro
 // input and gate rows with the non-temporal hint (the chunk layer, whose norm input the scan stored past the caches).
 RoostStatus RunNorm(const RoostGatedRmsNormParams& p, hipStream_t s, bool stream_input, const char* op);
 
+// RunNorm (input read as cached), then ConvStateUpdate, in one launch where both take their vector forms (a bf16
+// single-pass norm over 128 columns; bf16 input with 2 to 4 taps and 16-byte aligned buffers), else as the two calls.
+RoostStatus RunNormAndConvState(const RoostGatedRmsNormParams& np, const RoostCausalConv1dParams& cp, hipStream_t s,
+                                const char* op);
+
 }  // namespace roost_layer
 
 #endif  // ROOST_AMD_GDN_LAYER_H_

@@ -136,15 +136,15 @@ __device__ __forceinline__ void LoadWordsNt(const void* p, uint32_t* w) {
   }
 }
 template <typename T, int kR, bool kStream = false>
-__global__ void __launch_bounds__(256) GatedRmsNormRowKernel(const T* __restrict__ x, const T* __restrict__ gate,
-                                                             const void* __restrict__ weight, uint32_t w_t,
-                                                             T* __restrict__ out, uint64_t rows, uint32_t dim,
-                                                             uint32_t lanes_per_row, float eps) {
+__device__ __forceinline__ void GatedRmsNormRows(const T* __restrict__ x, const T* __restrict__ gate,
+                                                 const void* __restrict__ weight, uint32_t w_t, T* __restrict__ out,
+                                                 uint64_t rows, uint32_t dim, uint32_t lanes_per_row, float eps,
+                                                 uint32_t block) {
   constexpr int kV = 16 / static_cast<int>(sizeof(T));
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t sub = lane % lanes_per_row;
   const uint64_t rows_per_pass = 4ull * (64 / lanes_per_row);  // rows one pass of the block covers
-  const uint64_t row0 = static_cast<uint64_t>(blockIdx.x) * rows_per_pass * kR +
+  const uint64_t row0 = static_cast<uint64_t>(block) * rows_per_pass * kR +
                         (threadIdx.x >> 6) * (64 / lanes_per_row) + lane / lanes_per_row;
   const uint32_t col = sub * kV;
   uint4 xq[kR], gq[kR];
@@ -197,6 +197,13 @@ __global__ void __launch_bounds__(256) GatedRmsNormRowKernel(const T* __restrict
     const uint64_t row = row0 + r * rows_per_pass;
     if (row < rows) StoreRun<T, true>(out, row * dim + col, y);
   }
+}
+template <typename T, int kR, bool kStream = false>
+__global__ void __launch_bounds__(256) GatedRmsNormRowKernel(const T* __restrict__ x, const T* __restrict__ gate,
+                                                             const void* __restrict__ weight, uint32_t w_t,
+                                                             T* __restrict__ out, uint64_t rows, uint32_t dim,
+                                                             uint32_t lanes_per_row, float eps) {
+  GatedRmsNormRows<T, kR, kStream>(x, gate, weight, w_t, out, rows, dim, lanes_per_row, eps, blockIdx.x);
 }
 
 // ---- SigmoidMul ----------------------------------------------------------------------------------------------------
@@ -604,10 +611,9 @@ __global__ void __launch_bounds__(256) ConvStateKernel(ConvArgs a) {
 // 8 x (width - 1) state entries are contiguous, so they are read and written as 16-byte vectors, and each input row it
 // needs is one vector.
 template <int kW>
-__global__ void __launch_bounds__(256) ConvStateVecKernel(ConvArgs a) {
+__device__ __forceinline__ void ConvStateVecBlock(const ConvArgs& a, uint32_t b, uint32_t by) {
   constexpr int kV = 8, sl = kW - 1;
-  const uint32_t b = blockIdx.x;
-  const uint32_t c0 = (blockIdx.y * blockDim.x + threadIdx.x) * kV;
+  const uint32_t c0 = (by * blockDim.x + threadIdx.x) * kV;
   if (c0 >= a.channels) return;
   const int32_t t0 = a.cu[b], t1 = a.cu[b + 1];
   const int32_t n = t1 - t0;
@@ -664,6 +670,10 @@ __global__ void __launch_bounds__(256) ConvStateVecKernel(ConvArgs a) {
       StoreWords<16>(static_cast<float*>(a.state) + so + 4 * q, qw);
     }
   }
+}
+template <int kW>
+__global__ void __launch_bounds__(256) ConvStateVecKernel(ConvArgs a) {
+  ConvStateVecBlock<kW>(a, blockIdx.x, blockIdx.y);
 }
 
 // ---- Recurrent-state copies ----------------------------------------------------------------------------------------
@@ -1011,6 +1021,22 @@ ConvArgs MakeConvArgs(const RoostCausalConv1dParams& p) {
   return a;
 }
 
+// A layer call's last two steps in one launch: workgroups [0, norm_blocks) run GatedRmsNormRowKernel's rows (bf16,
+// the input read as cached), the rest ConvStateVecKernel's (sequence, channel block) pairs, state_by blocks per
+// sequence. The two touch disjoint memory, so their order within the launch does not matter.
+template <int kW>
+__global__ void __launch_bounds__(256) LayerTailKernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ gate,
+                                                       const void* __restrict__ weight, uint32_t w_t,
+                                                       uint16_t* __restrict__ out, uint64_t rows, uint32_t lanes,
+                                                       float eps, uint32_t norm_blocks, ConvArgs a, uint32_t state_by) {
+  const uint32_t bx = blockIdx.x;
+  if (bx < norm_blocks) {
+    GatedRmsNormRows<uint16_t, kRmsRows, false>(x, gate, weight, w_t, out, rows, 128, lanes, eps, bx);
+  } else {
+    ConvStateVecBlock<kW>(a, (bx - norm_blocks) / state_by, (bx - norm_blocks) % state_by);
+  }
+}
+
 }  // namespace
 
 RoostStatus roost_layer::ConvStateUpdate(const RoostCausalConv1dParams& p, hipStream_t s, const char* op) {
@@ -1030,6 +1056,43 @@ RoostStatus roost_layer::ConvStateUpdate(const RoostCausalConv1dParams& p, hipSt
     hipLaunchKernelGGL(ConvStateKernel, dim3(Blocks(uint64_t{p.batch} * p.channels, 256)), dim3(256), 0, s, a);
   }
   return roost::HipStatus(hipGetLastError(), op, "state update launch");
+}
+
+RoostStatus roost_layer::RunNormAndConvState(const RoostGatedRmsNormParams& np, const RoostCausalConv1dParams& cp,
+                                             hipStream_t s, const char* op) {
+  const NormShape f = NormForm(np);
+  const bool state_vec = cp.batch != 0 && cp.tokens != 0 && cp.width >= 2 && cp.width <= 4 &&
+                         cp.input.dtype == ROOST_DTYPE_BF16 && cp.channels % 8 == 0 &&
+                         roost::IsAligned(cp.input.address, 16) && roost::IsAligned(cp.conv_state.address, 16) &&
+                         cp.channels / 8 <= 65535u * 256u;
+  const bool norm_rows = np.rows != 0 && np.input.dtype == ROOST_DTYPE_BF16 && f.single && np.dim == 128;
+  if (!state_vec || !norm_rows) {
+    ROOST_RETURN_IF_FAILED(RunNorm(np, s, false, op));
+    return ConvStateUpdate(cp, s, op);
+  }
+  const uint64_t rows_per_block = 4ull * (64 / f.lanes) * kRmsRows;
+  const uint64_t norm_blocks = (uint64_t{np.rows} + rows_per_block - 1) / rows_per_block;
+  const uint32_t state_by = Blocks(cp.channels / 8, 256);
+  const uint64_t total = norm_blocks + uint64_t{cp.batch} * state_by;
+  if (total > 0xFFFFFFFFull) {
+    ROOST_RETURN_IF_FAILED(RunNorm(np, s, false, op));
+    return ConvStateUpdate(cp, s, op);
+  }
+  const ConvArgs a = MakeConvArgs(cp);
+  const auto* x = static_cast<const uint16_t*>(np.input.address);
+  const auto* g = static_cast<const uint16_t*>(np.gate.address);
+  auto* o = static_cast<uint16_t*>(np.output.address);
+  const dim3 grid(static_cast<uint32_t>(total));
+  const uint32_t nb = static_cast<uint32_t>(norm_blocks);
+  switch (cp.width) {
+    case 2: hipLaunchKernelGGL(LayerTailKernel<2>, grid, dim3(256), 0, s, x, g, np.weight.address, np.weight.dtype, o,
+                               uint64_t{np.rows}, f.lanes, np.eps, nb, a, state_by); break;
+    case 3: hipLaunchKernelGGL(LayerTailKernel<3>, grid, dim3(256), 0, s, x, g, np.weight.address, np.weight.dtype, o,
+                               uint64_t{np.rows}, f.lanes, np.eps, nb, a, state_by); break;
+    default: hipLaunchKernelGGL(LayerTailKernel<4>, grid, dim3(256), 0, s, x, g, np.weight.address, np.weight.dtype, o,
+                                uint64_t{np.rows}, f.lanes, np.eps, nb, a, state_by); break;
+  }
+  return roost::HipStatus(hipGetLastError(), op, "norm and state launch");
 }
 
 extern "C" ROOST_API RoostStatus roost_causal_conv1d_run(RoostContext* ctx, const void* params, const RoostWorkspace*,

@@ -24,6 +24,10 @@ LAYER_CASES = [
     ("group 2, width 3, unslotted rows", [1] * 10, 8, 16, 3, True, "bf16", True,
      [0, -1, 2, 3, 4, 5, 6, 7, 8, 9], [9, 8, 7, -1, 5, 4, 3, 2, 1, 0]),
     ("width 2, two heads", [2, 1, 4], 2, 2, 2, True, "f32", True, None, None),
+    # Sequences sharing a recurrent state slot run in batch order, as the recurrent variant (and CpuOps) runs them.
+    ("shared state slots in batch order", [1, 3, 0, 1, 2, 1], 4, 8, 4, True, "bf16", True, [3, 3, 3, 1, 3, 1],
+     [0, 1, 2, 3, 4, 5]),
+    ("width 1", [1, 2, 1], 2, 4, 1, False, "bf16", False, None, None),
 ]
 
 
