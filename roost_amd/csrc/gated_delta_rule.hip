@@ -192,6 +192,40 @@ __device__ __forceinline__ void GateAt(const GdnArgs& a, uint64_t tok, uint32_t 
   GateFrom(a, GateLoad(a, tok, h), g, beta);
 }
 
+// Zeros in device memory: the stand-in a kernel reads for an absent operand, so that its request needs no branch.
+__device__ __align__(16) uint32_t kZeroTaps[4] = {0u, 0u, 0u, 0u};
+
+// GateLoad / GateFrom in the same two steps, without a branch around any request: every input is requested both as
+// bf16 and as f32, the form its dtype does not use (and every input of the source not in use) from kZeroTaps, so the
+// two requests' bits combine into the value's f32 bits with one shift and one or. (Requests inside a dtype branch made
+// each wait for everything in flight before it.)
+struct GateRaw {
+  uint32_t h[4], w[4];  // bf16 and f32 requests of a, dt_bias, a_log, b (folded) or of g and beta (read)
+};
+__device__ __forceinline__ GateRaw GateRequest(const GdnArgs& a, uint64_t tok, uint32_t h) {
+  const bool fold = a.gs.a != nullptr;
+  const auto* z16 = reinterpret_cast<const uint16_t*>(kZeroTaps);
+  GateRaw r;
+  auto both = [&](int q, bool use, const void* p, uint32_t dt, uint64_t i) {
+    const bool bf = use && dt == ROOST_DTYPE_BF16, f32 = use && dt != ROOST_DTYPE_BF16;
+    r.h[q] = *(bf ? static_cast<const uint16_t*>(p) + i : z16);
+    r.w[q] = *(f32 ? static_cast<const uint32_t*>(p) + i : kZeroTaps);
+  };
+  const uint64_t gi = tok * a.vh + h;
+  both(0, true, fold ? a.gs.a : a.g, fold ? a.gs.a_t : ROOST_DTYPE_F32, fold ? tok * a.gs.a_stride + h : gi);
+  both(1, true, fold ? a.gs.dt_bias : static_cast<const void*>(a.beta), fold ? a.gs.dtb_t : ROOST_DTYPE_BF16,
+       fold ? h : gi);
+  both(2, fold, a.gs.a_log, a.gs.alog_t, h);
+  both(3, fold, a.gs.b, a.gs.b_t, tok * a.gs.b_stride + h);
+  return r;
+}
+__device__ __forceinline__ GateIn GateWiden(const GdnArgs& a, const GateRaw& r) {
+  float x[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) x[q] = __uint_as_float((r.h[q] << 16) | r.w[q]);
+  return a.gs.a != nullptr ? GateIn{x[0], x[1], x[2], x[3]} : GateIn{x[0], x[1], 0.0f, 0.0f};
+}
+
 typedef float f32x4v_t __attribute__((ext_vector_type(4)));
 
 // The recurrent step reads each state row once and writes it once, in whole 512-byte runs per wavefront: non-temporal
@@ -319,14 +353,15 @@ __device__ __forceinline__ void RecurrentStep(float (&s)[4][kC], const float (&q
 }
 
 // The state rows row0 .. + 3 of a lane's kC columns (groups of 4 at sp + 32 m, row stride kDim), as fp32 streams that
-// skip the caches.
+// skip the caches; zeros (read from kZeroTaps, without a branch) when `valid` is false.
 template <int kC>
-__device__ __forceinline__ void LoadStateRows(const float* sp, int row0, float (&s)[4][kC]) {
+__device__ __forceinline__ void LoadStateRows(bool valid, const float* sp, int row0, float (&s)[4][kC]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int c = 0; c < kC; c += 4) {
-      const float4 v = LoadStreamF4(sp + (row0 + i) * kDim + 8 * c);
+      const float4 v =
+          LoadStreamF4(valid ? sp + (row0 + i) * kDim + 8 * c : reinterpret_cast<const float*>(kZeroTaps));
       s[i][c] = v.x;
       s[i][c + 1] = v.y;
       s[i][c + 2] = v.z;
@@ -395,18 +430,18 @@ __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint
     }
   };
   GateIn gin{};
+  GateRaw graw0{};
   if constexpr (kPreload) load_rows(t0);
-  if constexpr (kPreGate) gin = GateLoad(a, static_cast<uint64_t>(t0), h);
+  if constexpr (kPreGate) graw0 = GateRequest(a, static_cast<uint64_t>(t0), h);
   bool first_step = kPreload, first_gate = kPreGate;
   float4 s[4];
   float* sp = has_slot ? a.state + (static_cast<uint64_t>(slot) * a.vh + h) * kDim * kDim + col : nullptr;
-  if (has_slot && a.use_initial_state) {
+  // Requested without a branch (zeros from kZeroTaps without a slot or an initial state): behind a branch, every wait
+  // after it for a request made before it would also wait for the state, as on the path that skips it.
+  const bool load_state = has_slot && a.use_initial_state;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s[i] = LoadStreamF4(sp + (row0 + i) * kDim);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) s[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
+  for (int i = 0; i < 4; ++i)
+    s[i] = LoadStreamF4(load_state ? sp + (row0 + i) * kDim : reinterpret_cast<const float*>(kZeroTaps));
   // Sequences of one call that share a slot run in batch order, as CpuOps runs them: each starts from the state the
   // one before it left (or from zero without use_initial_state). The workgroup of the first such sequence carries
   // the state through all of them in registers and writes it once; the others' workgroups leave.
@@ -441,7 +476,7 @@ __device__ __forceinline__ void RecurrentUnit(const GdnArgs& a, uint32_t b, uint
         vv[i] = Bf16ToF32(vrow[i]);
       }
     }
-    if (!first_gate) gin = GateLoad(a, static_cast<uint64_t>(tok), h);
+    gin = first_gate ? GateWiden(a, graw0) : GateLoad(a, static_cast<uint64_t>(tok), h);
     first_step = false;
     first_gate = false;
     float graw, beta;
@@ -622,40 +657,6 @@ struct LayerArgs {
 
 constexpr uint32_t kLayerMaxWidth = 4;
 
-// A float input of dtype bf16 or f32 in two steps, so that the load can be issued early and its value used late: the
-// request keeps the loaded bits as they are (no use of them inside the dtype branch, which would make the request wait
-// for everything in flight before it), and RawToF widens them where they are needed. LoadF's values, bit for bit.
-__device__ __forceinline__ uint32_t RawLoad(const void* p, uint32_t dt, int64_t i) {
-  return dt == ROOST_DTYPE_BF16 ? static_cast<uint32_t>(static_cast<const uint16_t*>(p)[i])
-                                : static_cast<const uint32_t*>(p)[i];
-}
-__device__ __forceinline__ float RawToF(uint32_t r, uint32_t dt) {
-  return dt == ROOST_DTYPE_BF16 ? __uint_as_float(r << 16) : __uint_as_float(r);
-}
-
-// Zeros in device memory: the stand-in a kernel reads for an absent operand, so that its request needs no branch.
-__device__ __align__(16) uint32_t kZeroTaps[4] = {0u, 0u, 0u, 0u};
-
-// GateLoad / GateFrom in the same two steps.
-struct GateRaw {
-  uint32_t r0, r1, r2, r3;
-};
-__device__ __forceinline__ GateRaw GateRequest(const GdnArgs& a, uint64_t tok, uint32_t h) {
-  if (a.gs.a != nullptr) {
-    return GateRaw{RawLoad(a.gs.a, a.gs.a_t, static_cast<int64_t>(tok * a.gs.a_stride + h)),
-                   RawLoad(a.gs.dt_bias, a.gs.dtb_t, h), RawLoad(a.gs.a_log, a.gs.alog_t, h),
-                   RawLoad(a.gs.b, a.gs.b_t, static_cast<int64_t>(tok * a.gs.b_stride + h))};
-  }
-  const uint64_t gi = tok * a.vh + h;
-  return GateRaw{__float_as_uint(a.g[gi]), static_cast<uint32_t>(a.beta[gi]), 0u, 0u};
-}
-__device__ __forceinline__ GateIn GateWiden(const GdnArgs& a, const GateRaw& r) {
-  if (a.gs.a != nullptr) {
-    return GateIn{RawToF(r.r0, a.gs.a_t), RawToF(r.r1, a.gs.dtb_t), RawToF(r.r2, a.gs.alog_t), RawToF(r.r3, a.gs.b_t)};
-  }
-  return GateIn{__uint_as_float(r.r0), __uint_as_float(r.r1 << 16), 0.0f, 0.0f};
-}
-
 // The decode layer's recurrence on the recurrent kernel's quarter workgroups (sequence b, value head h, 32 value
 // columns), with the convolution folded in: per token the workgroup convolves the 288 channels it reads (the key head's
 // 128 q and 128 k channels and its 32 v channels; CausalConv1d's arithmetic: bias, then the taps oldest first with
@@ -723,9 +724,9 @@ __global__ void __launch_bounds__(kRecThreads) ConvRecurrentKernel(LayerArgs L) 
   int32_t sj[kScanNow];
 #pragma unroll
   for (int i = 0; i < kScanNow; ++i) sj[i] = a.slots[min(static_cast<uint32_t>(lane + 64 * i), a.batch - 1)];
-  float s[4][4] = {};
+  float s[4][4];
   float* sp = has_slot ? a.state + (static_cast<uint64_t>(slot) * a.vh + h) * kDim * kDim + col : nullptr;
-  if (has_slot && a.use_initial_state) LoadStateRows<4>(sp, row0, s);
+  LoadStateRows<4>(has_slot && a.use_initial_state, sp, row0, s);
   auto state_tap = [&](CS v) { return kBf16State ? Bf16ToF32(static_cast<uint16_t>(v)) : static_cast<float>(v); };
   bool scan_pending = has_slot, chained = false, first = true;
   uint32_t cur = b;  // the sequence whose tokens run now (later members of a chain follow in turn)
