@@ -1133,6 +1133,7 @@ __device__ __forceinline__ void WyPrepChunk(const ChunkArgs& ca, uint32_t x, uin
     const int qrow = 16 * w + r16;
     const uint32_t qkeep = qrow < n ? ~0u : 0u;
     const uint16_t* qp = a.q + static_cast<uint64_t>(t0 + min(qrow, n - 1)) * a.q_stride + kh * kDim + 8 * kq;
+    const GateRaw gr = GateRequest(a, static_cast<uint64_t>(t0 + min(lane, n - 1)), h);  // in flight with the rows
     uint4 kv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -1140,7 +1141,7 @@ __device__ __forceinline__ void WyPrepChunk(const ChunkArgs& ca, uint32_t x, uin
       bq[i] = Load8<kVec>(qp + 32 * i);
     }
     float graw, braw;
-    GateAt(a, static_cast<uint64_t>(t0 + min(lane, n - 1)), h, graw, braw);
+    GateFrom(a, GateWiden(a, gr), graw, braw);
     float kk = 0.0f, qq = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
