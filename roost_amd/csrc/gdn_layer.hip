@@ -314,6 +314,9 @@ __device__ __forceinline__ void PackWords(const float* v, uint32_t* w) {
 // the last kW - 1 inputs of its channels in registers, so every input row is read once plus a kW - 1 row halo per tile,
 // and loads its kV x kW weights once. Narrow vectors (8 bytes for bf16) keep the register count low enough for eight
 // waves per SIMD, which with long tiles keeps the halo small while the grid still fills the chip several times over.
+// Zeros in device memory, read in place of an absent bias so that the request needs no branch.
+__device__ __align__(16) uint32_t kConvZeros[4] = {0u, 0u, 0u, 0u};
+
 constexpr int kConvTile = 32;
 constexpr int kConvChunk = 4;  // rows requested ahead of the arithmetic
 
@@ -332,30 +335,27 @@ __global__ void __launch_bounds__(256) ConvTileKernel(ConvArgs a, uint32_t cbloc
     LoadWords<kBytes>(x + static_cast<uint64_t>(t) * a.channels + c0, q);
     UnpackWords<T, kWords>(q, v);
   };
-  // Weights of channels c0 .. c0 + kV - 1: kV * kW consecutive elements, channel-major.
+  // Weights of channels c0 .. c0 + kV - 1: kV * kW consecutive elements, channel-major (kBytes-aligned: the launcher
+  // checks the base). Weights and bias are requested as words without a branch (no bias: zeros from kConvZeros) and
+  // unpacked after: a request inside a branch, used there, waited for everything before it.
   float w[kV][kW];
+  float bias[kV];
   {
-    float flat[kV * kW];
+    uint32_t qw[kW][kWords], qb[kWords];
     const T* wrow = static_cast<const T*>(a.w) + static_cast<uint64_t>(c0) * kW;
-    if ((reinterpret_cast<uintptr_t>(wrow) & (kBytes - 1)) == 0) {
 #pragma unroll
-      for (int q = 0; q < kW; ++q) {
-        uint32_t qw[kWords];
-        LoadWords<kBytes>(wrow + q * kV, qw);
-        UnpackWords<T, kWords>(qw, flat + q * kV);
-      }
-    } else {
+    for (int q = 0; q < kW; ++q) LoadWords<kBytes>(wrow + q * kV, qw[q]);
+    LoadWords<kBytes>(a.bias != nullptr ? static_cast<const T*>(a.bias) + c0 : reinterpret_cast<const T*>(kConvZeros),
+                      qb);
+    float flat[kV * kW];
 #pragma unroll
-      for (int i = 0; i < kV * kW; ++i) flat[i] = LoadF(wrow, a.act_t, i);
-    }
+    for (int q = 0; q < kW; ++q) UnpackWords<T, kWords>(qw[q], flat + q * kV);
 #pragma unroll
     for (int e = 0; e < kV; ++e)
 #pragma unroll
       for (int j = 0; j < kW; ++j) w[e][j] = flat[e * kW + j];
+    UnpackWords<T, kWords>(qb, bias);
   }
-  float bias[kV];
-#pragma unroll
-  for (int e = 0; e < kV; ++e) bias[e] = a.bias != nullptr ? LoadF(a.bias, a.act_t, c0 + e) : 0.0f;
 
   const int32_t seq0 = SeqOfToken(a.cu, a.batch, t_begin, a.tokens);
   const int32_t s0 = a.cu[seq0], s1 = a.cu[seq0 + 1];
@@ -1115,7 +1115,8 @@ extern "C" ROOST_API RoostStatus roost_causal_conv1d_run(RoostContext* ctx, cons
     // The tiled kernel takes 8-byte channel vectors (4 bf16 or 2 f32 channels) when the channel count and the
     // buffers allow them.
     const bool vec8 = p.channels % (8 / ElemBytes(act)) == 0 && roost::IsAligned(p.input.address, 8) &&
-                      roost::IsAligned(p.output.address, 8);
+                      roost::IsAligned(p.output.address, 8) && roost::IsAligned(p.weight.address, 8) &&
+                      roost::IsAligned(p.bias.address, 8);
     const uint32_t cblocks = Blocks(p.channels / (8 / ElemBytes(act)), 256);
     const uint64_t tiled_blocks = uint64_t{cblocks} * Blocks(p.tokens, kConvTile);
     // Tiles of kConvTile tokens pay off when sequences are long; a batch of short ones (a decode step: every tile
