@@ -439,9 +439,15 @@ __global__ void __launch_bounds__(256) QkNormKernel(T* q, T* k, const T* qw, con
   T* x = is_q ? q + t * q_stride + static_cast<uint64_t>(h) * head_dim
               : k + t * k_stride + static_cast<uint64_t>(h - q_heads) * head_dim;
   const uint32_t chunks = head_dim / kV;
+  // The row and the weight requested together, without a branch around either (lanes past the row read the weight's
+  // first chunk instead), and unpacked after: a request made and used inside a branch waited for everything before it.
+  const T* wp = is_q ? qw : kw;
+  RowRaw<T, kV, kJ> rr, wr;
+  FetchRow<T, kV, kJ>(rr, x, wp, l.sub, g, chunks, live);
+  FetchRow<T, kV, kJ>(wr, wp, wp, l.sub, g, chunks, true);
   RowRegs<kV, kJ> r, w;
-  LoadRow<T, kV, kJ>(r, x, l.sub, g, chunks, live);
-  LoadRow<T, kV, kJ>(w, is_q ? qw : kw, l.sub, g, chunks, true);
+  UnpackRow<T, kV, kJ>(rr, r, l.sub, g, chunks, live);
+  UnpackRow<T, kV, kJ>(wr, w, l.sub, g, chunks, true);
   NormRow<T, kV, kJ>(r, w, l.sub, g, chunks, 1.0f / static_cast<float>(head_dim), eps);
   if (live) StoreRow<T, kV, kJ>(r, x, l.sub, g, chunks);
 }
