@@ -450,64 +450,72 @@ __global__ void __launch_bounds__(256) ConvTileKernel(ConvArgs a, uint32_t cbloc
 template <int kW>
 __global__ void __launch_bounds__(256) ConvShortKernel(ConvArgs a) {
   constexpr int kV = 8, sl = kW - 1;
+  constexpr int kSq = sl > 0 ? 2 * sl : 1;  // 16-byte state words: sl for bf16, 2 sl for f32
   const int32_t t = static_cast<int32_t>(blockIdx.x);
   const uint32_t c0 = (blockIdx.y * blockDim.x + threadIdx.x) * kV;
   if (c0 >= a.channels) return;
+  // Every operand is requested as raw words first (no bias: zeros from kConvZeros; the state and input words in
+  // branches that do not use them) and unpacked after: a thread lives for a few round trips, and a request used
+  // inside its own branch waited for everything requested before it.
+  uint32_t wq[kW][4], bq[4];
+  const auto* wp = static_cast<const uint16_t*>(a.w) + static_cast<uint64_t>(c0) * kW;
+#pragma unroll
+  for (int q = 0; q < kW; ++q) LoadWords<16>(wp + 8 * q, wq[q]);
+  LoadWords<16>(a.bias != nullptr ? static_cast<const uint16_t*>(a.bias) + c0
+                                  : reinterpret_cast<const uint16_t*>(kConvZeros),
+                bq);
+  const int32_t b = SeqOfToken(a.cu, a.batch, t, a.tokens);
+  const int32_t t0 = a.cu[b];
+  if (t < t0 || t >= a.cu[b + 1]) return;  // a token outside every sequence (cu does not cover it): no output
+  const int32_t rel = t - t0;              // tap j of this token is entry rel + j of [state, inputs]
+  const bool bf_state = a.state_t == ROOST_DTYPE_BF16;
+  const int32_t slot = rel < sl ? a.slots[b] : -1;
+  const bool ok = slot >= 0 && static_cast<uint64_t>(slot) < a.pool_slots;
+  uint32_t sq[kSq][4] = {};
+  if (rel < sl) {  // some taps come from the state: the 8 channels' entries are 8 x sl contiguous elements
+    const uint64_t so = (static_cast<uint64_t>(ok ? slot : 0) * a.channels + c0) * sl;
+    if (bf_state) {
+#pragma unroll
+      for (int q = 0; q < sl; ++q) LoadWords<16>(static_cast<const uint16_t*>(a.state) + so + 8 * q, sq[q]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 2 * sl; ++q) LoadWords<16>(static_cast<const float*>(a.state) + so + 4 * q, sq[q]);
+    }
+  }
+  const auto* x = static_cast<const uint16_t*>(a.x);
+  uint32_t xq[kW][4] = {};
+#pragma unroll
+  for (int j = 0; j < kW; ++j) {
+    const int32_t hi = rel + j;
+    if (hi >= sl) LoadWords<16>(x + static_cast<uint64_t>(t0 + hi - sl) * a.channels + c0, xq[j]);
+  }
   float w[kV][kW];
   {
     float flat[kV * kW];
-    const auto* wp = static_cast<const uint16_t*>(a.w) + static_cast<uint64_t>(c0) * kW;
 #pragma unroll
-    for (int q = 0; q < kW; ++q) {
-      uint32_t qw[4];
-      LoadWords<16>(wp + 8 * q, qw);
-      UnpackWords<uint16_t, 4>(qw, flat + 8 * q);
-    }
+    for (int q = 0; q < kW; ++q) UnpackWords<uint16_t, 4>(wq[q], flat + 8 * q);
 #pragma unroll
     for (int e = 0; e < kV; ++e)
 #pragma unroll
       for (int j = 0; j < kW; ++j) w[e][j] = flat[e * kW + j];
   }
   float acc[kV];
-  if (a.bias != nullptr) {
-    uint32_t qw[4];
-    LoadWords<16>(static_cast<const uint16_t*>(a.bias) + c0, qw);
-    UnpackWords<uint16_t, 4>(qw, acc);
-  } else {
+  UnpackWords<uint16_t, 4>(bq, acc);
+  float st[kV][sl > 0 ? sl : 1];
+  if (rel < sl) {
+    float flat[kV * (sl > 0 ? sl : 1)];
+    if (bf_state) {
 #pragma unroll
-    for (int e = 0; e < kV; ++e) acc[e] = 0.0f;
-  }
-  const int32_t b = SeqOfToken(a.cu, a.batch, t, a.tokens);
-  const int32_t t0 = a.cu[b];
-  if (t < t0 || t >= a.cu[b + 1]) return;  // a token outside every sequence (cu does not cover it): no output
-  const int32_t rel = t - t0;              // tap j of this token is entry rel + j of [state, inputs]
-  float st[kV][sl];
-  if (rel < sl) {  // some taps come from the state: the 8 channels' entries are 8 x sl contiguous elements
-    const int32_t slot = a.slots[b];
-    const bool ok = slot >= 0 && static_cast<uint64_t>(slot) < a.pool_slots;
-    const uint64_t so = (static_cast<uint64_t>(ok ? slot : 0) * a.channels + c0) * sl;
-    float flat[kV * sl];
-    if (a.state_t == ROOST_DTYPE_BF16) {
-#pragma unroll
-      for (int q = 0; q < sl; ++q) {
-        uint32_t qw[4];
-        LoadWords<16>(static_cast<const uint16_t*>(a.state) + so + 8 * q, qw);
-        UnpackWords<uint16_t, 4>(qw, flat + 8 * q);
-      }
+      for (int q = 0; q < sl; ++q) UnpackWords<uint16_t, 4>(sq[q], flat + 8 * q);
     } else {
 #pragma unroll
-      for (int q = 0; q < 2 * sl; ++q) {
-        uint32_t qw[4];
-        LoadWords<16>(static_cast<const float*>(a.state) + so + 4 * q, qw);
-        UnpackWords<float, 4>(qw, flat + 4 * q);
-      }
+      for (int q = 0; q < 2 * sl; ++q) UnpackWords<float, 4>(sq[q], flat + 4 * q);
     }
 #pragma unroll
     for (int e = 0; e < kV; ++e)
 #pragma unroll
       for (int i = 0; i < sl; ++i) st[e][i] = ok ? flat[e * sl + i] : 0.0f;
   }
-  const auto* x = static_cast<const uint16_t*>(a.x);
 #pragma unroll
   for (int j = 0; j < kW; ++j) {
     const int32_t hi = rel + j;
@@ -516,9 +524,7 @@ __global__ void __launch_bounds__(256) ConvShortKernel(ConvArgs a) {
 #pragma unroll
       for (int e = 0; e < kV; ++e) tap[e] = st[e][hi < sl ? hi : 0];
     } else {
-      uint32_t qw[4];
-      LoadWords<16>(x + static_cast<uint64_t>(t0 + hi - sl) * a.channels + c0, qw);
-      UnpackWords<uint16_t, 4>(qw, tap);
+      UnpackWords<uint16_t, 4>(xq[j], tap);
     }
 #pragma unroll
     for (int e = 0; e < kV; ++e) acc[e] = fmaf(w[e][j], tap[e], acc[e]);
